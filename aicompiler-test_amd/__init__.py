@@ -1,0 +1,258 @@
+"""Python front end of the gfx950 decode backend (libtmc_hip.so).
+
+The product is the C ABI declared in include/tmc_hip.h; this module binds it
+with ctypes so tests, bench.py and __graft_entry__ can drive it with torch
+device tensors.  torch is imported before the library is opened so that the
+library binds to the HIP runtime torch already loaded (one runtime per
+process).  There is no fallback: if the library is missing or fails to load,
+every call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtmc_hip.so")
+
+F16, F32, BF16, I32 = 0, 1, 2, 3
+
+_lib = None
+
+
+class TmcError(RuntimeError):
+    pass
+
+
+def build() -> str:
+    from importlib import util
+    spec = util.spec_from_file_location("tmc_build", os.path.join(HERE, "build.py"))
+    mod = util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.build()
+
+
+def _declare(l):
+    vp, i64, sz, i32, f, d = C.c_void_p, C.c_int64, C.c_size_t, C.c_int, C.c_float, C.c_double
+    sigs = {
+        "tmc_last_error": (C.c_char_p, []),
+        "tmc_gemv_f16": (i32, [vp, vp, vp, i32, i64, i64, i64, vp]),
+        "tmc_skinny_gemm_f16_mfma": (i32, [vp, vp, vp, i32, i64, i64, i64, vp]),
+        "tmc_gate_up_silu_f16": (i32, [vp, vp, vp, vp, i64, i64, i64, vp]),
+        "tmc_rmsnorm": (i32, [vp, vp, vp, i32, i64, i64, f, vp]),
+        "tmc_add_rmsnorm": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, f, vp]),
+        "tmc_silu_mul": (i32, [vp, vp, vp, i32, i64, vp]),
+        "tmc_add": (i32, [vp, vp, vp, i32, i64, vp]),
+        "tmc_embedding": (i32, [vp, vp, vp, i32, i64, i64, i64, vp]),
+        "tmc_rope": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, vp]),
+        "tmc_serving_rope": (i32, [vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, vp]),
+        "tmc_kv_append": (i32, [vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, vp]),
+        "tmc_paged_kv_append": (i32, [vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, i32, vp]),
+        "tmc_serving_kv_append": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, vp]),
+        "tmc_attention_workspace_bytes": (sz, [i64, i64, i64, i64]),
+        "tmc_decode_attention": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, vp, sz,
+                                       vp]),
+        "tmc_paged_decode_attention": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64,
+                                             i64, i64, i64, i64, vp, sz, vp]),
+        "tmc_argmax_f32": (i32, [vp, vp, i64, i64, vp]),
+        "tmc_fill_normal": (i32, [vp, i32, i64, C.c_uint64, f, f, vp]),
+        "tmc_copy_bytes": (i32, [vp, vp, sz, vp]),
+        "tmc_rt_create": (i32, [C.POINTER(vp)]),
+        "tmc_rt_destroy": (None, [vp]),
+        "tmc_rt_is_available": (i32, [vp]),
+        "tmc_rt_device_name": (C.c_char_p, [vp]),
+        "tmc_rt_init_error": (C.c_char_p, [vp]),
+        "tmc_rt_stream": (vp, [vp]),
+        "tmc_rt_fail_next": (None, [vp, i32]),
+        "tmc_buf_create": (i32, [vp, sz, i32, vp, C.POINTER(vp)]),
+        "tmc_buf_wrap": (i32, [vp, vp, sz, i32, C.POINTER(vp)]),
+        "tmc_buf_write": (i32, [vp, vp, sz, sz]),
+        "tmc_buf_write_raw": (i32, [vp, vp, sz, sz]),
+        "tmc_buf_read_raw": (i32, [vp, vp, sz, sz]),
+        "tmc_buf_read": (i32, [vp, vp]),
+        "tmc_buf_count": (sz, [vp]),
+        "tmc_buf_dtype": (i32, [vp]),
+        "tmc_buf_device_ptr": (vp, [vp]),
+        "tmc_buf_release": (None, [vp]),
+        "tmc_kernel_resolve": (i32, [vp, C.c_char_p, C.POINTER(vp), C.POINTER(i32), vp, vp]),
+        "tmc_kernel_dispatch": (i32, [vp, C.POINTER(sz), C.POINTER(sz)]),
+        "tmc_kernel_release": (None, [vp]),
+        "tmc_prepare": (i32, [vp, vp, vp, sz, vp, sz, sz, sz, vp, sz, C.POINTER(vp)]),
+        "tmc_exec_run": (i32, [vp, i32, C.POINTER(d), C.POINTER(d)]),
+        "tmc_exec_release": (None, [vp]),
+        "tmc_seq_create": (i32, [vp, vp, sz, C.POINTER(vp)]),
+        "tmc_seq_run": (i32, [vp, C.POINTER(d), C.POINTER(d)]),
+        "tmc_seq_launch": (i32, [vp]),
+        "tmc_seq_release": (None, [vp]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(l, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def lib() -> C.CDLL:
+    """Open libtmc_hip.so (raises TmcError when it is missing)."""
+    global _lib
+    if _lib is None:
+        try:
+            import torch  # noqa: F401  (binds one HIP runtime per process)
+        except ImportError:
+            pass
+        if not os.path.exists(LIB_PATH):
+            raise TmcError(f"{LIB_PATH} is missing; run aicompiler-test_amd/build.py")
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+def last_error() -> str:
+    return lib().tmc_last_error().decode()
+
+
+def check(rc: int, what: str = "tmc call") -> None:
+    if rc != 0:
+        raise TmcError(f"{what}: {last_error()}")
+
+
+# ---------------------------------------------------------------- torch helpers
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+def _dtype_code(t) -> int:
+    import torch
+    return {torch.float16: F16, torch.float32: F32, torch.bfloat16: BF16,
+            torch.int32: I32}[t.dtype]
+
+
+def gemv(x, w, y, stream=None):
+    """y = x @ w.T (fp16 x, w; y fp16 or fp32)."""
+    b, k = x.shape
+    n = w.shape[0]
+    check(lib().tmc_gemv_f16(_ptr(x), _ptr(w), _ptr(y), _dtype_code(y), b, k, n, _stream(stream)),
+          "tmc_gemv_f16")
+
+
+def skinny_gemm(x, w, y, stream=None):
+    b, k = x.shape
+    n = w.shape[0]
+    check(lib().tmc_skinny_gemm_f16_mfma(_ptr(x), _ptr(w), _ptr(y), _dtype_code(y), b, k, n,
+                                         _stream(stream)), "tmc_skinny_gemm_f16_mfma")
+
+
+def gate_up_silu(x, wg, wu, out, stream=None):
+    b, h = x.shape
+    f = wg.shape[0]
+    check(lib().tmc_gate_up_silu_f16(_ptr(x), _ptr(wg), _ptr(wu), _ptr(out), b, h, f,
+                                     _stream(stream)), "tmc_gate_up_silu_f16")
+
+
+def rmsnorm(x, w, y, eps, stream=None):
+    rows, width = x.shape
+    check(lib().tmc_rmsnorm(_ptr(x), _ptr(w), _ptr(y), _dtype_code(x), rows, width, eps,
+                            _stream(stream)), "tmc_rmsnorm")
+
+
+def add_rmsnorm(residual, update, w, sum_out, norm_out, eps, stream=None):
+    rows, width = residual.shape
+    check(lib().tmc_add_rmsnorm(_ptr(residual), _ptr(update), _ptr(w), _ptr(sum_out),
+                                _ptr(norm_out), _dtype_code(residual), rows, width, eps,
+                                _stream(stream)), "tmc_add_rmsnorm")
+
+
+def silu_mul(gate, up, out, stream=None):
+    check(lib().tmc_silu_mul(_ptr(gate), _ptr(up), _ptr(out), _dtype_code(gate), gate.numel(),
+                             _stream(stream)), "tmc_silu_mul")
+
+
+def add(a, b, out, stream=None):
+    check(lib().tmc_add(_ptr(a), _ptr(b), _ptr(out), _dtype_code(a), a.numel(), _stream(stream)),
+          "tmc_add")
+
+
+def embedding(tokens, table, out, stream=None):
+    vocab, hidden = table.shape
+    check(lib().tmc_embedding(_ptr(tokens), _ptr(table), _ptr(out), _dtype_code(table),
+                              tokens.numel(), hidden, vocab, _stream(stream)), "tmc_embedding")
+
+
+def rope(x, cos, sin, valid_length, out, batch, seq, heads, head_dim, capacity, stream=None):
+    check(lib().tmc_rope(_ptr(x), _ptr(cos), _ptr(sin), _ptr(valid_length), _ptr(out),
+                         _dtype_code(x), batch, seq, heads, head_dim, capacity, _stream(stream)),
+          "tmc_rope")
+
+
+def serving_rope(x, cos, sin, valid_lengths, active, out, max_batch, heads, head_dim, capacity,
+                 stream=None):
+    check(lib().tmc_serving_rope(_ptr(x), _ptr(cos), _ptr(sin), _ptr(valid_lengths), _ptr(active),
+                                 _ptr(out), _dtype_code(x), max_batch, heads, head_dim, capacity,
+                                 _stream(stream)), "tmc_serving_rope")
+
+
+def kv_append(inp, valid_length, cache, batch, seq, heads, head_dim, capacity, head_major,
+              stream=None):
+    check(lib().tmc_kv_append(_ptr(inp), _ptr(valid_length), _ptr(cache), _dtype_code(inp), batch,
+                              seq, heads, head_dim, capacity, int(head_major), _stream(stream)),
+          "tmc_kv_append")
+
+
+def paged_kv_append(inp, valid_length, table, cache, batch, seq, heads, head_dim, capacity,
+                    page_size, head_major, stream=None):
+    check(lib().tmc_paged_kv_append(_ptr(inp), _ptr(valid_length), _ptr(table), _ptr(cache),
+                                    _dtype_code(inp), batch, seq, heads, head_dim, capacity,
+                                    page_size, int(head_major), _stream(stream)),
+          "tmc_paged_kv_append")
+
+
+def serving_kv_append(inp, valid_lengths, tables, active, cache, max_batch, heads, head_dim,
+                      capacity, page_size, head_major, stream=None):
+    check(lib().tmc_serving_kv_append(_ptr(inp), _ptr(valid_lengths), _ptr(tables), _ptr(active),
+                                      _ptr(cache), _dtype_code(inp), max_batch, heads, head_dim,
+                                      capacity, page_size, int(head_major), _stream(stream)),
+          "tmc_serving_kv_append")
+
+
+def attention_workspace_bytes(batch, q_heads, head_dim, capacity) -> int:
+    return int(lib().tmc_attention_workspace_bytes(batch, q_heads, head_dim, capacity))
+
+
+def decode_attention(q, k_cache, v_cache, valid_length, out, batch, q_heads, kv_heads, head_dim,
+                     capacity, workspace=None, stream=None):
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib().tmc_decode_attention(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(valid_length),
+                                     _ptr(out), _dtype_code(q), batch, q_heads, kv_heads, head_dim,
+                                     capacity, _ptr(workspace), ws_bytes, _stream(stream)),
+          "tmc_decode_attention")
+
+
+def paged_decode_attention(q, k_pool, v_pool, valid_lengths, tables, active, out, max_batch,
+                           q_heads, kv_heads, head_dim, page_size, max_pages, page_stride,
+                           head_stride, workspace=None, stream=None):
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib().tmc_paged_decode_attention(
+        _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(valid_lengths), _ptr(tables), _ptr(active),
+        _ptr(out), _dtype_code(q), max_batch, q_heads, kv_heads, head_dim, page_size, max_pages,
+        page_stride, head_stride, _ptr(workspace), ws_bytes, _stream(stream)),
+        "tmc_paged_decode_attention")
+
+
+def argmax(logits, tokens, stream=None):
+    rows, vocab = logits.shape
+    check(lib().tmc_argmax_f32(_ptr(logits), _ptr(tokens), rows, vocab, _stream(stream)),
+          "tmc_argmax_f32")
+
+
+def fill_normal(t, seed, mean=0.0, std=1.0, stream=None):
+    check(lib().tmc_fill_normal(_ptr(t), _dtype_code(t), t.numel(), seed, mean, std,
+                                _stream(stream)), "tmc_fill_normal")
+
+
+def copy_bytes(src, dst, nbytes, stream=None):
+    check(lib().tmc_copy_bytes(_ptr(src), _ptr(dst), nbytes, _stream(stream)), "tmc_copy_bytes")

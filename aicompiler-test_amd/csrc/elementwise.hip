@@ -1,0 +1,509 @@
+// Row reductions and elementwise decode kernels for gfx950:
+// RMSNorm, Add+RMSNorm, SiLU*Mul, residual add, embedding gather, RoPE,
+// KV-cache appends (contiguous, paged, serving), argmax, synthetic fill and
+// a copy probe.  Each kernel keeps the reference kernel's arithmetic and
+// rounding points (cited per kernel); launch shapes are chosen for wave64.
+#include "tmc_abi.hpp"
+#include "tmc_device.hpp"
+
+namespace tmc {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+
+// Block-wide sum for 256 threads; every thread gets the total.
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+  v = wave_sum(v);
+  if ((threadIdx.x & (kWave - 1)) == 0) scratch[threadIdx.x / kWave] = v;
+  __syncthreads();
+  const float total = (scratch[0] + scratch[1]) + (scratch[2] + scratch[3]);
+  return total;
+}
+
+// emitDecoderRMSNorm (DecoderLLMMetalEmitter.cpp:63-108): fp32 sum of
+// squares, inverse = rsqrt(sum/width + eps), y = T(x * inverse * w).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const T* __restrict__ x,
+                                                          const T* __restrict__ w,
+                                                          T* __restrict__ y, int width,
+                                                          float eps) {
+  __shared__ float scratch[kWaves];
+  const size_t base = (size_t)blockIdx.x * width;
+  float squares = 0.0f;
+  for (int i = threadIdx.x; i < width; i += kThreads) {
+    const float v = to_float<T>(x[base + i]);
+    squares += v * v;
+  }
+  const float total = block_sum(squares, scratch);
+  const float inverse = 1.0f / sqrtf(total / (float)width + eps);
+  for (int i = threadIdx.x; i < width; i += kThreads)
+    y[base + i] = from_float<T>(to_float<T>(x[base + i]) * inverse * to_float<T>(w[i]));
+}
+
+// emitDecoderResidualRMSNorm (DecoderLLMMetalEmitter.cpp:417-477).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(
+    const T* __restrict__ residual, const T* __restrict__ update, const T* __restrict__ w,
+    T* __restrict__ sum_out, T* __restrict__ norm_out, int width, float eps) {
+  __shared__ float scratch[kWaves];
+  const size_t base = (size_t)blockIdx.x * width;
+  float squares = 0.0f;
+  for (int i = threadIdx.x; i < width; i += kThreads) {
+    const float v = through<T>(to_float<T>(residual[base + i]) + to_float<T>(update[base + i]));
+    sum_out[base + i] = from_float<T>(v);
+    squares += v * v;
+  }
+  const float total = block_sum(squares, scratch);
+  const float inverse = 1.0f / sqrtf(total / (float)width + eps);
+  for (int i = threadIdx.x; i < width; i += kThreads) {
+    const float v = through<T>(to_float<T>(residual[base + i]) + to_float<T>(update[base + i]));
+    norm_out[base + i] = from_float<T>(v * inverse * to_float<T>(w[i]));
+  }
+}
+
+// emitDecoderSiLUMul (DecoderLLMMetalEmitter.cpp:395-415).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const T* __restrict__ gate,
+                                                           const T* __restrict__ up,
+                                                           T* __restrict__ out, size_t count) {
+  for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < count;
+       i += (size_t)gridDim.x * kThreads) {
+    const float g = to_float<T>(gate[i]);
+    const float activated = through<T>(g / (1.0f + expf(-g)));
+    out[i] = from_float<T>(activated * to_float<T>(up[i]));
+  }
+}
+
+// emitDecoderAdd (DecoderLLMMetalEmitter.cpp:375-393).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void add_kernel(const T* __restrict__ a,
+                                                      const T* __restrict__ b,
+                                                      T* __restrict__ out, size_t count) {
+  for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < count;
+       i += (size_t)gridDim.x * kThreads)
+    out[i] = from_float<T>(to_float<T>(a[i]) + to_float<T>(b[i]));
+}
+
+// emitDecoderEmbedding (DecoderLLMMetalEmitter.cpp:35-61).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void embedding_kernel(const int32_t* __restrict__ tokens,
+                                                            const T* __restrict__ table,
+                                                            T* __restrict__ out, int hidden,
+                                                            int vocabulary) {
+  const int row = blockIdx.y;
+  const int token = tokens[row];
+  if (token < 0 || token >= vocabulary) return;
+  for (int f = blockIdx.x * kThreads + threadIdx.x; f < hidden; f += gridDim.x * kThreads)
+    out[(size_t)row * hidden + f] = table[(size_t)token * hidden + f];
+}
+
+// emitDecoderRoPE (DecoderLLMMetalEmitter.cpp:110-158).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void rope_kernel(const T* __restrict__ x,
+                                                       const float* __restrict__ cosine,
+                                                       const float* __restrict__ sine,
+                                                       const int32_t* __restrict__ valid_length,
+                                                       T* __restrict__ out, int batch, int seq,
+                                                       int heads, int head_dim, int capacity) {
+  const int pairs = head_dim / 2;
+  const long items = (long)batch * heads * seq * pairs;
+  const long gid = (long)blockIdx.x * kThreads + threadIdx.x;
+  if (gid >= items) return;
+  const int valid = valid_length[0];
+  if (valid < seq || valid > capacity) return;
+  const int pair = (int)(gid % pairs);
+  const int token = (int)((gid / pairs) % seq);
+  const int head = (int)((gid / ((long)pairs * seq)) % heads);
+  const int b = (int)(gid / ((long)pairs * seq * heads));
+  const int position = valid - seq + token;
+  const size_t hidden = (size_t)heads * head_dim;
+  const size_t in_base = ((size_t)b * seq + token) * hidden + (size_t)head * head_dim + 2 * pair;
+  const size_t out_base = (((size_t)b * heads + head) * seq + token) * head_dim + 2 * pair;
+  const float c = cosine[(size_t)position * pairs + pair];
+  const float s = sine[(size_t)position * pairs + pair];
+  const float even = to_float<T>(x[in_base]);
+  const float odd = to_float<T>(x[in_base + 1]);
+  out[out_base] = from_float<T>(even * c - odd * s);
+  out[out_base + 1] = from_float<T>(even * s + odd * c);
+}
+
+// emitServingRoPE (DecoderLLMMetalEmitter.cpp:260-312).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void serving_rope_kernel(
+    const T* __restrict__ x, const float* __restrict__ cosine, const float* __restrict__ sine,
+    const int32_t* __restrict__ valid_lengths, const int32_t* __restrict__ active_count,
+    T* __restrict__ out, int max_batch, int heads, int head_dim, int capacity) {
+  const int pairs = head_dim / 2;
+  const long per_request = (long)heads * pairs;
+  const long gid = (long)blockIdx.x * kThreads + threadIdx.x;
+  const long request = gid / per_request;
+  if (gid >= (long)max_batch * per_request || request >= active_count[0]) return;
+  const int pair = (int)(gid % pairs);
+  const int head = (int)((gid / pairs) % heads);
+  const int valid = valid_lengths[request];
+  if (valid <= 0 || valid > capacity) return;
+  const int position = valid - 1;
+  const size_t base = ((size_t)request * heads + head) * head_dim + 2 * pair;
+  const float c = cosine[(size_t)position * pairs + pair];
+  const float s = sine[(size_t)position * pairs + pair];
+  const float even = to_float<T>(x[base]);
+  const float odd = to_float<T>(x[base + 1]);
+  out[base] = from_float<T>(even * c - odd * s);
+  out[base + 1] = from_float<T>(even * s + odd * c);
+}
+
+// emitDecoderCacheAppend / emitDecoderPagedCacheAppend
+// (DecoderLLMMetalEmitter.cpp:160-258): bit copies, one element per thread.
+template <typename T, bool PAGED>
+__global__ __launch_bounds__(kThreads) void append_kernel(
+    const T* __restrict__ input, const int32_t* __restrict__ valid_length,
+    const int32_t* __restrict__ block_table, T* __restrict__ cache, int batch, int seq,
+    int heads, int head_dim, int capacity, int page_size, int head_major) {
+  const long hidden = (long)heads * head_dim;
+  const long items = (long)batch * seq * hidden;
+  const long gid = (long)blockIdx.x * kThreads + threadIdx.x;
+  if (gid >= items) return;
+  const int valid = valid_length[0];
+  if (valid < seq || valid > capacity) return;
+  const long feature = gid % hidden;
+  const int token = (int)((gid / hidden) % seq);
+  const int b = (int)(gid / (hidden * seq));
+  const int head = (int)(feature / head_dim);
+  const int component = (int)(feature % head_dim);
+  const int position = valid - seq + token;
+  size_t dst;
+  if constexpr (PAGED) {
+    const int page = block_table[position / page_size];
+    if (page < 0) return;
+    dst = ((((size_t)page * batch + b) * heads + head) * page_size + position % page_size) *
+              head_dim + component;
+  } else {
+    dst = (((size_t)b * heads + head) * capacity + position) * head_dim + component;
+  }
+  const size_t src = head_major ? (((size_t)b * heads + head) * seq + token) * head_dim + component
+                                : ((size_t)b * seq + token) * hidden + feature;
+  cache[dst] = input[src];
+}
+
+// emitServingPagedCacheAppend (DecoderLLMMetalEmitter.cpp:314-373).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void serving_append_kernel(
+    const T* __restrict__ input, const int32_t* __restrict__ valid_lengths,
+    const int32_t* __restrict__ block_tables, const int32_t* __restrict__ active_count,
+    T* __restrict__ cache, int max_batch, int heads, int head_dim, int capacity, int page_size,
+    int head_major) {
+  const long hidden = (long)heads * head_dim;
+  const long gid = (long)blockIdx.x * kThreads + threadIdx.x;
+  const long request = gid / hidden;
+  if (gid >= (long)max_batch * hidden || request >= active_count[0]) return;
+  const long feature = gid % hidden;
+  const int head = (int)(feature / head_dim);
+  const int component = (int)(feature % head_dim);
+  const int valid = valid_lengths[request];
+  if (valid <= 0 || valid > capacity) return;
+  const int position = valid - 1;
+  const int max_pages = (capacity + page_size - 1) / page_size;
+  const int page = block_tables[request * max_pages + position / page_size];
+  if (page < 0) return;
+  const size_t dst =
+      (((size_t)page * heads + head) * page_size + position % page_size) * head_dim + component;
+  const size_t src = head_major ? ((size_t)request * heads + head) * head_dim + component
+                                : (size_t)request * hidden + feature;
+  cache[dst] = input[src];
+}
+
+__device__ __forceinline__ bool better(float cv, int ci, float bv, int bi) {
+  return cv > bv || (cv == bv && ci >= 0 && (bi < 0 || ci < bi));
+}
+
+// emitTokenArgmax (TransformerDecodeMetalEmitter.cpp:198-256).
+__global__ __launch_bounds__(kThreads) void argmax_kernel(const float* __restrict__ logits,
+                                                         int32_t* __restrict__ tokens,
+                                                         int vocabulary) {
+  __shared__ float best_v[kWaves];
+  __shared__ int best_i[kWaves];
+  const size_t base = (size_t)blockIdx.x * vocabulary;
+  float best = -INFINITY;
+  int selected = -1;
+  for (int t = threadIdx.x; t < vocabulary; t += kThreads) {
+    const float c = logits[base + t];
+    if (c > best || (c == best && (selected < 0 || t < selected))) {
+      best = c;
+      selected = t;
+    }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(best, off, kWave);
+    const int oi = __shfl_xor(selected, off, kWave);
+    if (better(ov, oi, best, selected)) {
+      best = ov;
+      selected = oi;
+    }
+  }
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    best_v[threadIdx.x / kWave] = best;
+    best_i[threadIdx.x / kWave] = selected;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float bv = best_v[0];
+    int bi = best_i[0];
+    for (int w = 1; w < kWaves; ++w)
+      if (better(best_v[w], best_i[w], bv, bi)) {
+        bv = best_v[w];
+        bi = best_i[w];
+      }
+    tokens[blockIdx.x] = bi;
+  }
+}
+
+// Counter-based N(mean, std) generator: splitmix64 of (seed, index) gives two
+// uniforms per pair of outputs, Box-Muller maps them to normals.
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void fill_normal_kernel(T* __restrict__ out, size_t count,
+                                                              uint64_t seed, float mean,
+                                                              float std) {
+  for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < count;
+       i += (size_t)gridDim.x * kThreads) {
+    const uint64_t pair = i >> 1;
+    const uint64_t a = splitmix64(seed * 0xD1B54A32D192ED03ull + 2 * pair);
+    const uint64_t b = splitmix64(seed * 0xD1B54A32D192ED03ull + 2 * pair + 1);
+    const float u1 = ((float)(a >> 40) + 1.0f) * (1.0f / 16777216.0f);  // (0, 1]
+    const float u2 = (float)(b >> 40) * (1.0f / 16777216.0f);           // [0, 1)
+    const float r = sqrtf(-2.0f * logf(u1));
+    const float angle = 6.283185307179586f * u2;
+    const float z = (i & 1) ? r * sinf(angle) : r * cosf(angle);
+    out[i] = from_float<T>(mean + std * z);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void copy_kernel(const uint4* __restrict__ src,
+                                                       uint4* __restrict__ dst, size_t count) {
+  for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < count;
+       i += (size_t)gridDim.x * kThreads)
+    dst[i] = src[i];
+}
+
+unsigned grid_for(size_t items) {
+  const size_t blocks = (items + kThreads - 1) / kThreads;
+  return (unsigned)(blocks < 65536 * 8 ? (blocks ? blocks : 1) : 65536 * 8);
+}
+
+bool float_dtype(int dtype) { return dtype == TMC_F16 || dtype == TMC_F32; }
+
+}  // namespace
+}  // namespace tmc
+
+using namespace tmc;
+
+#define TMC_DISPATCH_T(dtype, FN)                 \
+  do {                                            \
+    if ((dtype) == TMC_F32) {                     \
+      typedef float T;                            \
+      FN;                                         \
+    } else {                                      \
+      typedef half_t T;                           \
+      FN;                                         \
+    }                                             \
+  } while (0)
+
+extern "C" int tmc_rmsnorm(const void* x, const void* w, void* y, int dtype, int64_t rows,
+                           int64_t width, float epsilon, void* stream) {
+  TMC_REQUIRE(x && w && y, "RMSNorm: null device pointer.");
+  TMC_REQUIRE(float_dtype(dtype), "RMSNorm: dtype must be fp16 or fp32.");
+  TMC_REQUIRE(rows > 0 && width > 0 && width < (1LL << 31) && rows < (1LL << 31),
+              "RMSNorm: invalid shape.");
+  TMC_REQUIRE(std::isfinite(epsilon) && epsilon > 0.0f, "RMSNorm: epsilon must be finite and positive.");
+  TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((rmsnorm_kernel<T>), dim3((unsigned)rows), dim3(kThreads), 0,
+                                            as_stream(stream), static_cast<const T*>(x),
+                                            static_cast<const T*>(w), static_cast<T*>(y),
+                                            (int)width, epsilon));
+  return check_launch("rmsnorm_kernel");
+}
+
+extern "C" int tmc_add_rmsnorm(const void* residual, const void* update, const void* w,
+                               void* sum_out, void* norm_out, int dtype, int64_t rows,
+                               int64_t width, float epsilon, void* stream) {
+  TMC_REQUIRE(residual && update && w && sum_out && norm_out, "Add+RMSNorm: null device pointer.");
+  TMC_REQUIRE(float_dtype(dtype), "Add+RMSNorm: dtype must be fp16 or fp32.");
+  TMC_REQUIRE(rows > 0 && width > 0 && width < (1LL << 31) && rows < (1LL << 31),
+              "Add+RMSNorm: invalid shape.");
+  TMC_REQUIRE(std::isfinite(epsilon) && epsilon > 0.0f, "Add+RMSNorm: epsilon must be finite and positive.");
+  TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((add_rmsnorm_kernel<T>), dim3((unsigned)rows), dim3(kThreads), 0,
+                                            as_stream(stream), static_cast<const T*>(residual),
+                                            static_cast<const T*>(update), static_cast<const T*>(w),
+                                            static_cast<T*>(sum_out), static_cast<T*>(norm_out),
+                                            (int)width, epsilon));
+  return check_launch("add_rmsnorm_kernel");
+}
+
+extern "C" int tmc_silu_mul(const void* gate, const void* up, void* out, int dtype, int64_t count,
+                            void* stream) {
+  TMC_REQUIRE(gate && up && out, "SiLU*Mul: null device pointer.");
+  TMC_REQUIRE(float_dtype(dtype) && count > 0, "SiLU*Mul: invalid dtype or count.");
+  TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((silu_mul_kernel<T>), dim3(grid_for(count)), dim3(kThreads), 0,
+                                            as_stream(stream), static_cast<const T*>(gate),
+                                            static_cast<const T*>(up), static_cast<T*>(out),
+                                            (size_t)count));
+  return check_launch("silu_mul_kernel");
+}
+
+extern "C" int tmc_add(const void* a, const void* b, void* out, int dtype, int64_t count,
+                       void* stream) {
+  TMC_REQUIRE(a && b && out, "Add: null device pointer.");
+  TMC_REQUIRE(float_dtype(dtype) && count > 0, "Add: invalid dtype or count.");
+  TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((add_kernel<T>), dim3(grid_for(count)), dim3(kThreads), 0,
+                                            as_stream(stream), static_cast<const T*>(a),
+                                            static_cast<const T*>(b), static_cast<T*>(out),
+                                            (size_t)count));
+  return check_launch("add_kernel");
+}
+
+extern "C" int tmc_embedding(const int32_t* tokens, const void* table, void* out, int dtype,
+                             int64_t rows, int64_t hidden, int64_t vocabulary, void* stream) {
+  TMC_REQUIRE(tokens && table && out, "Embedding: null device pointer.");
+  TMC_REQUIRE(float_dtype(dtype) && rows > 0 && rows < 65536 && hidden > 0 && vocabulary > 0 &&
+                  hidden < (1LL << 31) && vocabulary < (1LL << 31),
+              "Embedding: invalid dtype or shape.");
+  const dim3 grid((unsigned)((hidden + kThreads - 1) / kThreads), (unsigned)rows);
+  TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((embedding_kernel<T>), grid, dim3(kThreads), 0,
+                                            as_stream(stream), tokens, static_cast<const T*>(table),
+                                            static_cast<T*>(out), (int)hidden, (int)vocabulary));
+  return check_launch("embedding_kernel");
+}
+
+extern "C" int tmc_rope(const void* x, const float* cosine, const float* sine,
+                        const int32_t* valid_length, void* out, int dtype, int64_t batch,
+                        int64_t seq, int64_t heads, int64_t head_dim, int64_t capacity,
+                        void* stream) {
+  TMC_REQUIRE(x && cosine && sine && valid_length && out, "RoPE: null device pointer.");
+  TMC_REQUIRE(float_dtype(dtype) && batch > 0 && seq > 0 && heads > 0 && head_dim > 0 &&
+                  head_dim % 2 == 0 && capacity >= seq,
+              "RoPE: invalid dtype or shape.");
+  const size_t items = (size_t)batch * heads * seq * (head_dim / 2);
+  TMC_REQUIRE(items < (1ull << 40), "RoPE: too many elements.");
+  TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((rope_kernel<T>), dim3((unsigned)((items + kThreads - 1) / kThreads)),
+                                            dim3(kThreads), 0, as_stream(stream),
+                                            static_cast<const T*>(x), cosine, sine, valid_length,
+                                            static_cast<T*>(out), (int)batch, (int)seq, (int)heads,
+                                            (int)head_dim, (int)capacity));
+  return check_launch("rope_kernel");
+}
+
+extern "C" int tmc_serving_rope(const void* x, const float* cosine, const float* sine,
+                                const int32_t* valid_lengths, const int32_t* active_count,
+                                void* out, int dtype, int64_t max_batch, int64_t heads,
+                                int64_t head_dim, int64_t capacity, void* stream) {
+  TMC_REQUIRE(x && cosine && sine && valid_lengths && active_count && out,
+              "Serving RoPE: null device pointer.");
+  TMC_REQUIRE(float_dtype(dtype) && max_batch > 0 && heads > 0 && head_dim > 0 &&
+                  head_dim % 2 == 0 && capacity > 0,
+              "Serving RoPE: invalid dtype or shape.");
+  const size_t items = (size_t)max_batch * heads * (head_dim / 2);
+  TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((serving_rope_kernel<T>), dim3((unsigned)((items + kThreads - 1) / kThreads)),
+                                            dim3(kThreads), 0, as_stream(stream),
+                                            static_cast<const T*>(x), cosine, sine, valid_lengths,
+                                            active_count, static_cast<T*>(out), (int)max_batch,
+                                            (int)heads, (int)head_dim, (int)capacity));
+  return check_launch("serving_rope_kernel");
+}
+
+static int append_common(const void* input, const int32_t* valid_length, const int32_t* table,
+                         void* cache, int dtype, int64_t batch, int64_t seq, int64_t heads,
+                         int64_t head_dim, int64_t capacity, int64_t page_size, int head_major,
+                         bool paged, void* stream) {
+  TMC_REQUIRE(input && valid_length && cache && (!paged || table), "KV append: null device pointer.");
+  TMC_REQUIRE(float_dtype(dtype) && batch > 0 && seq > 0 && heads > 0 && head_dim > 0 &&
+                  capacity >= seq && (!paged || (page_size > 0 && page_size <= capacity)),
+              "KV append: invalid dtype or shape.");
+  const size_t items = (size_t)batch * seq * heads * head_dim;
+  const dim3 grid((unsigned)((items + kThreads - 1) / kThreads));
+  if (paged) {
+    TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((append_kernel<T, true>), grid, dim3(kThreads), 0,
+                                              as_stream(stream), static_cast<const T*>(input),
+                                              valid_length, table, static_cast<T*>(cache),
+                                              (int)batch, (int)seq, (int)heads, (int)head_dim,
+                                              (int)capacity, (int)page_size, head_major));
+  } else {
+    TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((append_kernel<T, false>), grid, dim3(kThreads), 0,
+                                              as_stream(stream), static_cast<const T*>(input),
+                                              valid_length, table, static_cast<T*>(cache),
+                                              (int)batch, (int)seq, (int)heads, (int)head_dim,
+                                              (int)capacity, 1, head_major));
+  }
+  return check_launch("append_kernel");
+}
+
+extern "C" int tmc_kv_append(const void* input, const int32_t* valid_length, void* cache,
+                             int dtype, int64_t batch, int64_t seq, int64_t heads,
+                             int64_t head_dim, int64_t capacity, int head_major, void* stream) {
+  return append_common(input, valid_length, nullptr, cache, dtype, batch, seq, heads, head_dim,
+                       capacity, 0, head_major, false, stream);
+}
+
+extern "C" int tmc_paged_kv_append(const void* input, const int32_t* valid_length,
+                                   const int32_t* block_table, void* cache, int dtype,
+                                   int64_t batch, int64_t seq, int64_t heads, int64_t head_dim,
+                                   int64_t capacity, int64_t page_size, int head_major,
+                                   void* stream) {
+  return append_common(input, valid_length, block_table, cache, dtype, batch, seq, heads,
+                       head_dim, capacity, page_size, head_major, true, stream);
+}
+
+extern "C" int tmc_serving_kv_append(const void* input, const int32_t* valid_lengths,
+                                     const int32_t* block_tables, const int32_t* active_count,
+                                     void* cache, int dtype, int64_t max_batch, int64_t heads,
+                                     int64_t head_dim, int64_t capacity, int64_t page_size,
+                                     int head_major, void* stream) {
+  TMC_REQUIRE(input && valid_lengths && block_tables && active_count && cache,
+              "Serving KV append: null device pointer.");
+  TMC_REQUIRE(float_dtype(dtype) && max_batch > 0 && heads > 0 && head_dim > 0 && capacity > 0 &&
+                  page_size > 0 && page_size <= capacity,
+              "Serving KV append: invalid dtype or shape.");
+  const size_t items = (size_t)max_batch * heads * head_dim;
+  const dim3 grid((unsigned)((items + kThreads - 1) / kThreads));
+  TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((serving_append_kernel<T>), grid, dim3(kThreads), 0,
+                                            as_stream(stream), static_cast<const T*>(input),
+                                            valid_lengths, block_tables, active_count,
+                                            static_cast<T*>(cache), (int)max_batch, (int)heads,
+                                            (int)head_dim, (int)capacity, (int)page_size,
+                                            head_major));
+  return check_launch("serving_append_kernel");
+}
+
+extern "C" int tmc_argmax_f32(const float* logits, int32_t* tokens, int64_t rows,
+                              int64_t vocabulary, void* stream) {
+  TMC_REQUIRE(logits && tokens, "Argmax: null device pointer.");
+  TMC_REQUIRE(rows > 0 && rows < (1LL << 31) && vocabulary > 0 && vocabulary < (1LL << 31),
+              "Argmax: invalid shape.");
+  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(kThreads), 0, as_stream(stream),
+                     logits, tokens, (int)vocabulary);
+  return check_launch("argmax_kernel");
+}
+
+extern "C" int tmc_fill_normal(void* ptr, int dtype, int64_t count, uint64_t seed, float mean,
+                               float std, void* stream) {
+  TMC_REQUIRE(ptr && count > 0 && float_dtype(dtype), "Fill: invalid arguments.");
+  TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((fill_normal_kernel<T>), dim3(grid_for(count)), dim3(kThreads), 0,
+                                            as_stream(stream), static_cast<T*>(ptr), (size_t)count,
+                                            seed, mean, std));
+  return check_launch("fill_normal_kernel");
+}
+
+extern "C" int tmc_copy_bytes(const void* src, void* dst, size_t bytes, void* stream) {
+  TMC_REQUIRE(src && dst && bytes > 0 && bytes % 16 == 0 && aligned16(src) && aligned16(dst),
+              "Copy: pointers must be 16-byte aligned and size a multiple of 16.");
+  const size_t count = bytes / 16;
+  hipLaunchKernelGGL(copy_kernel, dim3(grid_for(count)), dim3(kThreads), 0, as_stream(stream),
+                     static_cast<const uint4*>(src), static_cast<uint4*>(dst), count);
+  return check_launch("copy_kernel");
+}

@@ -1,0 +1,829 @@
+// Runtime objects of the C ABI: the HIP counterpart of MetalRuntime,
+// MetalBuffer, PreparedExecution and PreparedSequence
+// (/root/reference/src/backend/metal/MetalRuntime.hpp:56-208, .mm:140-781).
+//
+//  * Buffers are hipMalloc allocations with the reference's host conversion
+//    rules (fp16 ties away from zero, bf16 RNE, int32 truncation) and its
+//    NaN / zero fill for fresh buffers.
+//  * Kernels are resolved from a static table keyed "name?k=v&...", which
+//    replaces runtime MSL compilation plus pipeline reflection: each entry
+//    declares its binding types and writability and launches one of the
+//    typed gfx950 entry points.
+//  * A prepared execution owns its bindings, constants and any workspace.
+//  * A sequence is captured once into a HIP graph and replayed with a single
+//    hipGraphLaunch (the counterpart of one Metal command buffer).
+#include "tmc_abi.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <functional>
+#include <limits>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace tmc {
+
+namespace {
+thread_local std::string g_error;
+}
+
+void set_error(const std::string& message) { g_error = message; }
+void clear_error() { g_error.clear(); }
+
+int check_launch(const char* what) {
+  const hipError_t err = hipGetLastError();
+  if (err == hipSuccess) return 0;
+  set_error(std::string(what) + ": launch failed: " + hipGetErrorString(err));
+  return 1;
+}
+
+namespace {
+
+// ------------------------------------------------------------------ host conversions
+uint16_t host_f32_to_f16(float value) {
+  uint32_t bits;
+  std::memcpy(&bits, &value, sizeof bits);
+  const uint32_t sign = (bits >> 16) & 0x8000u;
+  const uint32_t biased = (bits >> 23) & 0xffu;
+  const uint32_t fraction = bits & 0x7fffffu;
+  if (biased == 0xffu) return (uint16_t)(sign | (fraction ? 0x7e00u : 0x7c00u));
+  const int exponent = (int)biased - 112;
+  if (exponent >= 31) return (uint16_t)(sign | 0x7c00u);
+  if (exponent <= 0) {
+    if (exponent < -10) return (uint16_t)sign;
+    const uint32_t significand = fraction | 0x800000u;
+    const int shift = 14 - exponent;
+    return (uint16_t)(sign | ((significand + (1u << (shift - 1))) >> shift));
+  }
+  const uint32_t rounded = fraction + 0x1000u;
+  if (rounded & 0x800000u) {
+    if (exponent + 1 >= 31) return (uint16_t)(sign | 0x7c00u);
+    return (uint16_t)(sign | ((uint32_t)(exponent + 1) << 10));
+  }
+  return (uint16_t)(sign | ((uint32_t)exponent << 10) | (rounded >> 13));
+}
+
+float host_f16_to_f32(uint16_t half) {
+  const uint32_t sign = (uint32_t)(half & 0x8000u) << 16;
+  uint32_t exponent = (half >> 10) & 0x1fu;
+  uint32_t mantissa = half & 0x3ffu;
+  uint32_t bits;
+  if (exponent == 0) {
+    if (mantissa == 0) {
+      bits = sign;
+    } else {
+      int shift = 0;
+      while ((mantissa & 0x400u) == 0) {
+        mantissa <<= 1;
+        ++shift;
+      }
+      bits = sign | ((uint32_t)(113 - shift) << 23) | ((mantissa & 0x3ffu) << 13);
+    }
+  } else if (exponent == 31) {
+    bits = sign | 0x7f800000u | (mantissa << 13);
+  } else {
+    bits = sign | ((exponent + 112) << 23) | (mantissa << 13);
+  }
+  float out;
+  std::memcpy(&out, &bits, sizeof out);
+  return out;
+}
+
+uint16_t host_f32_to_bf16(float value) {
+  uint32_t bits;
+  std::memcpy(&bits, &value, sizeof bits);
+  return (uint16_t)((bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16);
+}
+
+float host_bf16_to_f32(uint16_t v) {
+  const uint32_t bits = (uint32_t)v << 16;
+  float out;
+  std::memcpy(&out, &bits, sizeof out);
+  return out;
+}
+
+size_t element_bytes(int dtype) { return dtype == TMC_F16 || dtype == TMC_BF16 ? 2 : 4; }
+bool valid_dtype(int dtype) { return dtype >= TMC_F16 && dtype <= TMC_I32; }
+
+std::vector<uint8_t> encode(const float* src, size_t count, int dtype) {
+  std::vector<uint8_t> out(count * element_bytes(dtype));
+  for (size_t i = 0; i < count; ++i) {
+    switch (dtype) {
+    case TMC_F16: reinterpret_cast<uint16_t*>(out.data())[i] = host_f32_to_f16(src[i]); break;
+    case TMC_BF16: reinterpret_cast<uint16_t*>(out.data())[i] = host_f32_to_bf16(src[i]); break;
+    case TMC_I32: reinterpret_cast<int32_t*>(out.data())[i] = (int32_t)src[i]; break;
+    default: reinterpret_cast<float*>(out.data())[i] = src[i]; break;
+    }
+  }
+  return out;
+}
+
+int hip_ok(hipError_t err, const char* what) {
+  if (err == hipSuccess) return 0;
+  set_error(std::string(what) + ": " + hipGetErrorString(err));
+  return 1;
+}
+
+// Fill with the reference sentinel of each dtype (MetalRuntime.mm:200-215,
+// :548-556).  `fresh` selects createBuffer's int fill (0) over run()'s
+// INT32_MIN.
+int fill_sentinel(void* ptr, size_t count, int dtype, bool fresh, hipStream_t stream) {
+  hipError_t err;
+  switch (dtype) {
+  case TMC_F32: err = hipMemsetD32Async(ptr, 0x7fc00000, count, stream); break;
+  case TMC_F16: err = hipMemsetD16Async(ptr, 0x7e00, count, stream); break;
+  case TMC_BF16: err = hipMemsetD16Async(ptr, 0x7fc0, count, stream); break;
+  default: err = hipMemsetD32Async(ptr, fresh ? 0 : (int)0x80000000u, count, stream); break;
+  }
+  return hip_ok(err, "sentinel fill");
+}
+
+}  // namespace
+}  // namespace tmc
+
+using namespace tmc;
+
+// ====================================================================== objects
+struct tmc_runtime {
+  bool available = false;
+  std::string device_name;
+  std::string init_error;
+  hipStream_t stream = nullptr;
+  hipDeviceProp_t props{};
+  int fail_next = 0;
+};
+
+struct tmc_buffer {
+  tmc_runtime* rt = nullptr;
+  void* ptr = nullptr;
+  size_t count = 0;
+  int dtype = TMC_F32;
+  bool owned = true;
+};
+
+namespace {
+
+struct LaunchContext {
+  std::vector<void*> ptrs;  // inputs then outputs, device addresses
+  std::vector<uint32_t> constants;
+  void* workspace = nullptr;
+  size_t workspace_bytes = 0;
+  hipStream_t stream = nullptr;
+};
+
+using Params = std::map<std::string, std::string>;
+
+struct KernelSpec {
+  std::vector<int> inputs;
+  std::vector<int> outputs;
+  size_t groups = 1;
+  size_t threads = 256;
+  size_t workspace_bytes = 0;
+  std::function<int(const LaunchContext&)> launch;
+};
+
+}  // namespace
+
+struct tmc_kernel {
+  std::string key;
+  KernelSpec spec;
+};
+
+// A prepared execution keeps its own copy of the kernel entry, so releasing
+// the resolved kernel does not invalidate it (PreparedExecution owns its
+// pipeline, MetalRuntime.hpp:101-102).
+struct tmc_exec {
+  tmc_runtime* rt = nullptr;
+  KernelSpec spec;
+  std::vector<tmc_buffer*> outputs;
+  LaunchContext ctx;
+};
+
+struct tmc_seq {
+  tmc_runtime* rt = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+namespace {
+
+int64_t param_int(const Params& p, const char* name, int64_t fallback = -1) {
+  const auto it = p.find(name);
+  if (it == p.end()) return fallback;
+  return std::strtoll(it->second.c_str(), nullptr, 10);
+}
+
+double param_double(const Params& p, const char* name, double fallback) {
+  const auto it = p.find(name);
+  if (it == p.end()) return fallback;
+  return std::strtod(it->second.c_str(), nullptr);
+}
+
+int param_dtype(const Params& p, const char* name, int fallback) {
+  const auto it = p.find(name);
+  if (it == p.end()) return fallback;
+  const std::string& v = it->second;
+  if (v == "f16" || v == "fp16") return TMC_F16;
+  if (v == "f32" || v == "fp32") return TMC_F32;
+  if (v == "bf16") return TMC_BF16;
+  if (v == "i32" || v == "int32") return TMC_I32;
+  return -1;
+}
+
+bool parse_key(const std::string& key, std::string& name, Params& params) {
+  const auto q = key.find('?');
+  name = key.substr(0, q);
+  if (q == std::string::npos) return !name.empty();
+  size_t pos = q + 1;
+  while (pos < key.size()) {
+    auto amp = key.find('&', pos);
+    if (amp == std::string::npos) amp = key.size();
+    const auto item = key.substr(pos, amp - pos);
+    const auto eq = item.find('=');
+    if (eq == std::string::npos || eq == 0) return false;
+    params[item.substr(0, eq)] = item.substr(eq + 1);
+    pos = amp + 1;
+  }
+  return !name.empty();
+}
+
+#define NEED(cond, msg)          \
+  do {                           \
+    if (!(cond)) {               \
+      set_error(msg);            \
+      return false;              \
+    }                            \
+  } while (0)
+
+// Build the kernel table entry for `name` with its specialization.
+bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
+  const int dt = param_dtype(p, "dtype", TMC_F16);
+  NEED(dt >= 0, "Unknown dtype in kernel key.");
+  if (name == "decode_gemv") {
+    const int64_t b = param_int(p, "batch"), k = param_int(p, "in"), n = param_int(p, "out");
+    const int od = param_dtype(p, "out_dtype", TMC_F16);
+    NEED(b > 0 && k > 0 && n > 0 && (od == TMC_F16 || od == TMC_F32) && dt == TMC_F16,
+         "decode_gemv needs batch, in, out > 0, dtype=f16 and out_dtype f16|f32.");
+    s.inputs = {TMC_F16, TMC_F16};
+    s.outputs = {od};
+    s.groups = (size_t)((n + 3) / 4);
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_gemv_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], od, b, k, n, c.stream);
+    };
+    return true;
+  }
+  if (name == "gate_up_silu") {
+    const int64_t b = param_int(p, "batch"), h = param_int(p, "hidden"), f = param_int(p, "inter");
+    NEED(b > 0 && h > 0 && f > 0 && dt == TMC_F16, "gate_up_silu needs batch, hidden, inter and f16.");
+    s.inputs = {TMC_F16, TMC_F16, TMC_F16};
+    s.outputs = {TMC_F16};
+    s.groups = (size_t)((f + 3) / 4);
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_gate_up_silu_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], b, h, f, c.stream);
+    };
+    return true;
+  }
+  if (name == "rmsnorm" || name == "add_rmsnorm") {
+    const int64_t rows = param_int(p, "rows"), width = param_int(p, "width");
+    const float eps = (float)param_double(p, "eps", 1e-5);
+    NEED(rows > 0 && width > 0 && (dt == TMC_F16 || dt == TMC_F32), "rmsnorm needs rows, width, f16|f32.");
+    s.groups = (size_t)rows;
+    if (name == "rmsnorm") {
+      s.inputs = {dt, dt};
+      s.outputs = {dt};
+      s.launch = [=](const LaunchContext& c) {
+        return tmc_rmsnorm(c.ptrs[0], c.ptrs[1], c.ptrs[2], dt, rows, width, eps, c.stream);
+      };
+    } else {
+      s.inputs = {dt, dt, dt};
+      s.outputs = {dt, dt};
+      s.launch = [=](const LaunchContext& c) {
+        return tmc_add_rmsnorm(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], c.ptrs[4], dt, rows,
+                               width, eps, c.stream);
+      };
+    }
+    return true;
+  }
+  if (name == "silu_mul" || name == "add") {
+    const int64_t n = param_int(p, "count");
+    NEED(n > 0 && (dt == TMC_F16 || dt == TMC_F32), "elementwise kernel needs count and f16|f32.");
+    s.inputs = {dt, dt};
+    s.outputs = {dt};
+    s.groups = (size_t)((n + 255) / 256);
+    const bool silu = name == "silu_mul";
+    s.launch = [=](const LaunchContext& c) {
+      return silu ? tmc_silu_mul(c.ptrs[0], c.ptrs[1], c.ptrs[2], dt, n, c.stream)
+                  : tmc_add(c.ptrs[0], c.ptrs[1], c.ptrs[2], dt, n, c.stream);
+    };
+    return true;
+  }
+  if (name == "embedding") {
+    const int64_t rows = param_int(p, "rows"), h = param_int(p, "hidden"), v = param_int(p, "vocab");
+    NEED(rows > 0 && h > 0 && v > 0, "embedding needs rows, hidden, vocab.");
+    s.inputs = {TMC_I32, dt};
+    s.outputs = {dt};
+    s.groups = (size_t)rows;
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_embedding(static_cast<const int32_t*>(c.ptrs[0]), c.ptrs[1], c.ptrs[2], dt, rows,
+                           h, v, c.stream);
+    };
+    return true;
+  }
+  if (name == "rope") {
+    const int64_t b = param_int(p, "batch"), sq = param_int(p, "seq"), hd = param_int(p, "heads"),
+                  d = param_int(p, "head_dim"), cap = param_int(p, "capacity");
+    NEED(b > 0 && sq > 0 && hd > 0 && d > 0 && cap > 0, "rope needs batch, seq, heads, head_dim, capacity.");
+    s.inputs = {dt, TMC_F32, TMC_F32, TMC_I32};
+    s.outputs = {dt};
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_rope(c.ptrs[0], static_cast<const float*>(c.ptrs[1]),
+                      static_cast<const float*>(c.ptrs[2]), static_cast<const int32_t*>(c.ptrs[3]),
+                      c.ptrs[4], dt, b, sq, hd, d, cap, c.stream);
+    };
+    return true;
+  }
+  if (name == "serving_rope") {
+    const int64_t b = param_int(p, "max_batch"), hd = param_int(p, "heads"),
+                  d = param_int(p, "head_dim"), cap = param_int(p, "capacity");
+    NEED(b > 0 && hd > 0 && d > 0 && cap > 0, "serving_rope needs max_batch, heads, head_dim, capacity.");
+    s.inputs = {dt, TMC_F32, TMC_F32, TMC_I32, TMC_I32};
+    s.outputs = {dt};
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_serving_rope(c.ptrs[0], static_cast<const float*>(c.ptrs[1]),
+                              static_cast<const float*>(c.ptrs[2]),
+                              static_cast<const int32_t*>(c.ptrs[3]),
+                              static_cast<const int32_t*>(c.ptrs[4]), c.ptrs[5], dt, b, hd, d, cap,
+                              c.stream);
+    };
+    return true;
+  }
+  if (name == "kv_append" || name == "paged_kv_append") {
+    const int64_t b = param_int(p, "batch"), sq = param_int(p, "seq"), hd = param_int(p, "heads"),
+                  d = param_int(p, "head_dim"), cap = param_int(p, "capacity");
+    const int hm = (int)param_int(p, "head_major", 0);
+    NEED(b > 0 && sq > 0 && hd > 0 && d > 0 && cap > 0, "kv_append needs batch, seq, heads, head_dim, capacity.");
+    if (name == "kv_append") {
+      s.inputs = {dt, TMC_I32};
+      s.outputs = {dt};
+      s.launch = [=](const LaunchContext& c) {
+        return tmc_kv_append(c.ptrs[0], static_cast<const int32_t*>(c.ptrs[1]), c.ptrs[2], dt, b,
+                             sq, hd, d, cap, hm, c.stream);
+      };
+    } else {
+      const int64_t ps = param_int(p, "page_size");
+      NEED(ps > 0, "paged_kv_append needs page_size.");
+      s.inputs = {dt, TMC_I32, TMC_I32};
+      s.outputs = {dt};
+      s.launch = [=](const LaunchContext& c) {
+        return tmc_paged_kv_append(c.ptrs[0], static_cast<const int32_t*>(c.ptrs[1]),
+                                   static_cast<const int32_t*>(c.ptrs[2]), c.ptrs[3], dt, b, sq,
+                                   hd, d, cap, ps, hm, c.stream);
+      };
+    }
+    return true;
+  }
+  if (name == "serving_kv_append") {
+    const int64_t b = param_int(p, "max_batch"), hd = param_int(p, "heads"),
+                  d = param_int(p, "head_dim"), cap = param_int(p, "capacity"),
+                  ps = param_int(p, "page_size");
+    const int hm = (int)param_int(p, "head_major", 0);
+    NEED(b > 0 && hd > 0 && d > 0 && cap > 0 && ps > 0, "serving_kv_append needs max_batch, heads, head_dim, capacity, page_size.");
+    s.inputs = {dt, TMC_I32, TMC_I32, TMC_I32};
+    s.outputs = {dt};
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_serving_kv_append(c.ptrs[0], static_cast<const int32_t*>(c.ptrs[1]),
+                                   static_cast<const int32_t*>(c.ptrs[2]),
+                                   static_cast<const int32_t*>(c.ptrs[3]), c.ptrs[4], dt, b, hd,
+                                   d, cap, ps, hm, c.stream);
+    };
+    return true;
+  }
+  if (name == "decode_attention") {
+    const int64_t b = param_int(p, "batch"), qh = param_int(p, "q_heads"),
+                  kvh = param_int(p, "kv_heads", param_int(p, "q_heads")),
+                  d = param_int(p, "head_dim"), cap = param_int(p, "capacity");
+    NEED(b > 0 && qh > 0 && kvh > 0 && d > 0 && cap > 0, "decode_attention needs batch, q_heads, head_dim, capacity.");
+    s.inputs = {dt, dt, dt, TMC_I32};
+    s.outputs = {dt};
+    s.workspace_bytes = tmc_attention_workspace_bytes(b, qh, d, cap);
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_decode_attention(c.ptrs[0], c.ptrs[1], c.ptrs[2],
+                                  static_cast<const int32_t*>(c.ptrs[3]), c.ptrs[4], dt, b, qh, kvh,
+                                  d, cap, c.workspace, c.workspace_bytes, c.stream);
+    };
+    return true;
+  }
+  if (name == "paged_attention") {
+    const int64_t b = param_int(p, "max_batch"), qh = param_int(p, "q_heads"),
+                  kvh = param_int(p, "kv_heads", param_int(p, "q_heads")),
+                  d = param_int(p, "head_dim"), ps = param_int(p, "page_size"),
+                  mp = param_int(p, "max_pages");
+    NEED(b > 0 && qh > 0 && kvh > 0 && d > 0 && ps > 0 && mp > 0,
+         "paged_attention needs max_batch, q_heads, head_dim, page_size, max_pages.");
+    const int64_t head_stride = param_int(p, "head_stride", ps * d);
+    const int64_t page_stride = param_int(p, "page_stride", kvh * ps * d);
+    s.inputs = {dt, dt, dt, TMC_I32, TMC_I32, TMC_I32};
+    s.outputs = {dt};
+    s.workspace_bytes = tmc_attention_workspace_bytes(b, qh, d, ps * mp);
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_paged_decode_attention(
+          c.ptrs[0], c.ptrs[1], c.ptrs[2], static_cast<const int32_t*>(c.ptrs[3]),
+          static_cast<const int32_t*>(c.ptrs[4]), static_cast<const int32_t*>(c.ptrs[5]),
+          c.ptrs[6], dt, b, qh, kvh, d, ps, mp, page_stride, head_stride, c.workspace,
+          c.workspace_bytes, c.stream);
+    };
+    return true;
+  }
+  if (name == "argmax") {
+    const int64_t rows = param_int(p, "rows"), v = param_int(p, "vocab");
+    NEED(rows > 0 && v > 0, "argmax needs rows and vocab.");
+    s.inputs = {TMC_F32};
+    s.outputs = {TMC_I32};
+    s.groups = (size_t)rows;
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_argmax_f32(static_cast<const float*>(c.ptrs[0]), static_cast<int32_t*>(c.ptrs[1]),
+                            rows, v, c.stream);
+    };
+    return true;
+  }
+  set_error("Unknown gfx950 kernel '" + name + "'.");
+  return false;
+}
+
+#undef NEED
+
+int consume_failure(tmc_runtime* rt) {
+  if (rt->fail_next > 0) {
+    --rt->fail_next;
+    set_error("Injected execution failure (tmc_rt_fail_next).");
+    return 1;
+  }
+  return 0;
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+extern "C" const char* tmc_last_error(void) { return g_error.c_str(); }
+
+extern "C" int tmc_rt_create(tmc_runtime** out) {
+  clear_error();
+  if (!out) return fail("tmc_rt_create: null output.");
+  auto rt = std::make_unique<tmc_runtime>();
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count == 0) {
+    rt->init_error = "No HIP device was found.";
+  } else if (hipGetDeviceProperties(&rt->props, 0) != hipSuccess) {
+    rt->init_error = "hipGetDeviceProperties failed.";
+  } else if (std::string(rt->props.gcnArchName).rfind("gfx950", 0) != 0) {
+    rt->init_error = std::string("Device ") + rt->props.gcnArchName +
+                     " is not gfx950; this library holds gfx950 code only.";
+  } else if (hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking) != hipSuccess) {
+    rt->init_error = "hipStreamCreate failed.";
+  } else {
+    rt->available = true;
+    rt->device_name = rt->props.name;
+    if (rt->device_name.empty()) rt->device_name = rt->props.gcnArchName;
+  }
+  *out = rt.release();
+  return 0;
+}
+
+extern "C" void tmc_rt_destroy(tmc_runtime* rt) {
+  if (!rt) return;
+  if (rt->stream) {
+    (void)hipStreamSynchronize(rt->stream);
+    (void)hipStreamDestroy(rt->stream);
+  }
+  delete rt;
+}
+
+extern "C" int tmc_rt_is_available(const tmc_runtime* rt) { return rt && rt->available; }
+extern "C" const char* tmc_rt_device_name(const tmc_runtime* rt) {
+  return rt ? rt->device_name.c_str() : "";
+}
+extern "C" const char* tmc_rt_init_error(const tmc_runtime* rt) {
+  return rt ? rt->init_error.c_str() : "null runtime";
+}
+extern "C" void* tmc_rt_stream(const tmc_runtime* rt) { return rt ? (void*)rt->stream : nullptr; }
+extern "C" void tmc_rt_fail_next(tmc_runtime* rt, int count) {
+  if (rt) rt->fail_next = count;
+}
+
+extern "C" int tmc_rt_device_info(const tmc_runtime* rt, tmc_hardware_info* info) {
+  if (!rt || !info) return fail("tmc_rt_device_info: null argument.");
+  if (!rt->available) return fail(rt->init_error);
+  info->max_threads_per_threadgroup = (size_t)rt->props.maxThreadsPerBlock;
+  info->max_threadgroup_memory_length = (size_t)rt->props.sharedMemPerBlock;
+  info->max_buffer_length = (size_t)rt->props.totalGlobalMem;
+  info->supports_bfloat16 = 1;
+  info->compute_units = rt->props.multiProcessorCount;
+  info->wave_size = rt->props.warpSize;
+  return 0;
+}
+
+extern "C" int tmc_buf_create(tmc_runtime* rt, size_t count, int dtype, const float* init,
+                              tmc_buffer** out) {
+  clear_error();
+  if (!rt || !out) return fail("tmc_buf_create: null argument.");
+  if (!rt->available) return fail(rt->init_error);
+  if (!valid_dtype(dtype)) return fail("tmc_buf_create: unknown dtype.");
+  const size_t bytes = count * element_bytes(dtype);
+  if (count == 0 || bytes / element_bytes(dtype) != count || bytes > rt->props.totalGlobalMem)
+    return fail("Buffer size is zero or exceeds the device limit.");
+  auto buf = std::make_unique<tmc_buffer>();
+  buf->rt = rt;
+  buf->count = count;
+  buf->dtype = dtype;
+  if (hip_ok(hipMalloc(&buf->ptr, bytes), "Failed to allocate a device buffer")) return 1;
+  int rc;
+  if (init) {
+    const auto host = encode(init, count, dtype);
+    rc = hip_ok(hipMemcpy(buf->ptr, host.data(), bytes, hipMemcpyHostToDevice), "buffer upload");
+  } else {
+    rc = fill_sentinel(buf->ptr, count, dtype, true, rt->stream);
+    if (!rc) rc = hip_ok(hipStreamSynchronize(rt->stream), "buffer fill");
+  }
+  if (rc) {
+    (void)hipFree(buf->ptr);
+    return 1;
+  }
+  *out = buf.release();
+  return 0;
+}
+
+extern "C" int tmc_buf_wrap(tmc_runtime* rt, void* device_ptr, size_t count, int dtype,
+                            tmc_buffer** out) {
+  clear_error();
+  if (!rt || !out || !device_ptr || count == 0 || !valid_dtype(dtype))
+    return fail("tmc_buf_wrap: invalid argument.");
+  auto buf = std::make_unique<tmc_buffer>();
+  buf->rt = rt;
+  buf->ptr = device_ptr;
+  buf->count = count;
+  buf->dtype = dtype;
+  buf->owned = false;
+  *out = buf.release();
+  return 0;
+}
+
+extern "C" int tmc_buf_write(tmc_buffer* buf, const float* data, size_t count, size_t offset) {
+  clear_error();
+  if (!buf) return fail("Buffer is missing or belongs to another device.");
+  if (!data || count == 0 || offset > buf->count || count > buf->count - offset)
+    return fail("Host update range is invalid for the device buffer.");
+  const auto host = encode(data, count, buf->dtype);
+  const size_t eb = element_bytes(buf->dtype);
+  // Ordered after earlier work on the runtime stream, complete on return.
+  if (hip_ok(hipMemcpyAsync(static_cast<char*>(buf->ptr) + offset * eb, host.data(), count * eb,
+                            hipMemcpyHostToDevice, buf->rt->stream),
+             "buffer write"))
+    return 1;
+  return hip_ok(hipStreamSynchronize(buf->rt->stream), "buffer write");
+}
+
+extern "C" int tmc_buf_write_raw(tmc_buffer* buf, const void* data, size_t count, size_t offset) {
+  clear_error();
+  if (!buf || !data || count == 0 || offset > buf->count || count > buf->count - offset)
+    return fail("tmc_buf_write_raw: invalid range.");
+  const size_t eb = element_bytes(buf->dtype);
+  if (hip_ok(hipMemcpyAsync(static_cast<char*>(buf->ptr) + offset * eb, data, count * eb,
+                            hipMemcpyHostToDevice, buf->rt->stream),
+             "raw write"))
+    return 1;
+  return hip_ok(hipStreamSynchronize(buf->rt->stream), "raw write");
+}
+
+extern "C" int tmc_buf_read_raw(const tmc_buffer* buf, void* data, size_t count, size_t offset) {
+  clear_error();
+  if (!buf || !data || offset > buf->count || count > buf->count - offset)
+    return fail("tmc_buf_read_raw: invalid range.");
+  const size_t eb = element_bytes(buf->dtype);
+  if (hip_ok(hipMemcpyAsync(data, static_cast<const char*>(buf->ptr) + offset * eb, count * eb,
+                            hipMemcpyDeviceToHost, buf->rt->stream),
+             "raw read"))
+    return 1;
+  return hip_ok(hipStreamSynchronize(buf->rt->stream), "raw read");
+}
+
+extern "C" int tmc_buf_read(const tmc_buffer* buf, float* out) {
+  clear_error();
+  if (!buf || !out) return fail("tmc_buf_read: null argument.");
+  std::vector<uint8_t> host(buf->count * element_bytes(buf->dtype));
+  if (tmc_buf_read_raw(buf, host.data(), buf->count, 0)) return 1;
+  for (size_t i = 0; i < buf->count; ++i) {
+    switch (buf->dtype) {
+    case TMC_F16: out[i] = host_f16_to_f32(reinterpret_cast<uint16_t*>(host.data())[i]); break;
+    case TMC_BF16: out[i] = host_bf16_to_f32(reinterpret_cast<uint16_t*>(host.data())[i]); break;
+    case TMC_I32: out[i] = (float)reinterpret_cast<int32_t*>(host.data())[i]; break;
+    default: out[i] = reinterpret_cast<float*>(host.data())[i]; break;
+    }
+  }
+  return 0;
+}
+
+extern "C" size_t tmc_buf_count(const tmc_buffer* buf) { return buf ? buf->count : 0; }
+extern "C" int tmc_buf_dtype(const tmc_buffer* buf) { return buf ? buf->dtype : -1; }
+extern "C" void* tmc_buf_device_ptr(const tmc_buffer* buf) { return buf ? buf->ptr : nullptr; }
+
+extern "C" void tmc_buf_release(tmc_buffer* buf) {
+  if (!buf) return;
+  if (buf->owned && buf->ptr) {
+    (void)hipStreamSynchronize(buf->rt->stream);
+    (void)hipFree(buf->ptr);
+  }
+  delete buf;
+}
+
+extern "C" int tmc_kernel_resolve(tmc_runtime* rt, const char* key, tmc_kernel** out,
+                                  int* bindings, int* types, int* writable) {
+  clear_error();
+  if (!rt || !key || !out) return fail("tmc_kernel_resolve: null argument.");
+  if (!rt->available) return fail(rt->init_error);
+  std::string name;
+  Params params;
+  if (!parse_key(key, name, params)) return fail(std::string("Malformed kernel key '") + key + "'.");
+  auto kernel = std::make_unique<tmc_kernel>();
+  kernel->key = key;
+  if (!make_spec(name, params, kernel->spec)) return 1;
+  const auto& s = kernel->spec;
+  const int n = (int)(s.inputs.size() + s.outputs.size());
+  if (bindings) *bindings = n;
+  for (int i = 0; i < n; ++i) {
+    const bool is_out = i >= (int)s.inputs.size();
+    if (types) types[i] = is_out ? s.outputs[i - s.inputs.size()] : s.inputs[i];
+    if (writable) writable[i] = is_out ? 1 : 0;
+  }
+  *out = kernel.release();
+  return 0;
+}
+
+extern "C" int tmc_kernel_dispatch(const tmc_kernel* kernel, size_t* groups, size_t* threads) {
+  if (!kernel) return fail("tmc_kernel_dispatch: null kernel.");
+  if (groups) *groups = kernel->spec.groups;
+  if (threads) *threads = kernel->spec.threads;
+  return 0;
+}
+
+extern "C" void tmc_kernel_release(tmc_kernel* kernel) { delete kernel; }
+
+extern "C" int tmc_prepare(tmc_runtime* rt, const tmc_kernel* kernel, tmc_buffer* const* inputs,
+                           size_t n_in, tmc_buffer* const* outputs, size_t n_out, size_t groups,
+                           size_t threads, const uint32_t* constants, size_t n_constants,
+                           tmc_exec** out) {
+  clear_error();
+  if (!rt || !out) return fail("tmc_prepare: null argument.");
+  if (!rt->available) return fail(rt->init_error);
+  if (!kernel) return fail("Create a compute pipeline before execution.");
+  const size_t binding_count = n_in + n_out + (n_constants ? 1 : 0);
+  if (n_in == 0 || n_out == 0 || binding_count > 31 || n_constants > 1024)
+    return fail("Invalid buffer binding count or oversized inline constants.");
+  if (groups == 0 || groups > std::numeric_limits<uint32_t>::max() || threads == 0 ||
+      threads > (size_t)rt->props.maxThreadsPerBlock)
+    return fail("Kernel dispatch exceeds device or pipeline limits.");
+  const auto& s = kernel->spec;
+  if (n_in != s.inputs.size() || n_out != s.outputs.size())
+    return fail("Reflection must contain exactly the expected input and output buffers.");
+  auto exec = std::make_unique<tmc_exec>();
+  exec->rt = rt;
+  exec->spec = s;
+  for (size_t i = 0; i < n_out; ++i) {
+    tmc_buffer* o = outputs[i];
+    if (!o || o->rt != rt || std::find(outputs, outputs + i, o) != outputs + i)
+      return fail("Outputs must be distinct buffers on the current device.");
+    if (o->dtype != s.outputs[i]) return fail("Reflected buffer element type disagrees with TensorIR.");
+    exec->outputs.push_back(o);
+  }
+  for (size_t i = 0; i < n_in; ++i) {
+    tmc_buffer* b = inputs[i];
+    if (!b || b->rt != rt || std::find(outputs, outputs + n_out, b) != outputs + n_out)
+      return fail("Input is missing, on another device, or aliases an output.");
+    if (b->dtype != s.inputs[i]) return fail("Reflected buffer element type disagrees with TensorIR.");
+    exec->ctx.ptrs.push_back(b->ptr);
+  }
+  for (auto* o : exec->outputs) exec->ctx.ptrs.push_back(o->ptr);
+  if (constants) exec->ctx.constants.assign(constants, constants + n_constants);
+  exec->ctx.stream = rt->stream;
+  if (s.workspace_bytes) {
+    if (hip_ok(hipMalloc(&exec->ctx.workspace, s.workspace_bytes), "workspace allocation")) return 1;
+    exec->ctx.workspace_bytes = s.workspace_bytes;
+  }
+  *out = exec.release();
+  return 0;
+}
+
+extern "C" int tmc_exec_run(tmc_exec* exec, int reset_outputs, double* gpu_us, double* cpu_us) {
+  clear_error();
+  if (!exec) return fail("tmc_exec_run: null execution.");
+  tmc_runtime* rt = exec->rt;
+  if (consume_failure(rt)) return 1;
+  if (reset_outputs)
+    for (auto* o : exec->outputs)
+      if (fill_sentinel(o->ptr, o->count, o->dtype, false, rt->stream)) return 1;
+  hipEvent_t start = nullptr, stop = nullptr;
+  if (gpu_us) {
+    if (hip_ok(hipEventCreate(&start), "event") || hip_ok(hipEventCreate(&stop), "event")) return 1;
+    (void)hipEventRecord(start, rt->stream);
+  }
+  const auto t0 = std::chrono::steady_clock::now();
+  int rc = exec->spec.launch(exec->ctx);
+  if (gpu_us) (void)hipEventRecord(stop, rt->stream);
+  const hipError_t sync = hipStreamSynchronize(rt->stream);
+  const auto t1 = std::chrono::steady_clock::now();
+  if (!rc && sync != hipSuccess) rc = hip_ok(sync, "execution");
+  if (cpu_us) *cpu_us = std::chrono::duration<double, std::micro>(t1 - t0).count();
+  if (gpu_us) {
+    float ms = 0.0f;
+    *gpu_us = (!rc && hipEventElapsedTime(&ms, start, stop) == hipSuccess) ? ms * 1000.0 : -1.0;
+    (void)hipEventDestroy(start);
+    (void)hipEventDestroy(stop);
+  }
+  return rc;
+}
+
+extern "C" void tmc_exec_release(tmc_exec* exec) {
+  if (!exec) return;
+  if (exec->ctx.workspace) {
+    (void)hipStreamSynchronize(exec->rt->stream);
+    (void)hipFree(exec->ctx.workspace);
+  }
+  delete exec;
+}
+
+extern "C" int tmc_seq_create(tmc_runtime* rt, tmc_exec* const* steps, size_t n, tmc_seq** out) {
+  clear_error();
+  if (!rt || !out) return fail("tmc_seq_create: null argument.");
+  if (n == 0 || !steps) return fail("A prepared region sequence cannot be empty.");
+  for (size_t i = 0; i < n; ++i) {
+    if (!steps[i] || !steps[i]->spec.launch) return fail("A region contains an invalid prepared execution.");
+    if (steps[i]->rt != rt) return fail("All region steps must use the same runtime stream.");
+  }
+  auto seq = std::make_unique<tmc_seq>();
+  seq->rt = rt;
+  if (hip_ok(hipStreamSynchronize(rt->stream), "sequence capture")) return 1;
+  if (hip_ok(hipStreamBeginCapture(rt->stream, hipStreamCaptureModeThreadLocal), "begin capture"))
+    return 1;
+  int rc = 0;
+  for (size_t i = 0; i < n && !rc; ++i) rc = steps[i]->spec.launch(steps[i]->ctx);
+  hipGraph_t graph = nullptr;
+  const hipError_t end = hipStreamEndCapture(rt->stream, &graph);
+  if (rc) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return 1;
+  }
+  if (hip_ok(end, "end capture")) return 1;
+  seq->graph = graph;
+  if (hip_ok(hipGraphInstantiate(&seq->exec, graph, nullptr, nullptr, 0), "graph instantiate")) {
+    (void)hipGraphDestroy(graph);
+    return 1;
+  }
+  *out = seq.release();
+  return 0;
+}
+
+extern "C" int tmc_seq_launch(tmc_seq* seq) {
+  clear_error();
+  if (!seq) return fail("tmc_seq_launch: null sequence.");
+  if (consume_failure(seq->rt)) return 1;
+  return hip_ok(hipGraphLaunch(seq->exec, seq->rt->stream), "graph launch");
+}
+
+extern "C" int tmc_seq_run(tmc_seq* seq, double* gpu_us, double* cpu_us) {
+  clear_error();
+  if (!seq) return fail("tmc_seq_run: null sequence.");
+  tmc_runtime* rt = seq->rt;
+  if (consume_failure(rt)) return 1;
+  hipEvent_t start = nullptr, stop = nullptr;
+  if (gpu_us) {
+    if (hip_ok(hipEventCreate(&start), "event") || hip_ok(hipEventCreate(&stop), "event")) return 1;
+    (void)hipEventRecord(start, rt->stream);
+  }
+  const auto t0 = std::chrono::steady_clock::now();
+  int rc = hip_ok(hipGraphLaunch(seq->exec, rt->stream), "graph launch");
+  if (gpu_us) (void)hipEventRecord(stop, rt->stream);
+  const hipError_t sync = hipStreamSynchronize(rt->stream);
+  const auto t1 = std::chrono::steady_clock::now();
+  if (!rc && sync != hipSuccess) rc = hip_ok(sync, "sequence execution");
+  if (cpu_us) *cpu_us = std::chrono::duration<double, std::micro>(t1 - t0).count();
+  if (gpu_us) {
+    float ms = 0.0f;
+    *gpu_us = (!rc && hipEventElapsedTime(&ms, start, stop) == hipSuccess) ? ms * 1000.0 : -1.0;
+    (void)hipEventDestroy(start);
+    (void)hipEventDestroy(stop);
+  }
+  return rc;
+}
+
+extern "C" void tmc_seq_release(tmc_seq* seq) {
+  if (!seq) return;
+  (void)hipStreamSynchronize(seq->rt->stream);
+  if (seq->exec) (void)hipGraphExecDestroy(seq->exec);
+  if (seq->graph) (void)hipGraphDestroy(seq->graph);
+  delete seq;
+}

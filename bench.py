@@ -1,0 +1,276 @@
+"""Benchmark of the gfx950 decode backend on one MI355X.
+
+Headline workload: the fused Llama decode MLP
+block at batch 1 — Add+RMSNorm (hidden 4096), gate/up projection with
+SiLU*Mul (intermediate 11008), down projection with fp32 output — with fp16
+weights ~N(0, 0.02).  One step = one pass of the block over one batch.
+`value` is the algorithmic HBM bytes of the block per step x steps / wall
+time (GB/s), with every input already resident in HBM.  Weights rotate over
+several distinct copies so that the 256 MB Infinity Cache cannot serve them.
+
+Printed JSON line extras:
+  roofline      the dominant kernel (gate/up + SiLU*Mul) timed alone with HIP
+                events on the launch stream: algorithmic bytes per launch /
+                average launch time, against the 8 TB/s HBM peak;
+  cpu_baseline  the CPU oracle (oracle/libtmc_oracle.so, a single-threaded
+                C restatement of the reference CPU path) on a bounded number
+                of whole blocks of the same workload;
+  extra         GB/s of the other BASELINE configs (C1 GEMV, C2 at B=8, C3
+                contiguous attention at L=4095, C4 paged GQA attention).
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "GEMV/paged-attn HBM GB/s (% of peak); decode tokens/s at batch 1 and 16"
+HIDDEN, INTER = 4096, 11008
+
+
+def load_tmc():
+    import importlib.util
+    name = "aicompiler_test_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    pkg = os.path.join(ROOT, "aicompiler-test_amd")
+    spec = importlib.util.spec_from_file_location(name, os.path.join(pkg, "__init__.py"),
+                                                  submodule_search_locations=[pkg])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def mlp_block_bytes(batch: int) -> dict:
+    """Algorithmic bytes of each kernel of the block (fp16 = 2 B, fp32 = 4 B)."""
+    h, i = HIDDEN, INTER
+    add_norm = batch * h * 2 * 4 + h * 2          # read h, r; write s, n; gamma
+    gate_up = 2 * i * h * 2 + batch * h * 2 + batch * i * 2
+    down = i * h * 2 + batch * i * 2 + batch * h * 4
+    return {"add_rmsnorm": add_norm, "gate_up_silu": gate_up, "down": down,
+            "total": add_norm + gate_up + down}
+
+
+class MlpBlock:
+    """Device buffers of the C2 block with `copies` rotating weight sets."""
+
+    def __init__(self, tmc, torch, batch: int, copies: int):
+        self.tmc, self.torch, self.batch, self.copies = tmc, torch, batch, copies
+        f16 = torch.float16
+        dev = "cuda"
+        self.h = torch.empty((batch, HIDDEN), dtype=f16, device=dev)
+        self.r = torch.empty((batch, HIDDEN), dtype=f16, device=dev)
+        tmc.fill_normal(self.h, 201)
+        tmc.fill_normal(self.r, 202)
+        self.weights = []
+        for c in range(copies):
+            gamma = torch.empty(HIDDEN, dtype=f16, device=dev)
+            # U(0.5, 1.5) is not needed bit-exactly: gamma ~ 1 + N(0, 0.25) clipped
+            tmc.fill_normal(gamma, 203 + 1000 * c, 1.0, 0.25)
+            gamma.clamp_(0.5, 1.5)
+            wg = torch.empty((INTER, HIDDEN), dtype=f16, device=dev)
+            wu = torch.empty((INTER, HIDDEN), dtype=f16, device=dev)
+            wd = torch.empty((HIDDEN, INTER), dtype=f16, device=dev)
+            tmc.fill_normal(wg, 204 + 1000 * c, 0.0, 0.02)
+            tmc.fill_normal(wu, 205 + 1000 * c, 0.0, 0.02)
+            tmc.fill_normal(wd, 206 + 1000 * c, 0.0, 0.02)
+            self.weights.append((gamma, wg, wu, wd))
+        self.s = torch.empty((batch, HIDDEN), dtype=f16, device=dev)
+        self.n = torch.empty((batch, HIDDEN), dtype=f16, device=dev)
+        self.g = torch.empty((batch, INTER), dtype=f16, device=dev)
+        self.y = torch.empty((batch, HIDDEN), dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+
+    def step(self, i: int) -> None:
+        gamma, wg, wu, wd = self.weights[i % self.copies]
+        t = self.tmc
+        t.add_rmsnorm(self.h, self.r, gamma, self.s, self.n, 1e-6)
+        t.gate_up_silu(self.n, wg, wu, self.g)
+        t.gemv(self.g, wd, self.y)
+
+
+def time_loop(torch, fn, iters: int) -> float:
+    """Seconds per iteration of fn(i), measured with events on the current stream."""
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(iters):
+        fn(i)
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / 1000.0 / iters
+
+
+def cpu_baseline(block: MlpBlock, seconds: float) -> dict:
+    """Whole C2 blocks on the CPU oracle (single thread) with the GPU's copy-0 data."""
+    import numpy as np
+    from oracle import oracle as orc
+    orc.build()
+    gamma, wg, wu, wd = block.weights[0]
+    as_bits = lambda t: t.detach().cpu().contiguous().numpy().view(np.uint16)  # noqa: E731
+    h, r, g16 = as_bits(block.h), as_bits(block.r), as_bits(gamma)
+    wg16, wu16, wd16 = as_bits(wg), as_bits(wu), as_bits(wd)
+    done, elapsed = 0, 0.0
+    t0 = time.perf_counter()
+    while done == 0 or elapsed < seconds:
+        _, n = orc.add_rmsnorm(h, r, g16, orc.F16, 1e-6)
+        n16 = orc.f16(n.astype(np.float32))  # storeValue: float cast, then fp16 (ties away)
+        gated = orc.gated_mlp(n16, wg16, wu16, orc.F16)
+        orc.linear(orc.f16(gated.astype(np.float32)), wd16, orc.F16)
+        done += 1
+        elapsed = time.perf_counter() - t0
+    total = mlp_block_bytes(block.batch)["total"] * done
+    return {"value": round(total / elapsed / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{done} whole C2 blocks (B={block.batch}) on oracle/libtmc_oracle.so, "
+                      f"{elapsed:.1f} s, 1 thread"}
+
+
+def extra_measurements(tmc, torch, iters: int) -> dict:
+    import numpy as np
+    out = {}
+    f16 = torch.float16
+    # C1: GEMV fp16 W[4096,4096] -> fp32 y, 8 rotating weight copies (256 MiB)
+    ws = [torch.empty((4096, 4096), dtype=f16, device="cuda") for _ in range(8)]
+    for c, w in enumerate(ws):
+        tmc.fill_normal(w, 103 + c, 0.0, 0.02)
+    x = torch.empty((1, 4096), dtype=f16, device="cuda")
+    tmc.fill_normal(x, 101)
+    y = torch.empty((1, 4096), dtype=torch.float32, device="cuda")
+    sec = time_loop(torch, lambda i: tmc.gemv(x, ws[i % 8], y), iters)
+    gemv_bytes = 4096 * 4096 * 2 + 4096 * 2 + 4096 * 4
+    out["c1_gemv_4096x4096_gbps"] = round(gemv_bytes / sec / 1e9, 1)
+    out["c1_gemv_us"] = round(sec * 1e6, 2)
+    del ws
+    # C2 at B=8
+    blk = MlpBlock(tmc, torch, 8, 4)
+    sec = time_loop(torch, blk.step, iters)
+    out["c2_mlp_block_b8_gbps"] = round(mlp_block_bytes(8)["total"] / sec / 1e9, 1)
+    del blk
+    # C3: contiguous attention, 32 heads x 128, capacity 4096, valid 4096 (L=4095 + 1)
+    heads, d, cap = 32, 128, 4096
+    copies = 4
+    ks = [torch.empty((1, heads, cap, d), dtype=f16, device="cuda") for _ in range(copies)]
+    vs = [torch.empty((1, heads, cap, d), dtype=f16, device="cuda") for _ in range(copies)]
+    for c in range(copies):
+        tmc.fill_normal(ks[c], 301 + 10 * c)
+        tmc.fill_normal(vs[c], 302 + 10 * c)
+    q = torch.empty((1, heads * d), dtype=f16, device="cuda")
+    tmc.fill_normal(q, 303)
+    o = torch.empty((1, heads * d), dtype=f16, device="cuda")
+    valid = torch.tensor([4096], dtype=torch.int32, device="cuda")
+    wsb = tmc.attention_workspace_bytes(1, heads, d, cap)
+    wsp = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device="cuda")
+    sec = time_loop(torch, lambda i: tmc.decode_attention(q, ks[i % copies], vs[i % copies], valid,
+                                                          o, 1, heads, heads, d, cap, wsp), iters)
+    c3_bytes = 2 * heads * 4096 * d * 2 + 2 * heads * d * 2
+    out["c3_attention_L4095_gbps"] = round(c3_bytes / sec / 1e9, 1)
+    del ks, vs
+    # C4: paged GQA attention, 16 requests, 32 q / 8 kv heads, pages of 16
+    batch, qh, kvh, p, pages, max_pages = 16, 32, 8, 16, 8192, 256
+    lengths = np.random.default_rng(403).integers(64, 4096, size=batch) + 1
+    perm = np.random.default_rng(404).permutation(pages).astype(np.int32)
+    need = (lengths + p - 1) // p
+    sets = []
+    cursor = 0
+    while cursor + need.sum() <= pages and len(sets) < 3:  # disjoint table sets rotate
+        t = np.full((batch, max_pages), -1, np.int32)
+        for i in range(batch):
+            t[i, :need[i]] = perm[cursor:cursor + need[i]]
+            cursor += need[i]
+        sets.append(torch.from_numpy(t).cuda())
+    kp = torch.empty((pages, kvh, p, d), dtype=f16, device="cuda")
+    vp = torch.empty((pages, kvh, p, d), dtype=f16, device="cuda")
+    tmc.fill_normal(kp, 401)
+    tmc.fill_normal(vp, 402)
+    qd = torch.empty((batch, qh * d), dtype=f16, device="cuda")
+    tmc.fill_normal(qd, 405)
+    od = torch.empty((batch, qh * d), dtype=f16, device="cuda")
+    vl = torch.from_numpy(lengths.astype(np.int32)).cuda()
+    active = torch.tensor([batch], dtype=torch.int32, device="cuda")
+    wsb = tmc.attention_workspace_bytes(batch, qh, d, max_pages * p)
+    wsp = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device="cuda")
+    sec = time_loop(torch, lambda i: tmc.paged_decode_attention(
+        qd, kp, vp, vl, sets[i % len(sets)], active, od, batch, qh, kvh, d, p, max_pages,
+        kvh * p * d, p * d, wsp), iters)
+    c4_bytes = int(lengths.sum()) * kvh * d * 2 * 2 + 4 * int(need.sum()) + 2 * batch * qh * d * 2
+    out["c4_paged_gqa_attention_gbps"] = round(c4_bytes / sec / 1e9, 1)
+    out["c4_paged_gqa_attention_us"] = round(sec * 1e6, 2)
+    out["c4_bytes"] = c4_bytes
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--copies", type=int, default=4)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(run with --gpus 1).", file=sys.stderr)
+        return 2
+
+    import torch
+    tmc = load_tmc()
+    tmc.lib()
+    block = MlpBlock(tmc, torch, args.batch, args.copies)
+    print(f"[bench] C2 block B={args.batch}, {args.copies} weight copies; warmup", flush=True)
+    for i in range(args.warmup):
+        block.step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        block.step(i)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    bytes_ = mlp_block_bytes(args.batch)
+    value = bytes_["total"] * args.steps / elapsed / 1e9
+    print(f"[bench] timed {args.steps} steps in {elapsed:.3f} s", flush=True)
+
+    # dominant kernel alone: gate/up + SiLU*Mul, rotating weight copies
+    sec = time_loop(torch, lambda i: tmc.gate_up_silu(block.n, block.weights[i % args.copies][1],
+                                                      block.weights[i % args.copies][2], block.g),
+                    args.steps)
+    achieved = bytes_["gate_up_silu"] / sec / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                "kernel": "gate_up_silu_kernel", "bytes_per_launch": bytes_["gate_up_silu"],
+                "avg_launch_us": round(sec * 1e6, 3)}
+    print(f"[bench] gate_up_silu {sec * 1e6:.2f} us/launch", flush=True)
+
+    extra = {} if args.no_extra else extra_measurements(tmc, torch, 200)
+    print("[bench] extras done", flush=True)
+    cpu = None if args.no_cpu else cpu_baseline(block, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "C2 fused decode MLP block: Add+RMSNorm -> gate/up+SiLU*Mul -> "
+                               "down (fp32 out); hidden 4096, intermediate 11008",
+                   "batch": args.batch, "weight_copies": args.copies, "accumulate": "f32",
+                   "bytes_per_step": bytes_["total"], "frac_of_hbm_peak":
+                       round(value / HBM_PEAK_GBPS, 4)},
+        "roofline": roofline, "cpu_baseline": cpu, "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

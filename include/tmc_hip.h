@@ -1,0 +1,265 @@
+/*
+ * tmc_hip.h — C ABI of the MI355X (gfx950) decode backend, libtmc_hip.so.
+ *
+ * This is the drop-in boundary for the reference's Metal backend
+ * (/root/reference/src/backend/metal): plain pointers and sizes, no C++ or
+ * torch types.  Every function returns 0 on success and a nonzero status on
+ * failure; the failure text is then available from tmc_last_error() (a
+ * thread-local string, the counterpart of the reference's
+ * `std::string errorMessage` results, MetalRuntime.hpp:33-44,74-77,91-99).
+ *
+ * Two layers:
+ *  1. Runtime objects (tmc_rt_*, tmc_buf_*, tmc_kernel_*, tmc_prepare,
+ *     tmc_exec_*, tmc_seq_*) replace MetalRuntime / MetalBuffer /
+ *     PreparedExecution / PreparedSequence (MetalRuntime.hpp:56-208).
+ *  2. Typed kernel entry points (tmc_gemv_f16 ... tmc_argmax_f32) replace the
+ *     MSL emitters of DecodeGEMVMetalEmitter / DecoderLLMMetalEmitter /
+ *     KVCacheMetalEmitter / TransformerDecodeMetalEmitter.  They take device
+ *     pointers, shapes and a hipStream_t passed as `void *stream` (NULL =
+ *     the default stream) and enqueue asynchronously.
+ *
+ * Storage dtype codes follow tensor::metal::ElementType (MetalRuntime.hpp:12).
+ * Weights are [out_features, in_features] row-major (nn.Linear layout, as in
+ * DecodeGEMVMetalEmitter.cpp:97-103).
+ */
+#ifndef TMC_HIP_H
+#define TMC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum tmc_dtype { TMC_F16 = 0, TMC_F32 = 1, TMC_BF16 = 2, TMC_I32 = 3 } tmc_dtype;
+
+/* Thread-local text of the last failure on this thread ("" when none). */
+const char *tmc_last_error(void);
+
+/* ===================================================================== */
+/* 1. Runtime objects                                                     */
+/* ===================================================================== */
+
+typedef struct tmc_runtime tmc_runtime;
+typedef struct tmc_buffer tmc_buffer;
+typedef struct tmc_kernel tmc_kernel;
+typedef struct tmc_exec tmc_exec;
+typedef struct tmc_seq tmc_seq;
+
+/* tensor::metal::HardwareInfo (MetalRuntime.hpp:14-19). */
+typedef struct tmc_hardware_info {
+  size_t max_threads_per_threadgroup;
+  size_t max_threadgroup_memory_length; /* LDS bytes per workgroup */
+  size_t max_buffer_length;
+  int supports_bfloat16;
+  int compute_units;
+  int wave_size;
+} tmc_hardware_info;
+
+/* MetalRuntime::MetalRuntime / ~MetalRuntime / isAvailable / deviceName /
+ * initializationError / hardwareInfo (MetalRuntime.hpp:151-166). */
+int tmc_rt_create(tmc_runtime **out);
+void tmc_rt_destroy(tmc_runtime *rt);
+int tmc_rt_is_available(const tmc_runtime *rt);
+const char *tmc_rt_device_name(const tmc_runtime *rt);
+const char *tmc_rt_init_error(const tmc_runtime *rt);
+int tmc_rt_device_info(const tmc_runtime *rt, tmc_hardware_info *info);
+/* The stream every prepared execution and sequence of this runtime uses. */
+void *tmc_rt_stream(const tmc_runtime *rt);
+
+/* MetalRuntime::createBuffer (MetalRuntime.hpp:186-188; .mm:515-561): host
+ * floats converted per dtype (fp16 ties away from zero, bf16 RNE, int32
+ * truncation); without data the buffer is filled with NaN (float types) or 0
+ * (int32). */
+int tmc_buf_create(tmc_runtime *rt, size_t count, int dtype, const float *init,
+                   tmc_buffer **out);
+/* Wrap existing device memory (not owned, never freed by the runtime). */
+int tmc_buf_wrap(tmc_runtime *rt, void *device_ptr, size_t count, int dtype, tmc_buffer **out);
+/* MetalRuntime::writeBuffer (MetalRuntime.hpp:189-192; .mm:563-592). */
+int tmc_buf_write(tmc_buffer *buf, const float *data, size_t count, size_t offset);
+/* Raw storage copies (no conversion); bytes/offsets in elements of the dtype. */
+int tmc_buf_write_raw(tmc_buffer *buf, const void *data, size_t count, size_t offset);
+int tmc_buf_read_raw(const tmc_buffer *buf, void *data, size_t count, size_t offset);
+/* MetalBuffer::read (MetalRuntime.hpp:66; .mm:171-186). */
+int tmc_buf_read(const tmc_buffer *buf, float *out);
+size_t tmc_buf_count(const tmc_buffer *buf);
+int tmc_buf_dtype(const tmc_buffer *buf);
+void *tmc_buf_device_ptr(const tmc_buffer *buf);
+void tmc_buf_release(tmc_buffer *buf);
+
+/* Replaces MetalRuntime::createComputePipeline(source, functionName)
+ * (MetalRuntime.hpp:168-170; .mm:397-513).  `key` names a built-in gfx950
+ * kernel and its specialization as "name?k=v&k=v" (the string an emitter
+ * returns in GeneratedKernel::source, MetalEmitter.hpp:13-18).  On success
+ * `*bindings` receives the binding count and `types`/`writable` (each of
+ * length >= 32) describe every buffer binding in ABI order: inputs, outputs,
+ * then an optional uint32 constants binding (type TMC_I32, writable 0). */
+int tmc_kernel_resolve(tmc_runtime *rt, const char *key, tmc_kernel **out, int *bindings,
+                       int *types, int *writable);
+/* Grid the resolved kernel needs (DispatchSize, MetalRuntime.hpp:87-90). */
+int tmc_kernel_dispatch(const tmc_kernel *kernel, size_t *groups, size_t *threads);
+void tmc_kernel_release(tmc_kernel *kernel);
+
+/* MetalRuntime::prepareBuffers (MetalRuntime.hpp:193-201; .mm:594-648):
+ * inputs [0,n_in), outputs [n_in, n_in+n_out), u32 constants last.  Outputs
+ * must be distinct and must not alias inputs; at most 31 bindings and 1024
+ * constants. */
+int tmc_prepare(tmc_runtime *rt, const tmc_kernel *kernel, tmc_buffer *const *inputs,
+                size_t n_in, tmc_buffer *const *outputs, size_t n_out, size_t groups,
+                size_t threads, const uint32_t *constants, size_t n_constants, tmc_exec **out);
+/* PreparedExecution::run / execute (MetalRuntime.hpp:110-115): with
+ * `reset_outputs` the outputs are first filled with sentinels (NaN, 0x7e00,
+ * 0x7fc0, INT32_MIN; .mm:200-215).  Synchronous; times are optional outputs
+ * (gpu_us from hipEvents, cpu_us from submit to completion). */
+int tmc_exec_run(tmc_exec *exec, int reset_outputs, double *gpu_us, double *cpu_us);
+void tmc_exec_release(tmc_exec *exec);
+
+/* MetalRuntime::prepareSequence / PreparedSequence::execute
+ * (MetalRuntime.hpp:130-142,202-203; .mm:292-341,751-781): the steps are
+ * captured once into a HIP graph and replayed with one hipGraphLaunch. */
+int tmc_seq_create(tmc_runtime *rt, tmc_exec *const *steps, size_t n, tmc_seq **out);
+int tmc_seq_run(tmc_seq *seq, double *gpu_us, double *cpu_us);
+/* Enqueue one replay on the runtime stream without waiting. */
+int tmc_seq_launch(tmc_seq *seq);
+void tmc_seq_release(tmc_seq *seq);
+
+/* Test hook: make the next `count` executions (exec or sequence) fail before
+ * they launch, so host rollback paths can be exercised without a GPU fault. */
+void tmc_rt_fail_next(tmc_runtime *rt, int count);
+
+/* ===================================================================== */
+/* 2. Typed kernel entry points                                           */
+/* ===================================================================== */
+
+/* Decode GEMV, emitDecodeGEMV (DecodeGEMVMetalEmitter.cpp:68-132):
+ * y[r,n] = sum_k x[r,k] * W[n,k] with fp16 x and W, fp32 accumulation, y in
+ * y_dtype (TMC_F16 or TMC_F32).  batch <= 8 runs the wave64 split-K GEMV;
+ * larger batches run the MFMA skinny GEMM. */
+int tmc_gemv_f16(const void *x, const void *w, void *y, int y_dtype, int64_t batch,
+                 int64_t in_features, int64_t out_features, void *stream);
+
+/* Skinny GEMM with fp16 MFMA (v_mfma_f32_16x16x32_f16), any batch >= 1;
+ * same semantics as tmc_gemv_f16.  No reference counterpart: the reference
+ * batched decode runs emitDecodeGEMV per row (ServingRuntime.cpp:281-291). */
+int tmc_skinny_gemm_f16_mfma(const void *x, const void *w, void *y, int y_dtype,
+                             int64_t batch, int64_t in_features, int64_t out_features,
+                             void *stream);
+
+/* Gated MLP, emitDecoderGatedMLP (DecoderLLMMetalEmitter.cpp:479-536):
+ * out[r,f] = h(h(silu(h(g))) * h(u)) with g = x.Wg[f], u = x.Wu[f] and h()
+ * the fp16 rounding; Wg, Wu are [intermediate, hidden]. */
+int tmc_gate_up_silu_f16(const void *x, const void *w_gate, const void *w_up, void *out,
+                         int64_t batch, int64_t hidden, int64_t intermediate, void *stream);
+
+/* emitDecoderRMSNorm (DecoderLLMMetalEmitter.cpp:63-108) / emitRMSNorm
+ * (MetalEmitter.cpp:12-76): y = x * rsqrt(mean(x^2) + eps) * w, fp32
+ * reduction, dtype TMC_F16 or TMC_F32 for x, w, y. */
+int tmc_rmsnorm(const void *x, const void *w, void *y, int dtype, int64_t rows, int64_t width,
+                float epsilon, void *stream);
+
+/* emitDecoderResidualRMSNorm (DecoderLLMMetalEmitter.cpp:417-477):
+ * s = h(r + u) written to sum_out, n = h(s * rsqrt(mean(s^2)+eps) * w). */
+int tmc_add_rmsnorm(const void *residual, const void *update, const void *w, void *sum_out,
+                    void *norm_out, int dtype, int64_t rows, int64_t width, float epsilon,
+                    void *stream);
+
+/* emitDecoderSiLUMul (DecoderLLMMetalEmitter.cpp:395-415):
+ * out = h(h(g / (1 + exp(-g))) * u). */
+int tmc_silu_mul(const void *gate, const void *up, void *out, int dtype, int64_t count,
+                 void *stream);
+
+/* emitDecoderAdd (DecoderLLMMetalEmitter.cpp:375-393): out = h(a + b). */
+int tmc_add(const void *a, const void *b, void *out, int dtype, int64_t count, void *stream);
+
+/* emitDecoderEmbedding (DecoderLLMMetalEmitter.cpp:35-61): out[r] =
+ * table[token[r]]; an out-of-range token leaves its row untouched. */
+int tmc_embedding(const int32_t *tokens, const void *table, void *out, int dtype, int64_t rows,
+                  int64_t hidden, int64_t vocabulary, void *stream);
+
+/* emitDecoderRoPE (DecoderLLMMetalEmitter.cpp:110-158): x token-major
+ * [batch, seq, heads*D], fp32 tables [capacity, D/2], position
+ * valid - seq + t with valid read from valid_length[0]; out head-major
+ * [batch, heads, seq, D].  valid < seq or valid > capacity: no-op. */
+int tmc_rope(const void *x, const float *cosine, const float *sine,
+             const int32_t *valid_length, void *out, int dtype, int64_t batch, int64_t seq,
+             int64_t heads, int64_t head_dim, int64_t capacity, void *stream);
+
+/* emitServingRoPE (DecoderLLMMetalEmitter.cpp:260-312): one token per
+ * request, position valid_lengths[r] - 1, requests >= active_count[0] and
+ * invalid lengths skipped; out [max_batch, heads, D]. */
+int tmc_serving_rope(const void *x, const float *cosine, const float *sine,
+                     const int32_t *valid_lengths, const int32_t *active_count, void *out,
+                     int dtype, int64_t max_batch, int64_t heads, int64_t head_dim,
+                     int64_t capacity, void *stream);
+
+/* emitDecoderCacheAppend (DecoderLLMMetalEmitter.cpp:160-203): bit copy of
+ * seq tokens into a contiguous cache [batch, heads, capacity, D] at
+ * positions valid-seq..valid-1. `head_major` selects the input layout. */
+int tmc_kv_append(const void *input, const int32_t *valid_length, void *cache, int dtype,
+                  int64_t batch, int64_t seq, int64_t heads, int64_t head_dim, int64_t capacity,
+                  int head_major, void *stream);
+
+/* emitDecoderPagedCacheAppend (DecoderLLMMetalEmitter.cpp:205-258): cache
+ * pages [page][batch][heads][page_size][D] through block_table[pos/page]. */
+int tmc_paged_kv_append(const void *input, const int32_t *valid_length,
+                        const int32_t *block_table, void *cache, int dtype, int64_t batch,
+                        int64_t seq, int64_t heads, int64_t head_dim, int64_t capacity,
+                        int64_t page_size, int head_major, void *stream);
+
+/* emitServingPagedCacheAppend (DecoderLLMMetalEmitter.cpp:314-373): one
+ * token per request into pool pages [page][heads][page_size][D] through
+ * block_tables[r*max_pages + pos/page]. */
+int tmc_serving_kv_append(const void *input, const int32_t *valid_lengths,
+                          const int32_t *block_tables, const int32_t *active_count, void *cache,
+                          int dtype, int64_t max_batch, int64_t heads, int64_t head_dim,
+                          int64_t capacity, int64_t page_size, int head_major, void *stream);
+
+/* Bytes of device workspace the split-KV attention needs for these limits
+ * (0 when a single split covers `capacity`). */
+size_t tmc_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_dim,
+                                     int64_t capacity);
+
+/* Decode attention over a contiguous cache (emitKVAttention,
+ * KVCacheMetalEmitter.cpp:119-208, queryLength 1): caches
+ * [batch, kv_heads, capacity, D], q [batch, q_heads, D], out
+ * [batch, q_heads*D]; attends [0, valid_length[0]); query head h reads kv
+ * head h / (q_heads/kv_heads).  valid < 1 or > capacity: no-op. */
+int tmc_decode_attention(const void *q, const void *key_cache, const void *value_cache,
+                         const int32_t *valid_length, void *out, int dtype, int64_t batch,
+                         int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t capacity,
+                         void *workspace, size_t workspace_bytes, void *stream);
+
+/* Paged decode attention (emitServingPagedKVAttention,
+ * KVCacheMetalEmitter.cpp:312-406, generalised to GQA): element
+ * (page, kvh, offset, d) at page*page_stride + kvh*head_stride +
+ * offset*D + d; request r attends [0, valid_lengths[r]) through
+ * block_tables[r*max_pages + pos/page_size].  Requests >= active_count[0]
+ * (active_count may be NULL = all), invalid lengths, or a negative page in
+ * range leave their output untouched. */
+int tmc_paged_decode_attention(const void *q, const void *key_pool, const void *value_pool,
+                               const int32_t *valid_lengths, const int32_t *block_tables,
+                               const int32_t *active_count, void *out, int dtype,
+                               int64_t max_batch, int64_t q_heads, int64_t kv_heads,
+                               int64_t head_dim, int64_t page_size, int64_t max_pages,
+                               int64_t page_stride, int64_t head_stride, void *workspace,
+                               size_t workspace_bytes, void *stream);
+
+/* emitTokenArgmax (TransformerDecodeMetalEmitter.cpp:198-256): greedy token
+ * per row over fp32 logits, ties to the lowest index. */
+int tmc_argmax_f32(const float *logits, int32_t *tokens, int64_t rows, int64_t vocabulary,
+                   void *stream);
+
+/* Synthetic data: fill `count` elements with N(mean, std) values from a
+ * counter-based generator (splitmix64 + Box-Muller) keyed by `seed`. */
+int tmc_fill_normal(void *ptr, int dtype, int64_t count, uint64_t seed, float mean, float std,
+                    void *stream);
+
+/* Plain device copy kernel (bandwidth probe used to calibrate counters). */
+int tmc_copy_bytes(const void *src, void *dst, size_t bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TMC_HIP_H */

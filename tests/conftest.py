@@ -25,3 +25,31 @@ def golden():
     path = os.path.join(ROOT, "tests", "golden", "golden.npz")
     with np.load(path, allow_pickle=False) as data:
         return {k: data[k] for k in data.files}
+
+
+def load_tmc():
+    """Import the backend package (its directory name is not a Python identifier)."""
+    import importlib.util
+    name = "aicompiler_test_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    pkg_dir = os.path.join(ROOT, "aicompiler-test_amd")
+    spec = importlib.util.spec_from_file_location(
+        name, os.path.join(pkg_dir, "__init__.py"), submodule_search_locations=[pkg_dir])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+@pytest.fixture(scope="session")
+def tmc():
+    return load_tmc()
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    # Name the case before any GPU work so a crash log identifies it.
+    if request.node.get_closest_marker("gpu"):
+        print(f"\n[gpu-case] {request.node.nodeid}", flush=True)
+    yield

@@ -1,0 +1,54 @@
+"""CPU checks of the boundary: the built library loads and exports every
+function include/tmc_hip.h declares; argument validation fails loudly
+before touching a device."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    text = open(os.path.join(ROOT, "include", "tmc_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"\b(tmc_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for required in ("tmc_gemv_f16", "tmc_skinny_gemm_f16_mfma", "tmc_rmsnorm", "tmc_add_rmsnorm",
+                     "tmc_silu_mul", "tmc_gate_up_silu_f16", "tmc_kv_append", "tmc_paged_kv_append",
+                     "tmc_decode_attention", "tmc_paged_decode_attention", "tmc_rt_create",
+                     "tmc_buf_create", "tmc_kernel_resolve", "tmc_prepare", "tmc_exec_run",
+                     "tmc_seq_create", "tmc_seq_run", "tmc_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(tmc):
+    lib = tmc.lib()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"missing exports: {missing}"
+
+
+def test_argument_validation_fails_before_device_work(tmc):
+    lib = tmc.lib()
+    assert lib.tmc_gemv_f16(None, None, None, 1, 1, 8, 8, None) != 0
+    assert "null" in tmc.last_error()
+    assert lib.tmc_rmsnorm(C.c_void_p(16), C.c_void_p(16), C.c_void_p(16), 1, 1, 8, -1.0, None) != 0
+    assert "epsilon" in tmc.last_error()
+    assert lib.tmc_decode_attention(C.c_void_p(16), C.c_void_p(16), C.c_void_p(16),
+                                    C.c_void_p(16), C.c_void_p(16), 0, 1, 32, 8, 96, 64, None, 0,
+                                    None) != 0
+    assert "head_dim" in tmc.last_error()
+    with pytest.raises(tmc.TmcError):
+        tmc.check(lib.tmc_silu_mul(None, None, None, 0, 4, None), "silu")
+
+
+def test_attention_workspace_sizes(tmc):
+    # one split covers 256 positions at D=128: no workspace
+    assert tmc.attention_workspace_bytes(16, 32, 128, 256) == 0
+    # C4: 16 requests x 32 heads x 16 splits x (128 + 2) floats
+    assert tmc.attention_workspace_bytes(16, 32, 128, 4096) == 16 * 32 * 16 * 130 * 4

@@ -1,0 +1,402 @@
+"""GPU parity: every gfx950 kernel entry point against the CPU oracle on the
+same seeded inputs, at BASELINE.json sizes where the oracle finishes in
+seconds.  Calls go through the C ABI (libtmc_hip.so via ctypes)."""
+import numpy as np
+import pytest
+
+from tests.helpers import (F16, F32, assert_f16_path, assert_f32_rel, bits, dev, dev_f16, normal,
+                           uniform, values)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    assert t.cuda.is_available(), "GPU tests need a GPU"
+    return t
+
+
+# ---------------------------------------------------------------- config 1
+def test_c1_rmsnorm_then_linear(tmc, orc, torch):
+    """RMSNorm fp32 [1,4096] -> host fp16 cast -> GEMV fp16 W[4096,4096] -> fp32 y."""
+    x = normal(101, (1, 4096))
+    gamma = uniform(102, (4096,), 0.5, 1.5)
+    w = orc.f16(normal(103, (4096, 4096), 0.02))
+    xd, gd = dev(x), dev(gamma)
+    yd = torch.empty_like(xd)
+    tmc.rmsnorm(xd, gd, yd, 1e-6)
+    torch.cuda.synchronize()
+    ref_norm = orc.rmsnorm(x, gamma, F32, 1e-6)
+    assert_f32_rel(values(yd), ref_norm, what="rmsnorm fp32")
+    xh = orc.f16(values(yd))  # the host cast between the two graphs (ties away)
+    out = torch.empty((1, 4096), dtype=torch.float32, device="cuda")
+    tmc.gemv(dev_f16(xh), dev_f16(w), out)
+    torch.cuda.synchronize()
+    assert_f32_rel(values(out), orc.linear(xh, w, F16), what="gemv fp32 out")
+
+
+@pytest.mark.parametrize("rows,width", [(3, 4097), (1, 4096), (2, 1), (5, 257)])
+def test_rmsnorm_fp32_ragged_zero_and_tiny_rows(tmc, orc, torch, rows, width):
+    x = normal(104, (rows, width))
+    if rows > 1:
+        x[0] = 0.0
+        x[1] *= 1e-4
+    gamma = uniform(105, (width,), 0.5, 1.5)
+    y = torch.empty((rows, width), dtype=torch.float32, device="cuda")
+    tmc.rmsnorm(dev(x), dev(gamma), y, 1e-6)
+    torch.cuda.synchronize()
+    assert_f32_rel(values(y), orc.rmsnorm(x, gamma, F32, 1e-6), what=f"rmsnorm {rows}x{width}")
+
+
+@pytest.mark.parametrize("rows,width", [(1, 4096), (16, 4096), (1, 257)])
+def test_rmsnorm_fp16(tmc, orc, torch, rows, width):
+    x = orc.f16(normal(106, (rows, width)))
+    gamma = orc.f16(uniform(107, (width,), 0.5, 1.5))
+    y = torch.empty((rows, width), dtype=torch.float16, device="cuda")
+    tmc.rmsnorm(dev_f16(x), dev_f16(gamma), y, 1e-6)
+    torch.cuda.synchronize()
+    assert_f16_path(values(y), orc.rmsnorm(x, gamma, F16, 1e-6), what="rmsnorm fp16")
+
+
+# ---------------------------------------------------------------- GEMV family
+@pytest.mark.parametrize("batch,k,n,out_dtype", [
+    (1, 4096, 4096, F32), (1, 4096, 4096, F16), (2, 4096, 1024, F16), (3, 11008, 512, F32),
+    (8, 4096, 4096, F16), (1, 4096, 32000, F32), (1, 11008, 4096, F32), (4, 136, 72, F32),
+])
+def test_gemv_fma_path(tmc, orc, torch, batch, k, n, out_dtype):
+    x = orc.f16(normal(201, (batch, k)))
+    w = orc.f16(normal(202, (n, k), 0.02))
+    y = torch.empty((batch, n), dtype=torch.float32 if out_dtype == F32 else torch.float16,
+                    device="cuda")
+    tmc.gemv(dev_f16(x), dev_f16(w), y)
+    torch.cuda.synchronize()
+    ref = orc.linear(x, w, F16)
+    if out_dtype == F32:
+        assert_f32_rel(values(y), ref, what=f"gemv b{batch} k{k} n{n}")
+    else:
+        assert_f16_path(values(y), ref, what=f"gemv b{batch} k{k} n{n}")
+
+
+@pytest.mark.parametrize("batch,k,n,out_dtype", [
+    (16, 4096, 4096, F32), (16, 11008, 4096, F16), (9, 4096, 1000, F32), (33, 256, 72, F32),
+    (64, 512, 48, F16), (1, 4096, 256, F32), (100, 128, 40, F32),
+])
+def test_skinny_gemm_mfma(tmc, orc, torch, batch, k, n, out_dtype):
+    x = orc.f16(normal(203, (batch, k)))
+    w = orc.f16(normal(204, (n, k), 0.02))
+    y = torch.empty((batch, n), dtype=torch.float32 if out_dtype == F32 else torch.float16,
+                    device="cuda")
+    tmc.skinny_gemm(dev_f16(x), dev_f16(w), y)
+    torch.cuda.synchronize()
+    ref = orc.linear(x, w, F16)
+    if out_dtype == F32:
+        assert_f32_rel(values(y), ref, what=f"mfma b{batch} k{k} n{n}")
+    else:
+        assert_f16_path(values(y), ref, what=f"mfma b{batch} k{k} n{n}")
+
+
+def test_gemv_unaligned_k_generic_path(tmc, orc, torch):
+    x = orc.f16(normal(205, (2, 4097)))
+    w = orc.f16(normal(206, (33, 4097), 0.02))
+    y = torch.empty((2, 33), dtype=torch.float32, device="cuda")
+    tmc.gemv(dev_f16(x), dev_f16(w), y)
+    torch.cuda.synchronize()
+    assert_f32_rel(values(y), orc.linear(x, w, F16), what="generic gemv")
+
+
+def test_gemv_rejects_bad_arguments(tmc, torch):
+    x = torch.zeros((1, 8), dtype=torch.float16, device="cuda")
+    with pytest.raises(tmc.TmcError):
+        tmc.gemv(x, x, torch.zeros((1, 1), dtype=torch.int32, device="cuda"))
+
+
+# ---------------------------------------------------------------- config 2
+@pytest.mark.parametrize("batch", [1, 8])
+def test_c2_fused_mlp_block(tmc, orc, torch, batch):
+    h_, inter = 4096, 11008
+    h = orc.f16(normal(201, (batch, h_)))
+    r = orc.f16(normal(202, (batch, h_)))
+    gamma = orc.f16(uniform(203, (h_,), 0.5, 1.5))
+    wg = orc.f16(normal(204, (inter, h_), 0.02))
+    wu = orc.f16(normal(205, (inter, h_), 0.02))
+    wd = orc.f16(normal(206, (h_, inter), 0.02))
+    s_d = torch.empty((batch, h_), dtype=torch.float16, device="cuda")
+    n_d = torch.empty_like(s_d)
+    g_d = torch.empty((batch, inter), dtype=torch.float16, device="cuda")
+    y_d = torch.empty((batch, h_), dtype=torch.float32, device="cuda")
+    tmc.add_rmsnorm(dev_f16(h), dev_f16(r), dev_f16(gamma), s_d, n_d, 1e-6)
+    tmc.gate_up_silu(n_d, dev_f16(wg), dev_f16(wu), g_d)
+    tmc.gemv(g_d, dev_f16(wd), y_d)
+    torch.cuda.synchronize()
+    # stage by stage on the GPU's own stage inputs
+    s_ref, n_ref = orc.add_rmsnorm(h, r, gamma, F16, 1e-6)
+    assert_f16_path(values(s_d), s_ref, what="residual sum")
+    assert_f16_path(values(n_d), n_ref, what="add+rmsnorm")
+    assert_f16_path(values(g_d), orc.gated_mlp(bits(n_d), wg, wu, F16), what="gate/up silu")
+    assert_f32_rel(values(y_d), orc.linear(bits(g_d), wd, F16), what="down fp32")
+    # end to end against the oracle chain
+    n_chain = orc.f16(orc.store(n_ref, F16))
+    g_chain = orc.f16(orc.store(orc.gated_mlp(n_chain, wg, wu, F16), F16))
+    assert_f16_path(values(y_d), orc.linear(g_chain, wd, F16), what="mlp block end to end")
+
+
+def test_gate_up_silu_batches_and_generic(tmc, orc, torch):
+    for batch, hidden, inter in ((3, 256, 200), (16, 512, 64), (2, 100, 30)):
+        x = orc.f16(normal(207, (batch, hidden)))
+        wg = orc.f16(normal(208, (inter, hidden), 0.1))
+        wu = orc.f16(normal(209, (inter, hidden), 0.1))
+        out = torch.empty((batch, inter), dtype=torch.float16, device="cuda")
+        tmc.gate_up_silu(dev_f16(x), dev_f16(wg), dev_f16(wu), out)
+        torch.cuda.synchronize()
+        assert_f16_path(values(out), orc.gated_mlp(x, wg, wu, F16),
+                        what=f"gated mlp {batch}x{hidden}x{inter}")
+
+
+def test_silu_mul_and_add(tmc, orc, torch):
+    g = orc.f16(normal(210, (3, 11008)) * 4)
+    u = orc.f16(normal(211, (3, 11008)))
+    out = torch.empty((3, 11008), dtype=torch.float16, device="cuda")
+    tmc.silu_mul(dev_f16(g), dev_f16(u), out)
+    torch.cuda.synchronize()
+    assert_f16_path(values(out), orc.silu_mul(g, u, F16), what="silu_mul fp16")
+    g32, u32 = normal(212, (4097,)) * 8, normal(213, (4097,))
+    o32 = torch.empty(4097, dtype=torch.float32, device="cuda")
+    tmc.silu_mul(dev(g32), dev(u32), o32)
+    s = torch.empty(4097, dtype=torch.float32, device="cuda")
+    tmc.add(dev(g32), dev(u32), s)
+    torch.cuda.synchronize()
+    assert_f32_rel(values(o32), orc.silu_mul(g32, u32, F32), what="silu_mul fp32")
+    assert np.array_equal(values(s), (g32 + u32).astype(np.float32))
+
+
+# ---------------------------------------------------------------- appends
+@pytest.mark.parametrize("length", [128, 1024, 4095])
+def test_c3_contiguous_append_bit_exact(tmc, orc, torch, length):
+    heads, d, cap = 32, 128, 4096
+    cache = orc.f16(normal(301, (1, heads, cap, d)))
+    new = orc.f16(normal(304, (1, heads * d)))
+    cache_d = dev_f16(cache)
+    valid = torch.tensor([length + 1], dtype=torch.int32, device="cuda")
+    tmc.kv_append(dev_f16(new), valid, cache_d, 1, 1, heads, d, cap, False)
+    torch.cuda.synchronize()
+    expect = orc.append_contiguous(new, cache.ravel(), 1, heads, d, 1, cap, False, length + 1)
+    assert np.array_equal(bits(cache_d).ravel(), expect)
+
+
+def test_append_rejects_out_of_range_valid(tmc, orc, torch):
+    heads, d, cap = 4, 16, 8
+    cache = orc.f16(normal(305, (1, heads, cap, d)))
+    cache_d = dev_f16(cache)
+    for bad in (0, cap + 1):
+        valid = torch.tensor([bad], dtype=torch.int32, device="cuda")
+        tmc.kv_append(dev_f16(orc.f16(normal(306, (1, heads * d)))), valid, cache_d, 1, 1, heads,
+                      d, cap, False)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(cache_d), cache)
+
+
+def test_paged_and_serving_append_bit_exact(tmc, orc, torch):
+    heads, d, p, seq = 4, 32, 4, 3
+    cap = 16
+    table = np.array([2, 0, 3, 1], np.int32)
+    pool = orc.f16(normal(307, (4 * heads * p * d,)))
+    new = orc.f16(normal(308, (1, seq * heads * d)))
+    pool_d = dev_f16(pool)
+    valid = torch.tensor([7], dtype=torch.int32, device="cuda")
+    tmc.paged_kv_append(dev_f16(new), valid, dev(table), pool_d, 1, seq, heads, d, cap, p, False)
+    torch.cuda.synchronize()
+    expect = orc.append_paged(new, pool, 1, heads, d, seq, cap, p, False, 7, table)
+    assert np.array_equal(bits(pool_d), expect)
+    # serving layout [page][heads][page][D], 3 active of 4 rows, one invalid
+    max_b, max_pages = 4, cap // p
+    tables = np.array([[5, 1, -1, -1], [0, 2, 7, -1], [3, -1, -1, -1], [6, 4, -1, -1]], np.int32)
+    lengths = np.array([6, 9, 0, 8], np.int32)
+    pool2 = orc.f16(normal(309, (8 * heads * p * d,)))
+    new2 = orc.f16(normal(310, (max_b, heads * d)))
+    pool2_d = dev_f16(pool2)
+    active = torch.tensor([3], dtype=torch.int32, device="cuda")
+    tmc.serving_kv_append(dev_f16(new2), dev(lengths), dev(tables), active, pool2_d, max_b, heads,
+                          d, cap, p, True)
+    torch.cuda.synchronize()
+    expect2 = orc.append_serving(new2, pool2, max_b, heads, d, cap, p, True, lengths, tables, 3)
+    assert np.array_equal(bits(pool2_d), expect2)
+
+
+# ---------------------------------------------------------------- attention
+def _ws(tmc, torch, batch, qh, d, cap):
+    n = tmc.attention_workspace_bytes(batch, qh, d, cap)
+    return torch.empty(max(n // 4, 1), dtype=torch.float32, device="cuda") if n else None
+
+
+@pytest.mark.parametrize("length", [128, 1024, 4095])
+def test_c3_contiguous_decode_attention(tmc, orc, torch, length):
+    heads, d, cap = 32, 128, 4096
+    k = orc.f16(normal(301, (1, heads, cap, d)))
+    v = orc.f16(normal(302, (1, heads, cap, d)))
+    q = orc.f16(normal(303, (1, heads * d)))
+    nk = orc.f16(normal(304, (1, heads * d)))
+    nv = orc.f16(normal(305, (1, heads * d)))
+    k_d, v_d = dev_f16(k), dev_f16(v)
+    valid = torch.tensor([length + 1], dtype=torch.int32, device="cuda")
+    tmc.kv_append(dev_f16(nk), valid, k_d, 1, 1, heads, d, cap, False)
+    tmc.kv_append(dev_f16(nv), valid, v_d, 1, 1, heads, d, cap, False)
+    out = torch.full((1, heads * d), float("nan"), dtype=torch.float16, device="cuda")
+    tmc.decode_attention(dev_f16(q), k_d, v_d, valid, out, 1, heads, heads, d, cap,
+                         _ws(tmc, torch, 1, heads, d, cap))
+    torch.cuda.synchronize()
+    kk = orc.append_contiguous(nk, k.ravel(), 1, heads, d, 1, cap, False, length + 1)
+    vv = orc.append_contiguous(nv, v.ravel(), 1, heads, d, 1, cap, False, length + 1)
+    ref = orc.decode_attention(q, kk, vv, F16, heads, heads, d, cap, length + 1)
+    assert_f16_path(values(out), ref, what=f"contiguous attention L={length}")
+
+
+@pytest.mark.parametrize("valid,d,qh,kvh", [(1, 128, 32, 32), (256, 128, 8, 2), (257, 128, 8, 8),
+                                            (513, 64, 4, 1), (700, 16, 4, 4), (2049, 32, 8, 1)])
+def test_decode_attention_edges(tmc, orc, torch, valid, d, qh, kvh):
+    cap = 2304
+    b = 2
+    k = orc.f16(normal(311, (b, kvh, cap, d)))
+    v = orc.f16(normal(312, (b, kvh, cap, d)))
+    q = orc.f16(normal(313, (b, qh * d)) * 2)
+    out = torch.full((b, qh * d), float("nan"), dtype=torch.float16, device="cuda")
+    vl = torch.tensor([valid], dtype=torch.int32, device="cuda")
+    tmc.decode_attention(dev_f16(q), dev_f16(k), dev_f16(v), vl, out, b, qh, kvh, d, cap,
+                         _ws(tmc, torch, b, qh, d, cap))
+    torch.cuda.synchronize()
+    ref = orc.decode_attention(q, k, v, F16, qh, kvh, d, cap, valid)
+    assert_f16_path(values(out), ref, what=f"attention valid={valid} d={d} group={qh // kvh}")
+
+
+def _c4_inputs(orc, torch, batch=16, qh=32, kvh=8, d=128, p=16, pages=8192, max_pages=256):
+    # contexts U[64, 4095] so that the appended token keeps valid <= 4096
+    lengths = np.random.default_rng(403).integers(64, 4096, size=batch).astype(np.int32)
+    perm = np.random.default_rng(404).permutation(pages).astype(np.int32)
+    tables = np.full((batch, max_pages), -1, np.int32)
+    cursor = 0
+    for i, length in enumerate(lengths):
+        need = (int(length) + 1 + p - 1) // p  # room for the appended token
+        tables[i, :need] = perm[cursor:cursor + need]
+        cursor += need
+    k_pool = orc.f16(normal(401, (pages, kvh, p, d)))
+    v_pool = orc.f16(normal(402, (pages, kvh, p, d)))
+    q = orc.f16(normal(405, (batch, qh * d)))
+    return lengths, tables, k_pool, v_pool, q
+
+
+def test_c4_paged_gqa_attention(tmc, orc, torch):
+    batch, qh, kvh, d, p, pages, max_pages = 16, 32, 8, 128, 16, 8192, 256
+    lengths, tables, k_pool, v_pool, q = _c4_inputs(orc, torch)
+    nk = orc.f16(normal(406, (batch, kvh * d)))
+    nv = orc.f16(normal(407, (batch, kvh * d)))
+    k_d, v_d = dev_f16(k_pool), dev_f16(v_pool)
+    tables_d = dev(tables)
+    valid = lengths + 1
+    valid_d = dev(valid)
+    active = torch.tensor([batch], dtype=torch.int32, device="cuda")
+    cap = max_pages * p
+    tmc.serving_kv_append(dev_f16(nk), valid_d, tables_d, active, k_d, batch, kvh, d, cap, p, True)
+    tmc.serving_kv_append(dev_f16(nv), valid_d, tables_d, active, v_d, batch, kvh, d, cap, p, True)
+    out = torch.full((batch, qh * d), float("nan"), dtype=torch.float16, device="cuda")
+    tmc.paged_decode_attention(dev_f16(q), k_d, v_d, valid_d, tables_d, active, out, batch, qh,
+                               kvh, d, p, max_pages, kvh * p * d, p * d,
+                               _ws(tmc, torch, batch, qh, d, cap))
+    torch.cuda.synchronize()
+    kp = orc.append_serving(nk, k_pool.ravel(), batch, kvh, d, cap, p, True, valid, tables, batch)
+    vp = orc.append_serving(nv, v_pool.ravel(), batch, kvh, d, cap, p, True, valid, tables, batch)
+    assert np.array_equal(bits(k_d).ravel(), kp)
+    ref, written = orc.paged_attention(q, kp, vp, F16, qh, kvh, d, p, kvh * p * d, p * d, tables,
+                                       max_pages, valid, batch)
+    assert written.all()
+    assert_f16_path(values(out), ref, what="paged GQA attention (C4)")
+
+
+def test_paged_attention_inactive_and_bad_pages_untouched(tmc, orc, torch):
+    batch, qh, kvh, d, p, max_pages = 4, 8, 2, 64, 16, 8
+    pages = 32
+    k_pool = orc.f16(normal(410, (pages, kvh, p, d)))
+    v_pool = orc.f16(normal(411, (pages, kvh, p, d)))
+    q = orc.f16(normal(412, (batch, qh * d)))
+    tables = np.full((batch, max_pages), -1, np.int32)
+    tables[0, :3] = [4, 9, 1]
+    tables[1, :2] = [7, -1]  # hole inside the valid range
+    tables[2, :8] = np.arange(10, 18)
+    tables[3, :1] = [3]
+    lengths = np.array([40, 20, 128, 5], np.int32)
+    out = torch.full((batch, qh * d), float("nan"), dtype=torch.float16, device="cuda")
+    active = torch.tensor([3], dtype=torch.int32, device="cuda")
+    cap = max_pages * p
+    tmc.paged_decode_attention(dev_f16(q), dev_f16(k_pool), dev_f16(v_pool), dev(lengths),
+                               dev(tables), active, out, batch, qh, kvh, d, p, max_pages,
+                               kvh * p * d, p * d, _ws(tmc, torch, batch, qh, d, cap))
+    torch.cuda.synchronize()
+    got = values(out)
+    ref, written = orc.paged_attention(q, k_pool, v_pool, F16, qh, kvh, d, p, kvh * p * d, p * d,
+                                       tables, max_pages, lengths, 3)
+    assert list(written.all(axis=1)) == [True, False, True, False]
+    assert np.isnan(got[1]).all() and np.isnan(got[3]).all()
+    assert_f16_path(got[[0, 2]], ref[[0, 2]], what="paged attention written rows")
+
+
+# ---------------------------------------------------------------- rope / embedding / argmax
+def test_rope_decoder_and_serving(tmc, orc, torch):
+    heads, d, cap, seq, batch = 4, 16, 32, 3, 2
+    pairs = d // 2
+    pos = np.arange(cap)[:, None]
+    freq = np.exp(np.arange(0, d, 2) * (-np.log(10000.0) / d))
+    cos, sin = np.cos(pos * freq).astype(np.float32), np.sin(pos * freq).astype(np.float32)
+    x = orc.f16(normal(501, (batch, seq, heads * d)))
+    out = torch.empty((batch, heads, seq, d), dtype=torch.float16, device="cuda")
+    valid = 9
+    tmc.rope(dev_f16(x), dev(cos), dev(sin), torch.tensor([valid], dtype=torch.int32,
+                                                          device="cuda"),
+             out, batch, seq, heads, d, cap)
+    torch.cuda.synchronize()
+    positions = np.tile(np.arange(valid - seq, valid), batch)
+    ref = orc.rope(x.reshape(batch * seq, heads * d), cos, sin, F16, heads, d, positions)
+    ref = ref.reshape(batch, seq, heads, d).transpose(0, 2, 1, 3)
+    assert_f16_path(values(out), ref, what="decoder rope")
+    assert pairs == cos.shape[1]
+    # serving: one token per request at valid-1, inactive rows untouched
+    xs = orc.f16(normal(502, (4, heads * d)))
+    lengths = np.array([1, 30, 7, 5], np.int32)
+    outs = torch.full((4, heads * d), float("nan"), dtype=torch.float16, device="cuda")
+    tmc.serving_rope(dev_f16(xs), dev(cos), dev(sin), dev(lengths),
+                     torch.tensor([3], dtype=torch.int32, device="cuda"), outs, 4, heads, d, cap)
+    torch.cuda.synchronize()
+    refs = orc.rope(xs, cos, sin, F16, heads, d, lengths - 1)
+    got = values(outs)
+    assert_f16_path(got[:3], refs[:3], what="serving rope")
+    assert np.isnan(got[3]).all()
+
+
+def test_embedding_and_argmax(tmc, orc, torch):
+    vocab, hidden = 1000, 64
+    table = orc.f16(normal(601, (vocab, hidden)))
+    tokens = np.array([5, 999, -1, 1000, 0], np.int32)
+    out = torch.full((5, hidden), float("nan"), dtype=torch.float16, device="cuda")
+    tmc.embedding(dev(tokens), dev_f16(table), out)
+    torch.cuda.synchronize()
+    got = bits(out)
+    assert np.array_equal(got[[0, 1, 4]], table[[5, 999, 0]])
+    assert np.isnan(values(out)[[2, 3]]).all()
+    logits = normal(602, (4, 32000))
+    logits[1, 100] = logits[1, 31999] = 50.0  # tie -> lowest index
+    logits[2, :] = -np.inf
+    logits[3, 7] = np.nan
+    toks = torch.empty(4, dtype=torch.int32, device="cuda")
+    tmc.argmax(dev(logits), toks)
+    torch.cuda.synchronize()
+    assert list(toks.cpu().numpy()) == list(orc.argmax(logits))
+    assert toks.cpu().numpy()[1] == 100 and toks.cpu().numpy()[2] == 0
+
+
+def test_fill_normal_statistics(tmc, torch):
+    t = torch.empty(1 << 20, dtype=torch.float16, device="cuda")
+    tmc.fill_normal(t, 77, 0.0, 0.02)
+    u = torch.empty(1 << 20, dtype=torch.float16, device="cuda")
+    tmc.fill_normal(u, 77, 0.0, 0.02)
+    torch.cuda.synchronize()
+    a = values(t)
+    assert abs(a.mean()) < 1e-4 and abs(a.std() - 0.02) < 2e-4
+    assert np.array_equal(bits(t), bits(u))  # deterministic in the seed
