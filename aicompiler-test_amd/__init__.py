@@ -38,6 +38,9 @@ def _declare(l):
         "tmc_last_error": (C.c_char_p, []),
         "tmc_gemv_f16": (i32, [vp, vp, vp, i32, i64, i64, i64, vp]),
         "tmc_skinny_gemm_f16_mfma": (i32, [vp, vp, vp, i32, i64, i64, i64, vp]),
+        "tmc_gemv_f16_config": (i32, [vp, vp, vp, i32, i64, i64, i64, vp, vp]),
+        "tmc_gate_up_silu_f16_config": (i32, [vp, vp, vp, vp, i64, i64, i64, vp, vp]),
+        "tmc_gemv_default_config": (i32, [i64, i64, i64, i32, vp]),
         "tmc_gate_up_silu_f16": (i32, [vp, vp, vp, vp, i64, i64, i64, vp]),
         "tmc_rmsnorm": (i32, [vp, vp, vp, i32, i64, i64, f, vp]),
         "tmc_add_rmsnorm": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, f, vp]),
@@ -49,7 +52,7 @@ def _declare(l):
         "tmc_kv_append": (i32, [vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, vp]),
         "tmc_paged_kv_append": (i32, [vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, i32, vp]),
         "tmc_serving_kv_append": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, vp]),
-        "tmc_attention_workspace_bytes": (sz, [i64, i64, i64, i64]),
+        "tmc_attention_workspace_bytes": (sz, [i64, i64, i64, i64, i64]),
         "tmc_decode_attention": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, vp, sz,
                                        vp]),
         "tmc_paged_decode_attention": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64,
@@ -140,6 +143,37 @@ def gemv(x, w, y, stream=None):
           "tmc_gemv_f16")
 
 
+class GemvConfig(C.Structure):
+    """tmc_gemv_config (include/tmc_hip.h)."""
+    _fields_ = [("algorithm", C.c_int), ("rows_per_wave", C.c_int), ("unroll", C.c_int),
+                ("k_split", C.c_int)]
+
+    def astuple(self):
+        return (self.algorithm, self.rows_per_wave, self.unroll, self.k_split)
+
+
+def default_config(batch, in_features, out_features, gated=False) -> GemvConfig:
+    cfg = GemvConfig()
+    check(lib().tmc_gemv_default_config(batch, in_features, out_features, int(gated),
+                                        C.byref(cfg)), "tmc_gemv_default_config")
+    return cfg
+
+
+def gemv_config(x, w, y, cfg, stream=None):
+    b, k = x.shape
+    n = w.shape[0]
+    check(lib().tmc_gemv_f16_config(_ptr(x), _ptr(w), _ptr(y), _dtype_code(y), b, k, n,
+                                    C.byref(cfg), _stream(stream)), "tmc_gemv_f16_config")
+
+
+def gate_up_silu_config(x, wg, wu, out, cfg, stream=None):
+    b, h = x.shape
+    f = wg.shape[0]
+    check(lib().tmc_gate_up_silu_f16_config(_ptr(x), _ptr(wg), _ptr(wu), _ptr(out), b, h, f,
+                                            C.byref(cfg), _stream(stream)),
+          "tmc_gate_up_silu_f16_config")
+
+
 def skinny_gemm(x, w, y, stream=None):
     b, k = x.shape
     n = w.shape[0]
@@ -219,8 +253,8 @@ def serving_kv_append(inp, valid_lengths, tables, active, cache, max_batch, head
           "tmc_serving_kv_append")
 
 
-def attention_workspace_bytes(batch, q_heads, head_dim, capacity) -> int:
-    return int(lib().tmc_attention_workspace_bytes(batch, q_heads, head_dim, capacity))
+def attention_workspace_bytes(batch, q_heads, kv_heads, head_dim, capacity) -> int:
+    return int(lib().tmc_attention_workspace_bytes(batch, q_heads, kv_heads, head_dim, capacity))
 
 
 def decode_attention(q, k_cache, v_cache, valid_length, out, batch, q_heads, kv_heads, head_dim,
@@ -256,3 +290,183 @@ def fill_normal(t, seed, mean=0.0, std=1.0, stream=None):
 
 def copy_bytes(src, dst, nbytes, stream=None):
     check(lib().tmc_copy_bytes(_ptr(src), _ptr(dst), nbytes, _stream(stream)), "tmc_copy_bytes")
+
+
+# ---------------------------------------------------------------- runtime objects
+class Runtime:
+    """Python mirror of tensor::metal::MetalRuntime over the tmc_rt_* ABI
+    (MetalRuntime.hpp:149-208): buffers, kernel resolution, prepared
+    executions and HIP-graph sequences on the runtime's own stream."""
+
+    def __init__(self):
+        self._h = C.c_void_p()
+        check(lib().tmc_rt_create(C.byref(self._h)), "tmc_rt_create")
+
+    def close(self):
+        if self._h:
+            lib().tmc_rt_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self):
+        return self._h
+
+    def is_available(self) -> bool:
+        return bool(lib().tmc_rt_is_available(self._h))
+
+    def device_name(self) -> str:
+        return lib().tmc_rt_device_name(self._h).decode()
+
+    def initialization_error(self) -> str:
+        return lib().tmc_rt_init_error(self._h).decode()
+
+    def stream_handle(self) -> int:
+        return lib().tmc_rt_stream(self._h) or 0
+
+    def torch_stream(self):
+        import torch
+        return torch.cuda.ExternalStream(self.stream_handle())
+
+    def fail_next(self, count: int) -> None:
+        lib().tmc_rt_fail_next(self._h, count)
+
+    def create_buffer(self, count: int, dtype: int, data=None) -> "Buffer":
+        import numpy as np
+        h = C.c_void_p()
+        src = None
+        if data is not None:
+            src = np.ascontiguousarray(data, dtype=np.float32)
+            assert src.size == count
+        check(lib().tmc_buf_create(self._h, count, dtype,
+                                   None if src is None else src.ctypes.data_as(C.c_void_p),
+                                   C.byref(h)), "tmc_buf_create")
+        return Buffer(h, self)
+
+    def wrap(self, tensor) -> "Buffer":
+        h = C.c_void_p()
+        check(lib().tmc_buf_wrap(self._h, C.c_void_p(tensor.data_ptr()), tensor.numel(),
+                                 _dtype_code(tensor), C.byref(h)), "tmc_buf_wrap")
+        b = Buffer(h, self)
+        b._keep = tensor
+        return b
+
+    def resolve(self, key: str) -> "Kernel":
+        h = C.c_void_p()
+        n = C.c_int()
+        types = (C.c_int * 32)()
+        writable = (C.c_int * 32)()
+        check(lib().tmc_kernel_resolve(self._h, key.encode(), C.byref(h), C.byref(n), types,
+                                       writable), "tmc_kernel_resolve")
+        return Kernel(h, [types[i] for i in range(n.value)],
+                      [bool(writable[i]) for i in range(n.value)])
+
+    def prepare(self, kernel: "Kernel", inputs, outputs, constants=()) -> "Exec":
+        groups, threads = C.c_size_t(), C.c_size_t()
+        check(lib().tmc_kernel_dispatch(kernel.handle, C.byref(groups), C.byref(threads)),
+              "tmc_kernel_dispatch")
+        ins = (C.c_void_p * max(len(inputs), 1))(*[b.handle for b in inputs])
+        outs = (C.c_void_p * max(len(outputs), 1))(*[b.handle for b in outputs])
+        consts = (C.c_uint32 * max(len(constants), 1))(*constants)
+        h = C.c_void_p()
+        check(lib().tmc_prepare(self._h, kernel.handle, ins, len(inputs), outs, len(outputs),
+                                groups.value, threads.value, consts, len(constants),
+                                C.byref(h)), "tmc_prepare")
+        return Exec(h, list(inputs) + list(outputs))
+
+    def sequence(self, steps) -> "Sequence":
+        arr = (C.c_void_p * len(steps))(*[s.handle for s in steps])
+        h = C.c_void_p()
+        check(lib().tmc_seq_create(self._h, arr, len(steps), C.byref(h)), "tmc_seq_create")
+        return Sequence(h, list(steps))
+
+
+class Buffer:
+    def __init__(self, handle, rt):
+        self.handle, self.rt, self._keep = handle, rt, None
+
+    def __del__(self):
+        try:
+            lib().tmc_buf_release(self.handle)
+        except Exception:
+            pass
+
+    @property
+    def count(self) -> int:
+        return int(lib().tmc_buf_count(self.handle))
+
+    @property
+    def dtype(self) -> int:
+        return int(lib().tmc_buf_dtype(self.handle))
+
+    def write(self, data, offset: int = 0) -> None:
+        import numpy as np
+        src = np.ascontiguousarray(data, dtype=np.float32).ravel()
+        check(lib().tmc_buf_write(self.handle, src.ctypes.data_as(C.c_void_p), src.size, offset),
+              "tmc_buf_write")
+
+    def read(self):
+        import numpy as np
+        out = np.empty(self.count, dtype=np.float32)
+        check(lib().tmc_buf_read(self.handle, out.ctypes.data_as(C.c_void_p)), "tmc_buf_read")
+        return out
+
+    def read_raw(self):
+        import numpy as np
+        dt = {F16: np.uint16, BF16: np.uint16, F32: np.float32, I32: np.int32}[self.dtype]
+        out = np.empty(self.count, dtype=dt)
+        check(lib().tmc_buf_read_raw(self.handle, out.ctypes.data_as(C.c_void_p), self.count, 0),
+              "tmc_buf_read_raw")
+        return out
+
+
+class Kernel:
+    def __init__(self, handle, types, writable):
+        self.handle, self.types, self.writable = handle, types, writable
+
+    def __del__(self):
+        try:
+            lib().tmc_kernel_release(self.handle)
+        except Exception:
+            pass
+
+
+class Exec:
+    def __init__(self, handle, keep):
+        self.handle, self._keep = handle, keep
+
+    def __del__(self):
+        try:
+            lib().tmc_exec_release(self.handle)
+        except Exception:
+            pass
+
+    def run(self, reset_outputs: bool = True):
+        gpu, cpu = C.c_double(), C.c_double()
+        check(lib().tmc_exec_run(self.handle, int(reset_outputs), C.byref(gpu), C.byref(cpu)),
+              "tmc_exec_run")
+        return gpu.value, cpu.value
+
+
+class Sequence:
+    def __init__(self, handle, steps):
+        self.handle, self._steps = handle, steps
+
+    def __del__(self):
+        try:
+            lib().tmc_seq_release(self.handle)
+        except Exception:
+            pass
+
+    def run(self):
+        gpu, cpu = C.c_double(), C.c_double()
+        check(lib().tmc_seq_run(self.handle, C.byref(gpu), C.byref(cpu)), "tmc_seq_run")
+        return gpu.value, cpu.value
+
+    def launch(self):
+        check(lib().tmc_seq_launch(self.handle), "tmc_seq_launch")

@@ -16,6 +16,10 @@
 // its own 4 positions' softmax terms and its 8 output columns, and rows are
 // folded together only once per split (cross-row shuffles), then the 4 waves
 // of the block merge through LDS.  Splits merge in attn_combine_kernel.
+//
+// For D = 128 (attn_mfma_partial_kernel) the scores of a 16-position tile
+// come from v_mfma_f32_16x16x32_f16, so no cross-lane reduction is needed for
+// q.K; see the comment above that kernel.
 #include "tmc_abi.hpp"
 #include "tmc_device.hpp"
 
@@ -24,7 +28,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kTilesPerWave = 4;
+constexpr int kTilesPerWave = 2;  // VALU kernel (D < 128)
+constexpr int kMfmaTilesPerWave = 4;  // D == 128 kernel: tiles of 16 positions per wave
+constexpr int kMfmaChunk = kWaves * kMfmaTilesPerWave * 16;
 
 struct AttnParams {
   const half_t* q;
@@ -41,8 +47,10 @@ struct AttnParams {
   float scale_log2;       // (1/sqrt(D)) * log2(e)
 };
 
+// Positions per split: D == 128 runs the MFMA kernel (kMfmaChunk); smaller
+// heads run the VALU kernel (4 waves x 2 tiles of 4*64/(D/8) positions).
 template <int D> constexpr int chunk_positions() {
-  return kWaves * kTilesPerWave * 4 * (kWave / (D / 8));
+  return D == 128 ? kMfmaChunk : kWaves * kTilesPerWave * 4 * (kWave / (D / 8));
 }
 
 template <bool PAGED>
@@ -60,16 +68,82 @@ __device__ __forceinline__ bool has_bad_page(const AttnParams& p, int b, int val
   return __syncthreads_or(bad) != 0;
 }
 
+// Positions [p0, p0 + TILE) of one wave: K/V slices for lane (row r, column
+// chunk c) at positions p0 + r + NR*j, j < 4.
+template <int D, bool PAGED>
+struct TileLoad {
+  static constexpr int RL = D / 8;
+  static constexpr int NR = kWave / RL;
+  h8 k[4], v[4];
+  bool ok[4];
+
+  __device__ __forceinline__ void load(const AttnParams& p, const int* s_pages, int page0,
+                                       size_t contiguous_base, int kvh, int p0, int end, int r,
+                                       int c) {
+    const h8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int pos = p0 + r + NR * j;
+      ok[j] = pos < end;
+      size_t off = 0;
+      if constexpr (PAGED) {
+        const int page = ok[j] ? s_pages[pos / p.page_size - page0] : -1;
+        ok[j] = ok[j] && page >= 0;
+        off = (size_t)page * p.page_stride + (size_t)kvh * p.head_stride +
+              (size_t)(pos % p.page_size) * D + 8 * c;
+      } else {
+        off = contiguous_base + (size_t)pos * D + 8 * c;
+      }
+      k[j] = ok[j] ? load_h8(p.k + off) : zero;
+      v[j] = ok[j] ? load_h8(p.v + off) : zero;
+    }
+  }
+};
+
+// Online-softmax update of the GROUP heads with one loaded tile.
+template <int D, int GROUP>
+__device__ __forceinline__ void attend_tile(const h8 (&qv)[GROUP], const h8 (&kt)[4],
+                                            const h8 (&vt)[4], const bool (&ok)[4],
+                                            float scale_log2, float (&m)[GROUP],
+                                            float (&l)[GROUP], float (&o)[GROUP][8]) {
+  constexpr int RL = D / 8;
+#pragma unroll
+  for (int g = 0; g < GROUP; ++g) {
+    float s[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float dot = group_sum<RL>(dot8(qv[g], kt[j], 0.0f));
+      s[j] = ok[j] ? dot * scale_log2 : -INFINITY;
+    }
+    float tile_max = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    tile_max = cross_max<RL>(tile_max);
+    const float next = fmaxf(m[g], tile_max);
+    const float alpha = next == -INFINITY ? 1.0f : fast_exp2(m[g] - next);
+    float psum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) o[g][t] *= alpha;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float pj = ok[j] ? fast_exp2(s[j] - next) : 0.0f;
+      psum += pj;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) o[g][t] += pj * (float)vt[j][t];
+    }
+    l[g] = l[g] * alpha + psum;
+    m[g] = next;
+  }
+}
+
 template <int D, int GROUP, bool PAGED>
 __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnParams p) {
   constexpr int RL = D / 8;
   constexpr int NR = kWave / RL;
-  constexpr int J = 4;
-  constexpr int TILE = NR * J;
+  constexpr int TILE = NR * 4;
   constexpr int CHUNK = chunk_positions<D>();
   __shared__ float s_m[kWaves][GROUP];
   __shared__ float s_l[kWaves][GROUP];
   __shared__ float s_o[kWaves][GROUP][D];
+  __shared__ int s_pages[PAGED ? CHUNK + 1 : 1];
 
   const int b = blockIdx.z, kvh = blockIdx.y, split = blockIdx.x;
   if (PAGED && p.active && b >= p.active[0]) return;
@@ -85,6 +159,17 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnParams p) {
   const int begin = split * CHUNK;
   const int end = min(valid, begin + CHUNK);
 
+  // Block-table entries of this split, fetched once (one latency period
+  // instead of one per tile before each K/V load).
+  int page0 = 0;
+  if constexpr (PAGED) {
+    page0 = begin / p.page_size;
+    const int entries = (end - 1) / p.page_size - page0 + 1;
+    for (int i = threadIdx.x; i < entries; i += kThreads)
+      s_pages[i] = p.tables[(size_t)b * p.max_pages + page0 + i];
+    __syncthreads();
+  }
+
   h8 qv[GROUP];
 #pragma unroll
   for (int g = 0; g < GROUP; ++g)
@@ -98,55 +183,18 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnParams p) {
 #pragma unroll
     for (int t = 0; t < 8; ++t) o[g][t] = 0.0f;
   }
-  const h8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
   const size_t contiguous_base = ((size_t)b * p.kv_heads + kvh) * (size_t)p.capacity * D;
 
-  for (int tile = wave;; tile += kWaves) {
-    const int p0 = begin + tile * TILE;
-    if (p0 >= end) break;  // wave-uniform
-    h8 kv[J], vv[J];
-    bool ok[J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const int pos = p0 + r + NR * j;
-      ok[j] = pos < end;
-      size_t off = 0;
-      if constexpr (PAGED) {
-        const int page = ok[j] ? p.tables[(size_t)b * p.max_pages + pos / p.page_size] : -1;
-        ok[j] = ok[j] && page >= 0;
-        off = (size_t)page * p.page_stride + (size_t)kvh * p.head_stride +
-              (size_t)(pos % p.page_size) * D + 8 * c;
-      } else {
-        off = contiguous_base + (size_t)pos * D + 8 * c;
-      }
-      kv[j] = ok[j] ? load_h8(p.k + off) : zero;
-      vv[j] = ok[j] ? load_h8(p.v + off) : zero;
-    }
-#pragma unroll
-    for (int g = 0; g < GROUP; ++g) {
-      float s[J];
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        const float dot = group_sum<RL>(dot8(qv[g], kv[j], 0.0f));
-        s[j] = ok[j] ? dot * p.scale_log2 : -INFINITY;
-      }
-      float tile_max = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-      tile_max = cross_max<RL>(tile_max);
-      const float next = fmaxf(m[g], tile_max);
-      const float alpha = next == -INFINITY ? 1.0f : fast_exp2(m[g] - next);
-      float psum = 0.0f;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) o[g][t] *= alpha;
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        const float pj = ok[j] ? fast_exp2(s[j] - next) : 0.0f;
-        psum += pj;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) o[g][t] += pj * (float)vv[j][t];
-      }
-      l[g] = l[g] * alpha + psum;
-      m[g] = next;
-    }
+  // Two tiles in flight per wave: this wave's tiles t and t + 4.
+  for (int tile = wave;; tile += 2 * kWaves) {
+    const int p0a = begin + tile * TILE;
+    if (p0a >= end) break;  // wave-uniform
+    const int p0b = p0a + kWaves * TILE;
+    TileLoad<D, PAGED> a, bt;
+    a.load(p, s_pages, page0, contiguous_base, kvh, p0a, end, r, c);
+    bt.load(p, s_pages, page0, contiguous_base, kvh, p0b, end, r, c);
+    attend_tile<D, GROUP>(qv, a.k, a.v, a.ok, p.scale_log2, m, l, o);
+    if (p0b < end) attend_tile<D, GROUP>(qv, bt.k, bt.v, bt.ok, p.scale_log2, m, l, o);
   }
 
   // Fold the NR position rows of the wave (each row held other positions).
@@ -197,22 +245,56 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnParams p) {
   }
 }
 
-template <int D, bool PAGED>
-__global__ __launch_bounds__(D) void attn_combine_kernel(AttnParams p) {
+// Merge the per-split (max, sum, weighted) partials of the GROUP query
+// heads of one (request, kv head).  Thread (g, d) issues every load it needs
+// (the split statistics and its weighted column of each split, plus a slice
+// of the block table for the negative-page rule) before using any of them,
+// so the merge costs one memory round trip.
+template <int D, int GROUP, bool PAGED>
+__global__ __launch_bounds__(GROUP * D) void attn_combine_kernel(AttnParams p) {
   constexpr int CHUNK = chunk_positions<D>();
-  const int qh = blockIdx.x, b = blockIdx.y;
+  constexpr int kRegSplits = 32;
+  const int kvh = blockIdx.x, b = blockIdx.y;
   if (PAGED && p.active && b >= p.active[0]) return;
   const int valid = valid_length<PAGED>(p, b);
   if (valid < 1 || valid > p.capacity) return;
   const int nsplit = (valid + CHUNK - 1) / CHUNK;
   if (nsplit <= 1) return;
-  if (PAGED && has_bad_page(p, b, valid)) return;
-  const int d = threadIdx.x;
+  const int g = threadIdx.x / D, d = threadIdx.x % D;
+  const int qh = kvh * GROUP + g;
   const float* base = p.ws + ((size_t)b * p.q_heads + qh) * p.max_splits * (D + 2);
+  int bad = 0;
+  if constexpr (PAGED) {
+    const int pages = (valid + p.page_size - 1) / p.page_size;
+    for (int lp = threadIdx.x; lp < pages; lp += GROUP * D)
+      bad |= p.tables[(size_t)b * p.max_pages + lp] < 0;
+  }
+  float m[kRegSplits], l[kRegSplits], o[kRegSplits];
+#pragma unroll
+  for (int s = 0; s < kRegSplits; ++s) {
+    if (s < nsplit) {
+      const float* slot = base + (size_t)s * (D + 2);
+      m[s] = slot[D];
+      l[s] = slot[D + 1];
+      o[s] = slot[d];
+    }
+  }
+  if (PAGED && __syncthreads_or(bad)) return;
   float mx = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, base[(size_t)s * (D + 2) + D]);
+#pragma unroll
+  for (int s = 0; s < kRegSplits; ++s)
+    if (s < nsplit) mx = fmaxf(mx, m[s]);
+  for (int s = kRegSplits; s < nsplit; ++s) mx = fmaxf(mx, base[(size_t)s * (D + 2) + D]);
   float lsum = 0.0f, osum = 0.0f;
-  for (int s = 0; s < nsplit; ++s) {
+#pragma unroll
+  for (int s = 0; s < kRegSplits; ++s) {
+    if (s < nsplit) {
+      const float scale = m[s] == -INFINITY ? 0.0f : fast_exp2(m[s] - mx);
+      lsum += scale * l[s];
+      osum += scale * o[s];
+    }
+  }
+  for (int s = kRegSplits; s < nsplit; ++s) {
     const float* slot = base + (size_t)s * (D + 2);
     const float scale = slot[D] == -INFINITY ? 0.0f : fast_exp2(slot[D] - mx);
     lsum += scale * slot[D + 1];
@@ -221,24 +303,230 @@ __global__ __launch_bounds__(D) void attn_combine_kernel(AttnParams p) {
   p.out[((size_t)b * p.q_heads + qh) * D + d] = (half_t)(osum / lsum);
 }
 
-template <int D, bool PAGED>
-int launch_attention(const AttnParams& p, int batch, hipStream_t stream) {
-  const int group = p.q_heads / p.kv_heads;
-  const dim3 grid((unsigned)p.max_splits, (unsigned)p.kv_heads, (unsigned)batch);
-  switch (group) {
-  case 1: hipLaunchKernelGGL((attn_partial_kernel<D, 1, PAGED>), grid, dim3(kThreads), 0, stream, p); break;
-  case 2: hipLaunchKernelGGL((attn_partial_kernel<D, 2, PAGED>), grid, dim3(kThreads), 0, stream, p); break;
-  case 4: hipLaunchKernelGGL((attn_partial_kernel<D, 4, PAGED>), grid, dim3(kThreads), 0, stream, p); break;
-  case 8: hipLaunchKernelGGL((attn_partial_kernel<D, 8, PAGED>), grid, dim3(kThreads), 0, stream, p); break;
-  default: return fail("Attention: q_heads / kv_heads must be 1, 2, 4 or 8.");
+// ---------------------------------------------------------------- D = 128
+// Split partial for D = 128: grid (split, kv head, request), a split is
+// kWaves * kMfmaTilesPerWave tiles of 16 positions; wave w takes tiles w,
+// w + kWaves, ...  (Keeping a second tile's loads in flight per wave was
+// measured slower: the extra registers cost more occupancy than it gains.)
+//
+// Scores come from v_mfma_f32_16x16x32_f16: A = the tile's 16 K rows, B = the
+// GROUP query heads of the kv head as columns (zero columns beyond GROUP).
+// Lane l: MFMA row/column j = l % 16, k-group g = l / 16 (MFMA s takes d chunk
+// 4s+g); acc[r] = score(position p0 + 4g + r, head j).  PV: lane (row g,
+// column chunk j) accumulates positions p0 + 4i + g, i < 4, with the
+// probabilities read back from the wave's LDS slice.
+template <bool PAGED>
+struct MfmaTile {
+  h8 ka[4], vv[4];
+
+  __device__ __forceinline__ void load(const AttnParams& p, const int* s_pages, int page0,
+                                       size_t contiguous_base, int kvh, int p0, int end, int j,
+                                       int g) {
+    const h8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+    {
+      const long off = offset(p, s_pages, page0, contiguous_base, kvh, p0 + j, end);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) ka[s] = off >= 0 ? load_h8(p.k + off + 8 * (4 * s + g)) : zero;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const long off = offset(p, s_pages, page0, contiguous_base, kvh, p0 + 4 * i + g, end);
+      vv[i] = off >= 0 ? load_h8(p.v + off + 8 * j) : zero;
+    }
   }
+
+  // Element offset of position `pos` of the segment, -1 when absent.
+  static __device__ __forceinline__ long offset(const AttnParams& p, const int* s_pages, int page0,
+                                                size_t contiguous_base, int kvh, int pos,
+                                                int end) {
+    if (pos >= end) return -1;
+    if constexpr (PAGED) {
+      const int page = s_pages[pos / p.page_size - page0];
+      if (page < 0) return -1;
+      return (long)page * p.page_stride + (long)kvh * p.head_stride +
+             (long)(pos % p.page_size) * 128;
+    } else {
+      return (long)(contiguous_base + (size_t)pos * 128);
+    }
+  }
+};
+
+template <int GROUP, bool PAGED>
+__device__ __forceinline__ void mfma_attend(const MfmaTile<PAGED>& t, const h8 (&qb)[4],
+                                            const AttnParams& p, const int* s_pages, int page0,
+                                            int p0, int end, int j, int g, float (*s_pw)[GROUP],
+                                            float& m, float& lsum, float (&o)[GROUP][8]) {
+  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(t.ka[s], qb[s], acc, 0, 0, 0);
+  float sc[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int pos = p0 + 4 * g + r;
+    bool ok = pos < end;
+    if constexpr (PAGED) ok = ok && s_pages[pos / p.page_size - page0] >= 0;
+    sc[r] = ok ? acc[r] * p.scale_log2 : -INFINITY;
+  }
+  float tile_max = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+  tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16, kWave));
+  tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32, kWave));
+  const float next = fmaxf(m, tile_max);
+  const float alpha = next == -INFINITY ? 1.0f : fast_exp2(m - next);
+  float psum = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float pr = sc[r] == -INFINITY ? 0.0f : fast_exp2(sc[r] - next);
+    psum += pr;
+    if (j < GROUP) s_pw[4 * g + r][j] = pr;
+  }
+  lsum = lsum * alpha + psum;
+  m = next;
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int h = 0; h < GROUP; ++h) {
+    const float ah = readlane(alpha, h);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[h][e] *= ah;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float pv[GROUP];
+#pragma unroll
+    for (int h = 0; h < GROUP; ++h) pv[h] = s_pw[4 * i + g][h];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = (float)t.vv[i][e];
+#pragma unroll
+      for (int h = 0; h < GROUP; ++h) o[h][e] += pv[h] * v;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+template <int GROUP, bool PAGED>
+__global__ __launch_bounds__(kThreads) void attn_mfma_partial_kernel(AttnParams p) {
+  constexpr int D = 128;
+  constexpr int CHUNK = kMfmaChunk;
+  __shared__ float s_m[kWaves][GROUP];
+  __shared__ float s_l[kWaves][GROUP];
+  __shared__ float s_o[kWaves][GROUP][D];
+  __shared__ float s_p[kWaves][16][GROUP];
+  __shared__ int s_pages[PAGED ? CHUNK + 1 : 1];
+
+  const int b = blockIdx.z, kvh = blockIdx.y, split = blockIdx.x;
+  if (PAGED && p.active && b >= p.active[0]) return;
+  const int valid = valid_length<PAGED>(p, b);
+  if (valid < 1 || valid > p.capacity) return;
+  const int nsplit = (valid + CHUNK - 1) / CHUNK;
+  if (split >= nsplit) return;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int j = lane & 15;
+  const int g = lane >> 4;
+  const int begin = split * CHUNK;
+  const int end = min(valid, begin + CHUNK);
+
+  const h8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  h8 qb[4];
+  {
+    const half_t* qrow = p.q + ((size_t)b * p.q_heads + kvh * GROUP + (j < GROUP ? j : 0)) * D;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qb[s] = j < GROUP ? load_h8(qrow + 8 * (4 * s + g)) : zero;
+  }
+  int page0 = 0;
+  if constexpr (PAGED) {
+    page0 = begin / p.page_size;
+    const int entries = (end - 1) / p.page_size - page0 + 1;
+    for (int i = threadIdx.x; i < entries; i += kThreads)
+      s_pages[i] = p.tables[(size_t)b * p.max_pages + page0 + i];
+    __syncthreads();
+  }
+  float m = -INFINITY, lsum = 0.0f;
+  float o[GROUP][8];
+#pragma unroll
+  for (int h = 0; h < GROUP; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
+  const size_t base = ((size_t)b * p.kv_heads + kvh) * (size_t)p.capacity * D;
+
+  for (int tile = wave; begin + 16 * tile < end; tile += kWaves) {
+    MfmaTile<PAGED> t;
+    t.load(p, s_pages, page0, base, kvh, begin + 16 * tile, end, j, g);
+    mfma_attend<GROUP, PAGED>(t, qb, p, s_pages, page0, begin + 16 * tile, end, j, g, s_p[wave],
+                              m, lsum, o);
+  }
+
+#pragma unroll
+  for (int h = 0; h < GROUP; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[h][e] = cross_sum<16>(o[h][e]);
+  lsum = cross_sum<16>(lsum);
+  if (g == 0) {
+#pragma unroll
+    for (int h = 0; h < GROUP; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_o[wave][h][8 * j + e] = o[h][e];
+    if (j < GROUP) {
+      s_m[wave][j] = m;
+      s_l[wave][j] = lsum;
+    }
+  }
+  __syncthreads();
+
+  const bool single = nsplit == 1;
+  if (PAGED && single && has_bad_page(p, b, valid)) return;
+  for (int idx = threadIdx.x; idx < GROUP * D; idx += kThreads) {
+    const int h = idx / D, d = idx % D;
+    float mx = s_m[0][h];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][h]);
+    float ltot = 0.0f, otot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float scale = s_m[w][h] == -INFINITY ? 0.0f : fast_exp2(s_m[w][h] - mx);
+      ltot += scale * s_l[w][h];
+      otot += scale * s_o[w][h][d];
+    }
+    const int qh = kvh * GROUP + h;
+    if (single) {
+      p.out[((size_t)b * p.q_heads + qh) * D + d] = (half_t)(otot / ltot);
+    } else {
+      float* slot = p.ws + (((size_t)b * p.q_heads + qh) * p.max_splits + split) * (D + 2);
+      slot[d] = otot;
+      if (d == 0) {
+        slot[D] = mx;
+        slot[D + 1] = ltot;
+      }
+    }
+  }
+}
+
+template <int D, int GROUP, bool PAGED>
+int launch_group(const AttnParams& p, int batch, hipStream_t stream) {
+  const dim3 grid((unsigned)p.max_splits, (unsigned)p.kv_heads, (unsigned)batch);
+  if constexpr (D == 128)
+    hipLaunchKernelGGL((attn_mfma_partial_kernel<GROUP, PAGED>), grid, dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((attn_partial_kernel<D, GROUP, PAGED>), grid, dim3(kThreads), 0, stream, p);
   if (check_launch("attn_partial_kernel")) return 1;
   if (p.max_splits > 1) {
-    hipLaunchKernelGGL((attn_combine_kernel<D, PAGED>), dim3((unsigned)p.q_heads, (unsigned)batch),
-                       dim3(D), 0, stream, p);
+    hipLaunchKernelGGL((attn_combine_kernel<D, GROUP, PAGED>),
+                       dim3((unsigned)p.kv_heads, (unsigned)batch), dim3(GROUP * D), 0, stream, p);
     return check_launch("attn_combine_kernel");
   }
   return 0;
+}
+
+template <int D, bool PAGED>
+int launch_attention(const AttnParams& p, int batch, hipStream_t stream) {
+  switch (p.q_heads / p.kv_heads) {
+  case 1: return launch_group<D, 1, PAGED>(p, batch, stream);
+  case 2: return launch_group<D, 2, PAGED>(p, batch, stream);
+  case 4: return launch_group<D, 4, PAGED>(p, batch, stream);
+  case 8: return launch_group<D, 8, PAGED>(p, batch, stream);
+  default: return fail("Attention: q_heads / kv_heads must be 1, 2, 4 or 8.");
+  }
 }
 
 int chunk_for(int64_t head_dim) {
@@ -250,6 +538,8 @@ int chunk_for(int64_t head_dim) {
   default: return 0;
   }
 }
+
+bool head_dim_ok(int64_t head_dim) { return chunk_for(head_dim) > 0; }
 
 template <bool PAGED>
 int dispatch_attention(const AttnParams& p, int batch, int head_dim, hipStream_t stream) {
@@ -266,11 +556,16 @@ int common_checks(const void* q, const void* k, const void* v, const void* out, 
                   int64_t capacity) {
   TMC_REQUIRE(q && k && v && out, "Attention: null device pointer.");
   TMC_REQUIRE(dtype == TMC_F16, "Attention: the gfx950 kernel stores K/V in fp16.");
-  TMC_REQUIRE(chunk_for(head_dim) > 0, "Attention: head_dim must be 16, 32, 64 or 128.");
+  TMC_REQUIRE(head_dim_ok(head_dim), "Attention: head_dim must be 16, 32, 64 or 128.");
+  TMC_REQUIRE(q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 &&
+                  (q_heads / kv_heads) <= 8 && ((q_heads / kv_heads) & (q_heads / kv_heads - 1)) == 0,
+              "Attention: q_heads / kv_heads must be 1, 2, 4 or 8.");
   TMC_REQUIRE(batch > 0 && batch < 65536 && q_heads > 0 && kv_heads > 0 && kv_heads < 65536 &&
                   q_heads % kv_heads == 0 && capacity > 0 && capacity < (1LL << 30),
               "Attention: invalid batch, head counts or capacity.");
   TMC_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v), "Attention: q, K and V must be 16-byte aligned.");
+  TMC_REQUIRE((capacity + chunk_for(head_dim) - 1) / chunk_for(head_dim) <= 1024,
+              "Attention: capacity exceeds 1024 splits.");
   return 0;
 }
 
@@ -279,10 +574,11 @@ int common_checks(const void* q, const void* k, const void* v, const void* out, 
 
 using namespace tmc;
 
-extern "C" size_t tmc_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_dim,
-                                                int64_t capacity) {
+extern "C" size_t tmc_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                                int64_t head_dim, int64_t capacity) {
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || capacity <= 0 || q_heads % kv_heads) return 0;
   const int chunk = chunk_for(head_dim);
-  if (chunk <= 0 || batch <= 0 || q_heads <= 0 || capacity <= 0) return 0;
+  if (chunk <= 0) return 0;
   const int64_t splits = (capacity + chunk - 1) / chunk;
   if (splits <= 1) return 0;
   return (size_t)batch * q_heads * splits * (head_dim + 2) * sizeof(float);
@@ -297,7 +593,7 @@ extern "C" int tmc_decode_attention(const void* q, const void* key_cache, const 
                     capacity))
     return 1;
   TMC_REQUIRE(valid_length, "Attention: null valid-length pointer.");
-  const size_t need = tmc_attention_workspace_bytes(batch, q_heads, head_dim, capacity);
+  const size_t need = tmc_attention_workspace_bytes(batch, q_heads, kv_heads, head_dim, capacity);
   TMC_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
               "Attention: workspace is smaller than tmc_attention_workspace_bytes().");
   AttnParams p{};
@@ -334,7 +630,7 @@ extern "C" int tmc_paged_decode_attention(const void* q, const void* key_pool,
   TMC_REQUIRE(page_size > 0 && max_pages > 0 && page_stride > 0 && head_stride >= 0 &&
                   (page_stride % 8) == 0 && (head_stride % 8) == 0,
               "Paged attention: invalid page geometry (strides must be multiples of 8 elements).");
-  const size_t need = tmc_attention_workspace_bytes(max_batch, q_heads, head_dim, capacity);
+  const size_t need = tmc_attention_workspace_bytes(max_batch, q_heads, kv_heads, head_dim, capacity);
   TMC_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
               "Paged attention: workspace is smaller than tmc_attention_workspace_bytes().");
   AttnParams p{};

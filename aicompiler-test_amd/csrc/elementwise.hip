@@ -62,6 +62,80 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(
   }
 }
 
+// Register-resident variants for rows of at most kMaxVec * 8 * 256
+// elements with vector-aligned rows: each thread loads its 8-element
+// slices once, the row is reduced once, and the outputs are written from
+// registers (one global read pass instead of two).
+constexpr int kMaxVec = 4;
+
+template <typename T> struct Vec8;
+template <> struct Vec8<half_t> { typedef h8 type; };
+template <> struct Vec8<float> { typedef float type __attribute__((ext_vector_type(8))); };
+
+template <typename T, int NV, bool ADD>
+__global__ __launch_bounds__(kThreads) void norm_vec_kernel(const T* __restrict__ residual,
+                                                           const T* __restrict__ update,
+                                                           const T* __restrict__ w,
+                                                           T* __restrict__ sum_out,
+                                                           T* __restrict__ norm_out, int width,
+                                                           float eps) {
+  typedef typename Vec8<T>::type V;
+  __shared__ float scratch[kWaves];
+  const size_t base = (size_t)blockIdx.x * width;
+  const int vecs = width / 8;
+  V val[NV];
+  float squares = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = threadIdx.x + i * kThreads;
+    if (v < vecs) {
+      V a = *reinterpret_cast<const V*>(residual + base + 8 * v);
+      if constexpr (ADD) {
+        const V b = *reinterpret_cast<const V*>(update + base + 8 * v);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) a[t] = from_float<T>(to_float<T>(a[t]) + to_float<T>(b[t]));
+      }
+      val[i] = a;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) squares += to_float<T>(a[t]) * to_float<T>(a[t]);
+    }
+  }
+  const float total = block_sum(squares, scratch);
+  const float inverse = 1.0f / sqrtf(total / (float)width + eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = threadIdx.x + i * kThreads;
+    if (v < vecs) {
+      const V wv = *reinterpret_cast<const V*>(w + 8 * v);
+      V n;
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        n[t] = from_float<T>(to_float<T>(val[i][t]) * inverse * to_float<T>(wv[t]));
+      if constexpr (ADD) *reinterpret_cast<V*>(sum_out + base + 8 * v) = val[i];
+      *reinterpret_cast<V*>(norm_out + base + 8 * v) = n;
+    }
+  }
+}
+
+template <typename T, bool ADD>
+bool launch_norm_vec(const T* r, const T* u, const T* w, T* s, T* n, int64_t rows, int64_t width,
+                     float eps, hipStream_t stream) {
+  constexpr uintptr_t align = sizeof(typename Vec8<T>::type);
+  auto ok = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) % align) == 0; };
+  if (width % 8 != 0 || !ok(r) || !ok(w) || !ok(n) || (ADD && (!ok(u) || !ok(s)))) return false;
+  const int64_t vecs = width / 8;
+  const int nv = (int)((vecs + kThreads - 1) / kThreads);
+  if (nv > kMaxVec) return false;
+  const dim3 grid((unsigned)rows);
+  switch (nv) {
+  case 1: hipLaunchKernelGGL((norm_vec_kernel<T, 1, ADD>), grid, dim3(kThreads), 0, stream, r, u, w, s, n, (int)width, eps); break;
+  case 2: hipLaunchKernelGGL((norm_vec_kernel<T, 2, ADD>), grid, dim3(kThreads), 0, stream, r, u, w, s, n, (int)width, eps); break;
+  case 3: hipLaunchKernelGGL((norm_vec_kernel<T, 3, ADD>), grid, dim3(kThreads), 0, stream, r, u, w, s, n, (int)width, eps); break;
+  default: hipLaunchKernelGGL((norm_vec_kernel<T, 4, ADD>), grid, dim3(kThreads), 0, stream, r, u, w, s, n, (int)width, eps); break;
+  }
+  return true;
+}
+
 // emitDecoderSiLUMul (DecoderLLMMetalEmitter.cpp:395-415).
 template <typename T>
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const T* __restrict__ gate,
@@ -323,10 +397,14 @@ extern "C" int tmc_rmsnorm(const void* x, const void* w, void* y, int dtype, int
   TMC_REQUIRE(rows > 0 && width > 0 && width < (1LL << 31) && rows < (1LL << 31),
               "RMSNorm: invalid shape.");
   TMC_REQUIRE(std::isfinite(epsilon) && epsilon > 0.0f, "RMSNorm: epsilon must be finite and positive.");
-  TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((rmsnorm_kernel<T>), dim3((unsigned)rows), dim3(kThreads), 0,
-                                            as_stream(stream), static_cast<const T*>(x),
-                                            static_cast<const T*>(w), static_cast<T*>(y),
-                                            (int)width, epsilon));
+  TMC_DISPATCH_T(dtype, {
+    if (!launch_norm_vec<T, false>(static_cast<const T*>(x), nullptr, static_cast<const T*>(w),
+                                   nullptr, static_cast<T*>(y), rows, width, epsilon,
+                                   as_stream(stream)))
+      hipLaunchKernelGGL((rmsnorm_kernel<T>), dim3((unsigned)rows), dim3(kThreads), 0,
+                         as_stream(stream), static_cast<const T*>(x), static_cast<const T*>(w),
+                         static_cast<T*>(y), (int)width, epsilon);
+  });
   return check_launch("rmsnorm_kernel");
 }
 
@@ -338,11 +416,17 @@ extern "C" int tmc_add_rmsnorm(const void* residual, const void* update, const v
   TMC_REQUIRE(rows > 0 && width > 0 && width < (1LL << 31) && rows < (1LL << 31),
               "Add+RMSNorm: invalid shape.");
   TMC_REQUIRE(std::isfinite(epsilon) && epsilon > 0.0f, "Add+RMSNorm: epsilon must be finite and positive.");
-  TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((add_rmsnorm_kernel<T>), dim3((unsigned)rows), dim3(kThreads), 0,
-                                            as_stream(stream), static_cast<const T*>(residual),
-                                            static_cast<const T*>(update), static_cast<const T*>(w),
-                                            static_cast<T*>(sum_out), static_cast<T*>(norm_out),
-                                            (int)width, epsilon));
+  TMC_DISPATCH_T(dtype, {
+    if (!launch_norm_vec<T, true>(static_cast<const T*>(residual), static_cast<const T*>(update),
+                                  static_cast<const T*>(w), static_cast<T*>(sum_out),
+                                  static_cast<T*>(norm_out), rows, width, epsilon,
+                                  as_stream(stream)))
+      hipLaunchKernelGGL((add_rmsnorm_kernel<T>), dim3((unsigned)rows), dim3(kThreads), 0,
+                         as_stream(stream), static_cast<const T*>(residual),
+                         static_cast<const T*>(update), static_cast<const T*>(w),
+                         static_cast<T*>(sum_out), static_cast<T*>(norm_out), (int)width,
+                         epsilon);
+  });
   return check_launch("add_rmsnorm_kernel");
 }
 

@@ -411,7 +411,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     NEED(b > 0 && qh > 0 && kvh > 0 && d > 0 && cap > 0, "decode_attention needs batch, q_heads, head_dim, capacity.");
     s.inputs = {dt, dt, dt, TMC_I32};
     s.outputs = {dt};
-    s.workspace_bytes = tmc_attention_workspace_bytes(b, qh, d, cap);
+    s.workspace_bytes = tmc_attention_workspace_bytes(b, qh, kvh, d, cap);
     s.launch = [=](const LaunchContext& c) {
       return tmc_decode_attention(c.ptrs[0], c.ptrs[1], c.ptrs[2],
                                   static_cast<const int32_t*>(c.ptrs[3]), c.ptrs[4], dt, b, qh, kvh,
@@ -430,7 +430,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     const int64_t page_stride = param_int(p, "page_stride", kvh * ps * d);
     s.inputs = {dt, dt, dt, TMC_I32, TMC_I32, TMC_I32};
     s.outputs = {dt};
-    s.workspace_bytes = tmc_attention_workspace_bytes(b, qh, d, ps * mp);
+    s.workspace_bytes = tmc_attention_workspace_bytes(b, qh, kvh, d, ps * mp);
     s.launch = [=](const LaunchContext& c) {
       return tmc_paged_decode_attention(
           c.ptrs[0], c.ptrs[1], c.ptrs[2], static_cast<const int32_t*>(c.ptrs[3]),

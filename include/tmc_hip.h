@@ -134,10 +134,33 @@ void tmc_rt_fail_next(tmc_runtime *rt, int count);
 
 /* Decode GEMV, emitDecodeGEMV (DecodeGEMVMetalEmitter.cpp:68-132):
  * y[r,n] = sum_k x[r,k] * W[n,k] with fp16 x and W, fp32 accumulation, y in
- * y_dtype (TMC_F16 or TMC_F32).  batch <= 8 runs the wave64 split-K GEMV;
- * larger batches run the MFMA skinny GEMM. */
+ * y_dtype (TMC_F16 or TMC_F32).  Batch 1 runs the wave64 split-K dot
+ * GEMV; larger batches run the MFMA skinny GEMM (see tmc_gemv_config). */
 int tmc_gemv_f16(const void *x, const void *w, void *y, int y_dtype, int64_t batch,
                  int64_t in_features, int64_t out_features, void *stream);
+
+/* Launch configuration of the GEMV family (the decode GEMV tuner's
+ * candidates; DecodeGEMVConfig, DecodeGEMVMetalEmitter.hpp:11-16, retargeted
+ * to gfx950).  algorithm 0 = default for the shape, 1 = wave64 split-K dot
+ * (rows_per_wave 1|2 rows per wave, unroll 2|4 16-byte loads per row in
+ * flight, k_split 1|2|4 waves sharing a row), 2 = MFMA (rows_per_wave =
+ * 16-row output tiles per block, k_split waves per tile, n_tiles*k_split
+ * <= 16, unroll 1|2 K tiles in flight). */
+typedef struct tmc_gemv_config {
+  int algorithm;
+  int rows_per_wave;
+  int unroll;
+  int k_split;
+} tmc_gemv_config;
+
+/* tmc_gemv_f16 with an explicit launch configuration. */
+int tmc_gemv_f16_config(const void *x, const void *w, void *y, int y_dtype, int64_t batch,
+                        int64_t in_features, int64_t out_features, const tmc_gemv_config *config,
+                        void *stream);
+
+/* The configuration tmc_gemv_f16 / tmc_gate_up_silu_f16 pick for a shape. */
+int tmc_gemv_default_config(int64_t batch, int64_t in_features, int64_t out_features, int gated,
+                            tmc_gemv_config *out);
 
 /* Skinny GEMM with fp16 MFMA (v_mfma_f32_16x16x32_f16), any batch >= 1;
  * same semantics as tmc_gemv_f16.  No reference counterpart: the reference
@@ -151,6 +174,9 @@ int tmc_skinny_gemm_f16_mfma(const void *x, const void *w, void *y, int y_dtype,
  * the fp16 rounding; Wg, Wu are [intermediate, hidden]. */
 int tmc_gate_up_silu_f16(const void *x, const void *w_gate, const void *w_up, void *out,
                          int64_t batch, int64_t hidden, int64_t intermediate, void *stream);
+int tmc_gate_up_silu_f16_config(const void *x, const void *w_gate, const void *w_up, void *out,
+                                int64_t batch, int64_t hidden, int64_t intermediate,
+                                const tmc_gemv_config *config, void *stream);
 
 /* emitDecoderRMSNorm (DecoderLLMMetalEmitter.cpp:63-108) / emitRMSNorm
  * (MetalEmitter.cpp:12-76): y = x * rsqrt(mean(x^2) + eps) * w, fp32
@@ -216,9 +242,9 @@ int tmc_serving_kv_append(const void *input, const int32_t *valid_lengths,
                           int64_t capacity, int64_t page_size, int head_major, void *stream);
 
 /* Bytes of device workspace the split-KV attention needs for these limits
- * (0 when a single split covers `capacity`). */
-size_t tmc_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_dim,
-                                     int64_t capacity);
+ * on the current device (0 when none is needed). */
+size_t tmc_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                     int64_t head_dim, int64_t capacity);
 
 /* Decode attention over a contiguous cache (emitKVAttention,
  * KVCacheMetalEmitter.cpp:119-208, queryLength 1): caches

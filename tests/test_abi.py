@@ -48,7 +48,9 @@ def test_argument_validation_fails_before_device_work(tmc):
 
 
 def test_attention_workspace_sizes(tmc):
-    # one split covers 256 positions at D=128: no workspace
-    assert tmc.attention_workspace_bytes(16, 32, 128, 256) == 0
-    # C4: 16 requests x 32 heads x 16 splits x (128 + 2) floats
-    assert tmc.attention_workspace_bytes(16, 32, 128, 4096) == 16 * 32 * 16 * 130 * 4
+    # VALU kernel (D=64): one split of 256 positions needs no workspace,
+    # otherwise batch x q_heads x splits x (D + 2) floats
+    assert tmc.attention_workspace_bytes(2, 8, 8, 64, 256) == 0
+    assert tmc.attention_workspace_bytes(2, 8, 8, 64, 1024) == 2 * 8 * 4 * 66 * 4
+    # bad head ratio
+    assert tmc.attention_workspace_bytes(2, 6, 4, 64, 1024) == 0

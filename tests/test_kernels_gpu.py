@@ -224,8 +224,8 @@ def test_paged_and_serving_append_bit_exact(tmc, orc, torch):
 
 
 # ---------------------------------------------------------------- attention
-def _ws(tmc, torch, batch, qh, d, cap):
-    n = tmc.attention_workspace_bytes(batch, qh, d, cap)
+def _ws(tmc, torch, batch, qh, kvh, d, cap):
+    n = tmc.attention_workspace_bytes(batch, qh, kvh, d, cap)
     return torch.empty(max(n // 4, 1), dtype=torch.float32, device="cuda") if n else None
 
 
@@ -243,7 +243,7 @@ def test_c3_contiguous_decode_attention(tmc, orc, torch, length):
     tmc.kv_append(dev_f16(nv), valid, v_d, 1, 1, heads, d, cap, False)
     out = torch.full((1, heads * d), float("nan"), dtype=torch.float16, device="cuda")
     tmc.decode_attention(dev_f16(q), k_d, v_d, valid, out, 1, heads, heads, d, cap,
-                         _ws(tmc, torch, 1, heads, d, cap))
+                         _ws(tmc, torch, 1, heads, heads, d, cap))
     torch.cuda.synchronize()
     kk = orc.append_contiguous(nk, k.ravel(), 1, heads, d, 1, cap, False, length + 1)
     vv = orc.append_contiguous(nv, v.ravel(), 1, heads, d, 1, cap, False, length + 1)
@@ -262,7 +262,7 @@ def test_decode_attention_edges(tmc, orc, torch, valid, d, qh, kvh):
     out = torch.full((b, qh * d), float("nan"), dtype=torch.float16, device="cuda")
     vl = torch.tensor([valid], dtype=torch.int32, device="cuda")
     tmc.decode_attention(dev_f16(q), dev_f16(k), dev_f16(v), vl, out, b, qh, kvh, d, cap,
-                         _ws(tmc, torch, b, qh, d, cap))
+                         _ws(tmc, torch, b, qh, kvh, d, cap))
     torch.cuda.synchronize()
     ref = orc.decode_attention(q, k, v, F16, qh, kvh, d, cap, valid)
     assert_f16_path(values(out), ref, what=f"attention valid={valid} d={d} group={qh // kvh}")
@@ -300,7 +300,7 @@ def test_c4_paged_gqa_attention(tmc, orc, torch):
     out = torch.full((batch, qh * d), float("nan"), dtype=torch.float16, device="cuda")
     tmc.paged_decode_attention(dev_f16(q), k_d, v_d, valid_d, tables_d, active, out, batch, qh,
                                kvh, d, p, max_pages, kvh * p * d, p * d,
-                               _ws(tmc, torch, batch, qh, d, cap))
+                               _ws(tmc, torch, batch, qh, kvh, d, cap))
     torch.cuda.synchronize()
     kp = orc.append_serving(nk, k_pool.ravel(), batch, kvh, d, cap, p, True, valid, tables, batch)
     vp = orc.append_serving(nv, v_pool.ravel(), batch, kvh, d, cap, p, True, valid, tables, batch)
@@ -328,7 +328,7 @@ def test_paged_attention_inactive_and_bad_pages_untouched(tmc, orc, torch):
     cap = max_pages * p
     tmc.paged_decode_attention(dev_f16(q), dev_f16(k_pool), dev_f16(v_pool), dev(lengths),
                                dev(tables), active, out, batch, qh, kvh, d, p, max_pages,
-                               kvh * p * d, p * d, _ws(tmc, torch, batch, qh, d, cap))
+                               kvh * p * d, p * d, _ws(tmc, torch, batch, qh, kvh, d, cap))
     torch.cuda.synchronize()
     got = values(out)
     ref, written = orc.paged_attention(q, k_pool, v_pool, F16, qh, kvh, d, p, kvh * p * d, p * d,
@@ -400,3 +400,28 @@ def test_fill_normal_statistics(tmc, torch):
     a = values(t)
     assert abs(a.mean()) < 1e-4 and abs(a.std() - 0.02) < 2e-4
     assert np.array_equal(bits(t), bits(u))  # deterministic in the seed
+
+
+CONFIGS = ([(1, r, u, k) for r in (1, 2) for u in (2, 4) for k in (1, 2, 4)] +
+           [(2, nt, u, ks) for nt in (1, 2) for u in (1, 2) for ks in (1, 2, 4, 8, 16)
+            if nt * ks <= 16])
+
+
+@pytest.mark.parametrize("algo,rpw,unroll,ks", CONFIGS)
+def test_gemv_and_gated_mlp_every_config(tmc, orc, torch, algo, rpw, unroll, ks):
+    """Every tuner candidate is parity-checked, at a shape with K and N tails."""
+    cfg = tmc.GemvConfig()
+    cfg.algorithm, cfg.rows_per_wave, cfg.unroll, cfg.k_split = algo, rpw, unroll, ks
+    for batch in ((1, 3, 8) if algo == 1 else (1, 5, 16, 20)):
+        k, n = 1160, 200  # 9.06 K tiles of 128, 145 16-byte chunks, N tail of 8
+        x = orc.f16(normal(220 + batch, (batch, k)))
+        w = orc.f16(normal(221, (n, k), 0.02))
+        w2 = orc.f16(normal(222, (n, k), 0.02))
+        y = torch.empty((batch, n), dtype=torch.float32, device="cuda")
+        tmc.gemv_config(dev_f16(x), dev_f16(w), y, cfg)
+        g = torch.empty((batch, n), dtype=torch.float16, device="cuda")
+        tmc.gate_up_silu_config(dev_f16(x), dev_f16(w), dev_f16(w2), g, cfg)
+        torch.cuda.synchronize()
+        assert_f32_rel(values(y), orc.linear(x, w, F16), what=f"cfg {cfg.astuple()} b{batch}")
+        assert_f16_path(values(g), orc.gated_mlp(x, w, w2, F16),
+                        what=f"gated cfg {cfg.astuple()} b{batch}")
