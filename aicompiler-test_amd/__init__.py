@@ -52,6 +52,8 @@ def _declare(l):
         "tmc_kv_append": (i32, [vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, vp]),
         "tmc_paged_kv_append": (i32, [vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, i32, vp]),
         "tmc_serving_kv_append": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, vp]),
+        "tmc_decode_rope_append": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64,
+                                         i64, i64, i64, i64, vp]),
         "tmc_attention_workspace_bytes": (sz, [i64, i64, i64, i64, i64]),
         "tmc_decode_attention": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, vp, sz,
                                        vp]),
@@ -107,6 +109,27 @@ def lib() -> C.CDLL:
         _lib = C.CDLL(LIB_PATH)
         _declare(_lib)
     return _lib
+
+
+_host = None
+
+
+def host():
+    """The C++ host layer as a Python module (_tmc_host, built next to this
+    file).  torch is imported first so one HIP runtime serves the process."""
+    global _host
+    if _host is None:
+        import importlib.util
+        import sysconfig
+        lib()  # loads torch's HIP runtime and libtmc_hip.so first
+        path = os.path.join(HERE, "_tmc_host" + sysconfig.get_config_var("EXT_SUFFIX"))
+        if not os.path.exists(path):
+            raise TmcError(f"{path} is missing; run aicompiler-test_amd/build.py")
+        spec = importlib.util.spec_from_file_location("_tmc_host", path)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        _host = mod
+    return _host
 
 
 def last_error() -> str:
@@ -251,6 +274,17 @@ def serving_kv_append(inp, valid_lengths, tables, active, cache, max_batch, head
                                       _ptr(cache), _dtype_code(inp), max_batch, heads, head_dim,
                                       capacity, page_size, int(head_major), _stream(stream)),
           "tmc_serving_kv_append")
+
+
+def decode_rope_append(qkv, cos, sin, valid_lengths, tables, active, q_out, k_pool, v_pool,
+                       max_batch, q_heads, kv_heads, head_dim, capacity, page_size, max_pages,
+                       stream=None):
+    check(lib().tmc_decode_rope_append(_ptr(qkv), _ptr(cos), _ptr(sin), _ptr(valid_lengths),
+                                       _ptr(tables), _ptr(active), _ptr(q_out), _ptr(k_pool),
+                                       _ptr(v_pool), _dtype_code(qkv), max_batch, q_heads,
+                                       kv_heads, head_dim, capacity, page_size, max_pages,
+                                       _stream(stream)),
+          "tmc_decode_rope_append")
 
 
 def attention_workspace_bytes(batch, q_heads, kv_heads, head_dim, capacity) -> int:

@@ -1,8 +1,13 @@
-"""Compile the gfx950 decode backend into aicompiler-test_amd/libtmc_hip.so.
+"""Compile the gfx950 decode backend in-tree.
 
-Each .hip source under csrc/ is compiled by hipcc for gfx950 in parallel
-(objects under _build/, git-ignored) and linked into one shared library
-in-tree, so the built library travels with the source tree to the GPU box.
+  libtmc_hip.so   every .hip source under csrc/, compiled by hipcc for gfx950
+                  (the C ABI of include/tmc_hip.h);
+  libtmc_host.so  the C++ host layer under host/ (HipRuntime, KV pools and
+                  states, decoder executors, serving loop) over that ABI;
+  _tmc_host*.so   its Python module (pybind11), for tests and bench.py.
+
+Objects go under _build/ (git-ignored); the libraries land next to this file
+so they travel with the source tree to the GPU box.
 
 Usage: python aicompiler-test_amd/build.py
 """
@@ -18,6 +23,14 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "libtmc_hip.so")
+HOST = os.path.join(HERE, "host")
+HOST_OUT = os.path.join(HERE, "libtmc_host.so")
+HOST_SOURCES = ["HipRuntime.cpp", "KVCacheState.cpp", "DecoderLLM.cpp", "Benchmark.cpp",
+                "ServingRuntime.cpp"]
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
+CXX = os.environ.get("CXX", "g++")
+CXXFLAGS = ["-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",
+            f"-I{INCLUDE}", f"-I{HOST}"]
 
 SOURCES = ["runtime.hip", "gemv.hip", "elementwise.hip", "attention.hip"]
 
@@ -48,16 +61,54 @@ def _compile(src: str) -> str:
     return obj
 
 
+def _run(cmd, what):
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"{what} failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    if res.stderr.strip():
+        sys.stderr.write(f"[{what}]\n{res.stderr}")
+
+
+def _compile_host(src: str) -> str:
+    obj = os.path.join(BUILD, "host_" + os.path.splitext(src)[0] + ".o")
+    _run([CXX, *CXXFLAGS, "-c", os.path.join(HOST, src), "-o", obj], f"g++ {src}")
+    return obj
+
+
+def _module_path() -> str:
+    import sysconfig
+    return os.path.join(HERE, "_tmc_host" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def _build_module() -> str:
+    import sysconfig
+    import pybind11
+    obj = os.path.join(BUILD, "host_bindings.o")
+    _run([CXX, *CXXFLAGS, f"-I{pybind11.get_include()}", f"-I{sysconfig.get_paths()['include']}",
+          "-fvisibility=hidden", "-c", os.path.join(HOST, "bindings.cpp"), "-o", obj],
+         "g++ bindings.cpp")
+    out = _module_path()
+    _run([CXX, "-shared", "-o", out + ".tmp", obj, f"-L{HERE}", "-ltmc_host", "-ltmc_hip",
+          "-Wl,-rpath,$ORIGIN"], "link _tmc_host")
+    shutil.move(out + ".tmp", out)
+    return out
+
+
 def build(jobs: int = 4) -> str:
     os.makedirs(BUILD, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
         objs = list(pool.map(_compile, SOURCES))
+        host_objs = list(pool.map(_compile_host, HOST_SOURCES))
     tmp = OUT + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     shutil.move(tmp, OUT)
+    _run([CXX, "-shared", "-o", HOST_OUT + ".tmp", *host_objs, f"-L{HERE}", "-ltmc_hip",
+          "-Wl,-rpath,$ORIGIN"], "link libtmc_host.so")
+    shutil.move(HOST_OUT + ".tmp", HOST_OUT)
+    _build_module()
     return OUT
 
 

@@ -172,6 +172,15 @@ __global__ __launch_bounds__(kThreads) void embedding_kernel(const int32_t* __re
     out[(size_t)row * hidden + f] = table[(size_t)token * hidden + f];
 }
 
+// Interleaved pair rotation shared by every RoPE kernel, written with explicit
+// fused multiply-adds so that all of them produce the same bits for the same
+// pair (the fused decode kernel below relies on it).
+__device__ __forceinline__ void rotate_pair(float even, float odd, float c, float s,
+                                            float& out_even, float& out_odd) {
+  out_even = __fmaf_rn(even, c, -(odd * s));
+  out_odd = __fmaf_rn(even, s, odd * c);
+}
+
 // emitDecoderRoPE (DecoderLLMMetalEmitter.cpp:110-158).
 template <typename T>
 __global__ __launch_bounds__(kThreads) void rope_kernel(const T* __restrict__ x,
@@ -196,10 +205,10 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(const T* __restrict__ x,
   const size_t out_base = (((size_t)b * heads + head) * seq + token) * head_dim + 2 * pair;
   const float c = cosine[(size_t)position * pairs + pair];
   const float s = sine[(size_t)position * pairs + pair];
-  const float even = to_float<T>(x[in_base]);
-  const float odd = to_float<T>(x[in_base + 1]);
-  out[out_base] = from_float<T>(even * c - odd * s);
-  out[out_base + 1] = from_float<T>(even * s + odd * c);
+  float re, ro;
+  rotate_pair(to_float<T>(x[in_base]), to_float<T>(x[in_base + 1]), c, s, re, ro);
+  out[out_base] = from_float<T>(re);
+  out[out_base + 1] = from_float<T>(ro);
 }
 
 // emitServingRoPE (DecoderLLMMetalEmitter.cpp:260-312).
@@ -221,10 +230,10 @@ __global__ __launch_bounds__(kThreads) void serving_rope_kernel(
   const size_t base = ((size_t)request * heads + head) * head_dim + 2 * pair;
   const float c = cosine[(size_t)position * pairs + pair];
   const float s = sine[(size_t)position * pairs + pair];
-  const float even = to_float<T>(x[base]);
-  const float odd = to_float<T>(x[base + 1]);
-  out[base] = from_float<T>(even * c - odd * s);
-  out[base + 1] = from_float<T>(even * s + odd * c);
+  float re, ro;
+  rotate_pair(to_float<T>(x[base]), to_float<T>(x[base + 1]), c, s, re, ro);
+  out[base] = from_float<T>(re);
+  out[base + 1] = from_float<T>(ro);
 }
 
 // emitDecoderCacheAppend / emitDecoderPagedCacheAppend
@@ -285,6 +294,64 @@ __global__ __launch_bounds__(kThreads) void serving_append_kernel(
   const size_t src = head_major ? ((size_t)request * heads + head) * head_dim + component
                                 : (size_t)request * hidden + feature;
   cache[dst] = input[src];
+}
+
+// Decode-step fusion of emitServingRoPE (DecoderLLMMetalEmitter.cpp:260-312)
+// for the query and key heads with emitServingPagedCacheAppend (:314-373) for
+// the rotated key and the value, reading one fused q|k|v projection row per
+// request: row b = [q heads | kv key heads | kv value heads] x head_dim.  One
+// thread moves one interleaved pair.  The rotated query goes to q_out
+// [max_batch, q_heads * head_dim]; the rotated key and the value are stored
+// at position valid_lengths[b] - 1 of the pools [page][kv_heads][page_size]
+// [head_dim] through block_tables[b * max_pages + position / page_size].
+// Rows at or beyond active_count[0], rows whose length is outside
+// [1, capacity] and positions whose page entry is negative are skipped.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void decode_rope_append_kernel(
+    const T* __restrict__ qkv, const float* __restrict__ cosine, const float* __restrict__ sine,
+    const int32_t* __restrict__ valid_lengths, const int32_t* __restrict__ block_tables,
+    const int32_t* __restrict__ active_count, T* __restrict__ q_out, T* __restrict__ k_pool,
+    T* __restrict__ v_pool, int max_batch, int q_heads, int kv_heads, int head_dim, int capacity,
+    int page_size, int max_pages) {
+  const int pairs = head_dim / 2;
+  const int row_pairs = (q_heads + 2 * kv_heads) * pairs;
+  const long gid = (long)blockIdx.x * kThreads + threadIdx.x;
+  const int request = (int)(gid / row_pairs);
+  if (request >= max_batch || request >= active_count[0]) return;
+  const int valid = valid_lengths[request];
+  if (valid <= 0 || valid > capacity) return;
+  const int position = valid - 1;
+  const int column = 2 * (int)(gid % row_pairs);
+  const int q_width = q_heads * head_dim, kv_width = kv_heads * head_dim;
+  const T* src = qkv + (size_t)request * (q_width + 2 * kv_width) + column;
+  const int pair = (column % head_dim) / 2;
+  if (column < q_width + kv_width) {
+    const float c = cosine[(size_t)position * pairs + pair];
+    const float s = sine[(size_t)position * pairs + pair];
+    float re, ro;
+    rotate_pair(to_float<T>(src[0]), to_float<T>(src[1]), c, s, re, ro);
+    if (column < q_width) {
+      T* dst = q_out + (size_t)request * q_width + column;
+      dst[0] = from_float<T>(re);
+      dst[1] = from_float<T>(ro);
+      return;
+    }
+    const int page = block_tables[(size_t)request * max_pages + position / page_size];
+    if (page < 0) return;
+    const int feature = column - q_width;
+    T* dst = k_pool + (((size_t)page * kv_heads + feature / head_dim) * page_size +
+                       position % page_size) * head_dim + feature % head_dim;
+    dst[0] = from_float<T>(re);
+    dst[1] = from_float<T>(ro);
+    return;
+  }
+  const int page = block_tables[(size_t)request * max_pages + position / page_size];
+  if (page < 0) return;
+  const int feature = column - q_width - kv_width;
+  T* dst = v_pool + (((size_t)page * kv_heads + feature / head_dim) * page_size +
+                     position % page_size) * head_dim + feature % head_dim;
+  dst[0] = src[0];
+  dst[1] = src[1];
 }
 
 __device__ __forceinline__ bool better(float cv, int ci, float bv, int bi) {
@@ -562,6 +629,36 @@ extern "C" int tmc_serving_kv_append(const void* input, const int32_t* valid_len
                                             (int)head_dim, (int)capacity, (int)page_size,
                                             head_major));
   return check_launch("serving_append_kernel");
+}
+
+extern "C" int tmc_decode_rope_append(const void* qkv, const float* cosine, const float* sine,
+                                      const int32_t* valid_lengths, const int32_t* block_tables,
+                                      const int32_t* active_count, void* q_out, void* key_pool,
+                                      void* value_pool, int dtype, int64_t max_batch,
+                                      int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                      int64_t capacity, int64_t page_size, int64_t max_pages,
+                                      void* stream) {
+  TMC_REQUIRE(qkv && cosine && sine && valid_lengths && block_tables && active_count && q_out &&
+                  key_pool && value_pool,
+              "Decode RoPE+append: null device pointer.");
+  TMC_REQUIRE(float_dtype(dtype) && max_batch > 0 && max_batch < 65536 && q_heads > 0 &&
+                  kv_heads > 0 && q_heads % kv_heads == 0 && head_dim > 0 && head_dim % 2 == 0 &&
+                  head_dim <= 1024 && capacity > 0 && page_size > 0 && page_size <= capacity &&
+                  max_pages == (capacity + page_size - 1) / page_size,
+              "Decode RoPE+append: invalid dtype or shape (max_pages must be "
+              "ceil(capacity / page_size)).");
+  const size_t items = (size_t)max_batch * (q_heads + 2 * kv_heads) * (head_dim / 2);
+  TMC_REQUIRE(items < (1ull << 31), "Decode RoPE+append: too many elements.");
+  TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((decode_rope_append_kernel<T>),
+                                            dim3((unsigned)((items + kThreads - 1) / kThreads)),
+                                            dim3(kThreads), 0, as_stream(stream),
+                                            static_cast<const T*>(qkv), cosine, sine,
+                                            valid_lengths, block_tables, active_count,
+                                            static_cast<T*>(q_out), static_cast<T*>(key_pool),
+                                            static_cast<T*>(value_pool), (int)max_batch,
+                                            (int)q_heads, (int)kv_heads, (int)head_dim,
+                                            (int)capacity, (int)page_size, (int)max_pages));
+  return check_launch("decode_rope_append_kernel");
 }
 
 extern "C" int tmc_argmax_f32(const float* logits, int32_t* tokens, int64_t rows,

@@ -185,6 +185,10 @@ struct KernelSpec {
   size_t groups = 1;
   size_t threads = 256;
   size_t workspace_bytes = 0;
+  // Minimum element count of every binding (inputs, then outputs) that the
+  // launch reads or writes at this specialization; 0 = not checked (page
+  // pools, whose extent the block tables decide).
+  std::vector<size_t> counts;
   std::function<int(const LaunchContext&)> launch;
 };
 
@@ -272,6 +276,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
          "decode_gemv needs batch, in, out > 0, dtype=f16 and out_dtype f16|f32.");
     s.inputs = {TMC_F16, TMC_F16};
     s.outputs = {od};
+    s.counts = {(size_t)(b * k), (size_t)(n * k), (size_t)(b * n)};
     s.groups = (size_t)((n + 3) / 4);
     s.launch = [=](const LaunchContext& c) {
       return tmc_gemv_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], od, b, k, n, c.stream);
@@ -284,6 +289,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     s.inputs = {TMC_F16, TMC_F16, TMC_F16};
     s.outputs = {TMC_F16};
     s.groups = (size_t)((f + 3) / 4);
+    s.counts = {(size_t)(b * h), (size_t)(f * h), (size_t)(f * h), (size_t)(b * f)};
     s.launch = [=](const LaunchContext& c) {
       return tmc_gate_up_silu_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], b, h, f, c.stream);
     };
@@ -297,12 +303,15 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     if (name == "rmsnorm") {
       s.inputs = {dt, dt};
       s.outputs = {dt};
+      s.counts = {(size_t)(rows * width), (size_t)width, (size_t)(rows * width)};
       s.launch = [=](const LaunchContext& c) {
         return tmc_rmsnorm(c.ptrs[0], c.ptrs[1], c.ptrs[2], dt, rows, width, eps, c.stream);
       };
     } else {
       s.inputs = {dt, dt, dt};
       s.outputs = {dt, dt};
+      s.counts = {(size_t)(rows * width), (size_t)(rows * width), (size_t)width,
+                  (size_t)(rows * width), (size_t)(rows * width)};
       s.launch = [=](const LaunchContext& c) {
         return tmc_add_rmsnorm(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], c.ptrs[4], dt, rows,
                                width, eps, c.stream);
@@ -316,6 +325,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     s.inputs = {dt, dt};
     s.outputs = {dt};
     s.groups = (size_t)((n + 255) / 256);
+    s.counts = {(size_t)n, (size_t)n, (size_t)n};
     const bool silu = name == "silu_mul";
     s.launch = [=](const LaunchContext& c) {
       return silu ? tmc_silu_mul(c.ptrs[0], c.ptrs[1], c.ptrs[2], dt, n, c.stream)
@@ -329,6 +339,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     s.inputs = {TMC_I32, dt};
     s.outputs = {dt};
     s.groups = (size_t)rows;
+    s.counts = {(size_t)rows, (size_t)(v * h), (size_t)(rows * h)};
     s.launch = [=](const LaunchContext& c) {
       return tmc_embedding(static_cast<const int32_t*>(c.ptrs[0]), c.ptrs[1], c.ptrs[2], dt, rows,
                            h, v, c.stream);
@@ -341,6 +352,8 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     NEED(b > 0 && sq > 0 && hd > 0 && d > 0 && cap > 0, "rope needs batch, seq, heads, head_dim, capacity.");
     s.inputs = {dt, TMC_F32, TMC_F32, TMC_I32};
     s.outputs = {dt};
+    s.counts = {(size_t)(b * sq * hd * d), (size_t)(cap * (d / 2)), (size_t)(cap * (d / 2)), 1,
+                (size_t)(b * sq * hd * d)};
     s.launch = [=](const LaunchContext& c) {
       return tmc_rope(c.ptrs[0], static_cast<const float*>(c.ptrs[1]),
                       static_cast<const float*>(c.ptrs[2]), static_cast<const int32_t*>(c.ptrs[3]),
@@ -354,6 +367,8 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     NEED(b > 0 && hd > 0 && d > 0 && cap > 0, "serving_rope needs max_batch, heads, head_dim, capacity.");
     s.inputs = {dt, TMC_F32, TMC_F32, TMC_I32, TMC_I32};
     s.outputs = {dt};
+    s.counts = {(size_t)(b * hd * d), (size_t)(cap * (d / 2)), (size_t)(cap * (d / 2)), (size_t)b, 1,
+                (size_t)(b * hd * d)};
     s.launch = [=](const LaunchContext& c) {
       return tmc_serving_rope(c.ptrs[0], static_cast<const float*>(c.ptrs[1]),
                               static_cast<const float*>(c.ptrs[2]),
@@ -371,6 +386,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     if (name == "kv_append") {
       s.inputs = {dt, TMC_I32};
       s.outputs = {dt};
+      s.counts = {(size_t)(b * sq * hd * d), 1, (size_t)(b * hd * cap * d)};
       s.launch = [=](const LaunchContext& c) {
         return tmc_kv_append(c.ptrs[0], static_cast<const int32_t*>(c.ptrs[1]), c.ptrs[2], dt, b,
                              sq, hd, d, cap, hm, c.stream);
@@ -380,6 +396,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
       NEED(ps > 0, "paged_kv_append needs page_size.");
       s.inputs = {dt, TMC_I32, TMC_I32};
       s.outputs = {dt};
+      s.counts = {(size_t)(b * sq * hd * d), 1, (size_t)((cap + ps - 1) / ps), 0};
       s.launch = [=](const LaunchContext& c) {
         return tmc_paged_kv_append(c.ptrs[0], static_cast<const int32_t*>(c.ptrs[1]),
                                    static_cast<const int32_t*>(c.ptrs[2]), c.ptrs[3], dt, b, sq,
@@ -396,11 +413,35 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     NEED(b > 0 && hd > 0 && d > 0 && cap > 0 && ps > 0, "serving_kv_append needs max_batch, heads, head_dim, capacity, page_size.");
     s.inputs = {dt, TMC_I32, TMC_I32, TMC_I32};
     s.outputs = {dt};
+    s.counts = {(size_t)(b * hd * d), (size_t)b, (size_t)(b * ((cap + ps - 1) / ps)), 1, 0};
     s.launch = [=](const LaunchContext& c) {
       return tmc_serving_kv_append(c.ptrs[0], static_cast<const int32_t*>(c.ptrs[1]),
                                    static_cast<const int32_t*>(c.ptrs[2]),
                                    static_cast<const int32_t*>(c.ptrs[3]), c.ptrs[4], dt, b, hd,
                                    d, cap, ps, hm, c.stream);
+    };
+    return true;
+  }
+  if (name == "decode_rope_append") {
+    const int64_t b = param_int(p, "max_batch"), qh = param_int(p, "q_heads"),
+                  kvh = param_int(p, "kv_heads", param_int(p, "q_heads")),
+                  d = param_int(p, "head_dim"), cap = param_int(p, "capacity"),
+                  ps = param_int(p, "page_size");
+    NEED(b > 0 && qh > 0 && kvh > 0 && d > 0 && cap > 0 && ps > 0,
+         "decode_rope_append needs max_batch, q_heads, head_dim, capacity, page_size.");
+    const int64_t mp = (cap + ps - 1) / ps;
+    // inputs: qkv, cos, sin, valid_lengths, block_tables, active; outputs: q, key pool, value pool
+    s.inputs = {dt, TMC_F32, TMC_F32, TMC_I32, TMC_I32, TMC_I32};
+    s.outputs = {dt, dt, dt};
+    s.counts = {(size_t)(b * (qh + 2 * kvh) * d), (size_t)(cap * (d / 2)),
+                (size_t)(cap * (d / 2)), (size_t)b, (size_t)(b * mp), 1, (size_t)(b * qh * d), 0, 0};
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_decode_rope_append(c.ptrs[0], static_cast<const float*>(c.ptrs[1]),
+                                    static_cast<const float*>(c.ptrs[2]),
+                                    static_cast<const int32_t*>(c.ptrs[3]),
+                                    static_cast<const int32_t*>(c.ptrs[4]),
+                                    static_cast<const int32_t*>(c.ptrs[5]), c.ptrs[6], c.ptrs[7],
+                                    c.ptrs[8], dt, b, qh, kvh, d, cap, ps, mp, c.stream);
     };
     return true;
   }
@@ -411,6 +452,8 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     NEED(b > 0 && qh > 0 && kvh > 0 && d > 0 && cap > 0, "decode_attention needs batch, q_heads, head_dim, capacity.");
     s.inputs = {dt, dt, dt, TMC_I32};
     s.outputs = {dt};
+    s.counts = {(size_t)(b * qh * d), (size_t)(b * kvh * cap * d), (size_t)(b * kvh * cap * d), 1,
+                (size_t)(b * qh * d)};
     s.workspace_bytes = tmc_attention_workspace_bytes(b, qh, kvh, d, cap);
     s.launch = [=](const LaunchContext& c) {
       return tmc_decode_attention(c.ptrs[0], c.ptrs[1], c.ptrs[2],
@@ -430,6 +473,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     const int64_t page_stride = param_int(p, "page_stride", kvh * ps * d);
     s.inputs = {dt, dt, dt, TMC_I32, TMC_I32, TMC_I32};
     s.outputs = {dt};
+    s.counts = {(size_t)(b * qh * d), 0, 0, (size_t)b, (size_t)(b * mp), 1, (size_t)(b * qh * d)};
     s.workspace_bytes = tmc_attention_workspace_bytes(b, qh, kvh, d, ps * mp);
     s.launch = [=](const LaunchContext& c) {
       return tmc_paged_decode_attention(
@@ -446,6 +490,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     s.inputs = {TMC_F32};
     s.outputs = {TMC_I32};
     s.groups = (size_t)rows;
+    s.counts = {(size_t)(rows * v), (size_t)rows};
     s.launch = [=](const LaunchContext& c) {
       return tmc_argmax_f32(static_cast<const float*>(c.ptrs[0]), static_cast<int32_t*>(c.ptrs[1]),
                             rows, v, c.stream);
@@ -512,6 +557,13 @@ extern "C" const char* tmc_rt_init_error(const tmc_runtime* rt) {
   return rt ? rt->init_error.c_str() : "null runtime";
 }
 extern "C" void* tmc_rt_stream(const tmc_runtime* rt) { return rt ? (void*)rt->stream : nullptr; }
+extern "C" int tmc_rt_synchronize(tmc_runtime* rt) {
+  clear_error();
+  if (!rt) return fail("tmc_rt_synchronize: null runtime.");
+  if (!rt->available) return fail(rt->init_error);
+  return hip_ok(hipStreamSynchronize(rt->stream), "stream synchronize");
+}
+
 extern "C" void tmc_rt_fail_next(tmc_runtime* rt, int count) {
   if (rt) rt->fail_next = count;
 }
@@ -698,6 +750,9 @@ extern "C" int tmc_prepare(tmc_runtime* rt, const tmc_kernel* kernel, tmc_buffer
     if (!o || o->rt != rt || std::find(outputs, outputs + i, o) != outputs + i)
       return fail("Outputs must be distinct buffers on the current device.");
     if (o->dtype != s.outputs[i]) return fail("Reflected buffer element type disagrees with TensorIR.");
+    if (!s.counts.empty() && o->count < s.counts[n_in + i])
+      return fail("Output buffer " + std::to_string(i) + " holds " + std::to_string(o->count) +
+                  " elements; the kernel writes " + std::to_string(s.counts[n_in + i]) + ".");
     exec->outputs.push_back(o);
   }
   for (size_t i = 0; i < n_in; ++i) {
@@ -705,6 +760,9 @@ extern "C" int tmc_prepare(tmc_runtime* rt, const tmc_kernel* kernel, tmc_buffer
     if (!b || b->rt != rt || std::find(outputs, outputs + n_out, b) != outputs + n_out)
       return fail("Input is missing, on another device, or aliases an output.");
     if (b->dtype != s.inputs[i]) return fail("Reflected buffer element type disagrees with TensorIR.");
+    if (!s.counts.empty() && b->count < s.counts[i])
+      return fail("Input buffer " + std::to_string(i) + " holds " + std::to_string(b->count) +
+                  " elements; the kernel reads " + std::to_string(s.counts[i]) + ".");
     exec->ctx.ptrs.push_back(b->ptr);
   }
   for (auto* o : exec->outputs) exec->ctx.ptrs.push_back(o->ptr);

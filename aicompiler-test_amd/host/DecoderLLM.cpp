@@ -1,0 +1,832 @@
+// Decoder-LLM decode path on gfx950; see DecoderLLM.hpp.
+#include "DecoderLLM.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <ostream>
+#include <sstream>
+#include <stdexcept>
+#include <utility>
+
+namespace tensor {
+
+// ---------------------------------------------------------------------- plan
+namespace planner {
+
+std::size_t DecoderLLMPlan::hiddenSize() const { return attention.modelDimension(); }
+
+std::size_t DecoderLLMPlan::hiddenElementCount(std::size_t sequenceLength) const {
+  return attention.inputElementCount(sequenceLength);
+}
+
+std::size_t DecoderLLMPlan::intermediateElementCount(std::size_t sequenceLength) const {
+  return attention.batch * sequenceLength * intermediateSize;
+}
+
+std::size_t DecoderLLMPlan::logitsElementCount(std::size_t sequenceLength) const {
+  return attention.batch * sequenceLength * vocabularySize;
+}
+
+void DecoderLLMPlan::validate() const {
+  attention.validate();
+  if (layerCount == 0 || intermediateSize == 0 || vocabularySize == 0)
+    throw std::invalid_argument("Decoder-only dimensions must be nonzero.");
+  if (attention.headDimension % 2 != 0)
+    throw std::invalid_argument("Decoder-only RoPE requires an even head dimension.");
+  if (!std::isfinite(rmsNormEpsilon) || rmsNormEpsilon <= 0.0f)
+    throw std::invalid_argument("Decoder-only RMSNorm epsilon must be positive.");
+  if (accumulationDtype != DType::Float32)
+    throw std::invalid_argument("Decoder-only reductions currently require fp32 accumulation.");
+  if (attention.heads % kvHeads() != 0)
+    throw std::invalid_argument("Query heads must be a multiple of the key/value heads.");
+  if (attention.dtype != DType::Float16)
+    throw std::invalid_argument("The gfx950 decoder path stores activations and weights in fp16.");
+  if (vocabularySize > static_cast<std::size_t>(std::numeric_limits<std::int32_t>::max()))
+    throw std::invalid_argument("Vocabulary exceeds int32 token ids.");
+}
+
+KVCachePlan DecoderLLMPlan::kvPlan() const {
+  KVCachePlan plan = attention;
+  plan.batch = 1;
+  plan.heads = kvHeads();
+  plan.prefillLength = 1;
+  return plan;
+}
+
+}  // namespace planner
+
+void ropeTables(std::size_t capacity, std::size_t headDimension, double theta,
+                std::vector<float>& cosine, std::vector<float>& sine) {
+  const std::size_t pairs = headDimension / 2;
+  cosine.assign(capacity * pairs, 0.0f);
+  sine.assign(capacity * pairs, 0.0f);
+  for (std::size_t i = 0; i < pairs; ++i) {
+    const double frequency =
+        std::exp(static_cast<double>(2 * i) * (-std::log(theta) / static_cast<double>(headDimension)));
+    for (std::size_t position = 0; position < capacity; ++position) {
+      const double angle = static_cast<double>(position) * frequency;
+      cosine[position * pairs + i] = static_cast<float>(std::cos(angle));
+      sine[position * pairs + i] = static_cast<float>(std::sin(angle));
+    }
+  }
+}
+
+namespace runtime {
+namespace {
+
+using hip::BufferHandle;
+using hip::ElementType;
+
+BufferHandle allocate(hip::HipRuntime& runtime, std::size_t count, const float* data,
+                      ElementType type) {
+  auto result = runtime.createBuffer(count, data, type);
+  if (!result.buffer) throw std::runtime_error(result.errorMessage);
+  return std::move(result.buffer);
+}
+
+BufferHandle view(hip::HipRuntime& runtime, const BufferHandle& base, std::size_t offset,
+                  std::size_t count) {
+  auto* bytes = static_cast<unsigned char*>(base->devicePointer()) +
+                offset * hip::elementBytes(base->elementType());
+  auto result = runtime.wrapBuffer(bytes, count, base->elementType());
+  if (!result.buffer) throw std::runtime_error(result.errorMessage);
+  return std::move(result.buffer);
+}
+
+void requireCount(const std::string& name, const std::vector<float>& values, std::size_t expected) {
+  if (values.size() != expected)
+    throw std::invalid_argument(name + " has " + std::to_string(values.size()) +
+                                " elements; expected " + std::to_string(expected) + ".");
+}
+
+// validateWeights (DecoderLLMExecutor.cpp:169-204) with GQA key/value shapes.
+void validateWeights(const DecoderLLMWorkload& workload) {
+  const auto& plan = workload.plan;
+  const std::size_t H = plan.hiddenSize(), KV = plan.kvWidth();
+  if (workload.layers.size() != plan.layerCount)
+    throw std::invalid_argument("Decoder workload layer count differs from the plan.");
+  requireCount("embedding.weight", workload.embeddingWeight, plan.vocabularySize * H);
+  requireCount("final_norm.weight", workload.finalNormWeight, H);
+  requireCount("lm_head.weight", workload.languageModelHeadWeight, plan.vocabularySize * H);
+  const std::size_t rope = plan.attention.capacity * plan.attention.headDimension / 2;
+  requireCount("rope.cosine", workload.ropeCosine, rope);
+  requireCount("rope.sine", workload.ropeSine, rope);
+  for (std::size_t l = 0; l < workload.layers.size(); ++l) {
+    const auto& layer = workload.layers[l];
+    const std::string prefix = "layer" + std::to_string(l) + ".";
+    requireCount(prefix + "input_norm.weight", layer.inputNormWeight, H);
+    requireCount(prefix + "q.weight", layer.queryWeight, H * H);
+    requireCount(prefix + "k.weight", layer.keyWeight, KV * H);
+    requireCount(prefix + "v.weight", layer.valueWeight, KV * H);
+    requireCount(prefix + "o.weight", layer.outputWeight, H * H);
+    requireCount(prefix + "post_norm.weight", layer.postAttentionNormWeight, H);
+    requireCount(prefix + "gate.weight", layer.gateWeight, plan.intermediateSize * H);
+    requireCount(prefix + "up.weight", layer.upWeight, plan.intermediateSize * H);
+    requireCount(prefix + "down.weight", layer.downWeight, H * plan.intermediateSize);
+  }
+}
+
+void describe(DecoderLLMModelResources& r, const planner::DecoderLLMPlan& plan) {
+  r.storageDtype = DType::Float16;
+  r.plan = plan;
+  r.hiddenSize = plan.hiddenSize();
+  r.headCount = plan.attention.heads;
+  r.kvHeadCount = plan.kvHeads();
+  r.headDimension = plan.attention.headDimension;
+  r.cacheCapacity = plan.attention.capacity;
+  r.intermediateSize = plan.intermediateSize;
+  r.vocabularySize = plan.vocabularySize;
+  r.layerCount = plan.layerCount;
+}
+
+std::string fmt(double value) {
+  std::ostringstream out;
+  out.precision(9);
+  out << value;
+  return out.str();
+}
+
+}  // namespace
+
+// ------------------------------------------------------------ model resources
+ModelResourcesCreation createModelResources(hip::HipRuntime& runtime,
+                                            const DecoderLLMWorkload& workload) {
+  ModelResourcesCreation result;
+  try {
+    workload.plan.validate();
+    validateWeights(workload);
+    auto r = std::make_shared<DecoderLLMModelResources>();
+    describe(*r, workload.plan);
+    auto upload = [&](const std::vector<float>& values) {
+      r->storageBytes += values.size() * 2;
+      return allocate(runtime, values.size(), values.data(), ElementType::Float16);
+    };
+    r->embeddingWeight = upload(workload.embeddingWeight);
+    r->finalNormWeight = upload(workload.finalNormWeight);
+    r->languageModelHeadWeight = upload(workload.languageModelHeadWeight);
+    r->ropeCosine = allocate(runtime, workload.ropeCosine.size(), workload.ropeCosine.data(),
+                             ElementType::Float32);
+    r->ropeSine = allocate(runtime, workload.ropeSine.size(), workload.ropeSine.data(),
+                           ElementType::Float32);
+    r->storageBytes += (workload.ropeCosine.size() + workload.ropeSine.size()) * 4;
+    for (const auto& layer : workload.layers) {
+      DecoderLLMModelLayerBuffers b;
+      b.inputNormWeight = upload(layer.inputNormWeight);
+      std::vector<float> qkv;
+      qkv.reserve(layer.queryWeight.size() + 2 * layer.keyWeight.size());
+      qkv.insert(qkv.end(), layer.queryWeight.begin(), layer.queryWeight.end());
+      qkv.insert(qkv.end(), layer.keyWeight.begin(), layer.keyWeight.end());
+      qkv.insert(qkv.end(), layer.valueWeight.begin(), layer.valueWeight.end());
+      b.queryKeyValueWeight = upload(qkv);
+      b.outputWeight = upload(layer.outputWeight);
+      b.postAttentionNormWeight = upload(layer.postAttentionNormWeight);
+      b.gateWeight = upload(layer.gateWeight);
+      b.upWeight = upload(layer.upWeight);
+      b.downWeight = upload(layer.downWeight);
+      r->layers.push_back(std::move(b));
+    }
+    result.resources = std::move(r);
+  } catch (const std::exception& error) {
+    result.errorMessage = error.what();
+  }
+  return result;
+}
+
+ModelResourcesCreation createSyntheticModelResources(hip::HipRuntime& runtime,
+                                                     const planner::DecoderLLMPlan& plan,
+                                                     std::uint64_t seed, float stddev,
+                                                     double theta) {
+  ModelResourcesCreation result;
+  try {
+    plan.validate();
+    auto r = std::make_shared<DecoderLLMModelResources>();
+    describe(*r, plan);
+    const std::size_t H = plan.hiddenSize(), I = plan.intermediateSize, V = plan.vocabularySize;
+    const std::size_t QKV = H + 2 * plan.kvWidth();
+    std::uint64_t tensor = 0;
+    auto random = [&](std::size_t count) {
+      auto buffer = allocate(runtime, count, nullptr, ElementType::Float16);
+      const auto error = runtime.fillNormal(buffer, seed + tensor++, 0.0f, stddev);
+      if (!error.empty()) throw std::runtime_error(error);
+      r->storageBytes += count * 2;
+      return buffer;
+    };
+    const std::vector<float> ones(H, 1.0f);
+    auto norm = [&]() {
+      r->storageBytes += H * 2;
+      return allocate(runtime, H, ones.data(), ElementType::Float16);
+    };
+    r->embeddingWeight = random(V * H);
+    for (std::size_t l = 0; l < plan.layerCount; ++l) {
+      DecoderLLMModelLayerBuffers b;
+      b.inputNormWeight = norm();
+      b.queryKeyValueWeight = random(QKV * H);
+      b.outputWeight = random(H * H);
+      b.postAttentionNormWeight = norm();
+      b.gateWeight = random(I * H);
+      b.upWeight = random(I * H);
+      b.downWeight = random(H * I);
+      r->layers.push_back(std::move(b));
+    }
+    r->finalNormWeight = norm();
+    r->languageModelHeadWeight = random(V * H);
+    std::vector<float> cosine, sine;
+    ropeTables(plan.attention.capacity, plan.attention.headDimension, theta, cosine, sine);
+    r->ropeCosine = allocate(runtime, cosine.size(), cosine.data(), ElementType::Float32);
+    r->ropeSine = allocate(runtime, sine.size(), sine.data(), ElementType::Float32);
+    r->storageBytes += (cosine.size() + sine.size()) * 4;
+    const auto error = runtime.synchronize();
+    if (!error.empty()) throw std::runtime_error(error);
+    result.resources = std::move(r);
+  } catch (const std::exception& error) {
+    result.errorMessage = error.what();
+  }
+  return result;
+}
+
+// ------------------------------------------------------ BatchedDecodeExecutor
+struct BatchedDecodeExecutor::Bucket {
+  std::size_t rows = 0;
+  std::vector<std::unique_ptr<hip::PreparedExecution>> steps;
+  std::unique_ptr<hip::PreparedSequence> sequence;
+};
+
+BatchedDecodeExecutor::~BatchedDecodeExecutor() = default;
+
+std::vector<std::size_t> BatchedDecodeExecutor::buckets() const {
+  std::vector<std::size_t> rows;
+  for (const auto& b : buckets_) rows.push_back(b->rows);
+  return rows;
+}
+
+std::size_t BatchedDecodeExecutor::dispatchesPerStep(std::size_t bucket) const {
+  for (const auto& b : buckets_)
+    if (b->rows == bucket) return b->steps.size();
+  return 0;
+}
+
+void BatchedDecodeExecutor::build(std::ostream* log) {
+  auto& rt = *runtime_;
+  const auto& plan = model_->plan;
+  const std::size_t M = maximumBatchSize_, L = plan.layerCount;
+  const std::size_t H = plan.hiddenSize(), I = plan.intermediateSize, V = plan.vocabularySize;
+  const std::size_t QH = plan.attention.heads, KVH = plan.kvHeads(), D = plan.attention.headDimension;
+  const std::size_t QKV = H + 2 * plan.kvWidth();
+  const std::size_t capacity = plan.attention.capacity;
+  maxPages_ = (capacity + pageSize_ - 1) / pageSize_;
+
+  // Metadata and block tables: one buffer each, per-layer views into the tables.
+  std::vector<float> zeros(2 * M + 1, 0.0f);
+  meta_ = allocate(rt, 2 * M + 1, zeros.data(), ElementType::Int32);
+  tokensView_ = view(rt, meta_, 0, M);
+  lengthsView_ = view(rt, meta_, M, M);
+  activeView_ = view(rt, meta_, 2 * M, 1);
+  const std::vector<float> none(L * M * maxPages_, -1.0f);
+  tables_ = allocate(rt, none.size(), none.data(), ElementType::Int32);
+  for (std::size_t l = 0; l < L; ++l)
+    tableViews_.push_back(view(rt, tables_, l * M * maxPages_, M * maxPages_));
+  metaShadow_.assign(2 * M + 1, 0);
+  tableShadow_.assign(L * M * maxPages_, -1);
+
+  auto act = [&](std::size_t count, ElementType type = ElementType::Float16) {
+    activationBytes_ += count * hip::elementBytes(type);
+    return allocate(rt, count, nullptr, type);
+  };
+  residual_ = act(M * H);
+  after_ = act(M * H);
+  normalized_ = act(M * H);
+  qkv_ = act(M * QKV);
+  query_ = act(M * H);
+  context_ = act(M * H);
+  projected_ = act(M * H);
+  gated_ = act(M * I);
+  mlp_ = act(M * H);
+  logits_ = act(M * V, ElementType::Float32);
+  nextTokens_ = act(M, ElementType::Int32);
+
+  std::vector<std::size_t> rows;
+  for (std::size_t r = 1; r < M; r *= 2) rows.push_back(r);
+  rows.push_back(M);
+
+  const std::string eps = fmt(plan.rmsNormEpsilon);
+  for (const std::size_t m : rows) {
+    auto bucket = std::make_unique<Bucket>();
+    bucket->rows = m;
+    const std::string B = std::to_string(m);
+    auto add = [&](const std::string& key, const std::string& name,
+                   const std::vector<BufferHandle>& inputs,
+                   const std::vector<BufferHandle>& outputs) {
+      const auto pipeline = rt.createComputePipeline(key, name);
+      if (!pipeline.pipelineCreationPassed)
+        throw std::runtime_error(name + ": " + pipeline.errorMessage);
+      auto prepared = rt.prepareBuffers(
+          inputs, outputs, {pipeline.threadgroupCount, pipeline.threadsPerThreadgroup});
+      if (!prepared.execution) throw std::runtime_error(name + ": " + prepared.errorMessage);
+      bucket->steps.push_back(std::move(prepared.execution));
+    };
+    auto gemv = [&](std::size_t in, std::size_t out, const char* outType) {
+      return "decode_gemv?batch=" + B + "&in=" + std::to_string(in) + "&out=" + std::to_string(out) +
+             "&out_dtype=" + outType;
+    };
+    const std::string norm = "rows=" + B + "&width=" + std::to_string(H) + "&eps=" + eps + "&dtype=f16";
+    add("embedding?rows=" + B + "&hidden=" + std::to_string(H) + "&vocab=" + std::to_string(V),
+        "embedding", {tokensView_, model_->embeddingWeight}, {residual_});
+    add("rmsnorm?" + norm, "l0_input_norm", {residual_, model_->layers[0].inputNormWeight},
+        {normalized_});
+    const std::string ropeKey = "decode_rope_append?max_batch=" + B + "&q_heads=" + std::to_string(QH) +
+                                "&kv_heads=" + std::to_string(KVH) + "&head_dim=" + std::to_string(D) +
+                                "&capacity=" + std::to_string(capacity) +
+                                "&page_size=" + std::to_string(pageSize_);
+    const std::string attentionKey =
+        "paged_attention?max_batch=" + B + "&q_heads=" + std::to_string(QH) +
+        "&kv_heads=" + std::to_string(KVH) + "&head_dim=" + std::to_string(D) +
+        "&page_size=" + std::to_string(pageSize_) + "&max_pages=" + std::to_string(maxPages_);
+    for (std::size_t l = 0; l < L; ++l) {
+      const auto& w = model_->layers[l];
+      const std::string p = "l" + std::to_string(l) + "_";
+      if (l > 0)
+        add("add_rmsnorm?" + norm, p + "residual_input_norm", {after_, mlp_, w.inputNormWeight},
+            {residual_, normalized_});
+      add(gemv(H, QKV, "f16"), p + "qkv", {normalized_, w.queryKeyValueWeight}, {qkv_});
+      add(ropeKey, p + "rope_append",
+          {qkv_, model_->ropeCosine, model_->ropeSine, lengthsView_, tableViews_[l], activeView_},
+          {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer()});
+      add(attentionKey, p + "attention",
+          {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer(), lengthsView_, tableViews_[l],
+           activeView_},
+          {context_});
+      add(gemv(H, H, "f16"), p + "o", {context_, w.outputWeight}, {projected_});
+      add("add_rmsnorm?" + norm, p + "residual_post_norm",
+          {residual_, projected_, w.postAttentionNormWeight}, {after_, normalized_});
+      add("gate_up_silu?batch=" + B + "&hidden=" + std::to_string(H) + "&inter=" + std::to_string(I),
+          p + "gate_up_silu", {normalized_, w.gateWeight, w.upWeight}, {gated_});
+      add(gemv(I, H, "f16"), p + "down", {gated_, w.downWeight}, {mlp_});
+    }
+    add("add_rmsnorm?" + norm, "residual_final_norm", {after_, mlp_, model_->finalNormWeight},
+        {residual_, normalized_});
+    add(gemv(H, V, "f32"), "lm_head", {normalized_, model_->languageModelHeadWeight}, {logits_});
+    add("argmax?rows=" + B + "&vocab=" + std::to_string(V), "argmax", {logits_}, {nextTokens_});
+    std::vector<const hip::PreparedExecution*> pointers;
+    for (const auto& step : bucket->steps) pointers.push_back(step.get());
+    auto sequence = rt.prepareSequence(pointers);
+    if (!sequence.execution) throw std::runtime_error(sequence.errorMessage);
+    bucket->sequence = std::move(sequence.execution);
+    if (log)
+      *log << "Batched decode bucket rows=" << m << ": " << bucket->steps.size()
+           << " dispatches captured\n";
+    buckets_.push_back(std::move(bucket));
+  }
+}
+
+BatchedDecodeExecutor::Creation createBatchedDecodeExecutor(
+    hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
+    std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t maximumBatchSize,
+    std::ostream* log) {
+  BatchedDecodeExecutor::Creation result;
+  try {
+    if (!model) throw std::invalid_argument("Batched decode needs model resources.");
+    const auto& plan = model->plan;
+    if (maximumBatchSize == 0 || maximumBatchSize > 4096)
+      throw std::invalid_argument("Batched decode maximum batch must be in [1, 4096].");
+    if (pools.size() != plan.layerCount)
+      throw std::invalid_argument("Batched decode needs one KV page pool per layer.");
+    const auto kv = plan.kvPlan();
+    for (const auto& pool : pools) {
+      if (!pool || !pool->hasStorage() || pool->pageSize() != pools.front()->pageSize() ||
+          pool->plan().heads != kv.heads || pool->plan().headDimension != kv.headDimension ||
+          pool->plan().dtype != DType::Float16 || pool->plan().batch != 1)
+        throw std::invalid_argument("Batched decode KV pools do not match the model.");
+    }
+    std::unique_ptr<BatchedDecodeExecutor> executor(new BatchedDecodeExecutor());
+    executor->runtime_ = &runtime;
+    executor->model_ = std::move(model);
+    executor->pools_ = std::move(pools);
+    executor->maximumBatchSize_ = maximumBatchSize;
+    executor->pageSize_ = executor->pools_.front()->pageSize();
+    executor->build(log);
+    result.executor = std::move(executor);
+  } catch (const std::exception& error) {
+    result.errorMessage = error.what();
+  }
+  return result;
+}
+
+std::string BatchedDecodeExecutor::upload(const std::vector<std::int32_t>& tokens,
+                                          const std::vector<std::int32_t>& lengths,
+                                          const std::vector<std::vector<std::int32_t>>& tables,
+                                          std::size_t rows, std::size_t bucket) {
+  const std::size_t M = maximumBatchSize_;
+  std::vector<std::int32_t> meta(2 * M + 1, 0);
+  std::copy(tokens.begin(), tokens.end(), meta.begin());
+  std::copy(lengths.begin(), lengths.end(), meta.begin() + static_cast<std::ptrdiff_t>(M));
+  meta[2 * M] = static_cast<std::int32_t>(rows);
+  (void)bucket;
+  if (meta != metaShadow_) {
+    auto error = meta_->writeRaw(meta.data(), meta.size());
+    if (!error.empty()) return error;
+    metaShadow_ = std::move(meta);
+  }
+  // Pack [layer][M][maxPages] and write the span that changed.
+  std::vector<std::int32_t> packed(tableShadow_.size(), -1);
+  for (std::size_t l = 0; l < tables.size(); ++l)
+    std::copy(tables[l].begin(), tables[l].end(),
+              packed.begin() + static_cast<std::ptrdiff_t>(l * M * maxPages_));
+  std::size_t first = 0, last = packed.size();
+  while (first < last && packed[first] == tableShadow_[first]) ++first;
+  while (last > first && packed[last - 1] == tableShadow_[last - 1]) --last;
+  if (first < last) {
+    auto error = tables_->writeRaw(packed.data() + first, last - first, first);
+    if (!error.empty()) return error;
+    tableShadow_ = std::move(packed);
+  }
+  return {};
+}
+
+BatchedDecodeRun BatchedDecodeExecutor::run(const std::vector<float>& tokenIds,
+                                            const std::vector<float>& validLengths,
+                                            const std::vector<std::vector<float>>& blockTables,
+                                            bool readLogits) {
+  std::vector<std::int32_t> tokens(tokenIds.begin(), tokenIds.end());
+  std::vector<std::int32_t> lengths(validLengths.begin(), validLengths.end());
+  std::vector<std::vector<std::int32_t>> tables;
+  tables.reserve(blockTables.size());
+  for (const auto& table : blockTables) tables.emplace_back(table.begin(), table.end());
+  return run(tokens, lengths, tables, readLogits, true);
+}
+
+BatchedDecodeRun BatchedDecodeExecutor::run(const std::vector<std::int32_t>& tokenIds,
+                                            const std::vector<std::int32_t>& validLengths,
+                                            const std::vector<std::vector<std::int32_t>>& blockTables,
+                                            bool readLogits, bool timeGpu) {
+  BatchedDecodeRun result;
+  const auto& plan = model_->plan;
+  const std::size_t rows = tokenIds.size();
+  if (rows == 0 || rows > maximumBatchSize_ || validLengths.size() != rows ||
+      blockTables.size() != plan.layerCount) {
+    result.errorMessage = "Batched decode metadata shape is invalid.";
+    return result;
+  }
+  for (std::size_t l = 0; l < blockTables.size(); ++l) {
+    if (blockTables[l].size() != rows * maxPages_) {
+      result.errorMessage = "Batched decode block-table shape is invalid.";
+      return result;
+    }
+  }
+  // Host checks that keep every device access inside its buffer: token ids in
+  // the vocabulary, lengths in [1, capacity], pages allocated in their pool
+  // and present for every attended position.
+  for (std::size_t r = 0; r < rows; ++r) {
+    if (tokenIds[r] < 0 || static_cast<std::size_t>(tokenIds[r]) >= plan.vocabularySize) {
+      result.errorMessage = "Batched decode token id is outside the vocabulary.";
+      return result;
+    }
+    if (validLengths[r] <= 0 || static_cast<std::size_t>(validLengths[r]) > plan.attention.capacity) {
+      result.errorMessage = "KV cache valid length is outside the configured capacity.";
+      return result;
+    }
+    const std::size_t needed = (static_cast<std::size_t>(validLengths[r]) + pageSize_ - 1) / pageSize_;
+    for (std::size_t l = 0; l < blockTables.size(); ++l) {
+      for (std::size_t p = 0; p < maxPages_; ++p) {
+        const std::int32_t page = blockTables[l][r * maxPages_ + p];
+        if ((p < needed && !pools_[l]->isAllocated(page)) || (page >= 0 && !pools_[l]->isAllocated(page))) {
+          result.errorMessage = "Batched decode block table names a page that is not allocated "
+                                "in its layer's pool.";
+          return result;
+        }
+      }
+    }
+  }
+  std::size_t index = 0;
+  while (buckets_[index]->rows < rows) ++index;
+  auto& bucket = *buckets_[index];
+  auto error = upload(tokenIds, validLengths, blockTables, rows, bucket.rows);
+  if (!error.empty()) {
+    result.errorMessage = error;
+    return result;
+  }
+  if (timeGpu) {
+    const auto execution = bucket.sequence->execute();
+    if (!execution.executionPassed) {
+      result.errorMessage = execution.errorMessage;
+      return result;
+    }
+    result.gpuExecutionTimeUs = execution.gpuExecutionTimeUs;
+    result.cpuSubmitToCompletionTimeUs = execution.cpuSubmitToCompletionTimeUs;
+  } else {
+    error = bucket.sequence->launch();
+    if (!error.empty()) {
+      result.errorMessage = error;
+      return result;
+    }
+  }
+  std::vector<std::int32_t> next(rows);
+  error = nextTokens_->readRaw(next.data(), rows);  // waits for the stream
+  if (!error.empty()) {
+    result.errorMessage = error;
+    return result;
+  }
+  result.nextTokenIds.assign(next.begin(), next.end());
+  if (readLogits) {
+    result.logits.resize(rows * plan.vocabularySize);
+    error = logits_->readRaw(result.logits.data(), result.logits.size());
+    if (!error.empty()) {
+      result.errorMessage = error;
+      return result;
+    }
+  }
+  result.passed = true;
+  return result;
+}
+
+// --------------------------------------------------------- CompiledDecoderLLM
+class CompiledDecoderLLM::Impl {
+ public:
+  hip::HipRuntime* runtime = nullptr;
+  planner::DecoderLLMPlan plan;
+  std::shared_ptr<DecoderLLMModelResources> model;
+  std::vector<std::shared_ptr<KVPagePool>> pools;
+  std::vector<std::unique_ptr<KVCacheState>> states;
+  std::unique_ptr<BatchedDecodeExecutor> executor;
+  std::size_t requestedPageSize = 0;
+  std::size_t kvBytes = 0;
+
+  [[nodiscard]] std::size_t currentLength() const noexcept {
+    return states.empty() ? 0 : states.front()->currentLength();
+  }
+
+  std::vector<std::vector<std::int32_t>> tables() const {
+    std::vector<std::vector<std::int32_t>> out;
+    out.reserve(states.size());
+    for (const auto& state : states) {
+      auto table = state->pageTable();
+      table.resize(executor->maxPages(), -1);
+      out.push_back(std::move(table));
+    }
+    return out;
+  }
+
+  std::string stage(std::size_t length) {
+    const std::size_t previous = currentLength();
+    for (auto& state : states) {
+      const auto error = state->stageLength(*runtime, length);
+      if (!error.empty()) {
+        for (auto& staged : states) (void)staged->rollbackLength(*runtime, previous);
+        return error;
+      }
+    }
+    return {};
+  }
+
+  DecoderLLMRunResult step(float token, bool readLogits) {
+    DecoderLLMRunResult result;
+    const std::size_t previous = currentLength();
+    const std::size_t next = previous + 1;
+    if (next > plan.attention.capacity) {
+      result.errorMessage = "Decoder KV cache capacity has been reached.";
+      return result;
+    }
+    auto error = stage(next);
+    if (!error.empty()) {
+      result.errorMessage = error;
+      return result;
+    }
+    const auto run = executor->run({static_cast<std::int32_t>(token)},
+                                   {static_cast<std::int32_t>(next)}, tables(), readLogits, true);
+    if (!run.passed) {
+      for (auto& state : states) (void)state->rollbackLength(*runtime, previous);
+      result.errorMessage = run.errorMessage;
+      return result;
+    }
+    for (auto& state : states) state->commitLength(next);
+    result.passed = true;
+    result.logits = run.logits;
+    result.nextTokenIds = run.nextTokenIds;
+    result.gpuExecutionTimeUs = run.gpuExecutionTimeUs;
+    result.cpuSubmitToCompletionTimeUs = run.cpuSubmitToCompletionTimeUs;
+    return result;
+  }
+};
+
+CompiledDecoderLLM::CompiledDecoderLLM(std::unique_ptr<Impl> impl) : impl_(std::move(impl)) {}
+CompiledDecoderLLM::~CompiledDecoderLLM() = default;
+
+std::string CompiledDecoderLLM::reset() {
+  for (auto& state : impl_->states) {
+    const auto error = state->reset(*impl_->runtime);
+    if (!error.empty()) return error;
+  }
+  return {};
+}
+
+DecoderLLMRunResult CompiledDecoderLLM::prefill(const std::vector<float>& tokenIds,
+                                                bool readLogits) {
+  DecoderLLMRunResult result;
+  if (currentLength() != 0) {
+    result.errorMessage = "Decoder prefill requires an empty cache; call reset first.";
+    return result;
+  }
+  if (tokenIds.empty() || tokenIds.size() > impl_->plan.attention.capacity) {
+    result.errorMessage = "Decoder prefill length is outside the cache capacity.";
+    return result;
+  }
+  double gpu = 0.0;
+  bool timed = true;
+  for (std::size_t i = 0; i < tokenIds.size(); ++i) {
+    auto step = impl_->step(tokenIds[i], readLogits);
+    if (!step.passed) {
+      (void)reset();
+      return step;
+    }
+    if (readLogits)
+      result.logits.insert(result.logits.end(), step.logits.begin(), step.logits.end());
+    result.nextTokenIds = step.nextTokenIds;
+    result.cpuSubmitToCompletionTimeUs += step.cpuSubmitToCompletionTimeUs;
+    if (step.gpuExecutionTimeUs) gpu += *step.gpuExecutionTimeUs; else timed = false;
+  }
+  if (timed) result.gpuExecutionTimeUs = gpu;
+  result.passed = true;
+  return result;
+}
+
+DecoderLLMRunResult CompiledDecoderLLM::decode(const std::vector<float>& tokenIds,
+                                               bool readLogits) {
+  DecoderLLMRunResult result;
+  if (currentLength() == 0) {
+    result.errorMessage = "Decoder decode requires a completed prefill.";
+    return result;
+  }
+  if (currentLength() >= impl_->plan.attention.capacity) {
+    result.errorMessage = "Decoder KV cache capacity has been reached.";
+    return result;
+  }
+  if (tokenIds.size() != 1) {
+    result.errorMessage = "Decoder token input shape does not match the compiled stage.";
+    return result;
+  }
+  return impl_->step(tokenIds.front(), readLogits);
+}
+
+std::size_t CompiledDecoderLLM::currentLength() const noexcept { return impl_->currentLength(); }
+
+std::vector<float> CompiledDecoderLLM::readKeyPrefix(std::size_t layer) const {
+  if (layer >= impl_->states.size()) throw std::out_of_range("Decoder layer index is out of range.");
+  return impl_->states[layer]->readKeyPrefix();
+}
+
+std::vector<float> CompiledDecoderLLM::readValuePrefix(std::size_t layer) const {
+  if (layer >= impl_->states.size()) throw std::out_of_range("Decoder layer index is out of range.");
+  return impl_->states[layer]->readValuePrefix();
+}
+
+bool CompiledDecoderLLM::cacheStorageReused() const noexcept {
+  for (const auto& state : impl_->states)
+    if (!state->storageReused()) return false;
+  return true;
+}
+
+bool CompiledDecoderLLM::usesPagedKVCache() const noexcept { return impl_->requestedPageSize != 0; }
+
+std::size_t CompiledDecoderLLM::kvPageSize() const noexcept { return impl_->requestedPageSize; }
+
+std::size_t CompiledDecoderLLM::allocatedKVPageCount() const noexcept {
+  return usesPagedKVCache() && !impl_->states.empty() ? impl_->states.front()->allocatedPageCount()
+                                                      : 0;
+}
+
+std::size_t CompiledDecoderLLM::modelStorageBytes() const noexcept {
+  return impl_->model->storageBytes;
+}
+
+std::size_t CompiledDecoderLLM::kvStorageBytes() const noexcept { return impl_->kvBytes; }
+
+std::size_t CompiledDecoderLLM::activationStorageBytes() const noexcept {
+  return impl_->executor->activationStorageBytes();
+}
+
+std::shared_ptr<DecoderLLMModelResources> CompiledDecoderLLM::sharedModelResources()
+    const noexcept {
+  return impl_->model;
+}
+
+std::vector<std::int32_t> CompiledDecoderLLM::kvBlockTable(std::size_t layer) const {
+  if (layer >= impl_->states.size()) throw std::out_of_range("Decoder layer index is out of range.");
+  return impl_->states[layer]->pageTable();
+}
+
+DecoderKVSnapshot CompiledDecoderLLM::snapshotKVCache() const {
+  DecoderKVSnapshot snapshot;
+  snapshot.length = currentLength();
+  for (const auto& state : impl_->states) {
+    snapshot.keyCaches.push_back(state->readKeyPrefix());
+    snapshot.valueCaches.push_back(state->readValuePrefix());
+  }
+  return snapshot;
+}
+
+std::string CompiledDecoderLLM::releaseKVCache() { return reset(); }
+
+std::string CompiledDecoderLLM::restoreKVCache(const DecoderKVSnapshot& snapshot) {
+  if (currentLength() != 0) return "Decoder KV restore requires an empty cache.";
+  if (snapshot.length == 0 || snapshot.keyCaches.size() != impl_->states.size() ||
+      snapshot.valueCaches.size() != impl_->states.size())
+    return "Decoder KV snapshot does not match the compiled model.";
+  for (std::size_t l = 0; l < impl_->states.size(); ++l) {
+    const auto error = impl_->states[l]->restore(*impl_->runtime, snapshot.length,
+                                                 snapshot.keyCaches[l], snapshot.valueCaches[l]);
+    if (!error.empty()) {
+      for (auto& state : impl_->states) (void)state->reset(*impl_->runtime);
+      return error;
+    }
+  }
+  return {};
+}
+
+std::string CompiledDecoderLLM::stageKVLength(std::size_t length) { return impl_->stage(length); }
+
+void CompiledDecoderLLM::commitKVLength(std::size_t length) {
+  for (auto& state : impl_->states) state->commitLength(length);
+}
+
+std::string CompiledDecoderLLM::rollbackKVLength(std::size_t length) {
+  std::string first;
+  for (auto& state : impl_->states) {
+    const auto error = state->rollbackLength(*impl_->runtime, length);
+    if (first.empty()) first = error;
+  }
+  return first;
+}
+
+DecoderLLMCompilation compileDecoderLLM(hip::HipRuntime& runtime,
+                                        const DecoderLLMWorkload& workload, std::ostream& log,
+                                        const DecoderLLMCompileOptions& options) {
+  DecoderLLMCompilation result;
+  try {
+    if (!runtime.isAvailable()) throw std::runtime_error(runtime.initializationError());
+    if (options.storageDtype != DType::Float16)
+      throw std::invalid_argument("The gfx950 decoder path stores weights and caches in fp16.");
+    auto impl = std::make_unique<CompiledDecoderLLM::Impl>();
+    impl->runtime = &runtime;
+    impl->plan = workload.plan;
+    impl->plan.attention.dtype = DType::Float16;
+    impl->plan.validate();
+    if (impl->plan.attention.batch != 1)
+      throw std::invalid_argument("CompiledDecoderLLM runs one request; use the batched executor.");
+    if (options.sharedModelResources) {
+      const auto& shared = options.sharedModelResources;
+      if (shared->layerCount != impl->plan.layerCount || shared->hiddenSize != impl->plan.hiddenSize() ||
+          shared->headCount != impl->plan.attention.heads ||
+          shared->kvHeadCount != impl->plan.kvHeads() ||
+          shared->headDimension != impl->plan.attention.headDimension ||
+          shared->cacheCapacity != impl->plan.attention.capacity ||
+          shared->intermediateSize != impl->plan.intermediateSize ||
+          shared->vocabularySize != impl->plan.vocabularySize)
+        throw std::invalid_argument("Shared model resources do not match the decoder plan.");
+      impl->model = shared;
+    } else {
+      auto created = createModelResources(runtime, workload);
+      if (!created.resources) throw std::runtime_error(created.errorMessage);
+      impl->model = std::move(created.resources);
+    }
+    const auto kvPlan = impl->plan.kvPlan();
+    impl->requestedPageSize = options.kvPageSize;
+    if (!options.sharedKVPools.empty()) {
+      if (options.kvPageSize == 0 || options.sharedKVPools.size() != impl->plan.layerCount)
+        throw std::invalid_argument("Shared KV pools need a page size and one pool per layer.");
+      for (const auto& pool : options.sharedKVPools)
+        if (!pool || pool->pageSize() != options.kvPageSize)
+          throw std::invalid_argument("Shared KV pool page size differs from the options.");
+      impl->pools = options.sharedKVPools;
+    } else {
+      // kvPageSize 0: one page of `capacity` tokens, which is the contiguous
+      // [heads][capacity][D] layout of the reference's unpaged cache.
+      const std::size_t pageSize = options.kvPageSize ? options.kvPageSize : kvPlan.capacity;
+      const std::size_t pages = (kvPlan.capacity + pageSize - 1) / pageSize;
+      for (std::size_t l = 0; l < impl->plan.layerCount; ++l) {
+        auto pool = createKVPagePool(runtime, kvPlan, pageSize, pages);
+        if (!pool.pool) throw std::runtime_error(pool.errorMessage);
+        impl->kvBytes += 2 * pool.pool->keyBuffer()->storageBytes();
+        impl->pools.push_back(std::move(pool.pool));
+      }
+    }
+    for (const auto& pool : impl->pools) {
+      auto state = createKVCacheState(runtime, kvPlan, pool, false);
+      if (!state.state) throw std::runtime_error(state.errorMessage);
+      impl->states.push_back(std::move(state.state));
+    }
+    auto executor = createBatchedDecodeExecutor(runtime, impl->model, impl->pools, 1, &log);
+    if (!executor.executor) throw std::runtime_error(executor.errorMessage);
+    impl->executor = std::move(executor.executor);
+    log << "Decoder compile: layers=" << impl->plan.layerCount
+        << ", kv_page_size=" << options.kvPageSize << ", dispatches/token="
+        << impl->executor->dispatchesPerStep(1) << '\n';
+    result.executable.reset(new CompiledDecoderLLM(std::move(impl)));
+  } catch (const std::exception& error) {
+    result.errorMessage = error.what();
+  }
+  return result;
+}
+
+}  // namespace runtime
+}  // namespace tensor

@@ -1,0 +1,311 @@
+// Decoder-LLM decode path on gfx950: model resources, the batched decode
+// executor and the single-request CompiledDecoderLLM.
+//
+// Interfaces follow the reference:
+//   planner::DecoderLLMPlan           src/planner/DecoderLLMPlan.hpp:9-23
+//   DecoderLLMWorkload / parameters   src/tensor/DecoderLLM.hpp:10-44
+//   DecoderLLMModelResources          src/runtime/DecoderLLMModelResources.hpp:10-41
+//   CompiledDecoderLLM / compile      src/runtime/DecoderLLMExecutor.hpp:16-102
+//   BatchedDecodeExecutor             src/runtime/ServingRuntime.cpp:119-407
+//
+// One decode step for m rows (rows >= active count are padding and leave the
+// caches alone) runs, per layer l, as gfx950 kernels:
+//   l == 0: embedding, RMSNorm                    -> x, n
+//   l  > 0: Add+RMSNorm(after, mlp)               -> x = h(after + mlp), n
+//   fused q|k|v GEMV [(QH+2KVH)*D, H]             -> qkv
+//   RoPE(q, k) + paged append of k and v          -> q, pools
+//   paged decode attention over [0, valid)        -> ctx
+//   o GEMV, Add+RMSNorm(x, o)                     -> after = h(x + o), n
+//   gate/up GEMV + SiLU*Mul, down GEMV            -> mlp
+// then Add+RMSNorm with the final norm, the LM-head GEMV (fp32 logits) and
+// argmax.  Every kernel output is stored in the storage dtype (fp16) before
+// the next kernel reads it, as in DecoderLLMExecutor.cpp:322-849.  The whole
+// step for one bucket of rows is captured once into a HIP graph.
+#pragma once
+
+#include "HipRuntime.hpp"
+#include "KVCacheState.hpp"
+
+#include <cstddef>
+#include <cstdint>
+#include <iosfwd>
+#include <memory>
+#include <optional>
+#include <string>
+#include <vector>
+
+namespace tensor {
+
+namespace planner {
+
+struct DecoderLLMPlan {
+  KVCachePlan attention;  // heads = query heads; batch = rows per step
+  std::size_t layerCount = 1;
+  std::size_t intermediateSize = 1;
+  std::size_t vocabularySize = 1;
+  float rmsNormEpsilon = 1e-5f;
+  DType accumulationDtype = DType::Float32;
+  // Grouped-query attention (an extension of the reference plan): key/value
+  // heads, 0 = attention.heads.  attention.heads must be a multiple of it.
+  std::size_t keyValueHeads = 0;
+
+  [[nodiscard]] std::size_t hiddenSize() const;
+  [[nodiscard]] std::size_t kvHeads() const noexcept {
+    return keyValueHeads ? keyValueHeads : attention.heads;
+  }
+  [[nodiscard]] std::size_t kvWidth() const noexcept { return kvHeads() * attention.headDimension; }
+  [[nodiscard]] std::size_t hiddenElementCount(std::size_t sequenceLength) const;
+  [[nodiscard]] std::size_t intermediateElementCount(std::size_t sequenceLength) const;
+  [[nodiscard]] std::size_t logitsElementCount(std::size_t sequenceLength) const;
+  // DecoderLLMPlan.cpp:40-58 plus the GQA and fp16-storage rules of this
+  // backend; throws std::invalid_argument.
+  void validate() const;
+  // KV plan of one layer's pool: one request, kvHeads heads.
+  [[nodiscard]] KVCachePlan kvPlan() const;
+};
+
+}  // namespace planner
+
+// Host weights as floats (values representable in the storage dtype), nn.Linear
+// layout [out, in].  key/value weights are [kvHeads*D, hidden].
+struct DecoderLLMLayerParameters {
+  std::vector<float> inputNormWeight;
+  std::vector<float> queryWeight;
+  std::vector<float> keyWeight;
+  std::vector<float> valueWeight;
+  std::vector<float> outputWeight;
+  std::vector<float> postAttentionNormWeight;
+  std::vector<float> gateWeight;
+  std::vector<float> upWeight;
+  std::vector<float> downWeight;
+};
+
+struct DecoderLLMWorkload {
+  std::string modelName;
+  planner::DecoderLLMPlan plan;
+  std::size_t decodeCount = 0;
+  std::vector<float> embeddingWeight;
+  std::vector<float> finalNormWeight;
+  std::vector<float> languageModelHeadWeight;
+  std::vector<float> ropeCosine;  // [capacity, head_dim/2]
+  std::vector<float> ropeSine;
+  std::vector<DecoderLLMLayerParameters> layers;
+};
+
+// RoPE tables as in workloads/pytorch/decoder_llm.py:48-55 (angle =
+// position * theta^(-2i/D), evaluated in double, stored as fp32).
+void ropeTables(std::size_t capacity, std::size_t headDimension, double theta,
+                std::vector<float>& cosine, std::vector<float>& sine);
+
+namespace runtime {
+
+struct DecoderLLMModelLayerBuffers {
+  hip::BufferHandle inputNormWeight;
+  hip::BufferHandle queryKeyValueWeight;  // rows: q (QH*D) | k (KVH*D) | v (KVH*D)
+  hip::BufferHandle outputWeight;
+  hip::BufferHandle postAttentionNormWeight;
+  hip::BufferHandle gateWeight;
+  hip::BufferHandle upWeight;
+  hip::BufferHandle downWeight;
+};
+
+// Immutable device model shared by every executor of one runtime.
+struct DecoderLLMModelResources {
+  DType storageDtype = DType::Float16;
+  planner::DecoderLLMPlan plan;
+  std::size_t hiddenSize = 0;
+  std::size_t headCount = 0;
+  std::size_t kvHeadCount = 0;
+  std::size_t headDimension = 0;
+  std::size_t cacheCapacity = 0;
+  std::size_t intermediateSize = 0;
+  std::size_t vocabularySize = 0;
+  std::size_t layerCount = 0;
+  std::size_t storageBytes = 0;
+  hip::BufferHandle embeddingWeight;
+  hip::BufferHandle finalNormWeight;
+  hip::BufferHandle languageModelHeadWeight;
+  hip::BufferHandle ropeCosine;
+  hip::BufferHandle ropeSine;
+  std::vector<DecoderLLMModelLayerBuffers> layers;
+};
+
+struct ModelResourcesCreation {
+  std::shared_ptr<DecoderLLMModelResources> resources;
+  std::string errorMessage;
+};
+
+// Upload a workload's weights (fp16 storage; q, k, v fused row-wise).
+[[nodiscard]] ModelResourcesCreation createModelResources(hip::HipRuntime& runtime,
+                                                          const DecoderLLMWorkload& workload);
+// Random-init weights on the device: every matrix and the embedding
+// ~ N(0, stddev) from seed + tensor index, norm weights 1, RoPE tables with
+// `theta`.  No host copy of the weights is made.
+[[nodiscard]] ModelResourcesCreation createSyntheticModelResources(
+    hip::HipRuntime& runtime, const planner::DecoderLLMPlan& plan, std::uint64_t seed,
+    float stddev = 0.02f, double theta = 10000.0);
+
+struct BatchedDecodeRun {
+  bool passed = false;
+  std::vector<float> logits;        // [rows, vocabulary] when requested
+  std::vector<float> nextTokenIds;  // [rows]
+  std::optional<double> gpuExecutionTimeUs;
+  double cpuSubmitToCompletionTimeUs = 0.0;
+  std::string errorMessage;
+};
+
+// Decode steps for up to maximumBatchSize rows over per-layer page pools.
+// Graphs are captured for row buckets 1, 2, 4, ... and maximumBatchSize; a
+// step runs the smallest bucket that holds its rows.
+class BatchedDecodeExecutor {
+ public:
+  struct Creation;
+  ~BatchedDecodeExecutor();
+  BatchedDecodeExecutor(const BatchedDecodeExecutor&) = delete;
+  BatchedDecodeExecutor& operator=(const BatchedDecodeExecutor&) = delete;
+
+  // ServingRuntime.cpp:155-226: tokens and valid lengths per row, block
+  // tables per layer as [rows * maxPages()] (-1 = no page).  The new token of
+  // row r lands at position validLengths[r] - 1.
+  [[nodiscard]] BatchedDecodeRun run(const std::vector<float>& tokenIds,
+                                     const std::vector<float>& validLengths,
+                                     const std::vector<std::vector<float>>& blockTables,
+                                     bool readLogits = true);
+  [[nodiscard]] BatchedDecodeRun run(const std::vector<std::int32_t>& tokenIds,
+                                     const std::vector<std::int32_t>& validLengths,
+                                     const std::vector<std::vector<std::int32_t>>& blockTables,
+                                     bool readLogits = true, bool timeGpu = false);
+
+  [[nodiscard]] std::size_t maximumBatchSize() const noexcept { return maximumBatchSize_; }
+  [[nodiscard]] std::size_t maxPages() const noexcept { return maxPages_; }
+  [[nodiscard]] std::size_t activationStorageBytes() const noexcept { return activationBytes_; }
+  [[nodiscard]] std::vector<std::size_t> buckets() const;
+  [[nodiscard]] std::size_t dispatchesPerStep(std::size_t bucket) const;
+  [[nodiscard]] const std::vector<std::shared_ptr<KVPagePool>>& pools() const noexcept {
+    return pools_;
+  }
+
+ private:
+  friend struct Creation;
+  friend Creation createBatchedDecodeExecutor(hip::HipRuntime&,
+                                              std::shared_ptr<DecoderLLMModelResources>,
+                                              std::vector<std::shared_ptr<KVPagePool>>,
+                                              std::size_t, std::ostream*);
+  BatchedDecodeExecutor() = default;
+  void build(std::ostream* log);
+  [[nodiscard]] std::string upload(const std::vector<std::int32_t>& tokens,
+                                   const std::vector<std::int32_t>& lengths,
+                                   const std::vector<std::vector<std::int32_t>>& tables,
+                                   std::size_t rows, std::size_t bucket);
+
+  struct Bucket;
+  hip::HipRuntime* runtime_ = nullptr;
+  std::shared_ptr<DecoderLLMModelResources> model_;
+  std::vector<std::shared_ptr<KVPagePool>> pools_;
+  std::size_t maximumBatchSize_ = 0;
+  std::size_t pageSize_ = 0;
+  std::size_t maxPages_ = 0;
+  std::size_t activationBytes_ = 0;
+  // Device buffers sized for maximumBatchSize rows.
+  hip::BufferHandle meta_;    // int32 [tokens M | lengths M | active 1]
+  hip::BufferHandle tables_;  // int32 [layers][M][maxPages]
+  hip::BufferHandle tokensView_, lengthsView_, activeView_;
+  std::vector<hip::BufferHandle> tableViews_;
+  hip::BufferHandle residual_, after_, normalized_, qkv_, query_, context_, projected_, gated_,
+      mlp_, logits_, nextTokens_;
+  std::vector<std::unique_ptr<Bucket>> buckets_;
+  std::vector<std::int32_t> metaShadow_, tableShadow_;
+};
+
+struct BatchedDecodeExecutor::Creation {
+  std::unique_ptr<BatchedDecodeExecutor> executor;
+  std::string errorMessage;
+};
+
+[[nodiscard]] BatchedDecodeExecutor::Creation createBatchedDecodeExecutor(
+    hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
+    std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t maximumBatchSize,
+    std::ostream* log = nullptr);
+
+struct DecoderLLMCompileOptions {
+  std::size_t kvPageSize = 0;  // 0 = contiguous cache (one page of `capacity`)
+  std::vector<std::shared_ptr<KVPagePool>> sharedKVPools;
+  DType storageDtype = DType::Float16;
+  std::shared_ptr<DecoderLLMModelResources> sharedModelResources;
+};
+
+struct DecoderKVSnapshot {
+  std::size_t length = 0;
+  std::vector<std::vector<float>> keyCaches;    // per layer [kvHeads][length][D]
+  std::vector<std::vector<float>> valueCaches;
+};
+
+struct DecoderLLMRunResult {
+  bool passed = false;
+  std::vector<float> logits;
+  std::vector<float> nextTokenIds;
+  std::optional<double> gpuExecutionTimeUs;
+  double cpuSubmitToCompletionTimeUs = 0.0;
+  std::string errorMessage;
+};
+
+struct DecoderLLMCompilation;
+
+// One request (batch 1): per-layer KV states over private or shared pools
+// and a one-row batched decode executor.  prefill() runs the prompt through
+// decode steps, one token per step (identical results to a causal prefill:
+// each position sees exactly the positions before it).
+class CompiledDecoderLLM {
+ public:
+  ~CompiledDecoderLLM();
+  CompiledDecoderLLM(const CompiledDecoderLLM&) = delete;
+  CompiledDecoderLLM& operator=(const CompiledDecoderLLM&) = delete;
+
+  [[nodiscard]] std::string reset();
+  [[nodiscard]] DecoderLLMRunResult prefill(const std::vector<float>& tokenIds,
+                                            bool readLogits = true);
+  [[nodiscard]] DecoderLLMRunResult decode(const std::vector<float>& tokenIds,
+                                           bool readLogits = true);
+
+  [[nodiscard]] std::size_t currentLength() const noexcept;
+  [[nodiscard]] std::vector<float> readKeyPrefix(std::size_t layer) const;
+  [[nodiscard]] std::vector<float> readValuePrefix(std::size_t layer) const;
+  [[nodiscard]] bool cacheStorageReused() const noexcept;
+  [[nodiscard]] bool usesPagedKVCache() const noexcept;
+  [[nodiscard]] std::size_t kvPageSize() const noexcept;
+  [[nodiscard]] std::size_t allocatedKVPageCount() const noexcept;
+  [[nodiscard]] DType storageDtype() const noexcept { return DType::Float16; }
+  [[nodiscard]] std::size_t modelStorageBytes() const noexcept;
+  [[nodiscard]] std::size_t kvStorageBytes() const noexcept;
+  [[nodiscard]] std::size_t activationStorageBytes() const noexcept;
+  [[nodiscard]] std::shared_ptr<DecoderLLMModelResources> sharedModelResources() const noexcept;
+  [[nodiscard]] std::vector<std::int32_t> kvBlockTable(std::size_t layer) const;
+  [[nodiscard]] DecoderKVSnapshot snapshotKVCache() const;
+  [[nodiscard]] std::string releaseKVCache();
+  [[nodiscard]] std::string restoreKVCache(const DecoderKVSnapshot& snapshot);
+  [[nodiscard]] std::string stageKVLength(std::size_t length);
+  void commitKVLength(std::size_t length);
+  [[nodiscard]] std::string rollbackKVLength(std::size_t length);
+
+ private:
+  class Impl;
+  explicit CompiledDecoderLLM(std::unique_ptr<Impl> impl);
+  friend DecoderLLMCompilation compileDecoderLLM(hip::HipRuntime&, const DecoderLLMWorkload&,
+                                                 std::ostream&, const DecoderLLMCompileOptions&);
+  std::unique_ptr<Impl> impl_;
+};
+
+struct DecoderLLMCompilation {
+  std::unique_ptr<CompiledDecoderLLM> executable;
+  std::string errorMessage;
+};
+
+// compileDecoderLLM (DecoderLLMExecutor.cpp:1100-1441): model weights come
+// from options.sharedModelResources when given, else from the workload.
+[[nodiscard]] DecoderLLMCompilation compileDecoderLLM(hip::HipRuntime& runtime,
+                                                      const DecoderLLMWorkload& workload,
+                                                      std::ostream& log,
+                                                      const DecoderLLMCompileOptions& options = {});
+
+}  // namespace runtime
+}  // namespace tensor

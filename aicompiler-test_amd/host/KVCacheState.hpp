@@ -1,0 +1,218 @@
+// Paged KV storage for the gfx950 decode path: KVPagePool and KVCacheState,
+// with the interface of the reference's src/runtime/KVCacheState.hpp:13-142
+// over HipRuntime buffers.
+//
+// Device layout (one pool pair per decoder layer):
+//   key/value pool   [page][heads][page_size][head_dim]   storage dtype
+//   length buffer    int32 [1]                           valid length
+//   block table      int32 [ceil(capacity / page_size)]  physical page or -1
+// A page is one contiguous slab of heads*page_size*head_dim elements, so a
+// request's pages move to and from the host with one copy each.
+//
+// Pool bookkeeping follows KVCacheState.cpp:30-90: a LIFO free list that
+// starts as 0..N-1 (allocation pops the back, release pushes back), peak /
+// allocation / release counters, and errors for releasing a page that is not
+// allocated.  A pool created without a runtime (createHostKVPagePool) keeps
+// the bookkeeping only; states over it skip every device write, which is how
+// the CPU tests exercise the host logic.
+#pragma once
+
+#include "HipRuntime.hpp"
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace tensor {
+
+// TensorIR DType (reference src/tensor/TensorIR.hpp:13); codes equal tmc_dtype.
+enum class DType { Float16 = 0, Float32 = 1, BFloat16 = 2, Int32 = 3 };
+
+[[nodiscard]] const char* dtypeName(DType dtype) noexcept;
+[[nodiscard]] std::size_t dtypeStorageBytes(DType dtype) noexcept;
+
+namespace planner {
+
+// planner::KVCachePlan (reference src/planner/KVCachePlan.hpp:9-23).
+struct KVCachePlan {
+  std::size_t batch = 1;
+  std::size_t heads = 1;
+  std::size_t headDimension = 1;
+  std::size_t capacity = 1;
+  std::size_t prefillLength = 1;
+  DType dtype = DType::Float32;
+  std::size_t threadsPerThreadgroup = 128;
+
+  [[nodiscard]] std::size_t modelDimension() const;
+  [[nodiscard]] std::size_t cacheElementCount() const;
+  [[nodiscard]] std::size_t inputElementCount(std::size_t sequenceLength) const;
+  // KVCachePlan.cpp:31-54; throws std::invalid_argument.
+  void validate() const;
+};
+
+}  // namespace planner
+
+namespace runtime {
+
+class KVPagePool;
+class KVCacheState;
+
+struct KVPagePoolCreation {
+  std::shared_ptr<KVPagePool> pool;
+  std::string errorMessage;
+};
+
+struct KVCacheStateCreation {
+  std::unique_ptr<KVCacheState> state;
+  std::string errorMessage;
+};
+
+// createKVPagePool (KVCacheState.cpp:92-123): device pools for one layer.
+[[nodiscard]] KVPagePoolCreation createKVPagePool(hip::HipRuntime& runtime,
+                                                  const planner::KVCachePlan& plan,
+                                                  std::size_t pageSize,
+                                                  std::size_t physicalPageCount);
+// Bookkeeping-only pool (no device storage).
+[[nodiscard]] KVPagePoolCreation createHostKVPagePool(const planner::KVCachePlan& plan,
+                                                      std::size_t pageSize,
+                                                      std::size_t physicalPageCount);
+
+class KVPagePool {
+ public:
+  KVPagePool(const KVPagePool&) = delete;
+  KVPagePool& operator=(const KVPagePool&) = delete;
+
+  [[nodiscard]] std::size_t pageSize() const noexcept { return pageSize_; }
+  [[nodiscard]] std::size_t capacityPages() const noexcept { return allocated_.size(); }
+  [[nodiscard]] std::size_t usedPages() const noexcept {
+    return allocated_.size() - freePages_.size();
+  }
+  [[nodiscard]] std::size_t availablePages() const noexcept { return freePages_.size(); }
+  [[nodiscard]] std::size_t peakUsedPages() const noexcept { return peakUsedPages_; }
+  [[nodiscard]] std::size_t allocationCount() const noexcept { return allocationCount_; }
+  [[nodiscard]] std::size_t releaseCount() const noexcept { return releaseCount_; }
+  [[nodiscard]] const hip::BufferHandle& keyBuffer() const noexcept { return key_; }
+  [[nodiscard]] const hip::BufferHandle& valueBuffer() const noexcept { return value_; }
+  [[nodiscard]] const planner::KVCachePlan& plan() const noexcept { return plan_; }
+  // Elements of one page: heads * page_size * head_dim.
+  [[nodiscard]] std::size_t pageElements() const noexcept {
+    return plan_.batch * plan_.heads * pageSize_ * plan_.headDimension;
+  }
+  [[nodiscard]] bool hasStorage() const noexcept { return key_ != nullptr; }
+  [[nodiscard]] bool isAllocated(std::int32_t page) const noexcept {
+    return page >= 0 && static_cast<std::size_t>(page) < allocated_.size() &&
+           allocated_[static_cast<std::size_t>(page)];
+  }
+
+ private:
+  friend KVPagePoolCreation createKVPagePool(hip::HipRuntime&, const planner::KVCachePlan&,
+                                             std::size_t, std::size_t);
+  friend KVPagePoolCreation createHostKVPagePool(const planner::KVCachePlan&, std::size_t,
+                                                 std::size_t);
+  friend KVCacheStateCreation createKVCacheState(hip::HipRuntime&, const planner::KVCachePlan&,
+                                                 std::shared_ptr<KVPagePool>, bool);
+  friend class KVCacheState;
+  KVPagePool(planner::KVCachePlan plan, std::size_t pageSize, hip::BufferHandle key,
+             hip::BufferHandle value, std::size_t physicalPageCount);
+  [[nodiscard]] std::int32_t allocatePage();
+  void releasePage(std::int32_t page);
+  [[nodiscard]] bool compatible(const planner::KVCachePlan& plan) const noexcept;
+
+  planner::KVCachePlan plan_;
+  std::size_t pageSize_ = 0;
+  hip::BufferHandle key_;
+  hip::BufferHandle value_;
+  std::vector<std::int32_t> freePages_;
+  std::vector<bool> allocated_;
+  std::size_t peakUsedPages_ = 0;
+  std::size_t allocationCount_ = 0;
+  std::size_t releaseCount_ = 0;
+};
+
+// createKVCacheState (KVCacheState.cpp:381-447): pageSize 0 = contiguous
+// [batch][heads][capacity][head_dim] storage; otherwise a private pool that can
+// hold one request at full capacity.
+[[nodiscard]] KVCacheStateCreation createKVCacheState(hip::HipRuntime& runtime,
+                                                      const planner::KVCachePlan& plan,
+                                                      std::size_t pageSize = 0);
+// A request state over a shared pool.  Without `deviceMirror` the state keeps
+// its length and block table on the host only (lengthBuffer() and
+// blockTableBuffer() are null): batched executors that pack many requests'
+// tables into one device buffer use that form.
+[[nodiscard]] KVCacheStateCreation createKVCacheState(hip::HipRuntime& runtime,
+                                                      const planner::KVCachePlan& plan,
+                                                      std::shared_ptr<KVPagePool> pagePool,
+                                                      bool deviceMirror = true);
+
+class KVCacheState {
+ public:
+  ~KVCacheState();
+  KVCacheState(const KVCacheState&) = delete;
+  KVCacheState& operator=(const KVCacheState&) = delete;
+
+  [[nodiscard]] std::size_t currentLength() const noexcept { return currentLength_; }
+  [[nodiscard]] std::size_t capacity() const noexcept { return plan_.capacity; }
+  [[nodiscard]] std::string reset(hip::HipRuntime& runtime);
+  // Pages for `length` tokens are allocated (or released) and the block table
+  // and length are written; currentLength() moves only on commitLength().
+  [[nodiscard]] std::string stageLength(hip::HipRuntime& runtime, std::size_t length);
+  [[nodiscard]] std::string rollbackLength(hip::HipRuntime& runtime, std::size_t length);
+  // Paged only, empty state only: stage `length` and write the prefixes,
+  // laid out [batch][heads][length][head_dim].
+  [[nodiscard]] std::string restore(hip::HipRuntime& runtime, std::size_t length,
+                                    const std::vector<float>& keyPrefix,
+                                    const std::vector<float>& valuePrefix);
+  void commitLength(std::size_t length);
+
+  // [batch][heads][currentLength][head_dim] read back from the device.
+  [[nodiscard]] std::vector<float> readKeyPrefix() const;
+  [[nodiscard]] std::vector<float> readValuePrefix() const;
+  [[nodiscard]] bool storageReused() const noexcept;
+  [[nodiscard]] bool isPaged() const noexcept { return pageSize_ != 0; }
+  [[nodiscard]] std::size_t pageSize() const noexcept { return pageSize_; }
+  [[nodiscard]] std::size_t allocatedPageCount() const noexcept;
+  [[nodiscard]] std::vector<std::int32_t> pageTable() const;
+
+  [[nodiscard]] const hip::BufferHandle& keyBuffer() const noexcept { return key_; }
+  [[nodiscard]] const hip::BufferHandle& valueBuffer() const noexcept { return value_; }
+  [[nodiscard]] const hip::BufferHandle& lengthBuffer() const noexcept { return length_; }
+  [[nodiscard]] const hip::BufferHandle& blockTableBuffer() const noexcept { return blockTable_; }
+  [[nodiscard]] const std::shared_ptr<KVPagePool>& pagePool() const noexcept { return pagePool_; }
+
+ private:
+  friend KVCacheStateCreation createKVCacheState(hip::HipRuntime&, const planner::KVCachePlan&,
+                                                 std::size_t);
+  friend KVCacheStateCreation createKVCacheState(hip::HipRuntime&, const planner::KVCachePlan&,
+                                                 std::shared_ptr<KVPagePool>, bool);
+  KVCacheState(planner::KVCachePlan plan, hip::BufferHandle key, hip::BufferHandle value,
+               hip::BufferHandle length, hip::BufferHandle blockTable,
+               std::shared_ptr<KVPagePool> pagePool);
+  [[nodiscard]] std::vector<float> readPrefix(const hip::BufferHandle& buffer) const;
+  [[nodiscard]] std::string writeBlockTable(hip::HipRuntime& runtime);
+  [[nodiscard]] std::string writeLength(hip::HipRuntime& runtime, std::size_t length);
+  [[nodiscard]] std::string writePagedPrefix(hip::HipRuntime& runtime,
+                                             const hip::BufferHandle& buffer,
+                                             const std::vector<float>& prefix,
+                                             std::size_t length);
+  void resizePageAllocation(std::size_t pageCount);
+
+  planner::KVCachePlan plan_;
+  hip::BufferHandle key_;
+  hip::BufferHandle value_;
+  hip::BufferHandle length_;
+  hip::BufferHandle blockTable_;
+  const hip::HipBuffer* initialKey_ = nullptr;
+  const hip::HipBuffer* initialValue_ = nullptr;
+  std::size_t currentLength_ = 0;
+  std::size_t pageSize_ = 0;
+  std::shared_ptr<KVPagePool> pagePool_;
+  std::vector<std::int32_t> logicalToPhysical_;
+};
+
+// Host conversion of one fp16 value (exact).
+[[nodiscard]] float halfToFloat(std::uint16_t bits) noexcept;
+
+}  // namespace runtime
+}  // namespace tensor

@@ -1,0 +1,418 @@
+// Continuous-batching serving loop; see ServingRuntime.hpp.
+#include "ServingRuntime.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <limits>
+#include <optional>
+#include <ostream>
+#include <set>
+#include <stdexcept>
+
+namespace tensor::runtime {
+namespace {
+
+using Clock = std::chrono::steady_clock;
+
+double elapsedUs(Clock::time_point start, Clock::time_point end) {
+  return std::chrono::duration<double, std::micro>(end - start).count();
+}
+
+std::size_t pagesFor(std::size_t tokens, std::size_t pageSize) {
+  return tokens == 0 ? 0 : (tokens + pageSize - 1) / pageSize;
+}
+
+enum class RequestState { Waiting, Active, Preempted, Finished };
+
+struct Snapshot {
+  std::size_t length = 0;
+  std::vector<std::vector<float>> keys, values;
+};
+
+struct Request {
+  ServingRequestSpec spec;
+  std::vector<std::int32_t> prompt;
+  RequestState state = RequestState::Waiting;
+  ServingRequestOutput output;
+  std::vector<std::unique_ptr<KVCacheState>> states;  // one per layer
+  std::size_t consumed = 0;                            // prompt tokens in the cache
+  std::int32_t lastToken = -1;
+  std::size_t decoded = 0;
+  std::optional<Snapshot> snapshot;
+  std::optional<Clock::time_point> arrivalTime;
+
+  [[nodiscard]] std::size_t length() const { return states.front()->currentLength(); }
+  [[nodiscard]] std::size_t pages() const { return states.front()->allocatedPageCount(); }
+  // Pages the rest of the prompt will still allocate.
+  [[nodiscard]] std::size_t outstandingPromptPages(std::size_t pageSize) const {
+    if (state != RequestState::Active || consumed >= prompt.size()) return 0;
+    return pagesFor(prompt.size(), pageSize) - pagesFor(length(), pageSize);
+  }
+};
+
+std::size_t availablePages(const std::vector<std::shared_ptr<KVPagePool>>& pools) {
+  std::size_t available = std::numeric_limits<std::size_t>::max();
+  for (const auto& pool : pools) available = std::min(available, pool->availablePages());
+  return pools.empty() ? 0 : available;
+}
+
+std::size_t promisedPages(const std::vector<Request>& requests, std::size_t pageSize) {
+  std::size_t pages = 0;
+  for (const auto& r : requests) pages += r.outstandingPromptPages(pageSize);
+  return pages;
+}
+
+std::size_t activeCount(const std::vector<Request>& requests) {
+  return static_cast<std::size_t>(std::count_if(requests.begin(), requests.end(), [](const Request& r) {
+    return r.state == RequestState::Active;
+  }));
+}
+
+// auditPageIsolation (ServingRuntime.cpp:436-452).
+bool auditPageIsolation(const std::vector<Request>& requests, std::size_t layers,
+                        std::string& error) {
+  for (std::size_t l = 0; l < layers; ++l) {
+    std::set<std::int32_t> owners;
+    for (const auto& r : requests) {
+      if (r.state != RequestState::Active) continue;
+      for (const auto page : r.states[l]->pageTable()) {
+        if (!owners.insert(page).second) {
+          error = "Two active requests own the same physical KV page in layer " +
+                  std::to_string(l) + ".";
+          return false;
+        }
+      }
+    }
+  }
+  return true;
+}
+
+std::string releaseAll(hip::HipRuntime& runtime, Request& r) {
+  for (auto& state : r.states) {
+    const auto error = state->reset(runtime);
+    if (!error.empty()) return error;
+  }
+  return {};
+}
+
+}  // namespace
+
+ServingExecutionResult runContinuousBatch(hip::HipRuntime& runtime,
+                                          const planner::DecoderLLMPlan& plan,
+                                          const std::vector<std::shared_ptr<KVPagePool>>& pools,
+                                          std::size_t maximumBatchSize, std::size_t maxPages,
+                                          const BatchedStep& step,
+                                          const std::vector<ServingRequestSpec>& specs,
+                                          const ServingConfig& config, std::ostream& log) {
+  ServingExecutionResult result;
+  auto& metrics = result.metrics;
+  try {
+    if (specs.empty() || config.pageSize == 0 || config.physicalPagesPerLayer == 0)
+      throw std::invalid_argument("Serving configuration and requests must be nonempty.");
+    if (pools.size() != plan.layerCount || maximumBatchSize == 0)
+      throw std::invalid_argument("Serving needs one page pool per layer and a batch size.");
+    const std::size_t capacity = plan.attention.capacity, P = config.pageSize;
+    const auto kvPlan = plan.kvPlan();
+    std::size_t largest = 0;
+    std::vector<Request> requests;
+    requests.reserve(specs.size());
+    for (const auto& spec : specs) {
+      if (spec.id.empty() || spec.promptTokenIds.size() < 2 ||
+          spec.promptTokenIds.size() >= capacity ||
+          spec.decodeTokenCount > capacity - spec.promptTokenIds.size())
+        throw std::invalid_argument("Serving request dimensions are invalid.");
+      Request r;
+      r.spec = spec;
+      for (const float token : spec.promptTokenIds) {
+        if (!(token >= 0.0f) || token != std::floor(token) ||
+            token >= static_cast<float>(plan.vocabularySize))
+          throw std::invalid_argument("Serving request " + spec.id + " has an invalid token id.");
+        r.prompt.push_back(static_cast<std::int32_t>(token));
+      }
+      r.output.id = spec.id;
+      largest = std::max(largest, pagesFor(spec.promptTokenIds.size() + spec.decodeTokenCount, P));
+      requests.push_back(std::move(r));
+    }
+    if (config.physicalPagesPerLayer < largest || pools.front()->capacityPages() < largest)
+      throw std::invalid_argument("Shared KV pool cannot hold the largest configured request.");
+    for (auto& r : requests) {
+      for (const auto& pool : pools) {
+        auto state = createKVCacheState(runtime, kvPlan, pool, false);
+        if (!state.state) throw std::runtime_error(state.errorMessage);
+        r.states.push_back(std::move(state.state));
+      }
+      log << "Serving request " << r.spec.id << ": prompt=" << r.prompt.size()
+          << ", decode=" << r.spec.decodeTokenCount << ", arrival_step=" << r.spec.arrivalStep
+          << '\n';
+    }
+
+    std::vector<double> gpuTimes, hostTimes;
+    std::size_t completed = 0, tick = 0, batchSamples = 0, batchSum = 0;
+    std::size_t decodeRows = 0;
+    double decodeOnlyUs = 0.0;
+    const auto start = Clock::now();
+    auto finish = [&](Request& r) {
+      const auto kvStart = Clock::now();
+      const auto error = releaseAll(runtime, r);
+      metrics.kvManagementOverheadUs += elapsedUs(kvStart, Clock::now());
+      if (!error.empty()) throw std::runtime_error(error);
+      r.state = RequestState::Finished;
+      ++completed;
+      log << "Serving request " << r.spec.id << ": finished\n";
+    };
+
+    while (completed < requests.size()) {
+      if (tick > 10000000) throw std::runtime_error("Serving scheduler exceeded its progress limit.");
+      bool progress = false;
+
+      // Resume preempted requests whose snapshot fits.
+      for (auto& r : requests) {
+        const auto t0 = Clock::now();
+        const bool fits = r.state == RequestState::Preempted && r.snapshot &&
+                          activeCount(requests) < maximumBatchSize &&
+                          availablePages(pools) >= promisedPages(requests, P) &&
+                          availablePages(pools) - promisedPages(requests, P) >=
+                              pagesFor(r.snapshot->length, P);
+        metrics.schedulerOverheadUs += elapsedUs(t0, Clock::now());
+        if (!fits) continue;
+        const auto restoreStart = Clock::now();
+        for (std::size_t l = 0; l < r.states.size(); ++l) {
+          const auto error = r.states[l]->restore(runtime, r.snapshot->length, r.snapshot->keys[l],
+                                                  r.snapshot->values[l]);
+          if (!error.empty())
+            throw std::runtime_error("Request " + r.spec.id + " resume failed: " + error);
+        }
+        metrics.preemptionOverheadUs += elapsedUs(restoreStart, Clock::now());
+        r.snapshot.reset();
+        r.state = RequestState::Active;
+        ++metrics.resumeCount;
+        log << "Serving request " << r.spec.id << ": resumed at length=" << r.length() << '\n';
+        progress = true;
+      }
+
+      // Admit arrived requests whose prompt pages fit.
+      for (auto& r : requests) {
+        const auto t0 = Clock::now();
+        const bool eligible = r.state == RequestState::Waiting && r.spec.arrivalStep <= tick;
+        if (eligible && !r.arrivalTime) r.arrivalTime = Clock::now();
+        const std::size_t promised = promisedPages(requests, P), available = availablePages(pools);
+        const bool fits = eligible && activeCount(requests) < maximumBatchSize &&
+                          available >= promised &&
+                          available - promised >= pagesFor(r.prompt.size(), P);
+        metrics.schedulerOverheadUs += elapsedUs(t0, Clock::now());
+        if (!fits) continue;
+        r.state = RequestState::Active;
+        progress = true;
+      }
+
+      // Pages for every active row's next token; preempt the largest owner
+      // while they are missing (selectPreemptionVictim, ServingRuntime.cpp:454-467).
+      auto active = [&]() {
+        std::vector<std::size_t> rows;
+        for (std::size_t i = 0; i < requests.size(); ++i)
+          if (requests[i].state == RequestState::Active) rows.push_back(i);
+        return rows;
+      };
+      auto rows = active();
+      auto required = [&]() {
+        std::size_t pages = 0;
+        for (const auto i : rows)
+          pages += pagesFor(requests[i].length() + 1, P) - pagesFor(requests[i].length(), P);
+        return pages;
+      };
+      while (!rows.empty() && availablePages(pools) < required()) {
+        std::optional<std::size_t> victim;
+        for (const auto i : rows)
+          if (!victim || requests[i].pages() > requests[*victim].pages()) victim = i;
+        auto& v = requests[*victim];
+        const auto t0 = Clock::now();
+        if (v.length() == 0) {
+          v.state = RequestState::Waiting;
+        } else {
+          Snapshot snap;
+          snap.length = v.length();
+          for (const auto& state : v.states) {
+            snap.keys.push_back(state->readKeyPrefix());
+            snap.values.push_back(state->readValuePrefix());
+          }
+          const auto error = releaseAll(runtime, v);
+          if (!error.empty())
+            throw std::runtime_error("Request " + v.spec.id + " preemption failed: " + error);
+          v.snapshot = std::move(snap);
+          v.state = RequestState::Preempted;
+          ++metrics.preemptionCount;
+        }
+        metrics.preemptionOverheadUs += elapsedUs(t0, Clock::now());
+        log << "Serving request " << v.spec.id << ": preempted for page pressure\n";
+        progress = true;
+        rows = active();
+      }
+
+      if (!rows.empty()) {
+        const auto stageStart = Clock::now();
+        std::vector<std::size_t> previous;
+        for (const auto i : rows) {
+          auto& r = requests[i];
+          previous.push_back(r.length());
+          for (auto& state : r.states) {
+            const auto error = state->stageLength(runtime, r.length() + 1);
+            if (!error.empty()) {
+              for (std::size_t k = 0; k < previous.size(); ++k)
+                for (auto& s : requests[rows[k]].states) (void)s->rollbackLength(runtime, previous[k]);
+              throw std::runtime_error("Request " + r.spec.id + " KV stage failed: " + error);
+            }
+          }
+        }
+        metrics.kvManagementOverheadUs += elapsedUs(stageStart, Clock::now());
+
+        const auto packStart = Clock::now();
+        std::vector<std::int32_t> tokens, lengths;
+        std::vector<std::vector<std::int32_t>> tables(plan.layerCount);
+        bool readLogits = false, promptRows = false;
+        for (std::size_t k = 0; k < rows.size(); ++k) {
+          const auto& r = requests[rows[k]];
+          const bool inPrompt = r.consumed < r.prompt.size();
+          promptRows = promptRows || inPrompt;
+          tokens.push_back(inPrompt ? r.prompt[r.consumed] : r.lastToken);
+          lengths.push_back(static_cast<std::int32_t>(previous[k] + 1));
+          readLogits = readLogits || (inPrompt && r.consumed + 1 == r.prompt.size() &&
+                                      config.recordPrefillLogits) ||
+                       (!inPrompt && config.recordDecodeLogits);
+          for (std::size_t l = 0; l < plan.layerCount; ++l) {
+            auto table = r.states[l]->pageTable();
+            table.resize(maxPages, -1);
+            tables[l].insert(tables[l].end(), table.begin(), table.end());
+          }
+        }
+        metrics.schedulerOverheadUs += elapsedUs(packStart, Clock::now());
+
+        const auto stepStart = Clock::now();
+        const auto out = step(tokens, lengths, tables, readLogits);
+        const double stepUs = elapsedUs(stepStart, Clock::now());
+        hostTimes.push_back(stepUs);
+        ++metrics.decodeCommandSubmissions;
+        if (!out.passed) {
+          for (std::size_t k = 0; k < rows.size(); ++k)
+            for (auto& s : requests[rows[k]].states) (void)s->rollbackLength(runtime, previous[k]);
+          throw std::runtime_error("Batched decode failed: " + out.errorMessage);
+        }
+        if (out.gpuExecutionTimeUs) gpuTimes.push_back(*out.gpuExecutionTimeUs);
+
+        const auto commitStart = Clock::now();
+        std::size_t stepDecodeRows = 0;
+        for (std::size_t k = 0; k < rows.size(); ++k) {
+          auto& r = requests[rows[k]];
+          for (auto& state : r.states) state->commitLength(previous[k] + 1);
+          const auto next = static_cast<std::int32_t>(out.nextTokenIds[k]);
+          auto logitsOf = [&]() {
+            const auto V = static_cast<std::ptrdiff_t>(plan.vocabularySize);
+            return std::vector<float>(out.logits.begin() + static_cast<std::ptrdiff_t>(k) * V,
+                                      out.logits.begin() + static_cast<std::ptrdiff_t>(k + 1) * V);
+          };
+          if (r.consumed < r.prompt.size()) {
+            ++r.consumed;
+            ++metrics.promptTokens;
+            if (r.consumed == r.prompt.size()) {
+              r.output.generatedTokenIds.push_back(static_cast<float>(next));
+              r.lastToken = next;
+              r.output.timeToFirstTokenUs = elapsedUs(*r.arrivalTime, Clock::now());
+              if (config.recordPrefillLogits && !out.logits.empty()) r.output.prefillLogits = logitsOf();
+              log << "Serving request " << r.spec.id << ": prompt complete, pages=" << r.pages()
+                  << ", ttft(us)=" << r.output.timeToFirstTokenUs << '\n';
+              if (r.spec.decodeTokenCount == 0) finish(r);
+            }
+          } else {
+            r.output.generatedTokenIds.push_back(static_cast<float>(next));
+            if (config.recordDecodeLogits && !out.logits.empty()) r.output.decodeLogits.push_back(logitsOf());
+            r.lastToken = next;
+            ++r.decoded;
+            ++metrics.decodedTokens;
+            ++stepDecodeRows;
+            if (r.decoded == r.spec.decodeTokenCount) finish(r);
+          }
+        }
+        metrics.kvManagementOverheadUs += elapsedUs(commitStart, Clock::now());
+        if (!promptRows) {
+          decodeRows += stepDecodeRows;
+          decodeOnlyUs += stepUs;
+        }
+        progress = true;
+        ++batchSamples;
+        batchSum += rows.size();
+        metrics.maximumActiveBatchSize = std::max(metrics.maximumActiveBatchSize, rows.size());
+      }
+
+      std::string isolation;
+      if (!auditPageIsolation(requests, plan.layerCount, isolation))
+        throw std::runtime_error(isolation);
+      if (!progress) {
+        const bool future = std::any_of(requests.begin(), requests.end(), [&](const Request& r) {
+          return r.state == RequestState::Waiting && r.spec.arrivalStep > tick;
+        });
+        if (!future) throw std::runtime_error("Serving scheduler made no progress.");
+      }
+      ++tick;
+    }
+
+    metrics.totalTimeUs = elapsedUs(start, Clock::now());
+    if (metrics.totalTimeUs > 0.0)
+      metrics.tokensPerSecond = static_cast<double>(metrics.decodedTokens) * 1e6 / metrics.totalTimeUs;
+    if (decodeOnlyUs > 0.0)
+      metrics.decodePhaseTokensPerSecond = static_cast<double>(decodeRows) * 1e6 / decodeOnlyUs;
+    if (batchSamples)
+      metrics.averageActiveBatchSize = static_cast<double>(batchSum) / static_cast<double>(batchSamples);
+    if (const auto s = benchmark::summarizeTimings(gpuTimes)) metrics.decodeGpu = *s;
+    if (const auto s = benchmark::summarizeTimings(hostTimes)) metrics.decodeEndToEnd = *s;
+    metrics.peakPagesPerLayer = pools.front()->peakUsedPages();
+    metrics.pageAllocationCount = pools.front()->allocationCount();
+    metrics.pageReleaseCount = pools.front()->releaseCount();
+    for (const auto& pool : pools) {
+      if (pool->usedPages() != 0) throw std::runtime_error("Serving completed with unreleased KV pages.");
+      if (pool->allocationCount() != metrics.pageAllocationCount ||
+          pool->releaseCount() != metrics.pageReleaseCount)
+        throw std::runtime_error("Per-layer KV page-pool lifecycle counts diverged.");
+    }
+    for (auto& r : requests) result.requests.push_back(std::move(r.output));
+    result.passed = true;
+  } catch (const std::exception& error) {
+    result.errorMessage = error.what();
+  }
+  return result;
+}
+
+ServingExecutionResult runContinuousBatch(hip::HipRuntime& runtime,
+                                          std::shared_ptr<DecoderLLMModelResources> model,
+                                          const std::vector<ServingRequestSpec>& requests,
+                                          const ServingConfig& config, std::ostream& log) {
+  ServingExecutionResult result;
+  try {
+    if (!model) throw std::invalid_argument("Serving needs model resources.");
+    const auto& plan = model->plan;
+    const std::size_t M = config.maximumBatchSize ? config.maximumBatchSize : requests.size();
+    std::vector<std::shared_ptr<KVPagePool>> pools;
+    for (std::size_t l = 0; l < plan.layerCount; ++l) {
+      auto pool = createKVPagePool(runtime, plan.kvPlan(), config.pageSize, config.physicalPagesPerLayer);
+      if (!pool.pool) throw std::runtime_error(pool.errorMessage);
+      pools.push_back(std::move(pool.pool));
+    }
+    auto created = createBatchedDecodeExecutor(runtime, model, pools, M, &log);
+    if (!created.executor) throw std::runtime_error(created.errorMessage);
+    auto& executor = *created.executor;
+    BatchedStep step = [&executor](const std::vector<std::int32_t>& tokens,
+                                   const std::vector<std::int32_t>& lengths,
+                                   const std::vector<std::vector<std::int32_t>>& tables,
+                                   bool readLogits) {
+      return executor.run(tokens, lengths, tables, readLogits, true);
+    };
+    result = runContinuousBatch(runtime, plan, pools, M, executor.maxPages(), step, requests, config, log);
+    result.metrics.modelStorageBytes = model->storageBytes;
+    result.metrics.kvPoolStorageBytes = 2 * plan.layerCount * pools.front()->keyBuffer()->storageBytes();
+    result.metrics.batchedActivationStorageBytes = executor.activationStorageBytes();
+  } catch (const std::exception& error) {
+    result.errorMessage = error.what();
+  }
+  return result;
+}
+
+}  // namespace tensor::runtime

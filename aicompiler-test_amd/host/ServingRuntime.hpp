@@ -1,0 +1,112 @@
+// Continuous-batching serving loop for the gfx950 decode path, with the
+// interface of the reference's src/runtime/ServingRuntime.hpp:13-74 and the
+// scheduling rules of ServingRuntime.cpp:426-930:
+//  * per-layer page pools shared by all requests (LIFO free lists);
+//  * a request is admitted when its arrival step has come and the pools hold
+//    pages for its prompt; preempted requests are resumed first, when the
+//    pools hold pages for their snapshot;
+//  * before every batched step the pages the active rows need for their next
+//    token are counted; while they are missing, the active request owning the
+//    most pages is preempted (KV snapshot to host memory, pages released);
+//  * after every step page isolation between active requests is audited and
+//    finished requests release their pages; at the end every pool must be
+//    empty with equal allocation/release counts across layers.
+// Prompts run through the batched decode graph one token per tick (prefill
+// by decode): a request's row carries its next prompt token until the prompt
+// is consumed, then its last generated token, so prompt and decode rows share
+// one batched step.  The tick that consumes the last prompt token yields the
+// first generated token (the reference's prefill output); each later tick is
+// one decode step.
+#pragma once
+
+#include "Benchmark.hpp"
+#include "DecoderLLM.hpp"
+
+#include <cstddef>
+#include <functional>
+#include <iosfwd>
+#include <string>
+#include <vector>
+
+namespace tensor::runtime {
+
+struct ServingRequestSpec {
+  std::string id;
+  std::vector<float> promptTokenIds;
+  std::size_t decodeTokenCount = 0;
+  std::size_t arrivalStep = 0;
+};
+
+struct ServingConfig {
+  std::size_t pageSize = 16;
+  std::size_t physicalPagesPerLayer = 8;
+  // Rows per batched step; 0 = the number of requests.
+  std::size_t maximumBatchSize = 0;
+  // Keep every decode step's logits per request (vocabulary floats each).
+  bool recordDecodeLogits = false;
+  // Keep the logits of the last prompt position.
+  bool recordPrefillLogits = true;
+};
+
+struct ServingRequestOutput {
+  std::string id;
+  std::vector<float> prefillLogits;
+  std::vector<std::vector<float>> decodeLogits;
+  std::vector<float> generatedTokenIds;
+  double timeToFirstTokenUs = 0.0;
+};
+
+struct ServingMetrics {
+  benchmark::Statistics decodeGpu;        // per batched step, GPU time
+  benchmark::Statistics decodeEndToEnd;   // per batched step, host time
+  double totalTimeUs = 0.0;
+  double tokensPerSecond = 0.0;           // decodedTokens / totalTime
+  double decodePhaseTokensPerSecond = 0.0;  // decode rows / time of steps with no prompt rows
+  double schedulerOverheadUs = 0.0;
+  double kvManagementOverheadUs = 0.0;
+  double preemptionOverheadUs = 0.0;
+  double averageActiveBatchSize = 0.0;
+  std::size_t maximumActiveBatchSize = 0;
+  std::size_t preemptionCount = 0;
+  std::size_t resumeCount = 0;
+  std::size_t peakPagesPerLayer = 0;
+  std::size_t pageAllocationCount = 0;
+  std::size_t pageReleaseCount = 0;
+  std::size_t decodeCommandSubmissions = 0;
+  std::size_t decodedTokens = 0;
+  std::size_t promptTokens = 0;
+  std::size_t modelStorageBytes = 0;
+  std::size_t kvPoolStorageBytes = 0;
+  std::size_t batchedActivationStorageBytes = 0;
+};
+
+struct ServingExecutionResult {
+  bool passed = false;
+  std::vector<ServingRequestOutput> requests;
+  ServingMetrics metrics;
+  std::string errorMessage;
+};
+
+// One batched step as the scheduler sees it: tokens, valid lengths and
+// per-layer tables in, next tokens (and logits when asked) out.
+using BatchedStep = std::function<BatchedDecodeRun(
+    const std::vector<std::int32_t>& tokens, const std::vector<std::int32_t>& validLengths,
+    const std::vector<std::vector<std::int32_t>>& tables, bool readLogits)>;
+
+// The scheduler over existing pools and any step function (the CPU tests
+// drive it with host-only pools and a host step).
+[[nodiscard]] ServingExecutionResult runContinuousBatch(
+    hip::HipRuntime& runtime, const planner::DecoderLLMPlan& plan,
+    const std::vector<std::shared_ptr<KVPagePool>>& pools, std::size_t maximumBatchSize,
+    std::size_t maxPages, const BatchedStep& step,
+    const std::vector<ServingRequestSpec>& requests, const ServingConfig& config,
+    std::ostream& log);
+
+// runContinuousBatch (ServingRuntime.cpp:513-930) on the GPU: creates the
+// per-layer pools and the batched decode executor over `model`.
+[[nodiscard]] ServingExecutionResult runContinuousBatch(
+    hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
+    const std::vector<ServingRequestSpec>& requests, const ServingConfig& config,
+    std::ostream& log);
+
+}  // namespace tensor::runtime

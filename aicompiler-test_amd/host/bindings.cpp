@@ -1,0 +1,450 @@
+// Python module _tmc_host: the C++ host layer (HipRuntime, KV pools and
+// states, the decoder executors and the serving loop) for tests and the
+// benchmark.  Names follow the C++ classes; weights and logits cross as numpy
+// float32 arrays.
+#include <pybind11/functional.h>
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include <sstream>
+
+#include "Benchmark.hpp"
+#include "DecoderLLM.hpp"
+#include "KVCacheState.hpp"
+#include "ServingRuntime.hpp"
+
+namespace py = pybind11;
+using namespace tensor;
+using namespace tensor::runtime;
+
+namespace {
+
+using FloatArray = py::array_t<float, py::array::c_style | py::array::forcecast>;
+
+std::vector<float> toVector(const FloatArray& a) {
+  return std::vector<float>(a.data(), a.data() + a.size());
+}
+
+py::array_t<float> toArray(const std::vector<float>& v) {
+  py::array_t<float> out(static_cast<py::ssize_t>(v.size()));
+  std::copy(v.begin(), v.end(), out.mutable_data());
+  return out;
+}
+
+template <typename T, typename Field>
+void weightProperty(py::class_<T>& cls, const char* name, Field T::*field) {
+  cls.def_property(
+      name, [field](const T& self) { return toArray(self.*field); },
+      [field](T& self, const FloatArray& a) { self.*field = toVector(a); });
+}
+
+py::dict runToDict(const BatchedDecodeRun& run) {
+  py::dict d;
+  d["passed"] = run.passed;
+  d["logits"] = toArray(run.logits);
+  d["next_token_ids"] = run.nextTokenIds;
+  d["gpu_us"] = run.gpuExecutionTimeUs ? py::cast(*run.gpuExecutionTimeUs) : py::none();
+  d["cpu_us"] = run.cpuSubmitToCompletionTimeUs;
+  d["error"] = run.errorMessage;
+  return d;
+}
+
+py::dict resultToDict(const DecoderLLMRunResult& run) {
+  py::dict d;
+  d["passed"] = run.passed;
+  d["logits"] = toArray(run.logits);
+  d["next_token_ids"] = run.nextTokenIds;
+  d["gpu_us"] = run.gpuExecutionTimeUs ? py::cast(*run.gpuExecutionTimeUs) : py::none();
+  d["cpu_us"] = run.cpuSubmitToCompletionTimeUs;
+  d["error"] = run.errorMessage;
+  return d;
+}
+
+py::dict statsToDict(const benchmark::Statistics& s) {
+  py::dict d;
+  d["samples"] = s.samples;
+  d["median_us"] = s.medianUs;
+  d["p90_us"] = s.p90Us;
+  d["min_us"] = s.minUs;
+  d["max_us"] = s.maxUs;
+  return d;
+}
+
+py::dict servingToDict(const ServingExecutionResult& r) {
+  py::dict d;
+  d["passed"] = r.passed;
+  d["error"] = r.errorMessage;
+  py::list requests;
+  for (const auto& out : r.requests) {
+    py::dict q;
+    q["id"] = out.id;
+    q["prefill_logits"] = toArray(out.prefillLogits);
+    py::list logits;
+    for (const auto& l : out.decodeLogits) logits.append(toArray(l));
+    q["decode_logits"] = logits;
+    q["generated_token_ids"] = out.generatedTokenIds;
+    q["ttft_us"] = out.timeToFirstTokenUs;
+    requests.append(q);
+  }
+  d["requests"] = requests;
+  const auto& m = r.metrics;
+  py::dict metrics;
+  metrics["decode_gpu"] = statsToDict(m.decodeGpu);
+  metrics["decode_end_to_end"] = statsToDict(m.decodeEndToEnd);
+  metrics["total_time_us"] = m.totalTimeUs;
+  metrics["tokens_per_second"] = m.tokensPerSecond;
+  metrics["decode_phase_tokens_per_second"] = m.decodePhaseTokensPerSecond;
+  metrics["scheduler_overhead_us"] = m.schedulerOverheadUs;
+  metrics["kv_management_overhead_us"] = m.kvManagementOverheadUs;
+  metrics["preemption_overhead_us"] = m.preemptionOverheadUs;
+  metrics["average_active_batch_size"] = m.averageActiveBatchSize;
+  metrics["maximum_active_batch_size"] = m.maximumActiveBatchSize;
+  metrics["preemption_count"] = m.preemptionCount;
+  metrics["resume_count"] = m.resumeCount;
+  metrics["peak_pages_per_layer"] = m.peakPagesPerLayer;
+  metrics["page_allocation_count"] = m.pageAllocationCount;
+  metrics["page_release_count"] = m.pageReleaseCount;
+  metrics["decode_command_submissions"] = m.decodeCommandSubmissions;
+  metrics["decoded_tokens"] = m.decodedTokens;
+  metrics["prompt_tokens"] = m.promptTokens;
+  metrics["model_storage_bytes"] = m.modelStorageBytes;
+  metrics["kv_pool_storage_bytes"] = m.kvPoolStorageBytes;
+  metrics["batched_activation_storage_bytes"] = m.batchedActivationStorageBytes;
+  d["metrics"] = metrics;
+  return d;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_tmc_host, m) {
+  m.doc() = "C++ host layer of the gfx950 decode backend.";
+
+  py::enum_<DType>(m, "DType")
+      .value("Float16", DType::Float16)
+      .value("Float32", DType::Float32)
+      .value("BFloat16", DType::BFloat16)
+      .value("Int32", DType::Int32);
+
+  py::class_<hip::HipRuntime>(m, "HipRuntime")
+      .def(py::init<>())
+      .def("is_available", &hip::HipRuntime::isAvailable)
+      .def("device_name", &hip::HipRuntime::deviceName)
+      .def("initialization_error", &hip::HipRuntime::initializationError)
+      .def("hardware_info",
+           [](const hip::HipRuntime& rt) {
+             const auto h = rt.hardwareInfo();
+             py::dict d;
+             d["max_threads_per_threadgroup"] = h.maxThreadsPerThreadgroup;
+             d["max_threadgroup_memory_length"] = h.maxThreadgroupMemoryLength;
+             d["max_buffer_length"] = h.maxBufferLength;
+             d["supports_bfloat16"] = h.supportsBFloat16;
+             d["compute_units"] = h.computeUnits;
+             d["wave_size"] = h.waveSize;
+             return d;
+           })
+      .def("synchronize", &hip::HipRuntime::synchronize)
+      .def("fail_next", &hip::HipRuntime::failNext)
+      .def("stream", [](const hip::HipRuntime& rt) {
+        return reinterpret_cast<std::uintptr_t>(rt.stream());
+      });
+
+  py::class_<planner::KVCachePlan>(m, "KVCachePlan")
+      .def(py::init<>())
+      .def_readwrite("batch", &planner::KVCachePlan::batch)
+      .def_readwrite("heads", &planner::KVCachePlan::heads)
+      .def_readwrite("head_dimension", &planner::KVCachePlan::headDimension)
+      .def_readwrite("capacity", &planner::KVCachePlan::capacity)
+      .def_readwrite("prefill_length", &planner::KVCachePlan::prefillLength)
+      .def_readwrite("dtype", &planner::KVCachePlan::dtype)
+      .def_readwrite("threads_per_threadgroup", &planner::KVCachePlan::threadsPerThreadgroup)
+      .def("validate", &planner::KVCachePlan::validate);
+
+  py::class_<planner::DecoderLLMPlan>(m, "DecoderLLMPlan")
+      .def(py::init<>())
+      .def_readwrite("attention", &planner::DecoderLLMPlan::attention)
+      .def_readwrite("layer_count", &planner::DecoderLLMPlan::layerCount)
+      .def_readwrite("intermediate_size", &planner::DecoderLLMPlan::intermediateSize)
+      .def_readwrite("vocabulary_size", &planner::DecoderLLMPlan::vocabularySize)
+      .def_readwrite("rms_norm_epsilon", &planner::DecoderLLMPlan::rmsNormEpsilon)
+      .def_readwrite("key_value_heads", &planner::DecoderLLMPlan::keyValueHeads)
+      .def("hidden_size", &planner::DecoderLLMPlan::hiddenSize)
+      .def("kv_heads", &planner::DecoderLLMPlan::kvHeads)
+      .def("validate", &planner::DecoderLLMPlan::validate)
+      .def("kv_plan", &planner::DecoderLLMPlan::kvPlan);
+
+  py::class_<KVPagePool, std::shared_ptr<KVPagePool>>(m, "KVPagePool")
+      .def("page_size", &KVPagePool::pageSize)
+      .def("capacity_pages", &KVPagePool::capacityPages)
+      .def("used_pages", &KVPagePool::usedPages)
+      .def("available_pages", &KVPagePool::availablePages)
+      .def("peak_used_pages", &KVPagePool::peakUsedPages)
+      .def("allocation_count", &KVPagePool::allocationCount)
+      .def("release_count", &KVPagePool::releaseCount)
+      .def("has_storage", &KVPagePool::hasStorage)
+      .def("page_elements", &KVPagePool::pageElements)
+      .def("key_pointer",
+           [](const KVPagePool& p) {
+             return p.keyBuffer() ? reinterpret_cast<std::uintptr_t>(p.keyBuffer()->devicePointer())
+                                  : std::uintptr_t{0};
+           })
+      .def("value_pointer", [](const KVPagePool& p) {
+        return p.valueBuffer() ? reinterpret_cast<std::uintptr_t>(p.valueBuffer()->devicePointer())
+                               : std::uintptr_t{0};
+      });
+
+  m.def("create_kv_page_pool",
+        [](hip::HipRuntime& rt, const planner::KVCachePlan& plan, std::size_t pageSize,
+           std::size_t pages) -> py::object {
+          auto r = createKVPagePool(rt, plan, pageSize, pages);
+          if (!r.pool) throw std::runtime_error(r.errorMessage);
+          return py::cast(r.pool);
+        });
+  m.def("create_host_kv_page_pool",
+        [](const planner::KVCachePlan& plan, std::size_t pageSize, std::size_t pages) {
+          auto r = createHostKVPagePool(plan, pageSize, pages);
+          if (!r.pool) throw std::runtime_error(r.errorMessage);
+          return r.pool;
+        });
+
+  py::class_<KVCacheState>(m, "KVCacheState")
+      .def("current_length", &KVCacheState::currentLength)
+      .def("capacity", &KVCacheState::capacity)
+      .def("reset", &KVCacheState::reset)
+      .def("stage_length", &KVCacheState::stageLength)
+      .def("rollback_length", &KVCacheState::rollbackLength)
+      .def("restore",
+           [](KVCacheState& s, hip::HipRuntime& rt, std::size_t length, const FloatArray& k,
+              const FloatArray& v) { return s.restore(rt, length, toVector(k), toVector(v)); })
+      .def("commit_length", &KVCacheState::commitLength)
+      .def("read_key_prefix", [](const KVCacheState& s) { return toArray(s.readKeyPrefix()); })
+      .def("read_value_prefix", [](const KVCacheState& s) { return toArray(s.readValuePrefix()); })
+      .def("storage_reused", &KVCacheState::storageReused)
+      .def("is_paged", &KVCacheState::isPaged)
+      .def("page_size", &KVCacheState::pageSize)
+      .def("allocated_page_count", &KVCacheState::allocatedPageCount)
+      .def("page_table", &KVCacheState::pageTable)
+      .def("has_device_mirror", [](const KVCacheState& s) { return s.blockTableBuffer() != nullptr; })
+      .def("read_device_table",
+           [](const KVCacheState& s) {
+             std::vector<std::int32_t> out;
+             if (!s.blockTableBuffer()) return out;
+             out.resize(s.blockTableBuffer()->elementCount());
+             const auto error = s.blockTableBuffer()->readRaw(out.data(), out.size());
+             if (!error.empty()) throw std::runtime_error(error);
+             return out;
+           })
+      .def("read_device_length", [](const KVCacheState& s) {
+        std::int32_t value = -1;
+        if (!s.lengthBuffer()) return value;
+        const auto error = s.lengthBuffer()->readRaw(&value, 1);
+        if (!error.empty()) throw std::runtime_error(error);
+        return value;
+      });
+
+  m.def("create_kv_cache_state",
+        [](hip::HipRuntime& rt, const planner::KVCachePlan& plan, std::shared_ptr<KVPagePool> pool,
+           bool mirror) {
+          auto r = createKVCacheState(rt, plan, std::move(pool), mirror);
+          if (!r.state) throw std::runtime_error(r.errorMessage);
+          return std::move(r.state);
+        },
+        py::arg("runtime"), py::arg("plan"), py::arg("pool"), py::arg("device_mirror") = true);
+  m.def("create_private_kv_cache_state",
+        [](hip::HipRuntime& rt, const planner::KVCachePlan& plan, std::size_t pageSize) {
+          auto r = createKVCacheState(rt, plan, pageSize);
+          if (!r.state) throw std::runtime_error(r.errorMessage);
+          return std::move(r.state);
+        });
+
+  py::class_<DecoderLLMLayerParameters> layer(m, "DecoderLLMLayerParameters");
+  layer.def(py::init<>());
+  weightProperty(layer, "input_norm_weight", &DecoderLLMLayerParameters::inputNormWeight);
+  weightProperty(layer, "query_weight", &DecoderLLMLayerParameters::queryWeight);
+  weightProperty(layer, "key_weight", &DecoderLLMLayerParameters::keyWeight);
+  weightProperty(layer, "value_weight", &DecoderLLMLayerParameters::valueWeight);
+  weightProperty(layer, "output_weight", &DecoderLLMLayerParameters::outputWeight);
+  weightProperty(layer, "post_attention_norm_weight",
+                 &DecoderLLMLayerParameters::postAttentionNormWeight);
+  weightProperty(layer, "gate_weight", &DecoderLLMLayerParameters::gateWeight);
+  weightProperty(layer, "up_weight", &DecoderLLMLayerParameters::upWeight);
+  weightProperty(layer, "down_weight", &DecoderLLMLayerParameters::downWeight);
+
+  py::class_<DecoderLLMWorkload> workload(m, "DecoderLLMWorkload");
+  workload.def(py::init<>())
+      .def_readwrite("model_name", &DecoderLLMWorkload::modelName)
+      .def_readwrite("plan", &DecoderLLMWorkload::plan)
+      .def_readwrite("decode_count", &DecoderLLMWorkload::decodeCount)
+      .def_readwrite("layers", &DecoderLLMWorkload::layers);
+  weightProperty(workload, "embedding_weight", &DecoderLLMWorkload::embeddingWeight);
+  weightProperty(workload, "final_norm_weight", &DecoderLLMWorkload::finalNormWeight);
+  weightProperty(workload, "language_model_head_weight", &DecoderLLMWorkload::languageModelHeadWeight);
+  weightProperty(workload, "rope_cosine", &DecoderLLMWorkload::ropeCosine);
+  weightProperty(workload, "rope_sine", &DecoderLLMWorkload::ropeSine);
+
+  m.def("rope_tables", [](std::size_t capacity, std::size_t headDimension, double theta) {
+    std::vector<float> c, s;
+    ropeTables(capacity, headDimension, theta, c, s);
+    return py::make_tuple(toArray(c), toArray(s));
+  });
+
+  py::class_<DecoderLLMModelResources, std::shared_ptr<DecoderLLMModelResources>>(
+      m, "DecoderLLMModelResources")
+      .def_readonly("storage_bytes", &DecoderLLMModelResources::storageBytes)
+      .def_readonly("layer_count", &DecoderLLMModelResources::layerCount)
+      .def_readonly("hidden_size", &DecoderLLMModelResources::hiddenSize)
+      .def_readonly("vocabulary_size", &DecoderLLMModelResources::vocabularySize)
+      .def_readonly("plan", &DecoderLLMModelResources::plan);
+
+  m.def("create_model_resources", [](hip::HipRuntime& rt, const DecoderLLMWorkload& w) {
+    auto r = createModelResources(rt, w);
+    if (!r.resources) throw std::runtime_error(r.errorMessage);
+    return r.resources;
+  });
+  m.def("create_synthetic_model_resources",
+        [](hip::HipRuntime& rt, const planner::DecoderLLMPlan& plan, std::uint64_t seed,
+           float stddev, double theta) {
+          auto r = createSyntheticModelResources(rt, plan, seed, stddev, theta);
+          if (!r.resources) throw std::runtime_error(r.errorMessage);
+          return r.resources;
+        },
+        py::arg("runtime"), py::arg("plan"), py::arg("seed"), py::arg("stddev") = 0.02f,
+        py::arg("theta") = 10000.0);
+
+  py::class_<BatchedDecodeExecutor>(m, "BatchedDecodeExecutor")
+      .def("run",
+           [](BatchedDecodeExecutor& e, const std::vector<std::int32_t>& tokens,
+              const std::vector<std::int32_t>& lengths,
+              const std::vector<std::vector<std::int32_t>>& tables, bool readLogits, bool timeGpu) {
+             BatchedDecodeRun run;
+             {
+               py::gil_scoped_release release;
+               run = e.run(tokens, lengths, tables, readLogits, timeGpu);
+             }
+             return runToDict(run);
+           },
+           py::arg("tokens"), py::arg("valid_lengths"), py::arg("tables"),
+           py::arg("read_logits") = true, py::arg("time_gpu") = false)
+      .def("maximum_batch_size", &BatchedDecodeExecutor::maximumBatchSize)
+      .def("max_pages", &BatchedDecodeExecutor::maxPages)
+      .def("buckets", &BatchedDecodeExecutor::buckets)
+      .def("dispatches_per_step", &BatchedDecodeExecutor::dispatchesPerStep)
+      .def("activation_storage_bytes", &BatchedDecodeExecutor::activationStorageBytes);
+
+  m.def("create_batched_decode_executor",
+        [](hip::HipRuntime& rt, std::shared_ptr<DecoderLLMModelResources> model,
+           std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t maxBatch) {
+          std::ostringstream log;
+          auto r = createBatchedDecodeExecutor(rt, std::move(model), std::move(pools), maxBatch, &log);
+          if (!r.executor) throw std::runtime_error(r.errorMessage);
+          return std::move(r.executor);
+        });
+
+  py::class_<DecoderLLMCompileOptions>(m, "DecoderLLMCompileOptions")
+      .def(py::init<>())
+      .def_readwrite("kv_page_size", &DecoderLLMCompileOptions::kvPageSize)
+      .def_readwrite("shared_kv_pools", &DecoderLLMCompileOptions::sharedKVPools)
+      .def_readwrite("storage_dtype", &DecoderLLMCompileOptions::storageDtype)
+      .def_readwrite("shared_model_resources", &DecoderLLMCompileOptions::sharedModelResources);
+
+  py::class_<DecoderKVSnapshot>(m, "DecoderKVSnapshot")
+      .def_readonly("length", &DecoderKVSnapshot::length)
+      .def("key_cache", [](const DecoderKVSnapshot& s, std::size_t l) { return toArray(s.keyCaches.at(l)); })
+      .def("value_cache",
+           [](const DecoderKVSnapshot& s, std::size_t l) { return toArray(s.valueCaches.at(l)); });
+
+  py::class_<CompiledDecoderLLM>(m, "CompiledDecoderLLM")
+      .def("reset", &CompiledDecoderLLM::reset)
+      .def("prefill",
+           [](CompiledDecoderLLM& d, const std::vector<float>& tokens, bool readLogits) {
+             return resultToDict(d.prefill(tokens, readLogits));
+           },
+           py::arg("token_ids"), py::arg("read_logits") = true)
+      .def("decode",
+           [](CompiledDecoderLLM& d, const std::vector<float>& tokens, bool readLogits) {
+             return resultToDict(d.decode(tokens, readLogits));
+           },
+           py::arg("token_ids"), py::arg("read_logits") = true)
+      .def("current_length", &CompiledDecoderLLM::currentLength)
+      .def("read_key_prefix", [](const CompiledDecoderLLM& d, std::size_t l) { return toArray(d.readKeyPrefix(l)); })
+      .def("read_value_prefix",
+           [](const CompiledDecoderLLM& d, std::size_t l) { return toArray(d.readValuePrefix(l)); })
+      .def("cache_storage_reused", &CompiledDecoderLLM::cacheStorageReused)
+      .def("uses_paged_kv_cache", &CompiledDecoderLLM::usesPagedKVCache)
+      .def("kv_page_size", &CompiledDecoderLLM::kvPageSize)
+      .def("allocated_kv_page_count", &CompiledDecoderLLM::allocatedKVPageCount)
+      .def("model_storage_bytes", &CompiledDecoderLLM::modelStorageBytes)
+      .def("kv_storage_bytes", &CompiledDecoderLLM::kvStorageBytes)
+      .def("activation_storage_bytes", &CompiledDecoderLLM::activationStorageBytes)
+      .def("shared_model_resources", &CompiledDecoderLLM::sharedModelResources)
+      .def("kv_block_table", &CompiledDecoderLLM::kvBlockTable)
+      .def("snapshot_kv_cache", &CompiledDecoderLLM::snapshotKVCache)
+      .def("release_kv_cache", &CompiledDecoderLLM::releaseKVCache)
+      .def("restore_kv_cache", &CompiledDecoderLLM::restoreKVCache)
+      .def("stage_kv_length", &CompiledDecoderLLM::stageKVLength)
+      .def("commit_kv_length", &CompiledDecoderLLM::commitKVLength)
+      .def("rollback_kv_length", &CompiledDecoderLLM::rollbackKVLength);
+
+  m.def("compile_decoder_llm",
+        [](hip::HipRuntime& rt, const DecoderLLMWorkload& w, const DecoderLLMCompileOptions& o) {
+          std::ostringstream log;
+          auto r = compileDecoderLLM(rt, w, log, o);
+          if (!r.executable) throw std::runtime_error(r.errorMessage);
+          return py::make_tuple(py::cast(std::move(r.executable)), log.str());
+        });
+
+  py::class_<ServingRequestSpec>(m, "ServingRequestSpec")
+      .def(py::init<>())
+      .def_readwrite("id", &ServingRequestSpec::id)
+      .def_readwrite("prompt_token_ids", &ServingRequestSpec::promptTokenIds)
+      .def_readwrite("decode_token_count", &ServingRequestSpec::decodeTokenCount)
+      .def_readwrite("arrival_step", &ServingRequestSpec::arrivalStep);
+
+  py::class_<ServingConfig>(m, "ServingConfig")
+      .def(py::init<>())
+      .def_readwrite("page_size", &ServingConfig::pageSize)
+      .def_readwrite("physical_pages_per_layer", &ServingConfig::physicalPagesPerLayer)
+      .def_readwrite("maximum_batch_size", &ServingConfig::maximumBatchSize)
+      .def_readwrite("record_decode_logits", &ServingConfig::recordDecodeLogits)
+      .def_readwrite("record_prefill_logits", &ServingConfig::recordPrefillLogits);
+
+  m.def("run_continuous_batch",
+        [](hip::HipRuntime& rt, std::shared_ptr<DecoderLLMModelResources> model,
+           const std::vector<ServingRequestSpec>& specs, const ServingConfig& config) {
+          std::ostringstream log;
+          ServingExecutionResult r;
+          {
+            py::gil_scoped_release release;
+            r = runContinuousBatch(rt, std::move(model), specs, config, log);
+          }
+          auto d = servingToDict(r);
+          d["log"] = log.str();
+          return d;
+        });
+
+  // The scheduler over host-only pools and a Python step (CPU tests):
+  // step(tokens, valid_lengths, tables, read_logits) -> (next_tokens, logits).
+  m.def("run_continuous_batch_with",
+        [](hip::HipRuntime& rt, const planner::DecoderLLMPlan& plan,
+           const std::vector<std::shared_ptr<KVPagePool>>& pools, std::size_t maxBatch,
+           std::size_t maxPages, py::function step, const std::vector<ServingRequestSpec>& specs,
+           const ServingConfig& config) {
+          BatchedStep wrapped = [&step](const std::vector<std::int32_t>& tokens,
+                                        const std::vector<std::int32_t>& lengths,
+                                        const std::vector<std::vector<std::int32_t>>& tables,
+                                        bool readLogits) {
+            BatchedDecodeRun run;
+            py::tuple out = step(tokens, lengths, tables, readLogits);
+            run.nextTokenIds = out[0].cast<std::vector<float>>();
+            if (readLogits) run.logits = toVector(out[1].cast<FloatArray>());
+            run.passed = run.nextTokenIds.size() == tokens.size();
+            if (!run.passed) run.errorMessage = "step returned the wrong number of tokens";
+            return run;
+          };
+          std::ostringstream log;
+          auto r = runContinuousBatch(rt, plan, pools, maxBatch, maxPages, wrapped, specs, config, log);
+          auto d = servingToDict(r);
+          d["log"] = log.str();
+          return d;
+        });
+}

@@ -67,6 +67,9 @@ const char *tmc_rt_init_error(const tmc_runtime *rt);
 int tmc_rt_device_info(const tmc_runtime *rt, tmc_hardware_info *info);
 /* The stream every prepared execution and sequence of this runtime uses. */
 void *tmc_rt_stream(const tmc_runtime *rt);
+/* Wait for all work enqueued on that stream (the reference's execute() is
+ * synchronous; this is the wait for work enqueued with tmc_seq_launch). */
+int tmc_rt_synchronize(tmc_runtime *rt);
 
 /* MetalRuntime::createBuffer (MetalRuntime.hpp:186-188; .mm:515-561): host
  * floats converted per dtype (fp16 ties away from zero, bf16 RNE, int32
@@ -270,6 +273,23 @@ int tmc_paged_decode_attention(const void *q, const void *key_pool, const void *
                                int64_t head_dim, int64_t page_size, int64_t max_pages,
                                int64_t page_stride, int64_t head_stride, void *workspace,
                                size_t workspace_bytes, void *stream);
+
+/* Decode-step fusion of emitServingRoPE (DecoderLLMMetalEmitter.cpp:260-312)
+ * for q and k with emitServingPagedCacheAppend (:314-373) for the rotated k
+ * and v, reading one fused projection row per request laid out
+ * [q_heads | kv_heads (key) | kv_heads (value)] x head_dim.  The token of
+ * request b sits at position valid_lengths[b]-1: the rotated query goes to
+ * q_out [max_batch, q_heads*head_dim]; the rotated key and the value (bit
+ * copy) go to the pools [page][kv_heads][page_size][head_dim] through
+ * block_tables [max_batch, max_pages], max_pages = ceil(capacity/page_size).
+ * Rows >= active_count[0], lengths outside [1, capacity] and negative page
+ * entries are skipped.  The rotation is bit-identical to tmc_serving_rope. */
+int tmc_decode_rope_append(const void *qkv, const float *cosine, const float *sine,
+                           const int32_t *valid_lengths, const int32_t *block_tables,
+                           const int32_t *active_count, void *q_out, void *key_pool,
+                           void *value_pool, int dtype, int64_t max_batch, int64_t q_heads,
+                           int64_t kv_heads, int64_t head_dim, int64_t capacity,
+                           int64_t page_size, int64_t max_pages, void *stream);
 
 /* emitTokenArgmax (TransformerDecodeMetalEmitter.cpp:198-256): greedy token
  * per row over fp32 logits, ties to the lowest index. */

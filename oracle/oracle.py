@@ -254,7 +254,7 @@ class _Model(C.Structure):
     _fields_ = [("layers", C.c_size_t), ("hidden", C.c_size_t), ("heads", C.c_size_t),
                 ("head_dim", C.c_size_t), ("intermediate", C.c_size_t),
                 ("vocabulary", C.c_size_t), ("capacity", C.c_size_t), ("epsilon", C.c_float),
-                ("embedding", C.c_void_p), ("final_norm", C.c_void_p), ("lm_head", C.c_void_p),
+                ("kv_heads", C.c_size_t), ("embedding", C.c_void_p), ("final_norm", C.c_void_p), ("lm_head", C.c_void_p),
                 ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p),
                 ("layer", C.POINTER(_Layer))]
 
@@ -278,7 +278,8 @@ def decoder_step(weights: dict, cfg: dict, key_pools, value_pools, page_size: in
     for name in ("rope_cos", "rope_sin"):
         top[name] = np.ascontiguousarray(weights[name], dtype=np.float32)
     m = _Model(cfg["layers"], cfg["hidden"], cfg["heads"], cfg["head_dim"], cfg["intermediate"],
-               cfg["vocabulary"], cfg["capacity"], cfg["epsilon"], top["embedding"].ctypes.data,
+               cfg["vocabulary"], cfg["capacity"], cfg["epsilon"], cfg.get("kv_heads", 0),
+               top["embedding"].ctypes.data,
                top["final_norm"].ctypes.data, top["lm_head"].ctypes.data,
                top["rope_cos"].ctypes.data, top["rope_sin"].ctypes.data, layers)
     for p in list(key_pools) + list(value_pools):

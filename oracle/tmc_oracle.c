@@ -563,7 +563,9 @@ int tmco_decoder_step(const tmco_model *m, uint16_t *const *key_pools,
                       float *logits, int32_t *next_tokens) {
   half_table_init();
   const size_t H = m->hidden, D = m->head_dim, NH = m->heads, I = m->intermediate;
+  const size_t KVH = m->kv_heads ? m->kv_heads : NH, KV = KVH * D, group = NH / KVH;
   const size_t pairs = D / 2;
+  if (KVH == 0 || NH % KVH != 0) return -3;
   const size_t layers = layer_limit && layer_limit < m->layers ? layer_limit : m->layers;
   const size_t widest = (I > m->vocabulary ? I : m->vocabulary) > H
                             ? (I > m->vocabulary ? I : m->vocabulary) : H;
@@ -602,39 +604,44 @@ int tmco_decoder_step(const tmco_model *m, uint16_t *const *key_pools,
     store_array(acc, batch * H, nrm);
     linear_f16(nrm, L->wq, batch, H, H, acc, row);
     store_array(acc, batch * H, q);
-    linear_f16(nrm, L->wk, batch, H, H, acc, row);
-    store_array(acc, batch * H, k);
-    linear_f16(nrm, L->wv, batch, H, H, acc, row);
-    store_array(acc, batch * H, v);
+    linear_f16(nrm, L->wk, batch, H, KV, acc, row);
+    store_array(acc, batch * KV, k);
+    linear_f16(nrm, L->wv, batch, H, KV, acc, row);
+    store_array(acc, batch * KV, v);
     for (size_t b = 0; b < batch; ++b) {
       const size_t valid = (size_t)valid_lengths[b];
       const size_t position = valid - 1;
       /* RoPE on q and k, stored. */
-      for (size_t h = 0; h < NH; ++h)
-        for (size_t p = 0; p < pairs; ++p) {
+      for (size_t p = 0; p < pairs; ++p) {
+        const double c = m->rope_cos[position * pairs + p];
+        const double s = m->rope_sin[position * pairs + p];
+        for (size_t h = 0; h < NH; ++h) {
           const size_t base = b * H + h * D + 2 * p;
-          const double c = m->rope_cos[position * pairs + p];
-          const double s = m->rope_sin[position * pairs + p];
-          const double qe = q[base], qo = q[base + 1], ke = k[base], ko = k[base + 1];
+          const double qe = q[base], qo = q[base + 1];
           q[base] = tmco_store(qe * c - qo * s, TMCO_F16);
           q[base + 1] = tmco_store(qe * s + qo * c, TMCO_F16);
+        }
+        for (size_t h = 0; h < KVH; ++h) {
+          const size_t base = b * KV + h * D + 2 * p;
+          const double ke = k[base], ko = k[base + 1];
           k[base] = tmco_store(ke * c - ko * s, TMCO_F16);
           k[base + 1] = tmco_store(ke * s + ko * c, TMCO_F16);
         }
-      /* Append k, v at position valid-1 ([page][head][page_size][D] pools). */
+      }
+      /* Append k, v at position valid-1 ([page][kv_head][page_size][D] pools). */
       const int32_t page = table[b * max_pages + position / page_size];
       if (page < 0) continue;
-      for (size_t h = 0; h < NH; ++h)
+      for (size_t h = 0; h < KVH; ++h)
         for (size_t c = 0; c < D; ++c) {
-          const size_t dst = (((size_t)page * NH + h) * page_size + position % page_size) * D + c;
-          key_pools[l][dst] = tmco_f32_to_f16(k[b * H + h * D + c]);
-          value_pools[l][dst] = tmco_f32_to_f16(v[b * H + h * D + c]);
+          const size_t dst = (((size_t)page * KVH + h) * page_size + position % page_size) * D + c;
+          key_pools[l][dst] = tmco_f32_to_f16(k[b * KV + h * D + c]);
+          value_pools[l][dst] = tmco_f32_to_f16(v[b * KV + h * D + c]);
         }
-      /* Attention over [0, valid), stored. */
+      /* Attention over [0, valid), stored; query head h reads kv head h/group. */
       for (size_t h = 0; h < NH; ++h) {
         for (size_t pos = 0; pos < valid; ++pos) {
           const size_t pg = (size_t)table[b * max_pages + pos / page_size];
-          const size_t base = ((pg * NH + h) * page_size + pos % page_size) * D;
+          const size_t base = ((pg * KVH + h / group) * page_size + pos % page_size) * D;
           for (size_t c = 0; c < D; ++c) {
             keys[pos * D + c] = g_half_table[key_pools[l][base + c]];
             vals[pos * D + c] = g_half_table[value_pools[l][base + c]];

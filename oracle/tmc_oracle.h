@@ -91,13 +91,16 @@ typedef struct tmco_layer {
 typedef struct tmco_model {
   size_t layers, hidden, heads, head_dim, intermediate, vocabulary, capacity;
   float epsilon;
+  size_t kv_heads; /* key/value heads (grouped-query attention); 0 = heads.
+                      wk, wv are [kv_heads*head_dim, hidden]; query head h
+                      reads kv head h / (heads / kv_heads). */
   const uint16_t *embedding, *final_norm, *lm_head;
   const float *rope_cos, *rope_sin;  /* [capacity, head_dim/2] */
   const tmco_layer *layer;
 } tmco_model;
 
 /* One decode step for `batch` requests over fp16 paged pools laid out
- * [page][heads][page_size][head_dim] (one pool pair per layer).  The new
+ * [page][kv_heads][page_size][head_dim] (one pool pair per layer).  The new
  * token of request b lands at position valid_lengths[b]-1.  Writes K/V into
  * the pools, fp32 logits [batch, vocabulary] (rounded from double) and the
  * greedy tokens. */

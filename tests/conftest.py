@@ -47,6 +47,12 @@ def tmc():
     return load_tmc()
 
 
+@pytest.fixture(scope="session")
+def host(tmc):
+    """The C++ host layer module (_tmc_host)."""
+    return tmc.host()
+
+
 @pytest.fixture(autouse=True)
 def _announce(request):
     # Name the case before any GPU work so a crash log identifies it.

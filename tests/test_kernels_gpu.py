@@ -370,6 +370,61 @@ def test_rope_decoder_and_serving(tmc, orc, torch):
     assert np.isnan(got[3]).all()
 
 
+@pytest.mark.parametrize("qh,kvh,d", [(32, 32, 128), (32, 8, 128), (4, 2, 64)])
+def test_decode_rope_append_is_rope_then_append(tmc, orc, torch, qh, kvh, d):
+    """Fused RoPE(q, k) + paged append of k, v (one fused projection row per
+    request) equals tmc_serving_rope followed by tmc_serving_kv_append bit for
+    bit, and the oracle's RoPE within the fp16-path tolerance; pages of other
+    rows, rows at or past the active count and positions without a page stay
+    untouched."""
+    cap, p, batch = 64, 16, 5
+    max_pages = cap // p
+    pos = np.arange(cap)[:, None]
+    freq = np.exp(np.arange(0, d, 2) * (-np.log(10000.0) / d))
+    cos, sin = np.cos(pos * freq).astype(np.float32), np.sin(pos * freq).astype(np.float32)
+    width = (qh + 2 * kvh) * d
+    qkv = orc.f16(normal(511, (batch, width)))
+    lengths = np.array([1, 17, 64, 33, 9], np.int32)
+    pages = 24
+    perm = np.random.default_rng(512).permutation(pages).astype(np.int32)
+    tables = perm[:batch * max_pages].reshape(batch, max_pages).copy()
+    tables[3, 2] = -1  # row 3's new token (position 32) has no page
+    active = 4          # row 4 is padding
+    pool0 = orc.f16(normal(513, (pages, kvh, p, d)))
+    kp, vp = dev_f16(pool0), dev_f16(pool0.copy())
+    q_out = torch.full((batch, qh * d), float("nan"), dtype=torch.float16, device="cuda")
+    args = (dev(cos), dev(sin), dev(lengths), dev(tables),
+            torch.tensor([active], dtype=torch.int32, device="cuda"))
+    tmc.decode_rope_append(dev_f16(qkv), *args, q_out, kp, vp, batch, qh, kvh, d, cap, p,
+                           max_pages)
+    # unfused path on the same inputs
+    q_in = dev_f16(np.ascontiguousarray(qkv[:, :qh * d]))
+    k_in = dev_f16(np.ascontiguousarray(qkv[:, qh * d:(qh + kvh) * d]))
+    v_in = dev_f16(np.ascontiguousarray(qkv[:, (qh + kvh) * d:]))
+    q_ref = torch.full_like(q_out, float("nan"))
+    k_rot = torch.empty((batch, kvh * d), dtype=torch.float16, device="cuda")
+    tmc.serving_rope(q_in, dev(cos), dev(sin), dev(lengths), args[4], q_ref, batch, qh, d, cap)
+    tmc.serving_rope(k_in, dev(cos), dev(sin), dev(lengths), args[4], k_rot, batch, kvh, d, cap)
+    kp2, vp2 = dev_f16(pool0), dev_f16(pool0.copy())
+    tmc.serving_kv_append(k_rot, dev(lengths), dev(tables), args[4], kp2, batch, kvh, d, cap, p,
+                          False)
+    tmc.serving_kv_append(v_in, dev(lengths), dev(tables), args[4], vp2, batch, kvh, d, cap, p,
+                          False)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(q_out)[:active], bits(q_ref)[:active])
+    assert np.isnan(values(q_out)[active:]).all()
+    assert np.array_equal(bits(kp), bits(kp2)) and np.array_equal(bits(vp), bits(vp2))
+    # oracle: rotation within tolerance, value append bit-exact
+    ref_q = orc.rope(qkv[:active, :qh * d], cos, sin, F16, qh, d, lengths[:active] - 1)
+    assert_f16_path(values(q_out)[:active], ref_q, what="fused rope q")
+    ref_v = orc.append_serving(np.ascontiguousarray(qkv[:, (qh + kvh) * d:]), pool0.ravel(), batch,
+                               kvh, d, cap, p, False, lengths, tables, active)
+    assert np.array_equal(bits(vp).ravel(), ref_v)
+    changed = np.flatnonzero((bits(kp) != pool0).reshape(pages, -1).any(axis=1))
+    expect = {int(tables[b, (lengths[b] - 1) // p]) for b in range(active)} - {-1}
+    assert set(changed.tolist()) <= expect
+
+
 def test_embedding_and_argmax(tmc, orc, torch):
     vocab, hidden = 1000, 64
     table = orc.f16(normal(601, (vocab, hidden)))
