@@ -58,7 +58,7 @@ def _declare(l):
         "tmc_decode_attention": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, vp, sz,
                                        vp]),
         "tmc_paged_decode_attention": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64,
-                                             i64, i64, i64, i64, vp, sz, vp]),
+                                             i64, i64, i64, i64, i64, vp, sz, vp]),
         "tmc_argmax_f32": (i32, [vp, vp, i64, i64, vp]),
         "tmc_fill_normal": (i32, [vp, i32, i64, C.c_uint64, f, f, vp]),
         "tmc_copy_bytes": (i32, [vp, vp, sz, vp]),
@@ -302,12 +302,15 @@ def decode_attention(q, k_cache, v_cache, valid_length, out, batch, q_heads, kv_
 
 def paged_decode_attention(q, k_pool, v_pool, valid_lengths, tables, active, out, max_batch,
                            q_heads, kv_heads, head_dim, page_size, max_pages, page_stride,
-                           head_stride, workspace=None, stream=None):
+                           head_stride, workspace=None, stream=None, pool_pages=None):
+    """pool_pages defaults to the pages the k_pool tensor holds."""
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    if pool_pages is None:
+        pool_pages = min(k_pool.numel(), v_pool.numel()) // page_stride
     check(lib().tmc_paged_decode_attention(
         _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(valid_lengths), _ptr(tables), _ptr(active),
         _ptr(out), _dtype_code(q), max_batch, q_heads, kv_heads, head_dim, page_size, max_pages,
-        page_stride, head_stride, _ptr(workspace), ws_bytes, _stream(stream)),
+        pool_pages, page_stride, head_stride, _ptr(workspace), ws_bytes, _stream(stream)),
         "tmc_paged_decode_attention")
 
 

@@ -9,17 +9,17 @@
 // one 256-thread block per split, and the GROUP query heads that share a kv
 // head (GQA) are served from the same K/V loads.
 //
-// Wave layout for head dim D: RL = D/8 lanes hold one position's 16-byte
-// slices, so one 16-byte load instruction covers NR = 64/RL consecutive
-// positions (one contiguous 1 KiB run for D = 128 inside a 16-token page).
-// A wave tile is J = 4 such loads (TILE = 4*NR positions); each lane keeps
-// its own 4 positions' softmax terms and its 8 output columns, and rows are
-// folded together only once per split (cross-row shuffles), then the 4 waves
-// of the block merge through LDS.  Splits merge in attn_combine_kernel.
+// A multi-split (request, kv head) stores one (max, sum, weighted) partial
+// per split in the workspace and attn_combine_kernel merges them, one block
+// per (request, query head), in split order.  (Merging in the last-arriving
+// split block needs device-scope fences, and each one writes back and
+// invalidates the XCD's L2: measured several times slower.)
 //
-// For D = 128 (attn_mfma_partial_kernel) the scores of a 16-position tile
-// come from v_mfma_f32_16x16x32_f16, so no cross-lane reduction is needed for
-// q.K; see the comment above that kernel.
+// D = 128 runs attn_mfma_kernel (scores from v_mfma_f32_16x16x32_f16, see the
+// comment above it); smaller heads run attn_partial_kernel: RL = D/8 lanes
+// hold one position's 16-byte slices, so one 16-byte load covers NR = 64/RL
+// consecutive positions, a wave tile is J = 4 such loads, and rows are
+// folded together once per split (cross-row shuffles).
 #include "tmc_abi.hpp"
 #include "tmc_device.hpp"
 
@@ -29,8 +29,15 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kTilesPerWave = 2;  // VALU kernel (D < 128)
-constexpr int kMfmaTilesPerWave = 4;  // D == 128 kernel: tiles of 16 positions per wave
-constexpr int kMfmaChunk = kWaves * kMfmaTilesPerWave * 16;
+// D == 128 kernel: a wave step is kMfmaTiles 16-position MFMA tiles whose
+// K/V loads are all issued before the first MFMA.  (Keeping a second step's
+// loads in flight was measured slower: the extra registers halve occupancy.)
+// Positions per split are chosen per launch from 256, 512 or 1024
+// (mfma_chunk): the largest that still gives about two blocks per CU, since
+// longer splits mean fewer partials to merge and fewer per-block costs.
+constexpr int kMfmaTiles = 2;
+constexpr int kMfmaStep = 16 * kMfmaTiles;
+constexpr int kMfmaMaxChunk = 1024;
 
 struct AttnParams {
   const half_t* q;
@@ -44,13 +51,25 @@ struct AttnParams {
   long page_stride;       // paged: elements between pages
   long head_stride;       // paged: elements between kv heads inside a page
   int q_heads, kv_heads, capacity, page_size, max_pages, max_splits;
+  int page_shift;         // log2(page_size) when it is a power of two, else -1
+  long pool_pages;        // paged: pages in each pool (0 = unknown, no bound check)
+  int chunk;              // positions per split
+  unsigned kv_bytes;      // bytes of the K (and of the V) buffer when < 4 GiB, else 0
   float scale_log2;       // (1/sqrt(D)) * log2(e)
 };
 
-// Positions per split: D == 128 runs the MFMA kernel (kMfmaChunk); smaller
-// heads run the VALU kernel (4 waves x 2 tiles of 4*64/(D/8) positions).
+// Positions per split of the VALU kernel (D < 128): 4 waves x 2 tiles of
+// 4*64/(D/8) positions.
 template <int D> constexpr int chunk_positions() {
-  return D == 128 ? kMfmaChunk : kWaves * kTilesPerWave * 4 * (kWave / (D / 8));
+  return kWaves * kTilesPerWave * 4 * (kWave / (D / 8));
+}
+
+__device__ __forceinline__ int page_of(const AttnParams& p, int pos) {
+  return p.page_shift >= 0 ? pos >> p.page_shift : pos / p.page_size;
+}
+
+__device__ __forceinline__ int slot_in_page(const AttnParams& p, int pos) {
+  return p.page_shift >= 0 ? pos & (p.page_size - 1) : pos % p.page_size;
 }
 
 template <bool PAGED>
@@ -59,12 +78,15 @@ __device__ __forceinline__ int valid_length(const AttnParams& p, int b) {
 }
 
 // True when a page needed by [0, valid) is negative (the reference kernel
-// returns before writing in that case).  Block-uniform result.
+// returns before writing in that case) or, when the pool size is known, past
+// the end of the pool.  Block-uniform result.
 __device__ __forceinline__ bool has_bad_page(const AttnParams& p, int b, int valid) {
   const int pages = (valid + p.page_size - 1) / p.page_size;
   int bad = 0;
-  for (int lp = threadIdx.x; lp < pages; lp += blockDim.x)
-    bad |= p.tables[(size_t)b * p.max_pages + lp] < 0;
+  for (int lp = threadIdx.x; lp < pages; lp += blockDim.x) {
+    const int page = p.tables[(size_t)b * p.max_pages + lp];
+    bad |= page < 0 || (p.pool_pages > 0 && page >= p.pool_pages);
+  }
   return __syncthreads_or(bad) != 0;
 }
 
@@ -87,10 +109,10 @@ struct TileLoad {
       ok[j] = pos < end;
       size_t off = 0;
       if constexpr (PAGED) {
-        const int page = ok[j] ? s_pages[pos / p.page_size - page0] : -1;
-        ok[j] = ok[j] && page >= 0;
+        const int page = ok[j] ? s_pages[page_of(p, pos) - page0] : -1;
+        ok[j] = ok[j] && page >= 0 && (p.pool_pages == 0 || page < p.pool_pages);
         off = (size_t)page * p.page_stride + (size_t)kvh * p.head_stride +
-              (size_t)(pos % p.page_size) * D + 8 * c;
+              (size_t)slot_in_page(p, pos) * D + 8 * c;
       } else {
         off = contiguous_base + (size_t)pos * D + 8 * c;
       }
@@ -134,6 +156,85 @@ __device__ __forceinline__ void attend_tile(const h8 (&qv)[GROUP], const h8 (&kt
   }
 }
 
+// End of a split block: merge the block's 4 wave partials (in LDS), then
+// write the output (one split) or the split's partial slot.  Rows whose
+// attended range needs a negative page keep their output untouched (the
+// reference kernel returns before writing); attn_combine_kernel applies the
+// same rule for multi-split rows.
+template <int D, int GROUP, bool PAGED>
+__device__ void finish_split(const AttnParams& p, int b, int kvh, int split, int nsplit,
+                             int valid, const float (*s_m)[GROUP], const float (*s_l)[GROUP],
+                             const float (*s_o)[GROUP][D]) {
+  const bool single = nsplit == 1;
+  if (single && PAGED && has_bad_page(p, b, valid)) return;
+  for (int idx = threadIdx.x; idx < GROUP * D; idx += kThreads) {
+    const int g = idx / D, d = idx % D;
+    float mx = s_m[0][g];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][g]);
+    float lsum = 0.0f, osum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float scale = s_m[w][g] == -INFINITY ? 0.0f : fast_exp2(s_m[w][g] - mx);
+      lsum += scale * s_l[w][g];
+      osum += scale * s_o[w][g][d];
+    }
+    const int qh = kvh * GROUP + g;
+    if (single) {
+      p.out[((size_t)b * p.q_heads + qh) * D + d] = (half_t)(osum / lsum);
+    } else {
+      float* slot = p.ws + (((size_t)b * p.q_heads + qh) * p.max_splits + split) * (D + 2);
+      slot[d] = osum;
+      if (d == 0) {
+        slot[D] = mx;
+        slot[D + 1] = lsum;
+      }
+    }
+  }
+}
+
+// Merge the split partials of one (request, query head): thread d owns
+// output column d; splits are read 8 at a time (all 24 loads issued before
+// use) and folded with a running maximum.
+template <int D, bool PAGED>
+__global__ __launch_bounds__(D) void attn_combine_kernel(AttnParams p) {
+  const int qh = blockIdx.x, b = blockIdx.y;
+  if (PAGED && p.active && b >= p.active[0]) return;
+  const int valid = valid_length<PAGED>(p, b);
+  if (valid < 1 || valid > p.capacity) return;
+  const int nsplit = (valid + p.chunk - 1) / p.chunk;
+  if (nsplit <= 1) return;
+  if (PAGED && has_bad_page(p, b, valid)) return;
+  const int d = threadIdx.x;
+  const float* base = p.ws + ((size_t)b * p.q_heads + qh) * p.max_splits * (D + 2);
+  float mx = -INFINITY, lsum = 0.0f, osum = 0.0f;
+  for (int s0 = 0; s0 < nsplit; s0 += 8) {
+    float ms[8], ls[8], os[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float* slot = base + (size_t)(s0 + k) * (D + 2);
+      const bool in = s0 + k < nsplit;
+      ms[k] = in ? slot[D] : -INFINITY;
+      ls[k] = in ? slot[D + 1] : 0.0f;
+      os[k] = in ? slot[d] : 0.0f;
+    }
+    float next = mx;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) next = fmaxf(next, ms[k]);
+    const float alpha = mx == -INFINITY ? 0.0f : fast_exp2(mx - next);
+    lsum *= alpha;
+    osum *= alpha;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float scale = ms[k] == -INFINITY ? 0.0f : fast_exp2(ms[k] - next);
+      lsum += scale * ls[k];
+      osum += scale * os[k];
+    }
+    mx = next;
+  }
+  p.out[((size_t)b * p.q_heads + qh) * D + d] = (half_t)(osum / lsum);
+}
+
 template <int D, int GROUP, bool PAGED>
 __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnParams p) {
   constexpr int RL = D / 8;
@@ -163,8 +264,8 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnParams p) {
   // instead of one per tile before each K/V load).
   int page0 = 0;
   if constexpr (PAGED) {
-    page0 = begin / p.page_size;
-    const int entries = (end - 1) / p.page_size - page0 + 1;
+    page0 = page_of(p, begin);
+    const int entries = page_of(p, end - 1) - page0 + 1;
     for (int i = threadIdx.x; i < entries; i += kThreads)
       s_pages[i] = p.tables[(size_t)b * p.max_pages + page0 + i];
     __syncthreads();
@@ -216,98 +317,13 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnParams p) {
     }
   }
   __syncthreads();
-
-  const bool single = nsplit == 1;
-  if (PAGED && single && has_bad_page(p, b, valid)) return;
-  for (int idx = threadIdx.x; idx < GROUP * D; idx += kThreads) {
-    const int g = idx / D, d = idx % D;
-    float mx = s_m[0][g];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][g]);
-    float lsum = 0.0f, osum = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float scale = s_m[w][g] == -INFINITY ? 0.0f : fast_exp2(s_m[w][g] - mx);
-      lsum += scale * s_l[w][g];
-      osum += scale * s_o[w][g][d];
-    }
-    const int qh = kvh * GROUP + g;
-    if (single) {
-      p.out[((size_t)b * p.q_heads + qh) * D + d] = (half_t)(osum / lsum);
-    } else {
-      float* slot = p.ws + (((size_t)b * p.q_heads + qh) * p.max_splits + split) * (D + 2);
-      slot[d] = osum;
-      if (d == 0) {
-        slot[D] = mx;
-        slot[D + 1] = lsum;
-      }
-    }
-  }
-}
-
-// Merge the per-split (max, sum, weighted) partials of the GROUP query
-// heads of one (request, kv head).  Thread (g, d) issues every load it needs
-// (the split statistics and its weighted column of each split, plus a slice
-// of the block table for the negative-page rule) before using any of them,
-// so the merge costs one memory round trip.
-template <int D, int GROUP, bool PAGED>
-__global__ __launch_bounds__(GROUP * D) void attn_combine_kernel(AttnParams p) {
-  constexpr int CHUNK = chunk_positions<D>();
-  constexpr int kRegSplits = 32;
-  const int kvh = blockIdx.x, b = blockIdx.y;
-  if (PAGED && p.active && b >= p.active[0]) return;
-  const int valid = valid_length<PAGED>(p, b);
-  if (valid < 1 || valid > p.capacity) return;
-  const int nsplit = (valid + CHUNK - 1) / CHUNK;
-  if (nsplit <= 1) return;
-  const int g = threadIdx.x / D, d = threadIdx.x % D;
-  const int qh = kvh * GROUP + g;
-  const float* base = p.ws + ((size_t)b * p.q_heads + qh) * p.max_splits * (D + 2);
-  int bad = 0;
-  if constexpr (PAGED) {
-    const int pages = (valid + p.page_size - 1) / p.page_size;
-    for (int lp = threadIdx.x; lp < pages; lp += GROUP * D)
-      bad |= p.tables[(size_t)b * p.max_pages + lp] < 0;
-  }
-  float m[kRegSplits], l[kRegSplits], o[kRegSplits];
-#pragma unroll
-  for (int s = 0; s < kRegSplits; ++s) {
-    if (s < nsplit) {
-      const float* slot = base + (size_t)s * (D + 2);
-      m[s] = slot[D];
-      l[s] = slot[D + 1];
-      o[s] = slot[d];
-    }
-  }
-  if (PAGED && __syncthreads_or(bad)) return;
-  float mx = -INFINITY;
-#pragma unroll
-  for (int s = 0; s < kRegSplits; ++s)
-    if (s < nsplit) mx = fmaxf(mx, m[s]);
-  for (int s = kRegSplits; s < nsplit; ++s) mx = fmaxf(mx, base[(size_t)s * (D + 2) + D]);
-  float lsum = 0.0f, osum = 0.0f;
-#pragma unroll
-  for (int s = 0; s < kRegSplits; ++s) {
-    if (s < nsplit) {
-      const float scale = m[s] == -INFINITY ? 0.0f : fast_exp2(m[s] - mx);
-      lsum += scale * l[s];
-      osum += scale * o[s];
-    }
-  }
-  for (int s = kRegSplits; s < nsplit; ++s) {
-    const float* slot = base + (size_t)s * (D + 2);
-    const float scale = slot[D] == -INFINITY ? 0.0f : fast_exp2(slot[D] - mx);
-    lsum += scale * slot[D + 1];
-    osum += scale * slot[d];
-  }
-  p.out[((size_t)b * p.q_heads + qh) * D + d] = (half_t)(osum / lsum);
+  finish_split<D, GROUP, PAGED>(p, b, kvh, split, nsplit, valid, s_m, s_l, s_o);
 }
 
 // ---------------------------------------------------------------- D = 128
-// Split partial for D = 128: grid (split, kv head, request), a split is
-// kWaves * kMfmaTilesPerWave tiles of 16 positions; wave w takes tiles w,
-// w + kWaves, ...  (Keeping a second tile's loads in flight per wave was
-// measured slower: the extra registers cost more occupancy than it gains.)
+// Split partial for D = 128: grid (split, kv head, request).  Wave w takes
+// the steps w, w + 4, ... of its split; a step is kMfmaTiles tiles of 16
+// positions.
 //
 // Scores come from v_mfma_f32_16x16x32_f16: A = the tile's 16 K rows, B = the
 // GROUP query heads of the kv head as columns (zero columns beyond GROUP).
@@ -315,70 +331,131 @@ __global__ __launch_bounds__(GROUP * D) void attn_combine_kernel(AttnParams p) {
 // 4s+g); acc[r] = score(position p0 + 4g + r, head j).  PV: lane (row g,
 // column chunk j) accumulates positions p0 + 4i + g, i < 4, with the
 // probabilities read back from the wave's LDS slice.
-template <bool PAGED>
-struct MfmaTile {
-  h8 ka[4], vv[4];
+//
+// MODE 0: contiguous cache [request][kv head][capacity][128].  MODE 1: pages
+// whose size is a multiple of 16 (a 16-aligned tile lies in one page: one
+// block-table lookup per tile).  Both read K/V with raw buffer loads: a
+// position that is absent (past the range, or in a missing page) gets an
+// offset past the buffer, which the hardware answers with zeros, so no load
+// is predicated.  MODE 2: any other page size, or buffers of 4 GiB or more:
+// one lookup per position and ordinary predicated loads.
+constexpr unsigned kAbsent = 0xFFFFFFF0u;
 
-  __device__ __forceinline__ void load(const AttnParams& p, const int* s_pages, int page0,
-                                       size_t contiguous_base, int kvh, int p0, int end, int j,
-                                       int g) {
-    const h8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-    {
-      const long off = offset(p, s_pages, page0, contiguous_base, kvh, p0 + j, end);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) ka[s] = off >= 0 ? load_h8(p.k + off + 8 * (4 * s + g)) : zero;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const long off = offset(p, s_pages, page0, contiguous_base, kvh, p0 + 4 * i + g, end);
-      vv[i] = off >= 0 ? load_h8(p.v + off + 8 * j) : zero;
-    }
-  }
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
 
-  // Element offset of position `pos` of the segment, -1 when absent.
-  static __device__ __forceinline__ long offset(const AttnParams& p, const int* s_pages, int page0,
-                                                size_t contiguous_base, int kvh, int pos,
-                                                int end) {
-    if (pos >= end) return -1;
-    if constexpr (PAGED) {
-      const int page = s_pages[pos / p.page_size - page0];
-      if (page < 0) return -1;
-      return (long)page * p.page_stride + (long)kvh * p.head_stride +
-             (long)(pos % p.page_size) * 128;
-    } else {
-      return (long)(contiguous_base + (size_t)pos * 128);
-    }
-  }
+__device__ __forceinline__ h8 buffer_h8(__amdgpu_buffer_rsrc_t r, unsigned byte_offset) {
+  return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_offset, 0, 0));
+}
+
+template <int MODE>
+struct KvStep {
+  h8 k[kMfmaTiles][4], v[kMfmaTiles][4];
+  long tile[kMfmaTiles];  // element offset of each tile's first position, -1 = absent
 };
 
-template <int GROUP, bool PAGED>
-__device__ __forceinline__ void mfma_attend(const MfmaTile<PAGED>& t, const h8 (&qb)[4],
-                                            const AttnParams& p, const int* s_pages, int page0,
-                                            int p0, int end, int j, int g, float (*s_pw)[GROUP],
-                                            float& m, float& lsum, float (&o)[GROUP][8]) {
-  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+template <int MODE>
+__device__ __forceinline__ bool page_ok(const AttnParams& p, int page) {
+  return page >= 0 && (p.pool_pages == 0 || page < p.pool_pages);
+}
+
+// Element offset of position `pos` (MODE 2 lookup), -1 when absent.
+__device__ __forceinline__ long paged_offset(const AttnParams& p, const int* s_pages, int page0,
+                                             int kvh, int pos, int end) {
+  if (pos >= end) return -1;
+  const int page = s_pages[page_of(p, pos) - page0];
+  if (!page_ok<2>(p, page)) return -1;
+  return (long)page * p.page_stride + (long)kvh * p.head_stride +
+         (long)slot_in_page(p, pos) * 128;
+}
+
+template <int MODE>
+__device__ __forceinline__ void issue_step(const AttnParams& p, const int* s_pages, int page0,
+                                           size_t cbase, int kvh, int p0, int end, int j, int g,
+                                           __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+                                           KvStep<MODE>& st) {
+  const h8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-  for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(t.ka[s], qb[s], acc, 0, 0, 0);
-  float sc[4];
+  for (int t = 0; t < kMfmaTiles; ++t) {
+    const int tp = p0 + 16 * t;
+    if constexpr (MODE < 2) {
+      long tile = -1;
+      if (tp < end) {
+        if constexpr (MODE == 0) {
+          tile = (long)(cbase + (size_t)tp * 128);
+        } else {
+          const int page = s_pages[page_of(p, tp) - page0];
+          if (page_ok<1>(p, page))
+            tile = (long)page * p.page_stride + (long)kvh * p.head_stride +
+                   (long)slot_in_page(p, tp) * 128;
+        }
+      }
+      st.tile[t] = tile;
+      const unsigned tb = tile < 0 ? kAbsent : (unsigned)(tile * 2);
+      const unsigned krow = (tile >= 0 && tp + j < end) ? tb + (unsigned)j * 256u : kAbsent;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int pos = p0 + 4 * g + r;
-    bool ok = pos < end;
-    if constexpr (PAGED) ok = ok && s_pages[pos / p.page_size - page0] >= 0;
-    sc[r] = ok ? acc[r] * p.scale_log2 : -INFINITY;
+      for (int s = 0; s < 4; ++s)
+        st.k[t][s] = buffer_h8(rk, krow == kAbsent ? kAbsent : krow + 16u * (4 * s + g));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const unsigned vrow =
+            (tile >= 0 && tp + 4 * i + g < end) ? tb + (unsigned)(4 * i + g) * 256u + 16u * j
+                                                : kAbsent;
+        st.v[t][i] = buffer_h8(rv, vrow);
+      }
+    } else {
+      st.tile[t] = tp < end ? 0 : -1;
+      const long krow = paged_offset(p, s_pages, page0, kvh, tp + j, end);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        st.k[t][s] = krow >= 0 ? load_h8(p.k + krow + 8 * (4 * s + g)) : zero;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const long vrow = paged_offset(p, s_pages, page0, kvh, tp + 4 * i + g, end);
+        st.v[t][i] = vrow >= 0 ? load_h8(p.v + vrow + 8 * j) : zero;
+      }
+    }
   }
-  float tile_max = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+}
+
+template <int GROUP, int MODE>
+__device__ __forceinline__ void consume_step(const AttnParams& p, const int* s_pages, int page0,
+                                             const KvStep<MODE>& st, const h8 (&qb)[4], int p0,
+                                             int end, int j, int g, float (*s_pw)[GROUP],
+                                             float& m, float& lsum, float (&o)[GROUP][8]) {
+  float sc[kMfmaTiles][4];
+  float tile_max = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < kMfmaTiles; ++t) {
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.k[t][s], qb[s], acc, 0, 0, 0);
+    const int tp = p0 + 16 * t;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int pos = tp + 4 * g + r;
+      bool ok = st.tile[t] >= 0 && pos < end;
+      if constexpr (MODE == 2) ok = ok && page_ok<2>(p, s_pages[page_of(p, pos) - page0]);
+      sc[t][r] = ok ? acc[r] * p.scale_log2 : -INFINITY;
+      tile_max = fmaxf(tile_max, sc[t][r]);
+    }
+  }
   tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16, kWave));
   tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32, kWave));
   const float next = fmaxf(m, tile_max);
   const float alpha = next == -INFINITY ? 1.0f : fast_exp2(m - next);
   float psum = 0.0f;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const float pr = sc[r] == -INFINITY ? 0.0f : fast_exp2(sc[r] - next);
-    psum += pr;
-    if (j < GROUP) s_pw[4 * g + r][j] = pr;
-  }
+  for (int t = 0; t < kMfmaTiles; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float pr = sc[t][r] == -INFINITY ? 0.0f : fast_exp2(sc[t][r] - next);
+      psum += pr;
+      if (j < GROUP) s_pw[16 * t + 4 * g + r][j] = pr;
+    }
   lsum = lsum * alpha + psum;
   m = next;
   __builtin_amdgcn_wave_barrier();
@@ -389,30 +466,33 @@ __device__ __forceinline__ void mfma_attend(const MfmaTile<PAGED>& t, const h8 (
     for (int e = 0; e < 8; ++e) o[h][e] *= ah;
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float pv[GROUP];
+  for (int t = 0; t < kMfmaTiles; ++t)
 #pragma unroll
-    for (int h = 0; h < GROUP; ++h) pv[h] = s_pw[4 * i + g][h];
+    for (int i = 0; i < 4; ++i) {
+      float pv[GROUP];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float v = (float)t.vv[i][e];
+      for (int h = 0; h < GROUP; ++h) pv[h] = s_pw[16 * t + 4 * i + g][h];
 #pragma unroll
-      for (int h = 0; h < GROUP; ++h) o[h][e] += pv[h] * v;
+      for (int e = 0; e < 8; ++e) {
+        const float v = (float)st.v[t][i][e];
+#pragma unroll
+        for (int h = 0; h < GROUP; ++h) o[h][e] += pv[h] * v;
+      }
     }
-  }
   __builtin_amdgcn_wave_barrier();
 }
 
-template <int GROUP, bool PAGED>
-__global__ __launch_bounds__(kThreads) void attn_mfma_partial_kernel(AttnParams p) {
+template <int GROUP, int MODE>
+__global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnParams p) {
   constexpr int D = 128;
-  constexpr int CHUNK = kMfmaChunk;
+  constexpr bool PAGED = MODE != 0;
   __shared__ float s_m[kWaves][GROUP];
   __shared__ float s_l[kWaves][GROUP];
   __shared__ float s_o[kWaves][GROUP][D];
-  __shared__ float s_p[kWaves][16][GROUP];
-  __shared__ int s_pages[PAGED ? CHUNK + 1 : 1];
+  __shared__ float s_p[kWaves][kMfmaStep][GROUP];
+  __shared__ int s_pages[PAGED ? kMfmaMaxChunk + 1 : 1];
 
+  const int CHUNK = p.chunk;
   const int b = blockIdx.z, kvh = blockIdx.y, split = blockIdx.x;
   if (PAGED && p.active && b >= p.active[0]) return;
   const int valid = valid_length<PAGED>(p, b);
@@ -436,8 +516,8 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_partial_kernel(AttnParams 
   }
   int page0 = 0;
   if constexpr (PAGED) {
-    page0 = begin / p.page_size;
-    const int entries = (end - 1) / p.page_size - page0 + 1;
+    page0 = page_of(p, begin);
+    const int entries = page_of(p, end - 1) - page0 + 1;
     for (int i = threadIdx.x; i < entries; i += kThreads)
       s_pages[i] = p.tables[(size_t)b * p.max_pages + page0 + i];
     __syncthreads();
@@ -448,13 +528,15 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_partial_kernel(AttnParams 
   for (int h = 0; h < GROUP; ++h)
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
-  const size_t base = ((size_t)b * p.kv_heads + kvh) * (size_t)p.capacity * D;
+  const size_t cbase = ((size_t)b * p.kv_heads + kvh) * (size_t)p.capacity * D;
+  const __amdgpu_buffer_rsrc_t rk = buffer_of(p.k, p.kv_bytes);
+  const __amdgpu_buffer_rsrc_t rv = buffer_of(p.v, p.kv_bytes);
+  float (*s_pw)[GROUP] = s_p[wave];
 
-  for (int tile = wave; begin + 16 * tile < end; tile += kWaves) {
-    MfmaTile<PAGED> t;
-    t.load(p, s_pages, page0, base, kvh, begin + 16 * tile, end, j, g);
-    mfma_attend<GROUP, PAGED>(t, qb, p, s_pages, page0, begin + 16 * tile, end, j, g, s_p[wave],
-                              m, lsum, o);
+  for (int p0 = begin + kMfmaStep * wave; p0 < end; p0 += kMfmaStep * kWaves) {
+    KvStep<MODE> st;
+    issue_step<MODE>(p, s_pages, page0, cbase, kvh, p0, end, j, g, rk, rv, st);
+    consume_step<GROUP, MODE>(p, s_pages, page0, st, qb, p0, end, j, g, s_pw, m, lsum, o);
   }
 
 #pragma unroll
@@ -473,46 +555,28 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_partial_kernel(AttnParams 
     }
   }
   __syncthreads();
-
-  const bool single = nsplit == 1;
-  if (PAGED && single && has_bad_page(p, b, valid)) return;
-  for (int idx = threadIdx.x; idx < GROUP * D; idx += kThreads) {
-    const int h = idx / D, d = idx % D;
-    float mx = s_m[0][h];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][h]);
-    float ltot = 0.0f, otot = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float scale = s_m[w][h] == -INFINITY ? 0.0f : fast_exp2(s_m[w][h] - mx);
-      ltot += scale * s_l[w][h];
-      otot += scale * s_o[w][h][d];
-    }
-    const int qh = kvh * GROUP + h;
-    if (single) {
-      p.out[((size_t)b * p.q_heads + qh) * D + d] = (half_t)(otot / ltot);
-    } else {
-      float* slot = p.ws + (((size_t)b * p.q_heads + qh) * p.max_splits + split) * (D + 2);
-      slot[d] = otot;
-      if (d == 0) {
-        slot[D] = mx;
-        slot[D + 1] = ltot;
-      }
-    }
-  }
+  finish_split<D, GROUP, PAGED>(p, b, kvh, split, nsplit, valid, s_m, s_l, s_o);
 }
 
 template <int D, int GROUP, bool PAGED>
 int launch_group(const AttnParams& p, int batch, hipStream_t stream) {
   const dim3 grid((unsigned)p.max_splits, (unsigned)p.kv_heads, (unsigned)batch);
-  if constexpr (D == 128)
-    hipLaunchKernelGGL((attn_mfma_partial_kernel<GROUP, PAGED>), grid, dim3(kThreads), 0, stream, p);
-  else
+  if constexpr (D == 128) {
+    if (p.kv_bytes != 0 && !PAGED)
+      hipLaunchKernelGGL((attn_mfma_kernel<GROUP, 0>), grid, dim3(kThreads), 0, stream, p);
+    else if (p.kv_bytes != 0 && p.page_size % 16 == 0)
+      hipLaunchKernelGGL((attn_mfma_kernel<GROUP, 1>), grid, dim3(kThreads), 0, stream, p);
+    else if (PAGED)
+      hipLaunchKernelGGL((attn_mfma_kernel<GROUP, 2>), grid, dim3(kThreads), 0, stream, p);
+    else
+      return fail("Attention: contiguous caches of 4 GiB or more are not supported.");
+  } else {
     hipLaunchKernelGGL((attn_partial_kernel<D, GROUP, PAGED>), grid, dim3(kThreads), 0, stream, p);
-  if (check_launch("attn_partial_kernel")) return 1;
+  }
+  if (check_launch("attention kernel")) return 1;
   if (p.max_splits > 1) {
-    hipLaunchKernelGGL((attn_combine_kernel<D, GROUP, PAGED>),
-                       dim3((unsigned)p.kv_heads, (unsigned)batch), dim3(GROUP * D), 0, stream, p);
+    hipLaunchKernelGGL((attn_combine_kernel<D, PAGED>),
+                       dim3((unsigned)p.q_heads, (unsigned)batch), dim3(D), 0, stream, p);
     return check_launch("attn_combine_kernel");
   }
   return 0;
@@ -529,17 +593,33 @@ int launch_attention(const AttnParams& p, int batch, hipStream_t stream) {
   }
 }
 
-int chunk_for(int64_t head_dim) {
+int page_shift_of(int64_t page_size) {
+  if (page_size <= 0 || (page_size & (page_size - 1))) return -1;
+  int shift = 0;
+  while ((1LL << shift) < page_size) ++shift;
+  return shift;
+}
+
+// Positions per split for a launch.  D = 128: the largest of 256, 512, 1024
+// that still leaves batch * kv_heads * splits >= 512 blocks (two per CU)
+// at full capacity; smaller heads use the VALU kernel's fixed split.
+int chunk_for(int64_t head_dim, int64_t batch, int64_t kv_heads, int64_t capacity) {
   switch (head_dim) {
   case 16: return chunk_positions<16>();
   case 32: return chunk_positions<32>();
   case 64: return chunk_positions<64>();
-  case 128: return chunk_positions<128>();
+  case 128: {
+    int chunk = 256;
+    while (chunk < kMfmaMaxChunk &&
+           batch * kv_heads * ((capacity + 2 * chunk - 1) / (2 * chunk)) >= 512)
+      chunk *= 2;
+    return chunk;
+  }
   default: return 0;
   }
 }
 
-bool head_dim_ok(int64_t head_dim) { return chunk_for(head_dim) > 0; }
+bool head_dim_ok(int64_t head_dim) { return chunk_for(head_dim, 1, 1, 1) > 0; }
 
 template <bool PAGED>
 int dispatch_attention(const AttnParams& p, int batch, int head_dim, hipStream_t stream) {
@@ -564,8 +644,8 @@ int common_checks(const void* q, const void* k, const void* v, const void* out, 
                   q_heads % kv_heads == 0 && capacity > 0 && capacity < (1LL << 30),
               "Attention: invalid batch, head counts or capacity.");
   TMC_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v), "Attention: q, K and V must be 16-byte aligned.");
-  TMC_REQUIRE((capacity + chunk_for(head_dim) - 1) / chunk_for(head_dim) <= 1024,
-              "Attention: capacity exceeds 1024 splits.");
+  const int chunk = chunk_for(head_dim, batch, kv_heads, capacity);
+  TMC_REQUIRE((capacity + chunk - 1) / chunk <= 1024, "Attention: capacity exceeds 1024 splits.");
   return 0;
 }
 
@@ -577,7 +657,7 @@ using namespace tmc;
 extern "C" size_t tmc_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads,
                                                 int64_t head_dim, int64_t capacity) {
   if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || capacity <= 0 || q_heads % kv_heads) return 0;
-  const int chunk = chunk_for(head_dim);
+  const int chunk = chunk_for(head_dim, batch, kv_heads, capacity);
   if (chunk <= 0) return 0;
   const int64_t splits = (capacity + chunk - 1) / chunk;
   if (splits <= 1) return 0;
@@ -607,8 +687,13 @@ extern "C" int tmc_decode_attention(const void* q, const void* key_cache, const 
   p.kv_heads = (int)kv_heads;
   p.capacity = (int)capacity;
   p.page_size = 1;
-  const int chunk = chunk_for(head_dim);
-  p.max_splits = (int)((capacity + chunk - 1) / chunk);
+  p.page_shift = 0;
+  {
+    const uint64_t bytes = (uint64_t)batch * kv_heads * capacity * head_dim * 2;
+    p.kv_bytes = bytes < kAbsent ? (unsigned)bytes : 0u;
+  }
+  p.chunk = chunk_for(head_dim, batch, kv_heads, capacity);
+  p.max_splits = (int)((capacity + p.chunk - 1) / p.chunk);
   p.scale_log2 = (float)(1.0 / std::sqrt((double)head_dim)) * 1.4426950408889634f;
   return dispatch_attention<false>(p, (int)batch, (int)head_dim, as_stream(stream));
 }
@@ -619,17 +704,20 @@ extern "C" int tmc_paged_decode_attention(const void* q, const void* key_pool,
                                           const int32_t* active_count, void* out, int dtype,
                                           int64_t max_batch, int64_t q_heads, int64_t kv_heads,
                                           int64_t head_dim, int64_t page_size, int64_t max_pages,
-                                          int64_t page_stride, int64_t head_stride,
-                                          void* workspace, size_t workspace_bytes,
-                                          void* stream) {
+                                          int64_t pool_pages, int64_t page_stride,
+                                          int64_t head_stride, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
   const int64_t capacity = page_size * max_pages;
   if (common_checks(q, key_pool, value_pool, out, dtype, max_batch, q_heads, kv_heads, head_dim,
                     capacity))
     return 1;
   TMC_REQUIRE(valid_lengths && block_tables, "Paged attention: null lengths or block tables.");
   TMC_REQUIRE(page_size > 0 && max_pages > 0 && page_stride > 0 && head_stride >= 0 &&
-                  (page_stride % 8) == 0 && (head_stride % 8) == 0,
+                  (page_stride % 8) == 0 && (head_stride % 8) == 0 && pool_pages >= 0 &&
+                  pool_pages < (1LL << 31),
               "Paged attention: invalid page geometry (strides must be multiples of 8 elements).");
+  TMC_REQUIRE(pool_pages == 0 || (kv_heads - 1) * head_stride + page_size * head_dim <= page_stride,
+              "Paged attention: a page's kv heads overrun the page stride.");
   const size_t need = tmc_attention_workspace_bytes(max_batch, q_heads, kv_heads, head_dim, capacity);
   TMC_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
               "Paged attention: workspace is smaller than tmc_attention_workspace_bytes().");
@@ -648,9 +736,15 @@ extern "C" int tmc_paged_decode_attention(const void* q, const void* key_pool,
   p.kv_heads = (int)kv_heads;
   p.capacity = (int)capacity;
   p.page_size = (int)page_size;
+  p.page_shift = page_shift_of(page_size);
+  p.pool_pages = (long)pool_pages;
+  {
+    const uint64_t bytes = (uint64_t)pool_pages * page_stride * 2;
+    p.kv_bytes = pool_pages > 0 && bytes < kAbsent ? (unsigned)bytes : 0u;
+  }
   p.max_pages = (int)max_pages;
-  const int chunk = chunk_for(head_dim);
-  p.max_splits = (int)((capacity + chunk - 1) / chunk);
+  p.chunk = chunk_for(head_dim, max_batch, kv_heads, capacity);
+  p.max_splits = (int)((capacity + p.chunk - 1) / p.chunk);
   p.scale_log2 = (float)(1.0 / std::sqrt((double)head_dim)) * 1.4426950408889634f;
   return dispatch_attention<true>(p, (int)max_batch, (int)head_dim, as_stream(stream));
 }

@@ -170,7 +170,8 @@ struct tmc_buffer {
 namespace {
 
 struct LaunchContext {
-  std::vector<void*> ptrs;  // inputs then outputs, device addresses
+  std::vector<void*> ptrs;     // inputs then outputs, device addresses
+  std::vector<size_t> counts;  // their element counts
   std::vector<uint32_t> constants;
   void* workspace = nullptr;
   size_t workspace_bytes = 0;
@@ -476,11 +477,13 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     s.counts = {(size_t)(b * qh * d), 0, 0, (size_t)b, (size_t)(b * mp), 1, (size_t)(b * qh * d)};
     s.workspace_bytes = tmc_attention_workspace_bytes(b, qh, kvh, d, ps * mp);
     s.launch = [=](const LaunchContext& c) {
+      const int64_t pool_pages =
+          (int64_t)(std::min(c.counts[1], c.counts[2]) / (size_t)page_stride);
       return tmc_paged_decode_attention(
           c.ptrs[0], c.ptrs[1], c.ptrs[2], static_cast<const int32_t*>(c.ptrs[3]),
           static_cast<const int32_t*>(c.ptrs[4]), static_cast<const int32_t*>(c.ptrs[5]),
-          c.ptrs[6], dt, b, qh, kvh, d, ps, mp, page_stride, head_stride, c.workspace,
-          c.workspace_bytes, c.stream);
+          c.ptrs[6], dt, b, qh, kvh, d, ps, mp, pool_pages, page_stride, head_stride,
+          c.workspace, c.workspace_bytes, c.stream);
     };
     return true;
   }
@@ -764,13 +767,25 @@ extern "C" int tmc_prepare(tmc_runtime* rt, const tmc_kernel* kernel, tmc_buffer
       return fail("Input buffer " + std::to_string(i) + " holds " + std::to_string(b->count) +
                   " elements; the kernel reads " + std::to_string(s.counts[i]) + ".");
     exec->ctx.ptrs.push_back(b->ptr);
+    exec->ctx.counts.push_back(b->count);
   }
-  for (auto* o : exec->outputs) exec->ctx.ptrs.push_back(o->ptr);
+  for (auto* o : exec->outputs) {
+    exec->ctx.ptrs.push_back(o->ptr);
+    exec->ctx.counts.push_back(o->count);
+  }
   if (constants) exec->ctx.constants.assign(constants, constants + n_constants);
   exec->ctx.stream = rt->stream;
   if (s.workspace_bytes) {
     if (hip_ok(hipMalloc(&exec->ctx.workspace, s.workspace_bytes), "workspace allocation")) return 1;
     exec->ctx.workspace_bytes = s.workspace_bytes;
+    // A defined starting state for the workspace (filled once, here,
+    // outside any captured sequence).
+    if (hip_ok(hipMemsetAsync(exec->ctx.workspace, 0, s.workspace_bytes, rt->stream),
+               "workspace fill") ||
+        hip_ok(hipStreamSynchronize(rt->stream), "workspace fill")) {
+      (void)hipFree(exec->ctx.workspace);
+      return 1;
+    }
   }
   *out = exec.release();
   return 0;

@@ -415,4 +415,121 @@ ServingExecutionResult runContinuousBatch(hip::HipRuntime& runtime,
   return result;
 }
 
+DecodeThroughput measureDecodeThroughput(hip::HipRuntime& runtime,
+                                         std::shared_ptr<DecoderLLMModelResources> model,
+                                         const std::vector<std::vector<std::int32_t>>& prompts,
+                                         std::size_t decodeTokens, std::size_t pageSize,
+                                         bool timeGpu) {
+  DecodeThroughput result;
+  try {
+    if (!model || prompts.empty() || pageSize == 0)
+      throw std::invalid_argument("Decode measurement needs a model, prompts and a page size.");
+    const auto& plan = model->plan;
+    const std::size_t B = prompts.size(), L = plan.layerCount;
+    std::size_t pagesNeeded = 0, longest = 0;
+    for (const auto& prompt : prompts) {
+      if (prompt.empty() || prompt.size() + decodeTokens > plan.attention.capacity)
+        throw std::invalid_argument("Prompt plus decode tokens exceed the cache capacity.");
+      for (const auto token : prompt)
+        if (token < 0 || static_cast<std::size_t>(token) >= plan.vocabularySize)
+          throw std::invalid_argument("Prompt token outside the vocabulary.");
+      pagesNeeded += pagesFor(prompt.size() + decodeTokens, pageSize);
+      longest = std::max(longest, prompt.size());
+    }
+    const std::size_t poolPages = std::max(pagesNeeded, pagesFor(plan.attention.capacity, pageSize));
+    std::vector<std::shared_ptr<KVPagePool>> pools;
+    for (std::size_t l = 0; l < L; ++l) {
+      auto pool = createKVPagePool(runtime, plan.kvPlan(), pageSize, poolPages);
+      if (!pool.pool) throw std::runtime_error(pool.errorMessage);
+      pools.push_back(std::move(pool.pool));
+    }
+    auto created = createBatchedDecodeExecutor(runtime, model, pools, B, nullptr);
+    if (!created.executor) throw std::runtime_error(created.errorMessage);
+    auto& executor = *created.executor;
+    std::vector<std::vector<std::unique_ptr<KVCacheState>>> states(B);
+    for (auto& row : states)
+      for (const auto& pool : pools) {
+        auto state = createKVCacheState(runtime, plan.kvPlan(), pool, false);
+        if (!state.state) throw std::runtime_error(state.errorMessage);
+        row.push_back(std::move(state.state));
+      }
+    result.rows = B;
+    result.generatedTokenIds.assign(B, {});
+    std::vector<std::int32_t> last(B, -1);
+
+    // One batched step over `rows`; commits the new lengths.
+    std::vector<double> gpuTimes, hostTimes;
+    auto step = [&](const std::vector<std::size_t>& rows, const std::vector<std::int32_t>& tokens,
+                    bool record) {
+      std::vector<std::int32_t> lengths;
+      std::vector<std::vector<std::int32_t>> tables(L);
+      for (const auto r : rows) {
+        const std::size_t next = states[r].front()->currentLength() + 1;
+        lengths.push_back(static_cast<std::int32_t>(next));
+        for (std::size_t l = 0; l < L; ++l) {
+          const auto error = states[r][l]->stageLength(runtime, next);
+          if (!error.empty()) throw std::runtime_error(error);
+          auto table = states[r][l]->pageTable();
+          table.resize(executor.maxPages(), -1);
+          tables[l].insert(tables[l].end(), table.begin(), table.end());
+        }
+      }
+      const auto t0 = Clock::now();
+      const auto out = executor.run(tokens, lengths, tables, false, timeGpu);
+      const double us = elapsedUs(t0, Clock::now());
+      if (!out.passed) throw std::runtime_error(out.errorMessage);
+      if (record) {
+        hostTimes.push_back(us);
+        if (out.gpuExecutionTimeUs) gpuTimes.push_back(*out.gpuExecutionTimeUs);
+      }
+      for (std::size_t k = 0; k < rows.size(); ++k)
+        for (auto& state : states[rows[k]]) state->commitLength(static_cast<std::size_t>(lengths[k]));
+      return out.nextTokenIds;
+    };
+
+    const auto promptStart = Clock::now();
+    for (std::size_t t = 0; t < longest; ++t) {
+      std::vector<std::size_t> rows;
+      std::vector<std::int32_t> tokens;
+      for (std::size_t r = 0; r < B; ++r)
+        if (t < prompts[r].size()) {
+          rows.push_back(r);
+          tokens.push_back(prompts[r][t]);
+        }
+      const auto next = step(rows, tokens, false);
+      for (std::size_t k = 0; k < rows.size(); ++k)
+        if (t + 1 == prompts[rows[k]].size()) {
+          last[rows[k]] = static_cast<std::int32_t>(next[k]);
+          result.generatedTokenIds[rows[k]].push_back(next[k]);
+        }
+    }
+    result.promptPhaseUs = elapsedUs(promptStart, Clock::now());
+
+    std::vector<std::size_t> all(B);
+    for (std::size_t r = 0; r < B; ++r) all[r] = r;
+    std::size_t kvTokens = 0;
+    for (std::size_t r = 0; r < B; ++r)
+      for (std::size_t s = 0; s < decodeTokens; ++s) kvTokens += prompts[r].size() + 1 + s;
+    result.kvBytesRead = kvTokens * L * 2 * plan.kvWidth() * 2;
+    const auto decodeStart = Clock::now();
+    for (std::size_t s = 0; s < decodeTokens; ++s) {
+      const auto next = step(all, last, true);
+      for (std::size_t r = 0; r < B; ++r) {
+        last[r] = static_cast<std::int32_t>(next[r]);
+        result.generatedTokenIds[r].push_back(next[r]);
+      }
+    }
+    result.decodePhaseUs = elapsedUs(decodeStart, Clock::now());
+    result.decodeSteps = decodeTokens;
+    if (result.decodePhaseUs > 0.0)
+      result.tokensPerSecond = static_cast<double>(B * decodeTokens) * 1e6 / result.decodePhaseUs;
+    if (const auto st = benchmark::summarizeTimings(gpuTimes)) result.stepGpu = *st;
+    if (const auto st = benchmark::summarizeTimings(hostTimes)) result.stepHost = *st;
+    result.passed = true;
+  } catch (const std::exception& error) {
+    result.errorMessage = error.what();
+  }
+  return result;
+}
+
 }  // namespace tensor::runtime

@@ -109,4 +109,27 @@ using BatchedStep = std::function<BatchedDecodeRun(
     const std::vector<ServingRequestSpec>& requests, const ServingConfig& config,
     std::ostream& log);
 
+// Steady-state decode throughput of `prompts.size()` requests decoding
+// together: every prompt is first run through batched steps (prefill by
+// decode, rows leave the batch when their prompt ends), then all rows decode
+// `decodeTokens` greedy tokens in lock-step; that second phase is timed.
+struct DecodeThroughput {
+  bool passed = false;
+  std::size_t rows = 0;
+  std::size_t decodeSteps = 0;
+  double promptPhaseUs = 0.0;
+  double decodePhaseUs = 0.0;      // host wall time of the timed steps
+  double tokensPerSecond = 0.0;    // rows * decodeSteps / decodePhaseUs
+  benchmark::Statistics stepGpu;   // per timed step, HIP-event time
+  benchmark::Statistics stepHost;  // per timed step, host wall time
+  std::vector<std::vector<float>> generatedTokenIds;  // per row
+  std::size_t kvBytesRead = 0;     // K/V bytes the timed attention steps read
+  std::string errorMessage;
+};
+
+[[nodiscard]] DecodeThroughput measureDecodeThroughput(
+    hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
+    const std::vector<std::vector<std::int32_t>>& prompts, std::size_t decodeTokens,
+    std::size_t pageSize, bool timeGpu);
+
 }  // namespace tensor::runtime

@@ -422,6 +422,32 @@ PYBIND11_MODULE(_tmc_host, m) {
           return d;
         });
 
+  m.def("measure_decode_throughput",
+        [](hip::HipRuntime& rt, std::shared_ptr<DecoderLLMModelResources> model,
+           const std::vector<std::vector<std::int32_t>>& prompts, std::size_t decodeTokens,
+           std::size_t pageSize, bool timeGpu) {
+          DecodeThroughput r;
+          {
+            py::gil_scoped_release release;
+            r = measureDecodeThroughput(rt, std::move(model), prompts, decodeTokens, pageSize, timeGpu);
+          }
+          py::dict d;
+          d["passed"] = r.passed;
+          d["error"] = r.errorMessage;
+          d["rows"] = r.rows;
+          d["decode_steps"] = r.decodeSteps;
+          d["prompt_phase_us"] = r.promptPhaseUs;
+          d["decode_phase_us"] = r.decodePhaseUs;
+          d["tokens_per_second"] = r.tokensPerSecond;
+          d["step_gpu"] = statsToDict(r.stepGpu);
+          d["step_host"] = statsToDict(r.stepHost);
+          d["generated_token_ids"] = r.generatedTokenIds;
+          d["kv_bytes_read"] = r.kvBytesRead;
+          return d;
+        },
+        py::arg("runtime"), py::arg("model"), py::arg("prompts"), py::arg("decode_tokens"),
+        py::arg("page_size") = 16, py::arg("time_gpu") = false);
+
   // The scheduler over host-only pools and a Python step (CPU tests):
   // step(tokens, valid_lengths, tables, read_logits) -> (next_tokens, logits).
   m.def("run_continuous_batch_with",

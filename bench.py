@@ -16,7 +16,12 @@ Printed JSON line extras:
                 C restatement of the reference CPU path) on a bounded number
                 of whole blocks of the same workload;
   extra         GB/s of the other BASELINE configs (C1 GEMV, C2 at B=8, C3
-                contiguous attention at L=4095, C4 paged GQA attention).
+                contiguous attention at L=4095, C4 paged GQA attention) and
+                C5: Llama-7B-shaped decode tokens/s at batch 1 and 16 (random
+                fp16 weights ~N(0, 0.02) made on the device, prompts ~U[32,512]
+                run through the batched decode graph, then 128 greedy tokens per
+                sequence decoded in lock-step and timed), with the CPU oracle's
+                decode step timed on a bounded layer sample beside it.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -188,7 +193,7 @@ def extra_measurements(tmc, torch, iters: int) -> dict:
     o = torch.empty((1, heads * d), dtype=f16, device="cuda")
     valid = torch.tensor([4096], dtype=torch.int32, device="cuda")
     wsb = tmc.attention_workspace_bytes(1, heads, heads, d, cap)
-    wsp = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device="cuda")
+    wsp = torch.zeros(max(wsb // 4, 1), dtype=torch.float32, device="cuda")
     sec = time_loop(torch, lambda i: tmc.decode_attention(q, ks[i % copies], vs[i % copies], valid,
                                                           o, 1, heads, heads, d, cap, wsp), iters)
     c3_bytes = 2 * heads * 4096 * d * 2 + 2 * heads * d * 2
@@ -217,7 +222,7 @@ def extra_measurements(tmc, torch, iters: int) -> dict:
     vl = torch.from_numpy(lengths.astype(np.int32)).cuda()
     active = torch.tensor([batch], dtype=torch.int32, device="cuda")
     wsb = tmc.attention_workspace_bytes(batch, qh, kvh, d, max_pages * p)
-    wsp = torch.empty(max(wsb // 4, 1), dtype=torch.float32, device="cuda")
+    wsp = torch.zeros(max(wsb // 4, 1), dtype=torch.float32, device="cuda")
     sec = time_loop(torch, lambda i: tmc.paged_decode_attention(
         qd, kp, vp, vl, sets[i % len(sets)], active, od, batch, qh, kvh, d, p, max_pages,
         kvh * p * d, p * d, wsp), iters)
@@ -225,6 +230,101 @@ def extra_measurements(tmc, torch, iters: int) -> dict:
     out["c4_paged_gqa_attention_gbps"] = round(c4_bytes / sec / 1e9, 1)
     out["c4_paged_gqa_attention_us"] = round(sec * 1e6, 2)
     out["c4_bytes"] = c4_bytes
+    return out
+
+
+C5 = dict(layers=32, hidden=4096, heads=32, head_dim=128, intermediate=11008, vocabulary=32000,
+          capacity=1024, epsilon=1e-6, page_size=16, decode_tokens=128)
+
+
+def c5_plan(host):
+    plan = host.DecoderLLMPlan()
+    att = host.KVCachePlan()
+    att.heads, att.head_dimension, att.capacity = C5["heads"], C5["head_dim"], C5["capacity"]
+    att.dtype = host.DType.Float16
+    plan.attention = att
+    plan.layer_count, plan.intermediate_size = C5["layers"], C5["intermediate"]
+    plan.vocabulary_size, plan.rms_norm_epsilon = C5["vocabulary"], C5["epsilon"]
+    return plan
+
+
+def c5_prompts(batch: int):
+    import numpy as np
+    rng = np.random.default_rng(502)
+    return [list(map(int, rng.integers(0, C5["vocabulary"], rng.integers(32, 513))))
+            for _ in range(batch)]
+
+
+def c5_gpu(tmc) -> dict:
+    """Decode tokens/s of the 7B-shaped model at batch 1 and 16 (C++ host
+    layer: graph-captured batched decode over paged KV pools)."""
+    host = tmc.host()
+    rt = host.HipRuntime()
+    model = host.create_synthetic_model_resources(rt, c5_plan(host), 501)
+    out = {"model_bytes": int(model.storage_bytes)}
+    for batch in (1, 16):
+        r = host.measure_decode_throughput(rt, model, c5_prompts(batch), C5["decode_tokens"],
+                                           C5["page_size"], False)
+        if not r["passed"]:
+            raise RuntimeError(f"C5 batch {batch}: {r['error']}")
+        steps = r["decode_steps"]
+        out[f"b{batch}_tokens_per_s"] = round(r["tokens_per_second"], 1)
+        out[f"b{batch}_ms_per_step"] = round(r["decode_phase_us"] / steps / 1e3, 4)
+        # bytes a step must read: every weight except the embedding table (B
+        # rows of it), plus the K/V of every attended position
+        weights = model.storage_bytes - C5["vocabulary"] * C5["hidden"] * 2
+        out[f"b{batch}_weight_and_kv_gbps"] = round(
+            (weights * steps + r["kv_bytes_read"]) / (r["decode_phase_us"] * 1e3), 1)
+        out[f"b{batch}_prompt_tokens"] = sum(len(p) for p in c5_prompts(batch))
+        print(f"[bench] C5 batch {batch}: {out[f'b{batch}_tokens_per_s']} tokens/s", flush=True)
+    del model
+    return out
+
+
+def c5_cpu_baseline(seconds_hint: float = 10.0) -> dict:
+    """The oracle's decode step (oracle/libtmc_oracle.so, one thread) at 7B
+    width on a bounded sample: `n` decoder layers (layer_limit) plus the LM
+    head, scaled to 32 layers.  Weight values do not change the oracle's
+    work, so fixed fp16 patterns stand in for random weights."""
+    import numpy as np
+    from oracle import oracle as orc
+    orc.build()
+    H, I, V, NH, D = C5["hidden"], C5["intermediate"], C5["vocabulary"], C5["heads"], C5["head_dim"]
+    pattern = np.random.default_rng(0).integers(0x2000, 0x2c00, 4096, dtype=np.uint16)
+    pattern[1::2] |= 0x8000
+    w = lambda *shape: np.resize(pattern, shape)  # noqa: E731
+    one = np.full(H, 0x3C00, np.uint16)
+    cap = 64
+    pos = np.arange(cap)[:, None]
+    freq = 10000.0 ** (-np.arange(0, D, 2) / D)
+    layer = dict(input_norm=one, wq=w(H, H), wk=w(H, H), wv=w(H, H), wo=w(H, H), post_norm=one,
+                 wg=w(I, H), wu=w(I, H), wd=w(H, I))
+    out = {}
+    for batch, n in ((1, 2), (16, 1)):
+        m = dict(embedding=w(batch, H), final_norm=one, lm_head=w(V, H),
+                 rope_cos=np.cos(pos * freq).astype(np.float32),
+                 rope_sin=np.sin(pos * freq).astype(np.float32), layers=[layer] * n)
+        cfg = dict(layers=C5["layers"], hidden=H, heads=NH, head_dim=D, intermediate=I,
+                   vocabulary=V, capacity=cap, epsilon=1e-6)
+        pages = cap // 16
+        kp = [np.zeros(batch * pages * NH * 16 * D, np.uint16) for _ in range(n)]
+        vp = [p.copy() for p in kp]
+        tables = np.zeros((C5["layers"], batch, pages), np.int32)
+        for b in range(batch):
+            tables[:, b, :] = b * pages + np.arange(pages)
+        t0 = time.perf_counter()
+        orc.decoder_step(m, cfg, kp, vp, 16, pages, tables, np.arange(batch, dtype=np.int32),
+                         np.ones(batch, np.int32), layer_limit=n)
+        per_layer = (time.perf_counter() - t0) / n
+        t0 = time.perf_counter()
+        orc.linear(w(batch, H), m["lm_head"], orc.F16)
+        head = time.perf_counter() - t0
+        step = per_layer * C5["layers"] + head
+        out[f"b{batch}_tokens_per_s"] = round(batch / step, 5)
+        out[f"b{batch}_sample"] = (f"{n} layer(s) of the decode step ({per_layer:.2f} s each) + "
+                                   f"LM head ({head:.2f} s), scaled to 32 layers")
+    out["cores"] = 1
+    out["kind"] = "port"
     return out
 
 
@@ -291,6 +391,10 @@ def main() -> int:
     steps_reported = steps
     extra = {} if args.no_extra else extra_measurements(tmc, torch, 200)
     print("[bench] extras done", flush=True)
+    if not args.no_extra:
+        extra["c5_decode"] = c5_gpu(tmc)
+        if not args.no_cpu:
+            extra["c5_decode"]["cpu_baseline"] = c5_cpu_baseline()
     cpu = None if args.no_cpu else cpu_baseline(block, args.cpu_seconds)
 
     line = {

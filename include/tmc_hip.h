@@ -245,7 +245,9 @@ int tmc_serving_kv_append(const void *input, const int32_t *valid_lengths,
                           int64_t capacity, int64_t page_size, int head_major, void *stream);
 
 /* Bytes of device workspace the split-KV attention needs for these limits
- * on the current device (0 when none is needed). */
+ * (0 when none is needed): one (max, sum, weighted[D]) fp32 partial per
+ * request, query head and split.  Launches that share one workspace must not
+ * overlap. */
 size_t tmc_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads,
                                      int64_t head_dim, int64_t capacity);
 
@@ -263,16 +265,19 @@ int tmc_decode_attention(const void *q, const void *key_cache, const void *value
  * KVCacheMetalEmitter.cpp:312-406, generalised to GQA): element
  * (page, kvh, offset, d) at page*page_stride + kvh*head_stride +
  * offset*D + d; request r attends [0, valid_lengths[r]) through
- * block_tables[r*max_pages + pos/page_size].  Requests >= active_count[0]
- * (active_count may be NULL = all), invalid lengths, or a negative page in
- * range leave their output untouched. */
+ * block_tables[r*max_pages + pos/page_size].  pool_pages is the number of
+ * pages each pool holds (0 = unknown); a page id at or past it counts as
+ * missing.  Requests >= active_count[0] (active_count may be NULL = all),
+ * invalid lengths, or a missing (negative) page in range leave their output
+ * untouched.  No counterpart of pool_pages in the reference: it bounds every
+ * pool access the kernel makes. */
 int tmc_paged_decode_attention(const void *q, const void *key_pool, const void *value_pool,
                                const int32_t *valid_lengths, const int32_t *block_tables,
                                const int32_t *active_count, void *out, int dtype,
                                int64_t max_batch, int64_t q_heads, int64_t kv_heads,
                                int64_t head_dim, int64_t page_size, int64_t max_pages,
-                               int64_t page_stride, int64_t head_stride, void *workspace,
-                               size_t workspace_bytes, void *stream);
+                               int64_t pool_pages, int64_t page_stride, int64_t head_stride,
+                               void *workspace, size_t workspace_bytes, void *stream);
 
 /* Decode-step fusion of emitServingRoPE (DecoderLLMMetalEmitter.cpp:260-312)
  * for q and k with emitServingPagedCacheAppend (:314-373) for the rotated k

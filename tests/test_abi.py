@@ -51,6 +51,10 @@ def test_attention_workspace_sizes(tmc):
     # VALU kernel (D=64): one split of 256 positions needs no workspace,
     # otherwise batch x q_heads x splits x (D + 2) floats
     assert tmc.attention_workspace_bytes(2, 8, 8, 64, 256) == 0
+    # [request][q head][split][D + 2] floats
     assert tmc.attention_workspace_bytes(2, 8, 8, 64, 1024) == 2 * 8 * 4 * 66 * 4
+    # D = 128: 1024-position splits once batch * kv_heads * splits keeps 512 blocks
+    assert tmc.attention_workspace_bytes(16, 32, 8, 128, 4096) == 16 * 32 * 4 * 130 * 4
+    assert tmc.attention_workspace_bytes(1, 32, 32, 128, 4096) == 1 * 32 * 16 * 130 * 4
     # bad head ratio
     assert tmc.attention_workspace_bytes(2, 6, 4, 64, 1024) == 0

@@ -226,7 +226,8 @@ def test_paged_and_serving_append_bit_exact(tmc, orc, torch):
 # ---------------------------------------------------------------- attention
 def _ws(tmc, torch, batch, qh, kvh, d, cap):
     n = tmc.attention_workspace_bytes(batch, qh, kvh, d, cap)
-    return torch.empty(max(n // 4, 1), dtype=torch.float32, device="cuda") if n else None
+    # zero-filled once: the kernels keep split counters there (and leave them at zero)
+    return torch.zeros(max(n // 4, 1), dtype=torch.float32, device="cuda") if n else None
 
 
 @pytest.mark.parametrize("length", [128, 1024, 4095])
@@ -311,8 +312,11 @@ def test_c4_paged_gqa_attention(tmc, orc, torch):
     assert_f16_path(values(out), ref, what="paged GQA attention (C4)")
 
 
-def test_paged_attention_inactive_and_bad_pages_untouched(tmc, orc, torch):
-    batch, qh, kvh, d, p, max_pages = 4, 8, 2, 64, 16, 8
+@pytest.mark.parametrize("d,p", [(64, 16), (128, 16), (128, 8)])
+def test_paged_attention_inactive_and_bad_pages_untouched(tmc, orc, torch, d, p):
+    """Rows past the active count, rows whose range needs a missing page (a
+    negative entry, or a page id past the pool) keep their output."""
+    batch, qh, kvh, max_pages = 5, 8, 2, 8
     pages = 32
     k_pool = orc.f16(normal(410, (pages, kvh, p, d)))
     v_pool = orc.f16(normal(411, (pages, kvh, p, d)))
@@ -321,20 +325,24 @@ def test_paged_attention_inactive_and_bad_pages_untouched(tmc, orc, torch):
     tables[0, :3] = [4, 9, 1]
     tables[1, :2] = [7, -1]  # hole inside the valid range
     tables[2, :8] = np.arange(10, 18)
-    tables[3, :1] = [3]
-    lengths = np.array([40, 20, 128, 5], np.int32)
+    tables[3, :1] = [pages + 3]  # past the end of the pool
+    tables[4, :1] = [3]
+    lengths = np.array([3 * p - 8, p + 4, 8 * p, 5, 5], np.int32)
     out = torch.full((batch, qh * d), float("nan"), dtype=torch.float16, device="cuda")
-    active = torch.tensor([3], dtype=torch.int32, device="cuda")
+    active = torch.tensor([4], dtype=torch.int32, device="cuda")
     cap = max_pages * p
     tmc.paged_decode_attention(dev_f16(q), dev_f16(k_pool), dev_f16(v_pool), dev(lengths),
                                dev(tables), active, out, batch, qh, kvh, d, p, max_pages,
                                kvh * p * d, p * d, _ws(tmc, torch, batch, qh, kvh, d, cap))
     torch.cuda.synchronize()
     got = values(out)
+    oracle_tables = tables.copy()
+    oracle_tables[3] = -1  # the oracle reads pools directly: give it the missing-page form
     ref, written = orc.paged_attention(q, k_pool, v_pool, F16, qh, kvh, d, p, kvh * p * d, p * d,
-                                       tables, max_pages, lengths, 3)
-    assert list(written.all(axis=1)) == [True, False, True, False]
-    assert np.isnan(got[1]).all() and np.isnan(got[3]).all()
+                                       oracle_tables, max_pages, lengths, 4)
+    assert list(written.all(axis=1)) == [True, False, True, False, False]
+    for row in (1, 3, 4):
+        assert np.isnan(got[row]).all(), row
     assert_f16_path(got[[0, 2]], ref[[0, 2]], what="paged attention written rows")
 
 
