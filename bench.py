@@ -123,16 +123,29 @@ def build_sequences(tmc, rt, block):
     return rt.sequence(execs), execs, rt.sequence(gates)
 
 
-def time_loop(torch, fn, iters: int) -> float:
-    """Seconds per iteration of fn(i), measured with events on the current stream."""
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+def time_loop(torch, fn, iters: int, replays: int = 5) -> float:
+    """Seconds per call of fn(i): `iters` calls captured once into a CUDA (HIP)
+    graph on a side stream, then the graph replayed `replays` times between
+    two events, so host launch cost stays out of the figure."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(3):
+            fn(i)
     torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for i in range(iters):
+            fn(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
-    for i in range(iters):
-        fn(i)
+    for _ in range(replays):
+        graph.replay()
     stop.record()
     stop.synchronize()
-    return start.elapsed_time(stop) / 1000.0 / iters
+    return start.elapsed_time(stop) / 1000.0 / (iters * replays)
 
 
 def cpu_baseline(block: MlpBlock, seconds: float) -> dict:
@@ -389,7 +402,7 @@ def main() -> int:
     print(f"[bench] gate_up_silu {sec * 1e6:.2f} us/launch", flush=True)
     del execs
     steps_reported = steps
-    extra = {} if args.no_extra else extra_measurements(tmc, torch, 200)
+    extra = {} if args.no_extra else extra_measurements(tmc, torch, 40)
     print("[bench] extras done", flush=True)
     if not args.no_extra:
         extra["c5_decode"] = c5_gpu(tmc)
