@@ -44,6 +44,8 @@ def _declare(l):
         "tmc_gate_up_silu_f16": (i32, [vp, vp, vp, vp, i64, i64, i64, vp]),
         "tmc_rmsnorm": (i32, [vp, vp, vp, i32, i64, i64, f, vp]),
         "tmc_add_rmsnorm": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, f, vp]),
+        "tmc_rmsnorm_threads": (i32, [vp, vp, vp, i32, i64, i64, f, i32, i32, vp]),
+        "tmc_add_rmsnorm_threads": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, f, i32, i32, vp]),
         "tmc_silu_mul": (i32, [vp, vp, vp, i32, i64, vp]),
         "tmc_add": (i32, [vp, vp, vp, i32, i64, vp]),
         "tmc_embedding": (i32, [vp, vp, vp, i32, i64, i64, i64, vp]),
@@ -222,6 +224,22 @@ def add_rmsnorm(residual, update, w, sum_out, norm_out, eps, stream=None):
     check(lib().tmc_add_rmsnorm(_ptr(residual), _ptr(update), _ptr(w), _ptr(sum_out),
                                 _ptr(norm_out), _dtype_code(residual), rows, width, eps,
                                 _stream(stream)), "tmc_add_rmsnorm")
+
+
+def rmsnorm_threads(x, w, y, eps, threads, variant=0, stream=None):
+    """tmc_rmsnorm_threads: threads 64..1024, variant 0 default / 1 two-pass."""
+    rows, width = x.shape
+    check(lib().tmc_rmsnorm_threads(_ptr(x), _ptr(w), _ptr(y), _dtype_code(x), rows, width, eps,
+                                    threads, variant, _stream(stream)), "tmc_rmsnorm_threads")
+
+
+def add_rmsnorm_threads(residual, update, w, sum_out, norm_out, eps, threads, variant=0,
+                        stream=None):
+    rows, width = residual.shape
+    check(lib().tmc_add_rmsnorm_threads(_ptr(residual), _ptr(update), _ptr(w), _ptr(sum_out),
+                                        _ptr(norm_out), _dtype_code(residual), rows, width, eps,
+                                        threads, variant, _stream(stream)),
+          "tmc_add_rmsnorm_threads")
 
 
 def silu_mul(gate, up, out, stream=None):

@@ -246,7 +246,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnParams p) {
   __shared__ float s_o[kWaves][GROUP][D];
   __shared__ int s_pages[PAGED ? CHUNK + 1 : 1];
 
-  const int b = blockIdx.z, kvh = blockIdx.y, split = blockIdx.x;
+  const int b = blockIdx.z, kvh = blockIdx.x, split = blockIdx.y;
   if (PAGED && p.active && b >= p.active[0]) return;
   const int valid = valid_length<PAGED>(p, b);
   if (valid < 1 || valid > p.capacity) return;
@@ -493,7 +493,7 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnParams p) {
   __shared__ int s_pages[PAGED ? kMfmaMaxChunk + 1 : 1];
 
   const int CHUNK = p.chunk;
-  const int b = blockIdx.z, kvh = blockIdx.y, split = blockIdx.x;
+  const int b = blockIdx.z, kvh = blockIdx.x, split = blockIdx.y;
   if (PAGED && p.active && b >= p.active[0]) return;
   const int valid = valid_length<PAGED>(p, b);
   if (valid < 1 || valid > p.capacity) return;
@@ -560,7 +560,7 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnParams p) {
 
 template <int D, int GROUP, bool PAGED>
 int launch_group(const AttnParams& p, int batch, hipStream_t stream) {
-  const dim3 grid((unsigned)p.max_splits, (unsigned)p.kv_heads, (unsigned)batch);
+  const dim3 grid((unsigned)p.kv_heads, (unsigned)p.max_splits, (unsigned)batch);
   if constexpr (D == 128) {
     if (p.kv_bytes != 0 && !PAGED)
       hipLaunchKernelGGL((attn_mfma_kernel<GROUP, 0>), grid, dim3(kThreads), 0, stream, p);

@@ -12,57 +12,64 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 
-// Block-wide sum for 256 threads; every thread gets the total.
+// Block-wide sum for THREADS threads (a multiple of 64); every thread gets
+// the total.
+template <int THREADS = kThreads>
 __device__ __forceinline__ float block_sum(float v, float* scratch) {
+  constexpr int waves = THREADS / kWave;
   v = wave_sum(v);
   if ((threadIdx.x & (kWave - 1)) == 0) scratch[threadIdx.x / kWave] = v;
   __syncthreads();
-  const float total = (scratch[0] + scratch[1]) + (scratch[2] + scratch[3]);
+  float total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < waves; ++i) total += scratch[i];
   return total;
 }
 
 // emitDecoderRMSNorm (DecoderLLMMetalEmitter.cpp:63-108): fp32 sum of
-// squares, inverse = rsqrt(sum/width + eps), y = T(x * inverse * w).
-template <typename T>
-__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const T* __restrict__ x,
-                                                          const T* __restrict__ w,
-                                                          T* __restrict__ y, int width,
-                                                          float eps) {
-  __shared__ float scratch[kWaves];
+// squares, inverse = rsqrt(sum/width + eps), y = T(x * inverse * w).  Two
+// passes over the row; at 256 threads this is the tuner's fixed baseline
+// (emitRMSNormBaseline, RMSNormBaseline.cpp:13-72).
+template <typename T, int THREADS = kThreads>
+__global__ __launch_bounds__(THREADS) void rmsnorm_kernel(const T* __restrict__ x,
+                                                         const T* __restrict__ w,
+                                                         T* __restrict__ y, int width,
+                                                         float eps) {
+  __shared__ float scratch[THREADS / kWave];
   const size_t base = (size_t)blockIdx.x * width;
   float squares = 0.0f;
-  for (int i = threadIdx.x; i < width; i += kThreads) {
+  for (int i = threadIdx.x; i < width; i += THREADS) {
     const float v = to_float<T>(x[base + i]);
     squares += v * v;
   }
-  const float total = block_sum(squares, scratch);
+  const float total = block_sum<THREADS>(squares, scratch);
   const float inverse = 1.0f / sqrtf(total / (float)width + eps);
-  for (int i = threadIdx.x; i < width; i += kThreads)
+  for (int i = threadIdx.x; i < width; i += THREADS)
     y[base + i] = from_float<T>(to_float<T>(x[base + i]) * inverse * to_float<T>(w[i]));
 }
 
 // emitDecoderResidualRMSNorm (DecoderLLMMetalEmitter.cpp:417-477).
-template <typename T>
-__global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(
+template <typename T, int THREADS = kThreads>
+__global__ __launch_bounds__(THREADS) void add_rmsnorm_kernel(
     const T* __restrict__ residual, const T* __restrict__ update, const T* __restrict__ w,
     T* __restrict__ sum_out, T* __restrict__ norm_out, int width, float eps) {
-  __shared__ float scratch[kWaves];
+  __shared__ float scratch[THREADS / kWave];
   const size_t base = (size_t)blockIdx.x * width;
   float squares = 0.0f;
-  for (int i = threadIdx.x; i < width; i += kThreads) {
+  for (int i = threadIdx.x; i < width; i += THREADS) {
     const float v = through<T>(to_float<T>(residual[base + i]) + to_float<T>(update[base + i]));
     sum_out[base + i] = from_float<T>(v);
     squares += v * v;
   }
-  const float total = block_sum(squares, scratch);
+  const float total = block_sum<THREADS>(squares, scratch);
   const float inverse = 1.0f / sqrtf(total / (float)width + eps);
-  for (int i = threadIdx.x; i < width; i += kThreads) {
+  for (int i = threadIdx.x; i < width; i += THREADS) {
     const float v = through<T>(to_float<T>(residual[base + i]) + to_float<T>(update[base + i]));
     norm_out[base + i] = from_float<T>(v * inverse * to_float<T>(w[i]));
   }
 }
 
-// Register-resident variants for rows of at most kMaxVec * 8 * 256
+// Register-resident variants for rows of at most kMaxVec * 8 * THREADS
 // elements with vector-aligned rows: each thread loads its 8-element
 // slices once, the row is reduced once, and the outputs are written from
 // registers (one global read pass instead of two).
@@ -72,22 +79,22 @@ template <typename T> struct Vec8;
 template <> struct Vec8<half_t> { typedef h8 type; };
 template <> struct Vec8<float> { typedef float type __attribute__((ext_vector_type(8))); };
 
-template <typename T, int NV, bool ADD>
-__global__ __launch_bounds__(kThreads) void norm_vec_kernel(const T* __restrict__ residual,
-                                                           const T* __restrict__ update,
-                                                           const T* __restrict__ w,
-                                                           T* __restrict__ sum_out,
-                                                           T* __restrict__ norm_out, int width,
-                                                           float eps) {
+template <typename T, int NV, bool ADD, int THREADS>
+__global__ __launch_bounds__(THREADS) void norm_vec_kernel(const T* __restrict__ residual,
+                                                          const T* __restrict__ update,
+                                                          const T* __restrict__ w,
+                                                          T* __restrict__ sum_out,
+                                                          T* __restrict__ norm_out, int width,
+                                                          float eps) {
   typedef typename Vec8<T>::type V;
-  __shared__ float scratch[kWaves];
+  __shared__ float scratch[THREADS / kWave];
   const size_t base = (size_t)blockIdx.x * width;
   const int vecs = width / 8;
   V val[NV];
   float squares = 0.0f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int v = threadIdx.x + i * kThreads;
+    const int v = threadIdx.x + i * THREADS;
     if (v < vecs) {
       V a = *reinterpret_cast<const V*>(residual + base + 8 * v);
       if constexpr (ADD) {
@@ -100,11 +107,11 @@ __global__ __launch_bounds__(kThreads) void norm_vec_kernel(const T* __restrict_
       for (int t = 0; t < 8; ++t) squares += to_float<T>(a[t]) * to_float<T>(a[t]);
     }
   }
-  const float total = block_sum(squares, scratch);
+  const float total = block_sum<THREADS>(squares, scratch);
   const float inverse = 1.0f / sqrtf(total / (float)width + eps);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int v = threadIdx.x + i * kThreads;
+    const int v = threadIdx.x + i * THREADS;
     if (v < vecs) {
       const V wv = *reinterpret_cast<const V*>(w + 8 * v);
       V n;
@@ -117,23 +124,53 @@ __global__ __launch_bounds__(kThreads) void norm_vec_kernel(const T* __restrict_
   }
 }
 
-template <typename T, bool ADD>
+template <typename T, bool ADD, int THREADS>
 bool launch_norm_vec(const T* r, const T* u, const T* w, T* s, T* n, int64_t rows, int64_t width,
                      float eps, hipStream_t stream) {
   constexpr uintptr_t align = sizeof(typename Vec8<T>::type);
   auto ok = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) % align) == 0; };
   if (width % 8 != 0 || !ok(r) || !ok(w) || !ok(n) || (ADD && (!ok(u) || !ok(s)))) return false;
   const int64_t vecs = width / 8;
-  const int nv = (int)((vecs + kThreads - 1) / kThreads);
+  const int nv = (int)((vecs + THREADS - 1) / THREADS);
   if (nv > kMaxVec) return false;
-  const dim3 grid((unsigned)rows);
+  const dim3 grid((unsigned)rows), block(THREADS);
   switch (nv) {
-  case 1: hipLaunchKernelGGL((norm_vec_kernel<T, 1, ADD>), grid, dim3(kThreads), 0, stream, r, u, w, s, n, (int)width, eps); break;
-  case 2: hipLaunchKernelGGL((norm_vec_kernel<T, 2, ADD>), grid, dim3(kThreads), 0, stream, r, u, w, s, n, (int)width, eps); break;
-  case 3: hipLaunchKernelGGL((norm_vec_kernel<T, 3, ADD>), grid, dim3(kThreads), 0, stream, r, u, w, s, n, (int)width, eps); break;
-  default: hipLaunchKernelGGL((norm_vec_kernel<T, 4, ADD>), grid, dim3(kThreads), 0, stream, r, u, w, s, n, (int)width, eps); break;
+  case 1: hipLaunchKernelGGL((norm_vec_kernel<T, 1, ADD, THREADS>), grid, block, 0, stream, r, u, w, s, n, (int)width, eps); break;
+  case 2: hipLaunchKernelGGL((norm_vec_kernel<T, 2, ADD, THREADS>), grid, block, 0, stream, r, u, w, s, n, (int)width, eps); break;
+  case 3: hipLaunchKernelGGL((norm_vec_kernel<T, 3, ADD, THREADS>), grid, block, 0, stream, r, u, w, s, n, (int)width, eps); break;
+  default: hipLaunchKernelGGL((norm_vec_kernel<T, 4, ADD, THREADS>), grid, block, 0, stream, r, u, w, s, n, (int)width, eps); break;
   }
   return true;
+}
+
+// One RMSNorm / Add+RMSNorm launch at THREADS threads per row: the
+// register-resident kernel when the row fits (unless two_pass), else the
+// two-pass kernel.
+template <typename T, bool ADD, int THREADS>
+void launch_norm(const T* r, const T* u, const T* w, T* s, T* n, int64_t rows, int64_t width,
+                 float eps, bool two_pass, hipStream_t stream) {
+  if (!two_pass && launch_norm_vec<T, ADD, THREADS>(r, u, w, s, n, rows, width, eps, stream))
+    return;
+  if constexpr (ADD)
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, THREADS>), dim3((unsigned)rows), dim3(THREADS), 0,
+                       stream, r, u, w, s, n, (int)width, eps);
+  else
+    hipLaunchKernelGGL((rmsnorm_kernel<T, THREADS>), dim3((unsigned)rows), dim3(THREADS), 0,
+                       stream, r, w, n, (int)width, eps);
+}
+
+template <typename T, bool ADD>
+bool launch_norm_threads(const T* r, const T* u, const T* w, T* s, T* n, int64_t rows,
+                         int64_t width, float eps, int threads, bool two_pass,
+                         hipStream_t stream) {
+  switch (threads) {
+  case 64: launch_norm<T, ADD, 64>(r, u, w, s, n, rows, width, eps, two_pass, stream); return true;
+  case 128: launch_norm<T, ADD, 128>(r, u, w, s, n, rows, width, eps, two_pass, stream); return true;
+  case 256: launch_norm<T, ADD, 256>(r, u, w, s, n, rows, width, eps, two_pass, stream); return true;
+  case 512: launch_norm<T, ADD, 512>(r, u, w, s, n, rows, width, eps, two_pass, stream); return true;
+  case 1024: launch_norm<T, ADD, 1024>(r, u, w, s, n, rows, width, eps, two_pass, stream); return true;
+  default: return false;
+  }
 }
 
 // emitDecoderSiLUMul (DecoderLLMMetalEmitter.cpp:395-415).
@@ -457,44 +494,77 @@ using namespace tmc;
     }                                             \
   } while (0)
 
+namespace {
+
+template <typename T>
+void launch_norm_typed(bool add, const void* residual, const void* update, const void* w,
+                       void* sum_out, void* norm_out, int64_t rows, int64_t width, float eps,
+                       int threads, bool two_pass, hipStream_t stream) {
+  const T* r = static_cast<const T*>(residual);
+  const T* wt = static_cast<const T*>(w);
+  T* n = static_cast<T*>(norm_out);
+  if (add)
+    launch_norm_threads<T, true>(r, static_cast<const T*>(update), wt, static_cast<T*>(sum_out),
+                                 n, rows, width, eps, threads, two_pass, stream);
+  else
+    launch_norm_threads<T, false>(r, nullptr, wt, nullptr, n, rows, width, eps, threads, two_pass,
+                                  stream);
+}
+
+int norm_entry(bool add, const void* residual, const void* update, const void* w, void* sum_out,
+               void* norm_out, int dtype, int64_t rows, int64_t width, float epsilon,
+               int threads, int variant, void* stream) {
+  const char* what = add ? "Add+RMSNorm" : "RMSNorm";
+  TMC_REQUIRE(residual && w && norm_out && (!add || (update && sum_out)),
+              std::string(what) + ": null device pointer.");
+  TMC_REQUIRE(float_dtype(dtype), std::string(what) + ": dtype must be fp16 or fp32.");
+  TMC_REQUIRE(rows > 0 && width > 0 && width < (1LL << 31) && rows < (1LL << 31),
+              std::string(what) + ": invalid shape.");
+  TMC_REQUIRE(std::isfinite(epsilon) && epsilon > 0.0f,
+              std::string(what) + ": epsilon must be finite and positive.");
+  TMC_REQUIRE(variant == 0 || variant == 1,
+              std::string(what) + ": variant must be 0 (default) or 1 (two-pass).");
+  if (threads == 0) threads = kThreads;
+  TMC_REQUIRE(threads == 64 || threads == 128 || threads == 256 || threads == 512 ||
+                  threads == 1024,
+              std::string(what) + ": threads must be 64, 128, 256, 512 or 1024.");
+  const bool two_pass = variant == 1;
+  if (dtype == TMC_F32)
+    launch_norm_typed<float>(add, residual, update, w, sum_out, norm_out, rows, width, epsilon,
+                             threads, two_pass, as_stream(stream));
+  else
+    launch_norm_typed<half_t>(add, residual, update, w, sum_out, norm_out, rows, width, epsilon,
+                              threads, two_pass, as_stream(stream));
+  return check_launch(add ? "add_rmsnorm kernel" : "rmsnorm kernel");
+}
+
+}  // namespace
+
 extern "C" int tmc_rmsnorm(const void* x, const void* w, void* y, int dtype, int64_t rows,
                            int64_t width, float epsilon, void* stream) {
-  TMC_REQUIRE(x && w && y, "RMSNorm: null device pointer.");
-  TMC_REQUIRE(float_dtype(dtype), "RMSNorm: dtype must be fp16 or fp32.");
-  TMC_REQUIRE(rows > 0 && width > 0 && width < (1LL << 31) && rows < (1LL << 31),
-              "RMSNorm: invalid shape.");
-  TMC_REQUIRE(std::isfinite(epsilon) && epsilon > 0.0f, "RMSNorm: epsilon must be finite and positive.");
-  TMC_DISPATCH_T(dtype, {
-    if (!launch_norm_vec<T, false>(static_cast<const T*>(x), nullptr, static_cast<const T*>(w),
-                                   nullptr, static_cast<T*>(y), rows, width, epsilon,
-                                   as_stream(stream)))
-      hipLaunchKernelGGL((rmsnorm_kernel<T>), dim3((unsigned)rows), dim3(kThreads), 0,
-                         as_stream(stream), static_cast<const T*>(x), static_cast<const T*>(w),
-                         static_cast<T*>(y), (int)width, epsilon);
-  });
-  return check_launch("rmsnorm_kernel");
+  return norm_entry(false, x, nullptr, w, nullptr, y, dtype, rows, width, epsilon, 0, 0, stream);
 }
 
 extern "C" int tmc_add_rmsnorm(const void* residual, const void* update, const void* w,
                                void* sum_out, void* norm_out, int dtype, int64_t rows,
                                int64_t width, float epsilon, void* stream) {
-  TMC_REQUIRE(residual && update && w && sum_out && norm_out, "Add+RMSNorm: null device pointer.");
-  TMC_REQUIRE(float_dtype(dtype), "Add+RMSNorm: dtype must be fp16 or fp32.");
-  TMC_REQUIRE(rows > 0 && width > 0 && width < (1LL << 31) && rows < (1LL << 31),
-              "Add+RMSNorm: invalid shape.");
-  TMC_REQUIRE(std::isfinite(epsilon) && epsilon > 0.0f, "Add+RMSNorm: epsilon must be finite and positive.");
-  TMC_DISPATCH_T(dtype, {
-    if (!launch_norm_vec<T, true>(static_cast<const T*>(residual), static_cast<const T*>(update),
-                                  static_cast<const T*>(w), static_cast<T*>(sum_out),
-                                  static_cast<T*>(norm_out), rows, width, epsilon,
-                                  as_stream(stream)))
-      hipLaunchKernelGGL((add_rmsnorm_kernel<T>), dim3((unsigned)rows), dim3(kThreads), 0,
-                         as_stream(stream), static_cast<const T*>(residual),
-                         static_cast<const T*>(update), static_cast<const T*>(w),
-                         static_cast<T*>(sum_out), static_cast<T*>(norm_out), (int)width,
-                         epsilon);
-  });
-  return check_launch("add_rmsnorm_kernel");
+  return norm_entry(true, residual, update, w, sum_out, norm_out, dtype, rows, width, epsilon, 0,
+                    0, stream);
+}
+
+extern "C" int tmc_rmsnorm_threads(const void* x, const void* w, void* y, int dtype,
+                                   int64_t rows, int64_t width, float epsilon, int threads,
+                                   int variant, void* stream) {
+  return norm_entry(false, x, nullptr, w, nullptr, y, dtype, rows, width, epsilon, threads,
+                    variant, stream);
+}
+
+extern "C" int tmc_add_rmsnorm_threads(const void* residual, const void* update, const void* w,
+                                       void* sum_out, void* norm_out, int dtype, int64_t rows,
+                                       int64_t width, float epsilon, int threads, int variant,
+                                       void* stream) {
+  return norm_entry(true, residual, update, w, sum_out, norm_out, dtype, rows, width, epsilon,
+                    threads, variant, stream);
 }
 
 extern "C" int tmc_silu_mul(const void* gate, const void* up, void* out, int dtype, int64_t count,

@@ -1,5 +1,5 @@
 // Decode GEMV family for gfx950: fp16 weights [out, in] row-major, fp32
-// accumulation.  Two algorithms, both streaming every weight byte once:
+// accumulation.  The fast algorithms stream every weight byte once:
 //
 //  * Wave64 split-K dot (algorithm 1, batch <= 8).  A wave owns RPW output
 //    rows; its 64 lanes split K in 16-byte chunks (lane l reads chunks
@@ -14,6 +14,17 @@
 //    128-element tiles, U tiles of loads in flight per wave, partials summed
 //    in LDS.  The x operand costs one 16-byte load per weight load whatever
 //    the batch, so it is the path for batch > 1.
+//
+//  * Linear baseline (algorithm 4): one thread per output, the reference
+//    tuner's baseline kept as the tuners' fallback.
+//
+//  * MFMA row-tile GEMM (algorithm 3, batch <= 16 per pass): the same
+//    instruction, but a wave owns RT 16-row output tiles (one activation
+//    fragment serves RT weight fragments) and every operand is read with raw
+//    buffer loads: rows past N, batch rows past B and k past K get an
+//    offset beyond the buffer, which reads as zero, so no load is
+//    predicated.  KS waves of a block split K; all waves share the LDS
+//    reduction.
 //
 // The gated MLP (emitDecoderGatedMLP, DecoderLLMMetalEmitter.cpp:479-536)
 // runs either algorithm over the Wg and Wu rows of each feature and finishes
@@ -167,6 +178,27 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(const half_t* __restr
   if (lane == 0) write_out<MATS>(y, (size_t)b * n_out + n, a0, a1);
 }
 
+// Linear baseline (algorithm 4), emitLinearBaseline
+// (DecodeGEMVMetalEmitter.cpp:18-66): one thread per output element with a
+// serial fp32 K loop.  It is the tuners' performance baseline and fallback,
+// not a fast path: lanes of a wave read rows K elements apart.
+template <int MATS, typename OutT>
+__global__ __launch_bounds__(128) void gemv_linear_baseline_kernel(
+    const half_t* __restrict__ x, const half_t* __restrict__ w0, const half_t* __restrict__ w1,
+    OutT* __restrict__ y, int batch, int n_out, int k_in) {
+  const long item = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= (long)batch * n_out) return;
+  const int b = (int)(item / n_out), n = (int)(item % n_out);
+  const half_t* xr = x + (size_t)b * k_in;
+  float a0 = 0.0f, a1 = 0.0f;
+  for (int k = 0; k < k_in; ++k) {
+    const float xv = (float)xr[k];
+    a0 += xv * (float)w0[(size_t)n * k_in + k];
+    if constexpr (MATS == 2) a1 += xv * (float)w1[(size_t)n * k_in + k];
+  }
+  write_out<MATS>(y, (size_t)item, a0, a1);
+}
+
 // ---------------------------------------------------------------- MFMA
 // D[i][j] = sum_k x[i][k] * w[n0+j][k] for MT 16-row tiles of x.  Lane l
 // supplies row l%16 of both operands and k-group g = l/16.  A 128-wide K tile
@@ -259,6 +291,111 @@ __global__ __launch_bounds__(1024) void mfma_gemm_kernel(const half_t* __restric
       const int col = n0 + j;
       if (row < m_rows && col < n_out) write_out<MATS>(y, (size_t)row * n_out + col, a[0], a[1]);
     }
+}
+
+// ---------------------------------------------------------------- MFMA row tiles
+constexpr unsigned kNoData = 0xFFFFFFF0u;  // buffer offset that reads as zero
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ h8 rsrc_h8(__amdgpu_buffer_rsrc_t r, unsigned byte_offset) {
+  return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_offset, 0, 0));
+}
+
+// Block = KS waves over RT tiles of 16 output rows; wave ks takes a
+// contiguous run of K tiles (128 k), U adjacent tiles per round trip.  Lane (j = l % 16,
+// g = l / 16): A = activations (batch row j, k chunk 4s+g of the tile), B =
+// weights (output row j of the tile, same k chunk); acc[r] = out[batch
+// 4g + r][row j].
+template <int MATS, int RT, int U, typename OutT>
+__global__ __launch_bounds__(1024) void mfma_rows_kernel(const half_t* __restrict__ x,
+                                                        const half_t* __restrict__ w0,
+                                                        const half_t* __restrict__ w1,
+                                                        OutT* __restrict__ y, int m_rows,
+                                                        int n_out, int k_in, int ks_count) {
+  extern __shared__ float red[];  // [ks][MATS][RT][4][64]
+  const int lane = threadIdx.x & (kWave - 1);
+  const int ks = threadIdx.x / kWave;
+  const int j = lane & 15;
+  const int g = lane >> 4;
+  const int n0 = blockIdx.x * RT * 16;
+  const unsigned x_bytes = (unsigned)m_rows * (unsigned)k_in * 2u;
+  const unsigned w_bytes = (unsigned)n_out * (unsigned)k_in * 2u;
+  const __amdgpu_buffer_rsrc_t rx = rsrc_of(x, x_bytes);
+  const __amdgpu_buffer_rsrc_t rw0 = rsrc_of(w0, w_bytes);
+  const __amdgpu_buffer_rsrc_t rw1 = rsrc_of(MATS == 2 ? w1 : w0, w_bytes);
+  const unsigned x_row = j < m_rows ? (unsigned)j * (unsigned)k_in * 2u : kNoData;
+  unsigned w_row[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row = n0 + rt * 16 + j;
+    w_row[rt] = row < n_out ? (unsigned)row * (unsigned)k_in * 2u : kNoData;
+  }
+  f4 acc[MATS][RT];
+#pragma unroll
+  for (int m = 0; m < MATS; ++m)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[m][rt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  // Wave ks owns the contiguous K tiles [first, last): the U tiles of one
+  // round trip are adjacent, so each weight row is read in U*256-byte runs.
+  const int tiles = (k_in + 127) / 128;
+  const int per_wave = (tiles + ks_count - 1) / ks_count;
+  const int first = ks * per_wave;
+  const int last = min(tiles, first + per_wave);
+  for (int t0 = first; t0 < last; t0 += U) {
+    h8 xv[U][4], wv[U][MATS][RT][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int k = (t0 + u) * 128 + 32 * s + 8 * g;
+        const bool kok = t0 + u < last && k < k_in;
+        const unsigned kb = (unsigned)k * 2u;
+        xv[u][s] = rsrc_h8(rx, kok && x_row != kNoData ? x_row + kb : kNoData);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          const unsigned off = kok && w_row[rt] != kNoData ? w_row[rt] + kb : kNoData;
+          wv[u][0][rt][s] = rsrc_h8(rw0, off);
+          if constexpr (MATS == 2) wv[u][1][rt][s] = rsrc_h8(rw1, off);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int m = 0; m < MATS; ++m)
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt)
+            acc[m][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv[u][s], wv[u][m][rt][s],
+                                                                acc[m][rt], 0, 0, 0);
+  }
+  constexpr int kValues = MATS * RT * 4;  // per lane
+#pragma unroll
+  for (int m = 0; m < MATS; ++m)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        red[((size_t)ks * kValues + (m * RT + rt) * 4 + r) * kWave + lane] = acc[m][rt][r];
+  __syncthreads();
+  // Every thread finishes some (rt, r, lane) outputs: sum the KS partials.
+  const int total = RT * 4 * kWave;
+  for (int idx = threadIdx.x; idx < total; idx += ks_count * kWave) {
+    const int l = idx % kWave, rt = (idx / kWave) / 4, r = (idx / kWave) % 4;
+    float a[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+      for (int w = 0; w < ks_count; ++w)
+        a[m] += red[((size_t)w * kValues + (m * RT + rt) * 4 + r) * kWave + l];
+    const int row = 4 * (l >> 4) + r;       // batch row
+    const int col = n0 + rt * 16 + (l & 15);  // output feature
+    if (row < m_rows && col < n_out) write_out<MATS>(y, (size_t)row * n_out + col, a[0], a[1]);
+  }
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -360,26 +497,77 @@ int run_mfma(const Shape& s, const tmc_gemv_config& cfg, hipStream_t st) {
   return 0;
 }
 
+template <int MATS, int RT, int U, typename OutT>
+int launch_rows(const Shape& s, const half_t* x, OutT* y, int rows, int ks, hipStream_t st) {
+  const dim3 grid((unsigned)((s.n + RT * 16 - 1) / (RT * 16)));
+  const size_t lds = (size_t)ks * MATS * RT * 4 * kWave * sizeof(float);
+  hipLaunchKernelGGL((mfma_rows_kernel<MATS, RT, U, OutT>), grid, dim3(ks * kWave), lds, st, x,
+                     s.w0, s.w1, y, rows, s.n, s.k, ks);
+  return check_launch("mfma_rows_kernel");
+}
+
+template <int MATS, typename OutT>
+int run_rows(const Shape& s, const tmc_gemv_config& cfg, hipStream_t st) {
+  // The LDS reduction holds k_split x MATS x tiles 16x16 fp32 partials.
+  TMC_REQUIRE((size_t)cfg.k_split * MATS * cfg.rows_per_wave * 4 * kWave * sizeof(float) <= 65536,
+              "GEMV config: MFMA row tiles need k_split * tiles * matrices <= 64 (64 KiB LDS).");
+  OutT* y = static_cast<OutT*>(s.y);
+  for (int r0 = 0; r0 < s.batch; r0 += 16) {
+    const int rows = min(16, s.batch - r0);
+    const half_t* xs = s.x + (size_t)r0 * s.k;
+    OutT* ys = y + (size_t)r0 * s.n;
+    int rc;
+    const int ks = cfg.k_split;
+    switch (cfg.rows_per_wave * 8 + cfg.unroll) {
+    case 9: rc = launch_rows<MATS, 1, 1, OutT>(s, xs, ys, rows, ks, st); break;
+    case 10: rc = launch_rows<MATS, 1, 2, OutT>(s, xs, ys, rows, ks, st); break;
+    case 12: rc = launch_rows<MATS, 1, 4, OutT>(s, xs, ys, rows, ks, st); break;
+    case 17: rc = launch_rows<MATS, 2, 1, OutT>(s, xs, ys, rows, ks, st); break;
+    case 18: rc = launch_rows<MATS, 2, 2, OutT>(s, xs, ys, rows, ks, st); break;
+    case 20: rc = launch_rows<MATS, 2, 4, OutT>(s, xs, ys, rows, ks, st); break;
+    case 33: rc = launch_rows<MATS, 4, 1, OutT>(s, xs, ys, rows, ks, st); break;
+    default: rc = launch_rows<MATS, 4, 2, OutT>(s, xs, ys, rows, ks, st); break;
+    }
+    if (rc) return rc;
+  }
+  return 0;
+}
+
 // Default configuration per shape (the tuner may override it), from graph-
-// timed sweeps on MI355X: batch 1 streams rows with the dot algorithm and 4
-// waves per row (2 rows per wave for rows longer than 8K); larger batches use
-// MFMA with one 16-row tile per block, 2 waves per tile for the gated pair
-// and 16 for a single matrix.
+// timed sweeps on MI355X with weights larger than the Infinity Cache: batch 1
+// streams rows with the dot algorithm and 4 waves per row (2 rows per wave
+// for rows longer than 8K); larger batches use the MFMA row-tile kernel.
+// Sweep winners (batch 8 / 16, K 4096 unless noted): N 12288 -> 1|2 tiles,
+// unroll 1, 4 waves; N 4096 (K 4096 and K 11008) -> 1 tile, 8 waves; N 32000
+// -> 2 tiles, unroll 1, 2 waves; gated N 11008 -> 1 tile, 4 waves, unroll 1
+// at batch 8 and 4 at batch 16.
 tmc_gemv_config default_config(int batch, int n, int k, int mats) {
   tmc_gemv_config c{};
-  (void)n;
+  (void)k;
   if (batch == 1) {
     c.algorithm = 1;
     c.rows_per_wave = k > 8192 ? 2 : 1;
     c.unroll = mats == 2 ? 2 : 4;
     c.k_split = 4;
-  } else {
-    c.algorithm = 2;
+    return c;
+  }
+  c.algorithm = 3;
+  if (mats == 2) {
     c.rows_per_wave = 1;
-    c.unroll = 2;
-    c.k_split = mats == 2 ? 2 : 16;
-    const int tiles = (k + 127) / 128;
-    while (c.k_split > 1 && tiles < 2 * c.k_split) c.k_split /= 2;
+    c.unroll = batch > 8 ? 4 : 1;
+    c.k_split = 4;
+  } else if (n >= 16384) {
+    c.rows_per_wave = 2;
+    c.unroll = 1;
+    c.k_split = 2;
+  } else if (n >= 8192) {
+    c.rows_per_wave = batch > 8 ? 2 : 1;
+    c.unroll = 1;
+    c.k_split = 4;
+  } else {
+    c.rows_per_wave = 1;
+    c.unroll = batch > 8 ? 1 : 2;
+    c.k_split = 8;
   }
   return c;
 }
@@ -390,12 +578,21 @@ int validate_config(const tmc_gemv_config& c) {
                     (c.unroll == 2 || c.unroll == 4) &&
                     (c.k_split == 1 || c.k_split == 2 || c.k_split == 4),
                 "GEMV config: dot algorithm needs rows_per_wave 1|2, unroll 2|4, k_split 1|2|4.");
+  } else if (c.algorithm == 3) {
+    TMC_REQUIRE((c.rows_per_wave == 1 || c.rows_per_wave == 2 || c.rows_per_wave == 4) &&
+                    c.k_split >= 1 && c.k_split <= 16 &&
+                    (c.unroll == 1 || c.unroll == 2 || (c.unroll == 4 && c.rows_per_wave <= 2)),
+                "GEMV config: MFMA row tiles need rows_per_wave 1|2|4 tiles, k_split 1..16 "
+                "waves and unroll 1|2 (or 4 with at most 2 tiles).");
+  } else if (c.algorithm == 4) {
+    return 0;
   } else if (c.algorithm == 2) {
     TMC_REQUIRE(c.rows_per_wave >= 1 && c.k_split >= 1 && c.rows_per_wave * c.k_split <= 16 &&
                     (c.unroll == 1 || c.unroll == 2),
                 "GEMV config: MFMA needs n_tiles * k_split <= 16 waves and unroll 1|2.");
   } else {
-    return fail("GEMV config: algorithm must be 0 (auto), 1 (dot) or 2 (MFMA).");
+    return fail("GEMV config: algorithm must be 0 (auto), 1 (dot), 2 (MFMA), 3 (MFMA row tiles) "
+                "or 4 (linear baseline).");
   }
   return 0;
 }
@@ -413,6 +610,21 @@ int run_linear(int mats, const void* x, const void* w0, const void* w1, void* y,
           static_cast<const half_t*>(w1), y, y_dtype, (int)batch, (int)n, (int)k};
   const hipStream_t st = as_stream(stream);
   const bool vec = (k % 8) == 0 && aligned16(x) && aligned16(w0) && (mats == 1 || aligned16(w1));
+  if (user && user->algorithm == 4) {
+    const long items = (long)batch * n;
+    TMC_REQUIRE(items < (1LL << 31) * 128LL, std::string(what) + ": too many outputs.");
+    const dim3 grid((unsigned)((items + 127) / 128));
+    if (mats == 2)
+      hipLaunchKernelGGL((gemv_linear_baseline_kernel<2, half_t>), grid, dim3(128), 0, st, s.x,
+                         s.w0, s.w1, static_cast<half_t*>(y), s.batch, s.n, s.k);
+    else if (y_dtype == TMC_F32)
+      hipLaunchKernelGGL((gemv_linear_baseline_kernel<1, float>), grid, dim3(128), 0, st, s.x,
+                         s.w0, s.w1, static_cast<float*>(y), s.batch, s.n, s.k);
+    else
+      hipLaunchKernelGGL((gemv_linear_baseline_kernel<1, half_t>), grid, dim3(128), 0, st, s.x,
+                         s.w0, s.w1, static_cast<half_t*>(y), s.batch, s.n, s.k);
+    return check_launch("gemv_linear_baseline_kernel");
+  }
   if (!vec) {
     const long items = (long)batch * n;
     const dim3 grid((unsigned)((items + 3) / 4));
@@ -433,6 +645,15 @@ int run_linear(int mats, const void* x, const void* w0, const void* w1, void* y,
   if (cfg.algorithm == 1) {
     if (mats == 2) return run_dot<2, half_t>(s, cfg, st);
     return y_dtype == TMC_F32 ? run_dot<1, float>(s, cfg, st) : run_dot<1, half_t>(s, cfg, st);
+  }
+  if (cfg.algorithm == 3) {
+    // raw buffers address at most 4 GiB - 16 bytes
+    const uint64_t wb = (uint64_t)s.n * s.k * 2, xb = (uint64_t)min(s.batch, 16) * s.k * 2;
+    if (wb < kNoData && xb < kNoData) {
+      if (mats == 2) return run_rows<2, half_t>(s, cfg, st);
+      return y_dtype == TMC_F32 ? run_rows<1, float>(s, cfg, st) : run_rows<1, half_t>(s, cfg, st);
+    }
+    cfg = tmc_gemv_config{2, 1, 2, 4};
   }
   if (mats == 2) return run_mfma<2, half_t>(s, cfg, st);
   return y_dtype == TMC_F32 ? run_mfma<1, float>(s, cfg, st) : run_mfma<1, half_t>(s, cfg, st);
@@ -459,7 +680,10 @@ extern "C" int tmc_gemv_f16_config(const void* x, const void* w, void* y, int y_
 extern "C" int tmc_skinny_gemm_f16_mfma(const void* x, const void* w, void* y, int y_dtype,
                                         int64_t batch, int64_t in_features, int64_t out_features,
                                         void* stream) {
-  tmc_gemv_config cfg = default_config(2, (int)out_features, (int)in_features, 1);
+  TMC_REQUIRE(batch > 0 && in_features > 0 && out_features > 0,
+              "MFMA GEMM: dimensions must be positive.");
+  tmc_gemv_config cfg =
+      default_config((int)std::max<int64_t>(batch, 2), (int)out_features, (int)in_features, 1);
   TMC_REQUIRE((in_features % 8) == 0 && aligned16(x) && aligned16(w),
               "MFMA GEMM: in_features must be a multiple of 8 and x, W 16-byte aligned.");
   return run_linear(1, x, w, nullptr, y, y_dtype, batch, in_features, out_features, &cfg, stream);

@@ -258,6 +258,17 @@ bool parse_key(const std::string& key, std::string& name, Params& params) {
   return !name.empty();
 }
 
+// Optional GEMV launch configuration in a key: algorithm (0 auto, 1 dot,
+// 2 MFMA, 3 MFMA row tiles, 4 linear baseline), rows_per_wave, unroll,
+// k_split.  Validated when the kernel launches.
+bool gemv_config_param(const Params& p, tmc_gemv_config& cfg) {
+  cfg.algorithm = (int)param_int(p, "algorithm", 0);
+  cfg.rows_per_wave = (int)param_int(p, "rows_per_wave", 1);
+  cfg.unroll = (int)param_int(p, "unroll", 1);
+  cfg.k_split = (int)param_int(p, "k_split", 1);
+  return cfg.algorithm >= 0 && cfg.algorithm <= 4;
+}
+
 #define NEED(cond, msg)          \
   do {                           \
     if (!(cond)) {               \
@@ -275,24 +286,29 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     const int od = param_dtype(p, "out_dtype", TMC_F16);
     NEED(b > 0 && k > 0 && n > 0 && (od == TMC_F16 || od == TMC_F32) && dt == TMC_F16,
          "decode_gemv needs batch, in, out > 0, dtype=f16 and out_dtype f16|f32.");
+    tmc_gemv_config cfg{};
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
     s.inputs = {TMC_F16, TMC_F16};
     s.outputs = {od};
     s.counts = {(size_t)(b * k), (size_t)(n * k), (size_t)(b * n)};
     s.groups = (size_t)((n + 3) / 4);
     s.launch = [=](const LaunchContext& c) {
-      return tmc_gemv_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], od, b, k, n, c.stream);
+      return tmc_gemv_f16_config(c.ptrs[0], c.ptrs[1], c.ptrs[2], od, b, k, n, &cfg, c.stream);
     };
     return true;
   }
   if (name == "gate_up_silu") {
     const int64_t b = param_int(p, "batch"), h = param_int(p, "hidden"), f = param_int(p, "inter");
     NEED(b > 0 && h > 0 && f > 0 && dt == TMC_F16, "gate_up_silu needs batch, hidden, inter and f16.");
+    tmc_gemv_config cfg{};
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
     s.inputs = {TMC_F16, TMC_F16, TMC_F16};
     s.outputs = {TMC_F16};
     s.groups = (size_t)((f + 3) / 4);
     s.counts = {(size_t)(b * h), (size_t)(f * h), (size_t)(f * h), (size_t)(b * f)};
     s.launch = [=](const LaunchContext& c) {
-      return tmc_gate_up_silu_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], b, h, f, c.stream);
+      return tmc_gate_up_silu_f16_config(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], b, h, f,
+                                         &cfg, c.stream);
     };
     return true;
   }
@@ -300,13 +316,24 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     const int64_t rows = param_int(p, "rows"), width = param_int(p, "width");
     const float eps = (float)param_double(p, "eps", 1e-5);
     NEED(rows > 0 && width > 0 && (dt == TMC_F16 || dt == TMC_F32), "rmsnorm needs rows, width, f16|f32.");
+    // Tuner candidates: threads (64..1024, default 256) and variant
+    // (default | two_pass, the fixed baseline at 256 threads).
+    const int threads = (int)param_int(p, "threads", 256);
+    const auto vit = p.find("variant");
+    const std::string vname = vit == p.end() ? "default" : vit->second;
+    NEED(threads == 64 || threads == 128 || threads == 256 || threads == 512 || threads == 1024,
+         "rmsnorm threads must be 64, 128, 256, 512 or 1024.");
+    NEED(vname == "default" || vname == "two_pass", "rmsnorm variant must be default or two_pass.");
+    const int variant = vname == "two_pass" ? 1 : 0;
     s.groups = (size_t)rows;
+    s.threads = (size_t)threads;
     if (name == "rmsnorm") {
       s.inputs = {dt, dt};
       s.outputs = {dt};
       s.counts = {(size_t)(rows * width), (size_t)width, (size_t)(rows * width)};
       s.launch = [=](const LaunchContext& c) {
-        return tmc_rmsnorm(c.ptrs[0], c.ptrs[1], c.ptrs[2], dt, rows, width, eps, c.stream);
+        return tmc_rmsnorm_threads(c.ptrs[0], c.ptrs[1], c.ptrs[2], dt, rows, width, eps, threads,
+                                   variant, c.stream);
       };
     } else {
       s.inputs = {dt, dt, dt};
@@ -314,8 +341,8 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
       s.counts = {(size_t)(rows * width), (size_t)(rows * width), (size_t)width,
                   (size_t)(rows * width), (size_t)(rows * width)};
       s.launch = [=](const LaunchContext& c) {
-        return tmc_add_rmsnorm(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], c.ptrs[4], dt, rows,
-                               width, eps, c.stream);
+        return tmc_add_rmsnorm_threads(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], c.ptrs[4], dt,
+                                       rows, width, eps, threads, variant, c.stream);
       };
     }
     return true;

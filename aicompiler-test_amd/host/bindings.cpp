@@ -13,6 +13,7 @@
 #include "DecoderLLM.hpp"
 #include "KVCacheState.hpp"
 #include "ServingRuntime.hpp"
+#include "Tuning.hpp"
 
 namespace py = pybind11;
 using namespace tensor;
@@ -473,4 +474,195 @@ PYBIND11_MODULE(_tmc_host, m) {
           d["log"] = log.str();
           return d;
         });
+  // Kernel selection (tuners and admission).
+  py::class_<hip::DecodeGEMVConfig>(m, "DecodeGEMVConfig")
+      .def(py::init<>())
+      .def(py::init([](int a, int r, int u, int k) { return hip::DecodeGEMVConfig{a, r, u, k}; }))
+      .def_readwrite("algorithm", &hip::DecodeGEMVConfig::algorithm)
+      .def_readwrite("rows_per_wave", &hip::DecodeGEMVConfig::rowsPerWave)
+      .def_readwrite("unroll", &hip::DecodeGEMVConfig::unroll)
+      .def_readwrite("k_split", &hip::DecodeGEMVConfig::kSplit)
+      .def("astuple", [](const hip::DecodeGEMVConfig& c) {
+        return py::make_tuple(c.algorithm, c.rowsPerWave, c.unroll, c.kSplit);
+      });
+  m.def("decode_gemv_candidates", &planner::decodeGEMVCandidates, py::arg("batch"),
+        py::arg("prefill") = false);
+  m.def("decode_gemv_hardware_filter",
+        [](const hip::DecodeGEMVConfig& c, std::size_t batch, std::size_t in, std::size_t out,
+           std::size_t maxThreads, std::size_t lds, std::size_t maxBuffer) {
+          hip::HardwareInfo h;
+          h.maxThreadsPerThreadgroup = maxThreads;
+          h.maxThreadgroupMemoryLength = lds;
+          h.maxBufferLength = maxBuffer;
+          return planner::decodeGEMVHardwareFilter(c, batch, in, out, h);
+        });
+  m.def("decode_gemv_lds_bytes", &hip::decodeGEMVLdsBytes);
+  m.def("decode_gemv_threads", &hip::decodeGEMVThreads);
+  m.def("emit_decode_gemv_key",
+        [](std::size_t batch, std::size_t in, std::size_t out, const hip::DecodeGEMVConfig& c,
+           bool f32) {
+          return hip::emitDecodeGEMV(batch, in, out, c, "decode_gemv", hip::ElementType::Float16,
+                                     f32 ? hip::ElementType::Float32 : hip::ElementType::Float16)
+              .source;
+        });
+  m.def("admission_decision",
+        [](bool firstPassed, double firstSpeedup, py::object second) {
+          benchmark::PairedResult first;
+          first.passed = firstPassed;
+          first.speedup = firstSpeedup;
+          std::optional<benchmark::PairedResult> confirmation;
+          if (!second.is_none()) {
+            benchmark::PairedResult c;
+            c.passed = true;
+            c.speedup = second.cast<double>();
+            confirmation = c;
+          }
+          const auto d = planner::admissionDecision(first, confirmation);
+          return py::make_tuple(d.admitted, d.conservativeSpeedup, d.reason);
+        });
+  m.def("tune_decode_gemv",
+        [](hip::HipRuntime& rt, std::size_t batch, std::size_t in, std::size_t out,
+           const FloatArray& input, const FloatArray& weight) {
+          std::ostringstream log;
+          const auto r = planner::tuneDecodeGEMV(rt, batch, in, out, toVector(input),
+                                                 toVector(weight), log);
+          py::dict d;
+          d["success"] = r.success;
+          d["use_baseline"] = r.useBaseline;
+          d["config"] = py::make_tuple(r.config.algorithm, r.config.rowsPerWave, r.config.unroll,
+                                       r.config.kSplit);
+          d["speedup"] = r.conservativeSpeedup;
+          d["error"] = r.errorMessage;
+          d["log"] = log.str();
+          return d;
+        });
+  m.def("rms_norm_hardware_filter",
+        [](std::size_t rows, std::size_t width, bool f16, std::size_t threads) {
+          RMSNormOp op;
+          const DType t = f16 ? DType::Float16 : DType::Float32;
+          op.input = {{rows, width}, t};
+          op.weight = {{width}, t};
+          op.output = {{rows, width}, t};
+          hip::HardwareInfo h;
+          h.maxThreadsPerThreadgroup = 1024;
+          h.maxThreadgroupMemoryLength = 160 * 1024;
+          return planner::rmsNormHardwareFilter(op, threads, h);
+        });
+  m.def("rms_norm_reference",
+        [](std::size_t rows, std::size_t width, float eps, const FloatArray& input,
+           const FloatArray& weight) {
+          RMSNormOp op;
+          op.input = {{rows, width}, DType::Float32};
+          op.weight = {{width}, DType::Float32};
+          op.output = {{rows, width}, DType::Float32};
+          op.epsilon = eps;
+          const auto ref = validation::rmsNormReference(op, toVector(input), toVector(weight));
+          return std::vector<double>(ref.begin(), ref.end());
+        });
+  m.def("tune_rms_norm",
+        [](hip::HipRuntime& rt, std::size_t rows, std::size_t width, float eps, bool f16,
+           const FloatArray& input, const FloatArray& weight, std::vector<std::size_t> threads) {
+          RMSNormOp op;
+          const DType t = f16 ? DType::Float16 : DType::Float32;
+          op.input = {{rows, width}, t};
+          op.weight = {{width}, t};
+          op.output = {{rows, width}, t};
+          op.epsilon = eps;
+          if (threads.empty()) threads = planner::defaultRMSNormCandidates();
+          std::ostringstream log;
+          auto r = planner::tuneRMSNorm(rt, op, toVector(input), toVector(weight), threads, log);
+          py::dict d;
+          d["success"] = r.success;
+          d["used_baseline"] = r.usedBaseline;
+          d["selected_threads"] = r.selectedThreads;
+          d["output"] = toArray(r.finalExecution.output);
+          d["max_abs_error"] = r.finalValidation.maxAbsoluteError;
+          py::list cands;
+          for (const auto& c : r.candidates) {
+            py::dict cd;
+            cd["name"] = c.name;
+            cd["threads"] = c.threads;
+            cd["outcome"] = c.outcome;
+            cd["reason"] = c.reason;
+            cd["speedup"] = c.speedup ? py::cast(*c.speedup) : py::none();
+            cands.append(cd);
+          }
+          d["candidates"] = cands;
+          d["error"] = r.errorMessage;
+          d["log"] = log.str();
+          return d;
+        },
+        py::arg("runtime"), py::arg("rows"), py::arg("width"), py::arg("eps"), py::arg("f16"),
+        py::arg("input"), py::arg("weight"), py::arg("threads") = std::vector<std::size_t>{});
+  // admitFusion over Add+RMSNorm: the unfused region (add, then rmsnorm over
+  // the sum) against the fused add_rmsnorm kernel, both over the same buffers.
+  m.def("admit_add_rmsnorm_fusion",
+        [](hip::HipRuntime& rt, std::size_t rows, std::size_t width, bool f16) {
+          const auto t = f16 ? hip::ElementType::Float16 : hip::ElementType::Float32;
+          const std::string dt = f16 ? "f16" : "f32";
+          const std::size_t n = rows * width;
+          auto make = [&](std::size_t count) {
+            auto b = rt.createBuffer(count, nullptr, t);
+            if (!b.buffer) throw std::runtime_error(b.errorMessage);
+            return b.buffer;
+          };
+          auto residual = make(n), update = make(n), gamma = make(width), sum = make(n),
+               norm = make(n);
+          std::vector<float> g(width);
+          for (std::size_t i = 0; i < width; ++i) g[i] = 0.5f + static_cast<float>(i % 11) / 10.0f;
+          if (auto e = rt.writeBuffer(gamma, g.data(), g.size()); !e.empty())
+            throw std::runtime_error(e);
+          auto prepare = [&](const std::string& key, std::vector<hip::BufferHandle> in,
+                             std::vector<hip::BufferHandle> out) {
+            const auto p = rt.createComputePipeline(key, "fusion_step");
+            if (!p.pipelineCreationPassed) throw std::runtime_error(p.errorMessage);
+            auto prepared =
+                rt.prepareBuffers(in, out, {p.threadgroupCount, p.threadsPerThreadgroup});
+            if (!prepared.execution) throw std::runtime_error(prepared.errorMessage);
+            return std::move(prepared.execution);
+          };
+          const std::string shape = "rows=" + std::to_string(rows) + "&width=" +
+                                    std::to_string(width) + "&eps=1e-06&dtype=" + dt;
+          std::vector<std::unique_ptr<hip::PreparedExecution>> steps;
+          steps.push_back(prepare("add?count=" + std::to_string(n) + "&dtype=" + dt,
+                                  {residual, update}, {sum}));
+          steps.push_back(prepare("rmsnorm?" + shape, {sum, gamma}, {norm}));
+          runtime::FusionDecisionCache cache;
+          std::ostringstream log;
+          const bool admitted = runtime::admitFusion(
+              rt, steps, 0,
+              [&]() {
+                std::vector<std::unique_ptr<hip::PreparedExecution>> fused;
+                fused.push_back(prepare("add_rmsnorm?" + shape, {residual, update, gamma},
+                                        {sum, norm}));
+                return fused;
+              },
+              {residual, update}, {sum, norm}, "AddRMSNorm", "add_rmsnorm:" + shape, cache, log);
+          const bool cachedAgain = runtime::admitFusion(
+              rt, steps, 0, [&]() {
+                std::vector<std::unique_ptr<hip::PreparedExecution>> fused;
+                fused.push_back(prepare("add_rmsnorm?" + shape, {residual, update, gamma},
+                                        {sum, norm}));
+                return fused;
+              },
+              {residual, update}, {sum, norm}, "AddRMSNorm", "add_rmsnorm:" + shape, cache, log);
+          py::dict d;
+          d["admitted"] = admitted;
+          d["cached_admitted"] = cachedAgain;
+          d["steps"] = steps.size();
+          d["sum"] = toArray(sum->read());
+          d["norm"] = toArray(norm->read());
+          d["log"] = log.str();
+          return d;
+        });
+  m.def("admit_generated_kernel",
+        [](hip::HipRuntime& rt, const std::string& pattern, const std::string& response,
+           const std::string& feedback, const std::string& artifact) {
+          std::ostringstream log;
+          const bool ok = runtime::admitGeneratedKernel(rt, pattern, response, feedback, log,
+                                                        artifact);
+          return py::make_tuple(ok, log.str());
+        },
+        py::arg("runtime"), py::arg("pattern"), py::arg("response"), py::arg("feedback"),
+        py::arg("artifact") = std::string());
 }

@@ -148,7 +148,14 @@ int tmc_gemv_f16(const void *x, const void *w, void *y, int y_dtype, int64_t bat
  * (rows_per_wave 1|2 rows per wave, unroll 2|4 16-byte loads per row in
  * flight, k_split 1|2|4 waves sharing a row), 2 = MFMA (rows_per_wave =
  * 16-row output tiles per block, k_split waves per tile, n_tiles*k_split
- * <= 16, unroll 1|2 K tiles in flight). */
+ * <= 16, unroll 1|2 K tiles in flight), 3 = MFMA row tiles with buffer loads
+ * (rows_per_wave 1|2|4 16-row tiles per wave, k_split 1..16 waves per block
+ * each taking a contiguous K run, unroll 1|2|4 adjacent K tiles in flight,
+ * 4 only with at most 2 tiles; batch handled 16 rows per pass), 4 = linear
+ * baseline, one thread per output (emitLinearBaseline,
+ * DecodeGEMVMetalEmitter.cpp:18-66; the tuners' baseline and fallback, other
+ * fields ignored).  Algorithms 1-3 need in_features % 8 == 0 and 16-byte
+ * aligned x and W; otherwise a scalar per-output kernel runs. */
 typedef struct tmc_gemv_config {
   int algorithm;
   int rows_per_wave;
@@ -192,6 +199,20 @@ int tmc_rmsnorm(const void *x, const void *w, void *y, int dtype, int64_t rows, 
 int tmc_add_rmsnorm(const void *residual, const void *update, const void *w, void *sum_out,
                     void *norm_out, int dtype, int64_t rows, int64_t width, float epsilon,
                     void *stream);
+
+/* RMSNorm / Add+RMSNorm at a chosen workgroup size: the RMSNorm tuner's
+ * candidates (emitRMSNorm(op, threads), MetalEmitter.cpp:12-76, and its
+ * baseline emitRMSNormBaseline, RMSNormBaseline.cpp:13-72, retargeted to
+ * gfx950).  threads is 64, 128, 256, 512 or 1024 (0 = 256).  variant 0 keeps
+ * the row in registers when width % 8 == 0 and width <= 32 * threads (one
+ * read pass), else reads it twice; variant 1 always runs the two-pass kernel
+ * (at 256 threads, the tuner's fixed baseline).  Same results as
+ * tmc_rmsnorm / tmc_add_rmsnorm up to fp32 summation order. */
+int tmc_rmsnorm_threads(const void *x, const void *w, void *y, int dtype, int64_t rows,
+                        int64_t width, float epsilon, int threads, int variant, void *stream);
+int tmc_add_rmsnorm_threads(const void *residual, const void *update, const void *w,
+                            void *sum_out, void *norm_out, int dtype, int64_t rows, int64_t width,
+                            float epsilon, int threads, int variant, void *stream);
 
 /* emitDecoderSiLUMul (DecoderLLMMetalEmitter.cpp:395-415):
  * out = h(h(g / (1 + exp(-g))) * u). */

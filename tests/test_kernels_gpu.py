@@ -59,6 +59,45 @@ def test_rmsnorm_fp16(tmc, orc, torch, rows, width):
     assert_f16_path(values(y), orc.rmsnorm(x, gamma, F16, 1e-6), what="rmsnorm fp16")
 
 
+@pytest.mark.parametrize("threads", [64, 128, 256, 512, 1024])
+@pytest.mark.parametrize("variant", [0, 1])
+def test_rmsnorm_threads_variants(tmc, orc, torch, threads, variant):
+    """The RMSNorm tuner's candidates: every workgroup size, register-resident
+    and two-pass, ragged fp32 rows and fp16 rows, plain and fused add."""
+    for rows, width in ((3, 4097), (2, 4096), (1, 8)):
+        x = normal(330, (rows, width))
+        x[0] *= 1e-4
+        gamma = uniform(331, (width,), 0.5, 1.5)
+        y = torch.empty((rows, width), dtype=torch.float32, device="cuda")
+        tmc.rmsnorm_threads(dev(x), dev(gamma), y, 1e-6, threads, variant)
+        torch.cuda.synchronize()
+        assert_f32_rel(values(y), orc.rmsnorm(x, gamma, F32, 1e-6),
+                       what=f"rmsnorm t{threads} v{variant} {rows}x{width}")
+    for rows, width in ((16, 4096), (3, 8200)):
+        h = orc.f16(normal(332, (rows, width)))
+        r = orc.f16(normal(333, (rows, width)))
+        gamma = orc.f16(uniform(334, (width,), 0.5, 1.5))
+        y = torch.empty((rows, width), dtype=torch.float16, device="cuda")
+        tmc.rmsnorm_threads(dev_f16(h), dev_f16(gamma), y, 1e-6, threads, variant)
+        s_out = torch.empty((rows, width), dtype=torch.float16, device="cuda")
+        n_out = torch.empty((rows, width), dtype=torch.float16, device="cuda")
+        tmc.add_rmsnorm_threads(dev_f16(r), dev_f16(h), dev_f16(gamma), s_out, n_out, 1e-6,
+                                threads, variant)
+        torch.cuda.synchronize()
+        assert_f16_path(values(y), orc.rmsnorm(h, gamma, F16, 1e-6),
+                        what=f"rmsnorm fp16 t{threads} v{variant}")
+        ref_s, ref_n = orc.add_rmsnorm(r, h, gamma, F16, 1e-6)
+        assert_f16_path(values(s_out), ref_s, what=f"residual sum t{threads} v{variant}")
+        assert_f16_path(values(n_out), ref_n, what=f"add_rmsnorm t{threads} v{variant}")
+
+
+def test_rmsnorm_threads_rejects_bad_workgroups(tmc, torch):
+    x = torch.zeros((1, 64), dtype=torch.float32, device="cuda")
+    for threads, variant in ((96, 0), (2048, 0), (256, 2)):
+        with pytest.raises(tmc.TmcError):
+            tmc.rmsnorm_threads(x, x[0], x, 1e-6, threads, variant)
+
+
 # ---------------------------------------------------------------- GEMV family
 @pytest.mark.parametrize("batch,k,n,out_dtype", [
     (1, 4096, 4096, F32), (1, 4096, 4096, F16), (2, 4096, 1024, F16), (3, 11008, 512, F32),
@@ -467,7 +506,12 @@ def test_fill_normal_statistics(tmc, torch):
 
 CONFIGS = ([(1, r, u, k) for r in (1, 2) for u in (2, 4) for k in (1, 2, 4)] +
            [(2, nt, u, ks) for nt in (1, 2) for u in (1, 2) for ks in (1, 2, 4, 8, 16)
-            if nt * ks <= 16])
+            if nt * ks <= 16] +
+           # MFMA row tiles: the gated pair doubles the LDS partials, so
+           # tiles * k_split <= 32 keeps both within 64 KiB
+           [(3, rt, u, ks) for rt in (1, 2, 4) for u in (1, 2, 4) for ks in (1, 2, 4, 8, 16)
+            if rt * ks <= 32 and not (u == 4 and rt == 4)] +
+           [(4, 1, 1, 1)])
 
 
 @pytest.mark.parametrize("algo,rpw,unroll,ks", CONFIGS)
@@ -476,7 +520,9 @@ def test_gemv_and_gated_mlp_every_config(tmc, orc, torch, algo, rpw, unroll, ks)
     cfg = tmc.GemvConfig()
     cfg.algorithm, cfg.rows_per_wave, cfg.unroll, cfg.k_split = algo, rpw, unroll, ks
     for batch in ((1, 3, 8) if algo == 1 else (1, 5, 16, 20)):
-        k, n = 1160, 200  # 9.06 K tiles of 128, 145 16-byte chunks, N tail of 8
+        # 9.06 K tiles of 128, 145 16-byte chunks, N tail of 8 (the linear
+        # baseline also takes a K that is not a multiple of 8)
+        k, n = (1160, 200) if algo != 4 else (1163, 200)
         x = orc.f16(normal(220 + batch, (batch, k)))
         w = orc.f16(normal(221, (n, k), 0.02))
         w2 = orc.f16(normal(222, (n, k), 0.02))
