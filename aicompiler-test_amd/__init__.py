@@ -44,6 +44,10 @@ def _declare(l):
         "tmc_gate_up_silu_f16": (i32, [vp, vp, vp, vp, i64, i64, i64, vp]),
         "tmc_rmsnorm": (i32, [vp, vp, vp, i32, i64, i64, f, vp]),
         "tmc_add_rmsnorm": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, f, vp]),
+        "tmc_packed_weight_elements": (C.c_int64, [i64, i64]),
+        "tmc_pack_weights_f16": (i32, [vp, vp, i64, i64, vp]),
+        "tmc_gemm_packed_f16": (i32, [vp, vp, vp, i32, i64, i64, i64, vp, vp]),
+        "tmc_gate_up_silu_packed_f16": (i32, [vp, vp, vp, vp, i64, i64, i64, vp, vp]),
         "tmc_rmsnorm_threads": (i32, [vp, vp, vp, i32, i64, i64, f, i32, i32, vp]),
         "tmc_add_rmsnorm_threads": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, f, i32, i32, vp]),
         "tmc_silu_mul": (i32, [vp, vp, vp, i32, i64, vp]),
@@ -197,6 +201,36 @@ def gate_up_silu_config(x, wg, wu, out, cfg, stream=None):
     check(lib().tmc_gate_up_silu_f16_config(_ptr(x), _ptr(wg), _ptr(wu), _ptr(out), b, h, f,
                                             C.byref(cfg), _stream(stream)),
           "tmc_gate_up_silu_f16_config")
+
+
+def packed_weight_elements(out_features, in_features) -> int:
+    return int(lib().tmc_packed_weight_elements(out_features, in_features))
+
+
+def pack_weights(w, packed=None, stream=None):
+    """Fragment-packed copy of fp16 W [out, in] (tmc_pack_weights_f16)."""
+    import torch
+    n, k = w.shape
+    if packed is None:
+        packed = torch.empty(packed_weight_elements(n, k), dtype=torch.float16, device=w.device)
+    check(lib().tmc_pack_weights_f16(_ptr(w), _ptr(packed), n, k, _stream(stream)),
+          "tmc_pack_weights_f16")
+    return packed
+
+
+def gemm_packed(x, packed, y, out_features, cfg=None, stream=None):
+    b, k = x.shape
+    check(lib().tmc_gemm_packed_f16(_ptr(x), _ptr(packed), _ptr(y), _dtype_code(y), b, k,
+                                    out_features, C.byref(cfg) if cfg is not None else None,
+                                    _stream(stream)), "tmc_gemm_packed_f16")
+
+
+def gate_up_silu_packed(x, packed_gate, packed_up, out, intermediate, cfg=None, stream=None):
+    b, h = x.shape
+    check(lib().tmc_gate_up_silu_packed_f16(_ptr(x), _ptr(packed_gate), _ptr(packed_up), _ptr(out),
+                                            b, h, intermediate,
+                                            C.byref(cfg) if cfg is not None else None,
+                                            _stream(stream)), "tmc_gate_up_silu_packed_f16")
 
 
 def skinny_gemm(x, w, y, stream=None):

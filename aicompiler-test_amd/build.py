@@ -32,7 +32,7 @@ CXX = os.environ.get("CXX", "g++")
 CXXFLAGS = ["-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",
             f"-I{INCLUDE}", f"-I{HOST}"]
 
-SOURCES = ["runtime.hip", "gemv.hip", "elementwise.hip", "attention.hip"]
+SOURCES = ["runtime.hip", "gemv.hip", "packed.hip", "elementwise.hip", "attention.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -1,0 +1,251 @@
+// Skinny GEMM over fragment-packed fp16 weights (batch > 1 decode) for
+// gfx950.  Same arithmetic as the decode GEMV / gated MLP (emitDecodeGEMV,
+// DecodeGEMVMetalEmitter.cpp:68-132; emitDecoderGatedMLP,
+// DecoderLLMMetalEmitter.cpp:479-536): y[r,n] = sum_k x[r,k] W[n,k], fp32
+// accumulation; only the weight layout in HBM differs.
+//
+// Packed layout.  W [N, K] row-major becomes tiles of 16 output rows x 32 k:
+// tile (nt, c) holds rows 16nt..16nt+15 and k 32c..32c+31 as 64 lanes x 8
+// halves, lane l = (n % 16) + 16 * ((k % 32) / 8), element k % 8 -- exactly
+// the B operand of v_mfma_f32_16x16x32_f16 -- stored at
+// ((nt * C + c) * 64 + l) * 16 bytes, C = ceil(K / 32); rows past N and k
+// past K are zero.  One weight load instruction of a wave then reads 1 KiB of
+// contiguous HBM (a row-major fragment touches 16 rows K*2 bytes apart), which
+// measured 20-25% faster for 16-row activations on MI355X.
+//
+// Kernel: one block per 16-row output tile; KS waves split the K tiles of
+// 128 (4 fragments) into contiguous runs, U tiles in flight per wave, and meet
+// in LDS.  Activations stay row-major; batch rows past B and k past K read
+// as zero through buffer-load range checks.
+#include "tmc_abi.hpp"
+#include "tmc_device.hpp"
+
+namespace tmc {
+namespace {
+
+constexpr unsigned kNone = 0xFFFFFFF0u;  // buffer offset that reads as zero
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ h8 buffer_load16(__amdgpu_buffer_rsrc_t r, unsigned offset) {
+  return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)offset, 0, 0));
+}
+
+__device__ __forceinline__ half_t gated_value(float gate_sum, float up_sum) {
+  // h(h(silu(h(g))) * h(u)), DecoderLLMMetalEmitter.cpp:528-532
+  const float g = through<half_t>(gate_sum);
+  const float u = through<half_t>(up_sum);
+  const float activated = through<half_t>(g / (1.0f + expf(-g)));
+  return (half_t)(activated * u);
+}
+
+// One thread per packed lane slot (16 bytes).
+__global__ __launch_bounds__(256) void pack_kernel(const half_t* __restrict__ w,
+                                                   half_t* __restrict__ packed, int n, int k,
+                                                   long slots) {
+  const int chunks = (k + 31) / 32;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < slots;
+       i += (long)gridDim.x * blockDim.x) {
+    const int lane = (int)(i & 63);
+    const long frag = i >> 6;
+    const int c = (int)(frag % chunks);
+    const int nt = (int)(frag / chunks);
+    const int row = nt * 16 + (lane & 15);
+    const int k0 = c * 32 + 8 * (lane >> 4);
+    h8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      v[e] = (row < n && k0 + e < k) ? w[(size_t)row * k + k0 + e] : (half_t)0.0f;
+    *reinterpret_cast<h8*>(packed + i * 8) = v;
+  }
+}
+
+template <int MATS, int U, typename OutT>
+__global__ __launch_bounds__(1024) void packed_gemm_kernel(const half_t* __restrict__ x,
+                                                           const half_t* __restrict__ p0,
+                                                           const half_t* __restrict__ p1,
+                                                           OutT* __restrict__ y, int m_rows,
+                                                           int n_out, int k_in, int ks_count,
+                                                           unsigned packed_bytes) {
+  extern __shared__ float red[];  // [ks][MATS][4][64]
+  const int lane = threadIdx.x & (kWave - 1);
+  const int ks = threadIdx.x / kWave;
+  const int j = lane & 15;
+  const int g = lane >> 4;
+  const int nt = blockIdx.x;
+  const int chunks = (k_in + 31) / 32;
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(x, (unsigned)m_rows * (unsigned)k_in * 2u);
+  const __amdgpu_buffer_rsrc_t r0 = buffer_rsrc(p0, packed_bytes);
+  const __amdgpu_buffer_rsrc_t r1 = buffer_rsrc(MATS == 2 ? p1 : p0, packed_bytes);
+  const unsigned x_row = j < m_rows ? (unsigned)j * (unsigned)k_in * 2u : kNone;
+  const unsigned w_base = (unsigned)nt * (unsigned)chunks * 1024u + (unsigned)lane * 16u;
+  f4 acc[MATS];
+#pragma unroll
+  for (int m = 0; m < MATS; ++m) acc[m] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int tiles = (chunks + 3) / 4;
+  const int per_wave = (tiles + ks_count - 1) / ks_count;
+  const int first = ks * per_wave;
+  const int last = min(tiles, first + per_wave);
+  for (int t0 = first; t0 < last; t0 += U) {
+    h8 xv[U][4], wv[U][MATS][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int c = (t0 + u) * 4 + s;
+        const bool live = t0 + u < last && c < chunks;
+        const unsigned w_off = live ? w_base + (unsigned)c * 1024u : kNone;
+        wv[u][0][s] = buffer_load16(r0, w_off);
+        if constexpr (MATS == 2) wv[u][1][s] = buffer_load16(r1, w_off);
+        const int kk = c * 32 + 8 * g;
+        xv[u][s] = buffer_load16(
+            rx, live && kk < k_in && x_row != kNone ? x_row + (unsigned)kk * 2u : kNone);
+      }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int m = 0; m < MATS; ++m)
+          acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv[u][s], wv[u][m][s], acc[m], 0, 0, 0);
+  }
+#pragma unroll
+  for (int m = 0; m < MATS; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[((ks * MATS + m) * 4 + r) * kWave + lane] = acc[m][r];
+  __syncthreads();
+  // acc[r] of lane (j, g) = out[batch 4g + r][row 16nt + j]
+  for (int idx = threadIdx.x; idx < 4 * kWave; idx += ks_count * kWave) {
+    const int l = idx % kWave, r = idx / kWave;
+    float a[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+      for (int w = 0; w < ks_count; ++w) a[m] += red[((w * MATS + m) * 4 + r) * kWave + l];
+    const int row = 4 * (l >> 4) + r;
+    const int col = nt * 16 + (l & 15);
+    if (row < m_rows && col < n_out) {
+      if constexpr (MATS == 2)
+        y[(size_t)row * n_out + col] = gated_value(a[0], a[1]);
+      else
+        y[(size_t)row * n_out + col] = from_float<OutT>(a[0]);
+    }
+  }
+}
+
+int64_t packed_elements(int64_t n, int64_t k) { return ((n + 15) / 16) * 16 * ((k + 31) / 32) * 32; }
+
+// Default (unroll, k_split) per shape from MI355X sweeps at batch 8 and 16
+// with weights beyond the Infinity Cache (K 4096 unless noted): N 32000 and
+// the gated N 11008 pair at batch 16 -> 1 wave per tile; N 12288 -> 2 waves
+// (4 at batch 8); N 4096 (K 4096 and 11008) -> 8 waves.  Wide N streams
+// with few waves per tile; narrow N needs more waves per tile to fill 256 CUs.
+void default_packed(int64_t batch, int64_t n, int mats, int& unroll, int& ks) {
+  unroll = 2;
+  if (mats == 2)
+    ks = batch > 8 ? 1 : 4;
+  else if (n >= 16384)
+    ks = 1;
+  else if (n >= 8192)
+    ks = batch > 8 ? 2 : 4;
+  else
+    ks = 8;
+}
+
+template <int MATS, typename OutT>
+int run_packed(const half_t* x, const half_t* p0, const half_t* p1, OutT* y, int64_t batch,
+               int64_t k, int64_t n, int unroll, int ks, hipStream_t st) {
+  const int64_t bytes = packed_elements(n, k) * 2;
+  const dim3 grid((unsigned)((n + 15) / 16));
+  const size_t lds = (size_t)ks * MATS * 4 * kWave * sizeof(float);
+  for (int64_t r0 = 0; r0 < batch; r0 += 16) {
+    const int rows = (int)std::min<int64_t>(16, batch - r0);
+    const half_t* xs = x + r0 * k;
+    OutT* ys = y + r0 * n;
+    if (unroll == 1)
+      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 1, OutT>), grid, dim3(ks * kWave), lds, st, xs,
+                         p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes);
+    else if (unroll == 2)
+      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 2, OutT>), grid, dim3(ks * kWave), lds, st, xs,
+                         p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes);
+    else
+      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 4, OutT>), grid, dim3(ks * kWave), lds, st, xs,
+                         p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes);
+    if (check_launch("packed_gemm_kernel")) return 1;
+  }
+  return 0;
+}
+
+int packed_entry(int mats, const void* x, const void* p0, const void* p1, void* y, int y_dtype,
+                 int64_t batch, int64_t k, int64_t n, const tmc_gemv_config* config,
+                 void* stream) {
+  const char* what = mats == 2 ? "Packed gated MLP" : "Packed GEMM";
+  TMC_REQUIRE(x && p0 && y && (mats == 1 || p1), std::string(what) + ": null device pointer.");
+  TMC_REQUIRE(y_dtype == TMC_F16 || y_dtype == TMC_F32,
+              std::string(what) + ": output dtype must be fp16 or fp32.");
+  TMC_REQUIRE(batch > 0 && k > 0 && n > 0, std::string(what) + ": dimensions must be positive.");
+  TMC_REQUIRE(k % 8 == 0 && aligned16(x) && aligned16(p0) && (mats == 1 || aligned16(p1)),
+              std::string(what) + ": in_features must be a multiple of 8 and x, W 16-byte aligned.");
+  TMC_REQUIRE((uint64_t)packed_elements(n, k) * 2 < kNone && (uint64_t)16 * k * 2 < kNone &&
+                  n < (1LL << 31) && batch < (1LL << 31),
+              std::string(what) + ": operands exceed the 4 GiB buffer range.");
+  int unroll, ks;
+  default_packed(batch, n, mats, unroll, ks);
+  if (config && config->algorithm != 0) {
+    unroll = config->unroll;
+    ks = config->k_split;
+  }
+  TMC_REQUIRE((unroll == 1 || unroll == 2 || unroll == 4) && ks >= 1 && ks <= 16,
+              std::string(what) + ": config needs unroll 1|2|4 and k_split 1..16.");
+  const hipStream_t st = as_stream(stream);
+  const half_t* xs = static_cast<const half_t*>(x);
+  const half_t* a = static_cast<const half_t*>(p0);
+  const half_t* b = static_cast<const half_t*>(p1);
+  if (mats == 2)
+    return run_packed<2, half_t>(xs, a, b, static_cast<half_t*>(y), batch, k, n, unroll, ks, st);
+  if (y_dtype == TMC_F32)
+    return run_packed<1, float>(xs, a, a, static_cast<float*>(y), batch, k, n, unroll, ks, st);
+  return run_packed<1, half_t>(xs, a, a, static_cast<half_t*>(y), batch, k, n, unroll, ks, st);
+}
+
+}  // namespace
+}  // namespace tmc
+
+using namespace tmc;
+
+extern "C" int64_t tmc_packed_weight_elements(int64_t out_features, int64_t in_features) {
+  if (out_features <= 0 || in_features <= 0) return 0;
+  return packed_elements(out_features, in_features);
+}
+
+extern "C" int tmc_pack_weights_f16(const void* w, void* packed, int64_t out_features,
+                                    int64_t in_features, void* stream) {
+  TMC_REQUIRE(w && packed, "Pack weights: null device pointer.");
+  TMC_REQUIRE(out_features > 0 && in_features > 0 && out_features < (1LL << 31) &&
+                  in_features < (1LL << 31),
+              "Pack weights: invalid shape.");
+  TMC_REQUIRE(aligned16(packed), "Pack weights: the packed buffer must be 16-byte aligned.");
+  const long slots = (long)(packed_elements(out_features, in_features) / 8);
+  const unsigned blocks = (unsigned)std::min<long>((slots + 255) / 256, 65536);
+  hipLaunchKernelGGL(pack_kernel, dim3(blocks), dim3(256), 0, as_stream(stream),
+                     static_cast<const half_t*>(w), static_cast<half_t*>(packed),
+                     (int)out_features, (int)in_features, slots);
+  return check_launch("pack_kernel");
+}
+
+extern "C" int tmc_gemm_packed_f16(const void* x, const void* packed_w, void* y, int y_dtype,
+                                   int64_t batch, int64_t in_features, int64_t out_features,
+                                   const tmc_gemv_config* config, void* stream) {
+  return packed_entry(1, x, packed_w, nullptr, y, y_dtype, batch, in_features, out_features,
+                      config, stream);
+}
+
+extern "C" int tmc_gate_up_silu_packed_f16(const void* x, const void* packed_gate,
+                                           const void* packed_up, void* out, int64_t batch,
+                                           int64_t hidden, int64_t intermediate,
+                                           const tmc_gemv_config* config, void* stream) {
+  return packed_entry(2, x, packed_gate, packed_up, out, TMC_F16, batch, hidden, intermediate,
+                      config, stream);
+}

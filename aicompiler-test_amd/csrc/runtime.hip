@@ -297,6 +297,51 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     };
     return true;
   }
+  if (name == "pack_weights") {
+    const int64_t n = param_int(p, "out"), k = param_int(p, "in");
+    NEED(n > 0 && k > 0 && dt == TMC_F16, "pack_weights needs out, in > 0 and f16.");
+    s.inputs = {TMC_F16};
+    s.outputs = {TMC_F16};
+    s.counts = {(size_t)(n * k), (size_t)tmc_packed_weight_elements(n, k)};
+    s.groups = (size_t)((tmc_packed_weight_elements(n, k) / 8 + 255) / 256);
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_pack_weights_f16(c.ptrs[0], c.ptrs[1], n, k, c.stream);
+    };
+    return true;
+  }
+  if (name == "gemm_packed") {
+    const int64_t b = param_int(p, "batch"), k = param_int(p, "in"), n = param_int(p, "out");
+    const int od = param_dtype(p, "out_dtype", TMC_F16);
+    NEED(b > 0 && k > 0 && n > 0 && (od == TMC_F16 || od == TMC_F32) && dt == TMC_F16,
+         "gemm_packed needs batch, in, out > 0, dtype=f16 and out_dtype f16|f32.");
+    tmc_gemv_config cfg{};
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    s.inputs = {TMC_F16, TMC_F16};
+    s.outputs = {od};
+    s.counts = {(size_t)(b * k), (size_t)tmc_packed_weight_elements(n, k), (size_t)(b * n)};
+    s.groups = (size_t)((n + 15) / 16);
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_gemm_packed_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], od, b, k, n, &cfg, c.stream);
+    };
+    return true;
+  }
+  if (name == "gate_up_silu_packed") {
+    const int64_t b = param_int(p, "batch"), h = param_int(p, "hidden"), f = param_int(p, "inter");
+    NEED(b > 0 && h > 0 && f > 0 && dt == TMC_F16,
+         "gate_up_silu_packed needs batch, hidden, inter and f16.");
+    tmc_gemv_config cfg{};
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    const size_t pe = (size_t)tmc_packed_weight_elements(f, h);
+    s.inputs = {TMC_F16, TMC_F16, TMC_F16};
+    s.outputs = {TMC_F16};
+    s.groups = (size_t)((f + 15) / 16);
+    s.counts = {(size_t)(b * h), pe, pe, (size_t)(b * f)};
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_gate_up_silu_packed_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], b, h, f,
+                                         &cfg, c.stream);
+    };
+    return true;
+  }
   if (name == "gate_up_silu") {
     const int64_t b = param_int(p, "batch"), h = param_int(p, "hidden"), f = param_int(p, "inter");
     NEED(b > 0 && h > 0 && f > 0 && dt == TMC_F16, "gate_up_silu needs batch, hidden, inter and f16.");

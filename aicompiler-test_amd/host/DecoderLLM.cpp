@@ -1,6 +1,8 @@
 // Decoder-LLM decode path on gfx950; see DecoderLLM.hpp.
 #include "DecoderLLM.hpp"
 
+#include "tmc_hip.h"
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -246,6 +248,48 @@ ModelResourcesCreation createSyntheticModelResources(hip::HipRuntime& runtime,
   return result;
 }
 
+std::string ensurePackedWeights(hip::HipRuntime& runtime, DecoderLLMModelResources& model) {
+  if (!model.packedLayers.empty() || model.layers.empty()) return {};
+  try {
+    const auto& plan = model.plan;
+    const std::size_t H = plan.hiddenSize(), I = plan.intermediateSize, V = plan.vocabularySize;
+    const std::size_t QKV = H + 2 * plan.kvWidth();
+    std::size_t bytes = 0;
+    auto pack = [&](const BufferHandle& w, std::size_t out, std::size_t in) {
+      const auto count = tmc_packed_weight_elements(static_cast<int64_t>(out),
+                                                    static_cast<int64_t>(in));
+      if (count <= 0) throw std::runtime_error("Packed weights: invalid matrix shape.");
+      auto packed = allocate(runtime, static_cast<std::size_t>(count), nullptr,
+                             ElementType::Float16);
+      if (tmc_pack_weights_f16(w->devicePointer(), packed->devicePointer(),
+                               static_cast<int64_t>(out), static_cast<int64_t>(in),
+                               runtime.stream()) != 0)
+        throw std::runtime_error(std::string("Packed weights: ") + tmc_last_error());
+      bytes += static_cast<std::size_t>(count) * 2;
+      return packed;
+    };
+    std::vector<DecoderLLMModelLayerBuffers> layers;
+    for (const auto& w : model.layers) {
+      DecoderLLMModelLayerBuffers b;
+      b.queryKeyValueWeight = pack(w.queryKeyValueWeight, QKV, H);
+      b.outputWeight = pack(w.outputWeight, H, H);
+      b.gateWeight = pack(w.gateWeight, I, H);
+      b.upWeight = pack(w.upWeight, I, H);
+      b.downWeight = pack(w.downWeight, H, I);
+      layers.push_back(std::move(b));
+    }
+    auto head = pack(model.languageModelHeadWeight, V, H);
+    const auto error = runtime.synchronize();
+    if (!error.empty()) throw std::runtime_error(error);
+    model.packedLayers = std::move(layers);
+    model.packedLanguageModelHead = std::move(head);
+    model.packedBytes = bytes;
+  } catch (const std::exception& e) {
+    return e.what();
+  }
+  return {};
+}
+
 // ------------------------------------------------------ BatchedDecodeExecutor
 struct BatchedDecodeExecutor::Bucket {
   std::size_t rows = 0;
@@ -309,6 +353,10 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
   std::vector<std::size_t> rows;
   for (std::size_t r = 1; r < M; r *= 2) rows.push_back(r);
   rows.push_back(M);
+  if (M > 1) {
+    const auto error = ensurePackedWeights(rt, *model_);
+    if (!error.empty()) throw std::runtime_error(error);
+  }
 
   const std::string eps = fmt(plan.rmsNormEpsilon);
   for (const std::size_t m : rows) {
@@ -326,9 +374,15 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
       if (!prepared.execution) throw std::runtime_error(name + ": " + prepared.errorMessage);
       bucket->steps.push_back(std::move(prepared.execution));
     };
+    // Batch 1 streams row-major weights with the dot GEMV; larger buckets run
+    // the MFMA GEMM over the fragment-packed copies.
+    const bool packed = m > 1;
     auto gemv = [&](std::size_t in, std::size_t out, const char* outType) {
-      return "decode_gemv?batch=" + B + "&in=" + std::to_string(in) + "&out=" + std::to_string(out) +
-             "&out_dtype=" + outType;
+      return std::string(packed ? "gemm_packed" : "decode_gemv") + "?batch=" + B +
+             "&in=" + std::to_string(in) + "&out=" + std::to_string(out) + "&out_dtype=" + outType;
+    };
+    auto weights = [&](std::size_t l) -> const DecoderLLMModelLayerBuffers& {
+      return packed ? model_->packedLayers[l] : model_->layers[l];
     };
     const std::string norm = "rows=" + B + "&width=" + std::to_string(H) + "&eps=" + eps + "&dtype=f16";
     add("embedding?rows=" + B + "&hidden=" + std::to_string(H) + "&vocab=" + std::to_string(V),
@@ -349,7 +403,8 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
       if (l > 0)
         add("add_rmsnorm?" + norm, p + "residual_input_norm", {after_, mlp_, w.inputNormWeight},
             {residual_, normalized_});
-      add(gemv(H, QKV, "f16"), p + "qkv", {normalized_, w.queryKeyValueWeight}, {qkv_});
+      const auto& pw = weights(l);
+      add(gemv(H, QKV, "f16"), p + "qkv", {normalized_, pw.queryKeyValueWeight}, {qkv_});
       add(ropeKey, p + "rope_append",
           {qkv_, model_->ropeCosine, model_->ropeSine, lengthsView_, tableViews_[l], activeView_},
           {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer()});
@@ -357,16 +412,19 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
           {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer(), lengthsView_, tableViews_[l],
            activeView_},
           {context_});
-      add(gemv(H, H, "f16"), p + "o", {context_, w.outputWeight}, {projected_});
+      add(gemv(H, H, "f16"), p + "o", {context_, pw.outputWeight}, {projected_});
       add("add_rmsnorm?" + norm, p + "residual_post_norm",
           {residual_, projected_, w.postAttentionNormWeight}, {after_, normalized_});
-      add("gate_up_silu?batch=" + B + "&hidden=" + std::to_string(H) + "&inter=" + std::to_string(I),
-          p + "gate_up_silu", {normalized_, w.gateWeight, w.upWeight}, {gated_});
-      add(gemv(I, H, "f16"), p + "down", {gated_, w.downWeight}, {mlp_});
+      add(std::string(packed ? "gate_up_silu_packed" : "gate_up_silu") + "?batch=" + B +
+              "&hidden=" + std::to_string(H) + "&inter=" + std::to_string(I),
+          p + "gate_up_silu", {normalized_, pw.gateWeight, pw.upWeight}, {gated_});
+      add(gemv(I, H, "f16"), p + "down", {gated_, pw.downWeight}, {mlp_});
     }
     add("add_rmsnorm?" + norm, "residual_final_norm", {after_, mlp_, model_->finalNormWeight},
         {residual_, normalized_});
-    add(gemv(H, V, "f32"), "lm_head", {normalized_, model_->languageModelHeadWeight}, {logits_});
+    add(gemv(H, V, "f32"), "lm_head",
+        {normalized_, packed ? model_->packedLanguageModelHead : model_->languageModelHeadWeight},
+        {logits_});
     add("argmax?rows=" + B + "&vocab=" + std::to_string(V), "argmax", {logits_}, {nextTokens_});
     std::vector<const hip::PreparedExecution*> pointers;
     for (const auto& step : bucket->steps) pointers.push_back(step.get());

@@ -128,7 +128,17 @@ struct DecoderLLMModelResources {
   hip::BufferHandle ropeCosine;
   hip::BufferHandle ropeSine;
   std::vector<DecoderLLMModelLayerBuffers> layers;
+  // Fragment-packed copies of the matrices for the batch > 1 skinny GEMM
+  // (tmc_pack_weights_f16); empty until ensurePackedWeights runs.  Batch 1
+  // keeps streaming the row-major weights, which the dot GEMV reads faster.
+  std::vector<DecoderLLMModelLayerBuffers> packedLayers;
+  hip::BufferHandle packedLanguageModelHead;
+  std::size_t packedBytes = 0;
 };
+
+// Create the packed copies once per model (idempotent; "" on success).
+[[nodiscard]] std::string ensurePackedWeights(hip::HipRuntime& runtime,
+                                              DecoderLLMModelResources& model);
 
 struct ModelResourcesCreation {
   std::shared_ptr<DecoderLLMModelResources> resources;

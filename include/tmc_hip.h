@@ -188,6 +188,30 @@ int tmc_gate_up_silu_f16_config(const void *x, const void *w_gate, const void *w
                                 int64_t batch, int64_t hidden, int64_t intermediate,
                                 const tmc_gemv_config *config, void *stream);
 
+/* Fragment-packed weights for the batch > 1 skinny GEMM.  No reference
+ * counterpart (the reference streams row-major weights, DecodeGEMVMetalEmitter
+ * .cpp:68-132): a one-time repacking of W [out, in] row-major into tiles of
+ * 16 rows x 32 k, each 64 lanes x 8 halves in the B-operand order of
+ * v_mfma_f32_16x16x32_f16 (lane = n % 16 + 16 * ((k % 32) / 8), element
+ * k % 8), tile (n / 16, k / 32) at ((n / 16) * ceil(in / 32) + k / 32) * 1024
+ * bytes, zero-padded.  tmc_packed_weight_elements gives the packed fp16
+ * element count (0 for a bad shape). */
+int64_t tmc_packed_weight_elements(int64_t out_features, int64_t in_features);
+int tmc_pack_weights_f16(const void *w, void *packed, int64_t out_features, int64_t in_features,
+                         void *stream);
+
+/* tmc_gemv_f16 / tmc_gate_up_silu_f16 semantics over packed weights, any
+ * batch (16 rows per pass); in_features % 8 == 0, x and the packed buffers
+ * 16-byte aligned.  config (may be NULL): algorithm 0 = default for the shape,
+ * otherwise unroll 1|2|4 K tiles of 128 in flight and k_split 1..16 waves
+ * per 16-row output tile. */
+int tmc_gemm_packed_f16(const void *x, const void *packed_w, void *y, int y_dtype, int64_t batch,
+                        int64_t in_features, int64_t out_features, const tmc_gemv_config *config,
+                        void *stream);
+int tmc_gate_up_silu_packed_f16(const void *x, const void *packed_gate, const void *packed_up,
+                                void *out, int64_t batch, int64_t hidden, int64_t intermediate,
+                                const tmc_gemv_config *config, void *stream);
+
 /* emitDecoderRMSNorm (DecoderLLMMetalEmitter.cpp:63-108) / emitRMSNorm
  * (MetalEmitter.cpp:12-76): y = x * rsqrt(mean(x^2) + eps) * w, fp32
  * reduction, dtype TMC_F16 or TMC_F32 for x, w, y. */

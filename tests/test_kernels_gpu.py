@@ -534,3 +534,74 @@ def test_gemv_and_gated_mlp_every_config(tmc, orc, torch, algo, rpw, unroll, ks)
         assert_f32_rel(values(y), orc.linear(x, w, F16), what=f"cfg {cfg.astuple()} b{batch}")
         assert_f16_path(values(g), orc.gated_mlp(x, w, w2, F16),
                         what=f"gated cfg {cfg.astuple()} b{batch}")
+
+
+# ---------------------------------------------------------------- packed weights
+def _pack_reference(w_bits):
+    """Numpy restatement of the packed layout (include/tmc_hip.h): tile
+    (n // 16, k // 32), lane n % 16 + 16 * ((k % 32) // 8), element k % 8."""
+    n, k = w_bits.shape
+    nt, kc = (n + 15) // 16, (k + 31) // 32
+    padded = np.zeros((nt * 16, kc * 32), np.uint16)
+    padded[:n, :k] = w_bits
+    # [nt, 16 rows, kc, 4 groups, 8] -> [nt, kc, 4 groups, 16 rows, 8]
+    t = padded.reshape(nt, 16, kc, 4, 8).transpose(0, 2, 3, 1, 4)
+    return t.reshape(-1)
+
+
+@pytest.mark.parametrize("n,k", [(16, 32), (200, 1160), (33, 8), (4096, 4096)])
+def test_pack_weights_layout_bit_exact(tmc, orc, torch, n, k):
+    w = orc.f16(normal(340, (n, k)))
+    packed = tmc.pack_weights(dev_f16(w))
+    torch.cuda.synchronize()
+    assert packed.numel() == tmc.packed_weight_elements(n, k)
+    assert np.array_equal(bits(packed), _pack_reference(w))
+
+
+PACKED_CONFIGS = [(u, ks) for u in (1, 2, 4) for ks in (1, 2, 4, 8, 16)]
+
+
+@pytest.mark.parametrize("unroll,ks", PACKED_CONFIGS)
+def test_packed_gemm_and_gated_every_config(tmc, orc, torch, unroll, ks):
+    cfg = tmc.GemvConfig(3, 1, unroll, ks)
+    for batch, k, n in ((2, 1160, 200), (16, 1160, 200), (20, 4096, 48), (5, 8, 40)):
+        x = orc.f16(normal(350 + batch, (batch, k)))
+        w = orc.f16(normal(351, (n, k), 0.02))
+        w2 = orc.f16(normal(352, (n, k), 0.02))
+        pw, pw2 = tmc.pack_weights(dev_f16(w)), tmc.pack_weights(dev_f16(w2))
+        y = torch.empty((batch, n), dtype=torch.float32, device="cuda")
+        tmc.gemm_packed(dev_f16(x), pw, y, n, cfg)
+        g = torch.empty((batch, n), dtype=torch.float16, device="cuda")
+        tmc.gate_up_silu_packed(dev_f16(x), pw, pw2, g, n, cfg)
+        torch.cuda.synchronize()
+        what = f"packed u{unroll} ks{ks} b{batch} k{k} n{n}"
+        assert_f32_rel(values(y), orc.linear(x, w, F16), what=what)
+        assert_f16_path(values(g), orc.gated_mlp(x, w, w2, F16), what="gated " + what)
+
+
+@pytest.mark.parametrize("batch,k,n,out_dtype", [
+    (16, 4096, 12288, F16), (16, 4096, 4096, F32), (8, 11008, 4096, F16), (16, 4096, 32000, F32),
+    (33, 256, 72, F32), (1, 4096, 256, F16),
+])
+def test_packed_gemm_default_configs(tmc, orc, torch, batch, k, n, out_dtype):
+    x = orc.f16(normal(360, (batch, k)))
+    w = orc.f16(normal(361, (n, k), 0.02))
+    y = torch.empty((batch, n), dtype=torch.float32 if out_dtype == F32 else torch.float16,
+                    device="cuda")
+    tmc.gemm_packed(dev_f16(x), tmc.pack_weights(dev_f16(w)), y, n)
+    torch.cuda.synchronize()
+    ref = orc.linear(x, w, F16)
+    if out_dtype == F32:
+        assert_f32_rel(values(y), ref, what=f"packed default b{batch} n{n}")
+    else:
+        assert_f16_path(values(y), ref, what=f"packed default b{batch} n{n}")
+
+
+def test_packed_gemm_rejects_bad_arguments(tmc, torch):
+    x = torch.zeros((2, 12), dtype=torch.float16, device="cuda")
+    p = torch.zeros(4096, dtype=torch.float16, device="cuda")
+    y = torch.zeros((2, 16), dtype=torch.float32, device="cuda")
+    with pytest.raises(tmc.TmcError):
+        tmc.gemm_packed(x, p, y, 16)                            # in_features % 8 != 0
+    with pytest.raises(tmc.TmcError):
+        tmc.gemm_packed(x[:, :8].contiguous(), p, y, 16, tmc.GemvConfig(3, 1, 3, 4))  # unroll 3
