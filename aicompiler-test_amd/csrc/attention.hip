@@ -32,11 +32,10 @@ constexpr int kTilesPerWave = 2;  // VALU kernel (D < 128)
 // D == 128 kernel: a wave step is kMfmaTiles 16-position MFMA tiles whose
 // K/V loads are all issued before the first MFMA.  (Keeping a second step's
 // loads in flight was measured slower: the extra registers halve occupancy.)
-// Positions per split are chosen per launch from 256, 512 or 1024
-// (mfma_chunk): the largest that still gives about two blocks per CU, since
-// longer splits mean fewer partials to merge and fewer per-block costs.
+// Positions per split are chosen per launch from 128 ... 1024 (chunk_for).
 constexpr int kMfmaTiles = 2;
 constexpr int kMfmaStep = 16 * kMfmaTiles;
+constexpr int kMfmaMinChunk = 128;  // four waves x one 32-position step
 constexpr int kMfmaMaxChunk = 1024;
 
 struct AttnParams {
@@ -75,19 +74,6 @@ __device__ __forceinline__ int slot_in_page(const AttnParams& p, int pos) {
 template <bool PAGED>
 __device__ __forceinline__ int valid_length(const AttnParams& p, int b) {
   return PAGED ? p.valid[b] : p.valid[0];
-}
-
-// True when a page needed by [0, valid) is negative (the reference kernel
-// returns before writing in that case) or, when the pool size is known, past
-// the end of the pool.  Block-uniform result.
-__device__ __forceinline__ bool has_bad_page(const AttnParams& p, int b, int valid) {
-  const int pages = (valid + p.page_size - 1) / p.page_size;
-  int bad = 0;
-  for (int lp = threadIdx.x; lp < pages; lp += blockDim.x) {
-    const int page = p.tables[(size_t)b * p.max_pages + lp];
-    bad |= page < 0 || (p.pool_pages > 0 && page >= p.pool_pages);
-  }
-  return __syncthreads_or(bad) != 0;
 }
 
 // Positions [p0, p0 + TILE) of one wave: K/V slices for lane (row r, column
@@ -163,10 +149,14 @@ __device__ __forceinline__ void attend_tile(const h8 (&qv)[GROUP], const h8 (&kt
 // same rule for multi-split rows.
 template <int D, int GROUP, bool PAGED>
 __device__ void finish_split(const AttnParams& p, int b, int kvh, int split, int nsplit,
-                             int valid, const float (*s_m)[GROUP], const float (*s_l)[GROUP],
+                             bool bad, const float (*s_m)[GROUP], const float (*s_l)[GROUP],
                              const float (*s_o)[GROUP][D]) {
+  // `bad`: a page of this split's range is negative or past the pool.  One
+  // split covers the whole attended range, so its output stays untouched; a
+  // split of several marks its slot (denominator -1) and the merge leaves the
+  // output untouched when any slot is marked.
   const bool single = nsplit == 1;
-  if (single && PAGED && has_bad_page(p, b, valid)) return;
+  if (single && bad) return;
   for (int idx = threadIdx.x; idx < GROUP * D; idx += kThreads) {
     const int g = idx / D, d = idx % D;
     float mx = s_m[0][g];
@@ -187,37 +177,53 @@ __device__ void finish_split(const AttnParams& p, int b, int kvh, int split, int
       slot[d] = osum;
       if (d == 0) {
         slot[D] = mx;
-        slot[D + 1] = lsum;
+        slot[D + 1] = bad ? -1.0f : lsum;
       }
     }
   }
 }
 
 // Merge the split partials of one (request, query head): thread d owns
-// output column d; splits are read 8 at a time (all 24 loads issued before
-// use) and folded with a running maximum.
+// output column d.  The first 8 slots are loaded together with the valid
+// length (one memory round trip; slots past the request's splits are read
+// but ignored), later ones 8 at a time, folded with a running maximum.  A
+// slot whose denominator is negative marks a bad page: the output stays
+// untouched.
 template <int D, bool PAGED>
 __global__ __launch_bounds__(D) void attn_combine_kernel(AttnParams p) {
   const int qh = blockIdx.x, b = blockIdx.y;
   if (PAGED && p.active && b >= p.active[0]) return;
-  const int valid = valid_length<PAGED>(p, b);
-  if (valid < 1 || valid > p.capacity) return;
-  const int nsplit = (valid + p.chunk - 1) / p.chunk;
-  if (nsplit <= 1) return;
-  if (PAGED && has_bad_page(p, b, valid)) return;
   const int d = threadIdx.x;
   const float* base = p.ws + ((size_t)b * p.q_heads + qh) * p.max_splits * (D + 2);
-  float mx = -INFINITY, lsum = 0.0f, osum = 0.0f;
-  for (int s0 = 0; s0 < nsplit; s0 += 8) {
-    float ms[8], ls[8], os[8];
+  float ms[8], ls[8], os[8];
+  auto fetch = [&](int s0) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const float* slot = base + (size_t)(s0 + k) * (D + 2);
-      const bool in = s0 + k < nsplit;
+      const bool in = s0 + k < p.max_splits;  // stays inside this row's workspace
       ms[k] = in ? slot[D] : -INFINITY;
       ls[k] = in ? slot[D + 1] : 0.0f;
       os[k] = in ? slot[d] : 0.0f;
     }
+  };
+  fetch(0);
+  const int valid = valid_length<PAGED>(p, b);
+  if (valid < 1 || valid > p.capacity) return;
+  const int nsplit = (valid + p.chunk - 1) / p.chunk;
+  if (nsplit <= 1) return;
+  float mx = -INFINITY, lsum = 0.0f, osum = 0.0f;
+  bool bad = false;
+  for (int s0 = 0; s0 < nsplit; s0 += 8) {
+    if (s0 > 0) fetch(s0);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (s0 + k >= nsplit) {
+        ms[k] = -INFINITY;
+        ls[k] = 0.0f;
+        os[k] = 0.0f;
+      } else {
+        bad |= ls[k] < 0.0f;
+      }
     float next = mx;
 #pragma unroll
     for (int k = 0; k < 8; ++k) next = fmaxf(next, ms[k]);
@@ -232,6 +238,7 @@ __global__ __launch_bounds__(D) void attn_combine_kernel(AttnParams p) {
     }
     mx = next;
   }
+  if (PAGED && bad) return;
   p.out[((size_t)b * p.q_heads + qh) * D + d] = (half_t)(osum / lsum);
 }
 
@@ -263,12 +270,17 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnParams p) {
   // Block-table entries of this split, fetched once (one latency period
   // instead of one per tile before each K/V load).
   int page0 = 0;
+  bool bad = false;
   if constexpr (PAGED) {
     page0 = page_of(p, begin);
     const int entries = page_of(p, end - 1) - page0 + 1;
-    for (int i = threadIdx.x; i < entries; i += kThreads)
-      s_pages[i] = p.tables[(size_t)b * p.max_pages + page0 + i];
-    __syncthreads();
+    int bad_page = 0;
+    for (int i = threadIdx.x; i < entries; i += kThreads) {
+      const int page = p.tables[(size_t)b * p.max_pages + page0 + i];
+      s_pages[i] = page;
+      bad_page |= page < 0 || (p.pool_pages > 0 && page >= p.pool_pages);
+    }
+    bad = __syncthreads_or(bad_page) != 0;
   }
 
   h8 qv[GROUP];
@@ -317,7 +329,7 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnParams p) {
     }
   }
   __syncthreads();
-  finish_split<D, GROUP, PAGED>(p, b, kvh, split, nsplit, valid, s_m, s_l, s_o);
+  finish_split<D, GROUP, PAGED>(p, b, kvh, split, nsplit, bad, s_m, s_l, s_o);
 }
 
 // ---------------------------------------------------------------- D = 128
@@ -515,12 +527,17 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnParams p) {
     for (int s = 0; s < 4; ++s) qb[s] = j < GROUP ? load_h8(qrow + 8 * (4 * s + g)) : zero;
   }
   int page0 = 0;
+  bool bad = false;
   if constexpr (PAGED) {
     page0 = page_of(p, begin);
     const int entries = page_of(p, end - 1) - page0 + 1;
-    for (int i = threadIdx.x; i < entries; i += kThreads)
-      s_pages[i] = p.tables[(size_t)b * p.max_pages + page0 + i];
-    __syncthreads();
+    int bad_page = 0;
+    for (int i = threadIdx.x; i < entries; i += kThreads) {
+      const int page = p.tables[(size_t)b * p.max_pages + page0 + i];
+      s_pages[i] = page;
+      bad_page |= page < 0 || (p.pool_pages > 0 && page >= p.pool_pages);
+    }
+    bad = __syncthreads_or(bad_page) != 0;
   }
   float m = -INFINITY, lsum = 0.0f;
   float o[GROUP][8];
@@ -555,7 +572,7 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnParams p) {
     }
   }
   __syncthreads();
-  finish_split<D, GROUP, PAGED>(p, b, kvh, split, nsplit, valid, s_m, s_l, s_o);
+  finish_split<D, GROUP, PAGED>(p, b, kvh, split, nsplit, bad, s_m, s_l, s_o);
 }
 
 template <int D, int GROUP, bool PAGED>
@@ -600,19 +617,21 @@ int page_shift_of(int64_t page_size) {
   return shift;
 }
 
-// Positions per split for a launch.  D = 128: the largest of 256, 512, 1024
-// that still leaves batch * kv_heads * splits >= 512 blocks (two per CU)
-// at full capacity; smaller heads use the VALU kernel's fixed split.
+// Positions per split for a launch.  D = 128: the largest power of two in
+// [128, 1024] not above batch * kv_heads * capacity / 256 (one block per CU
+// at full capacity); smaller heads use the VALU kernel's fixed split.
 int chunk_for(int64_t head_dim, int64_t batch, int64_t kv_heads, int64_t capacity) {
   switch (head_dim) {
   case 16: return chunk_positions<16>();
   case 32: return chunk_positions<32>();
   case 64: return chunk_positions<64>();
   case 128: {
-    int chunk = 256;
-    while (chunk < kMfmaMaxChunk &&
-           batch * kv_heads * ((capacity + 2 * chunk - 1) / (2 * chunk)) >= 512)
-      chunk *= 2;
+    // About one block per CU when every row fills its capacity: on MI355X
+    // (256 CUs) this measured best for contiguous batch-1 attention at
+    // L 4095 (chunk 512) and paged batch-16 GQA with L ~ U[64, 4096] (1024).
+    const int64_t target = batch * kv_heads * capacity / 256;
+    int chunk = kMfmaMinChunk;
+    while (chunk < kMfmaMaxChunk && 2 * chunk <= target) chunk *= 2;
     return chunk;
   }
   default: return 0;

@@ -53,8 +53,10 @@ def test_attention_workspace_sizes(tmc):
     assert tmc.attention_workspace_bytes(2, 8, 8, 64, 256) == 0
     # [request][q head][split][D + 2] floats
     assert tmc.attention_workspace_bytes(2, 8, 8, 64, 1024) == 2 * 8 * 4 * 66 * 4
-    # D = 128: 1024-position splits once batch * kv_heads * splits keeps 512 blocks
+    # D = 128: chunk = pow2 in [128, 1024] not above batch * kv_heads * capacity / 256
     assert tmc.attention_workspace_bytes(16, 32, 8, 128, 4096) == 16 * 32 * 4 * 130 * 4
-    assert tmc.attention_workspace_bytes(1, 32, 32, 128, 4096) == 1 * 32 * 16 * 130 * 4
+    assert tmc.attention_workspace_bytes(1, 32, 32, 128, 4096) == 1 * 32 * 8 * 130 * 4
+    assert tmc.attention_workspace_bytes(1, 32, 32, 128, 1024) == 1 * 32 * 8 * 130 * 4
+    assert tmc.attention_workspace_bytes(1, 8, 8, 128, 1024) == 1 * 8 * 8 * 130 * 4
     # bad head ratio
     assert tmc.attention_workspace_bytes(2, 6, 4, 64, 1024) == 0
