@@ -44,6 +44,9 @@ def _declare(l):
         "tmc_gate_up_silu_f16": (i32, [vp, vp, vp, vp, i64, i64, i64, vp]),
         "tmc_rmsnorm": (i32, [vp, vp, vp, i32, i64, i64, f, vp]),
         "tmc_add_rmsnorm": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, f, vp]),
+        "tmc_add_rmsnorm_gemv_f16": (i32, [vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, f, vp, vp]),
+        "tmc_add_rmsnorm_gate_up_silu_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, f, vp,
+                                                   vp]),
         "tmc_packed_weight_elements": (C.c_int64, [i64, i64]),
         "tmc_pack_weights_f16": (i32, [vp, vp, i64, i64, vp]),
         "tmc_gemm_packed_f16": (i32, [vp, vp, vp, i32, i64, i64, i64, vp, vp]),
@@ -201,6 +204,29 @@ def gate_up_silu_config(x, wg, wu, out, cfg, stream=None):
     check(lib().tmc_gate_up_silu_f16_config(_ptr(x), _ptr(wg), _ptr(wu), _ptr(out), b, h, f,
                                             C.byref(cfg), _stream(stream)),
           "tmc_gate_up_silu_f16_config")
+
+
+def add_rmsnorm_gemv(residual, update, gamma, w, sum_out, y, eps, cfg=None, stream=None):
+    """Batch-1 GEMV of RMSNorm(residual + update) (update None: RMSNorm(residual))."""
+    b, k = residual.shape
+    n = w.shape[0]
+    check(lib().tmc_add_rmsnorm_gemv_f16(_ptr(residual), _ptr(update) if update is not None else None,
+                                         _ptr(gamma), _ptr(w),
+                                         _ptr(sum_out) if sum_out is not None else None, _ptr(y),
+                                         _dtype_code(y), b, k, n, eps,
+                                         C.byref(cfg) if cfg is not None else None,
+                                         _stream(stream)), "tmc_add_rmsnorm_gemv_f16")
+
+
+def add_rmsnorm_gate_up_silu(residual, update, gamma, wg, wu, sum_out, out, eps, cfg=None,
+                             stream=None):
+    b, h = residual.shape
+    f = wg.shape[0]
+    check(lib().tmc_add_rmsnorm_gate_up_silu_f16(
+        _ptr(residual), _ptr(update) if update is not None else None, _ptr(gamma), _ptr(wg),
+        _ptr(wu), _ptr(sum_out) if sum_out is not None else None, _ptr(out), b, h, f, eps,
+        C.byref(cfg) if cfg is not None else None, _stream(stream)),
+        "tmc_add_rmsnorm_gate_up_silu_f16")
 
 
 def packed_weight_elements(out_features, in_features) -> int:

@@ -297,6 +297,49 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     };
     return true;
   }
+  if (name == "add_rmsnorm_gemv" || name == "rmsnorm_gemv" || name == "add_rmsnorm_gate_up_silu" ||
+      name == "rmsnorm_gate_up_silu") {
+    // Batch-1 norm folded into the GEMV: inputs residual[, update], gamma,
+    // weight(s); outputs [sum,] y.
+    const bool add = name.rfind("add_", 0) == 0;
+    const bool gated = name.find("gate_up") != std::string::npos;
+    const int64_t k = param_int(p, "in"), n = param_int(p, "out");
+    const float eps = (float)param_double(p, "eps", 1e-5);
+    const int od = gated ? TMC_F16 : param_dtype(p, "out_dtype", TMC_F16);
+    NEED(param_int(p, "batch", 1) == 1 && k > 0 && n > 0 && dt == TMC_F16 &&
+             (od == TMC_F16 || od == TMC_F32),
+         "fused norm kernels need batch=1, in, out > 0, f16 and out_dtype f16|f32.");
+    tmc_gemv_config cfg{};
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    s.inputs = add ? std::vector<int>{TMC_F16, TMC_F16, TMC_F16} : std::vector<int>{TMC_F16, TMC_F16};
+    s.inputs.push_back(TMC_F16);
+    if (gated) s.inputs.push_back(TMC_F16);
+    s.outputs = add ? std::vector<int>{TMC_F16, od} : std::vector<int>{od};
+    s.counts = {(size_t)k};
+    if (add) s.counts.push_back((size_t)k);
+    s.counts.push_back((size_t)k);
+    s.counts.push_back((size_t)(n * k));
+    if (gated) s.counts.push_back((size_t)(n * k));
+    if (add) s.counts.push_back((size_t)k);
+    s.counts.push_back((size_t)n);
+    s.groups = (size_t)((n + 7) / 8);
+    s.launch = [=](const LaunchContext& c) {
+      const int i = add ? 1 : 0;  // index shift past the update binding
+      const void* update = add ? c.ptrs[1] : nullptr;
+      const void* gamma = c.ptrs[1 + i];
+      const void* w0 = c.ptrs[2 + i];
+      const void* w1 = gated ? c.ptrs[3 + i] : nullptr;
+      const int out0 = gated ? 4 + i : 3 + i;
+      void* sum = add ? c.ptrs[out0] : nullptr;
+      void* y = c.ptrs[add ? out0 + 1 : out0];
+      if (gated)
+        return tmc_add_rmsnorm_gate_up_silu_f16(c.ptrs[0], update, gamma, w0, w1, sum, y, 1, k, n,
+                                                eps, &cfg, c.stream);
+      return tmc_add_rmsnorm_gemv_f16(c.ptrs[0], update, gamma, w0, sum, y, od, 1, k, n, eps, &cfg,
+                                      c.stream);
+    };
+    return true;
+  }
   if (name == "pack_weights") {
     const int64_t n = param_int(p, "out"), k = param_int(p, "in");
     NEED(n > 0 && k > 0 && dt == TMC_F16, "pack_weights needs out, in > 0 and f16.");

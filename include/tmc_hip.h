@@ -188,6 +188,26 @@ int tmc_gate_up_silu_f16_config(const void *x, const void *w_gate, const void *w
                                 int64_t batch, int64_t hidden, int64_t intermediate,
                                 const tmc_gemv_config *config, void *stream);
 
+/* Batch-1 decode GEMV / gated MLP with the preceding Add+RMSNorm folded in
+ * (emitDecoderResidualRMSNorm, DecoderLLMMetalEmitter.cpp:417-477, then
+ * emitDecodeGEMV / emitDecoderGatedMLP): x = h(s * rsqrt(mean(s^2) + eps) *
+ * gamma) with s = h(residual + update) written to sum_out, or s = residual
+ * when update is NULL (plain RMSNorm; sum_out unused).  Every block rebuilds
+ * the normalized row in LDS with the arithmetic and summation order of
+ * tmc_add_rmsnorm / tmc_rmsnorm, so results equal the two-kernel sequence bit
+ * for bit.  batch must be 1; in_features a multiple of 8 up to 32768; all
+ * operands 16-byte aligned; fp16 operands.  config: NULL / algorithm 0 = the
+ * fused default, else a dot configuration (algorithm 1). */
+int tmc_add_rmsnorm_gemv_f16(const void *residual, const void *update, const void *gamma,
+                             const void *w, void *sum_out, void *y, int y_dtype, int64_t batch,
+                             int64_t in_features, int64_t out_features, float epsilon,
+                             const tmc_gemv_config *config, void *stream);
+int tmc_add_rmsnorm_gate_up_silu_f16(const void *residual, const void *update, const void *gamma,
+                                     const void *w_gate, const void *w_up, void *sum_out,
+                                     void *out, int64_t batch, int64_t hidden,
+                                     int64_t intermediate, float epsilon,
+                                     const tmc_gemv_config *config, void *stream);
+
 /* Fragment-packed weights for the batch > 1 skinny GEMM.  No reference
  * counterpart (the reference streams row-major weights, DecodeGEMVMetalEmitter
  * .cpp:68-132): a one-time repacking of W [out, in] row-major into tiles of

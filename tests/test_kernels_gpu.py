@@ -605,3 +605,72 @@ def test_packed_gemm_rejects_bad_arguments(tmc, torch):
         tmc.gemm_packed(x, p, y, 16)                            # in_features % 8 != 0
     with pytest.raises(tmc.TmcError):
         tmc.gemm_packed(x[:, :8].contiguous(), p, y, 16, tmc.GemvConfig(3, 1, 3, 4))  # unroll 3
+
+
+# ---------------------------------------------------------------- fused norm + GEMV
+DOT_CONFIGS = [(1, r, u, k) for r in (1, 2) for u in (2, 4) for k in (1, 2, 4)]
+
+
+@pytest.mark.parametrize("cfg_t", DOT_CONFIGS + [None])
+def test_fused_norm_gemv_equals_two_kernels_bit_exact(tmc, orc, torch, cfg_t):
+    """The batch-1 GEMV / gated MLP with Add+RMSNorm (or RMSNorm) folded in
+    reproduces tmc_add_rmsnorm (tmc_rmsnorm) followed by the same GEMV config
+    bit for bit, residual sum included."""
+    cfg = tmc.GemvConfig(*cfg_t) if cfg_t else None
+    ref_cfg = cfg if cfg else None  # the fused default differs by matrix count
+    for k, n in ((4096, 200), (1160, 4096)):
+        h = dev_f16(orc.f16(normal(370, (1, k))))
+        r = dev_f16(orc.f16(normal(371, (1, k))))
+        gamma = dev_f16(orc.f16(uniform(372, (k,), 0.5, 1.5)))
+        w = dev_f16(orc.f16(normal(373, (n, k), 0.02)))
+        w2 = dev_f16(orc.f16(normal(374, (n, k), 0.02)))
+        for add in (True, False):
+            s_ref = torch.empty((1, k), dtype=torch.float16, device="cuda")
+            n_ref = torch.empty_like(s_ref)
+            if add:
+                tmc.add_rmsnorm(r, h, gamma, s_ref, n_ref, 1e-6)
+            else:
+                tmc.rmsnorm(r, gamma, n_ref, 1e-6)
+            y_ref = torch.empty((1, n), dtype=torch.float32, device="cuda")
+            tmc.gemv_config(n_ref, w, y_ref, ref_cfg or tmc.GemvConfig(1, 2, 4, 1))
+            g_ref = torch.empty((1, n), dtype=torch.float16, device="cuda")
+            tmc.gate_up_silu_config(n_ref, w, w2, g_ref, ref_cfg or tmc.GemvConfig(1, 2, 4, 2))
+            s_out = torch.full((1, k), 7.0, dtype=torch.float16, device="cuda")
+            y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+            tmc.add_rmsnorm_gemv(r, h if add else None, gamma, w, s_out if add else None, y, 1e-6,
+                                 cfg)
+            g = torch.empty((1, n), dtype=torch.float16, device="cuda")
+            s2 = torch.empty((1, k), dtype=torch.float16, device="cuda")
+            tmc.add_rmsnorm_gate_up_silu(r, h if add else None, gamma, w, w2, s2 if add else None,
+                                         g, 1e-6, cfg)
+            torch.cuda.synchronize()
+            what = f"cfg {cfg_t} k{k} n{n} add={add}"
+            assert torch.equal(y, y_ref), what
+            assert np.array_equal(bits(g), bits(g_ref)), what
+            if add:
+                assert np.array_equal(bits(s_out), bits(s_ref)), what
+                assert np.array_equal(bits(s2), bits(s_ref)), what
+            else:
+                assert torch.all(s_out == 7.0)
+
+
+def test_fused_norm_gemv_matches_oracle_and_rejects_batches(tmc, orc, torch):
+    k, n = 4096, 11008
+    h = orc.f16(normal(380, (1, k)))
+    r = orc.f16(normal(381, (1, k)))
+    gamma = orc.f16(uniform(382, (k,), 0.5, 1.5))
+    wg = orc.f16(normal(383, (n, k), 0.02))
+    wu = orc.f16(normal(384, (n, k), 0.02))
+    s_out = torch.empty((1, k), dtype=torch.float16, device="cuda")
+    g = torch.empty((1, n), dtype=torch.float16, device="cuda")
+    tmc.add_rmsnorm_gate_up_silu(dev_f16(r), dev_f16(h), dev_f16(gamma), dev_f16(wg), dev_f16(wu),
+                                 s_out, g, 1e-6)
+    torch.cuda.synchronize()
+    s_ref, n_ref = orc.add_rmsnorm(r, h, gamma, F16, 1e-6)
+    assert_f16_path(values(s_out), s_ref, what="fused residual sum")
+    n_chain = orc.f16(orc.store(n_ref, F16))
+    assert_f16_path(values(g), orc.gated_mlp(n_chain, wg, wu, F16), what="fused gated mlp")
+    x2 = torch.zeros((2, k), dtype=torch.float16, device="cuda")
+    with pytest.raises(tmc.TmcError):
+        tmc.add_rmsnorm_gemv(x2, x2, dev_f16(gamma), dev_f16(wg), x2,
+                             torch.empty((2, n), dtype=torch.float32, device="cuda"), 1e-6)
