@@ -170,6 +170,20 @@ def time_loop(torch, fn, iters: int, replays: int = 5) -> float:
     return start.elapsed_time(stop) / 1000.0 / (iters * replays)
 
 
+def host_cpu() -> dict:
+    """The host the CPU baseline ran on: model name and logical CPU count."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count()}
+
+
 def cpu_baseline(block: MlpBlock, seconds: float) -> dict:
     """Whole C2 blocks on the CPU oracle (single thread) with the GPU's copy-0 data."""
     import numpy as np
@@ -191,7 +205,7 @@ def cpu_baseline(block: MlpBlock, seconds: float) -> dict:
     total = mlp_block_bytes(block.batch)["total"] * done
     return {"value": round(total / elapsed / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{done} whole C2 blocks (B={block.batch}) on oracle/libtmc_oracle.so, "
-                      f"{elapsed:.1f} s, 1 thread"}
+                      f"{elapsed:.1f} s, 1 thread", **host_cpu()}
 
 
 def extra_measurements(tmc, torch, iters: int) -> dict:
@@ -365,6 +379,7 @@ def c5_cpu_baseline(seconds_hint: float = 10.0) -> dict:
         out[f"b{batch}_sample"] = (f"{n} layer(s) of the decode step ({per_layer:.2f} s each) + "
                                    f"LM head ({head:.2f} s), scaled to 32 layers")
     out["cores"] = 1
+    out.update(host_cpu())
     out["kind"] = "port"
     return out
 
