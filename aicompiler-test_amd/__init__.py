@@ -47,6 +47,11 @@ def _declare(l):
         "tmc_add_rmsnorm_gemv_f16": (i32, [vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, f, vp, vp]),
         "tmc_add_rmsnorm_gate_up_silu_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, f, vp,
                                                    vp]),
+        "tmc_add_rmsnorm_ex": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, f, i32, vp]),
+        "tmc_packed_activation_elements": (C.c_int64, [i64, i64]),
+        "tmc_pack_activations_f16": (i32, [vp, vp, i64, i64, i32, vp]),
+        "tmc_gemm_packed_ex_f16": (i32, [vp, vp, vp, i32, i64, i64, i64, i32, vp, vp]),
+        "tmc_gate_up_silu_packed_ex_f16": (i32, [vp, vp, vp, vp, i64, i64, i64, i32, vp, vp]),
         "tmc_packed_weight_elements": (C.c_int64, [i64, i64]),
         "tmc_pack_weights_f16": (i32, [vp, vp, i64, i64, vp]),
         "tmc_gemm_packed_f16": (i32, [vp, vp, vp, i32, i64, i64, i64, vp, vp]),
@@ -227,6 +232,55 @@ def add_rmsnorm_gate_up_silu(residual, update, gamma, wg, wu, sum_out, out, eps,
         _ptr(wu), _ptr(sum_out) if sum_out is not None else None, _ptr(out), b, h, f, eps,
         C.byref(cfg) if cfg is not None else None, _stream(stream)),
         "tmc_add_rmsnorm_gate_up_silu_f16")
+
+
+X_PACKED, Y_PACKED = 1, 2  # TMC_LAYOUT_X_PACKED, TMC_LAYOUT_Y_PACKED
+
+
+def packed_activation_elements(rows, cols) -> int:
+    return int(lib().tmc_packed_activation_elements(rows, cols))
+
+
+def pack_activations(x, out=None, unpack=False, rows=None, cols=None, stream=None):
+    """Row-major fp16 [rows, cols] <-> fragment order (tmc_pack_activations_f16)."""
+    import torch
+    if unpack:
+        assert out is not None and rows is not None and cols is not None
+    else:
+        rows, cols = x.shape
+        if out is None:
+            out = torch.empty(packed_activation_elements(rows, cols), dtype=torch.float16,
+                              device=x.device)
+    check(lib().tmc_pack_activations_f16(_ptr(x), _ptr(out), rows, cols, int(unpack),
+                                         _stream(stream)), "tmc_pack_activations_f16")
+    return out
+
+
+def add_rmsnorm_ex(residual, update, w, sum_out, norm_out, eps, layout, rows=None, width=None,
+                   stream=None):
+    rows = rows if rows is not None else residual.shape[0]
+    width = width if width is not None else residual.shape[1]
+    check(lib().tmc_add_rmsnorm_ex(_ptr(residual), _ptr(update) if update is not None else None,
+                                   _ptr(w), _ptr(sum_out) if sum_out is not None else None,
+                                   _ptr(norm_out), _dtype_code(residual), rows, width, eps, layout,
+                                   _stream(stream)), "tmc_add_rmsnorm_ex")
+
+
+def gemm_packed_ex(x, packed, y, batch, in_features, out_features, layout, cfg=None, y_dtype=None,
+                   stream=None):
+    check(lib().tmc_gemm_packed_ex_f16(_ptr(x), _ptr(packed), _ptr(y),
+                                       _dtype_code(y) if y_dtype is None else y_dtype, batch,
+                                       in_features, out_features, layout,
+                                       C.byref(cfg) if cfg is not None else None, _stream(stream)),
+          "tmc_gemm_packed_ex_f16")
+
+
+def gate_up_silu_packed_ex(x, packed_gate, packed_up, out, batch, hidden, intermediate, layout,
+                           cfg=None, stream=None):
+    check(lib().tmc_gate_up_silu_packed_ex_f16(_ptr(x), _ptr(packed_gate), _ptr(packed_up),
+                                               _ptr(out), batch, hidden, intermediate, layout,
+                                               C.byref(cfg) if cfg is not None else None,
+                                               _stream(stream)), "tmc_gate_up_silu_packed_ex_f16")
 
 
 def packed_weight_elements(out_features, in_features) -> int:

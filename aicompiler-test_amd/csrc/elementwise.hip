@@ -79,7 +79,10 @@ template <typename T> struct Vec8;
 template <> struct Vec8<half_t> { typedef h8 type; };
 template <> struct Vec8<float> { typedef float type __attribute__((ext_vector_type(8))); };
 
-template <typename T, int NV, bool ADD, int THREADS>
+// POUT: the normalized row is written in the activation fragment order of
+// the packed GEMM (include/tmc_hip.h): 16-row pass r / 16, 32-k chunk
+// v / 4, lane r % 16 + 16 * (v % 4) for the 8 elements 8v..8v+7.
+template <typename T, int NV, bool ADD, int THREADS, bool POUT = false>
 __global__ __launch_bounds__(THREADS) void norm_vec_kernel(const T* __restrict__ residual,
                                                           const T* __restrict__ update,
                                                           const T* __restrict__ w,
@@ -119,8 +122,34 @@ __global__ __launch_bounds__(THREADS) void norm_vec_kernel(const T* __restrict__
       for (int t = 0; t < 8; ++t)
         n[t] = from_float<T>(to_float<T>(val[i][t]) * inverse * to_float<T>(wv[t]));
       if constexpr (ADD) *reinterpret_cast<V*>(sum_out + base + 8 * v) = val[i];
-      *reinterpret_cast<V*>(norm_out + base + 8 * v) = n;
+      if constexpr (POUT) {
+        const size_t chunks = (size_t)(width + 31) / 32;
+        const size_t slot = ((size_t)(blockIdx.x >> 4) * chunks + (size_t)(v >> 2)) * 64 +
+                            (blockIdx.x & 15) + 16 * (v & 3);
+        *reinterpret_cast<V*>(norm_out + slot * 8) = n;
+      } else {
+        *reinterpret_cast<V*>(norm_out + base + 8 * v) = n;
+      }
     }
+  }
+}
+
+// RMSNorm / Add+RMSNorm (fp16, 256 threads) with the normalized row written
+// in the packed activation order; false when the row does not fit the
+// register-resident kernel.
+template <bool ADD>
+bool launch_norm_packed_out(const half_t* r, const half_t* u, const half_t* w, half_t* s,
+                            half_t* n, int64_t rows, int64_t width, float eps,
+                            hipStream_t stream) {
+  if (width % 8 != 0) return false;
+  const int nv = (int)((width / 8 + kThreads - 1) / kThreads);
+  const dim3 grid((unsigned)rows), block(kThreads);
+  switch (nv) {
+  case 1: hipLaunchKernelGGL((norm_vec_kernel<half_t, 1, ADD, kThreads, true>), grid, block, 0, stream, r, u, w, s, n, (int)width, eps); return true;
+  case 2: hipLaunchKernelGGL((norm_vec_kernel<half_t, 2, ADD, kThreads, true>), grid, block, 0, stream, r, u, w, s, n, (int)width, eps); return true;
+  case 3: hipLaunchKernelGGL((norm_vec_kernel<half_t, 3, ADD, kThreads, true>), grid, block, 0, stream, r, u, w, s, n, (int)width, eps); return true;
+  case 4: hipLaunchKernelGGL((norm_vec_kernel<half_t, 4, ADD, kThreads, true>), grid, block, 0, stream, r, u, w, s, n, (int)width, eps); return true;
+  default: return false;
   }
 }
 
@@ -550,6 +579,35 @@ extern "C" int tmc_add_rmsnorm(const void* residual, const void* update, const v
                                int64_t width, float epsilon, void* stream) {
   return norm_entry(true, residual, update, w, sum_out, norm_out, dtype, rows, width, epsilon, 0,
                     0, stream);
+}
+
+extern "C" int tmc_add_rmsnorm_ex(const void* residual, const void* update, const void* w,
+                                  void* sum_out, void* norm_out, int dtype, int64_t rows,
+                                  int64_t width, float epsilon, int layout, void* stream) {
+  TMC_REQUIRE(layout == 0 || layout == TMC_LAYOUT_Y_PACKED,
+              "Add+RMSNorm: layout must be 0 or TMC_LAYOUT_Y_PACKED.");
+  if (layout == 0)
+    return norm_entry(update != nullptr, residual, update, w, sum_out, norm_out, dtype, rows,
+                      width, epsilon, 0, 0, stream);
+  TMC_REQUIRE(residual && w && norm_out && (!update || sum_out), "Add+RMSNorm: null device pointer.");
+  TMC_REQUIRE(dtype == TMC_F16, "Add+RMSNorm: packed output needs fp16.");
+  TMC_REQUIRE(rows > 0 && width > 0 && rows < (1LL << 31), "Add+RMSNorm: invalid shape.");
+  TMC_REQUIRE(std::isfinite(epsilon) && epsilon > 0.0f,
+              "Add+RMSNorm: epsilon must be finite and positive.");
+  TMC_REQUIRE(aligned16(residual) && aligned16(w) && aligned16(norm_out) &&
+                  (!update || (aligned16(update) && aligned16(sum_out))),
+              "Add+RMSNorm: packed output needs 16-byte aligned operands.");
+  const half_t* r = static_cast<const half_t*>(residual);
+  const half_t* u = static_cast<const half_t*>(update);
+  const half_t* g = static_cast<const half_t*>(w);
+  half_t* s = static_cast<half_t*>(sum_out);
+  half_t* n = static_cast<half_t*>(norm_out);
+  const bool ok = update ? launch_norm_packed_out<true>(r, u, g, s, n, rows, width, epsilon,
+                                                        as_stream(stream))
+                         : launch_norm_packed_out<false>(r, nullptr, g, nullptr, n, rows, width,
+                                                         epsilon, as_stream(stream));
+  TMC_REQUIRE(ok, "Add+RMSNorm: packed output needs width % 8 == 0 and width <= 8192.");
+  return check_launch("add_rmsnorm packed kernel");
 }
 
 extern "C" int tmc_rmsnorm_threads(const void* x, const void* w, void* y, int dtype,

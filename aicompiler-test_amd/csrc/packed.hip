@@ -63,7 +63,10 @@ __global__ __launch_bounds__(256) void pack_kernel(const half_t* __restrict__ w,
   }
 }
 
-template <int MATS, int U, typename OutT>
+// XP: x is one 16-row pass in fragment order (lane l of chunk c holds row
+// l % 16, k 32c + 8(l / 16) .. +7, the A operand as loaded); YP: the fp16
+// output pass is written in the same order for the next GEMM.
+template <int MATS, int U, typename OutT, bool XP = false, bool YP = false>
 __global__ __launch_bounds__(1024) void packed_gemm_kernel(const half_t* __restrict__ x,
                                                            const half_t* __restrict__ p0,
                                                            const half_t* __restrict__ p1,
@@ -77,7 +80,8 @@ __global__ __launch_bounds__(1024) void packed_gemm_kernel(const half_t* __restr
   const int g = lane >> 4;
   const int nt = blockIdx.x;
   const int chunks = (k_in + 31) / 32;
-  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(x, (unsigned)m_rows * (unsigned)k_in * 2u);
+  const __amdgpu_buffer_rsrc_t rx =
+      buffer_rsrc(x, XP ? (unsigned)chunks * 1024u : (unsigned)m_rows * (unsigned)k_in * 2u);
   const __amdgpu_buffer_rsrc_t r0 = buffer_rsrc(p0, packed_bytes);
   const __amdgpu_buffer_rsrc_t r1 = buffer_rsrc(MATS == 2 ? p1 : p0, packed_bytes);
   const unsigned x_row = j < m_rows ? (unsigned)j * (unsigned)k_in * 2u : kNone;
@@ -101,8 +105,13 @@ __global__ __launch_bounds__(1024) void packed_gemm_kernel(const half_t* __restr
         wv[u][0][s] = buffer_load16(r0, w_off);
         if constexpr (MATS == 2) wv[u][1][s] = buffer_load16(r1, w_off);
         const int kk = c * 32 + 8 * g;
-        xv[u][s] = buffer_load16(
-            rx, live && kk < k_in && x_row != kNone ? x_row + (unsigned)kk * 2u : kNone);
+        if constexpr (XP)  // rows past the batch are never read (their slots are unset)
+          xv[u][s] = buffer_load16(
+              rx, live && kk < k_in && j < m_rows ? ((unsigned)c * 64u + (unsigned)lane) * 16u
+                                                  : kNone);
+        else
+          xv[u][s] = buffer_load16(
+              rx, live && kk < k_in && x_row != kNone ? x_row + (unsigned)kk * 2u : kNone);
       }
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -127,10 +136,13 @@ __global__ __launch_bounds__(1024) void packed_gemm_kernel(const half_t* __restr
     const int row = 4 * (l >> 4) + r;
     const int col = nt * 16 + (l & 15);
     if (row < m_rows && col < n_out) {
+      size_t at = (size_t)row * n_out + col;
+      if constexpr (YP)  // pass-relative fragment slot of (row, col)
+        at = ((size_t)(col >> 5) * 64 + row + 16 * ((col & 31) >> 3)) * 8 + (col & 7);
       if constexpr (MATS == 2)
-        y[(size_t)row * n_out + col] = gated_value(a[0], a[1]);
+        y[at] = gated_value(a[0], a[1]);
       else
-        y[(size_t)row * n_out + col] = from_float<OutT>(a[0]);
+        y[at] = from_float<OutT>(a[0]);
     }
   }
 }
@@ -154,32 +166,67 @@ void default_packed(int64_t batch, int64_t n, int mats, int& unroll, int& ks) {
     ks = 8;
 }
 
-template <int MATS, typename OutT>
+template <int MATS, typename OutT, bool XP, bool YP>
 int run_packed(const half_t* x, const half_t* p0, const half_t* p1, OutT* y, int64_t batch,
                int64_t k, int64_t n, int unroll, int ks, hipStream_t st) {
   const int64_t bytes = packed_elements(n, k) * 2;
   const dim3 grid((unsigned)((n + 15) / 16));
   const size_t lds = (size_t)ks * MATS * 4 * kWave * sizeof(float);
+  const int64_t x_pass = XP ? ((k + 31) / 32) * 512 : 16 * k;  // elements per 16-row pass
+  const int64_t y_pass = YP ? ((n + 31) / 32) * 512 : 16 * n;
   for (int64_t r0 = 0; r0 < batch; r0 += 16) {
     const int rows = (int)std::min<int64_t>(16, batch - r0);
-    const half_t* xs = x + r0 * k;
-    OutT* ys = y + r0 * n;
+    const half_t* xs = x + (r0 / 16) * x_pass;
+    OutT* ys = y + (r0 / 16) * y_pass;
     if (unroll == 1)
-      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 1, OutT>), grid, dim3(ks * kWave), lds, st, xs,
-                         p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes);
+      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 1, OutT, XP, YP>), grid, dim3(ks * kWave), lds,
+                         st, xs, p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes);
     else if (unroll == 2)
-      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 2, OutT>), grid, dim3(ks * kWave), lds, st, xs,
-                         p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes);
+      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 2, OutT, XP, YP>), grid, dim3(ks * kWave), lds,
+                         st, xs, p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes);
     else
-      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 4, OutT>), grid, dim3(ks * kWave), lds, st, xs,
-                         p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes);
+      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 4, OutT, XP, YP>), grid, dim3(ks * kWave), lds,
+                         st, xs, p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes);
     if (check_launch("packed_gemm_kernel")) return 1;
   }
   return 0;
 }
 
+template <int MATS, typename OutT>
+int run_packed_layout(const half_t* x, const half_t* p0, const half_t* p1, OutT* y,
+                      int64_t batch, int64_t k, int64_t n, int unroll, int ks, int layout,
+                      hipStream_t st) {
+  const bool xp = layout & TMC_LAYOUT_X_PACKED, yp = layout & TMC_LAYOUT_Y_PACKED;
+  if (xp && yp) return run_packed<MATS, OutT, true, true>(x, p0, p1, y, batch, k, n, unroll, ks, st);
+  if (xp) return run_packed<MATS, OutT, true, false>(x, p0, p1, y, batch, k, n, unroll, ks, st);
+  if (yp) return run_packed<MATS, OutT, false, true>(x, p0, p1, y, batch, k, n, unroll, ks, st);
+  return run_packed<MATS, OutT, false, false>(x, p0, p1, y, batch, k, n, unroll, ks, st);
+}
+
+// One thread per 8-element slot of a 16-row pass in fragment order.
+__global__ __launch_bounds__(256) void pack_activations_kernel(const half_t* __restrict__ src,
+                                                               half_t* __restrict__ dst, int rows,
+                                                               int cols, int unpack, long slots) {
+  const int chunks = (cols + 31) / 32;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < slots;
+       i += (long)gridDim.x * blockDim.x) {
+    const int lane = (int)(i & 63);
+    const long frag = i >> 6;
+    const int c = (int)(frag % chunks);
+    const long pass = frag / chunks;
+    const long row = pass * 16 + (lane & 15);
+    const int col = c * 32 + 8 * (lane >> 4);
+    if (row >= rows || col >= cols) continue;
+    const size_t rm = (size_t)row * cols + col;
+    if (unpack)
+      *reinterpret_cast<h8*>(dst + rm) = *reinterpret_cast<const h8*>(src + i * 8);
+    else
+      *reinterpret_cast<h8*>(dst + i * 8) = *reinterpret_cast<const h8*>(src + rm);
+  }
+}
+
 int packed_entry(int mats, const void* x, const void* p0, const void* p1, void* y, int y_dtype,
-                 int64_t batch, int64_t k, int64_t n, const tmc_gemv_config* config,
+                 int64_t batch, int64_t k, int64_t n, int layout, const tmc_gemv_config* config,
                  void* stream) {
   const char* what = mats == 2 ? "Packed gated MLP" : "Packed GEMM";
   TMC_REQUIRE(x && p0 && y && (mats == 1 || p1), std::string(what) + ": null device pointer.");
@@ -199,15 +246,24 @@ int packed_entry(int mats, const void* x, const void* p0, const void* p1, void* 
   }
   TMC_REQUIRE((unroll == 1 || unroll == 2 || unroll == 4) && ks >= 1 && ks <= 16,
               std::string(what) + ": config needs unroll 1|2|4 and k_split 1..16.");
+  TMC_REQUIRE((layout & ~(TMC_LAYOUT_X_PACKED | TMC_LAYOUT_Y_PACKED)) == 0,
+              std::string(what) + ": unknown layout bits.");
+  TMC_REQUIRE(!(layout & TMC_LAYOUT_Y_PACKED) || y_dtype == TMC_F16,
+              std::string(what) + ": a packed output must be fp16.");
+  TMC_REQUIRE(!(layout & TMC_LAYOUT_Y_PACKED) || aligned16(y),
+              std::string(what) + ": a packed output must be 16-byte aligned.");
   const hipStream_t st = as_stream(stream);
   const half_t* xs = static_cast<const half_t*>(x);
   const half_t* a = static_cast<const half_t*>(p0);
   const half_t* b = static_cast<const half_t*>(p1);
   if (mats == 2)
-    return run_packed<2, half_t>(xs, a, b, static_cast<half_t*>(y), batch, k, n, unroll, ks, st);
+    return run_packed_layout<2, half_t>(xs, a, b, static_cast<half_t*>(y), batch, k, n, unroll,
+                                        ks, layout, st);
   if (y_dtype == TMC_F32)
-    return run_packed<1, float>(xs, a, a, static_cast<float*>(y), batch, k, n, unroll, ks, st);
-  return run_packed<1, half_t>(xs, a, a, static_cast<half_t*>(y), batch, k, n, unroll, ks, st);
+    return run_packed_layout<1, float>(xs, a, a, static_cast<float*>(y), batch, k, n, unroll, ks,
+                                       layout & TMC_LAYOUT_X_PACKED, st);
+  return run_packed_layout<1, half_t>(xs, a, a, static_cast<half_t*>(y), batch, k, n, unroll, ks,
+                                      layout, st);
 }
 
 }  // namespace
@@ -238,7 +294,7 @@ extern "C" int tmc_pack_weights_f16(const void* w, void* packed, int64_t out_fea
 extern "C" int tmc_gemm_packed_f16(const void* x, const void* packed_w, void* y, int y_dtype,
                                    int64_t batch, int64_t in_features, int64_t out_features,
                                    const tmc_gemv_config* config, void* stream) {
-  return packed_entry(1, x, packed_w, nullptr, y, y_dtype, batch, in_features, out_features,
+  return packed_entry(1, x, packed_w, nullptr, y, y_dtype, batch, in_features, out_features, 0,
                       config, stream);
 }
 
@@ -246,6 +302,40 @@ extern "C" int tmc_gate_up_silu_packed_f16(const void* x, const void* packed_gat
                                            const void* packed_up, void* out, int64_t batch,
                                            int64_t hidden, int64_t intermediate,
                                            const tmc_gemv_config* config, void* stream) {
-  return packed_entry(2, x, packed_gate, packed_up, out, TMC_F16, batch, hidden, intermediate,
+  return packed_entry(2, x, packed_gate, packed_up, out, TMC_F16, batch, hidden, intermediate, 0,
                       config, stream);
+}
+
+extern "C" int tmc_gemm_packed_ex_f16(const void* x, const void* packed_w, void* y, int y_dtype,
+                                      int64_t batch, int64_t in_features, int64_t out_features,
+                                      int layout, const tmc_gemv_config* config, void* stream) {
+  return packed_entry(1, x, packed_w, nullptr, y, y_dtype, batch, in_features, out_features,
+                      layout, config, stream);
+}
+
+extern "C" int tmc_gate_up_silu_packed_ex_f16(const void* x, const void* packed_gate,
+                                              const void* packed_up, void* out, int64_t batch,
+                                              int64_t hidden, int64_t intermediate, int layout,
+                                              const tmc_gemv_config* config, void* stream) {
+  return packed_entry(2, x, packed_gate, packed_up, out, TMC_F16, batch, hidden, intermediate,
+                      layout, config, stream);
+}
+
+extern "C" int64_t tmc_packed_activation_elements(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return ((rows + 15) / 16) * ((cols + 31) / 32) * 512;
+}
+
+extern "C" int tmc_pack_activations_f16(const void* src, void* dst, int64_t rows, int64_t cols,
+                                        int unpack, void* stream) {
+  TMC_REQUIRE(src && dst, "Pack activations: null device pointer.");
+  TMC_REQUIRE(rows > 0 && cols > 0 && cols % 8 == 0 && rows < (1LL << 31) && cols < (1LL << 31),
+              "Pack activations: cols must be a positive multiple of 8.");
+  TMC_REQUIRE(aligned16(src) && aligned16(dst), "Pack activations: operands must be 16-byte aligned.");
+  const long slots = (long)(tmc_packed_activation_elements(rows, cols) / 8);
+  const unsigned blocks = (unsigned)std::min<long>((slots + 255) / 256, 65536);
+  hipLaunchKernelGGL(pack_activations_kernel, dim3(blocks), dim3(256), 0, as_stream(stream),
+                     static_cast<const half_t*>(src), static_cast<half_t*>(dst), (int)rows,
+                     (int)cols, unpack, slots);
+  return check_launch("pack_activations_kernel");
 }

@@ -258,6 +258,20 @@ bool parse_key(const std::string& key, std::string& name, Params& params) {
   return !name.empty();
 }
 
+// Activation layouts of the packed GEMM keys: x_layout / y_layout =
+// row_major (default) | packed.
+bool layout_param(const Params& p, int& layout) {
+  layout = 0;
+  for (const auto& [field, bit] :
+       {std::pair<const char*, int>{"x_layout", TMC_LAYOUT_X_PACKED}, {"y_layout", TMC_LAYOUT_Y_PACKED}}) {
+    const auto it = p.find(field);
+    if (it == p.end() || it->second == "row_major") continue;
+    if (it->second != "packed") return false;
+    layout |= bit;
+  }
+  return true;
+}
+
 // Optional GEMV launch configuration in a key: algorithm (0 auto, 1 dot,
 // 2 MFMA, 3 MFMA row tiles, 4 linear baseline), rows_per_wave, unroll,
 // k_split.  Validated when the kernel launches.
@@ -359,12 +373,18 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
          "gemm_packed needs batch, in, out > 0, dtype=f16 and out_dtype f16|f32.");
     tmc_gemv_config cfg{};
     NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    int layout = 0;
+    NEED(layout_param(p, layout), "packed GEMM key: x_layout / y_layout must be row_major or packed.");
+    NEED(!(layout & TMC_LAYOUT_Y_PACKED) || od == TMC_F16, "gemm_packed: a packed output is fp16.");
     s.inputs = {TMC_F16, TMC_F16};
     s.outputs = {od};
-    s.counts = {(size_t)(b * k), (size_t)tmc_packed_weight_elements(n, k), (size_t)(b * n)};
+    s.counts = {(size_t)((layout & TMC_LAYOUT_X_PACKED) ? tmc_packed_activation_elements(b, k) : b * k),
+                (size_t)tmc_packed_weight_elements(n, k),
+                (size_t)((layout & TMC_LAYOUT_Y_PACKED) ? tmc_packed_activation_elements(b, n) : b * n)};
     s.groups = (size_t)((n + 15) / 16);
     s.launch = [=](const LaunchContext& c) {
-      return tmc_gemm_packed_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], od, b, k, n, &cfg, c.stream);
+      return tmc_gemm_packed_ex_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], od, b, k, n, layout, &cfg,
+                                    c.stream);
     };
     return true;
   }
@@ -374,14 +394,18 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
          "gate_up_silu_packed needs batch, hidden, inter and f16.");
     tmc_gemv_config cfg{};
     NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    int layout = 0;
+    NEED(layout_param(p, layout), "packed GEMM key: x_layout / y_layout must be row_major or packed.");
     const size_t pe = (size_t)tmc_packed_weight_elements(f, h);
     s.inputs = {TMC_F16, TMC_F16, TMC_F16};
     s.outputs = {TMC_F16};
     s.groups = (size_t)((f + 15) / 16);
-    s.counts = {(size_t)(b * h), pe, pe, (size_t)(b * f)};
+    s.counts = {(size_t)((layout & TMC_LAYOUT_X_PACKED) ? tmc_packed_activation_elements(b, h) : b * h),
+                pe, pe,
+                (size_t)((layout & TMC_LAYOUT_Y_PACKED) ? tmc_packed_activation_elements(b, f) : b * f)};
     s.launch = [=](const LaunchContext& c) {
-      return tmc_gate_up_silu_packed_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], b, h, f,
-                                         &cfg, c.stream);
+      return tmc_gate_up_silu_packed_ex_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], b, h, f,
+                                            layout, &cfg, c.stream);
     };
     return true;
   }
@@ -413,8 +437,31 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
          "rmsnorm threads must be 64, 128, 256, 512 or 1024.");
     NEED(vname == "default" || vname == "two_pass", "rmsnorm variant must be default or two_pass.");
     const int variant = vname == "two_pass" ? 1 : 0;
+    const auto lit = p.find("out_layout");
+    const bool packed_out = lit != p.end() && lit->second == "packed";
+    NEED(lit == p.end() || lit->second == "packed" || lit->second == "row_major",
+         "rmsnorm out_layout must be row_major or packed.");
+    NEED(!packed_out || (dt == TMC_F16 && threads == 256 && variant == 0),
+         "rmsnorm packed output needs f16 and the default 256-thread kernel.");
     s.groups = (size_t)rows;
     s.threads = (size_t)threads;
+    if (packed_out) {
+      const bool add = name == "add_rmsnorm";
+      const size_t n_count = (size_t)tmc_packed_activation_elements(rows, width);
+      s.inputs = add ? std::vector<int>{dt, dt, dt} : std::vector<int>{dt, dt};
+      s.outputs = add ? std::vector<int>{dt, dt} : std::vector<int>{dt};
+      s.counts = add ? std::vector<size_t>{(size_t)(rows * width), (size_t)(rows * width),
+                                           (size_t)width, (size_t)(rows * width), n_count}
+                     : std::vector<size_t>{(size_t)(rows * width), (size_t)width, n_count};
+      s.launch = [=](const LaunchContext& c) {
+        if (add)
+          return tmc_add_rmsnorm_ex(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], c.ptrs[4], dt, rows,
+                                    width, eps, TMC_LAYOUT_Y_PACKED, c.stream);
+        return tmc_add_rmsnorm_ex(c.ptrs[0], nullptr, c.ptrs[1], nullptr, c.ptrs[2], dt, rows,
+                                  width, eps, TMC_LAYOUT_Y_PACKED, c.stream);
+      };
+      return true;
+    }
     if (name == "rmsnorm") {
       s.inputs = {dt, dt};
       s.outputs = {dt};

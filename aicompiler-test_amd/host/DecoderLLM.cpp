@@ -338,14 +338,17 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
     activationBytes_ += count * hip::elementBytes(type);
     return allocate(rt, count, nullptr, type);
   };
+  // normalized_ and gated_ also hold the fragment-ordered activations of the
+  // batch > 1 buckets: whole 16-row passes.
+  const std::size_t passRows = (M + 15) / 16 * 16;
   residual_ = act(M * H);
   after_ = act(M * H);
-  normalized_ = act(M * H);
+  normalized_ = act(std::max(M * H, passRows * ((H + 31) / 32 * 32)));
   qkv_ = act(M * QKV);
   query_ = act(M * H);
   context_ = act(M * H);
   projected_ = act(M * H);
-  gated_ = act(M * I);
+  gated_ = act(std::max(M * I, passRows * ((I + 31) / 32 * 32)));
   mlp_ = act(M * H);
   logits_ = act(M * V, ElementType::Float32);
   nextTokens_ = act(M, ElementType::Int32);
@@ -376,15 +379,21 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
     };
     // Batch 1 streams row-major weights with the dot GEMV; larger buckets run
     // the MFMA GEMM over the fragment-packed copies.
+    // Above batch 1 the norms write the normalized rows, and the gated MLP
+    // its output, in the GEMM's activation fragment order (x_layout=packed
+    // for q.k.v, gate/up, down and the LM head; o reads the attention output
+    // row-major).
     const bool packed = m > 1;
-    auto gemv = [&](std::size_t in, std::size_t out, const char* outType) {
+    auto gemv = [&](std::size_t in, std::size_t out, const char* outType, bool xPacked = true) {
       return std::string(packed ? "gemm_packed" : "decode_gemv") + "?batch=" + B +
-             "&in=" + std::to_string(in) + "&out=" + std::to_string(out) + "&out_dtype=" + outType;
+             "&in=" + std::to_string(in) + "&out=" + std::to_string(out) + "&out_dtype=" + outType +
+             (packed && xPacked ? "&x_layout=packed" : "");
     };
     auto weights = [&](std::size_t l) -> const DecoderLLMModelLayerBuffers& {
       return packed ? model_->packedLayers[l] : model_->layers[l];
     };
-    const std::string norm = "rows=" + B + "&width=" + std::to_string(H) + "&eps=" + eps + "&dtype=f16";
+    const std::string norm = "rows=" + B + "&width=" + std::to_string(H) + "&eps=" + eps +
+                             "&dtype=f16" + (packed ? "&out_layout=packed" : "");
     add("embedding?rows=" + B + "&hidden=" + std::to_string(H) + "&vocab=" + std::to_string(V),
         "embedding", {tokensView_, model_->embeddingWeight}, {residual_});
     add("rmsnorm?" + norm, "l0_input_norm", {residual_, model_->layers[0].inputNormWeight},
@@ -412,11 +421,12 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
           {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer(), lengthsView_, tableViews_[l],
            activeView_},
           {context_});
-      add(gemv(H, H, "f16"), p + "o", {context_, pw.outputWeight}, {projected_});
+      add(gemv(H, H, "f16", false), p + "o", {context_, pw.outputWeight}, {projected_});
       add("add_rmsnorm?" + norm, p + "residual_post_norm",
           {residual_, projected_, w.postAttentionNormWeight}, {after_, normalized_});
       add(std::string(packed ? "gate_up_silu_packed" : "gate_up_silu") + "?batch=" + B +
-              "&hidden=" + std::to_string(H) + "&inter=" + std::to_string(I),
+              "&hidden=" + std::to_string(H) + "&inter=" + std::to_string(I) +
+              (packed ? "&x_layout=packed&y_layout=packed" : ""),
           p + "gate_up_silu", {normalized_, pw.gateWeight, pw.upWeight}, {gated_});
       add(gemv(I, H, "f16"), p + "down", {gated_, pw.downWeight}, {mlp_});
     }

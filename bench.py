@@ -108,19 +108,23 @@ class MlpBlock:
                 wg, wu, wd = tmc.pack_weights(wg), tmc.pack_weights(wu), tmc.pack_weights(wd)
             self.weights.append((gamma, wg, wu, wd))
         self.s = torch.empty((batch, HIDDEN), dtype=f16, device=dev)
-        self.n = torch.empty((batch, HIDDEN), dtype=f16, device=dev)
-        self.g = torch.empty((batch, INTER), dtype=f16, device=dev)
+        rows16 = (batch + 15) // 16 * 16  # packed activations fill whole 16-row passes
+        self.n = torch.empty((rows16 if packed else batch, HIDDEN), dtype=f16, device=dev)
+        self.g = torch.empty((rows16 if packed else batch, INTER), dtype=f16, device=dev)
         self.y = torch.empty((batch, HIDDEN), dtype=torch.float32, device=dev)
         torch.cuda.synchronize()
 
     def step(self, i: int) -> None:
         gamma, wg, wu, wd = self.weights[i % self.copies]
         t = self.tmc
-        t.add_rmsnorm(self.h, self.r, gamma, self.s, self.n, 1e-6)
-        if self.packed:
-            t.gate_up_silu_packed(self.n, wg, wu, self.g, INTER)
-            t.gemm_packed(self.g, wd, self.y, HIDDEN)
+        if self.packed:  # activations between the kernels in fragment order
+            b = self.batch
+            t.add_rmsnorm_ex(self.h, self.r, gamma, self.s, self.n, 1e-6, t.Y_PACKED)
+            t.gate_up_silu_packed_ex(self.n, wg, wu, self.g, b, HIDDEN, INTER,
+                                     t.X_PACKED | t.Y_PACKED)
+            t.gemm_packed_ex(self.g, wd, self.y, b, INTER, HIDDEN, t.X_PACKED)
         else:
+            t.add_rmsnorm(self.h, self.r, gamma, self.s, self.n, 1e-6)
             t.gate_up_silu(self.n, wg, wu, self.g)
             t.gemv(self.g, wd, self.y)
 

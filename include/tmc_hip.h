@@ -208,6 +208,30 @@ int tmc_add_rmsnorm_gate_up_silu_f16(const void *residual, const void *update, c
                                      int64_t intermediate, float epsilon,
                                      const tmc_gemv_config *config, void *stream);
 
+/* Activation layouts of the batch > 1 GEMM path.  TMC_LAYOUT_X_PACKED: the
+ * GEMM's activations x [batch, in] are in fragment order; TMC_LAYOUT_Y_PACKED:
+ * the kernel writes its fp16 output in fragment order (for the next GEMM).
+ * Fragment order of A [rows, cols]: 16-row pass r / 16, 32-column chunk
+ * c / 32, lane r % 16 + 16 * ((c % 32) / 8), element c % 8 -- the A operand of
+ * v_mfma_f32_16x16x32_f16 -- at ((r / 16) * ceil(cols / 32) + c / 32) * 1024
+ * bytes; rows past `rows` and columns past `cols` inside the last pass and
+ * chunk are never read. */
+#define TMC_LAYOUT_X_PACKED 1
+#define TMC_LAYOUT_Y_PACKED 2
+int64_t tmc_packed_activation_elements(int64_t rows, int64_t cols);
+/* Reorder row-major fp16 activations into fragment order (and back with
+ * `unpack` != 0). */
+int tmc_pack_activations_f16(const void *src, void *dst, int64_t rows, int64_t cols, int unpack,
+                             void *stream);
+
+/* tmc_add_rmsnorm (update != NULL) or tmc_rmsnorm (update == NULL; sum_out
+ * unused) with a layout: 0 = row-major, TMC_LAYOUT_Y_PACKED = the normalized
+ * rows in fragment order (fp16, width % 8 == 0, width <= 8192, 16-byte
+ * aligned operands); the sum stays row-major. */
+int tmc_add_rmsnorm_ex(const void *residual, const void *update, const void *w, void *sum_out,
+                       void *norm_out, int dtype, int64_t rows, int64_t width, float epsilon,
+                       int layout, void *stream);
+
 /* Fragment-packed weights for the batch > 1 skinny GEMM.  No reference
  * counterpart (the reference streams row-major weights, DecodeGEMVMetalEmitter
  * .cpp:68-132): a one-time repacking of W [out, in] row-major into tiles of
@@ -231,6 +255,14 @@ int tmc_gemm_packed_f16(const void *x, const void *packed_w, void *y, int y_dtyp
 int tmc_gate_up_silu_packed_f16(const void *x, const void *packed_gate, const void *packed_up,
                                 void *out, int64_t batch, int64_t hidden, int64_t intermediate,
                                 const tmc_gemv_config *config, void *stream);
+/* The same with activation layouts (TMC_LAYOUT_* bits): x packed, and/or
+ * an fp16 output written packed. */
+int tmc_gemm_packed_ex_f16(const void *x, const void *packed_w, void *y, int y_dtype,
+                           int64_t batch, int64_t in_features, int64_t out_features, int layout,
+                           const tmc_gemv_config *config, void *stream);
+int tmc_gate_up_silu_packed_ex_f16(const void *x, const void *packed_gate, const void *packed_up,
+                                   void *out, int64_t batch, int64_t hidden, int64_t intermediate,
+                                   int layout, const tmc_gemv_config *config, void *stream);
 
 /* emitDecoderRMSNorm (DecoderLLMMetalEmitter.cpp:63-108) / emitRMSNorm
  * (MetalEmitter.cpp:12-76): y = x * rsqrt(mean(x^2) + eps) * w, fp32

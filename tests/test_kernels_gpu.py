@@ -674,3 +674,96 @@ def test_fused_norm_gemv_matches_oracle_and_rejects_batches(tmc, orc, torch):
     with pytest.raises(tmc.TmcError):
         tmc.add_rmsnorm_gemv(x2, x2, dev_f16(gamma), dev_f16(wg), x2,
                              torch.empty((2, n), dtype=torch.float32, device="cuda"), 1e-6)
+
+
+# ---------------------------------------------------------------- packed activations
+def _pack_act_reference(a_bits):
+    """Fragment order of A [rows, cols] (include/tmc_hip.h), unwritten slots 0."""
+    rows, cols = a_bits.shape
+    passes, kc = (rows + 15) // 16, (cols + 31) // 32
+    padded = np.zeros((passes * 16, kc * 32), np.uint16)
+    padded[:rows, :cols] = a_bits
+    return padded.reshape(passes, 16, kc, 4, 8).transpose(0, 2, 3, 1, 4).reshape(-1)
+
+
+def _unwritten_mask(rows, cols):
+    """Slots of the fragment order that hold real (row, col) elements."""
+    passes, kc = (rows + 15) // 16, (cols + 31) // 32
+    live = np.zeros((passes * 16, kc * 32), bool)
+    live[:rows, :cols] = True
+    return live.reshape(passes, 16, kc, 4, 8).transpose(0, 2, 3, 1, 4).reshape(-1)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 8), (5, 40), (16, 4096), (20, 4096), (33, 1160)])
+def test_pack_activations_layout_and_round_trip(tmc, orc, torch, rows, cols):
+    a = orc.f16(normal(390, (rows, cols)))
+    packed = tmc.pack_activations(dev_f16(a))
+    back = torch.empty((rows, cols), dtype=torch.float16, device="cuda")
+    tmc.pack_activations(packed, back, unpack=True, rows=rows, cols=cols)
+    torch.cuda.synchronize()
+    live = _unwritten_mask(rows, cols)
+    assert packed.numel() == tmc.packed_activation_elements(rows, cols) == live.size
+    assert np.array_equal(bits(packed)[live], _pack_act_reference(a)[live])
+    assert np.array_equal(bits(back), a)
+
+
+@pytest.mark.parametrize("rows", [1, 5, 16, 20])
+def test_add_rmsnorm_packed_output_bit_exact(tmc, orc, torch, rows):
+    k = 4096
+    h = dev_f16(orc.f16(normal(391, (rows, k))))
+    r = dev_f16(orc.f16(normal(392, (rows, k))))
+    gamma = dev_f16(orc.f16(uniform(393, (k,), 0.5, 1.5)))
+    s_ref, n_ref = torch.empty((rows, k), dtype=torch.float16, device="cuda"), None
+    n_ref = torch.empty_like(s_ref)
+    tmc.add_rmsnorm(r, h, gamma, s_ref, n_ref, 1e-6)
+    s_out = torch.empty_like(s_ref)
+    n_packed = torch.empty(tmc.packed_activation_elements(rows, k), dtype=torch.float16,
+                           device="cuda")
+    tmc.add_rmsnorm_ex(r, h, gamma, s_out, n_packed, 1e-6, tmc.Y_PACKED)
+    n_only = torch.empty_like(n_packed)
+    tmc.add_rmsnorm_ex(r, None, gamma, None, n_only, 1e-6, tmc.Y_PACKED)
+    plain = torch.empty_like(s_ref)
+    tmc.rmsnorm(r, gamma, plain, 1e-6)
+    torch.cuda.synchronize()
+    live = _unwritten_mask(rows, k)
+    assert np.array_equal(bits(s_out), bits(s_ref))
+    assert np.array_equal(bits(n_packed)[live], _pack_act_reference(bits(n_ref))[live])
+    assert np.array_equal(bits(n_only)[live], _pack_act_reference(bits(plain))[live])
+
+
+@pytest.mark.parametrize("layout", [1, 2, 3])
+def test_packed_gemm_activation_layouts_bit_exact(tmc, orc, torch, layout):
+    """x packed and/or y packed gives the same bits as row-major activations."""
+    for batch, k, n in ((5, 1160, 200), (16, 4096, 4096), (20, 4096, 11008)):
+        x = dev_f16(orc.f16(normal(394 + batch, (batch, k))))
+        w = dev_f16(orc.f16(normal(395, (n, k), 0.02)))
+        w2 = dev_f16(orc.f16(normal(396, (n, k), 0.02)))
+        pw, pw2 = tmc.pack_weights(w), tmc.pack_weights(w2)
+        xin = tmc.pack_activations(x) if layout & 1 else x
+        # plain GEMM (fp16 out)
+        ref = torch.empty((batch, n), dtype=torch.float16, device="cuda")
+        tmc.gemm_packed(x, pw, ref, n)
+        y = (torch.empty(tmc.packed_activation_elements(batch, n), dtype=torch.float16,
+                         device="cuda") if layout & 2 else torch.empty_like(ref))
+        tmc.gemm_packed_ex(xin, pw, y, batch, k, n, layout, y_dtype=0)
+        g_ref = torch.empty((batch, n), dtype=torch.float16, device="cuda")
+        tmc.gate_up_silu_packed(x, pw, pw2, g_ref, n)
+        g = torch.empty_like(y)
+        tmc.gate_up_silu_packed_ex(xin, pw, pw2, g, batch, k, n, layout)
+        torch.cuda.synchronize()
+        if layout & 2:
+            live = _unwritten_mask(batch, n)
+            assert np.array_equal(bits(y)[live], _pack_act_reference(bits(ref))[live])
+            assert np.array_equal(bits(g)[live], _pack_act_reference(bits(g_ref))[live])
+        else:
+            assert torch.equal(y, ref) and torch.equal(g, g_ref)
+    # fp32 output with x packed
+    f = torch.empty((batch, n), dtype=torch.float32, device="cuda")
+    f_ref = torch.empty_like(f)
+    tmc.gemm_packed(x, pw, f_ref, n)
+    tmc.gemm_packed_ex(xin, pw, f, batch, k, n, layout & 1, y_dtype=1)
+    torch.cuda.synchronize()
+    assert torch.equal(f, f_ref)
+    if layout & 2:
+        with pytest.raises(tmc.TmcError):  # a packed output must be fp16
+            tmc.gemm_packed_ex(xin, pw, f, batch, k, n, layout, y_dtype=1)
