@@ -10,7 +10,6 @@ namespace tmc {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / kWave;
 
 // Block-wide sum for THREADS threads (a multiple of 64); every thread gets
 // the total.
@@ -93,8 +92,14 @@ __global__ __launch_bounds__(THREADS) void norm_vec_kernel(const T* __restrict__
   __shared__ float scratch[THREADS / kWave];
   const size_t base = (size_t)blockIdx.x * width;
   const int vecs = width / 8;
-  V val[NV];
+  V val[NV], wv[NV];
   float squares = 0.0f;
+  // gamma is loaded with the row, so the reduction is the only wait
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int v = threadIdx.x + i * THREADS;
+    if (v < vecs) wv[i] = *reinterpret_cast<const V*>(w + 8 * v);
+  }
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int v = threadIdx.x + i * THREADS;
@@ -116,11 +121,10 @@ __global__ __launch_bounds__(THREADS) void norm_vec_kernel(const T* __restrict__
   for (int i = 0; i < NV; ++i) {
     const int v = threadIdx.x + i * THREADS;
     if (v < vecs) {
-      const V wv = *reinterpret_cast<const V*>(w + 8 * v);
       V n;
 #pragma unroll
       for (int t = 0; t < 8; ++t)
-        n[t] = from_float<T>(to_float<T>(val[i][t]) * inverse * to_float<T>(wv[t]));
+        n[t] = from_float<T>(to_float<T>(val[i][t]) * inverse * to_float<T>(wv[i][t]));
       if constexpr (ADD) *reinterpret_cast<V*>(sum_out + base + 8 * v) = val[i];
       if constexpr (POUT) {
         const size_t chunks = (size_t)(width + 31) / 32;
@@ -383,19 +387,24 @@ __global__ __launch_bounds__(kThreads) void decode_rope_append_kernel(
   const int row_pairs = (q_heads + 2 * kv_heads) * pairs;
   const long gid = (long)blockIdx.x * kThreads + threadIdx.x;
   const int request = (int)(gid / row_pairs);
-  if (request >= max_batch || request >= active_count[0]) return;
+  if (request >= max_batch) return;
+  // The active count, the row's length and its q.k.v pair are read together
+  // (all in bounds for request < max_batch), so the tables are the only
+  // dependent round trip.
+  const int active = active_count[0];
   const int valid = valid_lengths[request];
-  if (valid <= 0 || valid > capacity) return;
-  const int position = valid - 1;
   const int column = 2 * (int)(gid % row_pairs);
   const int q_width = q_heads * head_dim, kv_width = kv_heads * head_dim;
   const T* src = qkv + (size_t)request * (q_width + 2 * kv_width) + column;
+  const T x0 = src[0], x1 = src[1];
+  if (request >= active || valid <= 0 || valid > capacity) return;
+  const int position = valid - 1;
   const int pair = (column % head_dim) / 2;
   if (column < q_width + kv_width) {
     const float c = cosine[(size_t)position * pairs + pair];
     const float s = sine[(size_t)position * pairs + pair];
     float re, ro;
-    rotate_pair(to_float<T>(src[0]), to_float<T>(src[1]), c, s, re, ro);
+    rotate_pair(to_float<T>(x0), to_float<T>(x1), c, s, re, ro);
     if (column < q_width) {
       T* dst = q_out + (size_t)request * q_width + column;
       dst[0] = from_float<T>(re);
@@ -416,28 +425,59 @@ __global__ __launch_bounds__(kThreads) void decode_rope_append_kernel(
   const int feature = column - q_width - kv_width;
   T* dst = v_pool + (((size_t)page * kv_heads + feature / head_dim) * page_size +
                      position % page_size) * head_dim + feature % head_dim;
-  dst[0] = src[0];
-  dst[1] = src[1];
+  dst[0] = x0;
+  dst[1] = x1;
 }
 
 __device__ __forceinline__ bool better(float cv, int ci, float bv, int bi) {
   return cv > bv || (cv == bv && ci >= 0 && (bi < 0 || ci < bi));
 }
 
-// emitTokenArgmax (TransformerDecodeMetalEmitter.cpp:198-256).
-__global__ __launch_bounds__(kThreads) void argmax_kernel(const float* __restrict__ logits,
-                                                         int32_t* __restrict__ tokens,
-                                                         int vocabulary) {
-  __shared__ float best_v[kWaves];
-  __shared__ int best_i[kWaves];
-  const size_t base = (size_t)blockIdx.x * vocabulary;
+// emitTokenArgmax (TransformerDecodeMetalEmitter.cpp:198-256): greedy
+// token, ties to the lowest index, NaN never selected.  One 1024-thread block
+// per row; each thread issues all of its 16-byte loads (up to kArgmaxLoads)
+// before comparing, so a 32000-entry row costs one memory round trip.
+constexpr int kArgmaxThreads = 1024;
+constexpr int kArgmaxLoads = 8;
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits,
+                                                               int32_t* __restrict__ tokens,
+                                                               int vocabulary) {
+  __shared__ float best_v[kArgmaxThreads / kWave];
+  __shared__ int best_i[kArgmaxThreads / kWave];
+  const float* row = logits + (size_t)blockIdx.x * vocabulary;
   float best = -INFINITY;
   int selected = -1;
-  for (int t = threadIdx.x; t < vocabulary; t += kThreads) {
-    const float c = logits[base + t];
-    if (c > best || (c == best && (selected < 0 || t < selected))) {
-      best = c;
-      selected = t;
+  const bool vec = (vocabulary & 3) == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0;
+  if (vec) {
+    const int quads = vocabulary >> 2;
+    for (int q0 = threadIdx.x; q0 < quads; q0 += kArgmaxThreads * kArgmaxLoads) {
+      float4 v[kArgmaxLoads];
+#pragma unroll
+      for (int u = 0; u < kArgmaxLoads; ++u) {
+        const int q = q0 + u * kArgmaxThreads;
+        v[u] = q < quads ? reinterpret_cast<const float4*>(row)[q]
+                         : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      }
+#pragma unroll
+      for (int u = 0; u < kArgmaxLoads; ++u) {
+        const int t = 4 * (q0 + u * kArgmaxThreads);
+        const float c[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (t + e < vocabulary && (c[e] > best || (c[e] == best && (selected < 0 || t + e < selected)))) {
+            best = c[e];
+            selected = t + e;
+          }
+      }
+    }
+  } else {
+    for (int t = threadIdx.x; t < vocabulary; t += kArgmaxThreads) {
+      const float c = row[t];
+      if (c > best || (c == best && (selected < 0 || t < selected))) {
+        best = c;
+        selected = t;
+      }
     }
   }
 #pragma unroll
@@ -457,7 +497,7 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const float* __restric
   if (threadIdx.x == 0) {
     float bv = best_v[0];
     int bi = best_i[0];
-    for (int w = 1; w < kWaves; ++w)
+    for (int w = 1; w < kArgmaxThreads / kWave; ++w)
       if (better(best_v[w], best_i[w], bv, bi)) {
         bv = best_v[w];
         bi = best_i[w];
@@ -794,8 +834,8 @@ extern "C" int tmc_argmax_f32(const float* logits, int32_t* tokens, int64_t rows
   TMC_REQUIRE(logits && tokens, "Argmax: null device pointer.");
   TMC_REQUIRE(rows > 0 && rows < (1LL << 31) && vocabulary > 0 && vocabulary < (1LL << 31),
               "Argmax: invalid shape.");
-  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(kThreads), 0, as_stream(stream),
-                     logits, tokens, (int)vocabulary);
+  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(kArgmaxThreads), 0,
+                     as_stream(stream), logits, tokens, (int)vocabulary);
   return check_launch("argmax_kernel");
 }
 

@@ -493,6 +493,29 @@ def test_embedding_and_argmax(tmc, orc, torch):
     assert toks.cpu().numpy()[1] == 100 and toks.cpu().numpy()[2] == 0
 
 
+@pytest.mark.parametrize("rows,vocab", [(16, 32000), (3, 32001), (2, 4099), (1, 5), (2, 40000)])
+def test_argmax_ties_nan_and_tails(tmc, orc, torch, rows, vocab):
+    """Vector (vocab % 4 == 0) and scalar paths, ties across threads and
+    load rounds, NaN entries, an all -inf row, the last element."""
+    logits = normal(603 + vocab, (rows, vocab))
+    logits[0, vocab - 1] = 60.0
+    if rows > 1:
+        logits[1, :] = -np.inf
+        logits[1, vocab // 2] = np.nan
+    if rows > 2:
+        logits[2, 3] = logits[2, vocab - 2] = logits[2, 1024 * 4 + 1] = 70.0  # tie -> 3
+    toks = torch.empty(rows, dtype=torch.int32, device="cuda")
+    tmc.argmax(dev(logits), toks)
+    torch.cuda.synchronize()
+    got = list(toks.cpu().numpy())
+    assert got == list(orc.argmax(logits))
+    assert got[0] == vocab - 1
+    if rows > 1:
+        assert got[1] == 0
+    if rows > 2:
+        assert got[2] == 3
+
+
 def test_fill_normal_statistics(tmc, torch):
     t = torch.empty(1 << 20, dtype=torch.float16, device="cuda")
     tmc.fill_normal(t, 77, 0.0, 0.02)
