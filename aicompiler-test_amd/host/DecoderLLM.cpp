@@ -1,12 +1,14 @@
 // Decoder-LLM decode path on gfx950; see DecoderLLM.hpp.
 #include "DecoderLLM.hpp"
 
+#include "Tuning.hpp"
 #include "tmc_hip.h"
 
 #include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <limits>
+#include <map>
 #include <ostream>
 #include <sstream>
 #include <stdexcept>
@@ -361,6 +363,37 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
     if (!error.empty()) throw std::runtime_error(error);
   }
 
+  // Tuned batch-1 GEMV configurations per shape (on finite scratch inputs and
+  // layer 0's weights; a shape with no admitted candidate keeps its default).
+  std::map<std::string, std::string> tunedSuffix;
+  if (tuneKernels_) {
+    std::ostringstream tuneLog;
+    std::uint64_t seed = 9001;
+    for (const auto& buffer : {normalized_, context_, gated_}) {
+      const auto error = rt.fillNormal(buffer, seed++, 0.0f, 1.0f);
+      if (!error.empty()) throw std::runtime_error(error);
+    }
+    const auto& w0 = model_->layers.front();
+    struct Shape { std::size_t in, out; BufferHandle x, w; ElementType type; };
+    const Shape shapes[] = {{H, QKV, normalized_, w0.queryKeyValueWeight, ElementType::Float16},
+                            {H, H, context_, w0.outputWeight, ElementType::Float16},
+                            {I, H, gated_, w0.downWeight, ElementType::Float16},
+                            {H, V, normalized_, model_->languageModelHeadWeight,
+                             ElementType::Float32}};
+    for (const auto& shape : shapes) {
+      const auto selection = planner::cachedDecodeGEMV(rt, 1, shape.in, shape.out, shape.x,
+                                                       shape.w, tuneLog, shape.type);
+      if (!selection.success) throw std::runtime_error("GEMV tuning: " + selection.errorMessage);
+      if (selection.useBaseline) continue;
+      const auto& c = selection.config;
+      tunedSuffix[std::to_string(shape.in) + "x" + std::to_string(shape.out)] =
+          "&algorithm=" + std::to_string(c.algorithm) + "&rows_per_wave=" +
+          std::to_string(c.rowsPerWave) + "&unroll=" + std::to_string(c.unroll) +
+          "&k_split=" + std::to_string(c.kSplit);
+    }
+    if (log) *log << tuneLog.str();
+  }
+
   const std::string eps = fmt(plan.rmsNormEpsilon);
   for (const std::size_t m : rows) {
     auto bucket = std::make_unique<Bucket>();
@@ -385,9 +418,14 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
     // row-major).
     const bool packed = m > 1;
     auto gemv = [&](std::size_t in, std::size_t out, const char* outType, bool xPacked = true) {
+      std::string tuned;
+      if (!packed) {
+        const auto it = tunedSuffix.find(std::to_string(in) + "x" + std::to_string(out));
+        if (it != tunedSuffix.end()) tuned = it->second;
+      }
       return std::string(packed ? "gemm_packed" : "decode_gemv") + "?batch=" + B +
              "&in=" + std::to_string(in) + "&out=" + std::to_string(out) + "&out_dtype=" + outType +
-             (packed && xPacked ? "&x_layout=packed" : "");
+             (packed && xPacked ? "&x_layout=packed" : "") + tuned;
     };
     auto weights = [&](std::size_t l) -> const DecoderLLMModelLayerBuffers& {
       return packed ? model_->packedLayers[l] : model_->layers[l];
@@ -451,7 +489,7 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
 BatchedDecodeExecutor::Creation createBatchedDecodeExecutor(
     hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
     std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t maximumBatchSize,
-    std::ostream* log) {
+    std::ostream* log, bool tuneKernels) {
   BatchedDecodeExecutor::Creation result;
   try {
     if (!model) throw std::invalid_argument("Batched decode needs model resources.");
@@ -473,6 +511,7 @@ BatchedDecodeExecutor::Creation createBatchedDecodeExecutor(
     executor->pools_ = std::move(pools);
     executor->maximumBatchSize_ = maximumBatchSize;
     executor->pageSize_ = executor->pools_.front()->pageSize();
+    executor->tuneKernels_ = tuneKernels;
     executor->build(log);
     result.executor = std::move(executor);
   } catch (const std::exception& error) {

@@ -200,7 +200,7 @@ class BatchedDecodeExecutor {
   friend Creation createBatchedDecodeExecutor(hip::HipRuntime&,
                                               std::shared_ptr<DecoderLLMModelResources>,
                                               std::vector<std::shared_ptr<KVPagePool>>,
-                                              std::size_t, std::ostream*);
+                                              std::size_t, std::ostream*, bool);
   BatchedDecodeExecutor() = default;
   void build(std::ostream* log);
   [[nodiscard]] std::string upload(const std::vector<std::int32_t>& tokens,
@@ -215,6 +215,7 @@ class BatchedDecodeExecutor {
   std::size_t maximumBatchSize_ = 0;
   std::size_t pageSize_ = 0;
   std::size_t maxPages_ = 0;
+  bool tuneKernels_ = false;
   std::size_t activationBytes_ = 0;
   // Device buffers sized for maximumBatchSize rows.
   hip::BufferHandle meta_;    // int32 [tokens M | lengths M | active 1]
@@ -232,10 +233,13 @@ struct BatchedDecodeExecutor::Creation {
   std::string errorMessage;
 };
 
+// tuneKernels: the batch-1 GEMVs use the decode GEMV tuner's selection for
+// their shapes (tuned once per process on this model's weights and cached;
+// planner::decodeGEMVTuningCache), instead of the default configurations.
 [[nodiscard]] BatchedDecodeExecutor::Creation createBatchedDecodeExecutor(
     hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
     std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t maximumBatchSize,
-    std::ostream* log = nullptr);
+    std::ostream* log = nullptr, bool tuneKernels = false);
 
 struct DecoderLLMCompileOptions {
   std::size_t kvPageSize = 0;  // 0 = contiguous cache (one page of `capacity`)

@@ -396,7 +396,7 @@ ServingExecutionResult runContinuousBatch(hip::HipRuntime& runtime,
       if (!pool.pool) throw std::runtime_error(pool.errorMessage);
       pools.push_back(std::move(pool.pool));
     }
-    auto created = createBatchedDecodeExecutor(runtime, model, pools, M, &log);
+    auto created = createBatchedDecodeExecutor(runtime, model, pools, M, &log, config.tuneKernels);
     if (!created.executor) throw std::runtime_error(created.errorMessage);
     auto& executor = *created.executor;
     BatchedStep step = [&executor](const std::vector<std::int32_t>& tokens,
@@ -419,7 +419,7 @@ DecodeThroughput measureDecodeThroughput(hip::HipRuntime& runtime,
                                          std::shared_ptr<DecoderLLMModelResources> model,
                                          const std::vector<std::vector<std::int32_t>>& prompts,
                                          std::size_t decodeTokens, std::size_t pageSize,
-                                         bool timeGpu) {
+                                         bool timeGpu, bool tuneKernels) {
   DecodeThroughput result;
   try {
     if (!model || prompts.empty() || pageSize == 0)
@@ -443,7 +443,7 @@ DecodeThroughput measureDecodeThroughput(hip::HipRuntime& runtime,
       if (!pool.pool) throw std::runtime_error(pool.errorMessage);
       pools.push_back(std::move(pool.pool));
     }
-    auto created = createBatchedDecodeExecutor(runtime, model, pools, B, nullptr);
+    auto created = createBatchedDecodeExecutor(runtime, model, pools, B, nullptr, tuneKernels);
     if (!created.executor) throw std::runtime_error(created.errorMessage);
     auto& executor = *created.executor;
     std::vector<std::vector<std::unique_ptr<KVCacheState>>> states(B);

@@ -46,6 +46,8 @@ struct ServingConfig {
   bool recordDecodeLogits = false;
   // Keep the logits of the last prompt position.
   bool recordPrefillLogits = true;
+  // Batch-1 GEMVs with the decode GEMV tuner's cached per-shape selection.
+  bool tuneKernels = false;
 };
 
 struct ServingRequestOutput {
@@ -130,6 +132,6 @@ struct DecodeThroughput {
 [[nodiscard]] DecodeThroughput measureDecodeThroughput(
     hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
     const std::vector<std::vector<std::int32_t>>& prompts, std::size_t decodeTokens,
-    std::size_t pageSize, bool timeGpu);
+    std::size_t pageSize, bool timeGpu, bool tuneKernels = false);
 
 }  // namespace tensor::runtime

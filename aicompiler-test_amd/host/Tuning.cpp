@@ -443,6 +443,161 @@ DecodeGEMVSelection tuneDecodeGEMV(hip::HipRuntime& runtime, std::size_t batch,
   return result;
 }
 
+DecodeGEMVSelection tuneDecodeGEMV(hip::HipRuntime& runtime, std::size_t batch,
+                                   std::size_t inputSize, std::size_t outputSize,
+                                   const hip::BufferHandle& input,
+                                   const hip::BufferHandle& weight, std::ostream& log,
+                                   hip::ElementType outputType) {
+  DecodeGEMVSelection result;
+  if (!input || !weight || batch == 0 || inputSize == 0 || outputSize == 0 ||
+      input->elementCount() < batch * inputSize ||
+      weight->elementCount() < outputSize * inputSize ||
+      input->elementType() != hip::ElementType::Float16 ||
+      weight->elementType() != hip::ElementType::Float16) {
+    result.errorMessage = "Decode GEMV tuning buffers do not match the shape (fp16 input, weight).";
+    return result;
+  }
+  const double tolerance = outputType == hip::ElementType::Float32 ? 2e-3 : 2e-2;
+  const std::size_t samples = 9;
+  auto output = runtime.createBuffer(batch * outputSize, nullptr, outputType);
+  if (!output.buffer) {
+    result.errorMessage = output.errorMessage;
+    return result;
+  }
+  auto prepare = [&](const hip::GeneratedKernel& kernel,
+                     std::string& error) -> std::unique_ptr<hip::PreparedExecution> {
+    const auto pipeline = runtime.createComputePipeline(kernel.source, kernel.functionName);
+    if (!pipeline.pipelineCreationPassed) {
+      error = pipeline.errorMessage;
+      return {};
+    }
+    auto prepared = runtime.prepareBuffers({input, weight}, output.buffer,
+                                           {kernel.threadgroupCount, kernel.threadsPerThreadgroup});
+    if (!prepared.execution) error = prepared.errorMessage;
+    return std::move(prepared.execution);
+  };
+  std::string error;
+  auto baseline = prepare(hip::emitLinearBaseline(batch, inputSize, outputSize, "decode_gemv_baseline",
+                                                  hip::ElementType::Float16, outputType),
+                          error);
+  if (!baseline) {
+    result.errorMessage = "Decode GEMV baseline failed: " + error;
+    return result;
+  }
+  const auto baseRun = baseline->run();
+  if (!baseRun.executionPassed) {
+    result.errorMessage = "Decode GEMV baseline failed: " + baseRun.errorMessage;
+    return result;
+  }
+  const std::vector<double> expected(baseRun.output.begin(), baseRun.output.end());
+  for (const double v : expected)
+    if (!std::isfinite(v)) {
+      result.errorMessage = "Decode GEMV tuning input produced non-finite outputs.";
+      return result;
+    }
+  const auto baselineSampler = benchmark::sampler(*baseline);
+  const auto warm = benchmark::warmup(baselineSampler, kTuningWarmup);
+  if (!warm.empty()) {
+    result.errorMessage = "Decode GEMV baseline warmup failed: " + warm;
+    return result;
+  }
+  log << "Decode GEMV shape M=" << batch << ", K=" << inputSize << ", N=" << outputSize
+      << " (device buffers, baseline output as reference, samples=" << samples << ")\n";
+  const auto hardware = runtime.hardwareInfo();
+  double best = 1.0;
+  for (const auto& config : decodeGEMVCandidates(batch)) {
+    log << "  candidate " << configText(config);
+    const auto filter = decodeGEMVHardwareFilter(config, batch, inputSize, outputSize, hardware);
+    if (!filter.empty()) {
+      log << " | Hardware Filter: FAIL (" << filter << ")\n";
+      continue;
+    }
+    auto candidate = prepare(hip::emitDecodeGEMV(batch, inputSize, outputSize, config,
+                                                 "decode_gemv_candidate", hip::ElementType::Float16,
+                                                 outputType),
+                             error);
+    if (!candidate) {
+      log << " | Compile/interface: FAIL: " << error << '\n';
+      continue;
+    }
+    const auto run = candidate->run();
+    const auto check = run.executionPassed
+                           ? validation::compare(run.output, expected, tolerance, tolerance)
+                           : validation::ValidationResult{};
+    if (!check.passed) {
+      log << " | numerical: FAIL: " << (run.executionPassed ? check.errorMessage : run.errorMessage)
+          << '\n';
+      continue;
+    }
+    const auto candidateSampler = benchmark::sampler(*candidate);
+    const auto candidateWarm = benchmark::warmup(candidateSampler, kTuningWarmup);
+    if (!candidateWarm.empty()) {
+      log << " | Warmup: FAIL: " << candidateWarm << '\n';
+      continue;
+    }
+    const auto first = benchmark::measurePair(baselineSampler, candidateSampler, samples);
+    std::optional<benchmark::PairedResult> confirmation;
+    if (first.passed && first.speedup >= kMinimumSpeedup)
+      confirmation = benchmark::measurePair(baselineSampler, candidateSampler, samples);
+    const auto decision = admissionDecision(first, confirmation);
+    if (first.passed) log << " | speedup=" << first.speedup << 'x';
+    if (!decision.admitted) {
+      log << " -> fallback (" << decision.reason << ")\n";
+      continue;
+    }
+    log << ", confirmed " << decision.conservativeSpeedup << "x -> admitted\n";
+    if (decision.conservativeSpeedup > best) {
+      best = decision.conservativeSpeedup;
+      result.useBaseline = false;
+      result.config = config;
+      result.conservativeSpeedup = decision.conservativeSpeedup;
+    }
+  }
+  result.success = true;
+  if (result.useBaseline) result.config = hip::DecodeGEMVConfig{4, 1, 1, 1};
+  log << "Decode GEMV selected: " << configText(result.config)
+      << ", conservative speedup=" << result.conservativeSpeedup << "x\n";
+  return result;
+}
+
+std::string DecodeGEMVTuningCache::key(std::size_t batch, std::size_t inputSize,
+                                       std::size_t outputSize, hip::ElementType outputType) {
+  return "decode_gemv:b" + std::to_string(batch) + ":k" + std::to_string(inputSize) + ":n" +
+         std::to_string(outputSize) + ":" + hip::elementTypeName(outputType);
+}
+
+std::optional<DecodeGEMVSelection> DecodeGEMVTuningCache::find(const std::string& key) const {
+  const auto it = entries_.find(key);
+  if (it == entries_.end()) return std::nullopt;
+  return it->second;
+}
+
+void DecodeGEMVTuningCache::store(const std::string& key, const DecodeGEMVSelection& selection) {
+  entries_[key] = selection;
+}
+
+DecodeGEMVTuningCache& decodeGEMVTuningCache() {
+  static DecodeGEMVTuningCache cache;
+  return cache;
+}
+
+DecodeGEMVSelection cachedDecodeGEMV(hip::HipRuntime& runtime, std::size_t batch,
+                                     std::size_t inputSize, std::size_t outputSize,
+                                     const hip::BufferHandle& input,
+                                     const hip::BufferHandle& weight, std::ostream& log,
+                                     hip::ElementType outputType) {
+  auto& cache = decodeGEMVTuningCache();
+  const auto key = DecodeGEMVTuningCache::key(batch, inputSize, outputSize, outputType);
+  if (const auto hit = cache.find(key)) {
+    log << "Decode GEMV " << key << ": cached " << configText(hit->config) << '\n';
+    return *hit;
+  }
+  auto selection = tuneDecodeGEMV(runtime, batch, inputSize, outputSize, input, weight, log,
+                                  outputType);
+  if (selection.success) cache.store(key, selection);
+  return selection;
+}
+
 std::vector<std::size_t> defaultRMSNormCandidates() { return {64, 128, 256, 512, 1024}; }
 
 std::string rmsNormHardwareFilter(const RMSNormOp& op, std::size_t threads,

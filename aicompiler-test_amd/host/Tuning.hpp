@@ -165,6 +165,46 @@ struct DecodeGEMVSelection {
                                                  DType storageDtype = DType::Float16,
                                                  bool prefill = false);
 
+// tuneDecodeGEMV over device buffers already resident (fp16 input
+// [batch, in] and weight [out, in], finite values): no host copies of the
+// weights; the linear baseline's output on the same buffers is the reference
+// (the reference tuner's large-shape path, DecodeGEMVTuner.cpp:197-203).
+[[nodiscard]] DecodeGEMVSelection tuneDecodeGEMV(hip::HipRuntime& runtime, std::size_t batch,
+                                                 std::size_t inputSize, std::size_t outputSize,
+                                                 const hip::BufferHandle& input,
+                                                 const hip::BufferHandle& weight,
+                                                 std::ostream& log,
+                                                 hip::ElementType outputType =
+                                                     hip::ElementType::Float16);
+
+// Per-shape decode GEMV selections shared by every executor of the process.
+// The reference tunes again for every compiled request (ServingRuntime.cpp
+// :582-617); a shape is tuned once here.
+class DecodeGEMVTuningCache {
+ public:
+  [[nodiscard]] static std::string key(std::size_t batch, std::size_t inputSize,
+                                       std::size_t outputSize, hip::ElementType outputType);
+  [[nodiscard]] std::optional<DecodeGEMVSelection> find(const std::string& key) const;
+  void store(const std::string& key, const DecodeGEMVSelection& selection);
+  [[nodiscard]] std::size_t size() const { return entries_.size(); }
+  void clear() { entries_.clear(); }
+
+ private:
+  std::map<std::string, DecodeGEMVSelection> entries_;
+};
+
+[[nodiscard]] DecodeGEMVTuningCache& decodeGEMVTuningCache();
+
+// The cached selection for the shape, tuning it on `input` / `weight` first
+// when the cache has none.
+[[nodiscard]] DecodeGEMVSelection cachedDecodeGEMV(hip::HipRuntime& runtime, std::size_t batch,
+                                                   std::size_t inputSize, std::size_t outputSize,
+                                                   const hip::BufferHandle& input,
+                                                   const hip::BufferHandle& weight,
+                                                   std::ostream& log,
+                                                   hip::ElementType outputType =
+                                                       hip::ElementType::Float16);
+
 // CandidateReport / TuningResult (RMSNormTuner.hpp:12-38).
 struct CandidateReport {
   std::string name;

@@ -334,12 +334,17 @@ PYBIND11_MODULE(_tmc_host, m) {
 
   m.def("create_batched_decode_executor",
         [](hip::HipRuntime& rt, std::shared_ptr<DecoderLLMModelResources> model,
-           std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t maxBatch) {
+           std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t maxBatch, bool tune) {
           std::ostringstream log;
-          auto r = createBatchedDecodeExecutor(rt, std::move(model), std::move(pools), maxBatch, &log);
-          if (!r.executor) throw std::runtime_error(r.errorMessage);
+          auto r = createBatchedDecodeExecutor(rt, std::move(model), std::move(pools), maxBatch,
+                                               &log, tune);
+          if (!r.executor) throw std::runtime_error(r.errorMessage + "\n" + log.str());
           return std::move(r.executor);
-        });
+        },
+        py::arg("runtime"), py::arg("model"), py::arg("pools"), py::arg("maximum_batch_size"),
+        py::arg("tune_kernels") = false);
+  m.def("decode_gemv_cache_size", []() { return planner::decodeGEMVTuningCache().size(); });
+  m.def("clear_decode_gemv_cache", []() { planner::decodeGEMVTuningCache().clear(); });
 
   py::class_<DecoderLLMCompileOptions>(m, "DecoderLLMCompileOptions")
       .def(py::init<>())
@@ -407,7 +412,8 @@ PYBIND11_MODULE(_tmc_host, m) {
       .def_readwrite("physical_pages_per_layer", &ServingConfig::physicalPagesPerLayer)
       .def_readwrite("maximum_batch_size", &ServingConfig::maximumBatchSize)
       .def_readwrite("record_decode_logits", &ServingConfig::recordDecodeLogits)
-      .def_readwrite("record_prefill_logits", &ServingConfig::recordPrefillLogits);
+      .def_readwrite("record_prefill_logits", &ServingConfig::recordPrefillLogits)
+      .def_readwrite("tune_kernels", &ServingConfig::tuneKernels);
 
   m.def("run_continuous_batch",
         [](hip::HipRuntime& rt, std::shared_ptr<DecoderLLMModelResources> model,
@@ -426,11 +432,12 @@ PYBIND11_MODULE(_tmc_host, m) {
   m.def("measure_decode_throughput",
         [](hip::HipRuntime& rt, std::shared_ptr<DecoderLLMModelResources> model,
            const std::vector<std::vector<std::int32_t>>& prompts, std::size_t decodeTokens,
-           std::size_t pageSize, bool timeGpu) {
+           std::size_t pageSize, bool timeGpu, bool tune) {
           DecodeThroughput r;
           {
             py::gil_scoped_release release;
-            r = measureDecodeThroughput(rt, std::move(model), prompts, decodeTokens, pageSize, timeGpu);
+            r = measureDecodeThroughput(rt, std::move(model), prompts, decodeTokens, pageSize,
+                                        timeGpu, tune);
           }
           py::dict d;
           d["passed"] = r.passed;
@@ -447,7 +454,7 @@ PYBIND11_MODULE(_tmc_host, m) {
           return d;
         },
         py::arg("runtime"), py::arg("model"), py::arg("prompts"), py::arg("decode_tokens"),
-        py::arg("page_size") = 16, py::arg("time_gpu") = false);
+        py::arg("page_size") = 16, py::arg("time_gpu") = false, py::arg("tune_kernels") = false);
 
   // The scheduler over host-only pools and a Python step (CPU tests):
   // step(tokens, valid_lengths, tables, read_logits) -> (next_tokens, logits).

@@ -344,3 +344,39 @@ def test_serving_matches_single_request_decoding(host, orc, rt):
                 _check_token(int(gen[i + 1]), int(step["next_token_ids"][0]), step["logits"],
                              f"{spec.id} step {i}")
                 break
+
+
+def test_tuned_executor_matches_default_and_caches_shapes(host, orc, rt):
+    """Batch-1 GEMVs with the decode GEMV tuner's per-shape selections: the
+    shapes are tuned once (process cache), and the step's logits match the
+    default-configuration executor within the fp16-path tolerance."""
+    cfg = CONFIGS["gqa4_d128"]
+    m = _weights(orc, cfg, 61)
+    w = _workload(host, orc, cfg, m)
+    model = host.create_model_resources(rt, w)
+    host.clear_decode_gemv_cache()
+    runs = []
+    for tune in (False, True, True):
+        pools = [host.create_kv_page_pool(rt, w.plan.kv_plan(), P, 16)
+                 for _ in range(cfg["layers"])]
+        ex = host.create_batched_decode_executor(rt, model, pools, 1, tune_kernels=tune)
+        states = [host.create_kv_cache_state(rt, w.plan.kv_plan(), pools[l], False)
+                  for l in range(cfg["layers"])]
+        logits = None
+        for i, tok in enumerate([3, 14, 15, 92, 65]):
+            for s in states:
+                assert s.stage_length(rt, i + 1) == ""
+                s.commit_length(i + 1)
+            tables = [s.page_table() + [-1] * (ex.max_pages() - len(s.page_table())) for s in states]
+            out = ex.run([tok], [i + 1], tables, True, False)
+            assert out["passed"], out["error"]
+            logits = np.asarray(out["logits"])
+        runs.append(logits)
+        # q.k.v, o, down and the LM head shapes (distinct ones) are cached
+        # after the first tuned build
+        H, I, V = cfg["hidden"], cfg["intermediate"], cfg["vocabulary"]
+        qkv = H + 2 * cfg["kv_heads"] * cfg["head_dim"]
+        shapes = {(H, qkv, "f16"), (H, H, "f16"), (I, H, "f16"), (H, V, "f32")}
+        assert host.decode_gemv_cache_size() == (0 if not tune else len(shapes))
+    assert_f16_path(runs[1], runs[0], "tuned vs default")
+    np.testing.assert_array_equal(runs[2], runs[1])  # the cached selection is the same
