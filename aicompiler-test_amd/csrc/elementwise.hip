@@ -848,6 +848,53 @@ extern "C" int tmc_fill_normal(void* ptr, int dtype, int64_t count, uint64_t see
   return check_launch("fill_normal_kernel");
 }
 
+namespace tmc {
+namespace {
+
+// blockIdx.y = page index i; threads copy 16-byte units of one page.
+__global__ __launch_bounds__(256) void copy_pages_kernel(const uint4* __restrict__ src,
+                                                         uint4* __restrict__ dst,
+                                                         const int32_t* __restrict__ pages,
+                                                         size_t units, int scatter) {
+  const size_t i = blockIdx.y;
+  const size_t page = (size_t)pages[i];
+  const size_t from = scatter ? i : page, to = scatter ? page : i;
+  for (size_t u = (size_t)blockIdx.x * 256 + threadIdx.x; u < units; u += (size_t)gridDim.x * 256)
+    dst[to * units + u] = src[from * units + u];
+}
+
+}  // namespace
+}  // namespace tmc
+
+extern "C" int tmc_host_alloc(size_t bytes, void** out) {
+  TMC_REQUIRE(out && bytes > 0, "Host alloc: invalid arguments.");
+  *out = nullptr;
+  // Mapped: kernels read and write it directly (ROCm gives it the same
+  // address on the device).
+  const hipError_t rc = hipHostMalloc(out, bytes, hipHostMallocMapped);
+  TMC_REQUIRE(rc == hipSuccess, std::string("Host alloc: hipHostMalloc failed: ") +
+                                    hipGetErrorString(rc));
+  return 0;
+}
+
+extern "C" void tmc_host_free(void* ptr) {
+  if (ptr) (void)hipHostFree(ptr);
+}
+
+extern "C" int tmc_copy_pages(const void* src, void* dst, const int32_t* pages, int64_t count,
+                              int64_t page_bytes, int scatter, void* stream) {
+  TMC_REQUIRE(src && dst && pages, "Copy pages: null pointer.");
+  TMC_REQUIRE(count > 0 && count < 65536 && page_bytes > 0 && page_bytes % 16 == 0,
+              "Copy pages: count must be in [1, 65535] and page_bytes a multiple of 16.");
+  TMC_REQUIRE(aligned16(src) && aligned16(dst), "Copy pages: buffers must be 16-byte aligned.");
+  const size_t units = (size_t)page_bytes / 16;
+  const dim3 grid((unsigned)std::min<size_t>((units + 255) / 256, 64), (unsigned)count);
+  hipLaunchKernelGGL(copy_pages_kernel, grid, dim3(256), 0, as_stream(stream),
+                     static_cast<const uint4*>(src), static_cast<uint4*>(dst), pages, units,
+                     scatter);
+  return check_launch("copy_pages_kernel");
+}
+
 extern "C" int tmc_copy_bytes(const void* src, void* dst, size_t bytes, void* stream) {
   TMC_REQUIRE(src && dst && bytes > 0 && bytes % 16 == 0 && aligned16(src) && aligned16(dst),
               "Copy: pointers must be 16-byte aligned and size a multiple of 16.");

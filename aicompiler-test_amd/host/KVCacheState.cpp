@@ -1,6 +1,8 @@
 // KVPagePool / KVCacheState on HipRuntime; see KVCacheState.hpp.
 #include "KVCacheState.hpp"
 
+#include "tmc_hip.h"
+
 #include <algorithm>
 #include <cstring>
 #include <limits>
@@ -290,6 +292,65 @@ std::string KVCacheState::restore(hip::HipRuntime& runtime, std::size_t length,
     return error;
   }
   commitLength(length);
+  return {};
+}
+
+namespace {
+constexpr std::size_t kSpillHeader = 256;  // bytes reserved ahead of the pages
+}
+
+std::string KVCacheState::spillPages(hip::HipRuntime& runtime, KVPageSpill& out) const {
+  if (!isPaged() || !key_ || !value_) return "KV page spill requires paged device storage.";
+  out = KVPageSpill{};
+  out.length = currentLength_;
+  out.pages = (currentLength_ + pageSize_ - 1) / pageSize_;
+  out.pageBytes = plan_.batch * plan_.heads * pageSize_ * plan_.headDimension *
+                  hip::elementBytes(key_->elementType());
+  if (out.pages == 0) return {};
+  const std::size_t header =
+      (out.pages * sizeof(std::int32_t) + kSpillHeader - 1) / kSpillHeader * kSpillHeader;
+  void* raw = nullptr;
+  if (tmc_host_alloc(header + out.bytes(), &raw) != 0) return tmc_last_error();
+  out.host = std::shared_ptr<void>(raw, [](void* p) { tmc_host_free(p); });
+  auto* ids = static_cast<std::int32_t*>(raw);
+  for (std::size_t i = 0; i < out.pages; ++i) ids[i] = logicalToPhysical_.at(i);
+  auto* pagesBase = static_cast<unsigned char*>(raw) + header;
+  const auto count = static_cast<std::int64_t>(out.pages);
+  const auto bytes = static_cast<std::int64_t>(out.pageBytes);
+  if (tmc_copy_pages(key_->devicePointer(), pagesBase, ids, count, bytes, 0, runtime.stream()) != 0 ||
+      tmc_copy_pages(value_->devicePointer(), pagesBase + out.pages * out.pageBytes, ids, count,
+                     bytes, 0, runtime.stream()) != 0)
+    return tmc_last_error();
+  return runtime.synchronize();
+}
+
+std::string KVCacheState::restorePages(hip::HipRuntime& runtime, const KVPageSpill& spill) {
+  if (!isPaged() || !key_ || !value_) return "KV page restore requires paged device storage.";
+  if (currentLength_ != 0) return "KV page restore requires an empty request state.";
+  const std::size_t pageBytes = plan_.batch * plan_.heads * pageSize_ * plan_.headDimension *
+                                hip::elementBytes(key_->elementType());
+  if (!spill.host || spill.length == 0 || spill.length > plan_.capacity ||
+      spill.pages != (spill.length + pageSize_ - 1) / pageSize_ || spill.pageBytes != pageBytes)
+    return "KV page restore: the spill does not match this state.";
+  auto error = stageLength(runtime, spill.length);
+  if (!error.empty()) return error;
+  const std::size_t header =
+      (spill.pages * sizeof(std::int32_t) + kSpillHeader - 1) / kSpillHeader * kSpillHeader;
+  auto* ids = static_cast<std::int32_t*>(spill.host.get());
+  for (std::size_t i = 0; i < spill.pages; ++i) ids[i] = logicalToPhysical_.at(i);
+  const auto* pagesBase = static_cast<const unsigned char*>(spill.host.get()) + header;
+  const auto count = static_cast<std::int64_t>(spill.pages);
+  const auto bytes = static_cast<std::int64_t>(pageBytes);
+  if (tmc_copy_pages(pagesBase, key_->devicePointer(), ids, count, bytes, 1, runtime.stream()) != 0 ||
+      tmc_copy_pages(pagesBase + spill.pages * pageBytes, value_->devicePointer(), ids, count, bytes,
+                     1, runtime.stream()) != 0)
+    error = tmc_last_error();
+  if (error.empty()) error = runtime.synchronize();
+  if (!error.empty()) {
+    (void)rollbackLength(runtime, 0);
+    return error;
+  }
+  commitLength(spill.length);
   return {};
 }
 

@@ -146,6 +146,17 @@ class KVPagePool {
                                                       std::shared_ptr<KVPagePool> pagePool,
                                                       bool deviceMirror = true);
 
+// The pages of one request state copied, as stored, into pinned host memory
+// (a preempted request's spill).  Layout of `host`: the page ids (int32,
+// 256-byte aligned area), then the K pages, then the V pages.
+struct KVPageSpill {
+  std::size_t length = 0;
+  std::size_t pages = 0;
+  std::size_t pageBytes = 0;
+  std::shared_ptr<void> host;  // tmc_host_alloc'ed, freed with the last owner
+  [[nodiscard]] std::size_t bytes() const noexcept { return 2 * pages * pageBytes; }
+};
+
 class KVCacheState {
  public:
   ~KVCacheState();
@@ -165,6 +176,13 @@ class KVCacheState {
                                     const std::vector<float>& keyPrefix,
                                     const std::vector<float>& valuePrefix);
   void commitLength(std::size_t length);
+
+  // Paged device storage only: copy this state's pages (K and V, raw bits)
+  // into pinned host memory, one page-copy launch each, and wait.  The caller
+  // then releases the pages; restorePages() brings them back into freshly
+  // allocated pages of an empty state, bit for bit.
+  [[nodiscard]] std::string spillPages(hip::HipRuntime& runtime, KVPageSpill& out) const;
+  [[nodiscard]] std::string restorePages(hip::HipRuntime& runtime, const KVPageSpill& spill);
 
   // [batch][heads][currentLength][head_dim] read back from the device.
   [[nodiscard]] std::vector<float> readKeyPrefix() const;

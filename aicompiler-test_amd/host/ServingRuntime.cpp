@@ -25,8 +25,11 @@ std::size_t pagesFor(std::size_t tokens, std::size_t pageSize) {
 
 enum class RequestState { Waiting, Active, Preempted, Finished };
 
+// A preempted request's KV state: raw pages in pinned host memory per layer
+// for device pools, float prefixes for the host-only pools of the CPU tests.
 struct Snapshot {
   std::size_t length = 0;
+  std::vector<KVPageSpill> spills;
   std::vector<std::vector<float>> keys, values;
 };
 
@@ -178,8 +181,11 @@ ServingExecutionResult runContinuousBatch(hip::HipRuntime& runtime,
         if (!fits) continue;
         const auto restoreStart = Clock::now();
         for (std::size_t l = 0; l < r.states.size(); ++l) {
-          const auto error = r.states[l]->restore(runtime, r.snapshot->length, r.snapshot->keys[l],
-                                                  r.snapshot->values[l]);
+          const auto error =
+              l < r.snapshot->spills.size()
+                  ? r.states[l]->restorePages(runtime, r.snapshot->spills[l])
+                  : r.states[l]->restore(runtime, r.snapshot->length, r.snapshot->keys[l],
+                                         r.snapshot->values[l]);
           if (!error.empty())
             throw std::runtime_error("Request " + r.spec.id + " resume failed: " + error);
         }
@@ -233,8 +239,17 @@ ServingExecutionResult runContinuousBatch(hip::HipRuntime& runtime,
           Snapshot snap;
           snap.length = v.length();
           for (const auto& state : v.states) {
-            snap.keys.push_back(state->readKeyPrefix());
-            snap.values.push_back(state->readValuePrefix());
+            if (state->keyBuffer()) {
+              KVPageSpill spill;
+              const auto error = state->spillPages(runtime, spill);
+              if (!error.empty())
+                throw std::runtime_error("Request " + v.spec.id + " spill failed: " + error);
+              metrics.spilledBytes += spill.bytes();
+              snap.spills.push_back(std::move(spill));
+            } else {
+              snap.keys.push_back(state->readKeyPrefix());
+              snap.values.push_back(state->readValuePrefix());
+            }
           }
           const auto error = releaseAll(runtime, v);
           if (!error.empty())

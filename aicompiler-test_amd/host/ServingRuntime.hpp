@@ -7,7 +7,8 @@
 //    pools hold pages for their snapshot;
 //  * before every batched step the pages the active rows need for their next
 //    token are counted; while they are missing, the active request owning the
-//    most pages is preempted (KV snapshot to host memory, pages released);
+//    most pages is preempted (its KV pages copied raw into pinned host memory,
+//    pages released);
 //  * after every step page isolation between active requests is audited and
 //    finished requests release their pages; at the end every pool must be
 //    empty with equal allocation/release counts across layers.
@@ -70,6 +71,7 @@ struct ServingMetrics {
   double averageActiveBatchSize = 0.0;
   std::size_t maximumActiveBatchSize = 0;
   std::size_t preemptionCount = 0;
+  std::size_t spilledBytes = 0;           // KV pages copied to pinned host memory
   std::size_t resumeCount = 0;
   std::size_t peakPagesPerLayer = 0;
   std::size_t pageAllocationCount = 0;

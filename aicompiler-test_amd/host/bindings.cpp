@@ -102,6 +102,7 @@ py::dict servingToDict(const ServingExecutionResult& r) {
   metrics["average_active_batch_size"] = m.averageActiveBatchSize;
   metrics["maximum_active_batch_size"] = m.maximumActiveBatchSize;
   metrics["preemption_count"] = m.preemptionCount;
+  metrics["spilled_bytes"] = m.spilledBytes;
   metrics["resume_count"] = m.resumeCount;
   metrics["peak_pages_per_layer"] = m.peakPagesPerLayer;
   metrics["page_allocation_count"] = m.pageAllocationCount;
@@ -208,7 +209,21 @@ PYBIND11_MODULE(_tmc_host, m) {
           return r.pool;
         });
 
+  py::class_<KVPageSpill>(m, "KVPageSpill")
+      .def_readonly("length", &KVPageSpill::length)
+      .def_readonly("pages", &KVPageSpill::pages)
+      .def_readonly("page_bytes", &KVPageSpill::pageBytes)
+      .def("bytes", &KVPageSpill::bytes);
+
   py::class_<KVCacheState>(m, "KVCacheState")
+      .def("spill_pages",
+           [](const KVCacheState& s, hip::HipRuntime& rt) {
+             KVPageSpill spill;
+             const auto error = s.spillPages(rt, spill);
+             if (!error.empty()) throw std::runtime_error(error);
+             return spill;
+           })
+      .def("restore_pages", &KVCacheState::restorePages)
       .def("current_length", &KVCacheState::currentLength)
       .def("capacity", &KVCacheState::capacity)
       .def("reset", &KVCacheState::reset)

@@ -406,6 +406,21 @@ int tmc_fill_normal(void *ptr, int dtype, int64_t count, uint64_t seed, float me
 /* Plain device copy kernel (bandwidth probe used to calibrate counters). */
 int tmc_copy_bytes(const void *src, void *dst, size_t bytes, void *stream);
 
+/* Pinned host memory (hipHostMalloc), readable and writable by kernels:
+ * the spill space of preempted requests' KV pages.  No reference counterpart
+ * (the reference snapshots float vectors, ServingRuntime.cpp:426-930). */
+int tmc_host_alloc(size_t bytes, void **out);
+void tmc_host_free(void *ptr);
+
+/* Page-granular copies between a KV pool and a contiguous buffer (device or
+ * pinned host): scatter == 0 gathers dst[i] = src page pages[i]; scatter != 0
+ * writes dst page pages[i] = src[i]; i < count, each page page_bytes bytes
+ * (a multiple of 16).  `pages` must be readable by the device (device or
+ * pinned host memory) and hold ids below the pool's page count; bits are
+ * copied unchanged. */
+int tmc_copy_pages(const void *src, void *dst, const int32_t *pages, int64_t count,
+                   int64_t page_bytes, int scatter, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -323,6 +323,9 @@ def test_serving_matches_single_request_decoding(host, orc, rt):
     metrics = result["metrics"]
     assert metrics["decoded_tokens"] == sum(s.decode_token_count for s in specs)
     assert metrics["maximum_active_batch_size"] > 1
+    # page pressure preempts: the KV pages spill raw to pinned host memory
+    assert metrics["preemption_count"] > 0 and metrics["spilled_bytes"] > 0
+    assert metrics["resume_count"] == metrics["preemption_count"]
     print("serving metrics:", {k: v for k, v in metrics.items() if not isinstance(v, dict)})
     opts = host.DecoderLLMCompileOptions()
     opts.kv_page_size = P
