@@ -68,6 +68,12 @@ def _declare(l):
         "tmc_serving_kv_append": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, vp]),
         "tmc_decode_rope_append": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64,
                                          i64, i64, i64, i64, vp]),
+        "tmc_prefill_rope_append": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64,
+                                          i64, i64, i64, i64, vp]),
+        "tmc_gemm_rows_workspace_bytes": (sz, []),
+        "tmc_gemm_rows_f16": (i32, [vp, vp, vp, i32, i64, i64, i64, vp, sz, vp]),
+        "tmc_prefill_attention_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64,
+                                            i64, i64, i64, i64, vp]),
         "tmc_attention_workspace_bytes": (sz, [i64, i64, i64, i64, i64]),
         "tmc_decode_attention": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, vp, sz,
                                        vp]),
@@ -417,6 +423,41 @@ def decode_rope_append(qkv, cos, sin, valid_lengths, tables, active, q_out, k_po
                                        kv_heads, head_dim, capacity, page_size, max_pages,
                                        _stream(stream)),
           "tmc_decode_rope_append")
+
+
+def prefill_rope_append(qkv, cos, sin, valid_lengths, table, active, q_out, k_pool, v_pool, rows,
+                        q_heads, kv_heads, head_dim, capacity, page_size, max_pages, stream=None):
+    check(lib().tmc_prefill_rope_append(_ptr(qkv), _ptr(cos), _ptr(sin), _ptr(valid_lengths),
+                                        _ptr(table), _ptr(active), _ptr(q_out), _ptr(k_pool),
+                                        _ptr(v_pool), _dtype_code(qkv), rows, q_heads, kv_heads,
+                                        head_dim, capacity, page_size, max_pages, _stream(stream)),
+          "tmc_prefill_rope_append")
+
+
+def gemm_rows_workspace_bytes() -> int:
+    return int(lib().tmc_gemm_rows_workspace_bytes())
+
+
+def gemm_rows(x, w, y, workspace=None, stream=None):
+    """y[m, n] = x[m, k] w[n, k]^T on hipBLASLt (fp16 in, fp32 accumulation)."""
+    m, k = x.shape
+    n = w.shape[0]
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib().tmc_gemm_rows_f16(_ptr(x), _ptr(w), _ptr(y), _dtype_code(y), m, k, n,
+                                  _ptr(workspace), ws_bytes, _stream(stream)), "tmc_gemm_rows_f16")
+
+
+def prefill_attention(q, k_pool, v_pool, valid_lengths, table, active, out, rows, q_heads,
+                      kv_heads, head_dim, page_size, max_pages, page_stride, head_stride,
+                      stream=None, pool_pages=None):
+    """Causal chunk attention over one request's pages; pool_pages defaults
+    to the pages the k_pool tensor holds."""
+    if pool_pages is None:
+        pool_pages = min(k_pool.numel(), v_pool.numel()) // page_stride
+    check(lib().tmc_prefill_attention_f16(
+        _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(valid_lengths), _ptr(table), _ptr(active),
+        _ptr(out), rows, q_heads, kv_heads, head_dim, page_size, max_pages, pool_pages,
+        page_stride, head_stride, _stream(stream)), "tmc_prefill_attention_f16")
 
 
 def attention_workspace_bytes(batch, q_heads, kv_heads, head_dim, capacity) -> int:

@@ -373,7 +373,8 @@ __global__ __launch_bounds__(kThreads) void serving_append_kernel(
 // thread moves one interleaved pair.  The rotated query goes to q_out
 // [max_batch, q_heads * head_dim]; the rotated key and the value are stored
 // at position valid_lengths[b] - 1 of the pools [page][kv_heads][page_size]
-// [head_dim] through block_tables[b * max_pages + position / page_size].
+// [head_dim] through block_tables[b * table_stride + position / page_size]
+// (table_stride = max_pages, or 0 when every row is a token of one request).
 // Rows at or beyond active_count[0], rows whose length is outside
 // [1, capacity] and positions whose page entry is negative are skipped.
 template <typename T>
@@ -382,7 +383,7 @@ __global__ __launch_bounds__(kThreads) void decode_rope_append_kernel(
     const int32_t* __restrict__ valid_lengths, const int32_t* __restrict__ block_tables,
     const int32_t* __restrict__ active_count, T* __restrict__ q_out, T* __restrict__ k_pool,
     T* __restrict__ v_pool, int max_batch, int q_heads, int kv_heads, int head_dim, int capacity,
-    int page_size, int max_pages) {
+    int page_size, int table_stride) {
   const int pairs = head_dim / 2;
   const int row_pairs = (q_heads + 2 * kv_heads) * pairs;
   const long gid = (long)blockIdx.x * kThreads + threadIdx.x;
@@ -411,7 +412,7 @@ __global__ __launch_bounds__(kThreads) void decode_rope_append_kernel(
       dst[1] = from_float<T>(ro);
       return;
     }
-    const int page = block_tables[(size_t)request * max_pages + position / page_size];
+    const int page = block_tables[(size_t)request * table_stride + position / page_size];
     if (page < 0) return;
     const int feature = column - q_width;
     T* dst = k_pool + (((size_t)page * kv_heads + feature / head_dim) * page_size +
@@ -420,7 +421,7 @@ __global__ __launch_bounds__(kThreads) void decode_rope_append_kernel(
     dst[1] = from_float<T>(ro);
     return;
   }
-  const int page = block_tables[(size_t)request * max_pages + position / page_size];
+  const int page = block_tables[(size_t)request * table_stride + position / page_size];
   if (page < 0) return;
   const int feature = column - q_width - kv_width;
   T* dst = v_pool + (((size_t)page * kv_heads + feature / head_dim) * page_size +
@@ -799,24 +800,24 @@ extern "C" int tmc_serving_kv_append(const void* input, const int32_t* valid_len
   return check_launch("serving_append_kernel");
 }
 
-extern "C" int tmc_decode_rope_append(const void* qkv, const float* cosine, const float* sine,
-                                      const int32_t* valid_lengths, const int32_t* block_tables,
-                                      const int32_t* active_count, void* q_out, void* key_pool,
-                                      void* value_pool, int dtype, int64_t max_batch,
-                                      int64_t q_heads, int64_t kv_heads, int64_t head_dim,
-                                      int64_t capacity, int64_t page_size, int64_t max_pages,
-                                      void* stream) {
+namespace {
+int launch_rope_append(const void* qkv, const float* cosine, const float* sine,
+                       const int32_t* valid_lengths, const int32_t* block_tables,
+                       const int32_t* active_count, void* q_out, void* key_pool, void* value_pool,
+                       int dtype, int64_t max_batch, int64_t q_heads, int64_t kv_heads,
+                       int64_t head_dim, int64_t capacity, int64_t page_size, int64_t max_pages,
+                       bool shared_table, void* stream) {
   TMC_REQUIRE(qkv && cosine && sine && valid_lengths && block_tables && active_count && q_out &&
                   key_pool && value_pool,
-              "Decode RoPE+append: null device pointer.");
+              "RoPE+append: null device pointer.");
   TMC_REQUIRE(float_dtype(dtype) && max_batch > 0 && max_batch < 65536 && q_heads > 0 &&
                   kv_heads > 0 && q_heads % kv_heads == 0 && head_dim > 0 && head_dim % 2 == 0 &&
                   head_dim <= 1024 && capacity > 0 && page_size > 0 && page_size <= capacity &&
                   max_pages == (capacity + page_size - 1) / page_size,
-              "Decode RoPE+append: invalid dtype or shape (max_pages must be "
+              "RoPE+append: invalid dtype or shape (max_pages must be "
               "ceil(capacity / page_size)).");
   const size_t items = (size_t)max_batch * (q_heads + 2 * kv_heads) * (head_dim / 2);
-  TMC_REQUIRE(items < (1ull << 31), "Decode RoPE+append: too many elements.");
+  TMC_REQUIRE(items < (1ull << 31), "RoPE+append: too many elements.");
   TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((decode_rope_append_kernel<T>),
                                             dim3((unsigned)((items + kThreads - 1) / kThreads)),
                                             dim3(kThreads), 0, as_stream(stream),
@@ -825,8 +826,33 @@ extern "C" int tmc_decode_rope_append(const void* qkv, const float* cosine, cons
                                             static_cast<T*>(q_out), static_cast<T*>(key_pool),
                                             static_cast<T*>(value_pool), (int)max_batch,
                                             (int)q_heads, (int)kv_heads, (int)head_dim,
-                                            (int)capacity, (int)page_size, (int)max_pages));
+                                            (int)capacity, (int)page_size,
+                                            shared_table ? 0 : (int)max_pages));
   return check_launch("decode_rope_append_kernel");
+}
+}  // namespace
+
+extern "C" int tmc_decode_rope_append(const void* qkv, const float* cosine, const float* sine,
+                                      const int32_t* valid_lengths, const int32_t* block_tables,
+                                      const int32_t* active_count, void* q_out, void* key_pool,
+                                      void* value_pool, int dtype, int64_t max_batch,
+                                      int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                      int64_t capacity, int64_t page_size, int64_t max_pages,
+                                      void* stream) {
+  return launch_rope_append(qkv, cosine, sine, valid_lengths, block_tables, active_count, q_out,
+                            key_pool, value_pool, dtype, max_batch, q_heads, kv_heads, head_dim,
+                            capacity, page_size, max_pages, false, stream);
+}
+
+extern "C" int tmc_prefill_rope_append(const void* qkv, const float* cosine, const float* sine,
+                                       const int32_t* valid_lengths, const int32_t* block_table,
+                                       const int32_t* active_count, void* q_out, void* key_pool,
+                                       void* value_pool, int dtype, int64_t rows, int64_t q_heads,
+                                       int64_t kv_heads, int64_t head_dim, int64_t capacity,
+                                       int64_t page_size, int64_t max_pages, void* stream) {
+  return launch_rope_append(qkv, cosine, sine, valid_lengths, block_table, active_count, q_out,
+                            key_pool, value_pool, dtype, rows, q_heads, kv_heads, head_dim,
+                            capacity, page_size, max_pages, true, stream);
 }
 
 extern "C" int tmc_argmax_f32(const float* logits, int32_t* tokens, int64_t rows,

@@ -1,0 +1,478 @@
+// Chunked prefill for gfx950: the prompt GEMMs and causal paged attention
+// over a chunk of one request's tokens.
+//
+// Reference: prefillChunked (DecoderLLMExecutor.cpp:982-1034) runs a stage
+// whose linear layers are emitTiledGEMM (DecodeGEMVMetalEmitter.cpp:134-169,
+// Y[m, n] = X[m, k] W[n, k]^T with fp32 accumulation) and whose attention is
+// emitPagedKVAttention with causalPrefill (KVCacheMetalEmitter.cpp:210-310):
+// query token q of a chunk of S tokens attends positions [0, valid - S + q + 1).
+//
+//  * tmc_gemm_rows_f16: the prompt projections are plain GEMMs with M = chunk
+//    tokens, so they go to hipBLASLt.  Per (device, shape, output type,
+//    workspace) the first call that is not under stream capture times the
+//    library's heuristic candidates on the caller's buffers and keeps the
+//    fastest; captured calls use the first candidate.
+//  * prefill_attention_kernel: one 256-thread workgroup per (kv head, tile of
+//    64 query vectors = 64/G tokens x the G query heads of that kv head).
+//    K/V blocks of 64 positions are staged through LDS (K row-major, V
+//    transposed) and both products run on v_mfma_f32_16x16x32_f16: scores
+//    transposed (S^T = K Q^T), so each lane owns one query column and the
+//    softmax max is two cross-lane steps, and O^T = V^T P^T takes P^T
+//    straight from the score registers (the k-slot order of both operands is
+//    the same permutation of the 32 positions of a step).
+#include "tmc_abi.hpp"
+#include "tmc_device.hpp"
+
+#include <hipblaslt/hipblaslt.h>
+
+#include <cmath>
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <vector>
+
+namespace tmc {
+namespace {
+
+// ------------------------------------------------------------ prefill attention
+constexpr int kPaThreads = 256;
+constexpr int kPaWaves = kPaThreads / kWave;
+constexpr int kPaVectors = 16 * kPaWaves;  // query vectors per workgroup
+constexpr int kPaBlock = 64;               // positions per K/V block
+constexpr int kKPad = 8;                   // halves of padding per K row in LDS
+constexpr int kVPad = 8;                   // halves of padding per V^T row in LDS
+
+struct PrefillParams {
+  const half_t* q;       // [rows, q_heads, D]
+  const half_t* k;       // pool [pages][kv_heads][page_size][D]
+  const half_t* v;
+  half_t* out;           // [rows, q_heads, D]
+  const int32_t* valid;  // [rows] valid length of each query token
+  const int32_t* table;  // [max_pages] pages of the request
+  const int32_t* active; // [1] query tokens present
+  long page_stride, head_stride, pool_pages;
+  int rows, q_heads, kv_heads, group, tokens_per_tile, tiles;
+  int page_size, max_pages;
+  float scale_log2;
+};
+
+// Per-thread share of one block: K as 16-byte chunks (item = position x
+// chunk), V as items of 4 positions x 8 dims (item = quad + 16 * octet).
+template <int D>
+struct PaBlockRegs {
+  static constexpr int kItems = kPaBlock * D / 8;
+  static constexpr int vItems = (kPaBlock / 4) * (D / 8);
+  static constexpr int kPer = (kItems + kPaThreads - 1) / kPaThreads;
+  static constexpr int vPer = (vItems + kPaThreads - 1) / kPaThreads;
+  h8 k[kPer];
+  h8 v[4][vPer];
+};
+
+// Global loads of one 64-position block into registers (zero where the
+// position is at or past `end` or its page is absent).
+template <int D>
+__device__ __forceinline__ void pa_load(const PrefillParams& p, int kvh, int base, int end,
+                                        PaBlockRegs<D>& r) {
+  constexpr int CH = D / 8;  // 16-byte chunks per position
+  const h8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < PaBlockRegs<D>::kPer; ++i) {
+    const int item = threadIdx.x + i * kPaThreads;
+    const int pos = base + item / CH, chunk = item % CH;
+    r.k[i] = zero;
+    if (item < PaBlockRegs<D>::kItems && pos < end) {
+      const int page = p.table[pos / p.page_size];
+      if (page >= 0 && page < p.pool_pages)
+        r.k[i] = load_h8(p.k + (long)page * p.page_stride + (long)kvh * p.head_stride +
+                         (long)(pos % p.page_size) * D + 8 * chunk);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < PaBlockRegs<D>::vPer; ++i) {
+    const int item = threadIdx.x + i * kPaThreads;
+    const int quad = item % (kPaBlock / 4), octet = item / (kPaBlock / 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int pos = base + 4 * quad + e;
+      r.v[e][i] = zero;
+      if (item < PaBlockRegs<D>::vItems && pos < end) {
+        const int page = p.table[pos / p.page_size];
+        if (page >= 0 && page < p.pool_pages)
+          r.v[e][i] = load_h8(p.v + (long)page * p.page_stride + (long)kvh * p.head_stride +
+                              (long)(pos % p.page_size) * D + 8 * octet);
+      }
+    }
+  }
+}
+
+// Registers -> LDS: K row-major [64][D + kKPad], V transposed [D][64 + kVPad].
+template <int D>
+__device__ __forceinline__ void pa_store(const PaBlockRegs<D>& r, half_t* sk, half_t* svt) {
+  constexpr int CH = D / 8;
+#pragma unroll
+  for (int i = 0; i < PaBlockRegs<D>::kPer; ++i) {
+    const int item = threadIdx.x + i * kPaThreads;
+    if (item >= PaBlockRegs<D>::kItems) break;
+    *reinterpret_cast<h8*>(sk + (item / CH) * (D + kKPad) + 8 * (item % CH)) = r.k[i];
+  }
+#pragma unroll
+  for (int i = 0; i < PaBlockRegs<D>::vPer; ++i) {
+    const int item = threadIdx.x + i * kPaThreads;
+    if (item >= PaBlockRegs<D>::vItems) break;
+    const int quad = item % (kPaBlock / 4), octet = item / (kPaBlock / 4);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const h4 col = {r.v[0][i][d], r.v[1][i][d], r.v[2][i][d], r.v[3][i][d]};
+      *reinterpret_cast<h4*>(svt + (8 * octet + d) * (kPaBlock + kVPad) + 4 * quad) = col;
+    }
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillParams p) {
+  constexpr int KS = D / 32;  // k-steps of the score product
+  constexpr int DT = D / 16;  // 16-dim output tiles
+  __shared__ __attribute__((aligned(16))) half_t s_k[kPaBlock * (D + kKPad)];
+  __shared__ __attribute__((aligned(16))) half_t s_vt[D * (kPaBlock + kVPad)];
+  __shared__ int s_bounds[2];
+
+  // Workgroup -> (kv head, tile).  With kv_heads a multiple of 8, the tiles
+  // of one kv head stay on one XCD (workgroups are dealt to the 8 XCDs
+  // round-robin), so its K/V blocks are shared through that XCD's L2; the
+  // longest (last) tiles of each head start first.
+  const int id = blockIdx.x;
+  int kvh, tile;
+  if (p.kv_heads % 8 == 0) {
+    const int xcd = id % 8, j = id / 8;
+    kvh = xcd + 8 * (j / p.tiles);
+    tile = p.tiles - 1 - j % p.tiles;
+  } else {
+    kvh = id / p.tiles;
+    tile = p.tiles - 1 - id % p.tiles;
+  }
+  const int active = min(p.active[0], p.rows);
+  const int t0 = tile * p.tokens_per_tile;
+  if (t0 >= active) return;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int j = lane & 15, g = lane >> 4;
+  // This lane's query column: vector wave*16 + j = token offset * G + head offset.
+  const int vec = wave * 16 + j;
+  const int token = t0 + vec / p.group;
+  const int head = kvh * p.group + vec % p.group;
+  const int capacity = p.page_size * p.max_pages;
+  int len = 0;
+  if (vec < p.tokens_per_tile * p.group && token < active) {
+    len = p.valid[token];
+    if (len < 1 || len > capacity) len = -1;  // no output for this query
+  }
+
+  // Attended extent of the tile and the first absent page below it.
+  if (threadIdx.x == 0) {
+    s_bounds[0] = 0;
+    s_bounds[1] = 0x7fffffff;
+  }
+  __syncthreads();
+  if (g == 0 && len > 0) atomicMax(&s_bounds[0], len);
+  __syncthreads();
+  const int end = s_bounds[0];
+  if (end == 0) return;
+  {
+    const int pages = (end + p.page_size - 1) / p.page_size;
+    int first_bad = 0x7fffffff;
+    for (int i = threadIdx.x; i < pages; i += kPaThreads) {
+      const int page = p.table[i];
+      if (page < 0 || page >= p.pool_pages) first_bad = min(first_bad, i);
+    }
+    if (first_bad != 0x7fffffff) atomicMin(&s_bounds[1], first_bad);
+  }
+  __syncthreads();
+  const long bad_from = (long)s_bounds[1] * p.page_size;  // positions at/after: absent page
+
+  const h8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  h8 qb[KS];
+  {
+    const half_t* qrow = p.q + ((size_t)token * p.q_heads + head) * D;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qb[s] = len > 0 ? load_h8(qrow + 32 * s + 8 * g) : zero;
+  }
+  f4 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) o[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m = -INFINITY, lsum = 0.0f;
+
+  PaBlockRegs<D> regs;
+  pa_load<D>(p, kvh, 0, end, regs);
+  for (int base = 0; base < end; base += kPaBlock) {
+    __syncthreads();  // the previous block's LDS reads are done
+    pa_store<D>(regs, s_k, s_vt);
+    __syncthreads();
+    if (base + kPaBlock < end) pa_load<D>(p, kvh, base + kPaBlock, end, regs);
+
+    // Scores S^T[pos][query] for 4 tiles of 16 positions.
+    float sc[4][4];
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      const half_t* krow = s_k + (16 * kt + j) * (D + kKPad) + 8 * g;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const h8*>(krow + 32 * s),
+                                                     qb[s], acc, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int pos = base + 16 * kt + 4 * g + r;
+        sc[kt][r] = pos < len ? acc[r] * p.scale_log2 : -INFINITY;
+        bmax = fmaxf(bmax, sc[kt][r]);
+      }
+    }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    const float next = fmaxf(m, bmax);
+    const float alpha = next == -INFINITY ? 1.0f : fast_exp2(m - next);
+    m = next;
+    h8 pb[2];
+    float psum = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pr = sc[kt][r] == -INFINITY ? 0.0f : fast_exp2(sc[kt][r] - next);
+        const half_t ph = (half_t)pr;
+        psum += (float)ph;  // the denominator sums the weights the product uses
+        pb[kt >> 1][4 * (kt & 1) + r] = ph;
+      }
+    lsum = lsum * alpha + psum;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[t] *= alpha;
+    // O^T[d][query] += V^T[d][pos] P^T[pos][query]; slot 8g+e of step c is
+    // position 32c + 4g + e (e < 4) or 32c + 16 + 4g + (e - 4).
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const half_t* vrow = s_vt + (16 * t + j) * (kPaBlock + kVPad) + 4 * g;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const h4 lo = *reinterpret_cast<const h4*>(vrow + 32 * c);
+        const h4 hi = *reinterpret_cast<const h4*>(vrow + 32 * c + 16);
+        const h8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[c], o[t], 0, 0, 0);
+      }
+    }
+  }
+
+  lsum += __shfl_xor(lsum, 16, kWave);
+  lsum += __shfl_xor(lsum, 32, kWave);
+  if (len <= 0 || len > bad_from) return;
+  const float inv = 1.0f / lsum;
+  half_t* orow = p.out + ((size_t)token * p.q_heads + head) * D;
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    const h4 val = {(half_t)(o[t][0] * inv), (half_t)(o[t][1] * inv), (half_t)(o[t][2] * inv),
+                    (half_t)(o[t][3] * inv)};
+    *reinterpret_cast<h4*>(orow + 16 * t + 4 * g) = val;
+  }
+}
+
+// ------------------------------------------------------------------ prompt GEMM
+struct GemmKey {
+  int device, out_dtype;
+  int64_t m, k, n;
+  size_t workspace;
+  bool operator<(const GemmKey& o) const {
+    return std::tie(device, out_dtype, m, k, n, workspace) <
+           std::tie(o.device, o.out_dtype, o.m, o.k, o.n, o.workspace);
+  }
+};
+
+struct GemmPlan {
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
+  std::vector<hipblasLtMatmulHeuristicResult_t> candidates;
+  int chosen = 0;
+  bool timed = false;
+};
+
+std::mutex g_gemm_mutex;
+std::map<int, hipblasLtHandle_t> g_lt_handles;
+std::map<GemmKey, GemmPlan> g_gemm_plans;
+
+constexpr int kGemmCandidates = 8;
+
+int lt_ok(hipblasStatus_t status, const char* what) {
+  if (status == HIPBLAS_STATUS_SUCCESS) return 0;
+  return fail(std::string("hipBLASLt ") + what + " failed (status " +
+              std::to_string((int)status) + ").");
+}
+
+// Column-major view of the row-major problem: Y^T[n, m] = W[n, k] X^T[k, m],
+// i.e. op(A) = A^T with A = W as a k x n column-major matrix (ld k), B = X as
+// k x m (ld k), C = Y as n x m (ld n).
+int make_plan(hipblasLtHandle_t handle, const GemmKey& key, GemmPlan& plan) {
+  if (lt_ok(hipblasLtMatmulDescCreate(&plan.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F), "desc"))
+    return 1;
+  const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+  if (lt_ok(hipblasLtMatmulDescSetAttribute(plan.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta),
+            "transA") ||
+      lt_ok(hipblasLtMatmulDescSetAttribute(plan.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb),
+            "transB"))
+    return 1;
+  const hipDataType out = key.out_dtype == TMC_F32 ? HIP_R_32F : HIP_R_16F;
+  if (lt_ok(hipblasLtMatrixLayoutCreate(&plan.a, HIP_R_16F, (uint64_t)key.k, (uint64_t)key.n, key.k),
+            "layout A") ||
+      lt_ok(hipblasLtMatrixLayoutCreate(&plan.b, HIP_R_16F, (uint64_t)key.k, (uint64_t)key.m, key.k),
+            "layout B") ||
+      lt_ok(hipblasLtMatrixLayoutCreate(&plan.c, out, (uint64_t)key.n, (uint64_t)key.m, key.n),
+            "layout C"))
+    return 1;
+  hipblasLtMatmulPreference_t pref = nullptr;
+  if (lt_ok(hipblasLtMatmulPreferenceCreate(&pref), "preference")) return 1;
+  uint64_t ws = key.workspace;
+  (void)hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
+                                              sizeof ws);
+  hipblasLtMatmulHeuristicResult_t results[kGemmCandidates];
+  int returned = 0;
+  const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(handle, plan.desc, plan.a, plan.b, plan.c,
+                                                             plan.c, pref, kGemmCandidates, results,
+                                                             &returned);
+  (void)hipblasLtMatmulPreferenceDestroy(pref);
+  if (lt_ok(st, "heuristic")) return 1;
+  for (int i = 0; i < returned; ++i)
+    if (results[i].state == HIPBLAS_STATUS_SUCCESS && results[i].workspaceSize <= key.workspace)
+      plan.candidates.push_back(results[i]);
+  if (plan.candidates.empty()) return fail("hipBLASLt has no algorithm for this GEMM.");
+  return 0;
+}
+
+hipblasStatus_t run_plan(hipblasLtHandle_t handle, const GemmPlan& plan, int index, const void* x,
+                         const void* w, void* y, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream) {
+  const float alpha = 1.0f, beta = 0.0f;
+  return hipblasLtMatmul(handle, plan.desc, &alpha, w, plan.a, x, plan.b, &beta, y, plan.c, y,
+                         plan.c, &plan.candidates[(size_t)index].algo, workspace, workspace_bytes,
+                         stream);
+}
+
+// Time every candidate (one warm-up and three timed calls each) on the
+// caller's stream and buffers; the last call leaves Y from the fastest.
+int time_plan(hipblasLtHandle_t handle, GemmPlan& plan, const void* x, const void* w, void* y,
+              void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  hipEvent_t start = nullptr, stop = nullptr;
+  if (hipEventCreate(&start) != hipSuccess || hipEventCreate(&stop) != hipSuccess)
+    return fail("hipEventCreate failed.");
+  float best = 0.0f;
+  int chosen = -1;
+  for (int i = 0; i < (int)plan.candidates.size(); ++i) {
+    if (run_plan(handle, plan, i, x, w, y, workspace, workspace_bytes, stream) !=
+        HIPBLAS_STATUS_SUCCESS)
+      continue;
+    (void)hipEventRecord(start, stream);
+    bool ok = true;
+    for (int r = 0; r < 3 && ok; ++r)
+      ok = run_plan(handle, plan, i, x, w, y, workspace, workspace_bytes, stream) ==
+           HIPBLAS_STATUS_SUCCESS;
+    (void)hipEventRecord(stop, stream);
+    float ms = 0.0f;
+    if (hipEventSynchronize(stop) != hipSuccess ||
+        hipEventElapsedTime(&ms, start, stop) != hipSuccess)
+      ok = false;
+    if (ok && (chosen < 0 || ms < best)) {
+      best = ms;
+      chosen = i;
+    }
+  }
+  (void)hipEventDestroy(start);
+  (void)hipEventDestroy(stop);
+  if (chosen < 0) return fail("hipBLASLt: no candidate algorithm ran for this GEMM.");
+  plan.chosen = chosen;
+  plan.timed = true;
+  return 0;
+}
+
+}  // namespace
+}  // namespace tmc
+
+using namespace tmc;
+
+extern "C" size_t tmc_gemm_rows_workspace_bytes(void) { return (size_t)32 << 20; }
+
+extern "C" int tmc_gemm_rows_f16(const void* x, const void* weight, void* y, int out_dtype,
+                                 int64_t m, int64_t k, int64_t n, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  TMC_REQUIRE(x && weight && y, "Prompt GEMM: null device pointer.");
+  TMC_REQUIRE(out_dtype == TMC_F16 || out_dtype == TMC_F32, "Prompt GEMM: output must be f16 or f32.");
+  TMC_REQUIRE(m > 0 && k > 0 && n > 0 && m < (1LL << 31) && k < (1LL << 31) && n < (1LL << 31),
+              "Prompt GEMM: invalid shape.");
+  TMC_REQUIRE(workspace || workspace_bytes == 0, "Prompt GEMM: null workspace with a nonzero size.");
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return fail("hipGetDevice failed.");
+  const hipStream_t s = as_stream(stream);
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &capture) != hipSuccess) return fail("hipStreamIsCapturing failed.");
+  std::lock_guard<std::mutex> lock(g_gemm_mutex);
+  auto& handle = g_lt_handles[device];
+  if (!handle && lt_ok(hipblasLtCreate(&handle), "create")) return 1;
+  const GemmKey key{device, out_dtype, m, k, n, workspace_bytes};
+  auto it = g_gemm_plans.find(key);
+  if (it == g_gemm_plans.end()) {
+    GemmPlan plan;
+    if (make_plan(handle, key, plan)) return 1;
+    it = g_gemm_plans.emplace(key, std::move(plan)).first;
+  }
+  GemmPlan& plan = it->second;
+  if (!plan.timed && capture == hipStreamCaptureStatusNone && plan.candidates.size() > 1)
+    return time_plan(handle, plan, x, weight, y, workspace, workspace_bytes, s);
+  return lt_ok(run_plan(handle, plan, plan.chosen, x, weight, y, workspace, workspace_bytes, s),
+               "matmul");
+}
+
+extern "C" int tmc_prefill_attention_f16(const void* q, const void* key_pool, const void* value_pool,
+                                         const int32_t* valid_lengths, const int32_t* block_table,
+                                         const int32_t* active_count, void* out, int64_t rows,
+                                         int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                         int64_t page_size, int64_t max_pages, int64_t pool_pages,
+                                         int64_t page_stride, int64_t head_stride, void* stream) {
+  TMC_REQUIRE(q && key_pool && value_pool && valid_lengths && block_table && active_count && out,
+              "Prefill attention: null device pointer.");
+  TMC_REQUIRE(head_dim == 64 || head_dim == 128, "Prefill attention: head_dim must be 64 or 128.");
+  TMC_REQUIRE(rows > 0 && rows < (1LL << 24) && q_heads > 0 && kv_heads > 0 &&
+                  q_heads % kv_heads == 0,
+              "Prefill attention: invalid rows or heads.");
+  const int64_t group = q_heads / kv_heads;
+  TMC_REQUIRE(group <= kPaVectors && kPaVectors % group == 0,
+              "Prefill attention: q_heads / kv_heads must divide 64.");
+  TMC_REQUIRE(page_size > 0 && max_pages > 0 && page_size * max_pages < (1LL << 30) &&
+                  pool_pages > 0 && pool_pages < (1LL << 31),
+              "Prefill attention: invalid page geometry.");
+  TMC_REQUIRE(head_stride >= page_size * head_dim &&
+                  page_stride >= (kv_heads - 1) * head_stride + page_size * head_dim,
+              "Prefill attention: the head stride must hold a head's page rows and the page "
+              "stride every kv head.");
+  PrefillParams p{};
+  p.q = static_cast<const half_t*>(q);
+  p.k = static_cast<const half_t*>(key_pool);
+  p.v = static_cast<const half_t*>(value_pool);
+  p.out = static_cast<half_t*>(out);
+  p.valid = valid_lengths;
+  p.table = block_table;
+  p.active = active_count;
+  p.page_stride = page_stride;
+  p.head_stride = head_stride;
+  p.pool_pages = pool_pages;
+  p.rows = (int)rows;
+  p.q_heads = (int)q_heads;
+  p.kv_heads = (int)kv_heads;
+  p.group = (int)group;
+  p.tokens_per_tile = (int)(kPaVectors / group);
+  p.tiles = (int)((rows + p.tokens_per_tile - 1) / p.tokens_per_tile);
+  p.page_size = (int)page_size;
+  p.max_pages = (int)max_pages;
+  p.scale_log2 = (float)(1.0 / std::sqrt((double)head_dim)) * 1.4426950408889634f;
+  const dim3 grid((unsigned)((int64_t)p.tiles * kv_heads));
+  if (head_dim == 128)
+    hipLaunchKernelGGL(prefill_attention_kernel<128>, grid, dim3(kPaThreads), 0, as_stream(stream), p);
+  else
+    hipLaunchKernelGGL(prefill_attention_kernel<64>, grid, dim3(kPaThreads), 0, as_stream(stream), p);
+  return check_launch("prefill_attention_kernel");
+}

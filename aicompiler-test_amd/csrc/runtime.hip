@@ -11,7 +11,9 @@
 //    typed gfx950 entry points.
 //  * A prepared execution owns its bindings, constants and any workspace.
 //  * A sequence is captured once into a HIP graph and replayed with a single
-//    hipGraphLaunch (the counterpart of one Metal command buffer).
+//    hipGraphLaunch (the counterpart of one Metal command buffer); one that
+//    holds a library call kept out of graphs (the prompt GEMM) replays its
+//    steps eagerly on the same stream instead.
 #include "tmc_abi.hpp"
 
 #include <hip/hip_runtime.h>
@@ -191,6 +193,9 @@ struct KernelSpec {
   // pools, whose extent the block tables decide).
   std::vector<size_t> counts;
   std::function<int(const LaunchContext&)> launch;
+  // false: the launch calls a library that is not recorded into a graph
+  // (the prompt GEMM); a sequence holding such a step replays eagerly.
+  bool capturable = true;
 };
 
 }  // namespace
@@ -214,6 +219,8 @@ struct tmc_seq {
   tmc_runtime* rt = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  // Eager replay (a step is not capturable): the steps' launches in order.
+  std::vector<std::pair<std::function<int(const LaunchContext&)>, LaunchContext>> eager;
 };
 
 namespace {
@@ -649,6 +656,77 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     };
     return true;
   }
+  if (name == "gemm_rows") {
+    // Prompt GEMM y[m, out] = x[m, in] w[out, in]^T; workspace=1 binds a
+    // trailing int32 scratch input of tmc_gemm_rows_workspace_bytes().
+    const int64_t m = param_int(p, "m"), k = param_int(p, "in"), n = param_int(p, "out");
+    const int od = param_dtype(p, "out_dtype", TMC_F16);
+    const bool ws = param_int(p, "workspace", 0) != 0;
+    NEED(m > 0 && k > 0 && n > 0 && dt == TMC_F16 && (od == TMC_F16 || od == TMC_F32),
+         "gemm_rows needs m, in, out > 0, dtype=f16 and out_dtype f16|f32.");
+    const size_t ws_bytes = ws ? tmc_gemm_rows_workspace_bytes() : 0;
+    s.inputs = {TMC_F16, TMC_F16};
+    s.counts = {(size_t)(m * k), (size_t)(n * k)};
+    if (ws) {
+      s.inputs.push_back(TMC_I32);
+      s.counts.push_back(ws_bytes / 4);
+    }
+    s.outputs = {od};
+    s.counts.push_back((size_t)(m * n));
+    s.groups = (size_t)(((m + 255) / 256) * ((n + 255) / 256));
+    s.capturable = false;
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_gemm_rows_f16(c.ptrs[0], c.ptrs[1], c.ptrs[ws ? 3 : 2], od, m, k, n,
+                               ws ? c.ptrs[2] : nullptr, ws_bytes, c.stream);
+    };
+    return true;
+  }
+  if (name == "prefill_rope_append") {
+    const int64_t rows = param_int(p, "rows"), qh = param_int(p, "q_heads"),
+                  kvh = param_int(p, "kv_heads", param_int(p, "q_heads")),
+                  d = param_int(p, "head_dim"), cap = param_int(p, "capacity"),
+                  ps = param_int(p, "page_size");
+    NEED(rows > 0 && qh > 0 && kvh > 0 && d > 0 && cap > 0 && ps > 0,
+         "prefill_rope_append needs rows, q_heads, head_dim, capacity, page_size.");
+    const int64_t mp = (cap + ps - 1) / ps;
+    // inputs: qkv, cos, sin, valid_lengths, block_table, active; outputs: q, key pool, value pool
+    s.inputs = {dt, TMC_F32, TMC_F32, TMC_I32, TMC_I32, TMC_I32};
+    s.outputs = {dt, dt, dt};
+    s.counts = {(size_t)(rows * (qh + 2 * kvh) * d), (size_t)(cap * (d / 2)),
+                (size_t)(cap * (d / 2)), (size_t)rows, (size_t)mp, 1, (size_t)(rows * qh * d), 0, 0};
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_prefill_rope_append(c.ptrs[0], static_cast<const float*>(c.ptrs[1]),
+                                     static_cast<const float*>(c.ptrs[2]),
+                                     static_cast<const int32_t*>(c.ptrs[3]),
+                                     static_cast<const int32_t*>(c.ptrs[4]),
+                                     static_cast<const int32_t*>(c.ptrs[5]), c.ptrs[6], c.ptrs[7],
+                                     c.ptrs[8], dt, rows, qh, kvh, d, cap, ps, mp, c.stream);
+    };
+    return true;
+  }
+  if (name == "prefill_attention") {
+    const int64_t rows = param_int(p, "rows"), qh = param_int(p, "q_heads"),
+                  kvh = param_int(p, "kv_heads", param_int(p, "q_heads")),
+                  d = param_int(p, "head_dim"), ps = param_int(p, "page_size"),
+                  mp = param_int(p, "max_pages");
+    NEED(rows > 0 && qh > 0 && kvh > 0 && d > 0 && ps > 0 && mp > 0 && dt == TMC_F16,
+         "prefill_attention needs rows, q_heads, head_dim, page_size, max_pages and dtype=f16.");
+    const int64_t head_stride = param_int(p, "head_stride", ps * d);
+    const int64_t page_stride = param_int(p, "page_stride", kvh * ps * d);
+    // inputs: q, key pool, value pool, valid_lengths, block_table, active; output: context
+    s.inputs = {dt, dt, dt, TMC_I32, TMC_I32, TMC_I32};
+    s.outputs = {dt};
+    s.counts = {(size_t)(rows * qh * d), 0, 0, (size_t)rows, (size_t)mp, 1, (size_t)(rows * qh * d)};
+    s.launch = [=](const LaunchContext& c) {
+      const int64_t pool_pages =
+          (int64_t)(std::min(c.counts[1], c.counts[2]) / (size_t)page_stride);
+      return tmc_prefill_attention_f16(
+          c.ptrs[0], c.ptrs[1], c.ptrs[2], static_cast<const int32_t*>(c.ptrs[3]),
+          static_cast<const int32_t*>(c.ptrs[4]), static_cast<const int32_t*>(c.ptrs[5]),
+          c.ptrs[6], rows, qh, kvh, d, ps, mp, pool_pages, page_stride, head_stride, c.stream);
+    };
+    return true;
+  }
   if (name == "argmax") {
     const int64_t rows = param_int(p, "rows"), v = param_int(p, "vocab");
     NEED(rows > 0 && v > 0, "argmax needs rows and vocab.");
@@ -995,12 +1073,19 @@ extern "C" int tmc_seq_create(tmc_runtime* rt, tmc_exec* const* steps, size_t n,
   clear_error();
   if (!rt || !out) return fail("tmc_seq_create: null argument.");
   if (n == 0 || !steps) return fail("A prepared region sequence cannot be empty.");
+  bool capturable = true;
   for (size_t i = 0; i < n; ++i) {
     if (!steps[i] || !steps[i]->spec.launch) return fail("A region contains an invalid prepared execution.");
     if (steps[i]->rt != rt) return fail("All region steps must use the same runtime stream.");
+    capturable = capturable && steps[i]->spec.capturable;
   }
   auto seq = std::make_unique<tmc_seq>();
   seq->rt = rt;
+  if (!capturable) {
+    for (size_t i = 0; i < n; ++i) seq->eager.emplace_back(steps[i]->spec.launch, steps[i]->ctx);
+    *out = seq.release();
+    return 0;
+  }
   if (hip_ok(hipStreamSynchronize(rt->stream), "sequence capture")) return 1;
   if (hip_ok(hipStreamBeginCapture(rt->stream, hipStreamCaptureModeThreadLocal), "begin capture"))
     return 1;
@@ -1022,11 +1107,22 @@ extern "C" int tmc_seq_create(tmc_runtime* rt, tmc_exec* const* steps, size_t n,
   return 0;
 }
 
+namespace {
+// One replay of the sequence on its runtime's stream: the graph, or the
+// eager steps in order (stops at the first failing launch).
+int replay(tmc_seq* seq) {
+  if (seq->exec) return hip_ok(hipGraphLaunch(seq->exec, seq->rt->stream), "graph launch");
+  for (const auto& [launch, ctx] : seq->eager)
+    if (launch(ctx)) return 1;
+  return 0;
+}
+}  // namespace
+
 extern "C" int tmc_seq_launch(tmc_seq* seq) {
   clear_error();
   if (!seq) return fail("tmc_seq_launch: null sequence.");
   if (consume_failure(seq->rt)) return 1;
-  return hip_ok(hipGraphLaunch(seq->exec, seq->rt->stream), "graph launch");
+  return replay(seq);
 }
 
 extern "C" int tmc_seq_run(tmc_seq* seq, double* gpu_us, double* cpu_us) {
@@ -1040,7 +1136,7 @@ extern "C" int tmc_seq_run(tmc_seq* seq, double* gpu_us, double* cpu_us) {
     (void)hipEventRecord(start, rt->stream);
   }
   const auto t0 = std::chrono::steady_clock::now();
-  int rc = hip_ok(hipGraphLaunch(seq->exec, rt->stream), "graph launch");
+  int rc = replay(seq);
   if (gpu_us) (void)hipEventRecord(stop, rt->stream);
   const hipError_t sync = hipStreamSynchronize(rt->stream);
   const auto t1 = std::chrono::steady_clock::now();

@@ -647,6 +647,283 @@ BatchedDecodeRun BatchedDecodeExecutor::run(const std::vector<std::int32_t>& tok
   return result;
 }
 
+// ----------------------------------------------------- ChunkedPrefillExecutor
+struct ChunkedPrefillExecutor::Stage {
+  std::size_t rows = 0;
+  std::vector<std::unique_ptr<hip::PreparedExecution>> steps;
+  std::unique_ptr<hip::PreparedSequence> sequence;
+};
+
+ChunkedPrefillExecutor::~ChunkedPrefillExecutor() = default;
+
+std::vector<std::size_t> ChunkedPrefillExecutor::buckets() const {
+  std::vector<std::size_t> rows;
+  for (const auto& stage : stages_) rows.push_back(stage->rows);
+  return rows;
+}
+
+std::size_t ChunkedPrefillExecutor::dispatchesPerChunk(std::size_t bucket) const {
+  for (const auto& stage : stages_)
+    if (stage->rows == bucket) return stage->steps.size();
+  return 0;
+}
+
+void ChunkedPrefillExecutor::build(std::ostream* log) {
+  auto& rt = *runtime_;
+  const auto& plan = model_->plan;
+  const std::size_t S = chunkSize_, L = plan.layerCount;
+  const std::size_t H = plan.hiddenSize(), I = plan.intermediateSize, V = plan.vocabularySize;
+  const std::size_t QH = plan.attention.heads, KVH = plan.kvHeads(), D = plan.attention.headDimension;
+  const std::size_t QKV = H + 2 * plan.kvWidth();
+  const std::size_t capacity = plan.attention.capacity;
+  maxPages_ = (capacity + pageSize_ - 1) / pageSize_;
+
+  std::vector<float> zeros(2 * S + 1, 0.0f);
+  meta_ = allocate(rt, 2 * S + 1, zeros.data(), ElementType::Int32);
+  tokensView_ = view(rt, meta_, 0, S);
+  lengthsView_ = view(rt, meta_, S, S);
+  activeView_ = view(rt, meta_, 2 * S, 1);
+  const std::vector<float> none(L * maxPages_, -1.0f);
+  tables_ = allocate(rt, none.size(), none.data(), ElementType::Int32);
+  for (std::size_t l = 0; l < L; ++l) tableViews_.push_back(view(rt, tables_, l * maxPages_, maxPages_));
+  metaShadow_.assign(2 * S + 1, 0);
+  tableShadow_.assign(L * maxPages_, -1);
+
+  auto act = [&](std::size_t count, ElementType type = ElementType::Float16) {
+    activationBytes_ += count * hip::elementBytes(type);
+    return allocate(rt, count, nullptr, type);
+  };
+  residual_ = act(S * H);
+  after_ = act(S * H);
+  normalized_ = act(S * H);
+  qkv_ = act(S * QKV);
+  query_ = act(S * H);
+  context_ = act(S * H);
+  projected_ = act(S * H);
+  gate_ = act(S * I);
+  up_ = act(S * I);
+  gated_ = act(S * I);
+  mlp_ = act(S * H);
+  logits_ = act(S * V, ElementType::Float32);
+  nextTokens_ = act(S, ElementType::Int32);
+  workspace_ = act(tmc_gemm_rows_workspace_bytes() / 4, ElementType::Int32);
+
+  std::vector<std::size_t> rows;
+  for (std::size_t r = 16; r < S; r *= 2) rows.push_back(r);
+  rows.push_back(S);
+
+  const std::string eps = fmt(plan.rmsNormEpsilon);
+  for (const std::size_t m : rows) {
+    auto stage = std::make_unique<Stage>();
+    stage->rows = m;
+    const std::string B = std::to_string(m);
+    auto add = [&](const std::string& key, const std::string& name,
+                   const std::vector<BufferHandle>& inputs,
+                   const std::vector<BufferHandle>& outputs) {
+      const auto pipeline = rt.createComputePipeline(key, name);
+      if (!pipeline.pipelineCreationPassed)
+        throw std::runtime_error(name + ": " + pipeline.errorMessage);
+      auto prepared = rt.prepareBuffers(
+          inputs, outputs, {pipeline.threadgroupCount, pipeline.threadsPerThreadgroup});
+      if (!prepared.execution) throw std::runtime_error(name + ": " + prepared.errorMessage);
+      stage->steps.push_back(std::move(prepared.execution));
+    };
+    auto gemm = [&](std::size_t in, std::size_t out, const char* outType) {
+      return "gemm_rows?m=" + B + "&in=" + std::to_string(in) + "&out=" + std::to_string(out) +
+             "&out_dtype=" + outType + "&workspace=1";
+    };
+    const std::string norm = "rows=" + B + "&width=" + std::to_string(H) + "&eps=" + eps + "&dtype=f16";
+    const std::string heads = "&q_heads=" + std::to_string(QH) + "&kv_heads=" + std::to_string(KVH) +
+                              "&head_dim=" + std::to_string(D) +
+                              "&page_size=" + std::to_string(pageSize_);
+    const std::string ropeKey =
+        "prefill_rope_append?rows=" + B + heads + "&capacity=" + std::to_string(capacity);
+    const std::string attentionKey =
+        "prefill_attention?rows=" + B + heads + "&max_pages=" + std::to_string(maxPages_);
+    add("embedding?rows=" + B + "&hidden=" + std::to_string(H) + "&vocab=" + std::to_string(V),
+        "embedding", {tokensView_, model_->embeddingWeight}, {residual_});
+    add("rmsnorm?" + norm, "l0_input_norm", {residual_, model_->layers[0].inputNormWeight},
+        {normalized_});
+    for (std::size_t l = 0; l < L; ++l) {
+      const auto& w = model_->layers[l];
+      const std::string p = "l" + std::to_string(l) + "_";
+      if (l > 0)
+        add("add_rmsnorm?" + norm, p + "residual_input_norm", {after_, mlp_, w.inputNormWeight},
+            {residual_, normalized_});
+      add(gemm(H, QKV, "f16"), p + "qkv", {normalized_, w.queryKeyValueWeight, workspace_}, {qkv_});
+      add(ropeKey, p + "rope_append",
+          {qkv_, model_->ropeCosine, model_->ropeSine, lengthsView_, tableViews_[l], activeView_},
+          {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer()});
+      add(attentionKey, p + "attention",
+          {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer(), lengthsView_, tableViews_[l],
+           activeView_},
+          {context_});
+      add(gemm(H, H, "f16"), p + "o", {context_, w.outputWeight, workspace_}, {projected_});
+      add("add_rmsnorm?" + norm, p + "residual_post_norm",
+          {residual_, projected_, w.postAttentionNormWeight}, {after_, normalized_});
+      add(gemm(H, I, "f16"), p + "gate", {normalized_, w.gateWeight, workspace_}, {gate_});
+      add(gemm(H, I, "f16"), p + "up", {normalized_, w.upWeight, workspace_}, {up_});
+      add("silu_mul?count=" + std::to_string(m * I) + "&dtype=f16", p + "silu_mul", {gate_, up_},
+          {gated_});
+      add(gemm(I, H, "f16"), p + "down", {gated_, w.downWeight, workspace_}, {mlp_});
+    }
+    add("add_rmsnorm?" + norm, "residual_final_norm", {after_, mlp_, model_->finalNormWeight},
+        {residual_, normalized_});
+    add(gemm(H, V, "f32"), "lm_head", {normalized_, model_->languageModelHeadWeight, workspace_},
+        {logits_});
+    add("argmax?rows=" + B + "&vocab=" + std::to_string(V), "argmax", {logits_}, {nextTokens_});
+    std::vector<const hip::PreparedExecution*> pointers;
+    for (const auto& step : stage->steps) pointers.push_back(step.get());
+    auto sequence = rt.prepareSequence(pointers);
+    if (!sequence.execution) throw std::runtime_error(sequence.errorMessage);
+    stage->sequence = std::move(sequence.execution);
+    if (log)
+      *log << "Chunked prefill stage rows=" << m << ": " << stage->steps.size()
+           << " dispatches (eager)\n";
+    stages_.push_back(std::move(stage));
+  }
+}
+
+ChunkedPrefillExecutor::Creation createChunkedPrefillExecutor(
+    hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
+    std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t chunkSize, std::ostream* log) {
+  ChunkedPrefillExecutor::Creation result;
+  try {
+    if (!model) throw std::invalid_argument("Chunked prefill needs model resources.");
+    const auto& plan = model->plan;
+    if (chunkSize == 0 || chunkSize > 8192)
+      throw std::invalid_argument("Chunked prefill chunk size must be in [1, 8192].");
+    if (pools.size() != plan.layerCount)
+      throw std::invalid_argument("Chunked prefill needs one KV page pool per layer.");
+    const auto kv = plan.kvPlan();
+    for (const auto& pool : pools) {
+      if (!pool || !pool->hasStorage() || pool->pageSize() != pools.front()->pageSize() ||
+          pool->plan().heads != kv.heads || pool->plan().headDimension != kv.headDimension ||
+          pool->plan().dtype != DType::Float16 || pool->plan().batch != 1)
+        throw std::invalid_argument("Chunked prefill KV pools do not match the model.");
+    }
+    const std::size_t D = plan.attention.headDimension;
+    const std::size_t group = plan.attention.heads / plan.kvHeads();
+    if ((D != 64 && D != 128) || 64 % group != 0)
+      throw std::invalid_argument(
+          "Chunked prefill attention needs head_dim 64 or 128 and heads / kv_heads dividing 64.");
+    std::unique_ptr<ChunkedPrefillExecutor> executor(new ChunkedPrefillExecutor());
+    executor->runtime_ = &runtime;
+    executor->model_ = std::move(model);
+    executor->pools_ = std::move(pools);
+    executor->chunkSize_ = chunkSize;
+    executor->pageSize_ = executor->pools_.front()->pageSize();
+    executor->build(log);
+    result.executor = std::move(executor);
+  } catch (const std::exception& error) {
+    result.errorMessage = error.what();
+  }
+  return result;
+}
+
+BatchedDecodeRun ChunkedPrefillExecutor::run(const std::vector<std::int32_t>& tokenIds,
+                                             std::size_t start,
+                                             const std::vector<std::vector<std::int32_t>>& blockTables,
+                                             bool readLogits, bool timeGpu) {
+  BatchedDecodeRun result;
+  const auto& plan = model_->plan;
+  const std::size_t rows = tokenIds.size(), S = chunkSize_;
+  if (rows == 0 || rows > S || blockTables.size() != plan.layerCount) {
+    result.errorMessage = "Chunked prefill input shape is invalid.";
+    return result;
+  }
+  if (start + rows > plan.attention.capacity) {
+    result.errorMessage = "KV cache valid length is outside the configured capacity.";
+    return result;
+  }
+  for (const auto token : tokenIds) {
+    if (token < 0 || static_cast<std::size_t>(token) >= plan.vocabularySize) {
+      result.errorMessage = "Chunked prefill token id is outside the vocabulary.";
+      return result;
+    }
+  }
+  // Every page the chunk writes or attends is allocated in its layer's pool;
+  // entries past them are absent or allocated.
+  const std::size_t needed = (start + rows + pageSize_ - 1) / pageSize_;
+  for (std::size_t l = 0; l < blockTables.size(); ++l) {
+    if (blockTables[l].size() != maxPages_) {
+      result.errorMessage = "Chunked prefill block-table shape is invalid.";
+      return result;
+    }
+    for (std::size_t p = 0; p < maxPages_; ++p) {
+      const std::int32_t page = blockTables[l][p];
+      if ((p < needed || page >= 0) && !pools_[l]->isAllocated(page)) {
+        result.errorMessage = "Chunked prefill block table names a page that is not allocated "
+                              "in its layer's pool.";
+        return result;
+      }
+    }
+  }
+  std::vector<std::int32_t> meta(2 * S + 1, 0);
+  std::copy(tokenIds.begin(), tokenIds.end(), meta.begin());
+  for (std::size_t r = 0; r < rows; ++r) meta[S + r] = static_cast<std::int32_t>(start + r + 1);
+  meta[2 * S] = static_cast<std::int32_t>(rows);
+  std::string error;
+  if (meta != metaShadow_) {
+    error = meta_->writeRaw(meta.data(), meta.size());
+    if (!error.empty()) {
+      result.errorMessage = error;
+      return result;
+    }
+    metaShadow_ = std::move(meta);
+  }
+  std::vector<std::int32_t> packed(tableShadow_.size(), -1);
+  for (std::size_t l = 0; l < blockTables.size(); ++l)
+    std::copy(blockTables[l].begin(), blockTables[l].end(),
+              packed.begin() + static_cast<std::ptrdiff_t>(l * maxPages_));
+  std::size_t first = 0, last = packed.size();
+  while (first < last && packed[first] == tableShadow_[first]) ++first;
+  while (last > first && packed[last - 1] == tableShadow_[last - 1]) --last;
+  if (first < last) {
+    error = tables_->writeRaw(packed.data() + first, last - first, first);
+    if (!error.empty()) {
+      result.errorMessage = error;
+      return result;
+    }
+    tableShadow_ = std::move(packed);
+  }
+  std::size_t index = 0;
+  while (stages_[index]->rows < rows) ++index;
+  auto& stage = *stages_[index];
+  if (timeGpu) {
+    const auto execution = stage.sequence->execute();
+    if (!execution.executionPassed) {
+      result.errorMessage = execution.errorMessage;
+      return result;
+    }
+    result.gpuExecutionTimeUs = execution.gpuExecutionTimeUs;
+    result.cpuSubmitToCompletionTimeUs = execution.cpuSubmitToCompletionTimeUs;
+  } else {
+    error = stage.sequence->launch();
+    if (!error.empty()) {
+      result.errorMessage = error;
+      return result;
+    }
+  }
+  std::vector<std::int32_t> next(rows);
+  error = nextTokens_->readRaw(next.data(), rows);  // waits for the stream
+  if (!error.empty()) {
+    result.errorMessage = error;
+    return result;
+  }
+  result.nextTokenIds.assign(next.begin(), next.end());
+  if (readLogits) {
+    result.logits.resize(rows * plan.vocabularySize);
+    error = logits_->readRaw(result.logits.data(), result.logits.size());
+    if (!error.empty()) {
+      result.errorMessage = error;
+      return result;
+    }
+  }
+  result.passed = true;
+  return result;
+}
+
 // --------------------------------------------------------- CompiledDecoderLLM
 class CompiledDecoderLLM::Impl {
  public:
@@ -656,6 +933,7 @@ class CompiledDecoderLLM::Impl {
   std::vector<std::shared_ptr<KVPagePool>> pools;
   std::vector<std::unique_ptr<KVCacheState>> states;
   std::unique_ptr<BatchedDecodeExecutor> executor;
+  std::unique_ptr<ChunkedPrefillExecutor> prefillExecutor;
   std::size_t requestedPageSize = 0;
   std::size_t kvBytes = 0;
 
@@ -757,6 +1035,65 @@ DecoderLLMRunResult CompiledDecoderLLM::prefill(const std::vector<float>& tokenI
   return result;
 }
 
+DecoderLLMRunResult CompiledDecoderLLM::prefillChunked(const std::vector<float>& tokenIds,
+                                                       bool readLogits) {
+  DecoderLLMRunResult result;
+  if (currentLength() != 0) {
+    result.errorMessage = "Chunked decoder prefill requires an empty cache; call reset first.";
+    return result;
+  }
+  if (!impl_->prefillExecutor) {
+    result.errorMessage = "Chunked decoder prefill was not compiled.";
+    return result;
+  }
+  if (tokenIds.empty() || tokenIds.size() > impl_->plan.attention.capacity) {
+    result.errorMessage = "Decoder prefill length is outside the cache capacity.";
+    return result;
+  }
+  auto& executor = *impl_->prefillExecutor;
+  const std::size_t chunk = executor.chunkSize();
+  double gpu = 0.0;
+  bool timed = true;
+  for (std::size_t offset = 0; offset < tokenIds.size();) {
+    const std::size_t count = std::min(chunk, tokenIds.size() - offset);
+    const std::size_t start = currentLength();
+    auto error = impl_->stage(start + count);
+    if (!error.empty()) {
+      (void)reset();
+      result.errorMessage = error;
+      return result;
+    }
+    std::vector<std::int32_t> tokens(count);
+    for (std::size_t i = 0; i < count; ++i)
+      tokens[i] = static_cast<std::int32_t>(tokenIds[offset + i]);
+    std::vector<std::vector<std::int32_t>> tables;
+    for (const auto& state : impl_->states) {
+      auto table = state->pageTable();
+      table.resize(executor.maxPages(), -1);
+      tables.push_back(std::move(table));
+    }
+    const auto run = executor.run(tokens, start, tables, readLogits, true);
+    if (!run.passed) {
+      (void)reset();
+      result.errorMessage = run.errorMessage;
+      return result;
+    }
+    for (auto& state : impl_->states) state->commitLength(start + count);
+    if (readLogits) result.logits.insert(result.logits.end(), run.logits.begin(), run.logits.end());
+    result.nextTokenIds = run.nextTokenIds;
+    result.cpuSubmitToCompletionTimeUs += run.cpuSubmitToCompletionTimeUs;
+    if (run.gpuExecutionTimeUs) gpu += *run.gpuExecutionTimeUs; else timed = false;
+    offset += count;
+  }
+  if (timed) result.gpuExecutionTimeUs = gpu;
+  result.passed = true;
+  return result;
+}
+
+std::size_t CompiledDecoderLLM::prefillChunkSize() const noexcept {
+  return impl_->prefillExecutor ? impl_->prefillExecutor->chunkSize() : 0;
+}
+
 DecoderLLMRunResult CompiledDecoderLLM::decode(const std::vector<float>& tokenIds,
                                                bool readLogits) {
   DecoderLLMRunResult result;
@@ -809,7 +1146,8 @@ std::size_t CompiledDecoderLLM::modelStorageBytes() const noexcept {
 std::size_t CompiledDecoderLLM::kvStorageBytes() const noexcept { return impl_->kvBytes; }
 
 std::size_t CompiledDecoderLLM::activationStorageBytes() const noexcept {
-  return impl_->executor->activationStorageBytes();
+  return impl_->executor->activationStorageBytes() +
+         (impl_->prefillExecutor ? impl_->prefillExecutor->activationStorageBytes() : 0);
 }
 
 std::shared_ptr<DecoderLLMModelResources> CompiledDecoderLLM::sharedModelResources()
@@ -925,6 +1263,12 @@ DecoderLLMCompilation compileDecoderLLM(hip::HipRuntime& runtime,
     auto executor = createBatchedDecodeExecutor(runtime, impl->model, impl->pools, 1, &log);
     if (!executor.executor) throw std::runtime_error(executor.errorMessage);
     impl->executor = std::move(executor.executor);
+    if (options.prefillChunkSize != 0) {
+      auto prefill = createChunkedPrefillExecutor(runtime, impl->model, impl->pools,
+                                                  options.prefillChunkSize, &log);
+      if (!prefill.executor) throw std::runtime_error(prefill.errorMessage);
+      impl->prefillExecutor = std::move(prefill.executor);
+    }
     log << "Decoder compile: layers=" << impl->plan.layerCount
         << ", kv_page_size=" << options.kvPageSize << ", dispatches/token="
         << impl->executor->dispatchesPerStep(1) << '\n';

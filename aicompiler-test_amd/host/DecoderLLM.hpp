@@ -241,8 +241,75 @@ struct BatchedDecodeExecutor::Creation {
     std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t maximumBatchSize,
     std::ostream* log = nullptr, bool tuneKernels = false);
 
+// Chunked prefill (prefillChunked, DecoderLLMExecutor.cpp:982-1034): the
+// tokens of one request's prompt chunk are the rows of one stage.  Linear
+// layers are prompt GEMMs (hipBLASLt, kernel key gemm_rows), RoPE and the
+// cache append share the request's block table (prefill_rope_append) and
+// attention is causal over the chunk (prefill_attention): row r of a chunk
+// starting at position `start` attends [0, start + r + 1), which is what
+// start + r + 1 decode steps would attend.  Stages are prepared for row
+// buckets 16, 32, ... and chunkSize; a chunk runs the smallest that holds it
+// (spare rows are computed and discarded).  A stage replays eagerly on the
+// runtime's stream (the library GEMMs are kept out of graphs).
+class ChunkedPrefillExecutor {
+ public:
+  struct Creation;
+  ~ChunkedPrefillExecutor();
+  ChunkedPrefillExecutor(const ChunkedPrefillExecutor&) = delete;
+  ChunkedPrefillExecutor& operator=(const ChunkedPrefillExecutor&) = delete;
+
+  // Tokens at positions start .. start + tokens - 1 of one request; block
+  // tables per layer as [maxPages()] holding pages for every position below
+  // start + tokens.  Logits (when read) and next tokens are per row.
+  [[nodiscard]] BatchedDecodeRun run(const std::vector<std::int32_t>& tokenIds, std::size_t start,
+                                     const std::vector<std::vector<std::int32_t>>& blockTables,
+                                     bool readLogits = true, bool timeGpu = false);
+
+  [[nodiscard]] std::size_t chunkSize() const noexcept { return chunkSize_; }
+  [[nodiscard]] std::size_t maxPages() const noexcept { return maxPages_; }
+  [[nodiscard]] std::size_t activationStorageBytes() const noexcept { return activationBytes_; }
+  [[nodiscard]] std::vector<std::size_t> buckets() const;
+  [[nodiscard]] std::size_t dispatchesPerChunk(std::size_t bucket) const;
+
+ private:
+  friend Creation createChunkedPrefillExecutor(hip::HipRuntime&,
+                                               std::shared_ptr<DecoderLLMModelResources>,
+                                               std::vector<std::shared_ptr<KVPagePool>>,
+                                               std::size_t, std::ostream*);
+  ChunkedPrefillExecutor() = default;
+  void build(std::ostream* log);
+
+  struct Stage;
+  hip::HipRuntime* runtime_ = nullptr;
+  std::shared_ptr<DecoderLLMModelResources> model_;
+  std::vector<std::shared_ptr<KVPagePool>> pools_;
+  std::size_t chunkSize_ = 0;
+  std::size_t pageSize_ = 0;
+  std::size_t maxPages_ = 0;
+  std::size_t activationBytes_ = 0;
+  hip::BufferHandle meta_;    // int32 [tokens S | lengths S | active 1]
+  hip::BufferHandle tables_;  // int32 [layers][maxPages]
+  hip::BufferHandle tokensView_, lengthsView_, activeView_;
+  std::vector<hip::BufferHandle> tableViews_;
+  hip::BufferHandle residual_, after_, normalized_, qkv_, query_, context_, projected_, gate_, up_,
+      gated_, mlp_, logits_, nextTokens_, workspace_;
+  std::vector<std::unique_ptr<Stage>> stages_;
+  std::vector<std::int32_t> metaShadow_, tableShadow_;
+};
+
+struct ChunkedPrefillExecutor::Creation {
+  std::unique_ptr<ChunkedPrefillExecutor> executor;
+  std::string errorMessage;
+};
+
+[[nodiscard]] ChunkedPrefillExecutor::Creation createChunkedPrefillExecutor(
+    hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
+    std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t chunkSize,
+    std::ostream* log = nullptr);
+
 struct DecoderLLMCompileOptions {
   std::size_t kvPageSize = 0;  // 0 = contiguous cache (one page of `capacity`)
+  std::size_t prefillChunkSize = 0;  // > 0: prefillChunked runs chunks of this many tokens
   std::vector<std::shared_ptr<KVPagePool>> sharedKVPools;
   DType storageDtype = DType::Float16;
   std::shared_ptr<DecoderLLMModelResources> sharedModelResources;
@@ -267,8 +334,9 @@ struct DecoderLLMCompilation;
 
 // One request (batch 1): per-layer KV states over private or shared pools
 // and a one-row batched decode executor.  prefill() runs the prompt through
-// decode steps, one token per step (identical results to a causal prefill:
-// each position sees exactly the positions before it).
+// decode steps, one token per step (a causal prefill: each position sees
+// exactly the positions before it); prefillChunked() runs it through the
+// chunked prefill executor when a chunk size was compiled.
 class CompiledDecoderLLM {
  public:
   ~CompiledDecoderLLM();
@@ -278,8 +346,15 @@ class CompiledDecoderLLM {
   [[nodiscard]] std::string reset();
   [[nodiscard]] DecoderLLMRunResult prefill(const std::vector<float>& tokenIds,
                                             bool readLogits = true);
+  // DecoderLLMExecutor.cpp:982-1034: the prompt in chunks of
+  // prefillChunkSize() tokens through the chunked prefill stage (needs an
+  // empty cache and a nonzero DecoderLLMCompileOptions::prefillChunkSize).
+  // Logits are per prompt position; nextTokenIds holds the last chunk's.
+  [[nodiscard]] DecoderLLMRunResult prefillChunked(const std::vector<float>& tokenIds,
+                                                   bool readLogits = true);
   [[nodiscard]] DecoderLLMRunResult decode(const std::vector<float>& tokenIds,
                                            bool readLogits = true);
+  [[nodiscard]] std::size_t prefillChunkSize() const noexcept;
 
   [[nodiscard]] std::size_t currentLength() const noexcept;
   [[nodiscard]] std::vector<float> readKeyPrefix(std::size_t layer) const;

@@ -358,12 +358,42 @@ PYBIND11_MODULE(_tmc_host, m) {
         },
         py::arg("runtime"), py::arg("model"), py::arg("pools"), py::arg("maximum_batch_size"),
         py::arg("tune_kernels") = false);
+  py::class_<ChunkedPrefillExecutor>(m, "ChunkedPrefillExecutor")
+      .def("run",
+           [](ChunkedPrefillExecutor& e, const std::vector<std::int32_t>& tokens, std::size_t start,
+              const std::vector<std::vector<std::int32_t>>& tables, bool readLogits, bool timeGpu) {
+             BatchedDecodeRun run;
+             {
+               py::gil_scoped_release release;
+               run = e.run(tokens, start, tables, readLogits, timeGpu);
+             }
+             return runToDict(run);
+           },
+           py::arg("tokens"), py::arg("start"), py::arg("tables"), py::arg("read_logits") = true,
+           py::arg("time_gpu") = false)
+      .def("chunk_size", &ChunkedPrefillExecutor::chunkSize)
+      .def("max_pages", &ChunkedPrefillExecutor::maxPages)
+      .def("buckets", &ChunkedPrefillExecutor::buckets)
+      .def("dispatches_per_chunk", &ChunkedPrefillExecutor::dispatchesPerChunk)
+      .def("activation_storage_bytes", &ChunkedPrefillExecutor::activationStorageBytes);
+
+  m.def("create_chunked_prefill_executor",
+        [](hip::HipRuntime& rt, std::shared_ptr<DecoderLLMModelResources> model,
+           std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t chunkSize) {
+          std::ostringstream log;
+          auto r = createChunkedPrefillExecutor(rt, std::move(model), std::move(pools), chunkSize,
+                                                &log);
+          if (!r.executor) throw std::runtime_error(r.errorMessage + "\n" + log.str());
+          return std::move(r.executor);
+        },
+        py::arg("runtime"), py::arg("model"), py::arg("pools"), py::arg("chunk_size"));
   m.def("decode_gemv_cache_size", []() { return planner::decodeGEMVTuningCache().size(); });
   m.def("clear_decode_gemv_cache", []() { planner::decodeGEMVTuningCache().clear(); });
 
   py::class_<DecoderLLMCompileOptions>(m, "DecoderLLMCompileOptions")
       .def(py::init<>())
       .def_readwrite("kv_page_size", &DecoderLLMCompileOptions::kvPageSize)
+      .def_readwrite("prefill_chunk_size", &DecoderLLMCompileOptions::prefillChunkSize)
       .def_readwrite("shared_kv_pools", &DecoderLLMCompileOptions::sharedKVPools)
       .def_readwrite("storage_dtype", &DecoderLLMCompileOptions::storageDtype)
       .def_readwrite("shared_model_resources", &DecoderLLMCompileOptions::sharedModelResources);
@@ -381,6 +411,17 @@ PYBIND11_MODULE(_tmc_host, m) {
              return resultToDict(d.prefill(tokens, readLogits));
            },
            py::arg("token_ids"), py::arg("read_logits") = true)
+      .def("prefill_chunked",
+           [](CompiledDecoderLLM& d, const std::vector<float>& tokens, bool readLogits) {
+             DecoderLLMRunResult r;
+             {
+               py::gil_scoped_release release;
+               r = d.prefillChunked(tokens, readLogits);
+             }
+             return resultToDict(r);
+           },
+           py::arg("token_ids"), py::arg("read_logits") = true)
+      .def("prefill_chunk_size", &CompiledDecoderLLM::prefillChunkSize)
       .def("decode",
            [](CompiledDecoderLLM& d, const std::vector<float>& tokens, bool readLogits) {
              return resultToDict(d.decode(tokens, readLogits));

@@ -120,7 +120,11 @@ void tmc_exec_release(tmc_exec *exec);
 
 /* MetalRuntime::prepareSequence / PreparedSequence::execute
  * (MetalRuntime.hpp:130-142,202-203; .mm:292-341,751-781): the steps are
- * captured once into a HIP graph and replayed with one hipGraphLaunch. */
+ * captured once into a HIP graph and replayed with one hipGraphLaunch.  A
+ * sequence that holds a step kept out of graphs (kernel key gemm_rows, a
+ * hipBLASLt call) replays its steps eagerly, in order, on the runtime's
+ * stream instead.  Either way the steps and their buffers must outlive the
+ * sequence. */
 int tmc_seq_create(tmc_runtime *rt, tmc_exec *const *steps, size_t n, tmc_seq **out);
 int tmc_seq_run(tmc_seq *seq, double *gpu_us, double *cpu_us);
 /* Enqueue one replay on the runtime stream without waiting. */
@@ -392,6 +396,47 @@ int tmc_decode_rope_append(const void *qkv, const float *cosine, const float *si
                            void *value_pool, int dtype, int64_t max_batch, int64_t q_heads,
                            int64_t kv_heads, int64_t head_dim, int64_t capacity,
                            int64_t page_size, int64_t max_pages, void *stream);
+
+/* The chunk-prefill form of tmc_decode_rope_append: every row is a token of
+ * one request, so the rows share one block table [max_pages]; row r's token
+ * sits at position valid_lengths[r]-1 (causal chunk: start + r + 1).  Stage
+ * building of prefillChunked (DecoderLLMExecutor.cpp:982-1034) with the
+ * RoPE and cache append of emitServingRoPE / emitServingPagedCacheAppend. */
+int tmc_prefill_rope_append(const void *qkv, const float *cosine, const float *sine,
+                            const int32_t *valid_lengths, const int32_t *block_table,
+                            const int32_t *active_count, void *q_out, void *key_pool,
+                            void *value_pool, int dtype, int64_t rows, int64_t q_heads,
+                            int64_t kv_heads, int64_t head_dim, int64_t capacity,
+                            int64_t page_size, int64_t max_pages, void *stream);
+
+/* emitTiledGEMM (DecodeGEMVMetalEmitter.cpp:134-169), the prefill linear
+ * layer: y[m, n] = x[m, k] weight[n, k]^T, fp16 inputs, fp32 accumulation,
+ * y fp16 or fp32 (out_dtype), all row-major.  Runs on hipBLASLt; the first
+ * call of a (device, shape, out_dtype, workspace_bytes) outside stream
+ * capture times up to 8 library candidates on these buffers (it waits for
+ * the stream) and keeps the fastest.  workspace may be NULL with
+ * workspace_bytes 0; tmc_gemm_rows_workspace_bytes() is the size that admits
+ * every candidate measured on gfx950 (32 MiB).  Calls that share a workspace
+ * must be ordered on one stream. */
+size_t tmc_gemm_rows_workspace_bytes(void);
+int tmc_gemm_rows_f16(const void *x, const void *weight, void *y, int out_dtype, int64_t m,
+                      int64_t k, int64_t n, void *workspace, size_t workspace_bytes,
+                      void *stream);
+
+/* emitPagedKVAttention with causalPrefill (KVCacheMetalEmitter.cpp:210-310,
+ * attended = valid - S + q + 1): query token r of a chunk (q [rows, q_heads,
+ * D], RoPE applied) attends positions [0, valid_lengths[r]) of one request's
+ * pages (block_table [max_pages]; pools [pages][kv_heads][page_size][D] with
+ * the given strides in elements); out [rows, q_heads, D].  Rows >=
+ * active_count[0] and lengths outside [1, page_size * max_pages] are left
+ * untouched, as is a row whose range reaches a page entry outside
+ * [0, pool_pages).  D is 64 or 128; q_heads / kv_heads must divide 64. */
+int tmc_prefill_attention_f16(const void *q, const void *key_pool, const void *value_pool,
+                              const int32_t *valid_lengths, const int32_t *block_table,
+                              const int32_t *active_count, void *out, int64_t rows,
+                              int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                              int64_t page_size, int64_t max_pages, int64_t pool_pages,
+                              int64_t page_stride, int64_t head_stride, void *stream);
 
 /* emitTokenArgmax (TransformerDecodeMetalEmitter.cpp:198-256): greedy token
  * per row over fp32 logits, ties to the lowest index. */

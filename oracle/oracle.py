@@ -207,6 +207,23 @@ def paged_attention(q, k_pool, v_pool, dtype: int, q_heads: int, kv_heads: int, 
     return out, written.astype(bool)
 
 
+def causal_prefill_attention(q, k_pool, v_pool, dtype: int, q_heads: int, kv_heads: int,
+                             head_dim: int, page_size: int, page_stride: int, head_stride: int,
+                             block_table, max_pages: int, valid: int, chunk: int,
+                             active_count: int | None = None):
+    """Causal chunk attention of emitPagedKVAttention with causalPrefill
+    (KVCacheMetalEmitter.cpp:159-163, queryLength = chunk): query row r of a
+    chunk of ``chunk`` tokens attends ``valid - chunk + r + 1`` positions of
+    one request's pages, ``valid`` being the cache length with the chunk
+    appended.  Each row is tmco_paged_attention at that length over the
+    request's one block table; returns (out [chunk, q_heads*D], written)."""
+    lengths = np.array([valid - chunk + r + 1 for r in range(chunk)], np.int32)
+    tables = np.tile(np.asarray(block_table, np.int32).reshape(1, max_pages), (chunk, 1))
+    return paged_attention(q, k_pool, v_pool, dtype, q_heads, kv_heads, head_dim, page_size,
+                           page_stride, head_stride, tables, max_pages, lengths,
+                           chunk if active_count is None else active_count)
+
+
 def argmax(logits) -> np.ndarray:
     x = np.ascontiguousarray(logits, dtype=np.float32)
     rows, vocab = x.shape

@@ -191,6 +191,45 @@ def test_paged_attention_matches_contiguous_through_tables(orc, golden):
     assert not written.any()
 
 
+def test_causal_prefill_attention_is_masked_softmax(orc):
+    """The causal chunk rule (query r of a chunk of S attends valid - S + r + 1
+    positions) against textbook causal attention written independently here:
+    softmax(Q K^T / sqrt(D) + M) V with M = -inf above the diagonal shifted by
+    the tokens before the chunk (GQA 4:2, pages out of order, a 3-token
+    prefix).  The last row of a chunk is the decode rule (valid positions),
+    and a chunk of one is a decode step."""
+    rng = np.random.default_rng(17)
+    d, qh, kvh, p, pages = 16, 4, 2, 4, 6
+    start, chunk = 3, 9
+    valid = start + chunk
+    pool_k = orc.f16(rng.standard_normal((pages, kvh, p, d)))
+    pool_v = orc.f16(rng.standard_normal((pages, kvh, p, d)))
+    table = np.array([4, 1, 5, 0], np.int32)  # 12 positions
+    q = orc.f16(rng.standard_normal((chunk, qh * d)))
+    out, written = orc.causal_prefill_attention(q, pool_k, pool_v, F16, qh, kvh, d, p,
+                                                kvh * p * d, p * d, table, 4, valid, chunk)
+    assert written.all()
+    kf = orc.f16_values(pool_k)[table].transpose(1, 0, 2, 3).reshape(kvh, 4 * p, d)[:, :valid]
+    vf = orc.f16_values(pool_v)[table].transpose(1, 0, 2, 3).reshape(kvh, 4 * p, d)[:, :valid]
+    qf = orc.f16_values(q).reshape(chunk, qh, d).astype(np.float64)
+    mask = np.arange(valid)[None, :] <= (start + np.arange(chunk))[:, None]  # [chunk, valid]
+    expect = np.empty((chunk, qh, d))
+    for h in range(qh):
+        s = qf[:, h, :] @ kf[h // (qh // kvh)].T.astype(np.float64) / np.sqrt(d)
+        s = np.where(mask, s, -np.inf)
+        w = np.exp(s - s.max(axis=1, keepdims=True))
+        w /= w.sum(axis=1, keepdims=True)
+        expect[:, h, :] = w @ vf[h // (qh // kvh)].astype(np.float64)
+    # the oracle stores outputs in fp16, the textbook form is exact
+    assert np.max(np.abs(out.reshape(chunk, qh, d) - expect)) <= 2e-3 * max(1.0, np.abs(expect).max())
+    last, _ = orc.paged_attention(q[-1:], pool_k, pool_v, F16, qh, kvh, d, p, kvh * p * d, p * d,
+                                  table[None, :], 4, [valid], 1)
+    assert close(out[-1:], last)
+    one, _ = orc.causal_prefill_attention(q[:1], pool_k, pool_v, F16, qh, kvh, d, p, kvh * p * d,
+                                          p * d, table, 4, start + 1, 1)
+    assert close(one, out[:1])
+
+
 def test_argmax_rules(orc):
     x = np.array([[1.0, 3.0, 3.0, 2.0], [np.nan, 0.5, np.nan, 0.5],
                   [-np.inf, -np.inf, -np.inf, -np.inf], [np.nan] * 4], np.float32)
