@@ -40,7 +40,15 @@ constexpr int kPaWaves = kPaThreads / kWave;
 constexpr int kPaVectors = 16 * kPaWaves;  // query vectors per workgroup
 constexpr int kPaBlock = 64;               // positions per K/V block
 constexpr int kKPad = 8;                   // halves of padding per K row in LDS
-constexpr int kVPad = 8;                   // halves of padding per V^T row in LDS
+// V^T rows of 64 + 4 halves (34 dwords): the 16 lanes of one 8-byte LDS
+// access phase (rows j = 0..15, 32 banks) land on distinct bank pairs; a
+// 36-dword row stride puts rows j and j + 8 on the same banks.
+constexpr int kVPad = 4;                   // halves of padding per V^T row in LDS
+constexpr size_t kPaMaxLds = 64 * 1024;    // LDS per workgroup the launch stays within
+#ifndef TMC_PA_PREFETCH
+#define TMC_PA_PREFETCH 1
+#endif
+constexpr int kPaPrefetch = TMC_PA_PREFETCH;  // K/V blocks in flight per workgroup
 
 struct PrefillParams {
   const half_t* q;       // [rows, q_heads, D]
@@ -51,8 +59,10 @@ struct PrefillParams {
   const int32_t* table;  // [max_pages] pages of the request
   const int32_t* active; // [1] query tokens present
   long page_stride, head_stride, pool_pages;
+  unsigned pool_bytes;   // bytes of each pool when below 4 GiB (buffer loads), else 0
   int rows, q_heads, kv_heads, group, tokens_per_tile, tiles;
   int page_size, max_pages;
+  int page_shift;        // log2(page_size) when it is a power of two, else -1
   float scale_log2;
 };
 
@@ -69,37 +79,60 @@ struct PaBlockRegs {
 };
 
 // Global loads of one 64-position block into registers (zero where the
-// position is at or past `end` or its page is absent).
-template <int D>
-__device__ __forceinline__ void pa_load(const PrefillParams& p, int kvh, int base, int end,
-                                        PaBlockRegs<D>& r) {
+// position is at or past `end` or its page is absent).  BUF (pools below
+// 4 GiB): raw buffer loads with the out-of-range offset for absent data, so
+// every load issues unconditionally; otherwise predicated global loads.
+template <int D, bool BUF>
+__device__ __forceinline__ void pa_load(const PrefillParams& p, const int* table, int kvh, int base,
+                                        int end, PaBlockRegs<D>& r) {
+  using R = PaBlockRegs<D>;
   constexpr int CH = D / 8;  // 16-byte chunks per position
+  const int tid = (int)threadIdx.x;
+  __builtin_assume(tid < kPaThreads);
+  const bool pow2 = p.page_shift >= 0;
+  // Element offset of (pos, 8-element column), or -1 when absent; computed
+  // with selects only (table[0] exists whenever end > 0).
+  auto at = [&](int pos, int column) -> long {
+    const bool in_range = pos < end;
+    const int slot = pow2 ? pos >> p.page_shift : pos / p.page_size;
+    const int row = pow2 ? pos & (p.page_size - 1) : pos - slot * p.page_size;
+    const int page = table[in_range ? slot : 0];
+    const bool ok = in_range && page >= 0 && page < p.pool_pages;
+    if constexpr (BUF) {  // below 4 GiB: 32-bit element offsets
+      const unsigned e = (unsigned)page * (unsigned)p.page_stride +
+                         (unsigned)kvh * (unsigned)p.head_stride + (unsigned)(row * D + column);
+      return ok ? (long)e : -1;
+    } else {
+      const long e = (long)page * p.page_stride + (long)kvh * p.head_stride + (long)row * D + column;
+      return ok ? e : -1;
+    }
+  };
   const h8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  const __amdgpu_buffer_rsrc_t rk = buffer_resource(p.k, p.pool_bytes);
+  const __amdgpu_buffer_rsrc_t rv = buffer_resource(p.v, p.pool_bytes);
 #pragma unroll
-  for (int i = 0; i < PaBlockRegs<D>::kPer; ++i) {
-    const int item = threadIdx.x + i * kPaThreads;
-    const int pos = base + item / CH, chunk = item % CH;
-    r.k[i] = zero;
-    if (item < PaBlockRegs<D>::kItems && pos < end) {
-      const int page = p.table[pos / p.page_size];
-      if (page >= 0 && page < p.pool_pages)
-        r.k[i] = load_h8(p.k + (long)page * p.page_stride + (long)kvh * p.head_stride +
-                         (long)(pos % p.page_size) * D + 8 * chunk);
+  for (int i = 0; i < R::kPer; ++i) {
+    const int item = tid + i * kPaThreads;
+    long e = at(base + item / CH, 8 * (item % CH));
+    if constexpr (R::kItems % kPaThreads != 0) e = item < R::kItems ? e : -1;
+    if constexpr (BUF) {
+      r.k[i] = buffer_load_h8(rk, e < 0 ? kBufferAbsent : (unsigned)e * 2u);
+    } else {
+      r.k[i] = e < 0 ? zero : load_h8(p.k + e);
     }
   }
 #pragma unroll
-  for (int i = 0; i < PaBlockRegs<D>::vPer; ++i) {
-    const int item = threadIdx.x + i * kPaThreads;
+  for (int i = 0; i < R::vPer; ++i) {
+    const int item = tid + i * kPaThreads;
     const int quad = item % (kPaBlock / 4), octet = item / (kPaBlock / 4);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int pos = base + 4 * quad + e;
-      r.v[e][i] = zero;
-      if (item < PaBlockRegs<D>::vItems && pos < end) {
-        const int page = p.table[pos / p.page_size];
-        if (page >= 0 && page < p.pool_pages)
-          r.v[e][i] = load_h8(p.v + (long)page * p.page_stride + (long)kvh * p.head_stride +
-                              (long)(pos % p.page_size) * D + 8 * octet);
+    for (int q = 0; q < 4; ++q) {
+      long e = at(base + 4 * quad + q, 8 * octet);
+      if constexpr (R::vItems % kPaThreads != 0) e = item < R::vItems ? e : -1;
+      if constexpr (BUF) {
+        r.v[q][i] = buffer_load_h8(rv, e < 0 ? kBufferAbsent : (unsigned)e * 2u);
+      } else {
+        r.v[q][i] = e < 0 ? zero : load_h8(p.v + e);
       }
     }
   }
@@ -107,8 +140,17 @@ __device__ __forceinline__ void pa_load(const PrefillParams& p, int kvh, int bas
 
 // Registers -> LDS: K row-major [64][D + kKPad], V transposed [D][64 + kVPad].
 template <int D>
-__device__ __forceinline__ void pa_store(const PaBlockRegs<D>& r, half_t* sk, half_t* svt) {
+__device__ __forceinline__ void pa_store(PaBlockRegs<D>& r, half_t* sk, half_t* svt) {
   constexpr int CH = D / 8;
+  // Pin the loaded registers here (after the barrier that precedes this
+  // call): without it the compiler moves the V transposition up to the
+  // loads and waits for each load as soon as it is issued.
+#pragma unroll
+  for (int i = 0; i < PaBlockRegs<D>::kPer; ++i) asm volatile("" : "+v"(r.k[i]));
+#pragma unroll
+  for (int i = 0; i < PaBlockRegs<D>::vPer; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) asm volatile("" : "+v"(r.v[q][i]));
 #pragma unroll
   for (int i = 0; i < PaBlockRegs<D>::kPer; ++i) {
     const int item = threadIdx.x + i * kPaThreads;
@@ -128,13 +170,78 @@ __device__ __forceinline__ void pa_store(const PaBlockRegs<D>& r, half_t* sk, ha
   }
 }
 
+// One staged 64-position block for this lane's query column: scores on
+// MFMA, online softmax in the log2 domain, then O^T += V^T P^T on MFMA.
 template <int D>
+__device__ __forceinline__ void pa_compute(const PrefillParams& p, const half_t* s_k,
+                                           const half_t* s_vt, const h8 (&qb)[D / 32], int base,
+                                           int len, int j, int g, float& m, float& lsum,
+                                           f4 (&o)[D / 16]) {
+  constexpr int KS = D / 32;
+  constexpr int DT = D / 16;
+  // Scores S^T[pos][query] for 4 tiles of 16 positions.
+  float sc[4][4];
+  float bmax = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt) {
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const half_t* krow = s_k + (16 * kt + j) * (D + kKPad) + 8 * g;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const h8*>(krow + 32 * s),
+                                                   qb[s], acc, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int pos = base + 16 * kt + 4 * g + r;
+      sc[kt][r] = pos < len ? acc[r] * p.scale_log2 : -INFINITY;
+      bmax = fmaxf(bmax, sc[kt][r]);
+    }
+  }
+  bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
+  bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+  const float next = fmaxf(m, bmax);
+  const float alpha = next == -INFINITY ? 1.0f : fast_exp2(m - next);
+  m = next;
+  h8 pb[2];
+  float psum = 0.0f;
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float pr = sc[kt][r] == -INFINITY ? 0.0f : fast_exp2(sc[kt][r] - next);
+      const half_t ph = (half_t)pr;
+      psum += (float)ph;  // the denominator sums the weights the product uses
+      pb[kt >> 1][4 * (kt & 1) + r] = ph;
+    }
+  lsum = lsum * alpha + psum;
+#pragma unroll
+  for (int t = 0; t < DT; ++t) o[t] *= alpha;
+  // O^T[d][query] += V^T[d][pos] P^T[pos][query]; slot 8g+e of step c is
+  // position 32c + 4g + e (e < 4) or 32c + 16 + 4g + (e - 4).
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    const half_t* vrow = s_vt + (16 * t + j) * (kPaBlock + kVPad) + 4 * g;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const h4 lo = *reinterpret_cast<const h4*>(vrow + 32 * c);
+      const h4 hi = *reinterpret_cast<const h4*>(vrow + 32 * c + 16);
+      const h8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[c], o[t], 0, 0, 0);
+    }
+  }
+}
+
+// TLDS: the request's block table is staged in LDS (dynamic, max_pages
+// entries) so a block's K/V addresses need no global round trip first.
+// NB: blocks whose loads are in flight at once.  BUF: see pa_load.
+template <int D, bool TLDS, int NB, bool BUF>
 __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillParams p) {
   constexpr int KS = D / 32;  // k-steps of the score product
   constexpr int DT = D / 16;  // 16-dim output tiles
   __shared__ __attribute__((aligned(16))) half_t s_k[kPaBlock * (D + kKPad)];
   __shared__ __attribute__((aligned(16))) half_t s_vt[D * (kPaBlock + kVPad)];
   __shared__ int s_bounds[2];
+  extern __shared__ int s_table[];
 
   // Workgroup -> (kv head, tile).  With kv_heads a multiple of 8, the tiles
   // of one kv head stay on one XCD (workgroups are dealt to the 8 XCDs
@@ -183,6 +290,7 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillPa
     int first_bad = 0x7fffffff;
     for (int i = threadIdx.x; i < pages; i += kPaThreads) {
       const int page = p.table[i];
+      if (TLDS) s_table[i] = page;
       if (page < 0 || page >= p.pool_pages) first_bad = min(first_bad, i);
     }
     if (first_bad != 0x7fffffff) atomicMin(&s_bounds[1], first_bad);
@@ -202,62 +310,23 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillPa
   for (int t = 0; t < DT; ++t) o[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   float m = -INFINITY, lsum = 0.0f;
 
-  PaBlockRegs<D> regs;
-  pa_load<D>(p, kvh, 0, end, regs);
-  for (int base = 0; base < end; base += kPaBlock) {
-    __syncthreads();  // the previous block's LDS reads are done
-    pa_store<D>(regs, s_k, s_vt);
-    __syncthreads();
-    if (base + kPaBlock < end) pa_load<D>(p, kvh, base + kPaBlock, end, regs);
-
-    // Scores S^T[pos][query] for 4 tiles of 16 positions.
-    float sc[4][4];
-    float bmax = -INFINITY;
+  const int* table = TLDS ? s_table : p.table;
+  // NB blocks in flight: the loads of block i + NB are issued right after
+  // block i is in LDS, so a load has NB blocks of compute to arrive.
+  PaBlockRegs<D> regs[NB];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-      const half_t* krow = s_k + (16 * kt + j) * (D + kKPad) + 8 * g;
+  for (int b = 0; b < NB; ++b) pa_load<D, BUF>(p, table, kvh, b * kPaBlock, end, regs[b]);
+  for (int base = 0; base < end; base += NB * kPaBlock) {
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const h8*>(krow + 32 * s),
-                                                     qb[s], acc, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int pos = base + 16 * kt + 4 * g + r;
-        sc[kt][r] = pos < len ? acc[r] * p.scale_log2 : -INFINITY;
-        bmax = fmaxf(bmax, sc[kt][r]);
-      }
-    }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, kWave));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
-    const float next = fmaxf(m, bmax);
-    const float alpha = next == -INFINITY ? 1.0f : fast_exp2(m - next);
-    m = next;
-    h8 pb[2];
-    float psum = 0.0f;
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float pr = sc[kt][r] == -INFINITY ? 0.0f : fast_exp2(sc[kt][r] - next);
-        const half_t ph = (half_t)pr;
-        psum += (float)ph;  // the denominator sums the weights the product uses
-        pb[kt >> 1][4 * (kt & 1) + r] = ph;
-      }
-    lsum = lsum * alpha + psum;
-#pragma unroll
-    for (int t = 0; t < DT; ++t) o[t] *= alpha;
-    // O^T[d][query] += V^T[d][pos] P^T[pos][query]; slot 8g+e of step c is
-    // position 32c + 4g + e (e < 4) or 32c + 16 + 4g + (e - 4).
-#pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      const half_t* vrow = s_vt + (16 * t + j) * (kPaBlock + kVPad) + 4 * g;
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const h4 lo = *reinterpret_cast<const h4*>(vrow + 32 * c);
-        const h4 hi = *reinterpret_cast<const h4*>(vrow + 32 * c + 16);
-        const h8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[c], o[t], 0, 0, 0);
+    for (int b = 0; b < NB; ++b) {
+      const int blk = base + b * kPaBlock;
+      if (blk < end) {  // uniform across the workgroup
+        __syncthreads();  // the previous block's LDS reads are done
+        pa_store<D>(regs[b], s_k, s_vt);
+        __syncthreads();
+        if (blk + NB * kPaBlock < end)
+          pa_load<D, BUF>(p, table, kvh, blk + NB * kPaBlock, end, regs[b]);
+        pa_compute<D>(p, s_k, s_vt, qb, blk, len, j, g, m, lsum, o);
       }
     }
   }
@@ -468,11 +537,37 @@ extern "C" int tmc_prefill_attention_f16(const void* q, const void* key_pool, co
   p.tiles = (int)((rows + p.tokens_per_tile - 1) / p.tokens_per_tile);
   p.page_size = (int)page_size;
   p.max_pages = (int)max_pages;
+  p.page_shift = -1;
+  for (int b = 0; b < 31; ++b)
+    if (page_size == (int64_t)1 << b) p.page_shift = b;
   p.scale_log2 = (float)(1.0 / std::sqrt((double)head_dim)) * 1.4426950408889634f;
   const dim3 grid((unsigned)((int64_t)p.tiles * kv_heads));
-  if (head_dim == 128)
-    hipLaunchKernelGGL(prefill_attention_kernel<128>, grid, dim3(kPaThreads), 0, as_stream(stream), p);
-  else
-    hipLaunchKernelGGL(prefill_attention_kernel<64>, grid, dim3(kPaThreads), 0, as_stream(stream), p);
+  // The table goes to LDS when it fits beside the K/V blocks in 64 KiB.
+  const size_t static_lds = (size_t)kPaBlock * (head_dim + kKPad) * 2 +
+                            (size_t)head_dim * (kPaBlock + kVPad) * 2 + 16;
+  const size_t table_lds = (size_t)max_pages * 4;
+  const bool tlds = static_lds + table_lds <= kPaMaxLds;
+  const size_t dyn = tlds ? table_lds : 0;
+  const hipStream_t s = as_stream(stream);
+  constexpr int NB = kPaPrefetch;
+  const uint64_t pool_bytes = (uint64_t)pool_pages * (uint64_t)page_stride * 2;
+  const bool buf = pool_bytes < kBufferAbsent;
+  p.pool_bytes = buf ? (unsigned)pool_bytes : 0u;
+#define TMC_PA_LAUNCH(DIM, T, B)                                                                  \
+  hipLaunchKernelGGL((prefill_attention_kernel<DIM, T, NB, B>), grid, dim3(kPaThreads), dyn, s, p)
+  if (head_dim == 128) {
+    if (tlds) {
+      if (buf) TMC_PA_LAUNCH(128, true, true); else TMC_PA_LAUNCH(128, true, false);
+    } else {
+      if (buf) TMC_PA_LAUNCH(128, false, true); else TMC_PA_LAUNCH(128, false, false);
+    }
+  } else {
+    if (tlds) {
+      if (buf) TMC_PA_LAUNCH(64, true, true); else TMC_PA_LAUNCH(64, true, false);
+    } else {
+      if (buf) TMC_PA_LAUNCH(64, false, true); else TMC_PA_LAUNCH(64, false, false);
+    }
+  }
+#undef TMC_PA_LAUNCH
   return check_launch("prefill_attention_kernel");
 }

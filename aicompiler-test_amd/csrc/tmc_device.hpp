@@ -105,4 +105,18 @@ template <int FROM> __device__ __forceinline__ float cross_max(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Raw buffer loads: an offset at or past the resource's byte count reads as
+// zero, so an absent element needs a select, not a branch.
+constexpr unsigned kBufferAbsent = 0xFFFFFFF0u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_resource(const void* base,
+                                                                  unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ h8 buffer_load_h8(__amdgpu_buffer_rsrc_t r, unsigned byte_offset) {
+  return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_offset, 0, 0));
+}
+
 }  // namespace tmc

@@ -434,7 +434,8 @@ DecodeThroughput measureDecodeThroughput(hip::HipRuntime& runtime,
                                          std::shared_ptr<DecoderLLMModelResources> model,
                                          const std::vector<std::vector<std::int32_t>>& prompts,
                                          std::size_t decodeTokens, std::size_t pageSize,
-                                         bool timeGpu, bool tuneKernels) {
+                                         bool timeGpu, bool tuneKernels,
+                                         std::size_t prefillChunkSize) {
   DecodeThroughput result;
   try {
     if (!model || prompts.empty() || pageSize == 0)
@@ -502,8 +503,64 @@ DecodeThroughput measureDecodeThroughput(hip::HipRuntime& runtime,
       return out.nextTokenIds;
     };
 
+    std::unique_ptr<ChunkedPrefillExecutor> prefill;
+    if (prefillChunkSize != 0) {
+      auto made = createChunkedPrefillExecutor(runtime, model, pools,
+                                               std::min(prefillChunkSize, plan.attention.capacity));
+      if (!made.executor) throw std::runtime_error(made.errorMessage);
+      prefill = std::move(made.executor);
+      // One chunk per stage on row 0's states, then released: the prompt
+      // GEMMs pick their library algorithms here, outside the timed phase.
+      for (const auto rows : prefill->buckets()) {
+        std::vector<std::vector<std::int32_t>> tables;
+        for (auto& state : states[0]) {
+          const auto error = state->stageLength(runtime, rows);
+          if (!error.empty()) throw std::runtime_error(error);
+          auto table = state->pageTable();
+          table.resize(prefill->maxPages(), -1);
+          tables.push_back(std::move(table));
+        }
+        const auto out = prefill->run(std::vector<std::int32_t>(rows, 0), 0, tables, false, false);
+        if (!out.passed) throw std::runtime_error(out.errorMessage);
+        for (auto& state : states[0]) {
+          const auto error = state->reset(runtime);
+          if (!error.empty()) throw std::runtime_error(error);
+        }
+      }
+      result.prefillChunkSize = prefill->chunkSize();
+    }
+
     const auto promptStart = Clock::now();
-    for (std::size_t t = 0; t < longest; ++t) {
+    if (prefill) {
+      // Each prompt in chunks through the prefill stage; the last row's
+      // greedy token is the request's first generated token.
+      for (std::size_t r = 0; r < B; ++r) {
+        const auto& prompt = prompts[r];
+        for (std::size_t start = 0; start < prompt.size();) {
+          const std::size_t count = std::min(prefill->chunkSize(), prompt.size() - start);
+          std::vector<std::vector<std::int32_t>> tables;
+          for (auto& state : states[r]) {
+            const auto error = state->stageLength(runtime, start + count);
+            if (!error.empty()) throw std::runtime_error(error);
+            auto table = state->pageTable();
+            table.resize(prefill->maxPages(), -1);
+            tables.push_back(std::move(table));
+          }
+          const std::vector<std::int32_t> tokens(prompt.begin() + static_cast<std::ptrdiff_t>(start),
+                                                 prompt.begin() +
+                                                     static_cast<std::ptrdiff_t>(start + count));
+          const auto out = prefill->run(tokens, start, tables, false, false);
+          if (!out.passed) throw std::runtime_error(out.errorMessage);
+          for (auto& state : states[r]) state->commitLength(start + count);
+          start += count;
+          if (start == prompt.size()) {
+            last[r] = static_cast<std::int32_t>(out.nextTokenIds.back());
+            result.generatedTokenIds[r].push_back(out.nextTokenIds.back());
+          }
+        }
+      }
+    }
+    for (std::size_t t = 0; !prefill && t < longest; ++t) {
       std::vector<std::size_t> rows;
       std::vector<std::int32_t> tokens;
       for (std::size_t r = 0; r < B; ++r)
@@ -519,6 +576,10 @@ DecodeThroughput measureDecodeThroughput(hip::HipRuntime& runtime,
         }
     }
     result.promptPhaseUs = elapsedUs(promptStart, Clock::now());
+    std::size_t promptTokens = 0;
+    for (const auto& prompt : prompts) promptTokens += prompt.size();
+    if (result.promptPhaseUs > 0.0)
+      result.promptTokensPerSecond = static_cast<double>(promptTokens) * 1e6 / result.promptPhaseUs;
 
     std::vector<std::size_t> all(B);
     for (std::size_t r = 0; r < B; ++r) all[r] = r;

@@ -115,13 +115,18 @@ using BatchedStep = std::function<BatchedDecodeRun(
 
 // Steady-state decode throughput of `prompts.size()` requests decoding
 // together: every prompt is first run through batched steps (prefill by
-// decode, rows leave the batch when their prompt ends), then all rows decode
-// `decodeTokens` greedy tokens in lock-step; that second phase is timed.
+// decode, rows leave the batch when their prompt ends) or, with
+// prefillChunkSize > 0, request by request through the chunked prefill
+// executor (its library GEMM algorithms are chosen before the prompt phase
+// starts); then all rows decode `decodeTokens` greedy tokens in lock-step.
+// Both phases are timed on the host clock.
 struct DecodeThroughput {
   bool passed = false;
   std::size_t rows = 0;
   std::size_t decodeSteps = 0;
   double promptPhaseUs = 0.0;
+  double promptTokensPerSecond = 0.0;  // prompt tokens / promptPhaseUs
+  std::size_t prefillChunkSize = 0;    // 0: prompts ran one token per batched step
   double decodePhaseUs = 0.0;      // host wall time of the timed steps
   double tokensPerSecond = 0.0;    // rows * decodeSteps / decodePhaseUs
   benchmark::Statistics stepGpu;   // per timed step, HIP-event time
@@ -134,6 +139,7 @@ struct DecodeThroughput {
 [[nodiscard]] DecodeThroughput measureDecodeThroughput(
     hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
     const std::vector<std::vector<std::int32_t>>& prompts, std::size_t decodeTokens,
-    std::size_t pageSize, bool timeGpu, bool tuneKernels = false);
+    std::size_t pageSize, bool timeGpu, bool tuneKernels = false,
+    std::size_t prefillChunkSize = 0);
 
 }  // namespace tensor::runtime

@@ -488,12 +488,12 @@ PYBIND11_MODULE(_tmc_host, m) {
   m.def("measure_decode_throughput",
         [](hip::HipRuntime& rt, std::shared_ptr<DecoderLLMModelResources> model,
            const std::vector<std::vector<std::int32_t>>& prompts, std::size_t decodeTokens,
-           std::size_t pageSize, bool timeGpu, bool tune) {
+           std::size_t pageSize, bool timeGpu, bool tune, std::size_t prefillChunk) {
           DecodeThroughput r;
           {
             py::gil_scoped_release release;
             r = measureDecodeThroughput(rt, std::move(model), prompts, decodeTokens, pageSize,
-                                        timeGpu, tune);
+                                        timeGpu, tune, prefillChunk);
           }
           py::dict d;
           d["passed"] = r.passed;
@@ -501,6 +501,8 @@ PYBIND11_MODULE(_tmc_host, m) {
           d["rows"] = r.rows;
           d["decode_steps"] = r.decodeSteps;
           d["prompt_phase_us"] = r.promptPhaseUs;
+          d["prompt_tokens_per_second"] = r.promptTokensPerSecond;
+          d["prefill_chunk_size"] = r.prefillChunkSize;
           d["decode_phase_us"] = r.decodePhaseUs;
           d["tokens_per_second"] = r.tokensPerSecond;
           d["step_gpu"] = statsToDict(r.stepGpu);
@@ -510,7 +512,8 @@ PYBIND11_MODULE(_tmc_host, m) {
           return d;
         },
         py::arg("runtime"), py::arg("model"), py::arg("prompts"), py::arg("decode_tokens"),
-        py::arg("page_size") = 16, py::arg("time_gpu") = false, py::arg("tune_kernels") = false);
+        py::arg("page_size") = 16, py::arg("time_gpu") = false, py::arg("tune_kernels") = false,
+        py::arg("prefill_chunk_size") = 0);
 
   // The scheduler over host-only pools and a Python step (CPU tests):
   // step(tokens, valid_lengths, tables, read_logits) -> (next_tokens, logits).

@@ -293,13 +293,16 @@ def extra_measurements(tmc, torch, iters: int) -> dict:
 
 
 C5 = dict(layers=32, hidden=4096, heads=32, head_dim=128, intermediate=11008, vocabulary=32000,
-          capacity=1024, epsilon=1e-6, page_size=16, decode_tokens=128)
+          capacity=1024, epsilon=1e-6, page_size=16, decode_tokens=128, prefill_chunk=512)
+# Chunked prefill of one long prompt on the same 7B shape (capacity 4096).
+PREFILL = dict(capacity=4096, prompts=(4095, 512), chunks=(512, 2048))
 
 
-def c5_plan(host):
+def c5_plan(host, capacity=None):
     plan = host.DecoderLLMPlan()
     att = host.KVCachePlan()
-    att.heads, att.head_dimension, att.capacity = C5["heads"], C5["head_dim"], C5["capacity"]
+    att.heads, att.head_dimension = C5["heads"], C5["head_dim"]
+    att.capacity = capacity or C5["capacity"]
     att.dtype = host.DType.Float16
     plan.attention = att
     plan.layer_count, plan.intermediate_size = C5["layers"], C5["intermediate"]
@@ -316,14 +319,15 @@ def c5_prompts(batch: int):
 
 def c5_gpu(tmc) -> dict:
     """Decode tokens/s of the 7B-shaped model at batch 1 and 16 (C++ host
-    layer: graph-captured batched decode over paged KV pools)."""
+    layer: graph-captured batched decode over paged KV pools).  Prompts run
+    through the chunked prefill executor first (its own timed phase)."""
     host = tmc.host()
     rt = host.HipRuntime()
     model = host.create_synthetic_model_resources(rt, c5_plan(host), 501)
     out = {"model_bytes": int(model.storage_bytes)}
     for batch in (1, 16):
         r = host.measure_decode_throughput(rt, model, c5_prompts(batch), C5["decode_tokens"],
-                                           C5["page_size"], False)
+                                           C5["page_size"], False, False, C5["prefill_chunk"])
         if not r["passed"]:
             raise RuntimeError(f"C5 batch {batch}: {r['error']}")
         steps = r["decode_steps"]
@@ -335,7 +339,52 @@ def c5_gpu(tmc) -> dict:
         out[f"b{batch}_weight_and_kv_gbps"] = round(
             (weights * steps + r["kv_bytes_read"]) / (r["decode_phase_us"] * 1e3), 1)
         out[f"b{batch}_prompt_tokens"] = sum(len(p) for p in c5_prompts(batch))
-        print(f"[bench] C5 batch {batch}: {out[f'b{batch}_tokens_per_s']} tokens/s", flush=True)
+        out[f"b{batch}_prompt_ms"] = round(r["prompt_phase_us"] / 1e3, 2)
+        out[f"b{batch}_prompt_tokens_per_s"] = round(r["prompt_tokens_per_second"], 1)
+        print(f"[bench] C5 batch {batch}: {out[f'b{batch}_tokens_per_s']} tokens/s, prompts "
+              f"{out[f'b{batch}_prompt_tokens_per_s']} tokens/s", flush=True)
+    out["prefill_chunk"] = C5["prefill_chunk"]
+    del model
+    return out
+
+
+def prefill_flops(tokens: int) -> float:
+    """Prompt FLOPs of the 7B shape: 2 per weight per token for every matrix
+    (q.k.v, o, gate, up, down in 32 layers, and the LM head on every row) plus
+    causal attention, 4 * D * heads per attended position per layer."""
+    h, i, v, layers = C5["hidden"], C5["intermediate"], C5["vocabulary"], C5["layers"]
+    weights = layers * (h * 3 * h + h * h + 3 * h * i) + v * h
+    attended = tokens * (tokens + 1) / 2
+    return 2.0 * weights * tokens + 4.0 * C5["head_dim"] * C5["heads"] * layers * attended
+
+
+def prefill_gpu(tmc) -> dict:
+    """Chunked prefill throughput of the 7B shape: one prompt per run through
+    hipBLASLt prompt GEMMs and the MFMA causal chunk attention; TFLOP/s
+    against the 2.5 PFLOP/s dense fp16 peak."""
+    host = tmc.host()
+    rt = host.HipRuntime()
+    model = host.create_synthetic_model_resources(rt, c5_plan(host, PREFILL["capacity"]), 503)
+    import numpy as np
+    rng = np.random.default_rng(504)
+    out = {"capacity": PREFILL["capacity"]}
+    for length in PREFILL["prompts"]:
+        prompt = [list(map(int, rng.integers(0, C5["vocabulary"], length)))]
+        for chunk in PREFILL["chunks"]:
+            if chunk > length and chunk != PREFILL["chunks"][0]:
+                continue
+            r = host.measure_decode_throughput(rt, model, prompt, 1, C5["page_size"], False, False,
+                                               chunk)
+            if not r["passed"]:
+                raise RuntimeError(f"prefill {length}/{chunk}: {r['error']}")
+            sec = r["prompt_phase_us"] / 1e6
+            key = f"p{length}_c{chunk}"
+            out[key + "_ms"] = round(sec * 1e3, 2)
+            out[key + "_tokens_per_s"] = round(length / sec, 1)
+            out[key + "_tflops"] = round(prefill_flops(length) / sec / 1e12, 1)
+            print(f"[bench] prefill {length} tokens, chunk {chunk}: {out[key + '_ms']} ms, "
+                  f"{out[key + '_tokens_per_s']} tokens/s", flush=True)
+    out["peak_tflops"] = 2500.0
     del model
     return out
 
@@ -470,6 +519,7 @@ def main() -> int:
         extra["c5_decode"] = c5_gpu(tmc)
         if not args.no_cpu:
             extra["c5_decode"]["cpu_baseline"] = c5_cpu_baseline()
+        extra["prefill"] = prefill_gpu(tmc)
     cpu = None if args.no_cpu else cpu_baseline(block, args.cpu_seconds)
 
     line = {

@@ -117,6 +117,7 @@ CASES = [
     (130, 32, 8, 128, 16, 200, None),
     (48, 16, 1, 64, 5, 7, None),
     (256, 8, 8, 128, 16, 1000, None),
+    (16, 4, 2, 128, 1, 7990, None),  # 8007-entry table: read from global memory, not LDS
 ]
 
 
