@@ -80,9 +80,21 @@ struct DecoderLLMLayerParameters {
   std::vector<float> downWeight;
 };
 
+// A step's reference results (src/tensor/DecoderLLM.hpp:22-28): tokens
+// [batch, seq], logits [batch, seq, vocabulary], next tokens [batch], K/V
+// caches per layer [batch, heads, length, D].
+struct DecoderLLMReference {
+  std::vector<float> tokenIds;
+  std::vector<double> logits;
+  std::vector<double> nextTokenIds;
+  std::vector<std::vector<double>> keyCaches;
+  std::vector<std::vector<double>> valueCaches;
+};
+
 struct DecoderLLMWorkload {
   std::string modelName;
   planner::DecoderLLMPlan plan;
+  DType requestedStorageDtype = DType::Float32;
   std::size_t decodeCount = 0;
   std::vector<float> embeddingWeight;
   std::vector<float> finalNormWeight;
@@ -90,6 +102,8 @@ struct DecoderLLMWorkload {
   std::vector<float> ropeCosine;  // [capacity, head_dim/2]
   std::vector<float> ropeSine;
   std::vector<DecoderLLMLayerParameters> layers;
+  DecoderLLMReference prefill;  // filled by the .tmc importer
+  std::vector<DecoderLLMReference> decodeSteps;
 };
 
 // RoPE tables as in workloads/pytorch/decoder_llm.py:48-55 (angle =

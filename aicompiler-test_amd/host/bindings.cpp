@@ -11,6 +11,7 @@
 
 #include "Benchmark.hpp"
 #include "DecoderLLM.hpp"
+#include "Importer.hpp"
 #include "KVCacheState.hpp"
 #include "ServingRuntime.hpp"
 #include "Tuning.hpp"
@@ -30,6 +31,18 @@ std::vector<float> toVector(const FloatArray& a) {
 py::array_t<float> toArray(const std::vector<float>& v) {
   py::array_t<float> out(static_cast<py::ssize_t>(v.size()));
   std::copy(v.begin(), v.end(), out.mutable_data());
+  return out;
+}
+
+py::array_t<double> toArray(const std::vector<double>& v) {
+  py::array_t<double> out(static_cast<py::ssize_t>(v.size()));
+  std::copy(v.begin(), v.end(), out.mutable_data());
+  return out;
+}
+
+py::list toArrays(const std::vector<std::vector<double>>& vs) {
+  py::list out;
+  for (const auto& v : vs) out.append(toArray(v));
   return out;
 }
 
@@ -297,6 +310,50 @@ PYBIND11_MODULE(_tmc_host, m) {
   weightProperty(workload, "language_model_head_weight", &DecoderLLMWorkload::languageModelHeadWeight);
   weightProperty(workload, "rope_cosine", &DecoderLLMWorkload::ropeCosine);
   weightProperty(workload, "rope_sine", &DecoderLLMWorkload::ropeSine);
+  workload.def_readwrite("requested_storage_dtype", &DecoderLLMWorkload::requestedStorageDtype)
+      .def_readonly("prefill", &DecoderLLMWorkload::prefill)
+      .def_readonly("decode_steps", &DecoderLLMWorkload::decodeSteps);
+
+  py::class_<DecoderLLMReference>(m, "DecoderLLMReference")
+      .def_property_readonly("token_ids", [](const DecoderLLMReference& r) { return toArray(r.tokenIds); })
+      .def_property_readonly("logits", [](const DecoderLLMReference& r) { return toArray(r.logits); })
+      .def_property_readonly("next_token_ids",
+                             [](const DecoderLLMReference& r) { return toArray(r.nextTokenIds); })
+      .def_property_readonly("key_caches", [](const DecoderLLMReference& r) { return toArrays(r.keyCaches); })
+      .def_property_readonly("value_caches",
+                             [](const DecoderLLMReference& r) { return toArrays(r.valueCaches); });
+
+  // importDecoderLLMWorkload / importKVCacheWorkload: (workload or None, error).
+  m.def("import_decoder_llm_workload", [](const std::string& path) {
+    auto r = importer::importDecoderLLMWorkload(path);
+    return py::make_tuple(r.workload ? py::cast(std::move(r.workload)) : py::none(), r.errorMessage);
+  });
+  py::class_<importer::KVCacheReferenceStep>(m, "KVCacheReferenceStep")
+      .def_property_readonly("query", [](const importer::KVCacheReferenceStep& s) { return toArray(s.query); })
+      .def_property_readonly("key", [](const importer::KVCacheReferenceStep& s) { return toArray(s.key); })
+      .def_property_readonly("value", [](const importer::KVCacheReferenceStep& s) { return toArray(s.value); })
+      .def_property_readonly("output", [](const importer::KVCacheReferenceStep& s) { return toArray(s.output); })
+      .def_property_readonly("key_cache",
+                             [](const importer::KVCacheReferenceStep& s) { return toArray(s.keyCache); })
+      .def_property_readonly("value_cache",
+                             [](const importer::KVCacheReferenceStep& s) { return toArray(s.valueCache); });
+  py::class_<importer::ImportedKVCacheWorkload>(m, "ImportedKVCacheWorkload")
+      .def_readonly("model_name", &importer::ImportedKVCacheWorkload::modelName)
+      .def_readonly("plan", &importer::ImportedKVCacheWorkload::plan)
+      .def_property_readonly("query_weight",
+                             [](const importer::ImportedKVCacheWorkload& w) { return toArray(w.queryWeight); })
+      .def_property_readonly("key_weight",
+                             [](const importer::ImportedKVCacheWorkload& w) { return toArray(w.keyWeight); })
+      .def_property_readonly("value_weight",
+                             [](const importer::ImportedKVCacheWorkload& w) { return toArray(w.valueWeight); })
+      .def_property_readonly("output_weight",
+                             [](const importer::ImportedKVCacheWorkload& w) { return toArray(w.outputWeight); })
+      .def_readonly("prefill", &importer::ImportedKVCacheWorkload::prefill)
+      .def_readonly("decode_steps", &importer::ImportedKVCacheWorkload::decodeSteps);
+  m.def("import_kv_cache_workload", [](const std::string& path) {
+    auto r = importer::importKVCacheWorkload(path);
+    return py::make_tuple(r.workload ? py::cast(std::move(r.workload)) : py::none(), r.errorMessage);
+  });
 
   m.def("rope_tables", [](std::size_t capacity, std::size_t headDimension, double theta) {
     std::vector<float> c, s;
