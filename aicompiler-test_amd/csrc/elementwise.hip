@@ -208,14 +208,33 @@ bool launch_norm_threads(const T* r, const T* u, const T* w, T* s, T* n, int64_t
 
 // emitDecoderSiLUMul (DecoderLLMMetalEmitter.cpp:395-415).
 template <typename T>
+__device__ __forceinline__ T silu_mul_one(T gate, T up) {
+  const float g = to_float<T>(gate);
+  const float activated = through<T>(g / (1.0f + expf(-g)));
+  return from_float<T>(activated * to_float<T>(up));
+}
+
+template <typename T>
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const T* __restrict__ gate,
                                                            const T* __restrict__ up,
                                                            T* __restrict__ out, size_t count) {
   for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < count;
+       i += (size_t)gridDim.x * kThreads)
+    out[i] = silu_mul_one<T>(gate[i], up[i]);
+}
+
+// fp16, 16-byte aligned, count % 8 == 0: eight elements per thread with
+// 16-byte loads and stores (same per-element arithmetic).
+__global__ __launch_bounds__(kThreads) void silu_mul_h8_kernel(const h8* __restrict__ gate,
+                                                              const h8* __restrict__ up,
+                                                              h8* __restrict__ out, size_t vectors) {
+  for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < vectors;
        i += (size_t)gridDim.x * kThreads) {
-    const float g = to_float<T>(gate[i]);
-    const float activated = through<T>(g / (1.0f + expf(-g)));
-    out[i] = from_float<T>(activated * to_float<T>(up[i]));
+    const h8 g = gate[i], u = up[i];
+    h8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = silu_mul_one<half_t>(g[e], u[e]);
+    out[i] = r;
   }
 }
 
@@ -428,6 +447,63 @@ __global__ __launch_bounds__(kThreads) void decode_rope_append_kernel(
                      position % page_size) * head_dim + feature % head_dim;
   dst[0] = x0;
   dst[1] = x1;
+}
+
+// fp16 with head_dim % 8 == 0 and 16-byte aligned buffers: one thread per
+// 8 consecutive elements (4 interleaved pairs of one head) with 16-byte
+// loads and stores; the rotation is rotate_pair, so the bits match the
+// one-pair kernel.
+__global__ __launch_bounds__(kThreads) void decode_rope_append_h8_kernel(
+    const half_t* __restrict__ qkv, const float* __restrict__ cosine,
+    const float* __restrict__ sine, const int32_t* __restrict__ valid_lengths,
+    const int32_t* __restrict__ block_tables, const int32_t* __restrict__ active_count,
+    half_t* __restrict__ q_out, half_t* __restrict__ k_pool, half_t* __restrict__ v_pool,
+    int max_batch, int q_heads, int kv_heads, int head_dim, int capacity, int page_size,
+    int table_stride) {
+  const int pairs = head_dim / 2;
+  const int row_octs = (q_heads + 2 * kv_heads) * head_dim / 8;
+  const long gid = (long)blockIdx.x * kThreads + threadIdx.x;
+  const int request = (int)(gid / row_octs);
+  if (request >= max_batch) return;
+  const int active = active_count[0];
+  const int valid = valid_lengths[request];
+  const int column = 8 * (int)(gid % row_octs);
+  const int q_width = q_heads * head_dim, kv_width = kv_heads * head_dim;
+  const h8 x = *reinterpret_cast<const h8*>(qkv + (size_t)request * (q_width + 2 * kv_width) + column);
+  if (request >= active || valid <= 0 || valid > capacity) return;
+  const int position = valid - 1;
+  if (column < q_width + kv_width) {
+    const int pair0 = (column % head_dim) / 2;
+    const f4 c = *reinterpret_cast<const f4*>(cosine + (size_t)position * pairs + pair0);
+    const f4 sn = *reinterpret_cast<const f4*>(sine + (size_t)position * pairs + pair0);
+    h8 y;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float re, ro;
+      rotate_pair((float)x[2 * i], (float)x[2 * i + 1], c[i], sn[i], re, ro);
+      // Round to fp32 first, then to fp16, as the one-pair kernels do: keep
+      // the compiler from folding the fma and the conversion into one
+      // mixed-precision op that rounds once.
+      asm volatile("" : "+v"(re), "+v"(ro));
+      y[2 * i] = (half_t)re;
+      y[2 * i + 1] = (half_t)ro;
+    }
+    if (column < q_width) {
+      *reinterpret_cast<h8*>(q_out + (size_t)request * q_width + column) = y;
+      return;
+    }
+    const int page = block_tables[(size_t)request * table_stride + position / page_size];
+    if (page < 0) return;
+    const int feature = column - q_width;
+    *reinterpret_cast<h8*>(k_pool + (((size_t)page * kv_heads + feature / head_dim) * page_size +
+                                     position % page_size) * head_dim + feature % head_dim) = y;
+    return;
+  }
+  const int page = block_tables[(size_t)request * table_stride + position / page_size];
+  if (page < 0) return;
+  const int feature = column - q_width - kv_width;
+  *reinterpret_cast<h8*>(v_pool + (((size_t)page * kv_heads + feature / head_dim) * page_size +
+                                   position % page_size) * head_dim + feature % head_dim) = x;
 }
 
 __device__ __forceinline__ bool better(float cv, int ci, float bv, int bi) {
@@ -670,6 +746,13 @@ extern "C" int tmc_silu_mul(const void* gate, const void* up, void* out, int dty
                             void* stream) {
   TMC_REQUIRE(gate && up && out, "SiLU*Mul: null device pointer.");
   TMC_REQUIRE(float_dtype(dtype) && count > 0, "SiLU*Mul: invalid dtype or count.");
+  if (dtype == TMC_F16 && count % 8 == 0 && aligned16(gate) && aligned16(up) && aligned16(out)) {
+    const size_t vectors = (size_t)count / 8;
+    hipLaunchKernelGGL(silu_mul_h8_kernel, dim3(grid_for(vectors)), dim3(kThreads), 0,
+                       as_stream(stream), static_cast<const h8*>(gate), static_cast<const h8*>(up),
+                       static_cast<h8*>(out), vectors);
+    return check_launch("silu_mul_h8_kernel");
+  }
   TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((silu_mul_kernel<T>), dim3(grid_for(count)), dim3(kThreads), 0,
                                             as_stream(stream), static_cast<const T*>(gate),
                                             static_cast<const T*>(up), static_cast<T*>(out),
@@ -818,6 +901,19 @@ int launch_rope_append(const void* qkv, const float* cosine, const float* sine,
               "ceil(capacity / page_size)).");
   const size_t items = (size_t)max_batch * (q_heads + 2 * kv_heads) * (head_dim / 2);
   TMC_REQUIRE(items < (1ull << 31), "RoPE+append: too many elements.");
+  const int table_stride = shared_table ? 0 : (int)max_pages;
+  if (dtype == TMC_F16 && head_dim % 8 == 0 && aligned16(qkv) && aligned16(cosine) &&
+      aligned16(sine) && aligned16(q_out) && aligned16(key_pool) && aligned16(value_pool)) {
+    const size_t octs = items / 4;
+    hipLaunchKernelGGL(decode_rope_append_h8_kernel,
+                       dim3((unsigned)((octs + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                       as_stream(stream), static_cast<const half_t*>(qkv), cosine, sine,
+                       valid_lengths, block_tables, active_count, static_cast<half_t*>(q_out),
+                       static_cast<half_t*>(key_pool), static_cast<half_t*>(value_pool),
+                       (int)max_batch, (int)q_heads, (int)kv_heads, (int)head_dim, (int)capacity,
+                       (int)page_size, table_stride);
+    return check_launch("decode_rope_append_h8_kernel");
+  }
   TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((decode_rope_append_kernel<T>),
                                             dim3((unsigned)((items + kThreads - 1) / kThreads)),
                                             dim3(kThreads), 0, as_stream(stream),
@@ -826,8 +922,7 @@ int launch_rope_append(const void* qkv, const float* cosine, const float* sine,
                                             static_cast<T*>(q_out), static_cast<T*>(key_pool),
                                             static_cast<T*>(value_pool), (int)max_batch,
                                             (int)q_heads, (int)kv_heads, (int)head_dim,
-                                            (int)capacity, (int)page_size,
-                                            shared_table ? 0 : (int)max_pages));
+                                            (int)capacity, (int)page_size, table_stride));
   return check_launch("decode_rope_append_kernel");
 }
 }  // namespace

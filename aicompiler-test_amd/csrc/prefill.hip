@@ -45,10 +45,6 @@ constexpr int kKPad = 8;                   // halves of padding per K row in LDS
 // 36-dword row stride puts rows j and j + 8 on the same banks.
 constexpr int kVPad = 4;                   // halves of padding per V^T row in LDS
 constexpr size_t kPaMaxLds = 64 * 1024;    // LDS per workgroup the launch stays within
-#ifndef TMC_PA_PREFETCH
-#define TMC_PA_PREFETCH 1
-#endif
-constexpr int kPaPrefetch = TMC_PA_PREFETCH;  // K/V blocks in flight per workgroup
 
 struct PrefillParams {
   const half_t* q;       // [rows, q_heads, D]
@@ -233,8 +229,8 @@ __device__ __forceinline__ void pa_compute(const PrefillParams& p, const half_t*
 
 // TLDS: the request's block table is staged in LDS (dynamic, max_pages
 // entries) so a block's K/V addresses need no global round trip first.
-// NB: blocks whose loads are in flight at once.  BUF: see pa_load.
-template <int D, bool TLDS, int NB, bool BUF>
+// BUF: see pa_load.
+template <int D, bool TLDS, bool BUF>
 __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillParams p) {
   constexpr int KS = D / 32;  // k-steps of the score product
   constexpr int DT = D / 16;  // 16-dim output tiles
@@ -311,24 +307,17 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillPa
   float m = -INFINITY, lsum = 0.0f;
 
   const int* table = TLDS ? s_table : p.table;
-  // NB blocks in flight: the loads of block i + NB are issued right after
-  // block i is in LDS, so a load has NB blocks of compute to arrive.
-  PaBlockRegs<D> regs[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) pa_load<D, BUF>(p, table, kvh, b * kPaBlock, end, regs[b]);
-  for (int base = 0; base < end; base += NB * kPaBlock) {
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const int blk = base + b * kPaBlock;
-      if (blk < end) {  // uniform across the workgroup
-        __syncthreads();  // the previous block's LDS reads are done
-        pa_store<D>(regs[b], s_k, s_vt);
-        __syncthreads();
-        if (blk + NB * kPaBlock < end)
-          pa_load<D, BUF>(p, table, kvh, blk + NB * kPaBlock, end, regs[b]);
-        pa_compute<D>(p, s_k, s_vt, qb, blk, len, j, g, m, lsum, o);
-      }
-    }
+  // The next block's loads are issued as soon as the current one is in LDS
+  // and land during its compute.  (Two or three blocks in flight measured
+  // no faster.)
+  PaBlockRegs<D> regs;
+  pa_load<D, BUF>(p, table, kvh, 0, end, regs);
+  for (int base = 0; base < end; base += kPaBlock) {
+    __syncthreads();  // the previous block's LDS reads are done
+    pa_store<D>(regs, s_k, s_vt);
+    __syncthreads();
+    if (base + kPaBlock < end) pa_load<D, BUF>(p, table, kvh, base + kPaBlock, end, regs);
+    pa_compute<D>(p, s_k, s_vt, qb, base, len, j, g, m, lsum, o);
   }
 
   lsum += __shfl_xor(lsum, 16, kWave);
@@ -549,12 +538,11 @@ extern "C" int tmc_prefill_attention_f16(const void* q, const void* key_pool, co
   const bool tlds = static_lds + table_lds <= kPaMaxLds;
   const size_t dyn = tlds ? table_lds : 0;
   const hipStream_t s = as_stream(stream);
-  constexpr int NB = kPaPrefetch;
   const uint64_t pool_bytes = (uint64_t)pool_pages * (uint64_t)page_stride * 2;
   const bool buf = pool_bytes < kBufferAbsent;
   p.pool_bytes = buf ? (unsigned)pool_bytes : 0u;
 #define TMC_PA_LAUNCH(DIM, T, B)                                                                  \
-  hipLaunchKernelGGL((prefill_attention_kernel<DIM, T, NB, B>), grid, dim3(kPaThreads), dyn, s, p)
+  hipLaunchKernelGGL((prefill_attention_kernel<DIM, T, B>), grid, dim3(kPaThreads), dyn, s, p)
   if (head_dim == 128) {
     if (tlds) {
       if (buf) TMC_PA_LAUNCH(128, true, true); else TMC_PA_LAUNCH(128, true, false);

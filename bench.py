@@ -447,6 +447,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the chunked prefill measurement and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -456,6 +458,9 @@ def main() -> int:
     import torch
     tmc = load_tmc()
     tmc.lib()
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill_gpu(tmc)}), flush=True)
+        return 0
     block = MlpBlock(tmc, torch, args.batch, args.copies)
     # The timed region replays a HIP graph built by the backend's own
     # PreparedSequence counterpart (tmc_seq_*): one graph holds one step per

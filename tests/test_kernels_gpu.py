@@ -199,6 +199,13 @@ def test_silu_mul_and_add(tmc, orc, torch):
     tmc.silu_mul(dev_f16(g), dev_f16(u), out)
     torch.cuda.synchronize()
     assert_f16_path(values(out), orc.silu_mul(g, u, F16), what="silu_mul fp16")
+    # the 8-wide path (16-byte aligned, count % 8 == 0) and the one-element
+    # path (a 2-byte-offset view) agree bit for bit
+    gd, ud = dev_f16(g).reshape(-1), dev_f16(u).reshape(-1)
+    one = torch.empty(gd.numel() - 1, dtype=torch.float16, device="cuda")
+    tmc.silu_mul(gd[1:], ud[1:], one)
+    torch.cuda.synchronize()
+    assert torch.equal(out.reshape(-1)[1:], one)
     g32, u32 = normal(212, (4097,)) * 8, normal(213, (4097,))
     o32 = torch.empty(4097, dtype=torch.float32, device="cuda")
     tmc.silu_mul(dev(g32), dev(u32), o32)
@@ -417,7 +424,7 @@ def test_rope_decoder_and_serving(tmc, orc, torch):
     assert np.isnan(got[3]).all()
 
 
-@pytest.mark.parametrize("qh,kvh,d", [(32, 32, 128), (32, 8, 128), (4, 2, 64)])
+@pytest.mark.parametrize("qh,kvh,d", [(32, 32, 128), (32, 8, 128), (4, 2, 64), (2, 1, 12)])
 def test_decode_rope_append_is_rope_then_append(tmc, orc, torch, qh, kvh, d):
     """Fused RoPE(q, k) + paged append of k, v (one fused projection row per
     request) equals tmc_serving_rope followed by tmc_serving_kv_append bit for
