@@ -107,12 +107,15 @@ ServingExecutionResult runContinuousBatch(hip::HipRuntime& runtime,
                                           std::size_t maximumBatchSize, std::size_t maxPages,
                                           const BatchedStep& step,
                                           const std::vector<ServingRequestSpec>& specs,
-                                          const ServingConfig& config, std::ostream& log) {
+                                          const ServingConfig& config, std::ostream& log,
+                                          const PrefillStep& prefill) {
   ServingExecutionResult result;
   auto& metrics = result.metrics;
   try {
     if (specs.empty() || config.pageSize == 0 || config.physicalPagesPerLayer == 0)
       throw std::invalid_argument("Serving configuration and requests must be nonempty.");
+    if (config.prefillChunkSize != 0 && !prefill)
+      throw std::invalid_argument("Chunked serving prefill needs a prefill step.");
     if (pools.size() != plan.layerCount || maximumBatchSize == 0)
       throw std::invalid_argument("Serving needs one page pool per layer and a batch size.");
     const std::size_t capacity = plan.attention.capacity, P = config.pageSize;
@@ -210,6 +213,57 @@ ServingExecutionResult runContinuousBatch(hip::HipRuntime& runtime,
         if (!fits) continue;
         r.state = RequestState::Active;
         progress = true;
+      }
+
+      // Chunked prefill of the prompts admitted above (their pages were
+      // counted at admission): the last chunk's last row is the first token.
+      for (auto& r : requests) {
+        if (config.prefillChunkSize == 0 || r.state != RequestState::Active ||
+            r.consumed >= r.prompt.size())
+          continue;
+        while (r.consumed < r.prompt.size()) {
+          const std::size_t start = r.consumed;
+          const std::size_t count = std::min(config.prefillChunkSize, r.prompt.size() - start);
+          const bool last = start + count == r.prompt.size();
+          const auto kvStart = Clock::now();
+          std::vector<std::vector<std::int32_t>> tables;
+          for (auto& state : r.states) {
+            const auto error = state->stageLength(runtime, start + count);
+            if (!error.empty()) {
+              for (auto& s : r.states) (void)s->rollbackLength(runtime, start);
+              throw std::runtime_error("Request " + r.spec.id + " KV stage failed: " + error);
+            }
+            auto table = state->pageTable();
+            table.resize(maxPages, -1);
+            tables.push_back(std::move(table));
+          }
+          metrics.kvManagementOverheadUs += elapsedUs(kvStart, Clock::now());
+          const std::vector<std::int32_t> tokens(
+              r.prompt.begin() + static_cast<std::ptrdiff_t>(start),
+              r.prompt.begin() + static_cast<std::ptrdiff_t>(start + count));
+          const auto out = prefill(tokens, start, tables, last && config.recordPrefillLogits);
+          ++metrics.prefillChunkSubmissions;
+          if (!out.passed || out.nextTokenIds.size() != count) {
+            for (auto& s : r.states) (void)s->rollbackLength(runtime, start);
+            throw std::runtime_error("Chunked prefill failed: " + out.errorMessage);
+          }
+          for (auto& state : r.states) state->commitLength(start + count);
+          r.consumed += count;
+          metrics.promptTokens += count;
+          if (!last) continue;
+          const auto next = static_cast<std::int32_t>(out.nextTokenIds.back());
+          r.output.generatedTokenIds.push_back(static_cast<float>(next));
+          r.lastToken = next;
+          r.output.timeToFirstTokenUs = elapsedUs(*r.arrivalTime, Clock::now());
+          if (config.recordPrefillLogits && !out.logits.empty()) {
+            const auto V = static_cast<std::ptrdiff_t>(plan.vocabularySize);
+            r.output.prefillLogits.assign(out.logits.end() - V, out.logits.end());
+          }
+          log << "Serving request " << r.spec.id << ": prompt complete (chunked), pages="
+              << r.pages() << ", ttft(us)=" << r.output.timeToFirstTokenUs << '\n';
+        }
+        progress = true;
+        if (r.spec.decodeTokenCount == 0) finish(r);
       }
 
       // Pages for every active row's next token; preempt the largest owner
@@ -420,10 +474,25 @@ ServingExecutionResult runContinuousBatch(hip::HipRuntime& runtime,
                                    bool readLogits) {
       return executor.run(tokens, lengths, tables, readLogits, true);
     };
-    result = runContinuousBatch(runtime, plan, pools, M, executor.maxPages(), step, requests, config, log);
+    std::unique_ptr<ChunkedPrefillExecutor> prefillExecutor;
+    PrefillStep prefill;
+    if (config.prefillChunkSize != 0) {
+      auto made = createChunkedPrefillExecutor(runtime, model, pools, config.prefillChunkSize, &log);
+      if (!made.executor) throw std::runtime_error(made.errorMessage);
+      prefillExecutor = std::move(made.executor);
+      prefill = [&prefillExecutor](const std::vector<std::int32_t>& tokens, std::size_t start,
+                                   const std::vector<std::vector<std::int32_t>>& tables,
+                                   bool readLogits) {
+        return prefillExecutor->run(tokens, start, tables, readLogits, false);
+      };
+    }
+    result = runContinuousBatch(runtime, plan, pools, M, executor.maxPages(), step, requests,
+                                config, log, prefill);
     result.metrics.modelStorageBytes = model->storageBytes;
     result.metrics.kvPoolStorageBytes = 2 * plan.layerCount * pools.front()->keyBuffer()->storageBytes();
-    result.metrics.batchedActivationStorageBytes = executor.activationStorageBytes();
+    result.metrics.batchedActivationStorageBytes =
+        executor.activationStorageBytes() +
+        (prefillExecutor ? prefillExecutor->activationStorageBytes() : 0);
   } catch (const std::exception& error) {
     result.errorMessage = error.what();
   }

@@ -17,7 +17,11 @@
 // is consumed, then its last generated token, so prompt and decode rows share
 // one batched step.  The tick that consumes the last prompt token yields the
 // first generated token (the reference's prefill output); each later tick is
-// one decode step.
+// one decode step.  With ServingConfig::prefillChunkSize > 0 an admitted
+// request's prompt instead runs at admission through the chunked prefill
+// executor (the reference's prefillChunked per request,
+// ServingRuntime.cpp:682-700), and the request joins the decode ticks with
+// its first token.
 #pragma once
 
 #include "Benchmark.hpp"
@@ -49,6 +53,9 @@ struct ServingConfig {
   bool recordPrefillLogits = true;
   // Batch-1 GEMVs with the decode GEMV tuner's cached per-shape selection.
   bool tuneKernels = false;
+  // > 0: prompts run at admission in chunks of this many tokens through the
+  // chunked prefill executor; 0: prefill by decode in the batched ticks.
+  std::size_t prefillChunkSize = 0;
 };
 
 struct ServingRequestOutput {
@@ -77,6 +84,7 @@ struct ServingMetrics {
   std::size_t pageAllocationCount = 0;
   std::size_t pageReleaseCount = 0;
   std::size_t decodeCommandSubmissions = 0;
+  std::size_t prefillChunkSubmissions = 0;  // chunked prefill stages run
   std::size_t decodedTokens = 0;
   std::size_t promptTokens = 0;
   std::size_t modelStorageBytes = 0;
@@ -97,14 +105,21 @@ using BatchedStep = std::function<BatchedDecodeRun(
     const std::vector<std::int32_t>& tokens, const std::vector<std::int32_t>& validLengths,
     const std::vector<std::vector<std::int32_t>>& tables, bool readLogits)>;
 
+// One prompt chunk of one request: tokens at positions start.. and the
+// request's per-layer tables in, per-row next tokens (and logits) out.
+using PrefillStep = std::function<BatchedDecodeRun(
+    const std::vector<std::int32_t>& tokens, std::size_t start,
+    const std::vector<std::vector<std::int32_t>>& tables, bool readLogits)>;
+
 // The scheduler over existing pools and any step function (the CPU tests
-// drive it with host-only pools and a host step).
+// drive it with host-only pools and a host step).  `prefill` is used when
+// config.prefillChunkSize > 0.
 [[nodiscard]] ServingExecutionResult runContinuousBatch(
     hip::HipRuntime& runtime, const planner::DecoderLLMPlan& plan,
     const std::vector<std::shared_ptr<KVPagePool>>& pools, std::size_t maximumBatchSize,
     std::size_t maxPages, const BatchedStep& step,
     const std::vector<ServingRequestSpec>& requests, const ServingConfig& config,
-    std::ostream& log);
+    std::ostream& log, const PrefillStep& prefill = {});
 
 // runContinuousBatch (ServingRuntime.cpp:513-930) on the GPU: creates the
 // per-layer pools and the batched decode executor over `model`.

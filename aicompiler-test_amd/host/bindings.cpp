@@ -121,6 +121,7 @@ py::dict servingToDict(const ServingExecutionResult& r) {
   metrics["page_allocation_count"] = m.pageAllocationCount;
   metrics["page_release_count"] = m.pageReleaseCount;
   metrics["decode_command_submissions"] = m.decodeCommandSubmissions;
+  metrics["prefill_chunk_submissions"] = m.prefillChunkSubmissions;
   metrics["decoded_tokens"] = m.decodedTokens;
   metrics["prompt_tokens"] = m.promptTokens;
   metrics["model_storage_bytes"] = m.modelStorageBytes;
@@ -526,7 +527,8 @@ PYBIND11_MODULE(_tmc_host, m) {
       .def_readwrite("maximum_batch_size", &ServingConfig::maximumBatchSize)
       .def_readwrite("record_decode_logits", &ServingConfig::recordDecodeLogits)
       .def_readwrite("record_prefill_logits", &ServingConfig::recordPrefillLogits)
-      .def_readwrite("tune_kernels", &ServingConfig::tuneKernels);
+      .def_readwrite("tune_kernels", &ServingConfig::tuneKernels)
+      .def_readwrite("prefill_chunk_size", &ServingConfig::prefillChunkSize);
 
   m.def("run_continuous_batch",
         [](hip::HipRuntime& rt, std::shared_ptr<DecoderLLMModelResources> model,
@@ -578,7 +580,22 @@ PYBIND11_MODULE(_tmc_host, m) {
         [](hip::HipRuntime& rt, const planner::DecoderLLMPlan& plan,
            const std::vector<std::shared_ptr<KVPagePool>>& pools, std::size_t maxBatch,
            std::size_t maxPages, py::function step, const std::vector<ServingRequestSpec>& specs,
-           const ServingConfig& config) {
+           const ServingConfig& config, py::object prefillStep) {
+          // prefill(tokens, start, tables, read_logits) -> (next_tokens, logits)
+          PrefillStep prefill;
+          if (!prefillStep.is_none()) {
+            prefill = [prefillStep](const std::vector<std::int32_t>& tokens, std::size_t start,
+                                    const std::vector<std::vector<std::int32_t>>& tables,
+                                    bool readLogits) {
+              BatchedDecodeRun run;
+              py::tuple out = prefillStep(tokens, start, tables, readLogits);
+              run.nextTokenIds = out[0].cast<std::vector<float>>();
+              if (readLogits) run.logits = toVector(out[1].cast<FloatArray>());
+              run.passed = run.nextTokenIds.size() == tokens.size();
+              if (!run.passed) run.errorMessage = "prefill returned the wrong number of tokens";
+              return run;
+            };
+          }
           BatchedStep wrapped = [&step](const std::vector<std::int32_t>& tokens,
                                         const std::vector<std::int32_t>& lengths,
                                         const std::vector<std::vector<std::int32_t>>& tables,
@@ -592,11 +609,15 @@ PYBIND11_MODULE(_tmc_host, m) {
             return run;
           };
           std::ostringstream log;
-          auto r = runContinuousBatch(rt, plan, pools, maxBatch, maxPages, wrapped, specs, config, log);
+          auto r = runContinuousBatch(rt, plan, pools, maxBatch, maxPages, wrapped, specs, config,
+                                      log, prefill);
           auto d = servingToDict(r);
           d["log"] = log.str();
           return d;
-        });
+        },
+        py::arg("runtime"), py::arg("plan"), py::arg("pools"), py::arg("maximum_batch_size"),
+        py::arg("max_pages"), py::arg("step"), py::arg("specs"), py::arg("config"),
+        py::arg("prefill") = py::none());
   // Kernel selection (tuners and admission).
   py::class_<hip::DecodeGEMVConfig>(m, "DecodeGEMVConfig")
       .def(py::init<>())

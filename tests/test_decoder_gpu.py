@@ -300,7 +300,10 @@ def test_batched_executor_rows_match_oracle(host, orc, rt):
     assert "capacity" in ex.run([1] * 5, [0] + lengths[1:], tables, False, False)["error"]
 
 
-def test_serving_matches_single_request_decoding(host, orc, rt):
+@pytest.mark.parametrize("chunk", [0, 8])
+def test_serving_matches_single_request_decoding(host, orc, rt, chunk):
+    """chunk 0: prompts by decode in the batched ticks; chunk 8: prompts in
+    chunks through the chunked prefill executor at admission."""
     cfg = CONFIGS["serve"]
     m = _weights(orc, cfg, 61)
     w = _workload(host, orc, cfg, m)
@@ -318,13 +321,19 @@ def test_serving_matches_single_request_decoding(host, orc, rt):
     config.page_size = P
     config.physical_pages_per_layer = 6  # 4 pages hold one full request: page pressure
     config.record_decode_logits = True
+    config.prefill_chunk_size = chunk
     result = host.run_continuous_batch(rt, model, specs, config)
     assert result["passed"], result["error"]
     metrics = result["metrics"]
+    assert (metrics["prefill_chunk_submissions"] > 0) == (chunk > 0)
     assert metrics["decoded_tokens"] == sum(s.decode_token_count for s in specs)
     assert metrics["maximum_active_batch_size"] > 1
     # page pressure preempts: the KV pages spill raw to pinned host memory
-    assert metrics["preemption_count"] > 0 and metrics["spilled_bytes"] > 0
+    # (prompts consumed at admission change the schedule: no preemption is
+    # required there)
+    if chunk == 0:
+        assert metrics["preemption_count"] > 0 and metrics["spilled_bytes"] > 0
+    assert (metrics["spilled_bytes"] > 0) == (metrics["preemption_count"] > 0)
     assert metrics["resume_count"] == metrics["preemption_count"]
     print("serving metrics:", {k: v for k, v in metrics.items() if not isinstance(v, dict)})
     opts = host.DecoderLLMCompileOptions()

@@ -114,7 +114,7 @@ def _reference_tokens(prompt, decode):
     return out
 
 
-def _run(host, specs, pages_per_layer, max_batch, page_size=4, layers=2, capacity=64):
+def _run(host, specs, pages_per_layer, max_batch, page_size=4, layers=2, capacity=64, chunk=0):
     rt = host.HipRuntime()
     plan = _decoder_plan(host, layers, capacity)
     pools = [host.create_host_kv_page_pool(plan.kv_plan(), page_size, pages_per_layer)
@@ -137,12 +137,25 @@ def _run(host, specs, pages_per_layer, max_batch, page_size=4, layers=2, capacit
         logits = np.zeros(rows * V, np.float32)
         return nxt, logits
 
+    def prefill(tokens, start, tables, read_logits):
+        """One prompt chunk of one request: rows are positions start.."""
+        rows = len(tokens)
+        assert 0 < rows <= chunk
+        need = (start + rows + page_size - 1) // page_size
+        for l in range(layers):
+            t = np.asarray(tables[l])
+            assert (t[:need] >= 0).all() and (t[need:] < 0).all()
+        seen.setdefault("chunks", []).append(rows)
+        nxt = [_next(t, start + r + 1) for r, t in enumerate(tokens)]
+        return nxt, np.zeros(rows * V, np.float32)
+
     config = host.ServingConfig()
     config.page_size = page_size
     config.physical_pages_per_layer = pages_per_layer
     config.maximum_batch_size = max_batch
+    config.prefill_chunk_size = chunk
     result = host.run_continuous_batch_with(rt, plan, pools, max_batch, max_pages, step, specs,
-                                            config)
+                                            config, prefill if chunk else None)
     return result, pools, seen
 
 
@@ -187,6 +200,27 @@ def test_scheduler_preempts_under_page_pressure_and_stays_exact(host):
                                                                spec.decode_token_count)
     assert all(p.used_pages() == 0 for p in pools)
     assert m["peak_pages_per_layer"] <= 16
+
+
+@pytest.mark.parametrize("pages,chunk", [(64, 5), (16, 8)])
+def test_scheduler_chunked_prefill_matches_sequential(host, pages, chunk):
+    """Prompts run at admission in chunks (prefillChunked per request,
+    ServingRuntime.cpp:682-700); the outputs equal one-request decoding,
+    also when page pressure preempts decoding requests."""
+    rng = np.random.default_rng(4)
+    specs = _specs(host, rng, 8, prompt=(10, 24), decode=(4, 16), arrivals=3)
+    result, pools, seen = _run(host, specs, pages_per_layer=pages, max_batch=8, chunk=chunk)
+    assert result["passed"], result["error"]
+    for spec, out in zip(specs, result["requests"]):
+        assert out["generated_token_ids"] == _reference_tokens(spec.prompt_token_ids,
+                                                               spec.decode_token_count), spec.id
+    m = result["metrics"]
+    total = sum(len(s.prompt_token_ids) for s in specs)
+    assert m["prompt_tokens"] == total == sum(seen["chunks"])
+    assert m["prefill_chunk_submissions"] == len(seen["chunks"])
+    assert m["prefill_chunk_submissions"] == sum(-(-len(s.prompt_token_ids) // chunk) for s in specs)
+    assert all(p.used_pages() == 0 for p in pools)
+    assert m["peak_pages_per_layer"] <= pages
 
 
 def test_scheduler_batch_cap_and_validation(host):
