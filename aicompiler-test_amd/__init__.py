@@ -70,6 +70,10 @@ def _declare(l):
                                          i64, i64, i64, i64, vp]),
         "tmc_prefill_rope_append": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64,
                                           i64, i64, i64, i64, vp]),
+        "tmc_prefill_rope_append_rows": (i32, [vp, vp, vp, vp, vp, vp, i64, vp, vp, vp, vp, i32,
+                                               i64, i64, i64, i64, i64, i64, i64, vp]),
+        "tmc_prefill_attention_rows_f16": (i32, [vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i64,
+                                                 i64, i64, i64, i64, i64, i64, i64, vp]),
         "tmc_gemm_rows_workspace_bytes": (sz, []),
         "tmc_gemm_rows_f16": (i32, [vp, vp, vp, i32, i64, i64, i64, vp, sz, vp]),
         "tmc_prefill_attention_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64,
@@ -432,6 +436,29 @@ def prefill_rope_append(qkv, cos, sin, valid_lengths, table, active, q_out, k_po
                                         _ptr(v_pool), _dtype_code(qkv), rows, q_heads, kv_heads,
                                         head_dim, capacity, page_size, max_pages, _stream(stream)),
           "tmc_prefill_rope_append")
+
+
+def prefill_rope_append_rows(qkv, cos, sin, valid_lengths, tables, row_table, active, q_out,
+                             k_pool, v_pool, rows, q_heads, kv_heads, head_dim, capacity,
+                             page_size, max_pages, stream=None):
+    """tables [table_rows, max_pages]; row_table [rows] int32."""
+    check(lib().tmc_prefill_rope_append_rows(
+        _ptr(qkv), _ptr(cos), _ptr(sin), _ptr(valid_lengths), _ptr(tables), _ptr(row_table),
+        tables.shape[0], _ptr(active), _ptr(q_out), _ptr(k_pool), _ptr(v_pool), _dtype_code(qkv),
+        rows, q_heads, kv_heads, head_dim, capacity, page_size, max_pages, _stream(stream)),
+        "tmc_prefill_rope_append_rows")
+
+
+def prefill_attention_rows(q, k_pool, v_pool, valid_lengths, tables, row_table, active, out, rows,
+                           q_heads, kv_heads, head_dim, page_size, max_pages, page_stride,
+                           head_stride, stream=None, pool_pages=None):
+    if pool_pages is None:
+        pool_pages = min(k_pool.numel(), v_pool.numel()) // page_stride
+    check(lib().tmc_prefill_attention_rows_f16(
+        _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(valid_lengths), _ptr(tables), _ptr(row_table),
+        tables.shape[0], _ptr(active), _ptr(out), rows, q_heads, kv_heads, head_dim, page_size,
+        max_pages, pool_pages, page_stride, head_stride, _stream(stream)),
+        "tmc_prefill_attention_rows_f16")
 
 
 def gemm_rows_workspace_bytes() -> int:

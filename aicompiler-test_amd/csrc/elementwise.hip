@@ -402,7 +402,7 @@ __global__ __launch_bounds__(kThreads) void decode_rope_append_kernel(
     const int32_t* __restrict__ valid_lengths, const int32_t* __restrict__ block_tables,
     const int32_t* __restrict__ active_count, T* __restrict__ q_out, T* __restrict__ k_pool,
     T* __restrict__ v_pool, int max_batch, int q_heads, int kv_heads, int head_dim, int capacity,
-    int page_size, int table_stride) {
+    int page_size, int table_stride, const int32_t* __restrict__ row_table, int table_rows) {
   const int pairs = head_dim / 2;
   const int row_pairs = (q_heads + 2 * kv_heads) * pairs;
   const long gid = (long)blockIdx.x * kThreads + threadIdx.x;
@@ -419,6 +419,10 @@ __global__ __launch_bounds__(kThreads) void decode_rope_append_kernel(
   const T x0 = src[0], x1 = src[1];
   if (request >= active || valid <= 0 || valid > capacity) return;
   const int position = valid - 1;
+  // Table row: the row table's entry (several requests in one prefill
+  // chunk), else the request itself (table_stride 0: one shared table).
+  const int trow = row_table ? row_table[request] : request;
+  if (row_table && (trow < 0 || trow >= table_rows)) return;
   const int pair = (column % head_dim) / 2;
   if (column < q_width + kv_width) {
     const float c = cosine[(size_t)position * pairs + pair];
@@ -431,7 +435,7 @@ __global__ __launch_bounds__(kThreads) void decode_rope_append_kernel(
       dst[1] = from_float<T>(ro);
       return;
     }
-    const int page = block_tables[(size_t)request * table_stride + position / page_size];
+    const int page = block_tables[(size_t)trow * table_stride + position / page_size];
     if (page < 0) return;
     const int feature = column - q_width;
     T* dst = k_pool + (((size_t)page * kv_heads + feature / head_dim) * page_size +
@@ -440,7 +444,7 @@ __global__ __launch_bounds__(kThreads) void decode_rope_append_kernel(
     dst[1] = from_float<T>(ro);
     return;
   }
-  const int page = block_tables[(size_t)request * table_stride + position / page_size];
+  const int page = block_tables[(size_t)trow * table_stride + position / page_size];
   if (page < 0) return;
   const int feature = column - q_width - kv_width;
   T* dst = v_pool + (((size_t)page * kv_heads + feature / head_dim) * page_size +
@@ -459,7 +463,7 @@ __global__ __launch_bounds__(kThreads) void decode_rope_append_h8_kernel(
     const int32_t* __restrict__ block_tables, const int32_t* __restrict__ active_count,
     half_t* __restrict__ q_out, half_t* __restrict__ k_pool, half_t* __restrict__ v_pool,
     int max_batch, int q_heads, int kv_heads, int head_dim, int capacity, int page_size,
-    int table_stride) {
+    int table_stride, const int32_t* __restrict__ row_table, int table_rows) {
   const int pairs = head_dim / 2;
   const int row_octs = (q_heads + 2 * kv_heads) * head_dim / 8;
   const long gid = (long)blockIdx.x * kThreads + threadIdx.x;
@@ -472,6 +476,10 @@ __global__ __launch_bounds__(kThreads) void decode_rope_append_h8_kernel(
   const h8 x = *reinterpret_cast<const h8*>(qkv + (size_t)request * (q_width + 2 * kv_width) + column);
   if (request >= active || valid <= 0 || valid > capacity) return;
   const int position = valid - 1;
+  // Table row: the row table's entry (several requests in one prefill
+  // chunk), else the request itself (table_stride 0: one shared table).
+  const int trow = row_table ? row_table[request] : request;
+  if (row_table && (trow < 0 || trow >= table_rows)) return;
   if (column < q_width + kv_width) {
     const int pair0 = (column % head_dim) / 2;
     const f4 c = *reinterpret_cast<const f4*>(cosine + (size_t)position * pairs + pair0);
@@ -492,14 +500,14 @@ __global__ __launch_bounds__(kThreads) void decode_rope_append_h8_kernel(
       *reinterpret_cast<h8*>(q_out + (size_t)request * q_width + column) = y;
       return;
     }
-    const int page = block_tables[(size_t)request * table_stride + position / page_size];
+    const int page = block_tables[(size_t)trow * table_stride + position / page_size];
     if (page < 0) return;
     const int feature = column - q_width;
     *reinterpret_cast<h8*>(k_pool + (((size_t)page * kv_heads + feature / head_dim) * page_size +
                                      position % page_size) * head_dim + feature % head_dim) = y;
     return;
   }
-  const int page = block_tables[(size_t)request * table_stride + position / page_size];
+  const int page = block_tables[(size_t)trow * table_stride + position / page_size];
   if (page < 0) return;
   const int feature = column - q_width - kv_width;
   *reinterpret_cast<h8*>(v_pool + (((size_t)page * kv_heads + feature / head_dim) * page_size +
@@ -889,7 +897,8 @@ int launch_rope_append(const void* qkv, const float* cosine, const float* sine,
                        const int32_t* active_count, void* q_out, void* key_pool, void* value_pool,
                        int dtype, int64_t max_batch, int64_t q_heads, int64_t kv_heads,
                        int64_t head_dim, int64_t capacity, int64_t page_size, int64_t max_pages,
-                       bool shared_table, void* stream) {
+                       bool shared_table, const int32_t* row_table, int64_t table_rows,
+                       void* stream) {
   TMC_REQUIRE(qkv && cosine && sine && valid_lengths && block_tables && active_count && q_out &&
                   key_pool && value_pool,
               "RoPE+append: null device pointer.");
@@ -901,7 +910,9 @@ int launch_rope_append(const void* qkv, const float* cosine, const float* sine,
               "ceil(capacity / page_size)).");
   const size_t items = (size_t)max_batch * (q_heads + 2 * kv_heads) * (head_dim / 2);
   TMC_REQUIRE(items < (1ull << 31), "RoPE+append: too many elements.");
-  const int table_stride = shared_table ? 0 : (int)max_pages;
+  TMC_REQUIRE(!row_table || (table_rows >= 1 && table_rows < (1LL << 24)),
+              "RoPE+append: a row table needs table_rows >= 1.");
+  const int table_stride = shared_table && !row_table ? 0 : (int)max_pages;
   if (dtype == TMC_F16 && head_dim % 8 == 0 && aligned16(qkv) && aligned16(cosine) &&
       aligned16(sine) && aligned16(q_out) && aligned16(key_pool) && aligned16(value_pool)) {
     const size_t octs = items / 4;
@@ -911,7 +922,7 @@ int launch_rope_append(const void* qkv, const float* cosine, const float* sine,
                        valid_lengths, block_tables, active_count, static_cast<half_t*>(q_out),
                        static_cast<half_t*>(key_pool), static_cast<half_t*>(value_pool),
                        (int)max_batch, (int)q_heads, (int)kv_heads, (int)head_dim, (int)capacity,
-                       (int)page_size, table_stride);
+                       (int)page_size, table_stride, row_table, (int)table_rows);
     return check_launch("decode_rope_append_h8_kernel");
   }
   TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((decode_rope_append_kernel<T>),
@@ -922,7 +933,8 @@ int launch_rope_append(const void* qkv, const float* cosine, const float* sine,
                                             static_cast<T*>(q_out), static_cast<T*>(key_pool),
                                             static_cast<T*>(value_pool), (int)max_batch,
                                             (int)q_heads, (int)kv_heads, (int)head_dim,
-                                            (int)capacity, (int)page_size, table_stride));
+                                            (int)capacity, (int)page_size, table_stride,
+                                            row_table, (int)table_rows));
   return check_launch("decode_rope_append_kernel");
 }
 }  // namespace
@@ -936,7 +948,7 @@ extern "C" int tmc_decode_rope_append(const void* qkv, const float* cosine, cons
                                       void* stream) {
   return launch_rope_append(qkv, cosine, sine, valid_lengths, block_tables, active_count, q_out,
                             key_pool, value_pool, dtype, max_batch, q_heads, kv_heads, head_dim,
-                            capacity, page_size, max_pages, false, stream);
+                            capacity, page_size, max_pages, false, nullptr, 0, stream);
 }
 
 extern "C" int tmc_prefill_rope_append(const void* qkv, const float* cosine, const float* sine,
@@ -947,7 +959,21 @@ extern "C" int tmc_prefill_rope_append(const void* qkv, const float* cosine, con
                                        int64_t page_size, int64_t max_pages, void* stream) {
   return launch_rope_append(qkv, cosine, sine, valid_lengths, block_table, active_count, q_out,
                             key_pool, value_pool, dtype, rows, q_heads, kv_heads, head_dim,
-                            capacity, page_size, max_pages, true, stream);
+                            capacity, page_size, max_pages, true, nullptr, 0, stream);
+}
+
+extern "C" int tmc_prefill_rope_append_rows(const void* qkv, const float* cosine, const float* sine,
+                                            const int32_t* valid_lengths,
+                                            const int32_t* block_tables, const int32_t* row_table,
+                                            int64_t table_rows, const int32_t* active_count,
+                                            void* q_out, void* key_pool, void* value_pool,
+                                            int dtype, int64_t rows, int64_t q_heads,
+                                            int64_t kv_heads, int64_t head_dim, int64_t capacity,
+                                            int64_t page_size, int64_t max_pages, void* stream) {
+  TMC_REQUIRE(row_table, "RoPE+append: null row table.");
+  return launch_rope_append(qkv, cosine, sine, valid_lengths, block_tables, active_count, q_out,
+                            key_pool, value_pool, dtype, rows, q_heads, kv_heads, head_dim,
+                            capacity, page_size, max_pages, true, row_table, table_rows, stream);
 }
 
 extern "C" int tmc_argmax_f32(const float* logits, int32_t* tokens, int64_t rows,

@@ -52,7 +52,9 @@ struct PrefillParams {
   const half_t* v;
   half_t* out;           // [rows, q_heads, D]
   const int32_t* valid;  // [rows] valid length of each query token
-  const int32_t* table;  // [max_pages] pages of the request
+  const int32_t* table;  // [table_rows][max_pages] pages of the chunk's requests
+  const int32_t* row_table;  // [rows] table row of each token, or null: row 0 for all
+  int table_rows;
   const int32_t* active; // [1] query tokens present
   long page_stride, head_stride, pool_pages;
   unsigned pool_bytes;   // bytes of each pool when below 4 GiB (buffer loads), else 0
@@ -256,6 +258,12 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillPa
   const int active = min(p.active[0], p.rows);
   const int t0 = tile * p.tokens_per_tile;
   if (t0 >= active) return;
+  // The tile's request: the table row of its first token (a caller packing
+  // several requests starts each at a tile boundary; a token of another
+  // table row in the tile gets no output).
+  const int tile_table = p.row_table ? p.row_table[t0] : 0;
+  if (tile_table < 0 || tile_table >= p.table_rows) return;
+  const int32_t* request_table = p.table + (size_t)tile_table * p.max_pages;
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
@@ -269,6 +277,7 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillPa
   if (vec < p.tokens_per_tile * p.group && token < active) {
     len = p.valid[token];
     if (len < 1 || len > capacity) len = -1;  // no output for this query
+    if (p.row_table && p.row_table[token] != tile_table) len = -1;
   }
 
   // Attended extent of the tile and the first absent page below it.
@@ -285,7 +294,7 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillPa
     const int pages = (end + p.page_size - 1) / p.page_size;
     int first_bad = 0x7fffffff;
     for (int i = threadIdx.x; i < pages; i += kPaThreads) {
-      const int page = p.table[i];
+      const int page = request_table[i];
       if (TLDS) s_table[i] = page;
       if (page < 0 || page >= p.pool_pages) first_bad = min(first_bad, i);
     }
@@ -306,7 +315,7 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillPa
   for (int t = 0; t < DT; ++t) o[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   float m = -INFINITY, lsum = 0.0f;
 
-  const int* table = TLDS ? s_table : p.table;
+  const int* table = TLDS ? s_table : request_table;
   // The next block's loads are issued as soon as the current one is in LDS
   // and land during its compute.  (Two or three blocks in flight measured
   // no faster.)
@@ -485,14 +494,19 @@ extern "C" int tmc_gemm_rows_f16(const void* x, const void* weight, void* y, int
                "matmul");
 }
 
-extern "C" int tmc_prefill_attention_f16(const void* q, const void* key_pool, const void* value_pool,
-                                         const int32_t* valid_lengths, const int32_t* block_table,
-                                         const int32_t* active_count, void* out, int64_t rows,
-                                         int64_t q_heads, int64_t kv_heads, int64_t head_dim,
-                                         int64_t page_size, int64_t max_pages, int64_t pool_pages,
-                                         int64_t page_stride, int64_t head_stride, void* stream) {
-  TMC_REQUIRE(q && key_pool && value_pool && valid_lengths && block_table && active_count && out,
+extern "C" int tmc_prefill_attention_rows_f16(const void* q, const void* key_pool,
+                                              const void* value_pool, const int32_t* valid_lengths,
+                                              const int32_t* block_tables, const int32_t* row_table,
+                                              int64_t table_rows, const int32_t* active_count,
+                                              void* out, int64_t rows, int64_t q_heads,
+                                              int64_t kv_heads, int64_t head_dim, int64_t page_size,
+                                              int64_t max_pages, int64_t pool_pages,
+                                              int64_t page_stride, int64_t head_stride,
+                                              void* stream) {
+  TMC_REQUIRE(q && key_pool && value_pool && valid_lengths && block_tables && active_count && out,
               "Prefill attention: null device pointer.");
+  TMC_REQUIRE(table_rows >= 1 && (row_table || table_rows == 1) && table_rows < (1LL << 24),
+              "Prefill attention: table_rows must be 1 without a row table, else at least 1.");
   TMC_REQUIRE(head_dim == 64 || head_dim == 128, "Prefill attention: head_dim must be 64 or 128.");
   TMC_REQUIRE(rows > 0 && rows < (1LL << 24) && q_heads > 0 && kv_heads > 0 &&
                   q_heads % kv_heads == 0,
@@ -513,7 +527,9 @@ extern "C" int tmc_prefill_attention_f16(const void* q, const void* key_pool, co
   p.v = static_cast<const half_t*>(value_pool);
   p.out = static_cast<half_t*>(out);
   p.valid = valid_lengths;
-  p.table = block_table;
+  p.table = block_tables;
+  p.row_table = row_table;
+  p.table_rows = (int)table_rows;
   p.active = active_count;
   p.page_stride = page_stride;
   p.head_stride = head_stride;
@@ -558,4 +574,16 @@ extern "C" int tmc_prefill_attention_f16(const void* q, const void* key_pool, co
   }
 #undef TMC_PA_LAUNCH
   return check_launch("prefill_attention_kernel");
+}
+
+extern "C" int tmc_prefill_attention_f16(const void* q, const void* key_pool, const void* value_pool,
+                                         const int32_t* valid_lengths, const int32_t* block_table,
+                                         const int32_t* active_count, void* out, int64_t rows,
+                                         int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                         int64_t page_size, int64_t max_pages, int64_t pool_pages,
+                                         int64_t page_stride, int64_t head_stride, void* stream) {
+  return tmc_prefill_attention_rows_f16(q, key_pool, value_pool, valid_lengths, block_table,
+                                        nullptr, 1, active_count, out, rows, q_heads, kv_heads,
+                                        head_dim, page_size, max_pages, pool_pages, page_stride,
+                                        head_stride, stream);
 }

@@ -689,18 +689,35 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     NEED(rows > 0 && qh > 0 && kvh > 0 && d > 0 && cap > 0 && ps > 0,
          "prefill_rope_append needs rows, q_heads, head_dim, capacity, page_size.");
     const int64_t mp = (cap + ps - 1) / ps;
-    // inputs: qkv, cos, sin, valid_lengths, block_table, active; outputs: q, key pool, value pool
-    s.inputs = {dt, TMC_F32, TMC_F32, TMC_I32, TMC_I32, TMC_I32};
-    s.outputs = {dt, dt, dt};
+    // tables=N > 0: N table rows and a row table (int32 [rows]) after them.
+    const int64_t tr = param_int(p, "tables", 0);
+    NEED(tr >= 0 && tr < (1 << 20), "prefill_rope_append: tables must be >= 0.");
+    // inputs: qkv, cos, sin, valid_lengths, block table(s)[, row table], active;
+    // outputs: q, key pool, value pool
+    s.inputs = {dt, TMC_F32, TMC_F32, TMC_I32, TMC_I32};
     s.counts = {(size_t)(rows * (qh + 2 * kvh) * d), (size_t)(cap * (d / 2)),
-                (size_t)(cap * (d / 2)), (size_t)rows, (size_t)mp, 1, (size_t)(rows * qh * d), 0, 0};
+                (size_t)(cap * (d / 2)), (size_t)rows, (size_t)(mp * (tr ? tr : 1))};
+    if (tr) {
+      s.inputs.push_back(TMC_I32);
+      s.counts.push_back((size_t)rows);
+    }
+    s.inputs.push_back(TMC_I32);
+    s.counts.push_back(1);
+    s.outputs = {dt, dt, dt};
+    s.counts.insert(s.counts.end(), {(size_t)(rows * qh * d), 0, 0});
+    const int a = tr ? 6 : 5;  // index of the active count
     s.launch = [=](const LaunchContext& c) {
+      const auto i32 = [&](int i) { return static_cast<const int32_t*>(c.ptrs[i]); };
+      if (tr)
+        return tmc_prefill_rope_append_rows(c.ptrs[0], static_cast<const float*>(c.ptrs[1]),
+                                            static_cast<const float*>(c.ptrs[2]), i32(3), i32(4),
+                                            i32(5), tr, i32(a), c.ptrs[a + 1], c.ptrs[a + 2],
+                                            c.ptrs[a + 3], dt, rows, qh, kvh, d, cap, ps, mp,
+                                            c.stream);
       return tmc_prefill_rope_append(c.ptrs[0], static_cast<const float*>(c.ptrs[1]),
-                                     static_cast<const float*>(c.ptrs[2]),
-                                     static_cast<const int32_t*>(c.ptrs[3]),
-                                     static_cast<const int32_t*>(c.ptrs[4]),
-                                     static_cast<const int32_t*>(c.ptrs[5]), c.ptrs[6], c.ptrs[7],
-                                     c.ptrs[8], dt, rows, qh, kvh, d, cap, ps, mp, c.stream);
+                                     static_cast<const float*>(c.ptrs[2]), i32(3), i32(4), i32(a),
+                                     c.ptrs[a + 1], c.ptrs[a + 2], c.ptrs[a + 3], dt, rows, qh, kvh,
+                                     d, cap, ps, mp, c.stream);
     };
     return true;
   }
@@ -713,17 +730,29 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
          "prefill_attention needs rows, q_heads, head_dim, page_size, max_pages and dtype=f16.");
     const int64_t head_stride = param_int(p, "head_stride", ps * d);
     const int64_t page_stride = param_int(p, "page_stride", kvh * ps * d);
-    // inputs: q, key pool, value pool, valid_lengths, block_table, active; output: context
-    s.inputs = {dt, dt, dt, TMC_I32, TMC_I32, TMC_I32};
+    const int64_t tr = param_int(p, "tables", 0);  // > 0: table rows + a row table
+    NEED(tr >= 0 && tr < (1 << 20), "prefill_attention: tables must be >= 0.");
+    // inputs: q, key pool, value pool, valid_lengths, block table(s)[, row table], active;
+    // output: context
+    s.inputs = {dt, dt, dt, TMC_I32, TMC_I32};
+    s.counts = {(size_t)(rows * qh * d), 0, 0, (size_t)rows, (size_t)(mp * (tr ? tr : 1))};
+    if (tr) {
+      s.inputs.push_back(TMC_I32);
+      s.counts.push_back((size_t)rows);
+    }
+    s.inputs.push_back(TMC_I32);
+    s.counts.push_back(1);
     s.outputs = {dt};
-    s.counts = {(size_t)(rows * qh * d), 0, 0, (size_t)rows, (size_t)mp, 1, (size_t)(rows * qh * d)};
+    s.counts.push_back((size_t)(rows * qh * d));
+    const int a = tr ? 6 : 5;  // index of the active count
     s.launch = [=](const LaunchContext& c) {
       const int64_t pool_pages =
           (int64_t)(std::min(c.counts[1], c.counts[2]) / (size_t)page_stride);
-      return tmc_prefill_attention_f16(
-          c.ptrs[0], c.ptrs[1], c.ptrs[2], static_cast<const int32_t*>(c.ptrs[3]),
-          static_cast<const int32_t*>(c.ptrs[4]), static_cast<const int32_t*>(c.ptrs[5]),
-          c.ptrs[6], rows, qh, kvh, d, ps, mp, pool_pages, page_stride, head_stride, c.stream);
+      const auto i32 = [&](int i) { return static_cast<const int32_t*>(c.ptrs[i]); };
+      return tmc_prefill_attention_rows_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], i32(3), i32(4),
+                                            tr ? i32(5) : nullptr, tr ? tr : 1, i32(a),
+                                            c.ptrs[a + 1], rows, qh, kvh, d, ps, mp, pool_pages,
+                                            page_stride, head_stride, c.stream);
     };
     return true;
   }

@@ -678,16 +678,18 @@ void ChunkedPrefillExecutor::build(std::ostream* log) {
   const std::size_t capacity = plan.attention.capacity;
   maxPages_ = (capacity + pageSize_ - 1) / pageSize_;
 
-  std::vector<float> zeros(2 * S + 1, 0.0f);
-  meta_ = allocate(rt, 2 * S + 1, zeros.data(), ElementType::Int32);
+  const std::size_t R = maxRequests_, T = R * maxPages_;  // table entries per layer
+  std::vector<float> zeros(3 * S + 1, 0.0f);
+  meta_ = allocate(rt, 3 * S + 1, zeros.data(), ElementType::Int32);
   tokensView_ = view(rt, meta_, 0, S);
   lengthsView_ = view(rt, meta_, S, S);
-  activeView_ = view(rt, meta_, 2 * S, 1);
-  const std::vector<float> none(L * maxPages_, -1.0f);
+  rowTableView_ = view(rt, meta_, 2 * S, S);
+  activeView_ = view(rt, meta_, 3 * S, 1);
+  const std::vector<float> none(L * T, -1.0f);
   tables_ = allocate(rt, none.size(), none.data(), ElementType::Int32);
-  for (std::size_t l = 0; l < L; ++l) tableViews_.push_back(view(rt, tables_, l * maxPages_, maxPages_));
-  metaShadow_.assign(2 * S + 1, 0);
-  tableShadow_.assign(L * maxPages_, -1);
+  for (std::size_t l = 0; l < L; ++l) tableViews_.push_back(view(rt, tables_, l * T, T));
+  metaShadow_.assign(3 * S + 1, 0);
+  tableShadow_.assign(L * T, -1);
 
   auto act = [&](std::size_t count, ElementType type = ElementType::Float16) {
     activationBytes_ += count * hip::elementBytes(type);
@@ -736,10 +738,18 @@ void ChunkedPrefillExecutor::build(std::ostream* log) {
     const std::string heads = "&q_heads=" + std::to_string(QH) + "&kv_heads=" + std::to_string(KVH) +
                               "&head_dim=" + std::to_string(D) +
                               "&page_size=" + std::to_string(pageSize_);
+    // Several requests per chunk: R table rows and the per-row table index.
+    const std::string multi = R > 1 ? "&tables=" + std::to_string(R) : "";
     const std::string ropeKey =
-        "prefill_rope_append?rows=" + B + heads + "&capacity=" + std::to_string(capacity);
+        "prefill_rope_append?rows=" + B + heads + "&capacity=" + std::to_string(capacity) + multi;
     const std::string attentionKey =
-        "prefill_attention?rows=" + B + heads + "&max_pages=" + std::to_string(maxPages_);
+        "prefill_attention?rows=" + B + heads + "&max_pages=" + std::to_string(maxPages_) + multi;
+    auto tableInputs = [&](std::size_t l) {
+      std::vector<BufferHandle> in{lengthsView_, tableViews_[l]};
+      if (R > 1) in.push_back(rowTableView_);
+      in.push_back(activeView_);
+      return in;
+    };
     add("embedding?rows=" + B + "&hidden=" + std::to_string(H) + "&vocab=" + std::to_string(V),
         "embedding", {tokensView_, model_->embeddingWeight}, {residual_});
     add("rmsnorm?" + norm, "l0_input_norm", {residual_, model_->layers[0].inputNormWeight},
@@ -751,13 +761,19 @@ void ChunkedPrefillExecutor::build(std::ostream* log) {
         add("add_rmsnorm?" + norm, p + "residual_input_norm", {after_, mlp_, w.inputNormWeight},
             {residual_, normalized_});
       add(gemm(H, QKV, "f16"), p + "qkv", {normalized_, w.queryKeyValueWeight, workspace_}, {qkv_});
-      add(ropeKey, p + "rope_append",
-          {qkv_, model_->ropeCosine, model_->ropeSine, lengthsView_, tableViews_[l], activeView_},
-          {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer()});
-      add(attentionKey, p + "attention",
-          {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer(), lengthsView_, tableViews_[l],
-           activeView_},
-          {context_});
+      {
+        std::vector<BufferHandle> in{qkv_, model_->ropeCosine, model_->ropeSine};
+        const auto t = tableInputs(l);
+        in.insert(in.end(), t.begin(), t.end());
+        add(ropeKey, p + "rope_append", in,
+            {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer()});
+      }
+      {
+        std::vector<BufferHandle> in{query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer()};
+        const auto t = tableInputs(l);
+        in.insert(in.end(), t.begin(), t.end());
+        add(attentionKey, p + "attention", in, {context_});
+      }
       add(gemm(H, H, "f16"), p + "o", {context_, w.outputWeight, workspace_}, {projected_});
       add("add_rmsnorm?" + norm, p + "residual_post_norm",
           {residual_, projected_, w.postAttentionNormWeight}, {after_, normalized_});
@@ -786,7 +802,8 @@ void ChunkedPrefillExecutor::build(std::ostream* log) {
 
 ChunkedPrefillExecutor::Creation createChunkedPrefillExecutor(
     hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
-    std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t chunkSize, std::ostream* log) {
+    std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t chunkSize, std::ostream* log,
+    std::size_t maximumRequests) {
   ChunkedPrefillExecutor::Creation result;
   try {
     if (!model) throw std::invalid_argument("Chunked prefill needs model resources.");
@@ -807,11 +824,15 @@ ChunkedPrefillExecutor::Creation createChunkedPrefillExecutor(
     if ((D != 64 && D != 128) || 64 % group != 0)
       throw std::invalid_argument(
           "Chunked prefill attention needs head_dim 64 or 128 and heads / kv_heads dividing 64.");
+    if (maximumRequests == 0 || maximumRequests > 1024)
+      throw std::invalid_argument("Chunked prefill requests per chunk must be in [1, 1024].");
     std::unique_ptr<ChunkedPrefillExecutor> executor(new ChunkedPrefillExecutor());
     executor->runtime_ = &runtime;
     executor->model_ = std::move(model);
     executor->pools_ = std::move(pools);
     executor->chunkSize_ = chunkSize;
+    executor->maxRequests_ = maximumRequests;
+    executor->tileRows_ = 64 / group;  // tokens per query tile of tmc_prefill_attention_f16
     executor->pageSize_ = executor->pools_.front()->pageSize();
     executor->build(log);
     result.executor = std::move(executor);
@@ -821,48 +842,94 @@ ChunkedPrefillExecutor::Creation createChunkedPrefillExecutor(
   return result;
 }
 
+std::size_t ChunkedPrefillExecutor::packedRows(const std::vector<std::size_t>& counts) const noexcept {
+  std::size_t rows = 0;
+  for (std::size_t i = 0; i < counts.size(); ++i)
+    rows = i + 1 < counts.size() ? (rows + counts[i] + tileRows_ - 1) / tileRows_ * tileRows_
+                                 : rows + counts[i];
+  return rows;
+}
+
+std::string ChunkedPrefillExecutor::validate(const PrefillSegment& segment) const {
+  const auto& plan = model_->plan;
+  const std::size_t rows = segment.tokenIds.size();
+  if (rows == 0 || segment.blockTables.size() != plan.layerCount)
+    return "Chunked prefill input shape is invalid.";
+  if (segment.start + rows > plan.attention.capacity)
+    return "KV cache valid length is outside the configured capacity.";
+  for (const auto token : segment.tokenIds)
+    if (token < 0 || static_cast<std::size_t>(token) >= plan.vocabularySize)
+      return "Chunked prefill token id is outside the vocabulary.";
+  // Every page the segment writes or attends is allocated in its layer's
+  // pool; entries past them are absent or allocated.
+  const std::size_t needed = (segment.start + rows + pageSize_ - 1) / pageSize_;
+  for (std::size_t l = 0; l < segment.blockTables.size(); ++l) {
+    if (segment.blockTables[l].size() != maxPages_) return "Chunked prefill block-table shape is invalid.";
+    for (std::size_t p = 0; p < maxPages_; ++p) {
+      const std::int32_t page = segment.blockTables[l][p];
+      if ((p < needed || page >= 0) && !pools_[l]->isAllocated(page))
+        return "Chunked prefill block table names a page that is not allocated in its layer's pool.";
+    }
+  }
+  return {};
+}
+
 BatchedDecodeRun ChunkedPrefillExecutor::run(const std::vector<std::int32_t>& tokenIds,
                                              std::size_t start,
                                              const std::vector<std::vector<std::int32_t>>& blockTables,
                                              bool readLogits, bool timeGpu) {
+  PrefillSegment segment{tokenIds, start, blockTables};
+  auto result = runBatch({segment}, false, timeGpu);
+  if (!result.passed || !readLogits) return result;
+  // All rows' logits of the one segment (rows 0 .. n-1 of the chunk).
+  result.logits.resize(tokenIds.size() * model_->plan.vocabularySize);
+  const auto error = logits_->readRaw(result.logits.data(), result.logits.size());
+  if (!error.empty()) {
+    result.passed = false;
+    result.errorMessage = error;
+  }
+  return result;
+}
+
+BatchedDecodeRun ChunkedPrefillExecutor::runBatch(const std::vector<PrefillSegment>& segments,
+                                                  bool readLogits, bool timeGpu) {
   BatchedDecodeRun result;
   const auto& plan = model_->plan;
-  const std::size_t rows = tokenIds.size(), S = chunkSize_;
-  if (rows == 0 || rows > S || blockTables.size() != plan.layerCount) {
-    result.errorMessage = "Chunked prefill input shape is invalid.";
+  const std::size_t S = chunkSize_, L = plan.layerCount, V = plan.vocabularySize;
+  if (segments.empty() || segments.size() > maxRequests_) {
+    result.errorMessage = "Chunked prefill needs 1 to maximumRequests() segments.";
     return result;
   }
-  if (start + rows > plan.attention.capacity) {
-    result.errorMessage = "KV cache valid length is outside the configured capacity.";
+  std::vector<std::size_t> counts;
+  for (const auto& segment : segments) {
+    auto error = validate(segment);
+    if (!error.empty()) {
+      result.errorMessage = error;
+      return result;
+    }
+    counts.push_back(segment.tokenIds.size());
+  }
+  const std::size_t rows = packedRows(counts);
+  if (rows > S) {
+    result.errorMessage = "Chunked prefill segments do not fit the chunk.";
     return result;
   }
-  for (const auto token : tokenIds) {
-    if (token < 0 || static_cast<std::size_t>(token) >= plan.vocabularySize) {
-      result.errorMessage = "Chunked prefill token id is outside the vocabulary.";
-      return result;
+  // Pack: segment i's rows from a tile boundary; padding rows have length 0
+  // (skipped by the kernels) and row table -1.
+  std::vector<std::int32_t> meta(3 * S + 1, 0);
+  std::vector<std::size_t> first(segments.size());
+  std::fill(meta.begin() + static_cast<std::ptrdiff_t>(2 * S),
+            meta.begin() + static_cast<std::ptrdiff_t>(3 * S), -1);
+  for (std::size_t i = 0, row = 0; i < segments.size(); ++i) {
+    first[i] = row;
+    for (std::size_t r = 0; r < counts[i]; ++r) {
+      meta[row + r] = segments[i].tokenIds[r];
+      meta[S + row + r] = static_cast<std::int32_t>(segments[i].start + r + 1);
+      meta[2 * S + row + r] = static_cast<std::int32_t>(i);
     }
+    row = (row + counts[i] + tileRows_ - 1) / tileRows_ * tileRows_;
   }
-  // Every page the chunk writes or attends is allocated in its layer's pool;
-  // entries past them are absent or allocated.
-  const std::size_t needed = (start + rows + pageSize_ - 1) / pageSize_;
-  for (std::size_t l = 0; l < blockTables.size(); ++l) {
-    if (blockTables[l].size() != maxPages_) {
-      result.errorMessage = "Chunked prefill block-table shape is invalid.";
-      return result;
-    }
-    for (std::size_t p = 0; p < maxPages_; ++p) {
-      const std::int32_t page = blockTables[l][p];
-      if ((p < needed || page >= 0) && !pools_[l]->isAllocated(page)) {
-        result.errorMessage = "Chunked prefill block table names a page that is not allocated "
-                              "in its layer's pool.";
-        return result;
-      }
-    }
-  }
-  std::vector<std::int32_t> meta(2 * S + 1, 0);
-  std::copy(tokenIds.begin(), tokenIds.end(), meta.begin());
-  for (std::size_t r = 0; r < rows; ++r) meta[S + r] = static_cast<std::int32_t>(start + r + 1);
-  meta[2 * S] = static_cast<std::int32_t>(rows);
+  meta[3 * S] = static_cast<std::int32_t>(rows);
   std::string error;
   if (meta != metaShadow_) {
     error = meta_->writeRaw(meta.data(), meta.size());
@@ -872,15 +939,17 @@ BatchedDecodeRun ChunkedPrefillExecutor::run(const std::vector<std::int32_t>& to
     }
     metaShadow_ = std::move(meta);
   }
+  const std::size_t T = maxRequests_ * maxPages_;
   std::vector<std::int32_t> packed(tableShadow_.size(), -1);
-  for (std::size_t l = 0; l < blockTables.size(); ++l)
-    std::copy(blockTables[l].begin(), blockTables[l].end(),
-              packed.begin() + static_cast<std::ptrdiff_t>(l * maxPages_));
-  std::size_t first = 0, last = packed.size();
-  while (first < last && packed[first] == tableShadow_[first]) ++first;
-  while (last > first && packed[last - 1] == tableShadow_[last - 1]) --last;
-  if (first < last) {
-    error = tables_->writeRaw(packed.data() + first, last - first, first);
+  for (std::size_t l = 0; l < L; ++l)
+    for (std::size_t i = 0; i < segments.size(); ++i)
+      std::copy(segments[i].blockTables[l].begin(), segments[i].blockTables[l].end(),
+                packed.begin() + static_cast<std::ptrdiff_t>(l * T + i * maxPages_));
+  std::size_t lo = 0, hi = packed.size();
+  while (lo < hi && packed[lo] == tableShadow_[lo]) ++lo;
+  while (hi > lo && packed[hi - 1] == tableShadow_[hi - 1]) --hi;
+  if (lo < hi) {
+    error = tables_->writeRaw(packed.data() + lo, hi - lo, lo);
     if (!error.empty()) {
       result.errorMessage = error;
       return result;
@@ -911,13 +980,17 @@ BatchedDecodeRun ChunkedPrefillExecutor::run(const std::vector<std::int32_t>& to
     result.errorMessage = error;
     return result;
   }
-  result.nextTokenIds.assign(next.begin(), next.end());
+  for (std::size_t i = 0; i < segments.size(); ++i)
+    for (std::size_t r = 0; r < counts[i]; ++r)
+      result.nextTokenIds.push_back(static_cast<float>(next[first[i] + r]));
   if (readLogits) {
-    result.logits.resize(rows * plan.vocabularySize);
-    error = logits_->readRaw(result.logits.data(), result.logits.size());
-    if (!error.empty()) {
-      result.errorMessage = error;
-      return result;
+    result.logits.resize(segments.size() * V);
+    for (std::size_t i = 0; i < segments.size(); ++i) {
+      error = logits_->readRaw(result.logits.data() + i * V, V, (first[i] + counts[i] - 1) * V);
+      if (!error.empty()) {
+        result.errorMessage = error;
+        return result;
+      }
     }
   }
   result.passed = true;

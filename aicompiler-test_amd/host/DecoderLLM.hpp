@@ -265,6 +265,15 @@ struct BatchedDecodeExecutor::Creation {
 // buckets 16, 32, ... and chunkSize; a chunk runs the smallest that holds it
 // (spare rows are computed and discarded).  A stage replays eagerly on the
 // runtime's stream (the library GEMMs are kept out of graphs).
+// One request's part of a prefill chunk: tokens at positions start ..
+// start + tokens - 1, block tables per layer as [maxPages()] holding pages
+// for every position below start + tokens.
+struct PrefillSegment {
+  std::vector<std::int32_t> tokenIds;
+  std::size_t start = 0;
+  std::vector<std::vector<std::int32_t>> blockTables;
+};
+
 class ChunkedPrefillExecutor {
  public:
   struct Creation;
@@ -272,14 +281,23 @@ class ChunkedPrefillExecutor {
   ChunkedPrefillExecutor(const ChunkedPrefillExecutor&) = delete;
   ChunkedPrefillExecutor& operator=(const ChunkedPrefillExecutor&) = delete;
 
-  // Tokens at positions start .. start + tokens - 1 of one request; block
-  // tables per layer as [maxPages()] holding pages for every position below
-  // start + tokens.  Logits (when read) and next tokens are per row.
+  // One request's segment.  Logits (when read) and next tokens are per row.
   [[nodiscard]] BatchedDecodeRun run(const std::vector<std::int32_t>& tokenIds, std::size_t start,
                                      const std::vector<std::vector<std::int32_t>>& blockTables,
                                      bool readLogits = true, bool timeGpu = false);
+  // Up to maximumRequests() segments of different requests in one chunk:
+  // each starts at a multiple of tileRows() rows (the attention kernel's
+  // query tile), so packedRows(segments) must not exceed chunkSize().  Next
+  // tokens are per segment row, in segment order; logits (when read) are
+  // the last row's of each segment, [segments, vocabulary].
+  [[nodiscard]] BatchedDecodeRun runBatch(const std::vector<PrefillSegment>& segments,
+                                          bool readLogits = false, bool timeGpu = false);
 
   [[nodiscard]] std::size_t chunkSize() const noexcept { return chunkSize_; }
+  [[nodiscard]] std::size_t maximumRequests() const noexcept { return maxRequests_; }
+  [[nodiscard]] std::size_t tileRows() const noexcept { return tileRows_; }
+  // Rows a chunk of segments with these token counts occupies.
+  [[nodiscard]] std::size_t packedRows(const std::vector<std::size_t>& counts) const noexcept;
   [[nodiscard]] std::size_t maxPages() const noexcept { return maxPages_; }
   [[nodiscard]] std::size_t activationStorageBytes() const noexcept { return activationBytes_; }
   [[nodiscard]] std::vector<std::size_t> buckets() const;
@@ -289,21 +307,24 @@ class ChunkedPrefillExecutor {
   friend Creation createChunkedPrefillExecutor(hip::HipRuntime&,
                                                std::shared_ptr<DecoderLLMModelResources>,
                                                std::vector<std::shared_ptr<KVPagePool>>,
-                                               std::size_t, std::ostream*);
+                                               std::size_t, std::ostream*, std::size_t);
   ChunkedPrefillExecutor() = default;
   void build(std::ostream* log);
+  [[nodiscard]] std::string validate(const PrefillSegment& segment) const;
 
   struct Stage;
   hip::HipRuntime* runtime_ = nullptr;
   std::shared_ptr<DecoderLLMModelResources> model_;
   std::vector<std::shared_ptr<KVPagePool>> pools_;
   std::size_t chunkSize_ = 0;
+  std::size_t maxRequests_ = 1;
+  std::size_t tileRows_ = 64;
   std::size_t pageSize_ = 0;
   std::size_t maxPages_ = 0;
   std::size_t activationBytes_ = 0;
-  hip::BufferHandle meta_;    // int32 [tokens S | lengths S | active 1]
-  hip::BufferHandle tables_;  // int32 [layers][maxPages]
-  hip::BufferHandle tokensView_, lengthsView_, activeView_;
+  hip::BufferHandle meta_;    // int32 [tokens S | lengths S | row tables S | active 1]
+  hip::BufferHandle tables_;  // int32 [layers][maxRequests][maxPages]
+  hip::BufferHandle tokensView_, lengthsView_, rowTableView_, activeView_;
   std::vector<hip::BufferHandle> tableViews_;
   hip::BufferHandle residual_, after_, normalized_, qkv_, query_, context_, projected_, gate_, up_,
       gated_, mlp_, logits_, nextTokens_, workspace_;
@@ -316,10 +337,11 @@ struct ChunkedPrefillExecutor::Creation {
   std::string errorMessage;
 };
 
+// maximumRequests: segments one chunk may hold (1 = one request per chunk).
 [[nodiscard]] ChunkedPrefillExecutor::Creation createChunkedPrefillExecutor(
     hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
     std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t chunkSize,
-    std::ostream* log = nullptr);
+    std::ostream* log = nullptr, std::size_t maximumRequests = 1);
 
 struct DecoderLLMCompileOptions {
   std::size_t kvPageSize = 0;  // 0 = contiguous cache (one page of `capacity`)

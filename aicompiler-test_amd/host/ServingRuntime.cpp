@@ -108,14 +108,16 @@ ServingExecutionResult runContinuousBatch(hip::HipRuntime& runtime,
                                           const BatchedStep& step,
                                           const std::vector<ServingRequestSpec>& specs,
                                           const ServingConfig& config, std::ostream& log,
-                                          const PrefillStep& prefill) {
+                                          const PrefillStep& prefill,
+                                          const PrefillPacking& packing) {
   ServingExecutionResult result;
   auto& metrics = result.metrics;
   try {
     if (specs.empty() || config.pageSize == 0 || config.physicalPagesPerLayer == 0)
       throw std::invalid_argument("Serving configuration and requests must be nonempty.");
-    if (config.prefillChunkSize != 0 && !prefill)
-      throw std::invalid_argument("Chunked serving prefill needs a prefill step.");
+    if (config.prefillChunkSize != 0 &&
+        (!prefill || packing.chunkRows == 0 || packing.tileRows == 0 || packing.maxRequests == 0))
+      throw std::invalid_argument("Chunked serving prefill needs a prefill step and its packing.");
     if (pools.size() != plan.layerCount || maximumBatchSize == 0)
       throw std::invalid_argument("Serving needs one page pool per layer and a batch size.");
     const std::size_t capacity = plan.attention.capacity, P = config.pageSize;
@@ -216,54 +218,77 @@ ServingExecutionResult runContinuousBatch(hip::HipRuntime& runtime,
       }
 
       // Chunked prefill of the prompts admitted above (their pages were
-      // counted at admission): the last chunk's last row is the first token.
-      for (auto& r : requests) {
-        if (config.prefillChunkSize == 0 || r.state != RequestState::Active ||
-            r.consumed >= r.prompt.size())
-          continue;
-        while (r.consumed < r.prompt.size()) {
+      // counted at admission), several requests per chunk when the packing
+      // allows: each request's rows start at a tile boundary.  The last row
+      // of a request's last segment is its first generated token.
+      while (config.prefillChunkSize != 0) {
+        std::vector<std::size_t> who, starts;
+        std::vector<PrefillSegment> segments;
+        std::size_t row = 0;
+        const auto kvStart = Clock::now();
+        auto rollback = [&]() {
+          for (std::size_t k = 0; k < who.size(); ++k)
+            for (auto& s : requests[who[k]].states) (void)s->rollbackLength(runtime, starts[k]);
+        };
+        for (std::size_t i = 0; i < requests.size(); ++i) {
+          auto& r = requests[i];
+          if (r.state != RequestState::Active || r.consumed >= r.prompt.size()) continue;
+          if (segments.size() == packing.maxRequests || row >= packing.chunkRows) break;
           const std::size_t start = r.consumed;
-          const std::size_t count = std::min(config.prefillChunkSize, r.prompt.size() - start);
-          const bool last = start + count == r.prompt.size();
-          const auto kvStart = Clock::now();
-          std::vector<std::vector<std::int32_t>> tables;
+          const std::size_t count = std::min(r.prompt.size() - start, packing.chunkRows - row);
+          PrefillSegment segment;
+          segment.start = start;
+          segment.tokenIds.assign(r.prompt.begin() + static_cast<std::ptrdiff_t>(start),
+                                  r.prompt.begin() + static_cast<std::ptrdiff_t>(start + count));
           for (auto& state : r.states) {
             const auto error = state->stageLength(runtime, start + count);
             if (!error.empty()) {
               for (auto& s : r.states) (void)s->rollbackLength(runtime, start);
+              rollback();
               throw std::runtime_error("Request " + r.spec.id + " KV stage failed: " + error);
             }
             auto table = state->pageTable();
             table.resize(maxPages, -1);
-            tables.push_back(std::move(table));
+            segment.blockTables.push_back(std::move(table));
           }
-          metrics.kvManagementOverheadUs += elapsedUs(kvStart, Clock::now());
-          const std::vector<std::int32_t> tokens(
-              r.prompt.begin() + static_cast<std::ptrdiff_t>(start),
-              r.prompt.begin() + static_cast<std::ptrdiff_t>(start + count));
-          const auto out = prefill(tokens, start, tables, last && config.recordPrefillLogits);
-          ++metrics.prefillChunkSubmissions;
-          if (!out.passed || out.nextTokenIds.size() != count) {
-            for (auto& s : r.states) (void)s->rollbackLength(runtime, start);
-            throw std::runtime_error("Chunked prefill failed: " + out.errorMessage);
-          }
-          for (auto& state : r.states) state->commitLength(start + count);
+          who.push_back(i);
+          starts.push_back(start);
+          segments.push_back(std::move(segment));
+          row = (row + count + packing.tileRows - 1) / packing.tileRows * packing.tileRows;
+        }
+        metrics.kvManagementOverheadUs += elapsedUs(kvStart, Clock::now());
+        if (segments.empty()) break;
+        const auto out = prefill(segments, config.recordPrefillLogits);
+        ++metrics.prefillChunkSubmissions;
+        std::size_t rowsOut = 0;
+        for (const auto& segment : segments) rowsOut += segment.tokenIds.size();
+        if (!out.passed || out.nextTokenIds.size() != rowsOut) {
+          rollback();
+          throw std::runtime_error("Chunked prefill failed: " + out.errorMessage);
+        }
+        std::size_t offset = 0;
+        for (std::size_t k = 0; k < who.size(); ++k) {
+          auto& r = requests[who[k]];
+          const std::size_t count = segments[k].tokenIds.size();
+          for (auto& state : r.states) state->commitLength(starts[k] + count);
           r.consumed += count;
           metrics.promptTokens += count;
-          if (!last) continue;
-          const auto next = static_cast<std::int32_t>(out.nextTokenIds.back());
+          offset += count;
+          if (r.consumed < r.prompt.size()) continue;
+          const auto next = static_cast<std::int32_t>(out.nextTokenIds[offset - 1]);
           r.output.generatedTokenIds.push_back(static_cast<float>(next));
           r.lastToken = next;
           r.output.timeToFirstTokenUs = elapsedUs(*r.arrivalTime, Clock::now());
-          if (config.recordPrefillLogits && !out.logits.empty()) {
+          if (config.recordPrefillLogits && out.logits.size() == segments.size() * plan.vocabularySize) {
             const auto V = static_cast<std::ptrdiff_t>(plan.vocabularySize);
-            r.output.prefillLogits.assign(out.logits.end() - V, out.logits.end());
+            r.output.prefillLogits.assign(out.logits.begin() + static_cast<std::ptrdiff_t>(k) * V,
+                                          out.logits.begin() + static_cast<std::ptrdiff_t>(k + 1) * V);
           }
           log << "Serving request " << r.spec.id << ": prompt complete (chunked), pages="
               << r.pages() << ", ttft(us)=" << r.output.timeToFirstTokenUs << '\n';
+          if (r.spec.decodeTokenCount == 0) finish(r);
         }
         progress = true;
-        if (r.spec.decodeTokenCount == 0) finish(r);
       }
 
       // Pages for every active row's next token; preempt the largest owner
@@ -476,18 +501,21 @@ ServingExecutionResult runContinuousBatch(hip::HipRuntime& runtime,
     };
     std::unique_ptr<ChunkedPrefillExecutor> prefillExecutor;
     PrefillStep prefill;
+    PrefillPacking packing;
     if (config.prefillChunkSize != 0) {
-      auto made = createChunkedPrefillExecutor(runtime, model, pools, config.prefillChunkSize, &log);
+      auto made = createChunkedPrefillExecutor(runtime, model, pools, config.prefillChunkSize, &log,
+                                               std::max<std::size_t>(1, config.prefillRequestsPerChunk));
       if (!made.executor) throw std::runtime_error(made.errorMessage);
       prefillExecutor = std::move(made.executor);
-      prefill = [&prefillExecutor](const std::vector<std::int32_t>& tokens, std::size_t start,
-                                   const std::vector<std::vector<std::int32_t>>& tables,
-                                   bool readLogits) {
-        return prefillExecutor->run(tokens, start, tables, readLogits, false);
+      prefill = [&prefillExecutor](const std::vector<PrefillSegment>& segments, bool readLogits) {
+        return prefillExecutor->runBatch(segments, readLogits, false);
       };
+      packing.chunkRows = prefillExecutor->chunkSize();
+      packing.tileRows = prefillExecutor->tileRows();
+      packing.maxRequests = prefillExecutor->maximumRequests();
     }
     result = runContinuousBatch(runtime, plan, pools, M, executor.maxPages(), step, requests,
-                                config, log, prefill);
+                                config, log, prefill, packing);
     result.metrics.modelStorageBytes = model->storageBytes;
     result.metrics.kvPoolStorageBytes = 2 * plan.layerCount * pools.front()->keyBuffer()->storageBytes();
     result.metrics.batchedActivationStorageBytes =
@@ -575,7 +603,8 @@ DecodeThroughput measureDecodeThroughput(hip::HipRuntime& runtime,
     std::unique_ptr<ChunkedPrefillExecutor> prefill;
     if (prefillChunkSize != 0) {
       auto made = createChunkedPrefillExecutor(runtime, model, pools,
-                                               std::min(prefillChunkSize, plan.attention.capacity));
+                                               std::min(prefillChunkSize, plan.attention.capacity),
+                                               nullptr, B);
       if (!made.executor) throw std::runtime_error(made.errorMessage);
       prefill = std::move(made.executor);
       // One chunk per stage on row 0's states, then released: the prompt
@@ -601,30 +630,44 @@ DecodeThroughput measureDecodeThroughput(hip::HipRuntime& runtime,
 
     const auto promptStart = Clock::now();
     if (prefill) {
-      // Each prompt in chunks through the prefill stage; the last row's
-      // greedy token is the request's first generated token.
-      for (std::size_t r = 0; r < B; ++r) {
-        const auto& prompt = prompts[r];
-        for (std::size_t start = 0; start < prompt.size();) {
-          const std::size_t count = std::min(prefill->chunkSize(), prompt.size() - start);
-          std::vector<std::vector<std::int32_t>> tables;
+      // Prompts packed into chunks, several requests per chunk (each from a
+      // tile boundary); a request's last row gives its first generated token.
+      std::vector<std::size_t> consumed(B, 0);
+      for (std::size_t next = 0; next < B;) {
+        std::vector<std::size_t> who;
+        std::vector<PrefillSegment> segments;
+        std::size_t row = 0;
+        for (std::size_t r = next; r < B && row < prefill->chunkSize(); ++r) {
+          const auto& prompt = prompts[r];
+          const std::size_t start = consumed[r];
+          const std::size_t count = std::min(prompt.size() - start, prefill->chunkSize() - row);
+          PrefillSegment segment;
+          segment.start = start;
+          segment.tokenIds.assign(prompt.begin() + static_cast<std::ptrdiff_t>(start),
+                                  prompt.begin() + static_cast<std::ptrdiff_t>(start + count));
           for (auto& state : states[r]) {
             const auto error = state->stageLength(runtime, start + count);
             if (!error.empty()) throw std::runtime_error(error);
             auto table = state->pageTable();
             table.resize(prefill->maxPages(), -1);
-            tables.push_back(std::move(table));
+            segment.blockTables.push_back(std::move(table));
           }
-          const std::vector<std::int32_t> tokens(prompt.begin() + static_cast<std::ptrdiff_t>(start),
-                                                 prompt.begin() +
-                                                     static_cast<std::ptrdiff_t>(start + count));
-          const auto out = prefill->run(tokens, start, tables, false, false);
-          if (!out.passed) throw std::runtime_error(out.errorMessage);
-          for (auto& state : states[r]) state->commitLength(start + count);
-          start += count;
-          if (start == prompt.size()) {
-            last[r] = static_cast<std::int32_t>(out.nextTokenIds.back());
-            result.generatedTokenIds[r].push_back(out.nextTokenIds.back());
+          who.push_back(r);
+          segments.push_back(std::move(segment));
+          row = (row + count + prefill->tileRows() - 1) / prefill->tileRows() * prefill->tileRows();
+        }
+        const auto out = prefill->runBatch(segments, false, false);
+        if (!out.passed) throw std::runtime_error(out.errorMessage);
+        std::size_t offset = 0;
+        for (std::size_t k = 0; k < who.size(); ++k) {
+          const std::size_t r = who[k], count = segments[k].tokenIds.size();
+          for (auto& state : states[r]) state->commitLength(consumed[r] + count);
+          consumed[r] += count;
+          offset += count;
+          if (consumed[r] == prompts[r].size()) {
+            last[r] = static_cast<std::int32_t>(out.nextTokenIds[offset - 1]);
+            result.generatedTokenIds[r].push_back(out.nextTokenIds[offset - 1]);
+            next = std::max(next, r + 1);
           }
         }
       }

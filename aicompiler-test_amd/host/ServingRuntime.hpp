@@ -56,6 +56,9 @@ struct ServingConfig {
   // > 0: prompts run at admission in chunks of this many tokens through the
   // chunked prefill executor; 0: prefill by decode in the batched ticks.
   std::size_t prefillChunkSize = 0;
+  // Requests whose prompts may share one chunk (1: one request per chunk,
+  // as the reference's per-request prefillChunked).
+  std::size_t prefillRequestsPerChunk = 1;
 };
 
 struct ServingRequestOutput {
@@ -105,11 +108,17 @@ using BatchedStep = std::function<BatchedDecodeRun(
     const std::vector<std::int32_t>& tokens, const std::vector<std::int32_t>& validLengths,
     const std::vector<std::vector<std::int32_t>>& tables, bool readLogits)>;
 
-// One prompt chunk of one request: tokens at positions start.. and the
-// request's per-layer tables in, per-row next tokens (and logits) out.
-using PrefillStep = std::function<BatchedDecodeRun(
-    const std::vector<std::int32_t>& tokens, std::size_t start,
-    const std::vector<std::vector<std::int32_t>>& tables, bool readLogits)>;
+// One prefill chunk: segments of up to `maxRequests` requests, each from a
+// multiple of `tileRows` rows, at most `chunkRows` rows in all
+// (ChunkedPrefillExecutor::runBatch).  Out: next tokens per segment row and,
+// when asked, each segment's last-row logits.
+using PrefillStep = std::function<BatchedDecodeRun(const std::vector<PrefillSegment>& segments,
+                                                   bool readLogits)>;
+struct PrefillPacking {
+  std::size_t chunkRows = 0;
+  std::size_t tileRows = 1;
+  std::size_t maxRequests = 1;
+};
 
 // The scheduler over existing pools and any step function (the CPU tests
 // drive it with host-only pools and a host step).  `prefill` is used when
@@ -119,7 +128,7 @@ using PrefillStep = std::function<BatchedDecodeRun(
     const std::vector<std::shared_ptr<KVPagePool>>& pools, std::size_t maximumBatchSize,
     std::size_t maxPages, const BatchedStep& step,
     const std::vector<ServingRequestSpec>& requests, const ServingConfig& config,
-    std::ostream& log, const PrefillStep& prefill = {});
+    std::ostream& log, const PrefillStep& prefill = {}, const PrefillPacking& packing = {});
 
 // runContinuousBatch (ServingRuntime.cpp:513-930) on the GPU: creates the
 // per-layer pools and the batched decode executor over `model`.

@@ -429,6 +429,25 @@ PYBIND11_MODULE(_tmc_host, m) {
            },
            py::arg("tokens"), py::arg("start"), py::arg("tables"), py::arg("read_logits") = true,
            py::arg("time_gpu") = false)
+      .def("run_batch",
+           [](ChunkedPrefillExecutor& e, const std::vector<py::tuple>& segments, bool readLogits,
+              bool timeGpu) {
+             std::vector<PrefillSegment> segs;
+             for (const auto& t : segments)
+               segs.push_back(PrefillSegment{t[0].cast<std::vector<std::int32_t>>(),
+                                             t[1].cast<std::size_t>(),
+                                             t[2].cast<std::vector<std::vector<std::int32_t>>>()});
+             BatchedDecodeRun run;
+             {
+               py::gil_scoped_release release;
+               run = e.runBatch(segs, readLogits, timeGpu);
+             }
+             return runToDict(run);
+           },
+           py::arg("segments"), py::arg("read_logits") = false, py::arg("time_gpu") = false)
+      .def("maximum_requests", &ChunkedPrefillExecutor::maximumRequests)
+      .def("tile_rows", &ChunkedPrefillExecutor::tileRows)
+      .def("packed_rows", &ChunkedPrefillExecutor::packedRows)
       .def("chunk_size", &ChunkedPrefillExecutor::chunkSize)
       .def("max_pages", &ChunkedPrefillExecutor::maxPages)
       .def("buckets", &ChunkedPrefillExecutor::buckets)
@@ -437,14 +456,16 @@ PYBIND11_MODULE(_tmc_host, m) {
 
   m.def("create_chunked_prefill_executor",
         [](hip::HipRuntime& rt, std::shared_ptr<DecoderLLMModelResources> model,
-           std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t chunkSize) {
+           std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t chunkSize,
+           std::size_t maxRequests) {
           std::ostringstream log;
           auto r = createChunkedPrefillExecutor(rt, std::move(model), std::move(pools), chunkSize,
-                                                &log);
+                                                &log, maxRequests);
           if (!r.executor) throw std::runtime_error(r.errorMessage + "\n" + log.str());
           return std::move(r.executor);
         },
-        py::arg("runtime"), py::arg("model"), py::arg("pools"), py::arg("chunk_size"));
+        py::arg("runtime"), py::arg("model"), py::arg("pools"), py::arg("chunk_size"),
+        py::arg("maximum_requests") = 1);
   m.def("decode_gemv_cache_size", []() { return planner::decodeGEMVTuningCache().size(); });
   m.def("clear_decode_gemv_cache", []() { planner::decodeGEMVTuningCache().clear(); });
 
@@ -528,7 +549,8 @@ PYBIND11_MODULE(_tmc_host, m) {
       .def_readwrite("record_decode_logits", &ServingConfig::recordDecodeLogits)
       .def_readwrite("record_prefill_logits", &ServingConfig::recordPrefillLogits)
       .def_readwrite("tune_kernels", &ServingConfig::tuneKernels)
-      .def_readwrite("prefill_chunk_size", &ServingConfig::prefillChunkSize);
+      .def_readwrite("prefill_chunk_size", &ServingConfig::prefillChunkSize)
+      .def_readwrite("prefill_requests_per_chunk", &ServingConfig::prefillRequestsPerChunk);
 
   m.def("run_continuous_batch",
         [](hip::HipRuntime& rt, std::shared_ptr<DecoderLLMModelResources> model,
@@ -580,21 +602,31 @@ PYBIND11_MODULE(_tmc_host, m) {
         [](hip::HipRuntime& rt, const planner::DecoderLLMPlan& plan,
            const std::vector<std::shared_ptr<KVPagePool>>& pools, std::size_t maxBatch,
            std::size_t maxPages, py::function step, const std::vector<ServingRequestSpec>& specs,
-           const ServingConfig& config, py::object prefillStep) {
-          // prefill(tokens, start, tables, read_logits) -> (next_tokens, logits)
+           const ServingConfig& config, py::object prefillStep, std::size_t tileRows,
+           std::size_t maxRequests) {
+          // prefill([(tokens, start, tables), ...], read_logits) ->
+          //   (next tokens of every segment row, last-row logits per segment)
           PrefillStep prefill;
+          PrefillPacking packing;
           if (!prefillStep.is_none()) {
-            prefill = [prefillStep](const std::vector<std::int32_t>& tokens, std::size_t start,
-                                    const std::vector<std::vector<std::int32_t>>& tables,
-                                    bool readLogits) {
+            prefill = [prefillStep](const std::vector<PrefillSegment>& segments, bool readLogits) {
               BatchedDecodeRun run;
-              py::tuple out = prefillStep(tokens, start, tables, readLogits);
+              py::list arg;
+              std::size_t rows = 0;
+              for (const auto& s : segments) {
+                arg.append(py::make_tuple(s.tokenIds, s.start, s.blockTables));
+                rows += s.tokenIds.size();
+              }
+              py::tuple out = prefillStep(arg, readLogits);
               run.nextTokenIds = out[0].cast<std::vector<float>>();
               if (readLogits) run.logits = toVector(out[1].cast<FloatArray>());
-              run.passed = run.nextTokenIds.size() == tokens.size();
+              run.passed = run.nextTokenIds.size() == rows;
               if (!run.passed) run.errorMessage = "prefill returned the wrong number of tokens";
               return run;
             };
+            packing.chunkRows = config.prefillChunkSize;
+            packing.tileRows = tileRows;
+            packing.maxRequests = maxRequests;
           }
           BatchedStep wrapped = [&step](const std::vector<std::int32_t>& tokens,
                                         const std::vector<std::int32_t>& lengths,
@@ -610,14 +642,15 @@ PYBIND11_MODULE(_tmc_host, m) {
           };
           std::ostringstream log;
           auto r = runContinuousBatch(rt, plan, pools, maxBatch, maxPages, wrapped, specs, config,
-                                      log, prefill);
+                                      log, prefill, packing);
           auto d = servingToDict(r);
           d["log"] = log.str();
           return d;
         },
         py::arg("runtime"), py::arg("plan"), py::arg("pools"), py::arg("maximum_batch_size"),
         py::arg("max_pages"), py::arg("step"), py::arg("specs"), py::arg("config"),
-        py::arg("prefill") = py::none());
+        py::arg("prefill") = py::none(), py::arg("prefill_tile_rows") = 1,
+        py::arg("prefill_max_requests") = 1);
   // Kernel selection (tuners and admission).
   py::class_<hip::DecodeGEMVConfig>(m, "DecodeGEMVConfig")
       .def(py::init<>())

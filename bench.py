@@ -293,7 +293,7 @@ def extra_measurements(tmc, torch, iters: int) -> dict:
 
 
 C5 = dict(layers=32, hidden=4096, heads=32, head_dim=128, intermediate=11008, vocabulary=32000,
-          capacity=1024, epsilon=1e-6, page_size=16, decode_tokens=128, prefill_chunk=512)
+          capacity=1024, epsilon=1e-6, page_size=16, decode_tokens=128, prefill_chunk=1024)
 # Chunked prefill of one long prompt on the same 7B shape (capacity 4096).
 PREFILL = dict(capacity=4096, prompts=(4095, 512), chunks=(512, 2048))
 

@@ -409,6 +409,17 @@ int tmc_prefill_rope_append(const void *qkv, const float *cosine, const float *s
                             int64_t kv_heads, int64_t head_dim, int64_t capacity,
                             int64_t page_size, int64_t max_pages, void *stream);
 
+/* Several requests in one prefill chunk: row r uses table row row_table[r]
+ * of block_tables [table_rows, max_pages]; rows whose entry is outside
+ * [0, table_rows) are skipped.  Otherwise as tmc_prefill_rope_append. */
+int tmc_prefill_rope_append_rows(const void *qkv, const float *cosine, const float *sine,
+                                 const int32_t *valid_lengths, const int32_t *block_tables,
+                                 const int32_t *row_table, int64_t table_rows,
+                                 const int32_t *active_count, void *q_out, void *key_pool,
+                                 void *value_pool, int dtype, int64_t rows, int64_t q_heads,
+                                 int64_t kv_heads, int64_t head_dim, int64_t capacity,
+                                 int64_t page_size, int64_t max_pages, void *stream);
+
 /* emitTiledGEMM (DecodeGEMVMetalEmitter.cpp:134-169), the prefill linear
  * layer: y[m, n] = x[m, k] weight[n, k]^T, fp16 inputs, fp32 accumulation,
  * y fp16 or fp32 (out_dtype), all row-major.  Runs on hipBLASLt; the first
@@ -437,6 +448,20 @@ int tmc_prefill_attention_f16(const void *q, const void *key_pool, const void *v
                               int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                               int64_t page_size, int64_t max_pages, int64_t pool_pages,
                               int64_t page_stride, int64_t head_stride, void *stream);
+
+/* Several requests in one prefill chunk: the rows are cut into tiles of
+ * 64 / (q_heads / kv_heads) tokens and a tile uses table row
+ * row_table[first row of the tile] of block_tables [table_rows, max_pages];
+ * a caller packing several requests starts each request at a tile boundary
+ * (a row of another table row inside a tile is left untouched).  With
+ * row_table NULL, table_rows must be 1 (tmc_prefill_attention_f16). */
+int tmc_prefill_attention_rows_f16(const void *q, const void *key_pool, const void *value_pool,
+                                   const int32_t *valid_lengths, const int32_t *block_tables,
+                                   const int32_t *row_table, int64_t table_rows,
+                                   const int32_t *active_count, void *out, int64_t rows,
+                                   int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                   int64_t page_size, int64_t max_pages, int64_t pool_pages,
+                                   int64_t page_stride, int64_t head_stride, void *stream);
 
 /* emitTokenArgmax (TransformerDecodeMetalEmitter.cpp:198-256): greedy token
  * per row over fp32 logits, ties to the lowest index. */

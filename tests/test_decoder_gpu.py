@@ -300,10 +300,11 @@ def test_batched_executor_rows_match_oracle(host, orc, rt):
     assert "capacity" in ex.run([1] * 5, [0] + lengths[1:], tables, False, False)["error"]
 
 
-@pytest.mark.parametrize("chunk", [0, 8])
-def test_serving_matches_single_request_decoding(host, orc, rt, chunk):
-    """chunk 0: prompts by decode in the batched ticks; chunk 8: prompts in
-    chunks through the chunked prefill executor at admission."""
+@pytest.mark.parametrize("chunk,per_chunk", [(0, 1), (8, 1), (64, 4)])
+def test_serving_matches_single_request_decoding(host, orc, rt, chunk, per_chunk):
+    """chunk 0: prompts by decode in the batched ticks; chunk > 0: prompts
+    in chunks through the chunked prefill executor at admission, one request
+    per chunk or up to four packed together."""
     cfg = CONFIGS["serve"]
     m = _weights(orc, cfg, 61)
     w = _workload(host, orc, cfg, m)
@@ -322,6 +323,7 @@ def test_serving_matches_single_request_decoding(host, orc, rt, chunk):
     config.physical_pages_per_layer = 6  # 4 pages hold one full request: page pressure
     config.record_decode_logits = True
     config.prefill_chunk_size = chunk
+    config.prefill_requests_per_chunk = per_chunk
     result = host.run_continuous_batch(rt, model, specs, config)
     assert result["passed"], result["error"]
     metrics = result["metrics"]

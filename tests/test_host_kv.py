@@ -114,7 +114,8 @@ def _reference_tokens(prompt, decode):
     return out
 
 
-def _run(host, specs, pages_per_layer, max_batch, page_size=4, layers=2, capacity=64, chunk=0):
+def _run(host, specs, pages_per_layer, max_batch, page_size=4, layers=2, capacity=64, chunk=0,
+         tile=1, per_chunk=1):
     rt = host.HipRuntime()
     plan = _decoder_plan(host, layers, capacity)
     pools = [host.create_host_kv_page_pool(plan.kv_plan(), page_size, pages_per_layer)
@@ -137,17 +138,26 @@ def _run(host, specs, pages_per_layer, max_batch, page_size=4, layers=2, capacit
         logits = np.zeros(rows * V, np.float32)
         return nxt, logits
 
-    def prefill(tokens, start, tables, read_logits):
-        """One prompt chunk of one request: rows are positions start.."""
-        rows = len(tokens)
-        assert 0 < rows <= chunk
-        need = (start + rows + page_size - 1) // page_size
-        for l in range(layers):
-            t = np.asarray(tables[l])
-            assert (t[:need] >= 0).all() and (t[need:] < 0).all()
-        seen.setdefault("chunks", []).append(rows)
-        nxt = [_next(t, start + r + 1) for r, t in enumerate(tokens)]
-        return nxt, np.zeros(rows * V, np.float32)
+    def prefill(segments, read_logits):
+        """One chunk: segments (tokens, start, tables) of different requests,
+        each from a multiple of `tile` rows, at most `chunk` rows in all."""
+        assert 0 < len(segments) <= per_chunk
+        row, out = 0, []
+        for i, (tokens, start, tables) in enumerate(segments):
+            rows = len(tokens)
+            assert rows > 0
+            row += rows
+            if i + 1 < len(segments):
+                row = -(-row // tile) * tile
+            need = (start + rows + page_size - 1) // page_size
+            for l in range(layers):
+                t = np.asarray(tables[l])
+                assert (t[:need] >= 0).all() and (t[need:] < 0).all()
+            out += [_next(t, start + r + 1) for r, t in enumerate(tokens)]
+            seen.setdefault("chunks", []).append(rows)
+        assert row <= chunk
+        seen.setdefault("segments_per_chunk", []).append(len(segments))
+        return out, np.zeros(len(segments) * V, np.float32)
 
     config = host.ServingConfig()
     config.page_size = page_size
@@ -155,7 +165,7 @@ def _run(host, specs, pages_per_layer, max_batch, page_size=4, layers=2, capacit
     config.maximum_batch_size = max_batch
     config.prefill_chunk_size = chunk
     result = host.run_continuous_batch_with(rt, plan, pools, max_batch, max_pages, step, specs,
-                                            config, prefill if chunk else None)
+                                            config, prefill if chunk else None, tile, per_chunk)
     return result, pools, seen
 
 
@@ -202,14 +212,17 @@ def test_scheduler_preempts_under_page_pressure_and_stays_exact(host):
     assert m["peak_pages_per_layer"] <= 16
 
 
-@pytest.mark.parametrize("pages,chunk", [(64, 5), (16, 8)])
-def test_scheduler_chunked_prefill_matches_sequential(host, pages, chunk):
+@pytest.mark.parametrize("pages,chunk,tile,per_chunk", [(64, 5, 1, 1), (16, 8, 1, 1),
+                                                     (64, 32, 8, 4), (16, 24, 4, 8)])
+def test_scheduler_chunked_prefill_matches_sequential(host, pages, chunk, tile, per_chunk):
     """Prompts run at admission in chunks (prefillChunked per request,
-    ServingRuntime.cpp:682-700); the outputs equal one-request decoding,
-    also when page pressure preempts decoding requests."""
+    ServingRuntime.cpp:682-700), one request per chunk or several packed at
+    tile boundaries; the outputs equal one-request decoding, also when page
+    pressure preempts decoding requests."""
     rng = np.random.default_rng(4)
     specs = _specs(host, rng, 8, prompt=(10, 24), decode=(4, 16), arrivals=3)
-    result, pools, seen = _run(host, specs, pages_per_layer=pages, max_batch=8, chunk=chunk)
+    result, pools, seen = _run(host, specs, pages_per_layer=pages, max_batch=8, chunk=chunk,
+                               tile=tile, per_chunk=per_chunk)
     assert result["passed"], result["error"]
     for spec, out in zip(specs, result["requests"]):
         assert out["generated_token_ids"] == _reference_tokens(spec.prompt_token_ids,
@@ -217,8 +230,12 @@ def test_scheduler_chunked_prefill_matches_sequential(host, pages, chunk):
     m = result["metrics"]
     total = sum(len(s.prompt_token_ids) for s in specs)
     assert m["prompt_tokens"] == total == sum(seen["chunks"])
-    assert m["prefill_chunk_submissions"] == len(seen["chunks"])
-    assert m["prefill_chunk_submissions"] == sum(-(-len(s.prompt_token_ids) // chunk) for s in specs)
+    assert m["prefill_chunk_submissions"] == len(seen["segments_per_chunk"])
+    if per_chunk == 1:
+        assert m["prefill_chunk_submissions"] == sum(-(-len(s.prompt_token_ids) // chunk)
+                                                     for s in specs)
+    else:
+        assert max(seen["segments_per_chunk"]) > 1
     assert all(p.used_pages() == 0 for p in pools)
     assert m["peak_pages_per_layer"] <= pages
 

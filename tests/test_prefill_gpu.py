@@ -320,3 +320,147 @@ def test_chunked_prefill_executor_direct(host, orc, rt):
     short = [t[:1] + [-1] * (max_pages - 1) for t in tables]
     r = ex.run([1] * 20, 10, short)
     assert not r["passed"] and "not allocated" in r["error"]
+
+
+# ------------------------------------------------- several requests per chunk
+@pytest.mark.parametrize("qh,kvh,d", [(8, 8, 128), (16, 4, 128), (4, 2, 64)])
+def test_prefill_rows_several_requests(tmc, orc, torch, qh, kvh, d):
+    """Three requests packed in one chunk, each from a tile boundary (tile =
+    64 / group rows), with their own tables and starts: RoPE + append equals
+    the per-row decode form bit for bit, attention equals the oracle's causal
+    attention per request, and padding rows are left untouched."""
+    group = qh // kvh
+    tile = 64 // group
+    p, cap = 16, 256
+    max_pages = cap // p
+    pages = 3 * max_pages + 4
+    perm = np.random.default_rng(760).permutation(pages).astype(np.int32)
+    tables = perm[:3 * max_pages].reshape(3, max_pages).copy()
+    counts, starts = [tile + 5, 3, 2 * tile], [17, 0, 100]
+    firsts, row = [], 0
+    for i, c in enumerate(counts):
+        firsts.append(row)
+        row = row + c if i == 2 else -(-(row + c) // tile) * tile
+    rows = row
+    lengths = np.zeros(rows, np.int32)
+    row_table = np.full(rows, -1, np.int32)
+    for i, (f, c, s0) in enumerate(zip(firsts, counts, starts)):
+        lengths[f:f + c] = s0 + np.arange(c) + 1
+        row_table[f:f + c] = i
+    pos = np.arange(cap)[:, None]
+    freq = np.exp(np.arange(0, d, 2) * (-np.log(10000.0) / d))
+    cos, sin = np.cos(pos * freq).astype(np.float32), np.sin(pos * freq).astype(np.float32)
+    qkv = orc.f16(normal(761, (rows, (qh + 2 * kvh) * d)))
+    pool0 = orc.f16(normal(762, (pages, kvh, p, d)))
+    act = torch.tensor([rows], dtype=torch.int32, device="cuda")
+    # RoPE + append: row-table form vs per-row decode form
+    outs = []
+    for form in ("rows", "decode"):
+        kp, vp = dev_f16(pool0), dev_f16(pool0.copy())
+        q_out = torch.full((rows, qh * d), float("nan"), dtype=torch.float16, device="cuda")
+        if form == "rows":
+            tmc.prefill_rope_append_rows(dev_f16(qkv), dev(cos), dev(sin), dev(lengths),
+                                         dev(tables), dev(row_table), act, q_out, kp, vp, rows, qh,
+                                         kvh, d, cap, p, max_pages)
+        else:
+            per_row = np.where(row_table[:, None] >= 0, tables[np.maximum(row_table, 0)], -1)
+            tmc.decode_rope_append(dev_f16(qkv), dev(cos), dev(sin), dev(lengths),
+                                   dev(per_row.astype(np.int32)), act, q_out, kp, vp, rows, qh, kvh,
+                                   d, cap, p, max_pages)
+        torch.cuda.synchronize()
+        outs.append((bits(q_out), bits(kp), bits(vp), q_out, kp, vp))
+    for a, b in zip(outs[0][:3], outs[1][:3]):
+        assert np.array_equal(a, b)
+    # attention over the pools the append wrote
+    q_out, kp, vp = outs[0][3:]
+    ctx = torch.full((rows, qh * d), float("nan"), dtype=torch.float16, device="cuda")
+    tmc.prefill_attention_rows(q_out, kp, vp, dev(lengths), dev(tables), dev(row_table), act, ctx,
+                               rows, qh, kvh, d, p, max_pages, kvh * p * d, p * d)
+    torch.cuda.synchronize()
+    got = values(ctx)
+    k_np, v_np = bits(kp).reshape(pages, kvh, p, d), bits(vp).reshape(pages, kvh, p, d)
+    q_np = bits(q_out)
+    padding = row_table < 0
+    assert np.isnan(got[padding]).all()
+    for i, (f, c, s0) in enumerate(zip(firsts, counts, starts)):
+        ref, written = orc.causal_prefill_attention(q_np[f:f + c], k_np, v_np, F16, qh, kvh, d, p,
+                                                    kvh * p * d, p * d, tables[i], max_pages,
+                                                    s0 + c, c)
+        assert written.all()
+        assert_f16_path(got[f:f + c], ref, what=f"request {i} rows")
+
+
+def test_chunked_prefill_run_batch_matches_single_requests(host, orc, rt):
+    """runBatch of three requests' segments (one split across two chunks)
+    gives the next tokens, last-row logits and caches that single-request
+    chunks give."""
+    cfg = CONFIGS["serve"]
+    m = _weights(orc, cfg, 71)
+    w = _workload(host, orc, cfg, m)
+    model = host.create_model_resources(rt, w)
+    kv = w.plan.kv_plan()
+    V = cfg["vocabulary"]
+    prompts = [np.random.default_rng(72 + i).integers(0, V, n) for i, n in enumerate((21, 7, 40))]
+
+    def run(batched):
+        pools = [host.create_kv_page_pool(rt, kv, P, 16) for _ in range(cfg["layers"])]
+        ex = host.create_chunked_prefill_executor(rt, model, pools, 64, 4 if batched else 1)
+        states = [[host.create_kv_cache_state(rt, kv, pool, False) for pool in pools]
+                  for _ in prompts]
+
+        def segment(i, start, count):
+            for s in states[i]:
+                assert s.stage_length(rt, start + count) == ""
+            tables = [s.page_table() + [-1] * (ex.max_pages() - len(s.page_table()))
+                      for s in states[i]]
+            return ([int(t) for t in prompts[i][start:start + count]], start, tables)
+
+        def commit(i, length):
+            for s in states[i]:
+                s.commit_length(length)
+
+        nxt, logits = {}, {}
+        if batched:
+            assert ex.tile_rows() == 32 and ex.maximum_requests() == 4
+            # chunk 1: request 0 (21 rows, padded to 32) and request 1 (7)
+            first = [segment(0, 0, 21), segment(1, 0, 7)]
+            assert ex.packed_rows([21, 7]) == 39
+            out = ex.run_batch(first, True)
+            assert out["passed"], out["error"]
+            commit(0, 21)
+            commit(1, 7)
+            ids = out["next_token_ids"]
+            nxt[0], nxt[1] = ids[20], ids[27]
+            logits[0], logits[1] = out["logits"][:V], out["logits"][V:]
+            second = [segment(2, 0, 30)]
+            out = ex.run_batch(second, False)
+            assert out["passed"], out["error"]
+            commit(2, 30)
+            third = [segment(2, 30, 10)]
+            out = ex.run_batch(third, True)
+            assert out["passed"], out["error"]
+            commit(2, 40)
+            nxt[2], logits[2] = out["next_token_ids"][-1], out["logits"]
+        else:
+            for i, prompt in enumerate(prompts):
+                done = 0
+                while done < len(prompt):
+                    c = min(64, len(prompt) - done)
+                    tokens, start, tables = segment(i, done, c)
+                    out = ex.run(tokens, start, tables, True)
+                    assert out["passed"], out["error"]
+                    commit(i, done + c)
+                    done += c
+                nxt[i], logits[i] = out["next_token_ids"][-1], out["logits"][-V:]
+        caches = [[s.read_key_prefix() for s in st] for st in states]
+        return nxt, logits, caches
+
+    n1, l1, c1 = run(False)
+    n2, l2, c2 = run(True)
+    for i in range(3):
+        assert_f16_path(l2[i], l1[i], what=f"request {i} last-row logits")
+        if n1[i] != n2[i]:
+            top = np.sort(l1[i])[-2:]
+            assert top[1] - top[0] <= 2e-2
+        for a, b in zip(c1[i], c2[i]):
+            assert_f16_path(b, a, what=f"request {i} keys")
