@@ -80,13 +80,49 @@ struct PaBlockRegs {
 // position is at or past `end` or its page is absent).  BUF (pools below
 // 4 GiB): raw buffer loads with the out-of-range offset for absent data, so
 // every load issues unconditionally; otherwise predicated global loads.
-template <int D, bool BUF>
+template <int D, bool BUF, bool OFFS>
 __device__ __forceinline__ void pa_load(const PrefillParams& p, const int* table, int kvh, int base,
                                         int end, PaBlockRegs<D>& r) {
   using R = PaBlockRegs<D>;
   constexpr int CH = D / 8;  // 16-byte chunks per position
   const int tid = (int)threadIdx.x;
   __builtin_assume(tid < kPaThreads);
+  const h8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  const __amdgpu_buffer_rsrc_t rk = buffer_resource(p.k, p.pool_bytes);
+  const __amdgpu_buffer_rsrc_t rv = buffer_resource(p.v, p.pool_bytes);
+  if constexpr (OFFS) {
+    // `table` holds each page's byte offset for this kv head (kBufferAbsent
+    // for an absent page) and the page size is a power of two of at least 4:
+    // a 4-position V group lies in one page, so it costs one lookup.
+    const int shift = p.page_shift, mask = p.page_size - 1;
+    auto page_off = [&](int pos) -> unsigned {
+      return (unsigned)table[pos < end ? pos >> shift : 0];
+    };
+#pragma unroll
+    for (int i = 0; i < R::kPer; ++i) {
+      const int item = tid + i * kPaThreads;
+      const int pos = base + item / CH;
+      const unsigned off = page_off(pos);
+      const bool ok = pos < end && off != kBufferAbsent &&
+                      (R::kItems % kPaThreads == 0 || item < R::kItems);
+      r.k[i] = buffer_load_h8(
+          rk, ok ? off + (unsigned)(((pos & mask) * D + 8 * (item % CH)) * 2) : kBufferAbsent);
+    }
+#pragma unroll
+    for (int i = 0; i < R::vPer; ++i) {
+      const int item = tid + i * kPaThreads;
+      const int quad = item % (kPaBlock / 4), octet = item / (kPaBlock / 4);
+      const int pos0 = base + 4 * quad;
+      const unsigned off = page_off(pos0);
+      const unsigned row0 = off + (unsigned)(((pos0 & mask) * D + 8 * octet) * 2);
+      const bool group_ok = off != kBufferAbsent && (R::vItems % kPaThreads == 0 || item < R::vItems);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        r.v[q][i] = buffer_load_h8(
+            rv, group_ok && pos0 + q < end ? row0 + (unsigned)(q * D * 2) : kBufferAbsent);
+    }
+    return;
+  }
   const bool pow2 = p.page_shift >= 0;
   // Element offset of (pos, 8-element column), or -1 when absent; computed
   // with selects only (table[0] exists whenever end > 0).
@@ -105,9 +141,6 @@ __device__ __forceinline__ void pa_load(const PrefillParams& p, const int* table
       return ok ? e : -1;
     }
   };
-  const h8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-  const __amdgpu_buffer_rsrc_t rk = buffer_resource(p.k, p.pool_bytes);
-  const __amdgpu_buffer_rsrc_t rv = buffer_resource(p.v, p.pool_bytes);
 #pragma unroll
   for (int i = 0; i < R::kPer; ++i) {
     const int item = tid + i * kPaThreads;
@@ -173,8 +206,8 @@ __device__ __forceinline__ void pa_store(PaBlockRegs<D>& r, half_t* sk, half_t* 
 template <int D>
 __device__ __forceinline__ void pa_compute(const PrefillParams& p, const half_t* s_k,
                                            const half_t* s_vt, const h8 (&qb)[D / 32], int base,
-                                           int len, int j, int g, float& m, float& lsum,
-                                           f4 (&o)[D / 16]) {
+                                           int len, bool full, int j, int g, float& m,
+                                           float& lsum, f4 (&o)[D / 16]) {
   constexpr int KS = D / 32;
   constexpr int DT = D / 16;
   // Scores S^T[pos][query] for 4 tiles of 16 positions.
@@ -191,7 +224,8 @@ __device__ __forceinline__ void pa_compute(const PrefillParams& p, const half_t*
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int pos = base + 16 * kt + 4 * g + r;
-      sc[kt][r] = pos < len ? acc[r] * p.scale_log2 : -INFINITY;
+      // full: the whole block lies below every query's length in this wave
+      sc[kt][r] = full || pos < len ? acc[r] * p.scale_log2 : -INFINITY;
       bmax = fmaxf(bmax, sc[kt][r]);
     }
   }
@@ -206,7 +240,7 @@ __device__ __forceinline__ void pa_compute(const PrefillParams& p, const half_t*
   for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float pr = sc[kt][r] == -INFINITY ? 0.0f : fast_exp2(sc[kt][r] - next);
+      const float pr = !full && sc[kt][r] == -INFINITY ? 0.0f : fast_exp2(sc[kt][r] - next);
       const half_t ph = (half_t)pr;
       psum += (float)ph;  // the denominator sums the weights the product uses
       pb[kt >> 1][4 * (kt & 1) + r] = ph;
@@ -231,7 +265,8 @@ __device__ __forceinline__ void pa_compute(const PrefillParams& p, const half_t*
 
 // TLDS: the request's block table is staged in LDS (dynamic, max_pages
 // entries) so a block's K/V addresses need no global round trip first.
-// BUF: see pa_load.
+// BUF: see pa_load.  With TLDS, BUF and a power-of-two page size of at
+// least 4 the LDS table holds byte offsets (pa_load's OFFS form).
 template <int D, bool TLDS, bool BUF>
 __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillParams p) {
   constexpr int KS = D / 32;  // k-steps of the score product
@@ -280,6 +315,7 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillPa
     if (p.row_table && p.row_table[token] != tile_table) len = -1;
   }
 
+  const bool offs = TLDS && BUF && p.page_shift >= 2;  // workgroup-uniform
   // Attended extent of the tile and the first absent page below it.
   if (threadIdx.x == 0) {
     s_bounds[0] = 0;
@@ -295,8 +331,16 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillPa
     int first_bad = 0x7fffffff;
     for (int i = threadIdx.x; i < pages; i += kPaThreads) {
       const int page = request_table[i];
-      if (TLDS) s_table[i] = page;
-      if (page < 0 || page >= p.pool_pages) first_bad = min(first_bad, i);
+      const bool ok = page >= 0 && page < p.pool_pages;
+      if (TLDS) {
+        if (offs)
+          s_table[i] = (int)(ok ? (unsigned)(((long)page * p.page_stride +
+                                              (long)kvh * p.head_stride) * 2)
+                                : kBufferAbsent);
+        else
+          s_table[i] = page;
+      }
+      if (!ok) first_bad = min(first_bad, i);
     }
     if (first_bad != 0x7fffffff) atomicMin(&s_bounds[1], first_bad);
   }
@@ -316,17 +360,26 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillPa
   float m = -INFINITY, lsum = 0.0f;
 
   const int* table = TLDS ? s_table : request_table;
+  // Shortest length among the wave's live queries: blocks below it need no mask.
+  int wave_min = len > 0 ? len : 0x7fffffff;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) wave_min = min(wave_min, __shfl_xor(wave_min, off, kWave));
   // The next block's loads are issued as soon as the current one is in LDS
   // and land during its compute.  (Two or three blocks in flight measured
   // no faster.)
   PaBlockRegs<D> regs;
-  pa_load<D, BUF>(p, table, kvh, 0, end, regs);
+  auto load = [&](int at) {
+    if (offs) pa_load<D, BUF, TLDS && BUF>(p, table, kvh, at, end, regs);
+    else pa_load<D, BUF, false>(p, table, kvh, at, end, regs);
+  };
+  load(0);
   for (int base = 0; base < end; base += kPaBlock) {
     __syncthreads();  // the previous block's LDS reads are done
     pa_store<D>(regs, s_k, s_vt);
     __syncthreads();
-    if (base + kPaBlock < end) pa_load<D, BUF>(p, table, kvh, base + kPaBlock, end, regs);
-    pa_compute<D>(p, s_k, s_vt, qb, base, len, j, g, m, lsum, o);
+    if (base + kPaBlock < end) load(base + kPaBlock);
+    const bool full = base + kPaBlock <= wave_min;  // wave-uniform
+    pa_compute<D>(p, s_k, s_vt, qb, base, len, full, j, g, m, lsum, o);
   }
 
   lsum += __shfl_xor(lsum, 16, kWave);
