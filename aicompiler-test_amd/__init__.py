@@ -39,6 +39,8 @@ def _declare(l):
         "tmc_gemv_f16": (i32, [vp, vp, vp, i32, i64, i64, i64, vp]),
         "tmc_skinny_gemm_f16_mfma": (i32, [vp, vp, vp, i32, i64, i64, i64, vp]),
         "tmc_gemv_f16_config": (i32, [vp, vp, vp, i32, i64, i64, i64, vp, vp]),
+        "tmc_qkv_rope_append_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64,
+                                          i64, i64, i64, vp, vp]),
         "tmc_gate_up_silu_f16_config": (i32, [vp, vp, vp, vp, i64, i64, i64, vp, vp]),
         "tmc_gemv_default_config": (i32, [i64, i64, i64, i32, vp]),
         "tmc_gate_up_silu_f16": (i32, [vp, vp, vp, vp, i64, i64, i64, vp]),
@@ -97,6 +99,7 @@ def _declare(l):
         "tmc_buf_wrap": (i32, [vp, vp, sz, i32, C.POINTER(vp)]),
         "tmc_buf_write": (i32, [vp, vp, sz, sz]),
         "tmc_buf_write_raw": (i32, [vp, vp, sz, sz]),
+        "tmc_buf_write_raw_async": (i32, [vp, vp, sz, sz]),
         "tmc_buf_read_raw": (i32, [vp, vp, sz, sz]),
         "tmc_buf_read": (i32, [vp, vp]),
         "tmc_buf_count": (sz, [vp]),
@@ -429,6 +432,21 @@ def decode_rope_append(qkv, cos, sin, valid_lengths, tables, active, q_out, k_po
           "tmc_decode_rope_append")
 
 
+def qkv_rope_append(x, w, cos, sin, valid_lengths, table, active, q_out, k_pool, v_pool, q_heads,
+                    kv_heads, head_dim, capacity, page_size, config=None, stream=None):
+    """Batch-1 q.k.v projection x @ w.T with RoPE and the paged K/V append
+    fused in its epilogue (tmc_qkv_rope_append_f16)."""
+    cfg = None
+    if config is not None:
+        cfg = GemvConfig(*config) if isinstance(config, tuple) else config
+    check(lib().tmc_qkv_rope_append_f16(_ptr(x), _ptr(w), _ptr(cos), _ptr(sin), _ptr(valid_lengths),
+                                        _ptr(table), _ptr(active), _ptr(q_out), _ptr(k_pool),
+                                        _ptr(v_pool), x.shape[-1], q_heads, kv_heads, head_dim,
+                                        capacity, page_size, None if cfg is None else C.byref(cfg),
+                                        _stream(stream)),
+          "tmc_qkv_rope_append_f16")
+
+
 def prefill_rope_append(qkv, cos, sin, valid_lengths, table, active, q_out, k_pool, v_pool, rows,
                         q_heads, kv_heads, head_dim, capacity, page_size, max_pages, stream=None):
     check(lib().tmc_prefill_rope_append(_ptr(qkv), _ptr(cos), _ptr(sin), _ptr(valid_lengths),
@@ -652,6 +670,15 @@ class Buffer:
         out = np.empty(self.count, dtype=np.float32)
         check(lib().tmc_buf_read(self.handle, out.ctypes.data_as(C.c_void_p)), "tmc_buf_read")
         return out
+
+    def write_raw_async(self, data, offset: int = 0) -> None:
+        """Raw storage bits queued on the runtime stream (no host wait);
+        `data` may be reused as soon as this returns."""
+        import numpy as np
+        dt = {F16: np.uint16, BF16: np.uint16, F32: np.float32, I32: np.int32}[self.dtype]
+        src = np.ascontiguousarray(data, dtype=dt).ravel()
+        check(lib().tmc_buf_write_raw_async(self.handle, src.ctypes.data_as(C.c_void_p), src.size,
+                                            offset), "tmc_buf_write_raw_async")
 
     def read_raw(self):
         import numpy as np

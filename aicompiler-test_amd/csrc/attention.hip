@@ -37,6 +37,11 @@ constexpr int kMfmaTiles = 2;
 constexpr int kMfmaStep = 16 * kMfmaTiles;
 constexpr int kMfmaMinChunk = 128;  // four waves x one 32-position step
 constexpr int kMfmaMaxChunk = 1024;
+// One-split blocks of 16 waves (D = 128, see split_plan): a wave walks at
+// most two 32-position steps of a 1024-position row.  GQA groups up to 2:
+// at 1024 threads a lane has 128 registers, and a group of 4 spills.
+constexpr int kWideWaves = 16;
+constexpr int kWideMaxGroup = 2;
 
 struct AttnParams {
   const half_t* q;
@@ -53,6 +58,7 @@ struct AttnParams {
   int page_shift;         // log2(page_size) when it is a power of two, else -1
   long pool_pages;        // paged: pages in each pool (0 = unknown, no bound check)
   int chunk;              // positions per split
+  int waves;              // waves per block (D = 128: kWaves, or kWideWaves for one split)
   unsigned kv_bytes;      // bytes of the K (and of the V) buffer when < 4 GiB, else 0
   float scale_log2;       // (1/sqrt(D)) * log2(e)
 };
@@ -147,7 +153,7 @@ __device__ __forceinline__ void attend_tile(const h8 (&qv)[GROUP], const h8 (&kt
 // attended range needs a negative page keep their output untouched (the
 // reference kernel returns before writing); attn_combine_kernel applies the
 // same rule for multi-split rows.
-template <int D, int GROUP, bool PAGED>
+template <int D, int GROUP, bool PAGED, int WAVES = kWaves>
 __device__ void finish_split(const AttnParams& p, int b, int kvh, int split, int nsplit,
                              bool bad, const float (*s_m)[GROUP], const float (*s_l)[GROUP],
                              const float (*s_o)[GROUP][D]) {
@@ -157,14 +163,14 @@ __device__ void finish_split(const AttnParams& p, int b, int kvh, int split, int
   // output untouched when any slot is marked.
   const bool single = nsplit == 1;
   if (single && bad) return;
-  for (int idx = threadIdx.x; idx < GROUP * D; idx += kThreads) {
+  for (int idx = threadIdx.x; idx < GROUP * D; idx += WAVES * kWave) {
     const int g = idx / D, d = idx % D;
     float mx = s_m[0][g];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][g]);
+    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, s_m[w][g]);
     float lsum = 0.0f, osum = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < WAVES; ++w) {
       const float scale = s_m[w][g] == -INFINITY ? 0.0f : fast_exp2(s_m[w][g] - mx);
       lsum += scale * s_l[w][g];
       osum += scale * s_o[w][g][d];
@@ -494,14 +500,14 @@ __device__ __forceinline__ void consume_step(const AttnParams& p, const int* s_p
   __builtin_amdgcn_wave_barrier();
 }
 
-template <int GROUP, int MODE>
-__global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnParams p) {
+template <int GROUP, int MODE, int WAVES>
+__global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) {
   constexpr int D = 128;
   constexpr bool PAGED = MODE != 0;
-  __shared__ float s_m[kWaves][GROUP];
-  __shared__ float s_l[kWaves][GROUP];
-  __shared__ float s_o[kWaves][GROUP][D];
-  __shared__ float s_p[kWaves][kMfmaStep][GROUP];
+  __shared__ float s_m[WAVES][GROUP];
+  __shared__ float s_l[WAVES][GROUP];
+  __shared__ float s_o[WAVES][GROUP][D];
+  __shared__ float s_p[WAVES][kMfmaStep][GROUP];
   __shared__ int s_pages[PAGED ? kMfmaMaxChunk + 1 : 1];
 
   const int CHUNK = p.chunk;
@@ -532,7 +538,7 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnParams p) {
     page0 = page_of(p, begin);
     const int entries = page_of(p, end - 1) - page0 + 1;
     int bad_page = 0;
-    for (int i = threadIdx.x; i < entries; i += kThreads) {
+    for (int i = threadIdx.x; i < entries; i += WAVES * kWave) {
       const int page = p.tables[(size_t)b * p.max_pages + page0 + i];
       s_pages[i] = page;
       bad_page |= page < 0 || (p.pool_pages > 0 && page >= p.pool_pages);
@@ -550,7 +556,7 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnParams p) {
   const __amdgpu_buffer_rsrc_t rv = buffer_of(p.v, p.kv_bytes);
   float (*s_pw)[GROUP] = s_p[wave];
 
-  for (int p0 = begin + kMfmaStep * wave; p0 < end; p0 += kMfmaStep * kWaves) {
+  for (int p0 = begin + kMfmaStep * wave; p0 < end; p0 += kMfmaStep * WAVES) {
     KvStep<MODE> st;
     issue_step<MODE>(p, s_pages, page0, cbase, kvh, p0, end, j, g, rk, rv, st);
     consume_step<GROUP, MODE>(p, s_pages, page0, st, qb, p0, end, j, g, s_pw, m, lsum, o);
@@ -572,19 +578,33 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnParams p) {
     }
   }
   __syncthreads();
-  finish_split<D, GROUP, PAGED>(p, b, kvh, split, nsplit, bad, s_m, s_l, s_o);
+  finish_split<D, GROUP, PAGED, WAVES>(p, b, kvh, split, nsplit, bad, s_m, s_l, s_o);
 }
 
 template <int D, int GROUP, bool PAGED>
 int launch_group(const AttnParams& p, int batch, hipStream_t stream) {
   const dim3 grid((unsigned)p.kv_heads, (unsigned)p.max_splits, (unsigned)batch);
   if constexpr (D == 128) {
-    if (p.kv_bytes != 0 && !PAGED)
-      hipLaunchKernelGGL((attn_mfma_kernel<GROUP, 0>), grid, dim3(kThreads), 0, stream, p);
+    if (p.waves == kWideWaves) {
+      if constexpr (GROUP <= kWideMaxGroup) {
+        const dim3 block(kWideWaves * kWave);
+        if (p.kv_bytes != 0 && !PAGED)
+          hipLaunchKernelGGL((attn_mfma_kernel<GROUP, 0, kWideWaves>), grid, block, 0, stream, p);
+        else if (p.kv_bytes != 0 && p.page_size % 16 == 0)
+          hipLaunchKernelGGL((attn_mfma_kernel<GROUP, 1, kWideWaves>), grid, block, 0, stream, p);
+        else if (PAGED)
+          hipLaunchKernelGGL((attn_mfma_kernel<GROUP, 2, kWideWaves>), grid, block, 0, stream, p);
+        else
+          return fail("Attention: contiguous caches of 4 GiB or more are not supported.");
+      } else {
+        return fail("Attention: internal error (wide blocks for a large GQA group).");
+      }
+    } else if (p.kv_bytes != 0 && !PAGED)
+      hipLaunchKernelGGL((attn_mfma_kernel<GROUP, 0, kWaves>), grid, dim3(kThreads), 0, stream, p);
     else if (p.kv_bytes != 0 && p.page_size % 16 == 0)
-      hipLaunchKernelGGL((attn_mfma_kernel<GROUP, 1>), grid, dim3(kThreads), 0, stream, p);
+      hipLaunchKernelGGL((attn_mfma_kernel<GROUP, 1, kWaves>), grid, dim3(kThreads), 0, stream, p);
     else if (PAGED)
-      hipLaunchKernelGGL((attn_mfma_kernel<GROUP, 2>), grid, dim3(kThreads), 0, stream, p);
+      hipLaunchKernelGGL((attn_mfma_kernel<GROUP, 2, kWaves>), grid, dim3(kThreads), 0, stream, p);
     else
       return fail("Attention: contiguous caches of 4 GiB or more are not supported.");
   } else {
@@ -640,6 +660,25 @@ int chunk_for(int64_t head_dim, int64_t batch, int64_t kv_heads, int64_t capacit
 
 bool head_dim_ok(int64_t head_dim) { return chunk_for(head_dim, 1, 1, 1) > 0; }
 
+// Split geometry of a launch.  When chunk_for would cut a row into several
+// splits but the whole capacity fits one block (<= 1024 positions, D = 128,
+// GQA group <= 2), one block of 16 waves covers the row instead: no partial
+// slots and no combine launch.  Small batches (batch-1 decode, whose
+// attention is launch-latency bound) take this path.
+struct SplitPlan {
+  int chunk;
+  int waves;
+};
+
+SplitPlan split_plan(int64_t head_dim, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                     int64_t capacity) {
+  const int chunk = chunk_for(head_dim, batch, kv_heads, capacity);
+  if (head_dim == 128 && chunk > 0 && capacity > chunk && capacity <= kMfmaMaxChunk &&
+      q_heads / kv_heads <= kWideMaxGroup)
+    return {(int)((capacity + kMfmaStep - 1) / kMfmaStep * kMfmaStep), kWideWaves};
+  return {chunk, kWaves};
+}
+
 template <bool PAGED>
 int dispatch_attention(const AttnParams& p, int batch, int head_dim, hipStream_t stream) {
   switch (head_dim) {
@@ -663,7 +702,7 @@ int common_checks(const void* q, const void* k, const void* v, const void* out, 
                   q_heads % kv_heads == 0 && capacity > 0 && capacity < (1LL << 30),
               "Attention: invalid batch, head counts or capacity.");
   TMC_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v), "Attention: q, K and V must be 16-byte aligned.");
-  const int chunk = chunk_for(head_dim, batch, kv_heads, capacity);
+  const int chunk = split_plan(head_dim, batch, q_heads, kv_heads, capacity).chunk;
   TMC_REQUIRE((capacity + chunk - 1) / chunk <= 1024, "Attention: capacity exceeds 1024 splits.");
   return 0;
 }
@@ -676,7 +715,7 @@ using namespace tmc;
 extern "C" size_t tmc_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads,
                                                 int64_t head_dim, int64_t capacity) {
   if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || capacity <= 0 || q_heads % kv_heads) return 0;
-  const int chunk = chunk_for(head_dim, batch, kv_heads, capacity);
+  const int chunk = split_plan(head_dim, batch, q_heads, kv_heads, capacity).chunk;
   if (chunk <= 0) return 0;
   const int64_t splits = (capacity + chunk - 1) / chunk;
   if (splits <= 1) return 0;
@@ -711,7 +750,9 @@ extern "C" int tmc_decode_attention(const void* q, const void* key_cache, const 
     const uint64_t bytes = (uint64_t)batch * kv_heads * capacity * head_dim * 2;
     p.kv_bytes = bytes < kAbsent ? (unsigned)bytes : 0u;
   }
-  p.chunk = chunk_for(head_dim, batch, kv_heads, capacity);
+  const SplitPlan plan = split_plan(head_dim, batch, q_heads, kv_heads, capacity);
+  p.chunk = plan.chunk;
+  p.waves = plan.waves;
   p.max_splits = (int)((capacity + p.chunk - 1) / p.chunk);
   p.scale_log2 = (float)(1.0 / std::sqrt((double)head_dim)) * 1.4426950408889634f;
   return dispatch_attention<false>(p, (int)batch, (int)head_dim, as_stream(stream));
@@ -762,7 +803,9 @@ extern "C" int tmc_paged_decode_attention(const void* q, const void* key_pool,
     p.kv_bytes = pool_pages > 0 && bytes < kAbsent ? (unsigned)bytes : 0u;
   }
   p.max_pages = (int)max_pages;
-  p.chunk = chunk_for(head_dim, max_batch, kv_heads, capacity);
+  const SplitPlan plan = split_plan(head_dim, max_batch, q_heads, kv_heads, capacity);
+  p.chunk = plan.chunk;
+  p.waves = plan.waves;
   p.max_splits = (int)((capacity + p.chunk - 1) / p.chunk);
   p.scale_log2 = (float)(1.0 / std::sqrt((double)head_dim)) * 1.4426950408889634f;
   return dispatch_attention<true>(p, (int)max_batch, (int)head_dim, as_stream(stream));

@@ -261,15 +261,6 @@ __global__ __launch_bounds__(kThreads) void embedding_kernel(const int32_t* __re
     out[(size_t)row * hidden + f] = table[(size_t)token * hidden + f];
 }
 
-// Interleaved pair rotation shared by every RoPE kernel, written with explicit
-// fused multiply-adds so that all of them produce the same bits for the same
-// pair (the fused decode kernel below relies on it).
-__device__ __forceinline__ void rotate_pair(float even, float odd, float c, float s,
-                                            float& out_even, float& out_odd) {
-  out_even = __fmaf_rn(even, c, -(odd * s));
-  out_odd = __fmaf_rn(even, s, odd * c);
-}
-
 // emitDecoderRoPE (DecoderLLMMetalEmitter.cpp:110-158).
 template <typename T>
 __global__ __launch_bounds__(kThreads) void rope_kernel(const T* __restrict__ x,

@@ -66,6 +66,61 @@ struct NormArgs {
   float eps = 0.0f;
 };
 
+// Epilogue of the batch-1 q.k.v projection fused with RoPE and the paged
+// K/V append (ROPE = true, two rows per wave): the rows 2i and 2i+1 of the
+// projection are one interleaved RoPE pair of q or k, or two v features.
+// The pair is rounded to fp16 as the projection output would be, rotated
+// exactly as decode_rope_append_kernel rotates it, and stored where that
+// kernel stores it: q to q_out, k and v into the pools at position
+// valid_lengths[0] - 1 through block_table (one request).
+struct RopeArgs {
+  const float* cosine = nullptr;
+  const float* sine = nullptr;
+  const int32_t* valid_lengths = nullptr;
+  const int32_t* block_table = nullptr;
+  const int32_t* active_count = nullptr;
+  half_t* q_out = nullptr;
+  half_t* k_pool = nullptr;
+  half_t* v_pool = nullptr;
+  int q_heads = 0, kv_heads = 0, head_dim = 0, capacity = 0, page_size = 0;
+};
+
+__device__ __forceinline__ void rope_append_pair(const RopeArgs& ra, int column, float sum_even,
+                                                 float sum_odd) {
+  const int valid = ra.valid_lengths[0];
+  if (ra.active_count[0] < 1 || valid <= 0 || valid > ra.capacity) return;
+  const int position = valid - 1;
+  const int d = ra.head_dim, pairs = d / 2;
+  const int q_width = ra.q_heads * d, kv_width = ra.kv_heads * d;
+  const half_t x0 = from_float<half_t>(sum_even), x1 = from_float<half_t>(sum_odd);
+  half_t* dst;
+  half_t y0 = x0, y1 = x1;
+  if (column < q_width + kv_width) {
+    const int pair = (column % d) / 2;
+    const float c = ra.cosine[(size_t)position * pairs + pair];
+    const float s = ra.sine[(size_t)position * pairs + pair];
+    float re, ro;
+    rotate_pair(to_float<half_t>(x0), to_float<half_t>(x1), c, s, re, ro);
+    // the fp32 results are rounded once to fp16, as the unfused kernel does
+    asm volatile("" : "+v"(re), "+v"(ro));
+    y0 = from_float<half_t>(re);
+    y1 = from_float<half_t>(ro);
+  }
+  if (column < q_width) {
+    dst = ra.q_out + column;
+  } else {
+    const int page = ra.block_table[position / ra.page_size];
+    if (page < 0) return;
+    const bool key = column < q_width + kv_width;
+    const int feature = column - q_width - (key ? 0 : kv_width);
+    dst = (key ? ra.k_pool : ra.v_pool) +
+          (((size_t)page * ra.kv_heads + feature / d) * ra.page_size + position % ra.page_size) * d +
+          feature % d;
+  }
+  dst[0] = y0;
+  dst[1] = y1;
+}
+
 // PRO > 0 (batch 1): every block first builds the normalized row in LDS
 // exactly as norm_vec_kernel does (same per-thread chunk order, wave sums,
 // and 4-wave total, so the row is bit-identical), then streams its weight
@@ -106,12 +161,14 @@ __device__ __forceinline__ void normalized_row(const NormArgs& na, h8* x_lds, in
   __syncthreads();
 }
 
-template <int MATS, int NB, int RPW, int U, int KS, typename OutT, int PRO = 0>
+template <int MATS, int NB, int RPW, int U, int KS, typename OutT, int PRO = 0, bool ROPE = false>
 __global__ __launch_bounds__(256) void gemv_dot_kernel(const half_t* __restrict__ x,
                                                       const half_t* __restrict__ w0,
                                                       const half_t* __restrict__ w1,
                                                       OutT* __restrict__ y, int n_out, int k_in,
-                                                      NormArgs na) {
+                                                      NormArgs na, RopeArgs ra) {
+  static_assert(!ROPE || (MATS == 1 && NB == 1 && RPW == 2 && PRO == 0),
+                "the RoPE epilogue takes one projection row pair per wave at batch 1");
   constexpr int kWaves = 4;
   constexpr int kGroups = kWaves / KS;
   __shared__ float partial[kWaves][MATS][RPW][NB];
@@ -184,7 +241,11 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const half_t* __restrict_
         for (int b = 0; b < NB; ++b) acc[m][r][b] = dot8(wv, xv[b], acc[m][r][b]);
       }
   }
-  if constexpr (KS == 1) {
+  if constexpr (ROPE && KS == 1) {
+    const float even = wave_sum(acc[0][0][0]);
+    const float odd = wave_sum(acc[0][1][0]);
+    if (lane == 0 && live) rope_append_pair(ra, row0, even, odd);
+  } else if constexpr (KS == 1) {
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
 #pragma unroll
@@ -205,7 +266,17 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const half_t* __restrict_
           if (lane == 0) partial[wave][m][r][b] = total;
         }
     __syncthreads();
-    if (part == 0 && live) {
+    if constexpr (ROPE) {
+      if (part == 0 && live && lane == 0) {
+        float even = 0.0f, odd = 0.0f;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          even += partial[wave + s][0][0][0];
+          odd += partial[wave + s][0][1][0];
+        }
+        rope_append_pair(ra, row0, even, odd);
+      }
+    } else if (part == 0 && live) {
       for (int idx = lane; idx < RPW * NB; idx += kWave) {
         const int r = idx / NB, b = idx % NB;
         float a[2] = {0.0f, 0.0f};
@@ -470,14 +541,14 @@ struct Shape {
   int y_dtype, batch, n, k;
 };
 
-template <int MATS, int NB, int RPW, int U, int KS, typename OutT, int PRO = 0>
+template <int MATS, int NB, int RPW, int U, int KS, typename OutT, int PRO = 0, bool ROPE = false>
 int launch_dot(const Shape& s, const half_t* x, OutT* y, hipStream_t stream,
-               const NormArgs& na = NormArgs{}) {
+               const NormArgs& na = NormArgs{}, const RopeArgs& ra = RopeArgs{}) {
   const int rows_per_block = (4 / KS) * RPW;
   const dim3 grid((s.n + rows_per_block - 1) / rows_per_block);
   const size_t lds = PRO > 0 ? (size_t)s.k * sizeof(half_t) : 0;
-  hipLaunchKernelGGL((gemv_dot_kernel<MATS, NB, RPW, U, KS, OutT, PRO>), grid, dim3(256), lds,
-                     stream, x, s.w0, s.w1, y, s.n, s.k, na);
+  hipLaunchKernelGGL((gemv_dot_kernel<MATS, NB, RPW, U, KS, OutT, PRO, ROPE>), grid, dim3(256),
+                     lds, stream, x, s.w0, s.w1, y, s.n, s.k, na, ra);
   return check_launch("gemv_dot_kernel");
 }
 
@@ -862,6 +933,61 @@ extern "C" int tmc_add_rmsnorm_gate_up_silu_f16(const void* residual, const void
                                                 const tmc_gemv_config* config, void* stream) {
   return fused_entry(2, residual, update, gamma, w_gate, w_up, sum_out, out, TMC_F16, batch,
                      hidden, intermediate, epsilon, config, stream);
+}
+
+extern "C" int tmc_qkv_rope_append_f16(const void* x, const void* w, const float* cosine,
+                                       const float* sine, const int32_t* valid_lengths,
+                                       const int32_t* block_table, const int32_t* active_count,
+                                       void* q_out, void* key_pool, void* value_pool,
+                                       int64_t hidden, int64_t q_heads, int64_t kv_heads,
+                                       int64_t head_dim, int64_t capacity, int64_t page_size,
+                                       const tmc_gemv_config* config, void* stream) {
+  TMC_REQUIRE(x && w && cosine && sine && valid_lengths && block_table && active_count && q_out &&
+                  key_pool && value_pool,
+              "Fused q.k.v RoPE append: null pointer.");
+  TMC_REQUIRE(hidden > 0 && hidden < (1LL << 31) && hidden % 8 == 0 && aligned16(x) &&
+                  aligned16(w),
+              "Fused q.k.v RoPE append: hidden must be a positive multiple of 8 and x, W "
+              "16-byte aligned.");
+  TMC_REQUIRE(q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 && head_dim > 0 &&
+                  head_dim % 2 == 0 && capacity > 0 && page_size > 0 &&
+                  (q_heads + 2 * kv_heads) * head_dim < (1LL << 31),
+              "Fused q.k.v RoPE append: invalid head geometry, capacity or page size.");
+  tmc_gemv_config c{1, 2, 4, 4};
+  if (config && config->algorithm != 0) c = *config;
+  TMC_REQUIRE(c.algorithm == 1 && c.rows_per_wave == 2 && (c.unroll == 2 || c.unroll == 4) &&
+                  (c.k_split == 1 || c.k_split == 2 || c.k_split == 4),
+              "Fused q.k.v RoPE append: the dot algorithm with rows_per_wave 2, unroll 2|4 and "
+              "k_split 1|2|4.");
+  const int64_t n = (q_heads + 2 * kv_heads) * head_dim;
+  Shape s{static_cast<const half_t*>(x), static_cast<const half_t*>(w), nullptr, nullptr, TMC_F16,
+          1, (int)n, (int)hidden};
+  RopeArgs ra;
+  ra.cosine = cosine;
+  ra.sine = sine;
+  ra.valid_lengths = valid_lengths;
+  ra.block_table = block_table;
+  ra.active_count = active_count;
+  ra.q_out = static_cast<half_t*>(q_out);
+  ra.k_pool = static_cast<half_t*>(key_pool);
+  ra.v_pool = static_cast<half_t*>(value_pool);
+  ra.q_heads = (int)q_heads;
+  ra.kv_heads = (int)kv_heads;
+  ra.head_dim = (int)head_dim;
+  ra.capacity = (int)capacity;
+  ra.page_size = (int)page_size;
+  const hipStream_t st = as_stream(stream);
+  const half_t* xp = s.x;
+  half_t* none = nullptr;
+  const NormArgs na{};
+  switch ((c.unroll == 2 ? 10 : 0) + (c.k_split == 4 ? 2 : c.k_split == 2 ? 1 : 0)) {
+  case 0: return launch_dot<1, 1, 2, 4, 1, half_t, 0, true>(s, xp, none, st, na, ra);
+  case 1: return launch_dot<1, 1, 2, 4, 2, half_t, 0, true>(s, xp, none, st, na, ra);
+  case 2: return launch_dot<1, 1, 2, 4, 4, half_t, 0, true>(s, xp, none, st, na, ra);
+  case 10: return launch_dot<1, 1, 2, 2, 1, half_t, 0, true>(s, xp, none, st, na, ra);
+  case 11: return launch_dot<1, 1, 2, 2, 2, half_t, 0, true>(s, xp, none, st, na, ra);
+  default: return launch_dot<1, 1, 2, 2, 4, half_t, 0, true>(s, xp, none, st, na, ra);
+  }
 }
 
 extern "C" int tmc_gemv_default_config(int64_t batch, int64_t in_features, int64_t out_features,

@@ -159,6 +159,13 @@ struct tmc_runtime {
   hipStream_t stream = nullptr;
   hipDeviceProp_t props{};
   int fail_next = 0;
+  // Pinned staging of tmc_buf_write_raw_async: copies are appended at
+  // `staged`; once `staged_done` (recorded after the last queued copy) has
+  // completed, every staged byte has reached the device and the area is
+  // reused from the start.
+  char* staging = nullptr;
+  size_t staged = 0;
+  hipEvent_t staged_done = nullptr;
 };
 
 struct tmc_buffer {
@@ -615,6 +622,33 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     };
     return true;
   }
+  if (name == "qkv_rope_append") {
+    // Batch-1 q.k.v projection with RoPE and the paged K/V append fused in
+    // its epilogue: inputs x, fused weight, cos, sin, valid_lengths,
+    // block_table, active; outputs q, key pool, value pool.
+    const int64_t h = param_int(p, "hidden"), qh = param_int(p, "q_heads"),
+                  kvh = param_int(p, "kv_heads", param_int(p, "q_heads")),
+                  d = param_int(p, "head_dim"), cap = param_int(p, "capacity"),
+                  ps = param_int(p, "page_size");
+    NEED(h > 0 && qh > 0 && kvh > 0 && d > 0 && cap > 0 && ps > 0 && dt == TMC_F16,
+         "qkv_rope_append needs hidden, q_heads, head_dim, capacity, page_size and dtype=f16.");
+    tmc_gemv_config cfg{};
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    const int64_t mp = (cap + ps - 1) / ps;
+    s.inputs = {TMC_F16, TMC_F16, TMC_F32, TMC_F32, TMC_I32, TMC_I32, TMC_I32};
+    s.outputs = {TMC_F16, TMC_F16, TMC_F16};
+    s.counts = {(size_t)h, (size_t)((qh + 2 * kvh) * d * h), (size_t)(cap * (d / 2)),
+                (size_t)(cap * (d / 2)), 1, (size_t)mp, 1, (size_t)(qh * d), 0, 0};
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_qkv_rope_append_f16(c.ptrs[0], c.ptrs[1], static_cast<const float*>(c.ptrs[2]),
+                                     static_cast<const float*>(c.ptrs[3]),
+                                     static_cast<const int32_t*>(c.ptrs[4]),
+                                     static_cast<const int32_t*>(c.ptrs[5]),
+                                     static_cast<const int32_t*>(c.ptrs[6]), c.ptrs[7], c.ptrs[8],
+                                     c.ptrs[9], h, qh, kvh, d, cap, ps, &cfg, c.stream);
+    };
+    return true;
+  }
   if (name == "decode_attention") {
     const int64_t b = param_int(p, "batch"), qh = param_int(p, "q_heads"),
                   kvh = param_int(p, "kv_heads", param_int(p, "q_heads")),
@@ -818,6 +852,8 @@ extern "C" void tmc_rt_destroy(tmc_runtime* rt) {
     (void)hipStreamSynchronize(rt->stream);
     (void)hipStreamDestroy(rt->stream);
   }
+  if (rt->staged_done) (void)hipEventDestroy(rt->staged_done);
+  if (rt->staging) (void)hipHostFree(rt->staging);
   delete rt;
 }
 
@@ -922,6 +958,51 @@ extern "C" int tmc_buf_write_raw(tmc_buffer* buf, const void* data, size_t count
              "raw write"))
     return 1;
   return hip_ok(hipStreamSynchronize(buf->rt->stream), "raw write");
+}
+
+namespace {
+constexpr size_t kStagingBytes = size_t(4) << 20;
+}  // namespace
+
+extern "C" int tmc_buf_write_raw_async(tmc_buffer* buf, const void* data, size_t count,
+                                       size_t offset) {
+  clear_error();
+  if (!buf || !data || count == 0 || offset > buf->count || count > buf->count - offset)
+    return fail("tmc_buf_write_raw_async: invalid range.");
+  tmc_runtime* rt = buf->rt;
+  const size_t bytes = count * element_bytes(buf->dtype);
+  const size_t slot = (bytes + 255) / 256 * 256;
+  if (slot > kStagingBytes) return tmc_buf_write_raw(buf, data, count, offset);
+  if (!rt->staging) {
+    void* pinned = nullptr;
+    if (hip_ok(hipHostMalloc(&pinned, kStagingBytes, hipHostMallocDefault), "staging allocation"))
+      return 1;
+    if (hip_ok(hipEventCreateWithFlags(&rt->staged_done, hipEventDisableTiming), "staging event")) {
+      (void)hipHostFree(pinned);
+      return 1;
+    }
+    rt->staging = static_cast<char*>(pinned);
+    rt->staged = 0;
+  }
+  if (rt->staged != 0) {
+    const hipError_t state = hipEventQuery(rt->staged_done);
+    if (state == hipSuccess) {
+      rt->staged = 0;
+    } else if (state != hipErrorNotReady) {
+      return hip_ok(state, "staging event");
+    } else if (rt->staged + slot > kStagingBytes) {
+      if (hip_ok(hipEventSynchronize(rt->staged_done), "staging wait")) return 1;
+      rt->staged = 0;
+    }
+  }
+  char* stage = rt->staging + rt->staged;
+  std::memcpy(stage, data, bytes);
+  if (hip_ok(hipMemcpyAsync(static_cast<char*>(buf->ptr) + offset * element_bytes(buf->dtype),
+                            stage, bytes, hipMemcpyHostToDevice, rt->stream),
+             "staged write"))
+    return 1;
+  rt->staged += slot;
+  return hip_ok(hipEventRecord(rt->staged_done, rt->stream), "staging event");
 }
 
 extern "C" int tmc_buf_read_raw(const tmc_buffer* buf, void* data, size_t count, size_t offset) {

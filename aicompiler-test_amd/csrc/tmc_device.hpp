@@ -119,4 +119,13 @@ __device__ __forceinline__ h8 buffer_load_h8(__amdgpu_buffer_rsrc_t r, unsigned 
   return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_offset, 0, 0));
 }
 
+// Interleaved pair rotation shared by every RoPE kernel and the fused q.k.v
+// projection epilogue, written with explicit fused multiply-adds so that all
+// of them produce the same bits for the same pair.
+__device__ __forceinline__ void rotate_pair(float even, float odd, float c, float s,
+                                            float& out_even, float& out_odd) {
+  out_even = __fmaf_rn(even, c, -(odd * s));
+  out_odd = __fmaf_rn(even, s, odd * c);
+}
+
 }  // namespace tmc

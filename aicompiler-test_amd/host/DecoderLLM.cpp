@@ -440,6 +440,13 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
                                 "&kv_heads=" + std::to_string(KVH) + "&head_dim=" + std::to_string(D) +
                                 "&capacity=" + std::to_string(capacity) +
                                 "&page_size=" + std::to_string(pageSize_);
+    const bool fuseRope = !packed && H % 8 == 0 && D % 2 == 0;
+    const std::string qkvRopeKey = "qkv_rope_append?hidden=" + std::to_string(H) +
+                                   "&q_heads=" + std::to_string(QH) +
+                                   "&kv_heads=" + std::to_string(KVH) +
+                                   "&head_dim=" + std::to_string(D) +
+                                   "&capacity=" + std::to_string(capacity) +
+                                   "&page_size=" + std::to_string(pageSize_);
     const std::string attentionKey =
         "paged_attention?max_batch=" + B + "&q_heads=" + std::to_string(QH) +
         "&kv_heads=" + std::to_string(KVH) + "&head_dim=" + std::to_string(D) +
@@ -451,10 +458,18 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
         add("add_rmsnorm?" + norm, p + "residual_input_norm", {after_, mlp_, w.inputNormWeight},
             {residual_, normalized_});
       const auto& pw = weights(l);
-      add(gemv(H, QKV, "f16"), p + "qkv", {normalized_, pw.queryKeyValueWeight}, {qkv_});
-      add(ropeKey, p + "rope_append",
-          {qkv_, model_->ropeCosine, model_->ropeSine, lengthsView_, tableViews_[l], activeView_},
-          {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer()});
+      if (fuseRope) {
+        // Batch 1: RoPE and the K/V append run in the projection's epilogue.
+        add(qkvRopeKey, p + "qkv_rope_append",
+            {normalized_, pw.queryKeyValueWeight, model_->ropeCosine, model_->ropeSine,
+             lengthsView_, tableViews_[l], activeView_},
+            {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer()});
+      } else {
+        add(gemv(H, QKV, "f16"), p + "qkv", {normalized_, pw.queryKeyValueWeight}, {qkv_});
+        add(ropeKey, p + "rope_append",
+            {qkv_, model_->ropeCosine, model_->ropeSine, lengthsView_, tableViews_[l], activeView_},
+            {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer()});
+      }
       add(attentionKey, p + "attention",
           {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer(), lengthsView_, tableViews_[l],
            activeView_},
@@ -530,8 +545,10 @@ std::string BatchedDecodeExecutor::upload(const std::vector<std::int32_t>& token
   std::copy(lengths.begin(), lengths.end(), meta.begin() + static_cast<std::ptrdiff_t>(M));
   meta[2 * M] = static_cast<std::int32_t>(rows);
   (void)bucket;
+  // Both uploads are queued on the runtime stream ahead of the step's
+  // graph, with no host wait.
   if (meta != metaShadow_) {
-    auto error = meta_->writeRaw(meta.data(), meta.size());
+    auto error = meta_->writeRawAsync(meta.data(), meta.size());
     if (!error.empty()) return error;
     metaShadow_ = std::move(meta);
   }
@@ -544,7 +561,7 @@ std::string BatchedDecodeExecutor::upload(const std::vector<std::int32_t>& token
   while (first < last && packed[first] == tableShadow_[first]) ++first;
   while (last > first && packed[last - 1] == tableShadow_[last - 1]) --last;
   if (first < last) {
-    auto error = tables_->writeRaw(packed.data() + first, last - first, first);
+    auto error = tables_->writeRawAsync(packed.data() + first, last - first, first);
     if (!error.empty()) return error;
     tableShadow_ = std::move(packed);
   }
@@ -932,7 +949,7 @@ BatchedDecodeRun ChunkedPrefillExecutor::runBatch(const std::vector<PrefillSegme
   meta[3 * S] = static_cast<std::int32_t>(rows);
   std::string error;
   if (meta != metaShadow_) {
-    error = meta_->writeRaw(meta.data(), meta.size());
+    error = meta_->writeRawAsync(meta.data(), meta.size());
     if (!error.empty()) {
       result.errorMessage = error;
       return result;
@@ -949,7 +966,7 @@ BatchedDecodeRun ChunkedPrefillExecutor::runBatch(const std::vector<PrefillSegme
   while (lo < hi && packed[lo] == tableShadow_[lo]) ++lo;
   while (hi > lo && packed[hi - 1] == tableShadow_[hi - 1]) --hi;
   if (lo < hi) {
-    error = tables_->writeRaw(packed.data() + lo, hi - lo, lo);
+    error = tables_->writeRawAsync(packed.data() + lo, hi - lo, lo);
     if (!error.empty()) {
       result.errorMessage = error;
       return result;

@@ -114,6 +114,14 @@ std::string HipBuffer::writeRaw(const void* data, std::size_t count, std::size_t
                                                               : lastError("Buffer write failed.");
 }
 
+std::string HipBuffer::writeRawAsync(const void* data, std::size_t count,
+                                     std::size_t offset) const {
+  if (count == 0) return {};
+  return tmc_buf_write_raw_async(buffer_, data, count, offset) == 0
+             ? std::string()
+             : lastError("Buffer write failed.");
+}
+
 void* HipBuffer::devicePointer() const { return tmc_buf_device_ptr(buffer_); }
 
 std::size_t HipBuffer::storageBytes() const { return elementCount() * elementBytes(elementType()); }

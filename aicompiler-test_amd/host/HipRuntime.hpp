@@ -100,6 +100,10 @@ class HipBuffer {
   [[nodiscard]] std::string readRaw(void* out, std::size_t count, std::size_t offset = 0) const;
   [[nodiscard]] std::string writeRaw(const void* data, std::size_t count,
                                      std::size_t offset = 0) const;
+  // writeRaw queued on the runtime stream through pinned staging, without
+  // waiting: later launches on the stream see the data.
+  [[nodiscard]] std::string writeRawAsync(const void* data, std::size_t count,
+                                          std::size_t offset = 0) const;
   [[nodiscard]] void* devicePointer() const;
   [[nodiscard]] std::size_t storageBytes() const;
   [[nodiscard]] tmc_buffer* handle() const noexcept { return buffer_; }

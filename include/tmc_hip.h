@@ -84,6 +84,13 @@ int tmc_buf_write(tmc_buffer *buf, const float *data, size_t count, size_t offse
 /* Raw storage copies (no conversion); bytes/offsets in elements of the dtype. */
 int tmc_buf_write_raw(tmc_buffer *buf, const void *data, size_t count, size_t offset);
 int tmc_buf_read_raw(const tmc_buffer *buf, void *data, size_t count, size_t offset);
+/* tmc_buf_write_raw without the wait: `data` is copied into the runtime's
+ * pinned staging area and the host-to-device copy is queued on the runtime
+ * stream, ordered before later launches on it; the caller may reuse `data`
+ * on return.  No counterpart in the reference (its writes are synchronous):
+ * it is for per-step metadata uploads that precede a graph launch.  Copies
+ * larger than the staging area (4 MiB) fall back to tmc_buf_write_raw. */
+int tmc_buf_write_raw_async(tmc_buffer *buf, const void *data, size_t count, size_t offset);
 /* MetalBuffer::read (MetalRuntime.hpp:66; .mm:171-186). */
 int tmc_buf_read(const tmc_buffer *buf, float *out);
 size_t tmc_buf_count(const tmc_buffer *buf);
@@ -396,6 +403,24 @@ int tmc_decode_rope_append(const void *qkv, const float *cosine, const float *si
                            void *value_pool, int dtype, int64_t max_batch, int64_t q_heads,
                            int64_t kv_heads, int64_t head_dim, int64_t capacity,
                            int64_t page_size, int64_t max_pages, void *stream);
+
+/* Batch-1 decode fusion of the q.k.v projection (emitDecodeGEMV,
+ * DecodeGEMVMetalEmitter.cpp:68-132, over the fused [q | k | v] weight
+ * [(q_heads + 2*kv_heads)*head_dim, hidden]) with tmc_decode_rope_append for
+ * its one request: the projection row is never stored; each pair of output
+ * features is rounded to fp16, rotated (q, k) and written to q_out, or into
+ * the pools through block_table [max_pages] at position valid_lengths[0]-1,
+ * with the bits tmc_gemv_f16 followed by tmc_decode_rope_append produce.
+ * config: NULL or algorithm 0 for the default, else the dot algorithm with
+ * rows_per_wave 2 (a wave owns one pair).  Same skip rules as
+ * tmc_decode_rope_append (active_count[0] < 1, length outside [1, capacity],
+ * negative page). */
+int tmc_qkv_rope_append_f16(const void *x, const void *w, const float *cosine, const float *sine,
+                            const int32_t *valid_lengths, const int32_t *block_table,
+                            const int32_t *active_count, void *q_out, void *key_pool,
+                            void *value_pool, int64_t hidden, int64_t q_heads, int64_t kv_heads,
+                            int64_t head_dim, int64_t capacity, int64_t page_size,
+                            const tmc_gemv_config *config, void *stream);
 
 /* The chunk-prefill form of tmc_decode_rope_append: every row is a token of
  * one request, so the rows share one block table [max_pages]; row r's token

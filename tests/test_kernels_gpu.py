@@ -315,6 +315,25 @@ def test_decode_attention_edges(tmc, orc, torch, valid, d, qh, kvh):
     assert_f16_path(values(out), ref, what=f"attention valid={valid} d={d} group={qh // kvh}")
 
 
+@pytest.mark.parametrize("b,valid,qh,kvh,cap", [(1, 1, 32, 32, 1024), (1, 33, 32, 32, 1024),
+                                                 (1, 700, 32, 32, 1024), (1, 1024, 32, 32, 1024),
+                                                 (2, 999, 8, 4, 1000), (3, 129, 4, 2, 160)])
+def test_decode_attention_one_wide_split(tmc, orc, torch, b, valid, qh, kvh, cap):
+    """Small batches at capacity <= 1024 (head_dim 128, GQA group <= 2) run
+    one 16-wave block per (request, kv head): no workspace, no combine."""
+    d = 128
+    assert tmc.attention_workspace_bytes(b, qh, kvh, d, cap) == 0
+    k = orc.f16(normal(321, (b, kvh, cap, d)))
+    v = orc.f16(normal(322, (b, kvh, cap, d)))
+    q = orc.f16(normal(323, (b, qh * d)) * 2)
+    out = torch.full((b, qh * d), float("nan"), dtype=torch.float16, device="cuda")
+    vl = torch.tensor([valid], dtype=torch.int32, device="cuda")
+    tmc.decode_attention(dev_f16(q), dev_f16(k), dev_f16(v), vl, out, b, qh, kvh, d, cap, None)
+    torch.cuda.synchronize()
+    ref = orc.decode_attention(q, k, v, F16, qh, kvh, d, cap, valid)
+    assert_f16_path(values(out), ref, what=f"wide attention b={b} valid={valid} group={qh // kvh}")
+
+
 def _c4_inputs(orc, torch, batch=16, qh=32, kvh=8, d=128, p=16, pages=8192, max_pages=256):
     # contexts U[64, 4095] so that the appended token keeps valid <= 4096
     lengths = np.random.default_rng(403).integers(64, 4096, size=batch).astype(np.int32)
@@ -358,11 +377,13 @@ def test_c4_paged_gqa_attention(tmc, orc, torch):
     assert_f16_path(values(out), ref, what="paged GQA attention (C4)")
 
 
-@pytest.mark.parametrize("d,p", [(64, 16), (128, 16), (128, 8)])
-def test_paged_attention_inactive_and_bad_pages_untouched(tmc, orc, torch, d, p):
+@pytest.mark.parametrize("d,p,qh,max_pages", [(64, 16, 8, 8), (128, 16, 8, 8), (128, 8, 8, 8),
+                                               (128, 16, 4, 32), (128, 8, 4, 32)])
+def test_paged_attention_inactive_and_bad_pages_untouched(tmc, orc, torch, d, p, qh, max_pages):
     """Rows past the active count, rows whose range needs a missing page (a
-    negative entry, or a page id past the pool) keep their output."""
-    batch, qh, kvh, max_pages = 5, 8, 2, 8
+    negative entry, or a page id past the pool) keep their output.  GQA group
+    2 at max_pages 32 runs the one-split 16-wave blocks."""
+    batch, kvh = 5, 2
     pages = 32
     k_pool = orc.f16(normal(410, (pages, kvh, p, d)))
     v_pool = orc.f16(normal(411, (pages, kvh, p, d)))
@@ -477,6 +498,58 @@ def test_decode_rope_append_is_rope_then_append(tmc, orc, torch, qh, kvh, d):
     changed = np.flatnonzero((bits(kp) != pool0).reshape(pages, -1).any(axis=1))
     expect = {int(tables[b, (lengths[b] - 1) // p]) for b in range(active)} - {-1}
     assert set(changed.tolist()) <= expect
+
+
+QKV_ROPE_CONFIGS = [(1, 2, u, ks) for u in (2, 4) for ks in (1, 2, 4)]
+
+
+@pytest.mark.parametrize("qh,kvh,d,hidden", [(32, 32, 128, 4096), (32, 8, 128, 1024),
+                                             (4, 2, 64, 264), (2, 1, 12, 24)])
+def test_qkv_rope_append_equals_gemv_then_rope_append(tmc, orc, torch, qh, kvh, d, hidden):
+    """The batch-1 q.k.v projection with RoPE and the paged append in its
+    epilogue writes the bits of tmc_gemv_f16_config (same k split) followed by
+    tmc_decode_rope_append, for every dot configuration with two rows per
+    wave; the skip rules (inactive request, length outside [1, capacity],
+    missing page) leave q and both pools untouched."""
+    cap, p = 64, 16
+    max_pages = cap // p
+    pos = np.arange(cap)[:, None]
+    freq = np.exp(np.arange(0, d, 2) * (-np.log(10000.0) / d))
+    cos, sin = np.cos(pos * freq).astype(np.float32), np.sin(pos * freq).astype(np.float32)
+    width = (qh + 2 * kvh) * d
+    x = dev_f16(orc.f16(normal(531, (1, hidden))))
+    w = dev_f16(orc.f16(normal(532, (width, hidden)) * 0.05))
+    pages = 12
+    pool0 = orc.f16(normal(533, (pages, kvh, p, d)))
+    table = np.array([7, 2, -1, 5], np.int32)
+    cos_d, sin_d, table_d = dev(cos), dev(sin), dev(table)
+    one = torch.tensor([1], dtype=torch.int32, device="cuda")
+    cases = [(20, 1), (1, 1), (64, 1), (40, 1), (20, 0), (0, 1), (65, 1)]  # (valid, active)
+    for cfg in QKV_ROPE_CONFIGS:
+        for valid, active in cases:
+            lengths = torch.tensor([valid], dtype=torch.int32, device="cuda")
+            act = torch.tensor([active], dtype=torch.int32, device="cuda")
+            kp, vp = dev_f16(pool0), dev_f16(pool0.copy())
+            q = torch.full((1, qh * d), float("nan"), dtype=torch.float16, device="cuda")
+            tmc.qkv_rope_append(x, w, cos_d, sin_d, lengths, table_d, act, q, kp, vp, qh, kvh, d,
+                                cap, p, config=cfg)
+            qkv = torch.empty((1, width), dtype=torch.float16, device="cuda")
+            tmc.gemv_config(x, w, qkv, tmc.GemvConfig(1, 1, cfg[2], cfg[3]))
+            kp2, vp2 = dev_f16(pool0), dev_f16(pool0.copy())
+            q2 = torch.full_like(q, float("nan"))
+            tmc.decode_rope_append(qkv, cos_d, sin_d, lengths, table_d, act, q2, kp2, vp2, 1, qh,
+                                   kvh, d, cap, p, max_pages)
+            torch.cuda.synchronize()
+            what = f"config {cfg} valid {valid} active {active}"
+            assert np.array_equal(bits(q), bits(q2)), what
+            assert np.array_equal(bits(kp), bits(kp2)), what
+            assert np.array_equal(bits(vp), bits(vp2)), what
+            wrote = active == 1 and 1 <= valid <= cap and table[(valid - 1) // p] >= 0
+            assert (not np.array_equal(bits(kp), pool0)) == wrote, what
+            assert np.isnan(values(q)).all() == (active != 1 or not 1 <= valid <= cap), what
+    with pytest.raises(tmc.TmcError, match="rows_per_wave 2"):
+        tmc.qkv_rope_append(x, w, cos_d, sin_d, one, table_d, one, q, kp, vp, qh, kvh, d, cap, p,
+                            config=(1, 1, 4, 4))
 
 
 def test_embedding_and_argmax(tmc, orc, torch):
@@ -797,3 +870,26 @@ def test_packed_gemm_activation_layouts_bit_exact(tmc, orc, torch, layout):
     if layout & 2:
         with pytest.raises(tmc.TmcError):  # a packed output must be fp16
             tmc.gemm_packed_ex(xin, pw, f, batch, k, n, layout, y_dtype=1)
+
+
+def test_async_raw_writes_reach_the_device_in_order(tmc, torch):
+    """tmc_buf_write_raw_async: overlapping writes land in queue order, the
+    caller's memory is free on return, the staging area wraps (far more than
+    its 4 MiB pass through) and a copy larger than it falls back to the
+    synchronous path."""
+    rt = tmc.Runtime()
+    n = 3 << 19  # 6 MiB of int32
+    buf = rt.create_buffer(n, tmc.I32)
+    rng = np.random.default_rng(77)
+    expect = np.zeros(n, np.int32)
+    buf.write_raw_async(expect)  # larger than the staging area
+    for _ in range(300):
+        count = int(rng.integers(1, 60000))
+        offset = int(rng.integers(0, n - count))
+        data = rng.integers(-2**31, 2**31 - 1, count, dtype=np.int32)
+        expect[offset:offset + count] = data
+        buf.write_raw_async(data, offset)
+        data[:] = 0
+    assert np.array_equal(buf.read_raw(), expect)
+    with pytest.raises(tmc.TmcError):
+        buf.write_raw_async(np.zeros(4, np.int32), n - 3)
