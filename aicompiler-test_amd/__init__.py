@@ -41,6 +41,9 @@ def _declare(l):
         "tmc_gemv_f16_config": (i32, [vp, vp, vp, i32, i64, i64, i64, vp, vp]),
         "tmc_qkv_rope_append_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64,
                                           i64, i64, i64, vp, vp]),
+        "tmc_add_rmsnorm_qkv_rope_append_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
+                                                      vp, vp, i64, i64, i64, i64, i64, i64,
+                                                      C.c_float, vp, vp]),
         "tmc_gate_up_silu_f16_config": (i32, [vp, vp, vp, vp, i64, i64, i64, vp, vp]),
         "tmc_gemv_default_config": (i32, [i64, i64, i64, i32, vp]),
         "tmc_gate_up_silu_f16": (i32, [vp, vp, vp, vp, i64, i64, i64, vp]),
@@ -445,6 +448,23 @@ def qkv_rope_append(x, w, cos, sin, valid_lengths, table, active, q_out, k_pool,
                                         capacity, page_size, None if cfg is None else C.byref(cfg),
                                         _stream(stream)),
           "tmc_qkv_rope_append_f16")
+
+
+def add_rmsnorm_qkv_rope_append(residual, update, gamma, w, sum_out, cos, sin, valid_lengths,
+                                table, active, q_out, k_pool, v_pool, q_heads, kv_heads, head_dim,
+                                capacity, page_size, eps, config=None, stream=None):
+    """qkv_rope_append of RMSNorm(residual + update) * gamma (update None:
+    RMSNorm(residual) * gamma), the norm built inside the kernel."""
+    cfg = None
+    if config is not None:
+        cfg = GemvConfig(*config) if isinstance(config, tuple) else config
+    check(lib().tmc_add_rmsnorm_qkv_rope_append_f16(
+        _ptr(residual), _ptr(update) if update is not None else None, _ptr(gamma), _ptr(w),
+        _ptr(sum_out) if sum_out is not None else None, _ptr(cos), _ptr(sin), _ptr(valid_lengths),
+        _ptr(table), _ptr(active), _ptr(q_out), _ptr(k_pool), _ptr(v_pool), residual.shape[-1],
+        q_heads, kv_heads, head_dim, capacity, page_size, eps,
+        None if cfg is None else C.byref(cfg), _stream(stream)),
+        "tmc_add_rmsnorm_qkv_rope_append_f16")
 
 
 def prefill_rope_append(qkv, cos, sin, valid_lengths, table, active, q_out, k_pool, v_pool, rows,

@@ -167,7 +167,7 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const half_t* __restrict_
                                                       const half_t* __restrict__ w1,
                                                       OutT* __restrict__ y, int n_out, int k_in,
                                                       NormArgs na, RopeArgs ra) {
-  static_assert(!ROPE || (MATS == 1 && NB == 1 && RPW == 2 && PRO == 0),
+  static_assert(!ROPE || (MATS == 1 && NB == 1 && RPW == 2),
                 "the RoPE epilogue takes one projection row pair per wave at batch 1");
   constexpr int kWaves = 4;
   constexpr int kGroups = kWaves / KS;
@@ -186,107 +186,114 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const half_t* __restrict_
   };
   const int group = wave / KS;
   const int part = wave % KS;
-  const int row0 = (blockIdx.x * kGroups + group) * RPW;
-  const bool live = row0 < n_out;  // wave-uniform; dead waves still meet the barrier
-  const int chunks = k_in >> 3;
-  const half_t* wrow[MATS][RPW];
+  // PRO > 0: the grid is capped (launch_dot), so a block loops over row
+  // groups and builds the normalized row once; otherwise one pass.
+  for (int grp = blockIdx.x; grp * kGroups * RPW < n_out;
+       grp += PRO > 0 ? (int)gridDim.x : n_out) {
+    const int row0 = (grp * kGroups + group) * RPW;
+    const bool live = row0 < n_out;  // wave-uniform; dead waves still meet the barrier
+    const int chunks = k_in >> 3;
+    const half_t* wrow[MATS][RPW];
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    const size_t off = (size_t)min(row0 + r, n_out - 1) * k_in;
-    wrow[0][r] = w0 + off;
-    if constexpr (MATS == 2) wrow[1][r] = w1 + off;
-  }
-  float acc[MATS][RPW][NB];
-#pragma unroll
-  for (int m = 0; m < MATS; ++m)
-#pragma unroll
-    for (int r = 0; r < RPW; ++r)
-#pragma unroll
-      for (int b = 0; b < NB; ++b) acc[m][r][b] = 0.0f;
-
-  constexpr int stride = kWave * KS;
-  int c = live ? lane + kWave * part : chunks;
-  for (; c + stride * (U - 1) < chunks; c += stride * U) {
-    h8 wv[U][MATS][RPW];
-    h8 xv[U][NB];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int m = 0; m < MATS; ++m)
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) wv[u][m][r] = load_h8_stream(wrow[m][r] + 8 * (c + stride * u));
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int b = 0; b < NB; ++b) xv[u][b] = x_chunk(b, c + stride * u);
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int m = 0; m < MATS; ++m)
-#pragma unroll
-        for (int r = 0; r < RPW; ++r)
-#pragma unroll
-          for (int b = 0; b < NB; ++b) acc[m][r][b] = dot8(wv[u][m][r], xv[u][b], acc[m][r][b]);
-  }
-  for (; c < chunks; c += stride) {
-    h8 xv[NB];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) xv[b] = x_chunk(b, c);
-#pragma unroll
-    for (int m = 0; m < MATS; ++m)
-#pragma unroll
-      for (int r = 0; r < RPW; ++r) {
-        const h8 wv = load_h8_stream(wrow[m][r] + 8 * c);
-#pragma unroll
-        for (int b = 0; b < NB; ++b) acc[m][r][b] = dot8(wv, xv[b], acc[m][r][b]);
-      }
-  }
-  if constexpr (ROPE && KS == 1) {
-    const float even = wave_sum(acc[0][0][0]);
-    const float odd = wave_sum(acc[0][1][0]);
-    if (lane == 0 && live) rope_append_pair(ra, row0, even, odd);
-  } else if constexpr (KS == 1) {
-#pragma unroll
-    for (int r = 0; r < RPW; ++r)
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const float a0 = wave_sum(acc[0][r][b]);
-        const float a1 = MATS == 2 ? wave_sum(acc[MATS - 1][r][b]) : 0.0f;
-        if (lane == 0 && live && row0 + r < n_out)
-          write_out<MATS>(y, (size_t)b * n_out + row0 + r, a0, a1);
-      }
-  } else {
+    for (int r = 0; r < RPW; ++r) {
+      const size_t off = (size_t)min(row0 + r, n_out - 1) * k_in;
+      wrow[0][r] = w0 + off;
+      if constexpr (MATS == 2) wrow[1][r] = w1 + off;
+    }
+    float acc[MATS][RPW][NB];
 #pragma unroll
     for (int m = 0; m < MATS; ++m)
 #pragma unroll
       for (int r = 0; r < RPW; ++r)
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          const float total = wave_sum(acc[m][r][b]);
-          if (lane == 0) partial[wave][m][r][b] = total;
-        }
-    __syncthreads();
-    if constexpr (ROPE) {
-      if (part == 0 && live && lane == 0) {
-        float even = 0.0f, odd = 0.0f;
+        for (int b = 0; b < NB; ++b) acc[m][r][b] = 0.0f;
+
+    constexpr int stride = kWave * KS;
+    int c = live ? lane + kWave * part : chunks;
+    for (; c + stride * (U - 1) < chunks; c += stride * U) {
+      h8 wv[U][MATS][RPW];
+      h8 xv[U][NB];
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          even += partial[wave + s][0][0][0];
-          odd += partial[wave + s][0][1][0];
-        }
-        rope_append_pair(ra, row0, even, odd);
-      }
-    } else if (part == 0 && live) {
-      for (int idx = lane; idx < RPW * NB; idx += kWave) {
-        const int r = idx / NB, b = idx % NB;
-        float a[2] = {0.0f, 0.0f};
+      for (int u = 0; u < U; ++u)
 #pragma unroll
         for (int m = 0; m < MATS; ++m)
 #pragma unroll
-          for (int s = 0; s < KS; ++s) a[m] += partial[wave + s][m][r][b];
-        if (row0 + r < n_out) write_out<MATS>(y, (size_t)b * n_out + row0 + r, a[0], a[1]);
+          for (int r = 0; r < RPW; ++r) wv[u][m][r] = load_h8_stream(wrow[m][r] + 8 * (c + stride * u));
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) xv[u][b] = x_chunk(b, c + stride * u);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int m = 0; m < MATS; ++m)
+#pragma unroll
+          for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) acc[m][r][b] = dot8(wv[u][m][r], xv[u][b], acc[m][r][b]);
+    }
+    for (; c < chunks; c += stride) {
+      h8 xv[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) xv[b] = x_chunk(b, c);
+#pragma unroll
+      for (int m = 0; m < MATS; ++m)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+          const h8 wv = load_h8_stream(wrow[m][r] + 8 * c);
+#pragma unroll
+          for (int b = 0; b < NB; ++b) acc[m][r][b] = dot8(wv, xv[b], acc[m][r][b]);
+        }
+    }
+    if constexpr (ROPE && KS == 1) {
+      const float even = wave_sum(acc[0][0][0]);
+      const float odd = wave_sum(acc[0][1][0]);
+      if (lane == 0 && live) rope_append_pair(ra, row0, even, odd);
+    } else if constexpr (KS == 1) {
+#pragma unroll
+      for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const float a0 = wave_sum(acc[0][r][b]);
+          const float a1 = MATS == 2 ? wave_sum(acc[MATS - 1][r][b]) : 0.0f;
+          if (lane == 0 && live && row0 + r < n_out)
+            write_out<MATS>(y, (size_t)b * n_out + row0 + r, a0, a1);
+        }
+    } else {
+#pragma unroll
+      for (int m = 0; m < MATS; ++m)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            const float total = wave_sum(acc[m][r][b]);
+            if (lane == 0) partial[wave][m][r][b] = total;
+          }
+      __syncthreads();
+      if constexpr (ROPE) {
+        if (part == 0 && live && lane == 0) {
+          float even = 0.0f, odd = 0.0f;
+#pragma unroll
+          for (int s = 0; s < KS; ++s) {
+            even += partial[wave + s][0][0][0];
+            odd += partial[wave + s][0][1][0];
+          }
+          rope_append_pair(ra, row0, even, odd);
+        }
+      } else if (part == 0 && live) {
+        for (int idx = lane; idx < RPW * NB; idx += kWave) {
+          const int r = idx / NB, b = idx % NB;
+          float a[2] = {0.0f, 0.0f};
+#pragma unroll
+          for (int m = 0; m < MATS; ++m)
+#pragma unroll
+            for (int s = 0; s < KS; ++s) a[m] += partial[wave + s][m][r][b];
+          if (row0 + r < n_out) write_out<MATS>(y, (size_t)b * n_out + row0 + r, a[0], a[1]);
+        }
       }
     }
+    // the next group's partials reuse the LDS slots read above
+    if constexpr (KS > 1 && PRO > 0) __syncthreads();
   }
 }
 
@@ -533,6 +540,8 @@ __global__ __launch_bounds__(1024) void mfma_rows_kernel(const half_t* __restric
 }
 
 // ---------------------------------------------------------------- dispatch
+constexpr int kFusedMaxBlocks = 2048;
+
 struct Shape {
   const half_t* x;
   const half_t* w0;
@@ -545,7 +554,11 @@ template <int MATS, int NB, int RPW, int U, int KS, typename OutT, int PRO = 0, 
 int launch_dot(const Shape& s, const half_t* x, OutT* y, hipStream_t stream,
                const NormArgs& na = NormArgs{}, const RopeArgs& ra = RopeArgs{}) {
   const int rows_per_block = (4 / KS) * RPW;
-  const dim3 grid((s.n + rows_per_block - 1) / rows_per_block);
+  int blocks = (s.n + rows_per_block - 1) / rows_per_block;
+  // With the norm prologue every block re-reads the row (3 x k halves): at
+  // most kFusedMaxBlocks blocks (8 per CU) keep that L2 traffic small.
+  if (PRO > 0 && blocks > kFusedMaxBlocks) blocks = kFusedMaxBlocks;
+  const dim3 grid(blocks);
   const size_t lds = PRO > 0 ? (size_t)s.k * sizeof(half_t) : 0;
   hipLaunchKernelGGL((gemv_dot_kernel<MATS, NB, RPW, U, KS, OutT, PRO, ROPE>), grid, dim3(256),
                      lds, stream, x, s.w0, s.w1, y, s.n, s.k, na, ra);
@@ -935,25 +948,44 @@ extern "C" int tmc_add_rmsnorm_gate_up_silu_f16(const void* residual, const void
                      hidden, intermediate, epsilon, config, stream);
 }
 
-extern "C" int tmc_qkv_rope_append_f16(const void* x, const void* w, const float* cosine,
-                                       const float* sine, const int32_t* valid_lengths,
-                                       const int32_t* block_table, const int32_t* active_count,
-                                       void* q_out, void* key_pool, void* value_pool,
-                                       int64_t hidden, int64_t q_heads, int64_t kv_heads,
-                                       int64_t head_dim, int64_t capacity, int64_t page_size,
-                                       const tmc_gemv_config* config, void* stream) {
-  TMC_REQUIRE(x && w && cosine && sine && valid_lengths && block_table && active_count && q_out &&
-                  key_pool && value_pool,
+namespace {
+
+template <int PRO>
+int launch_qkv_rope(const Shape& s, const tmc_gemv_config& c, const NormArgs& na,
+                    const RopeArgs& ra, hipStream_t st) {
+  half_t* none = nullptr;
+  switch ((c.unroll == 2 ? 10 : 0) + (c.k_split == 4 ? 2 : c.k_split == 2 ? 1 : 0)) {
+  case 0: return launch_dot<1, 1, 2, 4, 1, half_t, PRO, true>(s, s.x, none, st, na, ra);
+  case 1: return launch_dot<1, 1, 2, 4, 2, half_t, PRO, true>(s, s.x, none, st, na, ra);
+  case 2: return launch_dot<1, 1, 2, 4, 4, half_t, PRO, true>(s, s.x, none, st, na, ra);
+  case 10: return launch_dot<1, 1, 2, 2, 1, half_t, PRO, true>(s, s.x, none, st, na, ra);
+  case 11: return launch_dot<1, 1, 2, 2, 2, half_t, PRO, true>(s, s.x, none, st, na, ra);
+  default: return launch_dot<1, 1, 2, 2, 4, half_t, PRO, true>(s, s.x, none, st, na, ra);
+  }
+}
+
+// q.k.v projection + RoPE + paged append at batch 1; norm: PRO 0 (x is the
+// projection input), 1 (x = RMSNorm(residual + update)) or 2 (RMSNorm(residual)).
+int qkv_rope_entry(int pro, const void* x, const NormArgs& na, const void* w,
+                   const float* cosine, const float* sine, const int32_t* valid_lengths,
+                   const int32_t* block_table, const int32_t* active_count, void* q_out,
+                   void* key_pool, void* value_pool, int64_t hidden, int64_t q_heads,
+                   int64_t kv_heads, int64_t head_dim, int64_t capacity, int64_t page_size,
+                   const tmc_gemv_config* config, void* stream) {
+  TMC_REQUIRE((pro > 0 || x) && w && cosine && sine && valid_lengths && block_table &&
+                  active_count && q_out && key_pool && value_pool,
               "Fused q.k.v RoPE append: null pointer.");
-  TMC_REQUIRE(hidden > 0 && hidden < (1LL << 31) && hidden % 8 == 0 && aligned16(x) &&
-                  aligned16(w),
-              "Fused q.k.v RoPE append: hidden must be a positive multiple of 8 and x, W "
-              "16-byte aligned.");
+  TMC_REQUIRE(hidden > 0 && hidden % 8 == 0 && (pro > 0 ? hidden <= 32768 : hidden < (1LL << 31)) &&
+                  (pro > 0 || aligned16(x)) && aligned16(w),
+              "Fused q.k.v RoPE append: hidden must be a positive multiple of 8 (at most 32768 "
+              "with the norm) and x, W 16-byte aligned.");
   TMC_REQUIRE(q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 && head_dim > 0 &&
                   head_dim % 2 == 0 && capacity > 0 && page_size > 0 &&
                   (q_heads + 2 * kv_heads) * head_dim < (1LL << 31),
               "Fused q.k.v RoPE append: invalid head geometry, capacity or page size.");
-  tmc_gemv_config c{1, 2, 4, 4};
+  // measured defaults (C5 q.k.v shape): unroll 4 / k split 4 without the
+  // norm, unroll 2 / k split 2 with it
+  tmc_gemv_config c = pro > 0 ? tmc_gemv_config{1, 2, 2, 2} : tmc_gemv_config{1, 2, 4, 4};
   if (config && config->algorithm != 0) c = *config;
   TMC_REQUIRE(c.algorithm == 1 && c.rows_per_wave == 2 && (c.unroll == 2 || c.unroll == 4) &&
                   (c.k_split == 1 || c.k_split == 2 || c.k_split == 4),
@@ -977,17 +1009,48 @@ extern "C" int tmc_qkv_rope_append_f16(const void* x, const void* w, const float
   ra.capacity = (int)capacity;
   ra.page_size = (int)page_size;
   const hipStream_t st = as_stream(stream);
-  const half_t* xp = s.x;
-  half_t* none = nullptr;
-  const NormArgs na{};
-  switch ((c.unroll == 2 ? 10 : 0) + (c.k_split == 4 ? 2 : c.k_split == 2 ? 1 : 0)) {
-  case 0: return launch_dot<1, 1, 2, 4, 1, half_t, 0, true>(s, xp, none, st, na, ra);
-  case 1: return launch_dot<1, 1, 2, 4, 2, half_t, 0, true>(s, xp, none, st, na, ra);
-  case 2: return launch_dot<1, 1, 2, 4, 4, half_t, 0, true>(s, xp, none, st, na, ra);
-  case 10: return launch_dot<1, 1, 2, 2, 1, half_t, 0, true>(s, xp, none, st, na, ra);
-  case 11: return launch_dot<1, 1, 2, 2, 2, half_t, 0, true>(s, xp, none, st, na, ra);
-  default: return launch_dot<1, 1, 2, 2, 4, half_t, 0, true>(s, xp, none, st, na, ra);
-  }
+  if (pro == 1) return launch_qkv_rope<1>(s, c, na, ra, st);
+  if (pro == 2) return launch_qkv_rope<2>(s, c, na, ra, st);
+  return launch_qkv_rope<0>(s, c, na, ra, st);
+}
+
+}  // namespace
+
+extern "C" int tmc_qkv_rope_append_f16(const void* x, const void* w, const float* cosine,
+                                       const float* sine, const int32_t* valid_lengths,
+                                       const int32_t* block_table, const int32_t* active_count,
+                                       void* q_out, void* key_pool, void* value_pool,
+                                       int64_t hidden, int64_t q_heads, int64_t kv_heads,
+                                       int64_t head_dim, int64_t capacity, int64_t page_size,
+                                       const tmc_gemv_config* config, void* stream) {
+  return qkv_rope_entry(0, x, NormArgs{}, w, cosine, sine, valid_lengths, block_table,
+                        active_count, q_out, key_pool, value_pool, hidden, q_heads, kv_heads,
+                        head_dim, capacity, page_size, config, stream);
+}
+
+extern "C" int tmc_add_rmsnorm_qkv_rope_append_f16(
+    const void* residual, const void* update, const void* gamma, const void* w, void* sum_out,
+    const float* cosine, const float* sine, const int32_t* valid_lengths,
+    const int32_t* block_table, const int32_t* active_count, void* q_out, void* key_pool,
+    void* value_pool, int64_t hidden, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+    int64_t capacity, int64_t page_size, float epsilon, const tmc_gemv_config* config,
+    void* stream) {
+  TMC_REQUIRE(residual && gamma && (!update || sum_out),
+              "Fused norm + q.k.v RoPE append: null pointer.");
+  TMC_REQUIRE(aligned16(residual) && aligned16(gamma) &&
+                  (!update || (aligned16(update) && aligned16(sum_out))),
+              "Fused norm + q.k.v RoPE append: operands must be 16-byte aligned.");
+  TMC_REQUIRE(std::isfinite(epsilon) && epsilon > 0.0f,
+              "Fused norm + q.k.v RoPE append: epsilon must be positive.");
+  NormArgs na;
+  na.residual = static_cast<const half_t*>(residual);
+  na.update = static_cast<const half_t*>(update);
+  na.gamma = static_cast<const half_t*>(gamma);
+  na.sum_out = static_cast<half_t*>(sum_out);
+  na.eps = epsilon;
+  return qkv_rope_entry(update ? 1 : 2, nullptr, na, w, cosine, sine, valid_lengths, block_table,
+                        active_count, q_out, key_pool, value_pool, hidden, q_heads, kv_heads,
+                        head_dim, capacity, page_size, config, stream);
 }
 
 extern "C" int tmc_gemv_default_config(int64_t batch, int64_t in_features, int64_t out_features,

@@ -622,6 +622,44 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     };
     return true;
   }
+  if (name == "add_rmsnorm_qkv_rope_append" || name == "rmsnorm_qkv_rope_append") {
+    // Batch-1 norm + q.k.v projection + RoPE + paged append: inputs
+    // residual[, update], gamma, fused weight, cos, sin, valid_lengths,
+    // block_table, active; outputs [sum,] q, key pool, value pool.
+    const bool add = name.rfind("add_", 0) == 0;
+    const int64_t h = param_int(p, "hidden"), qh = param_int(p, "q_heads"),
+                  kvh = param_int(p, "kv_heads", param_int(p, "q_heads")),
+                  d = param_int(p, "head_dim"), cap = param_int(p, "capacity"),
+                  ps = param_int(p, "page_size");
+    const float eps = (float)param_double(p, "eps", 1e-5);
+    NEED(h > 0 && qh > 0 && kvh > 0 && d > 0 && cap > 0 && ps > 0 && dt == TMC_F16,
+         "rmsnorm_qkv_rope_append needs hidden, q_heads, head_dim, capacity, page_size and "
+         "dtype=f16.");
+    tmc_gemv_config cfg{};
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    const int64_t mp = (cap + ps - 1) / ps;
+    s.inputs = add ? std::vector<int>{TMC_F16, TMC_F16} : std::vector<int>{TMC_F16};
+    s.inputs.insert(s.inputs.end(), {TMC_F16, TMC_F16, TMC_F32, TMC_F32, TMC_I32, TMC_I32, TMC_I32});
+    s.outputs = add ? std::vector<int>{TMC_F16, TMC_F16, TMC_F16, TMC_F16}
+                    : std::vector<int>{TMC_F16, TMC_F16, TMC_F16};
+    s.counts = add ? std::vector<size_t>{(size_t)h, (size_t)h} : std::vector<size_t>{(size_t)h};
+    s.counts.insert(s.counts.end(), {(size_t)h, (size_t)((qh + 2 * kvh) * d * h),
+                                     (size_t)(cap * (d / 2)), (size_t)(cap * (d / 2)), 1,
+                                     (size_t)mp, 1});
+    if (add) s.counts.push_back((size_t)h);
+    s.counts.insert(s.counts.end(), {(size_t)(qh * d), 0, 0});
+    s.launch = [=](const LaunchContext& c) {
+      const int o = add ? 1 : 0;  // index shift past the update input
+      return tmc_add_rmsnorm_qkv_rope_append_f16(
+          c.ptrs[0], add ? c.ptrs[1] : nullptr, c.ptrs[1 + o], c.ptrs[2 + o],
+          add ? c.ptrs[9] : nullptr, static_cast<const float*>(c.ptrs[3 + o]),
+          static_cast<const float*>(c.ptrs[4 + o]), static_cast<const int32_t*>(c.ptrs[5 + o]),
+          static_cast<const int32_t*>(c.ptrs[6 + o]), static_cast<const int32_t*>(c.ptrs[7 + o]),
+          c.ptrs[8 + 2 * o], c.ptrs[9 + 2 * o], c.ptrs[10 + 2 * o], h, qh, kvh, d, cap, ps, eps,
+          &cfg, c.stream);
+    };
+    return true;
+  }
   if (name == "qkv_rope_append") {
     // Batch-1 q.k.v projection with RoPE and the paged K/V append fused in
     // its epilogue: inputs x, fused weight, cos, sin, valid_lengths,

@@ -206,9 +206,11 @@ int tmc_gate_up_silu_f16_config(const void *x, const void *w_gate, const void *w
  * when update is NULL (plain RMSNorm; sum_out unused).  Every block rebuilds
  * the normalized row in LDS with the arithmetic and summation order of
  * tmc_add_rmsnorm / tmc_rmsnorm, so results equal the two-kernel sequence bit
- * for bit.  batch must be 1; in_features a multiple of 8 up to 32768; all
- * operands 16-byte aligned; fp16 operands.  config: NULL / algorithm 0 = the
- * fused default, else a dot configuration (algorithm 1). */
+ * for bit.  At most 2048 blocks run (each loops over its share of the
+ * output rows), so the row is rebuilt at most 2048 times.  batch must be 1;
+ * in_features a multiple of 8 up to 32768; all operands 16-byte aligned;
+ * fp16 operands.  config: NULL / algorithm 0 = the fused default, else a dot
+ * configuration (algorithm 1). */
 int tmc_add_rmsnorm_gemv_f16(const void *residual, const void *update, const void *gamma,
                              const void *w, void *sum_out, void *y, int y_dtype, int64_t batch,
                              int64_t in_features, int64_t out_features, float epsilon,
@@ -421,6 +423,25 @@ int tmc_qkv_rope_append_f16(const void *x, const void *w, const float *cosine, c
                             void *value_pool, int64_t hidden, int64_t q_heads, int64_t kv_heads,
                             int64_t head_dim, int64_t capacity, int64_t page_size,
                             const tmc_gemv_config *config, void *stream);
+
+/* tmc_qkv_rope_append_f16 of x = RMSNorm(residual + update) * gamma (update
+ * NULL: RMSNorm(residual) * gamma), the normalized row built in each block's
+ * LDS as tmc_add_rmsnorm_gemv_f16 builds it (bit-identical to tmc_add_rmsnorm
+ * / tmc_rmsnorm; emitDecoderResidualRMSNorm, DecoderLLMMetalEmitter.cpp:
+ * 417-477); with an update, sum_out receives h(residual + update).  It
+ * removes the norm launch but measured no faster than the norm kernel plus
+ * tmc_qkv_rope_append_f16 on the 7B shape (the row rebuild is a dependent
+ * load-reduce chain at the start of every block), so the batch-1 decoder
+ * keeps the two launches. */
+int tmc_add_rmsnorm_qkv_rope_append_f16(const void *residual, const void *update,
+                                        const void *gamma, const void *w, void *sum_out,
+                                        const float *cosine, const float *sine,
+                                        const int32_t *valid_lengths, const int32_t *block_table,
+                                        const int32_t *active_count, void *q_out, void *key_pool,
+                                        void *value_pool, int64_t hidden, int64_t q_heads,
+                                        int64_t kv_heads, int64_t head_dim, int64_t capacity,
+                                        int64_t page_size, float epsilon,
+                                        const tmc_gemv_config *config, void *stream);
 
 /* The chunk-prefill form of tmc_decode_rope_append: every row is a token of
  * one request, so the rows share one block table [max_pages]; row r's token

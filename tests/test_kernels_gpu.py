@@ -552,6 +552,58 @@ def test_qkv_rope_append_equals_gemv_then_rope_append(tmc, orc, torch, qh, kvh, 
                             config=(1, 1, 4, 4))
 
 
+@pytest.mark.parametrize("cfg_t", QKV_ROPE_CONFIGS + [None])
+def test_norm_qkv_rope_append_equals_norm_then_fused_projection(tmc, orc, torch, cfg_t):
+    """The Add+RMSNorm (or RMSNorm) prologue in the q.k.v RoPE append kernel
+    reproduces tmc_add_rmsnorm (tmc_rmsnorm) followed by
+    tmc_qkv_rope_append_f16 with the same configuration bit for bit, residual
+    sum included; at k split 4 the 4096 row pairs exceed the 2048-block grid,
+    so blocks loop."""
+    qh, kvh, d, hidden, cap, p = 32, 16, 128, 1024, 64, 16
+    cfg = tmc.GemvConfig(*cfg_t) if cfg_t else None
+    ref_cfg = cfg_t or (1, 2, 2, 2)
+    pos = np.arange(cap)[:, None]
+    freq = np.exp(np.arange(0, d, 2) * (-np.log(10000.0) / d))
+    cos = dev(np.cos(pos * freq).astype(np.float32))
+    sin = dev(np.sin(pos * freq).astype(np.float32))
+    width = (qh + 2 * kvh) * d
+    h = dev_f16(orc.f16(normal(541, (1, hidden))))
+    r = dev_f16(orc.f16(normal(542, (1, hidden))))
+    gamma = dev_f16(orc.f16(uniform(543, (hidden,), 0.5, 1.5)))
+    w = dev_f16(orc.f16(normal(544, (width, hidden), 0.05)))
+    pool0 = orc.f16(normal(545, (8, kvh, p, d)))
+    table = dev(np.array([3, 6, 1, 4], np.int32))
+    lengths = torch.tensor([37], dtype=torch.int32, device="cuda")
+    one = torch.tensor([1], dtype=torch.int32, device="cuda")
+    for add in (True, False):
+        s_ref = torch.empty((1, hidden), dtype=torch.float16, device="cuda")
+        n_ref = torch.empty_like(s_ref)
+        if add:
+            tmc.add_rmsnorm(r, h, gamma, s_ref, n_ref, 1e-6)
+        else:
+            tmc.rmsnorm(r, gamma, n_ref, 1e-6)
+        kp_ref, vp_ref = dev_f16(pool0), dev_f16(pool0.copy())
+        q_ref = torch.full((1, qh * d), float("nan"), dtype=torch.float16, device="cuda")
+        tmc.qkv_rope_append(n_ref, w, cos, sin, lengths, table, one, q_ref, kp_ref, vp_ref, qh,
+                            kvh, d, cap, p, config=ref_cfg)
+        kp, vp = dev_f16(pool0), dev_f16(pool0.copy())
+        q = torch.full_like(q_ref, float("nan"))
+        s_out = torch.full((1, hidden), 7.0, dtype=torch.float16, device="cuda")
+        tmc.add_rmsnorm_qkv_rope_append(r, h if add else None, gamma, w, s_out if add else None,
+                                        cos, sin, lengths, table, one, q, kp, vp, qh, kvh, d, cap,
+                                        p, 1e-6, config=cfg)
+        torch.cuda.synchronize()
+        what = f"cfg {cfg_t} add={add}"
+        assert np.array_equal(bits(q), bits(q_ref)), what
+        assert np.array_equal(bits(kp), bits(kp_ref)), what
+        assert np.array_equal(bits(vp), bits(vp_ref)), what
+        assert not np.array_equal(bits(kp), pool0), what
+        if add:
+            assert np.array_equal(bits(s_out), bits(s_ref)), what
+        else:
+            assert torch.all(s_out == 7.0)
+
+
 def test_embedding_and_argmax(tmc, orc, torch):
     vocab, hidden = 1000, 64
     table = orc.f16(normal(601, (vocab, hidden)))
@@ -721,7 +773,7 @@ def test_fused_norm_gemv_equals_two_kernels_bit_exact(tmc, orc, torch, cfg_t):
     bit for bit, residual sum included."""
     cfg = tmc.GemvConfig(*cfg_t) if cfg_t else None
     ref_cfg = cfg if cfg else None  # the fused default differs by matrix count
-    for k, n in ((4096, 200), (1160, 4096)):
+    for k, n in ((4096, 200), (1160, 4096), (1024, 9000)):  # the last loops over row groups
         h = dev_f16(orc.f16(normal(370, (1, k))))
         r = dev_f16(orc.f16(normal(371, (1, k))))
         gamma = dev_f16(orc.f16(uniform(372, (k,), 0.5, 1.5)))
