@@ -103,6 +103,7 @@ def _declare(l):
         "tmc_buf_write": (i32, [vp, vp, sz, sz]),
         "tmc_buf_write_raw": (i32, [vp, vp, sz, sz]),
         "tmc_buf_write_raw_async": (i32, [vp, vp, sz, sz]),
+        "tmc_buf_copy_async": (i32, [vp, sz, vp, sz, sz]),
         "tmc_buf_read_raw": (i32, [vp, vp, sz, sz]),
         "tmc_buf_read": (i32, [vp, vp]),
         "tmc_buf_count": (sz, [vp]),

@@ -660,11 +660,18 @@ int chunk_for(int64_t head_dim, int64_t batch, int64_t kv_heads, int64_t capacit
 
 bool head_dim_ok(int64_t head_dim) { return chunk_for(head_dim, 1, 1, 1) > 0; }
 
-// Split geometry of a launch.  When chunk_for would cut a row into several
-// splits but the whole capacity fits one block (<= 1024 positions, D = 128,
-// GQA group <= 2), one block of 16 waves covers the row instead: no partial
-// slots and no combine launch.  Small batches (batch-1 decode, whose
-// attention is launch-latency bound) take this path.
+// Split geometry of a launch.  When the whole capacity fits one block
+// (<= 1024 positions, D = 128, GQA group <= 2) and the (request, kv head)
+// rows number at most one per CU (256 on MI355X), one block of 16 waves
+// covers each row: no partial slots and no combine launch.  Measured on
+// random 16-position pages, lengths U[33, 640]: batch 1 (L 300) 7.3 us in
+// one launch against 5.8 + 4.7 us with the merge; batch 8 MHA 11.0 against
+// 15.3 us; batch 16 GQA-2 11.7 against 16.1 us.  With more rows (batch 16
+// MHA) the 4-wave blocks win (17.9 against 20.2 us).  A lone long row is
+// slower in one block (batch 1, L 1024: 13.4 us) than split, the price of
+// the short-context case.
+constexpr int kWideMaxRows = 256;
+
 struct SplitPlan {
   int chunk;
   int waves;
@@ -673,8 +680,8 @@ struct SplitPlan {
 SplitPlan split_plan(int64_t head_dim, int64_t batch, int64_t q_heads, int64_t kv_heads,
                      int64_t capacity) {
   const int chunk = chunk_for(head_dim, batch, kv_heads, capacity);
-  if (head_dim == 128 && chunk > 0 && capacity > chunk && capacity <= kMfmaMaxChunk &&
-      q_heads / kv_heads <= kWideMaxGroup)
+  if (head_dim == 128 && chunk > 0 && capacity <= kMfmaMaxChunk &&
+      batch * kv_heads <= kWideMaxRows && q_heads / kv_heads <= kWideMaxGroup)
     return {(int)((capacity + kMfmaStep - 1) / kMfmaStep * kMfmaStep), kWideWaves};
   return {chunk, kWaves};
 }

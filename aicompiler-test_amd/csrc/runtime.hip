@@ -1043,6 +1043,21 @@ extern "C" int tmc_buf_write_raw_async(tmc_buffer* buf, const void* data, size_t
   return hip_ok(hipEventRecord(rt->staged_done, rt->stream), "staging event");
 }
 
+extern "C" int tmc_buf_copy_async(tmc_buffer* dst, size_t dst_offset, const tmc_buffer* src,
+                                  size_t src_offset, size_t count) {
+  clear_error();
+  if (!dst || !src || dst->rt != src->rt || dst->dtype != src->dtype)
+    return fail("tmc_buf_copy_async: buffers of different runtimes or dtypes.");
+  if (count == 0 || dst_offset > dst->count || count > dst->count - dst_offset ||
+      src_offset > src->count || count > src->count - src_offset)
+    return fail("tmc_buf_copy_async: invalid range.");
+  const size_t eb = element_bytes(dst->dtype);
+  return hip_ok(hipMemcpyAsync(static_cast<char*>(dst->ptr) + dst_offset * eb,
+                               static_cast<const char*>(src->ptr) + src_offset * eb, count * eb,
+                               hipMemcpyDeviceToDevice, dst->rt->stream),
+                "device copy");
+}
+
 extern "C" int tmc_buf_read_raw(const tmc_buffer* buf, void* data, size_t count, size_t offset) {
   clear_error();
   if (!buf || !data || offset > buf->count || count > buf->count - offset)

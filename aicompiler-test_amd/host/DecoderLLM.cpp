@@ -580,6 +580,85 @@ BatchedDecodeRun BatchedDecodeExecutor::run(const std::vector<float>& tokenIds,
   return run(tokens, lengths, tables, readLogits, true);
 }
 
+std::string BatchedDecodeExecutor::checkStep(
+    const std::vector<std::int32_t>* tokenIds, const std::vector<std::int32_t>& validLengths,
+    const std::vector<std::vector<std::int32_t>>& blockTables) const {
+  const auto& plan = model_->plan;
+  const std::size_t rows = validLengths.size();
+  if (rows == 0 || rows > maximumBatchSize_ || (tokenIds && tokenIds->size() != rows) ||
+      blockTables.size() != plan.layerCount)
+    return "Batched decode metadata shape is invalid.";
+  for (std::size_t l = 0; l < blockTables.size(); ++l)
+    if (blockTables[l].size() != rows * maxPages_)
+      return "Batched decode block-table shape is invalid.";
+  // Host checks that keep every device access inside its buffer: token ids in
+  // the vocabulary, lengths in [1, capacity], pages allocated in their pool
+  // and present for every attended position.
+  for (std::size_t r = 0; r < rows; ++r) {
+    if (tokenIds &&
+        ((*tokenIds)[r] < 0 || static_cast<std::size_t>((*tokenIds)[r]) >= plan.vocabularySize))
+      return "Batched decode token id is outside the vocabulary.";
+    if (validLengths[r] <= 0 || static_cast<std::size_t>(validLengths[r]) > plan.attention.capacity)
+      return "KV cache valid length is outside the configured capacity.";
+    const std::size_t needed = (static_cast<std::size_t>(validLengths[r]) + pageSize_ - 1) / pageSize_;
+    for (std::size_t l = 0; l < blockTables.size(); ++l) {
+      for (std::size_t p = 0; p < maxPages_; ++p) {
+        const std::int32_t page = blockTables[l][r * maxPages_ + p];
+        if ((p < needed && !pools_[l]->isAllocated(page)) || (page >= 0 && !pools_[l]->isAllocated(page)))
+          return "Batched decode block table names a page that is not allocated in its layer's "
+                 "pool.";
+      }
+    }
+  }
+  return {};
+}
+
+std::string BatchedDecodeExecutor::reserveHistory(std::size_t steps) {
+  if (steps == 0) return "Chained decode needs at least one history step.";
+  if (steps <= historySteps_) return {};
+  try {
+    history_ = allocate(*runtime_, steps * maximumBatchSize_, nullptr, ElementType::Int32);
+  } catch (const std::exception& error) {
+    return error.what();
+  }
+  historySteps_ = steps;
+  return {};
+}
+
+std::string BatchedDecodeExecutor::launchChained(
+    const std::vector<std::int32_t>& tokenIds, const std::vector<std::int32_t>& validLengths,
+    const std::vector<std::vector<std::int32_t>>& blockTables, std::size_t historyStep) {
+  const std::size_t rows = validLengths.size();
+  if (historyStep >= historySteps_) return "Chained decode history step is out of range.";
+  if (tokenIds.empty() && rows != chainedRows_)
+    return "Chained decode without tokens needs the previous step's row count.";
+  auto error = checkStep(tokenIds.empty() ? nullptr : &tokenIds, validLengths, blockTables);
+  if (!error.empty()) return error;
+  std::size_t index = 0;
+  while (buckets_[index]->rows < rows) ++index;
+  auto& bucket = *buckets_[index];
+  // Tokens fed back on the device leave the host shadow stale: upload the
+  // metadata in full, then overwrite the token slots from nextTokens_.
+  std::fill(metaShadow_.begin(), metaShadow_.end(), std::numeric_limits<std::int32_t>::min());
+  const std::vector<std::int32_t> placeholder(rows, 0);
+  error = upload(tokenIds.empty() ? placeholder : tokenIds, validLengths, blockTables, rows,
+                 bucket.rows);
+  if (error.empty() && tokenIds.empty()) error = tokensView_->copyFromAsync(*nextTokens_, rows);
+  if (error.empty()) error = bucket.sequence->launch();
+  if (error.empty())
+    error = history_->copyFromAsync(*nextTokens_, rows, historyStep * maximumBatchSize_);
+  std::fill(metaShadow_.begin(), metaShadow_.end(), std::numeric_limits<std::int32_t>::min());
+  chainedRows_ = error.empty() ? rows : 0;
+  return error;
+}
+
+std::string BatchedDecodeExecutor::readHistory(std::size_t steps,
+                                               std::vector<std::int32_t>& out) const {
+  if (steps == 0 || steps > historySteps_) return "Chained decode history range is invalid.";
+  out.assign(steps * maximumBatchSize_, 0);
+  return history_->readRaw(out.data(), out.size());  // waits for the stream
+}
+
 BatchedDecodeRun BatchedDecodeExecutor::run(const std::vector<std::int32_t>& tokenIds,
                                             const std::vector<std::int32_t>& validLengths,
                                             const std::vector<std::vector<std::int32_t>>& blockTables,
@@ -587,41 +666,8 @@ BatchedDecodeRun BatchedDecodeExecutor::run(const std::vector<std::int32_t>& tok
   BatchedDecodeRun result;
   const auto& plan = model_->plan;
   const std::size_t rows = tokenIds.size();
-  if (rows == 0 || rows > maximumBatchSize_ || validLengths.size() != rows ||
-      blockTables.size() != plan.layerCount) {
-    result.errorMessage = "Batched decode metadata shape is invalid.";
-    return result;
-  }
-  for (std::size_t l = 0; l < blockTables.size(); ++l) {
-    if (blockTables[l].size() != rows * maxPages_) {
-      result.errorMessage = "Batched decode block-table shape is invalid.";
-      return result;
-    }
-  }
-  // Host checks that keep every device access inside its buffer: token ids in
-  // the vocabulary, lengths in [1, capacity], pages allocated in their pool
-  // and present for every attended position.
-  for (std::size_t r = 0; r < rows; ++r) {
-    if (tokenIds[r] < 0 || static_cast<std::size_t>(tokenIds[r]) >= plan.vocabularySize) {
-      result.errorMessage = "Batched decode token id is outside the vocabulary.";
-      return result;
-    }
-    if (validLengths[r] <= 0 || static_cast<std::size_t>(validLengths[r]) > plan.attention.capacity) {
-      result.errorMessage = "KV cache valid length is outside the configured capacity.";
-      return result;
-    }
-    const std::size_t needed = (static_cast<std::size_t>(validLengths[r]) + pageSize_ - 1) / pageSize_;
-    for (std::size_t l = 0; l < blockTables.size(); ++l) {
-      for (std::size_t p = 0; p < maxPages_; ++p) {
-        const std::int32_t page = blockTables[l][r * maxPages_ + p];
-        if ((p < needed && !pools_[l]->isAllocated(page)) || (page >= 0 && !pools_[l]->isAllocated(page))) {
-          result.errorMessage = "Batched decode block table names a page that is not allocated "
-                                "in its layer's pool.";
-          return result;
-        }
-      }
-    }
-  }
+  result.errorMessage = checkStep(&tokenIds, validLengths, blockTables);
+  if (!result.errorMessage.empty()) return result;
   std::size_t index = 0;
   while (buckets_[index]->rows < rows) ++index;
   auto& bucket = *buckets_[index];

@@ -200,6 +200,19 @@ class BatchedDecodeExecutor {
                                      const std::vector<std::vector<std::int32_t>>& blockTables,
                                      bool readLogits = true, bool timeGpu = false);
 
+  // Chained decode: steps queued back to back with no host wait.  A step
+  // with empty `tokenIds` takes the previous step's greedy tokens on the
+  // device (same row count); every step's next tokens are also copied to
+  // history slot `historyStep` (reserveHistory first).  readHistory waits for
+  // the stream and returns [steps][maximumBatchSize()] token ids.  Same
+  // checks and results as run(); the loop of measureDecodeThroughput.
+  [[nodiscard]] std::string reserveHistory(std::size_t steps);
+  [[nodiscard]] std::string launchChained(const std::vector<std::int32_t>& tokenIds,
+                                          const std::vector<std::int32_t>& validLengths,
+                                          const std::vector<std::vector<std::int32_t>>& blockTables,
+                                          std::size_t historyStep);
+  [[nodiscard]] std::string readHistory(std::size_t steps, std::vector<std::int32_t>& out) const;
+
   [[nodiscard]] std::size_t maximumBatchSize() const noexcept { return maximumBatchSize_; }
   [[nodiscard]] std::size_t maxPages() const noexcept { return maxPages_; }
   [[nodiscard]] std::size_t activationStorageBytes() const noexcept { return activationBytes_; }
@@ -221,6 +234,9 @@ class BatchedDecodeExecutor {
                                    const std::vector<std::int32_t>& lengths,
                                    const std::vector<std::vector<std::int32_t>>& tables,
                                    std::size_t rows, std::size_t bucket);
+  [[nodiscard]] std::string checkStep(const std::vector<std::int32_t>* tokenIds,
+                                      const std::vector<std::int32_t>& validLengths,
+                                      const std::vector<std::vector<std::int32_t>>& blockTables) const;
 
   struct Bucket;
   hip::HipRuntime* runtime_ = nullptr;
@@ -240,6 +256,8 @@ class BatchedDecodeExecutor {
       mlp_, logits_, nextTokens_;
   std::vector<std::unique_ptr<Bucket>> buckets_;
   std::vector<std::int32_t> metaShadow_, tableShadow_;
+  hip::BufferHandle history_;  // int32 [steps][M], chained decode
+  std::size_t historySteps_ = 0, chainedRows_ = 0;
 };
 
 struct BatchedDecodeExecutor::Creation {

@@ -122,6 +122,14 @@ std::string HipBuffer::writeRawAsync(const void* data, std::size_t count,
              : lastError("Buffer write failed.");
 }
 
+std::string HipBuffer::copyFromAsync(const HipBuffer& source, std::size_t count,
+                                     std::size_t offset, std::size_t sourceOffset) const {
+  if (count == 0) return {};
+  return tmc_buf_copy_async(buffer_, offset, source.handle(), sourceOffset, count) == 0
+             ? std::string()
+             : lastError("Buffer copy failed.");
+}
+
 void* HipBuffer::devicePointer() const { return tmc_buf_device_ptr(buffer_); }
 
 std::size_t HipBuffer::storageBytes() const { return elementCount() * elementBytes(elementType()); }

@@ -104,6 +104,11 @@ class HipBuffer {
   // waiting: later launches on the stream see the data.
   [[nodiscard]] std::string writeRawAsync(const void* data, std::size_t count,
                                           std::size_t offset = 0) const;
+  // Device copy of `count` elements from `source` (same dtype), queued on
+  // the runtime stream.
+  [[nodiscard]] std::string copyFromAsync(const HipBuffer& source, std::size_t count,
+                                          std::size_t offset = 0,
+                                          std::size_t sourceOffset = 0) const;
   [[nodiscard]] void* devicePointer() const;
   [[nodiscard]] std::size_t storageBytes() const;
   [[nodiscard]] tmc_buffer* handle() const noexcept { return buffer_; }

@@ -570,12 +570,12 @@ DecodeThroughput measureDecodeThroughput(hip::HipRuntime& runtime,
     result.generatedTokenIds.assign(B, {});
     std::vector<std::int32_t> last(B, -1);
 
-    // One batched step over `rows`; commits the new lengths.
+    // The next lengths and block tables of `rows` (pages staged as needed).
     std::vector<double> gpuTimes, hostTimes;
-    auto step = [&](const std::vector<std::size_t>& rows, const std::vector<std::int32_t>& tokens,
-                    bool record) {
-      std::vector<std::int32_t> lengths;
-      std::vector<std::vector<std::int32_t>> tables(L);
+    auto stage = [&](const std::vector<std::size_t>& rows, std::vector<std::int32_t>& lengths,
+                     std::vector<std::vector<std::int32_t>>& tables) {
+      lengths.clear();
+      tables.assign(L, {});
       for (const auto r : rows) {
         const std::size_t next = states[r].front()->currentLength() + 1;
         lengths.push_back(static_cast<std::int32_t>(next));
@@ -587,6 +587,17 @@ DecodeThroughput measureDecodeThroughput(hip::HipRuntime& runtime,
           tables[l].insert(tables[l].end(), table.begin(), table.end());
         }
       }
+    };
+    auto commit = [&](const std::vector<std::size_t>& rows, const std::vector<std::int32_t>& lengths) {
+      for (std::size_t k = 0; k < rows.size(); ++k)
+        for (auto& state : states[rows[k]]) state->commitLength(static_cast<std::size_t>(lengths[k]));
+    };
+    // One batched step over `rows`; commits the new lengths.
+    auto step = [&](const std::vector<std::size_t>& rows, const std::vector<std::int32_t>& tokens,
+                    bool record) {
+      std::vector<std::int32_t> lengths;
+      std::vector<std::vector<std::int32_t>> tables;
+      stage(rows, lengths, tables);
       const auto t0 = Clock::now();
       const auto out = executor.run(tokens, lengths, tables, false, timeGpu);
       const double us = elapsedUs(t0, Clock::now());
@@ -595,8 +606,7 @@ DecodeThroughput measureDecodeThroughput(hip::HipRuntime& runtime,
         hostTimes.push_back(us);
         if (out.gpuExecutionTimeUs) gpuTimes.push_back(*out.gpuExecutionTimeUs);
       }
-      for (std::size_t k = 0; k < rows.size(); ++k)
-        for (auto& state : states[rows[k]]) state->commitLength(static_cast<std::size_t>(lengths[k]));
+      commit(rows, lengths);
       return out.nextTokenIds;
     };
 
@@ -699,13 +709,43 @@ DecodeThroughput measureDecodeThroughput(hip::HipRuntime& runtime,
     for (std::size_t r = 0; r < B; ++r)
       for (std::size_t s = 0; s < decodeTokens; ++s) kvTokens += prompts[r].size() + 1 + s;
     result.kvBytesRead = kvTokens * L * 2 * plan.kvWidth() * 2;
+    if (!timeGpu && decodeTokens > 0) {
+      const auto error = executor.reserveHistory(decodeTokens);
+      if (!error.empty()) throw std::runtime_error(error);
+    }
     const auto decodeStart = Clock::now();
-    for (std::size_t s = 0; s < decodeTokens; ++s) {
-      const auto next = step(all, last, true);
-      for (std::size_t r = 0; r < B; ++r) {
-        last[r] = static_cast<std::int32_t>(next[r]);
-        result.generatedTokenIds[r].push_back(next[r]);
+    if (timeGpu) {
+      for (std::size_t s = 0; s < decodeTokens; ++s) {
+        const auto next = step(all, last, true);
+        for (std::size_t r = 0; r < B; ++r) {
+          last[r] = static_cast<std::int32_t>(next[r]);
+          result.generatedTokenIds[r].push_back(next[r]);
+        }
       }
+    } else if (decodeTokens > 0) {
+      // Greedy tokens stay on the device from step to step (chained steps,
+      // no host wait); they are read back once at the end, so the host's
+      // staging and graph launches overlap the GPU's work.
+      std::vector<std::int32_t> lengths;
+      std::vector<std::vector<std::int32_t>> tables;
+      for (std::size_t s = 0; s < decodeTokens; ++s) {
+        stage(all, lengths, tables);
+        const auto t0 = Clock::now();
+        const auto error =
+            executor.launchChained(s == 0 ? last : std::vector<std::int32_t>{}, lengths, tables, s);
+        if (!error.empty()) throw std::runtime_error(error);
+        hostTimes.push_back(elapsedUs(t0, Clock::now()));
+        commit(all, lengths);
+      }
+      std::vector<std::int32_t> history;
+      const auto error = executor.readHistory(decodeTokens, history);
+      if (!error.empty()) throw std::runtime_error(error);
+      const std::size_t M = executor.maximumBatchSize();
+      for (std::size_t s = 0; s < decodeTokens; ++s)
+        for (std::size_t r = 0; r < B; ++r) {
+          last[r] = history[s * M + r];
+          result.generatedTokenIds[r].push_back(static_cast<float>(last[r]));
+        }
     }
     result.decodePhaseUs = elapsedUs(decodeStart, Clock::now());
     result.decodeSteps = decodeTokens;

@@ -91,6 +91,12 @@ int tmc_buf_read_raw(const tmc_buffer *buf, void *data, size_t count, size_t off
  * it is for per-step metadata uploads that precede a graph launch.  Copies
  * larger than the staging area (4 MiB) fall back to tmc_buf_write_raw. */
 int tmc_buf_write_raw_async(tmc_buffer *buf, const void *data, size_t count, size_t offset);
+/* Device-to-device copy of `count` elements (same dtype, same runtime),
+ * queued on the runtime stream.  No counterpart in the reference: the
+ * chained decode loop uses it to feed each step's greedy tokens to the next
+ * step and into a history buffer without a host round trip. */
+int tmc_buf_copy_async(tmc_buffer *dst, size_t dst_offset, const tmc_buffer *src,
+                       size_t src_offset, size_t count);
 /* MetalBuffer::read (MetalRuntime.hpp:66; .mm:171-186). */
 int tmc_buf_read(const tmc_buffer *buf, float *out);
 size_t tmc_buf_count(const tmc_buffer *buf);

@@ -360,6 +360,39 @@ def test_serving_matches_single_request_decoding(host, orc, rt, chunk, per_chunk
                 break
 
 
+@pytest.mark.parametrize("chunk", [0, 16])
+def test_chained_decode_throughput_matches_stepped(host, orc, rt, chunk):
+    """measureDecodeThroughput's chained steps (greedy tokens fed back on the
+    device, read once at the end) generate exactly the tokens of the stepped
+    loop (one host round trip per step, the timeGpu path), batch 3 with
+    ragged prompts crossing page boundaries; and the first generated token
+    of each row equals the one-request decoder's."""
+    cfg = CONFIGS["serve"]
+    m = _weights(orc, cfg, 71)
+    w = _workload(host, orc, cfg, m)
+    model = host.create_model_resources(rt, w)
+    rng = np.random.default_rng(72)
+    prompts = [list(map(int, rng.integers(0, cfg["vocabulary"], n))) for n in (5, 17, 30)]
+    decode = 20
+    chained = host.measure_decode_throughput(rt, model, prompts, decode, P, False, False, chunk)
+    stepped = host.measure_decode_throughput(rt, model, prompts, decode, P, True, False, chunk)
+    assert chained["passed"], chained["error"]
+    assert stepped["passed"], stepped["error"]
+    assert stepped["step_gpu"]["samples"] == decode
+    for r, (a, b) in enumerate(zip(chained["generated_token_ids"], stepped["generated_token_ids"])):
+        assert len(a) == decode + 1, r
+        assert [int(t) for t in a] == [int(t) for t in b], r
+    opts = host.DecoderLLMCompileOptions()
+    opts.kv_page_size = P
+    opts.shared_model_resources = model
+    for r, prompt in enumerate(prompts):
+        dec, _ = host.compile_decoder_llm(rt, w, opts)
+        first = dec.prefill([float(t) for t in prompt], True)
+        V = cfg["vocabulary"]
+        _check_token(int(chained["generated_token_ids"][r][0]), int(first["next_token_ids"][0]),
+                     first["logits"][-V:], f"row {r}")
+
+
 def test_tuned_executor_matches_default_and_caches_shapes(host, orc, rt):
     """Batch-1 GEMVs with the decode GEMV tuner's per-shape selections: the
     shapes are tuned once (process cache), and the step's logits match the

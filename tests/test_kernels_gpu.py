@@ -317,10 +317,12 @@ def test_decode_attention_edges(tmc, orc, torch, valid, d, qh, kvh):
 
 @pytest.mark.parametrize("b,valid,qh,kvh,cap", [(1, 1, 32, 32, 1024), (1, 33, 32, 32, 1024),
                                                  (1, 700, 32, 32, 1024), (1, 1024, 32, 32, 1024),
-                                                 (2, 999, 8, 4, 1000), (3, 129, 4, 2, 160)])
+                                                 (2, 999, 8, 4, 1000), (3, 129, 4, 2, 160),
+                                                 (9, 500, 32, 32, 512)])
 def test_decode_attention_one_wide_split(tmc, orc, torch, b, valid, qh, kvh, cap):
-    """Small batches at capacity <= 1024 (head_dim 128, GQA group <= 2) run
-    one 16-wave block per (request, kv head): no workspace, no combine."""
+    """Capacity <= 1024 (head_dim 128, GQA group <= 2) runs one split per
+    (request, kv head): 16-wave blocks up to 256 such rows, 4-wave blocks
+    beyond (the last case, 288 rows); no workspace, no combine."""
     d = 128
     assert tmc.attention_workspace_bytes(b, qh, kvh, d, cap) == 0
     k = orc.f16(normal(321, (b, kvh, cap, d)))
