@@ -41,6 +41,8 @@ def _declare(l):
         "tmc_gemv_f16_config": (i32, [vp, vp, vp, i32, i64, i64, i64, vp, vp]),
         "tmc_qkv_rope_append_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64,
                                           i64, i64, i64, vp, vp]),
+        "tmc_qkv_rope_append_packed_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64,
+                                                 i64, i64, i64, i64, i64, i64, i32, vp, vp]),
         "tmc_add_rmsnorm_qkv_rope_append_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
                                                       vp, vp, i64, i64, i64, i64, i64, i64,
                                                       C.c_float, vp, vp]),
@@ -449,6 +451,21 @@ def qkv_rope_append(x, w, cos, sin, valid_lengths, table, active, q_out, k_pool,
                                         capacity, page_size, None if cfg is None else C.byref(cfg),
                                         _stream(stream)),
           "tmc_qkv_rope_append_f16")
+
+
+def qkv_rope_append_packed(x, packed_w, cos, sin, valid_lengths, tables, active, q_out, k_pool,
+                           v_pool, batch, hidden, q_heads, kv_heads, head_dim, capacity, page_size,
+                           max_pages, layout=0, config=None, stream=None):
+    """Batched q.k.v projection over packed weights with RoPE and the paged
+    append in its epilogue (tmc_qkv_rope_append_packed_f16)."""
+    cfg = None
+    if config is not None:
+        cfg = GemvConfig(*config) if isinstance(config, tuple) else config
+    check(lib().tmc_qkv_rope_append_packed_f16(
+        _ptr(x), _ptr(packed_w), _ptr(cos), _ptr(sin), _ptr(valid_lengths), _ptr(tables),
+        _ptr(active), _ptr(q_out), _ptr(k_pool), _ptr(v_pool), batch, hidden, q_heads, kv_heads,
+        head_dim, capacity, page_size, max_pages, layout, None if cfg is None else C.byref(cfg),
+        _stream(stream)), "tmc_qkv_rope_append_packed_f16")
 
 
 def add_rmsnorm_qkv_rope_append(residual, update, gamma, w, sum_out, cos, sin, valid_lengths,

@@ -66,61 +66,6 @@ struct NormArgs {
   float eps = 0.0f;
 };
 
-// Epilogue of the batch-1 q.k.v projection fused with RoPE and the paged
-// K/V append (ROPE = true, two rows per wave): the rows 2i and 2i+1 of the
-// projection are one interleaved RoPE pair of q or k, or two v features.
-// The pair is rounded to fp16 as the projection output would be, rotated
-// exactly as decode_rope_append_kernel rotates it, and stored where that
-// kernel stores it: q to q_out, k and v into the pools at position
-// valid_lengths[0] - 1 through block_table (one request).
-struct RopeArgs {
-  const float* cosine = nullptr;
-  const float* sine = nullptr;
-  const int32_t* valid_lengths = nullptr;
-  const int32_t* block_table = nullptr;
-  const int32_t* active_count = nullptr;
-  half_t* q_out = nullptr;
-  half_t* k_pool = nullptr;
-  half_t* v_pool = nullptr;
-  int q_heads = 0, kv_heads = 0, head_dim = 0, capacity = 0, page_size = 0;
-};
-
-__device__ __forceinline__ void rope_append_pair(const RopeArgs& ra, int column, float sum_even,
-                                                 float sum_odd) {
-  const int valid = ra.valid_lengths[0];
-  if (ra.active_count[0] < 1 || valid <= 0 || valid > ra.capacity) return;
-  const int position = valid - 1;
-  const int d = ra.head_dim, pairs = d / 2;
-  const int q_width = ra.q_heads * d, kv_width = ra.kv_heads * d;
-  const half_t x0 = from_float<half_t>(sum_even), x1 = from_float<half_t>(sum_odd);
-  half_t* dst;
-  half_t y0 = x0, y1 = x1;
-  if (column < q_width + kv_width) {
-    const int pair = (column % d) / 2;
-    const float c = ra.cosine[(size_t)position * pairs + pair];
-    const float s = ra.sine[(size_t)position * pairs + pair];
-    float re, ro;
-    rotate_pair(to_float<half_t>(x0), to_float<half_t>(x1), c, s, re, ro);
-    // the fp32 results are rounded once to fp16, as the unfused kernel does
-    asm volatile("" : "+v"(re), "+v"(ro));
-    y0 = from_float<half_t>(re);
-    y1 = from_float<half_t>(ro);
-  }
-  if (column < q_width) {
-    dst = ra.q_out + column;
-  } else {
-    const int page = ra.block_table[position / ra.page_size];
-    if (page < 0) return;
-    const bool key = column < q_width + kv_width;
-    const int feature = column - q_width - (key ? 0 : kv_width);
-    dst = (key ? ra.k_pool : ra.v_pool) +
-          (((size_t)page * ra.kv_heads + feature / d) * ra.page_size + position % ra.page_size) * d +
-          feature % d;
-  }
-  dst[0] = y0;
-  dst[1] = y1;
-}
-
 // PRO > 0 (batch 1): every block first builds the normalized row in LDS
 // exactly as norm_vec_kernel does (same per-thread chunk order, wave sums,
 // and 4-wave total, so the row is bit-identical), then streams its weight
@@ -248,7 +193,7 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const half_t* __restrict_
     if constexpr (ROPE && KS == 1) {
       const float even = wave_sum(acc[0][0][0]);
       const float odd = wave_sum(acc[0][1][0]);
-      if (lane == 0 && live) rope_append_pair(ra, row0, even, odd);
+      if (lane == 0 && live) rope_append_pair(ra, 0, row0, even, odd);
     } else if constexpr (KS == 1) {
 #pragma unroll
       for (int r = 0; r < RPW; ++r)
@@ -278,7 +223,7 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const half_t* __restrict_
             even += partial[wave + s][0][0][0];
             odd += partial[wave + s][0][1][0];
           }
-          rope_append_pair(ra, row0, even, odd);
+          rope_append_pair(ra, 0, row0, even, odd);
         }
       } else if (part == 0 && live) {
         for (int idx = lane; idx < RPW * NB; idx += kWave) {
@@ -998,7 +943,7 @@ int qkv_rope_entry(int pro, const void* x, const NormArgs& na, const void* w,
   ra.cosine = cosine;
   ra.sine = sine;
   ra.valid_lengths = valid_lengths;
-  ra.block_table = block_table;
+  ra.block_tables = block_table;
   ra.active_count = active_count;
   ra.q_out = static_cast<half_t*>(q_out);
   ra.k_pool = static_cast<half_t*>(key_pool);

@@ -66,13 +66,17 @@ __global__ __launch_bounds__(256) void pack_kernel(const half_t* __restrict__ w,
 // XP: x is one 16-row pass in fragment order (lane l of chunk c holds row
 // l % 16, k 32c + 8(l / 16) .. +7, the A operand as loaded); YP: the fp16
 // output pass is written in the same order for the next GEMM.
-template <int MATS, int U, typename OutT, bool XP = false, bool YP = false>
+// ROPE: y is not written; the q.k.v projection's column pairs of each batch
+// row go through rope_append_pair (RoPE + paged append, request
+// ra.request_base + row).
+template <int MATS, int U, typename OutT, bool XP = false, bool YP = false, bool ROPE = false>
 __global__ __launch_bounds__(1024) void packed_gemm_kernel(const half_t* __restrict__ x,
                                                            const half_t* __restrict__ p0,
                                                            const half_t* __restrict__ p1,
                                                            OutT* __restrict__ y, int m_rows,
                                                            int n_out, int k_in, int ks_count,
-                                                           unsigned packed_bytes) {
+                                                           unsigned packed_bytes, RopeArgs ra) {
+  static_assert(!ROPE || (MATS == 1 && !YP), "the RoPE epilogue serves the q.k.v projection");
   extern __shared__ float red[];  // [ks][MATS][4][64]
   const int lane = threadIdx.x & (kWave - 1);
   const int ks = threadIdx.x / kWave;
@@ -126,6 +130,22 @@ __global__ __launch_bounds__(1024) void packed_gemm_kernel(const half_t* __restr
 #pragma unroll
     for (int r = 0; r < 4; ++r) red[((ks * MATS + m) * 4 + r) * kWave + lane] = acc[m][r];
   __syncthreads();
+  if constexpr (ROPE) {
+    // 16 batch rows x 8 column pairs of the tile; the pair's even column sits
+    // in lane 16g + 2p and the odd one in the next lane
+    for (int idx = threadIdx.x; idx < 128; idx += ks_count * kWave) {
+      const int p = idx & 7, row = idx >> 3;
+      const int l = 16 * (row >> 2) + 2 * p, r = row & 3;
+      float even = 0.0f, odd = 0.0f;
+      for (int w = 0; w < ks_count; ++w) {
+        even += red[(w * 4 + r) * kWave + l];
+        odd += red[(w * 4 + r) * kWave + l + 1];
+      }
+      const int col = nt * 16 + 2 * p;
+      if (row < m_rows && col < n_out) rope_append_pair(ra, ra.request_base + row, col, even, odd);
+    }
+    return;
+  }
   // acc[r] of lane (j, g) = out[batch 4g + r][row 16nt + j]
   for (int idx = threadIdx.x; idx < 4 * kWave; idx += ks_count * kWave) {
     const int l = idx % kWave, r = idx / kWave;
@@ -166,9 +186,10 @@ void default_packed(int64_t batch, int64_t n, int mats, int& unroll, int& ks) {
     ks = 8;
 }
 
-template <int MATS, typename OutT, bool XP, bool YP>
+template <int MATS, typename OutT, bool XP, bool YP, bool ROPE = false>
 int run_packed(const half_t* x, const half_t* p0, const half_t* p1, OutT* y, int64_t batch,
-               int64_t k, int64_t n, int unroll, int ks, hipStream_t st) {
+               int64_t k, int64_t n, int unroll, int ks, hipStream_t st,
+               const RopeArgs& rope = RopeArgs{}) {
   const int64_t bytes = packed_elements(n, k) * 2;
   const dim3 grid((unsigned)((n + 15) / 16));
   const size_t lds = (size_t)ks * MATS * 4 * kWave * sizeof(float);
@@ -177,16 +198,18 @@ int run_packed(const half_t* x, const half_t* p0, const half_t* p1, OutT* y, int
   for (int64_t r0 = 0; r0 < batch; r0 += 16) {
     const int rows = (int)std::min<int64_t>(16, batch - r0);
     const half_t* xs = x + (r0 / 16) * x_pass;
-    OutT* ys = y + (r0 / 16) * y_pass;
+    OutT* ys = ROPE ? y : y + (r0 / 16) * y_pass;
+    RopeArgs ra = rope;
+    ra.request_base = (int)r0;
     if (unroll == 1)
-      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 1, OutT, XP, YP>), grid, dim3(ks * kWave), lds,
-                         st, xs, p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes);
+      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 1, OutT, XP, YP, ROPE>), grid, dim3(ks * kWave),
+                         lds, st, xs, p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes, ra);
     else if (unroll == 2)
-      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 2, OutT, XP, YP>), grid, dim3(ks * kWave), lds,
-                         st, xs, p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes);
+      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 2, OutT, XP, YP, ROPE>), grid, dim3(ks * kWave),
+                         lds, st, xs, p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes, ra);
     else
-      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 4, OutT, XP, YP>), grid, dim3(ks * kWave), lds,
-                         st, xs, p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes);
+      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 4, OutT, XP, YP, ROPE>), grid, dim3(ks * kWave),
+                         lds, st, xs, p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes, ra);
     if (check_launch("packed_gemm_kernel")) return 1;
   }
   return 0;
@@ -311,6 +334,62 @@ extern "C" int tmc_gemm_packed_ex_f16(const void* x, const void* packed_w, void*
                                       int layout, const tmc_gemv_config* config, void* stream) {
   return packed_entry(1, x, packed_w, nullptr, y, y_dtype, batch, in_features, out_features,
                       layout, config, stream);
+}
+
+extern "C" int tmc_qkv_rope_append_packed_f16(
+    const void* x, const void* packed_w, const float* cosine, const float* sine,
+    const int32_t* valid_lengths, const int32_t* block_tables, const int32_t* active_count,
+    void* q_out, void* key_pool, void* value_pool, int64_t batch, int64_t hidden,
+    int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t capacity, int64_t page_size,
+    int64_t max_pages, int layout, const tmc_gemv_config* config, void* stream) {
+  TMC_REQUIRE(x && packed_w && cosine && sine && valid_lengths && block_tables && active_count &&
+                  q_out && key_pool && value_pool,
+              "Packed q.k.v RoPE append: null pointer.");
+  TMC_REQUIRE(batch > 0 && batch < (1LL << 31) && hidden > 0 && hidden % 8 == 0 &&
+                  aligned16(x) && aligned16(packed_w),
+              "Packed q.k.v RoPE append: hidden must be a positive multiple of 8 and x, W "
+              "16-byte aligned.");
+  TMC_REQUIRE(q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 && head_dim > 0 &&
+                  head_dim % 2 == 0 && capacity > 0 && page_size > 0 && max_pages > 0 &&
+                  max_pages < (1LL << 31) && (q_heads + 2 * kv_heads) * head_dim < (1LL << 31),
+              "Packed q.k.v RoPE append: invalid head geometry, capacity or pages.");
+  const int64_t n = (q_heads + 2 * kv_heads) * head_dim;
+  TMC_REQUIRE((uint64_t)packed_elements(n, hidden) * 2 < kNone && (uint64_t)16 * hidden * 2 < kNone,
+              "Packed q.k.v RoPE append: operands exceed the 4 GiB buffer range.");
+  TMC_REQUIRE((layout & ~TMC_LAYOUT_X_PACKED) == 0,
+              "Packed q.k.v RoPE append: layout may only set TMC_LAYOUT_X_PACKED.");
+  int unroll, ks;
+  default_packed(batch, n, 1, unroll, ks);
+  if (config && config->algorithm != 0) {
+    unroll = config->unroll;
+    ks = config->k_split;
+  }
+  TMC_REQUIRE((unroll == 1 || unroll == 2 || unroll == 4) && ks >= 1 && ks <= 16,
+              "Packed q.k.v RoPE append: config needs unroll 1|2|4 and k_split 1..16.");
+  RopeArgs ra;
+  ra.cosine = cosine;
+  ra.sine = sine;
+  ra.valid_lengths = valid_lengths;
+  ra.block_tables = block_tables;
+  ra.active_count = active_count;
+  ra.q_out = static_cast<half_t*>(q_out);
+  ra.k_pool = static_cast<half_t*>(key_pool);
+  ra.v_pool = static_cast<half_t*>(value_pool);
+  ra.q_heads = (int)q_heads;
+  ra.kv_heads = (int)kv_heads;
+  ra.head_dim = (int)head_dim;
+  ra.capacity = (int)capacity;
+  ra.page_size = (int)page_size;
+  ra.table_stride = (int)max_pages;
+  const half_t* xs = static_cast<const half_t*>(x);
+  const half_t* w = static_cast<const half_t*>(packed_w);
+  half_t* none = static_cast<half_t*>(q_out);  // not written by the RoPE epilogue
+  const hipStream_t st = as_stream(stream);
+  if (layout & TMC_LAYOUT_X_PACKED)
+    return run_packed<1, half_t, true, false, true>(xs, w, w, none, batch, hidden, n, unroll, ks,
+                                                    st, ra);
+  return run_packed<1, half_t, false, false, true>(xs, w, w, none, batch, hidden, n, unroll, ks, st,
+                                                   ra);
 }
 
 extern "C" int tmc_gate_up_silu_packed_ex_f16(const void* x, const void* packed_gate,

@@ -402,6 +402,37 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     };
     return true;
   }
+  if (name == "qkv_rope_append_packed") {
+    // Batched q.k.v projection over packed weights with RoPE + paged append
+    // in its epilogue: inputs x, packed fused weight, cos, sin,
+    // valid_lengths, block_tables, active; outputs q, key pool, value pool.
+    const int64_t b = param_int(p, "batch"), h = param_int(p, "hidden"),
+                  qh = param_int(p, "q_heads"), kvh = param_int(p, "kv_heads", param_int(p, "q_heads")),
+                  d = param_int(p, "head_dim"), cap = param_int(p, "capacity"),
+                  ps = param_int(p, "page_size");
+    NEED(b > 0 && h > 0 && qh > 0 && kvh > 0 && d > 0 && cap > 0 && ps > 0 && dt == TMC_F16,
+         "qkv_rope_append_packed needs batch, hidden, q_heads, head_dim, capacity, page_size "
+         "and f16.");
+    tmc_gemv_config cfg{};
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    int layout = 0;
+    NEED(layout_param(p, layout) && !(layout & TMC_LAYOUT_Y_PACKED),
+         "qkv_rope_append_packed: x_layout must be row_major or packed, no y_layout.");
+    const int64_t mp = (cap + ps - 1) / ps, n = (qh + 2 * kvh) * d;
+    s.inputs = {TMC_F16, TMC_F16, TMC_F32, TMC_F32, TMC_I32, TMC_I32, TMC_I32};
+    s.outputs = {TMC_F16, TMC_F16, TMC_F16};
+    s.counts = {(size_t)((layout & TMC_LAYOUT_X_PACKED) ? tmc_packed_activation_elements(b, h) : b * h),
+                (size_t)tmc_packed_weight_elements(n, h), (size_t)(cap * (d / 2)),
+                (size_t)(cap * (d / 2)), (size_t)b, (size_t)(b * mp), 1, (size_t)(b * qh * d), 0, 0};
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_qkv_rope_append_packed_f16(
+          c.ptrs[0], c.ptrs[1], static_cast<const float*>(c.ptrs[2]),
+          static_cast<const float*>(c.ptrs[3]), static_cast<const int32_t*>(c.ptrs[4]),
+          static_cast<const int32_t*>(c.ptrs[5]), static_cast<const int32_t*>(c.ptrs[6]), c.ptrs[7],
+          c.ptrs[8], c.ptrs[9], b, h, qh, kvh, d, cap, ps, mp, layout, &cfg, c.stream);
+    };
+    return true;
+  }
   if (name == "gate_up_silu_packed") {
     const int64_t b = param_int(p, "batch"), h = param_int(p, "hidden"), f = param_int(p, "inter");
     NEED(b > 0 && h > 0 && f > 0 && dt == TMC_F16,

@@ -128,4 +128,63 @@ __device__ __forceinline__ void rotate_pair(float even, float odd, float c, floa
   out_odd = __fmaf_rn(even, s, odd * c);
 }
 
+// Epilogue of a q.k.v projection fused with RoPE and the paged K/V append:
+// output features 2i, 2i+1 of a request's projection row are one
+// interleaved RoPE pair of q or k, or two v features.  The pair is rounded
+// to fp16 as the projection output would be, rotated as
+// decode_rope_append_kernel rotates it, and stored where that kernel stores
+// it: q to q_out[request], k and v into the pools at position
+// valid_lengths[request] - 1 through block_tables + request * table_stride.
+// Requests at or past active_count[0], lengths outside [1, capacity] and
+// missing pages are skipped.
+struct RopeArgs {
+  const float* cosine = nullptr;
+  const float* sine = nullptr;
+  const int32_t* valid_lengths = nullptr;
+  const int32_t* block_tables = nullptr;
+  const int32_t* active_count = nullptr;
+  half_t* q_out = nullptr;
+  half_t* k_pool = nullptr;
+  half_t* v_pool = nullptr;
+  int q_heads = 0, kv_heads = 0, head_dim = 0, capacity = 0, page_size = 0, table_stride = 0;
+  int request_base = 0;  // request index of a kernel's first batch row
+};
+
+__device__ __forceinline__ void rope_append_pair(const RopeArgs& ra, int request, int column,
+                                                 float sum_even, float sum_odd) {
+  const int valid = ra.valid_lengths[request];
+  if (request >= ra.active_count[0] || valid <= 0 || valid > ra.capacity) return;
+  const int position = valid - 1;
+  const int d = ra.head_dim, pairs = d / 2;
+  const int q_width = ra.q_heads * d, kv_width = ra.kv_heads * d;
+  const half_t x0 = from_float<half_t>(sum_even), x1 = from_float<half_t>(sum_odd);
+  half_t y0 = x0, y1 = x1;
+  if (column < q_width + kv_width) {
+    const int pair = (column % d) / 2;
+    const float c = ra.cosine[(size_t)position * pairs + pair];
+    const float s = ra.sine[(size_t)position * pairs + pair];
+    float re, ro;
+    rotate_pair(to_float<half_t>(x0), to_float<half_t>(x1), c, s, re, ro);
+    // the fp32 results are rounded once to fp16, as the unfused kernel does
+    asm volatile("" : "+v"(re), "+v"(ro));
+    y0 = from_float<half_t>(re);
+    y1 = from_float<half_t>(ro);
+  }
+  half_t* dst;
+  if (column < q_width) {
+    dst = ra.q_out + (size_t)request * q_width + column;
+  } else {
+    const int page =
+        ra.block_tables[(size_t)request * ra.table_stride + position / ra.page_size];
+    if (page < 0) return;
+    const bool key = column < q_width + kv_width;
+    const int feature = column - q_width - (key ? 0 : kv_width);
+    dst = (key ? ra.k_pool : ra.v_pool) +
+          (((size_t)page * ra.kv_heads + feature / d) * ra.page_size + position % ra.page_size) * d +
+          feature % d;
+  }
+  dst[0] = y0;
+  dst[1] = y1;
+}
+
 }  // namespace tmc

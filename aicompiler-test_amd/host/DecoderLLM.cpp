@@ -440,13 +440,15 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
                                 "&kv_heads=" + std::to_string(KVH) + "&head_dim=" + std::to_string(D) +
                                 "&capacity=" + std::to_string(capacity) +
                                 "&page_size=" + std::to_string(pageSize_);
-    const bool fuseRope = !packed && H % 8 == 0 && D % 2 == 0;
-    const std::string qkvRopeKey = "qkv_rope_append?hidden=" + std::to_string(H) +
-                                   "&q_heads=" + std::to_string(QH) +
-                                   "&kv_heads=" + std::to_string(KVH) +
-                                   "&head_dim=" + std::to_string(D) +
-                                   "&capacity=" + std::to_string(capacity) +
-                                   "&page_size=" + std::to_string(pageSize_);
+    const bool fuseRope = H % 8 == 0 && D % 2 == 0;
+    const std::string ropeShape = "hidden=" + std::to_string(H) + "&q_heads=" + std::to_string(QH) +
+                                  "&kv_heads=" + std::to_string(KVH) +
+                                  "&head_dim=" + std::to_string(D) +
+                                  "&capacity=" + std::to_string(capacity) +
+                                  "&page_size=" + std::to_string(pageSize_);
+    const std::string qkvRopeKey = packed ? "qkv_rope_append_packed?batch=" + B + "&" + ropeShape +
+                                                "&x_layout=packed"
+                                          : "qkv_rope_append?" + ropeShape;
     const std::string attentionKey =
         "paged_attention?max_batch=" + B + "&q_heads=" + std::to_string(QH) +
         "&kv_heads=" + std::to_string(KVH) + "&head_dim=" + std::to_string(D) +
@@ -459,7 +461,8 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
             {residual_, normalized_});
       const auto& pw = weights(l);
       if (fuseRope) {
-        // Batch 1: RoPE and the K/V append run in the projection's epilogue.
+        // RoPE and the K/V append run in the projection's epilogue (the dot
+        // GEMV at batch 1, the packed GEMM above).
         add(qkvRopeKey, p + "qkv_rope_append",
             {normalized_, pw.queryKeyValueWeight, model_->ropeCosine, model_->ropeSine,
              lengthsView_, tableViews_[l], activeView_},

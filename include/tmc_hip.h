@@ -283,6 +283,23 @@ int tmc_gate_up_silu_packed_ex_f16(const void *x, const void *packed_gate, const
                                    void *out, int64_t batch, int64_t hidden, int64_t intermediate,
                                    int layout, const tmc_gemv_config *config, void *stream);
 
+/* Batched decode fusion of the q.k.v projection over fragment-packed
+ * weights (tmc_gemm_packed_ex_f16, same defaults and configs) with
+ * tmc_decode_rope_append: the projection rows are never stored; each output
+ * feature pair of request b is rounded to fp16, rotated (q, k) and written
+ * to q_out [batch, q_heads*head_dim] or into the pools through block_tables
+ * [batch, max_pages] at position valid_lengths[b]-1, with the bits of the
+ * two-kernel sequence.  layout: 0 or TMC_LAYOUT_X_PACKED.  Same skip rules
+ * as tmc_decode_rope_append. */
+int tmc_qkv_rope_append_packed_f16(const void *x, const void *packed_w, const float *cosine,
+                                   const float *sine, const int32_t *valid_lengths,
+                                   const int32_t *block_tables, const int32_t *active_count,
+                                   void *q_out, void *key_pool, void *value_pool, int64_t batch,
+                                   int64_t hidden, int64_t q_heads, int64_t kv_heads,
+                                   int64_t head_dim, int64_t capacity, int64_t page_size,
+                                   int64_t max_pages, int layout, const tmc_gemv_config *config,
+                                   void *stream);
+
 /* emitDecoderRMSNorm (DecoderLLMMetalEmitter.cpp:63-108) / emitRMSNorm
  * (MetalEmitter.cpp:12-76): y = x * rsqrt(mean(x^2) + eps) * w, fp32
  * reduction, dtype TMC_F16 or TMC_F32 for x, w, y. */

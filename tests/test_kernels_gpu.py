@@ -554,6 +554,58 @@ def test_qkv_rope_append_equals_gemv_then_rope_append(tmc, orc, torch, qh, kvh, 
                             config=(1, 1, 4, 4))
 
 
+@pytest.mark.parametrize("batch,layout,cfg_t", [(2, 0, None), (5, 1, None), (16, 1, (3, 1, 1, 4)),
+                                                (17, 1, (3, 1, 4, 1)), (16, 0, (3, 1, 2, 8))])
+def test_qkv_rope_append_packed_equals_gemm_then_rope_append(tmc, orc, torch, batch, layout,
+                                                             cfg_t):
+    """The batched q.k.v projection over packed weights with RoPE and the
+    paged append in its epilogue writes the bits of tmc_gemm_packed_ex_f16
+    (same configuration and x layout) followed by tmc_decode_rope_append:
+    every request's own length and block table, rows past the active count,
+    lengths outside [1, capacity] and missing pages skipped."""
+    qh, kvh, d, hidden, cap, p = 8, 4, 64, 512, 64, 16
+    mp = cap // p
+    cfg = tmc.GemvConfig(*cfg_t) if cfg_t else None
+    pos = np.arange(cap)[:, None]
+    freq = np.exp(np.arange(0, d, 2) * (-np.log(10000.0) / d))
+    cos = dev(np.cos(pos * freq).astype(np.float32))
+    sin = dev(np.sin(pos * freq).astype(np.float32))
+    width = (qh + 2 * kvh) * d
+    xr = orc.f16(normal(551, (batch, hidden)))
+    w = dev_f16(orc.f16(normal(552, (width, hidden), 0.05)))
+    packed = tmc.pack_weights(w)
+    x_rm = dev_f16(xr)
+    x = tmc.pack_activations(x_rm) if layout else x_rm
+    rng = np.random.default_rng(553)
+    pages = batch * mp + 4
+    tables = rng.permutation(pages)[:batch * mp].astype(np.int32).reshape(batch, mp)
+    lengths = rng.integers(1, cap + 1, batch).astype(np.int32)
+    lengths[0] = 0            # outside [1, capacity]
+    lengths[-1] = cap + 1
+    if batch > 2:
+        lengths[1] = 20
+        tables[1, 1] = -1     # missing page for row 1's token
+    active = batch - 1 if batch > 2 else batch
+    pool0 = orc.f16(normal(554, (pages, kvh, p, d)))
+    args = (cos, sin, dev(lengths), dev(tables), torch.tensor([active], dtype=torch.int32,
+                                                               device="cuda"))
+    kp, vp = dev_f16(pool0), dev_f16(pool0.copy())
+    q = torch.full((batch, qh * d), float("nan"), dtype=torch.float16, device="cuda")
+    tmc.qkv_rope_append_packed(x, packed, *args, q, kp, vp, batch, hidden, qh, kvh, d, cap, p, mp,
+                               layout, cfg)
+    qkv = torch.empty((batch, width), dtype=torch.float16, device="cuda")
+    tmc.gemm_packed_ex(x, packed, qkv, batch, hidden, width, layout, cfg)
+    kp2, vp2 = dev_f16(pool0), dev_f16(pool0.copy())
+    q2 = torch.full_like(q, float("nan"))
+    tmc.decode_rope_append(qkv, *args, q2, kp2, vp2, batch, qh, kvh, d, cap, p, mp)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(q), bits(q2))
+    assert np.array_equal(bits(kp), bits(kp2)) and np.array_equal(bits(vp), bits(vp2))
+    assert np.isnan(values(q)[0]).all()
+    if batch > 2:
+        assert not np.isnan(values(q)[2]).all()
+
+
 @pytest.mark.parametrize("cfg_t", QKV_ROPE_CONFIGS + [None])
 def test_norm_qkv_rope_append_equals_norm_then_fused_projection(tmc, orc, torch, cfg_t):
     """The Add+RMSNorm (or RMSNorm) prologue in the q.k.v RoPE append kernel
