@@ -170,20 +170,24 @@ __global__ __launch_bounds__(1024) void packed_gemm_kernel(const half_t* __restr
 int64_t packed_elements(int64_t n, int64_t k) { return ((n + 15) / 16) * 16 * ((k + 31) / 32) * 32; }
 
 // Default (unroll, k_split) per shape from MI355X sweeps at batch 8 and 16
-// with weights beyond the Infinity Cache (K 4096 unless noted): N 32000 and
-// the gated N 11008 pair at batch 16 -> 1 wave per tile; N 12288 -> 2 waves
-// (4 at batch 8); N 4096 (K 4096 and 11008) -> 8 waves.  Wide N streams
-// with few waves per tile; narrow N needs more waves per tile to fill 256 CUs.
+// with weights beyond the Infinity Cache (K 4096 unless noted): N 32000 ->
+// 1 wave per tile; the gated N 11008 pair -> 4 waves (batch 16: 32.9 us
+// against 34.4 with 1); N 12288 -> 2 waves (4 at batch 8); N 4096 (K 4096
+// and 11008) -> 16 waves from batch 8 (o 7.9 against 8.2 us, down 16.0
+// against 16.4 at batch 16), 8 below.  Wide N streams with few waves per
+// tile; narrow N needs more waves per tile to fill 256 CUs.  (Sharing each
+// activation fragment across 2 or 4 output tiles per block measured slower
+// at batch 16: the activation loads do not bound these kernels.)
 void default_packed(int64_t batch, int64_t n, int mats, int& unroll, int& ks) {
   unroll = 2;
   if (mats == 2)
-    ks = batch > 8 ? 1 : 4;
+    ks = 4;
   else if (n >= 16384)
     ks = 1;
   else if (n >= 8192)
     ks = batch > 8 ? 2 : 4;
   else
-    ks = 8;
+    ks = batch >= 8 ? 16 : 8;
 }
 
 template <int MATS, typename OutT, bool XP, bool YP, bool ROPE = false>
