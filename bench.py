@@ -449,6 +449,9 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the chunked prefill measurement and print its JSON (for profiling)")
+    ap.add_argument("--c5-only", action="store_true",
+                    help="run only the C5 decode measurement (batch 1 and 16) and print its JSON "
+                         "(for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -460,6 +463,9 @@ def main() -> int:
     tmc.lib()
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_gpu(tmc)}), flush=True)
+        return 0
+    if args.c5_only:
+        print(json.dumps({"c5_decode": c5_gpu(tmc)}), flush=True)
         return 0
     block = MlpBlock(tmc, torch, args.batch, args.copies)
     # The timed region replays a HIP graph built by the backend's own
