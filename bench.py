@@ -133,7 +133,9 @@ def build_sequences(tmc, rt, block):
     """Prepared executions of the block for every weight copy, captured as one
     HIP-graph sequence, plus a sequence of the gate/up kernel alone."""
     b = block.batch
-    k_norm = rt.resolve(f"add_rmsnorm?rows={b}&width={HIDDEN}&eps=1e-06&dtype=f16")
+    # 512 threads per row: the decoder's batch-1 norm configuration
+    threads = "&threads=512" if b == 1 else ""
+    k_norm = rt.resolve(f"add_rmsnorm?rows={b}&width={HIDDEN}&eps=1e-06&dtype=f16{threads}")
     k_gate = rt.resolve(f"gate_up_silu?batch={b}&hidden={HIDDEN}&inter={INTER}")
     k_down = rt.resolve(f"decode_gemv?batch={b}&in={INTER}&out={HIDDEN}&out_dtype=f32")
     h, r, s, n = rt.wrap(block.h), rt.wrap(block.r), rt.wrap(block.s), rt.wrap(block.n)
