@@ -23,6 +23,8 @@
 #include "tmc_abi.hpp"
 #include "tmc_device.hpp"
 
+#include <climits>
+
 namespace tmc {
 namespace {
 
@@ -512,19 +514,21 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
 
   const int CHUNK = p.chunk;
   const int b = blockIdx.z, kvh = blockIdx.x, split = blockIdx.y;
-  if (PAGED && p.active && b >= p.active[0]) return;
+  // One-split blocks (the whole row, max_pages <= the block's threads): each
+  // thread fetches one block-table entry together with the row's length, so
+  // the K/V addresses wait on one memory round trip instead of two.
+  int early_page = -1;
+  if constexpr (PAGED && WAVES == kWideWaves) {
+    if ((int)threadIdx.x < p.max_pages)
+      early_page = p.tables[(size_t)b * p.max_pages + threadIdx.x];
+  }
+  // the active count and the length are read together (both in bounds)
+  const int active_rows = PAGED && p.active ? p.active[0] : INT_MAX;
   const int valid = valid_length<PAGED>(p, b);
-  if (valid < 1 || valid > p.capacity) return;
-  const int nsplit = (valid + CHUNK - 1) / CHUNK;
-  if (split >= nsplit) return;
-
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int j = lane & 15;
   const int g = lane >> 4;
-  const int begin = split * CHUNK;
-  const int end = min(valid, begin + CHUNK);
-
   const h8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
   h8 qb[4];
   {
@@ -532,16 +536,30 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
 #pragma unroll
     for (int s = 0; s < 4; ++s) qb[s] = j < GROUP ? load_h8(qrow + 8 * (4 * s + g)) : zero;
   }
+  if (b >= active_rows) return;
+  if (valid < 1 || valid > p.capacity) return;
+  const int nsplit = (valid + CHUNK - 1) / CHUNK;
+  if (split >= nsplit) return;
+  const int begin = split * CHUNK;
+  const int end = min(valid, begin + CHUNK);
+
   int page0 = 0;
   bool bad = false;
   if constexpr (PAGED) {
     page0 = page_of(p, begin);
     const int entries = page_of(p, end - 1) - page0 + 1;
     int bad_page = 0;
-    for (int i = threadIdx.x; i < entries; i += WAVES * kWave) {
-      const int page = p.tables[(size_t)b * p.max_pages + page0 + i];
-      s_pages[i] = page;
-      bad_page |= page < 0 || (p.pool_pages > 0 && page >= p.pool_pages);
+    if constexpr (WAVES == kWideWaves) {  // one split: page0 == 0
+      if ((int)threadIdx.x < entries) {
+        s_pages[threadIdx.x] = early_page;
+        bad_page = early_page < 0 || (p.pool_pages > 0 && early_page >= p.pool_pages);
+      }
+    } else {
+      for (int i = threadIdx.x; i < entries; i += WAVES * kWave) {
+        const int page = p.tables[(size_t)b * p.max_pages + page0 + i];
+        s_pages[i] = page;
+        bad_page |= page < 0 || (p.pool_pages > 0 && page >= p.pool_pages);
+      }
     }
     bad = __syncthreads_or(bad_page) != 0;
   }
