@@ -924,7 +924,8 @@ def test_add_rmsnorm_packed_output_bit_exact(tmc, orc, torch, rows):
     gamma = dev_f16(orc.f16(uniform(393, (k,), 0.5, 1.5)))
     s_ref, n_ref = torch.empty((rows, k), dtype=torch.float16, device="cuda"), None
     n_ref = torch.empty_like(s_ref)
-    tmc.add_rmsnorm(r, h, gamma, s_ref, n_ref, 1e-6)
+    # width 4096 writes the packed rows with the 512-thread kernel
+    tmc.add_rmsnorm_threads(r, h, gamma, s_ref, n_ref, 1e-6, 512)
     s_out = torch.empty_like(s_ref)
     n_packed = torch.empty(tmc.packed_activation_elements(rows, k), dtype=torch.float16,
                            device="cuda")
@@ -932,7 +933,7 @@ def test_add_rmsnorm_packed_output_bit_exact(tmc, orc, torch, rows):
     n_only = torch.empty_like(n_packed)
     tmc.add_rmsnorm_ex(r, None, gamma, None, n_only, 1e-6, tmc.Y_PACKED)
     plain = torch.empty_like(s_ref)
-    tmc.rmsnorm(r, gamma, plain, 1e-6)
+    tmc.rmsnorm_threads(r, gamma, plain, 1e-6, 512)
     torch.cuda.synchronize()
     live = _unwritten_mask(rows, k)
     assert np.array_equal(bits(s_out), bits(s_ref))
