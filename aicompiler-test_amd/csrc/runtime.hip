@@ -1039,6 +1039,11 @@ extern "C" int tmc_buf_write_raw_async(tmc_buffer* buf, const void* data, size_t
   if (!buf || !data || count == 0 || offset > buf->count || count > buf->count - offset)
     return fail("tmc_buf_write_raw_async: invalid range.");
   tmc_runtime* rt = buf->rt;
+  // a captured copy would replay whatever the staging slot holds later
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(rt->stream, &capture) == hipSuccess &&
+      capture != hipStreamCaptureStatusNone)
+    return fail("tmc_buf_write_raw_async: not allowed while the runtime stream is captured.");
   const size_t bytes = count * element_bytes(buf->dtype);
   const size_t slot = (bytes + 255) / 256 * 256;
   if (slot > kStagingBytes) return tmc_buf_write_raw(buf, data, count, offset);

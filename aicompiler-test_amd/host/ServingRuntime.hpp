@@ -153,8 +153,10 @@ struct DecodeThroughput {
   std::size_t prefillChunkSize = 0;    // 0: prompts ran one token per batched step
   double decodePhaseUs = 0.0;      // host wall time of the timed steps
   double tokensPerSecond = 0.0;    // rows * decodeSteps / decodePhaseUs
-  benchmark::Statistics stepGpu;   // per timed step, HIP-event time
-  benchmark::Statistics stepHost;  // per timed step, host wall time
+  benchmark::Statistics stepGpu;   // per timed step, HIP-event time (timeGpu only)
+  // per timed step, host wall time: the whole step with timeGpu, else the
+  // enqueue time of a chained step (the GPU runs behind the host)
+  benchmark::Statistics stepHost;
   std::vector<std::vector<float>> generatedTokenIds;  // per row
   std::size_t kvBytesRead = 0;     // K/V bytes the timed attention steps read
   std::string errorMessage;

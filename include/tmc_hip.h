@@ -89,7 +89,8 @@ int tmc_buf_read_raw(const tmc_buffer *buf, void *data, size_t count, size_t off
  * stream, ordered before later launches on it; the caller may reuse `data`
  * on return.  No counterpart in the reference (its writes are synchronous):
  * it is for per-step metadata uploads that precede a graph launch.  Copies
- * larger than the staging area (4 MiB) fall back to tmc_buf_write_raw. */
+ * larger than the staging area (4 MiB) fall back to tmc_buf_write_raw.
+ * Refused while the runtime stream is being captured. */
 int tmc_buf_write_raw_async(tmc_buffer *buf, const void *data, size_t count, size_t offset);
 /* Device-to-device copy of `count` elements (same dtype, same runtime),
  * queued on the runtime stream.  No counterpart in the reference: the
