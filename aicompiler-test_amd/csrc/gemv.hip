@@ -133,8 +133,7 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const half_t* __restrict_
   const int part = wave % KS;
   // PRO > 0: the grid is capped (launch_dot), so a block loops over row
   // groups and builds the normalized row once; otherwise one pass.
-  for (int grp = blockIdx.x; grp * kGroups * RPW < n_out;
-       grp += PRO > 0 ? (int)gridDim.x : n_out) {
+  for (int grp = blockIdx.x; grp * kGroups * RPW < n_out; grp += (int)gridDim.x) {
     const int row0 = (grp * kGroups + group) * RPW;
     const bool live = row0 < n_out;  // wave-uniform; dead waves still meet the barrier
     const int chunks = k_in >> 3;
@@ -237,8 +236,9 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const half_t* __restrict_
         }
       }
     }
+    if constexpr (PRO == 0) break;  // the grid covers every row group
     // the next group's partials reuse the LDS slots read above
-    if constexpr (KS > 1 && PRO > 0) __syncthreads();
+    if constexpr (KS > 1) __syncthreads();
   }
 }
 
