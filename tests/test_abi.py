@@ -45,6 +45,28 @@ def test_argument_validation_fails_before_device_work(tmc):
     assert "head_dim" in tmc.last_error()
     with pytest.raises(tmc.TmcError):
         tmc.check(lib.tmc_silu_mul(None, None, None, 0, 4, None), "silu")
+    # the decode-step fusions and the staged / device copies
+    p = C.c_void_p(16)
+    assert lib.tmc_qkv_rope_append_f16(None, p, p, p, p, p, p, p, p, p, 64, 2, 1, 16, 32, 16, None,
+                                       None) != 0
+    assert "null" in tmc.last_error()
+    assert lib.tmc_qkv_rope_append_f16(p, p, p, p, p, p, p, p, p, p, 64, 3, 2, 16, 32, 16, None,
+                                       None) != 0
+    assert "head geometry" in tmc.last_error()
+    bad_cfg = tmc.GemvConfig(1, 1, 4, 4)  # the RoPE epilogue needs two rows per wave
+    assert lib.tmc_qkv_rope_append_f16(p, p, p, p, p, p, p, p, p, p, 64, 2, 1, 16, 32, 16,
+                                       C.byref(bad_cfg), None) != 0
+    assert "rows_per_wave 2" in tmc.last_error()
+    assert lib.tmc_qkv_rope_append_packed_f16(p, p, p, p, p, p, p, p, p, p, 4, 64, 2, 1, 16, 32, 16,
+                                              2, tmc.Y_PACKED, None, None) != 0
+    assert "layout" in tmc.last_error()
+    assert lib.tmc_add_rmsnorm_qkv_rope_append_f16(p, p, p, p, None, p, p, p, p, p, p, p, p, 64, 2,
+                                                   1, 16, 32, 16, 1e-6, None, None) != 0
+    assert "null" in tmc.last_error()
+    assert lib.tmc_buf_write_raw_async(None, p, 1, 0) != 0
+    assert "invalid range" in tmc.last_error()
+    assert lib.tmc_buf_copy_async(None, 0, None, 0, 1) != 0
+    assert "different runtimes" in tmc.last_error()
 
 
 def test_attention_workspace_sizes(tmc):
