@@ -112,6 +112,8 @@ def _declare(l):
         "tmc_buf_dtype": (i32, [vp]),
         "tmc_buf_device_ptr": (vp, [vp]),
         "tmc_buf_release": (None, [vp]),
+        "tmc_host_encode": (i32, [vp, sz, i32, vp]),
+        "tmc_host_decode": (i32, [vp, sz, i32, vp]),
         "tmc_kernel_resolve": (i32, [vp, C.c_char_p, C.POINTER(vp), C.POINTER(i32), vp, vp]),
         "tmc_kernel_dispatch": (i32, [vp, C.POINTER(sz), C.POINTER(sz)]),
         "tmc_kernel_release": (None, [vp]),
@@ -583,6 +585,29 @@ def fill_normal(t, seed, mean=0.0, std=1.0, stream=None):
 
 def copy_bytes(src, dst, nbytes, stream=None):
     check(lib().tmc_copy_bytes(_ptr(src), _ptr(dst), nbytes, _stream(stream)), "tmc_copy_bytes")
+
+
+# ---------------------------------------------------------------- host conversions
+def host_encode(values, dtype: int):
+    """fp32 -> storage bits with the runtime's upload rule (tmc_host_encode)."""
+    import numpy as np
+    src = np.ascontiguousarray(values, dtype=np.float32)
+    out = np.empty(src.shape, dtype={F16: np.uint16, BF16: np.uint16, F32: np.float32,
+                                     I32: np.int32}[dtype])
+    check(lib().tmc_host_encode(src.ctypes.data_as(C.c_void_p), src.size, dtype,
+                                out.ctypes.data_as(C.c_void_p)), "tmc_host_encode")
+    return out
+
+
+def host_decode(bits, dtype: int):
+    """Storage bits -> fp32 with the runtime's readback rule (tmc_host_decode)."""
+    import numpy as np
+    src = np.ascontiguousarray(bits, dtype={F16: np.uint16, BF16: np.uint16, F32: np.float32,
+                                            I32: np.int32}[dtype])
+    out = np.empty(src.shape, dtype=np.float32)
+    check(lib().tmc_host_decode(src.ctypes.data_as(C.c_void_p), src.size, dtype,
+                                out.ctypes.data_as(C.c_void_p)), "tmc_host_decode")
+    return out
 
 
 # ---------------------------------------------------------------- runtime objects

@@ -354,9 +354,11 @@ extern "C" int tmc_qkv_rope_append_packed_f16(
               "Packed q.k.v RoPE append: hidden must be a positive multiple of 8 and x, W "
               "16-byte aligned.");
   TMC_REQUIRE(q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 && head_dim > 0 &&
-                  head_dim % 2 == 0 && capacity > 0 && page_size > 0 && max_pages > 0 &&
-                  max_pages < (1LL << 31) && (q_heads + 2 * kv_heads) * head_dim < (1LL << 31),
-              "Packed q.k.v RoPE append: invalid head geometry, capacity or pages.");
+                  head_dim % 2 == 0 && capacity > 0 && capacity < (1LL << 31) && page_size > 0 &&
+                  page_size <= capacity && max_pages == (capacity + page_size - 1) / page_size &&
+                  (q_heads + 2 * kv_heads) * head_dim < (1LL << 31),
+              "Packed q.k.v RoPE append: invalid head geometry or capacity (max_pages must be "
+              "ceil(capacity / page_size)).");
   const int64_t n = (q_heads + 2 * kv_heads) * head_dim;
   TMC_REQUIRE((uint64_t)packed_elements(n, hidden) * 2 < kNone && (uint64_t)16 * hidden * 2 < kNone,
               "Packed q.k.v RoPE append: operands exceed the 4 GiB buffer range.");

@@ -48,62 +48,57 @@ int check_launch(const char* what) {
 namespace {
 
 // ------------------------------------------------------------------ host conversions
-uint16_t host_f32_to_f16(float value) {
-  uint32_t bits;
-  std::memcpy(&bits, &value, sizeof bits);
-  const uint32_t sign = (bits >> 16) & 0x8000u;
-  const uint32_t biased = (bits >> 23) & 0xffu;
-  const uint32_t fraction = bits & 0x7fffffu;
-  if (biased == 0xffu) return (uint16_t)(sign | (fraction ? 0x7e00u : 0x7c00u));
-  const int exponent = (int)biased - 112;
-  if (exponent >= 31) return (uint16_t)(sign | 0x7c00u);
-  if (exponent <= 0) {
-    if (exponent < -10) return (uint16_t)sign;
-    const uint32_t significand = fraction | 0x800000u;
-    const int shift = 14 - exponent;
-    return (uint16_t)(sign | ((significand + (1u << (shift - 1))) >> shift));
+// The upload/readback rules of MetalRuntime.mm:42-104: fp32 -> fp16 rounds
+// to nearest with ties away from zero (NaN -> 0x7e00 with its sign, overflow
+// -> inf), fp32 -> bf16 rounds to nearest even on the raw bits, int32 is a
+// truncating cast.  The fp16 rounding is done arithmetically: the magnitude
+// is scaled (exactly, in double) so that one fp16 step is 1, rounded with
+// floor(x + 0.5), and the step count is reassembled into the bit fields.
+uint16_t f16_bits(float value) {
+  const uint16_t sign = std::signbit(value) ? 0x8000u : 0u;
+  if (std::isnan(value)) return sign | 0x7e00u;
+  const double magnitude = std::fabs((double)value);
+  // 65520 is halfway between the largest fp16 (65504) and the next step.
+  if (magnitude >= 65520.0) return sign | 0x7c00u;
+  if (magnitude < 0x1p-14) {
+    // subnormal steps of 2^-24; 1024 steps carry into the smallest normal
+    return sign | (uint16_t)std::floor(std::ldexp(magnitude, 24) + 0.5);
   }
-  const uint32_t rounded = fraction + 0x1000u;
-  if (rounded & 0x800000u) {
-    if (exponent + 1 >= 31) return (uint16_t)(sign | 0x7c00u);
-    return (uint16_t)(sign | ((uint32_t)(exponent + 1) << 10));
+  int binary_exponent;
+  std::frexp(magnitude, &binary_exponent);  // magnitude in [2^(e-1), 2^e)
+  int exponent = binary_exponent - 1;
+  double steps = std::floor(std::ldexp(magnitude, 10 - exponent) + 0.5);  // [1024, 2048]
+  if (steps == 2048.0) {
+    steps = 1024.0;
+    ++exponent;
   }
-  return (uint16_t)(sign | ((uint32_t)exponent << 10) | (rounded >> 13));
+  return sign | (uint16_t)((exponent + 15) << 10) | (uint16_t)(steps - 1024.0);
 }
 
-float host_f16_to_f32(uint16_t half) {
-  const uint32_t sign = (uint32_t)(half & 0x8000u) << 16;
-  uint32_t exponent = (half >> 10) & 0x1fu;
-  uint32_t mantissa = half & 0x3ffu;
-  uint32_t bits;
-  if (exponent == 0) {
-    if (mantissa == 0) {
-      bits = sign;
-    } else {
-      int shift = 0;
-      while ((mantissa & 0x400u) == 0) {
-        mantissa <<= 1;
-        ++shift;
-      }
-      bits = sign | ((uint32_t)(113 - shift) << 23) | ((mantissa & 0x3ffu) << 13);
-    }
-  } else if (exponent == 31) {
-    bits = sign | 0x7f800000u | (mantissa << 13);
+float f16_value(uint16_t half) {
+  const unsigned exponent = (half >> 10) & 0x1fu, mantissa = half & 0x3ffu;
+  float magnitude;
+  if (exponent == 31) {
+    const uint32_t bits = 0x7f800000u | (mantissa << 13);  // inf, or NaN keeping its payload
+    std::memcpy(&magnitude, &bits, sizeof magnitude);
+  } else if (exponent == 0) {
+    magnitude = (float)std::ldexp((double)mantissa, -24);
   } else {
-    bits = sign | ((exponent + 112) << 23) | (mantissa << 13);
+    magnitude = (float)std::ldexp((double)(1024u + mantissa), (int)exponent - 25);
   }
-  float out;
-  std::memcpy(&out, &bits, sizeof out);
-  return out;
+  return std::copysign(magnitude, (half & 0x8000u) ? -1.0f : 1.0f);
 }
 
-uint16_t host_f32_to_bf16(float value) {
+uint16_t bf16_bits(float value) {
   uint32_t bits;
   std::memcpy(&bits, &value, sizeof bits);
-  return (uint16_t)((bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16);
+  uint32_t upper = bits >> 16;
+  const uint32_t lower = bits & 0xffffu;
+  if (lower > 0x8000u || (lower == 0x8000u && (upper & 1u))) ++upper;  // nearest, ties to even
+  return (uint16_t)upper;
 }
 
-float host_bf16_to_f32(uint16_t v) {
+float bf16_value(uint16_t v) {
   const uint32_t bits = (uint32_t)v << 16;
   float out;
   std::memcpy(&out, &bits, sizeof out);
@@ -113,16 +108,31 @@ float host_bf16_to_f32(uint16_t v) {
 size_t element_bytes(int dtype) { return dtype == TMC_F16 || dtype == TMC_BF16 ? 2 : 4; }
 bool valid_dtype(int dtype) { return dtype >= TMC_F16 && dtype <= TMC_I32; }
 
-std::vector<uint8_t> encode(const float* src, size_t count, int dtype) {
-  std::vector<uint8_t> out(count * element_bytes(dtype));
+void encode_into(const float* src, size_t count, int dtype, void* dst) {
   for (size_t i = 0; i < count; ++i) {
     switch (dtype) {
-    case TMC_F16: reinterpret_cast<uint16_t*>(out.data())[i] = host_f32_to_f16(src[i]); break;
-    case TMC_BF16: reinterpret_cast<uint16_t*>(out.data())[i] = host_f32_to_bf16(src[i]); break;
-    case TMC_I32: reinterpret_cast<int32_t*>(out.data())[i] = (int32_t)src[i]; break;
-    default: reinterpret_cast<float*>(out.data())[i] = src[i]; break;
+    case TMC_F16: static_cast<uint16_t*>(dst)[i] = f16_bits(src[i]); break;
+    case TMC_BF16: static_cast<uint16_t*>(dst)[i] = bf16_bits(src[i]); break;
+    case TMC_I32: static_cast<int32_t*>(dst)[i] = (int32_t)src[i]; break;
+    default: static_cast<float*>(dst)[i] = src[i]; break;
     }
   }
+}
+
+void decode_into(const void* src, size_t count, int dtype, float* dst) {
+  for (size_t i = 0; i < count; ++i) {
+    switch (dtype) {
+    case TMC_F16: dst[i] = f16_value(static_cast<const uint16_t*>(src)[i]); break;
+    case TMC_BF16: dst[i] = bf16_value(static_cast<const uint16_t*>(src)[i]); break;
+    case TMC_I32: dst[i] = (float)static_cast<const int32_t*>(src)[i]; break;
+    default: dst[i] = static_cast<const float*>(src)[i]; break;
+    }
+  }
+}
+
+std::vector<uint8_t> encode(const float* src, size_t count, int dtype) {
+  std::vector<uint8_t> out(count * element_bytes(dtype));
+  encode_into(src, count, dtype, out.data());
   return out;
 }
 
@@ -1111,14 +1121,23 @@ extern "C" int tmc_buf_read(const tmc_buffer* buf, float* out) {
   if (!buf || !out) return fail("tmc_buf_read: null argument.");
   std::vector<uint8_t> host(buf->count * element_bytes(buf->dtype));
   if (tmc_buf_read_raw(buf, host.data(), buf->count, 0)) return 1;
-  for (size_t i = 0; i < buf->count; ++i) {
-    switch (buf->dtype) {
-    case TMC_F16: out[i] = host_f16_to_f32(reinterpret_cast<uint16_t*>(host.data())[i]); break;
-    case TMC_BF16: out[i] = host_bf16_to_f32(reinterpret_cast<uint16_t*>(host.data())[i]); break;
-    case TMC_I32: out[i] = (float)reinterpret_cast<int32_t*>(host.data())[i]; break;
-    default: out[i] = reinterpret_cast<float*>(host.data())[i]; break;
-    }
-  }
+  decode_into(host.data(), buf->count, buf->dtype, out);
+  return 0;
+}
+
+extern "C" int tmc_host_encode(const float* src, size_t count, int dtype, void* dst) {
+  clear_error();
+  if (!valid_dtype(dtype)) return fail("tmc_host_encode: unknown dtype.");
+  if (count && (!src || !dst)) return fail("tmc_host_encode: null argument.");
+  encode_into(src, count, dtype, dst);
+  return 0;
+}
+
+extern "C" int tmc_host_decode(const void* src, size_t count, int dtype, float* dst) {
+  clear_error();
+  if (!valid_dtype(dtype)) return fail("tmc_host_decode: unknown dtype.");
+  if (count && (!src || !dst)) return fail("tmc_host_decode: null argument.");
+  decode_into(src, count, dtype, dst);
   return 0;
 }
 

@@ -83,26 +83,8 @@ void KVCachePlan::validate() const {
 namespace runtime {
 
 float halfToFloat(std::uint16_t bits) noexcept {
-  const std::uint32_t sign = static_cast<std::uint32_t>(bits & 0x8000u) << 16;
-  std::uint32_t exponent = (bits >> 10) & 0x1fu;
-  std::uint32_t mantissa = bits & 0x3ffu;
-  std::uint32_t out;
-  if (exponent == 0x1f) {
-    out = sign | 0x7f800000u | (mantissa << 13);
-  } else if (exponent != 0) {
-    out = sign | ((exponent + 112u) << 23) | (mantissa << 13);
-  } else if (mantissa == 0) {
-    out = sign;
-  } else {  // subnormal: normalise
-    exponent = 113;
-    while ((mantissa & 0x400u) == 0) {
-      mantissa <<= 1;
-      --exponent;
-    }
-    out = sign | (exponent << 23) | ((mantissa & 0x3ffu) << 13);
-  }
-  float value;
-  std::memcpy(&value, &out, sizeof value);
+  float value = 0.0f;
+  tmc_host_decode(&bits, 1, TMC_F16, &value);
   return value;
 }
 

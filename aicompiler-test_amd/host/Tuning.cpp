@@ -1,5 +1,7 @@
 #include "Tuning.hpp"
 
+#include "tmc_hip.h"
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -189,22 +191,15 @@ namespace {
 
 constexpr std::size_t kMaximumCpuReferenceOperations = 64u * 1024u * 1024u;
 
-// fp32 -> fp16 -> fp32 with ties away from zero, the runtime's upload
-// conversion (MetalRuntime.mm:42-104), so the CPU reference sees the stored
+// The value a float takes once uploaded as fp16 (the runtime's own upload
+// conversion, ties away from zero), so the CPU reference sees the stored
 // values.
 float roundHalf(float value) {
-  std::uint32_t bits;
-  std::memcpy(&bits, &value, sizeof(bits));
-  const std::uint32_t sign = bits & 0x80000000u;
-  const float magnitude = std::fabs(value);
-  if (!std::isfinite(value)) return value;
-  if (magnitude >= 65520.0f) return sign ? -INFINITY : INFINITY;
-  int exponent;
-  std::frexp(magnitude, &exponent);  // magnitude = m * 2^exponent, m in [0.5, 1)
-  const int e = std::max(exponent - 1, -14);
-  const double quantum = std::ldexp(1.0, e - 10);
-  const double q = std::floor(magnitude / quantum + 0.5) * quantum;  // ties away
-  return sign ? -static_cast<float>(q) : static_cast<float>(q);
+  std::uint16_t bits = 0;
+  tmc_host_encode(&value, 1, TMC_F16, &bits);
+  float stored = 0.0f;
+  tmc_host_decode(&bits, 1, TMC_F16, &stored);
+  return stored;
 }
 
 std::vector<double> gemvReference(std::size_t batch, std::size_t in, std::size_t out,

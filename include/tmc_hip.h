@@ -18,6 +18,14 @@
  *     pointers, shapes and a hipStream_t passed as `void *stream` (NULL =
  *     the default stream) and enqueue asynchronously.
  *
+ * Paged K/V writes (every *append* entry point and the q.k.v projections
+ * with a RoPE + append epilogue) skip a block-table entry < 0 and trust
+ * every other entry: the caller guarantees that each page id it stores in a
+ * block table is below the number of pages of the pool it passes (the
+ * KVPagePool / KVCacheState host layer only stores ids it allocated).  The
+ * paged attention reads take `pool_pages` and treat an id past it as
+ * missing, so a stale table can spoil reads but never read out of bounds.
+ *
  * Storage dtype codes follow tensor::metal::ElementType (MetalRuntime.hpp:12).
  * Weights are [out_features, in_features] row-major (nn.Linear layout, as in
  * DecodeGEMVMetalEmitter.cpp:97-103).
@@ -104,6 +112,16 @@ size_t tmc_buf_count(const tmc_buffer *buf);
 int tmc_buf_dtype(const tmc_buffer *buf);
 void *tmc_buf_device_ptr(const tmc_buffer *buf);
 void tmc_buf_release(tmc_buffer *buf);
+
+/* The host conversions behind tmc_buf_create / tmc_buf_write / tmc_buf_read,
+ * on host memory only (no device, no runtime): the reference's floatToHalf /
+ * halfToFloat / floatToBFloat16 / bfloat16ToFloat (MetalRuntime.mm:42-104)
+ * and its int32 truncating cast (.mm:545-547,585-589).  fp32 -> fp16 rounds
+ * to nearest with ties away from zero, NaN -> 0x7e00 with its sign, overflow
+ * -> inf; fp32 -> bf16 rounds to nearest even on the raw bits.  dst holds
+ * `count` elements of the storage dtype (encode) or floats (decode). */
+int tmc_host_encode(const float *src, size_t count, int dtype, void *dst);
+int tmc_host_decode(const void *src, size_t count, int dtype, float *dst);
 
 /* Replaces MetalRuntime::createComputePipeline(source, functionName)
  * (MetalRuntime.hpp:168-170; .mm:397-513).  `key` names a built-in gfx950

@@ -67,8 +67,9 @@ def _declare(l):
     l.tmco_append_contiguous.argtypes = [vp, sz, sz, sz, sz, sz, C.c_int, C.c_int32, vp]
     l.tmco_append_paged.argtypes = [vp, sz, sz, sz, sz, sz, sz, C.c_int, C.c_int32, vp, vp]
     l.tmco_append_serving.argtypes = [vp, sz, sz, sz, sz, sz, C.c_int, vp, vp, C.c_int32, vp]
+    l.tmco_set_threads.argtypes = [C.c_int]
     l.tmco_decoder_step.restype = C.c_int
-    l.tmco_decoder_step.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp, sz, sz, vp, vp]
+    l.tmco_decoder_step.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp, sz, sz, sz, vp, vp]
 
 
 # ---------------------------------------------------------------- conversions
@@ -276,8 +277,14 @@ class _Model(C.Structure):
                 ("layer", C.POINTER(_Layer))]
 
 
+def set_threads(threads: int) -> None:
+    """Threads of decoder_step (default 1); results do not depend on it."""
+    lib().tmco_set_threads(int(threads))
+
+
 def decoder_step(weights: dict, cfg: dict, key_pools, value_pools, page_size: int,
-                 max_pages: int, block_tables, tokens, valid_lengths, layer_limit: int = 0):
+                 max_pages: int, block_tables, tokens, valid_lengths, layer_limit: int = 0,
+                 logits_from: int = 0):
     """One decode step (tmco_decoder_step).  ``weights`` holds fp16 bit arrays:
     embedding, final_norm, lm_head, rope_cos/rope_sin (fp32) and ``layers`` (a
     list of dicts with input_norm, wq, wk, wv, wo, post_norm, wg, wu, wd).
@@ -310,7 +317,7 @@ def decoder_step(weights: dict, cfg: dict, key_pools, value_pools, page_size: in
     logits = np.zeros((batch, cfg["vocabulary"]), dtype=np.float32)
     nxt = np.zeros(batch, dtype=np.int32)
     rc = lib().tmco_decoder_step(C.byref(m), kp, vp, page_size, max_pages, _p(bt), _p(tk), _p(vl),
-                                 batch, layer_limit, _p(logits), _p(nxt))
+                                 batch, layer_limit, logits_from, _p(logits), _p(nxt))
     if rc != 0:
         raise ValueError(f"tmco_decoder_step failed with {rc}")
     return logits, nxt

@@ -524,20 +524,98 @@ static void store_array(const double *src, size_t count, float *dst) {
   for (size_t i = 0; i < count; ++i) dst[i] = tmco_store(src[i], TMCO_F16);
 }
 
-/* y[r,n] = sum_k x[r,k]*W[n,k] with x already float (storage values) and W
- * fp16 bits; double accumulation in k order. */
-static void linear_f16(const float *x, const uint16_t *w, size_t rows, size_t in_features,
-                       size_t out_features, double *y, float *row) {
-  for (size_t n = 0; n < out_features; ++n) {
-    const uint16_t *src = w + n * in_features;
-    for (size_t k = 0; k < in_features; ++k) row[k] = g_half_table[src[k]];
-    for (size_t r = 0; r < rows; ++r) {
-      const float *xr = x + r * in_features;
-      double sum = 0.0;
-      for (size_t k = 0; k < in_features; ++k) sum += (double)xr[k] * (double)row[k];
-      y[r * out_features + n] = sum;
+/* Threads of the decode-step composition (tmco_set_threads; 1 by default,
+ * so the CPU baseline stays single-threaded).  Work is split over output
+ * features and heads only: every sum keeps its own order, so the results do
+ * not depend on the thread count. */
+static int g_threads = 1;
+
+void tmco_set_threads(int threads) { g_threads = threads > 0 ? threads : 1; }
+
+/* Sixteen rows against two weight rows: the inputs are k-major
+ * (xt[k*16 + j] = x[row j][k], storage values as float) and every
+ * (row, weight row) pair keeps its own double sum in k order, so a
+ * vectorised build computes exactly the scalar sums. */
+__attribute__((target_clones("avx512f", "avx2", "default")))
+static void dot16x2(const float *xt, const float *w0, const float *w1, size_t in_features,
+                    double *sums0, double *sums1) {
+  double s0[16] = {0.0}, s1[16] = {0.0};
+  for (size_t k = 0; k < in_features; ++k) {
+    const double a = (double)w0[k], b = (double)w1[k];
+    const float *xk = xt + k * 16;
+    for (int j = 0; j < 16; ++j) {
+      const double xv = (double)xk[j];
+      s0[j] += xv * a;
+      s1[j] += xv * b;
     }
   }
+  for (int j = 0; j < 16; ++j) {
+    sums0[j] = s0[j];
+    sums1[j] = s1[j];
+  }
+}
+
+/* y[r,n] = sum_k x[r,k]*W[n,k] with x already float (storage values) and W
+ * fp16 bits; double accumulation in k order for every (r, n).  Rows go in
+ * blocks of 16 through dot16x2 (two output features at a time), a few
+ * blocks per pass over the weights so that their inputs stay in cache; the
+ * last rows % 16 go one at a time. */
+static void linear_f16(const float *x, const uint16_t *w, size_t rows, size_t in_features,
+                       size_t out_features, double *y) {
+  enum { kBlocksPerPass = 4 };
+  const size_t blocks = rows / 16;
+  const size_t passes = (blocks + kBlocksPerPass - 1) / kBlocksPerPass + (rows % 16 ? 1 : 0);
+  float *xt = NULL;
+  if (blocks) {
+    xt = (float *)malloc(blocks * in_features * 16 * sizeof(float));
+    if (!xt) abort();
+    for (size_t b = 0; b < blocks; ++b)
+      for (size_t k = 0; k < in_features; ++k)
+        for (size_t j = 0; j < 16; ++j)
+          xt[(b * in_features + k) * 16 + j] = x[(b * 16 + j) * in_features + k];
+  }
+  const size_t pairs = (out_features + 1) / 2;
+#pragma omp parallel num_threads(g_threads) if (g_threads > 1)
+  {
+    float *row = (float *)malloc(2 * in_features * sizeof(float));
+    if (!row) abort();
+    for (size_t pass = 0; pass < passes; ++pass) {
+      const size_t b0 = pass * kBlocksPerPass;
+      const size_t b1 = b0 + kBlocksPerPass < blocks ? b0 + kBlocksPerPass : blocks;
+      const int tail = b0 >= blocks; /* the pass over the last rows % 16 */
+#pragma omp for schedule(static)
+      for (size_t pair = 0; pair < pairs; ++pair) {
+        const size_t n0 = 2 * pair, count = n0 + 1 < out_features ? 2 : 1;
+        for (size_t i = 0; i < count; ++i) {
+          const uint16_t *src = w + (n0 + i) * in_features;
+          for (size_t k = 0; k < in_features; ++k) row[i * in_features + k] = g_half_table[src[k]];
+        }
+        if (tail) {
+          for (size_t i = 0; i < count; ++i) {
+            const float *wr = row + i * in_features;
+            for (size_t r = blocks * 16; r < rows; ++r) {
+              const float *xr = x + r * in_features;
+              double sum = 0.0;
+              for (size_t k = 0; k < in_features; ++k) sum += (double)xr[k] * (double)wr[k];
+              y[r * out_features + n0 + i] = sum;
+            }
+          }
+          continue;
+        }
+        const float *w1 = row + (count - 1) * in_features;
+        double sums0[16], sums1[16];
+        for (size_t b = b0; b < b1; ++b) {
+          dot16x2(xt + b * in_features * 16, row, w1, in_features, sums0, sums1);
+          for (size_t j = 0; j < 16; ++j) {
+            y[(b * 16 + j) * out_features + n0] = sums0[j];
+            if (count == 2) y[(b * 16 + j) * out_features + n0 + 1] = sums1[j];
+          }
+        }
+      }
+    }
+    free(row);
+  }
+  free(xt);
 }
 
 static void rmsnorm_f16(const float *x, const uint16_t *w, size_t rows, size_t width,
@@ -554,21 +632,26 @@ static void rmsnorm_f16(const float *x, const uint16_t *w, size_t rows, size_t w
 /* One decode step of the decoder kernel sequence (DecoderLLMExecutor.cpp:
  * 322-849; ServingRuntime.cpp:233-407): every kernel output is stored in fp16
  * (storeValue) before the next kernel reads it; logits are returned as fp32.
- * Pinned: composition of the pinned op oracles; tests compare it with an
- * independent torch float64 model at small shapes. */
+ * Pinned: composition of the pinned op oracles (tests/test_oracle_decoder.py
+ * rebuilds the step from the separately pinned ops and requires identical
+ * logits and pool bits). */
 int tmco_decoder_step(const tmco_model *m, uint16_t *const *key_pools,
                       uint16_t *const *value_pools, size_t page_size, size_t max_pages,
                       const int32_t *block_tables, const int32_t *tokens,
                       const int32_t *valid_lengths, size_t batch, size_t layer_limit,
-                      float *logits, int32_t *next_tokens) {
+                      size_t logits_from, float *logits, int32_t *next_tokens) {
   half_table_init();
   const size_t H = m->hidden, D = m->head_dim, NH = m->heads, I = m->intermediate;
   const size_t KVH = m->kv_heads ? m->kv_heads : NH, KV = KVH * D, group = NH / KVH;
   const size_t pairs = D / 2;
   if (KVH == 0 || NH % KVH != 0) return -3;
   const size_t layers = layer_limit && layer_limit < m->layers ? layer_limit : m->layers;
-  const size_t widest = (I > m->vocabulary ? I : m->vocabulary) > H
-                            ? (I > m->vocabulary ? I : m->vocabulary) : H;
+  /* acc holds one layer's widest output for every row, or the LM head's
+   * logits for the rows from logits_from on. */
+  const size_t layer_width = I > H ? I : H;
+  const size_t head_rows = logits_from < batch ? batch - logits_from : 0;
+  const size_t acc_size = batch * layer_width > head_rows * m->vocabulary
+                              ? batch * layer_width : head_rows * m->vocabulary;
   for (size_t b = 0; b < batch; ++b) {
     if (tokens[b] < 0 || (size_t)tokens[b] >= m->vocabulary) return -1;
     if (valid_lengths[b] <= 0 || (size_t)valid_lengths[b] > m->capacity) return -2;
@@ -581,16 +664,9 @@ int tmco_decoder_step(const tmco_model *m, uint16_t *const *key_pools,
   float *ctx = (float *)malloc(batch * H * sizeof(float));
   float *after = (float *)malloc(batch * H * sizeof(float));
   float *gated = (float *)malloc(batch * I * sizeof(float));
-  double *acc = (double *)malloc(batch * widest * sizeof(double));
+  double *acc = (double *)malloc(acc_size * sizeof(double));
   double *acc2 = (double *)malloc(batch * I * sizeof(double));
-  float *row = (float *)malloc(widest * sizeof(float));
-  float *keys = (float *)malloc(m->capacity * D * sizeof(float));
-  float *vals = (float *)malloc(m->capacity * D * sizeof(float));
-  double *scores = (double *)malloc((m->capacity + 1) * sizeof(double));
-  double *head_out = (double *)malloc(D * sizeof(double));
-  if (!cur || !nrm || !q || !k || !v || !ctx || !after || !gated || !acc || !acc2 || !row ||
-      !keys || !vals || !scores || !head_out)
-    abort();
+  if (!cur || !nrm || !q || !k || !v || !ctx || !after || !gated || !acc || !acc2) abort();
   const double scale = attention_scale(D);
 
   for (size_t b = 0; b < batch; ++b)
@@ -602,11 +678,11 @@ int tmco_decoder_step(const tmco_model *m, uint16_t *const *key_pools,
     const int32_t *table = block_tables + l * batch * max_pages;
     rmsnorm_f16(cur, L->input_norm, batch, H, m->epsilon, acc);
     store_array(acc, batch * H, nrm);
-    linear_f16(nrm, L->wq, batch, H, H, acc, row);
+    linear_f16(nrm, L->wq, batch, H, H, acc);
     store_array(acc, batch * H, q);
-    linear_f16(nrm, L->wk, batch, H, KV, acc, row);
+    linear_f16(nrm, L->wk, batch, H, KV, acc);
     store_array(acc, batch * KV, k);
-    linear_f16(nrm, L->wv, batch, H, KV, acc, row);
+    linear_f16(nrm, L->wv, batch, H, KV, acc);
     store_array(acc, batch * KV, v);
     for (size_t b = 0; b < batch; ++b) {
       const size_t valid = (size_t)valid_lengths[b];
@@ -638,50 +714,65 @@ int tmco_decoder_step(const tmco_model *m, uint16_t *const *key_pools,
           value_pools[l][dst] = tmco_f32_to_f16(v[b * KV + h * D + c]);
         }
       /* Attention over [0, valid), stored; query head h reads kv head h/group. */
-      for (size_t h = 0; h < NH; ++h) {
-        for (size_t pos = 0; pos < valid; ++pos) {
-          const size_t pg = (size_t)table[b * max_pages + pos / page_size];
-          const size_t base = ((pg * KVH + h / group) * page_size + pos % page_size) * D;
-          for (size_t c = 0; c < D; ++c) {
-            keys[pos * D + c] = g_half_table[key_pools[l][base + c]];
-            vals[pos * D + c] = g_half_table[value_pools[l][base + c]];
+#pragma omp parallel num_threads(g_threads) if (g_threads > 1)
+      {
+        float *keys = (float *)malloc(valid * D * sizeof(float));
+        float *vals = (float *)malloc(valid * D * sizeof(float));
+        double *scores = (double *)malloc((valid + 1) * sizeof(double));
+        double *head_out = (double *)malloc(D * sizeof(double));
+        if (!keys || !vals || !scores || !head_out) abort();
+#pragma omp for schedule(static)
+        for (size_t h = 0; h < NH; ++h) {
+          for (size_t pos = 0; pos < valid; ++pos) {
+            const size_t pg = (size_t)table[b * max_pages + pos / page_size];
+            const size_t base = ((pg * KVH + h / group) * page_size + pos % page_size) * D;
+            for (size_t c = 0; c < D; ++c) {
+              keys[pos * D + c] = g_half_table[key_pools[l][base + c]];
+              vals[pos * D + c] = g_half_table[value_pools[l][base + c]];
+            }
           }
+          attend(q + b * H + h * D, keys, vals, valid, D, scale, scores, head_out);
+          for (size_t c = 0; c < D; ++c)
+            ctx[b * H + h * D + c] = tmco_store(head_out[c], TMCO_F16);
         }
-        attend(q + b * H + h * D, keys, vals, valid, D, scale, scores, head_out);
-        for (size_t c = 0; c < D; ++c)
-          ctx[b * H + h * D + c] = tmco_store(head_out[c], TMCO_F16);
+        free(keys); free(vals); free(scores); free(head_out);
       }
     }
-    linear_f16(ctx, L->wo, batch, H, H, acc, row);
+    linear_f16(ctx, L->wo, batch, H, H, acc);
     for (size_t i = 0; i < batch * H; ++i) {
       const double attn = tmco_store(acc[i], TMCO_F16);
       after[i] = tmco_store((double)cur[i] + attn, TMCO_F16);
     }
     rmsnorm_f16(after, L->post_norm, batch, H, m->epsilon, acc);
     store_array(acc, batch * H, nrm);
-    linear_f16(nrm, L->wg, batch, H, I, acc, row);
-    linear_f16(nrm, L->wu, batch, H, I, acc2, row);
+    linear_f16(nrm, L->wg, batch, H, I, acc);
+    linear_f16(nrm, L->wu, batch, H, I, acc2);
     for (size_t i = 0; i < batch * I; ++i) {
       const double g = tmco_store(acc[i], TMCO_F16);
       const double u = tmco_store(acc2[i], TMCO_F16);
       gated[i] = tmco_store(tmco_store(silu(g), TMCO_F16) * u, TMCO_F16);
     }
-    linear_f16(gated, L->wd, batch, I, H, acc, row);
+    linear_f16(gated, L->wd, batch, I, H, acc);
     for (size_t i = 0; i < batch * H; ++i) {
       const double mlp = tmco_store(acc[i], TMCO_F16);
       cur[i] = tmco_store((double)after[i] + mlp, TMCO_F16);
     }
   }
 
-  if (layers == m->layers) {
-    rmsnorm_f16(cur, m->final_norm, batch, H, m->epsilon, acc);
-    store_array(acc, batch * H, nrm);
-    linear_f16(nrm, m->lm_head, batch, H, m->vocabulary, acc, row);
-    for (size_t i = 0; i < batch * m->vocabulary; ++i) logits[i] = (float)acc[i];
-    tmco_argmax(logits, batch, m->vocabulary, next_tokens);
+  if (layers == m->layers && logits_from < batch) {
+    /* Rows before logits_from (prompt rows whose logits are not needed) skip
+     * the LM head; their logits stay 0 and their next token -1. */
+    const size_t rows = batch - logits_from, V = m->vocabulary;
+    rmsnorm_f16(cur + logits_from * H, m->final_norm, rows, H, m->epsilon, acc);
+    store_array(acc, rows * H, nrm);
+    linear_f16(nrm, m->lm_head, rows, H, V, acc);
+    memset(logits, 0, logits_from * V * sizeof(float));
+    for (size_t i = 0; i < rows * V; ++i) logits[logits_from * V + i] = (float)acc[i];
+    for (size_t b = 0; b < logits_from; ++b) next_tokens[b] = -1;
+    tmco_argmax(logits + logits_from * V, rows, V, next_tokens + logits_from);
   }
 
   free(cur); free(nrm); free(q); free(k); free(v); free(ctx); free(after); free(gated);
-  free(acc); free(acc2); free(row); free(keys); free(vals); free(scores); free(head_out);
+  free(acc); free(acc2);
   return 0;
 }

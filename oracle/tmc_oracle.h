@@ -103,12 +103,18 @@ typedef struct tmco_model {
  * [page][kv_heads][page_size][head_dim] (one pool pair per layer).  The new
  * token of request b lands at position valid_lengths[b]-1.  Writes K/V into
  * the pools, fp32 logits [batch, vocabulary] (rounded from double) and the
- * greedy tokens. */
+ * greedy tokens.  Rows b < logits_from skip the final norm and LM head
+ * (logits 0, token -1); layer_limit > 0 and below the layer count stops
+ * after that many layers with no LM head at all. */
+/* Threads used by tmco_decoder_step (default 1).  Results do not depend on
+ * it: the work is split over output features and heads, never inside a sum. */
+void tmco_set_threads(int threads);
+
 int tmco_decoder_step(const tmco_model *model, uint16_t *const *key_pools,
                       uint16_t *const *value_pools, size_t page_size, size_t max_pages,
                       const int32_t *block_tables, const int32_t *tokens,
                       const int32_t *valid_lengths, size_t batch, size_t layer_limit,
-                      float *logits, int32_t *next_tokens);
+                      size_t logits_from, float *logits, int32_t *next_tokens);
 
 #ifdef __cplusplus
 }

@@ -60,6 +60,11 @@ def test_argument_validation_fails_before_device_work(tmc):
     assert lib.tmc_qkv_rope_append_packed_f16(p, p, p, p, p, p, p, p, p, p, 4, 64, 2, 1, 16, 32, 16,
                                               2, tmc.Y_PACKED, None, None) != 0
     assert "layout" in tmc.last_error()
+    # a block-table row shorter than ceil(capacity / page_size) would let a
+    # request index the next request's row
+    assert lib.tmc_qkv_rope_append_packed_f16(p, p, p, p, p, p, p, p, p, p, 4, 64, 2, 1, 16, 32, 16,
+                                              1, 0, None, None) != 0
+    assert "ceil(capacity / page_size)" in tmc.last_error()
     assert lib.tmc_add_rmsnorm_qkv_rope_append_f16(p, p, p, p, None, p, p, p, p, p, p, p, p, 64, 2,
                                                    1, 16, 32, 16, 1e-6, None, None) != 0
     assert "null" in tmc.last_error()

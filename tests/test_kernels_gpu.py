@@ -272,7 +272,8 @@ def test_paged_and_serving_append_bit_exact(tmc, orc, torch):
 # ---------------------------------------------------------------- attention
 def _ws(tmc, torch, batch, qh, kvh, d, cap):
     n = tmc.attention_workspace_bytes(batch, qh, kvh, d, cap)
-    # zero-filled once: the kernels keep split counters there (and leave them at zero)
+    # per-split partial results (weighted sums, maxima, denominators); the
+    # merge reads only the slots the split blocks wrote in this launch
     return torch.zeros(max(n // 4, 1), dtype=torch.float32, device="cuda") if n else None
 
 

@@ -15,8 +15,8 @@ CFG = dict(layers=2, hidden=64, heads=4, head_dim=16, intermediate=96, vocabular
 P = 4  # page size
 
 
-def _model(orc, rng, kv_heads):
-    H, I, V, D = CFG["hidden"], CFG["intermediate"], CFG["vocabulary"], CFG["head_dim"]
+def _model(orc, rng, kv_heads, vocabulary=CFG["vocabulary"]):
+    H, I, V, D = CFG["hidden"], CFG["intermediate"], vocabulary, CFG["head_dim"]
     kv = kv_heads * D
     f16 = lambda a: orc.f16(np.asarray(a, np.float32))  # noqa: E731
     w = lambda *shape: f16(rng.standard_normal(shape) * 0.2)  # noqa: E731
@@ -120,3 +120,42 @@ def test_decoder_step_layer_limit_and_bad_inputs(orc):
                                  layer_limit=1)
     assert not logits.any()  # the head runs only when every layer ran
     assert k[0].any() and not k[1].any()
+
+
+@pytest.mark.parametrize("threads", [1, 4])
+def test_decoder_step_row_blocks_threads_and_logits_from(orc, threads):
+    """35 rows (two 16-row blocks of the blocked linear plus a 3-row tail),
+    an odd vocabulary (a lone last output feature), 1 or 4 threads: the same
+    values as the composition of pinned ops; rows before logits_from skip the
+    LM head without changing the other rows' logits or any pool bit."""
+    rng = np.random.default_rng(91)
+    V, rows, kv_heads = 51, 35, 2
+    m = _model(orc, rng, kv_heads, vocabulary=V)
+    cfg = dict(CFG, kv_heads=kv_heads, vocabulary=V)
+    D, max_pages = CFG["head_dim"], CFG["capacity"] // P
+    pages = rows * 2
+    tables = np.full((CFG["layers"], rows, max_pages), -1, np.int32)
+    for l in range(CFG["layers"]):
+        perm = rng.permutation(pages).astype(np.int32)
+        tables[l, :, :2] = perm.reshape(rows, 2)
+    size = pages * kv_heads * P * D
+    pools = lambda: [np.zeros(size, np.uint16) for _ in range(CFG["layers"])]  # noqa: E731
+    a_k, a_v, b_k, b_v, c_k, c_v = pools(), pools(), pools(), pools(), pools(), pools()
+    tokens = rng.integers(0, V, rows).astype(np.int32)
+    lengths = rng.integers(1, 2 * P + 1, rows).astype(np.int32)
+    try:
+        orc.set_threads(threads)
+        got, got_tok = orc.decoder_step(m, cfg, a_k, a_v, P, max_pages, tables, tokens, lengths)
+        part, part_tok = orc.decoder_step(m, cfg, c_k, c_v, P, max_pages, tables, tokens, lengths,
+                                          logits_from=20)
+    finally:
+        orc.set_threads(1)
+    want, want_tok = _composed_step(orc, m, kv_heads, b_k, b_v, tables, tokens, lengths)
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6)
+    assert (got_tok == want_tok).all()
+    for l in range(CFG["layers"]):
+        assert (a_k[l] == b_k[l]).all() and (a_v[l] == b_v[l]).all()
+        assert (c_k[l] == a_k[l]).all() and (c_v[l] == a_v[l]).all()
+    assert not part[:20].any() and (part_tok[:20] == -1).all()
+    np.testing.assert_array_equal(part[20:], got[20:])
+    assert (part_tok[20:] == got_tok[20:]).all()
