@@ -62,6 +62,7 @@ def weights7b(orc):
                    wg=w(I, H), wu=w(I, H), wd=w(H, I)) for _ in range(SHAPE["layers"])]
     pos = np.arange(ROPE_ROWS, dtype=np.float64)[:, None]
     freq = 10000.0 ** (-np.arange(0, D, 2, dtype=np.float64) / D)
+    print("[7b] host weights ready", flush=True)
     return dict(embedding=w(V, H), final_norm=f16(rng.uniform(0.5, 1.5, H)), lm_head=w(V, H),
                 rope_cos=np.cos(pos * freq).astype(np.float32),
                 rope_sin=np.sin(pos * freq).astype(np.float32), layers=layers)
@@ -98,6 +99,7 @@ def models7b(host, orc, rt7b, weights7b):
             w = _workload(host, _FastValues, cfg, _at_capacity(weights7b, capacity))
             cache[capacity] = (host.create_model_resources(rt7b, w), w.plan)
             del w
+            print(f"[7b] model uploaded (capacity {capacity})", flush=True)
         return cache[capacity]
 
     yield get
@@ -208,10 +210,10 @@ def test_7b_serving_batch16_matches_oracle(host, orc, rt7b, weights7b, models7b)
     for spec, out in zip(specs, outs):
         assert out["id"] == spec.id and len(out["generated_token_ids"]) == steps + 1
 
-    # Oracle: every request owns `per_request` pages of one shared pool; all
-    # prompt rows run as one step (each request's rows in position order),
-    # with the last prompt row of every request at the end so the LM head
-    # runs only there.
+    # Oracle: every request owns `per_request` pages of one shared pool.  The
+    # prompts run in groups of 4 requests, all prompt rows of a group as one
+    # step (each request's rows in position order) with each request's last
+    # prompt row at the end, so the LM head runs only there.
     max_pages = capacity // P
     pool = batch * per_request * SHAPE["kv_heads"] * P * SHAPE["head_dim"]
     kp = [np.zeros(pool, np.uint16) for _ in range(SHAPE["layers"])]
@@ -219,21 +221,26 @@ def test_7b_serving_batch16_matches_oracle(host, orc, rt7b, weights7b, models7b)
     table = np.full((batch, max_pages), -1, np.int32)
     for r in range(batch):
         table[r, :per_request] = r * per_request + np.arange(per_request)
-    rows = [(r, i) for r in range(batch) for i in range(len(prompts[r]) - 1)]
-    rows += [(r, len(prompts[r]) - 1) for r in range(batch)]
-    req = np.array([r for r, _ in rows])
-    tokens = np.array([prompts[r][i] for r, i in rows], np.int32)
-    lengths = np.array([i + 1 for _, i in rows], np.int32)
-    tables = np.broadcast_to(table[req], (SHAPE["layers"], len(rows), max_pages))
     orc.set_threads(_oracle_threads())
     try:
-        logits, nxt = orc.decoder_step(m, cfg, kp, vp, P, max_pages, tables, tokens, lengths,
-                                       logits_from=len(rows) - batch)
-        tail = logits[len(rows) - batch:]
-        for r, out in enumerate(outs):
-            assert_f16_path(out["prefill_logits"], tail[r], f"request {r} prefill logits")
-            _check_token(int(out["generated_token_ids"][0]), int(nxt[len(rows) - batch + r]),
-                         tail[r], f"request {r} first token")
+        for group in range(0, batch, 4):
+            members = range(group, min(group + 4, batch))
+            rows = [(r, i) for r in members for i in range(len(prompts[r]) - 1)]
+            rows += [(r, len(prompts[r]) - 1) for r in members]
+            req = np.array([r for r, _ in rows])
+            tokens = np.array([prompts[r][i] for r, i in rows], np.int32)
+            lengths = np.array([i + 1 for _, i in rows], np.int32)
+            tables = np.broadcast_to(table[req], (SHAPE["layers"], len(rows), max_pages))
+            first = len(rows) - len(members)
+            logits, nxt = orc.decoder_step(m, cfg, kp, vp, P, max_pages, tables, tokens, lengths,
+                                           logits_from=first)
+            print(f"[7b] oracle prompts of requests {list(members)}: {len(rows)} rows", flush=True)
+            for j, r in enumerate(members):
+                out = outs[r]
+                assert_f16_path(out["prefill_logits"], logits[first + j],
+                                f"request {r} prefill logits")
+                _check_token(int(out["generated_token_ids"][0]), int(nxt[first + j]),
+                             logits[first + j], f"request {r} first token")
         step_tables = np.broadcast_to(table, (SHAPE["layers"], batch, max_pages))
         for step in range(steps):
             tok = np.array([out["generated_token_ids"][step] for out in outs], np.int32)
