@@ -90,6 +90,9 @@ def _declare(l):
                                        vp]),
         "tmc_paged_decode_attention": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64,
                                              i64, i64, i64, i64, i64, vp, sz, vp]),
+        "tmc_paged_decode_attention_noalloc": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i64, i64,
+                                                     i64, i64, i64, i64, i64, i64, i64, vp]),
+        "tmc_attention_scratch_bytes": (sz, []),
         "tmc_argmax_f32": (i32, [vp, vp, i64, i64, vp]),
         "tmc_fill_normal": (i32, [vp, i32, i64, C.c_uint64, f, f, vp]),
         "tmc_copy_bytes": (i32, [vp, vp, sz, vp]),

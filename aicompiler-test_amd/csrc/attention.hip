@@ -24,6 +24,14 @@
 #include "tmc_device.hpp"
 
 #include <climits>
+#include <mutex>
+
+// Split partials of tmc_paged_decode_attention_noalloc: a file-scope device
+// array, so that entry point needs no allocation.  Each GPU the library runs
+// on holds its own copy until the process ends; host code reaches it only
+// through the address hipGetSymbolAddress returns for the current device.
+constexpr size_t kScratchBytes = 16u << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
 namespace tmc {
 namespace {
@@ -834,4 +842,57 @@ extern "C" int tmc_paged_decode_attention(const void* q, const void* key_pool,
   p.max_splits = (int)((capacity + p.chunk - 1) / p.chunk);
   p.scale_log2 = (float)(1.0 / std::sqrt((double)head_dim)) * 1.4426950408889634f;
   return dispatch_attention<true>(p, (int)max_batch, (int)head_dim, as_stream(stream));
+}
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[kScratchDevices];  // per-device address of `scratch`, filled on first use
+
+// The current device's address of `scratch` (looked up once per device,
+// with that device current).  Returns 0 or sets the error text.
+int scratch_address(void** out) {
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return fail(std::string("Attention scratch: ") + hipGetErrorString(err));
+  TMC_REQUIRE(device >= 0 && device < kScratchDevices, "Attention scratch: device index too large.");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch[device]) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr)
+      return fail(std::string("Attention scratch: hipGetSymbolAddress failed: ") +
+                  hipGetErrorString(err));
+    g_scratch[device] = ptr;
+  }
+  *out = g_scratch[device];
+  return 0;
+}
+
+}  // namespace
+
+extern "C" size_t tmc_attention_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" int tmc_paged_decode_attention_noalloc(
+    const void* q, const void* key_pool, const void* value_pool, const int32_t* valid_lengths,
+    const int32_t* block_tables, const int32_t* active_count, void* out, int dtype,
+    int64_t max_batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t page_size,
+    int64_t max_pages, int64_t pool_pages, int64_t page_stride, int64_t head_stride,
+    void* stream) {
+  clear_error();
+  TMC_REQUIRE(page_size > 0 && max_pages > 0 && max_pages <= (INT64_MAX / page_size),
+              "Paged attention (no-alloc): invalid page geometry.");
+  const size_t need = tmc_attention_workspace_bytes(max_batch, q_heads, kv_heads, head_dim,
+                                                    page_size * max_pages);
+  if (need > kScratchBytes)
+    return fail("Paged attention (no-alloc): these limits need " + std::to_string(need) +
+                " bytes of split workspace; the static scratch holds " +
+                std::to_string(kScratchBytes) + " (use tmc_paged_decode_attention).");
+  void* ws = nullptr;
+  if (need > 0 && scratch_address(&ws)) return 1;
+  return tmc_paged_decode_attention(q, key_pool, value_pool, valid_lengths, block_tables,
+                                    active_count, out, dtype, max_batch, q_heads, kv_heads,
+                                    head_dim, page_size, max_pages, pool_pages, page_stride,
+                                    head_stride, ws, need > 0 ? kScratchBytes : 0, stream);
 }

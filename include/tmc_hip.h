@@ -431,6 +431,28 @@ int tmc_paged_decode_attention(const void *q, const void *key_pool, const void *
                                int64_t pool_pages, int64_t page_stride, int64_t head_stride,
                                void *workspace, size_t workspace_bytes, void *stream);
 
+/* tmc_paged_decode_attention without a workspace argument and without any
+ * allocation.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The split partials live in a
+ * static device array of tmc_attention_scratch_bytes() (16 MiB) per GPU,
+ * held until the process ends; limits whose tmc_attention_workspace_bytes()
+ * exceed it are rejected with an error before any launch.  All calls on one
+ * GPU share that array: calls that overlap on one GPU (different streams,
+ * different host threads) race and must be serialised by the caller.  Each
+ * call writes every partial it reads, so nothing needs clearing between
+ * calls.  Same arguments, results and errors as tmc_paged_decode_attention
+ * otherwise. */
+int tmc_paged_decode_attention_noalloc(const void *q, const void *key_pool,
+                                       const void *value_pool, const int32_t *valid_lengths,
+                                       const int32_t *block_tables, const int32_t *active_count,
+                                       void *out, int dtype, int64_t max_batch, int64_t q_heads,
+                                       int64_t kv_heads, int64_t head_dim, int64_t page_size,
+                                       int64_t max_pages, int64_t pool_pages, int64_t page_stride,
+                                       int64_t head_stride, void *stream);
+/* Bytes of the static scratch behind tmc_paged_decode_attention_noalloc. */
+size_t tmc_attention_scratch_bytes(void);
+
 /* Decode-step fusion of emitServingRoPE (DecoderLLMMetalEmitter.cpp:260-312)
  * for q and k with emitServingPagedCacheAppend (:314-373) for the rotated k
  * and v, reading one fused projection row per request laid out
