@@ -297,6 +297,7 @@ struct BatchedDecodeExecutor::Bucket {
   std::size_t rows = 0;
   std::vector<std::unique_ptr<hip::PreparedExecution>> steps;
   std::unique_ptr<hip::PreparedSequence> sequence;
+  std::vector<std::size_t> uses;  // registry usage entries of this bucket
 };
 
 BatchedDecodeExecutor::~BatchedDecodeExecutor() = default;
@@ -432,12 +433,47 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
     };
     // Batch 1: 512 threads per row (one 16-byte chunk each at H = 4096) cut
     // the latency-bound norm by ~0.5 us after a GEMV against 256 (measured).
-    const std::string norm = "rows=" + B + "&width=" + std::to_string(H) + "&eps=" + eps +
-                             "&dtype=f16" +
-                             (packed ? "&out_layout=packed" : H >= 4096 ? "&threads=512" : "");
+    const std::string normShape =
+        "rows=" + B + "&width=" + std::to_string(H) + "&eps=" + eps + "&dtype=f16";
+    // An admitted region kernel replaces the template's launch parameters
+    // where its contract shape (one row of width 4096, row-major output)
+    // matches; its threads / variant apply to every launch of the region.
+    const auto regionKernel = [&](const char* pattern) -> std::string {
+      const AdmittedKernel* entry = registry_ ? registry_->find(pattern) : nullptr;
+      if (!entry || packed || m != 1 || H != 4096) return {};
+      std::string tuning;
+      std::stringstream items(entry->source.substr(std::min(entry->source.size(),
+                                                            entry->source.find('?') + 1)));
+      for (std::string item; std::getline(items, item, '&');) {
+        const std::string field = item.substr(0, item.find('='));
+        if (field == "threads" || field == "variant") tuning += "&" + item;
+      }
+      if (tuning.find("threads=") == std::string::npos)
+        tuning += "&threads=" + std::to_string(entry->workgroupSize);
+      return tuning;
+    };
+    const std::string generatedNorm = regionKernel("decoder_rmsnorm");
+    const std::string generatedAddNorm = regionKernel("decoder_residual_rmsnorm");
+    const std::string templateTuning =
+        packed ? "&out_layout=packed" : H >= 4096 ? "&threads=512" : "";
+    const std::string firstNorm =
+        normShape + (generatedNorm.empty() ? templateTuning : generatedNorm);
+    const std::string norm =
+        normShape + (generatedAddNorm.empty() ? templateTuning : generatedAddNorm);
+    if (registry_) {
+      const auto track = [&](const char* node, const char* pattern, const std::string& tuning,
+                             const std::string& key, std::size_t launches) {
+        bucket->uses.push_back(registry_->track(
+            {"bucket " + B + " " + node, pattern, tuning.empty() ? "template" : "generated", key,
+             launches, 0}));
+      };
+      track("input norm", "decoder_rmsnorm", generatedNorm, "rmsnorm?" + firstNorm, 1);
+      track("residual norms", "decoder_residual_rmsnorm", generatedAddNorm,
+            "add_rmsnorm?" + norm, 2 * L);
+    }
     add("embedding?rows=" + B + "&hidden=" + std::to_string(H) + "&vocab=" + std::to_string(V),
         "embedding", {tokensView_, model_->embeddingWeight}, {residual_});
-    add("rmsnorm?" + norm, "l0_input_norm", {residual_, model_->layers[0].inputNormWeight},
+    add("rmsnorm?" + firstNorm, "l0_input_norm", {residual_, model_->layers[0].inputNormWeight},
         {normalized_});
     const std::string ropeKey = "decode_rope_append?max_batch=" + B + "&q_heads=" + std::to_string(QH) +
                                 "&kv_heads=" + std::to_string(KVH) + "&head_dim=" + std::to_string(D) +
@@ -510,7 +546,7 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
 BatchedDecodeExecutor::Creation createBatchedDecodeExecutor(
     hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
     std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t maximumBatchSize,
-    std::ostream* log, bool tuneKernels) {
+    std::ostream* log, bool tuneKernels, std::shared_ptr<KernelRegistry> registry) {
   BatchedDecodeExecutor::Creation result;
   try {
     if (!model) throw std::invalid_argument("Batched decode needs model resources.");
@@ -533,6 +569,7 @@ BatchedDecodeExecutor::Creation createBatchedDecodeExecutor(
     executor->maximumBatchSize_ = maximumBatchSize;
     executor->pageSize_ = executor->pools_.front()->pageSize();
     executor->tuneKernels_ = tuneKernels;
+    executor->registry_ = std::move(registry);
     executor->build(log);
     result.executor = std::move(executor);
   } catch (const std::exception& error) {
@@ -651,6 +688,7 @@ std::string BatchedDecodeExecutor::launchChained(
                  bucket.rows);
   if (error.empty() && tokenIds.empty()) error = tokensView_->copyFromAsync(*nextTokens_, rows);
   if (error.empty()) error = bucket.sequence->launch();
+  if (error.empty() && registry_) registry_->completed(bucket.uses);
   if (error.empty())
     error = history_->copyFromAsync(*nextTokens_, rows, historyStep * maximumBatchSize_);
   std::fill(metaShadow_.begin(), metaShadow_.end(), std::numeric_limits<std::int32_t>::min());
@@ -697,6 +735,7 @@ BatchedDecodeRun BatchedDecodeExecutor::run(const std::vector<std::int32_t>& tok
       return result;
     }
   }
+  if (registry_) registry_->completed(bucket.uses);
   std::vector<std::int32_t> next(rows);
   error = nextTokens_->readRaw(next.data(), rows);  // waits for the stream
   if (!error.empty()) {
@@ -1076,6 +1115,7 @@ class CompiledDecoderLLM::Impl {
   std::vector<std::unique_ptr<KVCacheState>> states;
   std::unique_ptr<BatchedDecodeExecutor> executor;
   std::unique_ptr<ChunkedPrefillExecutor> prefillExecutor;
+  std::shared_ptr<KernelRegistry> registry = std::make_shared<KernelRegistry>();
   std::size_t requestedPageSize = 0;
   std::size_t kvBytes = 0;
 
@@ -1292,6 +1332,13 @@ std::size_t CompiledDecoderLLM::activationStorageBytes() const noexcept {
          (impl_->prefillExecutor ? impl_->prefillExecutor->activationStorageBytes() : 0);
 }
 
+std::string CompiledDecoderLLM::kernelUsageReport(bool reset) const {
+  std::ostringstream out;
+  impl_->registry->report(out);
+  if (reset) impl_->registry->resetUsage();
+  return out.str();
+}
+
 std::shared_ptr<DecoderLLMModelResources> CompiledDecoderLLM::sharedModelResources()
     const noexcept {
   return impl_->model;
@@ -1402,7 +1449,9 @@ DecoderLLMCompilation compileDecoderLLM(hip::HipRuntime& runtime,
       if (!state.state) throw std::runtime_error(state.errorMessage);
       impl->states.push_back(std::move(state.state));
     }
-    auto executor = createBatchedDecodeExecutor(runtime, impl->model, impl->pools, 1, &log);
+    impl->registry->load(runtime, options.kernelLibrary, log);
+    auto executor =
+        createBatchedDecodeExecutor(runtime, impl->model, impl->pools, 1, &log, false, impl->registry);
     if (!executor.executor) throw std::runtime_error(executor.errorMessage);
     impl->executor = std::move(executor.executor);
     if (options.prefillChunkSize != 0) {

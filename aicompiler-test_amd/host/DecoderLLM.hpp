@@ -25,6 +25,7 @@
 
 #include "HipRuntime.hpp"
 #include "KVCacheState.hpp"
+#include "KernelRegistry.hpp"
 
 #include <cstddef>
 #include <cstdint>
@@ -227,7 +228,8 @@ class BatchedDecodeExecutor {
   friend Creation createBatchedDecodeExecutor(hip::HipRuntime&,
                                               std::shared_ptr<DecoderLLMModelResources>,
                                               std::vector<std::shared_ptr<KVPagePool>>,
-                                              std::size_t, std::ostream*, bool);
+                                              std::size_t, std::ostream*, bool,
+                                              std::shared_ptr<KernelRegistry>);
   BatchedDecodeExecutor() = default;
   void build(std::ostream* log);
   [[nodiscard]] std::string upload(const std::vector<std::int32_t>& tokens,
@@ -246,6 +248,7 @@ class BatchedDecodeExecutor {
   std::size_t pageSize_ = 0;
   std::size_t maxPages_ = 0;
   bool tuneKernels_ = false;
+  std::shared_ptr<KernelRegistry> registry_;  // admitted region kernels, may be null
   std::size_t activationBytes_ = 0;
   // Device buffers sized for maximumBatchSize rows.
   hip::BufferHandle meta_;    // int32 [tokens M | lengths M | active 1]
@@ -268,10 +271,15 @@ struct BatchedDecodeExecutor::Creation {
 // tuneKernels: the batch-1 GEMVs use the decode GEMV tuner's selection for
 // their shapes (tuned once per process on this model's weights and cached;
 // planner::decodeGEMVTuningCache), instead of the default configurations.
+// registry: admitted region kernels (KernelRegistry::load) that replace the
+// template norm kernels where their contract shape matches the step (the
+// one-row bucket at hidden 4096); each bucket's region launches are tracked
+// in the registry's usage audit.
 [[nodiscard]] BatchedDecodeExecutor::Creation createBatchedDecodeExecutor(
     hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
     std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t maximumBatchSize,
-    std::ostream* log = nullptr, bool tuneKernels = false);
+    std::ostream* log = nullptr, bool tuneKernels = false,
+    std::shared_ptr<KernelRegistry> registry = nullptr);
 
 // Chunked prefill (prefillChunked, DecoderLLMExecutor.cpp:982-1034): the
 // tokens of one request's prompt chunk are the rows of one stage.  Linear
@@ -367,6 +375,9 @@ struct DecoderLLMCompileOptions {
   std::vector<std::shared_ptr<KVPagePool>> sharedKVPools;
   DType storageDtype = DType::Float16;
   std::shared_ptr<DecoderLLMModelResources> sharedModelResources;
+  // Directory of admitted region kernels (<dir>/decoder_*/admitted.json,
+  // DecoderLLMExecutor.cpp:1319); empty = template kernels only.
+  std::string kernelLibrary;
 };
 
 struct DecoderKVSnapshot {
@@ -429,6 +440,9 @@ class CompiledDecoderLLM {
   [[nodiscard]] std::string stageKVLength(std::size_t length);
   void commitKVLength(std::size_t length);
   [[nodiscard]] std::string rollbackKVLength(std::size_t length);
+  // The kernel registry's usage audit since the last reset (KernelRegistry::
+  // report; DecoderLLMExecutor.cpp:1192-1196).
+  [[nodiscard]] std::string kernelUsageReport(bool reset = false) const;
 
  private:
   class Impl;

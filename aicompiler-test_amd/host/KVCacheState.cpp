@@ -7,6 +7,7 @@
 #include <cstring>
 #include <limits>
 #include <stdexcept>
+#include <tuple>
 #include <utility>
 
 namespace tensor {
@@ -95,33 +96,40 @@ KVPagePool::KVPagePool(planner::KVCachePlan plan, std::size_t pageSize, hip::Buf
       pageSize_(pageSize),
       key_(std::move(key)),
       value_(std::move(value)),
-      allocated_(physicalPageCount, false) {
-  freePages_.reserve(physicalPageCount);
-  for (std::size_t page = 0; page < physicalPageCount; ++page)
-    freePages_.push_back(static_cast<std::int32_t>(page));
+      link_(physicalPageCount),
+      freeCount_(physicalPageCount) {
+  // Free stack N-1 (top), N-2, ..., 0 (bottom): page p rests on page p - 1.
+  for (std::size_t p = 0; p < physicalPageCount; ++p)
+    link_[p] = static_cast<std::int32_t>(p) - 1;
+  top_ = static_cast<std::int32_t>(physicalPageCount) - 1;
 }
 
 std::int32_t KVPagePool::allocatePage() {
-  if (freePages_.empty()) return -1;
-  const std::int32_t page = freePages_.back();
-  freePages_.pop_back();
-  allocated_[static_cast<std::size_t>(page)] = true;
-  ++allocationCount_;
-  peakUsedPages_ = std::max(peakUsedPages_, usedPages());
+  if (top_ == kBottom) return -1;
+  const std::int32_t page = top_;
+  std::int32_t& link = link_[static_cast<std::size_t>(page)];
+  top_ = link;
+  link = kLent;
+  --freeCount_;
+  ++tally_.lent;
+  if (usedPages() > tally_.peak) tally_.peak = usedPages();
   return page;
 }
 
 void KVPagePool::releasePage(std::int32_t page) {
   if (!isAllocated(page))
     throw std::invalid_argument("Paged KV attempted to release an invalid page.");
-  allocated_[static_cast<std::size_t>(page)] = false;
-  freePages_.push_back(page);
-  ++releaseCount_;
+  link_[static_cast<std::size_t>(page)] = top_;
+  top_ = page;
+  ++freeCount_;
+  ++tally_.returned;
 }
 
 bool KVPagePool::compatible(const planner::KVCachePlan& plan) const noexcept {
-  return plan.batch == plan_.batch && plan.heads == plan_.heads &&
-         plan.headDimension == plan_.headDimension && plan.dtype == plan_.dtype;
+  const auto shape = [](const planner::KVCachePlan& q) {
+    return std::make_tuple(q.batch, q.heads, q.headDimension, q.dtype);
+  };
+  return shape(plan) == shape(plan_);
 }
 
 namespace {
@@ -186,19 +194,21 @@ KVCacheState::KVCacheState(planner::KVCachePlan plan, hip::BufferHandle key,
       initialValue_(value_.get()),
       pageSize_(pagePool ? pagePool->pageSize() : 0),
       pagePool_(std::move(pagePool)) {
-  if (pageSize_ != 0)
-    logicalToPhysical_.assign((plan_.capacity + pageSize_ - 1) / pageSize_, -1);
+  if (pageSize_ != 0) {
+    tableSlots_ = pagesFor(plan_.capacity);
+    pages_.reserve(tableSlots_);
+  }
 }
 
 KVCacheState::~KVCacheState() {
+  // The pages go back first to last (the reference's destructor order), so
+  // the last logical page ends on top of the pool's free stack.
   if (!pagePool_) return;
-  for (auto& page : logicalToPhysical_) {
-    if (page < 0) continue;
+  for (const std::int32_t page : pages_) {
     try {
       pagePool_->releasePage(page);
     } catch (...) {
     }
-    page = -1;
   }
 }
 
@@ -210,48 +220,41 @@ std::string KVCacheState::writeLength(hip::HipRuntime& runtime, std::size_t leng
 
 std::string KVCacheState::reset(hip::HipRuntime& runtime) {
   auto error = writeLength(runtime, 0);
-  if (!error.empty()) return error;
-  if (isPaged()) {
-    resizePageAllocation(0);
+  if (error.empty() && isPaged()) {
+    (void)resizePageAllocation(0);  // shrinking always succeeds
     error = writeBlockTable(runtime);
-    if (!error.empty()) return error;
   }
-  currentLength_ = 0;
-  return {};
+  if (error.empty()) currentLength_ = 0;
+  return error;
 }
 
 std::string KVCacheState::stageLength(hip::HipRuntime& runtime, std::size_t length) {
   if (length == 0 || length > plan_.capacity)
     return "KV cache valid length is outside the configured capacity.";
-  const std::size_t previousPages = allocatedPageCount();
-  if (isPaged()) {
-    const std::size_t required = (length + pageSize_ - 1) / pageSize_;
-    if (required > logicalToPhysical_.size())
-      return "Paged KV cache has no block-table capacity for this length.";
-    try {
-      resizePageAllocation(required);
-    } catch (const std::exception& error) {
-      return error.what();
-    }
-    auto error = writeBlockTable(runtime);
-    if (!error.empty()) {
-      resizePageAllocation(previousPages);
-      return error;
-    }
-  }
-  auto error = writeLength(runtime, length);
-  if (!error.empty() && isPaged()) {
-    resizePageAllocation(previousPages);
+  if (!isPaged()) return writeLength(runtime, length);
+  if (pagesFor(length) > tableSlots_)
+    return "Paged KV cache has no block-table capacity for this length.";
+  const std::size_t kept = pages_.size();
+  auto error = resizePageAllocation(pagesFor(length));
+  if (!error.empty()) return error;
+  error = writeBlockTable(runtime);
+  if (error.empty()) {
+    error = writeLength(runtime, length);
+    if (error.empty()) return {};
+    // the table already names the new pages: put the old set back on both sides
+    (void)resizePageAllocation(kept);
     (void)writeBlockTable(runtime);
+    return error;
   }
+  (void)resizePageAllocation(kept);
   return error;
 }
 
 std::string KVCacheState::rollbackLength(hip::HipRuntime& runtime, std::size_t length) {
   if (length > plan_.capacity) return "Cannot roll back KV cache beyond its configured capacity.";
   if (isPaged()) {
-    resizePageAllocation(length == 0 ? 0 : (length + pageSize_ - 1) / pageSize_);
-    auto error = writeBlockTable(runtime);
+    auto error = resizePageAllocation(pagesFor(length));
+    if (error.empty()) error = writeBlockTable(runtime);
     if (!error.empty()) return error;
   }
   return writeLength(runtime, length);
@@ -295,7 +298,7 @@ std::string KVCacheState::spillPages(hip::HipRuntime& runtime, KVPageSpill& out)
   if (tmc_host_alloc(header + out.bytes(), &raw) != 0) return tmc_last_error();
   out.host = std::shared_ptr<void>(raw, [](void* p) { tmc_host_free(p); });
   auto* ids = static_cast<std::int32_t*>(raw);
-  for (std::size_t i = 0; i < out.pages; ++i) ids[i] = logicalToPhysical_.at(i);
+  for (std::size_t i = 0; i < out.pages; ++i) ids[i] = pages_.at(i);
   auto* pagesBase = static_cast<unsigned char*>(raw) + header;
   const auto count = static_cast<std::int64_t>(out.pages);
   const auto bytes = static_cast<std::int64_t>(out.pageBytes);
@@ -319,7 +322,7 @@ std::string KVCacheState::restorePages(hip::HipRuntime& runtime, const KVPageSpi
   const std::size_t header =
       (spill.pages * sizeof(std::int32_t) + kSpillHeader - 1) / kSpillHeader * kSpillHeader;
   auto* ids = static_cast<std::int32_t*>(spill.host.get());
-  for (std::size_t i = 0; i < spill.pages; ++i) ids[i] = logicalToPhysical_.at(i);
+  for (std::size_t i = 0; i < spill.pages; ++i) ids[i] = pages_.at(i);
   const auto* pagesBase = static_cast<const unsigned char*>(spill.host.get()) + header;
   const auto count = static_cast<std::int64_t>(spill.pages);
   const auto bytes = static_cast<std::int64_t>(pageBytes);
@@ -382,7 +385,7 @@ std::vector<float> KVCacheState::readPrefix(const hip::BufferHandle& buffer) con
   const std::size_t P = pageSize_, pageElements = B * H * P * D;
   std::vector<unsigned char> raw(pageElements * bytes);
   for (std::size_t logical = 0; logical * P < L; ++logical) {
-    const auto physical = static_cast<std::size_t>(logicalToPhysical_.at(logical));
+    const auto physical = static_cast<std::size_t>(pages_.at(logical));
     if (!buffer->readRaw(raw.data(), pageElements, physical * pageElements).empty()) return {};
     const std::size_t first = logical * P, last = std::min(L, first + P);
     for (std::size_t b = 0; b < B; ++b)
@@ -402,21 +405,16 @@ bool KVCacheState::storageReused() const noexcept {
   return key_.get() == initialKey_ && value_.get() == initialValue_;
 }
 
-std::size_t KVCacheState::allocatedPageCount() const noexcept {
-  std::size_t count = 0;
-  while (count < logicalToPhysical_.size() && logicalToPhysical_[count] >= 0) ++count;
-  return count;
-}
+std::size_t KVCacheState::allocatedPageCount() const noexcept { return pages_.size(); }
 
-std::vector<std::int32_t> KVCacheState::pageTable() const {
-  return {logicalToPhysical_.begin(),
-          logicalToPhysical_.begin() + static_cast<std::ptrdiff_t>(allocatedPageCount())};
-}
+std::vector<std::int32_t> KVCacheState::pageTable() const { return pages_; }
 
 std::string KVCacheState::writeBlockTable(hip::HipRuntime& runtime) {
   if (!isPaged() || !blockTable_) return {};
   (void)runtime;
-  return blockTable_->writeRaw(logicalToPhysical_.data(), logicalToPhysical_.size());
+  std::vector<std::int32_t> table(tableSlots_, -1);  // unowned slots read as missing
+  std::copy(pages_.begin(), pages_.end(), table.begin());
+  return blockTable_->writeRaw(table.data(), table.size());
 }
 
 std::string KVCacheState::writePagedPrefix(hip::HipRuntime& runtime,
@@ -437,36 +435,25 @@ std::string KVCacheState::writePagedPrefix(hip::HipRuntime& runtime,
         for (std::size_t pos = first; pos < last; ++pos)
           std::copy_n(prefix.begin() + static_cast<std::ptrdiff_t>(((b * H + h) * length + pos) * D),
                       D, page.begin() + static_cast<std::ptrdiff_t>(((b * H + h) * P + pos - first) * D));
-    const auto physical = static_cast<std::size_t>(logicalToPhysical_.at(logical));
+    const auto physical = static_cast<std::size_t>(pages_.at(logical));
     auto error = runtime.writeBuffer(buffer, page.data(), pageElements, physical * pageElements);
     if (!error.empty()) return error;
   }
   return {};
 }
 
-void KVCacheState::resizePageAllocation(std::size_t pageCount) {
-  const std::size_t allocated = allocatedPageCount();
-  if (pageCount > allocated) {
-    std::size_t logical = allocated;
-    for (; logical < pageCount; ++logical) {
-      const std::int32_t physical = pagePool_->allocatePage();
-      if (physical < 0) break;
-      logicalToPhysical_[logical] = physical;
-    }
-    if (logical != pageCount) {
-      while (logical > allocated) {
-        --logical;
-        pagePool_->releasePage(logicalToPhysical_[logical]);
-        logicalToPhysical_[logical] = -1;
-      }
-      throw std::runtime_error("Paged KV cache physical page pool is exhausted.");
-    }
-    return;
+std::string KVCacheState::resizePageAllocation(std::size_t pageCount) {
+  if (pageCount > pages_.size()) {
+    if (pageCount - pages_.size() > pagePool_->availablePages())
+      return "Paged KV cache physical page pool is exhausted.";
+    while (pages_.size() < pageCount) pages_.push_back(pagePool_->allocatePage());
+    return {};
   }
-  for (std::size_t logical = allocated; logical > pageCount; --logical) {
-    pagePool_->releasePage(logicalToPhysical_[logical - 1]);
-    logicalToPhysical_[logical - 1] = -1;
+  while (pages_.size() > pageCount) {
+    pagePool_->releasePage(pages_.back());
+    pages_.pop_back();
   }
+  return {};
 }
 
 KVCacheStateCreation createKVCacheState(hip::HipRuntime& runtime,

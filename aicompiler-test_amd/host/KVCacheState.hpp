@@ -9,12 +9,16 @@
 // A page is one contiguous slab of heads*page_size*head_dim elements, so a
 // request's pages move to and from the host with one copy each.
 //
-// Pool bookkeeping follows KVCacheState.cpp:30-90: a LIFO free list that
-// starts as 0..N-1 (allocation pops the back, release pushes back), peak /
-// allocation / release counters, and errors for releasing a page that is not
-// allocated.  A pool created without a runtime (createHostKVPagePool) keeps
-// the bookkeeping only; states over it skip every device write, which is how
-// the CPU tests exercise the host logic.
+// Page bookkeeping keeps the reference's observable rules
+// (KVCacheState.cpp:30-90,355-379): pages are handed out last-in first-out
+// from a stack that starts as 0..N-1 with N-1 on top, a state returns its
+// pages last logical page first when it shrinks, and releasing a page that is
+// not lent out is an error.  The pool keeps its free stack threaded through a
+// per-page link array (no separate free list or flag vector); a state keeps
+// the pages it owns as a dense list in logical order.  A growth that does not
+// fit takes no page at all.  A pool created without a runtime
+// (createHostKVPagePool) keeps the bookkeeping only; states over it skip every
+// device write, which is how the CPU tests exercise the host logic.
 #pragma once
 
 #include "HipRuntime.hpp"
@@ -85,14 +89,12 @@ class KVPagePool {
   KVPagePool& operator=(const KVPagePool&) = delete;
 
   [[nodiscard]] std::size_t pageSize() const noexcept { return pageSize_; }
-  [[nodiscard]] std::size_t capacityPages() const noexcept { return allocated_.size(); }
-  [[nodiscard]] std::size_t usedPages() const noexcept {
-    return allocated_.size() - freePages_.size();
-  }
-  [[nodiscard]] std::size_t availablePages() const noexcept { return freePages_.size(); }
-  [[nodiscard]] std::size_t peakUsedPages() const noexcept { return peakUsedPages_; }
-  [[nodiscard]] std::size_t allocationCount() const noexcept { return allocationCount_; }
-  [[nodiscard]] std::size_t releaseCount() const noexcept { return releaseCount_; }
+  [[nodiscard]] std::size_t capacityPages() const noexcept { return link_.size(); }
+  [[nodiscard]] std::size_t usedPages() const noexcept { return link_.size() - freeCount_; }
+  [[nodiscard]] std::size_t availablePages() const noexcept { return freeCount_; }
+  [[nodiscard]] std::size_t peakUsedPages() const noexcept { return tally_.peak; }
+  [[nodiscard]] std::size_t allocationCount() const noexcept { return tally_.lent; }
+  [[nodiscard]] std::size_t releaseCount() const noexcept { return tally_.returned; }
   [[nodiscard]] const hip::BufferHandle& keyBuffer() const noexcept { return key_; }
   [[nodiscard]] const hip::BufferHandle& valueBuffer() const noexcept { return value_; }
   [[nodiscard]] const planner::KVCachePlan& plan() const noexcept { return plan_; }
@@ -102,8 +104,8 @@ class KVPagePool {
   }
   [[nodiscard]] bool hasStorage() const noexcept { return key_ != nullptr; }
   [[nodiscard]] bool isAllocated(std::int32_t page) const noexcept {
-    return page >= 0 && static_cast<std::size_t>(page) < allocated_.size() &&
-           allocated_[static_cast<std::size_t>(page)];
+    return page >= 0 && static_cast<std::size_t>(page) < link_.size() &&
+           link_[static_cast<std::size_t>(page)] == kLent;
   }
 
  private:
@@ -116,19 +118,31 @@ class KVPagePool {
   friend class KVCacheState;
   KVPagePool(planner::KVCachePlan plan, std::size_t pageSize, hip::BufferHandle key,
              hip::BufferHandle value, std::size_t physicalPageCount);
+  // The page on top of the free stack, or -1 when none is free.
   [[nodiscard]] std::int32_t allocatePage();
+  // Push a lent page back on top; throws std::invalid_argument otherwise.
   void releasePage(std::int32_t page);
+  // Same per-request tensor shape (batch, heads, head dim, dtype).
   [[nodiscard]] bool compatible(const planner::KVCachePlan& plan) const noexcept;
+
+  // link_[p]: for a free page, the page below it on the free stack (kBottom
+  // under the last one); kLent while a state owns it.
+  static constexpr std::int32_t kBottom = -1;
+  static constexpr std::int32_t kLent = -2;
+  struct Tally {
+    std::size_t lent = 0;      // pages handed out, over the pool's life
+    std::size_t returned = 0;  // pages given back
+    std::size_t peak = 0;      // most pages out at once
+  };
 
   planner::KVCachePlan plan_;
   std::size_t pageSize_ = 0;
   hip::BufferHandle key_;
   hip::BufferHandle value_;
-  std::vector<std::int32_t> freePages_;
-  std::vector<bool> allocated_;
-  std::size_t peakUsedPages_ = 0;
-  std::size_t allocationCount_ = 0;
-  std::size_t releaseCount_ = 0;
+  std::vector<std::int32_t> link_;
+  std::int32_t top_ = kBottom;
+  std::size_t freeCount_ = 0;
+  Tally tally_;
 };
 
 // createKVCacheState (KVCacheState.cpp:381-447): pageSize 0 = contiguous
@@ -214,7 +228,13 @@ class KVCacheState {
                                              const hip::BufferHandle& buffer,
                                              const std::vector<float>& prefix,
                                              std::size_t length);
-  void resizePageAllocation(std::size_t pageCount);
+  // Own exactly `pageCount` pages: take the missing ones from the pool (all
+  // or none) or give back the last ones.  "" or the exhaustion message.
+  [[nodiscard]] std::string resizePageAllocation(std::size_t pageCount);
+  // Pages that hold `length` tokens.
+  [[nodiscard]] std::size_t pagesFor(std::size_t length) const noexcept {
+    return length == 0 ? 0 : (length + pageSize_ - 1) / pageSize_;
+  }
 
   planner::KVCachePlan plan_;
   hip::BufferHandle key_;
@@ -226,7 +246,8 @@ class KVCacheState {
   std::size_t currentLength_ = 0;
   std::size_t pageSize_ = 0;
   std::shared_ptr<KVPagePool> pagePool_;
-  std::vector<std::int32_t> logicalToPhysical_;
+  std::vector<std::int32_t> pages_;  // owned pages, logical order
+  std::size_t tableSlots_ = 0;       // block-table entries: ceil(capacity / page size)
 };
 
 // Host conversion of one fp16 value (exact).

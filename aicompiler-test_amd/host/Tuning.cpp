@@ -1,5 +1,6 @@
 #include "Tuning.hpp"
 
+#include "KernelRegistry.hpp"
 #include "tmc_hip.h"
 
 #include <algorithm>
@@ -190,6 +191,8 @@ namespace planner {
 namespace {
 
 constexpr std::size_t kMaximumCpuReferenceOperations = 64u * 1024u * 1024u;
+// Shapes validated against the baseline's GPU output are large: fewer samples.
+constexpr std::size_t kLargeShapeSamples = 9;
 
 // The value a float takes once uploaded as fp16 (the runtime's own upload
 // conversion, ties away from zero), so the CPU reference sees the stored
@@ -202,12 +205,13 @@ float roundHalf(float value) {
   return stored;
 }
 
+// y[b, n] = sum_k x[b, k] W[n, k] in double over the stored (fp16) values.
 std::vector<double> gemvReference(std::size_t batch, std::size_t in, std::size_t out,
                                   const std::vector<float>& x, const std::vector<float>& w) {
   std::vector<double> y(batch * out);
   std::vector<double> xs(x.size()), ws(w.size());
-  for (std::size_t i = 0; i < x.size(); ++i) xs[i] = roundHalf(x[i]);
-  for (std::size_t i = 0; i < w.size(); ++i) ws[i] = roundHalf(w[i]);
+  std::transform(x.begin(), x.end(), xs.begin(), roundHalf);
+  std::transform(w.begin(), w.end(), ws.begin(), roundHalf);
   for (std::size_t b = 0; b < batch; ++b)
     for (std::size_t n = 0; n < out; ++n) {
       double acc = 0.0;
@@ -217,48 +221,135 @@ std::vector<double> gemvReference(std::size_t batch, std::size_t in, std::size_t
   return y;
 }
 
-std::string configText(const hip::DecodeGEMVConfig& c) {
+std::string describe(const hip::DecodeGEMVConfig& c) {
+  static const char* const names[] = {"default", "dot", "mfma", "mfma-rows", "linear"};
   std::ostringstream s;
-  s << "algorithm=" << c.algorithm << ", rows_per_wave=" << c.rowsPerWave
-    << ", unroll=" << c.unroll << ", k_split=" << c.kSplit;
+  s << (c.algorithm >= 0 && c.algorithm <= 4 ? names[c.algorithm] : "?") << '(' << c.rowsPerWave
+    << ',' << c.unroll << ',' << c.kSplit << ')';
   return s.str();
 }
 
-// Resolve `kernel`, prepare it over fresh buffers holding `input` and
-// `weight`, run it once and validate against `expected` when given.
+// ------------------------------------------------------------------ trials
+// One entrant against the baseline: a paired round, a confirmation round
+// only when the first reached the bar, and the admission rule over both.
+struct Trial {
+  benchmark::PairedResult first;
+  std::optional<benchmark::PairedResult> confirmation;
+  AdmissionDecision decision;
+};
+
+Trial runTrial(const benchmark::Sampler& baseline, const benchmark::Sampler& entrant,
+               std::size_t samples) {
+  Trial t;
+  t.first = benchmark::measurePair(baseline, entrant, samples);
+  if (t.first.passed && t.first.speedup >= kMinimumSpeedup)
+    t.confirmation = benchmark::measurePair(baseline, entrant, samples);
+  t.decision = admissionDecision(t.first, t.confirmation);
+  return t;
+}
+
+std::string trialText(const Trial& t) {
+  std::ostringstream s;
+  if (!t.first.passed) return "timing failed (" + t.first.errorMessage + ")";
+  s << "x" << t.first.speedup;
+  if (t.confirmation && t.confirmation->passed) s << ", again x" << t.confirmation->speedup;
+  s << (t.decision.admitted ? " -> admitted" : " -> not admitted: " + t.decision.reason);
+  return s.str();
+}
+
+// ------------------------------------------------------------------ decode GEMV
+// Builds one kernel over the tuning inputs, runs it once and checks its
+// output; null with `why` set when it cannot be used.
+using GemvBuilder = std::function<std::unique_ptr<hip::PreparedExecution>(
+    const hip::GeneratedKernel& kernel, std::string& why)>;
+
+// The sweep both tuneDecodeGEMV forms share: each candidate that passes the
+// hardware filter is built and checked, warmed, and put through a trial
+// against the baseline; the best conservative speedup is selected, else the
+// linear baseline.
+DecodeGEMVSelection sweepDecodeGEMV(hip::HipRuntime& runtime, std::size_t batch,
+                                    std::size_t inputSize, std::size_t outputSize,
+                                    const std::vector<hip::DecodeGEMVConfig>& candidates,
+                                    hip::ElementType outputType,
+                                    const benchmark::Sampler& baseline, const GemvBuilder& build,
+                                    std::size_t samples, std::ostream& log) {
+  DecodeGEMVSelection pick;
+  const auto hardware = runtime.hardwareInfo();
+  for (const auto& config : candidates) {
+    log << "[decode-gemv] " << describe(config) << ": ";
+    const std::string filtered =
+        decodeGEMVHardwareFilter(config, batch, inputSize, outputSize, hardware);
+    if (!filtered.empty()) {
+      log << "Hardware Filter drops it (" << filtered << ")\n";
+      continue;
+    }
+    std::string why;
+    std::unique_ptr<hip::PreparedExecution> built;
+    try {
+      built = build(hip::emitDecodeGEMV(batch, inputSize, outputSize, config,
+                                        "decode_gemv_candidate", hip::ElementType::Float16,
+                                        outputType),
+                    why);
+    } catch (const std::exception& e) {
+      why = e.what();
+    }
+    if (!built) {
+      log << "unusable (" << why << ")\n";
+      continue;
+    }
+    const auto sampler = benchmark::sampler(*built);
+    const std::string cold = benchmark::warmup(sampler, kTuningWarmup);
+    if (!cold.empty()) {
+      log << "warmup failed (" << cold << ")\n";
+      continue;
+    }
+    const Trial trial = runTrial(baseline, sampler, samples);
+    log << trialText(trial) << '\n';
+    if (trial.decision.admitted && trial.decision.conservativeSpeedup > pick.conservativeSpeedup) {
+      pick.useBaseline = false;
+      pick.config = config;
+      pick.conservativeSpeedup = trial.decision.conservativeSpeedup;
+    }
+  }
+  pick.success = true;
+  if (pick.useBaseline) pick.config = hip::DecodeGEMVConfig{4, 1, 1, 1};
+  log << "[decode-gemv] chosen: "
+      << (pick.useBaseline ? std::string("linear baseline") : describe(pick.config))
+      << " at x" << pick.conservativeSpeedup << '\n';
+  return pick;
+}
+
+// Resolve `kernel`, prepare it over fresh fp16 buffers holding `input` and
+// `weight`, run it once and compare with `expected` when given.
 std::unique_ptr<hip::PreparedExecution> prepareGemv(hip::HipRuntime& runtime,
                                                     const hip::GeneratedKernel& kernel,
                                                     const std::vector<float>& input,
                                                     const std::vector<float>& weight,
                                                     std::size_t outputCount,
                                                     const std::vector<double>& expected,
-                                                    std::string& error) {
-  const auto type = hip::ElementType::Float16;
+                                                    std::string& why) {
+  const auto fp16 = hip::ElementType::Float16;
   const auto pipeline = runtime.createComputePipeline(kernel.source, kernel.functionName);
-  if (!pipeline.pipelineCreationPassed) {
-    error = pipeline.errorMessage;
-    return {};
-  }
-  error = hip::checkBufferInterface(pipeline, {type, type}, type);
-  if (!error.empty()) return {};
-  auto prepared = runtime.prepare({{input.data(), input.size(), type},
-                                   {weight.data(), weight.size(), type}},
-                                  outputCount,
-                                  {kernel.threadgroupCount, kernel.threadsPerThreadgroup}, {},
-                                  type);
+  why = pipeline.pipelineCreationPassed ? hip::checkBufferInterface(pipeline, {fp16, fp16}, fp16)
+                                        : pipeline.errorMessage;
+  if (!why.empty()) return {};
+  auto prepared =
+      runtime.prepare({{input.data(), input.size(), fp16}, {weight.data(), weight.size(), fp16}},
+                      outputCount, {kernel.threadgroupCount, kernel.threadsPerThreadgroup}, {},
+                      fp16);
   if (!prepared.execution) {
-    error = prepared.errorMessage;
+    why = prepared.errorMessage;
     return {};
   }
-  const auto execution = prepared.execution->run();
-  if (!execution.executionPassed) {
-    error = execution.errorMessage;
+  const auto run = prepared.execution->run();
+  if (!run.executionPassed) {
+    why = run.errorMessage;
     return {};
   }
   if (!expected.empty()) {
-    const auto validation = validation::compare(execution.output, expected, 2e-2, 2e-2);
-    if (!validation.passed) {
-      error = validation.errorMessage;
+    const auto check = validation::compare(run.output, expected, 2e-2, 2e-2);
+    if (!check.passed) {
+      why = check.errorMessage;
       return {};
     }
   }
@@ -338,104 +429,52 @@ DecodeGEMVSelection tuneDecodeGEMV(hip::HipRuntime& runtime, std::size_t batch,
                                    const std::vector<float>& input,
                                    const std::vector<float>& weight, std::ostream& log,
                                    DType storageDtype, bool prefill) {
-  DecodeGEMVSelection result;
+  DecodeGEMVSelection fail;
   if (batch == 0 || inputSize == 0 || outputSize == 0 || input.size() != batch * inputSize ||
       weight.size() != outputSize * inputSize) {
-    result.errorMessage = "Decode GEMV tuning inputs do not match the shape.";
-    return result;
+    fail.errorMessage = "Decode GEMV tuning inputs do not match the shape.";
+    return fail;
   }
   if (storageDtype != DType::Float16) {
-    result.errorMessage = "gfx950 decode GEMV tuning supports fp16 storage.";
-    return result;
+    fail.errorMessage = "gfx950 decode GEMV tuning supports fp16 storage.";
+    return fail;
   }
-  const bool useCpuReference =
-      inputSize <= kMaximumCpuReferenceOperations / outputSize &&
-      batch <= kMaximumCpuReferenceOperations / (inputSize * outputSize);
-  const std::size_t samples = useCpuReference ? kTuningSamples : std::size_t{9};
-  auto expected = useCpuReference ? gemvReference(batch, inputSize, outputSize, input, weight)
-                                  : std::vector<double>{};
-  std::string error;
-  const auto baselineKernel =
-      hip::emitLinearBaseline(batch, inputSize, outputSize, "decode_gemv_baseline",
-                              hip::ElementType::Float16, hip::ElementType::Float16);
-  auto baseline = prepareGemv(runtime, baselineKernel, input, weight, batch * outputSize,
-                              expected, error);
+  // The CPU reference is affordable up to kMaximumCpuReferenceOperations
+  // multiply-adds; above it the baseline's own GPU output is the reference.
+  const bool cpuReference = inputSize <= kMaximumCpuReferenceOperations / outputSize &&
+                            batch <= kMaximumCpuReferenceOperations / (inputSize * outputSize);
+  std::vector<double> expected =
+      cpuReference ? gemvReference(batch, inputSize, outputSize, input, weight)
+                   : std::vector<double>{};
+  const GemvBuilder build = [&](const hip::GeneratedKernel& kernel, std::string& why) {
+    return prepareGemv(runtime, kernel, input, weight, batch * outputSize, expected, why);
+  };
+  std::string why;
+  auto baseline = build(hip::emitLinearBaseline(batch, inputSize, outputSize,
+                                                "decode_gemv_baseline", hip::ElementType::Float16,
+                                                hip::ElementType::Float16),
+                        why);
   if (!baseline) {
-    result.errorMessage = "Decode GEMV baseline failed: " + error;
-    return result;
+    fail.errorMessage = "Decode GEMV baseline failed: " + why;
+    return fail;
   }
-  if (!useCpuReference) {
+  if (!cpuReference) {
     const auto output = baseline->readOutputs().front();
     expected.assign(output.begin(), output.end());
-    log << "Decode GEMV large-shape validation: baseline GPU output is the reference\n";
   }
   const auto baselineSampler = benchmark::sampler(*baseline);
-  const auto warm = benchmark::warmup(baselineSampler, kTuningWarmup);
-  if (!warm.empty()) {
-    result.errorMessage = "Decode GEMV baseline warmup failed: " + warm;
-    return result;
+  const std::string cold = benchmark::warmup(baselineSampler, kTuningWarmup);
+  if (!cold.empty()) {
+    fail.errorMessage = "Decode GEMV baseline warmup failed: " + cold;
+    return fail;
   }
-  log << "Decode GEMV shape M=" << batch << ", K=" << inputSize << ", N=" << outputSize
-      << ", dtype=fp16, samples=" << samples << " | baseline validation/warmup: PASS\n";
-
-  const auto hardware = runtime.hardwareInfo();
-  double best = 1.0;
-  for (const auto& config : decodeGEMVCandidates(batch, prefill)) {
-    log << "  candidate " << configText(config);
-    const auto filter = decodeGEMVHardwareFilter(config, batch, inputSize, outputSize, hardware);
-    if (!filter.empty()) {
-      log << " | Hardware Filter: FAIL (" << filter << ")\n";
-      continue;
-    }
-    hip::GeneratedKernel kernel;
-    try {
-      kernel = hip::emitDecodeGEMV(batch, inputSize, outputSize, config, "decode_gemv_candidate",
-                                   hip::ElementType::Float16, hip::ElementType::Float16);
-    } catch (const std::exception& e) {
-      log << " | Emit: FAIL: " << e.what() << '\n';
-      continue;
-    }
-    auto candidate = prepareGemv(runtime, kernel, input, weight, batch * outputSize, expected,
-                                 error);
-    if (!candidate) {
-      log << " | Compile/interface/numerical: FAIL: " << error << '\n';
-      continue;
-    }
-    const auto candidateSampler = benchmark::sampler(*candidate);
-    const auto candidateWarm = benchmark::warmup(candidateSampler, kTuningWarmup);
-    if (!candidateWarm.empty()) {
-      log << " | Warmup: FAIL: " << candidateWarm << '\n';
-      continue;
-    }
-    const auto first = benchmark::measurePair(baselineSampler, candidateSampler, samples);
-    std::optional<benchmark::PairedResult> confirmation;
-    if (first.passed && first.speedup >= kMinimumSpeedup)
-      confirmation = benchmark::measurePair(baselineSampler, candidateSampler, samples);
-    const auto decision = admissionDecision(first, confirmation);
-    if (first.passed) log << " | validation: PASS, speedup=" << first.speedup << 'x';
-    if (confirmation && confirmation->passed)
-      log << ", confirmation=" << confirmation->speedup << 'x';
-    if (!decision.admitted) {
-      log << " -> fallback (" << decision.reason << ")\n";
-      continue;
-    }
-    log << " -> admitted\n";
-    if (decision.conservativeSpeedup > best) {
-      best = decision.conservativeSpeedup;
-      result.useBaseline = false;
-      result.config = config;
-      result.conservativeSpeedup = decision.conservativeSpeedup;
-    }
-  }
-  result.success = true;
-  if (result.useBaseline) {
-    result.config = hip::DecodeGEMVConfig{4, 1, 1, 1};
-    log << "Decode GEMV selected: linear baseline fallback\n";
-  } else {
-    log << "Decode GEMV selected: " << configText(result.config)
-        << ", conservative speedup=" << result.conservativeSpeedup << "x\n";
-  }
-  return result;
+  const std::size_t samples = cpuReference ? kTuningSamples : kLargeShapeSamples;
+  log << "[decode-gemv] " << batch << "x" << inputSize << " -> " << outputSize << " fp16; "
+      << (cpuReference ? "checked against the CPU double sums" : "checked against the baseline")
+      << "; " << samples << " paired samples per round\n";
+  return sweepDecodeGEMV(runtime, batch, inputSize, outputSize,
+                         decodeGEMVCandidates(batch, prefill), hip::ElementType::Float16,
+                         baselineSampler, build, samples, log);
 }
 
 DecodeGEMVSelection tuneDecodeGEMV(hip::HipRuntime& runtime, std::size_t batch,
@@ -443,116 +482,76 @@ DecodeGEMVSelection tuneDecodeGEMV(hip::HipRuntime& runtime, std::size_t batch,
                                    const hip::BufferHandle& input,
                                    const hip::BufferHandle& weight, std::ostream& log,
                                    hip::ElementType outputType) {
-  DecodeGEMVSelection result;
+  DecodeGEMVSelection fail;
+  const auto fp16 = hip::ElementType::Float16;
   if (!input || !weight || batch == 0 || inputSize == 0 || outputSize == 0 ||
       input->elementCount() < batch * inputSize ||
-      weight->elementCount() < outputSize * inputSize ||
-      input->elementType() != hip::ElementType::Float16 ||
-      weight->elementType() != hip::ElementType::Float16) {
-    result.errorMessage = "Decode GEMV tuning buffers do not match the shape (fp16 input, weight).";
-    return result;
+      weight->elementCount() < outputSize * inputSize || input->elementType() != fp16 ||
+      weight->elementType() != fp16) {
+    fail.errorMessage = "Decode GEMV tuning buffers do not match the shape (fp16 input, weight).";
+    return fail;
   }
-  const double tolerance = outputType == hip::ElementType::Float32 ? 2e-3 : 2e-2;
-  const std::size_t samples = 9;
   auto output = runtime.createBuffer(batch * outputSize, nullptr, outputType);
   if (!output.buffer) {
-    result.errorMessage = output.errorMessage;
-    return result;
+    fail.errorMessage = output.errorMessage;
+    return fail;
   }
-  auto prepare = [&](const hip::GeneratedKernel& kernel,
-                     std::string& error) -> std::unique_ptr<hip::PreparedExecution> {
+  // Every candidate writes the same output buffer; the baseline's run is the
+  // reference the others are checked against.
+  const double tolerance = outputType == hip::ElementType::Float32 ? 2e-3 : 2e-2;
+  std::vector<double> expected;
+  const GemvBuilder build = [&](const hip::GeneratedKernel& kernel,
+                                std::string& why) -> std::unique_ptr<hip::PreparedExecution> {
     const auto pipeline = runtime.createComputePipeline(kernel.source, kernel.functionName);
     if (!pipeline.pipelineCreationPassed) {
-      error = pipeline.errorMessage;
+      why = pipeline.errorMessage;
       return {};
     }
     auto prepared = runtime.prepareBuffers({input, weight}, output.buffer,
                                            {kernel.threadgroupCount, kernel.threadsPerThreadgroup});
-    if (!prepared.execution) error = prepared.errorMessage;
+    if (!prepared.execution) {
+      why = prepared.errorMessage;
+      return {};
+    }
+    const auto run = prepared.execution->run();
+    if (!run.executionPassed) {
+      why = run.errorMessage;
+      return {};
+    }
+    if (!expected.empty()) {
+      const auto check = validation::compare(run.output, expected, tolerance, tolerance);
+      if (!check.passed) {
+        why = check.errorMessage;
+        return {};
+      }
+    }
     return std::move(prepared.execution);
   };
-  std::string error;
-  auto baseline = prepare(hip::emitLinearBaseline(batch, inputSize, outputSize, "decode_gemv_baseline",
-                                                  hip::ElementType::Float16, outputType),
-                          error);
+  std::string why;
+  auto baseline = build(hip::emitLinearBaseline(batch, inputSize, outputSize,
+                                                "decode_gemv_baseline", fp16, outputType),
+                        why);
   if (!baseline) {
-    result.errorMessage = "Decode GEMV baseline failed: " + error;
-    return result;
+    fail.errorMessage = "Decode GEMV baseline failed: " + why;
+    return fail;
   }
-  const auto baseRun = baseline->run();
-  if (!baseRun.executionPassed) {
-    result.errorMessage = "Decode GEMV baseline failed: " + baseRun.errorMessage;
-    return result;
+  const auto first = baseline->readOutputs().front();
+  expected.assign(first.begin(), first.end());
+  if (!std::all_of(expected.begin(), expected.end(), [](double v) { return std::isfinite(v); })) {
+    fail.errorMessage = "Decode GEMV tuning input produced non-finite outputs.";
+    return fail;
   }
-  const std::vector<double> expected(baseRun.output.begin(), baseRun.output.end());
-  for (const double v : expected)
-    if (!std::isfinite(v)) {
-      result.errorMessage = "Decode GEMV tuning input produced non-finite outputs.";
-      return result;
-    }
   const auto baselineSampler = benchmark::sampler(*baseline);
-  const auto warm = benchmark::warmup(baselineSampler, kTuningWarmup);
-  if (!warm.empty()) {
-    result.errorMessage = "Decode GEMV baseline warmup failed: " + warm;
-    return result;
+  const std::string cold = benchmark::warmup(baselineSampler, kTuningWarmup);
+  if (!cold.empty()) {
+    fail.errorMessage = "Decode GEMV baseline warmup failed: " + cold;
+    return fail;
   }
-  log << "Decode GEMV shape M=" << batch << ", K=" << inputSize << ", N=" << outputSize
-      << " (device buffers, baseline output as reference, samples=" << samples << ")\n";
-  const auto hardware = runtime.hardwareInfo();
-  double best = 1.0;
-  for (const auto& config : decodeGEMVCandidates(batch)) {
-    log << "  candidate " << configText(config);
-    const auto filter = decodeGEMVHardwareFilter(config, batch, inputSize, outputSize, hardware);
-    if (!filter.empty()) {
-      log << " | Hardware Filter: FAIL (" << filter << ")\n";
-      continue;
-    }
-    auto candidate = prepare(hip::emitDecodeGEMV(batch, inputSize, outputSize, config,
-                                                 "decode_gemv_candidate", hip::ElementType::Float16,
-                                                 outputType),
-                             error);
-    if (!candidate) {
-      log << " | Compile/interface: FAIL: " << error << '\n';
-      continue;
-    }
-    const auto run = candidate->run();
-    const auto check = run.executionPassed
-                           ? validation::compare(run.output, expected, tolerance, tolerance)
-                           : validation::ValidationResult{};
-    if (!check.passed) {
-      log << " | numerical: FAIL: " << (run.executionPassed ? check.errorMessage : run.errorMessage)
-          << '\n';
-      continue;
-    }
-    const auto candidateSampler = benchmark::sampler(*candidate);
-    const auto candidateWarm = benchmark::warmup(candidateSampler, kTuningWarmup);
-    if (!candidateWarm.empty()) {
-      log << " | Warmup: FAIL: " << candidateWarm << '\n';
-      continue;
-    }
-    const auto first = benchmark::measurePair(baselineSampler, candidateSampler, samples);
-    std::optional<benchmark::PairedResult> confirmation;
-    if (first.passed && first.speedup >= kMinimumSpeedup)
-      confirmation = benchmark::measurePair(baselineSampler, candidateSampler, samples);
-    const auto decision = admissionDecision(first, confirmation);
-    if (first.passed) log << " | speedup=" << first.speedup << 'x';
-    if (!decision.admitted) {
-      log << " -> fallback (" << decision.reason << ")\n";
-      continue;
-    }
-    log << ", confirmed " << decision.conservativeSpeedup << "x -> admitted\n";
-    if (decision.conservativeSpeedup > best) {
-      best = decision.conservativeSpeedup;
-      result.useBaseline = false;
-      result.config = config;
-      result.conservativeSpeedup = decision.conservativeSpeedup;
-    }
-  }
-  result.success = true;
-  if (result.useBaseline) result.config = hip::DecodeGEMVConfig{4, 1, 1, 1};
-  log << "Decode GEMV selected: " << configText(result.config)
-      << ", conservative speedup=" << result.conservativeSpeedup << "x\n";
-  return result;
+  log << "[decode-gemv] " << batch << "x" << inputSize << " -> " << outputSize
+      << " on resident buffers, checked against the baseline; " << kLargeShapeSamples
+      << " paired samples per round\n";
+  return sweepDecodeGEMV(runtime, batch, inputSize, outputSize, decodeGEMVCandidates(batch),
+                         outputType, baselineSampler, build, kLargeShapeSamples, log);
 }
 
 std::string DecodeGEMVTuningCache::key(std::size_t batch, std::size_t inputSize,
@@ -584,7 +583,7 @@ DecodeGEMVSelection cachedDecodeGEMV(hip::HipRuntime& runtime, std::size_t batch
   auto& cache = decodeGEMVTuningCache();
   const auto key = DecodeGEMVTuningCache::key(batch, inputSize, outputSize, outputType);
   if (const auto hit = cache.find(key)) {
-    log << "Decode GEMV " << key << ": cached " << configText(hit->config) << '\n';
+    log << "[decode-gemv] " << key << ": reusing " << describe(hit->config) << '\n';
     return *hit;
   }
   auto selection = tuneDecodeGEMV(runtime, batch, inputSize, outputSize, input, weight, log,
@@ -610,84 +609,68 @@ std::string rmsNormHardwareFilter(const RMSNormOp& op, std::size_t threads,
 
 namespace {
 
-void reject(CandidateReport& report, const std::string& stage, const std::string& reason,
-            std::ostream& log) {
-  report.outcome = stage + " FAIL";
-  report.reason = reason;
-  log << report.name << " | " << stage << ": FAIL: " << reason << '\n';
-}
+// ------------------------------------------------------------------ RMSNorm
+// Where a kernel stopped on its way to being timed, and why.  The stage
+// names make up the reports' outcome text ("<stage> FAIL").
+struct Setback {
+  std::string stage;
+  std::string reason;
+};
 
-validation::ValidationResult validateExecution(const hip::ExecutionResult& execution,
-                                               const std::vector<double>& reference,
-                                               DType dtype) {
-  if (!execution.executionPassed) {
-    validation::ValidationResult r;
-    r.errorMessage = execution.errorMessage;
-    return r;
+validation::ValidationResult checkRMSNorm(const hip::ExecutionResult& run,
+                                          const std::vector<double>& reference, DType dtype) {
+  if (!run.executionPassed) {
+    validation::ValidationResult failed;
+    failed.errorMessage = run.errorMessage;
+    return failed;
   }
   const double tolerance = dtype == DType::Float16 ? 2e-3 : 1e-4;
-  return validation::compare(execution.output, reference, tolerance, tolerance);
+  return validation::compare(run.output, reference, tolerance, tolerance);
 }
 
-std::unique_ptr<hip::PreparedExecution> buildRMSNorm(hip::HipRuntime& runtime,
-                                                     const RMSNormOp& op,
+// Filter, emit, resolve, check the binding interface, prepare over the
+// inputs and validate one run; the setback says where it stopped.
+std::unique_ptr<hip::PreparedExecution> buildRMSNorm(hip::HipRuntime& runtime, const RMSNormOp& op,
                                                      const std::vector<float>& input,
                                                      const std::vector<float>& weight,
                                                      const std::vector<double>& reference,
-                                                     bool baseline, CandidateReport& report,
-                                                     std::ostream& log) {
-  const auto hardware = runtime.hardwareInfo();
-  const auto filter = rmsNormHardwareFilter(op, report.threads, hardware);
-  if (!filter.empty()) {
-    reject(report, "Hardware Filter", filter, log);
-    return {};
-  }
+                                                     std::size_t threads, bool baseline,
+                                                     Setback& setback, double& maxError) {
+  const auto stop = [&](const char* stage, std::string reason) {
+    setback = {stage, std::move(reason)};
+    return std::unique_ptr<hip::PreparedExecution>{};
+  };
+  const std::string filtered = rmsNormHardwareFilter(op, threads, runtime.hardwareInfo());
+  if (!filtered.empty()) return stop("Hardware Filter", filtered);
   hip::GeneratedKernel kernel;
   try {
-    kernel = baseline ? hip::emitRMSNormBaseline(op) : hip::emitRMSNorm(op, report.threads);
+    kernel = baseline ? hip::emitRMSNormBaseline(op) : hip::emitRMSNorm(op, threads);
   } catch (const std::exception& e) {
-    reject(report, "Emit", e.what(), log);
-    return {};
+    return stop("Emit", e.what());
   }
   const auto pipeline = runtime.createComputePipeline(kernel.source, kernel.functionName);
-  if (!pipeline.pipelineCreationPassed) {
-    reject(report, "Compile", pipeline.errorMessage, log);
-    return {};
-  }
-  const auto type = op.input.dtype == DType::Float16 ? hip::ElementType::Float16
-                                                     : hip::ElementType::Float32;
-  const auto interfaceError = hip::checkBufferInterface(pipeline, {type, type}, type);
-  if (!interfaceError.empty()) {
-    reject(report, "Interface Check", interfaceError, log);
-    return {};
-  }
-  auto prepared = runtime.prepare({{input.data(), input.size(), type},
-                                   {weight.data(), weight.size(), type}},
-                                  op.output.elementCount(),
-                                  {kernel.threadgroupCount, kernel.threadsPerThreadgroup}, {},
-                                  type);
-  if (!prepared.execution) {
-    reject(report, "Prepare", prepared.errorMessage, log);
-    return {};
-  }
-  const auto check = validateExecution(prepared.execution->run(), reference, op.output.dtype);
-  if (!check.passed) {
-    reject(report, "Numerical Validate", check.errorMessage, log);
-    return {};
-  }
-  log << report.name << " | Numerical Validate: PASS, max absolute error="
-      << check.maxAbsoluteError << '\n';
-  report.outcome = "Correctness PASS";
+  if (!pipeline.pipelineCreationPassed) return stop("Compile", pipeline.errorMessage);
+  const auto type =
+      op.input.dtype == DType::Float16 ? hip::ElementType::Float16 : hip::ElementType::Float32;
+  const std::string mismatch = hip::checkBufferInterface(pipeline, {type, type}, type);
+  if (!mismatch.empty()) return stop("Interface Check", mismatch);
+  auto prepared =
+      runtime.prepare({{input.data(), input.size(), type}, {weight.data(), weight.size(), type}},
+                      op.output.elementCount(),
+                      {kernel.threadgroupCount, kernel.threadsPerThreadgroup}, {}, type);
+  if (!prepared.execution) return stop("Prepare", prepared.errorMessage);
+  const auto check = checkRMSNorm(prepared.execution->run(), reference, op.output.dtype);
+  if (!check.passed) return stop("Numerical Validate", check.errorMessage);
+  maxError = check.maxAbsoluteError;
   return std::move(prepared.execution);
 }
 
-void printReport(const CandidateReport& report, std::ostream& log) {
-  log << "  " << report.name << " | threads=" << report.threads;
-  if (report.medianGpuUs) log << " | GPU median(us)=" << *report.medianGpuUs;
-  if (report.pairedBaselineUs) log << " | paired baseline(us)=" << *report.pairedBaselineUs;
-  if (report.speedup) log << " | speedup=" << *report.speedup << 'x';
-  log << " | " << report.outcome;
-  if (!report.reason.empty()) log << " (" << report.reason << ')';
+void summarize(const CandidateReport& r, std::ostream& log) {
+  log << "[rmsnorm]   " << r.name << " (" << r.threads << " threads): " << r.outcome;
+  if (!r.reason.empty()) log << " - " << r.reason;
+  if (r.medianGpuUs) log << "; median " << *r.medianGpuUs << " us";
+  if (r.pairedBaselineUs) log << " vs baseline " << *r.pairedBaselineUs << " us";
+  if (r.speedup) log << ", x" << *r.speedup;
   log << '\n';
 }
 
@@ -704,94 +687,97 @@ TuningResult tuneRMSNorm(hip::HipRuntime& runtime, const RMSNormOp& op,
     result.errorMessage = e.what();
     return result;
   }
-  log << "Enumerate: threads={";
-  for (std::size_t i = 0; i < candidateThreads.size(); ++i)
-    log << (i ? ", " : "") << candidateThreads[i];
-  log << "}\nCPU correctness baseline: double-accumulation reference\n"
-      << "GPU performance baseline: fixed 256-thread two-pass RMSNorm\n"
-      << "Warmup=" << kTuningWarmup << ", samples=" << kTuningSamples
-      << ", admission requires >= " << kMinimumSpeedup << "x in two paired rounds\n";
+  log << "[rmsnorm] " << candidateThreads.size() << " workgroup sizes against the 256-thread "
+      << "two-pass kernel; outputs checked against the CPU double reference; a winner needs x"
+      << kMinimumSpeedup << " in two paired rounds of " << kTuningSamples << " samples after "
+      << kTuningWarmup << " warmup runs\n";
+  const auto setBack = [&](CandidateReport& r, const Setback& s) {
+    r.outcome = s.stage + " FAIL";
+    r.reason = s.reason;
+    log << "[rmsnorm] " << r.name << " stopped at " << s.stage << ": " << s.reason << '\n';
+  };
 
   result.baseline.name = "baseline";
   result.baseline.threads = 256;
-  auto baseline = buildRMSNorm(runtime, op, input, weight, reference, true, result.baseline, log);
+  Setback setback;
+  double maxError = 0.0;
+  auto baseline = buildRMSNorm(runtime, op, input, weight, reference, 256, true, setback, maxError);
   if (!baseline) {
-    result.errorMessage = "Baseline failed; no valid fallback: " + result.baseline.reason;
+    setBack(result.baseline, setback);
+    result.errorMessage = "Baseline failed; no valid fallback: " + setback.reason;
     return result;
   }
   const auto baselineSampler = benchmark::sampler(*baseline);
-  const auto warm = benchmark::warmup(baselineSampler, kTuningWarmup);
-  if (!warm.empty()) {
-    reject(result.baseline, "Warmup", warm, log);
-    result.errorMessage = "Baseline warmup failed; no valid fallback: " + warm;
+  const std::string cold = benchmark::warmup(baselineSampler, kTuningWarmup);
+  if (!cold.empty()) {
+    setBack(result.baseline, {"Warmup", cold});
+    result.errorMessage = "Baseline warmup failed; no valid fallback: " + cold;
     return result;
   }
-  const auto baselineTiming = benchmark::measure(baselineSampler, kTuningSamples);
-  if (baselineTiming.passed) {
-    result.baseline.medianGpuUs = baselineTiming.stats.medianUs;
-    result.baseline.outcome = "Fallback ready";
-  } else {
-    result.baseline.outcome = "Performance unavailable";
-    result.baseline.reason = baselineTiming.errorMessage;
-  }
+  const auto alone = benchmark::measure(baselineSampler, kTuningSamples);
+  result.baseline.outcome = alone.passed ? "Fallback ready" : "Performance unavailable";
+  if (alone.passed) result.baseline.medianGpuUs = alone.stats.medianUs;
+  else result.baseline.reason = alone.errorMessage;
 
   std::unique_ptr<hip::PreparedExecution> winner;
   std::size_t winnerIndex = 0;
-  double best = 1.0;
+  double bestSpeedup = 1.0;
   for (const std::size_t threads : candidateThreads) {
-    CandidateReport report;
+    result.candidates.push_back({});
+    CandidateReport& report = result.candidates.back();
     report.name = "candidate_" + std::to_string(threads);
     report.threads = threads;
-    result.candidates.push_back(std::move(report));
-    auto& current = result.candidates.back();
-    auto candidate = buildRMSNorm(runtime, op, input, weight, reference, false, current, log);
-    if (!candidate) continue;
-    const auto candidateSampler = benchmark::sampler(*candidate);
-    const auto candidateWarm = benchmark::warmup(candidateSampler, kTuningWarmup);
-    if (!candidateWarm.empty()) {
-      reject(current, "Warmup", candidateWarm, log);
+    auto candidate =
+        buildRMSNorm(runtime, op, input, weight, reference, threads, false, setback, maxError);
+    if (!candidate) {
+      setBack(report, setback);
       continue;
     }
-    if (!baselineTiming.passed) {
-      current.outcome = "Not admitted";
-      current.reason = "No usable baseline timing; performance comparison skipped.";
+    log << "[rmsnorm] " << report.name << " matches the reference (max error " << maxError
+        << ")\n";
+    const auto sampler = benchmark::sampler(*candidate);
+    const std::string warm = benchmark::warmup(sampler, kTuningWarmup);
+    if (!warm.empty()) {
+      setBack(report, {"Warmup", warm});
       continue;
     }
-    const auto first = benchmark::measurePair(baselineSampler, candidateSampler, kTuningSamples);
-    if (first.passed) {
-      current.medianGpuUs = first.candidate.medianUs;
-      current.pairedBaselineUs = first.baseline.medianUs;
-      current.speedup = first.speedup;
-    }
-    std::optional<benchmark::PairedResult> confirmation;
-    if (first.passed && first.speedup >= kMinimumSpeedup)
-      confirmation = benchmark::measurePair(baselineSampler, candidateSampler, kTuningSamples);
-    const auto decision = admissionDecision(first, confirmation);
-    if (confirmation && confirmation->passed) current.speedup = decision.conservativeSpeedup;
-    if (!decision.admitted) {
-      reject(current, "Compare Baseline", decision.reason, log);
+    if (!alone.passed) {
+      report.outcome = "Not admitted";
+      report.reason = "the baseline could not be timed, so nothing is compared";
       continue;
     }
-    current.outcome = "Admitted";
-    log << current.name << " | Compare Baseline: PASS -> Admit\n";
-    if (decision.conservativeSpeedup > best) {
-      best = decision.conservativeSpeedup;
+    const Trial trial = runTrial(baselineSampler, sampler, kTuningSamples);
+    if (trial.first.passed) {
+      report.medianGpuUs = trial.first.candidate.medianUs;
+      report.pairedBaselineUs = trial.first.baseline.medianUs;
+      report.speedup = trial.decision.conservativeSpeedup;
+    }
+    if (!trial.decision.admitted) {
+      setBack(report, {"Compare Baseline", trial.decision.reason});
+      continue;
+    }
+    report.outcome = "Admitted";
+    log << "[rmsnorm] " << report.name << " admitted at x" << trial.decision.conservativeSpeedup
+        << '\n';
+    if (trial.decision.conservativeSpeedup > bestSpeedup) {
+      bestSpeedup = trial.decision.conservativeSpeedup;
       winnerIndex = result.candidates.size() - 1;
       winner = std::move(candidate);
     }
   }
 
-  // Run the selection once more with fresh sentinel outputs and readback.
-  result.finalExecution = winner ? winner->run() : baseline->run();
-  result.finalValidation = validateExecution(result.finalExecution, reference, op.output.dtype);
-  if (!result.finalValidation.passed && winner) {
-    reject(result.candidates[winnerIndex], "Final execution",
-           result.finalValidation.errorMessage, log);
+  // The selection runs once more from fresh sentinel outputs with a
+  // readback; a winner that fails there gives way to the baseline.
+  const auto finalRun = [&](hip::PreparedExecution& execution) {
+    result.finalExecution = execution.run();
+    result.finalValidation = checkRMSNorm(result.finalExecution, reference, op.output.dtype);
+    return result.finalValidation.passed;
+  };
+  if (winner && !finalRun(*winner)) {
+    setBack(result.candidates[winnerIndex], {"Final execution", result.finalValidation.errorMessage});
     winner.reset();
-    result.finalExecution = baseline->run();
-    result.finalValidation = validateExecution(result.finalExecution, reference, op.output.dtype);
   }
-  if (!result.finalValidation.passed) {
+  if (!winner && !finalRun(*baseline)) {
     result.errorMessage =
         "Final baseline execution/validation failed: " + result.finalValidation.errorMessage;
     return result;
@@ -800,13 +786,12 @@ TuningResult tuneRMSNorm(hip::HipRuntime& runtime, const RMSNormOp& op,
   result.selectedThreads = winner ? result.candidates[winnerIndex].threads : 256;
   result.selectedExecution = winner ? std::move(winner) : std::move(baseline);
   result.success = true;
-  log << "Admission report (speedup is the lower of both rounds when confirmed):\n";
-  printReport(result.baseline, log);
-  for (const auto& report : result.candidates) printReport(report, log);
-  log << "Selected: "
-      << (result.usedBaseline ? std::string("baseline (fallback)")
-                              : result.candidates[winnerIndex].name)
-      << ", threads=" << result.selectedThreads << '\n';
+  log << "[rmsnorm] summary (x = the lower speedup of the two rounds once confirmed):\n";
+  summarize(result.baseline, log);
+  for (const auto& report : result.candidates) summarize(report, log);
+  log << "[rmsnorm] chosen: "
+      << (result.usedBaseline ? std::string("the baseline") : result.candidates[winnerIndex].name)
+      << " at " << result.selectedThreads << " threads\n";
   return result;
 }
 
@@ -815,14 +800,77 @@ TuningResult tuneRMSNorm(hip::HipRuntime& runtime, const RMSNormOp& op,
 namespace runtime {
 namespace {
 
-std::unique_ptr<hip::PreparedSequence> makeSequence(
+// The deterministic fusion test pattern: element i holds ((i mod 31) - 15) / 31.
+std::vector<float> fusionTestPattern(std::size_t count) {
+  std::vector<float> v(count);
+  for (std::size_t i = 0; i < count; ++i)
+    v[i] = static_cast<float>(static_cast<int>(i % 31) - 15) / 31.0f;
+  return v;
+}
+
+std::unique_ptr<hip::PreparedSequence> sequenceOf(
     hip::HipRuntime& runtime, const std::vector<std::unique_ptr<hip::PreparedExecution>>& steps,
-    std::size_t begin = 0) {
+    std::size_t begin) {
   std::vector<const hip::PreparedExecution*> pointers;
   for (std::size_t i = begin; i < steps.size(); ++i) pointers.push_back(steps[i].get());
   auto prepared = runtime.prepareSequence(pointers);
   if (!prepared.execution) throw std::runtime_error(prepared.errorMessage);
   return std::move(prepared.execution);
+}
+
+// Run `sequence`; "" when every output agrees with its reference (2e-3 for
+// fp32 outputs, 2e-2 for fp16/bf16), else the first disagreement.
+std::string agrees(hip::PreparedSequence& sequence, const std::vector<hip::BufferHandle>& outputs,
+                   const std::vector<std::vector<double>>& references) {
+  const auto run = sequence.execute();
+  if (!run.executionPassed) return run.errorMessage;
+  for (std::size_t i = 0; i < outputs.size(); ++i) {
+    const double tolerance = outputs[i]->elementType() == hip::ElementType::Float32 ? 2e-3 : 2e-2;
+    const auto check = validation::compare(outputs[i]->read(), references[i], tolerance, tolerance);
+    if (!check.passed) return check.errorMessage;
+  }
+  return {};
+}
+
+// The fused steps take the region's place at the end of `steps`.
+void splice(std::vector<std::unique_ptr<hip::PreparedExecution>>& steps, std::size_t begin,
+            std::vector<std::unique_ptr<hip::PreparedExecution>> fused) {
+  steps.resize(begin);
+  for (auto& step : fused) steps.push_back(std::move(step));
+}
+
+// Whether the fused steps stand in for steps[begin..]: the same outputs on
+// the test pattern before and after timing, and the lower of two paired
+// rounds; throws with the reason when the comparison cannot be made.
+double fusionSpeedup(hip::HipRuntime& runtime, hip::PreparedSequence& unfused,
+                     hip::PreparedSequence& fused, const std::vector<hip::BufferHandle>& testInputs,
+                     const std::vector<hip::BufferHandle>& outputs) {
+  for (const auto& input : testInputs) {
+    const auto data = fusionTestPattern(input->elementCount());
+    const auto error = runtime.writeBuffer(input, data.data(), data.size());
+    if (!error.empty()) throw std::runtime_error(error);
+  }
+  const auto reference = unfused.execute();
+  if (!reference.executionPassed) throw std::runtime_error(reference.errorMessage);
+  std::vector<std::vector<double>> expected;
+  for (const auto& output : outputs) {
+    const auto values = output->read();
+    expected.emplace_back(values.begin(), values.end());
+  }
+  if (auto why = agrees(fused, outputs, expected); !why.empty()) throw std::runtime_error(why);
+  const auto before = benchmark::sampler(unfused);
+  const auto after = benchmark::sampler(fused);
+  for (const auto* s : {&before, &after})
+    if (auto why = benchmark::warmup(*s, planner::kTuningWarmup); !why.empty())
+      throw std::runtime_error(why);
+  double slowest = std::numeric_limits<double>::infinity();
+  for (int round = 0; round < 2; ++round) {
+    const auto timing = benchmark::measurePair(before, after, planner::kTuningSamples);
+    if (!timing.passed) throw std::runtime_error("Fusion benchmark failed.");
+    slowest = std::min(slowest, timing.speedup);
+  }
+  if (auto why = agrees(fused, outputs, expected); !why.empty()) throw std::runtime_error(why);
+  return slowest;
 }
 
 }  // namespace
@@ -834,158 +882,51 @@ bool admitFusion(hip::HipRuntime& runtime,
                  const std::vector<hip::BufferHandle>& outputs, const std::string& name,
                  const std::string& decisionKey, FusionDecisionCache& decisions,
                  std::ostream& log) {
-  try {
-    const auto cached = decisions.find(decisionKey);
-    if (cached != decisions.end()) {
-      if (!cached->second) {
-        log << "Fusion " << name << ": cached FALLBACK\n";
-        return false;
-      }
-      auto fused = build();
-      steps.resize(begin);
-      for (auto& step : fused) steps.push_back(std::move(step));
-      log << "Fusion " << name << ": cached ADMITTED\n";
+  if (const auto known = decisions.find(decisionKey); known != decisions.end()) {
+    log << "Fusion " << name << ": cached decision, " << (known->second ? "fused" : "unfused")
+        << '\n';
+    if (!known->second) return false;
+    try {
+      splice(steps, begin, build());
       return true;
+    } catch (const std::exception& e) {
+      log << "Fusion " << name << ": rebuild error: " << e.what() << '\n';
+      return false;
     }
+  }
+  bool admitted = false;
+  try {
     if (begin > steps.size()) throw std::runtime_error("Fusion region starts past the steps.");
     auto fused = build();
-    auto candidate = makeSequence(runtime, fused);
-    auto baseline = makeSequence(runtime, steps, begin);
-    for (const auto& input : testInputs) {
-      std::vector<float> data(input->elementCount());
-      for (std::size_t i = 0; i < data.size(); ++i)
-        data[i] = static_cast<float>(static_cast<int>(i % 31) - 15) / 31.0f;
-      const auto error = runtime.writeBuffer(input, data.data(), data.size());
-      if (!error.empty()) throw std::runtime_error(error);
-    }
-    const auto baseRun = baseline->execute();
-    if (!baseRun.executionPassed) throw std::runtime_error(baseRun.errorMessage);
-    std::vector<std::vector<double>> references;
-    for (const auto& output : outputs) {
-      const auto values = output->read();
-      references.emplace_back(values.begin(), values.end());
-    }
-    auto validateCandidate = [&]() {
-      const auto run = candidate->execute();
-      if (!run.executionPassed) throw std::runtime_error(run.errorMessage);
-      for (std::size_t i = 0; i < outputs.size(); ++i) {
-        const double tolerance =
-            outputs[i]->elementType() == hip::ElementType::Float32 ? 2e-3 : 2e-2;
-        const auto comparison =
-            validation::compare(outputs[i]->read(), references[i], tolerance, tolerance);
-        if (!comparison.passed) throw std::runtime_error(comparison.errorMessage);
-      }
-    };
-    validateCandidate();
-    const auto baseSampler = benchmark::sampler(*baseline);
-    const auto fusedSampler = benchmark::sampler(*candidate);
-    for (const auto* sampler : {&baseSampler, &fusedSampler}) {
-      const auto error = benchmark::warmup(*sampler, planner::kTuningWarmup);
-      if (!error.empty()) throw std::runtime_error(error);
-    }
-    const auto first =
-        benchmark::measurePair(baseSampler, fusedSampler, planner::kTuningSamples);
-    const auto second =
-        benchmark::measurePair(baseSampler, fusedSampler, planner::kTuningSamples);
-    if (!first.passed || !second.passed) throw std::runtime_error("Fusion benchmark failed.");
-    validateCandidate();
-    const double speedup = std::min(first.speedup, second.speedup);
-    const bool admitted = speedup >= planner::kMinimumSpeedup;
-    log << "Fusion " << name << ": compile/interface/template-comparison PASS, speedup="
-        << speedup << "x, " << (admitted ? "ADMITTED" : "FALLBACK") << '\n';
-    if (admitted) {
-      steps.resize(begin);
-      for (auto& step : fused) steps.push_back(std::move(step));
-    }
-    decisions.emplace(decisionKey, admitted);
-    return admitted;
+    auto fusedSequence = sequenceOf(runtime, fused, 0);
+    auto unfusedSequence = sequenceOf(runtime, steps, begin);
+    const double speedup =
+        fusionSpeedup(runtime, *unfusedSequence, *fusedSequence, testInputs, outputs);
+    admitted = speedup >= planner::kMinimumSpeedup;
+    log << "Fusion " << name << ": outputs agree, x" << speedup << " over the unfused steps -> "
+        << (admitted ? "fused" : "unfused") << '\n';
+    if (admitted) splice(steps, begin, std::move(fused));
   } catch (const std::exception& e) {
-    decisions[decisionKey] = false;
-    log << "Fusion " << name << ": FALLBACK: " << e.what() << '\n';
-    return false;
+    log << "Fusion " << name << ": error: " << e.what() << " -> unfused\n";
+    admitted = false;
   }
+  decisions[decisionKey] = admitted;
+  return admitted;
 }
 
 namespace {
 
 constexpr std::size_t kGuardElements = 512;
 
-struct Feedback {
-  Feedback(std::string status_, std::string stage_, std::string message_,
-           std::optional<double> baseline = std::nullopt,
-           std::optional<double> candidate = std::nullopt,
-           std::optional<double> ratio = std::nullopt)
-      : status(std::move(status_)), stage(std::move(stage_)), message(std::move(message_)),
-        baselineUs(baseline), candidateUs(candidate), speedup(ratio) {}
-  std::string status;
-  std::string stage;
-  std::string message;
-  std::optional<double> baselineUs;
-  std::optional<double> candidateUs;
-  std::optional<double> speedup;
-};
-
-std::string escapeJson(const std::string& text) {
-  std::ostringstream out;
-  const char hex[] = "0123456789abcdef";
-  for (const unsigned char c : text) {
-    switch (c) {
-    case '"': out << "\\\""; break;
-    case '\\': out << "\\\\"; break;
-    case '\n': out << "\\n"; break;
-    case '\r': out << "\\r"; break;
-    case '\t': out << "\\t"; break;
-    default:
-      if (c < 0x20) out << "\\u00" << hex[c >> 4] << hex[c & 0xf];
-      else out << static_cast<char>(c);
-    }
-  }
-  return out.str();
+std::vector<float> contractPattern(std::size_t count, std::size_t salt, float scale, float offset) {
+  std::vector<float> v(count);
+  for (std::size_t i = 0; i < count; ++i)
+    v[i] = offset + scale * static_cast<float>(static_cast<int>((i * 7 + salt) % 29) - 14) / 14.0f;
+  return v;
 }
 
-std::string writeFeedback(const Feedback& f, const std::string& path) {
-  std::ofstream out(path);
-  if (!out) return "Unable to open generated-kernel feedback output '" + path + "'.";
-  out << "{\n  \"version\":1,\n  \"status\":\"" << escapeJson(f.status) << "\",\n  \"stage\":\""
-      << escapeJson(f.stage) << "\",\n  \"message\":\"" << escapeJson(f.message)
-      << "\",\n  \"metrics\":";
-  if (f.baselineUs && f.candidateUs && f.speedup)
-    out << "{\"baseline_median_us\":" << *f.baselineUs
-        << ",\"candidate_median_us\":" << *f.candidateUs << ",\"speedup\":" << *f.speedup << '}';
-  else
-    out << "null";
-  out << "\n}\n";
-  if (!out) return "Failed while writing generated-kernel feedback '" + path + "'.";
-  return {};
-}
-
-// The few JSON fields a candidate response carries: flat object, string or
-// integer values.
-bool jsonField(const std::string& text, const std::string& key, std::string& value) {
-  const auto at = text.find("\"" + key + "\"");
-  if (at == std::string::npos) return false;
-  auto pos = text.find(':', at + key.size() + 2);
-  if (pos == std::string::npos) return false;
-  ++pos;
-  while (pos < text.size() && std::isspace(static_cast<unsigned char>(text[pos]))) ++pos;
-  if (pos < text.size() && text[pos] == '"') {
-    std::string out;
-    for (++pos; pos < text.size() && text[pos] != '"'; ++pos) {
-      if (text[pos] == '\\' && pos + 1 < text.size()) ++pos;
-      out.push_back(text[pos]);
-    }
-    if (pos >= text.size()) return false;
-    value = out;
-    return true;
-  }
-  const auto end = text.find_first_of(",}\n", pos);
-  value = text.substr(pos, end == std::string::npos ? std::string::npos : end - pos);
-  while (!value.empty() && std::isspace(static_cast<unsigned char>(value.back()))) value.pop_back();
-  return !value.empty();
-}
-
-// A contract case: named inputs (host floats) and the outputs the kernel
-// writes, with the template kernel key that produces the reference outputs.
+// One case of a region contract: its inputs, the sizes of the outputs and
+// the template kernel key that writes the reference outputs.
 struct ContractCase {
   std::vector<std::vector<float>> inputs;
   std::vector<std::size_t> outputCounts;
@@ -993,7 +934,8 @@ struct ContractCase {
 };
 
 struct Contract {
-  std::string functionName;
+  std::string pattern;       // registry name (decoder_...)
+  std::string functionName;  // kernel key name a candidate must use
   hip::ElementType storage = hip::ElementType::Float16;
   std::vector<std::string> outputNames;
   std::vector<std::size_t> workgroupSizes;
@@ -1001,40 +943,36 @@ struct Contract {
   std::vector<ContractCase> cases;
 };
 
-std::vector<float> pattern(std::size_t count, std::size_t salt, float scale, float offset) {
-  std::vector<float> v(count);
-  for (std::size_t i = 0; i < count; ++i)
-    v[i] = offset + scale * static_cast<float>(static_cast<int>((i * 7 + salt) % 29) - 14) / 14.0f;
-  return v;
-}
-
-Contract makeContract(const std::string& name) {
+Contract contractFor(const std::string& name) {
   Contract c;
   c.workgroupSizes = {64, 128, 256, 512, 1024};
-  if (name == "RMSNorm" || name == "AddRMSNorm") {
-    const bool add = name == "AddRMSNorm";
-    c.functionName = add ? "add_rmsnorm" : "rmsnorm";
-    c.outputNames = add ? std::vector<std::string>{"sum", "norm"} : std::vector<std::string>{"out"};
-    for (const auto& shape : {std::pair<std::size_t, std::size_t>{1, 4096}, {3, 4096}}) {
+  const bool norm = name == "RMSNorm" || name == "decoder_rmsnorm";
+  const bool addNorm = name == "AddRMSNorm" || name == "decoder_residual_rmsnorm";
+  if (norm || addNorm) {
+    c.pattern = addNorm ? "decoder_residual_rmsnorm" : "decoder_rmsnorm";
+    c.functionName = addNorm ? "add_rmsnorm" : "rmsnorm";
+    c.outputNames = addNorm ? std::vector<std::string>{"sum", "norm"}
+                            : std::vector<std::string>{"out"};
+    for (const std::size_t rows : {std::size_t{1}, std::size_t{3}}) {
+      const std::size_t width = 4096, n = rows * width;
       ContractCase k;
-      const std::size_t n = shape.first * shape.second;
-      k.inputs.push_back(pattern(n, 1, 1.0f, 0.0f));
-      if (add) k.inputs.push_back(pattern(n, 5, 1.0f, 0.0f));
-      k.inputs.push_back(pattern(shape.second, 3, 0.5f, 1.0f));
-      k.outputCounts = add ? std::vector<std::size_t>{n, n} : std::vector<std::size_t>{n};
-      k.templateKey = std::string(add ? "add_rmsnorm" : "rmsnorm") + "?rows=" +
-                      std::to_string(shape.first) + "&width=" + std::to_string(shape.second) +
-                      "&eps=1e-06&dtype=f16";
+      k.inputs.push_back(contractPattern(n, 1, 1.0f, 0.0f));
+      if (addNorm) k.inputs.push_back(contractPattern(n, 5, 1.0f, 0.0f));
+      k.inputs.push_back(contractPattern(width, 3, 0.5f, 1.0f));
+      k.outputCounts.assign(c.outputNames.size(), n);
+      k.templateKey = c.functionName + "?rows=" + std::to_string(rows) +
+                      "&width=" + std::to_string(width) + "&eps=1e-06&dtype=f16";
       c.cases.push_back(std::move(k));
     }
     return c;
   }
-  if (name == "SiLUMul") {
+  if (name == "SiLUMul" || name == "decoder_silu_mul") {
+    c.pattern = "decoder_silu_mul";
     c.functionName = "silu_mul";
     c.outputNames = {"out"};
     for (const std::size_t n : {std::size_t{11008}, std::size_t{8 * 11008}}) {
       ContractCase k;
-      k.inputs = {pattern(n, 2, 4.0f, 0.0f), pattern(n, 9, 2.0f, 0.0f)};
+      k.inputs = {contractPattern(n, 2, 4.0f, 0.0f), contractPattern(n, 9, 2.0f, 0.0f)};
       k.outputCounts = {n};
       k.templateKey = "silu_mul?count=" + std::to_string(n) + "&dtype=f16";
       c.cases.push_back(std::move(k));
@@ -1045,77 +983,75 @@ Contract makeContract(const std::string& name) {
                               "' (RMSNorm, AddRMSNorm, SiLUMul).");
 }
 
-// The candidate key must name the contract's function with the case's shape
-// parameters; the response gives the key for the first case and the other
-// cases reuse its tuning parameters.
-std::string keyForCase(const std::string& responseKey, const ContractCase& data) {
-  const auto q = responseKey.find('?');
+// The launch parameters a candidate key sets (threads, variant); the other
+// cases of a contract run the same parameters on their own shapes.
+std::string tuningOf(const std::string& key) {
   std::string tuning;
-  if (q != std::string::npos) {
-    std::stringstream items(responseKey.substr(q + 1));
-    std::string item;
-    while (std::getline(items, item, '&')) {
-      const auto eq = item.find('=');
-      const auto field = item.substr(0, eq);
-      if (field == "threads" || field == "variant") tuning += "&" + item;
-    }
+  const auto q = key.find('?');
+  if (q == std::string::npos) return tuning;
+  std::stringstream items(key.substr(q + 1));
+  for (std::string item; std::getline(items, item, '&');) {
+    const std::string field = item.substr(0, item.find('='));
+    if (field == "threads" || field == "variant") tuning += "&" + item;
   }
-  return data.templateKey + tuning;
+  return tuning;
 }
 
-struct CaseRun {
+// A contract case prepared over its own buffers, as one-step sequence.
+struct CaseRig {
   std::unique_ptr<hip::PreparedExecution> execution;
   std::unique_ptr<hip::PreparedSequence> sequence;
   std::vector<hip::BufferHandle> outputs;
 };
 
-CaseRun prepareCase(hip::HipRuntime& runtime, const Contract& contract, const ContractCase& data,
-                    const std::string& key, const std::string& functionName, bool guarded) {
-  const auto pipeline = runtime.createComputePipeline(key, functionName);
+// `guarded`: every buffer gets kGuardElements extra elements (inputs 1.0,
+// outputs NaN) that a correct kernel never touches.
+CaseRig rigCase(hip::HipRuntime& runtime, const Contract& contract, const ContractCase& data,
+                const std::string& key, bool guarded) {
+  const auto pipeline = runtime.createComputePipeline(key, contract.functionName);
   if (!pipeline.pipelineCreationPassed) throw std::runtime_error(pipeline.errorMessage);
-  CaseRun run;
+  const std::size_t extra = guarded ? kGuardElements : 0;
   std::vector<hip::BufferHandle> inputs;
-  for (const auto& values : data.inputs) {
-    auto padded = values;
-    if (guarded) padded.resize(padded.size() + kGuardElements, 1.0f);
-    auto buffer = runtime.createBuffer(padded.size(), padded.data(), contract.storage);
-    if (!buffer.buffer) throw std::runtime_error(buffer.errorMessage);
-    inputs.push_back(std::move(buffer.buffer));
+  for (auto values : data.inputs) {
+    values.resize(values.size() + extra, 1.0f);
+    auto made = runtime.createBuffer(values.size(), values.data(), contract.storage);
+    if (!made.buffer) throw std::runtime_error(made.errorMessage);
+    inputs.push_back(std::move(made.buffer));
   }
+  CaseRig rig;
   for (const auto count : data.outputCounts) {
-    auto buffer =
-        runtime.createBuffer(count + (guarded ? kGuardElements : 0), nullptr, contract.storage);
-    if (!buffer.buffer) throw std::runtime_error(buffer.errorMessage);
-    run.outputs.push_back(std::move(buffer.buffer));
+    auto made = runtime.createBuffer(count + extra, nullptr, contract.storage);
+    if (!made.buffer) throw std::runtime_error(made.errorMessage);
+    rig.outputs.push_back(std::move(made.buffer));
   }
   auto prepared = runtime.prepareBuffers(
-      inputs, run.outputs, {pipeline.threadgroupCount, pipeline.threadsPerThreadgroup});
+      inputs, rig.outputs, {pipeline.threadgroupCount, pipeline.threadsPerThreadgroup});
   if (!prepared.execution) throw std::runtime_error(prepared.errorMessage);
-  run.execution = std::move(prepared.execution);
-  auto sequence = runtime.prepareSequence({run.execution.get()});
+  rig.execution = std::move(prepared.execution);
+  auto sequence = runtime.prepareSequence({rig.execution.get()});
   if (!sequence.execution) throw std::runtime_error(sequence.errorMessage);
-  run.sequence = std::move(sequence.execution);
-  return run;
+  rig.sequence = std::move(sequence.execution);
+  return rig;
 }
 
-std::string validateCase(hip::HipRuntime& runtime, CaseRun& run, const Contract& contract,
-                         const ContractCase& data,
-                         const std::vector<std::vector<double>>& references, bool guarded) {
-  for (const auto& output : run.outputs) {
-    std::vector<float> sentinel(output->elementCount(), std::numeric_limits<float>::quiet_NaN());
-    const auto error = runtime.writeBuffer(output, sentinel.data(), sentinel.size());
-    if (!error.empty()) return error;
+// Reset the outputs to NaN, run once and compare with the references;
+// guard elements must still be NaN.  "" when correct.
+std::string checkCase(hip::HipRuntime& runtime, CaseRig& rig, const Contract& contract,
+                      const ContractCase& data, const std::vector<std::vector<double>>& expected,
+                      bool guarded) {
+  for (const auto& output : rig.outputs) {
+    const std::vector<float> nan(output->elementCount(), std::numeric_limits<float>::quiet_NaN());
+    if (auto why = runtime.writeBuffer(output, nan.data(), nan.size()); !why.empty()) return why;
   }
-  const auto result = run.sequence->execute();
-  if (!result.executionPassed) return result.errorMessage;
-  for (std::size_t i = 0; i < run.outputs.size(); ++i) {
-    const auto values = run.outputs[i]->read();
-    const auto count = data.outputCounts[i];
+  const auto run = rig.sequence->execute();
+  if (!run.executionPassed) return run.errorMessage;
+  for (std::size_t i = 0; i < rig.outputs.size(); ++i) {
+    const auto values = rig.outputs[i]->read();
+    const std::size_t count = data.outputCounts[i];
     if (values.size() != count + (guarded ? kGuardElements : 0)) return "Output size mismatch.";
-    const std::vector<float> logical(values.begin(), values.begin() + count);
-    const auto comparison =
-        validation::compare(logical, references[i], contract.tolerance, contract.tolerance);
-    if (!comparison.passed) return contract.outputNames[i] + ": " + comparison.errorMessage;
+    const auto check = validation::compare({values.begin(), values.begin() + count}, expected[i],
+                                           contract.tolerance, contract.tolerance);
+    if (!check.passed) return contract.outputNames[i] + ": " + check.errorMessage;
     if (guarded && !std::all_of(values.begin() + count, values.end(),
                                 [](float v) { return std::isnan(v); }))
       return "Output guard modified: " + contract.outputNames[i];
@@ -1125,139 +1061,150 @@ std::string validateCase(hip::HipRuntime& runtime, CaseRun& run, const Contract&
 
 }  // namespace
 
+std::string kernelContractText(const hip::HipRuntime& runtime, const std::string& pattern) {
+  const auto contract = contractFor(pattern);
+  const auto hw = runtime.hardwareInfo();
+  std::ostringstream out;
+  out << "{\"version\":1,\"pattern\":\"" << contract.pattern << "\",\"function_name\":\""
+      << contract.functionName << "\",\"storage_dtype\":\"half\",\"accumulation_dtype\":\"float\""
+      << ",\"target\":{\"backend\":\"hip\",\"arch\":\"gfx950\",\"device\":\""
+      << jsonEscape(runtime.deviceName()) << "\",\"wave_size\":" << hw.waveSize
+      << ",\"max_threads_per_workgroup\":" << hw.maxThreadsPerThreadgroup
+      << ",\"max_lds_bytes\":" << hw.maxThreadgroupMemoryLength << "},\"outputs\":[";
+  for (std::size_t i = 0; i < contract.outputNames.size(); ++i)
+    out << (i ? "," : "") << '"' << contract.outputNames[i] << '"';
+  out << "],\"workgroup_sizes\":[";
+  for (std::size_t i = 0; i < contract.workgroupSizes.size(); ++i)
+    out << (i ? "," : "") << contract.workgroupSizes[i];
+  out << "],\"cases\":[";
+  for (std::size_t i = 0; i < contract.cases.size(); ++i)
+    out << (i ? "," : "") << '"' << contract.cases[i].templateKey << '"';
+  out << "]}";
+  return out.str();
+}
+
+std::string canonicalKernelPattern(const std::string& pattern) {
+  return contractFor(pattern).pattern;
+}
+
 bool admitGeneratedKernel(hip::HipRuntime& runtime, const std::string& patternName,
                           const std::string& responsePath, const std::string& feedbackPath,
                           std::ostream& log, const std::string& artifactPath) {
-  auto report = [&](const Feedback& feedback) -> bool {
-    const auto error = writeFeedback(feedback, feedbackPath);
-    log << "Generated candidate " << feedback.stage << ": "
-        << (feedback.status == "admitted" ? "PASS" : "FAIL") << ": " << feedback.message << '\n';
-    if (!error.empty()) {
-      log << "Feedback error: " << error << '\n';
+  // Every exit writes the feedback file; only a fatal outcome returns false.
+  const auto finish = [&](const AdmissionFeedback& f) {
+    const std::string written = writeAdmissionFeedback(f, feedbackPath);
+    log << "[admission] " << patternName << " " << f.stage << " -> " << f.status << ": "
+        << f.message << '\n';
+    if (!written.empty()) {
+      log << "[admission] feedback not written: " << written << '\n';
       return false;
     }
-    log << "Generated kernel admission: "
-        << (feedback.status == "admitted" ? "PASS"
-                                          : feedback.status == "fatal" ? "FAIL" : "FALLBACK")
-        << "\nSelected: " << (feedback.status == "admitted" ? "generated " : "template ")
-        << patternName << '\n';
-    return feedback.status != "fatal";
+    log << "[admission] " << patternName << " runs the "
+        << (f.status == "admitted" ? "candidate" : "template") << " kernel\n";
+    return f.status != "fatal";
   };
+  Contract contract;
+  std::vector<CaseRig> templates;
+  std::vector<std::vector<std::vector<double>>> expected;
   try {
-    const auto contract = makeContract(patternName);
-    // Template baselines and their reference outputs.
-    std::vector<CaseRun> baselines;
-    std::vector<std::vector<std::vector<double>>> references;
-    for (std::size_t i = 0; i < contract.cases.size(); ++i) {
-      const auto& data = contract.cases[i];
-      auto base = prepareCase(runtime, contract, data, data.templateKey, contract.functionName,
-                              false);
-      const auto run = base.sequence->execute();
+    contract = contractFor(patternName);
+    for (const auto& data : contract.cases) {
+      auto rig = rigCase(runtime, contract, data, data.templateKey, false);
+      const auto run = rig.sequence->execute();
       if (!run.executionPassed) throw std::runtime_error(run.errorMessage);
       std::vector<std::vector<double>> outs;
-      for (const auto& output : base.outputs) {
+      for (const auto& output : rig.outputs) {
         const auto values = output->read();
         outs.emplace_back(values.begin(), values.end());
       }
-      references.push_back(std::move(outs));
-      const auto warm = benchmark::warmup(benchmark::sampler(*base.sequence), 5);
-      if (!warm.empty()) throw std::runtime_error(warm);
-      log << "Template baseline case " << i << ": " << data.templateKey << '\n';
-      baselines.push_back(std::move(base));
+      expected.push_back(std::move(outs));
+      if (auto why = benchmark::warmup(benchmark::sampler(*rig.sequence), planner::kTuningWarmup);
+          !why.empty())
+        throw std::runtime_error(why);
+      log << "[admission] template " << data.templateKey << " ready\n";
+      templates.push_back(std::move(rig));
     }
-    std::ifstream in(responsePath);
-    if (!in) return report({"retry", "response_parse", "Unable to read '" + responsePath + "'."});
-    std::stringstream buffer;
-    buffer << in.rdbuf();
-    const std::string text = buffer.str();
-    std::string functionName, source, workgroup;
-    if (!jsonField(text, "function_name", functionName) || !jsonField(text, "source", source) ||
-        !jsonField(text, "workgroup_size", workgroup))
-      return report({"retry", "response_parse",
-                     "Response needs function_name, source and workgroup_size."});
-    if (functionName != contract.functionName)
-      return report({"retry", "contract", "Expected function_name: " + contract.functionName});
-    const auto qpos = source.find('?');
-    if (source.substr(0, qpos) != contract.functionName)
-      return report({"retry", "contract",
-                     "The kernel key must name " + contract.functionName + "."});
-    std::size_t workgroupSize = 0;
-    try {
-      workgroupSize = static_cast<std::size_t>(std::stoul(workgroup));
-    } catch (const std::exception&) {
-      return report({"retry", "response_parse", "workgroup_size is not an integer."});
-    }
-    const auto hardware = runtime.hardwareInfo();
-    if (std::find(contract.workgroupSizes.begin(), contract.workgroupSizes.end(),
-                  workgroupSize) == contract.workgroupSizes.end() ||
-        workgroupSize > hardware.maxThreadsPerThreadgroup)
-      return report({"retry", "hardware_filter",
-                     "workgroup_size is not legal for this contract/device."});
-    std::vector<CaseRun> candidates;
-    for (std::size_t i = 0; i < contract.cases.size(); ++i) {
-      const auto& data = contract.cases[i];
-      std::string key = keyForCase(source, data);
-      if (key.find("threads=") == std::string::npos)
-        key += "&threads=" + std::to_string(workgroupSize);
-      CaseRun run;
-      try {
-        run = prepareCase(runtime, contract, data, key, functionName, true);
-      } catch (const std::exception& e) {
-        return report({"retry", i == 0 ? "compile" : "prepare", e.what()});
-      }
-      const auto error = validateCase(runtime, run, contract, data, references[i], true);
-      if (!error.empty())
-        return report({"retry", "numerical_validation",
-                       "case " + std::to_string(i) + ": " + error});
-      log << "Generated candidate case " << i << " (" << key
-          << ") all outputs numerical validation: PASS\n";
-      candidates.push_back(std::move(run));
-    }
-    double worst = std::numeric_limits<double>::infinity();
-    std::optional<Feedback> failure;
-    Feedback accepted{"admitted", "admission",
-                      "All cases passed correctness and two performance rounds."};
-    for (std::size_t i = 0; i < candidates.size(); ++i) {
-      const auto baseSampler = benchmark::sampler(*baselines[i].sequence);
-      const auto candSampler = benchmark::sampler(*candidates[i].sequence);
-      const auto warm = benchmark::warmup(candSampler, planner::kTuningWarmup);
-      if (!warm.empty()) return report({"retry", "warmup", warm});
-      for (int round = 0; round < 2; ++round) {
-        const auto timing =
-            benchmark::measurePair(baseSampler, candSampler, planner::kTuningSamples);
-        if (!timing.passed) return report({"retry", "benchmark", timing.errorMessage});
-        log << "Generated candidate case " << i << " round " << round + 1
-            << ": baseline(us)=" << timing.baseline.medianUs
-            << ", candidate(us)=" << timing.candidate.medianUs << ", speedup=" << timing.speedup
-            << "x\n";
-        if (timing.speedup < worst) {
-          worst = timing.speedup;
-          accepted.baselineUs = timing.baseline.medianUs;
-          accepted.candidateUs = timing.candidate.medianUs;
-          accepted.speedup = timing.speedup;
-        }
-        if (timing.speedup < planner::kMinimumSpeedup &&
-            (!failure || timing.speedup < *failure->speedup))
-          failure = Feedback{"retry", "performance",
-                             "case " + std::to_string(i) + " round " + std::to_string(round + 1) +
-                                 " speedup is below 1.05x.",
-                             timing.baseline.medianUs, timing.candidate.medianUs, timing.speedup};
-      }
-      const auto finalError =
-          validateCase(runtime, candidates[i], contract, contract.cases[i], references[i], true);
-      if (!finalError.empty()) return report({"retry", "final_validation", finalError});
-    }
-    if (failure) return report(*failure);
-    if (!artifactPath.empty()) {
-      std::ofstream out(artifactPath);
-      out << "{\"function_name\":\"" << escapeJson(functionName) << "\",\"source\":\""
-          << escapeJson(source) << "\",\"workgroup_size\":" << workgroupSize << "}\n";
-      if (!out) return report({"fatal", "artifact_write", "Unable to write " + artifactPath});
-    }
-    return report(accepted);
   } catch (const std::exception& e) {
-    return report(Feedback("fatal", "baseline_or_contract", e.what()));
+    return finish({"fatal", "baseline_or_contract", e.what()});
   }
+
+  AdmittedKernel candidate;
+  {
+    std::ifstream in(responsePath);
+    if (!in) return finish({"retry", "response_parse", "Unable to read '" + responsePath + "'."});
+    std::stringstream text;
+    text << in.rdbuf();
+    std::string workgroup;
+    if (!jsonStringField(text.str(), "function_name", candidate.functionName) ||
+        !jsonStringField(text.str(), "source", candidate.source) ||
+        !jsonStringField(text.str(), "workgroup_size", workgroup))
+      return finish({"retry", "response_parse",
+                     "Response needs function_name, source and workgroup_size."});
+    try {
+      candidate.workgroupSize = static_cast<std::size_t>(std::stoul(workgroup));
+    } catch (const std::exception&) {
+      return finish({"retry", "response_parse", "workgroup_size is not an integer."});
+    }
+  }
+  if (candidate.functionName != contract.functionName)
+    return finish({"retry", "contract", "Expected function_name: " + contract.functionName});
+  if (candidate.source.substr(0, candidate.source.find('?')) != contract.functionName)
+    return finish({"retry", "contract", "The kernel key must name " + contract.functionName + "."});
+  const bool legal = std::find(contract.workgroupSizes.begin(), contract.workgroupSizes.end(),
+                               candidate.workgroupSize) != contract.workgroupSizes.end() &&
+                     candidate.workgroupSize <= runtime.hardwareInfo().maxThreadsPerThreadgroup;
+  if (!legal)
+    return finish({"retry", "hardware_filter",
+                   "workgroup_size is not legal for this contract/device."});
+
+  std::string tuning = tuningOf(candidate.source);
+  if (tuning.find("threads=") == std::string::npos)
+    tuning += "&threads=" + std::to_string(candidate.workgroupSize);
+  std::vector<CaseRig> rigs;
+  for (std::size_t i = 0; i < contract.cases.size(); ++i) {
+    const auto& data = contract.cases[i];
+    const std::string key = data.templateKey + tuning;
+    try {
+      rigs.push_back(rigCase(runtime, contract, data, key, true));
+    } catch (const std::exception& e) {
+      return finish({"retry", i == 0 ? "compile" : "prepare", e.what()});
+    }
+    if (auto why = checkCase(runtime, rigs.back(), contract, data, expected[i], true); !why.empty())
+      return finish({"retry", "numerical_validation", "case " + std::to_string(i) + ": " + why});
+    log << "[admission] " << key << " matches the template outputs\n";
+  }
+
+  // Two paired rounds per case; the slowest round decides and is reported.
+  std::optional<AdmissionFeedback> slowest;
+  for (std::size_t i = 0; i < rigs.size(); ++i) {
+    const auto base = benchmark::sampler(*templates[i].sequence);
+    const auto cand = benchmark::sampler(*rigs[i].sequence);
+    if (auto why = benchmark::warmup(cand, planner::kTuningWarmup); !why.empty())
+      return finish({"retry", "warmup", why});
+    for (int round = 1; round <= 2; ++round) {
+      const auto t = benchmark::measurePair(base, cand, planner::kTuningSamples);
+      if (!t.passed) return finish({"retry", "benchmark", t.errorMessage});
+      log << "[admission] case " << i << " round " << round << ": template " << t.baseline.medianUs
+          << " us, candidate " << t.candidate.medianUs << " us, x" << t.speedup << '\n';
+      if (!slowest || t.speedup < *slowest->speedup) {
+        const bool fast = t.speedup >= planner::kMinimumSpeedup;
+        slowest = AdmissionFeedback{
+            fast ? "admitted" : "retry", fast ? "admission" : "performance",
+            fast ? "All cases passed correctness and two performance rounds."
+                 : "case " + std::to_string(i) + " round " + std::to_string(round) +
+                       " speedup is below 1.05x.",
+            t.baseline.medianUs, t.candidate.medianUs, t.speedup};
+      }
+    }
+    if (auto why = checkCase(runtime, rigs[i], contract, contract.cases[i], expected[i], true);
+        !why.empty())
+      return finish({"retry", "final_validation", why});
+  }
+  if (slowest->status == "admitted" && !artifactPath.empty()) {
+    const std::string why = writeAdmittedKernel(runtime, contract.pattern, candidate, artifactPath);
+    if (!why.empty()) return finish({"fatal", "artifact_write", why});
+  }
+  return finish(*slowest);
 }
 
 }  // namespace runtime

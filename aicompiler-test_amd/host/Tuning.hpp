@@ -260,16 +260,18 @@ using FusionDecisionCache = std::map<std::string, bool>;
     std::ostream& log);
 
 // admitGeneratedKernel (GeneratedKernelAdmission.cpp:204-318) for gfx950.
-// `pattern` names a contract: "RMSNorm", "AddRMSNorm" or "SiLUMul" (the
-// fused regions of this backend).  The response file is JSON with
-// "function_name" (must equal the contract's), "source" (a gfx950 kernel
-// key) and "workgroup_size" (a multiple of 64, at most the device limit).
-// Every contract case is validated with guarded outputs (512 extra elements
-// that must stay NaN) against the template baseline's result, then timed in
-// two paired rounds against the template.  Feedback JSON is written to
-// feedbackPath: {"version":1,"status","stage","message","metrics"}, status
-// "admitted" | "retry" | "fatal".  Returns false only on a fatal outcome.
-// When admitted and artifactPath is given, the admitted key is written there.
+// `pattern` names a region contract: "RMSNorm", "AddRMSNorm" or "SiLUMul"
+// (or decoder_rmsnorm, decoder_residual_rmsnorm, decoder_silu_mul).  The
+// response file is JSON with "function_name" (must equal the contract's),
+// "source" (a gfx950 kernel key naming that function; its threads / variant
+// parameters are applied to every contract case) and "workgroup_size" (a
+// contract workgroup size within the device limit).  Every case is validated
+// with guarded outputs (512 extra elements that must stay NaN) against the
+// template kernel's result, then timed in two paired rounds against the
+// template; the slowest round must reach 1.05x.  Feedback JSON goes to
+// feedbackPath (see AdmissionFeedback).  Returns false only on a fatal
+// outcome.  When admitted and artifactPath is given, the admitted-kernel
+// artifact for the KernelRegistry is written there.
 [[nodiscard]] bool admitGeneratedKernel(hip::HipRuntime& runtime, const std::string& pattern,
                                         const std::string& responsePath,
                                         const std::string& feedbackPath, std::ostream& log,

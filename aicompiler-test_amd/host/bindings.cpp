@@ -469,13 +469,42 @@ PYBIND11_MODULE(_tmc_host, m) {
   m.def("decode_gemv_cache_size", []() { return planner::decodeGEMVTuningCache().size(); });
   m.def("clear_decode_gemv_cache", []() { planner::decodeGEMVTuningCache().clear(); });
 
+  // Statistics and paired timing over Python samplers (host logic only): a
+  // sampler returns microseconds, None (no timestamp) or a str (a failure).
+  m.def("summarize_timings", [](const std::vector<double>& values) -> py::object {
+    const auto s = benchmark::summarizeTimings(values);
+    return s ? py::object(statsToDict(*s)) : py::object(py::none());
+  });
+  m.def("measure_pair", [](py::function baseline, py::function candidate, std::size_t samples) {
+    const auto wrap = [](py::function f) -> benchmark::Sampler {
+      return [f](std::string& failure) -> std::optional<double> {
+        const py::object r = f();
+        if (r.is_none()) return std::nullopt;
+        if (py::isinstance<py::str>(r)) {
+          failure = r.cast<std::string>();
+          return std::nullopt;
+        }
+        return r.cast<double>();
+      };
+    };
+    const auto r = benchmark::measurePair(wrap(baseline), wrap(candidate), samples);
+    py::dict d;
+    d["passed"] = r.passed;
+    d["error"] = r.errorMessage;
+    d["baseline"] = statsToDict(r.baseline);
+    d["candidate"] = statsToDict(r.candidate);
+    d["speedup"] = r.speedup;
+    return d;
+  });
+
   py::class_<DecoderLLMCompileOptions>(m, "DecoderLLMCompileOptions")
       .def(py::init<>())
       .def_readwrite("kv_page_size", &DecoderLLMCompileOptions::kvPageSize)
       .def_readwrite("prefill_chunk_size", &DecoderLLMCompileOptions::prefillChunkSize)
       .def_readwrite("shared_kv_pools", &DecoderLLMCompileOptions::sharedKVPools)
       .def_readwrite("storage_dtype", &DecoderLLMCompileOptions::storageDtype)
-      .def_readwrite("shared_model_resources", &DecoderLLMCompileOptions::sharedModelResources);
+      .def_readwrite("shared_model_resources", &DecoderLLMCompileOptions::sharedModelResources)
+      .def_readwrite("kernel_library", &DecoderLLMCompileOptions::kernelLibrary);
 
   py::class_<DecoderKVSnapshot>(m, "DecoderKVSnapshot")
       .def_readonly("length", &DecoderKVSnapshot::length)
@@ -513,6 +542,8 @@ PYBIND11_MODULE(_tmc_host, m) {
       .def("cache_storage_reused", &CompiledDecoderLLM::cacheStorageReused)
       .def("uses_paged_kv_cache", &CompiledDecoderLLM::usesPagedKVCache)
       .def("kv_page_size", &CompiledDecoderLLM::kvPageSize)
+      .def("kernel_usage_report", &CompiledDecoderLLM::kernelUsageReport,
+           py::arg("reset") = false)
       .def("allocated_kv_page_count", &CompiledDecoderLLM::allocatedKVPageCount)
       .def("model_storage_bytes", &CompiledDecoderLLM::modelStorageBytes)
       .def("kv_storage_bytes", &CompiledDecoderLLM::kvStorageBytes)
@@ -842,4 +873,46 @@ PYBIND11_MODULE(_tmc_host, m) {
         },
         py::arg("runtime"), py::arg("pattern"), py::arg("response"), py::arg("feedback"),
         py::arg("artifact") = std::string());
+
+  m.def("write_admitted_kernel",
+        [](const hip::HipRuntime& rt, const std::string& pattern, const std::string& function,
+           const std::string& source, std::size_t workgroup, const std::string& path) {
+          return runtime::writeAdmittedKernel(rt, runtime::canonicalKernelPattern(pattern),
+                                              {function, source, workgroup}, path);
+        });
+  m.def("kernel_contract_text", [](const hip::HipRuntime& rt, const std::string& pattern) {
+    return runtime::kernelContractText(rt, pattern);
+  });
+  py::class_<runtime::KernelRegistry, std::shared_ptr<runtime::KernelRegistry>>(m, "KernelRegistry")
+      .def(py::init<>())
+      .def("load",
+           [](runtime::KernelRegistry& r, const hip::HipRuntime& rt, const std::string& dir) {
+             std::ostringstream log;
+             r.load(rt, dir, log);
+             return log.str();
+           })
+      .def("find",
+           [](const runtime::KernelRegistry& r, const std::string& pattern) -> py::object {
+             const auto* k = r.find(pattern);
+             if (!k) return py::none();
+             py::dict d;
+             d["function_name"] = k->functionName;
+             d["source"] = k->source;
+             d["workgroup_size"] = k->workgroupSize;
+             return d;
+           })
+      .def("size", &runtime::KernelRegistry::size)
+      .def("track",
+           [](runtime::KernelRegistry& r, const std::string& node, const std::string& pattern,
+              const std::string& implementation, const std::string& functions,
+              std::size_t dispatches) {
+             return r.track({node, pattern, implementation, functions, dispatches, 0});
+           })
+      .def("completed", &runtime::KernelRegistry::completed)
+      .def("reset_usage", &runtime::KernelRegistry::resetUsage)
+      .def("report", [](const runtime::KernelRegistry& r) {
+        std::ostringstream log;
+        r.report(log);
+        return log.str();
+      });
 }

@@ -88,3 +88,36 @@ def test_rms_norm_reference_closed_form(host):
     # eps / (2 mean(x^2)) ~ 5e-7 relative for this row
     y = np.asarray(host.rms_norm_reference(1, 4097, 1e-6, (8.0 * x[2]).ravel(), w))
     np.testing.assert_allclose(y, got[2], rtol=1e-6)
+
+
+def test_timing_statistics_and_paired_order(host):
+    """benchmark::summarizeTimings / measurePair (Benchmark.cpp:51-95
+    semantics): median and linearly interpolated 90th percentile of the
+    samples, and paired rounds that alternate which arm runs first."""
+    rng = np.random.default_rng(3)
+    for n in (1, 2, 5, 31, 32):
+        v = rng.uniform(1.0, 50.0, n)
+        s = host.summarize_timings(list(v))
+        assert s["samples"] == n and s["min_us"] == v.min() and s["max_us"] == v.max()
+        assert abs(s["median_us"] - np.median(v)) <= 1e-12 * v.max()
+        assert abs(s["p90_us"] - np.percentile(v, 90)) <= 1e-12 * v.max()
+    assert host.summarize_timings([]) is None
+    order = []
+    times = {"b": iter([10.0, 12.0, 11.0, 13.0]), "c": iter([5.0, 6.0, 7.0, 8.0])}
+
+    def arm(name):
+        def run():
+            order.append(name)
+            return next(times[name])
+        return run
+
+    r = host.measure_pair(arm("b"), arm("c"), 4)
+    assert r["passed"] and order == ["b", "c", "c", "b", "b", "c", "c", "b"]
+    assert r["baseline"]["median_us"] == 11.5 and r["candidate"]["median_us"] == 6.5
+    assert abs(r["speedup"] - 11.5 / 6.5) < 1e-12
+    bad = host.measure_pair(lambda: 1.0, lambda: "device lost", 3)
+    assert not bad["passed"] and bad["error"] == "Candidate: GPU execution failed: device lost"
+    none = host.measure_pair(lambda: None, lambda: 1.0, 3)
+    assert none["error"].startswith("Baseline: GPU timestamps unavailable")
+    assert host.measure_pair(lambda: 1.0, lambda: 1.0, 0)["error"] == (
+        "Benchmark requires at least one sample.")

@@ -75,7 +75,7 @@ def test_admit_add_rmsnorm_fusion(orc, host, rt):
     rows, width = 4, 4096
     d = host.admit_add_rmsnorm_fusion(rt, rows, width, True)
     assert "Fusion AddRMSNorm" in d["log"]
-    assert "FALLBACK:" not in d["log"], d["log"]     # validation and timing ran
+    assert "error:" not in d["log"], d["log"]        # validation and timing ran
     # the second call reuses the cached decision
     assert d["cached_admitted"] == d["admitted"]
     assert "cached" in d["log"]
@@ -134,3 +134,40 @@ def test_admit_generated_kernel_outcomes(host, rt, tmp_path):
     # an unknown pattern is fatal
     ok, _ = host.admit_generated_kernel(rt, "Softmax", _response(tmp_path), str(fb))
     assert not ok and json.loads(fb.read_text())["status"] == "fatal"
+
+
+def test_registry_artifact_drives_the_decoder_norms(host, orc, rt, tmp_path):
+    """An admitted Add+RMSNorm artifact (KernelRegistry, written as
+    admitGeneratedKernel writes it) is loaded by compileDecoderLLM through
+    kernel_library and replaces the template launch parameters of the
+    one-row bucket's residual norms; the decode step still matches the
+    oracle, and the usage audit counts the generated dispatches."""
+    from tests.test_decoder_gpu import P, OracleRequest, _weights, _workload, assert_f16_path
+    cfg = dict(layers=1, hidden=4096, heads=32, head_dim=128, kv_heads=8, intermediate=512,
+               vocabulary=1000, capacity=64, epsilon=1e-6)
+    m = _weights(orc, cfg, 81)
+    w = _workload(host, orc, cfg, m)
+    lib = tmp_path / "lib"
+    err = host.write_admitted_kernel(rt, "AddRMSNorm", "add_rmsnorm",
+                                     "add_rmsnorm?rows=1&width=4096&eps=1e-06&dtype=f16&threads=256",
+                                     256, str(lib / "decoder_residual_rmsnorm" / "admitted.json"))
+    assert err == ""
+    opts = host.DecoderLLMCompileOptions()
+    opts.kv_page_size = P
+    opts.kernel_library = str(lib)
+    dec, log = host.compile_decoder_llm(rt, w, opts)
+    assert "decoder_residual_rmsnorm: admitted" in log, log
+    prompt = [float(t) for t in np.random.default_rng(82).integers(0, cfg["vocabulary"], 5)]
+    res = dec.prefill(prompt, True)
+    assert res["passed"], res["error"]
+    report = dec.kernel_usage_report()
+    assert "generated add_rmsnorm?" in report and "threads=256" in report, report
+    assert "entry decoder_residual_rmsnorm: ran" in report, report
+    # 5 one-row steps x 2 residual norms per layer (1 layer)
+    assert "5 calls, 10 dispatches" in report, report
+    ref = OracleRequest(orc, cfg, m, cfg["capacity"] // P)
+    tables = [dec.kv_block_table(l) for l in range(cfg["layers"])]
+    V = cfg["vocabulary"]
+    for i, tok in enumerate(prompt):
+        logits, _ = ref.step(int(tok), i + 1, tables)
+        assert_f16_path(res["logits"][i * V:(i + 1) * V], logits, f"position {i}")
