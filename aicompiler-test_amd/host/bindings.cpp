@@ -14,6 +14,7 @@
 #include "Importer.hpp"
 #include "KVCacheState.hpp"
 #include "ServingRuntime.hpp"
+#include "StatefulExecutor.hpp"
 #include "Tuning.hpp"
 
 namespace py = pybind11;
@@ -561,6 +562,44 @@ PYBIND11_MODULE(_tmc_host, m) {
         [](hip::HipRuntime& rt, const DecoderLLMWorkload& w, const DecoderLLMCompileOptions& o) {
           std::ostringstream log;
           auto r = compileDecoderLLM(rt, w, log, o);
+          if (!r.executable) throw std::runtime_error(r.errorMessage);
+          return py::make_tuple(py::cast(std::move(r.executable)), log.str());
+        });
+
+  const auto kvRun = [](const KVCacheRunResult& r) {
+    py::dict d;
+    d["passed"] = r.passed;
+    d["output"] = toArray(r.output);
+    d["gpu_us"] = r.gpuExecutionTimeUs ? py::cast(*r.gpuExecutionTimeUs) : py::none();
+    d["error"] = r.errorMessage;
+    return d;
+  };
+  py::class_<CompiledKVCacheAttention>(m, "CompiledKVCacheAttention")
+      .def("reset", &CompiledKVCacheAttention::reset)
+      .def("prefill",
+           [kvRun](CompiledKVCacheAttention& e, const std::vector<float>& q,
+                   const std::vector<float>& k, const std::vector<float>& v) {
+             return kvRun(e.prefill(q, k, v));
+           })
+      .def("decode",
+           [kvRun](CompiledKVCacheAttention& e, const std::vector<float>& q,
+                   const std::vector<float>& k, const std::vector<float>& v) {
+             return kvRun(e.decode(q, k, v));
+           })
+      .def("current_length", &CompiledKVCacheAttention::currentLength)
+      .def("read_key_prefix",
+           [](const CompiledKVCacheAttention& e) { return toArray(e.readKeyPrefix()); })
+      .def("read_value_prefix",
+           [](const CompiledKVCacheAttention& e) { return toArray(e.readValuePrefix()); })
+      .def("cache_storage_reused", &CompiledKVCacheAttention::cacheStorageReused);
+  m.def("compile_kv_cache_attention",
+        [](hip::HipRuntime& rt, const planner::KVCachePlan& plan, FloatArray wq, FloatArray wk,
+           FloatArray wv, FloatArray wo) {
+          const auto vec = [](const FloatArray& a) {
+            return std::vector<float>(a.data(), a.data() + a.size());
+          };
+          std::ostringstream log;
+          auto r = compileKVCacheAttention(rt, plan, vec(wq), vec(wk), vec(wv), vec(wo), log);
           if (!r.executable) throw std::runtime_error(r.errorMessage);
           return py::make_tuple(py::cast(std::move(r.executable)), log.str());
         });

@@ -68,6 +68,7 @@ def _declare(l):
     l.tmco_append_paged.argtypes = [vp, sz, sz, sz, sz, sz, sz, C.c_int, C.c_int32, vp, vp]
     l.tmco_append_serving.argtypes = [vp, sz, sz, sz, sz, sz, C.c_int, vp, vp, C.c_int32, vp]
     l.tmco_set_threads.argtypes = [C.c_int]
+    l.tmco_linear_values.argtypes = [vp, vp, sz, sz, sz, vp]
     l.tmco_decoder_step.restype = C.c_int
     l.tmco_decoder_step.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp, sz, sz, sz, vp, vp]
 
@@ -275,6 +276,17 @@ class _Model(C.Structure):
                 ("kv_heads", C.c_size_t), ("embedding", C.c_void_p), ("final_norm", C.c_void_p), ("lm_head", C.c_void_p),
                 ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p),
                 ("layer", C.POINTER(_Layer))]
+
+
+def linear_values(x_bits, weight) -> np.ndarray:
+    """tmco_linear_values: the same double sums as linear(x, w, F16) for fp16
+    bits x and W, computed by the decode step's blocked, threaded linear."""
+    x = decode(np.ascontiguousarray(x_bits, dtype=np.uint16), F16)
+    w = np.ascontiguousarray(weight, dtype=np.uint16)
+    rows, k = x.reshape(-1, w.shape[1]).shape
+    y = np.empty((rows, w.shape[0]), dtype=np.float64)
+    lib().tmco_linear_values(_p(x), _p(w), rows, k, w.shape[0], _p(y))
+    return y
 
 
 def set_threads(threads: int) -> None:

@@ -618,6 +618,16 @@ static void linear_f16(const float *x, const uint16_t *w, size_t rows, size_t in
   free(xt);
 }
 
+/* The decode step's linear on its own: x holds storage values as floats, W
+ * fp16 bits [out, in]; the same double sums, in the same k order, as
+ * tmco_linear (which decodes x itself), split over tmco_set_threads threads.
+ * Pinned: equality with tmco_linear (tests/test_oracle_decoder.py). */
+void tmco_linear_values(const float *x, const uint16_t *weight, size_t rows, size_t in_features,
+                        size_t out_features, double *y) {
+  half_table_init();
+  linear_f16(x, weight, rows, in_features, out_features, y);
+}
+
 static void rmsnorm_f16(const float *x, const uint16_t *w, size_t rows, size_t width,
                         float epsilon, double *out) {
   for (size_t r = 0; r < rows; ++r) {

@@ -106,6 +106,12 @@ typedef struct tmco_model {
  * greedy tokens.  Rows b < logits_from skip the final norm and LM head
  * (logits 0, token -1); layer_limit > 0 and below the layer count stops
  * after that many layers with no LM head at all. */
+/* y[r,n] = sum_k x[r,k] W[n,k] (double, k order) with x as float storage
+ * values and W fp16 bits; threaded by tmco_set_threads, same sums as
+ * tmco_linear. */
+void tmco_linear_values(const float *x, const uint16_t *weight, size_t rows, size_t in_features,
+                        size_t out_features, double *y);
+
 /* Threads used by tmco_decoder_step (default 1).  Results do not depend on
  * it: the work is split over output features and heads, never inside a sum. */
 void tmco_set_threads(int threads);

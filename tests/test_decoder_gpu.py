@@ -188,6 +188,38 @@ def test_decoder_rules_and_contiguous_cache(host, orc, rt):
     assert paged.reset() == "" and paged.current_length() == 0
 
 
+def test_decoder_capacity_reached_leaves_state_unchanged(host, orc, rt):
+    """DecoderLLMExecutor.cpp:1043-1046: at capacity the decoder refuses the
+    step with "Decoder KV cache capacity has been reached." and keeps its
+    length, pages and cache bits; a prompt beyond the capacity is refused
+    before any page is taken."""
+    cfg = dict(CONFIGS["gqa_d128"], capacity=32)
+    m = _weights(orc, cfg, 91)
+    opts = host.DecoderLLMCompileOptions()
+    opts.kv_page_size = P
+    dec, _ = host.compile_decoder_llm(rt, _workload(host, orc, cfg, m), opts)
+    too_long = dec.prefill([1.0] * 33, False)
+    assert not too_long["passed"] and dec.current_length() == 0
+    assert dec.allocated_kv_page_count() == 0
+    assert dec.prefill([float(t) for t in range(3, 33)], False)["passed"]
+    token = 7.0
+    for _ in range(2):
+        out = dec.decode([token], True)
+        assert out["passed"], out["error"]
+        token = float(out["next_token_ids"][0])
+    assert dec.current_length() == 32 and dec.allocated_kv_page_count() == 2
+    keys = [dec.read_key_prefix(l) for l in range(cfg["layers"])]
+    values = [dec.read_value_prefix(l) for l in range(cfg["layers"])]
+    tables = [dec.kv_block_table(l) for l in range(cfg["layers"])]
+    full = dec.decode([token], True)
+    assert not full["passed"] and full["error"] == "Decoder KV cache capacity has been reached."
+    assert dec.current_length() == 32 and dec.allocated_kv_page_count() == 2
+    assert [dec.kv_block_table(l) for l in range(cfg["layers"])] == tables
+    for l in range(cfg["layers"]):
+        assert np.array_equal(dec.read_key_prefix(l), keys[l])
+        assert np.array_equal(dec.read_value_prefix(l), values[l])
+
+
 def test_snapshot_restore_moves_pages_bit_exactly(host, orc, rt):
     cfg = CONFIGS["gqa_d128"]
     m = _weights(orc, cfg, 31)
@@ -338,6 +370,25 @@ def test_serving_matches_single_request_decoding(host, orc, rt, chunk, per_chunk
     assert (metrics["spilled_bytes"] > 0) == (metrics["preemption_count"] > 0)
     assert metrics["resume_count"] == metrics["preemption_count"]
     print("serving metrics:", {k: v for k, v in metrics.items() if not isinstance(v, dict)})
+    # oracle replay of every request: its prompt as one step (rows in
+    # position order), then one step per generated token, on the oracle's
+    # own pools; the serving loop's logits must match at every step
+    V = cfg["vocabulary"]
+    for spec, out in zip(specs, result["requests"]):
+        ref = OracleRequest(orc, cfg, m, cfg["capacity"] // P)
+        prompt = np.asarray(spec.prompt_token_ids, np.int32)
+        n = len(prompt)
+        table = np.arange(cfg["capacity"] // P, dtype=np.int32)
+        t = np.broadcast_to(table, (cfg["layers"], n, table.size))
+        logits, nxt = orc.decoder_step(m, cfg, ref.k, ref.v, P, table.size, t, prompt,
+                                       np.arange(1, n + 1), logits_from=n - 1)
+        assert_f16_path(out["prefill_logits"], logits[-1], f"{spec.id} prefill vs oracle")
+        gen = out["generated_token_ids"]
+        _check_token(int(gen[0]), int(nxt[-1]), logits[-1], f"{spec.id} first token vs oracle")
+        for i in range(spec.decode_token_count):
+            lg, nx = ref.step(int(gen[i]), n + i + 1, [table] * cfg["layers"])
+            assert_f16_path(out["decode_logits"][i], lg, f"{spec.id} step {i} vs oracle")
+            _check_token(int(gen[i + 1]), nx, lg, f"{spec.id} step {i} token vs oracle")
     opts = host.DecoderLLMCompileOptions()
     opts.kv_page_size = P
     opts.shared_model_resources = model

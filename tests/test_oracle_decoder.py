@@ -159,3 +159,20 @@ def test_decoder_step_row_blocks_threads_and_logits_from(orc, threads):
     assert not part[:20].any() and (part_tok[:20] == -1).all()
     np.testing.assert_array_equal(part[20:], got[20:])
     assert (part_tok[20:] == got_tok[20:]).all()
+
+
+@pytest.mark.parametrize("threads", [1, 3])
+def test_linear_values_equals_pinned_linear(orc, threads):
+    """The blocked, threaded linear of the decode step gives the pinned
+    tmco_linear's doubles bit for bit (rows 37: two 16-row blocks and a tail;
+    an odd output count)."""
+    rng = np.random.default_rng(17)
+    x = orc.f16(rng.standard_normal((37, 96)).astype(np.float32))
+    w = orc.f16((rng.standard_normal((51, 96)) * 0.1).astype(np.float32))
+    try:
+        orc.set_threads(threads)
+        fast = orc.linear_values(x, w)
+    finally:
+        orc.set_threads(1)
+    ref = orc.linear(x, w, orc.F16)
+    assert np.array_equal(fast.view(np.uint64), np.asarray(ref, np.float64).view(np.uint64))
