@@ -414,24 +414,30 @@ __device__ __forceinline__ void issue_step(const AttnParams& p, const int* s_pag
         if constexpr (MODE == 0) {
           tile = (long)(cbase + (size_t)tp * 128);
         } else {
-          const int page = s_pages[page_of(p, tp) - page0];
+          // The tile's page id is the same for every lane: in a scalar
+          // register the branch on it stays scalar, so the loads below are
+          // issued back to back (a per-lane value turned this into exec-mask
+          // control flow and a wait on every load already in flight).
+          const int page = __builtin_amdgcn_readfirstlane(s_pages[page_of(p, tp) - page0]);
           if (page_ok<1>(p, page))
             tile = (long)page * p.page_stride + (long)kvh * p.head_stride +
                    (long)slot_in_page(p, tp) * 128;
         }
       }
       st.tile[t] = tile;
-      const unsigned tb = tile < 0 ? kAbsent : (unsigned)(tile * 2);
-      const unsigned krow = (tile >= 0 && tp + j < end) ? tb + (unsigned)j * 256u : kAbsent;
+      // Absent positions OR kAbsent into an in-range offset: the result
+      // lies past the buffer (the hardware returns zeros) and is computed
+      // without a select or branch per load.
+      const unsigned tb = tile < 0 ? 0u : (unsigned)(tile * 2);
+      const unsigned tmask = tile < 0 ? kAbsent : 0u;
+      const unsigned kmask = tmask | (tp + j < end ? 0u : kAbsent);
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        st.k[t][s] = buffer_h8(rk, krow == kAbsent ? kAbsent : krow + 16u * (4 * s + g));
+        st.k[t][s] = buffer_h8(rk, (tb + (unsigned)j * 256u + 16u * (4 * s + g)) | kmask);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const unsigned vrow =
-            (tile >= 0 && tp + 4 * i + g < end) ? tb + (unsigned)(4 * i + g) * 256u + 16u * j
-                                                : kAbsent;
-        st.v[t][i] = buffer_h8(rv, vrow);
+        const unsigned vmask = tmask | (tp + 4 * i + g < end ? 0u : kAbsent);
+        st.v[t][i] = buffer_h8(rv, (tb + (unsigned)(4 * i + g) * 256u + 16u * j) | vmask);
       }
     } else {
       st.tile[t] = tp < end ? 0 : -1;
