@@ -93,6 +93,8 @@ def _declare(l):
         "tmc_paged_decode_attention_noalloc": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i64, i64,
                                                      i64, i64, i64, i64, i64, i64, i64, vp]),
         "tmc_attention_scratch_bytes": (sz, []),
+        "tmc_paged_gather_probe": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, i64,
+                                         vp, vp]),
         "tmc_argmax_f32": (i32, [vp, vp, i64, i64, vp]),
         "tmc_fill_normal": (i32, [vp, i32, i64, C.c_uint64, f, f, vp]),
         "tmc_copy_bytes": (i32, [vp, vp, sz, vp]),
@@ -559,6 +561,16 @@ def decode_attention(q, k_cache, v_cache, valid_length, out, batch, q_heads, kv_
                                      _ptr(out), _dtype_code(q), batch, q_heads, kv_heads, head_dim,
                                      capacity, _ptr(workspace), ws_bytes, _stream(stream)),
           "tmc_decode_attention")
+
+
+def paged_gather_probe(k_pool, v_pool, valid_lengths, tables, batch, kv_heads, head_dim,
+                       page_size, max_pages, page_stride, head_stride, sink, stream=None):
+    """Load-only pass over the K/V bytes paged attention reads (bandwidth probe)."""
+    pool_pages = min(k_pool.numel(), v_pool.numel()) // page_stride
+    check(lib().tmc_paged_gather_probe(
+        _ptr(k_pool), _ptr(v_pool), _ptr(valid_lengths), _ptr(tables), batch, kv_heads, head_dim,
+        page_size, max_pages, pool_pages, page_stride, head_stride, _ptr(sink), _stream(stream)),
+        "tmc_paged_gather_probe")
 
 
 def paged_decode_attention(q, k_pool, v_pool, valid_lengths, tables, active, out, max_batch,

@@ -902,3 +902,81 @@ extern "C" int tmc_paged_decode_attention_noalloc(
                                     head_dim, page_size, max_pages, pool_pages, page_stride,
                                     head_stride, ws, need > 0 ? kScratchBytes : 0, stream);
 }
+
+// ------------------------------------------------------------ gather probe
+// Bandwidth probe of the paged decode-attention access pattern: reads the K
+// and V bytes a launch of tmc_paged_decode_attention (D = 128) reads, page by
+// page through the same block tables, and nothing else (no scores, no
+// partials).  Block (kv head, 128-position split, request); 16 lanes cover a
+// position's 256 bytes, and each thread keeps four 16-byte loads of K and of
+// V in flight.  Pages hold a multiple of 16 positions.  The xor of the loaded words reaches `sink` only when it equals
+// a fixed constant, which keeps the loads without writing memory.
+namespace tmc {
+namespace {
+
+constexpr int kProbeChunk = 128;
+constexpr int kProbeDepth = 4;
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kThreads) void gather_probe_kernel(
+    const u32x4* k, const u32x4* v, const int32_t* lengths, const int32_t* tables, int max_pages,
+    int page_size, long page_stride, long head_stride, long pool_pages, uint32_t* sink) {
+  const int kvh = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
+  const int length = lengths[b];
+  const int begin = split * kProbeChunk;
+  if (length < 1 || length > max_pages * page_size || begin >= length) return;
+  const int end = min(length, begin + kProbeChunk);
+  const int c = threadIdx.x & 15, row = threadIdx.x >> 4;  // 16 positions per pass
+  uint32_t acc = 0;
+  for (int p0 = begin; p0 < end; p0 += 16 * kProbeDepth) {
+    u32x4 a[kProbeDepth], bv[kProbeDepth];
+#pragma unroll
+    for (int u = 0; u < kProbeDepth; ++u) {
+      // 16 positions from a multiple of 16 lie in one page: one table entry,
+      // the same for the whole block (a scalar load)
+      const int p16 = p0 + 16 * u;
+      const int page = p16 < end ? tables[(size_t)b * max_pages + p16 / page_size] : -1;
+      const int pos = p16 + row;
+      const bool ok = pos < end && page >= 0 && (pool_pages == 0 || page < pool_pages);
+      const size_t off = ok ? ((size_t)page * page_stride + (size_t)kvh * head_stride +
+                               (size_t)(pos % page_size) * 128) / 8 + c
+                            : 0;
+      const u32x4 none = {0u, 0u, 0u, 0u};
+      a[u] = ok ? __builtin_nontemporal_load(k + off) : none;
+      bv[u] = ok ? __builtin_nontemporal_load(v + off) : none;
+    }
+#pragma unroll
+    for (int u = 0; u < kProbeDepth; ++u) acc ^= a[u].x ^ a[u].w ^ bv[u].y ^ bv[u].z;
+  }
+  if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+}  // namespace
+}  // namespace tmc
+
+extern "C" int tmc_paged_gather_probe(const void* key_pool, const void* value_pool,
+                                      const int32_t* valid_lengths, const int32_t* block_tables,
+                                      int64_t batch, int64_t kv_heads, int64_t head_dim,
+                                      int64_t page_size, int64_t max_pages, int64_t pool_pages,
+                                      int64_t page_stride, int64_t head_stride, void* sink,
+                                      void* stream) {
+  TMC_REQUIRE(key_pool && value_pool && valid_lengths && block_tables && sink,
+              "Gather probe: null pointer.");
+  TMC_REQUIRE(head_dim == 128, "Gather probe: head_dim must be 128.");
+  TMC_REQUIRE(page_size % 16 == 0, "Gather probe: page_size must be a multiple of 16.");
+  TMC_REQUIRE(batch > 0 && batch < 65536 && kv_heads > 0 && kv_heads < 65536 && page_size > 0 &&
+                  max_pages > 0 && page_size * max_pages < (1LL << 30) && pool_pages >= 0 &&
+                  page_stride > 0 && head_stride >= 0 && page_stride % 8 == 0 &&
+                  head_stride % 8 == 0,
+              "Gather probe: invalid geometry.");
+  TMC_REQUIRE(aligned16(key_pool) && aligned16(value_pool),
+              "Gather probe: pools must be 16-byte aligned.");
+  const int64_t splits = (page_size * max_pages + kProbeChunk - 1) / kProbeChunk;
+  TMC_REQUIRE(splits < 65536, "Gather probe: capacity too large.");
+  hipLaunchKernelGGL(gather_probe_kernel, dim3((unsigned)kv_heads, (unsigned)splits, (unsigned)batch),
+                     dim3(kThreads), 0, as_stream(stream), static_cast<const u32x4*>(key_pool),
+                     static_cast<const u32x4*>(value_pool), valid_lengths, block_tables,
+                     (int)max_pages, (int)page_size, (long)page_stride, (long)head_stride,
+                     (long)pool_pages, static_cast<uint32_t*>(sink));
+  return check_launch("gather_probe_kernel");
+}

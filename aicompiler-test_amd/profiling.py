@@ -1,13 +1,25 @@
 """Summaries of rocprofv3 results for the gfx950 decode backend.
 
-Two subcommands over the rocpd SQLite databases rocprofv3 writes:
+Subcommands over the rocpd SQLite databases rocprofv3 writes:
 
   summary  kernel-trace table (per kernel and grid: calls, average / median /
            min / max duration, VGPR, AGPR, LDS) as markdown;
   traffic  HBM bytes per launch of one kernel from two counter runs
            (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by
            what the same counter reads for the plain copy probe of known size
-           (tmc_copy_bytes) in the same run, written as JSON.
+           (tmc_copy_bytes) in the same run, written as JSON;
+  table    every kernel of a run (calls and average duration from a kernel
+           trace; HBM bytes per dispatch from the FETCH_SIZE, WRITE_SIZE and
+           EA read-request passes, the first two scaled by the copy probe);
+           optional algorithmic bytes per kernel; markdown and JSON;
+  mfma     MfmaUtil and the f16 MFMA operation count per dispatch of every
+           kernel that issues MFMA, with achieved TFLOP/s from the trace.
+
+FETCH_SIZE on gfx950 counts each 128-byte EA read request as 64 bytes (its
+expression adds TCC_BUBBLE x 128, and TCC_BUBBLE stays 0), so a read-heavy
+kernel's FETCH_SIZE is half its bytes; the copy probe calibrates the factor,
+and the EA request counters (TCC_EA0_RDREQ_32B/64B/128B: 32, 64 and 128
+bytes per request) give the read bytes without a scale, as a cross-check.
 
 Example (MI355X, repo root):
   rocprofv3 --pmc FETCH_SIZE -d out/f -o run -- python3 bench.py --no-extra --no-cpu
@@ -110,6 +122,133 @@ def traffic(fetch_db: str, write_db: str, kernel: str, template: str | None, cop
     return result
 
 
+def _per_kernel(db: str, counters: tuple) -> dict:
+    """(short name, grid) -> {counter: [per-dispatch values]} from a
+    counters_collection database."""
+    con = sqlite3.connect(db)
+    rows = con.execute("select kernel_name, grid_size_x, grid_size_y, grid_size_z, counter_name, "
+                       "value from counters_collection").fetchall()
+    out = collections.defaultdict(lambda: collections.defaultdict(list))
+    for name, gx, gy, gz, cname, value in rows:
+        if cname in counters:
+            out[(short_name(name), f"{gx}x{gy}x{gz}")][cname].append(float(value))
+    return out
+
+
+def _trace(db: str) -> dict:
+    """(short name, grid) -> list of durations in microseconds."""
+    con = sqlite3.connect(db)
+    out = collections.defaultdict(list)
+    for name, gx, gy, gz, dur in con.execute(
+            "select name, grid_x, grid_y, grid_z, duration from kernels").fetchall():
+        out[(short_name(name), f"{gx}x{gy}x{gz}")].append(dur / 1000.0)
+    return out
+
+
+def _mean(values: list) -> float:
+    return statistics.mean(values) if values else float("nan")
+
+
+def _copy_scale(per_kernel: dict, counter: str, copy_bytes: int) -> float:
+    vals = [v for (name, _), d in per_kernel.items() if name.startswith("copy_kernel")
+            for v in d.get(counter, [])]
+    if not vals:
+        raise SystemExit(f"no copy_kernel dispatch with {counter} in the database")
+    return copy_bytes / (statistics.mean(vals) * 1024.0)
+
+
+def _algorithmic(specs: list) -> list:
+    """'name_substring[@grid]=bytes' -> [(substring, grid or None, bytes)]."""
+    out = []
+    for spec in specs or []:
+        key, value = spec.rsplit("=", 1)
+        name, _, grid = key.partition("@")
+        out.append((name, grid or None, int(float(value))))
+    return out
+
+
+def traffic_table(fetch_db: str, write_db: str, rdreq_db: str, trace_db: str, copy_bytes: int,
+                  min_calls: int, algorithmic: list, hit_db: str | None = None) -> list:
+    fetch = _per_kernel(fetch_db, ("FETCH_SIZE",))
+    write = _per_kernel(write_db, ("WRITE_SIZE",))
+    rd = _per_kernel(rdreq_db, ("TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum",
+                                "TCC_EA0_RDREQ_128B_sum"))
+    trace = _trace(trace_db)
+    hits = _per_kernel(hit_db, ("TCC_HIT_sum", "TCC_MISS_sum")) if hit_db else {}
+    f_scale = _copy_scale(fetch, "FETCH_SIZE", copy_bytes)
+    w_scale = _copy_scale(write, "WRITE_SIZE", copy_bytes)
+    algo = _algorithmic(algorithmic)
+    rows = []
+    for key, durs in trace.items():
+        if len(durs) < min_calls or key not in fetch or key not in write:
+            continue
+        name, grid = key
+        f = _mean(fetch[key]["FETCH_SIZE"]) * 1024.0 * f_scale
+        w = _mean(write[key]["WRITE_SIZE"]) * 1024.0 * w_scale
+        r = rd.get(key, {})
+        ea = None
+        if r:
+            ea = (32 * _mean(r.get("TCC_EA0_RDREQ_32B_sum", [0.0])) +
+                  64 * _mean(r.get("TCC_EA0_RDREQ_64B_sum", [0.0])) +
+                  128 * _mean(r.get("TCC_EA0_RDREQ_128B_sum", [0.0])))
+        us = _mean(durs)
+        row = {"kernel": name, "grid": grid, "calls": len(durs), "avg_us": round(us, 3),
+               "read_bytes": int(f), "ea_read_bytes": None if ea is None else int(ea),
+               "written_bytes": int(w),
+               "achieved_gbps": round((f + w) / (us * 1e3), 1)}
+        h = hits.get(key, {})
+        if h:
+            hit, miss = _mean(h.get("TCC_HIT_sum", [0.0])), _mean(h.get("TCC_MISS_sum", [0.0]))
+            row["l2_hit_pct"] = round(100.0 * hit / (hit + miss), 2) if hit + miss else None
+        for sub, g, b in algo:
+            if sub in name and (g is None or g == grid):
+                row["algorithmic_bytes"] = b
+                row["traffic_over_algorithmic"] = round((f + w) / b, 4)
+                row["algorithmic_gbps"] = round(b / (us * 1e3), 1)
+        rows.append(row)
+    rows.sort(key=lambda x: -x["avg_us"] * x["calls"])
+    return [{"fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4)}] + rows
+
+
+def table_markdown(rows: list, title: str, command: str) -> str:
+    scales, rows = rows[0], rows[1:]
+    out = [f"# {title}", "", "Commands (repo root, MI355X box):", "", f"    {command}", "",
+           f"FETCH_SIZE scale {scales['fetch_scale']} and WRITE_SIZE scale "
+           f"{scales['write_scale']} (bytes per counted byte, from the 256 MiB copy probe). "
+           "`EA read` = 32/64/128 x the TCC_EA0_RDREQ_32B/64B/128B requests per dispatch "
+           "(no scale). GB/s = (read + written) / average duration of the kernel trace.", "",
+           "| kernel | grid | calls | avg us | read MB | EA read MB | written MB | GB/s | "
+           "L2 hit % | algorithmic MB | traffic / algorithmic |",
+           "|---|---|---|---|---|---|---|---|---|---|---|"]
+    for r in rows:
+        ea = "" if r["ea_read_bytes"] is None else f"{r['ea_read_bytes'] / 1e6:.3f}"
+        alg = f"{r['algorithmic_bytes'] / 1e6:.3f}" if "algorithmic_bytes" in r else ""
+        ratio = str(r.get("traffic_over_algorithmic", ""))
+        out.append(f"| `{r['kernel']}` | {r['grid']} | {r['calls']} | {r['avg_us']:.2f} | "
+                   f"{r['read_bytes'] / 1e6:.3f} | {ea} | {r['written_bytes'] / 1e6:.3f} | "
+                   f"{r['achieved_gbps']} | {r.get('l2_hit_pct', '')} | {alg} | {ratio} |")
+    return "\n".join(out) + "\n"
+
+
+def mfma_table(mfma_db: str, trace_db: str, min_calls: int) -> list:
+    m = _per_kernel(mfma_db, ("MfmaUtil", "SQ_INSTS_VALU_MFMA_MOPS_F16"))
+    trace = _trace(trace_db)
+    rows = []
+    for key, d in m.items():
+        mops = _mean(d.get("SQ_INSTS_VALU_MFMA_MOPS_F16", []))
+        durs = trace.get(key, [])
+        if not mops or len(durs) < min_calls:
+            continue
+        flops = mops * 512.0
+        us = _mean(durs)
+        rows.append({"kernel": key[0], "grid": key[1], "calls": len(durs), "avg_us": round(us, 3),
+                     "mfma_util_pct": round(_mean(d.get("MfmaUtil", [])), 2),
+                     "mfma_f16_flops": int(flops),
+                     "achieved_tflops": round(flops / (us * 1e6), 2)})
+    rows.sort(key=lambda x: -x["avg_us"] * x["calls"])
+    return rows
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -126,7 +265,50 @@ def main(argv=None) -> int:
     t.add_argument("--algorithmic", type=int)
     t.add_argument("--command", default="")
     t.add_argument("--out")
+    b = sub.add_parser("table")
+    b.add_argument("--fetch", required=True)
+    b.add_argument("--write", required=True)
+    b.add_argument("--rdreq", required=True)
+    b.add_argument("--trace", required=True)
+    b.add_argument("--hit")
+    b.add_argument("--copy-bytes", type=int, required=True)
+    b.add_argument("--min-calls", type=int, default=2)
+    b.add_argument("--algorithmic", action="append",
+                   help="name_substring[@grid]=bytes (repeatable)")
+    b.add_argument("--title", required=True)
+    b.add_argument("--command", required=True)
+    b.add_argument("--md")
+    b.add_argument("--json")
+    m = sub.add_parser("mfma")
+    m.add_argument("--db", required=True)
+    m.add_argument("--trace", required=True)
+    m.add_argument("--min-calls", type=int, default=2)
+    m.add_argument("--command", default="")
+    m.add_argument("--json")
     a = ap.parse_args(argv)
+    if a.cmd == "table":
+        rows = traffic_table(a.fetch, a.write, a.rdreq, a.trace, a.copy_bytes, a.min_calls,
+                             a.algorithmic, a.hit)
+        text = table_markdown(rows, a.title, a.command)
+        if a.md:
+            with open(a.md, "w") as f:
+                f.write(text)
+        if a.json:
+            with open(a.json, "w") as f:
+                json.dump({"command": a.command, "scales": rows[0], "kernels": rows[1:]}, f,
+                          indent=1)
+                f.write("\n")
+        sys.stdout.write(text)
+        return 0
+    if a.cmd == "mfma":
+        rows = mfma_table(a.db, a.trace, a.min_calls)
+        text = json.dumps({"command": a.command, "peak_tflops_f16": 2500.0, "kernels": rows},
+                          indent=1) + "\n"
+        if a.json:
+            with open(a.json, "w") as f:
+                f.write(text)
+        sys.stdout.write(text)
+        return 0
     if a.cmd == "summary":
         sys.stdout.write(kernel_summary(a.db, a.title, a.command))
         return 0

@@ -38,6 +38,8 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
 COPY_PROBE_BYTES = 256 << 20
+# Distinct bytes every kernel-level rotation spans (2 x the 256 MB Infinity Cache)
+ROTATE_BYTES = 512 << 20
 # HBM bytes per launch of the dominant kernel, measured with rocprofv3
 # FETCH_SIZE / WRITE_SIZE and scaled by the copy probe (profiling.py traffic)
 TRAFFIC_FILE = "profiles/gate_up_traffic.json"
@@ -151,6 +153,19 @@ def build_sequences(tmc, rt, block):
     return rt.sequence(execs), execs, rt.sequence(gates)
 
 
+def copy_probe(tmc, torch) -> None:
+    """Three copies of known size (256 MiB read + 256 MiB written): the
+    reference dispatches that scale FETCH_SIZE / WRITE_SIZE (and the EA
+    request counters) when a command runs under rocprofv3 --pmc
+    (aicompiler-test_amd/profiling.py)."""
+    src = torch.empty(COPY_PROBE_BYTES // 2, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        tmc.copy_bytes(src, dst, COPY_PROBE_BYTES)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def time_loop(torch, fn, iters: int, replays: int = 5) -> float:
     """Seconds per call of fn(i): `iters` calls captured once into a CUDA (HIP)
     graph on a side stream, then the graph replayed `replays` times between
@@ -218,14 +233,17 @@ def extra_measurements(tmc, torch, iters: int) -> dict:
     import numpy as np
     out = {}
     f16 = torch.float16
-    # C1: GEMV fp16 W[4096,4096] -> fp32 y, 8 rotating weight copies (256 MiB)
-    ws = [torch.empty((4096, 4096), dtype=f16, device="cuda") for _ in range(8)]
+    # Every rotation below spans at least ROTATE_BYTES of distinct buffers,
+    # twice the 256 MB Infinity Cache, so no timed launch can be served from it.
+    # C1: GEMV fp16 W[4096,4096] -> fp32 y, 16 rotating weight copies (512 MiB)
+    c1_copies = -(-ROTATE_BYTES // (4096 * 4096 * 2))
+    ws = [torch.empty((4096, 4096), dtype=f16, device="cuda") for _ in range(c1_copies)]
     for c, w in enumerate(ws):
         tmc.fill_normal(w, 103 + c, 0.0, 0.02)
     x = torch.empty((1, 4096), dtype=f16, device="cuda")
     tmc.fill_normal(x, 101)
     y = torch.empty((1, 4096), dtype=torch.float32, device="cuda")
-    sec = time_loop(torch, lambda i: tmc.gemv(x, ws[i % 8], y), iters)
+    sec = time_loop(torch, lambda i: tmc.gemv(x, ws[i % c1_copies], y), iters)
     gemv_bytes = 4096 * 4096 * 2 + 4096 * 2 + 4096 * 4
     out["c1_gemv_4096x4096_gbps"] = round(gemv_bytes / sec / 1e9, 1)
     out["c1_gemv_us"] = round(sec * 1e6, 2)
@@ -243,7 +261,7 @@ def extra_measurements(tmc, torch, iters: int) -> dict:
     del blk
     # C3: contiguous attention, 32 heads x 128, capacity 4096, valid 4096 (L=4095 + 1)
     heads, d, cap = 32, 128, 4096
-    copies = 4
+    copies = -(-ROTATE_BYTES // (2 * heads * cap * d * 2))  # 8 K/V pairs of 64 MiB
     ks = [torch.empty((1, heads, cap, d), dtype=f16, device="cuda") for _ in range(copies)]
     vs = [torch.empty((1, heads, cap, d), dtype=f16, device="cuda") for _ in range(copies)]
     for c in range(copies):
@@ -260,23 +278,28 @@ def extra_measurements(tmc, torch, iters: int) -> dict:
     c3_bytes = 2 * heads * 4096 * d * 2 + 2 * heads * d * 2
     out["c3_attention_L4095_gbps"] = round(c3_bytes / sec / 1e9, 1)
     del ks, vs
-    # C4: paged GQA attention, 16 requests, 32 q / 8 kv heads, pages of 16
+    # C4: paged GQA attention, 16 requests, 32 q / 8 kv heads, pages of 16.
+    # Two pools of 8192 pages (K and V, 512 MiB each pool); each holds 3
+    # disjoint table sets, so the rotation reads 6 x 148 MB of distinct pages.
     batch, qh, kvh, p, pages, max_pages = 16, 32, 8, 16, 8192, 256
     lengths = np.random.default_rng(403).integers(64, 4096, size=batch) + 1
-    perm = np.random.default_rng(404).permutation(pages).astype(np.int32)
     need = (lengths + p - 1) // p
     sets = []
-    cursor = 0
-    while cursor + need.sum() <= pages and len(sets) < 3:  # disjoint table sets rotate
-        t = np.full((batch, max_pages), -1, np.int32)
-        for i in range(batch):
-            t[i, :need[i]] = perm[cursor:cursor + need[i]]
-            cursor += need[i]
-        sets.append(torch.from_numpy(t).cuda())
-    kp = torch.empty((pages, kvh, p, d), dtype=f16, device="cuda")
-    vp = torch.empty((pages, kvh, p, d), dtype=f16, device="cuda")
-    tmc.fill_normal(kp, 401)
-    tmc.fill_normal(vp, 402)
+    pools = []
+    for pool in range(2):
+        perm = np.random.default_rng(404 + pool).permutation(pages).astype(np.int32)
+        kp = torch.empty((pages, kvh, p, d), dtype=f16, device="cuda")
+        vp = torch.empty((pages, kvh, p, d), dtype=f16, device="cuda")
+        tmc.fill_normal(kp, 401 + 7 * pool)
+        tmc.fill_normal(vp, 402 + 7 * pool)
+        pools.append((kp, vp))
+        cursor = 0
+        for _ in range(3):
+            t = np.full((batch, max_pages), -1, np.int32)
+            for i in range(batch):
+                t[i, :need[i]] = perm[cursor:cursor + need[i]]
+                cursor += need[i]
+            sets.append((pool, torch.from_numpy(t).cuda()))
     qd = torch.empty((batch, qh * d), dtype=f16, device="cuda")
     tmc.fill_normal(qd, 405)
     od = torch.empty((batch, qh * d), dtype=f16, device="cuda")
@@ -284,13 +307,43 @@ def extra_measurements(tmc, torch, iters: int) -> dict:
     active = torch.tensor([batch], dtype=torch.int32, device="cuda")
     wsb = tmc.attention_workspace_bytes(batch, qh, kvh, d, max_pages * p)
     wsp = torch.zeros(max(wsb // 4, 1), dtype=torch.float32, device="cuda")
-    sec = time_loop(torch, lambda i: tmc.paged_decode_attention(
-        qd, kp, vp, vl, sets[i % len(sets)], active, od, batch, qh, kvh, d, p, max_pages,
-        kvh * p * d, p * d, wsp), iters)
+
+    def c4(i):
+        pool, table = sets[i % len(sets)]
+        kp, vp = pools[pool]
+        tmc.paged_decode_attention(qd, kp, vp, vl, table, active, od, batch, qh, kvh, d, p,
+                                   max_pages, kvh * p * d, p * d, wsp)
+
+    sec = time_loop(torch, c4, iters)
     c4_bytes = int(lengths.sum()) * kvh * d * 2 * 2 + 4 * int(need.sum()) + 2 * batch * qh * d * 2
     out["c4_paged_gqa_attention_gbps"] = round(c4_bytes / sec / 1e9, 1)
     out["c4_paged_gqa_attention_us"] = round(sec * 1e6, 2)
     out["c4_bytes"] = c4_bytes
+    # The same K/V bytes through the same tables with nothing but loads
+    # (tmc_paged_gather_probe): the ceiling of the gather itself.
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def gather(i):
+        pool, table = sets[i % len(sets)]
+        kp, vp = pools[pool]
+        tmc.paged_gather_probe(kp, vp, vl, table, batch, kvh, d, p, max_pages, kvh * p * d, p * d,
+                               sink)
+
+    sec = time_loop(torch, gather, iters)
+    kv_bytes = int(lengths.sum()) * kvh * d * 2 * 2
+    out["c4_gather_probe_gbps"] = round(kv_bytes / sec / 1e9, 1)
+    out["c4_gather_probe_us"] = round(sec * 1e6, 2)
+    del pools
+    out["rotation_min_bytes"] = ROTATE_BYTES
+    # rocprofv3 counter tables behind these figures (per-kernel HBM bytes
+    # from FETCH_SIZE / WRITE_SIZE and the EA request counters, L2 hit rate,
+    # MfmaUtil), made by aicompiler-test_amd/profile_counters.sh
+    out["counter_files"] = {
+        "c1_c2b8_c3_c4": "profiles/c1_c4_kernels_traffic.md",
+        "c4_attention": "profiles/attention_c4_counters.json",
+        "c2_b8_mfma": "profiles/c2_b8_mfma_utilisation.json",
+        "c5_decode": "profiles/c5_decode_prefill_traffic.md",
+        "c5_mfma": "profiles/c5_mfma_utilisation.json"}
     return out
 
 
@@ -454,7 +507,13 @@ def main() -> int:
     ap.add_argument("--c5-only", action="store_true",
                     help="run only the C5 decode measurement (batch 1 and 16) and print its JSON "
                          "(for profiling)")
+    ap.add_argument("--extra-only", action="store_true",
+                    help="run only the copy probe and the C1-C4 kernel measurements and print "
+                         "their JSON (for profiling)")
+    ap.add_argument("--decode-tokens", type=int, default=C5["decode_tokens"],
+                    help="greedy decode tokens per sequence in the C5 measurement")
     args = ap.parse_args()
+    C5["decode_tokens"] = args.decode_tokens
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(run with --gpus 1).", file=sys.stderr)
@@ -467,7 +526,12 @@ def main() -> int:
         print(json.dumps({"prefill": prefill_gpu(tmc)}), flush=True)
         return 0
     if args.c5_only:
+        copy_probe(tmc, torch)
         print(json.dumps({"c5_decode": c5_gpu(tmc)}), flush=True)
+        return 0
+    if args.extra_only:
+        copy_probe(tmc, torch)
+        print(json.dumps({"extra": extra_measurements(tmc, torch, 40)}), flush=True)
         return 0
     block = MlpBlock(tmc, torch, args.batch, args.copies)
     # The timed region replays a HIP graph built by the backend's own
@@ -492,15 +556,7 @@ def main() -> int:
     value = bytes_["total"] * steps / elapsed / 1e9
     print(f"[bench] timed {steps} steps in {elapsed:.4f} s", flush=True)
 
-    # copy probe of known size (256 MiB read + 256 MiB written): the
-    # reference dispatch that scales FETCH_SIZE / WRITE_SIZE counters when
-    # this command runs under rocprofv3 --pmc (aicompiler-test_amd/profiling.py)
-    probe_src = torch.empty(COPY_PROBE_BYTES // 2, dtype=torch.float16, device="cuda")
-    probe_dst = torch.empty_like(probe_src)
-    for _ in range(3):
-        tmc.copy_bytes(probe_src, probe_dst, COPY_PROBE_BYTES)
-    torch.cuda.synchronize()
-    del probe_src, probe_dst
+    copy_probe(tmc, torch)
 
     # dominant kernel alone: gate/up + SiLU*Mul over the rotating weight
     # copies, HIP events on the runtime stream around graph replays

@@ -453,6 +453,19 @@ int tmc_paged_decode_attention_noalloc(const void *q, const void *key_pool,
 /* Bytes of the static scratch behind tmc_paged_decode_attention_noalloc. */
 size_t tmc_attention_scratch_bytes(void);
 
+/* Bandwidth probe of the paged attention access pattern (head_dim 128, pages
+ * of a multiple of 16 positions): reads
+ * the K and V bytes tmc_paged_decode_attention would read for these lengths
+ * and block tables, and nothing else; `sink` (4 bytes of device memory) is
+ * written only when the xor of the loaded words hits a fixed constant.  No
+ * reference counterpart: it measures the ceiling of the gather itself, as
+ * tmc_copy_bytes does for streaming. */
+int tmc_paged_gather_probe(const void *key_pool, const void *value_pool,
+                           const int32_t *valid_lengths, const int32_t *block_tables,
+                           int64_t batch, int64_t kv_heads, int64_t head_dim, int64_t page_size,
+                           int64_t max_pages, int64_t pool_pages, int64_t page_stride,
+                           int64_t head_stride, void *sink, void *stream);
+
 /* Decode-step fusion of emitServingRoPE (DecoderLLMMetalEmitter.cpp:260-312)
  * for q and k with emitServingPagedCacheAppend (:314-373) for the rotated k
  * and v, reading one fused projection row per request laid out

@@ -70,6 +70,13 @@ def test_argument_validation_fails_before_device_work(tmc):
     assert "null" in tmc.last_error()
     assert lib.tmc_buf_write_raw_async(None, p, 1, 0) != 0
     assert "invalid range" in tmc.last_error()
+    # the gather probe takes the attention's geometry rules
+    assert lib.tmc_paged_gather_probe(p, p, p, p, 16, 8, 64, 16, 256, 8192, 16384, 2048, p,
+                                      None) != 0
+    assert "head_dim must be 128" in tmc.last_error()
+    assert lib.tmc_paged_gather_probe(p, p, p, None, 16, 8, 128, 16, 256, 8192, 16384, 2048, p,
+                                      None) != 0
+    assert "null" in tmc.last_error()
     assert lib.tmc_buf_copy_async(None, 0, None, 0, 1) != 0
     assert "different runtimes" in tmc.last_error()
 
