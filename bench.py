@@ -398,9 +398,50 @@ def c5_gpu(tmc) -> dict:
         out[f"b{batch}_prompt_tokens_per_s"] = round(r["prompt_tokens_per_second"], 1)
         print(f"[bench] C5 batch {batch}: {out[f'b{batch}_tokens_per_s']} tokens/s, prompts "
               f"{out[f'b{batch}_prompt_tokens_per_s']} tokens/s", flush=True)
+        out[f"b{batch}_serving"] = c5_serving(host, rt, model, batch)
     out["prefill_chunk"] = C5["prefill_chunk"]
     del model
     return out
+
+
+def c5_serving(host, rt, model, batch: int) -> dict:
+    """The same requests through runContinuousBatch (ServingRuntime.cpp:513-930):
+    admission with packed chunked prefill, then scheduler-driven batched decode
+    ticks with a host round trip per tick (tokens read back, tables updated),
+    as a serving loop runs them.  tokens/s over the whole run and over the
+    ticks without prompt rows."""
+    prompts = c5_prompts(batch)
+    specs = []
+    for i, prompt in enumerate(prompts):
+        spec = host.ServingRequestSpec()
+        spec.id = f"r{i}"
+        spec.prompt_token_ids = [float(t) for t in prompt]
+        spec.decode_token_count = C5["decode_tokens"]
+        spec.arrival_step = 0
+        specs.append(spec)
+    pages = (max(len(p) for p in prompts) + C5["decode_tokens"] + C5["page_size"] - 1) \
+        // C5["page_size"]
+    config = host.ServingConfig()
+    config.page_size = C5["page_size"]
+    config.physical_pages_per_layer = max(batch * pages, C5["capacity"] // C5["page_size"])
+    config.maximum_batch_size = batch
+    config.record_decode_logits = False
+    config.record_prefill_logits = False
+    config.prefill_chunk_size = C5["prefill_chunk"]
+    config.prefill_requests_per_chunk = batch
+    r = host.run_continuous_batch(rt, model, specs, config)
+    if not r["passed"]:
+        raise RuntimeError(f"C5 serving batch {batch}: {r['error']}")
+    m = r["metrics"]
+    print(f"[bench] C5 serving batch {batch}: {m['decode_phase_tokens_per_second']:.1f} decode "
+          f"tokens/s, {m['tokens_per_second']:.1f} over the run", flush=True)
+    return {"decode_tokens_per_s": round(m["decode_phase_tokens_per_second"], 1),
+            "run_tokens_per_s": round(m["tokens_per_second"], 1),
+            "total_ms": round(m["total_time_us"] / 1e3, 2),
+            "decoded_tokens": m["decoded_tokens"], "prompt_tokens": m["prompt_tokens"],
+            "decode_ticks": m["decode_command_submissions"],
+            "prefill_chunks": m["prefill_chunk_submissions"],
+            "scheduler_overhead_ms": round(m["scheduler_overhead_us"] / 1e3, 2)}
 
 
 def prefill_flops(tokens: int) -> float:
