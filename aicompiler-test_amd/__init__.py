@@ -98,6 +98,7 @@ def _declare(l):
         "tmc_argmax_f32": (i32, [vp, vp, i64, i64, vp]),
         "tmc_fill_normal": (i32, [vp, i32, i64, C.c_uint64, f, f, vp]),
         "tmc_copy_bytes": (i32, [vp, vp, sz, vp]),
+        "tmc_elementwise": (i32, [i32, vp, vp, vp, i32, i64, i32, vp]),
         "tmc_rt_create": (i32, [C.POINTER(vp)]),
         "tmc_rt_destroy": (None, [vp]),
         "tmc_rt_is_available": (i32, [vp]),

@@ -25,9 +25,9 @@ BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "libtmc_hip.so")
 HOST = os.path.join(HERE, "host")
 HOST_OUT = os.path.join(HERE, "libtmc_host.so")
-HOST_SOURCES = ["HipRuntime.cpp", "KVCacheState.cpp", "DecoderLLM.cpp", "Benchmark.cpp",
+HOST_SOURCES = ["TensorIR.cpp", "HipRuntime.cpp", "KVCacheState.cpp", "DecoderLLM.cpp", "Benchmark.cpp",
                 "ServingRuntime.cpp", "Tuning.cpp", "Importer.cpp", "KernelRegistry.cpp",
-                "StatefulExecutor.cpp"]
+                "StatefulExecutor.cpp", "GraphExecutor.cpp"]
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 CXX = os.environ.get("CXX", "g++")
 CXXFLAGS = ["-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",

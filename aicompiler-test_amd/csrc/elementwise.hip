@@ -256,6 +256,27 @@ __global__ __launch_bounds__(kThreads) void add_kernel(const T* __restrict__ a,
     out[i] = from_float<T>(to_float<T>(a[i]) + to_float<T>(b[i]));
 }
 
+// Element-wise operations of the graph path (TensorIR Add, Mul, SiLU and the
+// fused SiLU + Mul region, FusionMetalEmitter.cpp:103-210 in the reference),
+// for any workgroup size: one element per thread per grid stride.  SiLU
+// rounds its activation to T before a multiply, as a stored SiLU output
+// would be, so the fused form equals SiLU followed by Mul bit for bit.
+enum EwOp { kEwAdd = 0, kEwMul = 1, kEwSilu = 2, kEwSiluMul = 3 };
+
+template <typename T, int OP>
+__global__ __launch_bounds__(kThreads) void elementwise_kernel(const T* __restrict__ a,
+                                                              const T* __restrict__ b,
+                                                              T* __restrict__ out, size_t count) {
+  const size_t step = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += step) {
+    const float x = to_float<T>(a[i]);
+    if constexpr (OP == kEwAdd) out[i] = from_float<T>(x + to_float<T>(b[i]));
+    if constexpr (OP == kEwMul) out[i] = from_float<T>(x * to_float<T>(b[i]));
+    if constexpr (OP == kEwSilu) out[i] = from_float<T>(x / (1.0f + expf(-x)));
+    if constexpr (OP == kEwSiluMul) out[i] = silu_mul_one<T>(a[i], b[i]);
+  }
+}
+
 // emitDecoderEmbedding (DecoderLLMMetalEmitter.cpp:35-61).
 template <typename T>
 __global__ __launch_bounds__(kThreads) void embedding_kernel(const int32_t* __restrict__ tokens,
@@ -776,6 +797,33 @@ extern "C" int tmc_add(const void* a, const void* b, void* out, int dtype, int64
                                             static_cast<const T*>(b), static_cast<T*>(out),
                                             (size_t)count));
   return check_launch("add_kernel");
+}
+
+extern "C" int tmc_elementwise(int op, const void* a, const void* b, void* out, int dtype,
+                               int64_t count, int threads, void* stream) {
+  TMC_REQUIRE(op >= kEwAdd && op <= kEwSiluMul, "Elementwise: unknown operation.");
+  TMC_REQUIRE(a && out && (op == kEwSilu || b), "Elementwise: null device pointer.");
+  TMC_REQUIRE(float_dtype(dtype) && count > 0, "Elementwise: invalid dtype or count.");
+  TMC_REQUIRE(threads == 64 || threads == 128 || threads == 256,
+              "Elementwise: threads must be 64, 128 or 256.");
+  const unsigned blocks =
+      (unsigned)std::min<size_t>(((size_t)count + threads - 1) / threads, 65536);
+  switch (op) {
+#define TMC_EW_CASE(OPC)                                                                   \
+  case OPC:                                                                                \
+    TMC_DISPATCH_T(dtype, hipLaunchKernelGGL((elementwise_kernel<T, OPC>), dim3(blocks),   \
+                                              dim3(threads), 0, as_stream(stream),         \
+                                              static_cast<const T*>(a),                    \
+                                              static_cast<const T*>(b), static_cast<T*>(out), \
+                                              (size_t)count));                             \
+    break;
+    TMC_EW_CASE(kEwAdd)
+    TMC_EW_CASE(kEwMul)
+    TMC_EW_CASE(kEwSilu)
+    TMC_EW_CASE(kEwSiluMul)
+#undef TMC_EW_CASE
+  }
+  return check_launch("elementwise_kernel");
 }
 
 extern "C" int tmc_embedding(const int32_t* tokens, const void* table, void* out, int dtype,

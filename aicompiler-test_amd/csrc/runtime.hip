@@ -537,18 +537,37 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     }
     return true;
   }
-  if (name == "silu_mul" || name == "add") {
+  if (name == "silu_mul" || name == "add" || name == "mul" || name == "silu") {
+    // Element-wise ops of the decoder and of the graph path.  Without a
+    // `threads` parameter add and silu_mul keep the decoder's launches;
+    // with one (64, 128 or 256, the graph tuner's candidates) or for mul
+    // and silu they run tmc_elementwise.
     const int64_t n = param_int(p, "count");
     NEED(n > 0 && (dt == TMC_F16 || dt == TMC_F32), "elementwise kernel needs count and f16|f32.");
-    s.inputs = {dt, dt};
+    const bool explicit_threads = p.find("threads") != p.end();
+    const int threads = (int)param_int(p, "threads", 256);
+    NEED(threads == 64 || threads == 128 || threads == 256,
+         "elementwise threads must be 64, 128 or 256.");
+    const bool unary = name == "silu";
+    s.inputs = unary ? std::vector<int>{dt} : std::vector<int>{dt, dt};
     s.outputs = {dt};
-    s.groups = (size_t)((n + 255) / 256);
-    s.counts = {(size_t)n, (size_t)n, (size_t)n};
-    const bool silu = name == "silu_mul";
-    s.launch = [=](const LaunchContext& c) {
-      return silu ? tmc_silu_mul(c.ptrs[0], c.ptrs[1], c.ptrs[2], dt, n, c.stream)
-                  : tmc_add(c.ptrs[0], c.ptrs[1], c.ptrs[2], dt, n, c.stream);
-    };
+    s.threads = (size_t)threads;
+    s.groups = (size_t)((n + threads - 1) / threads);
+    s.counts = unary ? std::vector<size_t>{(size_t)n, (size_t)n}
+                     : std::vector<size_t>{(size_t)n, (size_t)n, (size_t)n};
+    const int op = name == "add" ? 0 : name == "mul" ? 1 : name == "silu" ? 2 : 3;
+    if (!explicit_threads && (op == 0 || op == 3)) {
+      s.launch = [=](const LaunchContext& c) {
+        return op == 3 ? tmc_silu_mul(c.ptrs[0], c.ptrs[1], c.ptrs[2], dt, n, c.stream)
+                       : tmc_add(c.ptrs[0], c.ptrs[1], c.ptrs[2], dt, n, c.stream);
+      };
+    } else {
+      s.launch = [=](const LaunchContext& c) {
+        return unary ? tmc_elementwise(op, c.ptrs[0], nullptr, c.ptrs[1], dt, n, threads, c.stream)
+                     : tmc_elementwise(op, c.ptrs[0], c.ptrs[1], c.ptrs[2], dt, n, threads,
+                                       c.stream);
+      };
+    }
     return true;
   }
   if (name == "embedding") {

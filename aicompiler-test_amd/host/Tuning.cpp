@@ -15,26 +15,6 @@
 
 namespace tensor {
 
-std::size_t TensorType::elementCount() const {
-  std::size_t count = 1;
-  for (const auto d : shape) count *= d;
-  return count;
-}
-
-void RMSNormOp::validate() const {
-  if (input.shape.empty()) throw std::invalid_argument("RMSNorm input must be ranked.");
-  const bool isFloat = input.dtype == DType::Float16 || input.dtype == DType::Float32 ||
-                       input.dtype == DType::BFloat16;
-  if (!isFloat || weight.dtype != input.dtype || output.dtype != input.dtype)
-    throw std::invalid_argument("RMSNorm requires matching floating-point tensors.");
-  if (output.shape != input.shape)
-    throw std::invalid_argument("RMSNorm output shape must match input shape.");
-  if (weight.shape.size() != 1 || weight.shape.front() != input.shape.back())
-    throw std::invalid_argument("RMSNorm weight must match the last input dimension.");
-  if (!std::isfinite(epsilon) || epsilon <= 0.0f)
-    throw std::invalid_argument("RMSNorm epsilon must be finite and positive.");
-}
-
 namespace validation {
 
 ValidationResult compare(const std::vector<float>& actual, const std::vector<double>& reference,

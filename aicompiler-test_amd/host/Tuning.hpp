@@ -18,6 +18,7 @@
 #include "Benchmark.hpp"
 #include "HipRuntime.hpp"
 #include "KVCacheState.hpp"
+#include "TensorIR.hpp"
 
 #include <cstddef>
 #include <functional>
@@ -29,23 +30,6 @@
 #include <vector>
 
 namespace tensor {
-
-// The fields of TensorType / RMSNormOp (TensorIR.hpp:21-27, 98-105) that the
-// RMSNorm tuner reads; contiguous row-major tensors.
-struct TensorType {
-  std::vector<std::size_t> shape;
-  DType dtype = DType::Float32;
-  [[nodiscard]] std::size_t elementCount() const;
-};
-
-struct RMSNormOp {
-  TensorType input;
-  TensorType weight;
-  TensorType output;
-  float epsilon = 1e-5f;
-  // RMSNormOp::validate (TensorIR.cpp:94-114); throws std::invalid_argument.
-  void validate() const;
-};
 
 namespace validation {
 

@@ -11,6 +11,7 @@
 
 #include "Benchmark.hpp"
 #include "DecoderLLM.hpp"
+#include "GraphExecutor.hpp"
 #include "Importer.hpp"
 #include "KVCacheState.hpp"
 #include "ServingRuntime.hpp"
@@ -129,6 +130,34 @@ py::dict servingToDict(const ServingExecutionResult& r) {
   metrics["kv_pool_storage_bytes"] = m.kvPoolStorageBytes;
   metrics["batched_activation_storage_bytes"] = m.batchedActivationStorageBytes;
   d["metrics"] = metrics;
+  return d;
+}
+
+OpAttributes toAttributes(const py::object& o) {
+  if (o.is_none()) return std::monostate{};
+  if (py::isinstance<RMSNormAttributes>(o)) return o.cast<RMSNormAttributes>();
+  if (py::isinstance<ReshapeAttributes>(o)) return o.cast<ReshapeAttributes>();
+  if (py::isinstance<TransposeAttributes>(o)) return o.cast<TransposeAttributes>();
+  if (py::isinstance<SoftmaxAttributes>(o)) return o.cast<SoftmaxAttributes>();
+  throw std::invalid_argument("Unsupported attribute object.");
+}
+
+GraphInputs toGraphInputs(const py::dict& d) {
+  GraphInputs in;
+  for (const auto& item : d) {
+    const auto values = py::array_t<float, py::array::c_style | py::array::forcecast>::ensure(item.second);
+    if (!values) throw std::invalid_argument("Graph input values must be a float sequence.");
+    in[item.first.cast<ValueId>()] = std::vector<float>(values.data(), values.data() + values.size());
+  }
+  return in;
+}
+
+py::dict graphResultDict(const runtime::GraphExecutionResult& r) {
+  py::dict d;
+  d["passed"] = r.passed;
+  d["outputs"] = r.outputs;
+  d["gpu_us"] = r.gpuExecutionTimeUs ? py::cast(*r.gpuExecutionTimeUs) : py::none();
+  d["error"] = r.errorMessage;
   return d;
 }
 
@@ -954,4 +983,108 @@ PYBIND11_MODULE(_tmc_host, m) {
         r.report(log);
         return log.str();
       });
+
+  // ---------------------------------------------------------------- graph path
+  py::enum_<Layout>(m, "Layout").value("Contiguous", Layout::Contiguous).value("Strided", Layout::Strided);
+  py::enum_<OpType>(m, "OpType")
+      .value("Add", OpType::Add).value("Mul", OpType::Mul).value("MatMul", OpType::MatMul)
+      .value("RMSNorm", OpType::RMSNorm).value("LayerNorm", OpType::LayerNorm)
+      .value("ReLU", OpType::ReLU).value("SiLU", OpType::SiLU).value("Softmax", OpType::Softmax)
+      .value("RoPE", OpType::RoPE).value("ReduceSum", OpType::ReduceSum)
+      .value("ReduceMean", OpType::ReduceMean).value("Reshape", OpType::Reshape)
+      .value("View", OpType::View).value("Transpose", OpType::Transpose)
+      .value("Contiguous", OpType::Contiguous).value("MaskedFill", OpType::MaskedFill)
+      .value("Slice", OpType::Slice).value("Embedding", OpType::Embedding)
+      .value("Gather", OpType::Gather);
+  py::class_<TensorType>(m, "TensorType")
+      .def(py::init([](std::vector<std::size_t> shape, DType dtype) {
+             TensorType t;
+             t.shape = std::move(shape);
+             t.dtype = dtype;
+             return t;
+           }),
+           py::arg("shape"), py::arg("dtype") = DType::Float32)
+      .def_readwrite("shape", &TensorType::shape)
+      .def_readwrite("dtype", &TensorType::dtype)
+      .def_readwrite("layout", &TensorType::layout)
+      .def_readwrite("explicit_strides", &TensorType::explicitStrides)
+      .def("element_count", &TensorType::elementCount)
+      .def("storage_element_count", &TensorType::storageElementCount)
+      .def("strides", &TensorType::strides)
+      .def("is_contiguous", &TensorType::isContiguous);
+  py::class_<RMSNormAttributes>(m, "RMSNormAttributes")
+      .def(py::init([](float eps, std::int64_t axis) { return RMSNormAttributes{eps, axis}; }),
+           py::arg("epsilon") = 1e-5f, py::arg("axis") = -1);
+  py::class_<ReshapeAttributes>(m, "ReshapeAttributes")
+      .def(py::init([](std::vector<std::size_t> shape) { return ReshapeAttributes{std::move(shape)}; }));
+  py::class_<TransposeAttributes>(m, "TransposeAttributes")
+      .def(py::init([](std::int64_t a, std::int64_t b) { return TransposeAttributes{a, b}; }),
+           py::arg("first") = 0, py::arg("second") = 1);
+  py::class_<SoftmaxAttributes>(m, "SoftmaxAttributes")
+      .def(py::init([](std::int64_t axis) { return SoftmaxAttributes{axis}; }), py::arg("axis") = -1);
+  py::class_<TensorGraph>(m, "TensorGraph")
+      .def(py::init<>())
+      .def("add_input", &TensorGraph::addInput)
+      .def("add_node",
+           [](TensorGraph& g, OpType op, std::vector<ValueId> operands, py::object attributes,
+              std::string name) { return g.addNode(op, std::move(operands), toAttributes(attributes), std::move(name)); },
+           py::arg("op"), py::arg("operands"), py::arg("attributes") = py::none(), py::arg("name") = "")
+      .def_readwrite("outputs", &TensorGraph::outputs)
+      .def_readonly("inputs", &TensorGraph::inputs)
+      .def("value_count", [](const TensorGraph& g) { return g.values.size(); });
+  m.def("analyze_graph", [](const TensorGraph& g) {
+    const auto a = analyzer::analyze(g);
+    py::dict d;
+    d["types"] = a.types;
+    std::vector<py::object> alias;
+    for (const auto& x : a.aliasOf) alias.push_back(x ? py::cast(*x) : py::none());
+    d["alias_of"] = alias;
+    return d;
+  });
+  m.def("graph_regions", [](const TensorGraph& g) {
+    py::list out;
+    for (const auto& r : analyzer::formRegions(analyzer::analyze(g))) {
+      py::dict d;
+      d["fusion"] = analyzer::fusionName(r.fusion);
+      d["nodes"] = r.nodes;
+      d["inputs"] = r.inputs;
+      d["outputs"] = r.outputs;
+      out.append(d);
+    }
+    return out;
+  });
+  m.def("evaluate_graph", [](const TensorGraph& g, const py::dict& inputs) {
+    const auto ref = validation::evaluateGraph(analyzer::analyze(g), toGraphInputs(inputs));
+    py::dict d;
+    d["values"] = ref.values;
+    d["outputs"] = ref.outputs;
+    return d;
+  });
+  py::class_<runtime::CompiledGraph, std::shared_ptr<runtime::CompiledGraph>>(m, "CompiledGraph")
+      .def("run", [](const runtime::CompiledGraph& c) {
+        runtime::GraphExecutionResult r;
+        {
+          py::gil_scoped_release release;
+          r = c.run();
+        }
+        return graphResultDict(r);
+      })
+      .def("unit_names", &runtime::CompiledGraph::unitNames);
+  m.def("compile_graph", [](hip::HipRuntime& rt, const TensorGraph& g, const py::dict& inputs) {
+    const GraphInputs in = toGraphInputs(inputs);
+    std::ostringstream log;
+    runtime::GraphCompilation c;
+    {
+      py::gil_scoped_release release;
+      c = runtime::compileGraph(rt, g, in, log);
+    }
+    py::dict d;
+    d["error"] = c.errorMessage;
+    d["log"] = log.str();
+    d["output_types"] = c.outputTypes;
+    d["reference_outputs"] = c.referenceOutputs;
+    d["graph"] = c.executable ? py::cast(std::shared_ptr<runtime::CompiledGraph>(std::move(c.executable)))
+                              : py::none();
+    return d;
+  });
 }

@@ -353,6 +353,14 @@ int tmc_silu_mul(const void *gate, const void *up, void *out, int dtype, int64_t
 /* emitDecoderAdd (DecoderLLMMetalEmitter.cpp:375-393): out = h(a + b). */
 int tmc_add(const void *a, const void *b, void *out, int dtype, int64_t count, void *stream);
 
+/* Element-wise kernels of the graph path with a chosen workgroup size (64,
+ * 128 or 256): op 0 Add h(a + b), 1 Mul h(a * b), 2 SiLU h(a / (1 + exp(-a)))
+ * (b unused, may be NULL), 3 the fused SiLU + Mul region
+ * (FusionMetalEmitter.cpp:103-210), equal to op 2 followed by op 1.  The
+ * graph executor's baseline and fused-region kernels. */
+int tmc_elementwise(int op, const void *a, const void *b, void *out, int dtype, int64_t count,
+                    int threads, void *stream);
+
 /* emitDecoderEmbedding (DecoderLLMMetalEmitter.cpp:35-61): out[r] =
  * table[token[r]]; an out-of-range token leaves its row untouched. */
 int tmc_embedding(const int32_t *tokens, const void *table, void *out, int dtype, int64_t rows,

@@ -70,6 +70,11 @@ def test_argument_validation_fails_before_device_work(tmc):
     assert "null" in tmc.last_error()
     assert lib.tmc_buf_write_raw_async(None, p, 1, 0) != 0
     assert "invalid range" in tmc.last_error()
+    # graph-path element-wise kernels: the tuner's workgroup sizes only
+    assert lib.tmc_elementwise(0, p, p, p, 0, 64, 512, None) != 0
+    assert "threads must be 64, 128 or 256" in tmc.last_error()
+    assert lib.tmc_elementwise(1, p, None, p, 0, 64, 64, None) != 0
+    assert "null" in tmc.last_error()
     # the gather probe takes the attention's geometry rules
     assert lib.tmc_paged_gather_probe(p, p, p, p, 16, 8, 64, 16, 256, 8192, 16384, 2048, p,
                                       None) != 0
