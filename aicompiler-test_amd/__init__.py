@@ -83,6 +83,7 @@ def _declare(l):
                                                  i64, i64, i64, i64, i64, i64, i64, vp]),
         "tmc_gemm_rows_workspace_bytes": (sz, []),
         "tmc_gemm_rows_f16": (i32, [vp, vp, vp, i32, i64, i64, i64, vp, sz, vp]),
+        "tmc_gemm_mfma_f16": (i32, [vp, vp, vp, i32, i64, i64, i64, vp]),
         "tmc_prefill_attention_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64,
                                             i64, i64, i64, i64, vp]),
         "tmc_attention_workspace_bytes": (sz, [i64, i64, i64, i64, i64]),
@@ -530,12 +531,21 @@ def gemm_rows_workspace_bytes() -> int:
 
 
 def gemm_rows(x, w, y, workspace=None, stream=None):
-    """y[m, n] = x[m, k] w[n, k]^T on hipBLASLt (fp16 in, fp32 accumulation)."""
+    """y[m, n] = x[m, k] w[n, k]^T on the MFMA GEMM (fp16 in, fp32 accumulation;
+    K split over the workspace when the tiles alone leave CUs idle)."""
     m, k = x.shape
     n = w.shape[0]
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     check(lib().tmc_gemm_rows_f16(_ptr(x), _ptr(w), _ptr(y), _dtype_code(y), m, k, n,
                                   _ptr(workspace), ws_bytes, _stream(stream)), "tmc_gemm_rows_f16")
+
+
+def gemm_mfma(x, w, y, stream=None):
+    """y[m, n] = x[m, k] w[n, k]^T on the hand-written gfx950 MFMA GEMM."""
+    m, k = x.shape
+    n = w.shape[0]
+    check(lib().tmc_gemm_mfma_f16(_ptr(x), _ptr(w), _ptr(y), _dtype_code(y), m, k, n,
+                                  _stream(stream)), "tmc_gemm_mfma_f16")
 
 
 def prefill_attention(q, k_pool, v_pool, valid_lengths, table, active, out, rows, q_heads,

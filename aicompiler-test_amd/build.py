@@ -35,7 +35,7 @@ CXXFLAGS = ["-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-param
 
 SOURCES = ["runtime.hip", "gemv.hip", "packed.hip", "elementwise.hip", "attention.hip",
            "prefill.hip"]
-# The prompt GEMMs (prefill.hip) call hipBLASLt from the ROCm install.
+# The HIP runtime library of the ROCm install (rpath of the built library).
 ROCM_LIB = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -111,7 +111,7 @@ def build(jobs: int = 4) -> str:
         host_objs = list(pool.map(_compile_host, HOST_SOURCES))
     tmp = OUT + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, f"-L{ROCM_LIB}",
-           "-lhipblaslt", f"-Wl,-rpath,{ROCM_LIB}"]
+           f"-Wl,-rpath,{ROCM_LIB}"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")

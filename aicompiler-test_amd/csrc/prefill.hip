@@ -7,11 +7,10 @@
 // emitPagedKVAttention with causalPrefill (KVCacheMetalEmitter.cpp:210-310):
 // query token q of a chunk of S tokens attends positions [0, valid - S + q + 1).
 //
-//  * tmc_gemm_rows_f16: the prompt projections are plain GEMMs with M = chunk
-//    tokens, so they go to hipBLASLt.  Per (device, shape, output type,
-//    workspace) the first call that is not under stream capture times the
-//    library's heuristic candidates on the caller's buffers and keeps the
-//    fastest; captured calls use the first candidate.
+//  * tmc_gemm_rows_f16: the prompt projections, GEMMs with M = chunk tokens,
+//    on gemm_nt_kernel (v_mfma_f32_16x16x32_f16, 128 x 128 tiles, see the
+//    comment above it), splitting K over a workspace when the tiles alone
+//    would leave CUs idle.
 //  * prefill_attention_kernel: one 256-thread workgroup per (kv head, tile of
 //    64 query vectors = 64/G tokens x the G query heads of that kv head).
 //    K/V blocks of 64 positions are staged through LDS (K row-major, V
@@ -23,12 +22,8 @@
 #include "tmc_abi.hpp"
 #include "tmc_device.hpp"
 
-#include <hipblaslt/hipblaslt.h>
-
 #include <cmath>
-#include <map>
 #include <mutex>
-#include <tuple>
 #include <vector>
 
 namespace tmc {
@@ -395,125 +390,224 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillPa
   }
 }
 
-// ------------------------------------------------------------------ prompt GEMM
-struct GemmKey {
-  int device, out_dtype;
-  int64_t m, k, n;
-  size_t workspace;
-  bool operator<(const GemmKey& o) const {
-    return std::tie(device, out_dtype, m, k, n, workspace) <
-           std::tie(o.device, o.out_dtype, o.m, o.k, o.n, o.workspace);
-  }
-};
+// ------------------------------------------------------------ prompt GEMM
+// y[m, n] = x[m, k] w[n, k]^T with fp16 operands and fp32 accumulation on
+// v_mfma_f32_16x16x32_f16.  Both operands are k-contiguous rows, which is the
+// MFMA operand order: lane (i, g) of a 16 x 32 fragment holds row i, k
+// 8g ... 8g + 7, for x (A) and for w (B) alike.
+//
+// Block: 256 threads = 2 x 2 waves over a 128 x 128 output tile, each wave
+// 64 x 64 (4 x 4 MFMA tiles, 64 accumulators per lane).  K advances in stages
+// of 64: while the waves multiply the current stage out of LDS, every thread
+// holds its share of the next stage's x and w tiles (16 KiB each) in
+// registers, and stores it to the other LDS buffer after the multiply; one
+// barrier per stage.  LDS rows are 64 + 8 halves (144 bytes), so the 16 rows
+// of an operand read start on 16 distinct 4-bank groups.  Raw buffer loads
+// read zero past m, n or k, so ragged tiles need no branches.
+//
+// Tiles are dealt XCD by XCD: blocks b, b + 8, b + 16, ... run on one XCD
+// and take consecutive tiles, which walk the m tiles of one n tile first, so
+// a weight slice is fetched from HBM once into that XCD's L2.
+constexpr int kGemmTile = 128;
+constexpr int kGemmK = 64;
+constexpr int kGemmRow = kGemmK + 8;  // halves per LDS row
+constexpr int kGemmThreads = 256;
 
-struct GemmPlan {
-  hipblasLtMatmulDesc_t desc = nullptr;
-  hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
-  std::vector<hipblasLtMatmulHeuristicResult_t> candidates;
-  int chosen = 0;
-  bool timed = false;
-};
+// Split K (SPLIT): block (tile, split s) multiplies k in [s * k_chunk,
+// (s + 1) * k_chunk) and writes fp32 partials y[s][m][n]; gemm_reduce_kernel
+// adds them in split order.
+template <typename OutT, bool SPLIT>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_nt_kernel(
+    const half_t* __restrict__ x, const half_t* __restrict__ w, OutT* __restrict__ y, int m,
+    int n, int k, int m_tiles, int tiles, int k_chunk, unsigned x_bytes, unsigned w_bytes) {
+  __shared__ __attribute__((aligned(16))) half_t lds[2][2][kGemmTile * kGemmRow];
+  const int per_xcd = (int)(gridDim.x / 8u);
+  const int unit = (int)(blockIdx.x % 8u) * per_xcd + (int)(blockIdx.x / 8u);
+  const int splits = SPLIT ? (k + k_chunk - 1) / k_chunk : 1;
+  if (unit >= tiles * splits) return;
+  const int t = unit % tiles;
+  const int k_begin = SPLIT ? (unit / tiles) * k_chunk : 0;
+  const int k_end = SPLIT ? min(k, k_begin + k_chunk) : k;
+  const int m0 = (t % m_tiles) * kGemmTile;
+  const int n0 = (t / m_tiles) * kGemmTile;
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & (kWave - 1), wave = tid / kWave;
+  const int i = lane & 15, g = lane >> 4;
+  const int wm = wave & 1, wn = wave >> 1;
+  const __amdgpu_buffer_rsrc_t rx = buffer_resource(x, x_bytes);
+  const __amdgpu_buffer_rsrc_t rw = buffer_resource(w, w_bytes);
 
-std::mutex g_gemm_mutex;
-std::map<int, hipblasLtHandle_t> g_lt_handles;
-std::map<GemmKey, GemmPlan> g_gemm_plans;
-
-constexpr int kGemmCandidates = 8;
-
-int lt_ok(hipblasStatus_t status, const char* what) {
-  if (status == HIPBLAS_STATUS_SUCCESS) return 0;
-  return fail(std::string("hipBLASLt ") + what + " failed (status " +
-              std::to_string((int)status) + ").");
-}
-
-// Column-major view of the row-major problem: Y^T[n, m] = W[n, k] X^T[k, m],
-// i.e. op(A) = A^T with A = W as a k x n column-major matrix (ld k), B = X as
-// k x m (ld k), C = Y as n x m (ld n).
-int make_plan(hipblasLtHandle_t handle, const GemmKey& key, GemmPlan& plan) {
-  if (lt_ok(hipblasLtMatmulDescCreate(&plan.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F), "desc"))
-    return 1;
-  const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-  if (lt_ok(hipblasLtMatmulDescSetAttribute(plan.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta),
-            "transA") ||
-      lt_ok(hipblasLtMatmulDescSetAttribute(plan.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb),
-            "transB"))
-    return 1;
-  const hipDataType out = key.out_dtype == TMC_F32 ? HIP_R_32F : HIP_R_16F;
-  if (lt_ok(hipblasLtMatrixLayoutCreate(&plan.a, HIP_R_16F, (uint64_t)key.k, (uint64_t)key.n, key.k),
-            "layout A") ||
-      lt_ok(hipblasLtMatrixLayoutCreate(&plan.b, HIP_R_16F, (uint64_t)key.k, (uint64_t)key.m, key.k),
-            "layout B") ||
-      lt_ok(hipblasLtMatrixLayoutCreate(&plan.c, out, (uint64_t)key.n, (uint64_t)key.m, key.n),
-            "layout C"))
-    return 1;
-  hipblasLtMatmulPreference_t pref = nullptr;
-  if (lt_ok(hipblasLtMatmulPreferenceCreate(&pref), "preference")) return 1;
-  uint64_t ws = key.workspace;
-  (void)hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
-                                              sizeof ws);
-  hipblasLtMatmulHeuristicResult_t results[kGemmCandidates];
-  int returned = 0;
-  const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(handle, plan.desc, plan.a, plan.b, plan.c,
-                                                             plan.c, pref, kGemmCandidates, results,
-                                                             &returned);
-  (void)hipblasLtMatmulPreferenceDestroy(pref);
-  if (lt_ok(st, "heuristic")) return 1;
-  for (int i = 0; i < returned; ++i)
-    if (results[i].state == HIPBLAS_STATUS_SUCCESS && results[i].workspaceSize <= key.workspace)
-      plan.candidates.push_back(results[i]);
-  if (plan.candidates.empty()) return fail("hipBLASLt has no algorithm for this GEMM.");
-  return 0;
-}
-
-hipblasStatus_t run_plan(hipblasLtHandle_t handle, const GemmPlan& plan, int index, const void* x,
-                         const void* w, void* y, void* workspace, size_t workspace_bytes,
-                         hipStream_t stream) {
-  const float alpha = 1.0f, beta = 0.0f;
-  return hipblasLtMatmul(handle, plan.desc, &alpha, w, plan.a, x, plan.b, &beta, y, plan.c, y,
-                         plan.c, &plan.candidates[(size_t)index].algo, workspace, workspace_bytes,
-                         stream);
-}
-
-// Time every candidate (one warm-up and three timed calls each) on the
-// caller's stream and buffers; the last call leaves Y from the fastest.
-int time_plan(hipblasLtHandle_t handle, GemmPlan& plan, const void* x, const void* w, void* y,
-              void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  hipEvent_t start = nullptr, stop = nullptr;
-  if (hipEventCreate(&start) != hipSuccess || hipEventCreate(&stop) != hipSuccess)
-    return fail("hipEventCreate failed.");
-  float best = 0.0f;
-  int chosen = -1;
-  for (int i = 0; i < (int)plan.candidates.size(); ++i) {
-    if (run_plan(handle, plan, i, x, w, y, workspace, workspace_bytes, stream) !=
-        HIPBLAS_STATUS_SUCCESS)
-      continue;
-    (void)hipEventRecord(start, stream);
-    bool ok = true;
-    for (int r = 0; r < 3 && ok; ++r)
-      ok = run_plan(handle, plan, i, x, w, y, workspace, workspace_bytes, stream) ==
-           HIPBLAS_STATUS_SUCCESS;
-    (void)hipEventRecord(stop, stream);
-    float ms = 0.0f;
-    if (hipEventSynchronize(stop) != hipSuccess ||
-        hipEventElapsedTime(&ms, start, stop) != hipSuccess)
-      ok = false;
-    if (ok && (chosen < 0 || ms < best)) {
-      best = ms;
-      chosen = i;
+  // Stage loads: thread tid moves rows tid / 8 + 32 q (q < 4), 16-byte chunk
+  // tid % 8, of both tiles.  Two stages are in flight in registers: the
+  // loads of stage st + 2 are issued before stage st is multiplied, and
+  // stage st + 1 (loaded one multiply earlier) is stored to LDS after it.
+  const int lr = tid >> 3, lc = tid & 7;
+  struct Stage {
+    h8 x[4], w[4];
+  };
+  auto load_stage = [&](Stage& sg, int k0) {
+    const int kk = k_begin + k0 + 8 * lc;
+    const bool k_ok = kk < k_end;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = lr + 32 * q;
+      const bool xo = k_ok && m0 + r < m, wo = k_ok && n0 + r < n;
+      sg.x[q] = buffer_load_h8(rx, xo ? (unsigned)(((size_t)(m0 + r) * k + kk) * 2) : kBufferAbsent);
+      sg.w[q] = buffer_load_h8(rw, wo ? (unsigned)(((size_t)(n0 + r) * k + kk) * 2) : kBufferAbsent);
     }
+  };
+  auto store_stage = [&](const Stage& sg, int buf) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = lr + 32 * q;
+      *reinterpret_cast<h8*>(&lds[buf][0][r * kGemmRow + 8 * lc]) = sg.x[q];
+      *reinterpret_cast<h8*>(&lds[buf][1][r * kGemmRow + 8 * lc]) = sg.w[q];
+    }
+  };
+
+  f4 acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto multiply = [&](int buf) {
+    const half_t* ax = lds[buf][0] + (wm * 64 + i) * kGemmRow + 8 * g;
+    const half_t* bw = lds[buf][1] + (wn * 64 + i) * kGemmRow + 8 * g;
+#pragma unroll
+    for (int s = 0; s < kGemmK / 32; ++s) {
+      h8 fa[4], fb[4];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) fa[a] = *reinterpret_cast<const h8*>(ax + a * 16 * kGemmRow + 32 * s);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) fb[b] = *reinterpret_cast<const h8*>(bw + b * 16 * kGemmRow + 32 * s);
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[a], fb[b], acc[a][b], 0, 0, 0);
+    }
+  };
+
+  const int stages = (k_end - k_begin + kGemmK - 1) / kGemmK;
+  Stage even, odd;  // registers of the stages with even / odd index
+  load_stage(even, 0);
+  if (stages > 1) load_stage(odd, kGemmK);
+  store_stage(even, 0);
+  __syncthreads();
+  // Stage st sits in LDS buffer st & 1.  At an even st, `odd` holds stage
+  // st + 1 and `even` is free for stage st + 2; at an odd st the other way
+  // round (the loop is unrolled by two so the registers are named).
+  auto step = [&](int st, Stage& free_regs, const Stage& next_regs) {
+    if (st + 2 < stages) load_stage(free_regs, (st + 2) * kGemmK);
+    multiply(st & 1);
+    if (st + 1 < stages) store_stage(next_regs, (st + 1) & 1);
+    __syncthreads();
+  };
+  for (int st = 0; st < stages; st += 2) {
+    step(st, even, odd);
+    if (st + 1 < stages) step(st + 1, odd, even);
   }
-  (void)hipEventDestroy(start);
-  (void)hipEventDestroy(stop);
-  if (chosen < 0) return fail("hipBLASLt: no candidate algorithm ran for this GEMM.");
-  plan.chosen = chosen;
-  plan.timed = true;
-  return 0;
+
+  // acc[a][b][r] = y[m0 + wm*64 + 16a + 4g + r][n0 + wn*64 + 16b + i]
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = m0 + wm * 64 + 16 * a + 4 * g + r;
+      if (row >= m) continue;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int col = n0 + wn * 64 + 16 * b + i;
+        if (col >= n) continue;
+        if constexpr (SPLIT)
+          reinterpret_cast<float*>(y)[((size_t)(unit / tiles) * m + row) * n + col] = acc[a][b][r];
+        else
+          y[(size_t)row * n + col] = from_float<OutT>(acc[a][b][r]);
+      }
+    }
+}
+
+template <typename OutT>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restrict__ partial,
+                                                         OutT* __restrict__ y, size_t count,
+                                                         int splits) {
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < count; e += (size_t)gridDim.x * 256) {
+    float sum = partial[e];
+    for (int s = 1; s < splits; ++s) sum += partial[(size_t)s * count + e];
+    y[e] = from_float<OutT>(sum);
+  }
+}
+
+// Splits of K for a launch of `tiles` output tiles: enough (tile, split)
+// units for two workgroups per CU on 256 CUs, each split at least 512 deep,
+// and the fp32 partials within `workspace_bytes`.  1 = no split.
+int gemm_splits(int64_t tiles, int64_t m, int64_t k, int64_t n, size_t workspace_bytes) {
+  int splits = 1;
+  while (tiles * splits < 512 && k / (2 * splits) >= 512 &&
+         (uint64_t)(splits * 2) * m * n * 4 <= workspace_bytes)
+    splits *= 2;
+  return splits;
+}
+
+int launch_gemm_nt(const half_t* x, const half_t* w, void* y, int out_dtype, int64_t m, int64_t k,
+                   int64_t n, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const uint64_t xb = (uint64_t)m * k * 2, wb = (uint64_t)n * k * 2;
+  TMC_REQUIRE(xb < kBufferAbsent && wb < kBufferAbsent,
+              "Prompt GEMM: each operand must stay below 4 GiB.");
+  TMC_REQUIRE(k % 8 == 0, "Prompt GEMM: k must be a multiple of 8.");
+  TMC_REQUIRE(aligned16(x) && aligned16(w), "Prompt GEMM: x and w must be 16-byte aligned.");
+  const int m_tiles = (int)((m + kGemmTile - 1) / kGemmTile);
+  const int64_t tiles = (int64_t)m_tiles * ((n + kGemmTile - 1) / kGemmTile);
+  TMC_REQUIRE(tiles < (1LL << 26), "Prompt GEMM: too many tiles.");
+  const int splits = workspace ? gemm_splits(tiles, m, k, n, workspace_bytes) : 1;
+  // k per split, in whole 64-deep stages
+  const int k_chunk = (int)(((k + splits - 1) / splits + kGemmK - 1) / kGemmK * kGemmK);
+  const int units = (int)(tiles * ((k + k_chunk - 1) / k_chunk));
+  const unsigned blocks = (unsigned)((units + 7) / 8 * 8);
+  if (units > (int)tiles) {
+    float* partial = static_cast<float*>(workspace);
+    hipLaunchKernelGGL((gemm_nt_kernel<float, true>), dim3(blocks), dim3(kGemmThreads), 0, stream,
+                       x, w, partial, (int)m, (int)n, (int)k, m_tiles, (int)tiles, k_chunk,
+                       (unsigned)xb, (unsigned)wb);
+    if (check_launch("gemm_nt_kernel")) return 1;
+    const size_t count = (size_t)m * n;
+    const unsigned rb = (unsigned)std::min<size_t>((count + 255) / 256, 8192);
+    const int used = (int)((k + k_chunk - 1) / k_chunk);
+    if (out_dtype == TMC_F32)
+      hipLaunchKernelGGL((gemm_reduce_kernel<float>), dim3(rb), dim3(256), 0, stream, partial,
+                         static_cast<float*>(y), count, used);
+    else
+      hipLaunchKernelGGL((gemm_reduce_kernel<half_t>), dim3(rb), dim3(256), 0, stream, partial,
+                         static_cast<half_t*>(y), count, used);
+    return check_launch("gemm_reduce_kernel");
+  }
+  if (out_dtype == TMC_F32)
+    hipLaunchKernelGGL((gemm_nt_kernel<float, false>), dim3(blocks), dim3(kGemmThreads), 0, stream,
+                       x, w, static_cast<float*>(y), (int)m, (int)n, (int)k, m_tiles, (int)tiles,
+                       (int)k, (unsigned)xb, (unsigned)wb);
+  else
+    hipLaunchKernelGGL((gemm_nt_kernel<half_t, false>), dim3(blocks), dim3(kGemmThreads), 0,
+                       stream, x, w, static_cast<half_t*>(y), (int)m, (int)n, (int)k, m_tiles,
+                       (int)tiles, (int)k, (unsigned)xb, (unsigned)wb);
+  return check_launch("gemm_nt_kernel");
 }
 
 }  // namespace
 }  // namespace tmc
 
 using namespace tmc;
+
+
+extern "C" int tmc_gemm_mfma_f16(const void* x, const void* weight, void* y, int out_dtype,
+                                 int64_t m, int64_t k, int64_t n, void* stream) {
+  TMC_REQUIRE(x && weight && y, "Prompt GEMM: null device pointer.");
+  TMC_REQUIRE(out_dtype == TMC_F16 || out_dtype == TMC_F32, "Prompt GEMM: output must be f16 or f32.");
+  TMC_REQUIRE(m > 0 && k > 0 && n > 0 && m < (1LL << 31) && k < (1LL << 31) && n < (1LL << 31),
+              "Prompt GEMM: invalid shape.");
+  return launch_gemm_nt(static_cast<const half_t*>(x), static_cast<const half_t*>(weight), y,
+                        out_dtype, m, k, n, nullptr, 0, as_stream(stream));
+}
 
 extern "C" size_t tmc_gemm_rows_workspace_bytes(void) { return (size_t)32 << 20; }
 
@@ -525,26 +619,9 @@ extern "C" int tmc_gemm_rows_f16(const void* x, const void* weight, void* y, int
   TMC_REQUIRE(m > 0 && k > 0 && n > 0 && m < (1LL << 31) && k < (1LL << 31) && n < (1LL << 31),
               "Prompt GEMM: invalid shape.");
   TMC_REQUIRE(workspace || workspace_bytes == 0, "Prompt GEMM: null workspace with a nonzero size.");
-  int device = 0;
-  if (hipGetDevice(&device) != hipSuccess) return fail("hipGetDevice failed.");
-  const hipStream_t s = as_stream(stream);
-  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(s, &capture) != hipSuccess) return fail("hipStreamIsCapturing failed.");
-  std::lock_guard<std::mutex> lock(g_gemm_mutex);
-  auto& handle = g_lt_handles[device];
-  if (!handle && lt_ok(hipblasLtCreate(&handle), "create")) return 1;
-  const GemmKey key{device, out_dtype, m, k, n, workspace_bytes};
-  auto it = g_gemm_plans.find(key);
-  if (it == g_gemm_plans.end()) {
-    GemmPlan plan;
-    if (make_plan(handle, key, plan)) return 1;
-    it = g_gemm_plans.emplace(key, std::move(plan)).first;
-  }
-  GemmPlan& plan = it->second;
-  if (!plan.timed && capture == hipStreamCaptureStatusNone && plan.candidates.size() > 1)
-    return time_plan(handle, plan, x, weight, y, workspace, workspace_bytes, s);
-  return lt_ok(run_plan(handle, plan, plan.chosen, x, weight, y, workspace, workspace_bytes, s),
-               "matmul");
+  TMC_REQUIRE(!workspace || aligned16(workspace), "Prompt GEMM: the workspace must be 16-byte aligned.");
+  return launch_gemm_nt(static_cast<const half_t*>(x), static_cast<const half_t*>(weight), y,
+                        out_dtype, m, k, n, workspace, workspace_bytes, as_stream(stream));
 }
 
 extern "C" int tmc_prefill_attention_rows_f16(const void* q, const void* key_pool,

@@ -805,8 +805,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     }
     s.outputs = {od};
     s.counts.push_back((size_t)(m * n));
-    s.groups = (size_t)(((m + 255) / 256) * ((n + 255) / 256));
-    s.capturable = false;
+    s.groups = (size_t)(((m + 127) / 128) * ((n + 127) / 128));
     s.launch = [=](const LaunchContext& c) {
       return tmc_gemm_rows_f16(c.ptrs[0], c.ptrs[1], c.ptrs[ws ? 3 : 2], od, m, k, n,
                                ws ? c.ptrs[2] : nullptr, ws_bytes, c.stream);

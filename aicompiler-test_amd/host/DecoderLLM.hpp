@@ -283,7 +283,7 @@ struct BatchedDecodeExecutor::Creation {
 
 // Chunked prefill (prefillChunked, DecoderLLMExecutor.cpp:982-1034): the
 // tokens of one request's prompt chunk are the rows of one stage.  Linear
-// layers are prompt GEMMs (hipBLASLt, kernel key gemm_rows), RoPE and the
+// layers are prompt GEMMs (MFMA GEMM, kernel key gemm_rows), RoPE and the
 // cache append share the request's block table (prefill_rope_append) and
 // attention is causal over the chunk (prefill_attention): row r of a chunk
 // starting at position `start` attends [0, start + r + 1), which is what

@@ -456,7 +456,7 @@ def prefill_flops(tokens: int) -> float:
 
 def prefill_gpu(tmc) -> dict:
     """Chunked prefill throughput of the 7B shape: one prompt per run through
-    hipBLASLt prompt GEMMs and the MFMA causal chunk attention; TFLOP/s
+    the MFMA prompt GEMMs and the MFMA causal chunk attention; TFLOP/s
     against the 2.5 PFLOP/s dense fp16 peak."""
     host = tmc.host()
     rt = host.HipRuntime()

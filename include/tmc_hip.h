@@ -153,10 +153,9 @@ void tmc_exec_release(tmc_exec *exec);
 /* MetalRuntime::prepareSequence / PreparedSequence::execute
  * (MetalRuntime.hpp:130-142,202-203; .mm:292-341,751-781): the steps are
  * captured once into a HIP graph and replayed with one hipGraphLaunch.  A
- * sequence that holds a step kept out of graphs (kernel key gemm_rows, a
- * hipBLASLt call) replays its steps eagerly, in order, on the runtime's
- * stream instead.  Either way the steps and their buffers must outlive the
- * sequence. */
+ * sequence that holds a step kept out of graphs replays its steps eagerly,
+ * in order, on the runtime's stream instead.  Either way the steps and their
+ * buffers must outlive the sequence. */
 int tmc_seq_create(tmc_runtime *rt, tmc_exec *const *steps, size_t n, tmc_seq **out);
 int tmc_seq_run(tmc_seq *seq, double *gpu_us, double *cpu_us);
 /* Enqueue one replay on the runtime stream without waiting. */
@@ -553,14 +552,20 @@ int tmc_prefill_rope_append_rows(const void *qkv, const float *cosine, const flo
 
 /* emitTiledGEMM (DecodeGEMVMetalEmitter.cpp:134-169), the prefill linear
  * layer: y[m, n] = x[m, k] weight[n, k]^T, fp16 inputs, fp32 accumulation,
- * y fp16 or fp32 (out_dtype), all row-major.  Runs on hipBLASLt; the first
- * call of a (device, shape, out_dtype, workspace_bytes) outside stream
- * capture times up to 8 library candidates on these buffers (it waits for
- * the stream) and keeps the fastest.  workspace may be NULL with
- * workspace_bytes 0; tmc_gemm_rows_workspace_bytes() is the size that admits
- * every candidate measured on gfx950 (32 MiB).  Calls that share a workspace
- * must be ordered on one stream. */
+ * y fp16 or fp32 (out_dtype), all row-major, on the hand-written gfx950 MFMA
+ * GEMM (v_mfma_f32_16x16x32_f16, 128 x 128 output tiles per 256-thread
+ * workgroup; k a multiple of 8, x and weight 16-byte aligned and each below
+ * 4 GiB).  When the output tiles alone would leave CUs idle and the
+ * workspace holds the fp32 partials, K is split over several workgroups and
+ * a second launch adds the partials in split order.  workspace may be NULL
+ * with workspace_bytes 0 (no split); tmc_gemm_rows_workspace_bytes() is the
+ * size the decoder binds (32 MiB).  Calls that share a workspace must be
+ * ordered on one stream.  Nothing is timed or allocated; calls may be
+ * captured in a graph. */
 size_t tmc_gemm_rows_workspace_bytes(void);
+/* tmc_gemm_rows_f16 without a workspace (never splits K). */
+int tmc_gemm_mfma_f16(const void *x, const void *weight, void *y, int out_dtype, int64_t m,
+                      int64_t k, int64_t n, void *stream);
 int tmc_gemm_rows_f16(const void *x, const void *weight, void *y, int out_dtype, int64_t m,
                       int64_t k, int64_t n, void *workspace, size_t workspace_bytes,
                       void *stream);

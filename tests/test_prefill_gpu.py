@@ -36,8 +36,14 @@ def rt(host):
 # ---------------------------------------------------------------- prompt GEMM
 @pytest.mark.parametrize("m,k,n,out,ws", [(1, 64, 48, F16, False), (37, 256, 200, F16, True),
                                           (64, 512, 1000, F32, True), (300, 1024, 768, F16, False),
-                                          (512, 4096, 4096, F16, True)])
+                                          (512, 4096, 4096, F16, True),
+                                          # split K over the workspace (few output tiles)
+                                          (37, 4096, 200, F16, True), (130, 4104, 4100, F32, True),
+                                          # ragged m, n and k (k % 64 != 0) without a split
+                                          (130, 4104, 4100, F16, False)])
 def test_gemm_rows_matches_oracle(tmc, orc, torch, m, k, n, out, ws):
+    """The MFMA prompt GEMM (emitTiledGEMM semantics) against the oracle, with
+    and without the split-K workspace; repeated calls are bit-identical."""
     x = orc.f16(normal(700 + m, (m, k)))
     w = orc.f16(normal(701 + n, (n, k), 0.03))
     dtype = torch.float16 if out == F16 else torch.float32
@@ -45,7 +51,7 @@ def test_gemm_rows_matches_oracle(tmc, orc, torch, m, k, n, out, ws):
                  if ws else None)
     xd, wd = dev_f16(x), dev_f16(w)
     y = torch.full((m, n), float("nan"), dtype=dtype, device="cuda")
-    tmc.gemm_rows(xd, wd, y, workspace)  # first call of the shape: picks the algorithm
+    tmc.gemm_rows(xd, wd, y, workspace)
     y2 = torch.full_like(y, float("nan"))
     tmc.gemm_rows(xd, wd, y2, workspace)
     y3 = torch.full_like(y, float("nan"))
@@ -57,10 +63,16 @@ def test_gemm_rows_matches_oracle(tmc, orc, torch, m, k, n, out, ws):
         assert_f16_path(values(y), ref, what=what)
     else:
         assert_f32_rel(values(y), ref, what=what)
-    # the selected algorithm is reused: later calls are bit-identical
-    assert torch.equal(y2, y3)
+    # deterministic: the split partials are added in split order
+    assert torch.equal(y, y2) and torch.equal(y2, y3)
+    # the no-workspace entry (never splits) agrees within the same tolerance
+    y4 = torch.full_like(y, float("nan"))
+    tmc.gemm_mfma(xd, wd, y4)
+    torch.cuda.synchronize()
     if out == F16:
-        assert_f16_path(values(y2), ref, what=what + " (cached)")
+        assert_f16_path(values(y4), ref, what=what + " (no split)")
+    else:
+        assert_f32_rel(values(y4), ref, what=what + " (no split)")
 
 
 def test_gemm_rows_rejects_bad_arguments(tmc, torch):
