@@ -399,25 +399,33 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillPa
 // Block: 256 threads = 2 x 2 waves over a 128 x 128 output tile, each wave
 // 64 x 64 (4 x 4 MFMA tiles, 64 accumulators per lane).  K advances in stages
 // of 64: while the waves multiply the current stage out of LDS, every thread
-// holds its share of the next stage's x and w tiles (16 KiB each) in
-// registers, and stores it to the other LDS buffer after the multiply; one
-// barrier per stage.  LDS rows are 64 + 8 halves (144 bytes), so the 16 rows
-// of an operand read start on 16 distinct 4-bank groups.  Raw buffer loads
-// read zero past m, n or k, so ragged tiles need no branches.
+// holds its share of the next two stages' x and w tiles (16 KiB each) in
+// registers, and stores the next one to the other LDS buffer after the
+// multiply; one barrier per stage.  An LDS row is the stage's 64 halves of
+// one tile row as eight 16-byte chunks, chunk c stored at slot
+// c ^ ((row / 2) % 8): the 16 rows an operand read touches, and the 16 lanes
+// of a store, then fall on 16 distinct 4-bank groups.  Raw buffer loads read
+// zero past m, n or k, so ragged tiles need no branches.
 //
 // Tiles are dealt XCD by XCD: blocks b, b + 8, b + 16, ... run on one XCD
 // and take consecutive tiles, which walk the m tiles of one n tile first, so
 // a weight slice is fetched from HBM once into that XCD's L2.
 constexpr int kGemmTile = 128;
-constexpr int kGemmK = 64;
-constexpr int kGemmRow = kGemmK + 8;  // halves per LDS row
+#ifndef TMC_GEMM_K
+#define TMC_GEMM_K 64
+#endif
+#ifndef TMC_GEMM_WPE
+#define TMC_GEMM_WPE 2
+#endif
+constexpr int kGemmK = TMC_GEMM_K;
+constexpr int kGemmRow = kGemmK;  // halves per LDS row (swizzled chunks, no padding)
 constexpr int kGemmThreads = 256;
 
 // Split K (SPLIT): block (tile, split s) multiplies k in [s * k_chunk,
 // (s + 1) * k_chunk) and writes fp32 partials y[s][m][n]; gemm_reduce_kernel
 // adds them in split order.
 template <typename OutT, bool SPLIT>
-__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_nt_kernel(
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(TMC_GEMM_WPE, TMC_GEMM_WPE))) void gemm_nt_kernel(
     const half_t* __restrict__ x, const half_t* __restrict__ w, OutT* __restrict__ y, int m,
     int n, int k, int m_tiles, int tiles, int k_chunk, unsigned x_bytes, unsigned w_bytes) {
   __shared__ __attribute__((aligned(16))) half_t lds[2][2][kGemmTile * kGemmRow];
@@ -437,20 +445,25 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2,
   const __amdgpu_buffer_rsrc_t rx = buffer_resource(x, x_bytes);
   const __amdgpu_buffer_rsrc_t rw = buffer_resource(w, w_bytes);
 
-  // Stage loads: thread tid moves rows tid / 8 + 32 q (q < 4), 16-byte chunk
-  // tid % 8, of both tiles.  Two stages are in flight in registers: the
+  // Stage loads: each thread moves kPasses 16-byte chunks of both tiles.  Two stages are in flight in registers: the
   // loads of stage st + 2 are issued before stage st is multiplied, and
   // stage st + 1 (loaded one multiply earlier) is stored to LDS after it.
-  const int lr = tid >> 3, lc = tid & 7;
+  // A row holds kChunks 16-byte chunks; 256 threads move kPass rows per
+  // pass and kPasses passes cover the tile's 128 rows.  A 256-byte LDS bank
+  // sweep holds kSweepRows rows; chunk c of row r sits at slot
+  // c ^ ((r / kSweepRows) % kChunks).
+  constexpr int kChunks = kGemmK / 8, kPass = kGemmThreads / kChunks;
+  constexpr int kPasses = kGemmTile / kPass, kSweepRows = 256 / (2 * kGemmK);
+  const int lr = tid / kChunks, lc = tid % kChunks;
   struct Stage {
-    h8 x[4], w[4];
+    h8 x[kPasses], w[kPasses];
   };
   auto load_stage = [&](Stage& sg, int k0) {
     const int kk = k_begin + k0 + 8 * lc;
     const bool k_ok = kk < k_end;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int r = lr + 32 * q;
+    for (int q = 0; q < kPasses; ++q) {
+      const int r = lr + kPass * q;
       const bool xo = k_ok && m0 + r < m, wo = k_ok && n0 + r < n;
       sg.x[q] = buffer_load_h8(rx, xo ? (unsigned)(((size_t)(m0 + r) * k + kk) * 2) : kBufferAbsent);
       sg.w[q] = buffer_load_h8(rw, wo ? (unsigned)(((size_t)(n0 + r) * k + kk) * 2) : kBufferAbsent);
@@ -458,10 +471,11 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2,
   };
   auto store_stage = [&](const Stage& sg, int buf) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int r = lr + 32 * q;
-      *reinterpret_cast<h8*>(&lds[buf][0][r * kGemmRow + 8 * lc]) = sg.x[q];
-      *reinterpret_cast<h8*>(&lds[buf][1][r * kGemmRow + 8 * lc]) = sg.w[q];
+    for (int q = 0; q < kPasses; ++q) {
+      const int r = lr + kPass * q;
+      const int slot = lc ^ ((r / kSweepRows) % kChunks);
+      *reinterpret_cast<h8*>(&lds[buf][0][r * kGemmRow + 8 * slot]) = sg.x[q];
+      *reinterpret_cast<h8*>(&lds[buf][1][r * kGemmRow + 8 * slot]) = sg.w[q];
     }
   };
 
@@ -472,15 +486,20 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2,
     for (int b = 0; b < 4; ++b) acc[a][b] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
   auto multiply = [&](int buf) {
-    const half_t* ax = lds[buf][0] + (wm * 64 + i) * kGemmRow + 8 * g;
-    const half_t* bw = lds[buf][1] + (wn * 64 + i) * kGemmRow + 8 * g;
+    // rows wm*64 + 16a + i (x) and wn*64 + 16b + i (w); chunk 4s + g of a
+    // row sits at slot (4s + g) ^ ((i / kSweepRows) % kChunks) (the row bases
+    // are multiples of 16)
+    const half_t* ax = lds[buf][0] + (wm * 64 + i) * kGemmRow;
+    const half_t* bw = lds[buf][1] + (wn * 64 + i) * kGemmRow;
+    const int sw = (i / kSweepRows) % kChunks;
 #pragma unroll
     for (int s = 0; s < kGemmK / 32; ++s) {
+      const int slot = 8 * ((4 * s + g) ^ sw);
       h8 fa[4], fb[4];
 #pragma unroll
-      for (int a = 0; a < 4; ++a) fa[a] = *reinterpret_cast<const h8*>(ax + a * 16 * kGemmRow + 32 * s);
+      for (int a = 0; a < 4; ++a) fa[a] = *reinterpret_cast<const h8*>(ax + a * 16 * kGemmRow + slot);
 #pragma unroll
-      for (int b = 0; b < 4; ++b) fb[b] = *reinterpret_cast<const h8*>(bw + b * 16 * kGemmRow + 32 * s);
+      for (int b = 0; b < 4; ++b) fb[b] = *reinterpret_cast<const h8*>(bw + b * 16 * kGemmRow + slot);
 #pragma unroll
       for (int a = 0; a < 4; ++a)
 #pragma unroll
