@@ -52,6 +52,7 @@ def _declare(l):
         "tmc_rmsnorm": (i32, [vp, vp, vp, i32, i64, i64, f, vp]),
         "tmc_add_rmsnorm": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, f, vp]),
         "tmc_add_rmsnorm_gemv_f16": (i32, [vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, f, vp, vp]),
+        "tmc_gemv_residual_f16": (i32, [vp, vp, vp, vp, i64, i64, i64, vp, vp]),
         "tmc_add_rmsnorm_gate_up_silu_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, f, vp,
                                                    vp]),
         "tmc_add_rmsnorm_ex": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, f, i32, vp]),
@@ -249,6 +250,16 @@ def add_rmsnorm_gemv(residual, update, gamma, w, sum_out, y, eps, cfg=None, stre
                                          _dtype_code(y), b, k, n, eps,
                                          C.byref(cfg) if cfg is not None else None,
                                          _stream(stream)), "tmc_add_rmsnorm_gemv_f16")
+
+
+def gemv_residual(x, w, residual, y, cfg=None, stream=None):
+    """Batch-1 y = h(h(W x) + residual) (the o / down projections of the
+    folded decode step)."""
+    b, k = x.shape
+    n = w.shape[0]
+    check(lib().tmc_gemv_residual_f16(_ptr(x), _ptr(w), _ptr(residual), _ptr(y), b, k, n,
+                                      C.byref(cfg) if cfg is not None else None, _stream(stream)),
+          "tmc_gemv_residual_f16")
 
 
 def add_rmsnorm_gate_up_silu(residual, update, gamma, wg, wu, sum_out, out, eps, cfg=None,

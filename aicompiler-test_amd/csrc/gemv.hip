@@ -29,6 +29,7 @@
 // The gated MLP (emitDecoderGatedMLP, DecoderLLMMetalEmitter.cpp:479-536)
 // runs either algorithm over the Wg and Wu rows of each feature and finishes
 // with the reference rounding points h(h(silu(h(g))) * h(u)).
+#include <algorithm>
 #include <cmath>
 
 #include "tmc_abi.hpp"
@@ -56,8 +57,23 @@ __device__ __forceinline__ void write_out(OutT* y, size_t i, float a0, float a1)
 }
 
 // ---------------------------------------------------------------- wave64 dot
-// Inputs of the fused Add+RMSNorm prologue (PRO 1: x = RMSNorm(residual +
-// update) * gamma, the sum written by block 0; PRO 2: x = RMSNorm(residual)).
+// Fusions of the batch-1 dot GEMV:
+//  * kFuseAddNorm / kFuseNorm (gemv_norm_kernel): the input is x = h(s *
+//    rsqrt(mean(s^2) + eps) * gamma) of a stored row s (kFuseAddNorm: s =
+//    h(residual + update), stored to sum_out by block 0; kFuseNorm: s =
+//    residual), computed in the kernel instead of by a norm launch.  The sum
+//    of squares runs in the order of norm_vec_kernel with one 16-byte chunk
+//    per thread: thread t owns chunk t, its 8 squares are added in order,
+//    each group of 64 chunks is reduced by wave_sum, and the group totals are
+//    added in group order.  That order does not depend on the thread count
+//    once every thread holds at most one chunk (idle threads add exact
+//    zeros), so x equals tmc_rmsnorm / tmc_add_rmsnorm at any thread count
+//    >= k / 8 bit for bit.
+//  * kFuseResidual (gemv_dot_kernel): the output is h(residual + h(W x)), the
+//    residual add of emitLinearResidual (DecoderLLMMetalEmitter.cpp:604-622),
+//    so the add no longer needs the norm kernel that follows.
+enum Fuse { kFuseNone = 0, kFuseAddNorm = 1, kFuseNorm = 2, kFuseResidual = 3 };
+
 struct NormArgs {
   const half_t* residual = nullptr;
   const half_t* update = nullptr;
@@ -66,47 +82,25 @@ struct NormArgs {
   float eps = 0.0f;
 };
 
-// PRO > 0 (batch 1): every block first builds the normalized row in LDS
-// exactly as norm_vec_kernel does (same per-thread chunk order, wave sums,
-// and 4-wave total, so the row is bit-identical), then streams its weight
-// rows against it.  This removes the norm launch from the decode step.
-template <int PRO>
-__device__ __forceinline__ void normalized_row(const NormArgs& na, h8* x_lds, int k_in,
-                                               float* scratch) {
-  const int chunks = k_in >> 3;
-  float squares = 0.0f;
-  for (int c = threadIdx.x; c < chunks; c += 256) {
-    h8 a = load_h8(na.residual + 8 * c);
-    if constexpr (PRO == 1) {
-      const h8 b = load_h8(na.update + 8 * c);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) a[t] = from_float<half_t>(to_float<half_t>(a[t]) + to_float<half_t>(b[t]));
-      if (blockIdx.x == 0) *reinterpret_cast<h8*>(na.sum_out + 8 * c) = a;
-    }
-#pragma unroll
-    for (int t = 0; t < 8; ++t) squares += to_float<half_t>(a[t]) * to_float<half_t>(a[t]);
-    x_lds[c] = a;
-  }
-  squares = wave_sum(squares);
-  if ((threadIdx.x & (kWave - 1)) == 0) scratch[threadIdx.x / kWave] = squares;
-  __syncthreads();
-  float total = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) total += scratch[i];
-  const float inverse = 1.0f / sqrtf(total / (float)k_in + na.eps);
-  for (int c = threadIdx.x; c < chunks; c += 256) {
-    const h8 v = x_lds[c];
-    const h8 g = load_h8(na.gamma + 8 * c);
-    h8 n;
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-      n[t] = from_float<half_t>(to_float<half_t>(v[t]) * inverse * to_float<half_t>(g[t]));
-    x_lds[c] = n;
-  }
-  __syncthreads();
+// Streaming 16-byte weight load through a buffer resource (non-temporal).
+__device__ __forceinline__ h8 buffer_stream_h8(__amdgpu_buffer_rsrc_t r, unsigned byte_offset) {
+  return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_offset, 0, 2));
 }
 
-template <int MATS, int NB, int RPW, int U, int KS, typename OutT, int PRO = 0, bool ROPE = false>
+template <int MATS, int FUSE, typename OutT>
+__device__ __forceinline__ void store_out(OutT* y, size_t i, float a0, float a1,
+                                          const NormArgs& na) {
+  if constexpr (FUSE == kFuseResidual) {
+    static_assert(MATS == 1, "the residual epilogue follows a plain projection");
+    const float projected = to_float<half_t>(from_float<half_t>(a0));
+    y[i] = from_float<half_t>(to_float<half_t>(na.residual[i]) + projected);
+  } else {
+    write_out<MATS>(y, i, a0, a1);
+  }
+}
+
+template <int MATS, int NB, int RPW, int U, int KS, typename OutT, int FUSE = kFuseNone,
+          bool ROPE = false>
 __global__ __launch_bounds__(256) void gemv_dot_kernel(const half_t* __restrict__ x,
                                                       const half_t* __restrict__ w0,
                                                       const half_t* __restrict__ w1,
@@ -114,131 +108,301 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const half_t* __restrict_
                                                       NormArgs na, RopeArgs ra) {
   static_assert(!ROPE || (MATS == 1 && NB == 1 && RPW == 2),
                 "the RoPE epilogue takes one projection row pair per wave at batch 1");
+  static_assert(FUSE == kFuseNone || FUSE == kFuseResidual, "norm fusions run gemv_norm_kernel");
+  static_assert(FUSE != kFuseResidual || (NB == 1 && !ROPE && MATS == 1),
+                "the residual epilogue serves a batch-1 projection");
   constexpr int kWaves = 4;
   constexpr int kGroups = kWaves / KS;
   __shared__ float partial[kWaves][MATS][RPW][NB];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  extern __shared__ h8 x_lds[];  // PRO > 0: the normalized row, k_in / 8 chunks
-  if constexpr (PRO > 0) {
-    static_assert(NB == 1, "the fused norm prologue serves batch 1");
-    __shared__ float scratch[kWaves];
-    normalized_row<PRO>(na, x_lds, k_in, scratch);
-  }
-  auto x_chunk = [&](int b, int c) -> h8 {
-    if constexpr (PRO > 0) return x_lds[c];
-    else return load_h8(x + (size_t)b * k_in + 8 * c);
-  };
   const int group = wave / KS;
   const int part = wave % KS;
-  // PRO > 0: the grid is capped (launch_dot), so a block loops over row
-  // groups and builds the normalized row once; otherwise one pass.
-  for (int grp = blockIdx.x; grp * kGroups * RPW < n_out; grp += (int)gridDim.x) {
-    const int row0 = (grp * kGroups + group) * RPW;
-    const bool live = row0 < n_out;  // wave-uniform; dead waves still meet the barrier
-    const int chunks = k_in >> 3;
-    const half_t* wrow[MATS][RPW];
+  const int row0 = (blockIdx.x * kGroups + group) * RPW;
+  const bool live = row0 < n_out;  // wave-uniform; dead waves still meet the barrier
+  const int chunks = k_in >> 3;
+  const half_t* wrow[MATS][RPW];
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-      const size_t off = (size_t)min(row0 + r, n_out - 1) * k_in;
-      wrow[0][r] = w0 + off;
-      if constexpr (MATS == 2) wrow[1][r] = w1 + off;
-    }
-    float acc[MATS][RPW][NB];
+  for (int r = 0; r < RPW; ++r) {
+    const size_t off = (size_t)min(row0 + r, n_out - 1) * k_in;
+    wrow[0][r] = w0 + off;
+    if constexpr (MATS == 2) wrow[1][r] = w1 + off;
+  }
+  float acc[MATS][RPW][NB];
 #pragma unroll
-    for (int m = 0; m < MATS; ++m)
+  for (int m = 0; m < MATS; ++m)
 #pragma unroll
-      for (int r = 0; r < RPW; ++r)
+    for (int r = 0; r < RPW; ++r)
 #pragma unroll
-        for (int b = 0; b < NB; ++b) acc[m][r][b] = 0.0f;
+      for (int b = 0; b < NB; ++b) acc[m][r][b] = 0.0f;
 
-    constexpr int stride = kWave * KS;
-    int c = live ? lane + kWave * part : chunks;
-    for (; c + stride * (U - 1) < chunks; c += stride * U) {
-      h8 wv[U][MATS][RPW];
-      h8 xv[U][NB];
+  constexpr int stride = kWave * KS;
+  int c = live ? lane + kWave * part : chunks;
+  for (; c + stride * (U - 1) < chunks; c += stride * U) {
+    h8 wv[U][MATS][RPW];
+    h8 xv[U][NB];
 #pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int m = 0; m < MATS; ++m)
-#pragma unroll
-          for (int r = 0; r < RPW; ++r) wv[u][m][r] = load_h8_stream(wrow[m][r] + 8 * (c + stride * u));
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int b = 0; b < NB; ++b) xv[u][b] = x_chunk(b, c + stride * u);
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int m = 0; m < MATS; ++m)
-#pragma unroll
-          for (int r = 0; r < RPW; ++r)
-#pragma unroll
-            for (int b = 0; b < NB; ++b) acc[m][r][b] = dot8(wv[u][m][r], xv[u][b], acc[m][r][b]);
-    }
-    for (; c < chunks; c += stride) {
-      h8 xv[NB];
-#pragma unroll
-      for (int b = 0; b < NB; ++b) xv[b] = x_chunk(b, c);
+    for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int m = 0; m < MATS; ++m)
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-          const h8 wv = load_h8_stream(wrow[m][r] + 8 * c);
+        for (int r = 0; r < RPW; ++r) wv[u][m][r] = load_h8_stream(wrow[m][r] + 8 * (c + stride * u));
 #pragma unroll
-          for (int b = 0; b < NB; ++b) acc[m][r][b] = dot8(wv, xv[b], acc[m][r][b]);
-        }
-    }
-    if constexpr (ROPE && KS == 1) {
-      const float even = wave_sum(acc[0][0][0]);
-      const float odd = wave_sum(acc[0][1][0]);
-      if (lane == 0 && live) rope_append_pair(ra, 0, row0, even, odd);
-    } else if constexpr (KS == 1) {
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int r = 0; r < RPW; ++r)
+      for (int b = 0; b < NB; ++b) xv[u][b] = load_h8(x + (size_t)b * k_in + 8 * (c + stride * u));
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          const float a0 = wave_sum(acc[0][r][b]);
-          const float a1 = MATS == 2 ? wave_sum(acc[MATS - 1][r][b]) : 0.0f;
-          if (lane == 0 && live && row0 + r < n_out)
-            write_out<MATS>(y, (size_t)b * n_out + row0 + r, a0, a1);
-        }
-    } else {
+    for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int m = 0; m < MATS; ++m)
 #pragma unroll
         for (int r = 0; r < RPW; ++r)
 #pragma unroll
-          for (int b = 0; b < NB; ++b) {
-            const float total = wave_sum(acc[m][r][b]);
-            if (lane == 0) partial[wave][m][r][b] = total;
-          }
-      __syncthreads();
-      if constexpr (ROPE) {
-        if (part == 0 && live && lane == 0) {
-          float even = 0.0f, odd = 0.0f;
+          for (int b = 0; b < NB; ++b) acc[m][r][b] = dot8(wv[u][m][r], xv[u][b], acc[m][r][b]);
+  }
+  for (; c < chunks; c += stride) {
+    h8 xv[NB];
 #pragma unroll
-          for (int s = 0; s < KS; ++s) {
-            even += partial[wave + s][0][0][0];
-            odd += partial[wave + s][0][1][0];
-          }
-          rope_append_pair(ra, 0, row0, even, odd);
+    for (int b = 0; b < NB; ++b) xv[b] = load_h8(x + (size_t)b * k_in + 8 * c);
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        const h8 w = load_h8_stream(wrow[m][r] + 8 * c);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[m][r][b] = dot8(w, xv[b], acc[m][r][b]);
+      }
+  }
+  if constexpr (ROPE && KS == 1) {
+    const float even = wave_sum(acc[0][0][0]);
+    const float odd = wave_sum(acc[0][1][0]);
+    if (lane == 0 && live) rope_append_pair(ra, 0, row0, even, odd);
+  } else if constexpr (KS == 1) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const float a0 = wave_sum(acc[0][r][b]);
+        const float a1 = MATS == 2 ? wave_sum(acc[MATS - 1][r][b]) : 0.0f;
+        if (lane == 0 && live && row0 + r < n_out)
+          store_out<MATS, FUSE>(y, (size_t)b * n_out + row0 + r, a0, a1, na);
+      }
+  } else {
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const float total = wave_sum(acc[m][r][b]);
+          if (lane == 0) partial[wave][m][r][b] = total;
         }
-      } else if (part == 0 && live) {
-        for (int idx = lane; idx < RPW * NB; idx += kWave) {
-          const int r = idx / NB, b = idx % NB;
-          float a[2] = {0.0f, 0.0f};
+    __syncthreads();
+    if constexpr (ROPE) {
+      if (part == 0 && live && lane == 0) {
+        float even = 0.0f, odd = 0.0f;
 #pragma unroll
-          for (int m = 0; m < MATS; ++m)
-#pragma unroll
-            for (int s = 0; s < KS; ++s) a[m] += partial[wave + s][m][r][b];
-          if (row0 + r < n_out) write_out<MATS>(y, (size_t)b * n_out + row0 + r, a[0], a[1]);
+        for (int s = 0; s < KS; ++s) {
+          even += partial[wave + s][0][0][0];
+          odd += partial[wave + s][0][1][0];
         }
+        rope_append_pair(ra, 0, row0, even, odd);
+      }
+    } else if (part == 0 && live) {
+      for (int idx = lane; idx < RPW * NB; idx += kWave) {
+        const int r = idx / NB, b = idx % NB;
+        float a[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int m = 0; m < MATS; ++m)
+#pragma unroll
+          for (int s = 0; s < KS; ++s) a[m] += partial[wave + s][m][r][b];
+        if (row0 + r < n_out) store_out<MATS, FUSE>(y, (size_t)b * n_out + row0 + r, a[0], a[1], na);
       }
     }
-    if constexpr (PRO == 0) break;  // the grid covers every row group
-    // the next group's partials reuse the LDS slots read above
-    if constexpr (KS > 1) __syncthreads();
+  }
+}
+
+// Batch-1 dot GEMV (or gated MLP, or q.k.v + RoPE + append) of a normalized
+// stored row, as a persistent kernel: the grid holds as many blocks as run at
+// once, and block b computes row groups (RPW rows each) b, b + G, b + 2G, ...
+// A block's 4 waves split K like the dot GEMV at k split 4: wave p holds the
+// 16-byte chunks p*64 + lane + 256*i (i < NC, K <= 2048 * NC), which are also
+// the 64-chunk groups p + 4*i of the norm's reduction.  The block loads its
+// row chunks and gamma once, and the weights of its first two row groups;
+// reduces its norm groups (one wave_sum each) and meets the other waves at
+// one LDS barrier (the weight loads stay in flight); normalizes its chunks
+// once, into registers; then streams its row groups two deep, the loads of
+// group j + 2 issued as group j is consumed.  Weights are read with raw
+// buffer loads, a group past the matrix with an out-of-range offset (zeros,
+// no memory traffic), so the stream has no branches.  Per-row partials wait
+// in LDS until the end and are summed in wave order as in the dot GEMV, so
+// results equal the norm kernel followed by tmc_gemv_f16 at k split 4 bit for
+// bit.
+constexpr int kNormMaxChunks = 1024;  // K <= 8192: four chunks per lane
+constexpr int kNormMaxSlots = 34;     // row groups per block (grid >= groups / 32)
+// Build parameter: blocks of the persistent grid per resident block slot
+// (1 = one wave of blocks; 2 = twice as many, each with half the groups).
+#ifndef TMC_NORM_GRID_FACTOR
+#define TMC_NORM_GRID_FACTOR 1
+#endif
+
+template <int FUSE>
+__device__ __forceinline__ h8 norm_source(const NormArgs& na, int c) {
+  h8 a = load_h8(na.residual + 8 * c);
+  if constexpr (FUSE == kFuseAddNorm) {
+    const h8 b = load_h8(na.update + 8 * c);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) a[t] = from_float<half_t>(to_float<half_t>(a[t]) + to_float<half_t>(b[t]));
+  }
+  return a;
+}
+
+// Workgroup barrier ordering LDS only (__syncthreads() also waits for every
+// outstanding global load, i.e. for the weight stream).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+
+template <int MATS, int RPW, int NC, typename OutT, int FUSE, bool ROPE = false>
+__global__ __launch_bounds__(256) void gemv_norm_kernel(const half_t* __restrict__ w0,
+                                                       const half_t* __restrict__ w1,
+                                                       OutT* __restrict__ y, int n_out, int k_in,
+                                                       NormArgs na, RopeArgs ra) {
+  static_assert(FUSE == kFuseAddNorm || FUSE == kFuseNorm, "a norm fusion");
+  static_assert(!ROPE || (MATS == 1 && RPW == 2), "the RoPE epilogue takes one row pair");
+  static_assert(NC == 1 || NC == 2 || NC == 4, "1, 2 or 4 chunks per lane");
+  constexpr int kWaves = 4;
+  __shared__ float totals[kNormMaxChunks / kWave];
+  __shared__ float partial[kWaves][kNormMaxSlots][MATS][RPW];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int chunks = k_in >> 3;
+  const int groups = (n_out + RPW - 1) / RPW;
+  const int grid = (int)gridDim.x;
+  const unsigned bytes = (unsigned)n_out * (unsigned)k_in * 2u;
+  const __amdgpu_buffer_rsrc_t rw0 = buffer_resource(w0, bytes);
+  const __amdgpu_buffer_rsrc_t rw1 = buffer_resource(MATS == 2 ? w1 : w0, bytes);
+  int c[NC];
+  bool ok[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    c[i] = wave * kWave + lane + 4 * kWave * i;
+    ok[i] = c[i] < chunks;
+  }
+  // the row and gamma first (clamped addresses, no branch; chunks past the
+  // row are zeroed where they are used, so no select waits on these loads
+  // before the weight loads are issued)
+  h8 src[NC], gam[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int at = min(c[i], chunks - 1);
+    src[i] = norm_source<FUSE>(na, at);
+    gam[i] = load_h8(na.gamma + 8 * at);
+  }
+  // weights of row group g: rows past the matrix (clamped to row n_out, so
+  // at or past the resource's end) and chunks past the row read as zero.  No
+  // select on the block-uniform row test: the compiler would branch on it,
+  // and the wait counters are counted conservatively at the join.
+  auto load_group = [&](h8 (&w)[NC][MATS][RPW], int g) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const unsigned row = (unsigned)min(g * RPW + r, n_out);
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        const unsigned off =
+            ok[i] ? (row * (unsigned)k_in + 8u * (unsigned)c[i]) * 2u : kBufferAbsent;
+        w[i][0][r] = buffer_stream_h8(rw0, off);
+        if constexpr (MATS == 2) w[i][1][r] = buffer_stream_h8(rw1, off);
+      }
+    }
+  };
+  h8 wa[NC][MATS][RPW], wb[NC][MATS][RPW];
+  int g = (int)blockIdx.x;
+  // keep the row loads ahead of the weight loads (loads return in issue
+  // order, so the norm then waits for the row only)
+  __builtin_amdgcn_sched_barrier(0);
+  load_group(wa, g);
+  load_group(wb, g + grid);
+  // norm: group wave + 4i (past the row: zero); block 0 stores the sums
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    src[i] = ok[i] ? src[i] : h8{};
+    float squares = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) squares += to_float<half_t>(src[i][t]) * to_float<half_t>(src[i][t]);
+    const float total = wave_sum(squares);
+    if (lane == 0) totals[wave + 4 * i] = total;
+  }
+  if (FUSE == kFuseAddNorm && blockIdx.x == 0) {
+#pragma unroll
+    for (int i = 0; i < NC; ++i)
+      if (ok[i]) *reinterpret_cast<h8*>(na.sum_out + 8 * c[i]) = src[i];
+  }
+  lds_barrier();
+  float total = 0.0f;
+  for (int q = 0; q * kWave < chunks; ++q) total += totals[q];
+  const float inverse = 1.0f / sqrtf(total / (float)k_in + na.eps);
+  h8 xn[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i)
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      xn[i][t] = from_float<half_t>(to_float<half_t>(src[i][t]) * inverse * to_float<half_t>(gam[i][t]));
+  auto consume = [&](const h8 (&w)[NC][MATS][RPW], int slot) {
+    float acc[MATS][RPW];
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        acc[m][r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) acc[m][r] = dot8(w[i][m][r], xn[i], acc[m][r]);
+      }
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        const float sum = wave_sum(acc[m][r]);
+        if (lane == 0) partial[wave][slot][m][r] = sum;
+      }
+  };
+  int slot = 0;
+  for (; g < groups; g += 2 * grid, slot += 2) {  // block-uniform
+    consume(wa, slot);
+    load_group(wa, g + 2 * grid);
+    consume(wb, slot + 1);
+    load_group(wb, g + 3 * grid);
+  }
+  __syncthreads();
+  // the block's rows: (slot, row of the group) pairs, wave 0
+  if (wave != 0) return;
+  if constexpr (ROPE) {
+    for (int s = lane; s < slot; s += kWave) {
+      const int gg = (int)blockIdx.x + s * grid;
+      if (gg >= groups) continue;
+      float even = 0.0f, odd = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        even += partial[w][s][0][0];
+        odd += partial[w][s][0][1];
+      }
+      rope_append_pair(ra, 0, gg * RPW, even, odd);
+    }
+  } else {
+    for (int idx = lane; idx < slot * RPW; idx += kWave) {
+      const int s = idx / RPW, r = idx % RPW;
+      const int row = ((int)blockIdx.x + s * grid) * RPW + r;
+      if (row >= n_out) continue;
+      float a[2] = {0.0f, 0.0f};
+#pragma unroll
+      for (int m = 0; m < MATS; ++m)
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) a[m] += partial[w][s][m][r];
+      write_out<MATS>(y, (size_t)row, a[0], a[1]);
+    }
   }
 }
 
@@ -485,7 +649,6 @@ __global__ __launch_bounds__(1024) void mfma_rows_kernel(const half_t* __restric
 }
 
 // ---------------------------------------------------------------- dispatch
-constexpr int kFusedMaxBlocks = 2048;
 
 struct Shape {
   const half_t* x;
@@ -495,41 +658,87 @@ struct Shape {
   int y_dtype, batch, n, k;
 };
 
-template <int MATS, int NB, int RPW, int U, int KS, typename OutT, int PRO = 0, bool ROPE = false>
+template <int MATS, int NB, int RPW, int U, int KS, typename OutT, int FUSE = kFuseNone,
+          bool ROPE = false>
 int launch_dot(const Shape& s, const half_t* x, OutT* y, hipStream_t stream,
                const NormArgs& na = NormArgs{}, const RopeArgs& ra = RopeArgs{}) {
   const int rows_per_block = (4 / KS) * RPW;
-  int blocks = (s.n + rows_per_block - 1) / rows_per_block;
-  // With the norm prologue every block re-reads the row (3 x k halves): at
-  // most kFusedMaxBlocks blocks (8 per CU) keep that L2 traffic small.
-  if (PRO > 0 && blocks > kFusedMaxBlocks) blocks = kFusedMaxBlocks;
-  const dim3 grid(blocks);
-  const size_t lds = PRO > 0 ? (size_t)s.k * sizeof(half_t) : 0;
-  hipLaunchKernelGGL((gemv_dot_kernel<MATS, NB, RPW, U, KS, OutT, PRO, ROPE>), grid, dim3(256),
-                     lds, stream, x, s.w0, s.w1, y, s.n, s.k, na, ra);
+  const dim3 grid((s.n + rows_per_block - 1) / rows_per_block);
+  hipLaunchKernelGGL((gemv_dot_kernel<MATS, NB, RPW, U, KS, OutT, FUSE, ROPE>), grid, dim3(256), 0,
+                     stream, x, s.w0, s.w1, y, s.n, s.k, na, ra);
   return check_launch("gemv_dot_kernel");
 }
 
-// Batch-1 dot GEMV with the fused norm prologue, by configuration.
-template <int MATS, typename OutT, int PRO>
+// Batch-1 dot GEMV with a fusion (norm prologue or residual epilogue), by
+// configuration.
+template <int MATS, typename OutT, int FUSE>
 int launch_dot_fused(const Shape& s, OutT* y, const tmc_gemv_config& c, const NormArgs& na,
                      hipStream_t st) {
   const int key = (c.rows_per_wave == 2 ? 100 : 0) + (c.unroll == 2 ? 10 : 0) +
                   (c.k_split == 4 ? 2 : c.k_split == 2 ? 1 : 0);
   switch (key) {
-  case 0: return launch_dot<MATS, 1, 1, 4, 1, OutT, PRO>(s, nullptr, y, st, na);
-  case 1: return launch_dot<MATS, 1, 1, 4, 2, OutT, PRO>(s, nullptr, y, st, na);
-  case 2: return launch_dot<MATS, 1, 1, 4, 4, OutT, PRO>(s, nullptr, y, st, na);
-  case 10: return launch_dot<MATS, 1, 1, 2, 1, OutT, PRO>(s, nullptr, y, st, na);
-  case 11: return launch_dot<MATS, 1, 1, 2, 2, OutT, PRO>(s, nullptr, y, st, na);
-  case 12: return launch_dot<MATS, 1, 1, 2, 4, OutT, PRO>(s, nullptr, y, st, na);
-  case 100: return launch_dot<MATS, 1, 2, 4, 1, OutT, PRO>(s, nullptr, y, st, na);
-  case 101: return launch_dot<MATS, 1, 2, 4, 2, OutT, PRO>(s, nullptr, y, st, na);
-  case 102: return launch_dot<MATS, 1, 2, 4, 4, OutT, PRO>(s, nullptr, y, st, na);
-  case 110: return launch_dot<MATS, 1, 2, 2, 1, OutT, PRO>(s, nullptr, y, st, na);
-  case 111: return launch_dot<MATS, 1, 2, 2, 2, OutT, PRO>(s, nullptr, y, st, na);
-  default: return launch_dot<MATS, 1, 2, 2, 4, OutT, PRO>(s, nullptr, y, st, na);
+  case 0: return launch_dot<MATS, 1, 1, 4, 1, OutT, FUSE>(s, s.x, y, st, na);
+  case 1: return launch_dot<MATS, 1, 1, 4, 2, OutT, FUSE>(s, s.x, y, st, na);
+  case 2: return launch_dot<MATS, 1, 1, 4, 4, OutT, FUSE>(s, s.x, y, st, na);
+  case 10: return launch_dot<MATS, 1, 1, 2, 1, OutT, FUSE>(s, s.x, y, st, na);
+  case 11: return launch_dot<MATS, 1, 1, 2, 2, OutT, FUSE>(s, s.x, y, st, na);
+  case 12: return launch_dot<MATS, 1, 1, 2, 4, OutT, FUSE>(s, s.x, y, st, na);
+  case 100: return launch_dot<MATS, 1, 2, 4, 1, OutT, FUSE>(s, s.x, y, st, na);
+  case 101: return launch_dot<MATS, 1, 2, 4, 2, OutT, FUSE>(s, s.x, y, st, na);
+  case 102: return launch_dot<MATS, 1, 2, 4, 4, OutT, FUSE>(s, s.x, y, st, na);
+  case 110: return launch_dot<MATS, 1, 2, 2, 1, OutT, FUSE>(s, s.x, y, st, na);
+  case 111: return launch_dot<MATS, 1, 2, 2, 2, OutT, FUSE>(s, s.x, y, st, na);
+  default: return launch_dot<MATS, 1, 2, 2, 4, OutT, FUSE>(s, s.x, y, st, na);
   }
+}
+
+// Batch-1 GEMV / gated MLP / q.k.v + RoPE of a normalized stored row: the
+// persistent grid holds at most the blocks resident at once (occupancy x
+// CUs, measured once per instance and device) and gives each block the same
+// number of row groups, at most 32 (its LDS partials).
+template <int MATS, int RPW, int NC, typename OutT, int FUSE, bool ROPE>
+int launch_norm_gemv_nc(const Shape& s, OutT* y, const NormArgs& na, const RopeArgs& ra,
+                        hipStream_t st) {
+  auto kernel = gemv_norm_kernel<MATS, RPW, NC, OutT, FUSE, ROPE>;
+  static int resident[64] = {0};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64)
+    return fail("gemv_norm_kernel: no current device.");
+  if (resident[device] == 0) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+        per_cu <= 0 || cus <= 0)
+      return fail("gemv_norm_kernel: occupancy query failed.");
+    resident[device] = per_cu * cus * TMC_NORM_GRID_FACTOR;
+  }
+  // as many row groups per block as the resident blocks need, then the
+  // fewest blocks that cover the groups with that count, so that every block
+  // streams the same number of groups (a block with one extra group would
+  // run alone at the end)
+  const int groups = (s.n + RPW - 1) / RPW;
+  const int per_block = std::min((groups + resident[device] - 1) / resident[device],
+                                 kNormMaxSlots - 2);
+  const int grid = (groups + per_block - 1) / per_block;
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, st, s.w0, s.w1, y, s.n, s.k, na, ra);
+  return check_launch("gemv_norm_kernel");
+}
+
+template <int MATS, int RPW, typename OutT, int FUSE, bool ROPE = false>
+int launch_norm_gemv_rpw(const Shape& s, OutT* y, const NormArgs& na, const RopeArgs& ra,
+                         hipStream_t st) {
+  const int chunks = s.k / 8;
+  if (chunks <= 256) return launch_norm_gemv_nc<MATS, RPW, 1, OutT, FUSE, ROPE>(s, y, na, ra, st);
+  if (chunks <= 512) return launch_norm_gemv_nc<MATS, RPW, 2, OutT, FUSE, ROPE>(s, y, na, ra, st);
+  return launch_norm_gemv_nc<MATS, RPW, 4, OutT, FUSE, ROPE>(s, y, na, ra, st);
+}
+
+template <int MATS, typename OutT, int FUSE>
+int launch_norm_gemv(const Shape& s, OutT* y, int rows_per_block, const NormArgs& na,
+                     hipStream_t st) {
+  return rows_per_block == 2
+             ? launch_norm_gemv_rpw<MATS, 2, OutT, FUSE>(s, y, na, RopeArgs{}, st)
+             : launch_norm_gemv_rpw<MATS, 1, OutT, FUSE>(s, y, na, RopeArgs{}, st);
 }
 
 template <int MATS, int NB, typename OutT>
@@ -828,14 +1037,22 @@ extern "C" int tmc_gate_up_silu_f16_config(const void* x, const void* w_gate, co
 
 namespace {
 
-// Default configuration of the fused norm + GEMV (batch 1), from MI355X
-// sweeps at K 4096: 2 rows per wave, 4 loads in flight, 2 waves per row for
-// the gated pair and 1 for a single matrix (N 12288 and 32000).  Measured
-// against the norm kernel followed by the GEMV in a graph: gated 29.7 vs
-// 29.4 us, QKV 18.1 vs 19.1 us, LM head 40.0 vs 41.0 us -- the separate norm
-// costs only ~2.4 us there, and every block's prologue costs about as much.
-tmc_gemv_config fused_default(int mats) {
-  return mats == 2 ? tmc_gemv_config{1, 2, 4, 2} : tmc_gemv_config{1, 2, 4, 1};
+// Configuration of the norm fusions: the dot algorithm at k split 4 (the
+// wave <-> norm group mapping of gemv_norm_kernel), rows_per_wave 1 or 2
+// rows per block; the unroll does not apply (a wave holds all its chunks).
+// Default: 2 rows per block for one matrix (halves the row and gamma reads
+// per weight byte), 1 for the gated pair (its 2 x 2 weight rows would cost
+// occupancy).
+int norm_config(const tmc_gemv_config* config, const std::string& what, int mats,
+                int& rows_per_block) {
+  rows_per_block = mats == 2 ? 1 : 2;
+  if (!config || config->algorithm == 0) return 0;
+  TMC_REQUIRE(config->algorithm == 1 && config->k_split == 4 &&
+                  (config->rows_per_wave == 1 || config->rows_per_wave == 2),
+              what + ": config must use the dot algorithm (1) with k_split 4 and rows_per_wave "
+                     "1|2.");
+  rows_per_block = config->rows_per_wave;
+  return 0;
 }
 
 int fused_entry(int mats, const void* residual, const void* update, const void* gamma,
@@ -849,16 +1066,16 @@ int fused_entry(int mats, const void* residual, const void* update, const void* 
               std::string(what) + ": output dtype must be fp16 or fp32.");
   TMC_REQUIRE(batch == 1, std::string(what) + ": batch must be 1 (larger batches run the "
                                               "norm and the packed GEMM).");
-  TMC_REQUIRE(k > 0 && n > 0 && k % 8 == 0 && k <= 32768 && n < (1LL << 31),
-              std::string(what) + ": in_features must be a positive multiple of 8 up to 32768.");
+  TMC_REQUIRE(k > 0 && n > 0 && k % 8 == 0 && k <= 8 * kNormMaxChunks && n < (1LL << 31),
+              std::string(what) + ": in_features must be a positive multiple of 8 up to 8192.");
+  TMC_REQUIRE((n + 1) * k * 2 < (int64_t)kBufferAbsent,
+              std::string(what) + ": a weight matrix must stay below 4 GiB.");
   TMC_REQUIRE(aligned16(residual) && aligned16(gamma) && aligned16(w0) &&
                   (mats == 1 || aligned16(w1)) && (!update || (aligned16(update) && aligned16(sum_out))),
               std::string(what) + ": operands must be 16-byte aligned.");
   TMC_REQUIRE(std::isfinite(eps) && eps > 0.0f, std::string(what) + ": epsilon must be positive.");
-  tmc_gemv_config cfg = fused_default(mats);
-  if (config && config->algorithm != 0) cfg = *config;
-  TMC_REQUIRE(cfg.algorithm == 1, std::string(what) + ": config must use the dot algorithm (1).");
-  if (validate_config(cfg)) return 1;
+  int rpb = 2;
+  if (norm_config(config, what, mats, rpb)) return 1;
   NormArgs na;
   na.residual = static_cast<const half_t*>(residual);
   na.update = static_cast<const half_t*>(update);
@@ -869,13 +1086,15 @@ int fused_entry(int mats, const void* residual, const void* update, const void* 
           1, (int)n, (int)k};
   const hipStream_t st = as_stream(stream);
   if (update) {
-    if (mats == 2) return launch_dot_fused<2, half_t, 1>(s, static_cast<half_t*>(y), cfg, na, st);
-    return y_dtype == TMC_F32 ? launch_dot_fused<1, float, 1>(s, static_cast<float*>(y), cfg, na, st)
-                              : launch_dot_fused<1, half_t, 1>(s, static_cast<half_t*>(y), cfg, na, st);
+    if (mats == 2) return launch_norm_gemv<2, half_t, kFuseAddNorm>(s, static_cast<half_t*>(y), rpb, na, st);
+    return y_dtype == TMC_F32
+               ? launch_norm_gemv<1, float, kFuseAddNorm>(s, static_cast<float*>(y), rpb, na, st)
+               : launch_norm_gemv<1, half_t, kFuseAddNorm>(s, static_cast<half_t*>(y), rpb, na, st);
   }
-  if (mats == 2) return launch_dot_fused<2, half_t, 2>(s, static_cast<half_t*>(y), cfg, na, st);
-  return y_dtype == TMC_F32 ? launch_dot_fused<1, float, 2>(s, static_cast<float*>(y), cfg, na, st)
-                            : launch_dot_fused<1, half_t, 2>(s, static_cast<half_t*>(y), cfg, na, st);
+  if (mats == 2) return launch_norm_gemv<2, half_t, kFuseNorm>(s, static_cast<half_t*>(y), rpb, na, st);
+  return y_dtype == TMC_F32
+             ? launch_norm_gemv<1, float, kFuseNorm>(s, static_cast<float*>(y), rpb, na, st)
+             : launch_norm_gemv<1, half_t, kFuseNorm>(s, static_cast<half_t*>(y), rpb, na, st);
 }
 
 }  // namespace
@@ -899,45 +1118,72 @@ extern "C" int tmc_add_rmsnorm_gate_up_silu_f16(const void* residual, const void
                      hidden, intermediate, epsilon, config, stream);
 }
 
+extern "C" int tmc_gemv_residual_f16(const void* x, const void* w, const void* residual, void* y,
+                                     int64_t batch, int64_t in_features, int64_t out_features,
+                                     const tmc_gemv_config* config, void* stream) {
+  TMC_REQUIRE(x && w && residual && y, "GEMV + residual: null device pointer.");
+  TMC_REQUIRE(batch == 1, "GEMV + residual: batch must be 1.");
+  TMC_REQUIRE(in_features > 0 && out_features > 0 && in_features % 8 == 0 &&
+                  in_features < (1LL << 31) && out_features < (1LL << 31),
+              "GEMV + residual: in_features must be a positive multiple of 8.");
+  TMC_REQUIRE(aligned16(x) && aligned16(w), "GEMV + residual: x and W must be 16-byte aligned.");
+  tmc_gemv_config cfg = default_config(1, (int)out_features, (int)in_features, 1);
+  if (config && config->algorithm != 0) cfg = *config;
+  TMC_REQUIRE(cfg.algorithm == 1, "GEMV + residual: config must use the dot algorithm (1).");
+  if (validate_config(cfg)) return 1;
+  NormArgs na;
+  na.residual = static_cast<const half_t*>(residual);
+  Shape s{static_cast<const half_t*>(x), static_cast<const half_t*>(w), nullptr, y, TMC_F16, 1,
+          (int)out_features, (int)in_features};
+  return launch_dot_fused<1, half_t, kFuseResidual>(s, static_cast<half_t*>(y), cfg, na,
+                                                    as_stream(stream));
+}
+
 namespace {
 
-template <int PRO>
-int launch_qkv_rope(const Shape& s, const tmc_gemv_config& c, const NormArgs& na,
-                    const RopeArgs& ra, hipStream_t st) {
+int launch_qkv_rope(const Shape& s, const tmc_gemv_config& c, hipStream_t st, const RopeArgs& ra) {
   half_t* none = nullptr;
+  const NormArgs na{};
   switch ((c.unroll == 2 ? 10 : 0) + (c.k_split == 4 ? 2 : c.k_split == 2 ? 1 : 0)) {
-  case 0: return launch_dot<1, 1, 2, 4, 1, half_t, PRO, true>(s, s.x, none, st, na, ra);
-  case 1: return launch_dot<1, 1, 2, 4, 2, half_t, PRO, true>(s, s.x, none, st, na, ra);
-  case 2: return launch_dot<1, 1, 2, 4, 4, half_t, PRO, true>(s, s.x, none, st, na, ra);
-  case 10: return launch_dot<1, 1, 2, 2, 1, half_t, PRO, true>(s, s.x, none, st, na, ra);
-  case 11: return launch_dot<1, 1, 2, 2, 2, half_t, PRO, true>(s, s.x, none, st, na, ra);
-  default: return launch_dot<1, 1, 2, 2, 4, half_t, PRO, true>(s, s.x, none, st, na, ra);
+  case 0: return launch_dot<1, 1, 2, 4, 1, half_t, kFuseNone, true>(s, s.x, none, st, na, ra);
+  case 1: return launch_dot<1, 1, 2, 4, 2, half_t, kFuseNone, true>(s, s.x, none, st, na, ra);
+  case 2: return launch_dot<1, 1, 2, 4, 4, half_t, kFuseNone, true>(s, s.x, none, st, na, ra);
+  case 10: return launch_dot<1, 1, 2, 2, 1, half_t, kFuseNone, true>(s, s.x, none, st, na, ra);
+  case 11: return launch_dot<1, 1, 2, 2, 2, half_t, kFuseNone, true>(s, s.x, none, st, na, ra);
+  default: return launch_dot<1, 1, 2, 2, 4, half_t, kFuseNone, true>(s, s.x, none, st, na, ra);
   }
 }
 
-// q.k.v projection + RoPE + paged append at batch 1; norm: PRO 0 (x is the
-// projection input), 1 (x = RMSNorm(residual + update)) or 2 (RMSNorm(residual)).
-int qkv_rope_entry(int pro, const void* x, const NormArgs& na, const void* w,
+// q.k.v projection + RoPE + paged append at batch 1; fuse: kFuseNone (x is
+// the projection input), kFuseAddNorm (x = RMSNorm(residual + update)) or
+// kFuseNorm (RMSNorm(residual)).
+int qkv_rope_entry(int fuse, const void* x, const NormArgs& na, const void* w,
                    const float* cosine, const float* sine, const int32_t* valid_lengths,
                    const int32_t* block_table, const int32_t* active_count, void* q_out,
                    void* key_pool, void* value_pool, int64_t hidden, int64_t q_heads,
                    int64_t kv_heads, int64_t head_dim, int64_t capacity, int64_t page_size,
                    const tmc_gemv_config* config, void* stream) {
-  TMC_REQUIRE((pro > 0 || x) && w && cosine && sine && valid_lengths && block_table &&
+  TMC_REQUIRE((fuse != kFuseNone || x) && w && cosine && sine && valid_lengths && block_table &&
                   active_count && q_out && key_pool && value_pool,
               "Fused q.k.v RoPE append: null pointer.");
-  TMC_REQUIRE(hidden > 0 && hidden % 8 == 0 && (pro > 0 ? hidden <= 32768 : hidden < (1LL << 31)) &&
-                  (pro > 0 || aligned16(x)) && aligned16(w),
-              "Fused q.k.v RoPE append: hidden must be a positive multiple of 8 (at most 32768 "
+  TMC_REQUIRE(hidden > 0 && hidden % 8 == 0 &&
+                  (fuse != kFuseNone ? hidden <= 8 * kNormMaxChunks : hidden < (1LL << 31)) &&
+                  (fuse != kFuseNone || aligned16(x)) && aligned16(w),
+              "Fused q.k.v RoPE append: hidden must be a positive multiple of 8 (at most 8192 "
               "with the norm) and x, W 16-byte aligned.");
   TMC_REQUIRE(q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 && head_dim > 0 &&
                   head_dim % 2 == 0 && capacity > 0 && page_size > 0 &&
                   (q_heads + 2 * kv_heads) * head_dim < (1LL << 31),
               "Fused q.k.v RoPE append: invalid head geometry, capacity or page size.");
-  // measured defaults (C5 q.k.v shape): unroll 4 / k split 4 without the
-  // norm, unroll 2 / k split 2 with it
-  tmc_gemv_config c = pro > 0 ? tmc_gemv_config{1, 2, 2, 2} : tmc_gemv_config{1, 2, 4, 4};
+  // measured default (C5 q.k.v shape): unroll 4, k split 4 (the norm form:
+  // k split 4 always, the unroll does not apply)
+  tmc_gemv_config c{1, 2, 4, 4};
   if (config && config->algorithm != 0) c = *config;
+  TMC_REQUIRE(fuse == kFuseNone || c.k_split == 4,
+              "Fused norm + q.k.v RoPE append: the norm form needs k_split 4.");
+  TMC_REQUIRE(fuse == kFuseNone ||
+                  ((q_heads + 2 * kv_heads) * head_dim + 1) * hidden * 2 < (int64_t)kBufferAbsent,
+              "Fused norm + q.k.v RoPE append: the weight must stay below 4 GiB.");
   TMC_REQUIRE(c.algorithm == 1 && c.rows_per_wave == 2 && (c.unroll == 2 || c.unroll == 4) &&
                   (c.k_split == 1 || c.k_split == 2 || c.k_split == 4),
               "Fused q.k.v RoPE append: the dot algorithm with rows_per_wave 2, unroll 2|4 and "
@@ -960,9 +1206,11 @@ int qkv_rope_entry(int pro, const void* x, const NormArgs& na, const void* w,
   ra.capacity = (int)capacity;
   ra.page_size = (int)page_size;
   const hipStream_t st = as_stream(stream);
-  if (pro == 1) return launch_qkv_rope<1>(s, c, na, ra, st);
-  if (pro == 2) return launch_qkv_rope<2>(s, c, na, ra, st);
-  return launch_qkv_rope<0>(s, c, na, ra, st);
+  if (fuse == kFuseAddNorm)
+    return launch_norm_gemv_rpw<1, 2, half_t, kFuseAddNorm, true>(s, nullptr, na, ra, st);
+  if (fuse == kFuseNorm)
+    return launch_norm_gemv_rpw<1, 2, half_t, kFuseNorm, true>(s, nullptr, na, ra, st);
+  return launch_qkv_rope(s, c, st, ra);
 }
 
 }  // namespace
@@ -974,7 +1222,7 @@ extern "C" int tmc_qkv_rope_append_f16(const void* x, const void* w, const float
                                        int64_t hidden, int64_t q_heads, int64_t kv_heads,
                                        int64_t head_dim, int64_t capacity, int64_t page_size,
                                        const tmc_gemv_config* config, void* stream) {
-  return qkv_rope_entry(0, x, NormArgs{}, w, cosine, sine, valid_lengths, block_table,
+  return qkv_rope_entry(kFuseNone, x, NormArgs{}, w, cosine, sine, valid_lengths, block_table,
                         active_count, q_out, key_pool, value_pool, hidden, q_heads, kv_heads,
                         head_dim, capacity, page_size, config, stream);
 }
@@ -999,7 +1247,7 @@ extern "C" int tmc_add_rmsnorm_qkv_rope_append_f16(
   na.gamma = static_cast<const half_t*>(gamma);
   na.sum_out = static_cast<half_t*>(sum_out);
   na.eps = epsilon;
-  return qkv_rope_entry(update ? 1 : 2, nullptr, na, w, cosine, sine, valid_lengths, block_table,
+  return qkv_rope_entry(update ? kFuseAddNorm : kFuseNorm, nullptr, na, w, cosine, sine, valid_lengths, block_table,
                         active_count, q_out, key_pool, value_pool, hidden, q_heads, kv_heads,
                         head_dim, capacity, page_size, config, stream);
 }

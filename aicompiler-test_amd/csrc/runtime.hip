@@ -335,6 +335,24 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     };
     return true;
   }
+  if (name == "gemv_residual") {
+    // Batch-1 GEMV with the residual add in its epilogue: inputs x, weight,
+    // residual; output h(residual + h(W x)).
+    const int64_t k = param_int(p, "in"), n = param_int(p, "out");
+    NEED(param_int(p, "batch", 1) == 1 && k > 0 && n > 0 && dt == TMC_F16,
+         "gemv_residual needs batch=1, in, out > 0 and dtype=f16.");
+    tmc_gemv_config cfg{};
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    s.inputs = {TMC_F16, TMC_F16, TMC_F16};
+    s.outputs = {TMC_F16};
+    s.counts = {(size_t)k, (size_t)(n * k), (size_t)n, (size_t)n};
+    s.groups = (size_t)((n + 3) / 4);
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_gemv_residual_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], 1, k, n, &cfg,
+                                   c.stream);
+    };
+    return true;
+  }
   if (name == "add_rmsnorm_gemv" || name == "rmsnorm_gemv" || name == "add_rmsnorm_gate_up_silu" ||
       name == "rmsnorm_gate_up_silu") {
     // Batch-1 norm folded into the GEMV: inputs residual[, update], gamma,

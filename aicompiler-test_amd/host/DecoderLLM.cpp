@@ -460,26 +460,35 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
         normShape + (generatedNorm.empty() ? templateTuning : generatedNorm);
     const std::string norm =
         normShape + (generatedAddNorm.empty() ? templateTuning : generatedAddNorm);
+    const bool fuseRope = H % 8 == 0 && D % 2 == 0;
+    // Batch 1 without admitted norm kernels: fold every norm into the
+    // neighbouring GEMVs when the template norm holds one 16-byte chunk per
+    // thread (512 threads at hidden 4096, 256 up to 2048), whose summation
+    // order the GEMV prologue follows, so the step's results do not change.
+    const std::size_t normThreads = H >= 4096 ? 512 : 256;
+    const bool fold = foldNorms_ && !packed && fuseRope && generatedNorm.empty() &&
+                      generatedAddNorm.empty() && H % 8 == 0 && H / 8 <= normThreads;
     if (registry_) {
       const auto track = [&](const char* node, const char* pattern, const std::string& tuning,
                              const std::string& key, std::size_t launches) {
+        const char* implementation = fold ? "folded" : tuning.empty() ? "template" : "generated";
         bucket->uses.push_back(registry_->track(
-            {"bucket " + B + " " + node, pattern, tuning.empty() ? "template" : "generated", key,
-             launches, 0}));
+            {"bucket " + B + " " + node, pattern, implementation, key, fold ? 0 : launches, 0}));
       };
-      track("input norm", "decoder_rmsnorm", generatedNorm, "rmsnorm?" + firstNorm, 1);
+      track("input norm", "decoder_rmsnorm", generatedNorm,
+            fold ? "rmsnorm_qkv_rope_append" : "rmsnorm?" + firstNorm, 1);
       track("residual norms", "decoder_residual_rmsnorm", generatedAddNorm,
-            "add_rmsnorm?" + norm, 2 * L);
+            fold ? "gemv_residual + rmsnorm_* prologues" : "add_rmsnorm?" + norm, 2 * L);
     }
     add("embedding?rows=" + B + "&hidden=" + std::to_string(H) + "&vocab=" + std::to_string(V),
         "embedding", {tokensView_, model_->embeddingWeight}, {residual_});
-    add("rmsnorm?" + firstNorm, "l0_input_norm", {residual_, model_->layers[0].inputNormWeight},
-        {normalized_});
+    if (!fold)
+      add("rmsnorm?" + firstNorm, "l0_input_norm", {residual_, model_->layers[0].inputNormWeight},
+          {normalized_});
     const std::string ropeKey = "decode_rope_append?max_batch=" + B + "&q_heads=" + std::to_string(QH) +
                                 "&kv_heads=" + std::to_string(KVH) + "&head_dim=" + std::to_string(D) +
                                 "&capacity=" + std::to_string(capacity) +
                                 "&page_size=" + std::to_string(pageSize_);
-    const bool fuseRope = H % 8 == 0 && D % 2 == 0;
     const std::string ropeShape = "hidden=" + std::to_string(H) + "&q_heads=" + std::to_string(QH) +
                                   "&kv_heads=" + std::to_string(KVH) +
                                   "&head_dim=" + std::to_string(D) +
@@ -492,44 +501,79 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
         "paged_attention?max_batch=" + B + "&q_heads=" + std::to_string(QH) +
         "&kv_heads=" + std::to_string(KVH) + "&head_dim=" + std::to_string(D) +
         "&page_size=" + std::to_string(pageSize_) + "&max_pages=" + std::to_string(maxPages_);
-    for (std::size_t l = 0; l < L; ++l) {
-      const auto& w = model_->layers[l];
-      const std::string p = "l" + std::to_string(l) + "_";
-      if (l > 0)
-        add("add_rmsnorm?" + norm, p + "residual_input_norm", {after_, mlp_, w.inputNormWeight},
-            {residual_, normalized_});
-      const auto& pw = weights(l);
-      if (fuseRope) {
-        // RoPE and the K/V append run in the projection's epilogue (the dot
-        // GEMV at batch 1, the packed GEMM above).
-        add(qkvRopeKey, p + "qkv_rope_append",
-            {normalized_, pw.queryKeyValueWeight, model_->ropeCosine, model_->ropeSine,
-             lengthsView_, tableViews_[l], activeView_},
+    if (fold) {
+      // residual_ -> [norm prologue] q.k.v + RoPE + append -> attention ->
+      // o + residual -> after_ -> [norm prologue] gate/up -> down + residual
+      // -> residual_; the LM head normalizes the last residual_.
+      const std::string normKey = "&eps=" + eps;
+      auto residualGemv = [&](std::size_t in, std::size_t out) {
+        std::string key = "gemv_residual?in=" + std::to_string(in) + "&out=" + std::to_string(out);
+        const auto it = tunedSuffix.find(std::to_string(in) + "x" + std::to_string(out));
+        return it != tunedSuffix.end() ? key + it->second : key;
+      };
+      for (std::size_t l = 0; l < L; ++l) {
+        const auto& w = model_->layers[l];
+        const std::string p = "l" + std::to_string(l) + "_";
+        add("rmsnorm_qkv_rope_append?" + ropeShape + normKey, p + "norm_qkv_rope_append",
+            {residual_, w.inputNormWeight, w.queryKeyValueWeight, model_->ropeCosine,
+             model_->ropeSine, lengthsView_, tableViews_[l], activeView_},
             {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer()});
-      } else {
-        add(gemv(H, QKV, "f16"), p + "qkv", {normalized_, pw.queryKeyValueWeight}, {qkv_});
-        add(ropeKey, p + "rope_append",
-            {qkv_, model_->ropeCosine, model_->ropeSine, lengthsView_, tableViews_[l], activeView_},
-            {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer()});
+        add(attentionKey, p + "attention",
+            {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer(), lengthsView_,
+             tableViews_[l], activeView_},
+            {context_});
+        add(residualGemv(H, H), p + "o_residual", {context_, w.outputWeight, residual_}, {after_});
+        add("rmsnorm_gate_up_silu?in=" + std::to_string(H) + "&out=" + std::to_string(I) + normKey,
+            p + "norm_gate_up_silu", {after_, w.postAttentionNormWeight, w.gateWeight, w.upWeight},
+            {gated_});
+        add(residualGemv(I, H), p + "down_residual", {gated_, w.downWeight, after_}, {residual_});
       }
-      add(attentionKey, p + "attention",
-          {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer(), lengthsView_, tableViews_[l],
-           activeView_},
-          {context_});
-      add(gemv(H, H, "f16", false), p + "o", {context_, pw.outputWeight}, {projected_});
-      add("add_rmsnorm?" + norm, p + "residual_post_norm",
-          {residual_, projected_, w.postAttentionNormWeight}, {after_, normalized_});
-      add(std::string(packed ? "gate_up_silu_packed" : "gate_up_silu") + "?batch=" + B +
-              "&hidden=" + std::to_string(H) + "&inter=" + std::to_string(I) +
-              (packed ? "&x_layout=packed&y_layout=packed" : ""),
-          p + "gate_up_silu", {normalized_, pw.gateWeight, pw.upWeight}, {gated_});
-      add(gemv(I, H, "f16"), p + "down", {gated_, pw.downWeight}, {mlp_});
+      std::string head = "rmsnorm_gemv?in=" + std::to_string(H) + "&out=" + std::to_string(V) +
+                         "&out_dtype=f32" + normKey;
+      const auto it = tunedSuffix.find(std::to_string(H) + "x" + std::to_string(V));
+      if (it != tunedSuffix.end()) head += it->second;
+      add(head, "norm_lm_head", {residual_, model_->finalNormWeight, model_->languageModelHeadWeight},
+          {logits_});
+    } else {
+      for (std::size_t l = 0; l < L; ++l) {
+        const auto& w = model_->layers[l];
+        const std::string p = "l" + std::to_string(l) + "_";
+        if (l > 0)
+          add("add_rmsnorm?" + norm, p + "residual_input_norm", {after_, mlp_, w.inputNormWeight},
+              {residual_, normalized_});
+        const auto& pw = weights(l);
+        if (fuseRope) {
+          // RoPE and the K/V append run in the projection's epilogue (the dot
+          // GEMV at batch 1, the packed GEMM above).
+          add(qkvRopeKey, p + "qkv_rope_append",
+              {normalized_, pw.queryKeyValueWeight, model_->ropeCosine, model_->ropeSine,
+               lengthsView_, tableViews_[l], activeView_},
+              {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer()});
+        } else {
+          add(gemv(H, QKV, "f16"), p + "qkv", {normalized_, pw.queryKeyValueWeight}, {qkv_});
+          add(ropeKey, p + "rope_append",
+              {qkv_, model_->ropeCosine, model_->ropeSine, lengthsView_, tableViews_[l], activeView_},
+              {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer()});
+        }
+        add(attentionKey, p + "attention",
+            {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer(), lengthsView_, tableViews_[l],
+             activeView_},
+            {context_});
+        add(gemv(H, H, "f16", false), p + "o", {context_, pw.outputWeight}, {projected_});
+        add("add_rmsnorm?" + norm, p + "residual_post_norm",
+            {residual_, projected_, w.postAttentionNormWeight}, {after_, normalized_});
+        add(std::string(packed ? "gate_up_silu_packed" : "gate_up_silu") + "?batch=" + B +
+                "&hidden=" + std::to_string(H) + "&inter=" + std::to_string(I) +
+                (packed ? "&x_layout=packed&y_layout=packed" : ""),
+            p + "gate_up_silu", {normalized_, pw.gateWeight, pw.upWeight}, {gated_});
+        add(gemv(I, H, "f16"), p + "down", {gated_, pw.downWeight}, {mlp_});
+      }
+      add("add_rmsnorm?" + norm, "residual_final_norm", {after_, mlp_, model_->finalNormWeight},
+          {residual_, normalized_});
+      add(gemv(H, V, "f32"), "lm_head",
+          {normalized_, packed ? model_->packedLanguageModelHead : model_->languageModelHeadWeight},
+          {logits_});
     }
-    add("add_rmsnorm?" + norm, "residual_final_norm", {after_, mlp_, model_->finalNormWeight},
-        {residual_, normalized_});
-    add(gemv(H, V, "f32"), "lm_head",
-        {normalized_, packed ? model_->packedLanguageModelHead : model_->languageModelHeadWeight},
-        {logits_});
     add("argmax?rows=" + B + "&vocab=" + std::to_string(V), "argmax", {logits_}, {nextTokens_});
     std::vector<const hip::PreparedExecution*> pointers;
     for (const auto& step : bucket->steps) pointers.push_back(step.get());
@@ -546,7 +590,8 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
 BatchedDecodeExecutor::Creation createBatchedDecodeExecutor(
     hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
     std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t maximumBatchSize,
-    std::ostream* log, bool tuneKernels, std::shared_ptr<KernelRegistry> registry) {
+    std::ostream* log, bool tuneKernels, std::shared_ptr<KernelRegistry> registry,
+    bool foldNorms) {
   BatchedDecodeExecutor::Creation result;
   try {
     if (!model) throw std::invalid_argument("Batched decode needs model resources.");
@@ -569,6 +614,7 @@ BatchedDecodeExecutor::Creation createBatchedDecodeExecutor(
     executor->maximumBatchSize_ = maximumBatchSize;
     executor->pageSize_ = executor->pools_.front()->pageSize();
     executor->tuneKernels_ = tuneKernels;
+    executor->foldNorms_ = foldNorms;
     executor->registry_ = std::move(registry);
     executor->build(log);
     result.executor = std::move(executor);

@@ -229,7 +229,7 @@ class BatchedDecodeExecutor {
                                               std::shared_ptr<DecoderLLMModelResources>,
                                               std::vector<std::shared_ptr<KVPagePool>>,
                                               std::size_t, std::ostream*, bool,
-                                              std::shared_ptr<KernelRegistry>);
+                                              std::shared_ptr<KernelRegistry>, bool);
   BatchedDecodeExecutor() = default;
   void build(std::ostream* log);
   [[nodiscard]] std::string upload(const std::vector<std::int32_t>& tokens,
@@ -248,6 +248,7 @@ class BatchedDecodeExecutor {
   std::size_t pageSize_ = 0;
   std::size_t maxPages_ = 0;
   bool tuneKernels_ = false;
+  bool foldNorms_ = true;
   std::shared_ptr<KernelRegistry> registry_;  // admitted region kernels, may be null
   std::size_t activationBytes_ = 0;
   // Device buffers sized for maximumBatchSize rows.
@@ -275,11 +276,18 @@ struct BatchedDecodeExecutor::Creation {
 // template norm kernels where their contract shape matches the step (the
 // one-row bucket at hidden 4096); each bucket's region launches are tracked
 // in the registry's usage audit.
+// foldNorms: the one-row bucket runs no norm kernel.  The o and down
+// projections add the residual in their epilogue (emitLinearResidual,
+// DecoderLLMMetalEmitter.cpp:604-622), and the q.k.v, gate/up and LM head
+// GEMVs normalize the stored row in their prologue, in the summation order
+// of the norm kernel the bucket would otherwise run, so results are the same
+// bit for bit.  Applies when that norm holds one 16-byte chunk per thread
+// (hidden <= 2048, or 4096) and no admitted region kernel replaces the norms.
 [[nodiscard]] BatchedDecodeExecutor::Creation createBatchedDecodeExecutor(
     hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
     std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t maximumBatchSize,
     std::ostream* log = nullptr, bool tuneKernels = false,
-    std::shared_ptr<KernelRegistry> registry = nullptr);
+    std::shared_ptr<KernelRegistry> registry = nullptr, bool foldNorms = true);
 
 // Chunked prefill (prefillChunked, DecoderLLMExecutor.cpp:982-1034): the
 // tokens of one request's prompt chunk are the rows of one stage.  Linear
@@ -289,8 +297,8 @@ struct BatchedDecodeExecutor::Creation {
 // starting at position `start` attends [0, start + r + 1), which is what
 // start + r + 1 decode steps would attend.  Stages are prepared for row
 // buckets 16, 32, ... and chunkSize; a chunk runs the smallest that holds it
-// (spare rows are computed and discarded).  A stage replays eagerly on the
-// runtime's stream (the library GEMMs are kept out of graphs).
+// (spare rows are computed and discarded).  Each stage is captured as a HIP
+// graph when it is prepared.
 // One request's part of a prefill chunk: tokens at positions start ..
 // start + tokens - 1, block tables per layer as [maxPages()] holding pages
 // for every position below start + tokens.

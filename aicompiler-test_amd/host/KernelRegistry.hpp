@@ -78,7 +78,7 @@ struct AdmissionFeedback {
 struct KernelUsage {
   std::string node;
   std::string pattern;
-  std::string implementation;  // "generated" or "template"
+  std::string implementation;  // "generated", "template" or "folded" (no launch)
   std::string functions;       // the kernel key it runs
   std::size_t dispatchesPerCall = 0;
   std::size_t completedCalls = 0;

@@ -227,14 +227,15 @@ int tmc_gate_up_silu_f16_config(const void *x, const void *w_gate, const void *w
  * (emitDecoderResidualRMSNorm, DecoderLLMMetalEmitter.cpp:417-477, then
  * emitDecodeGEMV / emitDecoderGatedMLP): x = h(s * rsqrt(mean(s^2) + eps) *
  * gamma) with s = h(residual + update) written to sum_out, or s = residual
- * when update is NULL (plain RMSNorm; sum_out unused).  Every block rebuilds
- * the normalized row in LDS with the arithmetic and summation order of
- * tmc_add_rmsnorm / tmc_rmsnorm, so results equal the two-kernel sequence bit
- * for bit.  At most 2048 blocks run (each loops over its share of the
- * output rows), so the row is rebuilt at most 2048 times.  batch must be 1;
- * in_features a multiple of 8 up to 32768; all operands 16-byte aligned;
- * fp16 operands.  config: NULL / algorithm 0 = the fused default, else a dot
- * configuration (algorithm 1). */
+ * when update is NULL (plain RMSNorm; sum_out unused).  Each block computes
+ * the row's sum of squares itself (its four waves share the row's 64-chunk
+ * groups, then one barrier) in the order of tmc_add_rmsnorm_threads /
+ * tmc_rmsnorm_threads with one 16-byte chunk per thread, so x equals those
+ * kernels' output bit for bit at any thread count >= in_features / 8 (the
+ * 512-thread norm the batch-1 decoder runs at hidden 4096).  batch must be 1;
+ * in_features a multiple of 8 up to 8192; all operands 16-byte aligned; fp16
+ * operands.  config: NULL / algorithm 0 = the GEMV's default for the shape,
+ * else a dot configuration (algorithm 1). */
 int tmc_add_rmsnorm_gemv_f16(const void *residual, const void *update, const void *gamma,
                              const void *w, void *sum_out, void *y, int y_dtype, int64_t batch,
                              int64_t in_features, int64_t out_features, float epsilon,
@@ -244,6 +245,18 @@ int tmc_add_rmsnorm_gate_up_silu_f16(const void *residual, const void *update, c
                                      void *out, int64_t batch, int64_t hidden,
                                      int64_t intermediate, float epsilon,
                                      const tmc_gemv_config *config, void *stream);
+
+/* Batch-1 GEMV with the residual add in its epilogue (emitLinearResidual,
+ * DecoderLLMMetalEmitter.cpp:604-622): y = h(h(W x) + residual), the fp16
+ * rounding of the projection kept, so y equals tmc_gemv_f16 followed by
+ * tmc_add bit for bit.  The batch-1 decoder runs its o and down projections
+ * through it and folds the following norms into the next GEMV's prologue.
+ * batch must be 1; in_features a multiple of 8; x and W 16-byte aligned.
+ * config: NULL / algorithm 0 = tmc_gemv_f16's default for the shape, else a
+ * dot configuration (algorithm 1). */
+int tmc_gemv_residual_f16(const void *x, const void *w, const void *residual, void *y,
+                          int64_t batch, int64_t in_features, int64_t out_features,
+                          const tmc_gemv_config *config, void *stream);
 
 /* Activation layouts of the batch > 1 GEMM path.  TMC_LAYOUT_X_PACKED: the
  * GEMM's activations x [batch, in] are in fragment order; TMC_LAYOUT_Y_PACKED:
@@ -509,14 +522,12 @@ int tmc_qkv_rope_append_f16(const void *x, const void *w, const float *cosine, c
                             const tmc_gemv_config *config, void *stream);
 
 /* tmc_qkv_rope_append_f16 of x = RMSNorm(residual + update) * gamma (update
- * NULL: RMSNorm(residual) * gamma), the normalized row built in each block's
- * LDS as tmc_add_rmsnorm_gemv_f16 builds it (bit-identical to tmc_add_rmsnorm
- * / tmc_rmsnorm; emitDecoderResidualRMSNorm, DecoderLLMMetalEmitter.cpp:
- * 417-477); with an update, sum_out receives h(residual + update).  It
- * removes the norm launch but measured no faster than the norm kernel plus
- * tmc_qkv_rope_append_f16 on the 7B shape (the row rebuild is a dependent
- * load-reduce chain at the start of every block), so the batch-1 decoder
- * keeps the two launches. */
+ * NULL: RMSNorm(residual) * gamma), the norm computed in each block as
+ * tmc_add_rmsnorm_gemv_f16 computes it (bit-identical to tmc_add_rmsnorm /
+ * tmc_rmsnorm with one 16-byte chunk per thread; emitDecoderResidualRMSNorm,
+ * DecoderLLMMetalEmitter.cpp:417-477); with an update, sum_out receives
+ * h(residual + update).  hidden at most 8192.  The batch-1 decoder runs it
+ * (update NULL) on the residual stream that tmc_gemv_residual_f16 wrote. */
 int tmc_add_rmsnorm_qkv_rope_append_f16(const void *residual, const void *update,
                                         const void *gamma, const void *w, void *sum_out,
                                         const float *cosine, const float *sine,

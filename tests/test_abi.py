@@ -82,6 +82,19 @@ def test_argument_validation_fails_before_device_work(tmc):
     assert lib.tmc_paged_gather_probe(p, p, p, None, 16, 8, 128, 16, 256, 8192, 16384, 2048, p,
                                       None) != 0
     assert "null" in tmc.last_error()
+    # the residual epilogue: batch 1 only, fp16 operands present
+    assert lib.tmc_gemv_residual_f16(p, p, None, p, 1, 64, 8, None, None) != 0
+    assert "null" in tmc.last_error()
+    assert lib.tmc_gemv_residual_f16(p, p, p, p, 2, 64, 8, None, None) != 0
+    assert "batch must be 1" in tmc.last_error()
+    # the fused norm holds at most 8192 features (four 16-byte chunks a lane)
+    assert lib.tmc_add_rmsnorm_gemv_f16(p, None, p, p, None, p, 0, 1, 8200, 8, C.c_float(1e-6),
+                                        None, None) != 0
+    assert "up to 8192" in tmc.last_error()
+    cfg = tmc.GemvConfig(1, 1, 2, 2)  # the norm fusion maps waves to norm groups at k split 4
+    assert lib.tmc_add_rmsnorm_gemv_f16(p, None, p, p, None, p, 0, 1, 4096, 8, C.c_float(1e-6),
+                                        C.byref(cfg), None) != 0
+    assert "k_split 4" in tmc.last_error()
     assert lib.tmc_buf_copy_async(None, 0, None, 0, 1) != 0
     assert "different runtimes" in tmc.last_error()
 

@@ -253,3 +253,36 @@ def test_7b_serving_batch16_matches_oracle(host, orc, rt7b, weights7b, models7b)
                              f"request {r} step {step}")
     finally:
         orc.set_threads(1)
+
+
+def test_7b_batch1_folded_norms_equal_norm_kernels(host, orc, rt7b, models7b):
+    """The one-row bucket with the norms folded into the neighbouring GEMVs
+    (o / down + residual epilogue, norm prologue in q.k.v, gate/up and the LM
+    head) against the same bucket with the 512-thread norm kernels: logits
+    and greedy tokens equal bit for bit over 40 steps that cross pages, with
+    2L + 1 fewer dispatches per step."""
+    model, plan = models7b(1024)
+    runs = {}
+    for fold in (True, False):
+        pools = [host.create_kv_page_pool(rt7b, plan.kv_plan(), P, 1024 // P)
+                 for _ in range(SHAPE["layers"])]
+        ex = host.create_batched_decode_executor(rt7b, model, pools, 1, fold_norms=fold)
+        states = [host.create_kv_cache_state(rt7b, plan.kv_plan(), pool, False) for pool in pools]
+        rng = np.random.default_rng(5101)
+        logits, tokens = [], []
+        for i in range(40):
+            for s in states:
+                assert s.stage_length(rt7b, i + 1) == ""
+                s.commit_length(i + 1)
+            tables = [s.page_table() + [-1] * (ex.max_pages() - len(s.page_table())) for s in states]
+            out = ex.run([int(rng.integers(0, SHAPE["vocabulary"]))], [i + 1], tables, True, False)
+            assert out["passed"], out["error"]
+            logits.append(np.asarray(out["logits"], np.float32))
+            tokens.append(int(out["next_token_ids"][0]))
+        runs[fold] = (ex.dispatches_per_step(1), logits, tokens)
+        del ex, states, pools
+    L = SHAPE["layers"]
+    assert runs[False][0] - runs[True][0] == 2 * L + 1
+    for i, (a, b) in enumerate(zip(runs[True][1], runs[False][1])):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"step {i}"
+    assert runs[True][2] == runs[False][2]

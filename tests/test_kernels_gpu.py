@@ -607,16 +607,15 @@ def test_qkv_rope_append_packed_equals_gemm_then_rope_append(tmc, orc, torch, ba
         assert not np.isnan(values(q)[2]).all()
 
 
-@pytest.mark.parametrize("cfg_t", QKV_ROPE_CONFIGS + [None])
+@pytest.mark.parametrize("cfg_t", [(1, 2, 2, 4), (1, 2, 4, 4), None])
 def test_norm_qkv_rope_append_equals_norm_then_fused_projection(tmc, orc, torch, cfg_t):
     """The Add+RMSNorm (or RMSNorm) prologue in the q.k.v RoPE append kernel
-    reproduces tmc_add_rmsnorm (tmc_rmsnorm) followed by
-    tmc_qkv_rope_append_f16 with the same configuration bit for bit, residual
-    sum included; at k split 4 the 4096 row pairs exceed the 2048-block grid,
-    so blocks loop."""
+    reproduces tmc_add_rmsnorm (tmc_rmsnorm; one chunk per thread at hidden
+    1024) followed by tmc_qkv_rope_append_f16 with the same configuration bit
+    for bit, residual sum included."""
     qh, kvh, d, hidden, cap, p = 32, 16, 128, 1024, 64, 16
     cfg = tmc.GemvConfig(*cfg_t) if cfg_t else None
-    ref_cfg = cfg_t or (1, 2, 2, 2)
+    ref_cfg = cfg_t or (1, 2, 4, 4)
     pos = np.arange(cap)[:, None]
     freq = np.exp(np.arange(0, d, 2) * (-np.log(10000.0) / d))
     cos = dev(np.cos(pos * freq).astype(np.float32))
@@ -821,30 +820,40 @@ def test_packed_gemm_rejects_bad_arguments(tmc, torch):
 DOT_CONFIGS = [(1, r, u, k) for r in (1, 2) for u in (2, 4) for k in (1, 2, 4)]
 
 
-@pytest.mark.parametrize("cfg_t", DOT_CONFIGS + [None])
+def _one_chunk_norm_threads(k):
+    """A norm thread count with at most one 16-byte chunk per thread."""
+    t = 256
+    while t * 8 < k:
+        t *= 2
+    return t
+
+
+@pytest.mark.parametrize("cfg_t", [(1, 1, 2, 4), (1, 2, 4, 4), None])
 def test_fused_norm_gemv_equals_two_kernels_bit_exact(tmc, orc, torch, cfg_t):
     """The batch-1 GEMV / gated MLP with Add+RMSNorm (or RMSNorm) folded in
-    reproduces tmc_add_rmsnorm (tmc_rmsnorm) followed by the same GEMV config
-    bit for bit, residual sum included."""
+    reproduces tmc_add_rmsnorm_threads (tmc_rmsnorm_threads) with one chunk
+    per thread followed by the dot GEMV at k split 4 bit for bit, residual
+    sum included; rows_per_wave 1 or 2 rows per block, odd row counts."""
     cfg = tmc.GemvConfig(*cfg_t) if cfg_t else None
-    ref_cfg = cfg if cfg else None  # the fused default differs by matrix count
-    for k, n in ((4096, 200), (1160, 4096), (1024, 9000)):  # the last loops over row groups
+    for k, n in ((4096, 201), (1160, 4096), (1024, 9000), (8192, 300), (64, 3)):
+        threads = _one_chunk_norm_threads(k)
         h = dev_f16(orc.f16(normal(370, (1, k))))
         r = dev_f16(orc.f16(normal(371, (1, k))))
         gamma = dev_f16(orc.f16(uniform(372, (k,), 0.5, 1.5)))
         w = dev_f16(orc.f16(normal(373, (n, k), 0.02)))
         w2 = dev_f16(orc.f16(normal(374, (n, k), 0.02)))
+        ref_cfg = ref_gated = tmc.GemvConfig(1, 1, 2, 4)  # the k split fixes the order
         for add in (True, False):
             s_ref = torch.empty((1, k), dtype=torch.float16, device="cuda")
             n_ref = torch.empty_like(s_ref)
             if add:
-                tmc.add_rmsnorm(r, h, gamma, s_ref, n_ref, 1e-6)
+                tmc.add_rmsnorm_threads(r, h, gamma, s_ref, n_ref, 1e-6, threads)
             else:
-                tmc.rmsnorm(r, gamma, n_ref, 1e-6)
+                tmc.rmsnorm_threads(r, gamma, n_ref, 1e-6, threads)
             y_ref = torch.empty((1, n), dtype=torch.float32, device="cuda")
-            tmc.gemv_config(n_ref, w, y_ref, ref_cfg or tmc.GemvConfig(1, 2, 4, 1))
+            tmc.gemv_config(n_ref, w, y_ref, ref_cfg)
             g_ref = torch.empty((1, n), dtype=torch.float16, device="cuda")
-            tmc.gate_up_silu_config(n_ref, w, w2, g_ref, ref_cfg or tmc.GemvConfig(1, 2, 4, 2))
+            tmc.gate_up_silu_config(n_ref, w, w2, g_ref, ref_gated)
             s_out = torch.full((1, k), 7.0, dtype=torch.float16, device="cuda")
             y = torch.empty((1, n), dtype=torch.float32, device="cuda")
             tmc.add_rmsnorm_gemv(r, h if add else None, gamma, w, s_out if add else None, y, 1e-6,
@@ -862,6 +871,31 @@ def test_fused_norm_gemv_equals_two_kernels_bit_exact(tmc, orc, torch, cfg_t):
                 assert np.array_equal(bits(s2), bits(s_ref)), what
             else:
                 assert torch.all(s_out == 7.0)
+
+
+@pytest.mark.parametrize("cfg_t", DOT_CONFIGS + [None])
+def test_gemv_residual_equals_gemv_then_add_bit_exact(tmc, orc, torch, cfg_t):
+    """h(h(W x) + residual) in the GEMV epilogue (emitLinearResidual) against
+    tmc_gemv_f16 with the same configuration followed by tmc_add, and against
+    the oracle; the residual may be the output buffer's neighbour, not the
+    output itself."""
+    cfg = tmc.GemvConfig(*cfg_t) if cfg_t else None
+    for k, n in ((4096, 4096), (11008, 4096), (1160, 200), (64, 9)):
+        x = orc.f16(normal(390, (1, k)))
+        w = orc.f16(normal(391, (n, k), 0.02))
+        res = orc.f16(normal(392, (1, n)))
+        y = torch.full((1, n), float("nan"), dtype=torch.float16, device="cuda")
+        tmc.gemv_residual(dev_f16(x), dev_f16(w), dev_f16(res), y, cfg)
+        proj = torch.empty((1, n), dtype=torch.float16, device="cuda")
+        tmc.gemv_config(dev_f16(x), dev_f16(w), proj, cfg or tmc.default_config(1, k, n))
+        want = torch.empty_like(proj)
+        tmc.add(proj, dev_f16(res), want)
+        torch.cuda.synchronize()
+        what = f"cfg {cfg_t} k{k} n{n}"
+        assert np.array_equal(bits(y), bits(want)), what
+        if cfg_t is None:
+            ref = orc.f16_values(res).astype(np.float64) + orc.store(orc.linear(x, w, F16), F16)
+            assert_f16_path(values(y), ref, what=what)
 
 
 def test_fused_norm_gemv_matches_oracle_and_rejects_batches(tmc, orc, torch):
