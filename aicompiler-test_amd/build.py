@@ -34,7 +34,7 @@ CXXFLAGS = ["-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-param
             f"-I{INCLUDE}", f"-I{HOST}"]
 
 SOURCES = ["runtime.hip", "gemv.hip", "packed.hip", "elementwise.hip", "attention.hip",
-           "prefill.hip"]
+           "prefill.hip", "gemm.hip"]
 # The HIP runtime library of the ROCm install (rpath of the built library).
 ROCM_LIB = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
 

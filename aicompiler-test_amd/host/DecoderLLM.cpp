@@ -528,10 +528,14 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
             {gated_});
         add(residualGemv(I, H), p + "down_residual", {gated_, w.downWeight, after_}, {residual_});
       }
+      // the norm-fused LM head maps its waves to the norm's groups at k split
+      // 4: a tuned dot configuration applies only with that split
       std::string head = "rmsnorm_gemv?in=" + std::to_string(H) + "&out=" + std::to_string(V) +
                          "&out_dtype=f32" + normKey;
       const auto it = tunedSuffix.find(std::to_string(H) + "x" + std::to_string(V));
-      if (it != tunedSuffix.end()) head += it->second;
+      if (it != tunedSuffix.end() && it->second.find("&algorithm=1&") != std::string::npos &&
+          it->second.find("&k_split=4") != std::string::npos)
+        head += it->second;
       add(head, "norm_lm_head", {residual_, model_->finalNormWeight, model_->languageModelHeadWeight},
           {logits_});
     } else {
