@@ -228,18 +228,18 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const half_t* __restrict_
 // A block's 4 waves split K like the dot GEMV at k split 4: wave p holds the
 // 16-byte chunks p*64 + lane + 256*i (i < NC, K <= 2048 * NC), which are also
 // the 64-chunk groups p + 4*i of the norm's reduction.  The block loads its
-// row chunks and gamma once, and the weights of its first two row groups;
+// row chunks and gamma once, and the weights of its first row groups;
 // reduces its norm groups (one wave_sum each) and meets the other waves at
 // one LDS barrier (the weight loads stay in flight); normalizes its chunks
-// once, into registers; then streams its row groups two deep, the loads of
-// group j + 2 issued as group j is consumed.  Weights are read with raw
+// once, into registers; then streams its row groups two or three deep, the
+// loads of group j + depth issued as group j is consumed.  Weights are read with raw
 // buffer loads, a group past the matrix with an out-of-range offset (zeros,
 // no memory traffic), so the stream has no branches.  Per-row partials wait
 // in LDS until the end and are summed in wave order as in the dot GEMV, so
 // results equal the norm kernel followed by tmc_gemv_f16 at k split 4 bit for
 // bit.
 constexpr int kNormMaxChunks = 1024;  // K <= 8192: four chunks per lane
-constexpr int kNormMaxSlots = 34;     // row groups per block (grid >= groups / 32)
+constexpr int kNormMaxSlots = 35;     // row groups per block (grid >= groups / 32), + overshoot
 // Build parameter: blocks of the persistent grid per resident block slot
 // (1 = one wave of blocks; 2 = twice as many, each with half the groups).
 #ifndef TMC_NORM_GRID_FACTOR
@@ -274,6 +274,10 @@ __global__ __launch_bounds__(256) void gemv_norm_kernel(const half_t* __restrict
   static_assert(FUSE == kFuseAddNorm || FUSE == kFuseNorm, "a norm fusion");
   static_assert(!ROPE || (MATS == 1 && RPW == 2), "the RoPE epilogue takes one row pair");
   static_assert(NC == 1 || NC == 2 || NC == 4, "1, 2 or 4 chunks per lane");
+  // row groups in flight per wave, measured on the 7B shapes: 3 for the gated
+  // pair (gate/up 28.2 against 30.5 us at 2), 2 for one matrix (q.k.v 16.4
+  // against 16.9 us at 3)
+  constexpr int kNormDepth = MATS == 2 ? 3 : 2;
   constexpr int kWaves = 4;
   __shared__ float totals[kNormMaxChunks / kWave];
   __shared__ float partial[kWaves][kNormMaxSlots][MATS][RPW];
@@ -319,13 +323,14 @@ __global__ __launch_bounds__(256) void gemv_norm_kernel(const half_t* __restrict
       }
     }
   };
-  h8 wa[NC][MATS][RPW], wb[NC][MATS][RPW];
+  h8 wa[NC][MATS][RPW], wb[NC][MATS][RPW], wc[NC][MATS][RPW];
   int g = (int)blockIdx.x;
   // keep the row loads ahead of the weight loads (loads return in issue
   // order, so the norm then waits for the row only)
   __builtin_amdgcn_sched_barrier(0);
   load_group(wa, g);
   load_group(wb, g + grid);
+  if constexpr (kNormDepth == 3) load_group(wc, g + 2 * grid);
   // norm: group wave + 4i (past the row: zero); block 0 stores the sums
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
@@ -370,11 +375,15 @@ __global__ __launch_bounds__(256) void gemv_norm_kernel(const half_t* __restrict
       }
   };
   int slot = 0;
-  for (; g < groups; g += 2 * grid, slot += 2) {  // block-uniform
+  for (; g < groups; g += kNormDepth * grid, slot += kNormDepth) {  // block-uniform
     consume(wa, slot);
-    load_group(wa, g + 2 * grid);
+    load_group(wa, g + kNormDepth * grid);
     consume(wb, slot + 1);
-    load_group(wb, g + 3 * grid);
+    load_group(wb, g + (kNormDepth + 1) * grid);
+    if constexpr (kNormDepth == 3) {
+      consume(wc, slot + 2);
+      load_group(wc, g + 5 * grid);
+    }
   }
   __syncthreads();
   // the block's rows: (slot, row of the group) pairs, wave 0
@@ -717,8 +726,7 @@ int launch_norm_gemv_nc(const Shape& s, OutT* y, const NormArgs& na, const RopeA
   // streams the same number of groups (a block with one extra group would
   // run alone at the end)
   const int groups = (s.n + RPW - 1) / RPW;
-  const int per_block = std::min((groups + resident[device] - 1) / resident[device],
-                                 kNormMaxSlots - 2);
+  const int per_block = std::min((groups + resident[device] - 1) / resident[device], 32);
   const int grid = (groups + per_block - 1) / per_block;
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, st, s.w0, s.w1, y, s.n, s.k, na, ra);
   return check_launch("gemv_norm_kernel");
