@@ -25,8 +25,8 @@ Example (MI355X, repo root):
   rocprofv3 --pmc FETCH_SIZE -d out/f -o run -- python3 bench.py --no-extra --no-cpu
   rocprofv3 --pmc WRITE_SIZE -d out/w -o run -- python3 bench.py --no-extra --no-cpu
   python3 aicompiler-test_amd/profiling.py traffic --fetch out/f/run_results.db \\
-      --write out/w/run_results.db --kernel gemv_dot_kernel --template Li2ELi1ELi1ELi2ELi4E \\
-      --copy-bytes 268435456 --algorithmic 180385280 --out profiles/gate_up_traffic.json
+      --write out/w/run_results.db --kernel gemv_norm_kernel --template Li2ELi1ELi2EDF16_Li1E \\
+      --copy-bytes 268435456 --algorithmic 180409856 --out profiles/norm_gate_up_traffic.json
 """
 from __future__ import annotations
 
@@ -264,6 +264,8 @@ def main(argv=None) -> int:
     t.add_argument("--copy-bytes", type=int, required=True)
     t.add_argument("--algorithmic", type=int)
     t.add_argument("--command", default="")
+    t.add_argument("--workload", default="")
+    t.add_argument("--batch", type=int, default=1)
     t.add_argument("--out")
     b = sub.add_parser("table")
     b.add_argument("--fetch", required=True)
@@ -313,6 +315,7 @@ def main(argv=None) -> int:
         sys.stdout.write(kernel_summary(a.db, a.title, a.command))
         return 0
     result = traffic(a.fetch, a.write, a.kernel, a.template, a.copy_bytes, a.algorithmic)
+    result = {"workload": a.workload, "batch": a.batch, **result} if a.workload else result
     if a.command:
         result["command"] = a.command
     text = json.dumps(result, indent=2) + "\n"

@@ -3,13 +3,16 @@
 Headline workload: the fused Llama decode MLP
 block at batch 1 — Add+RMSNorm (hidden 4096), gate/up projection with
 SiLU*Mul (intermediate 11008), down projection with fp32 output — with fp16
-weights ~N(0, 0.02).  One step = one pass of the block over one batch.
+weights ~N(0, 0.02).  One step = one pass of the block over one batch.  At
+batch 1 the block runs as the decoder's batch-1 step runs it: two launches,
+the gate/up kernel computing the Add+RMSNorm in its prologue, then down.
 `value` is the algorithmic HBM bytes of the block per step x steps / wall
 time (GB/s), with every input already resident in HBM.  Weights rotate over
 several distinct copies so that the 256 MB Infinity Cache cannot serve them.
 
 Printed JSON line extras:
-  roofline      the dominant kernel (gate/up + SiLU*Mul) timed alone with HIP
+  roofline      the dominant kernel (Add+RMSNorm + gate/up + SiLU*Mul at batch
+                1, gate/up + SiLU*Mul above) timed alone with HIP
                 events on the launch stream: algorithmic bytes per launch /
                 average launch time, against the 8 TB/s HBM peak;
   cpu_baseline  the CPU oracle (oracle/libtmc_oracle.so, a single-threaded
@@ -42,7 +45,7 @@ COPY_PROBE_BYTES = 256 << 20
 ROTATE_BYTES = 512 << 20
 # HBM bytes per launch of the dominant kernel, measured with rocprofv3
 # FETCH_SIZE / WRITE_SIZE and scaled by the copy probe (profiling.py traffic)
-TRAFFIC_FILE = "profiles/gate_up_traffic.json"
+TRAFFIC_FILE = "profiles/norm_gate_up_traffic.json"
 METRIC = "GEMV/paged-attn HBM GB/s (% of peak); decode tokens/s at batch 1 and 16"
 HIDDEN, INTER = 4096, 11008
 
@@ -62,13 +65,19 @@ def load_tmc():
 
 
 def mlp_block_bytes(batch: int) -> dict:
-    """Algorithmic bytes of each kernel of the block (fp16 = 2 B, fp32 = 4 B)."""
+    """Algorithmic bytes of each kernel of the block (fp16 = 2 B, fp32 = 4 B):
+    Add+RMSNorm, gate/up + SiLU*Mul and down as three kernels (batch > 1 and
+    the CPU oracle), and the batch-1 form whose gate/up kernel computes the
+    Add+RMSNorm itself (`norm_gate_up`: the normalized row is neither written
+    nor read back)."""
     h, i = HIDDEN, INTER
     add_norm = batch * h * 2 * 4 + h * 2          # read h, r; write s, n; gamma
     gate_up = 2 * i * h * 2 + batch * h * 2 + batch * i * 2
     down = i * h * 2 + batch * i * 2 + batch * h * 4
+    norm_gate_up = 2 * i * h * 2 + batch * h * 2 * 3 + h * 2 + batch * i * 2  # h, r, s; gamma
     return {"add_rmsnorm": add_norm, "gate_up_silu": gate_up, "down": down,
-            "total": add_norm + gate_up + down}
+            "total": add_norm + gate_up + down, "norm_gate_up": norm_gate_up,
+            "fused_total": norm_gate_up + down}
 
 
 def measured_traffic(batch: int):
@@ -133,16 +142,26 @@ class MlpBlock:
 
 def build_sequences(tmc, rt, block):
     """Prepared executions of the block for every weight copy, captured as one
-    HIP-graph sequence, plus a sequence of the gate/up kernel alone."""
+    HIP-graph sequence, plus a sequence of the gate/up kernel alone.  Batch 1
+    runs the decoder's batch-1 form: gate/up + SiLU*Mul with the Add+RMSNorm
+    in its prologue (the sum written, the normalized row kept in registers),
+    then down; above batch 1 the norm is its own kernel."""
     b = block.batch
-    # 512 threads per row: the decoder's batch-1 norm configuration
-    threads = "&threads=512" if b == 1 else ""
-    k_norm = rt.resolve(f"add_rmsnorm?rows={b}&width={HIDDEN}&eps=1e-06&dtype=f16{threads}")
-    k_gate = rt.resolve(f"gate_up_silu?batch={b}&hidden={HIDDEN}&inter={INTER}")
     k_down = rt.resolve(f"decode_gemv?batch={b}&in={INTER}&out={HIDDEN}&out_dtype=f32")
     h, r, s, n = rt.wrap(block.h), rt.wrap(block.r), rt.wrap(block.s), rt.wrap(block.n)
     g, y = rt.wrap(block.g), rt.wrap(block.y)
     execs, gates = [], []
+    if b == 1:
+        k_fused = rt.resolve(f"add_rmsnorm_gate_up_silu?in={HIDDEN}&out={INTER}&eps=1e-06")
+        for gamma, wg, wu, wd in block.weights:
+            gm, wgb, wub, wdb = rt.wrap(gamma), rt.wrap(wg), rt.wrap(wu), rt.wrap(wd)
+            gate = rt.prepare(k_fused, [h, r, gm, wgb, wub], [s, g])
+            execs.append(gate)
+            gates.append(gate)
+            execs.append(rt.prepare(k_down, [g, wdb], [y]))
+        return rt.sequence(execs), execs, rt.sequence(gates)
+    k_norm = rt.resolve(f"add_rmsnorm?rows={b}&width={HIDDEN}&eps=1e-06&dtype=f16")
+    k_gate = rt.resolve(f"gate_up_silu?batch={b}&hidden={HIDDEN}&inter={INTER}")
     for gamma, wg, wu, wd in block.weights:
         gm, wgb, wub, wdb = rt.wrap(gamma), rt.wrap(wg), rt.wrap(wu), rt.wrap(wd)
         execs.append(rt.prepare(k_norm, [h, r, gm], [s, n]))
@@ -594,7 +613,10 @@ def main() -> int:
     rs.synchronize()
     elapsed = time.perf_counter() - t0
     bytes_ = mlp_block_bytes(args.batch)
-    value = bytes_["total"] * steps / elapsed / 1e9
+    fused = args.batch == 1
+    block_bytes = bytes_["fused_total"] if fused else bytes_["total"]
+    gate_bytes = bytes_["norm_gate_up"] if fused else bytes_["gate_up_silu"]
+    value = block_bytes * steps / elapsed / 1e9
     print(f"[bench] timed {steps} steps in {elapsed:.4f} s", flush=True)
 
     copy_probe(tmc, torch)
@@ -610,17 +632,18 @@ def main() -> int:
     stop.record(rs)
     stop.synchronize()
     sec = start.elapsed_time(stop) / 1000.0 / (gate_replays * args.copies)
-    achieved = bytes_["gate_up_silu"] / sec / 1e9
+    achieved = gate_bytes / sec / 1e9
     measured = measured_traffic(args.batch)
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                 "traffic": measured["traffic_bytes_per_launch"] if measured else None,
-                "kernel": "gemv_dot_kernel<2,1,1,2,4> (gate/up + SiLU*Mul)",
-                "bytes_per_launch": bytes_["gate_up_silu"], "avg_launch_us": round(sec * 1e6, 3)}
+                "kernel": ("gemv_norm_kernel<2,1,2> (Add+RMSNorm + gate/up + SiLU*Mul)" if fused
+                           else "gemv_dot_kernel (gate/up + SiLU*Mul)"),
+                "bytes_per_launch": gate_bytes, "avg_launch_us": round(sec * 1e6, 3)}
     if measured:
         roofline["traffic_source"] = TRAFFIC_FILE
         roofline["traffic_over_algorithmic"] = measured.get("traffic_over_algorithmic")
-    print(f"[bench] gate_up_silu {sec * 1e6:.2f} us/launch", flush=True)
+    print(f"[bench] {'norm + ' if fused else ''}gate_up_silu {sec * 1e6:.2f} us/launch", flush=True)
     del execs
     steps_reported = steps
     extra = {} if args.no_extra else extra_measurements(tmc, torch, 40)
@@ -640,7 +663,7 @@ def main() -> int:
         "config": {"workload": "C2 fused decode MLP block: Add+RMSNorm -> gate/up+SiLU*Mul -> "
                                "down (fp32 out); hidden 4096, intermediate 11008",
                    "batch": args.batch, "weight_copies": args.copies, "accumulate": "f32",
-                   "bytes_per_step": bytes_["total"], "frac_of_hbm_peak":
+                   "bytes_per_step": block_bytes, "frac_of_hbm_peak":
                        round(value / HBM_PEAK_GBPS, 4)},
         "roofline": roofline, "cpu_baseline": cpu, "extra": extra,
     }
