@@ -95,6 +95,9 @@ def _declare(l):
         "tmc_paged_decode_attention_noalloc": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i64, i64,
                                                      i64, i64, i64, i64, i64, i64, i64, vp]),
         "tmc_attention_scratch_bytes": (sz, []),
+        "tmc_attention_output_workspace_bytes": (sz, [i64, i64, i64]),
+        "tmc_paged_attention_output_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64,
+                                                 i64, i64, i64, i64, i64, i64, i64, vp, sz, vp]),
         "tmc_paged_gather_probe": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, i64,
                                          vp, vp]),
         "tmc_argmax_f32": (i32, [vp, vp, i64, i64, vp]),
@@ -607,6 +610,26 @@ def paged_decode_attention(q, k_pool, v_pool, valid_lengths, tables, active, out
         _ptr(out), _dtype_code(q), max_batch, q_heads, kv_heads, head_dim, page_size, max_pages,
         pool_pages, page_stride, head_stride, _ptr(workspace), ws_bytes, _stream(stream)),
         "tmc_paged_decode_attention")
+
+
+def attention_output_workspace_bytes(q_heads, kv_heads, out_features):
+    return lib().tmc_attention_output_workspace_bytes(q_heads, kv_heads, out_features)
+
+
+def paged_attention_output(q, k_pool, v_pool, valid_lengths, tables, active, weight, residual,
+                           y, q_heads, kv_heads, head_dim, page_size, max_pages, page_stride,
+                           head_stride, workspace, stream=None, pool_pages=None):
+    """Batch-1 paged attention + output projection (+ residual unless None).
+    `workspace` must be zero before its first use (the kernel leaves its
+    arrival counters at zero after every call)."""
+    if pool_pages is None:
+        pool_pages = min(k_pool.numel(), v_pool.numel()) // page_stride
+    ws_bytes = workspace.numel() * workspace.element_size()
+    check(lib().tmc_paged_attention_output_f16(
+        _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(valid_lengths), _ptr(tables), _ptr(active),
+        _ptr(weight), _ptr(residual), _ptr(y), q_heads, kv_heads, head_dim, page_size, max_pages,
+        pool_pages, page_stride, head_stride, weight.shape[0], _ptr(workspace), ws_bytes,
+        _stream(stream)), "tmc_paged_attention_output_f16")
 
 
 def argmax(logits, tokens, stream=None):

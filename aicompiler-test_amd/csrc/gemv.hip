@@ -257,14 +257,6 @@ __device__ __forceinline__ h8 norm_source(const NormArgs& na, int c) {
   return a;
 }
 
-// Workgroup barrier ordering LDS only (__syncthreads() also waits for every
-// outstanding global load, i.e. for the weight stream).
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 
 template <int MATS, int RPW, int NC, typename OutT, int FUSE, bool ROPE = false>
 __global__ __launch_bounds__(256) void gemv_norm_kernel(const half_t* __restrict__ w0,

@@ -806,6 +806,41 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     };
     return true;
   }
+  if (name == "paged_attention_output") {
+    // Batch-1 paged attention + output projection (+ residual when
+    // residual=1): inputs q, key pool, value pool, lengths, block table,
+    // active count, W [out, q_heads*head_dim] (, residual [out]); output y.
+    const int64_t qh = param_int(p, "q_heads"), kvh = param_int(p, "kv_heads", qh),
+                  d = param_int(p, "head_dim"), ps = param_int(p, "page_size"),
+                  mp = param_int(p, "max_pages"), n = param_int(p, "out");
+    const bool res = param_int(p, "residual", 0) != 0;
+    NEED(qh > 0 && kvh > 0 && d > 0 && ps > 0 && mp > 0 && n > 0 && dt == TMC_F16,
+         "paged_attention_output needs q_heads, head_dim, page_size, max_pages, out and "
+         "dtype=f16.");
+    const int64_t head_stride = param_int(p, "head_stride", ps * d);
+    const int64_t page_stride = param_int(p, "page_stride", kvh * ps * d);
+    s.inputs = {dt, dt, dt, TMC_I32, TMC_I32, TMC_I32, dt};
+    s.counts = {(size_t)(qh * d), 0, 0, 1, (size_t)mp, 1, (size_t)(n * qh * d)};
+    if (res) {
+      s.inputs.push_back(dt);
+      s.counts.push_back((size_t)n);
+    }
+    s.outputs = {dt};
+    s.counts.push_back((size_t)n);
+    s.workspace_bytes = tmc_attention_output_workspace_bytes(qh, kvh, n);
+    NEED(s.workspace_bytes > 0,
+         "paged_attention_output: unsupported head grouping or output width.");
+    s.launch = [=](const LaunchContext& c) {
+      const int64_t pool_pages =
+          (int64_t)(std::min(c.counts[1], c.counts[2]) / (size_t)page_stride);
+      return tmc_paged_attention_output_f16(
+          c.ptrs[0], c.ptrs[1], c.ptrs[2], static_cast<const int32_t*>(c.ptrs[3]),
+          static_cast<const int32_t*>(c.ptrs[4]), static_cast<const int32_t*>(c.ptrs[5]),
+          c.ptrs[6], res ? c.ptrs[7] : nullptr, c.ptrs[res ? 8 : 7], qh, kvh, d, ps, mp,
+          pool_pages, page_stride, head_stride, n, c.workspace, c.workspace_bytes, c.stream);
+    };
+    return true;
+  }
   if (name == "gemm_rows") {
     // Prompt GEMM y[m, out] = x[m, in] w[out, in]^T; workspace=1 binds a
     // trailing int32 scratch input of tmc_gemm_rows_workspace_bytes().

@@ -105,6 +105,14 @@ template <int FROM> __device__ __forceinline__ float cross_max(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Workgroup barrier ordering LDS only (__syncthreads() also waits for every
+// outstanding global load, e.g. for a weight stream still in flight).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Raw buffer loads: an offset at or past the resource's byte count reads as
 // zero, so an absent element needs a select, not a branch.
 constexpr unsigned kBufferAbsent = 0xFFFFFFF0u;

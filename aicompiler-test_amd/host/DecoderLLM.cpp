@@ -468,6 +468,23 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
     const std::size_t normThreads = H >= 4096 ? 512 : 256;
     const bool fold = foldNorms_ && !packed && fuseRope && generatedNorm.empty() &&
                       generatedAddNorm.empty() && H % 8 == 0 && H / 8 <= normThreads;
+    // Paged attention + o projection + residual as one launch (opt-in; the
+    // kernel's limits: head_dim 128, GQA group 1 or 2, pages of a multiple
+    // of 16 positions, capacity <= 1024, pools below 4 GiB, an output width
+    // its row slices divide).
+    const std::string attentionOutputKey =
+        "paged_attention_output?q_heads=" + std::to_string(QH) + "&kv_heads=" +
+        std::to_string(KVH) + "&head_dim=" + std::to_string(D) + "&page_size=" +
+        std::to_string(pageSize_) + "&max_pages=" + std::to_string(maxPages_) +
+        "&out=" + std::to_string(H) + "&residual=1";
+    bool fuseAttention = fold && fuseAttentionOutput_ && D == 128 && KVH > 0 && QH % KVH == 0 &&
+                         QH / KVH <= 2 && pageSize_ % 16 == 0 && pageSize_ * maxPages_ <= 1024;
+    for (std::size_t l = 0; fuseAttention && l < L; ++l)
+      fuseAttention = pools_[l]->keyBuffer()->elementCount() * 2 < (std::size_t(1) << 32) - 16 &&
+                      pools_[l]->valueBuffer()->elementCount() * 2 < (std::size_t(1) << 32) - 16;
+    if (fuseAttention)
+      fuseAttention = rt.createComputePipeline(attentionOutputKey, "attention_output_probe")
+                          .pipelineCreationPassed;
     if (registry_) {
       const auto track = [&](const char* node, const char* pattern, const std::string& tuning,
                              const std::string& key, std::size_t launches) {
@@ -479,6 +496,10 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
             fold ? "rmsnorm_qkv_rope_append" : "rmsnorm?" + firstNorm, 1);
       track("residual norms", "decoder_residual_rmsnorm", generatedAddNorm,
             fold ? "gemv_residual + rmsnorm_* prologues" : "add_rmsnorm?" + norm, 2 * L);
+      if (fuseAttention)
+        bucket->uses.push_back(registry_->track({"bucket " + B + " attention output",
+                                                 "paged_attention_output_projection", "template",
+                                                 attentionOutputKey, L, 0}));
     }
     add("embedding?rows=" + B + "&hidden=" + std::to_string(H) + "&vocab=" + std::to_string(V),
         "embedding", {tokensView_, model_->embeddingWeight}, {residual_});
@@ -518,11 +539,19 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
             {residual_, w.inputNormWeight, w.queryKeyValueWeight, model_->ropeCosine,
              model_->ropeSine, lengthsView_, tableViews_[l], activeView_},
             {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer()});
-        add(attentionKey, p + "attention",
-            {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer(), lengthsView_,
-             tableViews_[l], activeView_},
-            {context_});
-        add(residualGemv(H, H), p + "o_residual", {context_, w.outputWeight, residual_}, {after_});
+        if (fuseAttention) {
+          add(attentionOutputKey, p + "attention_output",
+              {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer(), lengthsView_,
+               tableViews_[l], activeView_, w.outputWeight, residual_},
+              {after_});
+        } else {
+          add(attentionKey, p + "attention",
+              {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer(), lengthsView_,
+               tableViews_[l], activeView_},
+              {context_});
+          add(residualGemv(H, H), p + "o_residual", {context_, w.outputWeight, residual_},
+              {after_});
+        }
         add("rmsnorm_gate_up_silu?in=" + std::to_string(H) + "&out=" + std::to_string(I) + normKey,
             p + "norm_gate_up_silu", {after_, w.postAttentionNormWeight, w.gateWeight, w.upWeight},
             {gated_});
@@ -595,7 +624,7 @@ BatchedDecodeExecutor::Creation createBatchedDecodeExecutor(
     hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
     std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t maximumBatchSize,
     std::ostream* log, bool tuneKernels, std::shared_ptr<KernelRegistry> registry,
-    bool foldNorms) {
+    bool foldNorms, bool fuseAttentionOutput) {
   BatchedDecodeExecutor::Creation result;
   try {
     if (!model) throw std::invalid_argument("Batched decode needs model resources.");
@@ -619,6 +648,7 @@ BatchedDecodeExecutor::Creation createBatchedDecodeExecutor(
     executor->pageSize_ = executor->pools_.front()->pageSize();
     executor->tuneKernels_ = tuneKernels;
     executor->foldNorms_ = foldNorms;
+    executor->fuseAttentionOutput_ = fuseAttentionOutput;
     executor->registry_ = std::move(registry);
     executor->build(log);
     result.executor = std::move(executor);

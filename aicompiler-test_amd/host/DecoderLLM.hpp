@@ -229,7 +229,7 @@ class BatchedDecodeExecutor {
                                               std::shared_ptr<DecoderLLMModelResources>,
                                               std::vector<std::shared_ptr<KVPagePool>>,
                                               std::size_t, std::ostream*, bool,
-                                              std::shared_ptr<KernelRegistry>, bool);
+                                              std::shared_ptr<KernelRegistry>, bool, bool);
   BatchedDecodeExecutor() = default;
   void build(std::ostream* log);
   [[nodiscard]] std::string upload(const std::vector<std::int32_t>& tokens,
@@ -249,6 +249,7 @@ class BatchedDecodeExecutor {
   std::size_t maxPages_ = 0;
   bool tuneKernels_ = false;
   bool foldNorms_ = true;
+  bool fuseAttentionOutput_ = false;
   std::shared_ptr<KernelRegistry> registry_;  // admitted region kernels, may be null
   std::size_t activationBytes_ = 0;
   // Device buffers sized for maximumBatchSize rows.
@@ -283,11 +284,19 @@ struct BatchedDecodeExecutor::Creation {
 // of the norm kernel the bucket would otherwise run, so results are the same
 // bit for bit.  Applies when that norm holds one 16-byte chunk per thread
 // (hidden <= 2048, or 4096) and no admitted region kernel replaces the norms.
+// fuseAttentionOutput: in that folded one-row bucket, each layer's paged
+// attention and o projection + residual run as one launch
+// (paged_attention_output, the fusion candidate of
+// DecoderLLMExecutor.cpp:648-713) where its limits hold (head_dim 128, GQA
+// group 1 or 2, pages of a multiple of 16 positions, capacity <= 1024).  Off
+// by default: on MI355X it measured slower than the two launches at every
+// context length (the reference admits the fusion only when it times faster).
 [[nodiscard]] BatchedDecodeExecutor::Creation createBatchedDecodeExecutor(
     hip::HipRuntime& runtime, std::shared_ptr<DecoderLLMModelResources> model,
     std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t maximumBatchSize,
     std::ostream* log = nullptr, bool tuneKernels = false,
-    std::shared_ptr<KernelRegistry> registry = nullptr, bool foldNorms = true);
+    std::shared_ptr<KernelRegistry> registry = nullptr, bool foldNorms = true,
+    bool fuseAttentionOutput = false);
 
 // Chunked prefill (prefillChunked, DecoderLLMExecutor.cpp:982-1034): the
 // tokens of one request's prompt chunk are the rows of one stage.  Linear

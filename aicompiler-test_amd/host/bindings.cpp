@@ -438,15 +438,17 @@ PYBIND11_MODULE(_tmc_host, m) {
   m.def("create_batched_decode_executor",
         [](hip::HipRuntime& rt, std::shared_ptr<DecoderLLMModelResources> model,
            std::vector<std::shared_ptr<KVPagePool>> pools, std::size_t maxBatch, bool tune,
-           bool foldNorms) {
+           bool foldNorms, bool fuseAttentionOutput) {
           std::ostringstream log;
           auto r = createBatchedDecodeExecutor(rt, std::move(model), std::move(pools), maxBatch,
-                                               &log, tune, nullptr, foldNorms);
+                                               &log, tune, nullptr, foldNorms,
+                                               fuseAttentionOutput);
           if (!r.executor) throw std::runtime_error(r.errorMessage + "\n" + log.str());
           return std::move(r.executor);
         },
         py::arg("runtime"), py::arg("model"), py::arg("pools"), py::arg("maximum_batch_size"),
-        py::arg("tune_kernels") = false, py::arg("fold_norms") = true);
+        py::arg("tune_kernels") = false, py::arg("fold_norms") = true,
+        py::arg("fuse_attention_output") = false);
   py::class_<ChunkedPrefillExecutor>(m, "ChunkedPrefillExecutor")
       .def("run",
            [](ChunkedPrefillExecutor& e, const std::vector<std::int32_t>& tokens, std::size_t start,

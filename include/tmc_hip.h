@@ -473,6 +473,38 @@ int tmc_paged_decode_attention_noalloc(const void *q, const void *key_pool,
 /* Bytes of the static scratch behind tmc_paged_decode_attention_noalloc. */
 size_t tmc_attention_scratch_bytes(void);
 
+/* Paged attention + output projection for one decode token (batch 1), the
+ * fusion candidate emitPagedAttentionOutputProjection
+ * (DecoderLLMMetalEmitter.cpp:623-698, queryLength 1) with the residual add
+ * of emitLinearResidual (:604-621):
+ *   context = paged attention of request 0 (as tmc_paged_decode_attention,
+ *             rounded to fp16 as that kernel stores it),
+ *   y[n]    = fp16(fp16(sum_k weight[n, k] * context[k]) + residual[n]),
+ * or y[n] = fp16(sum) when residual is NULL.  weight is
+ * [out_features, q_heads*128] row-major fp16.  Limits: head_dim 128,
+ * q_heads / kv_heads 1 or 2, pages of a multiple of 16 positions,
+ * page_size * max_pages <= 1024, pool_pages > 0 with each pool below 4 GiB,
+ * out_features a multiple of 128 (64 when q_heads = 2 * kv_heads).  An
+ * inactive request (active_count[0] < 1), an invalid length or a missing page
+ * leaves y untouched.  The sum over k is taken per kv head and the kv heads'
+ * sums are added in head order: the result is deterministic.
+ * workspace: tmc_attention_output_workspace_bytes() bytes, zeroed once
+ * before the first call; it starts with per-slice arrival counters, which
+ * every call leaves at zero again.  Calls that share a workspace must not
+ * overlap.  Measured slower than tmc_paged_decode_attention followed by
+ * tmc_gemv_residual_f16 on MI355X (14.6 against 13.1 us at Llama-7B widths,
+ * 132 positions), so the decoder keeps the two launches by default. */
+size_t tmc_attention_output_workspace_bytes(int64_t q_heads, int64_t kv_heads,
+                                            int64_t out_features);
+int tmc_paged_attention_output_f16(const void *q, const void *key_pool, const void *value_pool,
+                                   const int32_t *valid_lengths, const int32_t *block_tables,
+                                   const int32_t *active_count, const void *weight,
+                                   const void *residual, void *y, int64_t q_heads,
+                                   int64_t kv_heads, int64_t head_dim, int64_t page_size,
+                                   int64_t max_pages, int64_t pool_pages, int64_t page_stride,
+                                   int64_t head_stride, int64_t out_features, void *workspace,
+                                   size_t workspace_bytes, void *stream);
+
 /* Bandwidth probe of the paged attention access pattern (head_dim 128, pages
  * of a multiple of 16 positions): reads
  * the K and V bytes tmc_paged_decode_attention would read for these lengths

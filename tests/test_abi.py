@@ -99,6 +99,39 @@ def test_argument_validation_fails_before_device_work(tmc):
     assert "different runtimes" in tmc.last_error()
 
 
+def test_attention_output_fusion_limits(tmc):
+    """tmc_paged_attention_output_f16 refuses what its one-launch form cannot
+    hold, before any device work: (q, k, v, lengths, tables, active, W,
+    residual, y, q_heads, kv_heads, head_dim, page, max_pages, pool_pages,
+    page_stride, head_stride, out, workspace, bytes, stream)."""
+    lib = tmc.lib()
+    p = C.c_void_p(256)
+    ws = tmc.attention_output_workspace_bytes(32, 32, 4096)
+    # arrival counters (8 slices of 512 rows, padded to 256 bytes) + the
+    # kv heads' fp32 partial sums [32][4096]
+    assert ws == 256 + 32 * 4096 * 4
+    assert tmc.attention_output_workspace_bytes(8, 4, 512) == 256 + 4 * 512 * 4
+    assert tmc.attention_output_workspace_bytes(32, 8, 4096) == 0  # group 4
+    assert tmc.attention_output_workspace_bytes(4, 4, 100) == 0  # no slice height divides 100
+
+    def call(q_heads=32, kv_heads=32, head_dim=128, page=16, max_pages=64, pool_pages=96,
+             out=4096, workspace=p, nbytes=ws, weight=p):
+        page_stride = kv_heads * page * head_dim
+        return lib.tmc_paged_attention_output_f16(
+            p, p, p, p, p, None, weight, None, p, q_heads, kv_heads, head_dim, page, max_pages,
+            pool_pages, page_stride, page * head_dim, out, workspace, nbytes, None)
+
+    assert call(weight=None) != 0 and "null" in tmc.last_error()
+    assert call(head_dim=64) != 0 and "head_dim must be 128" in tmc.last_error()
+    assert call(kv_heads=8) != 0 and "1 or 2" in tmc.last_error()
+    assert call(page=8, max_pages=128) != 0 and "multiple of 16" in tmc.last_error()
+    assert call(max_pages=65) != 0 and "at most 1024" in tmc.last_error()
+    assert call(pool_pages=0) != 0 and "known number of pages" in tmc.last_error()
+    assert call(out=100) != 0 and "multiple of 128" in tmc.last_error()
+    assert call(nbytes=ws - 4) != 0 and "workspace" in tmc.last_error()
+    assert call(workspace=None) != 0 and "workspace" in tmc.last_error()
+
+
 def test_attention_workspace_sizes(tmc):
     # VALU kernel (D=64): one split of 256 positions needs no workspace,
     # otherwise batch x q_heads x splits x (D + 2) floats

@@ -286,3 +286,38 @@ def test_7b_batch1_folded_norms_equal_norm_kernels(host, orc, rt7b, models7b):
     for i, (a, b) in enumerate(zip(runs[True][1], runs[False][1])):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"step {i}"
     assert runs[True][2] == runs[False][2]
+
+
+def test_7b_batch1_attention_output_fusion_matches_two_launches(host, orc, rt7b, models7b):
+    """The folded one-row bucket with each layer's paged attention and o
+    projection + residual in one launch (fuse_attention_output; the fusion
+    candidate of DecoderLLMExecutor.cpp:648-713) against the same bucket with
+    the two launches: one dispatch fewer per layer, logits within the fp16
+    path tolerance and the same greedy tokens (up to near-ties) over 40 steps
+    that cross pages.  The fused kernel sums the o projection per kv head,
+    so the two differ by rounding only."""
+    model, plan = models7b(1024)
+    runs = {}
+    for fused in (True, False):
+        pools = [host.create_kv_page_pool(rt7b, plan.kv_plan(), P, 1024 // P)
+                 for _ in range(SHAPE["layers"])]
+        ex = host.create_batched_decode_executor(rt7b, model, pools, 1,
+                                                 fuse_attention_output=fused)
+        states = [host.create_kv_cache_state(rt7b, plan.kv_plan(), pool, False) for pool in pools]
+        rng = np.random.default_rng(5102)
+        logits, tokens = [], []
+        for i in range(40):
+            for s in states:
+                assert s.stage_length(rt7b, i + 1) == ""
+                s.commit_length(i + 1)
+            tables = [s.page_table() + [-1] * (ex.max_pages() - len(s.page_table())) for s in states]
+            out = ex.run([int(rng.integers(0, SHAPE["vocabulary"]))], [i + 1], tables, True, False)
+            assert out["passed"], out["error"]
+            logits.append(np.asarray(out["logits"], np.float32))
+            tokens.append(int(out["next_token_ids"][0]))
+        runs[fused] = (ex.dispatches_per_step(1), logits, tokens)
+        del ex, states, pools
+    assert runs[False][0] - runs[True][0] == SHAPE["layers"]
+    for i, (a, b) in enumerate(zip(runs[True][1], runs[False][1])):
+        assert_f16_path(a, b.astype(np.float64), f"step {i}")
+        _check_token(runs[True][2][i], runs[False][2][i], b, f"step {i}")
