@@ -95,6 +95,14 @@ def _declare(l):
         "tmc_paged_decode_attention_noalloc": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i64, i64,
                                                      i64, i64, i64, i64, i64, i64, i64, vp]),
         "tmc_attention_scratch_bytes": (sz, []),
+        "tmc_gemm_packed_norm_f16": (i32, [vp, vp, vp, i32, i64, i64, i64, f, i32, vp, vp]),
+        "tmc_gate_up_silu_packed_norm_f16": (i32, [vp, vp, vp, vp, i64, i64, i64, f, i32, vp,
+                                                   vp]),
+        "tmc_rmsnorm_qkv_rope_append_packed_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
+                                                         i64, i64, i64, i64, i64, i64, i64, i64,
+                                                         f, i32, vp, vp]),
+        "tmc_pack_weights_scaled_f16": (i32, [vp, vp, vp, i64, i64, vp]),
+        "tmc_gemm_packed_residual_f16": (i32, [vp, vp, vp, vp, i64, i64, i64, i32, vp, vp]),
         "tmc_attention_output_workspace_bytes": (sz, [i64, i64, i64]),
         "tmc_paged_attention_output_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64,
                                                  i64, i64, i64, i64, i64, i64, i64, vp, sz, vp]),
@@ -325,18 +333,63 @@ def gate_up_silu_packed_ex(x, packed_gate, packed_up, out, batch, hidden, interm
                                                _stream(stream)), "tmc_gate_up_silu_packed_ex_f16")
 
 
+def _cfg_ref(cfg):
+    if cfg is None:
+        return None
+    return C.byref(GemvConfig(*cfg) if isinstance(cfg, tuple) else cfg)
+
+
+def gemm_packed_norm(x, packed_scaled, y, batch, in_features, out_features, eps, layout,
+                     cfg=None, stream=None):
+    """Packed GEMM of RMSNorm(x) * gamma with the norm folded in; the weights
+    come from pack_weights(w, gamma=...) (tmc_gemm_packed_norm_f16)."""
+    check(lib().tmc_gemm_packed_norm_f16(_ptr(x), _ptr(packed_scaled), _ptr(y), _dtype_code(y),
+                                         batch, in_features, out_features, eps, layout,
+                                         _cfg_ref(cfg), _stream(stream)),
+          "tmc_gemm_packed_norm_f16")
+
+
+def gate_up_silu_packed_norm(x, packed_gate, packed_up, out, batch, hidden, intermediate, eps,
+                             layout, cfg=None, stream=None):
+    check(lib().tmc_gate_up_silu_packed_norm_f16(_ptr(x), _ptr(packed_gate), _ptr(packed_up),
+                                                 _ptr(out), batch, hidden, intermediate, eps,
+                                                 layout, _cfg_ref(cfg), _stream(stream)),
+          "tmc_gate_up_silu_packed_norm_f16")
+
+
+def rmsnorm_qkv_rope_append_packed(x, packed_scaled, cos, sin, valid_lengths, tables, active,
+                                   q_out, k_pool, v_pool, batch, hidden, q_heads, kv_heads,
+                                   head_dim, capacity, page_size, max_pages, eps, layout=0,
+                                   config=None, stream=None):
+    check(lib().tmc_rmsnorm_qkv_rope_append_packed_f16(
+        _ptr(x), _ptr(packed_scaled), _ptr(cos), _ptr(sin), _ptr(valid_lengths), _ptr(tables),
+        _ptr(active), _ptr(q_out), _ptr(k_pool), _ptr(v_pool), batch, hidden, q_heads, kv_heads,
+        head_dim, capacity, page_size, max_pages, eps, layout, _cfg_ref(config),
+        _stream(stream)), "tmc_rmsnorm_qkv_rope_append_packed_f16")
+
+
+def gemm_packed_residual(x, packed, residual, y, batch, in_features, out_features, layout,
+                         cfg=None, stream=None):
+    """y = fp16(fp16(x W^T) + residual) over packed W (tmc_gemm_packed_residual_f16)."""
+    check(lib().tmc_gemm_packed_residual_f16(_ptr(x), _ptr(packed), _ptr(residual), _ptr(y),
+                                             batch, in_features, out_features, layout,
+                                             _cfg_ref(cfg), _stream(stream)),
+          "tmc_gemm_packed_residual_f16")
+
+
 def packed_weight_elements(out_features, in_features) -> int:
     return int(lib().tmc_packed_weight_elements(out_features, in_features))
 
 
-def pack_weights(w, packed=None, stream=None):
-    """Fragment-packed copy of fp16 W [out, in] (tmc_pack_weights_f16)."""
+def pack_weights(w, packed=None, stream=None, gamma=None):
+    """Fragment-packed copy of fp16 W [out, in] (tmc_pack_weights_f16); with
+    gamma, of W . diag(gamma) (tmc_pack_weights_scaled_f16)."""
     import torch
     n, k = w.shape
     if packed is None:
         packed = torch.empty(packed_weight_elements(n, k), dtype=torch.float16, device=w.device)
-    check(lib().tmc_pack_weights_f16(_ptr(w), _ptr(packed), n, k, _stream(stream)),
-          "tmc_pack_weights_f16")
+    check(lib().tmc_pack_weights_scaled_f16(_ptr(w), _ptr(gamma), _ptr(packed), n, k,
+                                            _stream(stream)), "tmc_pack_weights_scaled_f16")
     return packed
 
 

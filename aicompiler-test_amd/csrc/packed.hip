@@ -42,8 +42,11 @@ __device__ __forceinline__ half_t gated_value(float gate_sum, float up_sum) {
   return (half_t)(activated * u);
 }
 
-// One thread per packed lane slot (16 bytes).
+// One thread per packed lane slot (16 bytes).  gamma (may be null): the
+// slot holds fp16(W[row, k] * gamma[k]), the weights of a projection with
+// the preceding RMSNorm's gamma folded in.
 __global__ __launch_bounds__(256) void pack_kernel(const half_t* __restrict__ w,
+                                                   const half_t* __restrict__ gamma,
                                                    half_t* __restrict__ packed, int n, int k,
                                                    long slots) {
   const int chunks = (k + 31) / 32;
@@ -57,11 +60,33 @@ __global__ __launch_bounds__(256) void pack_kernel(const half_t* __restrict__ w,
     const int k0 = c * 32 + 8 * (lane >> 4);
     h8 v;
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
+    for (int e = 0; e < 8; ++e) {
       v[e] = (row < n && k0 + e < k) ? w[(size_t)row * k + k0 + e] : (half_t)0.0f;
+      if (gamma && k0 + e < k) v[e] = (half_t)((float)v[e] * (float)gamma[k0 + e]);
+    }
     *reinterpret_cast<h8*>(packed + i * 8) = v;
   }
 }
+
+// Folded neighbours of a packed GEMM (batch > 1 decode, no norm launch):
+//  kPackedNorm: RMSNorm (emitDecoderRMSNorm, DecoderLLMMetalEmitter.cpp:
+//    63-108) folded into the projection, as the reference's fusion candidate
+//    emitDecoderQKVFusion (:538-602) folds it: x is the residual stream s,
+//    the packed weights hold W . diag(gamma) (pack_kernel with gamma), and
+//    each output row r is scaled by 1 / sqrt(sum_k s[r, k]^2 / K + eps), the
+//    squares taken from the activation fragments the MFMA reads.  The fp16
+//    rounding falls on W * gamma rather than on the normalized value.  (A
+//    gamma fragment loaded beside every activation fragment measured 1.9 us
+//    slower on the batch-16 q.k.v projection: activation-side loads are what
+//    these kernels are sensitive to.)
+//  kPackedResidual: y = fp16(fp16(acc) + residual), residual in y's layout
+//    (emitLinearResidual, :604-621).
+enum PackedFuse : int { kPackedPlain = 0, kPackedNorm = 1, kPackedResidual = 2 };
+
+struct PackedFuseArgs {
+  const half_t* residual = nullptr;  // kPackedResidual: this pass, in y's layout
+  float eps = 0.0f;                  // kPackedNorm
+};
 
 // XP: x is one 16-row pass in fragment order (lane l of chunk c holds row
 // l % 16, k 32c + 8(l / 16) .. +7, the A operand as loaded); YP: the fp16
@@ -69,15 +94,23 @@ __global__ __launch_bounds__(256) void pack_kernel(const half_t* __restrict__ w,
 // ROPE: y is not written; the q.k.v projection's column pairs of each batch
 // row go through rope_append_pair (RoPE + paged append, request
 // ra.request_base + row).
-template <int MATS, int U, typename OutT, bool XP = false, bool YP = false, bool ROPE = false>
-__global__ __launch_bounds__(1024) void packed_gemm_kernel(const half_t* __restrict__ x,
+// At most kPackedNormWaves waves per tile with the folded norm (its extra
+// registers fit the 256-thread bound; the q.k.v, gated and LM head
+// defaults use 1-4).
+constexpr int kPackedNormWaves = 4;
+
+template <int MATS, int U, typename OutT, bool XP = false, bool YP = false, bool ROPE = false,
+          int FUSE = kPackedPlain>
+__global__ __launch_bounds__(FUSE == kPackedNorm ? kPackedNormWaves * kWave : 1024) void packed_gemm_kernel(const half_t* __restrict__ x,
                                                            const half_t* __restrict__ p0,
                                                            const half_t* __restrict__ p1,
                                                            OutT* __restrict__ y, int m_rows,
                                                            int n_out, int k_in, int ks_count,
-                                                           unsigned packed_bytes, RopeArgs ra) {
+                                                           unsigned packed_bytes, RopeArgs ra,
+                                                           PackedFuseArgs pf) {
   static_assert(!ROPE || (MATS == 1 && !YP), "the RoPE epilogue serves the q.k.v projection");
-  extern __shared__ float red[];  // [ks][MATS][4][64]
+  static_assert(FUSE != kPackedResidual || (MATS == 1 && !ROPE), "residual: plain projection");
+  extern __shared__ float red[];  // [ks][MATS][4][64], then kPackedNorm: [ks][16] squares
   const int lane = threadIdx.x & (kWave - 1);
   const int ks = threadIdx.x / kWave;
   const int j = lane & 15;
@@ -90,6 +123,7 @@ __global__ __launch_bounds__(1024) void packed_gemm_kernel(const half_t* __restr
   const __amdgpu_buffer_rsrc_t r1 = buffer_rsrc(MATS == 2 ? p1 : p0, packed_bytes);
   const unsigned x_row = j < m_rows ? (unsigned)j * (unsigned)k_in * 2u : kNone;
   const unsigned w_base = (unsigned)nt * (unsigned)chunks * 1024u + (unsigned)lane * 16u;
+  float squares = 0.0f;  // kPackedNorm: row j's sum of squares over this lane's k
   f4 acc[MATS];
 #pragma unroll
   for (int m = 0; m < MATS; ++m) acc[m] = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -117,6 +151,15 @@ __global__ __launch_bounds__(1024) void packed_gemm_kernel(const half_t* __restr
           xv[u][s] = buffer_load16(
               rx, live && kk < k_in && x_row != kNone ? x_row + (unsigned)kk * 2u : kNone);
       }
+    if constexpr (FUSE == kPackedNorm) {
+      // every load of the step goes out before the squares (left to itself
+      // the scheduler interleaves them and waits after every few)
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) squares = dot8(xv[u][s], xv[u][s], squares);
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -125,6 +168,22 @@ __global__ __launch_bounds__(1024) void packed_gemm_kernel(const half_t* __restr
         for (int m = 0; m < MATS; ++m)
           acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv[u][s], wv[u][m][s], acc[m], 0, 0, 0);
   }
+  float* red_sq = red + ks_count * MATS * 4 * kWave;
+  if constexpr (FUSE == kPackedNorm) {
+    squares += __shfl_xor(squares, 16, kWave);
+    squares += __shfl_xor(squares, 32, kWave);
+    if (g == 0) red_sq[ks * 16 + j] = squares;
+  }
+  // kPackedNorm: 1 / rms of batch row `row` (its waves' squares in order)
+  auto row_scale = [&](int row) -> float {
+    if constexpr (FUSE != kPackedNorm) {
+      return 1.0f;
+    } else {
+      float total = 0.0f;
+      for (int w = 0; w < ks_count; ++w) total += red_sq[w * 16 + row];
+      return 1.0f / sqrtf(total / (float)k_in + pf.eps);
+    }
+  };
 #pragma unroll
   for (int m = 0; m < MATS; ++m)
 #pragma unroll
@@ -142,7 +201,9 @@ __global__ __launch_bounds__(1024) void packed_gemm_kernel(const half_t* __restr
         odd += red[(w * 4 + r) * kWave + l + 1];
       }
       const int col = nt * 16 + 2 * p;
-      if (row < m_rows && col < n_out) rope_append_pair(ra, ra.request_base + row, col, even, odd);
+      const float scale = row_scale(row);
+      if (row < m_rows && col < n_out)
+        rope_append_pair(ra, ra.request_base + row, col, even * scale, odd * scale);
     }
     return;
   }
@@ -159,10 +220,14 @@ __global__ __launch_bounds__(1024) void packed_gemm_kernel(const half_t* __restr
       size_t at = (size_t)row * n_out + col;
       if constexpr (YP)  // pass-relative fragment slot of (row, col)
         at = ((size_t)(col >> 5) * 64 + row + 16 * ((col & 31) >> 3)) * 8 + (col & 7);
+      const float scale = row_scale(row);
       if constexpr (MATS == 2)
-        y[at] = gated_value(a[0], a[1]);
+        y[at] = gated_value(a[0] * scale, a[1] * scale);
+      else if constexpr (FUSE == kPackedResidual)
+        y[at] = from_float<OutT>(to_float<half_t>(pf.residual[at]) +
+                                 to_float<half_t>(from_float<half_t>(a[0])));
       else
-        y[at] = from_float<OutT>(a[0]);
+        y[at] = from_float<OutT>(a[0] * scale);
     }
   }
 }
@@ -190,13 +255,14 @@ void default_packed(int64_t batch, int64_t n, int mats, int& unroll, int& ks) {
     ks = batch >= 8 ? 16 : 8;
 }
 
-template <int MATS, typename OutT, bool XP, bool YP, bool ROPE = false>
+template <int MATS, typename OutT, bool XP, bool YP, bool ROPE = false, int FUSE = kPackedPlain>
 int run_packed(const half_t* x, const half_t* p0, const half_t* p1, OutT* y, int64_t batch,
                int64_t k, int64_t n, int unroll, int ks, hipStream_t st,
-               const RopeArgs& rope = RopeArgs{}) {
+               const RopeArgs& rope = RopeArgs{}, const PackedFuseArgs& fuse = PackedFuseArgs{}) {
   const int64_t bytes = packed_elements(n, k) * 2;
   const dim3 grid((unsigned)((n + 15) / 16));
-  const size_t lds = (size_t)ks * MATS * 4 * kWave * sizeof(float);
+  const size_t lds = (size_t)ks * MATS * 4 * kWave * sizeof(float) +
+                     (FUSE == kPackedNorm ? (size_t)ks * 16 * sizeof(float) : 0);
   const int64_t x_pass = XP ? ((k + 31) / 32) * 512 : 16 * k;  // elements per 16-row pass
   const int64_t y_pass = YP ? ((n + 31) / 32) * 512 : 16 * n;
   for (int64_t r0 = 0; r0 < batch; r0 += 16) {
@@ -205,29 +271,42 @@ int run_packed(const half_t* x, const half_t* p0, const half_t* p1, OutT* y, int
     OutT* ys = ROPE ? y : y + (r0 / 16) * y_pass;
     RopeArgs ra = rope;
     ra.request_base = (int)r0;
+    PackedFuseArgs pf = fuse;
+    if (FUSE == kPackedResidual) pf.residual = fuse.residual + (r0 / 16) * y_pass;
     if (unroll == 1)
-      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 1, OutT, XP, YP, ROPE>), grid, dim3(ks * kWave),
-                         lds, st, xs, p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes, ra);
+      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 1, OutT, XP, YP, ROPE, FUSE>), grid,
+                         dim3(ks * kWave), lds, st, xs, p0, p1, ys, rows, (int)n, (int)k, ks,
+                         (unsigned)bytes, ra, pf);
     else if (unroll == 2)
-      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 2, OutT, XP, YP, ROPE>), grid, dim3(ks * kWave),
-                         lds, st, xs, p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes, ra);
+      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 2, OutT, XP, YP, ROPE, FUSE>), grid,
+                         dim3(ks * kWave), lds, st, xs, p0, p1, ys, rows, (int)n, (int)k, ks,
+                         (unsigned)bytes, ra, pf);
     else
-      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 4, OutT, XP, YP, ROPE>), grid, dim3(ks * kWave),
-                         lds, st, xs, p0, p1, ys, rows, (int)n, (int)k, ks, (unsigned)bytes, ra);
+      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 4, OutT, XP, YP, ROPE, FUSE>), grid,
+                         dim3(ks * kWave), lds, st, xs, p0, p1, ys, rows, (int)n, (int)k, ks,
+                         (unsigned)bytes, ra, pf);
     if (check_launch("packed_gemm_kernel")) return 1;
   }
   return 0;
 }
 
-template <int MATS, typename OutT>
+template <int MATS, typename OutT, int FUSE = kPackedPlain>
 int run_packed_layout(const half_t* x, const half_t* p0, const half_t* p1, OutT* y,
                       int64_t batch, int64_t k, int64_t n, int unroll, int ks, int layout,
-                      hipStream_t st) {
+                      hipStream_t st, const PackedFuseArgs& pf = PackedFuseArgs{}) {
   const bool xp = layout & TMC_LAYOUT_X_PACKED, yp = layout & TMC_LAYOUT_Y_PACKED;
-  if (xp && yp) return run_packed<MATS, OutT, true, true>(x, p0, p1, y, batch, k, n, unroll, ks, st);
-  if (xp) return run_packed<MATS, OutT, true, false>(x, p0, p1, y, batch, k, n, unroll, ks, st);
-  if (yp) return run_packed<MATS, OutT, false, true>(x, p0, p1, y, batch, k, n, unroll, ks, st);
-  return run_packed<MATS, OutT, false, false>(x, p0, p1, y, batch, k, n, unroll, ks, st);
+  const RopeArgs none{};
+  if (xp && yp)
+    return run_packed<MATS, OutT, true, true, false, FUSE>(x, p0, p1, y, batch, k, n, unroll, ks,
+                                                           st, none, pf);
+  if (xp)
+    return run_packed<MATS, OutT, true, false, false, FUSE>(x, p0, p1, y, batch, k, n, unroll, ks,
+                                                            st, none, pf);
+  if (yp)
+    return run_packed<MATS, OutT, false, true, false, FUSE>(x, p0, p1, y, batch, k, n, unroll, ks,
+                                                            st, none, pf);
+  return run_packed<MATS, OutT, false, false, false, FUSE>(x, p0, p1, y, batch, k, n, unroll, ks,
+                                                           st, none, pf);
 }
 
 // One thread per 8-element slot of a 16-row pass in fragment order.
@@ -254,8 +333,12 @@ __global__ __launch_bounds__(256) void pack_activations_kernel(const half_t* __r
 
 int packed_entry(int mats, const void* x, const void* p0, const void* p1, void* y, int y_dtype,
                  int64_t batch, int64_t k, int64_t n, int layout, const tmc_gemv_config* config,
-                 void* stream) {
+                 void* stream, int fuse = kPackedPlain, const PackedFuseArgs& pf = PackedFuseArgs{}) {
   const char* what = mats == 2 ? "Packed gated MLP" : "Packed GEMM";
+  TMC_REQUIRE(fuse != kPackedNorm || (pf.eps > 0.0f && std::isfinite(pf.eps)),
+              std::string(what) + " with RMSNorm: epsilon must be positive.");
+  TMC_REQUIRE(fuse != kPackedResidual || (mats == 1 && y_dtype == TMC_F16 && pf.residual),
+              std::string(what) + " with residual: fp16 output and a residual are required.");
   TMC_REQUIRE(x && p0 && y && (mats == 1 || p1), std::string(what) + ": null device pointer.");
   TMC_REQUIRE(y_dtype == TMC_F16 || y_dtype == TMC_F32,
               std::string(what) + ": output dtype must be fp16 or fp32.");
@@ -267,12 +350,17 @@ int packed_entry(int mats, const void* x, const void* p0, const void* p1, void* 
               std::string(what) + ": operands exceed the 4 GiB buffer range.");
   int unroll, ks;
   default_packed(batch, n, mats, unroll, ks);
+  // folded norm: 4 waves per tile below the LM head's width (batch 16 q.k.v
+  // 20.5-20.9 us against 21.5 with the plain default of 2)
+  if (fuse == kPackedNorm) ks = n >= 16384 ? std::min(ks, kPackedNormWaves) : kPackedNormWaves;
   if (config && config->algorithm != 0) {
     unroll = config->unroll;
     ks = config->k_split;
   }
-  TMC_REQUIRE((unroll == 1 || unroll == 2 || unroll == 4) && ks >= 1 && ks <= 16,
-              std::string(what) + ": config needs unroll 1|2|4 and k_split 1..16.");
+  TMC_REQUIRE((unroll == 1 || unroll == 2 || unroll == 4) && ks >= 1 &&
+                  ks <= (fuse == kPackedNorm ? kPackedNormWaves : 16),
+              std::string(what) + ": config needs unroll 1|2|4 and k_split 1..16 (1..4 with "
+              "RMSNorm).");
   TMC_REQUIRE((layout & ~(TMC_LAYOUT_X_PACKED | TMC_LAYOUT_Y_PACKED)) == 0,
               std::string(what) + ": unknown layout bits.");
   TMC_REQUIRE(!(layout & TMC_LAYOUT_Y_PACKED) || y_dtype == TMC_F16,
@@ -283,6 +371,20 @@ int packed_entry(int mats, const void* x, const void* p0, const void* p1, void* 
   const half_t* xs = static_cast<const half_t*>(x);
   const half_t* a = static_cast<const half_t*>(p0);
   const half_t* b = static_cast<const half_t*>(p1);
+  if (fuse == kPackedNorm) {
+    if (mats == 2)
+      return run_packed_layout<2, half_t, kPackedNorm>(xs, a, b, static_cast<half_t*>(y), batch, k,
+                                                       n, unroll, ks, layout, st, pf);
+    if (y_dtype == TMC_F32)
+      return run_packed_layout<1, float, kPackedNorm>(xs, a, a, static_cast<float*>(y), batch, k,
+                                                      n, unroll, ks, layout & TMC_LAYOUT_X_PACKED,
+                                                      st, pf);
+    return run_packed_layout<1, half_t, kPackedNorm>(xs, a, a, static_cast<half_t*>(y), batch, k,
+                                                     n, unroll, ks, layout, st, pf);
+  }
+  if (fuse == kPackedResidual)
+    return run_packed_layout<1, half_t, kPackedResidual>(xs, a, a, static_cast<half_t*>(y), batch,
+                                                         k, n, unroll, ks, layout, st, pf);
   if (mats == 2)
     return run_packed_layout<2, half_t>(xs, a, b, static_cast<half_t*>(y), batch, k, n, unroll,
                                         ks, layout, st);
@@ -303,8 +405,9 @@ extern "C" int64_t tmc_packed_weight_elements(int64_t out_features, int64_t in_f
   return packed_elements(out_features, in_features);
 }
 
-extern "C" int tmc_pack_weights_f16(const void* w, void* packed, int64_t out_features,
-                                    int64_t in_features, void* stream) {
+extern "C" int tmc_pack_weights_scaled_f16(const void* w, const void* gamma, void* packed,
+                                           int64_t out_features, int64_t in_features,
+                                           void* stream) {
   TMC_REQUIRE(w && packed, "Pack weights: null device pointer.");
   TMC_REQUIRE(out_features > 0 && in_features > 0 && out_features < (1LL << 31) &&
                   in_features < (1LL << 31),
@@ -313,9 +416,14 @@ extern "C" int tmc_pack_weights_f16(const void* w, void* packed, int64_t out_fea
   const long slots = (long)(packed_elements(out_features, in_features) / 8);
   const unsigned blocks = (unsigned)std::min<long>((slots + 255) / 256, 65536);
   hipLaunchKernelGGL(pack_kernel, dim3(blocks), dim3(256), 0, as_stream(stream),
-                     static_cast<const half_t*>(w), static_cast<half_t*>(packed),
-                     (int)out_features, (int)in_features, slots);
+                     static_cast<const half_t*>(w), static_cast<const half_t*>(gamma),
+                     static_cast<half_t*>(packed), (int)out_features, (int)in_features, slots);
   return check_launch("pack_kernel");
+}
+
+extern "C" int tmc_pack_weights_f16(const void* w, void* packed, int64_t out_features,
+                                    int64_t in_features, void* stream) {
+  return tmc_pack_weights_scaled_f16(w, nullptr, packed, out_features, in_features, stream);
 }
 
 extern "C" int tmc_gemm_packed_f16(const void* x, const void* packed_w, void* y, int y_dtype,
@@ -340,15 +448,21 @@ extern "C" int tmc_gemm_packed_ex_f16(const void* x, const void* packed_w, void*
                       layout, config, stream);
 }
 
-extern "C" int tmc_qkv_rope_append_packed_f16(
-    const void* x, const void* packed_w, const float* cosine, const float* sine,
-    const int32_t* valid_lengths, const int32_t* block_tables, const int32_t* active_count,
-    void* q_out, void* key_pool, void* value_pool, int64_t batch, int64_t hidden,
-    int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t capacity, int64_t page_size,
-    int64_t max_pages, int layout, const tmc_gemv_config* config, void* stream) {
+namespace tmc {
+namespace {
+
+int qkv_rope_packed_entry(const void* x, bool norm, float eps, const void* packed_w,
+                          const float* cosine, const float* sine, const int32_t* valid_lengths,
+                          const int32_t* block_tables, const int32_t* active_count, void* q_out,
+                          void* key_pool, void* value_pool, int64_t batch, int64_t hidden,
+                          int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t capacity,
+                          int64_t page_size, int64_t max_pages, int layout,
+                          const tmc_gemv_config* config, void* stream) {
   TMC_REQUIRE(x && packed_w && cosine && sine && valid_lengths && block_tables && active_count &&
                   q_out && key_pool && value_pool,
               "Packed q.k.v RoPE append: null pointer.");
+  TMC_REQUIRE(!norm || (eps > 0.0f && std::isfinite(eps)),
+              "Packed q.k.v RoPE append with RMSNorm: epsilon must be positive.");
   TMC_REQUIRE(batch > 0 && batch < (1LL << 31) && hidden > 0 && hidden % 8 == 0 &&
                   aligned16(x) && aligned16(packed_w),
               "Packed q.k.v RoPE append: hidden must be a positive multiple of 8 and x, W "
@@ -366,12 +480,15 @@ extern "C" int tmc_qkv_rope_append_packed_f16(
               "Packed q.k.v RoPE append: layout may only set TMC_LAYOUT_X_PACKED.");
   int unroll, ks;
   default_packed(batch, n, 1, unroll, ks);
+  if (norm) ks = n >= 16384 ? std::min(ks, kPackedNormWaves) : kPackedNormWaves;
   if (config && config->algorithm != 0) {
     unroll = config->unroll;
     ks = config->k_split;
   }
-  TMC_REQUIRE((unroll == 1 || unroll == 2 || unroll == 4) && ks >= 1 && ks <= 16,
-              "Packed q.k.v RoPE append: config needs unroll 1|2|4 and k_split 1..16.");
+  TMC_REQUIRE((unroll == 1 || unroll == 2 || unroll == 4) && ks >= 1 &&
+                  ks <= (norm ? kPackedNormWaves : 16),
+              "Packed q.k.v RoPE append: config needs unroll 1|2|4 and k_split 1..16 (1..4 with "
+              "RMSNorm).");
   RopeArgs ra;
   ra.cosine = cosine;
   ra.sine = sine;
@@ -391,11 +508,78 @@ extern "C" int tmc_qkv_rope_append_packed_f16(
   const half_t* w = static_cast<const half_t*>(packed_w);
   half_t* none = static_cast<half_t*>(q_out);  // not written by the RoPE epilogue
   const hipStream_t st = as_stream(stream);
+  PackedFuseArgs pf;
+  pf.eps = eps;
+  if (norm) {
+    if (layout & TMC_LAYOUT_X_PACKED)
+      return run_packed<1, half_t, true, false, true, kPackedNorm>(xs, w, w, none, batch, hidden,
+                                                                   n, unroll, ks, st, ra, pf);
+    return run_packed<1, half_t, false, false, true, kPackedNorm>(xs, w, w, none, batch, hidden, n,
+                                                                  unroll, ks, st, ra, pf);
+  }
   if (layout & TMC_LAYOUT_X_PACKED)
     return run_packed<1, half_t, true, false, true>(xs, w, w, none, batch, hidden, n, unroll, ks,
                                                     st, ra);
   return run_packed<1, half_t, false, false, true>(xs, w, w, none, batch, hidden, n, unroll, ks, st,
                                                    ra);
+}
+
+}  // namespace
+}  // namespace tmc
+
+extern "C" int tmc_qkv_rope_append_packed_f16(
+    const void* x, const void* packed_w, const float* cosine, const float* sine,
+    const int32_t* valid_lengths, const int32_t* block_tables, const int32_t* active_count,
+    void* q_out, void* key_pool, void* value_pool, int64_t batch, int64_t hidden,
+    int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t capacity, int64_t page_size,
+    int64_t max_pages, int layout, const tmc_gemv_config* config, void* stream) {
+  return qkv_rope_packed_entry(x, false, 0.0f, packed_w, cosine, sine, valid_lengths,
+                               block_tables, active_count, q_out, key_pool, value_pool, batch,
+                               hidden, q_heads, kv_heads, head_dim, capacity, page_size, max_pages,
+                               layout, config, stream);
+}
+
+extern "C" int tmc_rmsnorm_qkv_rope_append_packed_f16(
+    const void* x, const void* packed_w, const float* cosine, const float* sine,
+    const int32_t* valid_lengths, const int32_t* block_tables, const int32_t* active_count,
+    void* q_out, void* key_pool, void* value_pool, int64_t batch, int64_t hidden,
+    int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t capacity, int64_t page_size,
+    int64_t max_pages, float epsilon, int layout, const tmc_gemv_config* config, void* stream) {
+  return qkv_rope_packed_entry(x, true, epsilon, packed_w, cosine, sine, valid_lengths,
+                               block_tables, active_count, q_out, key_pool, value_pool, batch,
+                               hidden, q_heads, kv_heads, head_dim, capacity, page_size, max_pages,
+                               layout, config, stream);
+}
+
+extern "C" int tmc_gemm_packed_norm_f16(const void* x, const void* packed_w, void* y,
+                                        int y_dtype, int64_t batch, int64_t in_features,
+                                        int64_t out_features, float epsilon, int layout,
+                                        const tmc_gemv_config* config, void* stream) {
+  PackedFuseArgs pf;
+  pf.eps = epsilon;
+  return packed_entry(1, x, packed_w, nullptr, y, y_dtype, batch, in_features, out_features,
+                      layout, config, stream, kPackedNorm, pf);
+}
+
+extern "C" int tmc_gate_up_silu_packed_norm_f16(const void* x, const void* packed_gate,
+                                                const void* packed_up, void* out, int64_t batch,
+                                                int64_t hidden, int64_t intermediate,
+                                                float epsilon, int layout,
+                                                const tmc_gemv_config* config, void* stream) {
+  PackedFuseArgs pf;
+  pf.eps = epsilon;
+  return packed_entry(2, x, packed_gate, packed_up, out, TMC_F16, batch, hidden, intermediate,
+                      layout, config, stream, kPackedNorm, pf);
+}
+
+extern "C" int tmc_gemm_packed_residual_f16(const void* x, const void* packed_w,
+                                            const void* residual, void* y, int64_t batch,
+                                            int64_t in_features, int64_t out_features, int layout,
+                                            const tmc_gemv_config* config, void* stream) {
+  PackedFuseArgs pf;
+  pf.residual = static_cast<const half_t*>(residual);
+  return packed_entry(1, x, packed_w, nullptr, y, TMC_F16, batch, in_features, out_features,
+                      layout, config, stream, kPackedResidual, pf);
 }
 
 extern "C" int tmc_gate_up_silu_packed_ex_f16(const void* x, const void* packed_gate,

@@ -409,24 +409,57 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     return true;
   }
   if (name == "gemm_packed") {
+    // norm=1&eps: RMSNorm folded in (W packed with its gamma,
+    // tmc_pack_weights_scaled_f16); residual=1: y = h(h(x W^T) + residual)
+    // (inputs x, W, residual in y's layout).
     const int64_t b = param_int(p, "batch"), k = param_int(p, "in"), n = param_int(p, "out");
     const int od = param_dtype(p, "out_dtype", TMC_F16);
+    const bool norm = param_int(p, "norm", 0) != 0, res = param_int(p, "residual", 0) != 0;
+    const float eps = (float)param_double(p, "eps", 1e-6);
     NEED(b > 0 && k > 0 && n > 0 && (od == TMC_F16 || od == TMC_F32) && dt == TMC_F16,
          "gemm_packed needs batch, in, out > 0, dtype=f16 and out_dtype f16|f32.");
+    NEED(!(norm && res) && (!res || od == TMC_F16),
+         "gemm_packed: norm and residual exclude each other; a residual output is fp16.");
     tmc_gemv_config cfg{};
     NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
     int layout = 0;
     NEED(layout_param(p, layout), "packed GEMM key: x_layout / y_layout must be row_major or packed.");
     NEED(!(layout & TMC_LAYOUT_Y_PACKED) || od == TMC_F16, "gemm_packed: a packed output is fp16.");
-    s.inputs = {TMC_F16, TMC_F16};
+    const size_t xc =
+        (size_t)((layout & TMC_LAYOUT_X_PACKED) ? tmc_packed_activation_elements(b, k) : b * k);
+    const size_t yc =
+        (size_t)((layout & TMC_LAYOUT_Y_PACKED) ? tmc_packed_activation_elements(b, n) : b * n);
+    const size_t wc = (size_t)tmc_packed_weight_elements(n, k);
+    if (res) {
+      s.inputs = {TMC_F16, TMC_F16, TMC_F16};
+      s.counts = {xc, wc, yc, yc};
+    } else {
+      s.inputs = {TMC_F16, TMC_F16};
+      s.counts = {xc, wc, yc};
+    }
     s.outputs = {od};
-    s.counts = {(size_t)((layout & TMC_LAYOUT_X_PACKED) ? tmc_packed_activation_elements(b, k) : b * k),
-                (size_t)tmc_packed_weight_elements(n, k),
-                (size_t)((layout & TMC_LAYOUT_Y_PACKED) ? tmc_packed_activation_elements(b, n) : b * n)};
     s.groups = (size_t)((n + 15) / 16);
     s.launch = [=](const LaunchContext& c) {
+      if (norm)
+        return tmc_gemm_packed_norm_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], od, b, k, n, eps, layout,
+                                        &cfg, c.stream);
+      if (res)
+        return tmc_gemm_packed_residual_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], b, k, n,
+                                            layout, &cfg, c.stream);
       return tmc_gemm_packed_ex_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], od, b, k, n, layout, &cfg,
                                     c.stream);
+    };
+    return true;
+  }
+  if (name == "pack_activations") {
+    const int64_t r = param_int(p, "rows"), k = param_int(p, "cols");
+    NEED(r > 0 && k > 0 && k % 8 == 0 && dt == TMC_F16,
+         "pack_activations needs rows, cols (a multiple of 8) and f16.");
+    s.inputs = {TMC_F16};
+    s.outputs = {TMC_F16};
+    s.counts = {(size_t)(r * k), (size_t)tmc_packed_activation_elements(r, k)};
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_pack_activations_f16(c.ptrs[0], c.ptrs[1], r, k, 0, c.stream);
     };
     return true;
   }
@@ -447,12 +480,23 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     NEED(layout_param(p, layout) && !(layout & TMC_LAYOUT_Y_PACKED),
          "qkv_rope_append_packed: x_layout must be row_major or packed, no y_layout.");
     const int64_t mp = (cap + ps - 1) / ps, n = (qh + 2 * kvh) * d;
+    // norm=1&eps: RMSNorm folded in (W packed with its gamma,
+    // tmc_pack_weights_scaled_f16)
+    const bool norm = param_int(p, "norm", 0) != 0;
+    const float eps = (float)param_double(p, "eps", 1e-6);
     s.inputs = {TMC_F16, TMC_F16, TMC_F32, TMC_F32, TMC_I32, TMC_I32, TMC_I32};
     s.outputs = {TMC_F16, TMC_F16, TMC_F16};
     s.counts = {(size_t)((layout & TMC_LAYOUT_X_PACKED) ? tmc_packed_activation_elements(b, h) : b * h),
                 (size_t)tmc_packed_weight_elements(n, h), (size_t)(cap * (d / 2)),
                 (size_t)(cap * (d / 2)), (size_t)b, (size_t)(b * mp), 1, (size_t)(b * qh * d), 0, 0};
     s.launch = [=](const LaunchContext& c) {
+      if (norm)
+        return tmc_rmsnorm_qkv_rope_append_packed_f16(
+            c.ptrs[0], c.ptrs[1], static_cast<const float*>(c.ptrs[2]),
+            static_cast<const float*>(c.ptrs[3]), static_cast<const int32_t*>(c.ptrs[4]),
+            static_cast<const int32_t*>(c.ptrs[5]), static_cast<const int32_t*>(c.ptrs[6]),
+            c.ptrs[7], c.ptrs[8], c.ptrs[9], b, h, qh, kvh, d, cap, ps, mp, eps, layout, &cfg,
+            c.stream);
       return tmc_qkv_rope_append_packed_f16(
           c.ptrs[0], c.ptrs[1], static_cast<const float*>(c.ptrs[2]),
           static_cast<const float*>(c.ptrs[3]), static_cast<const int32_t*>(c.ptrs[4]),
@@ -470,6 +514,10 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     int layout = 0;
     NEED(layout_param(p, layout), "packed GEMM key: x_layout / y_layout must be row_major or packed.");
     const size_t pe = (size_t)tmc_packed_weight_elements(f, h);
+    // norm=1&eps: RMSNorm folded in (gate and up packed with its gamma,
+    // tmc_pack_weights_scaled_f16)
+    const bool norm = param_int(p, "norm", 0) != 0;
+    const float eps = (float)param_double(p, "eps", 1e-6);
     s.inputs = {TMC_F16, TMC_F16, TMC_F16};
     s.outputs = {TMC_F16};
     s.groups = (size_t)((f + 15) / 16);
@@ -477,6 +525,9 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
                 pe, pe,
                 (size_t)((layout & TMC_LAYOUT_Y_PACKED) ? tmc_packed_activation_elements(b, f) : b * f)};
     s.launch = [=](const LaunchContext& c) {
+      if (norm)
+        return tmc_gate_up_silu_packed_norm_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], b, h,
+                                                f, eps, layout, &cfg, c.stream);
       return tmc_gate_up_silu_packed_ex_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], b, h, f,
                                             layout, &cfg, c.stream);
     };

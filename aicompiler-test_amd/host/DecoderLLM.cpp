@@ -250,42 +250,68 @@ ModelResourcesCreation createSyntheticModelResources(hip::HipRuntime& runtime,
   return result;
 }
 
-std::string ensurePackedWeights(hip::HipRuntime& runtime, DecoderLLMModelResources& model) {
-  if (!model.packedLayers.empty() || model.layers.empty()) return {};
+std::string ensurePackedWeights(hip::HipRuntime& runtime, DecoderLLMModelResources& model,
+                                bool normScaled) {
+  if (model.layers.empty()) return {};
   try {
     const auto& plan = model.plan;
     const std::size_t H = plan.hiddenSize(), I = plan.intermediateSize, V = plan.vocabularySize;
     const std::size_t QKV = H + 2 * plan.kvWidth();
     std::size_t bytes = 0;
-    auto pack = [&](const BufferHandle& w, std::size_t out, std::size_t in) {
+    bool made = false;
+    // fills `slot` once: W packed, with gamma folded in when given
+    auto pack = [&](BufferHandle& slot, const BufferHandle& w, const BufferHandle* gamma,
+                    std::size_t out, std::size_t in) {
+      if (slot) return;
       const auto count = tmc_packed_weight_elements(static_cast<int64_t>(out),
                                                     static_cast<int64_t>(in));
       if (count <= 0) throw std::runtime_error("Packed weights: invalid matrix shape.");
       auto packed = allocate(runtime, static_cast<std::size_t>(count), nullptr,
                              ElementType::Float16);
-      if (tmc_pack_weights_f16(w->devicePointer(), packed->devicePointer(),
-                               static_cast<int64_t>(out), static_cast<int64_t>(in),
-                               runtime.stream()) != 0)
+      if (tmc_pack_weights_scaled_f16(w->devicePointer(),
+                                      gamma ? (*gamma)->devicePointer() : nullptr,
+                                      packed->devicePointer(), static_cast<int64_t>(out),
+                                      static_cast<int64_t>(in), runtime.stream()) != 0)
         throw std::runtime_error(std::string("Packed weights: ") + tmc_last_error());
       bytes += static_cast<std::size_t>(count) * 2;
-      return packed;
+      slot = std::move(packed);
+      made = true;
     };
-    std::vector<DecoderLLMModelLayerBuffers> layers;
-    for (const auto& w : model.layers) {
-      DecoderLLMModelLayerBuffers b;
-      b.queryKeyValueWeight = pack(w.queryKeyValueWeight, QKV, H);
-      b.outputWeight = pack(w.outputWeight, H, H);
-      b.gateWeight = pack(w.gateWeight, I, H);
-      b.upWeight = pack(w.upWeight, I, H);
-      b.downWeight = pack(w.downWeight, H, I);
-      layers.push_back(std::move(b));
+    const std::size_t L = model.layers.size();
+    auto packedLayers = model.packedLayers;
+    auto scaledLayers = model.normScaledLayers;
+    packedLayers.resize(L);
+    if (normScaled) scaledLayers.resize(L);
+    auto head = model.packedLanguageModelHead;
+    auto scaledHead = model.normScaledLanguageModelHead;
+    for (std::size_t l = 0; l < L; ++l) {
+      const auto& w = model.layers[l];
+      auto& b = packedLayers[l];
+      pack(b.outputWeight, w.outputWeight, nullptr, H, H);
+      pack(b.downWeight, w.downWeight, nullptr, H, I);
+      if (normScaled) {
+        auto& c = scaledLayers[l];
+        pack(c.queryKeyValueWeight, w.queryKeyValueWeight, &w.inputNormWeight, QKV, H);
+        pack(c.gateWeight, w.gateWeight, &w.postAttentionNormWeight, I, H);
+        pack(c.upWeight, w.upWeight, &w.postAttentionNormWeight, I, H);
+      } else {
+        pack(b.queryKeyValueWeight, w.queryKeyValueWeight, nullptr, QKV, H);
+        pack(b.gateWeight, w.gateWeight, nullptr, I, H);
+        pack(b.upWeight, w.upWeight, nullptr, I, H);
+      }
     }
-    auto head = pack(model.languageModelHeadWeight, V, H);
+    if (normScaled)
+      pack(scaledHead, model.languageModelHeadWeight, &model.finalNormWeight, V, H);
+    else
+      pack(head, model.languageModelHeadWeight, nullptr, V, H);
+    if (!made) return {};
     const auto error = runtime.synchronize();
     if (!error.empty()) throw std::runtime_error(error);
-    model.packedLayers = std::move(layers);
+    model.packedLayers = std::move(packedLayers);
+    model.normScaledLayers = std::move(scaledLayers);
     model.packedLanguageModelHead = std::move(head);
-    model.packedBytes = bytes;
+    model.normScaledLanguageModelHead = std::move(scaledHead);
+    model.packedBytes += bytes;
   } catch (const std::exception& e) {
     return e.what();
   }
@@ -341,11 +367,12 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
     activationBytes_ += count * hip::elementBytes(type);
     return allocate(rt, count, nullptr, type);
   };
-  // normalized_ and gated_ also hold the fragment-ordered activations of the
-  // batch > 1 buckets: whole 16-row passes.
+  // normalized_ and gated_ (and, with the norms folded, residual_ and
+  // after_) also hold the fragment-ordered activations of the batch > 1
+  // buckets: whole 16-row passes.
   const std::size_t passRows = (M + 15) / 16 * 16;
-  residual_ = act(M * H);
-  after_ = act(M * H);
+  residual_ = act(std::max(M * H, passRows * ((H + 31) / 32 * 32)));
+  after_ = act(std::max(M * H, passRows * ((H + 31) / 32 * 32)));
   normalized_ = act(std::max(M * H, passRows * ((H + 31) / 32 * 32)));
   qkv_ = act(M * QKV);
   query_ = act(M * H);
@@ -360,7 +387,11 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
   for (std::size_t r = 1; r < M; r *= 2) rows.push_back(r);
   rows.push_back(M);
   if (M > 1) {
-    const auto error = ensurePackedWeights(rt, *model_);
+    // the batch > 1 buckets fold the norms under the same condition as the
+    // bucket build below (foldPacked)
+    const bool fuseRopeAll = H % 8 == 0 && D % 2 == 0;
+    const bool scaled = foldNorms_ && fuseRopeAll && H % 32 == 0;
+    const auto error = ensurePackedWeights(rt, *model_, scaled);
     if (!error.empty()) throw std::runtime_error(error);
   }
 
@@ -468,6 +499,12 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
     const std::size_t normThreads = H >= 4096 ? 512 : 256;
     const bool fold = foldNorms_ && !packed && fuseRope && generatedNorm.empty() &&
                       generatedAddNorm.empty() && H % 8 == 0 && H / 8 <= normThreads;
+    // Batch > 1: the packed projections fold the norms too (q.k.v + RoPE,
+    // gate/up and the LM head scale by the row's 1/rms; o and down add the
+    // residual), with the residual stream in fragment order.  Not bit for
+    // bit: the fp16 rounding falls on gamma * s rather than on the
+    // normalized value (within the fp16 path tolerance).
+    const bool foldPacked = foldNorms_ && packed && fuseRope && H % 32 == 0;
     // Paged attention + o projection + residual as one launch (opt-in; the
     // kernel's limits: head_dim 128, GQA group 1 or 2, pages of a multiple
     // of 16 positions, capacity <= 1024, pools below 4 GiB, an output width
@@ -486,11 +523,12 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
       fuseAttention = rt.createComputePipeline(attentionOutputKey, "attention_output_probe")
                           .pipelineCreationPassed;
     if (registry_) {
+      const bool folded = fold || foldPacked;
       const auto track = [&](const char* node, const char* pattern, const std::string& tuning,
                              const std::string& key, std::size_t launches) {
-        const char* implementation = fold ? "folded" : tuning.empty() ? "template" : "generated";
+        const char* implementation = folded ? "folded" : tuning.empty() ? "template" : "generated";
         bucket->uses.push_back(registry_->track(
-            {"bucket " + B + " " + node, pattern, implementation, key, fold ? 0 : launches, 0}));
+            {"bucket " + B + " " + node, pattern, implementation, key, folded ? 0 : launches, 0}));
       };
       track("input norm", "decoder_rmsnorm", generatedNorm,
             fold ? "rmsnorm_qkv_rope_append" : "rmsnorm?" + firstNorm, 1);
@@ -501,9 +539,17 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
                                                  "paged_attention_output_projection", "template",
                                                  attentionOutputKey, L, 0}));
     }
-    add("embedding?rows=" + B + "&hidden=" + std::to_string(H) + "&vocab=" + std::to_string(V),
-        "embedding", {tokensView_, model_->embeddingWeight}, {residual_});
-    if (!fold)
+    const std::string embeddingKey =
+        "embedding?rows=" + B + "&hidden=" + std::to_string(H) + "&vocab=" + std::to_string(V);
+    if (foldPacked) {
+      // the residual stream in fragment order from the start
+      add(embeddingKey, "embedding", {tokensView_, model_->embeddingWeight}, {projected_});
+      add("pack_activations?rows=" + B + "&cols=" + std::to_string(H), "embedding_pack",
+          {projected_}, {residual_});
+    } else {
+      add(embeddingKey, "embedding", {tokensView_, model_->embeddingWeight}, {residual_});
+    }
+    if (!fold && !foldPacked)
       add("rmsnorm?" + firstNorm, "l0_input_norm", {residual_, model_->layers[0].inputNormWeight},
           {normalized_});
     const std::string ropeKey = "decode_rope_append?max_batch=" + B + "&q_heads=" + std::to_string(QH) +
@@ -567,6 +613,38 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
         head += it->second;
       add(head, "norm_lm_head", {residual_, model_->finalNormWeight, model_->languageModelHeadWeight},
           {logits_});
+    } else if (foldPacked) {
+      // residual_ (packed) -> [norm] q.k.v + RoPE + append -> attention -> o
+      // + residual -> after_ -> [norm] gate/up -> down + residual ->
+      // residual_; the LM head folds the final norm.
+      // gamma lives in the scaled packed weights (ensurePackedWeights)
+      const std::string normKey = "&norm=1&eps=" + eps;
+      const std::string hs = std::to_string(H), is = std::to_string(I);
+      for (std::size_t l = 0; l < L; ++l) {
+        const auto& pw = weights(l);
+        const auto& sw = model_->normScaledLayers[l];
+        const std::string p = "l" + std::to_string(l) + "_";
+        add(qkvRopeKey + normKey, p + "norm_qkv_rope_append",
+            {residual_, sw.queryKeyValueWeight, model_->ropeCosine, model_->ropeSine,
+             lengthsView_, tableViews_[l], activeView_},
+            {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer()});
+        add(attentionKey, p + "attention",
+            {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer(), lengthsView_,
+             tableViews_[l], activeView_},
+            {context_});
+        add("gemm_packed?batch=" + B + "&in=" + hs + "&out=" + hs +
+                "&out_dtype=f16&y_layout=packed&residual=1",
+            p + "o_residual", {context_, pw.outputWeight, residual_}, {after_});
+        add("gate_up_silu_packed?batch=" + B + "&hidden=" + hs + "&inter=" + is +
+                "&x_layout=packed&y_layout=packed" + normKey,
+            p + "norm_gate_up_silu", {after_, sw.gateWeight, sw.upWeight}, {gated_});
+        add("gemm_packed?batch=" + B + "&in=" + is + "&out=" + hs +
+                "&out_dtype=f16&x_layout=packed&y_layout=packed&residual=1",
+            p + "down_residual", {gated_, pw.downWeight, after_}, {residual_});
+      }
+      add("gemm_packed?batch=" + B + "&in=" + hs + "&out=" + std::to_string(V) +
+              "&out_dtype=f32&x_layout=packed" + normKey,
+          "norm_lm_head", {residual_, model_->normScaledLanguageModelHead}, {logits_});
     } else {
       for (std::size_t l = 0; l < L; ++l) {
         const auto& w = model_->layers[l];

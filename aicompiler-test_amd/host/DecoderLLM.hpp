@@ -144,16 +144,28 @@ struct DecoderLLMModelResources {
   hip::BufferHandle ropeSine;
   std::vector<DecoderLLMModelLayerBuffers> layers;
   // Fragment-packed copies of the matrices for the batch > 1 skinny GEMM
-  // (tmc_pack_weights_f16); empty until ensurePackedWeights runs.  Batch 1
-  // keeps streaming the row-major weights, which the dot GEMV reads faster.
+  // (tmc_pack_weights_f16), created by ensurePackedWeights as the buckets
+  // need them.  Batch 1 keeps streaming the row-major weights, which the dot
+  // GEMV reads faster.  packedLayers: o and down always; q.k.v, gate and up
+  // (and packedLanguageModelHead) for buckets that run the norm kernels.
+  // normScaledLayers: q.k.v (x input norm gamma), gate and up (x post-
+  // attention norm gamma) and normScaledLanguageModelHead (x final norm
+  // gamma), packed with tmc_pack_weights_scaled_f16 for buckets that fold
+  // the norms into the projections.
   std::vector<DecoderLLMModelLayerBuffers> packedLayers;
   hip::BufferHandle packedLanguageModelHead;
+  std::vector<DecoderLLMModelLayerBuffers> normScaledLayers;
+  hip::BufferHandle normScaledLanguageModelHead;
   std::size_t packedBytes = 0;
 };
 
-// Create the packed copies once per model (idempotent; "" on success).
+// Create the packed copies a batch > 1 bucket needs, once per model
+// (idempotent; "" on success): normScaled selects the gamma-scaled q.k.v,
+// gate/up and LM head copies of the folded-norm buckets instead of the
+// plain ones.
 [[nodiscard]] std::string ensurePackedWeights(hip::HipRuntime& runtime,
-                                              DecoderLLMModelResources& model);
+                                              DecoderLLMModelResources& model,
+                                              bool normScaled = false);
 
 struct ModelResourcesCreation {
   std::shared_ptr<DecoderLLMModelResources> resources;
@@ -284,6 +296,11 @@ struct BatchedDecodeExecutor::Creation {
 // of the norm kernel the bucket would otherwise run, so results are the same
 // bit for bit.  Applies when that norm holds one 16-byte chunk per thread
 // (hidden <= 2048, or 4096) and no admitted region kernel replaces the norms.
+// Buckets above one row fold them into the packed projections (hidden a
+// multiple of 32): the residual stream stays in fragment order, o and down
+// add the residual in their epilogue, and q.k.v + RoPE, gate/up and the LM
+// head run over fp16(gamma * s) and scale each row by its 1/rms, so their
+// results match the norm kernels within the fp16 path tolerance.
 // fuseAttentionOutput: in that folded one-row bucket, each layer's paged
 // attention and o projection + residual run as one launch
 // (paged_attention_output, the fusion candidate of

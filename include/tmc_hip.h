@@ -293,6 +293,11 @@ int tmc_add_rmsnorm_ex(const void *residual, const void *update, const void *w, 
 int64_t tmc_packed_weight_elements(int64_t out_features, int64_t in_features);
 int tmc_pack_weights_f16(const void *w, void *packed, int64_t out_features, int64_t in_features,
                          void *stream);
+/* The same with gamma [in_features] folded in: element (n, k) is stored as
+ * fp16(W[n, k] * gamma[k]) (gamma NULL: tmc_pack_weights_f16).  The weights
+ * of the tmc_*_packed_norm_f16 entry points. */
+int tmc_pack_weights_scaled_f16(const void *w, const void *gamma, void *packed,
+                                int64_t out_features, int64_t in_features, void *stream);
 
 /* tmc_gemv_f16 / tmc_gate_up_silu_f16 semantics over packed weights, any
  * batch (16 rows per pass); in_features % 8 == 0, x and the packed buffers
@@ -330,6 +335,45 @@ int tmc_qkv_rope_append_packed_f16(const void *x, const void *packed_w, const fl
                                    int64_t head_dim, int64_t capacity, int64_t page_size,
                                    int64_t max_pages, int layout, const tmc_gemv_config *config,
                                    void *stream);
+
+/* Batched decode with the RMSNorm folded into the packed projection
+ * (emitDecoderRMSNorm, DecoderLLMMetalEmitter.cpp:63-108, applied in the
+ * projection as the fusion candidate emitDecoderQKVFusion :538-602 does):
+ * x is the un-normalized residual stream s [batch, in]; packed_w holds
+ * W . diag(gamma) (tmc_pack_weights_scaled_f16 with the norm's gamma); row r
+ * of the product is scaled by 1 / sqrt(sum_k s[r, k]^2 / in + epsilon)
+ * before the epilogue (fp16 / fp32 store, SiLU gating, RoPE + append), the
+ * squares taken from the activation fragments the MFMA reads.  The fp16
+ * rounding falls on W * gamma instead of the normalized value, so the
+ * result matches RMSNorm followed by the plain entry point within the fp16
+ * path tolerance, not bit for bit.  epsilon > 0; config k_split at most 4
+ * (the default is clamped there).  Arguments otherwise as the entry points
+ * above. */
+int tmc_gemm_packed_norm_f16(const void *x, const void *packed_w, void *y, int y_dtype,
+                             int64_t batch, int64_t in_features, int64_t out_features,
+                             float epsilon, int layout, const tmc_gemv_config *config,
+                             void *stream);
+int tmc_gate_up_silu_packed_norm_f16(const void *x, const void *packed_gate,
+                                     const void *packed_up, void *out, int64_t batch,
+                                     int64_t hidden, int64_t intermediate, float epsilon,
+                                     int layout, const tmc_gemv_config *config, void *stream);
+int tmc_rmsnorm_qkv_rope_append_packed_f16(const void *x, const void *packed_w,
+                                           const float *cosine, const float *sine,
+                                           const int32_t *valid_lengths,
+                                           const int32_t *block_tables,
+                                           const int32_t *active_count, void *q_out,
+                                           void *key_pool, void *value_pool, int64_t batch,
+                                           int64_t hidden, int64_t q_heads, int64_t kv_heads,
+                                           int64_t head_dim, int64_t capacity, int64_t page_size,
+                                           int64_t max_pages, float epsilon, int layout,
+                                           const tmc_gemv_config *config, void *stream);
+/* emitLinearResidual (DecoderLLMMetalEmitter.cpp:604-621) over packed
+ * weights, any batch: y = fp16(fp16(x W^T) + residual), residual [batch, out]
+ * in y's layout (TMC_LAYOUT_Y_PACKED: the packed activation order). */
+int tmc_gemm_packed_residual_f16(const void *x, const void *packed_w, const void *residual,
+                                 void *y, int64_t batch, int64_t in_features,
+                                 int64_t out_features, int layout, const tmc_gemv_config *config,
+                                 void *stream);
 
 /* emitDecoderRMSNorm (DecoderLLMMetalEmitter.cpp:63-108) / emitRMSNorm
  * (MetalEmitter.cpp:12-76): y = x * rsqrt(mean(x^2) + eps) * w, fp32

@@ -99,6 +99,28 @@ def test_argument_validation_fails_before_device_work(tmc):
     assert "different runtimes" in tmc.last_error()
 
 
+def test_packed_folded_norm_and_residual_validation(tmc):
+    """The folded-norm packed entry points need epsilon > 0 and at most 4
+    waves per tile; the residual epilogue writes fp16 and needs a residual."""
+    lib = tmc.lib()
+    p = C.c_void_p(256)
+    assert lib.tmc_gemm_packed_norm_f16(p, p, p, 0, 16, 4096, 4096, C.c_float(0.0), 1, None,
+                                        None) != 0
+    assert "epsilon" in tmc.last_error()
+    cfg = tmc.GemvConfig(3, 1, 2, 8)
+    assert lib.tmc_gate_up_silu_packed_norm_f16(p, p, p, p, 16, 4096, 11008, C.c_float(1e-6), 3,
+                                                C.byref(cfg), None) != 0
+    assert "1..4 with RMSNorm" in tmc.last_error()
+    assert lib.tmc_rmsnorm_qkv_rope_append_packed_f16(p, p, p, p, p, p, p, p, p, p, 16, 512, 8, 4,
+                                                      64, 64, 16, 4, C.c_float(-1.0), 1, None,
+                                                      None) != 0
+    assert "epsilon" in tmc.last_error()
+    assert lib.tmc_gemm_packed_residual_f16(p, p, None, p, 16, 4096, 4096, 2, None, None) != 0
+    assert "residual" in tmc.last_error()
+    assert lib.tmc_pack_weights_scaled_f16(None, p, p, 8, 8, None) != 0
+    assert "null" in tmc.last_error()
+
+
 def test_attention_output_fusion_limits(tmc):
     """tmc_paged_attention_output_f16 refuses what its one-launch form cannot
     hold, before any device work: (q, k, v, lengths, tables, active, W,

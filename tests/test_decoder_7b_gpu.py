@@ -321,3 +321,54 @@ def test_7b_batch1_attention_output_fusion_matches_two_launches(host, orc, rt7b,
     for i, (a, b) in enumerate(zip(runs[True][1], runs[False][1])):
         assert_f16_path(a, b.astype(np.float64), f"step {i}")
         _check_token(runs[True][2][i], runs[False][2][i], b, f"step {i}")
+
+
+def test_7b_batch16_folded_norms_match_norm_kernels(host, orc, rt7b, models7b):
+    """The 16-row bucket with the norms folded into the packed projections
+    (gamma-scaled packed q.k.v, gate/up and LM head weights, 1/rms from the
+    residual stream's fragments; o and down + residual) against the same
+    bucket with the Add+RMSNorm kernels: logits of every row within the fp16
+    path tolerance and the same greedy tokens (up to near-ties) over 24 steps
+    that cross a page (every row grows from length 1, so each attended
+    position was appended by an earlier step), with 2L fewer dispatches per
+    step (the embedding is packed once: one launch more, 2L + 1 norms
+    fewer)."""
+    model, plan = models7b(1024)
+    rows = 16
+    runs = {}
+    for fold in (True, False):
+        # the pool holds one request at full capacity (64 pages), which also
+        # covers 16 rows of 2 pages
+        pools = [host.create_kv_page_pool(rt7b, plan.kv_plan(), P, 1024 // P)
+                 for _ in range(SHAPE["layers"])]
+        ex = host.create_batched_decode_executor(rt7b, model, pools, rows, fold_norms=fold)
+        mp = ex.max_pages()
+        states = [[host.create_kv_cache_state(rt7b, plan.kv_plan(), pool, False) for pool in pools]
+                  for _ in range(rows)]
+        rng = np.random.default_rng(5103)
+        logits, tokens = [], []
+        for i in range(24):
+            lengths = [i + 1] * rows
+            for r in range(rows):
+                for s in states[r]:
+                    assert s.stage_length(rt7b, lengths[r]) == ""
+                    s.commit_length(lengths[r])
+            tables = []
+            for layer in range(SHAPE["layers"]):
+                flat = []
+                for r in range(rows):
+                    t = states[r][layer].page_table()
+                    flat += t + [-1] * (mp - len(t))
+                tables.append(flat)
+            toks = [int(t) for t in rng.integers(0, SHAPE["vocabulary"], rows)]
+            out = ex.run(toks, lengths, tables, True, False)
+            assert out["passed"], out["error"]
+            logits.append(np.asarray(out["logits"], np.float32).reshape(rows, -1))
+            tokens.append([int(t) for t in out["next_token_ids"]])
+        runs[fold] = (ex.dispatches_per_step(rows), logits, tokens)
+        del ex, states, pools
+    assert runs[False][0] - runs[True][0] == 2 * SHAPE["layers"]
+    for i, (a, b) in enumerate(zip(runs[True][1], runs[False][1])):
+        for r in range(rows):
+            assert_f16_path(a[r], b[r].astype(np.float64), f"step {i} row {r}")
+            _check_token(runs[True][2][i][r], runs[False][2][i][r], b[r], f"step {i} row {r}")

@@ -1035,3 +1035,150 @@ def test_async_raw_writes_reach_the_device_in_order(tmc, torch):
     assert np.array_equal(buf.read_raw(), expect)
     with pytest.raises(tmc.TmcError):
         buf.write_raw_async(np.zeros(4, np.int32), n - 3)
+
+
+# ---------------------------------------------------------------- batch > 1 folded norms
+@pytest.mark.parametrize("batch,k,n,layout,out_dtype", [
+    (16, 4096, 4096, 1, "f16"), (5, 1160, 200, 0, "f32"), (20, 4096, 12288, 3, "f16"),
+    (16, 4096, 32000, 1, "f32")])
+def test_packed_gemm_with_folded_norm_matches_oracle(tmc, orc, torch, batch, k, n, layout,
+                                                     out_dtype):
+    """tmc_gemm_packed_norm_f16: RMSNorm(s) * gamma folded into the packed GEMM
+    (weights packed as W . diag(gamma), each row scaled by its 1/rms) against
+    the oracle's RMSNorm (stored fp16) followed by its linear, within the
+    fp16 path tolerance (fp32 outputs too: the rounding point moves)."""
+    s = orc.f16(normal(1101 + batch, (batch, k)))
+    gamma = orc.f16(uniform(1102, (k,), 0.5, 1.5))
+    w = orc.f16(normal(1103, (n, k), 0.02))
+    pw = tmc.pack_weights(dev_f16(w), gamma=dev_f16(gamma))
+    x = dev_f16(s)
+    xin = tmc.pack_activations(x) if layout & 1 else x
+    dt = torch.float16 if out_dtype == "f16" else torch.float32
+    if layout & 2:
+        y = torch.empty(tmc.packed_activation_elements(batch, n), dtype=dt, device="cuda")
+    else:
+        y = torch.full((batch, n), float("nan"), dtype=dt, device="cuda")
+    tmc.gemm_packed_norm(xin, pw, y, batch, k, n, 1e-6, layout)
+    if layout & 2:
+        rm = torch.empty((batch, n), dtype=dt, device="cuda")
+        tmc.pack_activations(y, rm, unpack=True, rows=batch, cols=n)
+        y = rm
+    torch.cuda.synchronize()
+    normed = orc.f16(orc.store(orc.rmsnorm(s, gamma, F16, 1e-6), F16))
+    ref = orc.linear(normed, w, F16)
+    assert_f16_path(values(y), ref, what=f"folded norm GEMM b{batch} {k}->{n}")
+
+
+@pytest.mark.parametrize("batch,layout", [(16, 3), (7, 1), (17, 0)])
+def test_packed_gated_mlp_with_folded_norm_matches_oracle(tmc, orc, torch, batch, layout):
+    k, n = 4096, 11008
+    s = orc.f16(normal(1111 + batch, (batch, k)))
+    gamma = orc.f16(uniform(1112, (k,), 0.5, 1.5))
+    wg = orc.f16(normal(1113, (n, k), 0.02))
+    wu = orc.f16(normal(1114, (n, k), 0.02))
+    gd = dev_f16(gamma)
+    pg, pu = tmc.pack_weights(dev_f16(wg), gamma=gd), tmc.pack_weights(dev_f16(wu), gamma=gd)
+    x = dev_f16(s)
+    xin = tmc.pack_activations(x) if layout & 1 else x
+    if layout & 2:
+        g = torch.empty(tmc.packed_activation_elements(batch, n), dtype=torch.float16,
+                        device="cuda")
+    else:
+        g = torch.full((batch, n), float("nan"), dtype=torch.float16, device="cuda")
+    tmc.gate_up_silu_packed_norm(xin, pg, pu, g, batch, k, n, 1e-6, layout)
+    if layout & 2:
+        rm = torch.empty((batch, n), dtype=torch.float16, device="cuda")
+        tmc.pack_activations(g, rm, unpack=True, rows=batch, cols=n)
+        g = rm
+    torch.cuda.synchronize()
+    normed = orc.f16(orc.store(orc.rmsnorm(s, gamma, F16, 1e-6), F16))
+    assert_f16_path(values(g), orc.gated_mlp(normed, wg, wu, F16),
+                    what=f"folded norm gated MLP b{batch}")
+
+
+@pytest.mark.parametrize("batch,layout", [(16, 1), (5, 0), (17, 1)])
+def test_packed_qkv_rope_append_with_folded_norm(tmc, orc, torch, batch, layout):
+    """The norm-folded batched q.k.v + RoPE + append against RMSNorm (kernel)
+    followed by tmc_qkv_rope_append_packed_f16: q and every written pool
+    slot within the fp16 path tolerance, the same slots written (skipped
+    rows, lengths outside [1, capacity] and missing pages untouched)."""
+    qh, kvh, d, hidden, cap, p = 8, 4, 64, 512, 64, 16
+    mp = cap // p
+    pos = np.arange(cap)[:, None]
+    freq = np.exp(np.arange(0, d, 2) * (-np.log(10000.0) / d))
+    cos = dev(np.cos(pos * freq).astype(np.float32))
+    sin = dev(np.sin(pos * freq).astype(np.float32))
+    width = (qh + 2 * kvh) * d
+    s = orc.f16(normal(1121 + batch, (batch, hidden)))
+    gamma = dev_f16(orc.f16(uniform(1122, (hidden,), 0.5, 1.5)))
+    w = dev_f16(orc.f16(normal(1123, (width, hidden), 0.05)))
+    packed = tmc.pack_weights(w)
+    scaled = tmc.pack_weights(w, gamma=gamma)
+    x = dev_f16(s)
+    xin = tmc.pack_activations(x) if layout else x
+    rng = np.random.default_rng(1124)
+    pages = batch * mp + 4
+    tables = rng.permutation(pages)[:batch * mp].astype(np.int32).reshape(batch, mp)
+    lengths = rng.integers(1, cap + 1, batch).astype(np.int32)
+    lengths[0] = 0
+    lengths[-1] = cap + 1
+    if batch > 2:
+        lengths[1] = 20
+        tables[1, 1] = -1
+    active = batch - 1 if batch > 2 else batch
+    # NaN pools: the written slots are exactly the ones no longer NaN
+    pool0 = np.full((pages, kvh, p, d), 0x7E00, np.uint16)
+    args = (cos, sin, dev(lengths), dev(tables), torch.tensor([active], dtype=torch.int32,
+                                                               device="cuda"))
+    kp, vp = dev_f16(pool0), dev_f16(pool0.copy())
+    q = torch.full((batch, qh * d), float("nan"), dtype=torch.float16, device="cuda")
+    tmc.rmsnorm_qkv_rope_append_packed(xin, scaled, *args, q, kp, vp, batch, hidden, qh, kvh, d,
+                                       cap, p, mp, 1e-6, layout)
+    normed = torch.empty_like(x)
+    tmc.rmsnorm(x, gamma, normed, 1e-6)
+    kp2, vp2 = dev_f16(pool0), dev_f16(pool0.copy())
+    q2 = torch.full_like(q, float("nan"))
+    tmc.qkv_rope_append_packed(normed, packed, *args, q2, kp2, vp2, batch, hidden, qh, kvh, d, cap,
+                               p, mp, 0)
+    torch.cuda.synchronize()
+    a, b = values(q), values(q2)
+    assert np.array_equal(np.isnan(a), np.isnan(b))
+    live = ~np.isnan(b)
+    assert_f16_path(a[live], b[live].astype(np.float64), what="folded norm q")
+    for got, want in ((kp, kp2), (vp, vp2)):
+        written = ~np.isnan(values(want))
+        assert written.any()
+        assert np.array_equal(~np.isnan(values(got)), written)
+        assert_f16_path(values(got)[written], values(want)[written].astype(np.float64),
+                        what="folded norm pool slots")
+
+
+@pytest.mark.parametrize("batch,k,n,layout", [(16, 4096, 4096, 2), (5, 11008, 4096, 3),
+                                              (20, 4096, 4096, 0)])
+def test_packed_gemm_residual_equals_gemm_then_add_bit_exact(tmc, orc, torch, batch, k, n,
+                                                             layout):
+    """tmc_gemm_packed_residual_f16 (emitLinearResidual over packed weights):
+    the bits of tmc_gemm_packed_ex_f16 followed by tmc_add, in either
+    activation layout."""
+    x = dev_f16(orc.f16(normal(1131 + batch, (batch, k))))
+    w = dev_f16(orc.f16(normal(1132, (n, k), 0.02)))
+    res = dev_f16(orc.f16(normal(1133, (batch, n))))
+    pw = tmc.pack_weights(w)
+    xin = tmc.pack_activations(x) if layout & 1 else x
+    resin = tmc.pack_activations(res) if layout & 2 else res
+    if layout & 2:
+        y = torch.empty(tmc.packed_activation_elements(batch, n), dtype=torch.float16,
+                        device="cuda")
+    else:
+        y = torch.full((batch, n), float("nan"), dtype=torch.float16, device="cuda")
+    tmc.gemm_packed_residual(xin, pw, resin, y, batch, k, n, layout)
+    proj = torch.empty((batch, n), dtype=torch.float16, device="cuda")
+    tmc.gemm_packed_ex(xin, pw, proj, batch, k, n, layout & 1, y_dtype=0)
+    want = torch.empty_like(proj)
+    tmc.add(proj, res, want)
+    if layout & 2:
+        rm = torch.empty((batch, n), dtype=torch.float16, device="cuda")
+        tmc.pack_activations(y, rm, unpack=True, rows=batch, cols=n)
+        y = rm
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(y), bits(want))
