@@ -462,8 +462,11 @@ int tmc_serving_kv_append(const void *input, const int32_t *valid_lengths,
 
 /* Bytes of device workspace the split-KV attention needs for these limits
  * (0 when none is needed): one (max, sum, weighted[D]) fp32 partial per
- * request, query head and split.  Launches that share one workspace must not
- * overlap. */
+ * request, query head and split, and for head_dim 128 one int32 arrival
+ * counter per (request, kv head) after them: the last split block of a row
+ * merges the row's partials in the same launch.  The workspace must be zero
+ * before its first use; every launch leaves the counters at zero.  Launches
+ * that share one workspace must not overlap. */
 size_t tmc_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads,
                                      int64_t head_dim, int64_t capacity);
 
@@ -504,9 +507,10 @@ int tmc_paged_decode_attention(const void *q, const void *key_pool, const void *
  * exceed it are rejected with an error before any launch.  All calls on one
  * GPU share that array: calls that overlap on one GPU (different streams,
  * different host threads) race and must be serialised by the caller.  Each
- * call writes every partial it reads, so nothing needs clearing between
- * calls.  Same arguments, results and errors as tmc_paged_decode_attention
- * otherwise. */
+ * call writes every partial it reads, and the merge counters (zero when the
+ * library loads) are left at zero after every call, so nothing needs
+ * clearing between calls.  Same arguments, results and errors as
+ * tmc_paged_decode_attention otherwise. */
 int tmc_paged_decode_attention_noalloc(const void *q, const void *key_pool,
                                        const void *value_pool, const int32_t *valid_lengths,
                                        const int32_t *block_tables, const int32_t *active_count,

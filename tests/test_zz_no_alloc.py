@@ -1,6 +1,7 @@
 """tmc_paged_decode_attention_noalloc (static device scratch, no allocation)
 against tmc_paged_decode_attention with a caller workspace, through the C
-ABI: two calls in a row, the second with a smaller input, each bit-identical
+ABI: calls in a row, the second with a smaller input and two more of other
+shapes whose split merge runs inside the partial kernel, each bit-identical
 to the existing entry point on the same inputs (the two share their
 kernels); limits beyond the scratch are rejected before any launch."""
 import ctypes as C
@@ -80,6 +81,16 @@ def test_noalloc_paged_attention_matches_workspace_entry(tmc, orc, torch):
     need2, want2, got2 = _run_both(tmc, torch, small)
     assert 0 < need2 < need
     assert torch.equal(got2.view(torch.int16), want2.view(torch.int16))
+    # GQA groups 2 and 1 merge their splits inside the partial kernel through
+    # arrival counters in a fixed area at the scratch's start: two more
+    # shapes in a row (the scratch still holds the earlier calls' slots),
+    # each finding the counters its predecessor left at zero
+    for seed, shape in ((4300, (5, 16, 8, 128, 16, 1024, 128, 300, 2048)),
+                        (4400, (3, 8, 8, 128, 16, 1024, 256, 1500, 4000))):
+        case = _case(orc, torch, seed, *shape)
+        need3, want3, got3 = _run_both(tmc, torch, case)
+        assert need3 > 0 and not torch.isnan(want3).any()
+        assert torch.equal(got3.view(torch.int16), want3.view(torch.int16))
 
 
 def test_noalloc_rejects_limits_beyond_scratch(tmc):
