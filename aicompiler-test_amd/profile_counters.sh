@@ -28,14 +28,18 @@ case "$workload" in
           "mfma_rows_kernel [Li1ELi1ELi2Ef=90484736") ;;
   c5)
     args=(--c5-only --decode-tokens 8)
-    algo=("gemv_dot_kernel@2818048x1x1=180385280"                     # B=1 gate/up + SiLU*Mul
-          "gemv_dot_kernel@1572864x1x1=100696064"                     # B=1 q.k.v + RoPE
-          "gemv_dot_kernel@524288x1x1=90207744"                       # B=1 down
-          "gemv_dot_kernel@262144x1x1=33570816"                       # B=1 o
-          "packed_gemm_kernel [Li2ELi2EDF16_Lb1ELb1ELb0E]@176128x1x1=180838400"  # B=16 gate/up
-          "packed_gemm_kernel [Li1ELi2EDF16_Lb1ELb0ELb1E]@98304x1x1=101187584"   # B=16 q.k.v
-          "packed_gemm_kernel [Li1ELi2EDF16_Lb1ELb0ELb0E]@262144x1x1=90660864"   # B=16 down
-          "packed_gemm_kernel [Li1ELi2EDF16_Lb0ELb0ELb0E]@262144x1x1=33816576") ;; # B=16 o
+    # Batch 1 runs the norm-folded GEMVs (row + gamma read in the prologue)
+    # and the residual epilogues (residual read, sum written); batch 16 the
+    # packed GEMMs with the norm folded (gamma in the weights) or the
+    # residual added in the epilogue.
+    algo=("gemv_norm_kernel [Li2ELi1ELi2EDF16_Li2ELb0E]@313344x1x1=180393472"  # B=1 norm + gate/up + SiLU*Mul
+          "gemv_norm_kernel [Li1ELi2ELi2EDF16_Li2ELb1E]@393216x1x1=100704256"  # B=1 norm + q.k.v + RoPE + append
+          "gemv_dot_kernel [Li1ELi1ELi2ELi4ELi4EDF16_Li3ELb0E]@524288x1x1=90215936"  # B=1 down + residual
+          "gemv_dot_kernel [Li1ELi1ELi2ELi4ELi2EDF16_Li3ELb0E]@262144x1x1=33579008"  # B=1 o + residual
+          "packed_gemm_kernel [Li2ELi2EDF16_Lb1ELb1ELb0ELi1E]@176128x1x1=180838400"  # B=16 norm + gate/up
+          "packed_gemm_kernel [Li1ELi2EDF16_Lb1ELb0ELb1ELi1E]@196608x1x1=101187584"  # B=16 norm + q.k.v
+          "packed_gemm_kernel [Li1ELi2EDF16_Lb1ELb1ELb0ELi2E]@262144x1x1=90791936"   # B=16 down + residual
+          "packed_gemm_kernel [Li1ELi2EDF16_Lb0ELb1ELb0ELi2E]@262144x1x1=33947648") ;; # B=16 o + residual
   *) echo "workload must be extra or c5" >&2; exit 2 ;;
 esac
 algo_args=()
