@@ -92,6 +92,8 @@ def _declare(l):
                                        vp]),
         "tmc_paged_decode_attention": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64,
                                              i64, i64, i64, i64, i64, vp, sz, vp]),
+        "tmc_paged_decode_attention_ex": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64,
+                                                i64, i64, i64, i64, i64, i64, vp, sz, i32, vp]),
         "tmc_paged_decode_attention_noalloc": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i64, i64,
                                                      i64, i64, i64, i64, i64, i64, i64, vp]),
         "tmc_attention_scratch_bytes": (sz, []),
@@ -653,15 +655,18 @@ def paged_gather_probe(k_pool, v_pool, valid_lengths, tables, batch, kv_heads, h
 
 def paged_decode_attention(q, k_pool, v_pool, valid_lengths, tables, active, out, max_batch,
                            q_heads, kv_heads, head_dim, page_size, max_pages, page_stride,
-                           head_stride, workspace=None, stream=None, pool_pages=None):
-    """pool_pages defaults to the pages the k_pool tensor holds."""
+                           head_stride, workspace=None, stream=None, pool_pages=None,
+                           layout=0):
+    """pool_pages defaults to the pages the k_pool tensor holds; layout
+    Y_PACKED writes out in the packed activation order."""
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     if pool_pages is None:
         pool_pages = min(k_pool.numel(), v_pool.numel()) // page_stride
-    check(lib().tmc_paged_decode_attention(
+    check(lib().tmc_paged_decode_attention_ex(
         _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(valid_lengths), _ptr(tables), _ptr(active),
         _ptr(out), _dtype_code(q), max_batch, q_heads, kv_heads, head_dim, page_size, max_pages,
-        pool_pages, page_stride, head_stride, _ptr(workspace), ws_bytes, _stream(stream)),
+        pool_pages, page_stride, head_stride, _ptr(workspace), ws_bytes, layout,
+        _stream(stream)),
         "tmc_paged_decode_attention")
 
 

@@ -75,8 +75,19 @@ struct AttnParams {
   int waves;              // waves per block (D = 128: kWaves, or kWideWaves for one split)
   unsigned kv_bytes;      // bytes of the K (and of the V) buffer when < 4 GiB, else 0
   float scale_log2;       // (1/sqrt(D)) * log2(e)
-  int* arrivals;          // D = 128 multi-split: [batch][kv_heads] split counters (workspace end)
+  int* arrivals;          // D = 128 multi-split: [batch][kv_heads] split counters (workspace start)
+  long out_pass;          // > 0: out in the packed activation order, elements per 16-row pass
 };
+
+// Element of out for request b, column col (query head * D + d): row-major,
+// or with out_pass > 0 the packed GEMM's activation fragment order (16-row
+// pass b / 16, 32-column chunk, lane (b % 16) + 16 * (col % 32 / 8)), which
+// the o projection then reads as packed activations.
+__device__ __forceinline__ size_t out_index(const AttnParams& p, int b, int col, int width) {
+  if (p.out_pass <= 0) return (size_t)b * width + col;
+  return (size_t)(b >> 4) * p.out_pass +
+         ((size_t)(col >> 5) * 64 + (b & 15) + 16 * ((col & 31) >> 3)) * 8 + (col & 7);
+}
 
 // Positions per split of the VALU kernel (D < 128): 4 waves x 2 tiles of
 // 4*64/(D/8) positions.
@@ -194,7 +205,7 @@ __device__ void finish_split(const AttnParams& p, int b, int kvh, int split, int
     }
     const int qh = kvh * GROUP + g;
     if (single) {
-      p.out[((size_t)b * p.q_heads + qh) * D + d] = (half_t)(osum / lsum);
+      p.out[out_index(p, b, qh * D + d, p.q_heads * D)] = (half_t)(osum / lsum);
     } else {
       float* slot = p.ws + (((size_t)b * p.q_heads + qh) * p.max_splits + split) * (D + 2);
       if (p.arrivals) {
@@ -271,7 +282,7 @@ __global__ __launch_bounds__(D) void attn_combine_kernel(AttnParams p) {
     mx = next;
   }
   if (PAGED && bad) return;
-  p.out[((size_t)b * p.q_heads + qh) * D + d] = (half_t)(osum / lsum);
+  p.out[out_index(p, b, qh * D + d, p.q_heads * D)] = (half_t)(osum / lsum);
 }
 
 template <int D, int GROUP, bool PAGED>
@@ -594,7 +605,7 @@ __device__ void merge_if_last(const AttnParams& p, int b, int kvh, int nsplit) {
       mx = next;
     }
     if (PAGED && bad) continue;
-    p.out[((size_t)b * p.q_heads + qh) * D + d] = (half_t)(osum / lsum);
+    p.out[out_index(p, b, qh * D + d, p.q_heads * D)] = (half_t)(osum / lsum);
   }
 }
 
@@ -913,7 +924,8 @@ int paged_attention_impl(const void* q, const void* key_pool, const void* value_
                          const int32_t* active_count, void* out, int dtype, int64_t max_batch,
                          int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t page_size,
                          int64_t max_pages, int64_t pool_pages, int64_t page_stride,
-                         int64_t head_stride, float* slots, int* arrivals, void* stream) {
+                         int64_t head_stride, float* slots, int* arrivals, void* stream,
+                         int layout = 0) {
   const int64_t capacity = page_size * max_pages;
   if (common_checks(q, key_pool, value_pool, out, dtype, max_batch, q_heads, kv_heads, head_dim,
                     capacity))
@@ -932,6 +944,10 @@ int paged_attention_impl(const void* q, const void* key_pool, const void* value_
   p.out = static_cast<half_t*>(out);
   p.ws = slots;
   p.arrivals = arrivals;
+  TMC_REQUIRE(layout == 0 || (layout == TMC_LAYOUT_Y_PACKED && dtype == TMC_F16 && aligned16(out)),
+              "Paged attention: layout must be 0 or TMC_LAYOUT_Y_PACKED (fp16, 16-byte aligned "
+              "output).");
+  if (layout) p.out_pass = (long)((q_heads * head_dim + 31) / 32) * 512;
   p.valid = valid_lengths;
   p.tables = block_tables;
   p.active = active_count;
@@ -959,15 +975,12 @@ int paged_attention_impl(const void* q, const void* key_pool, const void* value_
 }  // namespace
 }  // namespace tmc
 
-extern "C" int tmc_paged_decode_attention(const void* q, const void* key_pool,
-                                          const void* value_pool, const int32_t* valid_lengths,
-                                          const int32_t* block_tables,
-                                          const int32_t* active_count, void* out, int dtype,
-                                          int64_t max_batch, int64_t q_heads, int64_t kv_heads,
-                                          int64_t head_dim, int64_t page_size, int64_t max_pages,
-                                          int64_t pool_pages, int64_t page_stride,
-                                          int64_t head_stride, void* workspace,
-                                          size_t workspace_bytes, void* stream) {
+extern "C" int tmc_paged_decode_attention_ex(
+    const void* q, const void* key_pool, const void* value_pool, const int32_t* valid_lengths,
+    const int32_t* block_tables, const int32_t* active_count, void* out, int dtype,
+    int64_t max_batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t page_size,
+    int64_t max_pages, int64_t pool_pages, int64_t page_stride, int64_t head_stride,
+    void* workspace, size_t workspace_bytes, int layout, void* stream) {
   TMC_REQUIRE(page_size > 0 && max_pages > 0 && max_pages <= (INT64_MAX / page_size),
               "Paged attention: invalid page geometry.");
   const size_t need = tmc_attention_workspace_bytes(max_batch, q_heads, kv_heads, head_dim,
@@ -984,7 +997,22 @@ extern "C" int tmc_paged_decode_attention(const void* q, const void* key_pool,
   return paged_attention_impl(q, key_pool, value_pool, valid_lengths, block_tables, active_count,
                               out, dtype, max_batch, q_heads, kv_heads, head_dim, page_size,
                               max_pages, pool_pages, page_stride, head_stride, slots, arrivals,
-                              stream);
+                              stream, layout);
+}
+
+extern "C" int tmc_paged_decode_attention(const void* q, const void* key_pool,
+                                          const void* value_pool, const int32_t* valid_lengths,
+                                          const int32_t* block_tables,
+                                          const int32_t* active_count, void* out, int dtype,
+                                          int64_t max_batch, int64_t q_heads, int64_t kv_heads,
+                                          int64_t head_dim, int64_t page_size, int64_t max_pages,
+                                          int64_t pool_pages, int64_t page_stride,
+                                          int64_t head_stride, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  return tmc_paged_decode_attention_ex(q, key_pool, value_pool, valid_lengths, block_tables,
+                                       active_count, out, dtype, max_batch, q_heads, kv_heads,
+                                       head_dim, page_size, max_pages, pool_pages, page_stride,
+                                       head_stride, workspace, workspace_bytes, 0, stream);
 }
 
 namespace {

@@ -842,18 +842,26 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
          "paged_attention needs max_batch, q_heads, head_dim, page_size, max_pages.");
     const int64_t head_stride = param_int(p, "head_stride", ps * d);
     const int64_t page_stride = param_int(p, "page_stride", kvh * ps * d);
+    const auto lit = p.find("out_layout");
+    const bool packed_out = lit != p.end() && lit->second == "packed";
+    NEED(lit == p.end() || packed_out || lit->second == "row_major",
+         "paged_attention out_layout must be row_major or packed.");
+    NEED(!packed_out || dt == TMC_F16, "paged_attention packed output needs f16.");
+    const int layout = packed_out ? TMC_LAYOUT_Y_PACKED : 0;
     s.inputs = {dt, dt, dt, TMC_I32, TMC_I32, TMC_I32};
     s.outputs = {dt};
-    s.counts = {(size_t)(b * qh * d), 0, 0, (size_t)b, (size_t)(b * mp), 1, (size_t)(b * qh * d)};
+    s.counts = {(size_t)(b * qh * d), 0, 0, (size_t)b, (size_t)(b * mp), 1,
+                packed_out ? (size_t)tmc_packed_activation_elements(b, qh * d)
+                           : (size_t)(b * qh * d)};
     s.workspace_bytes = tmc_attention_workspace_bytes(b, qh, kvh, d, ps * mp);
     s.launch = [=](const LaunchContext& c) {
       const int64_t pool_pages =
           (int64_t)(std::min(c.counts[1], c.counts[2]) / (size_t)page_stride);
-      return tmc_paged_decode_attention(
+      return tmc_paged_decode_attention_ex(
           c.ptrs[0], c.ptrs[1], c.ptrs[2], static_cast<const int32_t*>(c.ptrs[3]),
           static_cast<const int32_t*>(c.ptrs[4]), static_cast<const int32_t*>(c.ptrs[5]),
           c.ptrs[6], dt, b, qh, kvh, d, ps, mp, pool_pages, page_stride, head_stride,
-          c.workspace, c.workspace_bytes, c.stream);
+          c.workspace, c.workspace_bytes, layout, c.stream);
     };
     return true;
   }

@@ -367,8 +367,8 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
     activationBytes_ += count * hip::elementBytes(type);
     return allocate(rt, count, nullptr, type);
   };
-  // normalized_ and gated_ (and, with the norms folded, residual_ and
-  // after_) also hold the fragment-ordered activations of the batch > 1
+  // normalized_ and gated_ (and, with the norms folded, residual_, after_
+  // and context_) also hold the fragment-ordered activations of the batch > 1
   // buckets: whole 16-row passes.
   const std::size_t passRows = (M + 15) / 16 * 16;
   residual_ = act(std::max(M * H, passRows * ((H + 31) / 32 * 32)));
@@ -376,7 +376,7 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
   normalized_ = act(std::max(M * H, passRows * ((H + 31) / 32 * 32)));
   qkv_ = act(M * QKV);
   query_ = act(M * H);
-  context_ = act(M * H);
+  context_ = act(std::max(M * H, passRows * ((H + 31) / 32 * 32)));
   projected_ = act(M * H);
   gated_ = act(std::max(M * I, passRows * ((I + 31) / 32 * 32)));
   mlp_ = act(M * H);
@@ -620,6 +620,7 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
       // gamma lives in the scaled packed weights (ensurePackedWeights)
       const std::string normKey = "&norm=1&eps=" + eps;
       const std::string hs = std::to_string(H), is = std::to_string(I);
+      const bool packedContext = QH * D == H;
       for (std::size_t l = 0; l < L; ++l) {
         const auto& pw = weights(l);
         const auto& sw = model_->normScaledLayers[l];
@@ -628,12 +629,14 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
             {residual_, sw.queryKeyValueWeight, model_->ropeCosine, model_->ropeSine,
              lengthsView_, tableViews_[l], activeView_},
             {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer()});
-        add(attentionKey, p + "attention",
+        // the attention output in fragment order when its width is the o
+        // projection's input width (q_heads * head_dim == hidden)
+        add(attentionKey + (packedContext ? "&out_layout=packed" : ""), p + "attention",
             {query_, pools_[l]->keyBuffer(), pools_[l]->valueBuffer(), lengthsView_,
              tableViews_[l], activeView_},
             {context_});
-        add("gemm_packed?batch=" + B + "&in=" + hs + "&out=" + hs +
-                "&out_dtype=f16&y_layout=packed&residual=1",
+        add("gemm_packed?batch=" + B + "&in=" + hs + "&out=" + hs + "&out_dtype=f16" +
+                (packedContext ? "&x_layout=packed" : "") + "&y_layout=packed&residual=1",
             p + "o_residual", {context_, pw.outputWeight, residual_}, {after_});
         add("gate_up_silu_packed?batch=" + B + "&hidden=" + hs + "&inter=" + is +
                 "&x_layout=packed&y_layout=packed" + normKey,

@@ -498,6 +498,21 @@ int tmc_paged_decode_attention(const void *q, const void *key_pool, const void *
                                int64_t pool_pages, int64_t page_stride, int64_t head_stride,
                                void *workspace, size_t workspace_bytes, void *stream);
 
+/* The same with an output layout: 0 = out [max_batch, q_heads*D] row-major,
+ * TMC_LAYOUT_Y_PACKED = out in the packed activation order
+ * (tmc_packed_activation_elements(max_batch, q_heads*D) fp16 elements,
+ * 16-byte aligned), so that the o projection reads it as packed activations
+ * (tmc_gemm_packed_residual_f16 with TMC_LAYOUT_X_PACKED).  No counterpart in the
+ * reference, whose attention output feeds a GEMV in row-major order. */
+int tmc_paged_decode_attention_ex(const void *q, const void *key_pool, const void *value_pool,
+                                  const int32_t *valid_lengths, const int32_t *block_tables,
+                                  const int32_t *active_count, void *out, int dtype,
+                                  int64_t max_batch, int64_t q_heads, int64_t kv_heads,
+                                  int64_t head_dim, int64_t page_size, int64_t max_pages,
+                                  int64_t pool_pages, int64_t page_stride, int64_t head_stride,
+                                  void *workspace, size_t workspace_bytes, int layout,
+                                  void *stream);
+
 /* tmc_paged_decode_attention without a workspace argument and without any
  * allocation.  No counterpart in the reference: it is for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving

@@ -154,6 +154,23 @@ def test_attention_output_fusion_limits(tmc):
     assert call(workspace=None) != 0 and "workspace" in tmc.last_error()
 
 
+def test_paged_attention_output_layout_validation(tmc):
+    """tmc_paged_decode_attention_ex accepts layout 0 or TMC_LAYOUT_Y_PACKED
+    (fp16 only) and refuses anything else before any device work."""
+    lib = tmc.lib()
+    p = C.c_void_p(256)
+    ws = tmc.attention_workspace_bytes(4, 8, 8, 128, 4096)
+
+    def call(layout, dtype=0):
+        return lib.tmc_paged_decode_attention_ex(p, p, p, p, p, None, p, dtype, 4, 8, 8, 128, 16,
+                                                 256, 512, 8 * 16 * 128, 16 * 128, p, ws, layout,
+                                                 None)
+
+    assert call(3) != 0 and "layout must be 0 or TMC_LAYOUT_Y_PACKED" in tmc.last_error()
+    assert call(tmc.X_PACKED) != 0 and "layout" in tmc.last_error()
+    assert call(tmc.Y_PACKED, dtype=1) != 0 and "fp16" in tmc.last_error()
+
+
 def test_attention_workspace_sizes(tmc):
     # VALU kernel (D=64): one split of 256 positions needs no workspace,
     # otherwise batch x q_heads x splits x (D + 2) floats

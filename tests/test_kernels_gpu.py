@@ -416,6 +416,39 @@ def test_paged_attention_inactive_and_bad_pages_untouched(tmc, orc, torch, d, p,
     assert_f16_path(got[[0, 2]], ref[[0, 2]], what="paged attention written rows")
 
 
+@pytest.mark.parametrize("batch,qh,kvh,d,active", [(20, 32, 32, 128, 20), (20, 32, 16, 128, 17),
+                                                   (16, 32, 8, 128, 16), (5, 8, 2, 64, 4)])
+def test_paged_attention_packed_output_bit_exact(tmc, torch, batch, qh, kvh, d, active):
+    """The packed output layout holds the row-major result's bits, unpacked
+    by the activation packer (split merges in the kernel for groups 1 and 2,
+    the combine kernel for group 4, one-split head_dim 64); rows past the
+    active count stay untouched in both layouts; two 16-row passes at
+    batch 20."""
+    p, max_pages, pages = 16, 64, 256
+    rng = np.random.default_rng(420 + batch + kvh)
+    lengths = rng.integers(1, max_pages * p + 1, size=batch).astype(np.int32)
+    tables = rng.integers(0, pages, size=(batch, max_pages)).astype(np.int32)
+    k_pool = torch.from_numpy(normal(421, (pages, kvh, p, d))).half().cuda()
+    v_pool = torch.from_numpy(normal(422, (pages, kvh, p, d))).half().cuda()
+    q = torch.from_numpy(normal(423, (batch, qh * d))).half().cuda()
+    act = torch.tensor([active], dtype=torch.int32, device="cuda")
+    args = (q, k_pool, v_pool, dev(lengths), dev(tables), act)
+    shape = (batch, qh, kvh, d, p, max_pages, kvh * p * d, p * d)
+    ws = _ws(tmc, torch, batch, qh, kvh, d, max_pages * p)
+    rm = torch.full((batch, qh * d), float("nan"), dtype=torch.float16, device="cuda")
+    tmc.paged_decode_attention(*args, rm, *shape, ws)
+    packed = tmc.pack_activations(torch.full_like(rm, float("nan")))
+    tmc.paged_decode_attention(*args, packed, *shape, ws, layout=tmc.Y_PACKED)
+    back = torch.empty_like(rm)
+    tmc.pack_activations(packed, out=back, unpack=True, rows=batch, cols=qh * d)
+    torch.cuda.synchronize()
+    assert torch.equal(back.view(torch.int16), rm.view(torch.int16))
+    assert not torch.isnan(rm[:active]).any() and torch.isnan(rm[active:]).all()
+    with pytest.raises(RuntimeError, match="out_layout must be row_major or packed"):
+        tmc.Runtime().resolve("paged_attention?max_batch=4&q_heads=8&head_dim=128&page_size=16"
+                              "&max_pages=16&out_layout=tiled")
+
+
 # ---------------------------------------------------------------- rope / embedding / argmax
 def test_rope_decoder_and_serving(tmc, orc, torch):
     heads, d, cap, seq, batch = 4, 16, 32, 3, 2
