@@ -401,8 +401,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, un
                                            0x00020000);
 }
 
+// NT: non-temporal hint (cache policy bit nt) for K/V read once per launch.
+// Measured on MI355X: the contiguous cache (MODE 0, L = 4095) reads 3.75 ->
+// 4.03 TB/s with it; the paged GQA cache (16-position pages) 3.64 -> 3.40,
+// so pages keep the default policy.
+template <bool NT>
 __device__ __forceinline__ h8 buffer_h8(__amdgpu_buffer_rsrc_t r, unsigned byte_offset) {
-  return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_offset, 0, 0));
+  return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_offset, 0,
+                                                                      NT ? 2 : 0));
 }
 
 template <int MODE>
@@ -460,11 +466,11 @@ __device__ __forceinline__ void issue_step(const AttnParams& p, const int* s_pag
       const unsigned kmask = tmask | (tp + j < end ? 0u : kAbsent);
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        st.k[t][s] = buffer_h8(rk, (tb + (unsigned)j * 256u + 16u * (4 * s + g)) | kmask);
+        st.k[t][s] = buffer_h8<MODE == 0>(rk, (tb + (unsigned)j * 256u + 16u * (4 * s + g)) | kmask);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const unsigned vmask = tmask | (tp + 4 * i + g < end ? 0u : kAbsent);
-        st.v[t][i] = buffer_h8(rv, (tb + (unsigned)(4 * i + g) * 256u + 16u * j) | vmask);
+        st.v[t][i] = buffer_h8<MODE == 0>(rv, (tb + (unsigned)(4 * i + g) * 256u + 16u * j) | vmask);
       }
     } else {
       st.tile[t] = tp < end ? 0 : -1;

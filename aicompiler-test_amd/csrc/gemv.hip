@@ -606,6 +606,8 @@ __global__ __launch_bounds__(1024) void mfma_rows_kernel(const half_t* __restric
         const bool kok = t0 + u < last && k < k_in;
         const unsigned kb = (unsigned)k * 2u;
         xv[u][s] = rsrc_h8(rx, kok && x_row != kNoData ? x_row + kb : kNoData);
+        // default cache policy for the weights: the non-temporal hint
+        // measured slower here (C2 at batch 8, row-major: 3.90 -> 3.71 TB/s)
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
           const unsigned off = kok && w_row[rt] != kNoData ? w_row[rt] + kb : kNoData;

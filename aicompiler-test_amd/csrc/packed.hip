@@ -33,6 +33,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 __device__ __forceinline__ h8 buffer_load16(__amdgpu_buffer_rsrc_t r, unsigned offset) {
   return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)offset, 0, 0));
 }
+// Weight fragments are read once per launch: non-temporal hint (cache policy
+// bit nt), so that they do not evict the activation fragments every output
+// tile re-reads from L2.  Measured on MI355X against the default policy:
+// C2 at batch 8 5.22 -> 5.60 TB/s, the 7B decode step at batch 16 4706 ->
+// 4897 tokens/s.
+__device__ __forceinline__ h8 buffer_load16_stream(__amdgpu_buffer_rsrc_t r, unsigned offset) {
+  return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)offset, 0, 2));
+}
 
 __device__ __forceinline__ half_t gated_value(float gate_sum, float up_sum) {
   // h(h(silu(h(g))) * h(u)), DecoderLLMMetalEmitter.cpp:528-532
@@ -140,8 +148,8 @@ __global__ __launch_bounds__(FUSE == kPackedNorm ? kPackedNormWaves * kWave : 10
         const int c = (t0 + u) * 4 + s;
         const bool live = t0 + u < last && c < chunks;
         const unsigned w_off = live ? w_base + (unsigned)c * 1024u : kNone;
-        wv[u][0][s] = buffer_load16(r0, w_off);
-        if constexpr (MATS == 2) wv[u][1][s] = buffer_load16(r1, w_off);
+        wv[u][0][s] = buffer_load16_stream(r0, w_off);
+        if constexpr (MATS == 2) wv[u][1][s] = buffer_load16_stream(r1, w_off);
         const int kk = c * 32 + 8 * g;
         if constexpr (XP)  // rows past the batch are never read (their slots are unset)
           xv[u][s] = buffer_load16(
