@@ -38,8 +38,10 @@ case "$workload" in
           "gemv_dot_kernel [Li1ELi1ELi2ELi4ELi2EDF16_Li3ELb0E]@262144x1x1=33579008"  # B=1 o + residual
           "packed_gemm_kernel [Li2ELi2EDF16_Lb1ELb1ELb0ELi1E]@176128x1x1=180838400"  # B=16 norm + gate/up
           "packed_gemm_kernel [Li1ELi2EDF16_Lb1ELb0ELb1ELi1E]@196608x1x1=101187584"  # B=16 norm + q.k.v
-          "packed_gemm_kernel [Li1ELi2EDF16_Lb1ELb1ELb0ELi2E]@262144x1x1=90791936"   # B=16 down + residual
-          "packed_gemm_kernel [Li1ELi2EDF16_Lb0ELb1ELb0ELi2E]@262144x1x1=33947648") ;; # B=16 o + residual
+          # B=16 o + residual (33947648) and down + residual (90791936): with
+          # packed input both are this kernel at this grid, one table row
+          # over both launches, so the row's bytes are their mean
+          "packed_gemm_kernel [Li1ELi2EDF16_Lb1ELb1ELb0ELi2E]@262144x1x1=62369792") ;;
   *) echo "workload must be extra or c5" >&2; exit 2 ;;
 esac
 algo_args=()
