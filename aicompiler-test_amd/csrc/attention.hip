@@ -11,7 +11,7 @@
 //
 // A multi-split (request, kv head) stores one (max, sum, weighted) partial
 // per split in the workspace and the partials are merged in split order:
-// at D = 128 with a GQA group of at most 2 by the row's last-arriving split
+// at D = 128 with a GQA group of at most 4 by the row's last-arriving split
 // block (merge_if_last: agent-scope stores and loads and an arrival counter,
 // no fences), otherwise by attn_combine_kernel, one block per (request,
 // query head).  (An earlier in-kernel merge with device-scope fences, each
@@ -549,10 +549,12 @@ __device__ __forceinline__ void consume_step(const AttnParams& p, const int* s_p
   __builtin_amdgcn_wave_barrier();
 }
 
-// Split merge inside the partial kernel (D = 128, GQA group <= 2: the
-// GROUP * 128 outputs take one pass of the block's threads; wider groups
-// keep the merge launch, which spreads them over a block per query head and
-// measured 0.6% faster on C4).  Every split block of a
+// Split merge inside the partial kernel (D = 128, GQA group <= 4: each
+// thread takes GROUP * 128 / threads outputs and issues the slot loads of
+// all of them before using any, one memory round trip per 8 splits; on C4,
+// group 4, 40.5 -> 40.0 us against the merge launch, which a one-output-
+// per-pass loop here had lost by 0.6%; wider groups keep the launch).
+// Every split block of a
 // (request, kv head) row has written its slots with agent-scope stores;
 // once they have completed it counts itself in the row's arrival counter,
 // and the block that arrives last merges the row's GROUP heads exactly as
@@ -573,45 +575,67 @@ __device__ void merge_if_last(const AttnParams& p, int b, int kvh, int nsplit) {
   __syncthreads();
   if (!s_last) return;
   if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  for (int idx = threadIdx.x; idx < GROUP * D; idx += WAVES * kWave) {
-    const int qh = kvh * GROUP + idx / D, d = idx % D;
-    const float* base = p.ws + ((size_t)b * p.q_heads + qh) * p.max_splits * (D + 2);
-    float mx = -INFINITY, lsum = 0.0f, osum = 0.0f;
-    bool bad = false;
-    for (int s0 = 0; s0 < nsplit; s0 += 8) {
-      float ms[8], ls[8], os[8];
+  // R outputs per thread, all their slot loads of a pass issued before any
+  // is used (one memory round trip per 8 splits, whatever the group)
+  constexpr int T = WAVES * kWave;
+  constexpr int R = (GROUP * D + T - 1) / T;
+  float mx[R], lsum[R], osum[R];
+  bool bad[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    mx[r] = -INFINITY;
+    lsum[r] = 0.0f;
+    osum[r] = 0.0f;
+    bad[r] = false;
+  }
+  const int live = GROUP * D;
+  for (int s0 = 0; s0 < nsplit; s0 += 8) {
+    float ms[R][8], ls[R][8], os[R][8];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int idx = min((int)threadIdx.x + r * T, live - 1);
+      const int qh = kvh * GROUP + idx / D, d = idx % D;
+      const float* base = p.ws + ((size_t)b * p.q_heads + qh) * p.max_splits * (D + 2);
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const float* slot = base + (size_t)min(s0 + k, nsplit - 1) * (D + 2);
-        ms[k] = __hip_atomic_load(slot + D, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ls[k] = __hip_atomic_load(slot + D + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        os[k] = __hip_atomic_load(slot + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ms[r][k] = __hip_atomic_load(slot + D, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ls[r][k] = __hip_atomic_load(slot + D + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        os[r][k] = __hip_atomic_load(slot + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
 #pragma unroll
       for (int k = 0; k < 8; ++k)
         if (s0 + k >= nsplit) {
-          ms[k] = -INFINITY;
-          ls[k] = 0.0f;
-          os[k] = 0.0f;
+          ms[r][k] = -INFINITY;
+          ls[r][k] = 0.0f;
+          os[r][k] = 0.0f;
         } else {
-          bad |= ls[k] < 0.0f;
+          bad[r] |= ls[r][k] < 0.0f;
         }
-      float next = mx;
+      float next = mx[r];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) next = fmaxf(next, ms[k]);
-      const float alpha = mx == -INFINITY ? 0.0f : fast_exp2(mx - next);
-      lsum *= alpha;
-      osum *= alpha;
+      for (int k = 0; k < 8; ++k) next = fmaxf(next, ms[r][k]);
+      const float alpha = mx[r] == -INFINITY ? 0.0f : fast_exp2(mx[r] - next);
+      lsum[r] *= alpha;
+      osum[r] *= alpha;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const float scale = ms[k] == -INFINITY ? 0.0f : fast_exp2(ms[k] - next);
-        lsum += scale * ls[k];
-        osum += scale * os[k];
+        const float scale = ms[r][k] == -INFINITY ? 0.0f : fast_exp2(ms[r][k] - next);
+        lsum[r] += scale * ls[r][k];
+        osum[r] += scale * os[r][k];
       }
-      mx = next;
+      mx[r] = next;
     }
-    if (PAGED && bad) continue;
-    p.out[out_index(p, b, qh * D + d, p.q_heads * D)] = (half_t)(osum / lsum);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int idx = (int)threadIdx.x + r * T;
+    if (idx >= live || (PAGED && bad[r])) continue;
+    const int qh = kvh * GROUP + idx / D, d = idx % D;
+    p.out[out_index(p, b, qh * D + d, p.q_heads * D)] = (half_t)(osum[r] / lsum[r]);
   }
 }
 
@@ -716,7 +740,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
 template <int D, int GROUP, bool PAGED>
 int launch_group(const AttnParams& params, int batch, hipStream_t stream) {
   AttnParams p = params;
-  if (D != 128 || GROUP > 2) p.arrivals = nullptr;  // merge launch (see merge_if_last)
+  if (D != 128 || GROUP > 4) p.arrivals = nullptr;  // merge launch (see merge_if_last)
   const dim3 grid((unsigned)p.kv_heads, (unsigned)p.max_splits, (unsigned)batch);
   if constexpr (D == 128) {
     if (p.waves == kWideWaves) {
