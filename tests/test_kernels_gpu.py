@@ -417,11 +417,13 @@ def test_paged_attention_inactive_and_bad_pages_untouched(tmc, orc, torch, d, p,
 
 
 @pytest.mark.parametrize("batch,qh,kvh,d,active", [(20, 32, 32, 128, 20), (20, 32, 16, 128, 17),
-                                                   (16, 32, 8, 128, 16), (5, 8, 2, 64, 4)])
+                                                   (16, 32, 8, 128, 16), (16, 32, 4, 128, 11),
+                                                   (5, 8, 2, 64, 4)])
 def test_paged_attention_packed_output_bit_exact(tmc, torch, batch, qh, kvh, d, active):
     """The packed output layout holds the row-major result's bits, unpacked
     by the activation packer (split merges in the kernel for GQA groups 1, 2
-    and 4 at head_dim 128, the combine kernel at head_dim 64); rows past the
+    and 4 at head_dim 128, the combine kernel for group 8 and at head_dim
+    64); rows past the
     active count stay untouched in both layouts; two 16-row passes at
     batch 20."""
     p, max_pages, pages = 16, 64, 256
