@@ -81,12 +81,14 @@ def test_noalloc_paged_attention_matches_workspace_entry(tmc, orc, torch):
     need2, want2, got2 = _run_both(tmc, torch, small)
     assert 0 < need2 < need
     assert torch.equal(got2.view(torch.int16), want2.view(torch.int16))
-    # GQA groups 2 and 1 merge their splits inside the partial kernel through
-    # arrival counters in a fixed area at the scratch's start: two more
-    # shapes in a row (the scratch still holds the earlier calls' slots),
-    # each finding the counters its predecessor left at zero
+    # GQA groups 4, 2 and 1 merge their splits inside the partial kernel
+    # through arrival counters in a fixed area at the scratch's start (the
+    # calls above are group 4): more shapes in a row (the scratch still holds
+    # the earlier calls' slots), each finding the counters its predecessor
+    # left at zero; group 8 merges in the combine launch from the scratch
     for seed, shape in ((4300, (5, 16, 8, 128, 16, 1024, 128, 300, 2048)),
-                        (4400, (3, 8, 8, 128, 16, 1024, 256, 1500, 4000))):
+                        (4400, (3, 8, 8, 128, 16, 1024, 256, 1500, 4000)),
+                        (4500, (4, 32, 4, 128, 16, 1024, 256, 64, 4000))):
         case = _case(orc, torch, seed, *shape)
         need3, want3, got3 = _run_both(tmc, torch, case)
         assert need3 > 0 and not torch.isnan(want3).any()
