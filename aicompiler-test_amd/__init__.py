@@ -167,6 +167,19 @@ def lib() -> C.CDLL:
     return _lib
 
 
+def open_variant(name: str) -> C.CDLL:
+    """Another build of the same ABI next to libtmc_hip.so (for example
+    libtmc_hip_merge_launch.so), declared like the main library.  Tests swap
+    it in for lib() to run the same checks against that build."""
+    lib()  # the main library first: one HIP runtime, bound through torch
+    path = os.path.join(os.path.dirname(LIB_PATH), name)
+    if not os.path.exists(path):
+        raise TmcError(f"{path} is missing; run aicompiler-test_amd/build.py")
+    variant = C.CDLL(path)
+    _declare(variant)
+    return variant
+
+
 _host = None
 
 

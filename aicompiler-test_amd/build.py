@@ -6,6 +6,10 @@
                   states, decoder executors, serving loop) over that ABI;
   _tmc_host*.so   its Python module (pybind11), for tests and bench.py.
 
+  libtmc_hip_merge_launch.so  the same ABI built with TMC_ATTN_MERGE_LAUNCH=1
+                  (every split-attention merge in a launch of its own, no
+                  cross-block arrival counters), for the tests of that switch.
+
 Objects go under _build/ (git-ignored); the libraries land next to this file
 so they travel with the source tree to the GPU box.
 
@@ -38,6 +42,8 @@ SOURCES = ["runtime.hip", "gemv.hip", "packed.hip", "elementwise.hip", "attentio
 # The HIP runtime library of the ROCm install (rpath of the built library).
 ROCM_LIB = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
 
+MERGE_LAUNCH_OUT = os.path.join(HERE, "libtmc_hip_merge_launch.so")
+
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950",
@@ -58,9 +64,10 @@ FLAGS = [
 SOURCE_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
+def _compile(src: str, variant: str = "", defines: tuple = ()) -> str:
+    obj = os.path.join(BUILD, os.path.splitext(src)[0] + variant + ".o")
+    cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(src, []), *defines, "-c", os.path.join(CSRC, src),
+           "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stdout}\n{res.stderr}")
@@ -104,18 +111,27 @@ def _build_module() -> str:
     return out
 
 
-def build(jobs: int = 4) -> str:
-    os.makedirs(BUILD, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(_compile, SOURCES))
-        host_objs = list(pool.map(_compile_host, HOST_SOURCES))
-    tmp = OUT + ".tmp"
+def _link_hip(objs: list, out: str) -> None:
+    tmp = out + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, f"-L{ROCM_LIB}",
            f"-Wl,-rpath,{ROCM_LIB}"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    shutil.move(tmp, OUT)
+    shutil.move(tmp, out)
+
+
+def build(jobs: int = 4) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
+        merge_launch = pool.submit(_compile, "attention.hip", "_merge_launch",
+                                   ("-DTMC_ATTN_MERGE_LAUNCH=1",))
+        objs = list(pool.map(_compile, SOURCES))
+        host_objs = list(pool.map(_compile_host, HOST_SOURCES))
+        merge_launch_obj = merge_launch.result()
+    _link_hip(objs, OUT)
+    attention = os.path.join(BUILD, "attention.o")
+    _link_hip([merge_launch_obj if o == attention else o for o in objs], MERGE_LAUNCH_OUT)
     _run([CXX, "-shared", "-o", HOST_OUT + ".tmp", *host_objs, f"-L{HERE}", "-ltmc_hip",
           "-Wl,-rpath,$ORIGIN"], "link libtmc_host.so")
     shutil.move(HOST_OUT + ".tmp", HOST_OUT)

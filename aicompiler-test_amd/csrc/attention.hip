@@ -26,6 +26,7 @@
 #include "tmc_abi.hpp"
 #include "tmc_device.hpp"
 
+#include <algorithm>
 #include <climits>
 #include <mutex>
 
@@ -60,6 +61,19 @@ constexpr int kWideMaxGroup = 2;
 // blocks (MHA only).  Measured on the 7B decode step at batch 16: 4858 ->
 // 4919 tokens/s against 4-wave blocks.
 constexpr int kMidWaves = 8;
+// Build switch: 1 merges every multi-split row in a launch of its own
+// (attn_combine_kernel) instead of in the attention kernel, so that no
+// block reads another block's partials (no cross-block arrival counters).
+#ifndef TMC_ATTN_MERGE_LAUNCH
+#define TMC_ATTN_MERGE_LAUNCH 0
+#endif
+// Steps of K/V loads in flight per wave: two for the contiguous cache's
+// multi-split blocks (C3, L 4095: 15.8 -> 15.2 us; L 1024: 13.7 -> 12.4 us),
+// one elsewhere (paged C4: 38.5 -> 42.4 us with two, the 16-wave one-split
+// blocks have no registers to spare).
+template <int MODE, int WAVES> constexpr int attn_depth() {
+  return MODE == 0 && WAVES == kWaves ? 2 : 1;
+}
 
 struct AttnParams {
   const half_t* q;
@@ -715,10 +729,29 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   const __amdgpu_buffer_rsrc_t rv = buffer_of(p.v, p.kv_bytes);
   float (*s_pw)[GROUP] = s_p[wave];
 
-  for (int p0 = begin + kMfmaStep * wave; p0 < end; p0 += kMfmaStep * WAVES) {
-    KvStep<MODE> st;
-    issue_step<MODE>(p, s_pages, page0, cbase, kvh, p0, end, j, g, rk, rv, st);
-    consume_step<GROUP, MODE>(p, s_pages, page0, st, qb, p0, end, j, g, s_pw, m, lsum, o);
+  constexpr int kStride = kMfmaStep * WAVES;
+  if constexpr (attn_depth<MODE, WAVES>() == 2) {
+    // Two steps in flight per wave: the next step's K/V loads are issued
+    // before this step's scores and PV run, so the wave's compute overlaps
+    // its own memory latency (a step past the range issues out-of-range
+    // loads, which return zeros without memory traffic, and is not consumed).
+    int p0 = begin + kMfmaStep * wave;
+    KvStep<MODE> sa, sb;
+    issue_step<MODE>(p, s_pages, page0, cbase, kvh, p0, end, j, g, rk, rv, sa);
+    for (; p0 < end; p0 += 2 * kStride) {  // wave-uniform
+      issue_step<MODE>(p, s_pages, page0, cbase, kvh, p0 + kStride, end, j, g, rk, rv, sb);
+      consume_step<GROUP, MODE>(p, s_pages, page0, sa, qb, p0, end, j, g, s_pw, m, lsum, o);
+      if (p0 + kStride >= end) break;
+      issue_step<MODE>(p, s_pages, page0, cbase, kvh, p0 + 2 * kStride, end, j, g, rk, rv, sa);
+      consume_step<GROUP, MODE>(p, s_pages, page0, sb, qb, p0 + kStride, end, j, g, s_pw, m,
+                                lsum, o);
+    }
+  } else {
+    for (int p0 = begin + kMfmaStep * wave; p0 < end; p0 += kStride) {
+      KvStep<MODE> st;
+      issue_step<MODE>(p, s_pages, page0, cbase, kvh, p0, end, j, g, rk, rv, st);
+      consume_step<GROUP, MODE>(p, s_pages, page0, st, qb, p0, end, j, g, s_pw, m, lsum, o);
+    }
   }
 
 #pragma unroll
@@ -744,6 +777,9 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
 template <int D, int GROUP, bool PAGED>
 int launch_group(const AttnParams& params, int batch, hipStream_t stream) {
   AttnParams p = params;
+#if TMC_ATTN_MERGE_LAUNCH
+  p.arrivals = nullptr;  // build switch: every split merge in its own launch
+#endif
   if (D != 128 || GROUP > 4) p.arrivals = nullptr;  // merge launch (see merge_if_last)
   const dim3 grid((unsigned)p.kv_heads, (unsigned)p.max_splits, (unsigned)batch);
   if constexpr (D == 128) {
@@ -899,11 +935,16 @@ using namespace tmc;
 
 namespace tmc {
 namespace {
-// Workspace: D = 128 keeps the rows' arrival counters [batch][kv_heads]
-// first (256-byte aligned), then the split slots
-// [batch][q_heads][splits][head_dim + 2] fp32.
-size_t counter_bytes(int64_t batch, int64_t kv_heads, int64_t head_dim) {
-  return head_dim == 128 ? ((size_t)batch * kv_heads * sizeof(int) + 255) / 256 * 256 : 0;
+// Workspace layout, the same for every head size and kernel: the rows'
+// arrival counters ([batch][kv_heads] int) in a fixed 64 KiB area at the
+// start (shapes with more than 16384 rows take rows * 4 bytes), then the
+// partial slots.  Every launch leaves its counters at zero and no launch's
+// slots overlap the counter area, so one zeroed workspace serves launches of
+// any shapes with at most 16384 (request, kv head) rows, in any order.
+constexpr size_t kCounterAreaBytes = 64u << 10;
+size_t counter_bytes(int64_t batch, int64_t kv_heads) {
+  const size_t rows = (size_t)batch * kv_heads * sizeof(int);
+  return std::max(kCounterAreaBytes, (rows + 255) / 256 * 256);
 }
 size_t slot_bytes(int64_t batch, int64_t q_heads, int64_t head_dim, int64_t splits) {
   return (size_t)batch * q_heads * splits * (head_dim + 2) * sizeof(float);
@@ -913,15 +954,20 @@ int64_t split_count(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t he
   const int chunk = split_plan(head_dim, batch, q_heads, kv_heads, capacity).chunk;
   return chunk > 0 ? (capacity + chunk - 1) / chunk : 0;
 }
+// Slot bytes a launch of this shape may use (0: no workspace needed).
+size_t slots_needed(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                    int64_t capacity) {
+  const int64_t splits = split_count(batch, q_heads, kv_heads, head_dim, capacity);
+  return splits > 1 ? slot_bytes(batch, q_heads, head_dim, splits) : 0;
+}
 }  // namespace
 }  // namespace tmc
 
 extern "C" size_t tmc_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads,
                                                 int64_t head_dim, int64_t capacity) {
   if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || capacity <= 0 || q_heads % kv_heads) return 0;
-  const int64_t splits = split_count(batch, q_heads, kv_heads, head_dim, capacity);
-  if (splits <= 1) return 0;
-  return counter_bytes(batch, kv_heads, head_dim) + slot_bytes(batch, q_heads, head_dim, splits);
+  const size_t slots = slots_needed(batch, q_heads, kv_heads, head_dim, capacity);
+  return slots ? counter_bytes(batch, kv_heads) + slots : 0;
 }
 
 extern "C" int tmc_decode_attention(const void* q, const void* key_cache, const void* value_cache,
@@ -943,8 +989,7 @@ extern "C" int tmc_decode_attention(const void* q, const void* key_cache, const 
   p.out = static_cast<half_t*>(out);
   if (need > 0) {
     p.arrivals = static_cast<int*>(workspace);
-    p.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                    counter_bytes(batch, kv_heads, head_dim));
+    p.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + counter_bytes(batch, kv_heads));
   }
   p.valid = valid_length;
   p.q_heads = (int)q_heads;
@@ -1042,7 +1087,7 @@ extern "C" int tmc_paged_decode_attention_ex(
   if (need > 0) {
     arrivals = static_cast<int*>(workspace);
     slots = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                     counter_bytes(max_batch, kv_heads, head_dim));
+                                     counter_bytes(max_batch, kv_heads));
   }
   return paged_attention_impl(q, key_pool, value_pool, valid_lengths, block_tables, active_count,
                               out, dtype, max_batch, q_heads, kv_heads, head_dim, page_size,
@@ -1109,9 +1154,9 @@ extern "C" int tmc_paged_decode_attention_noalloc(
   // The scratch keeps the merge counters in a fixed area at its start, which
   // no call's slots overlap: every call leaves its counters at zero, so the
   // next call, whatever its shape, finds them zero.
-  const size_t counters = counter_bytes(max_batch, kv_heads, head_dim);
-  const size_t slots_needed = need > 0 ? need - counters : 0;
-  if (counters > kScratchCounterBytes || slots_needed > kScratchBytes - kScratchCounterBytes)
+  const size_t counters = counter_bytes(max_batch, kv_heads);
+  const size_t slot_need = need > 0 ? need - counters : 0;
+  if (counters > kScratchCounterBytes || slot_need > kScratchBytes - kScratchCounterBytes)
     return fail("Paged attention (no-alloc): these limits need " + std::to_string(need) +
                 " bytes of split workspace; the static scratch holds " +
                 std::to_string(kScratchBytes - kScratchCounterBytes) + " bytes of slots and " +

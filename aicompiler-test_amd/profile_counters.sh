@@ -4,6 +4,7 @@
 #
 #   bash aicompiler-test_amd/profile_counters.sh extra OUT   # C1-C4 kernels
 #   bash aicompiler-test_amd/profile_counters.sh c5 OUT      # 7B decode steps, B = 1 and 16
+#   bash aicompiler-test_amd/profile_counters.sh stalls OUT  # issue / stall counters, C1-C4 kernels
 #
 # Every pass is its own rocprofv3 run (a kernel trace, then FETCH_SIZE,
 # WRITE_SIZE, the EA read-request sizes, TCC hit/miss and MfmaUtil with the
@@ -42,7 +43,10 @@ case "$workload" in
           # packed input both are this kernel at this grid, one table row
           # over both launches, so the row's bytes are their mean
           "packed_gemm_kernel [Li1ELi2EDF16_Lb1ELb1ELb0ELi2E]@262144x1x1=62369792") ;;
-  *) echo "workload must be extra or c5" >&2; exit 2 ;;
+  stalls)
+    args=(--extra-only)
+    algo=() ;;
+  *) echo "workload must be extra, c5 or stalls" >&2; exit 2 ;;
 esac
 algo_args=()
 for a in "${algo[@]}"; do algo_args+=(--algorithmic "$a"); done
@@ -56,6 +60,29 @@ run() {  # run NAME [rocprofv3 options...]
     python3 "$root/bench.py" "${args[@]}" > "$out/db/$name.log" 2>&1
 }
 run trace --kernel-trace
+if [ "$workload" = stalls ]; then
+  # each pass within the per-block limits (8 SQ, 4 TCP, 2 TA); the derived
+  # accumulators (VmemLatency, MeanOccupancyPerCU) get passes of their own
+  run sq --pmc SQ_WAVES SQ_BUSY_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_ANY \
+    SQ_ACTIVE_INST_VMEM SQ_INSTS_VMEM_RD SQ_INSTS_VALU
+  run sq2 --pmc SQ_WAVES SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS SQ_INSTS_LDS SQ_INSTS_SMEM \
+    SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_BUSY_CU_CYCLES
+  run tcp --pmc TCP_TCC_READ_REQ_LATENCY_sum TCP_TCC_READ_REQ_sum \
+    TCP_UTCL1_TRANSLATION_MISS_sum TCP_UTCL1_TRANSLATION_HIT_sum TA_TA_BUSY_sum \
+    TA_ADDR_STALLED_BY_TC_CYCLES_sum
+  run lat --pmc VmemLatency
+  run occ --pmc MeanOccupancyPerCU
+  dbs=()
+  for pass in sq sq2 tcp lat occ; do dbs+=(--db "$out/db/$pass/run_results.db"); done
+  python3 "$root/aicompiler-test_amd/profiling.py" stalls "${dbs[@]}" \
+    --trace "$out/db/trace/run_results.db" --kernel attn_mfma_kernel \
+    --kernel gather_probe_kernel --kernel gemv_dot_kernel --kernel copy_kernel \
+    --command "bash aicompiler-test_amd/profile_counters.sh stalls OUT" \
+    --workload "bench.py --extra-only: C1 GEMV, C2 B=8, C3, C4 and the C4 gather probe" \
+    --json "$out/stalls.json" > /dev/null
+  echo "[profile] $workload: done" >&2
+  exit 0
+fi
 run fetch --pmc FETCH_SIZE
 run write --pmc WRITE_SIZE
 run rdreq --pmc TCC_EA0_RDREQ_32B_sum TCC_EA0_RDREQ_64B_sum TCC_EA0_RDREQ_128B_sum

@@ -13,7 +13,10 @@ Subcommands over the rocpd SQLite databases rocprofv3 writes:
            EA read-request passes, the first two scaled by the copy probe);
            optional algorithmic bytes per kernel; markdown and JSON;
   mfma     MfmaUtil and the f16 MFMA operation count per dispatch of every
-           kernel that issues MFMA, with achieved TFLOP/s from the trace.
+           kernel that issues MFMA, with achieved TFLOP/s from the trace;
+  stalls   issue and stall counters (SQ wave / wait / issue cycles, VMEM
+           latency, occupancy, TA busy, TCP-to-L2 request latency, address
+           translation) per dispatch of chosen kernels, with per-wave ratios.
 
 FETCH_SIZE on gfx950 counts each 128-byte EA read request as 64 bytes (its
 expression adds TCC_BUBBLE x 128, and TCC_BUBBLE stays 0), so a read-heavy
@@ -249,6 +252,60 @@ def mfma_table(mfma_db: str, trace_db: str, min_calls: int) -> list:
     return rows
 
 
+STALL_COUNTERS = (
+    "SQ_WAVES", "SQ_BUSY_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_ACTIVE_INST_ANY",
+    "SQ_ACTIVE_INST_VMEM", "SQ_INSTS_VMEM_RD", "SQ_INSTS_VALU", "SQ_ACTIVE_INST_VALU",
+    "SQ_ACTIVE_INST_LDS", "SQ_INSTS_LDS", "SQ_INSTS_SMEM", "SQ_BUSY_CU_CYCLES",
+    "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_MFMA", "GRBM_GUI_ACTIVE",
+    "VmemLatency", "MeanOccupancyPerCU", "MeanOccupancyPerActiveCU",
+    "TA_TA_BUSY_sum", "TA_ADDR_STALLED_BY_TC_CYCLES_sum",
+    "TCP_TCC_READ_REQ_LATENCY_sum", "TCP_TCC_READ_REQ_sum",
+    "TCP_UTCL1_TRANSLATION_MISS_sum", "TCP_UTCL1_TRANSLATION_HIT_sum")
+
+
+def stall_table(dbs: list, trace_db: str, kernels: list, min_calls: int) -> list:
+    """Mean of every stall counter per (kernel, grid) whose short name contains
+    one of `kernels`, merged over the pass databases, plus per-wave ratios:
+    SQ_WAIT_ANY / SQ_WAVES (cycles a wave spends waiting on a counter),
+    SQ_ACTIVE_INST_ANY / SQ_WAVES (cycles it issues), and the average
+    TCP-to-L2 read latency (TCP_TCC_READ_REQ_LATENCY / TCP_TCC_READ_REQ)."""
+    merged = collections.defaultdict(dict)
+    for db in dbs:
+        for key, d in _per_kernel(db, STALL_COUNTERS).items():
+            for cname, vals in d.items():
+                merged[key][cname] = _mean(vals)
+    trace = _trace(trace_db)
+    rows = []
+    for key, counters in merged.items():
+        name, grid = key
+        durs = trace.get(key, [])
+        if not any(k in name for k in kernels) or len(durs) < min_calls:
+            continue
+        row = {"kernel": name, "grid": grid, "calls": len(durs), "avg_us": round(_mean(durs), 3)}
+        row.update({c: round(v, 3) for c, v in sorted(counters.items())})
+        waves = counters.get("SQ_WAVES")
+        if waves:
+            for c, label in (("SQ_WAIT_ANY", "wait_any_per_wave"),
+                             ("SQ_WAIT_INST_ANY", "wait_inst_any_per_wave"),
+                             ("SQ_ACTIVE_INST_ANY", "active_inst_any_per_wave"),
+                             ("SQ_ACTIVE_INST_VMEM", "active_inst_vmem_per_wave"),
+                             ("SQ_INSTS_VMEM_RD", "vmem_rd_insts_per_wave"),
+                             ("SQ_INSTS_VALU", "valu_insts_per_wave")):
+                if c in counters:
+                    row[label] = round(counters[c] / waves, 2)
+        req = counters.get("TCP_TCC_READ_REQ_sum")
+        if req:
+            row["tcp_l2_read_latency_cycles"] = round(
+                counters.get("TCP_TCC_READ_REQ_LATENCY_sum", 0.0) / req, 1)
+        hit = counters.get("TCP_UTCL1_TRANSLATION_HIT_sum")
+        miss = counters.get("TCP_UTCL1_TRANSLATION_MISS_sum")
+        if hit is not None and miss is not None and hit + miss:
+            row["utcl1_miss_pct"] = round(100.0 * miss / (hit + miss), 2)
+        rows.append(row)
+    rows.sort(key=lambda x: -x["avg_us"] * x["calls"])
+    return rows
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -287,7 +344,25 @@ def main(argv=None) -> int:
     m.add_argument("--min-calls", type=int, default=2)
     m.add_argument("--command", default="")
     m.add_argument("--json")
+    st = sub.add_parser("stalls")
+    st.add_argument("--db", action="append", required=True, help="pass database (repeatable)")
+    st.add_argument("--trace", required=True)
+    st.add_argument("--kernel", action="append", required=True,
+                    help="short-name substring (repeatable)")
+    st.add_argument("--min-calls", type=int, default=2)
+    st.add_argument("--command", default="")
+    st.add_argument("--workload", default="")
+    st.add_argument("--json")
     a = ap.parse_args(argv)
+    if a.cmd == "stalls":
+        rows = stall_table(a.db, a.trace, a.kernel, a.min_calls)
+        text = json.dumps({"workload": a.workload, "command": a.command, "kernels": rows},
+                          indent=1) + "\n"
+        if a.json:
+            with open(a.json, "w") as f:
+                f.write(text)
+        sys.stdout.write(text)
+        return 0
     if a.cmd == "table":
         rows = traffic_table(a.fetch, a.write, a.rdreq, a.trace, a.copy_bytes, a.min_calls,
                              a.algorithmic, a.hit)

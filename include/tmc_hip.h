@@ -461,12 +461,18 @@ int tmc_serving_kv_append(const void *input, const int32_t *valid_lengths,
                           int64_t capacity, int64_t page_size, int head_major, void *stream);
 
 /* Bytes of device workspace the split-KV attention needs for these limits
- * (0 when none is needed): one (max, sum, weighted[D]) fp32 partial per
- * request, query head and split, and for head_dim 128 one int32 arrival
- * counter per (request, kv head) after them: the last split block of a row
- * merges the row's partials in the same launch.  The workspace must be zero
- * before its first use; every launch leaves the counters at zero.  Launches
- * that share one workspace must not overlap. */
+ * (0 when none is needed).  Layout, the same for every head size: int32
+ * arrival counters, one per (request, kv head), in a fixed 64 KiB area at
+ * the start (batch * kv_heads * 4 bytes rounded up to 256 when that is
+ * larger), then one (weighted[D], max, sum) fp32 partial per request, query
+ * head and split.  For head_dim 128 the last split block of a row merges the
+ * row's partials in the same launch and resets its counter.  The workspace
+ * must be zero before its first use; every launch leaves the counters at
+ * zero and no launch's partials overlap the counter area, so one workspace
+ * serves launches of different shapes in any order when it is large enough
+ * for each and batch * kv_heads <= 16384 for all of them (a larger shape
+ * needs a workspace of its own).  Launches that share one workspace must not
+ * overlap. */
 size_t tmc_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads,
                                      int64_t head_dim, int64_t capacity);
 

@@ -172,21 +172,25 @@ def test_paged_attention_output_layout_validation(tmc):
 
 
 def test_attention_workspace_sizes(tmc):
-    # VALU kernel (D=64): one split of 256 positions needs no workspace,
-    # otherwise batch x q_heads x splits x (D + 2) floats
+    # Every workspace starts with a fixed 64 KiB area of arrival counters
+    # (one int32 per (request, kv head)), the same for every head size, then
+    # the [request][q head][split][D + 2] fp32 partials.
+    area = 64 << 10
+    # VALU kernel (D=64): one split of 256 positions needs no workspace
     assert tmc.attention_workspace_bytes(2, 8, 8, 64, 256) == 0
-    # [request][q head][split][D + 2] floats
-    assert tmc.attention_workspace_bytes(2, 8, 8, 64, 1024) == 2 * 8 * 4 * 66 * 4
-    # D = 128: chunk = pow2 in [128, 1024] not above batch * kv_heads * capacity / 256;
-    # one int32 arrival counter per (request, kv head) for the merge inside
-    # the partial kernel (rounded up to 256 bytes), then the slots
-    assert tmc.attention_workspace_bytes(16, 32, 8, 128, 4096) == 512 + 16 * 32 * 4 * 130 * 4
-    assert tmc.attention_workspace_bytes(1, 32, 32, 128, 4096) == 256 + 1 * 32 * 8 * 130 * 4
+    assert tmc.attention_workspace_bytes(2, 8, 8, 64, 1024) == area + 2 * 8 * 4 * 66 * 4
+    # D = 128: chunk = pow2 in [128, 1024] not above batch * kv_heads * capacity / 256
+    assert tmc.attention_workspace_bytes(16, 32, 8, 128, 4096) == area + 16 * 32 * 4 * 130 * 4
+    assert tmc.attention_workspace_bytes(1, 32, 32, 128, 4096) == area + 1 * 32 * 8 * 130 * 4
     # capacity <= 1024 with a GQA group <= 2: one 16-wave block per row, no
     # workspace; a group of 4 keeps the split layout
     assert tmc.attention_workspace_bytes(1, 32, 32, 128, 1024) == 0
     assert tmc.attention_workspace_bytes(1, 8, 4, 128, 1024) == 0
-    assert tmc.attention_workspace_bytes(1, 8, 2, 128, 1024) == 256 + 1 * 8 * 8 * 130 * 4
+    assert tmc.attention_workspace_bytes(1, 8, 2, 128, 1024) == area + 1 * 8 * 8 * 130 * 4
     assert tmc.attention_workspace_bytes(1, 8, 8, 128, 128) == 0
+    # more than 16384 (request, kv head) rows: the counter area grows to one
+    # int32 per row, rounded up to 256 bytes
+    assert tmc.attention_workspace_bytes(4100, 8, 8, 64, 1024) == \
+        (4100 * 8 * 4 + 255) // 256 * 256 + 4100 * 8 * 4 * 66 * 4
     # bad head ratio
     assert tmc.attention_workspace_bytes(2, 6, 4, 64, 1024) == 0

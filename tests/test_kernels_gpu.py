@@ -380,6 +380,45 @@ def test_c4_paged_gqa_attention(tmc, orc, torch):
     assert_f16_path(values(out), ref, what="paged GQA attention (C4)")
 
 
+def test_paged_attention_workspace_reused_across_shapes(tmc, orc, torch):
+    """One zeroed workspace serves launches of different shapes in turn:
+    the arrival counters sit in a fixed area at the workspace's start that no
+    launch's partials overlap, and every launch leaves them at zero.  A small
+    batch with 16 splits per row, a larger batch with more (request, kv head)
+    rows, a head_dim 64 launch (partials merged by a second launch), then the
+    first shape again, each against the oracle."""
+    p = 16
+    cases = [  # batch, q heads, kv heads, head_dim, max_pages
+        (2, 8, 2, 128, 128),
+        (16, 32, 8, 128, 128),
+        (4, 8, 8, 64, 128),
+        (2, 8, 2, 128, 128),
+    ]
+    need = max(tmc.attention_workspace_bytes(b, qh, kvh, d, mp * p) for b, qh, kvh, d, mp in cases)
+    assert all(tmc.attention_workspace_bytes(b, qh, kvh, d, mp * p) > 0
+               for b, qh, kvh, d, mp in cases), "every case should split its rows"
+    ws = torch.zeros(need // 4, dtype=torch.float32, device="cuda")
+    for i, (batch, qh, kvh, d, max_pages) in enumerate(cases):
+        pages = batch * max_pages
+        k_pool = orc.f16(normal(430 + i, (pages, kvh, p, d)))
+        v_pool = orc.f16(normal(440 + i, (pages, kvh, p, d)))
+        q = orc.f16(normal(450 + i, (batch, qh * d)))
+        lengths = np.random.default_rng(460 + i).integers(1, max_pages * p + 1,
+                                                           size=batch).astype(np.int32)
+        tables = np.random.default_rng(470 + i).permutation(pages).astype(np.int32)
+        tables = tables.reshape(batch, max_pages)
+        out = torch.full((batch, qh * d), float("nan"), dtype=torch.float16, device="cuda")
+        active = torch.tensor([batch], dtype=torch.int32, device="cuda")
+        tmc.paged_decode_attention(dev_f16(q), dev_f16(k_pool), dev_f16(v_pool), dev(lengths),
+                                   dev(tables), active, out, batch, qh, kvh, d, p, max_pages,
+                                   kvh * p * d, p * d, ws)
+        torch.cuda.synchronize()
+        ref, written = orc.paged_attention(q, k_pool, v_pool, F16, qh, kvh, d, p, kvh * p * d,
+                                           p * d, tables, max_pages, lengths, batch)
+        assert written.all()
+        assert_f16_path(values(out), ref, what=f"workspace reuse, case {i} (b={batch}, d={d})")
+
+
 @pytest.mark.parametrize("d,p,qh,max_pages", [(64, 16, 8, 8), (128, 16, 8, 8), (128, 8, 8, 8),
                                                (128, 16, 4, 32), (128, 8, 4, 32)])
 def test_paged_attention_inactive_and_bad_pages_untouched(tmc, orc, torch, d, p, qh, max_pages):
@@ -1217,3 +1256,19 @@ def test_packed_gemm_residual_equals_gemm_then_add_bit_exact(tmc, orc, torch, ba
         y = rm
     torch.cuda.synchronize()
     assert np.array_equal(bits(y), bits(want))
+
+
+def test_attention_merge_launch_build(tmc, orc, torch):
+    """The build switch TMC_ATTN_MERGE_LAUNCH=1 (libtmc_hip_merge_launch.so)
+    merges every split row in a second launch, so no block reads partials
+    another block wrote in the same launch.  Its C3, C4 and workspace-reuse
+    results against the oracle, as for the default build."""
+    variant = tmc.open_variant("libtmc_hip_merge_launch.so")
+    saved = tmc._lib
+    tmc._lib = variant
+    try:
+        test_c3_contiguous_decode_attention(tmc, orc, torch, 4095)
+        test_c4_paged_gqa_attention(tmc, orc, torch)
+        test_paged_attention_workspace_reused_across_shapes(tmc, orc, torch)
+    finally:
+        tmc._lib = saved
