@@ -111,6 +111,11 @@ def _declare(l):
         "tmc_paged_gather_probe": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, i64,
                                          vp, vp]),
         "tmc_argmax_f32": (i32, [vp, vp, i64, i64, vp]),
+        "tmc_lm_head_argmax_workspace_bytes": (sz, [i64, i64]),
+        "tmc_rmsnorm_lm_head_partial_argmax_f16": (i32, [vp, vp, vp, vp, sz, i64, i64, f, vp, vp]),
+        "tmc_lm_head_partial_argmax_packed_norm_f16": (i32, [vp, vp, vp, sz, i64, i64, i64, f, i32,
+                                                              vp, vp]),
+        "tmc_lm_head_final_argmax": (i32, [vp, sz, vp, i64, i64, vp]),
         "tmc_fill_normal": (i32, [vp, i32, i64, C.c_uint64, f, f, vp]),
         "tmc_copy_bytes": (i32, [vp, vp, sz, vp]),
         "tmc_elementwise": (i32, [i32, vp, vp, vp, i32, i64, i32, vp]),
@@ -707,6 +712,35 @@ def argmax(logits, tokens, stream=None):
     rows, vocab = logits.shape
     check(lib().tmc_argmax_f32(_ptr(logits), _ptr(tokens), rows, vocab, _stream(stream)),
           "tmc_argmax_f32")
+
+
+def lm_head_argmax_workspace_bytes(rows, vocabulary) -> int:
+    return int(lib().tmc_lm_head_argmax_workspace_bytes(rows, vocabulary))
+
+
+def rmsnorm_lm_head_argmax(residual, gamma, w, workspace, tokens, eps, cfg=None, stream=None):
+    """Token-only batch-1 LM head: partial argmax of W * RMSNorm(residual)
+    (tmc_rmsnorm_lm_head_partial_argmax_f16), then the final argmax."""
+    _, k = residual.shape
+    n = w.shape[0]
+    nbytes = workspace.numel() * workspace.element_size()
+    check(lib().tmc_rmsnorm_lm_head_partial_argmax_f16(
+        _ptr(residual), _ptr(gamma), _ptr(w), _ptr(workspace), nbytes, k, n, eps, _cfg_ref(cfg),
+        _stream(stream)), "tmc_rmsnorm_lm_head_partial_argmax_f16")
+    check(lib().tmc_lm_head_final_argmax(_ptr(workspace), nbytes, _ptr(tokens), 1, n,
+                                         _stream(stream)), "tmc_lm_head_final_argmax")
+
+
+def lm_head_argmax_packed_norm(x, packed_scaled, workspace, tokens, batch, in_features,
+                               vocabulary, eps, layout=0, cfg=None, stream=None):
+    """Token-only batch > 1 LM head on packed gamma-scaled weights: partial
+    argmax (tmc_lm_head_partial_argmax_packed_norm_f16), then the final."""
+    nbytes = workspace.numel() * workspace.element_size()
+    check(lib().tmc_lm_head_partial_argmax_packed_norm_f16(
+        _ptr(x), _ptr(packed_scaled), _ptr(workspace), nbytes, batch, in_features, vocabulary, eps,
+        layout, _cfg_ref(cfg), _stream(stream)), "tmc_lm_head_partial_argmax_packed_norm_f16")
+    check(lib().tmc_lm_head_final_argmax(_ptr(workspace), nbytes, _ptr(tokens), batch,
+                                         vocabulary, _stream(stream)), "tmc_lm_head_final_argmax")
 
 
 def fill_normal(t, seed, mean=0.0, std=1.0, stream=None):

@@ -535,7 +535,7 @@ __global__ __launch_bounds__(kThreads) void decode_rope_append_h8_kernel(
 }
 
 __device__ __forceinline__ bool better(float cv, int ci, float bv, int bi) {
-  return cv > bv || (cv == bv && ci >= 0 && (bi < 0 || ci < bi));
+  return argmax_better(cv, ci, bv, bi);
 }
 
 // emitTokenArgmax (TransformerDecodeMetalEmitter.cpp:198-256): greedy
@@ -1021,6 +1021,66 @@ extern "C" int tmc_prefill_rope_append_rows(const void* qkv, const float* cosine
   return launch_rope_append(qkv, cosine, sine, valid_lengths, block_tables, active_count, q_out,
                             key_pool, value_pool, dtype, rows, q_heads, kv_heads, head_dim,
                             capacity, page_size, max_pages, true, row_table, table_rows, stream);
+}
+
+namespace tmc {
+namespace {
+// emitLMHeadFinalArgmax (DecoderLLMMetalEmitter.cpp:730-753): one block per
+// row folds the row's partial (value, index) slots, count from the
+// workspace header, in the greedy-token order.
+constexpr int kFinalArgmaxThreads = 256;
+__global__ __launch_bounds__(kFinalArgmaxThreads) void final_argmax_kernel(
+    void* workspace, int32_t* __restrict__ tokens, int rows, int cap) {
+  const ArgmaxPartials in = argmax_partials(workspace, rows, cap);
+  const int row = blockIdx.x;
+  const int count = min(*in.count, cap);
+  float best = -INFINITY;
+  int selected = -1;
+  for (int c = threadIdx.x; c < count; c += kFinalArgmaxThreads) {
+    const float v = in.values[(size_t)row * cap + c];
+    const int i = in.indices[(size_t)row * cap + c];
+    if (argmax_better(v, i, best, selected)) {
+      best = v;
+      selected = i;
+    }
+  }
+  argmax_wave(best, selected);
+  __shared__ float wv[kFinalArgmaxThreads / kWave];
+  __shared__ int wi[kFinalArgmaxThreads / kWave];
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    wv[wave] = best;
+    wi[wave] = selected;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kFinalArgmaxThreads / kWave; ++w)
+      if (argmax_better(wv[w], wi[w], best, selected)) {
+        best = wv[w];
+        selected = wi[w];
+      }
+    tokens[row] = selected;
+  }
+}
+}  // namespace
+}  // namespace tmc
+
+extern "C" size_t tmc_lm_head_argmax_workspace_bytes(int64_t rows, int64_t vocabulary) {
+  if (rows <= 0 || vocabulary <= 0 || rows >= (1LL << 20) || vocabulary >= (1LL << 28)) return 0;
+  return 256 + (size_t)rows * (size_t)vocabulary * (sizeof(float) + sizeof(int32_t));
+}
+
+extern "C" int tmc_lm_head_final_argmax(void* workspace, size_t workspace_bytes, int32_t* tokens,
+                                        int64_t rows, int64_t vocabulary, void* stream) {
+  TMC_REQUIRE(workspace && tokens, "LM head final argmax: null device pointer.");
+  TMC_REQUIRE(rows > 0 && vocabulary > 0 && rows < (1LL << 20) && vocabulary < (1LL << 28),
+              "LM head final argmax: invalid shape.");
+  TMC_REQUIRE(workspace_bytes >= tmc_lm_head_argmax_workspace_bytes(rows, vocabulary),
+              "LM head final argmax: workspace is smaller than "
+              "tmc_lm_head_argmax_workspace_bytes().");
+  hipLaunchKernelGGL(final_argmax_kernel, dim3((unsigned)rows), dim3(kFinalArgmaxThreads), 0,
+                     as_stream(stream), workspace, tokens, (int)rows, (int)vocabulary);
+  return check_launch("final_argmax_kernel");
 }
 
 extern "C" int tmc_argmax_f32(const float* logits, int32_t* tokens, int64_t rows,

@@ -258,13 +258,22 @@ __device__ __forceinline__ h8 norm_source(const NormArgs& na, int c) {
 }
 
 
-template <int MATS, int RPW, int NC, typename OutT, int FUSE, bool ROPE = false>
+// ARGMAX (the token-only LM head, emitLMHeadPartialArgmax,
+// DecoderLLMMetalEmitter.cpp:700-728): y is a partial-argmax workspace
+// (argmax_partials, one row of n_out slots): instead of storing the block's
+// logits, wave 0 keeps the greatest (value, row) of them in the greedy-token
+// order and writes it to slot blockIdx.x; block 0 writes the slot count.
+// The values are the logits the plain form stores, so the final argmax over
+// the slots is the argmax of those logits, ties and NaN included.
+template <int MATS, int RPW, int NC, typename OutT, int FUSE, bool ROPE = false,
+          bool ARGMAX = false>
 __global__ __launch_bounds__(256) void gemv_norm_kernel(const half_t* __restrict__ w0,
                                                        const half_t* __restrict__ w1,
                                                        OutT* __restrict__ y, int n_out, int k_in,
                                                        NormArgs na, RopeArgs ra) {
   static_assert(FUSE == kFuseAddNorm || FUSE == kFuseNorm, "a norm fusion");
   static_assert(!ROPE || (MATS == 1 && RPW == 2), "the RoPE epilogue takes one row pair");
+  static_assert(!ARGMAX || (MATS == 1 && !ROPE), "the argmax epilogue follows one matrix");
   static_assert(NC == 1 || NC == 2 || NC == 4, "1, 2 or 4 chunks per lane");
   // row groups in flight per wave, measured on the 7B shapes: 3 for the gated
   // pair (gate/up 28.2 against 30.5 us at 2), 2 for one matrix (q.k.v 16.4
@@ -391,6 +400,28 @@ __global__ __launch_bounds__(256) void gemv_norm_kernel(const half_t* __restrict
         odd += partial[w][s][0][1];
       }
       rope_append_pair(ra, 0, gg * RPW, even, odd);
+    }
+  } else if constexpr (ARGMAX) {
+    float best = -INFINITY;
+    int selected = -1;
+    for (int idx = lane; idx < slot * RPW; idx += kWave) {
+      const int s = idx / RPW, r = idx % RPW;
+      const int row = ((int)blockIdx.x + s * grid) * RPW + r;
+      if (row >= n_out) continue;
+      float a = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) a += partial[w][s][0][r];
+      if (argmax_better(a, row, best, selected)) {
+        best = a;
+        selected = row;
+      }
+    }
+    argmax_wave(best, selected);
+    if (lane == 0) {
+      const ArgmaxPartials out = argmax_partials(y, 1, n_out);
+      out.values[blockIdx.x] = best;
+      out.indices[blockIdx.x] = selected;
+      if (blockIdx.x == 0) *out.count = grid;
     }
   } else {
     for (int idx = lane; idx < slot * RPW; idx += kWave) {
@@ -699,10 +730,10 @@ int launch_dot_fused(const Shape& s, OutT* y, const tmc_gemv_config& c, const No
 // persistent grid holds at most the blocks resident at once (occupancy x
 // CUs, measured once per instance and device) and gives each block the same
 // number of row groups, at most 32 (its LDS partials).
-template <int MATS, int RPW, int NC, typename OutT, int FUSE, bool ROPE>
+template <int MATS, int RPW, int NC, typename OutT, int FUSE, bool ROPE, bool ARGMAX = false>
 int launch_norm_gemv_nc(const Shape& s, OutT* y, const NormArgs& na, const RopeArgs& ra,
                         hipStream_t st) {
-  auto kernel = gemv_norm_kernel<MATS, RPW, NC, OutT, FUSE, ROPE>;
+  auto kernel = gemv_norm_kernel<MATS, RPW, NC, OutT, FUSE, ROPE, ARGMAX>;
   static int resident[64] = {0};
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64)
@@ -726,13 +757,15 @@ int launch_norm_gemv_nc(const Shape& s, OutT* y, const NormArgs& na, const RopeA
   return check_launch("gemv_norm_kernel");
 }
 
-template <int MATS, int RPW, typename OutT, int FUSE, bool ROPE = false>
+template <int MATS, int RPW, typename OutT, int FUSE, bool ROPE = false, bool ARGMAX = false>
 int launch_norm_gemv_rpw(const Shape& s, OutT* y, const NormArgs& na, const RopeArgs& ra,
                          hipStream_t st) {
   const int chunks = s.k / 8;
-  if (chunks <= 256) return launch_norm_gemv_nc<MATS, RPW, 1, OutT, FUSE, ROPE>(s, y, na, ra, st);
-  if (chunks <= 512) return launch_norm_gemv_nc<MATS, RPW, 2, OutT, FUSE, ROPE>(s, y, na, ra, st);
-  return launch_norm_gemv_nc<MATS, RPW, 4, OutT, FUSE, ROPE>(s, y, na, ra, st);
+  if (chunks <= 256)
+    return launch_norm_gemv_nc<MATS, RPW, 1, OutT, FUSE, ROPE, ARGMAX>(s, y, na, ra, st);
+  if (chunks <= 512)
+    return launch_norm_gemv_nc<MATS, RPW, 2, OutT, FUSE, ROPE, ARGMAX>(s, y, na, ra, st);
+  return launch_norm_gemv_nc<MATS, RPW, 4, OutT, FUSE, ROPE, ARGMAX>(s, y, na, ra, st);
 }
 
 template <int MATS, typename OutT, int FUSE>
@@ -1108,6 +1141,39 @@ extern "C" int tmc_add_rmsnorm_gemv_f16(const void* residual, const void* update
                                         const tmc_gemv_config* config, void* stream) {
   return fused_entry(1, residual, update, gamma, w, nullptr, sum_out, y, y_dtype, batch,
                      in_features, out_features, epsilon, config, stream);
+}
+
+extern "C" int tmc_rmsnorm_lm_head_partial_argmax_f16(const void* residual, const void* gamma,
+                                                     const void* w, void* workspace,
+                                                     size_t workspace_bytes, int64_t in_features,
+                                                     int64_t vocabulary, float epsilon,
+                                                     const tmc_gemv_config* config, void* stream) {
+  const std::string what = "LM head partial argmax";
+  TMC_REQUIRE(residual && gamma && w && workspace, what + ": null device pointer.");
+  TMC_REQUIRE(in_features > 0 && vocabulary > 0 && in_features % 8 == 0 &&
+                  in_features <= 8 * kNormMaxChunks && vocabulary < (1LL << 28),
+              what + ": in_features must be a positive multiple of 8 up to 8192.");
+  TMC_REQUIRE((vocabulary + 1) * in_features * 2 < (int64_t)kBufferAbsent,
+              what + ": the weight matrix must stay below 4 GiB.");
+  TMC_REQUIRE(workspace_bytes >= tmc_lm_head_argmax_workspace_bytes(1, vocabulary),
+              what + ": workspace is smaller than tmc_lm_head_argmax_workspace_bytes().");
+  TMC_REQUIRE(aligned16(residual) && aligned16(gamma) && aligned16(w) && aligned16(workspace),
+              what + ": operands must be 16-byte aligned.");
+  TMC_REQUIRE(std::isfinite(epsilon) && epsilon > 0.0f, what + ": epsilon must be positive.");
+  int rpb = 2;
+  if (norm_config(config, what, 1, rpb)) return 1;
+  NormArgs na;
+  na.residual = static_cast<const half_t*>(residual);
+  na.gamma = static_cast<const half_t*>(gamma);
+  na.eps = epsilon;
+  Shape s{nullptr, static_cast<const half_t*>(w), nullptr, workspace, TMC_F32, 1, (int)vocabulary,
+          (int)in_features};
+  float* out = static_cast<float*>(workspace);
+  return rpb == 2
+             ? launch_norm_gemv_rpw<1, 2, float, kFuseNorm, false, true>(s, out, na, RopeArgs{},
+                                                                        as_stream(stream))
+             : launch_norm_gemv_rpw<1, 1, float, kFuseNorm, false, true>(s, out, na, RopeArgs{},
+                                                                        as_stream(stream));
 }
 
 extern "C" int tmc_add_rmsnorm_gate_up_silu_f16(const void* residual, const void* update,

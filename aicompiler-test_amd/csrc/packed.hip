@@ -94,6 +94,7 @@ enum PackedFuse : int { kPackedPlain = 0, kPackedNorm = 1, kPackedResidual = 2 }
 struct PackedFuseArgs {
   const half_t* residual = nullptr;  // kPackedResidual: this pass, in y's layout
   float eps = 0.0f;                  // kPackedNorm
+  int argmax_rows = 0;               // ARGMAX: rows of the partial-argmax workspace
 };
 
 // XP: x is one 16-row pass in fragment order (lane l of chunk c holds row
@@ -107,8 +108,14 @@ struct PackedFuseArgs {
 // defaults use 1-4).
 constexpr int kPackedNormWaves = 4;
 
+// ARGMAX (the token-only LM head, emitLMHeadPartialArgmax,
+// DecoderLLMMetalEmitter.cpp:700-728): y is a partial-argmax workspace
+// (argmax_partials, pf.argmax_rows rows of n_out slots); the tile writes,
+// for each batch row, the greatest (value, column) of its 16 logits in the
+// greedy-token order to slot blockIdx.x of that row, and block 0 writes the
+// slot count.  The values are the logits the plain form stores.
 template <int MATS, int U, typename OutT, bool XP = false, bool YP = false, bool ROPE = false,
-          int FUSE = kPackedPlain>
+          int FUSE = kPackedPlain, bool ARGMAX = false>
 __global__ __launch_bounds__(FUSE == kPackedNorm ? kPackedNormWaves * kWave : 1024) void packed_gemm_kernel(const half_t* __restrict__ x,
                                                            const half_t* __restrict__ p0,
                                                            const half_t* __restrict__ p1,
@@ -118,6 +125,8 @@ __global__ __launch_bounds__(FUSE == kPackedNorm ? kPackedNormWaves * kWave : 10
                                                            PackedFuseArgs pf) {
   static_assert(!ROPE || (MATS == 1 && !YP), "the RoPE epilogue serves the q.k.v projection");
   static_assert(FUSE != kPackedResidual || (MATS == 1 && !ROPE), "residual: plain projection");
+  static_assert(!ARGMAX || (MATS == 1 && !ROPE && !YP && FUSE != kPackedResidual),
+                "the argmax epilogue follows one fp32 projection");
   extern __shared__ float red[];  // [ks][MATS][4][64], then kPackedNorm: [ks][16] squares
   const int lane = threadIdx.x & (kWave - 1);
   const int ks = threadIdx.x / kWave;
@@ -215,6 +224,39 @@ __global__ __launch_bounds__(FUSE == kPackedNorm ? kPackedNormWaves * kWave : 10
     }
     return;
   }
+  if constexpr (ARGMAX) {
+    __shared__ float arg_v[16][16];
+    __shared__ int arg_i[16][16];
+    for (int idx = threadIdx.x; idx < 4 * kWave; idx += ks_count * kWave) {
+      const int l = idx % kWave, r = idx / kWave;
+      float a = 0.0f;
+      for (int w = 0; w < ks_count; ++w) a += red[(w * 4 + r) * kWave + l];
+      const int row = 4 * (l >> 4) + r;
+      const int col = nt * 16 + (l & 15);
+      arg_v[row][l & 15] = col < n_out ? from_float<OutT>(a * row_scale(row)) : -INFINITY;
+      arg_i[row][l & 15] = col < n_out ? col : -1;
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < 16 && (int)threadIdx.x < m_rows) {
+      const int row = threadIdx.x;
+      float best = -INFINITY;
+      int selected = -1;
+      for (int c = 0; c < 16; ++c)
+        if (argmax_better(arg_v[row][c], arg_i[row][c], best, selected)) {
+          best = arg_v[row][c];
+          selected = arg_i[row][c];
+        }
+      const ArgmaxPartials out = argmax_partials(y, pf.argmax_rows, n_out);
+      const size_t at = (size_t)(ra.request_base + row) * n_out + blockIdx.x;
+      out.values[at] = best;
+      out.indices[at] = selected;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0 && ra.request_base == 0) {
+      const ArgmaxPartials out = argmax_partials(y, pf.argmax_rows, n_out);
+      *out.count = (int)gridDim.x;
+    }
+    return;
+  }
   // acc[r] of lane (j, g) = out[batch 4g + r][row 16nt + j]
   for (int idx = threadIdx.x; idx < 4 * kWave; idx += ks_count * kWave) {
     const int l = idx % kWave, r = idx / kWave;
@@ -263,7 +305,8 @@ void default_packed(int64_t batch, int64_t n, int mats, int& unroll, int& ks) {
     ks = batch >= 8 ? 16 : 8;
 }
 
-template <int MATS, typename OutT, bool XP, bool YP, bool ROPE = false, int FUSE = kPackedPlain>
+template <int MATS, typename OutT, bool XP, bool YP, bool ROPE = false, int FUSE = kPackedPlain,
+          bool ARGMAX = false>
 int run_packed(const half_t* x, const half_t* p0, const half_t* p1, OutT* y, int64_t batch,
                int64_t k, int64_t n, int unroll, int ks, hipStream_t st,
                const RopeArgs& rope = RopeArgs{}, const PackedFuseArgs& fuse = PackedFuseArgs{}) {
@@ -276,21 +319,21 @@ int run_packed(const half_t* x, const half_t* p0, const half_t* p1, OutT* y, int
   for (int64_t r0 = 0; r0 < batch; r0 += 16) {
     const int rows = (int)std::min<int64_t>(16, batch - r0);
     const half_t* xs = x + (r0 / 16) * x_pass;
-    OutT* ys = ROPE ? y : y + (r0 / 16) * y_pass;
+    OutT* ys = ROPE || ARGMAX ? y : y + (r0 / 16) * y_pass;
     RopeArgs ra = rope;
     ra.request_base = (int)r0;
     PackedFuseArgs pf = fuse;
     if (FUSE == kPackedResidual) pf.residual = fuse.residual + (r0 / 16) * y_pass;
     if (unroll == 1)
-      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 1, OutT, XP, YP, ROPE, FUSE>), grid,
+      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 1, OutT, XP, YP, ROPE, FUSE, ARGMAX>), grid,
                          dim3(ks * kWave), lds, st, xs, p0, p1, ys, rows, (int)n, (int)k, ks,
                          (unsigned)bytes, ra, pf);
     else if (unroll == 2)
-      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 2, OutT, XP, YP, ROPE, FUSE>), grid,
+      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 2, OutT, XP, YP, ROPE, FUSE, ARGMAX>), grid,
                          dim3(ks * kWave), lds, st, xs, p0, p1, ys, rows, (int)n, (int)k, ks,
                          (unsigned)bytes, ra, pf);
     else
-      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 4, OutT, XP, YP, ROPE, FUSE>), grid,
+      hipLaunchKernelGGL((packed_gemm_kernel<MATS, 4, OutT, XP, YP, ROPE, FUSE, ARGMAX>), grid,
                          dim3(ks * kWave), lds, st, xs, p0, p1, ys, rows, (int)n, (int)k, ks,
                          (unsigned)bytes, ra, pf);
     if (check_launch("packed_gemm_kernel")) return 1;
@@ -567,6 +610,48 @@ extern "C" int tmc_gemm_packed_norm_f16(const void* x, const void* packed_w, voi
   pf.eps = epsilon;
   return packed_entry(1, x, packed_w, nullptr, y, y_dtype, batch, in_features, out_features,
                       layout, config, stream, kPackedNorm, pf);
+}
+
+extern "C" int tmc_lm_head_partial_argmax_packed_norm_f16(
+    const void* x, const void* packed_w, void* workspace, size_t workspace_bytes, int64_t batch,
+    int64_t in_features, int64_t vocabulary, float epsilon, int layout,
+    const tmc_gemv_config* config, void* stream) {
+  const std::string what = "Packed LM head partial argmax";
+  TMC_REQUIRE(x && packed_w && workspace, what + ": null device pointer.");
+  TMC_REQUIRE(epsilon > 0.0f && std::isfinite(epsilon), what + ": epsilon must be positive.");
+  TMC_REQUIRE(batch > 0 && in_features > 0 && vocabulary > 0 && batch < (1LL << 20) &&
+                  vocabulary < (1LL << 28) && in_features % 8 == 0,
+              what + ": dimensions must be positive and in_features a multiple of 8.");
+  TMC_REQUIRE((layout & ~TMC_LAYOUT_X_PACKED) == 0,
+              what + ": layout may only mark the input packed (TMC_LAYOUT_X_PACKED).");
+  TMC_REQUIRE(workspace_bytes >= tmc_lm_head_argmax_workspace_bytes(batch, vocabulary),
+              what + ": workspace is smaller than tmc_lm_head_argmax_workspace_bytes().");
+  TMC_REQUIRE(aligned16(x) && aligned16(packed_w) && aligned16(workspace),
+              what + ": operands must be 16-byte aligned.");
+  TMC_REQUIRE((uint64_t)packed_elements(vocabulary, in_features) * 2 < kNone &&
+                  (uint64_t)16 * in_features * 2 < kNone,
+              what + ": operands exceed the 4 GiB buffer range.");
+  int unroll, ks;
+  default_packed(batch, vocabulary, 1, unroll, ks);
+  ks = vocabulary >= 16384 ? std::min(ks, kPackedNormWaves) : kPackedNormWaves;
+  if (config && config->algorithm != 0) {
+    unroll = config->unroll;
+    ks = config->k_split;
+  }
+  TMC_REQUIRE((unroll == 1 || unroll == 2 || unroll == 4) && ks >= 1 && ks <= kPackedNormWaves,
+              what + ": config needs unroll 1|2|4 and k_split 1..4.");
+  PackedFuseArgs pf;
+  pf.eps = epsilon;
+  pf.argmax_rows = (int)batch;
+  const half_t* xs = static_cast<const half_t*>(x);
+  const half_t* w = static_cast<const half_t*>(packed_w);
+  float* out = static_cast<float*>(workspace);
+  const RopeArgs none{};
+  if (layout & TMC_LAYOUT_X_PACKED)
+    return run_packed<1, float, true, false, false, kPackedNorm, true>(
+        xs, w, w, out, batch, in_features, vocabulary, unroll, ks, as_stream(stream), none, pf);
+  return run_packed<1, float, false, false, false, kPackedNorm, true>(
+      xs, w, w, out, batch, in_features, vocabulary, unroll, ks, as_stream(stream), none, pf);
 }
 
 extern "C" int tmc_gate_up_silu_packed_norm_f16(const void* x, const void* packed_gate,

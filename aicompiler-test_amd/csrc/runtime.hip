@@ -1012,6 +1012,70 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     };
     return true;
   }
+  if (name == "rmsnorm_lm_head_partial_argmax") {
+    // Token-only LM head at batch 1 (emitLMHeadPartialArgmax): inputs the
+    // stored residual row, the final norm's gamma and W; output the
+    // partial-argmax workspace.
+    const int64_t k = param_int(p, "in"), n = param_int(p, "out");
+    const float eps = (float)param_double(p, "eps", 1e-6);
+    NEED(param_int(p, "batch", 1) == 1 && k > 0 && n > 0 && dt == TMC_F16,
+         "rmsnorm_lm_head_partial_argmax needs batch=1, in, out > 0 and f16.");
+    tmc_gemv_config cfg{};
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    const size_t ws = tmc_lm_head_argmax_workspace_bytes(1, n);
+    NEED(ws > 0, "rmsnorm_lm_head_partial_argmax: vocabulary out of range.");
+    s.inputs = {TMC_F16, TMC_F16, TMC_F16};
+    s.outputs = {TMC_F32};
+    s.counts = {(size_t)k, (size_t)k, (size_t)(n * k), ws / 4};
+    s.groups = (size_t)((n + 7) / 8);
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_rmsnorm_lm_head_partial_argmax_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], c.ptrs[3], ws,
+                                                    k, n, eps, &cfg, c.stream);
+    };
+    return true;
+  }
+  if (name == "lm_head_partial_argmax_packed") {
+    // Token-only LM head above batch 1 on the gamma-scaled packed weights:
+    // inputs x (x_layout) and W; output the partial-argmax workspace.
+    const int64_t b = param_int(p, "batch"), k = param_int(p, "in"), n = param_int(p, "out");
+    const float eps = (float)param_double(p, "eps", 1e-6);
+    NEED(b > 0 && k > 0 && n > 0 && dt == TMC_F16,
+         "lm_head_partial_argmax_packed needs batch, in, out > 0 and f16.");
+    tmc_gemv_config cfg{};
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    int layout = 0;
+    NEED(layout_param(p, layout) && !(layout & TMC_LAYOUT_Y_PACKED),
+         "lm_head_partial_argmax_packed: x_layout must be row_major or packed (no y_layout).");
+    const size_t ws = tmc_lm_head_argmax_workspace_bytes(b, n);
+    NEED(ws > 0, "lm_head_partial_argmax_packed: batch or vocabulary out of range.");
+    const size_t xc =
+        (size_t)((layout & TMC_LAYOUT_X_PACKED) ? tmc_packed_activation_elements(b, k) : b * k);
+    s.inputs = {TMC_F16, TMC_F16};
+    s.outputs = {TMC_F32};
+    s.counts = {xc, (size_t)tmc_packed_weight_elements(n, k), ws / 4};
+    s.groups = (size_t)((n + 15) / 16);
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_lm_head_partial_argmax_packed_norm_f16(c.ptrs[0], c.ptrs[1], c.ptrs[2], ws, b, k,
+                                                        n, eps, layout, &cfg, c.stream);
+    };
+    return true;
+  }
+  if (name == "lm_head_final_argmax") {
+    // emitLMHeadFinalArgmax: input the partial-argmax workspace, output the
+    // rows' tokens.
+    const int64_t rows = param_int(p, "rows"), v = param_int(p, "vocab");
+    const size_t ws = tmc_lm_head_argmax_workspace_bytes(rows, v);
+    NEED(rows > 0 && v > 0 && ws > 0, "lm_head_final_argmax needs rows and vocab.");
+    s.inputs = {TMC_F32};
+    s.outputs = {TMC_I32};
+    s.groups = (size_t)rows;
+    s.counts = {ws / 4, (size_t)rows};
+    s.launch = [=](const LaunchContext& c) {
+      return tmc_lm_head_final_argmax(c.ptrs[0], ws, static_cast<int32_t*>(c.ptrs[1]), rows, v,
+                                      c.stream);
+    };
+    return true;
+  }
   set_error("Unknown gfx950 kernel '" + name + "'.");
   return false;
 }

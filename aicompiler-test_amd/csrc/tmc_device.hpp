@@ -105,6 +105,48 @@ template <int FROM> __device__ __forceinline__ float cross_max(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Greedy-token order (emitTokenArgmax, TransformerDecodeMetalEmitter.cpp:
+// 198-256; emitLMHeadFinalArgmax, DecoderLLMMetalEmitter.cpp:730-753):
+// candidate (cv, ci) replaces the best (bv, bi) when larger, or equal with a
+// lower index; NaN never wins, and (-inf, -1) is the empty best.  The order
+// is total on the candidates it accepts, so any reduction tree over the
+// vocabulary gives the sequential scan's token.
+__device__ __forceinline__ bool argmax_better(float cv, int ci, float bv, int bi) {
+  return cv > bv || (cv == bv && ci >= 0 && (bi < 0 || ci < bi));
+}
+
+// Wave-wide argmax of (best, selected): every lane receives the winner.
+__device__ __forceinline__ void argmax_wave(float& best, int& selected) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(best, off, kWave);
+    const int oi = __shfl_xor(selected, off, kWave);
+    if (argmax_better(ov, oi, best, selected)) {
+      best = ov;
+      selected = oi;
+    }
+  }
+}
+
+// Partial-argmax workspace of the token-only LM heads: int32 count of
+// partials per row at the start, fp32 values [rows][cap] from byte 256, then
+// int32 indices [rows][cap].
+struct ArgmaxPartials {
+  int* count;
+  float* values;
+  int* indices;
+  int cap;
+};
+__device__ __forceinline__ ArgmaxPartials argmax_partials(void* workspace, int rows, int cap) {
+  char* base = static_cast<char*>(workspace);
+  ArgmaxPartials a;
+  a.count = reinterpret_cast<int*>(base);
+  a.values = reinterpret_cast<float*>(base + 256);
+  a.indices = reinterpret_cast<int*>(base + 256 + (size_t)rows * cap * sizeof(float));
+  a.cap = cap;
+  return a;
+}
+
 // Workgroup barrier ordering LDS only (__syncthreads() also waits for every
 // outstanding global load, e.g. for a weight stream still in flight).
 __device__ __forceinline__ void lds_barrier() {

@@ -9,6 +9,7 @@
 #include <cstring>
 #include <limits>
 #include <map>
+#include <mutex>
 #include <ostream>
 #include <sstream>
 #include <stdexcept>
@@ -324,6 +325,12 @@ struct BatchedDecodeExecutor::Bucket {
   std::vector<std::unique_ptr<hip::PreparedExecution>> steps;
   std::unique_ptr<hip::PreparedSequence> sequence;
   std::vector<std::size_t> uses;  // registry usage entries of this bucket
+  // Token-only tail (partial + final argmax) and the sequence of the trunk
+  // steps followed by it; null when the bucket has none.
+  std::vector<std::unique_ptr<hip::PreparedExecution>> tokenSteps;
+  std::unique_ptr<hip::PreparedSequence> tokenSequence;
+  bool tokenChecked = false, tokenAdmitted = false;
+  double tokenSpeedup = 0.0;
 };
 
 BatchedDecodeExecutor::~BatchedDecodeExecutor() = default;
@@ -382,6 +389,9 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
   mlp_ = act(M * H);
   logits_ = act(M * V, ElementType::Float32);
   nextTokens_ = act(M, ElementType::Int32);
+  argmaxWorkspace_ = act(tmc_lm_head_argmax_workspace_bytes(static_cast<int64_t>(M),
+                                                            static_cast<int64_t>(V)) / 4,
+                         ElementType::Float32);
 
   std::vector<std::size_t> rows;
   for (std::size_t r = 1; r < M; r *= 2) rows.push_back(r);
@@ -694,6 +704,33 @@ void BatchedDecodeExecutor::build(std::ostream* log) {
     auto sequence = rt.prepareSequence(pointers);
     if (!sequence.execution) throw std::runtime_error(sequence.errorMessage);
     bucket->sequence = std::move(sequence.execution);
+    if (fold || foldPacked) {
+      // Token-only tail: the LM head with a partial argmax, then the final
+      // argmax, after the same trunk (every step but the LM head and argmax).
+      const std::size_t trunk = bucket->steps.size() - 2;
+      const std::string vs = std::to_string(V), hs = std::to_string(H);
+      if (fold)
+        add("rmsnorm_lm_head_partial_argmax?in=" + hs + "&out=" + vs + "&eps=" + eps,
+            "lm_head_partial_argmax",
+            {residual_, model_->finalNormWeight, model_->languageModelHeadWeight},
+            {argmaxWorkspace_});
+      else
+        add("lm_head_partial_argmax_packed?batch=" + B + "&in=" + hs + "&out=" + vs + "&eps=" +
+                eps + "&x_layout=packed",
+            "lm_head_partial_argmax", {residual_, model_->normScaledLanguageModelHead},
+            {argmaxWorkspace_});
+      add("lm_head_final_argmax?rows=" + B + "&vocab=" + vs, "lm_head_final_argmax",
+          {argmaxWorkspace_}, {nextTokens_});
+      for (std::size_t i = bucket->steps.size() - 2; i < bucket->steps.size(); ++i)
+        bucket->tokenSteps.push_back(std::move(bucket->steps[i]));
+      bucket->steps.resize(bucket->steps.size() - 2);
+      std::vector<const hip::PreparedExecution*> tokenPointers(pointers.begin(),
+                                                               pointers.begin() + trunk);
+      for (const auto& step : bucket->tokenSteps) tokenPointers.push_back(step.get());
+      auto tokens = rt.prepareSequence(tokenPointers);
+      if (!tokens.execution) throw std::runtime_error(tokens.errorMessage);
+      bucket->tokenSequence = std::move(tokens.execution);
+    }
     if (log)
       *log << "Batched decode bucket rows=" << m << ": " << bucket->steps.size()
            << " dispatches captured\n";
@@ -848,7 +885,9 @@ std::string BatchedDecodeExecutor::launchChained(
   error = upload(tokenIds.empty() ? placeholder : tokenIds, validLengths, blockTables, rows,
                  bucket.rows);
   if (error.empty() && tokenIds.empty()) error = tokensView_->copyFromAsync(*nextTokens_, rows);
-  if (error.empty()) error = bucket.sequence->launch();
+  hip::PreparedSequence* sequence = nullptr;
+  if (error.empty()) error = stepSequence(bucket, false, sequence);
+  if (error.empty()) error = sequence->launch();
   if (error.empty() && registry_) registry_->completed(bucket.uses);
   if (error.empty())
     error = history_->copyFromAsync(*nextTokens_, rows, historyStep * maximumBatchSize_);
@@ -862,6 +901,120 @@ std::string BatchedDecodeExecutor::readHistory(std::size_t steps,
   if (steps == 0 || steps > historySteps_) return "Chained decode history range is invalid.";
   out.assign(steps * maximumBatchSize_, 0);
   return history_->readRaw(out.data(), out.size());  // waits for the stream
+}
+
+namespace {
+// Token-only admissions per process: key = model dimensions, bucket rows and
+// fold form; value = (admitted, measured speedup, 0 when untimed).
+std::mutex g_token_mutex;
+std::map<std::string, std::pair<bool, double>> g_token_decisions;
+}  // namespace
+
+std::string BatchedDecodeExecutor::tokenOnlyKey(const Bucket& bucket) const {
+  const auto& plan = model_->plan;
+  std::ostringstream key;
+  key << "H" << plan.hiddenSize() << "_I" << plan.intermediateSize << "_V"
+      << plan.vocabularySize << "_L" << plan.layerCount << "_QH" << plan.attention.heads << "_KVH"
+      << plan.kvHeads() << "_D" << plan.attention.headDimension << "_cap"
+      << plan.attention.capacity << "_page" << pageSize_ << "_rows" << bucket.rows
+      << (bucket.rows > 1 ? "_packed" : "_dot");
+  return key.str();
+}
+
+std::string BatchedDecodeExecutor::checkTokenOnly(Bucket& bucket) {
+  bucket.tokenChecked = true;
+  bucket.tokenAdmitted = false;
+  if (!bucket.tokenSequence || tokenPolicy_ == TokenOnlyPolicy::Never) return {};
+  const std::string key = tokenOnlyKey(bucket);
+  if (tokenPolicy_ != TokenOnlyPolicy::Always) {
+    std::lock_guard<std::mutex> lock(g_token_mutex);
+    const auto known = g_token_decisions.find(key);
+    if (known != g_token_decisions.end()) {
+      bucket.tokenAdmitted = known->second.first;
+      bucket.tokenSpeedup = known->second.second;
+      return {};
+    }
+  }
+  if (tokenPolicy_ == TokenOnlyPolicy::CachedOnly) {
+    bucket.tokenChecked = false;  // decided by a later admission, if any
+    return {};
+  }
+  // Both sequences write the same staged K/V slots and read the same
+  // uploaded metadata, so replaying the step is safe and appends nothing.
+  const std::size_t rows = bucket.rows;
+  std::vector<std::int32_t> expected(rows), actual(rows);
+  auto baseline = bucket.sequence->execute();
+  if (!baseline.executionPassed) return baseline.errorMessage;
+  auto error = nextTokens_->readRaw(expected.data(), rows);
+  if (!error.empty()) return error;
+  auto candidate = bucket.tokenSequence->execute();
+  if (!candidate.executionPassed) return candidate.errorMessage;
+  error = nextTokens_->readRaw(actual.data(), rows);
+  if (!error.empty()) return error;
+  if (actual != expected) {  // tokens disagree: keep the logits tail
+    std::lock_guard<std::mutex> lock(g_token_mutex);
+    g_token_decisions[key] = {false, 0.0};
+    return {};
+  }
+  if (tokenPolicy_ == TokenOnlyPolicy::Always) {
+    bucket.tokenAdmitted = true;
+    return {};
+  }
+  const auto base = benchmark::sampler(*bucket.sequence);
+  const auto cand = benchmark::sampler(*bucket.tokenSequence);
+  error = benchmark::warmup(cand, 5);
+  if (!error.empty()) return error;
+  const auto first = benchmark::measurePair(base, cand, 31);
+  const auto second = benchmark::measurePair(base, cand, 31);
+  if (first.passed && second.passed) {
+    bucket.tokenSpeedup = std::min(first.speedup, second.speedup);
+    bucket.tokenAdmitted = bucket.tokenSpeedup >= planner::kMinimumSpeedup;
+  }
+  std::lock_guard<std::mutex> lock(g_token_mutex);
+  g_token_decisions[key] = {bucket.tokenAdmitted, bucket.tokenSpeedup};
+  // the last replay was the token sequence: its tokens equal the logits tail's
+  return {};
+}
+
+std::string BatchedDecodeExecutor::stepSequence(Bucket& bucket, bool readLogits,
+                                                hip::PreparedSequence*& sequence) {
+  sequence = bucket.sequence.get();
+  if (readLogits || !bucket.tokenSequence || tokenPolicy_ == TokenOnlyPolicy::Never) return {};
+  if (!bucket.tokenChecked) {
+    const auto error = checkTokenOnly(bucket);
+    if (!error.empty()) return error;
+  }
+  if (bucket.tokenAdmitted) sequence = bucket.tokenSequence.get();
+  return {};
+}
+
+std::string BatchedDecodeExecutor::admitTokenOnly(
+    const std::vector<std::int32_t>& tokenIds, const std::vector<std::int32_t>& validLengths,
+    const std::vector<std::vector<std::int32_t>>& blockTables) {
+  const std::size_t rows = tokenIds.size();
+  auto error = checkStep(&tokenIds, validLengths, blockTables);
+  if (!error.empty()) return error;
+  std::size_t index = 0;
+  while (buckets_[index]->rows < rows) ++index;
+  auto& bucket = *buckets_[index];
+  if (bucket.tokenChecked || !bucket.tokenSequence) return {};
+  error = upload(tokenIds, validLengths, blockTables, rows, bucket.rows);
+  if (!error.empty()) return error;
+  return checkTokenOnly(bucket);
+}
+
+BatchedDecodeExecutor::TokenOnlyStatus BatchedDecodeExecutor::tokenOnlyStatus(
+    std::size_t rows) const {
+  TokenOnlyStatus status;
+  for (const auto& b : buckets_)
+    if (b->rows >= rows) {  // the bucket a step of `rows` rows runs
+      status.available = b->tokenSequence != nullptr;
+      status.checked = b->tokenChecked;
+      status.admitted = b->tokenAdmitted;
+      status.speedup = b->tokenSpeedup;
+      break;
+    }
+  return status;
 }
 
 BatchedDecodeRun BatchedDecodeExecutor::run(const std::vector<std::int32_t>& tokenIds,
@@ -881,8 +1034,14 @@ BatchedDecodeRun BatchedDecodeExecutor::run(const std::vector<std::int32_t>& tok
     result.errorMessage = error;
     return result;
   }
+  hip::PreparedSequence* sequence = nullptr;
+  error = stepSequence(bucket, readLogits, sequence);
+  if (!error.empty()) {
+    result.errorMessage = error;
+    return result;
+  }
   if (timeGpu) {
-    const auto execution = bucket.sequence->execute();
+    const auto execution = sequence->execute();
     if (!execution.executionPassed) {
       result.errorMessage = execution.errorMessage;
       return result;
@@ -890,7 +1049,7 @@ BatchedDecodeRun BatchedDecodeExecutor::run(const std::vector<std::int32_t>& tok
     result.gpuExecutionTimeUs = execution.gpuExecutionTimeUs;
     result.cpuSubmitToCompletionTimeUs = execution.cpuSubmitToCompletionTimeUs;
   } else {
-    error = bucket.sequence->launch();
+    error = sequence->launch();
     if (!error.empty()) {
       result.errorMessage = error;
       return result;

@@ -226,6 +226,36 @@ class BatchedDecodeExecutor {
                                           std::size_t historyStep);
   [[nodiscard]] std::string readHistory(std::size_t steps, std::vector<std::int32_t>& out) const;
 
+  // Token-only steps (DecoderLLMExecutor.cpp:837-845,906-931): the folded
+  // buckets (batch 1 with the norms folded, batch > 1 on packed weights)
+  // also hold a second sequence whose tail is the LM head with a partial
+  // argmax and a final argmax instead of the fp32 logits and the argmax.  A
+  // step that reads no logits (run with readLogits false, every chained
+  // step) uses it once admitted: at the bucket's first such step both
+  // sequences replay the staged step (they append the same K/V), the tokens
+  // must agree, and the token sequence must time >= 1.05x faster in two
+  // paired rounds of 31 samples.  admitTokenOnly runs that check for the
+  // bucket of these rows now (uploading their metadata), outside a timed
+  // phase.  Decisions are kept per process and shape (model dimensions,
+  // bucket rows, fold form), so a later executor of the same shape reuses
+  // them.  TokenOnlyPolicy::Always skips the timing (tokens must still
+  // agree), Never keeps the logits tail, CachedOnly uses the token tail only
+  // where an earlier admission of this shape admitted it and never times
+  // during steps (the serving loop's policy: no admission inside its ticks).
+  enum class TokenOnlyPolicy { Admission, Always, Never, CachedOnly };
+  void setTokenOnlyPolicy(TokenOnlyPolicy policy) noexcept { tokenPolicy_ = policy; }
+  [[nodiscard]] std::string admitTokenOnly(const std::vector<std::int32_t>& tokenIds,
+                                           const std::vector<std::int32_t>& validLengths,
+                                           const std::vector<std::vector<std::int32_t>>& blockTables);
+  struct TokenOnlyStatus {
+    bool available = false;  // the bucket has a token-only sequence
+    bool checked = false;
+    bool admitted = false;
+    double speedup = 0.0;    // min of the two paired rounds (0 when not timed)
+  };
+  // status of the bucket that runs steps of `rows` rows
+  [[nodiscard]] TokenOnlyStatus tokenOnlyStatus(std::size_t rows) const;
+
   [[nodiscard]] std::size_t maximumBatchSize() const noexcept { return maximumBatchSize_; }
   [[nodiscard]] std::size_t maxPages() const noexcept { return maxPages_; }
   [[nodiscard]] std::size_t activationStorageBytes() const noexcept { return activationBytes_; }
@@ -253,6 +283,12 @@ class BatchedDecodeExecutor {
                                       const std::vector<std::vector<std::int32_t>>& blockTables) const;
 
   struct Bucket;
+  // The sequence a step of `bucket` replays (metadata already uploaded).
+  [[nodiscard]] std::string stepSequence(Bucket& bucket, bool readLogits,
+                                         hip::PreparedSequence*& sequence);
+  [[nodiscard]] std::string checkTokenOnly(Bucket& bucket);
+  [[nodiscard]] std::string tokenOnlyKey(const Bucket& bucket) const;
+  TokenOnlyPolicy tokenPolicy_ = TokenOnlyPolicy::Admission;
   hip::HipRuntime* runtime_ = nullptr;
   std::shared_ptr<DecoderLLMModelResources> model_;
   std::vector<std::shared_ptr<KVPagePool>> pools_;
@@ -271,6 +307,7 @@ class BatchedDecodeExecutor {
   std::vector<hip::BufferHandle> tableViews_;
   hip::BufferHandle residual_, after_, normalized_, qkv_, query_, context_, projected_, gated_,
       mlp_, logits_, nextTokens_;
+  hip::BufferHandle argmaxWorkspace_;  // partial-argmax slots of the token-only tail
   std::vector<std::unique_ptr<Bucket>> buckets_;
   std::vector<std::int32_t> metaShadow_, tableShadow_;
   hip::BufferHandle history_;  // int32 [steps][M], chained decode

@@ -493,6 +493,9 @@ ServingExecutionResult runContinuousBatch(hip::HipRuntime& runtime,
     auto created = createBatchedDecodeExecutor(runtime, model, pools, M, &log, config.tuneKernels);
     if (!created.executor) throw std::runtime_error(created.errorMessage);
     auto& executor = *created.executor;
+    // ticks that read no logits take the token-only tail where an earlier
+    // admission of this shape admitted it; no candidate is timed mid-run
+    executor.setTokenOnlyPolicy(BatchedDecodeExecutor::TokenOnlyPolicy::CachedOnly);
     BatchedStep step = [&executor](const std::vector<std::int32_t>& tokens,
                                    const std::vector<std::int32_t>& lengths,
                                    const std::vector<std::vector<std::int32_t>>& tables,
@@ -709,9 +712,22 @@ DecodeThroughput measureDecodeThroughput(hip::HipRuntime& runtime,
     for (std::size_t r = 0; r < B; ++r)
       for (std::size_t s = 0; s < decodeTokens; ++s) kvTokens += prompts[r].size() + 1 + s;
     result.kvBytesRead = kvTokens * L * 2 * plan.kvWidth() * 2;
-    if (!timeGpu && decodeTokens > 0) {
-      const auto error = executor.reserveHistory(decodeTokens);
+    if (decodeTokens > 0) {
+      if (!timeGpu) {
+        const auto error = executor.reserveHistory(decodeTokens);
+        if (!error.empty()) throw std::runtime_error(error);
+      }
+      // The token-only admission of the decode bucket (both tails replay the
+      // first decode step at its staged length), outside the timed phase.
+      std::vector<std::int32_t> lengths;
+      std::vector<std::vector<std::int32_t>> tables;
+      stage(all, lengths, tables);
+      const auto error = executor.admitTokenOnly(last, lengths, tables);
       if (!error.empty()) throw std::runtime_error(error);
+      const auto status = executor.tokenOnlyStatus(B);
+      result.tokenOnlyAvailable = status.available;
+      result.tokenOnlyAdmitted = status.admitted;
+      result.tokenOnlySpeedup = status.speedup;
     }
     const auto decodeStart = Clock::now();
     if (timeGpu) {

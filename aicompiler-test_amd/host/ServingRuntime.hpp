@@ -159,6 +159,10 @@ struct DecodeThroughput {
   benchmark::Statistics stepHost;
   std::vector<std::vector<float>> generatedTokenIds;  // per row
   std::size_t kvBytesRead = 0;     // K/V bytes the timed attention steps read
+  // token-only tail of the decode bucket (BatchedDecodeExecutor::admitTokenOnly)
+  bool tokenOnlyAvailable = false;
+  bool tokenOnlyAdmitted = false;
+  double tokenOnlySpeedup = 0.0;
   std::string errorMessage;
 };
 

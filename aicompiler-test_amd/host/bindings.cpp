@@ -433,7 +433,58 @@ PYBIND11_MODULE(_tmc_host, m) {
       .def("max_pages", &BatchedDecodeExecutor::maxPages)
       .def("buckets", &BatchedDecodeExecutor::buckets)
       .def("dispatches_per_step", &BatchedDecodeExecutor::dispatchesPerStep)
-      .def("activation_storage_bytes", &BatchedDecodeExecutor::activationStorageBytes);
+      .def("activation_storage_bytes", &BatchedDecodeExecutor::activationStorageBytes)
+      .def("set_token_only_policy",
+           [](BatchedDecodeExecutor& e, const std::string& policy) {
+             using P = BatchedDecodeExecutor::TokenOnlyPolicy;
+             if (policy == "admission") e.setTokenOnlyPolicy(P::Admission);
+             else if (policy == "always") e.setTokenOnlyPolicy(P::Always);
+             else if (policy == "never") e.setTokenOnlyPolicy(P::Never);
+             else if (policy == "cached_only") e.setTokenOnlyPolicy(P::CachedOnly);
+             else throw std::invalid_argument("policy: admission | always | never | cached_only");
+           })
+      .def("admit_token_only",
+           [](BatchedDecodeExecutor& e, const std::vector<std::int32_t>& tokens,
+              const std::vector<std::int32_t>& lengths,
+              const std::vector<std::vector<std::int32_t>>& tables) {
+             std::string error;
+             {
+               py::gil_scoped_release release;
+               error = e.admitTokenOnly(tokens, lengths, tables);
+             }
+             if (!error.empty()) throw std::runtime_error(error);
+           })
+      .def("token_only_status", [](const BatchedDecodeExecutor& e, std::size_t rows) {
+        const auto st = e.tokenOnlyStatus(rows);
+        py::dict d;
+        d["available"] = st.available;
+        d["checked"] = st.checked;
+        d["admitted"] = st.admitted;
+        d["speedup"] = st.speedup;
+        return d;
+      })
+      .def("reserve_history",
+           [](BatchedDecodeExecutor& e, std::size_t steps) {
+             const auto error = e.reserveHistory(steps);
+             if (!error.empty()) throw std::runtime_error(error);
+           })
+      .def("launch_chained",
+           [](BatchedDecodeExecutor& e, const std::vector<std::int32_t>& tokens,
+              const std::vector<std::int32_t>& lengths,
+              const std::vector<std::vector<std::int32_t>>& tables, std::size_t step) {
+             std::string error;
+             {
+               py::gil_scoped_release release;
+               error = e.launchChained(tokens, lengths, tables, step);
+             }
+             if (!error.empty()) throw std::runtime_error(error);
+           })
+      .def("read_history", [](const BatchedDecodeExecutor& e, std::size_t steps) {
+        std::vector<std::int32_t> out;
+        const auto error = e.readHistory(steps, out);
+        if (!error.empty()) throw std::runtime_error(error);
+        return out;
+      });
 
   m.def("create_batched_decode_executor",
         [](hip::HipRuntime& rt, std::shared_ptr<DecoderLLMModelResources> model,
@@ -692,6 +743,9 @@ PYBIND11_MODULE(_tmc_host, m) {
           d["step_host"] = statsToDict(r.stepHost);
           d["generated_token_ids"] = r.generatedTokenIds;
           d["kv_bytes_read"] = r.kvBytesRead;
+          d["token_only_available"] = r.tokenOnlyAvailable;
+          d["token_only_admitted"] = r.tokenOnlyAdmitted;
+          d["token_only_speedup"] = r.tokenOnlySpeedup;
           return d;
         },
         py::arg("runtime"), py::arg("model"), py::arg("prompts"), py::arg("decode_tokens"),

@@ -415,6 +415,10 @@ def c5_gpu(tmc) -> dict:
         out[f"b{batch}_prompt_tokens"] = sum(len(p) for p in c5_prompts(batch))
         out[f"b{batch}_prompt_ms"] = round(r["prompt_phase_us"] / 1e3, 2)
         out[f"b{batch}_prompt_tokens_per_s"] = round(r["prompt_tokens_per_second"], 1)
+        # the token-only LM head tail (partial + final argmax), admitted only
+        # at >= 1.05x over the logits tail in two paired rounds
+        out[f"b{batch}_token_only"] = {"admitted": r["token_only_admitted"],
+                                        "speedup": round(r["token_only_speedup"], 4)}
         print(f"[bench] C5 batch {batch}: {out[f'b{batch}_tokens_per_s']} tokens/s, prompts "
               f"{out[f'b{batch}_prompt_tokens_per_s']} tokens/s", flush=True)
         out[f"b{batch}_serving"] = c5_serving(host, rt, model, batch)

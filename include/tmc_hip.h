@@ -716,6 +716,40 @@ int tmc_prefill_attention_rows_f16(const void *q, const void *key_pool, const vo
 int tmc_argmax_f32(const float *logits, int32_t *tokens, int64_t rows, int64_t vocabulary,
                    void *stream);
 
+/* Token-only LM head (the decode step's tail when no logits are read,
+ * DecoderLLMExecutor.cpp:837-845,929-930): a partial pass computes the LM
+ * head's logits and keeps, per block, the greatest (value, index) in the
+ * greedy-token order (ties to the lowest index, NaN never selected) in a
+ * workspace of partial slots; the final pass folds each row's slots into its
+ * token.  The tokens equal tmc_argmax_f32 over the logits the same LM head
+ * writes.  Workspace layout: int32 slot count at byte 0, fp32 values
+ * [rows][vocabulary] from byte 256, then int32 indices [rows][vocabulary]. */
+size_t tmc_lm_head_argmax_workspace_bytes(int64_t rows, int64_t vocabulary);
+
+/* emitLMHeadPartialArgmax (DecoderLLMMetalEmitter.cpp:700-728) for batch 1
+ * with the final RMSNorm folded in, as tmc_add_rmsnorm_gemv_f16 without an
+ * update: logits of W [vocabulary, in_features] times the normalized
+ * residual, reduced to partial slots. */
+int tmc_rmsnorm_lm_head_partial_argmax_f16(const void *residual, const void *gamma,
+                                           const void *w, void *workspace, size_t workspace_bytes,
+                                           int64_t in_features, int64_t vocabulary, float epsilon,
+                                           const tmc_gemv_config *config, void *stream);
+
+/* emitLMHeadPartialArgmax for batch > 1 on fragment-packed weights with the
+ * final norm folded in (as tmc_gemm_packed_norm_f16 with an fp32 output;
+ * layout 0 or TMC_LAYOUT_X_PACKED): one slot per 16-row tile of W per
+ * batch row. */
+int tmc_lm_head_partial_argmax_packed_norm_f16(const void *x, const void *packed_w,
+                                               void *workspace, size_t workspace_bytes,
+                                               int64_t batch, int64_t in_features,
+                                               int64_t vocabulary, float epsilon, int layout,
+                                               const tmc_gemv_config *config, void *stream);
+
+/* emitLMHeadFinalArgmax (DecoderLLMMetalEmitter.cpp:730-753): tokens[row]
+ * from the row's partial slots. */
+int tmc_lm_head_final_argmax(void *workspace, size_t workspace_bytes, int32_t *tokens,
+                             int64_t rows, int64_t vocabulary, void *stream);
+
 /* Synthetic data: fill `count` elements with N(mean, std) values from a
  * counter-based generator (splitmix64 + Box-Muller) keyed by `seed`. */
 int tmc_fill_normal(void *ptr, int dtype, int64_t count, uint64_t seed, float mean, float std,

@@ -478,3 +478,73 @@ def test_tuned_executor_matches_default_and_caches_shapes(host, orc, rt):
         assert host.decode_gemv_cache_size() == (0 if not tune else len(shapes))
     assert_f16_path(runs[1], runs[0], "tuned vs default")
     np.testing.assert_array_equal(runs[2], runs[1])  # the cached selection is the same
+
+
+def test_token_only_tail_matches_logits_tail(host, orc, rt):
+    """The token-only tail (LM head partial argmax + final argmax,
+    DecoderLLMExecutor.cpp:837-845) gives the logits tail's tokens step for
+    step: two executors over the same weights and histories, one forced to
+    the logits tail ("never"), one to the token tail ("always"), steps of 1,
+    3 and 5 rows (the one-row bucket folds the norms into the dot GEMV, the
+    others run the packed GEMM) with no logits read; every token also agrees
+    with the oracle's decoder step.  A third executor under the admission
+    rule times both tails on its first logits-free step and records the
+    decision and the speedup (two paired rounds)."""
+    cfg = CONFIGS["serve"]
+    m = _weights(orc, cfg, 91)
+    w = _workload(host, orc, cfg, m)
+    model = host.create_model_resources(rt, w)
+    pages, L, V = 64, cfg["layers"], cfg["vocabulary"]
+    execs, all_states = [], []
+    for policy in ("never", "always"):
+        pools = [host.create_kv_page_pool(rt, w.plan.kv_plan(), P, pages) for _ in range(L)]
+        ex = host.create_batched_decode_executor(rt, model, pools, 5)
+        ex.set_token_only_policy(policy)
+        execs.append(ex)
+        all_states.append([[host.create_kv_cache_state(rt, w.plan.kv_plan(), pools[l], False)
+                            for l in range(L)] for _ in range(5)])
+    refs = [OracleRequest(orc, cfg, m, pages) for _ in range(5)]
+    rng = np.random.default_rng(92)
+    tokens = [int(t) for t in rng.integers(0, V, 5)]
+    lengths = [0] * 5
+    for rows in (1, 3, 5, 5, 1, 3):
+        got = []
+        for ex, states in zip(execs, all_states):
+            tables = [[] for _ in range(L)]
+            for r in range(rows):
+                for l, s in enumerate(states[r]):
+                    assert s.stage_length(rt, lengths[r] + 1) == ""
+                    tables[l] += s.page_table() + [-1] * (ex.max_pages() - len(s.page_table()))
+            out = ex.run(tokens[:rows], [n + 1 for n in lengths[:rows]], tables, False, False)
+            assert out["passed"], out["error"]
+            assert len(out["logits"]) == 0
+            for r in range(rows):
+                for s in states[r]:
+                    s.commit_length(lengths[r] + 1)
+            got.append([int(t) for t in out["next_token_ids"]])
+        assert got[0] == got[1], rows
+        for r in range(rows):
+            logits, nxt = refs[r].step(tokens[r], lengths[r] + 1,
+                                       [s.page_table() for s in all_states[0][r]])
+            _check_token(got[1][r], nxt, logits, f"{rows} rows, row {r}")
+            lengths[r] += 1
+            tokens[r] = got[1][r]
+    for rows in (1, 3, 5):
+        st = execs[1].token_only_status(rows)
+        assert st["available"] and st["checked"] and st["admitted"], (rows, st)
+        assert not execs[0].token_only_status(rows)["admitted"]
+    # the admission rule: both tails timed on the first logits-free step
+    pools = [host.create_kv_page_pool(rt, w.plan.kv_plan(), P, pages) for _ in range(L)]
+    ex = host.create_batched_decode_executor(rt, model, pools, 2)
+    states = [host.create_kv_cache_state(rt, w.plan.kv_plan(), pools[l], False) for l in range(L)]
+    for s in states:
+        assert s.stage_length(rt, 1) == ""
+    tables = [s.page_table() + [-1] * (ex.max_pages() - len(s.page_table())) for s in states]
+    ex.admit_token_only([7], [1], tables)
+    st = ex.token_only_status(1)
+    assert st["checked"] and st["speedup"] > 0.0
+    assert st["admitted"] == (st["speedup"] >= 1.05)
+    out = ex.run([7], [1], tables, False, False)
+    assert out["passed"], out["error"]
+    logits, nxt = OracleRequest(orc, cfg, m, pages).step(7, 1, [s.page_table() for s in states])
+    _check_token(int(out["next_token_ids"][0]), nxt, logits, "admission executor")

@@ -1272,3 +1272,89 @@ def test_attention_merge_launch_build(tmc, orc, torch):
         test_paged_attention_workspace_reused_across_shapes(tmc, orc, torch)
     finally:
         tmc._lib = saved
+
+
+# ---------------------------------------------------------------- token-only LM head
+def _lm_head_inputs(orc, batch, k, vocab, seed):
+    """Residual rows, gamma and an LM head W with planted duplicates: rows 5
+    and vocab - 1 equal row 17 (exact ties of the same logit), and row 9
+    holds an fp16 NaN (its logit is NaN and is never selected)."""
+    s = orc.f16(normal(seed, (batch, k)))
+    gamma = orc.f16(uniform(seed + 1, (k,), 0.5, 1.5))
+    w = orc.f16(normal(seed + 2, (vocab, k), 0.02))
+    w[5] = w[17]
+    w[vocab - 1] = w[17]
+    w[9, 3] = 0x7E00  # NaN
+    return s, gamma, w
+
+
+@pytest.mark.parametrize("vocab", [32000, 4099, 5])
+def test_lm_head_token_only_batch1(tmc, orc, torch, vocab):
+    """tmc_rmsnorm_lm_head_partial_argmax_f16 + tmc_lm_head_final_argmax
+    equal the logits path (tmc_add_rmsnorm_gemv_f16, fp32 logits, then
+    tmc_argmax_f32) token for token, ties to the lowest index and NaN never
+    chosen; with row 17's logit raised to the maximum, rows 5, 17 and
+    vocab - 1 tie and the token is 5.  Against the oracle: the token is the
+    oracle's argmax over its own logits."""
+    k = 4096
+    s, gamma, w = _lm_head_inputs(orc, 1, k, max(vocab, 18), 1300)
+    w = w[:vocab]
+    s_values = np.asarray(s[0], np.uint16).view(np.float16).astype(np.float32)
+    ws = torch.zeros(tmc.lm_head_argmax_workspace_bytes(1, vocab) // 4, dtype=torch.float32,
+                     device="cuda")
+    for boost in (False, True):
+        wb = w.copy()
+        if boost and vocab >= 18:
+            wb[[5, 17, vocab - 1]] = orc.f16(0.05 * np.sign(s_values))
+        wd = dev_f16(wb)
+        logits = torch.empty((1, vocab), dtype=torch.float32, device="cuda")
+        tmc.add_rmsnorm_gemv(dev_f16(s), None, dev_f16(gamma), wd, None, logits, 1e-6)
+        ref_tok = torch.empty(1, dtype=torch.int32, device="cuda")
+        tmc.argmax(logits, ref_tok)
+        tok = torch.full((1,), -7, dtype=torch.int32, device="cuda")
+        tmc.rmsnorm_lm_head_argmax(dev_f16(s), dev_f16(gamma), wd, ws, tok, 1e-6)
+        torch.cuda.synchronize()
+        got = int(tok.cpu()[0])
+        assert got == int(ref_tok.cpu()[0]), (vocab, boost)
+        assert got != 9
+        if boost and vocab >= 18:
+            assert got == 5
+        # the oracle: its argmax, unless its top two logits are within the
+        # fp16-path tolerance (2e-2) and the chosen token is one of them
+        normed = orc.f16(orc.store(orc.rmsnorm(s, gamma, F16, 1e-6), F16))
+        ref_logits = orc.linear(normed, wb, F16)[0]
+        ref = int(orc.argmax(ref_logits[None, :])[0])
+        finite = np.where(np.isnan(ref_logits), -np.inf, ref_logits)
+        if got != ref:
+            gap = finite[ref] - finite[got]
+            assert gap <= 2e-2, (vocab, boost, got, ref, gap)
+
+
+@pytest.mark.parametrize("batch,layout", [(16, 1), (16, 0), (5, 1), (20, 1)])
+def test_lm_head_token_only_packed(tmc, orc, torch, batch, layout):
+    """tmc_lm_head_partial_argmax_packed_norm_f16 + the final argmax equal
+    tmc_gemm_packed_norm_f16 (fp32 logits) + tmc_argmax_f32 row by row at
+    V = 32000, with planted ties (rows 5, 17, 31999 equal) and a NaN row;
+    batches of one, a part of, and more than one 16-row pass."""
+    k, vocab = 4096, 32000
+    s, gamma, w = _lm_head_inputs(orc, batch, k, vocab, 1310 + batch)
+    pw = tmc.pack_weights(dev_f16(w), gamma=dev_f16(gamma))
+    x = dev_f16(s)
+    xin = tmc.pack_activations(x) if layout else x
+    logits = torch.empty((batch, vocab), dtype=torch.float32, device="cuda")
+    tmc.gemm_packed_norm(xin, pw, logits, batch, k, vocab, 1e-6, layout)
+    ref_tok = torch.empty(batch, dtype=torch.int32, device="cuda")
+    tmc.argmax(logits, ref_tok)
+    ws = torch.zeros(tmc.lm_head_argmax_workspace_bytes(batch, vocab) // 4, dtype=torch.float32,
+                     device="cuda")
+    tok = torch.full((batch,), -7, dtype=torch.int32, device="cuda")
+    tmc.lm_head_argmax_packed_norm(xin, pw, ws, tok, batch, k, vocab, 1e-6, layout)
+    torch.cuda.synchronize()
+    got = tok.cpu().numpy()
+    assert list(got) == list(ref_tok.cpu().numpy())
+    assert 9 not in got
+    # ties: where row 17's logit is a row's maximum, the token is 5
+    lg = logits.cpu().numpy()
+    for r in range(batch):
+        if lg[r, 17] >= np.nanmax(lg[r]):
+            assert got[r] == 5
