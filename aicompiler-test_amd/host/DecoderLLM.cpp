@@ -160,10 +160,14 @@ ModelResourcesCreation createModelResources(hip::HipRuntime& runtime,
                                             const DecoderLLMWorkload& workload) {
   ModelResourcesCreation result;
   try {
-    workload.plan.validate();
+    // weights are stored in fp16 whatever storage the workload's plan names
+    // (an fp32 or bf16 manifest's host floats are rounded on upload)
+    auto plan = workload.plan;
+    plan.attention.dtype = DType::Float16;
+    plan.validate();
     validateWeights(workload);
     auto r = std::make_shared<DecoderLLMModelResources>();
-    describe(*r, workload.plan);
+    describe(*r, plan);
     auto upload = [&](const std::vector<float>& values) {
       r->storageBytes += values.size() * 2;
       return allocate(runtime, values.size(), values.data(), ElementType::Float16);

@@ -2,6 +2,8 @@
 KVCacheImporter.cpp:95-200) read back exactly what the manifest writer put
 in, derive the plan as the reference does, and refuse malformed manifests
 with the reference's messages."""
+import os
+
 import numpy as np
 import pytest
 
@@ -186,3 +188,73 @@ def test_kv_manifest_errors(host, tmp_path, case, message):
         path.write_text(path.read_text().replace("TMC_KV_CACHE 1", "TMC_KV_CACHE 2", 1))
     w, err = host.import_kv_cache_workload(str(path))
     assert w is None and message in err, err
+
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.mark.parametrize("fixture,requested,effective", [
+    ("decoder_llm_fp16_seed11.tmc", "Float16", "Float16"),
+    ("decoder_llm_fp32_seed11.tmc", "Float32", "Float32"),
+])
+def test_reference_exporter_decoder_manifest(host, fixture, requested, effective):
+    """Manifests written by the reference's own exporter
+    (tools/export_decoder_llm.py, seed 11, default shape;
+    tests/golden/make_tmc_golden.py) import with this build's importer:
+    version 2 header, CONFIG, DTYPE requested/effective, every tensor range,
+    the prefill and 8 decode references.  Properties the exporter's PyTorch
+    run fixes: each reference's next token is the argmax of its last logits
+    row, each decode step's input token is the previous step's next token,
+    caches grow by one position per step, and fp16 exports store
+    fp16-representable weights."""
+    w, err = host.import_decoder_llm_workload(os.path.join(GOLDEN, fixture))
+    assert err == "" and w is not None, err
+    plan = w.plan
+    assert w.model_name == "DecoderOnlyLLM"
+    assert (plan.attention.batch, plan.attention.heads, plan.attention.head_dimension,
+            plan.attention.capacity, plan.attention.prefill_length) == (1, 4, 16, 32, 8)
+    assert (plan.layer_count, plan.intermediate_size, plan.vocabulary_size) == (2, 128, 128)
+    assert abs(plan.rms_norm_epsilon - 1e-5) < 1e-12
+    assert w.requested_storage_dtype == getattr(host.DType, requested)
+    assert plan.attention.dtype == getattr(host.DType, effective)
+    assert w.decode_count == 8 and len(w.decode_steps) == 8
+    V, H = 128, 64
+    assert w.embedding_weight.size == V * H and w.language_model_head_weight.size == V * H
+    assert w.layers[1].down_weight.size == 128 * H
+    if requested == "Float16":
+        for arr in (w.embedding_weight, w.layers[0].query_weight, w.layers[1].down_weight):
+            a = np.asarray(arr, np.float32)
+            assert np.array_equal(a.astype(np.float16).astype(np.float32), a)
+    logits = _f32(w.prefill.logits).reshape(8, V)
+    assert int(w.prefill.next_token_ids[0]) == int(np.argmax(logits[-1]))
+    previous = int(w.prefill.next_token_ids[0])
+    for s, step in enumerate(w.decode_steps):
+        assert int(step.token_ids[0]) == previous, s
+        assert int(step.next_token_ids[0]) == int(np.argmax(_f32(step.logits))), s
+        previous = int(step.next_token_ids[0])
+        assert step.key_caches[0].size == 4 * (8 + s + 1) * 16
+        # the prefix the step extends is the previous step's cache
+        earlier = w.prefill if s == 0 else w.decode_steps[s - 1]
+        n = 4 * (8 + s) * 16
+        k_now = _f32(step.key_caches[1]).reshape(4, 8 + s + 1, 16)[:, :8 + s]
+        k_before = _f32(earlier.key_caches[1]).reshape(4, 8 + s, 16)
+        assert k_now.size == n and np.array_equal(k_now, k_before), s
+
+
+def test_reference_exporter_kv_manifest(host):
+    """The reference exporter's KV-cache manifest (tools/export_kv_cache.py)
+    imports: CONFIG 1 4 16 15 7 8, ten tensors, eight steps whose caches
+    extend the previous ones by one position."""
+    w, err = host.import_kv_cache_workload(os.path.join(GOLDEN, "kv_cache.tmc"))
+    assert err == "" and w is not None, err
+    plan = w.plan
+    assert (plan.batch, plan.heads, plan.head_dimension, plan.capacity, plan.prefill_length) == \
+        (1, 4, 16, 15, 7)
+    assert w.model_name == "MultiHeadAttentionKVCache"
+    assert w.query_weight.size == 64 * 64 and w.prefill.output.size == 7 * 64
+    assert len(w.decode_steps) == 8
+    before = _f32(w.prefill.key_cache).reshape(4, 7, 16)
+    for s, step in enumerate(w.decode_steps):
+        now = _f32(step.key_cache).reshape(4, 8 + s, 16)
+        assert np.array_equal(now[:, :7 + s], before), s
+        before = now

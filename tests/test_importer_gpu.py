@@ -7,6 +7,8 @@ module).
 Tolerances: fp16-path values within 2e-2 absolute and 3e-3 relative RMS;
 greedy tokens equal unless the reference's top two logits are within that
 tolerance."""
+import os
+
 import numpy as np
 import pytest
 
@@ -134,3 +136,97 @@ def test_imported_kv_workload_on_gfx950_kernels(host, tmc, orc, rt, tmp_path, to
         assert_f16_path(got, step.output, what=f"KV decode {s} output")
         n = P + s + 1
         assert_f16_path(values(v_cache)[:, :n], step.value_cache, what=f"KV decode {s} value cache")
+
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.mark.parametrize("fixture", ["decoder_llm_fp16_seed11.tmc", "decoder_llm_fp32_seed11.tmc"])
+def test_reference_exported_decoder(host, orc, rt, fixture):
+    """A manifest written by the reference's own exporter
+    (tools/export_decoder_llm.py --seed 11 at its default shape, fp16 and
+    fp32; tests/golden/make_tmc_golden.py) imported and run through
+    compileDecoderLLM as decoder_llm_main.cpp runs it: prefill, then each
+    decode step's token.  Logits and K/V prefixes against the PyTorch
+    references in the manifest at the reference app's fp16 tolerance
+    (Validator::compare, 2e-2 absolute + 2e-2 relative,
+    decoder_llm_main.cpp:15-23; the fp32 manifest too, since this decoder
+    stores fp16), tokens equal unless the reference's top two logits are
+    within 2e-2; and every logit against the oracle's decoder step on the
+    same fp16 weights at the fp16-path tolerance."""
+    workload, err = host.import_decoder_llm_workload(os.path.join(GOLDEN, fixture))
+    assert err == "", err
+    plan = workload.plan
+    assert (plan.layer_count, plan.attention.heads, plan.attention.head_dimension,
+            plan.vocabulary_size, plan.attention.prefill_length) == (2, 4, 16, 128, 8)
+    opts = host.DecoderLLMCompileOptions()
+    opts.kv_page_size = 16
+    dec, _ = host.compile_decoder_llm(rt, workload, opts)
+    V, L, P = plan.vocabulary_size, plan.layer_count, plan.attention.prefill_length
+    ref = workload.prefill
+    decode_tokens = [int(s.token_ids[0]) for s in workload.decode_steps]
+    oracle = tm.oracle_decoder_run(orc, workload, [int(t) for t in ref.token_ids], decode_tokens)
+
+    def check(what, logits, reference, oracle_logits):
+        ok, worst, mismatches = orc.compare(logits, reference, 2e-2, 2e-2)
+        assert ok, f"{what}: {mismatches} logits outside 2e-2 + 2e-2 |ref| (worst {worst:.3e})"
+        assert_f16_path(logits, oracle_logits, what=f"{what} against the oracle")
+
+    out = dec.prefill([float(t) for t in ref.token_ids], True)
+    assert out["passed"], out["error"]
+    check(f"{fixture} prefill", out["logits"], ref.logits, oracle[0][0])
+    _token(int(out["next_token_ids"][-1]), int(ref.next_token_ids[0]),
+           ref.logits.reshape(P, V)[-1], f"{fixture} prefill token")
+    for l in range(L):
+        for got, want in ((dec.read_key_prefix(l), ref.key_caches[l]),
+                          (dec.read_value_prefix(l), ref.value_caches[l])):
+            ok, worst, _ = orc.compare(got, want, 2e-2, 2e-2)
+            assert ok, f"{fixture} prefill cache layer {l}: worst {worst:.3e}"
+        assert_f16_path(dec.read_key_prefix(l), oracle[0][2][l], what=f"prefill K{l} vs oracle")
+    for s, step in enumerate(workload.decode_steps):
+        out = dec.decode([float(step.token_ids[0])], True)
+        assert out["passed"], out["error"]
+        check(f"{fixture} decode {s}", out["logits"], step.logits, oracle[s + 1][0])
+        _token(int(out["next_token_ids"][0]), int(step.next_token_ids[0]), step.logits,
+               f"{fixture} decode {s} token")
+        for l in range(L):
+            ok, worst, _ = orc.compare(dec.read_value_prefix(l), step.value_caches[l], 2e-2, 2e-2)
+            assert ok, f"{fixture} decode {s} V{l}: worst {worst:.3e}"
+            assert_f16_path(dec.read_value_prefix(l), oracle[s + 1][3][l],
+                            what=f"decode {s} V{l} vs oracle")
+    assert dec.current_length() == P + len(workload.decode_steps)
+
+
+def test_reference_exported_kv_cache(host, orc, rt):
+    """The reference exporter's KV-cache manifest (tools/export_kv_cache.py,
+    MultiHeadAttentionKVCache: 4 heads x 16, prefill 7, 8 decode steps)
+    through compileKVCacheAttention as kv_cache_main.cpp runs it.  The
+    reference module is fp32 and its app checks 2e-4 + 2e-3 |ref|
+    (kv_cache_main.cpp:15-16); this module stores fp16 (inputs rounded on
+    upload), so outputs and caches are held to the fp16-path tolerance and
+    to the reference app's fp16 bound (2e-2 + 2e-2 |ref|)."""
+    w, err = host.import_kv_cache_workload(os.path.join(GOLDEN, "kv_cache.tmc"))
+    assert err == "", err
+    plan = w.plan
+    assert (plan.batch, plan.heads, plan.head_dimension, plan.capacity, plan.prefill_length) == \
+        (1, 4, 16, 15, 7)
+    exe, _ = host.compile_kv_cache_attention(rt, plan, w.query_weight, w.key_weight,
+                                             w.value_weight, w.output_weight)
+
+    def check(what, got, want):
+        ok, worst, _ = orc.compare(got, want, 2e-2, 2e-2)
+        assert ok, f"{what}: worst {worst:.3e}"
+        assert_f16_path(got, want, what=what)
+
+    out = exe.prefill(w.prefill.query, w.prefill.key, w.prefill.value)
+    assert out["passed"], out["error"]
+    check("prefill output", out["output"], w.prefill.output)
+    check("prefill key cache", exe.read_key_prefix(), w.prefill.key_cache)
+    check("prefill value cache", exe.read_value_prefix(), w.prefill.value_cache)
+    for s, step in enumerate(w.decode_steps):
+        out = exe.decode(step.query, step.key, step.value)
+        assert out["passed"], out["error"]
+        check(f"decode {s} output", out["output"], step.output)
+        check(f"decode {s} key cache", exe.read_key_prefix(), step.key_cache)
+        check(f"decode {s} value cache", exe.read_value_prefix(), step.value_cache)
+    assert exe.current_length() == plan.capacity

@@ -159,6 +159,58 @@ def decoder_tensors(orc, config: dict, seed: int, page: int = 16):
     return tensors
 
 
+def oracle_decoder_run(orc, workload, prompt, decode_tokens, page: int = 16):
+    """The oracle's decoder step (tmco_decoder_step) over an imported
+    workload's weights, rounded to fp16 with the host rule as the gfx950
+    decoder stores them: the prompt as one step whose rows are its tokens,
+    then one step per given decode token.  Returns [(logits, next tokens,
+    key caches, value caches)] per step, caches [heads, length, D] per
+    layer."""
+    plan = workload.plan
+    L, NH = plan.layer_count, plan.attention.heads
+    D, C = plan.attention.head_dimension, plan.attention.capacity
+    H, I, V = NH * D, plan.intermediate_size, plan.vocabulary_size
+    f16 = lambda a: orc.f16(np.asarray(a, np.float32))  # noqa: E731
+    rows = lambda a, n: f16(np.asarray(a, np.float32).reshape(n, -1))  # noqa: E731
+    layers = [dict(input_norm=f16(lw.input_norm_weight), wq=rows(lw.query_weight, H),
+                   wk=rows(lw.key_weight, H), wv=rows(lw.value_weight, H),
+                   wo=rows(lw.output_weight, H), post_norm=f16(lw.post_attention_norm_weight),
+                   wg=rows(lw.gate_weight, I), wu=rows(lw.up_weight, I),
+                   wd=rows(lw.down_weight, H)) for lw in workload.layers]
+    m = dict(embedding=rows(workload.embedding_weight, V), final_norm=f16(workload.final_norm_weight),
+             lm_head=rows(workload.language_model_head_weight, V),
+             rope_cos=np.asarray(workload.rope_cosine, np.float32),
+             rope_sin=np.asarray(workload.rope_sine, np.float32), layers=layers)
+    cfg = dict(layers=L, hidden=H, heads=NH, head_dim=D, kv_heads=NH, intermediate=I,
+               vocabulary=V, capacity=C, epsilon=plan.rms_norm_epsilon)
+    max_pages = (C + page - 1) // page
+    k = [np.zeros(max_pages * NH * page * D, np.uint16) for _ in range(L)]
+    v = [np.zeros_like(x) for x in k]
+    tables = np.tile(np.arange(max_pages, dtype=np.int32), (L, 1, 1))
+
+    def caches(length):
+        out = []
+        for pools in (k, v):
+            per_layer = []
+            for l in range(L):
+                pool = pools[l].reshape(max_pages, NH, page, D)
+                per_layer.append(orc.f16_values(np.stack(
+                    [pool[p // page, :, p % page, :] for p in range(length)], axis=1)))
+            out.append(per_layer)
+        return out
+
+    P = len(prompt)
+    t = np.tile(tables, (1, P, 1)).reshape(L, P, max_pages)
+    logits, nxt = orc.decoder_step(m, cfg, k, v, page, max_pages, t, np.asarray(prompt, np.int32),
+                                   np.arange(1, P + 1))
+    out = [(logits, nxt, *caches(P))]
+    for s, token in enumerate(decode_tokens):
+        lg, nx = orc.decoder_step(m, cfg, k, v, page, max_pages, tables, np.array([token]),
+                                  np.array([P + s + 1]))
+        out.append((lg, nx, *caches(P + s + 1)))
+    return out
+
+
 def mha_kv_reference(x_q, x_k, x_v, wq, wk, wv, wo, heads, past=None):
     """float64 MultiHeadAttentionKVCache.forward (workloads/pytorch/KVCache.py):
     q/k/v projections, split heads, append to the past caches, softmax over
