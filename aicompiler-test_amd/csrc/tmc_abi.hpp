@@ -7,6 +7,7 @@
 #include <string>
 
 #include "../../include/tmc_hip.h"
+#include "../../include/tmc_bench.h"
 
 namespace tmc {
 

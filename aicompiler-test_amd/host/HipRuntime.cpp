@@ -2,6 +2,7 @@
 #include "HipRuntime.hpp"
 
 #include "tmc_hip.h"
+#include "tmc_bench.h"
 
 #include <utility>
 

@@ -574,19 +574,6 @@ int tmc_paged_attention_output_f16(const void *q, const void *key_pool, const vo
                                    int64_t head_stride, int64_t out_features, void *workspace,
                                    size_t workspace_bytes, void *stream);
 
-/* Bandwidth probe of the paged attention access pattern (head_dim 128, pages
- * of a multiple of 16 positions): reads
- * the K and V bytes tmc_paged_decode_attention would read for these lengths
- * and block tables, and nothing else; `sink` (4 bytes of device memory) is
- * written only when the xor of the loaded words hits a fixed constant.  No
- * reference counterpart: it measures the ceiling of the gather itself, as
- * tmc_copy_bytes does for streaming. */
-int tmc_paged_gather_probe(const void *key_pool, const void *value_pool,
-                           const int32_t *valid_lengths, const int32_t *block_tables,
-                           int64_t batch, int64_t kv_heads, int64_t head_dim, int64_t page_size,
-                           int64_t max_pages, int64_t pool_pages, int64_t page_stride,
-                           int64_t head_stride, void *sink, void *stream);
-
 /* Decode-step fusion of emitServingRoPE (DecoderLLMMetalEmitter.cpp:260-312)
  * for q and k with emitServingPagedCacheAppend (:314-373) for the rotated k
  * and v, reading one fused projection row per request laid out
@@ -749,14 +736,6 @@ int tmc_lm_head_partial_argmax_packed_norm_f16(const void *x, const void *packed
  * from the row's partial slots. */
 int tmc_lm_head_final_argmax(void *workspace, size_t workspace_bytes, int32_t *tokens,
                              int64_t rows, int64_t vocabulary, void *stream);
-
-/* Synthetic data: fill `count` elements with N(mean, std) values from a
- * counter-based generator (splitmix64 + Box-Muller) keyed by `seed`. */
-int tmc_fill_normal(void *ptr, int dtype, int64_t count, uint64_t seed, float mean, float std,
-                    void *stream);
-
-/* Plain device copy kernel (bandwidth probe used to calibrate counters). */
-int tmc_copy_bytes(const void *src, void *dst, size_t bytes, void *stream);
 
 /* Pinned host memory (hipHostMalloc), readable and writable by kernels:
  * the spill space of preempted requests' KV pages.  No reference counterpart

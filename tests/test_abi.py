@@ -10,11 +10,14 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def declared_functions():
-    text = open(os.path.join(ROOT, "include", "tmc_hip.h")).read()
+def declared_functions(header="tmc_hip.h"):
+    text = open(os.path.join(ROOT, "include", header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     names = re.findall(r"\b(tmc_[a-z0-9_]+)\s*\(", text)
     return sorted(set(names))
+
+
+HEADERS = sorted(h for h in os.listdir(os.path.join(ROOT, "include")) if h.endswith(".h"))
 
 
 def test_header_declares_the_boundary():
@@ -27,10 +30,19 @@ def test_header_declares_the_boundary():
         assert required in names
 
 
-def test_library_exports_every_declared_symbol(tmc):
+@pytest.mark.parametrize("header", HEADERS)
+def test_library_exports_every_declared_symbol(tmc, header):
     lib = tmc.lib()
-    missing = [n for n in declared_functions() if not hasattr(lib, n)]
-    assert not missing, f"missing exports: {missing}"
+    missing = [n for n in declared_functions(header) if not hasattr(lib, n)]
+    assert not missing, f"{header}: missing exports: {missing}"
+
+
+def test_bench_helpers_stay_out_of_the_boundary():
+    """The measurement helpers (synthetic fill, copy and gather probes) are
+    declared in tmc_bench.h, not in the drop-in header."""
+    boundary, bench = set(declared_functions()), set(declared_functions("tmc_bench.h"))
+    assert bench == {"tmc_fill_normal", "tmc_copy_bytes", "tmc_paged_gather_probe"}
+    assert not boundary & bench
 
 
 def test_argument_validation_fails_before_device_work(tmc):

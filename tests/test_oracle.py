@@ -267,3 +267,50 @@ def test_append_maps_are_bit_copies(orc):
     for t in range(s):
         pos = 2 + t
         assert np.array_equal(pv[table[pos // p], 0, :, pos % p, :], tok[0, t])
+
+
+@pytest.mark.parametrize("head_major", [False, True])
+def test_append_serving_places_each_row_through_its_table(orc, head_major):
+    """tmco_append_serving (emitServingPagedCacheAppend,
+    DecoderLLMMetalEmitter.cpp:314-373) pinned by tagged values: every input
+    element carries its own (row, head, column) as its bits, so each written
+    pool element names where it came from.  Written elements must be exactly
+    those of the rows below active_count whose length lies in [1, capacity]
+    and whose page entry for position length - 1 is present; each sits in
+    page table[row][(length - 1) / page_size], head slab h, slot
+    (length - 1) % page_size, column c ([page][heads][page_size][head_dim]);
+    reading that position back through the row's table returns the row; and
+    nothing else in the pool changes."""
+    rng = np.random.default_rng(21)
+    rows, heads, d, p, cap = 7, 3, 4, 4, 16
+    max_pages = cap // p
+    pages = rows * max_pages + 2
+    hidden = heads * d
+    tags = np.arange(1, rows * hidden + 1, dtype=np.uint16)  # row-major tag r * hidden + f + 1
+    if head_major:  # [row][head][d]: the same element order for this layout
+        inp = tags.reshape(rows, heads, d).copy().ravel()
+    else:
+        inp = tags.copy()
+    tables = rng.permutation(pages)[:rows * max_pages].astype(np.int32).reshape(rows, max_pages)
+    lengths = np.array([1, 5, cap, 0, cap + 1, 9, 3], np.int32)
+    tables[5, (9 - 1) // p] = -1  # the target page of row 5 is missing
+    active = 6  # row 6 is past the active count
+    pool = np.zeros(pages * heads * p * d, np.uint16)
+    out = orc.append_serving(inp, pool, rows, heads, d, cap, p, head_major, lengths, tables, active)
+    view = out.reshape(pages, heads, p, d)
+    expected_rows = [r for r in range(rows)
+                     if r < active and 1 <= lengths[r] <= cap
+                     and tables[r, (lengths[r] - 1) // p] >= 0]
+    assert expected_rows == [0, 1, 2]
+    written = np.argwhere(view != 0)
+    assert len(written) == len(expected_rows) * hidden
+    for page, h, slot, c in written:
+        tag = int(view[page, h, slot, c]) - 1
+        r, f = divmod(tag, hidden)
+        assert r in expected_rows and divmod(f, d) == (h, c)
+        pos = int(lengths[r]) - 1
+        assert page == tables[r, pos // p] and slot == pos % p
+    for r in expected_rows:  # the row read back through its own table
+        pos = int(lengths[r]) - 1
+        got = view[tables[r, pos // p], :, pos % p, :].ravel()
+        assert np.array_equal(got, tags[r * hidden:(r + 1) * hidden])
