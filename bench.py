@@ -211,17 +211,28 @@ def time_loop(torch, fn, iters: int, replays: int = 5) -> float:
 
 
 def host_cpu() -> dict:
-    """The host the CPU baseline ran on: model name and logical CPU count."""
-    model = "unknown"
+    """The host the CPU baseline ran on: model name, x86 family / model /
+    stepping (the GPU boxes' KVM guests report the model name only as "AMD
+    EPYC"; family 26 is Zen 5), hypervisor flag and logical CPU count."""
+    fields = {"model name": "unknown", "cpu family": "", "model": "", "stepping": ""}
+    hypervisor = False
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
+                key, _, value = line.partition(":")
+                key = key.strip()
+                if key in fields and fields[key] in ("", "unknown"):
+                    fields[key] = value.strip()
+                if key == "flags":
+                    hypervisor = "hypervisor" in value.split()
+                if key == "" and fields["model name"] != "unknown":
                     break
     except OSError:
         pass
-    return {"cpu_model": model, "nproc": os.cpu_count()}
+    return {"cpu_model": fields["model name"],
+            "cpu_family_model_stepping": f"{fields['cpu family']}/{fields['model']}/"
+                                         f"{fields['stepping']}",
+            "virtualized": hypervisor, "nproc": os.cpu_count()}
 
 
 def cpu_baseline(block: MlpBlock, seconds: float) -> dict:
@@ -508,15 +519,19 @@ def prefill_gpu(tmc) -> dict:
     return out
 
 
-def c5_cpu_baseline(seconds_hint: float = 10.0) -> dict:
-    """The oracle's decode step (oracle/libtmc_oracle.so, one thread) at 7B
-    width on a bounded sample: `n` decoder layers (layer_limit) plus the LM
-    head, scaled to 32 layers.  Weight values do not change the oracle's
-    work, so fixed fp16 patterns stand in for random weights."""
+def c5_cpu_baseline(steps: int = 2) -> dict:
+    """The oracle's decode step (oracle/libtmc_oracle.so, one thread) at the
+    C5 shape: `steps` whole decode steps (32 layers, the LM head over every
+    row, greedy tokens) at batch 1 and at batch 16, fed back token to token.
+    Weight values do not change the oracle's work, so fixed fp16 patterns
+    stand in for random weights, and the 32 layers share one layer's arrays
+    (the same arithmetic as 32 distinct layers, a fraction of the host
+    memory)."""
     import numpy as np
     from oracle import oracle as orc
     orc.build()
     H, I, V, NH, D = C5["hidden"], C5["intermediate"], C5["vocabulary"], C5["heads"], C5["head_dim"]
+    L = C5["layers"]
     pattern = np.random.default_rng(0).integers(0x2000, 0x2c00, 4096, dtype=np.uint16)
     pattern[1::2] |= 0x8000
     w = lambda *shape: np.resize(pattern, shape)  # noqa: E731
@@ -527,29 +542,28 @@ def c5_cpu_baseline(seconds_hint: float = 10.0) -> dict:
     layer = dict(input_norm=one, wq=w(H, H), wk=w(H, H), wv=w(H, H), wo=w(H, H), post_norm=one,
                  wg=w(I, H), wu=w(I, H), wd=w(H, I))
     out = {}
-    for batch, n in ((1, 2), (16, 1)):
-        m = dict(embedding=w(batch, H), final_norm=one, lm_head=w(V, H),
+    for batch in (1, 16):
+        m = dict(embedding=w(V, H), final_norm=one, lm_head=w(V, H),
                  rope_cos=np.cos(pos * freq).astype(np.float32),
-                 rope_sin=np.sin(pos * freq).astype(np.float32), layers=[layer] * n)
-        cfg = dict(layers=C5["layers"], hidden=H, heads=NH, head_dim=D, intermediate=I,
-                   vocabulary=V, capacity=cap, epsilon=1e-6)
+                 rope_sin=np.sin(pos * freq).astype(np.float32), layers=[layer] * L)
+        cfg = dict(layers=L, hidden=H, heads=NH, head_dim=D, intermediate=I, vocabulary=V,
+                   capacity=cap, epsilon=1e-6)
         pages = cap // 16
-        kp = [np.zeros(batch * pages * NH * 16 * D, np.uint16) for _ in range(n)]
-        vp = [p.copy() for p in kp]
-        tables = np.zeros((C5["layers"], batch, pages), np.int32)
+        kp = [np.zeros(batch * pages * NH * 16 * D, np.uint16) for _ in range(L)]
+        vp = [np.zeros_like(p) for p in kp]
+        tables = np.zeros((L, batch, pages), np.int32)
         for b in range(batch):
             tables[:, b, :] = b * pages + np.arange(pages)
+        tokens = np.arange(batch, dtype=np.int32)
         t0 = time.perf_counter()
-        orc.decoder_step(m, cfg, kp, vp, 16, pages, tables, np.arange(batch, dtype=np.int32),
-                         np.ones(batch, np.int32), layer_limit=n)
-        per_layer = (time.perf_counter() - t0) / n
-        t0 = time.perf_counter()
-        orc.linear(w(batch, H), m["lm_head"], orc.F16)
-        head = time.perf_counter() - t0
-        step = per_layer * C5["layers"] + head
-        out[f"b{batch}_tokens_per_s"] = round(batch / step, 5)
-        out[f"b{batch}_sample"] = (f"{n} layer(s) of the decode step ({per_layer:.2f} s each) + "
-                                   f"LM head ({head:.2f} s), scaled to 32 layers")
+        for s in range(steps):
+            _, tokens = orc.decoder_step(m, cfg, kp, vp, 16, pages, tables, tokens,
+                                         np.full(batch, s + 1, np.int32))
+            tokens = np.asarray(tokens, np.int32)
+        elapsed = time.perf_counter() - t0
+        out[f"b{batch}_tokens_per_s"] = round(batch * steps / elapsed, 5)
+        out[f"b{batch}_sample"] = (f"{steps} whole decode steps (32 layers + LM head + argmax, "
+                                   f"{batch} row(s)) in {elapsed:.1f} s")
     out["cores"] = 1
     out.update(host_cpu())
     out["kind"] = "port"

@@ -372,3 +372,73 @@ def test_7b_batch16_folded_norms_match_norm_kernels(host, orc, rt7b, models7b):
         for r in range(rows):
             assert_f16_path(a[r], b[r].astype(np.float64), f"step {i} row {r}")
             _check_token(runs[True][2][i][r], runs[False][2][i][r], b[r], f"step {i} row {r}")
+
+
+@pytest.mark.parametrize("batch", [1, 16])
+def test_7b_full_depth_chained_steps_equal_serving(host, rt7b, batch):
+    """The configuration bench.py times (C5: 32 layers at 7B widths, random
+    weights made on the device, prompts ~U[32, 512] through chunked prefill,
+    capacity 1024, 16-position pages) checked by properties that hold at any
+    depth: the chained decode steps of measureDecodeThroughput (tokens fed
+    back on the device, the token-only tail where admitted) generate the
+    tokens runContinuousBatch generates for the same requests over 32 decode
+    steps, and every logit the serving loop records is finite.  A token may
+    differ only where the serving logits' top two are within the fp16-path
+    tolerance (2e-2) of each other; the sequences are compared up to there."""
+    plan = host.DecoderLLMPlan()
+    att = host.KVCachePlan()
+    att.heads, att.head_dimension, att.capacity = 32, 128, 1024
+    att.dtype = host.DType.Float16
+    plan.attention = att
+    plan.layer_count, plan.intermediate_size = 32, 11008
+    plan.vocabulary_size, plan.rms_norm_epsilon = 32000, 1e-6
+    model = host.create_synthetic_model_resources(rt7b, plan, 501)
+    rng = np.random.default_rng(502)
+    prompts = [list(map(int, rng.integers(0, 32000, rng.integers(32, 513))))
+               for _ in range(batch)]
+    steps = 32
+    print(f"[7b-full] batch {batch}: chained decode", flush=True)
+    chained = host.measure_decode_throughput(rt7b, model, prompts, steps, P, False, False, 1024)
+    assert chained["passed"], chained["error"]
+    specs = []
+    for i, prompt in enumerate(prompts):
+        spec = host.ServingRequestSpec()
+        spec.id = f"r{i}"
+        spec.prompt_token_ids = [float(t) for t in prompt]
+        spec.decode_token_count = steps
+        spec.arrival_step = 0
+        specs.append(spec)
+    config = host.ServingConfig()
+    config.page_size = P
+    config.physical_pages_per_layer = max(batch * ((512 + steps + P) // P + 1), 1024 // P)
+    config.maximum_batch_size = batch
+    config.record_decode_logits = True
+    config.prefill_chunk_size = 1024
+    config.prefill_requests_per_chunk = batch
+    print(f"[7b-full] batch {batch}: serving", flush=True)
+    served = host.run_continuous_batch(rt7b, model, specs, config)
+    assert served["passed"], served["error"]
+    compared, diverged_at_prompt = 0, 0
+    for r, out in enumerate(served["requests"]):
+        want = [int(t) for t in chained["generated_token_ids"][r]]
+        got = [int(t) for t in out["generated_token_ids"]]
+        assert len(want) == steps + 1 and len(got) == steps + 1, r
+        assert len(out["decode_logits"]) == steps, r
+        for s, logits in enumerate(out["decode_logits"]):
+            assert np.all(np.isfinite(logits)), f"row {r} step {s}: non-finite logits"
+        if got[0] != want[0]:
+            # the prompt's last token differs (the two loops pack prompts into
+            # chunks on their own): nothing further to compare for this row
+            diverged_at_prompt += 1
+            continue
+        for s in range(1, steps + 1):
+            if got[s] != want[s]:
+                logits = np.asarray(out["decode_logits"][s - 1])
+                gap = abs(float(logits[got[s]]) - float(logits[want[s]]))
+                assert gap <= 2e-2, f"row {r} step {s}: token {got[s]} != {want[s]} (gap {gap})"
+                break
+            compared += 1
+    assert diverged_at_prompt <= batch // 8, diverged_at_prompt
+    assert compared >= steps * batch * 3 // 4, compared
+    if batch > 1:
+        assert chained["token_only_available"]
