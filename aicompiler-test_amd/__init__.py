@@ -118,6 +118,7 @@ def _declare(l):
         "tmc_lm_head_final_argmax": (i32, [vp, sz, vp, i64, i64, vp]),
         "tmc_fill_normal": (i32, [vp, i32, i64, C.c_uint64, f, f, vp]),
         "tmc_copy_bytes": (i32, [vp, vp, sz, vp]),
+        "tmc_read_probe": (i32, [vp, sz, vp, vp]),
         "tmc_elementwise": (i32, [i32, vp, vp, vp, i32, i64, i32, vp]),
         "tmc_rt_create": (i32, [C.POINTER(vp)]),
         "tmc_rt_destroy": (None, [vp]),
@@ -746,6 +747,11 @@ def lm_head_argmax_packed_norm(x, packed_scaled, workspace, tokens, batch, in_fe
 def fill_normal(t, seed, mean=0.0, std=1.0, stream=None):
     check(lib().tmc_fill_normal(_ptr(t), _dtype_code(t), t.numel(), seed, mean, std,
                                 _stream(stream)), "tmc_fill_normal")
+
+
+def read_probe(src, nbytes, sink, stream=None):
+    """tmc_read_probe (include/tmc_bench.h): read nbytes of src once."""
+    check(lib().tmc_read_probe(_ptr(src), nbytes, _ptr(sink), _stream(stream)), "tmc_read_probe")
 
 
 def copy_bytes(src, dst, nbytes, stream=None):

@@ -645,6 +645,31 @@ __global__ __launch_bounds__(kThreads) void copy_kernel(const uint4* __restrict_
     dst[i] = src[i];
 }
 
+// Read-only stream: 4096 blocks, each a contiguous share of the buffer, four
+// 16-byte non-temporal loads per lane in flight; the sink is written only
+// when a block's sum hits a fixed constant, so the loads cannot be dropped.
+constexpr int kReadProbeBlocks = 4096;
+constexpr int kReadProbeDepth = 4;
+typedef float probe_f4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void read_probe_kernel(const probe_f4* __restrict__ src,
+                                                         float* __restrict__ sink, size_t count,
+                                                         size_t per_block) {
+  const size_t base = (size_t)blockIdx.x * per_block;
+  float acc = 0.0f;
+  for (size_t i = threadIdx.x; i < per_block; i += 256 * kReadProbeDepth) {
+    probe_f4 v[kReadProbeDepth];
+#pragma unroll
+    for (int d = 0; d < kReadProbeDepth; ++d) {
+      const size_t at = i + 256 * (size_t)d;
+      v[d] = at < per_block && base + at < count ? __builtin_nontemporal_load(src + base + at)
+                                                 : probe_f4{};
+    }
+#pragma unroll
+    for (int d = 0; d < kReadProbeDepth; ++d) acc += v[d].x + v[d].y + v[d].z + v[d].w;
+  }
+  if (acc == 1234.5f) sink[0] = acc;
+}
+
 unsigned grid_for(size_t items) {
   const size_t blocks = (items + kThreads - 1) / kThreads;
   return (unsigned)(blocks < 65536 * 8 ? (blocks ? blocks : 1) : 65536 * 8);
@@ -1147,6 +1172,16 @@ extern "C" int tmc_copy_pages(const void* src, void* dst, const int32_t* pages, 
                      static_cast<const uint4*>(src), static_cast<uint4*>(dst), pages, units,
                      scatter);
   return check_launch("copy_pages_kernel");
+}
+
+extern "C" int tmc_read_probe(const void* src, size_t bytes, void* sink, void* stream) {
+  TMC_REQUIRE(src && sink && bytes > 0 && bytes % 16 == 0 && aligned16(src),
+              "Read probe: src must be 16-byte aligned and size a multiple of 16.");
+  const size_t count = bytes / 16;
+  const size_t per_block = (count + kReadProbeBlocks - 1) / kReadProbeBlocks;
+  hipLaunchKernelGGL(read_probe_kernel, dim3(kReadProbeBlocks), dim3(256), 0, as_stream(stream),
+                     static_cast<const probe_f4*>(src), static_cast<float*>(sink), count, per_block);
+  return check_launch("read_probe_kernel");
 }
 
 extern "C" int tmc_copy_bytes(const void* src, void* dst, size_t bytes, void* stream) {

@@ -75,6 +75,7 @@ __device__ __forceinline__ void write_out(OutT* y, size_t i, float a0, float a1)
 enum Fuse { kFuseNone = 0, kFuseAddNorm = 1, kFuseNorm = 2, kFuseResidual = 3 };
 
 struct NormArgs {
+  const half_t* x = nullptr;  // kFuseNone / kFuseResidual in gemv_norm_kernel: the input row
   const half_t* residual = nullptr;
   const half_t* update = nullptr;
   const half_t* gamma = nullptr;
@@ -238,7 +239,7 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(const half_t* __restrict_
 // in LDS until the end and are summed in wave order as in the dot GEMV, so
 // results equal the norm kernel followed by tmc_gemv_f16 at k split 4 bit for
 // bit.
-constexpr int kNormMaxChunks = 1024;  // K <= 8192: four chunks per lane
+constexpr int kNormMaxChunks = 1024;  // normalized rows: K <= 8192, four chunks per lane
 constexpr int kNormMaxSlots = 35;     // row groups per block (grid >= groups / 32), + overshoot
 // Build parameter: blocks of the persistent grid per resident block slot
 // (1 = one wave of blocks; 2 = twice as many, each with half the groups).
@@ -271,10 +272,16 @@ __global__ __launch_bounds__(256) void gemv_norm_kernel(const half_t* __restrict
                                                        const half_t* __restrict__ w1,
                                                        OutT* __restrict__ y, int n_out, int k_in,
                                                        NormArgs na, RopeArgs ra) {
-  static_assert(FUSE == kFuseAddNorm || FUSE == kFuseNorm, "a norm fusion");
+  // kFuseNone / kFuseResidual: the same stream over a stored input row (no
+  // norm prologue, no barrier before the stream), the plain or residual
+  // batch-1 GEMV (algorithm 5, "persistent dot")
+  constexpr bool kNorm = FUSE == kFuseAddNorm || FUSE == kFuseNorm;
   static_assert(!ROPE || (MATS == 1 && RPW == 2), "the RoPE epilogue takes one row pair");
   static_assert(!ARGMAX || (MATS == 1 && !ROPE), "the argmax epilogue follows one matrix");
-  static_assert(NC == 1 || NC == 2 || NC == 4, "1, 2 or 4 chunks per lane");
+  static_assert(FUSE != kFuseResidual || (MATS == 1 && !ROPE && !ARGMAX),
+                "the residual epilogue follows one projection");
+  static_assert(NC == 1 || NC == 2 || NC == 4 || (!kNorm && (NC == 6 || NC == 8)),
+                "1, 2 or 4 chunks per lane (6 or 8 without the norm)");
   // row groups in flight per wave, measured on the 7B shapes: 3 for the gated
   // pair (gate/up 28.2 against 30.5 us at 2), 2 for one matrix (q.k.v 16.4
   // against 16.9 us at 3)
@@ -304,8 +311,12 @@ __global__ __launch_bounds__(256) void gemv_norm_kernel(const half_t* __restrict
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     const int at = min(c[i], chunks - 1);
-    src[i] = norm_source<FUSE>(na, at);
-    gam[i] = load_h8(na.gamma + 8 * at);
+    if constexpr (kNorm) {
+      src[i] = norm_source<FUSE>(na, at);
+      gam[i] = load_h8(na.gamma + 8 * at);
+    } else {
+      src[i] = load_h8(na.x + 8 * at);
+    }
   }
   // weights of row group g: rows past the matrix (clamped to row n_out, so
   // at or past the resource's end) and chunks past the row read as zero.  No
@@ -332,31 +343,37 @@ __global__ __launch_bounds__(256) void gemv_norm_kernel(const half_t* __restrict
   load_group(wa, g);
   load_group(wb, g + grid);
   if constexpr (kNormDepth == 3) load_group(wc, g + 2 * grid);
-  // norm: group wave + 4i (past the row: zero); block 0 stores the sums
+  h8 xn[NC];
+  if constexpr (kNorm) {
+    // norm: group wave + 4i (past the row: zero); block 0 stores the sums
 #pragma unroll
-  for (int i = 0; i < NC; ++i) {
-    src[i] = ok[i] ? src[i] : h8{};
-    float squares = 0.0f;
+    for (int i = 0; i < NC; ++i) {
+      src[i] = ok[i] ? src[i] : h8{};
+      float squares = 0.0f;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) squares += to_float<half_t>(src[i][t]) * to_float<half_t>(src[i][t]);
-    const float total = wave_sum(squares);
-    if (lane == 0) totals[wave + 4 * i] = total;
-  }
-  if (FUSE == kFuseAddNorm && blockIdx.x == 0) {
+      for (int t = 0; t < 8; ++t) squares += to_float<half_t>(src[i][t]) * to_float<half_t>(src[i][t]);
+      const float total = wave_sum(squares);
+      if (lane == 0) totals[wave + 4 * i] = total;
+    }
+    if (FUSE == kFuseAddNorm && blockIdx.x == 0) {
+#pragma unroll
+      for (int i = 0; i < NC; ++i)
+        if (ok[i]) *reinterpret_cast<h8*>(na.sum_out + 8 * c[i]) = src[i];
+    }
+    lds_barrier();
+    float total = 0.0f;
+    for (int q = 0; q * kWave < chunks; ++q) total += totals[q];
+    const float inverse = 1.0f / sqrtf(total / (float)k_in + na.eps);
 #pragma unroll
     for (int i = 0; i < NC; ++i)
-      if (ok[i]) *reinterpret_cast<h8*>(na.sum_out + 8 * c[i]) = src[i];
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        xn[i][t] = from_float<half_t>(to_float<half_t>(src[i][t]) * inverse * to_float<half_t>(gam[i][t]));
+  } else {
+    // chunks past the row: the weights read as zero there, the products are 0
+#pragma unroll
+    for (int i = 0; i < NC; ++i) xn[i] = ok[i] ? src[i] : h8{};
   }
-  lds_barrier();
-  float total = 0.0f;
-  for (int q = 0; q * kWave < chunks; ++q) total += totals[q];
-  const float inverse = 1.0f / sqrtf(total / (float)k_in + na.eps);
-  h8 xn[NC];
-#pragma unroll
-  for (int i = 0; i < NC; ++i)
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-      xn[i][t] = from_float<half_t>(to_float<half_t>(src[i][t]) * inverse * to_float<half_t>(gam[i][t]));
   auto consume = [&](const h8 (&w)[NC][MATS][RPW], int slot) {
     float acc[MATS][RPW];
 #pragma unroll
@@ -433,7 +450,10 @@ __global__ __launch_bounds__(256) void gemv_norm_kernel(const half_t* __restrict
       for (int m = 0; m < MATS; ++m)
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) a[m] += partial[w][s][m][r];
-      write_out<MATS>(y, (size_t)row, a[0], a[1]);
+      if constexpr (FUSE == kFuseResidual)
+        store_out<1, kFuseResidual>(y, (size_t)row, a[0], 0.0f, na);
+      else
+        write_out<MATS>(y, (size_t)row, a[0], a[1]);
     }
   }
 }
@@ -765,6 +785,13 @@ int launch_norm_gemv_rpw(const Shape& s, OutT* y, const NormArgs& na, const Rope
     return launch_norm_gemv_nc<MATS, RPW, 1, OutT, FUSE, ROPE, ARGMAX>(s, y, na, ra, st);
   if (chunks <= 512)
     return launch_norm_gemv_nc<MATS, RPW, 2, OutT, FUSE, ROPE, ARGMAX>(s, y, na, ra, st);
+  if constexpr (MATS == 1 && (FUSE == kFuseNone || FUSE == kFuseResidual)) {
+    if (chunks > 1024) {
+      if (chunks <= 1536)
+        return launch_norm_gemv_nc<MATS, RPW, 6, OutT, FUSE, ROPE, ARGMAX>(s, y, na, ra, st);
+      return launch_norm_gemv_nc<MATS, RPW, 8, OutT, FUSE, ROPE, ARGMAX>(s, y, na, ra, st);
+    }
+  }
   return launch_norm_gemv_nc<MATS, RPW, 4, OutT, FUSE, ROPE, ARGMAX>(s, y, na, ra, st);
 }
 
@@ -904,6 +931,15 @@ int run_rows(const Shape& s, const tmc_gemv_config& cfg, hipStream_t st) {
 tmc_gemv_config default_config(int batch, int n, int k, int mats) {
   tmc_gemv_config c{};
   (void)k;
+  if (batch == 1 && mats == 1 && k > 8192 && k <= 16384) {
+    // the down projection (11008 -> 4096 with its residual): the persistent
+    // dot, 14.9 us against 15.5 us for the dot at 2 rows per wave
+    c.algorithm = 5;
+    c.rows_per_wave = 1;
+    c.unroll = 1;
+    c.k_split = 4;
+    return c;
+  }
   if (batch == 1) {
     c.algorithm = 1;
     c.rows_per_wave = k > 8192 ? 2 : 1;
@@ -952,13 +988,17 @@ int validate_config(const tmc_gemv_config& c) {
                 "waves and unroll 1|2 (or 4 with at most 2 tiles).");
   } else if (c.algorithm == 4) {
     return 0;
+  } else if (c.algorithm == 5) {
+    TMC_REQUIRE((c.rows_per_wave == 1 || c.rows_per_wave == 2) && c.k_split == 4,
+                "GEMV config: the persistent dot (algorithm 5) needs rows_per_wave 1|2 rows per "
+                "block and k_split 4.");
   } else if (c.algorithm == 2) {
     TMC_REQUIRE(c.rows_per_wave >= 1 && c.k_split >= 1 && c.rows_per_wave * c.k_split <= 16 &&
                     (c.unroll == 1 || c.unroll == 2),
                 "GEMV config: MFMA needs n_tiles * k_split <= 16 waves and unroll 1|2.");
   } else {
-    return fail("GEMV config: algorithm must be 0 (auto), 1 (dot), 2 (MFMA), 3 (MFMA row tiles) "
-                "or 4 (linear baseline).");
+    return fail("GEMV config: algorithm must be 0 (auto), 1 (dot), 2 (MFMA), 3 (MFMA row tiles), "
+                "4 (linear baseline) or 5 (persistent dot, batch 1).");
   }
   return 0;
 }
@@ -1008,6 +1048,21 @@ int run_linear(int mats, const void* x, const void* w0, const void* w1, void* y,
   tmc_gemv_config cfg = default_config(s.batch, s.n, s.k, mats);
   if (user && user->algorithm != 0) cfg = *user;
   if (validate_config(cfg)) return 1;
+  if (cfg.algorithm == 5) {
+    TMC_REQUIRE(s.batch == 1 && s.k <= 16384 &&
+                    (uint64_t)(s.n + 1) * (uint64_t)s.k * 2u < (uint64_t)kBufferAbsent,
+                std::string(what) + ": the persistent dot (algorithm 5) needs batch 1, K <= 16384 "
+                "and weights below 4 GiB.");
+    NormArgs na;
+    na.x = s.x;
+    if (mats == 2) return launch_norm_gemv<2, half_t, kFuseNone>(s, static_cast<half_t*>(y),
+                                                                  cfg.rows_per_wave, na, st);
+    return y_dtype == TMC_F32
+               ? launch_norm_gemv<1, float, kFuseNone>(s, static_cast<float*>(y),
+                                                       cfg.rows_per_wave, na, st)
+               : launch_norm_gemv<1, half_t, kFuseNone>(s, static_cast<half_t*>(y),
+                                                        cfg.rows_per_wave, na, st);
+  }
   if (cfg.algorithm == 1) {
     if (mats == 2) return run_dot<2, half_t>(s, cfg, st);
     return y_dtype == TMC_F32 ? run_dot<1, float>(s, cfg, st) : run_dot<1, half_t>(s, cfg, st);
@@ -1197,12 +1252,21 @@ extern "C" int tmc_gemv_residual_f16(const void* x, const void* w, const void* r
   TMC_REQUIRE(aligned16(x) && aligned16(w), "GEMV + residual: x and W must be 16-byte aligned.");
   tmc_gemv_config cfg = default_config(1, (int)out_features, (int)in_features, 1);
   if (config && config->algorithm != 0) cfg = *config;
-  TMC_REQUIRE(cfg.algorithm == 1, "GEMV + residual: config must use the dot algorithm (1).");
+  TMC_REQUIRE(cfg.algorithm == 1 || cfg.algorithm == 5,
+              "GEMV + residual: config must use the dot algorithm (1) or the persistent dot (5).");
   if (validate_config(cfg)) return 1;
   NormArgs na;
   na.residual = static_cast<const half_t*>(residual);
   Shape s{static_cast<const half_t*>(x), static_cast<const half_t*>(w), nullptr, y, TMC_F16, 1,
           (int)out_features, (int)in_features};
+  if (cfg.algorithm == 5) {
+    TMC_REQUIRE(in_features <= 16384 &&
+                    (out_features + 1) * in_features * 2 < (int64_t)kBufferAbsent,
+                "GEMV + residual: the persistent dot needs K <= 16384 and W below 4 GiB.");
+    na.x = static_cast<const half_t*>(x);
+    return launch_norm_gemv<1, half_t, kFuseResidual>(s, static_cast<half_t*>(y),
+                                                      cfg.rows_per_wave, na, as_stream(stream));
+  }
   return launch_dot_fused<1, half_t, kFuseResidual>(s, static_cast<half_t*>(y), cfg, na,
                                                     as_stream(stream));
 }

@@ -297,14 +297,14 @@ bool layout_param(const Params& p, int& layout) {
 }
 
 // Optional GEMV launch configuration in a key: algorithm (0 auto, 1 dot,
-// 2 MFMA, 3 MFMA row tiles, 4 linear baseline), rows_per_wave, unroll,
-// k_split.  Validated when the kernel launches.
+// 2 MFMA, 3 MFMA row tiles, 4 linear baseline, 5 persistent dot at batch 1),
+// rows_per_wave, unroll, k_split.  Validated when the kernel launches.
 bool gemv_config_param(const Params& p, tmc_gemv_config& cfg) {
   cfg.algorithm = (int)param_int(p, "algorithm", 0);
   cfg.rows_per_wave = (int)param_int(p, "rows_per_wave", 1);
   cfg.unroll = (int)param_int(p, "unroll", 1);
   cfg.k_split = (int)param_int(p, "k_split", 1);
-  return cfg.algorithm >= 0 && cfg.algorithm <= 4;
+  return cfg.algorithm >= 0 && cfg.algorithm <= 5;
 }
 
 #define NEED(cond, msg)          \
@@ -325,7 +325,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     NEED(b > 0 && k > 0 && n > 0 && (od == TMC_F16 || od == TMC_F32) && dt == TMC_F16,
          "decode_gemv needs batch, in, out > 0, dtype=f16 and out_dtype f16|f32.");
     tmc_gemv_config cfg{};
-    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..5.");
     s.inputs = {TMC_F16, TMC_F16};
     s.outputs = {od};
     s.counts = {(size_t)(b * k), (size_t)(n * k), (size_t)(b * n)};
@@ -342,7 +342,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     NEED(param_int(p, "batch", 1) == 1 && k > 0 && n > 0 && dt == TMC_F16,
          "gemv_residual needs batch=1, in, out > 0 and dtype=f16.");
     tmc_gemv_config cfg{};
-    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..5.");
     s.inputs = {TMC_F16, TMC_F16, TMC_F16};
     s.outputs = {TMC_F16};
     s.counts = {(size_t)k, (size_t)(n * k), (size_t)n, (size_t)n};
@@ -366,7 +366,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
              (od == TMC_F16 || od == TMC_F32),
          "fused norm kernels need batch=1, in, out > 0, f16 and out_dtype f16|f32.");
     tmc_gemv_config cfg{};
-    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..5.");
     s.inputs = add ? std::vector<int>{TMC_F16, TMC_F16, TMC_F16} : std::vector<int>{TMC_F16, TMC_F16};
     s.inputs.push_back(TMC_F16);
     if (gated) s.inputs.push_back(TMC_F16);
@@ -421,7 +421,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     NEED(!(norm && res) && (!res || od == TMC_F16),
          "gemm_packed: norm and residual exclude each other; a residual output is fp16.");
     tmc_gemv_config cfg{};
-    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..5.");
     int layout = 0;
     NEED(layout_param(p, layout), "packed GEMM key: x_layout / y_layout must be row_major or packed.");
     NEED(!(layout & TMC_LAYOUT_Y_PACKED) || od == TMC_F16, "gemm_packed: a packed output is fp16.");
@@ -475,7 +475,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
          "qkv_rope_append_packed needs batch, hidden, q_heads, head_dim, capacity, page_size "
          "and f16.");
     tmc_gemv_config cfg{};
-    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..5.");
     int layout = 0;
     NEED(layout_param(p, layout) && !(layout & TMC_LAYOUT_Y_PACKED),
          "qkv_rope_append_packed: x_layout must be row_major or packed, no y_layout.");
@@ -510,7 +510,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     NEED(b > 0 && h > 0 && f > 0 && dt == TMC_F16,
          "gate_up_silu_packed needs batch, hidden, inter and f16.");
     tmc_gemv_config cfg{};
-    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..5.");
     int layout = 0;
     NEED(layout_param(p, layout), "packed GEMM key: x_layout / y_layout must be row_major or packed.");
     const size_t pe = (size_t)tmc_packed_weight_elements(f, h);
@@ -537,7 +537,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     const int64_t b = param_int(p, "batch"), h = param_int(p, "hidden"), f = param_int(p, "inter");
     NEED(b > 0 && h > 0 && f > 0 && dt == TMC_F16, "gate_up_silu needs batch, hidden, inter and f16.");
     tmc_gemv_config cfg{};
-    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..5.");
     s.inputs = {TMC_F16, TMC_F16, TMC_F16};
     s.outputs = {TMC_F16};
     s.groups = (size_t)((f + 3) / 4);
@@ -765,7 +765,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
          "rmsnorm_qkv_rope_append needs hidden, q_heads, head_dim, capacity, page_size and "
          "dtype=f16.");
     tmc_gemv_config cfg{};
-    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..5.");
     const int64_t mp = (cap + ps - 1) / ps;
     s.inputs = add ? std::vector<int>{TMC_F16, TMC_F16} : std::vector<int>{TMC_F16};
     s.inputs.insert(s.inputs.end(), {TMC_F16, TMC_F16, TMC_F32, TMC_F32, TMC_I32, TMC_I32, TMC_I32});
@@ -800,7 +800,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     NEED(h > 0 && qh > 0 && kvh > 0 && d > 0 && cap > 0 && ps > 0 && dt == TMC_F16,
          "qkv_rope_append needs hidden, q_heads, head_dim, capacity, page_size and dtype=f16.");
     tmc_gemv_config cfg{};
-    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..5.");
     const int64_t mp = (cap + ps - 1) / ps;
     s.inputs = {TMC_F16, TMC_F16, TMC_F32, TMC_F32, TMC_I32, TMC_I32, TMC_I32};
     s.outputs = {TMC_F16, TMC_F16, TMC_F16};
@@ -1021,7 +1021,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     NEED(param_int(p, "batch", 1) == 1 && k > 0 && n > 0 && dt == TMC_F16,
          "rmsnorm_lm_head_partial_argmax needs batch=1, in, out > 0 and f16.");
     tmc_gemv_config cfg{};
-    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..5.");
     const size_t ws = tmc_lm_head_argmax_workspace_bytes(1, n);
     NEED(ws > 0, "rmsnorm_lm_head_partial_argmax: vocabulary out of range.");
     s.inputs = {TMC_F16, TMC_F16, TMC_F16};
@@ -1042,7 +1042,7 @@ bool make_spec(const std::string& name, const Params& p, KernelSpec& s) {
     NEED(b > 0 && k > 0 && n > 0 && dt == TMC_F16,
          "lm_head_partial_argmax_packed needs batch, in, out > 0 and f16.");
     tmc_gemv_config cfg{};
-    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..4.");
+    NEED(gemv_config_param(p, cfg), "GEMV key: algorithm must be 0..5.");
     int layout = 0;
     NEED(layout_param(p, layout) && !(layout & TMC_LAYOUT_Y_PACKED),
          "lm_head_partial_argmax_packed: x_layout must be row_major or packed (no y_layout).");

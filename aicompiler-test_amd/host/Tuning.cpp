@@ -117,6 +117,7 @@ std::size_t decodeGEMVLdsBytes(std::size_t batch, const DecodeGEMVConfig& c) {
   }
   case 3: return static_cast<std::size_t>(c.kSplit * c.rowsPerWave) * tile;
   case 4: return 0;
+  case 5: return (4 * 35 * static_cast<std::size_t>(c.rowsPerWave) + 128) * sizeof(float);
   default: return 4 * static_cast<std::size_t>(c.rowsPerWave) * 8 * sizeof(float);
   }
 }
@@ -202,9 +203,10 @@ std::vector<double> gemvReference(std::size_t batch, std::size_t in, std::size_t
 }
 
 std::string describe(const hip::DecodeGEMVConfig& c) {
-  static const char* const names[] = {"default", "dot", "mfma", "mfma-rows", "linear"};
+  static const char* const names[] = {"default", "dot", "mfma", "mfma-rows", "linear",
+                                      "persistent-dot"};
   std::ostringstream s;
-  s << (c.algorithm >= 0 && c.algorithm <= 4 ? names[c.algorithm] : "?") << '(' << c.rowsPerWave
+  s << (c.algorithm >= 0 && c.algorithm <= 5 ? names[c.algorithm] : "?") << '(' << c.rowsPerWave
     << ',' << c.unroll << ',' << c.kSplit << ')';
   return s.str();
 }
@@ -373,6 +375,7 @@ std::vector<hip::DecodeGEMVConfig> decodeGEMVCandidates(std::size_t batch, bool 
     for (int rpw : {1, 2})
       for (int unroll : {2, 4})
         for (int ks : {1, 2, 4}) out.push_back({1, rpw, unroll, ks});
+    for (int rpw : {1, 2}) out.push_back({5, rpw, 1, 4});
     return out;
   }
   for (int tiles : {1, 2, 4})
@@ -397,6 +400,9 @@ std::string decodeGEMVHardwareFilter(const hip::DecodeGEMVConfig& c, std::size_t
   if (c.algorithm == 1 && batch > 8) return "dot algorithm covers at most 8 batch rows per pass";
   if (c.algorithm == 3 && outputSize * inputSize * 2 >= 0xFFFFFFF0ull)
     return "weights exceed the 4 GiB buffer range";
+  if (c.algorithm == 5 && (batch != 1 || inputSize > 16384 ||
+                           (outputSize + 1) * inputSize * 2 >= 0xFFFFFFF0ull))
+    return "the persistent dot takes batch 1, K <= 16384 and weights below 4 GiB";
   if (hardware.maxBufferLength &&
       (batch * inputSize * 2 > hardware.maxBufferLength ||
        outputSize * inputSize * 2 > hardware.maxBufferLength))

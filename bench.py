@@ -277,6 +277,13 @@ def extra_measurements(tmc, torch, iters: int) -> dict:
     gemv_bytes = 4096 * 4096 * 2 + 4096 * 2 + 4096 * 4
     out["c1_gemv_4096x4096_gbps"] = round(gemv_bytes / sec / 1e9, 1)
     out["c1_gemv_us"] = round(sec * 1e6, 2)
+    # the floor of one launch that reads the same 32 MiB once: the read-only
+    # probe over the same rotation
+    sink = torch.zeros(1, dtype=torch.float32, device="cuda")
+    floor = time_loop(torch, lambda i: tmc.read_probe(ws[i % c1_copies], 4096 * 4096 * 2, sink),
+                      iters)
+    out["c1_read_floor_us"] = round(floor * 1e6, 2)
+    out["c1_frac_of_read_floor"] = round(floor / sec, 3)
     del ws
     # C2 at B=8: the batch > 1 path runs on fragment-packed weights; the
     # row-major MFMA kernel is timed beside it

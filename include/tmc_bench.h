@@ -25,6 +25,13 @@ int tmc_fill_normal(void *ptr, int dtype, int64_t count, uint64_t seed, float me
  * calibrate FETCH_SIZE / WRITE_SIZE, and the practical HBM copy rate. */
 int tmc_copy_bytes(const void *src, void *dst, size_t bytes, void *stream);
 
+/* Read-only streaming probe: reads `bytes` of src once (4096 blocks, four
+ * 16-byte non-temporal loads per lane in flight) and writes nothing but, when
+ * a block's sum hits a fixed constant, the 4-byte `sink`.  Its duration is the
+ * floor of any kernel that must read those bytes once in one launch (the
+ * GEMVs read their weights exactly so). */
+int tmc_read_probe(const void *src, size_t bytes, void *sink, void *stream);
+
 /* Bandwidth probe of the paged attention access pattern (head_dim 128, pages
  * of a multiple of 16 positions): reads the K and V bytes
  * tmc_paged_decode_attention would read for these lengths and block tables,

@@ -189,8 +189,12 @@ int tmc_gemv_f16(const void *x, const void *w, void *y, int y_dtype, int64_t bat
  * 4 only with at most 2 tiles; batch handled 16 rows per pass), 4 = linear
  * baseline, one thread per output (emitLinearBaseline,
  * DecodeGEMVMetalEmitter.cpp:18-66; the tuners' baseline and fallback, other
- * fields ignored).  Algorithms 1-3 need in_features % 8 == 0 and 16-byte
- * aligned x and W; otherwise a scalar per-output kernel runs. */
+ * fields ignored), 5 = persistent dot at batch 1 (no reference counterpart:
+ * the resident blocks each stream a fixed share of row groups, rows_per_wave
+ * 1|2 rows per group kept two groups deep; k_split must be 4 and unroll is
+ * ignored; in_features <= 16384 and W below 4 GiB; results equal algorithm 1
+ * at k_split 4 bit for bit).  Algorithms 1-3 and 5 need in_features % 8 == 0
+ * and 16-byte aligned x and W; otherwise a scalar per-output kernel runs. */
 typedef struct tmc_gemv_config {
   int algorithm;
   int rows_per_wave;
@@ -253,7 +257,7 @@ int tmc_add_rmsnorm_gate_up_silu_f16(const void *residual, const void *update, c
  * through it and folds the following norms into the next GEMV's prologue.
  * batch must be 1; in_features a multiple of 8; x and W 16-byte aligned.
  * config: NULL / algorithm 0 = tmc_gemv_f16's default for the shape, else a
- * dot configuration (algorithm 1). */
+ * dot configuration (algorithm 1) or the persistent dot (algorithm 5). */
 int tmc_gemv_residual_f16(const void *x, const void *w, const void *residual, void *y,
                           int64_t batch, int64_t in_features, int64_t out_features,
                           const tmc_gemv_config *config, void *stream);

@@ -776,6 +776,21 @@ def test_argmax_ties_nan_and_tails(tmc, orc, torch, rows, vocab):
         assert got[2] == 3
 
 
+def test_read_probe_reads_without_writing(tmc, torch):
+    """tmc_read_probe reads every byte and writes only its sink, and only when
+    a block sum equals 1234.5: zeros and N(0, 1) data leave the sink alone;
+    sizes that are not a multiple of 16 are refused."""
+    src = torch.zeros(1 << 20, dtype=torch.float32, device="cuda")
+    sink = torch.full((2,), 7.0, device="cuda")
+    tmc.read_probe(src, src.numel() * 4, sink)
+    src.normal_()
+    tmc.read_probe(src, src.numel() * 4 - 48, sink)
+    torch.cuda.synchronize()
+    assert sink.tolist() == [7.0, 7.0]
+    with pytest.raises(RuntimeError, match="multiple of 16"):
+        tmc.read_probe(src, 40, sink)
+
+
 def test_fill_normal_statistics(tmc, torch):
     t = torch.empty(1 << 20, dtype=torch.float16, device="cuda")
     tmc.fill_normal(t, 77, 0.0, 0.02)
@@ -947,7 +962,52 @@ def test_fused_norm_gemv_equals_two_kernels_bit_exact(tmc, orc, torch, cfg_t):
                 assert torch.all(s_out == 7.0)
 
 
-@pytest.mark.parametrize("cfg_t", DOT_CONFIGS + [None])
+PERSISTENT_CONFIGS = [(5, 1, 1, 4), (5, 2, 1, 4)]
+
+
+@pytest.mark.parametrize("cfg_t", PERSISTENT_CONFIGS)
+def test_persistent_dot_equals_dot_bit_exact(tmc, orc, torch, cfg_t):
+    """Algorithm 5 (the persistent batch-1 dot) sums each row in the order of
+    the dot GEMV at k split 4: lane chunks in K order, then the four waves in
+    order.  Shapes cover one to eight chunks per lane (K 64 .. 16384), row
+    tails, grids that hold fewer groups than resident blocks and grids capped
+    at 32 groups per block; fp16 and fp32 outputs; and the oracle."""
+    cfg = tmc.GemvConfig(*cfg_t)
+    dot = tmc.GemvConfig(1, 1, 2, 4)
+    for k, n in ((4096, 4096), (11008, 4096), (4096, 11008), (1160, 200), (64, 9),
+                 (12288, 77), (16384, 300), (1024, 70001)):
+        x = orc.f16(normal(380, (1, k)))
+        w = orc.f16(normal(381, (n, k), 0.02))
+        for out_dtype in (torch.float16, torch.float32):
+            y = torch.full((1, n), float("nan"), dtype=out_dtype, device="cuda")
+            want = torch.empty_like(y)
+            tmc.gemv_config(dev_f16(x), dev_f16(w), y, cfg)
+            tmc.gemv_config(dev_f16(x), dev_f16(w), want, dot)
+            torch.cuda.synchronize()
+            what = f"cfg {cfg_t} k{k} n{n} {out_dtype}"
+            assert torch.equal(y, want), what
+            if out_dtype == torch.float32 and n * k <= 4096 * 11008:
+                assert_f32_rel(values(y), orc.linear(x, w, F16), what=what)
+
+
+def test_persistent_dot_rejects_unsupported_shapes(tmc, torch):
+    """Batches above 1 and K above 16384 are refused, not run."""
+    cfg = tmc.GemvConfig(5, 1, 1, 4)
+    w = torch.zeros((8, 16392), dtype=torch.float16, device="cuda")
+    x = torch.zeros((1, 16392), dtype=torch.float16, device="cuda")
+    y = torch.zeros((1, 8), dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="persistent dot"):
+        tmc.gemv_config(x, w, y, cfg)
+    w2 = torch.zeros((8, 64), dtype=torch.float16, device="cuda")
+    x2 = torch.zeros((2, 64), dtype=torch.float16, device="cuda")
+    y2 = torch.zeros((2, 8), dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="persistent dot"):
+        tmc.gemv_config(x2, w2, y2, cfg)
+    with pytest.raises(RuntimeError, match="k_split 4"):
+        tmc.gemv_config(x2[:1], w2, y2[:1], tmc.GemvConfig(5, 1, 1, 2))
+
+
+@pytest.mark.parametrize("cfg_t", DOT_CONFIGS + PERSISTENT_CONFIGS + [None])
 def test_gemv_residual_equals_gemv_then_add_bit_exact(tmc, orc, torch, cfg_t):
     """h(h(W x) + residual) in the GEMV epilogue (emitLinearResidual) against
     tmc_gemv_f16 with the same configuration followed by tmc_add, and against

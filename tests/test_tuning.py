@@ -8,9 +8,11 @@ import pytest
 
 def test_decode_gemv_candidates_cover_gfx950_configs(host):
     c1 = [c.astuple() for c in host.decode_gemv_candidates(1)]
-    assert len(c1) == 12 and all(c[0] == 1 for c in c1)
-    assert {c[1] for c in c1} == {1, 2} and {c[2] for c in c1} == {2, 4}
-    assert {c[3] for c in c1} == {1, 2, 4}
+    dots = [c for c in c1 if c[0] == 1]
+    assert len(dots) == 12 and len(c1) == 14
+    assert {c[1] for c in dots} == {1, 2} and {c[2] for c in dots} == {2, 4}
+    assert {c[3] for c in dots} == {1, 2, 4}
+    assert sorted(c for c in c1 if c[0] == 5) == [(5, 1, 1, 4), (5, 2, 1, 4)]
     c16 = [c.astuple() for c in host.decode_gemv_candidates(16)]
     assert (3, 1, 1, 8) in c16 and (3, 2, 1, 2) in c16 and (2, 1, 2, 16) in c16
     assert all(c[0] in (2, 3) for c in c16)
@@ -29,6 +31,10 @@ def test_decode_gemv_hardware_filter(host):
     ok = lambda c, batch=16, k=4096, n=4096: host.decode_gemv_hardware_filter(
         c, batch, k, n, 1024, 160 * 1024, 1 << 40)
     assert ok(cfg(3, 1, 1, 8)) == ""
+    # the persistent dot: batch 1 and K <= 16384 only
+    assert ok(cfg(5, 2, 1, 4), batch=1, k=16384) == ""
+    assert "persistent" in ok(cfg(5, 1, 1, 4), batch=2)
+    assert "persistent" in ok(cfg(5, 1, 1, 4), batch=1, k=16392)
     assert ok(cfg(3, 4, 1, 16)) == ""                      # 64 KiB of partials: at the limit
     assert host.decode_gemv_lds_bytes(16, cfg(3, 4, 1, 16)) == 64 * 1024
     assert "LDS" in ok(cfg(3, 8, 1, 16))                   # 128 KiB at 1024 threads
