@@ -21,6 +21,8 @@ case "$workload" in
   extra)
     args=(--extra-only)
     algo=("gemv_dot_kernel@262144x1x1=33579008"                      # C1 4096 x 4096
+          "read_probe_kernel=33554432"                                # C1's read floor, 32 MiB
+          "gather_probe_kernel=147775488"                             # C4 K/V bytes alone
           "attn_mfma_kernel<4, 1, 4>=148046676"                       # C4 paged GQA
           "attn_mfma_kernel<1, 0, 4>=67125248"                        # C3 L = 4095 (+1)
           "packed_gemm_kernel [Li2ELi2EDF16_=180596736"               # C2 B=8 gate/up
@@ -35,7 +37,7 @@ case "$workload" in
     # residual added in the epilogue.
     algo=("gemv_norm_kernel [Li2ELi1ELi2EDF16_Li2ELb0E]@313344x1x1=180393472"  # B=1 norm + gate/up + SiLU*Mul
           "gemv_norm_kernel [Li1ELi2ELi2EDF16_Li2ELb1E]@393216x1x1=100704256"  # B=1 norm + q.k.v + RoPE + append
-          "gemv_dot_kernel [Li1ELi1ELi2ELi4ELi4EDF16_Li3ELb0E]@524288x1x1=90215936"  # B=1 down + residual
+          "gemv_norm_kernel [Li1ELi1ELi6EDF16_Li3ELb0E]=90215936"      # B=1 down + residual (persistent dot)
           "gemv_dot_kernel [Li1ELi1ELi2ELi4ELi2EDF16_Li3ELb0E]@262144x1x1=33579008"  # B=1 o + residual
           "packed_gemm_kernel [Li2ELi2EDF16_Lb1ELb1ELb0ELi1E]@176128x1x1=180838400"  # B=16 norm + gate/up
           "packed_gemm_kernel [Li1ELi2EDF16_Lb1ELb0ELb1ELi1E]@196608x1x1=101187584"  # B=16 norm + q.k.v
@@ -76,7 +78,8 @@ if [ "$workload" = stalls ]; then
   for pass in sq sq2 tcp lat occ; do dbs+=(--db "$out/db/$pass/run_results.db"); done
   python3 "$root/aicompiler-test_amd/profiling.py" stalls "${dbs[@]}" \
     --trace "$out/db/trace/run_results.db" --kernel attn_mfma_kernel \
-    --kernel gather_probe_kernel --kernel gemv_dot_kernel --kernel copy_kernel \
+    --kernel gather_probe_kernel --kernel gemv_dot_kernel --kernel read_probe_kernel \
+    --kernel copy_kernel \
     --command "bash aicompiler-test_amd/profile_counters.sh stalls OUT" \
     --workload "bench.py --extra-only: C1 GEMV, C2 B=8, C3, C4 and the C4 gather probe" \
     --json "$out/stalls.json" > /dev/null

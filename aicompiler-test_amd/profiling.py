@@ -16,7 +16,10 @@ Subcommands over the rocpd SQLite databases rocprofv3 writes:
            kernel that issues MFMA, with achieved TFLOP/s from the trace;
   stalls   issue and stall counters (SQ wave / wait / issue cycles, VMEM
            latency, occupancy, TA busy, TCP-to-L2 request latency, address
-           translation) per dispatch of chosen kernels, with per-wave ratios.
+           translation) per dispatch of chosen kernels, with per-wave ratios;
+  c4       the C4 record: the paged attention kernel and the gather probe
+           over the same bytes, their traffic rows (from `table --json`) and
+           stall rows (from `stalls --json`) side by side.
 
 FETCH_SIZE on gfx950 counts each 128-byte EA read request as 64 bytes (its
 expression adds TCC_BUBBLE x 128, and TCC_BUBBLE stays 0), so a read-heavy
@@ -306,6 +309,47 @@ def stall_table(dbs: list, trace_db: str, kernels: list, min_calls: int) -> list
     return rows
 
 
+C4_WORKLOAD = ("C4 paged GQA decode attention: 16 requests, 32 q / 8 kv heads x 128, pages of "
+               "16, lengths U[65, 4096] (seed 403), 2 pools x 3 disjoint block-table sets")
+
+
+def c4_record(traffic_json: str, stalls_json: str, command: str) -> dict:
+    """The attention kernel and the gather probe of the C4 rotation: traffic
+    (bytes per launch, L2 hit rate) and stall counters, one entry each, and
+    the probe-over-attention ratios the account of the gap rests on."""
+    with open(traffic_json) as f:
+        traffic_rows = json.load(f)
+    with open(stalls_json) as f:
+        stall_rows = json.load(f)["kernels"]
+
+    def pick(rows, name):
+        found = [r for r in rows if r["kernel"].startswith(name)]
+        if not found:
+            raise SystemExit(f"{name}: no row")
+        return max(found, key=lambda r: r["calls"] * r["avg_us"])
+
+    out = {"workload": C4_WORKLOAD, "command": command, "scales": traffic_rows["scales"]}
+    for key, name in (("attention_kernel", "attn_mfma_kernel<4, 1, 4>"),
+                      ("gather_probe", "gather_probe_kernel")):
+        out[key] = {"traffic": pick(traffic_rows["kernels"], name),
+                    "stalls": pick(stall_rows, name)}
+    att, probe = out["attention_kernel"]["stalls"], out["gather_probe"]["stalls"]
+    ratios = {}
+    for field in ("avg_us", "MeanOccupancyPerCU", "VmemLatency", "TA_ADDR_STALLED_BY_TC_CYCLES_sum",
+                  "TA_TA_BUSY_sum", "SQ_INSTS_VALU", "SQ_WAIT_ANY"):
+        if field in att and field in probe and probe[field]:
+            ratios[field] = round(att[field] / probe[field], 3)
+    out["attention_over_probe"] = ratios
+    out["notes"] = {
+        "algorithmic_bytes": "sum of lengths x 8 kv heads x 128 x 2 B x (K and V) + 4 B per "
+                             "block-table entry + q and out (fp16)",
+        "ea_read_bytes": "32/64/128 B x TCC_EA0_RDREQ_32B/64B/128B per dispatch",
+        "MeanOccupancyPerCU": "resident waves per CU averaged over the dispatch",
+        "TA_ADDR_STALLED_BY_TC_CYCLES_sum": "texture-addresser cycles stalled by the vector L1, "
+                                            "summed over CUs"}
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -353,7 +397,19 @@ def main(argv=None) -> int:
     st.add_argument("--command", default="")
     st.add_argument("--workload", default="")
     st.add_argument("--json")
+    c = sub.add_parser("c4")
+    c.add_argument("--traffic", required=True, help="traffic.json of the extra workload")
+    c.add_argument("--stalls", required=True, help="stalls.json of the stalls workload")
+    c.add_argument("--command", required=True)
+    c.add_argument("--json")
     a = ap.parse_args(argv)
+    if a.cmd == "c4":
+        text = json.dumps(c4_record(a.traffic, a.stalls, a.command), indent=1) + "\n"
+        if a.json:
+            with open(a.json, "w") as f:
+                f.write(text)
+        sys.stdout.write(text)
+        return 0
     if a.cmd == "stalls":
         rows = stall_table(a.db, a.trace, a.kernel, a.min_calls)
         text = json.dumps({"workload": a.workload, "command": a.command, "kernels": rows},

@@ -378,6 +378,7 @@ def extra_measurements(tmc, torch, iters: int) -> dict:
     out["counter_files"] = {
         "c1_c2b8_c3_c4": "profiles/c1_c4_kernels_traffic.md",
         "c4_attention": "profiles/attention_c4_counters.json",
+        "c1_c4_stalls": "profiles/c1_c4_stall_counters.json",
         "c2_b8_mfma": "profiles/c2_b8_mfma_utilisation.json",
         "c5_decode": "profiles/c5_decode_prefill_traffic.md",
         "c5_mfma": "profiles/c5_mfma_utilisation.json"}
