@@ -35,16 +35,16 @@ case "$workload" in
     # and the residual epilogues (residual read, sum written); batch 16 the
     # packed GEMMs with the norm folded (gamma in the weights) or the
     # residual added in the epilogue.
-    algo=("gemv_norm_kernel [Li2ELi1ELi2EDF16_Li2ELb0E]@313344x1x1=180393472"  # B=1 norm + gate/up + SiLU*Mul
-          "gemv_norm_kernel [Li1ELi2ELi2EDF16_Li2ELb1E]@393216x1x1=100704256"  # B=1 norm + q.k.v + RoPE + append
-          "gemv_norm_kernel [Li1ELi1ELi6EDF16_Li3ELb0E]=90215936"      # B=1 down + residual (persistent dot)
+    algo=("gemv_norm_kernel [Li2ELi1ELi2EDF16_Li2ELb0E@313344x1x1=180393472"  # B=1 norm + gate/up + SiLU*Mul
+          "gemv_norm_kernel [Li1ELi2ELi2EDF16_Li2ELb1E@393216x1x1=100704256"  # B=1 norm + q.k.v + RoPE + append
+          "gemv_norm_kernel [Li1ELi1ELi6EDF16_Li3ELb0E=90215936"       # B=1 down + residual (persistent dot)
           "gemv_dot_kernel [Li1ELi1ELi2ELi4ELi2EDF16_Li3ELb0E]@262144x1x1=33579008"  # B=1 o + residual
-          "packed_gemm_kernel [Li2ELi2EDF16_Lb1ELb1ELb0ELi1E]@176128x1x1=180838400"  # B=16 norm + gate/up
-          "packed_gemm_kernel [Li1ELi2EDF16_Lb1ELb0ELb1ELi1E]@196608x1x1=101187584"  # B=16 norm + q.k.v
+          "packed_gemm_kernel [Li2ELi2EDF16_Lb1ELb1ELb0ELi1E@176128x1x1=180838400"  # B=16 norm + gate/up
+          "packed_gemm_kernel [Li1ELi2EDF16_Lb1ELb0ELb1ELi1E@196608x1x1=101187584"  # B=16 norm + q.k.v
           # B=16 o + residual (33947648) and down + residual (90791936): with
           # packed input both are this kernel at this grid, one table row
           # over both launches, so the row's bytes are their mean
-          "packed_gemm_kernel [Li1ELi2EDF16_Lb1ELb1ELb0ELi2E]@262144x1x1=62369792") ;;
+          "packed_gemm_kernel [Li1ELi2EDF16_Lb1ELb1ELb0ELi2E@262144x1x1=62369792") ;;
   stalls)
     args=(--extra-only)
     algo=() ;;

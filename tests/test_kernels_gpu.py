@@ -1334,6 +1334,50 @@ def test_attention_merge_launch_build(tmc, orc, torch):
         tmc._lib = saved
 
 
+@pytest.mark.parametrize("batch,qh,kvh,cap", [(16, 32, 8, 4096), (1, 32, 32, 4096),
+                                              (4, 16, 8, 2048), (3, 32, 4, 4096)])
+def test_merge_launch_build_equals_in_kernel_merge(tmc, orc, torch, batch, qh, kvh, cap):
+    """The in-kernel merge (last-arriving split block, agent-scope stores and
+    loads, no fences) against the merge launch of the TMC_ATTN_MERGE_LAUNCH=1
+    build, where stream order replaces the cross-block handshake: the same
+    partials merged in the same split order, so the output bits must agree.
+    GQA 4 (C4's group), MHA (C3-like rows), GQA 2, and GQA 8 (merge launch in
+    both builds); ragged lengths up to the capacity over random pages."""
+    d, p = 128, 16
+    max_pages = cap // p
+    rng = np.random.default_rng(1400 + batch)
+    lengths = rng.integers(1, cap + 1, size=batch).astype(np.int32)
+    lengths[0] = cap
+    pages = int(sum((int(n) + p - 1) // p for n in lengths)) + 3
+    perm = rng.permutation(pages).astype(np.int32)
+    tables = np.full((batch, max_pages), -1, np.int32)
+    cursor = 0
+    for i, n in enumerate(lengths):
+        need = (int(n) + p - 1) // p
+        tables[i, :need] = perm[cursor:cursor + need]
+        cursor += need
+    k_d = dev_f16(orc.f16(normal(1401, (pages, kvh, p, d))))
+    v_d = dev_f16(orc.f16(normal(1402, (pages, kvh, p, d))))
+    q_d = dev_f16(orc.f16(normal(1403, (batch, qh * d))))
+    valid_d, tables_d = dev(lengths), dev(tables)
+    active = torch.tensor([batch], dtype=torch.int32, device="cuda")
+    outs = []
+    saved = tmc._lib
+    try:
+        for lib in (saved, tmc.open_variant("libtmc_hip_merge_launch.so")):
+            tmc._lib = lib
+            out = torch.full((batch, qh * d), float("nan"), dtype=torch.float16, device="cuda")
+            tmc.paged_decode_attention(q_d, k_d, v_d, valid_d, tables_d, active, out, batch, qh,
+                                       kvh, d, p, max_pages, kvh * p * d, p * d,
+                                       _ws(tmc, torch, batch, qh, kvh, d, cap))
+            torch.cuda.synchronize()
+            outs.append(bits(out))
+    finally:
+        tmc._lib = saved
+    assert not np.isnan(outs[0].view(np.float16)).any()
+    assert np.array_equal(outs[0], outs[1])
+
+
 # ---------------------------------------------------------------- token-only LM head
 def _lm_head_inputs(orc, batch, k, vocab, seed):
     """Residual rows, gamma and an LM head W with planted duplicates: rows 5
