@@ -450,7 +450,7 @@ __device__ __forceinline__ long paged_offset(const AttnParams& p, const int* s_p
          (long)slot_in_page(p, pos) * 128;
 }
 
-template <int MODE>
+template <int MODE, bool VIA = false>
 __device__ __forceinline__ void issue_step(const AttnParams& p, const int* s_pages, int page0,
                                            size_t cbase, int kvh, int p0, int end, int j, int g,
                                            __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
@@ -481,10 +481,21 @@ __device__ __forceinline__ void issue_step(const AttnParams& p, const int* s_pag
       // without a select or branch per load.
       const unsigned tb = tile < 0 ? 0u : (unsigned)(tile * 2);
       const unsigned tmask = tile < 0 ? kAbsent : 0u;
-      const unsigned kmask = tmask | (tp + j < end ? 0u : kAbsent);
+      if constexpr (VIA) {
+        // whole rows: load q reads positions 4q .. 4q + 3 of the tile, lane
+        // (j, g) the 16-byte chunk j of position 4q + g (8 full cache lines
+        // per load); consume_step re-lays them in the MFMA operand order
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        st.k[t][s] = buffer_h8<MODE == 0>(rk, (tb + (unsigned)j * 256u + 16u * (4 * s + g)) | kmask);
+        for (int q = 0; q < 4; ++q) {
+          const unsigned rmask = tmask | (tp + 4 * q + g < end ? 0u : kAbsent);
+          st.k[t][q] = buffer_h8<MODE == 0>(rk, (tb + (unsigned)(4 * q + g) * 256u + 16u * j) | rmask);
+        }
+      } else {
+        const unsigned kmask = tmask | (tp + j < end ? 0u : kAbsent);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          st.k[t][s] = buffer_h8<MODE == 0>(rk, (tb + (unsigned)j * 256u + 16u * (4 * s + g)) | kmask);
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const unsigned vmask = tmask | (tp + 4 * i + g < end ? 0u : kAbsent);
@@ -505,19 +516,44 @@ __device__ __forceinline__ void issue_step(const AttnParams& p, const int* s_pag
   }
 }
 
-template <int GROUP, int MODE>
+template <int GROUP, int MODE, bool VIA = false>
 __device__ __forceinline__ void consume_step(const AttnParams& p, const int* s_pages, int page0,
                                              const KvStep<MODE>& st, const h8 (&qb)[4], int p0,
                                              int end, int j, int g, float (*s_pw)[GROUP],
-                                             float& m, float& lsum, float (&o)[GROUP][8]) {
+                                             float& m, float& lsum, float (&o)[GROUP][8],
+                                             h8* s_k = nullptr) {
   float sc[kMfmaTiles][4];
   float tile_max = -INFINITY;
+  h8 kf[kMfmaTiles][4];
+  if constexpr (VIA) {
+    // this wave's LDS slice, 16 rows x 16 chunks per tile; chunk c of row r
+    // at slot c ^ r, so the row-wise stores and the column-wise operand
+    // reads both touch 16 distinct bank groups per 16 lanes
+#pragma unroll
+    for (int t = 0; t < kMfmaTiles; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = 4 * q + g;
+        s_k[t * 256 + r * 16 + (j ^ r)] = st.k[t][q];
+      }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int t = 0; t < kMfmaTiles; ++t)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kf[t][s] = s_k[t * 256 + j * 16 + ((4 * s + g) ^ j)];
+    __builtin_amdgcn_wave_barrier();
+  } else {
+#pragma unroll
+    for (int t = 0; t < kMfmaTiles; ++t)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kf[t][s] = st.k[t][s];
+  }
 #pragma unroll
   for (int t = 0; t < kMfmaTiles; ++t) {
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.k[t][s], qb[s], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t][s], qb[s], acc, 0, 0, 0);
     const int tp = p0 + 16 * t;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -666,6 +702,14 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   __shared__ float s_o[WAVES][GROUP][D];
   __shared__ float s_p[WAVES][kMfmaStep][GROUP];
   __shared__ int s_pages[PAGED ? kMfmaMaxChunk + 1 : 1];
+  // Paged tiles (MODE 1) load K as whole rows and re-lay them for the MFMA
+  // through 8 KiB of LDS per wave.  Measured against the MFMA-order loads
+  // (16 positions x 64 bytes per load instruction): C4 38.7 -> 37.9 us,
+  // batch-16 MHA (8-wave blocks) 22.1 -> 21.5 us; the contiguous cache's
+  // two-step pipeline (MODE 0) lost 1.3% at L 4095 with it and keeps the
+  // direct loads; the 16-wave one-split blocks have no LDS to spare.
+  constexpr bool kVia = MODE == 1 && WAVES <= kMidWaves;
+  __shared__ h8 s_k[kVia ? WAVES : 1][kVia ? kMfmaTiles * 256 : 1];
 
   const int CHUNK = p.chunk;
   const int b = blockIdx.z, kvh = blockIdx.x, split = blockIdx.y;
@@ -737,20 +781,23 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
     // loads, which return zeros without memory traffic, and is not consumed).
     int p0 = begin + kMfmaStep * wave;
     KvStep<MODE> sa, sb;
-    issue_step<MODE>(p, s_pages, page0, cbase, kvh, p0, end, j, g, rk, rv, sa);
+    issue_step<MODE, kVia>(p, s_pages, page0, cbase, kvh, p0, end, j, g, rk, rv, sa);
     for (; p0 < end; p0 += 2 * kStride) {  // wave-uniform
-      issue_step<MODE>(p, s_pages, page0, cbase, kvh, p0 + kStride, end, j, g, rk, rv, sb);
-      consume_step<GROUP, MODE>(p, s_pages, page0, sa, qb, p0, end, j, g, s_pw, m, lsum, o);
+      issue_step<MODE, kVia>(p, s_pages, page0, cbase, kvh, p0 + kStride, end, j, g, rk, rv, sb);
+      consume_step<GROUP, MODE, kVia>(p, s_pages, page0, sa, qb, p0, end, j, g, s_pw, m, lsum, o,
+                                      s_k[kVia ? wave : 0]);
       if (p0 + kStride >= end) break;
-      issue_step<MODE>(p, s_pages, page0, cbase, kvh, p0 + 2 * kStride, end, j, g, rk, rv, sa);
-      consume_step<GROUP, MODE>(p, s_pages, page0, sb, qb, p0 + kStride, end, j, g, s_pw, m,
-                                lsum, o);
+      issue_step<MODE, kVia>(p, s_pages, page0, cbase, kvh, p0 + 2 * kStride, end, j, g, rk, rv,
+                             sa);
+      consume_step<GROUP, MODE, kVia>(p, s_pages, page0, sb, qb, p0 + kStride, end, j, g, s_pw, m,
+                                      lsum, o, s_k[kVia ? wave : 0]);
     }
   } else {
     for (int p0 = begin + kMfmaStep * wave; p0 < end; p0 += kStride) {
       KvStep<MODE> st;
-      issue_step<MODE>(p, s_pages, page0, cbase, kvh, p0, end, j, g, rk, rv, st);
-      consume_step<GROUP, MODE>(p, s_pages, page0, st, qb, p0, end, j, g, s_pw, m, lsum, o);
+      issue_step<MODE, kVia>(p, s_pages, page0, cbase, kvh, p0, end, j, g, rk, rv, st);
+      consume_step<GROUP, MODE, kVia>(p, s_pages, page0, st, qb, p0, end, j, g, s_pw, m, lsum, o,
+                                      s_k[kVia ? wave : 0]);
     }
   }
 
