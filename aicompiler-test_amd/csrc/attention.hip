@@ -705,10 +705,11 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   // Paged tiles (MODE 1) load K as whole rows and re-lay them for the MFMA
   // through 8 KiB of LDS per wave.  Measured against the MFMA-order loads
   // (16 positions x 64 bytes per load instruction): C4 38.7 -> 37.9 us,
-  // batch-16 MHA (8-wave blocks) 22.1 -> 21.5 us; the contiguous cache's
-  // two-step pipeline (MODE 0) lost 1.3% at L 4095 with it and keeps the
-  // direct loads; the 16-wave one-split blocks have no LDS to spare.
-  constexpr bool kVia = MODE == 1 && WAVES <= kMidWaves;
+  // batch-16 MHA (8-wave blocks) 22.1 -> 21.5 us, batch 1 (16-wave one-split
+  // blocks) at L 200 6.05 -> 5.45 us and at L 900 12.4 -> 10.2 us; the
+  // contiguous cache's two-step pipeline (MODE 0) lost 1.3% at L 4095 with
+  // it and keeps the direct loads.
+  constexpr bool kVia = MODE == 1;
   __shared__ h8 s_k[kVia ? WAVES : 1][kVia ? kMfmaTiles * 256 : 1];
 
   const int CHUNK = p.chunk;
