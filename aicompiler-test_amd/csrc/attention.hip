@@ -702,14 +702,16 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   __shared__ float s_o[WAVES][GROUP][D];
   __shared__ float s_p[WAVES][kMfmaStep][GROUP];
   __shared__ int s_pages[PAGED ? kMfmaMaxChunk + 1 : 1];
-  // Paged tiles (MODE 1) load K as whole rows and re-lay them for the MFMA
-  // through 8 KiB of LDS per wave.  Measured against the MFMA-order loads
-  // (16 positions x 64 bytes per load instruction): C4 38.7 -> 37.9 us,
-  // batch-16 MHA (8-wave blocks) 22.1 -> 21.5 us, batch 1 (16-wave one-split
-  // blocks) at L 200 6.05 -> 5.45 us and at L 900 12.4 -> 10.2 us; the
-  // contiguous cache's two-step pipeline (MODE 0) lost 1.3% at L 4095 with
-  // it and keeps the direct loads.
-  constexpr bool kVia = MODE == 1;
+  // 16-position tiles (MODE 0, MODE 1) load K as whole rows and re-lay them
+  // for the MFMA through 8 KiB of LDS per wave.  Measured against the
+  // MFMA-order loads (16 positions x 64 bytes per load instruction): C4
+  // 38.7 -> 37.9 us, batch-16 MHA (8-wave blocks) 22.1 -> 21.5 us, paged
+  // batch 1 (16-wave one-split blocks) at L 200 6.05 -> 5.45 us and at L 900
+  // 12.4 -> 10.2 us, contiguous batch 1 at capacity 1024, L 900 16.4 ->
+  // 12.4 us.  The contiguous cache's two-step pipeline (MODE 0, 4 waves)
+  // lost 1.3% at L 4095 with it and keeps the direct loads; MODE 2 looks up
+  // every position and keeps them too.
+  constexpr bool kVia = MODE == 1 || (MODE == 0 && WAVES != kWaves);
   __shared__ h8 s_k[kVia ? WAVES : 1][kVia ? kMfmaTiles * 256 : 1];
 
   const int CHUNK = p.chunk;
