@@ -67,14 +67,6 @@ constexpr int kMidWaves = 8;
 #ifndef TMC_ATTN_MERGE_LAUNCH
 #define TMC_ATTN_MERGE_LAUNCH 0
 #endif
-// Steps of K/V loads in flight per wave: two for the contiguous cache's
-// multi-split blocks (C3, L 4095: 15.8 -> 15.2 us; L 1024: 13.7 -> 12.4 us),
-// one elsewhere (paged C4: 38.5 -> 42.4 us with two, the 16-wave one-split
-// blocks have no registers to spare).
-template <int MODE, int WAVES> constexpr int attn_depth() {
-  return MODE == 0 && WAVES == kWaves ? 2 : 1;
-}
-
 struct AttnParams {
   const half_t* q;
   const half_t* k;
@@ -708,10 +700,10 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   // 38.7 -> 37.9 us, batch-16 MHA (8-wave blocks) 22.1 -> 21.5 us, paged
   // batch 1 (16-wave one-split blocks) at L 200 6.05 -> 5.45 us and at L 900
   // 12.4 -> 10.2 us, contiguous batch 1 at capacity 1024, L 900 16.4 ->
-  // 12.4 us.  The contiguous cache's two-step pipeline (MODE 0, 4 waves)
-  // lost 1.3% at L 4095 with it and keeps the direct loads; MODE 2 looks up
-  // every position and keeps them too.
-  constexpr bool kVia = MODE == 1 || (MODE == 0 && WAVES != kWaves);
+  // 12.4 us, contiguous C3 at L 1025 12.3 -> 11.0 us and at L 4095 the same
+  // 15.2-15.4 us as the direct loads with two steps in flight, which this
+  // replaces.  MODE 2 looks up every position and keeps the direct loads.
+  constexpr bool kVia = MODE != 2;
   __shared__ h8 s_k[kVia ? WAVES : 1][kVia ? kMfmaTiles * 256 : 1];
 
   const int CHUNK = p.chunk;
@@ -777,31 +769,11 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   float (*s_pw)[GROUP] = s_p[wave];
 
   constexpr int kStride = kMfmaStep * WAVES;
-  if constexpr (attn_depth<MODE, WAVES>() == 2) {
-    // Two steps in flight per wave: the next step's K/V loads are issued
-    // before this step's scores and PV run, so the wave's compute overlaps
-    // its own memory latency (a step past the range issues out-of-range
-    // loads, which return zeros without memory traffic, and is not consumed).
-    int p0 = begin + kMfmaStep * wave;
-    KvStep<MODE> sa, sb;
-    issue_step<MODE, kVia>(p, s_pages, page0, cbase, kvh, p0, end, j, g, rk, rv, sa);
-    for (; p0 < end; p0 += 2 * kStride) {  // wave-uniform
-      issue_step<MODE, kVia>(p, s_pages, page0, cbase, kvh, p0 + kStride, end, j, g, rk, rv, sb);
-      consume_step<GROUP, MODE, kVia>(p, s_pages, page0, sa, qb, p0, end, j, g, s_pw, m, lsum, o,
-                                      s_k[kVia ? wave : 0]);
-      if (p0 + kStride >= end) break;
-      issue_step<MODE, kVia>(p, s_pages, page0, cbase, kvh, p0 + 2 * kStride, end, j, g, rk, rv,
-                             sa);
-      consume_step<GROUP, MODE, kVia>(p, s_pages, page0, sb, qb, p0 + kStride, end, j, g, s_pw, m,
-                                      lsum, o, s_k[kVia ? wave : 0]);
-    }
-  } else {
-    for (int p0 = begin + kMfmaStep * wave; p0 < end; p0 += kStride) {
-      KvStep<MODE> st;
-      issue_step<MODE, kVia>(p, s_pages, page0, cbase, kvh, p0, end, j, g, rk, rv, st);
-      consume_step<GROUP, MODE, kVia>(p, s_pages, page0, st, qb, p0, end, j, g, s_pw, m, lsum, o,
-                                      s_k[kVia ? wave : 0]);
-    }
+  for (int p0 = begin + kMfmaStep * wave; p0 < end; p0 += kStride) {
+    KvStep<MODE> st;
+    issue_step<MODE, kVia>(p, s_pages, page0, cbase, kvh, p0, end, j, g, rk, rv, st);
+    consume_step<GROUP, MODE, kVia>(p, s_pages, page0, st, qb, p0, end, j, g, s_pw, m, lsum, o,
+                                    s_k[kVia ? wave : 0]);
   }
 
 #pragma unroll
