@@ -140,6 +140,31 @@ __global__ __launch_bounds__(FUSE == kPackedNorm ? kPackedNormWaves * kWave : 10
   const __amdgpu_buffer_rsrc_t r1 = buffer_rsrc(MATS == 2 ? p1 : p0, packed_bytes);
   const unsigned x_row = j < m_rows ? (unsigned)j * (unsigned)k_in * 2u : kNone;
   const unsigned w_base = (unsigned)nt * (unsigned)chunks * 1024u + (unsigned)lane * 16u;
+  // Output element of epilogue item q of this thread (item = threadIdx.x +
+  // q * threads, < 4 * 64): (row, col) and its index in y's layout.
+  auto item_at = [&](int idx, int& row, int& col) -> size_t {
+    const int l = idx % kWave, r = idx / kWave;
+    row = 4 * (l >> 4) + r;
+    col = nt * 16 + (l & 15);
+    if constexpr (YP)  // pass-relative fragment slot of (row, col)
+      return ((size_t)(col >> 5) * 64 + row + 16 * ((col & 31) >> 3)) * 8 + (col & 7);
+    return (size_t)row * n_out + col;
+  };
+  // kPackedResidual: the residual of each epilogue item is loaded first, ahead
+  // of the weight stream, so the epilogue waits on no memory (at batch 16 the
+  // o and down projections run one block per CU and end together, so a load
+  // in the epilogue was a round trip at the end of every launch)
+  constexpr int kItems = 4;  // epilogue items per thread at one wave per tile
+  half_t res_pre[kItems];
+  if constexpr (FUSE == kPackedResidual) {
+#pragma unroll
+    for (int q = 0; q < kItems; ++q) {
+      const int idx = (int)threadIdx.x + q * ks_count * kWave;
+      int row, col;
+      const size_t at = item_at(idx < 4 * kWave ? idx : 0, row, col);
+      res_pre[q] = idx < 4 * kWave && row < m_rows && col < n_out ? pf.residual[at] : half_t(0.0f);
+    }
+  }
   float squares = 0.0f;  // kPackedNorm: row j's sum of squares over this lane's k
   f4 acc[MATS];
 #pragma unroll
@@ -258,23 +283,23 @@ __global__ __launch_bounds__(FUSE == kPackedNorm ? kPackedNormWaves * kWave : 10
     return;
   }
   // acc[r] of lane (j, g) = out[batch 4g + r][row 16nt + j]
-  for (int idx = threadIdx.x; idx < 4 * kWave; idx += ks_count * kWave) {
+#pragma unroll
+  for (int q = 0; q < kItems; ++q) {
+    const int idx = (int)threadIdx.x + q * ks_count * kWave;
+    if (idx >= 4 * kWave) break;
     const int l = idx % kWave, r = idx / kWave;
     float a[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int m = 0; m < MATS; ++m)
       for (int w = 0; w < ks_count; ++w) a[m] += red[((w * MATS + m) * 4 + r) * kWave + l];
-    const int row = 4 * (l >> 4) + r;
-    const int col = nt * 16 + (l & 15);
+    int row, col;
+    const size_t at = item_at(idx, row, col);
     if (row < m_rows && col < n_out) {
-      size_t at = (size_t)row * n_out + col;
-      if constexpr (YP)  // pass-relative fragment slot of (row, col)
-        at = ((size_t)(col >> 5) * 64 + row + 16 * ((col & 31) >> 3)) * 8 + (col & 7);
       const float scale = row_scale(row);
       if constexpr (MATS == 2)
         y[at] = gated_value(a[0] * scale, a[1] * scale);
       else if constexpr (FUSE == kPackedResidual)
-        y[at] = from_float<OutT>(to_float<half_t>(pf.residual[at]) +
+        y[at] = from_float<OutT>(to_float<half_t>(res_pre[q]) +
                                  to_float<half_t>(from_float<half_t>(a[0])));
       else
         y[at] = from_float<OutT>(a[0] * scale);
