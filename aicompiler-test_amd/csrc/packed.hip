@@ -330,6 +330,13 @@ void default_packed(int64_t batch, int64_t n, int mats, int& unroll, int& ks) {
     ks = batch >= 8 ? 16 : 8;
 }
 
+// K tiles in flight per wave of the norm-folded LM head (N >= 16384, one
+// wave per 16-column tile), from MI355X sweeps at N 32000, K 4096 with
+// rotating weights: batch 16 1 (41.9 us against 44.8 with 2), batches 2-8 4
+// (40.3-40.8 against 40.8-41.4 us).  The norm form's 256-thread bound leaves
+// 4 tiles in flight without spills.
+int lm_head_unroll(int64_t batch) { return batch > 8 ? 1 : 4; }
+
 template <int MATS, typename OutT, bool XP, bool YP, bool ROPE = false, int FUSE = kPackedPlain,
           bool ARGMAX = false>
 int run_packed(const half_t* x, const half_t* p0, const half_t* p1, OutT* y, int64_t batch,
@@ -429,6 +436,7 @@ int packed_entry(int mats, const void* x, const void* p0, const void* p1, void* 
   // folded norm: 4 waves per tile below the LM head's width (batch 16 q.k.v
   // 20.5-20.9 us against 21.5 with the plain default of 2)
   if (fuse == kPackedNorm) ks = n >= 16384 ? std::min(ks, kPackedNormWaves) : kPackedNormWaves;
+  if (fuse == kPackedNorm && n >= 16384) unroll = lm_head_unroll(batch);
   if (config && config->algorithm != 0) {
     unroll = config->unroll;
     ks = config->k_split;
@@ -659,6 +667,7 @@ extern "C" int tmc_lm_head_partial_argmax_packed_norm_f16(
   int unroll, ks;
   default_packed(batch, vocabulary, 1, unroll, ks);
   ks = vocabulary >= 16384 ? std::min(ks, kPackedNormWaves) : kPackedNormWaves;
+  if (vocabulary >= 16384) unroll = lm_head_unroll(batch);
   if (config && config->algorithm != 0) {
     unroll = config->unroll;
     ks = config->k_split;
