@@ -118,6 +118,20 @@ __device__ __forceinline__ int valid_length(const AttnParams& p, int b) {
   return PAGED ? p.valid[b] : p.valid[0];
 }
 
+// Positions per split of the D = 128 kernel for a row of `valid` positions.
+// A contiguous cache (every row has the launch's one length) cuts the row
+// into max_splits splits of its own length, rounded up to 32-position
+// steps, instead of splits of the capacity's chunk, which leave blocks idle
+// when the length is far below the capacity (C3 at L 1025 of 4096: 11.0 ->
+// 8.7 us on MI355X; at L 4095 the splits are the same).  Paged rows, whose
+// lengths differ, keep the capacity's chunk.
+template <bool PAGED>
+__device__ __forceinline__ int mfma_chunk(const AttnParams& p, int valid) {
+  if (PAGED || p.max_splits <= 1) return p.chunk;
+  const int steps = (valid + kMfmaStep - 1) / kMfmaStep;
+  return (steps + p.max_splits - 1) / p.max_splits * kMfmaStep;
+}
+
 // Positions [p0, p0 + TILE) of one wave: K/V slices for lane (row r, column
 // chunk c) at positions p0 + r + NR*j, j < 4.
 template <int D, bool PAGED>
@@ -262,7 +276,8 @@ __global__ __launch_bounds__(D) void attn_combine_kernel(AttnParams p) {
   fetch(0);
   const int valid = valid_length<PAGED>(p, b);
   if (valid < 1 || valid > p.capacity) return;
-  const int nsplit = (valid + p.chunk - 1) / p.chunk;
+  const int chunk = D == 128 ? mfma_chunk<PAGED>(p, valid) : p.chunk;
+  const int nsplit = (valid + chunk - 1) / chunk;
   if (nsplit <= 1) return;
   float mx = -INFINITY, lsum = 0.0f, osum = 0.0f;
   bool bad = false;
@@ -706,7 +721,6 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   constexpr bool kVia = MODE != 2;
   __shared__ h8 s_k[kVia ? WAVES : 1][kVia ? kMfmaTiles * 256 : 1];
 
-  const int CHUNK = p.chunk;
   const int b = blockIdx.z, kvh = blockIdx.x, split = blockIdx.y;
   // One-split blocks (the whole row, max_pages <= the block's threads): each
   // thread fetches one block-table entry together with the row's length, so
@@ -732,6 +746,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   }
   if (b >= active_rows) return;
   if (valid < 1 || valid > p.capacity) return;
+  const int CHUNK = mfma_chunk<PAGED>(p, valid);
   const int nsplit = (valid + CHUNK - 1) / CHUNK;
   if (split >= nsplit) return;
   const int begin = split * CHUNK;

@@ -316,6 +316,26 @@ def test_decode_attention_edges(tmc, orc, torch, valid, d, qh, kvh):
     assert_f16_path(values(out), ref, what=f"attention valid={valid} d={d} group={qh // kvh}")
 
 
+@pytest.mark.parametrize("valid,qh,kvh", [(31, 32, 32), (33, 8, 2), (161, 32, 32), (512, 8, 8),
+                                           (1500, 16, 4), (3000, 32, 32)])
+def test_contiguous_splits_follow_the_length(tmc, orc, torch, valid, qh, kvh):
+    """A contiguous cache cuts each row into the capacity's split count of
+    its own length (32-position steps), not of the capacity: lengths on
+    both sides of the step and split boundaries at capacity 4096, batch 2,
+    against the oracle."""
+    b, d, cap = 2, 128, 4096
+    k = orc.f16(normal(331, (b, kvh, cap, d)))
+    v = orc.f16(normal(332, (b, kvh, cap, d)))
+    q = orc.f16(normal(333, (b, qh * d)) * 2)
+    out = torch.full((b, qh * d), float("nan"), dtype=torch.float16, device="cuda")
+    vl = torch.tensor([valid], dtype=torch.int32, device="cuda")
+    tmc.decode_attention(dev_f16(q), dev_f16(k), dev_f16(v), vl, out, b, qh, kvh, d, cap,
+                         _ws(tmc, torch, b, qh, kvh, d, cap))
+    torch.cuda.synchronize()
+    ref = orc.decode_attention(q, k, v, F16, qh, kvh, d, cap, valid)
+    assert_f16_path(values(out), ref, what=f"attention valid={valid} group={qh // kvh}")
+
+
 @pytest.mark.parametrize("b,valid,qh,kvh,cap", [(1, 1, 32, 32, 1024), (1, 33, 32, 32, 1024),
                                                  (1, 700, 32, 32, 1024), (1, 1024, 32, 32, 1024),
                                                  (2, 999, 8, 4, 1000), (3, 129, 4, 2, 160),
