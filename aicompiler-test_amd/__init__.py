@@ -110,6 +110,7 @@ def _declare(l):
                                                  i64, i64, i64, i64, i64, i64, i64, vp, sz, vp]),
         "tmc_paged_gather_probe": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, i64,
                                          vp, vp]),
+        "tmc_attention_timeline": (i32, [vp, i64]),
         "tmc_argmax_f32": (i32, [vp, vp, i64, i64, vp]),
         "tmc_lm_head_argmax_workspace_bytes": (sz, [i64, i64]),
         "tmc_rmsnorm_lm_head_partial_argmax_f16": (i32, [vp, vp, vp, vp, sz, i64, i64, f, vp, vp]),

@@ -9,6 +9,9 @@
   libtmc_hip_merge_launch.so  the same ABI built with TMC_ATTN_MERGE_LAUNCH=1
                   (every split-attention merge in a launch of its own, no
                   cross-block arrival counters), for the tests of that switch.
+  libtmc_hip_timeline.so  the same ABI built with TMC_ATTN_TIMELINE=1 (per-wave
+                  timestamps of the paged split-attention kernel, read by
+                  tmc_attention_timeline; profiling.py timeline).
 
 Objects go under _build/ (git-ignored); the libraries land next to this file
 so they travel with the source tree to the GPU box.
@@ -43,6 +46,7 @@ SOURCES = ["runtime.hip", "gemv.hip", "packed.hip", "elementwise.hip", "attentio
 ROCM_LIB = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
 
 MERGE_LAUNCH_OUT = os.path.join(HERE, "libtmc_hip_merge_launch.so")
+TIMELINE_OUT = os.path.join(HERE, "libtmc_hip_timeline.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -126,12 +130,15 @@ def build(jobs: int = 4) -> str:
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
         merge_launch = pool.submit(_compile, "attention.hip", "_merge_launch",
                                    ("-DTMC_ATTN_MERGE_LAUNCH=1",))
+        timeline = pool.submit(_compile, "attention.hip", "_timeline", ("-DTMC_ATTN_TIMELINE=1",))
         objs = list(pool.map(_compile, SOURCES))
         host_objs = list(pool.map(_compile_host, HOST_SOURCES))
         merge_launch_obj = merge_launch.result()
+        timeline_obj = timeline.result()
     _link_hip(objs, OUT)
     attention = os.path.join(BUILD, "attention.o")
     _link_hip([merge_launch_obj if o == attention else o for o in objs], MERGE_LAUNCH_OUT)
+    _link_hip([timeline_obj if o == attention else o for o in objs], TIMELINE_OUT)
     _run([CXX, "-shared", "-o", HOST_OUT + ".tmp", *host_objs, f"-L{HERE}", "-ltmc_hip",
           "-Wl,-rpath,$ORIGIN"], "link libtmc_host.so")
     shutil.move(HOST_OUT + ".tmp", HOST_OUT)

@@ -38,6 +38,26 @@ constexpr size_t kScratchBytes = 16u << 20;
 constexpr size_t kScratchCounterBytes = 64u << 10;  // merge counters at the scratch's start
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
+// Build switch: 1 records per-wave timestamps of the split kernel for
+// 16-position pages in 4-wave blocks (the GQA decode shape of bench.py's C4)
+// into `timeline`, read back by tmc_attention_timeline.  Per wave
+// (block-linear index * 4 + wave), kTimelineEvents slots: 0 / 1 the 100 MHz
+// real-time clock at entry and exit, 2 HW_ID | XCC_ID << 32, 3 the shader
+// clock (s_memtime) at entry, 4 before the first step, 5 before the
+// cross-wave merge and partial write, 6 after it, 7 at exit, 8 the wave's
+// step count (99: the block had no work), and for steps s < 12: 10 + 3s
+// before the step's loads, 11 + 3s once they have all arrived, 12 + 3s
+// after the step's arithmetic.  Waiting for every load of a step before
+// its timestamp costs the kernel about 10% (C4 37.9 -> 41.9 us on MI355X).
+#ifndef TMC_ATTN_TIMELINE
+#define TMC_ATTN_TIMELINE 0
+#endif
+constexpr int kTimelineWaves = 8192;
+constexpr int kTimelineEvents = 48;
+#if TMC_ATTN_TIMELINE
+static __device__ unsigned long long timeline[kTimelineWaves * kTimelineEvents];
+#endif
+
 namespace tmc {
 namespace {
 
@@ -98,6 +118,20 @@ __device__ __forceinline__ size_t out_index(const AttnParams& p, int b, int col,
   return (size_t)(b >> 4) * p.out_pass +
          ((size_t)(col >> 5) * 64 + (b & 15) + 16 * ((col & 31) >> 3)) * 8 + (col & 7);
 }
+
+// Timeline slot e of this wave (TMC_ATTN_TIMELINE builds; lane 0 writes).
+template <bool ON>
+__device__ __forceinline__ void timeline_put(int e, unsigned long long v) {
+#if TMC_ATTN_TIMELINE
+  if constexpr (ON) {
+    const unsigned w = (blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)) *
+                           (blockDim.x / kWave) + threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0 && w < (unsigned)kTimelineWaves)
+      timeline[(size_t)w * kTimelineEvents + e] = v;
+  }
+#endif
+}
+__device__ __forceinline__ unsigned long long shader_clock() { return __builtin_amdgcn_s_memtime(); }
 
 // Positions per split of the VALU kernel (D < 128): 4 waves x 2 tiles of
 // 4*64/(D/8) positions.
@@ -722,6 +756,14 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   __shared__ h8 s_k[kVia ? WAVES : 1][kVia ? kMfmaTiles * 256 : 1];
 
   const int b = blockIdx.z, kvh = blockIdx.x, split = blockIdx.y;
+  constexpr bool TL = TMC_ATTN_TIMELINE && MODE == 1 && WAVES == kWaves;
+  if constexpr (TL) {
+    timeline_put<TL>(0, __builtin_amdgcn_s_memrealtime());
+    timeline_put<TL>(3, shader_clock());
+    timeline_put<TL>(2, (unsigned long long)__builtin_amdgcn_s_getreg(4 | (31 << 11)) |
+                            ((unsigned long long)__builtin_amdgcn_s_getreg(20 | (15 << 11)) << 32));
+    timeline_put<TL>(8, 99);
+  }
   // One-split blocks (the whole row, max_pages <= the block's threads): each
   // thread fetches one block-table entry together with the row's length, so
   // the K/V addresses wait on one memory round trip instead of two.
@@ -784,11 +826,24 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   float (*s_pw)[GROUP] = s_p[wave];
 
   constexpr int kStride = kMfmaStep * WAVES;
+  int steps = 0;
+  if constexpr (TL) timeline_put<TL>(4, shader_clock());
   for (int p0 = begin + kMfmaStep * wave; p0 < end; p0 += kStride) {
     KvStep<MODE> st;
+    if constexpr (TL) if (steps < 12) timeline_put<TL>(10 + 3 * steps, shader_clock());
     issue_step<MODE, kVia>(p, s_pages, page0, cbase, kvh, p0, end, j, g, rk, rv, st);
+    if constexpr (TL) {
+      __builtin_amdgcn_s_waitcnt(0);
+      if (steps < 12) timeline_put<TL>(11 + 3 * steps, shader_clock());
+    }
     consume_step<GROUP, MODE, kVia>(p, s_pages, page0, st, qb, p0, end, j, g, s_pw, m, lsum, o,
                                     s_k[kVia ? wave : 0]);
+    if constexpr (TL) if (steps < 12) timeline_put<TL>(12 + 3 * steps, shader_clock());
+    ++steps;
+  }
+  if constexpr (TL) {
+    timeline_put<TL>(8, steps);
+    timeline_put<TL>(5, shader_clock());
   }
 
 #pragma unroll
@@ -808,7 +863,12 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   }
   __syncthreads();
   finish_split<D, GROUP, PAGED, WAVES>(p, b, kvh, split, nsplit, bad, s_m, s_l, s_o);
+  if constexpr (TL) timeline_put<TL>(6, shader_clock());
   if (nsplit > 1 && p.arrivals) merge_if_last<GROUP, PAGED, WAVES>(p, b, kvh, nsplit);
+  if constexpr (TL) {
+    timeline_put<TL>(7, shader_clock());
+    timeline_put<TL>(1, __builtin_amdgcn_s_memrealtime());
+  }
 }
 
 template <int D, int GROUP, bool PAGED>
@@ -1176,6 +1236,26 @@ int scratch_address(void** out) {
 }  // namespace
 
 extern "C" size_t tmc_attention_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" int tmc_attention_timeline(uint64_t* events, int64_t waves) {
+  clear_error();
+#if TMC_ATTN_TIMELINE
+  TMC_REQUIRE(events && waves > 0 && waves <= kTimelineWaves,
+              "Attention timeline: events must hold 1 .. " + std::to_string(kTimelineWaves) +
+                  " waves.");
+  const size_t bytes = (size_t)waves * kTimelineEvents * sizeof(uint64_t);
+  hipError_t err = hipDeviceSynchronize();
+  if (err == hipSuccess) err = hipMemcpyFromSymbol(events, HIP_SYMBOL(timeline), bytes);
+  if (err != hipSuccess)
+    return fail(std::string("Attention timeline: ") + hipGetErrorString(err));
+  return 0;
+#else
+  (void)events;
+  (void)waves;
+  return fail("Attention timeline: this library was built without TMC_ATTN_TIMELINE=1 "
+              "(libtmc_hip_timeline.so has it).");
+#endif
+}
 
 extern "C" int tmc_paged_decode_attention_noalloc(
     const void* q, const void* key_pool, const void* value_pool, const int32_t* valid_lengths,

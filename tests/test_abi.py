@@ -38,11 +38,12 @@ def test_library_exports_every_declared_symbol(tmc, header):
 
 
 def test_bench_helpers_stay_out_of_the_boundary():
-    """The measurement helpers (synthetic fill, copy and gather probes) are
-    declared in tmc_bench.h, not in the drop-in header."""
+    """The measurement helpers (synthetic fill, copy and gather probes, the
+    attention timeline) are declared in tmc_bench.h, not in the drop-in
+    header."""
     boundary, bench = set(declared_functions()), set(declared_functions("tmc_bench.h"))
     assert bench == {"tmc_fill_normal", "tmc_copy_bytes", "tmc_read_probe",
-                     "tmc_paged_gather_probe"}
+                     "tmc_paged_gather_probe", "tmc_attention_timeline"}
     assert not boundary & bench
 
 
@@ -95,6 +96,9 @@ def test_argument_validation_fails_before_device_work(tmc):
     assert lib.tmc_paged_gather_probe(p, p, p, None, 16, 8, 128, 16, 256, 8192, 16384, 2048, p,
                                       None) != 0
     assert "null" in tmc.last_error()
+    # the attention timeline exists only in the TMC_ATTN_TIMELINE build
+    assert lib.tmc_attention_timeline(p, 16) != 0
+    assert "TMC_ATTN_TIMELINE" in tmc.last_error()
     # the residual epilogue: batch 1 only, fp16 operands present
     assert lib.tmc_gemv_residual_f16(p, p, None, p, 1, 64, 8, None, None) != 0
     assert "null" in tmc.last_error()

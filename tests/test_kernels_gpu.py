@@ -1338,6 +1338,64 @@ def test_packed_gemm_residual_equals_gemm_then_add_bit_exact(tmc, orc, torch, ba
     assert np.array_equal(bits(y), bits(want))
 
 
+def test_attention_timeline_build(tmc, orc, torch):
+    """The build switch TMC_ATTN_TIMELINE=1 (libtmc_hip_timeline.so) stamps
+    the phases of every wave of the paged split kernel (16-position pages,
+    4-wave blocks) and leaves its results alone: the same bits as the plain
+    library on ragged GQA-4 rows, and per live wave the stamps in order
+    (entry, first step, each step's issue / arrival / end, merge, exit)."""
+    batch, qh, kvh, d, p, max_pages, pages = 8, 32, 8, 128, 16, 256, 2048
+    cap = p * max_pages  # 8 rows x 8 kv heads at capacity 4096: 1024-position splits
+    lengths = np.array([4096, 1, 700, 2049, 1500, 3333, 64, 1025], dtype=np.int32)
+    perm = np.random.default_rng(1410).permutation(pages).astype(np.int32)
+    tables = np.full((batch, max_pages), -1, np.int32)
+    cursor = 0
+    for i, n in enumerate(lengths):
+        need = (int(n) + p - 1) // p
+        tables[i, :need] = perm[cursor:cursor + need]
+        cursor += need
+    k_d = dev_f16(orc.f16(normal(1411, (pages, kvh, p, d))))
+    v_d = dev_f16(orc.f16(normal(1412, (pages, kvh, p, d))))
+    q_d = dev_f16(orc.f16(normal(1413, (batch, qh * d))))
+    valid_d, tables_d = dev(lengths), dev(tables)
+    active = torch.tensor([batch], dtype=torch.int32, device="cuda")
+    outs = []
+    saved = tmc._lib
+    variant = tmc.open_variant("libtmc_hip_timeline.so")
+    try:
+        for lib in (saved, variant):
+            tmc._lib = lib
+            out = torch.full((batch, qh * d), float("nan"), dtype=torch.float16, device="cuda")
+            tmc.paged_decode_attention(q_d, k_d, v_d, valid_d, tables_d, active, out, batch, qh,
+                                       kvh, d, p, max_pages, kvh * p * d, p * d,
+                                       _ws(tmc, torch, batch, qh, kvh, d, cap))
+            torch.cuda.synchronize()
+            outs.append(bits(out))
+        waves = kvh * (cap // 1024) * batch * 4  # grid (kv heads, splits, batch) x 4 waves
+        events = np.zeros(waves * 48, dtype=np.uint64)
+        tmc.check(variant.tmc_attention_timeline(events.ctypes.data, waves),
+                  "tmc_attention_timeline")
+    finally:
+        tmc._lib = saved
+    assert not np.isnan(outs[0].view(np.float16)).any()
+    assert np.array_equal(outs[0], outs[1])
+    ev = events.astype(np.int64).reshape(waves, 48)
+    steps = ev[:, 8]
+    live = ev[(steps > 0) & (steps < 99)]
+    # the live waves: 32 positions per step, 4 waves interleaved per 1024-position split
+    expect = sum(min(4, -(-(min(1024, int(n) - s) ) // 32)) for n in lengths
+                 for s in range(0, int(n), 1024)) * kvh
+    assert len(live) == expect
+    assert (steps == 99).sum() + len(live) + ((steps == 0) & (ev[:, 0] > 0)).sum() == waves
+    for w in live:
+        marks = [w[3], w[4]]
+        for s in range(min(int(w[8]), 12)):
+            marks += [w[10 + 3 * s], w[11 + 3 * s], w[12 + 3 * s]]
+        marks += [w[5], w[6], w[7]]
+        assert all(a <= b for a, b in zip(marks, marks[1:]))
+        assert w[0] <= w[1]
+
+
 def test_attention_merge_launch_build(tmc, orc, torch):
     """The build switch TMC_ATTN_MERGE_LAUNCH=1 (libtmc_hip_merge_launch.so)
     merges every split row in a second launch, so no block reads partials
