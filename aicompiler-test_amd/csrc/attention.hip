@@ -644,6 +644,108 @@ __device__ __forceinline__ void consume_step(const AttnParams& p, const int* s_p
   __builtin_amdgcn_wave_barrier();
 }
 
+// One step of the whole-row forms (MODE 0 / 1) with PV on the MFMA as well.
+// K goes through the wave's LDS slice as in consume_step; then V's 32 rows go
+// through the same slice (the 32-byte units of row R at unit slot u ^ (R & 7)),
+// and ds_read_b64_tr_b16 gives each lane the B operand of
+// v_mfma_f32_16x16x32_f16 with positions as k: a 16-lane group's result lane
+// n, element e, is the n-th 16-bit value of the 8-byte run its source lane
+// 4e + n/4 points at, so source lane s of group g points at position
+// (16h + 4g + s/4), dims 16db + 4(s%4): result lane (n, g) gets dims
+// 16db + n of positions 16h + 4g .. +3.  The probabilities are the A operand
+// just as the score MFMA left them: lane (head j, group g) holds positions
+// 4g .. 4g+3 of both 16-position tiles, the same k order.  oacc[db][r] is
+// O[head 4g + r][16 db + j], summed over the positions of the steps so far.
+template <int GROUP, int MODE>
+__device__ __forceinline__ void consume_step_pvm(const AttnParams& p, const int* s_pages,
+                                                 int page0, const KvStep<MODE>& st,
+                                                 const h8 (&qb)[4], int p0, int end, int j, int g,
+                                                 float& m, float& lsum, f4 (&oacc)[8], h8* s_k) {
+  static_assert(MODE != 2 && GROUP <= 16, "whole-row K/V forms, at most 16 heads per kv head");
+  typedef half_t v4h __attribute__((ext_vector_type(4)));
+  typedef __fp16 v4fp16 __attribute__((__vector_size__(8)));
+  float sc[kMfmaTiles][4];
+  float tile_max = -INFINITY;
+  h8 kf[kMfmaTiles][4];
+#pragma unroll
+  for (int t = 0; t < kMfmaTiles; ++t)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = 4 * q + g;
+      s_k[t * 256 + r * 16 + (j ^ r)] = st.k[t][q];
+    }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int t = 0; t < kMfmaTiles; ++t)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) kf[t][s] = s_k[t * 256 + j * 16 + ((4 * s + g) ^ j)];
+  __builtin_amdgcn_wave_barrier();
+  // V row R = 16t + 4i + g, 16-byte chunk j: unit j/2 at slot (j/2) ^ (R & 7)
+  char* vb = reinterpret_cast<char*>(s_k);
+#pragma unroll
+  for (int t = 0; t < kMfmaTiles; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int R = 16 * t + 4 * i + g;
+      *reinterpret_cast<h8*>(vb + R * 256 + (((j >> 1) ^ (R & 7)) << 5) + ((j & 1) << 4)) =
+          st.v[t][i];
+    }
+#pragma unroll
+  for (int t = 0; t < kMfmaTiles; ++t) {
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t][s], qb[s], acc, 0, 0, 0);
+    const int tp = p0 + 16 * t;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool ok = st.tile[t] >= 0 && tp + 4 * g + r < end;
+      sc[t][r] = ok ? acc[r] * p.scale_log2 : -INFINITY;
+      tile_max = fmaxf(tile_max, sc[t][r]);
+    }
+  }
+  tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16, kWave));
+  tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32, kWave));
+  const float next = fmaxf(m, tile_max);
+  const float alpha = next == -INFINITY ? 1.0f : fast_exp2(m - next);
+  float psum = 0.0f;
+  h8 pa;
+#pragma unroll
+  for (int t = 0; t < kMfmaTiles; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float pr = sc[t][r] == -INFINITY ? 0.0f : fast_exp2(sc[t][r] - next);
+      psum += pr;
+      pa[4 * t + r] = (half_t)(j < GROUP ? pr : 0.0f);
+    }
+  lsum = lsum * alpha + psum;
+  m = next;
+  // rows 4g .. 4g+3 of the accumulator are heads 4g + r: their alpha
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float ar = __shfl(alpha, 4 * g + r, kWave);
+#pragma unroll
+    for (int db = 0; db < 8; ++db) oacc[db][r] *= ar;
+  }
+  __builtin_amdgcn_wave_barrier();
+  const int s16 = j;  // source lane within the 16-lane group
+#pragma unroll
+  for (int db = 0; db < 8; ++db) {
+    v4h half_b[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int R = 16 * h + 4 * g + (s16 >> 2);
+      half_b[h] = __builtin_bit_cast(v4h, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+          reinterpret_cast<__attribute__((address_space(3))) v4fp16*>(
+              (__attribute__((address_space(3))) char*)vb + R * 256 + ((db ^ (R & 7)) << 5) +
+              ((s16 & 3) << 3))));
+    }
+    const h8 bv = __builtin_shufflevector(half_b[0], half_b[1], 0, 1, 2, 3, 4, 5, 6, 7);
+    oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, bv, oacc[db], 0, 0, 0);
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
 // Split merge inside the partial kernel (D = 128, GQA group <= 4: each
 // thread takes GROUP * 128 / threads outputs and issues the slot loads of
 // all of them before using any, one memory round trip per 8 splits; on C4,
@@ -741,7 +843,15 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   __shared__ float s_m[WAVES][GROUP];
   __shared__ float s_l[WAVES][GROUP];
   __shared__ float s_o[WAVES][GROUP][D];
-  __shared__ float s_p[WAVES][kMfmaStep][GROUP];
+  // PV on the MFMA (consume_step_pvm) for the whole-row forms (MODE 0, 1) of
+  // GQA groups of 4 and more below 16 waves, else on VALU with the
+  // probabilities passed through s_p.  The MFMA computes 16 head rows
+  // whatever the group, so for 1 or 2 heads the VALU form does less work with
+  // fewer registers (C3, MHA: 15.3 against 16.6 us with the MFMA form; C4,
+  // group 4: 37.5 -> 36.1 us); the 16-wave blocks would spill at their
+  // 128-register bound.
+  constexpr bool kPvm = MODE != 2 && WAVES != kWideWaves && GROUP >= 4;
+  __shared__ float s_p[kPvm ? 1 : WAVES][kMfmaStep][GROUP];
   __shared__ int s_pages[PAGED ? kMfmaMaxChunk + 1 : 1];
   // 16-position tiles (MODE 0, MODE 1) load K as whole rows and re-lay them
   // for the MFMA through 8 KiB of LDS per wave.  Measured against the
@@ -815,15 +925,20 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
     bad = __syncthreads_or(bad_page) != 0;
   }
   float m = -INFINITY, lsum = 0.0f;
-  float o[GROUP][8];
+  // kPvm: oacc[db][r] = O[head 4g + r][16 db + j]; else o[h][e] = this lane's
+  // share of O[head h][8 j + e]
+  float o[kPvm ? 1 : GROUP][8];
+  f4 oacc[kPvm ? 8 : 1];
 #pragma unroll
-  for (int h = 0; h < GROUP; ++h)
+  for (int h = 0; h < (kPvm ? 1 : GROUP); ++h)
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
+#pragma unroll
+  for (int db = 0; db < (kPvm ? 8 : 1); ++db) oacc[db] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   const size_t cbase = ((size_t)b * p.kv_heads + kvh) * (size_t)p.capacity * D;
   const __amdgpu_buffer_rsrc_t rk = buffer_of(p.k, p.kv_bytes);
   const __amdgpu_buffer_rsrc_t rv = buffer_of(p.v, p.kv_bytes);
-  float (*s_pw)[GROUP] = s_p[wave];
+  float (*s_pw)[GROUP] = s_p[kPvm ? 0 : wave];
 
   constexpr int kStride = kMfmaStep * WAVES;
   int steps = 0;
@@ -836,8 +951,12 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
       __builtin_amdgcn_s_waitcnt(0);
       if (steps < 12) timeline_put<TL>(11 + 3 * steps, shader_clock());
     }
-    consume_step<GROUP, MODE, kVia>(p, s_pages, page0, st, qb, p0, end, j, g, s_pw, m, lsum, o,
-                                    s_k[kVia ? wave : 0]);
+    if constexpr (kPvm)
+      consume_step_pvm<GROUP, MODE>(p, s_pages, page0, st, qb, p0, end, j, g, m, lsum, oacc,
+                                    s_k[wave]);
+    else
+      consume_step<GROUP, MODE, kVia>(p, s_pages, page0, st, qb, p0, end, j, g, s_pw, m, lsum, o,
+                                      s_k[kVia ? wave : 0]);
     if constexpr (TL) if (steps < 12) timeline_put<TL>(12 + 3 * steps, shader_clock());
     ++steps;
   }
@@ -846,20 +965,27 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
     timeline_put<TL>(5, shader_clock());
   }
 
-#pragma unroll
-  for (int h = 0; h < GROUP; ++h)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[h][e] = cross_sum<16>(o[h][e]);
   lsum = cross_sum<16>(lsum);
-  if (g == 0) {
+  if constexpr (kPvm) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (4 * g + r < GROUP)
+#pragma unroll
+        for (int db = 0; db < 8; ++db) s_o[wave][4 * g + r][16 * db + j] = oacc[db][r];
+  } else {
 #pragma unroll
     for (int h = 0; h < GROUP; ++h)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s_o[wave][h][8 * j + e] = o[h][e];
-    if (j < GROUP) {
-      s_m[wave][j] = m;
-      s_l[wave][j] = lsum;
-    }
+      for (int e = 0; e < 8; ++e) o[h][e] = cross_sum<16>(o[h][e]);
+    if (g == 0)
+#pragma unroll
+      for (int h = 0; h < GROUP; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s_o[wave][h][8 * j + e] = o[h][e];
+  }
+  if (g == 0 && j < GROUP) {
+    s_m[wave][j] = m;
+    s_l[wave][j] = lsum;
   }
   __syncthreads();
   finish_split<D, GROUP, PAGED, WAVES>(p, b, kvh, split, nsplit, bad, s_m, s_l, s_o);
