@@ -442,9 +442,10 @@ __global__ __launch_bounds__(kThreads) void attn_partial_kernel(AttnParams p) {
 // Scores come from v_mfma_f32_16x16x32_f16: A = the tile's 16 K rows, B = the
 // GROUP query heads of the kv head as columns (zero columns beyond GROUP).
 // Lane l: MFMA row/column j = l % 16, k-group g = l / 16 (MFMA s takes d chunk
-// 4s+g); acc[r] = score(position p0 + 4g + r, head j).  PV: lane (row g,
-// column chunk j) accumulates positions p0 + 4i + g, i < 4, with the
-// probabilities read back from the wave's LDS slice.
+// 4s+g); acc[r] = score(position p0 + 4g + r, head j).  PV on VALU
+// (consume_step): lane (row g, column chunk j) accumulates positions
+// p0 + 4i + g, i < 4, with the probabilities read back from the wave's LDS
+// slice; PV on the MFMA for GQA groups of 4 and more (consume_step_pvm).
 //
 // MODE 0: contiguous cache [request][kv head][capacity][128].  MODE 1: pages
 // whose size is a multiple of 16 (a 16-aligned tile lies in one page: one
