@@ -658,8 +658,7 @@ __device__ __forceinline__ void consume_step(const AttnParams& p, const int* s_p
 // 4g .. 4g+3 of both 16-position tiles, the same k order.  oacc[db][r] is
 // O[head 4g + r][16 db + j], summed over the positions of the steps so far.
 template <int GROUP, int MODE>
-__device__ __forceinline__ void consume_step_pvm(const AttnParams& p, const int* s_pages,
-                                                 int page0, const KvStep<MODE>& st,
+__device__ __forceinline__ void consume_step_pvm(const AttnParams& p, const KvStep<MODE>& st,
                                                  const h8 (&qb)[4], int p0, int end, int j, int g,
                                                  float& m, float& lsum, f4 (&oacc)[8], h8* s_k) {
   static_assert(MODE != 2 && GROUP <= 16, "whole-row K/V forms, at most 16 heads per kv head");
@@ -953,8 +952,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
       if (steps < 12) timeline_put<TL>(11 + 3 * steps, shader_clock());
     }
     if constexpr (kPvm)
-      consume_step_pvm<GROUP, MODE>(p, s_pages, page0, st, qb, p0, end, j, g, m, lsum, oacc,
-                                    s_k[wave]);
+      consume_step_pvm<GROUP, MODE>(p, st, qb, p0, end, j, g, m, lsum, oacc, s_k[wave]);
     else
       consume_step<GROUP, MODE, kVia>(p, s_pages, page0, st, qb, p0, end, j, g, s_pw, m, lsum, o,
                                       s_k[kVia ? wave : 0]);
