@@ -52,9 +52,9 @@ static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 #ifndef TMC_ATTN_TIMELINE
 #define TMC_ATTN_TIMELINE 0
 #endif
+#if TMC_ATTN_TIMELINE
 constexpr int kTimelineWaves = 8192;
 constexpr int kTimelineEvents = 48;
-#if TMC_ATTN_TIMELINE
 static __device__ unsigned long long timeline[kTimelineWaves * kTimelineEvents];
 #endif
 
