@@ -873,9 +873,9 @@ PYBIND11_MODULE(_tmc_host, m) {
         [](std::size_t rows, std::size_t width, bool f16, std::size_t threads) {
           RMSNormOp op;
           const DType t = f16 ? DType::Float16 : DType::Float32;
-          op.input = {{rows, width}, t};
-          op.weight = {{width}, t};
-          op.output = {{rows, width}, t};
+          op.input = {{rows, width}, t, Layout::Contiguous, {}};
+          op.weight = {{width}, t, Layout::Contiguous, {}};
+          op.output = {{rows, width}, t, Layout::Contiguous, {}};
           hip::HardwareInfo h;
           h.maxThreadsPerThreadgroup = 1024;
           h.maxThreadgroupMemoryLength = 160 * 1024;
@@ -885,9 +885,9 @@ PYBIND11_MODULE(_tmc_host, m) {
         [](std::size_t rows, std::size_t width, float eps, const FloatArray& input,
            const FloatArray& weight) {
           RMSNormOp op;
-          op.input = {{rows, width}, DType::Float32};
-          op.weight = {{width}, DType::Float32};
-          op.output = {{rows, width}, DType::Float32};
+          op.input = {{rows, width}, DType::Float32, Layout::Contiguous, {}};
+          op.weight = {{width}, DType::Float32, Layout::Contiguous, {}};
+          op.output = {{rows, width}, DType::Float32, Layout::Contiguous, {}};
           op.epsilon = eps;
           const auto ref = validation::rmsNormReference(op, toVector(input), toVector(weight));
           return std::vector<double>(ref.begin(), ref.end());
@@ -897,9 +897,9 @@ PYBIND11_MODULE(_tmc_host, m) {
            const FloatArray& input, const FloatArray& weight, std::vector<std::size_t> threads) {
           RMSNormOp op;
           const DType t = f16 ? DType::Float16 : DType::Float32;
-          op.input = {{rows, width}, t};
-          op.weight = {{width}, t};
-          op.output = {{rows, width}, t};
+          op.input = {{rows, width}, t, Layout::Contiguous, {}};
+          op.weight = {{width}, t, Layout::Contiguous, {}};
+          op.output = {{rows, width}, t, Layout::Contiguous, {}};
           op.epsilon = eps;
           if (threads.empty()) threads = planner::defaultRMSNormCandidates();
           std::ostringstream log;
