@@ -7,7 +7,6 @@
 #include <limits>
 #include <optional>
 #include <ostream>
-#include <set>
 #include <stdexcept>
 
 namespace tensor::runtime {
@@ -72,20 +71,44 @@ std::size_t activeCount(const std::vector<Request>& requests) {
   }));
 }
 
-// auditPageIsolation (ServingRuntime.cpp:436-452).
-bool auditPageIsolation(const std::vector<Request>& requests, std::size_t layers,
+// The check of auditPageIsolation (ServingRuntime.cpp:436-452): no physical
+// page of a layer's pool appears twice among the active requests' page
+// tables.  One mark per page of the pool (`seen`, reused across layers and
+// cleared through the pages it marked); a page id outside the pool is
+// reported as such.
+bool auditPageIsolation(const std::vector<Request>& requests,
+                        const std::vector<std::shared_ptr<KVPagePool>>& pools,
                         std::string& error) {
-  for (std::size_t l = 0; l < layers; ++l) {
-    std::set<std::int32_t> owners;
+  std::vector<std::uint8_t> seen;
+  std::vector<std::int32_t> marked;
+  for (std::size_t l = 0; l < pools.size(); ++l) {
+    const std::size_t capacity = pools[l]->capacityPages();
+    if (seen.size() < capacity) seen.resize(capacity, 0);
+    bool clash = false, outside = false;
     for (const auto& r : requests) {
       if (r.state != RequestState::Active) continue;
       for (const auto page : r.states[l]->pageTable()) {
-        if (!owners.insert(page).second) {
-          error = "Two active requests own the same physical KV page in layer " +
-                  std::to_string(l) + ".";
-          return false;
+        if (page < 0 || static_cast<std::size_t>(page) >= capacity) {
+          outside = true;
+        } else if (seen[static_cast<std::size_t>(page)]) {
+          clash = true;
+        } else {
+          seen[static_cast<std::size_t>(page)] = 1;
+          marked.push_back(page);
         }
       }
+    }
+    for (const auto page : marked) seen[static_cast<std::size_t>(page)] = 0;
+    marked.clear();
+    if (clash) {
+      error = "Two active requests own the same physical KV page in layer " + std::to_string(l) +
+              ".";
+      return false;
+    }
+    if (outside) {
+      error = "An active request holds a page id outside the pool in layer " + std::to_string(l) +
+              ".";
+      return false;
     }
   }
   return true;
@@ -438,7 +461,7 @@ ServingExecutionResult runContinuousBatch(hip::HipRuntime& runtime,
       }
 
       std::string isolation;
-      if (!auditPageIsolation(requests, plan.layerCount, isolation))
+      if (!auditPageIsolation(requests, pools, isolation))
         throw std::runtime_error(isolation);
       if (!progress) {
         const bool future = std::any_of(requests.begin(), requests.end(), [&](const Request& r) {
