@@ -1,7 +1,9 @@
-"""Per-wave timeline of the C4 paged attention kernel (MI355X).
+"""Per-wave timeline of the C4 paged (or C3 contiguous) attention kernel (MI355X).
 
 Runs bench.py's C4 workload (16 requests, 32 query / 8 kv heads of 128,
-16-position pages, lengths U[65, 4096], 6 rotating block-table sets) through
+16-position pages, lengths U[65, 4096], 6 rotating block-table sets), or with
+--workload c3 its C3 workload (one request, 32 heads of 128, L = 4095 + 1 of a
+4096 capacity, 8 rotating K/V copies), through
 the library built with TMC_ATTN_TIMELINE=1 (libtmc_hip_timeline.so), reads
 the per-wave timestamps of the last launch (tmc_attention_timeline; slot
 layout beside the switch in csrc/attention.hip) and reduces them to:
@@ -18,7 +20,7 @@ The timed figure of the plain library is printed beside it: the timeline
 build waits for each step's loads before stamping it, which costs about 10%.
 
 Usage (repo root, GPU box):
-  python3 aicompiler-test_amd/attention_timeline.py --json OUT.json --md OUT.md
+  python3 aicompiler-test_amd/attention_timeline.py [--workload c3] --json OUT.json --md OUT.md
 """
 from __future__ import annotations
 
@@ -35,8 +37,11 @@ ROOT = os.path.dirname(HERE)
 EVENTS = 48  # slots per wave (kTimelineEvents)
 MAX_WAVES = 8192
 STEPS = 12  # steps recorded per wave
-WORKLOAD = ("C4 paged GQA decode attention: 16 requests, 32 q / 8 kv heads x 128, pages of 16, "
-            "lengths U[65, 4096] (seed 403), 2 pools x 3 disjoint block-table sets")
+WORKLOADS = {
+    "c4": ("C4 paged GQA decode attention: 16 requests, 32 q / 8 kv heads x 128, pages of 16, "
+           "lengths U[65, 4096] (seed 403), 2 pools x 3 disjoint block-table sets"),
+    "c3": ("C3 contiguous decode attention: 1 request, 32 heads x 128, L = 4096 of a 4096 "
+           "capacity, 8 rotating K/V copies")}
 
 
 def c4_setup(tmc, torch):
@@ -75,6 +80,29 @@ def c4_setup(tmc, torch):
                                    max_pages, kvh * p * d, p * d, ws)
 
     return launch, int(lengths.sum()) * kvh * d * 2 * 2
+
+
+def c3_setup(tmc, torch):
+    """bench.py's C3 rotation (extra_measurements): returns (launch(i), K/V bytes)."""
+    f16 = torch.float16
+    heads, d, cap, copies, length = 32, 128, 4096, 8, 4096
+    ks = [torch.empty((1, heads, cap, d), dtype=f16, device="cuda") for _ in range(copies)]
+    vs = [torch.empty_like(ks[0]) for _ in range(copies)]
+    for c in range(copies):
+        tmc.fill_normal(ks[c], 301 + 10 * c)
+        tmc.fill_normal(vs[c], 302 + 10 * c)
+    q = torch.empty((1, heads * d), dtype=f16, device="cuda")
+    tmc.fill_normal(q, 303)
+    out = torch.empty((1, heads * d), dtype=f16, device="cuda")
+    valid = torch.tensor([length], dtype=torch.int32, device="cuda")
+    ws_bytes = tmc.attention_workspace_bytes(1, heads, heads, d, cap)
+    ws = torch.zeros(max(ws_bytes // 4, 1), dtype=torch.float32, device="cuda")
+
+    def launch(i: int) -> None:
+        tmc.decode_attention(q, ks[i % copies], vs[i % copies], valid, out, 1, heads, heads, d,
+                             cap, ws)
+
+    return launch, heads * length * d * 2 * 2
 
 
 def analyse(ev: np.ndarray, step_bytes: int = 16384) -> dict:
@@ -166,7 +194,7 @@ def analyse(ev: np.ndarray, step_bytes: int = 16384) -> dict:
 
 def markdown(rec: dict, command: str) -> str:
     a = rec["timeline"]
-    lines = ["# C4 paged attention: per-wave timeline (MI355X)", "",
+    lines = [f"# {rec['workload'].split(':')[0]}: per-wave timeline (MI355X)", "",
              "Command (repo root, MI355X box):", "", f"    {command}", "",
              f"Workload: {rec['workload']}.", "",
              f"Plain library: {rec['plain_us']} us per launch (graph-timed); timeline build "
@@ -215,12 +243,13 @@ def main(argv=None) -> int:
     ap.add_argument("--json", required=True)
     ap.add_argument("--md", required=True)
     ap.add_argument("--launches", type=int, default=40)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c4")
     args = ap.parse_args(argv)
     sys.path.insert(0, ROOT)
     import torch
     import bench
     tmc = bench.load_tmc()
-    launch, _ = c4_setup(tmc, torch)
+    launch, _ = (c3_setup if args.workload == "c3" else c4_setup)(tmc, torch)
     plain_us = bench.time_loop(torch, launch, 60) * 1e6
     saved = tmc.lib()
     variant = tmc.open_variant("libtmc_hip_timeline.so")
@@ -236,8 +265,9 @@ def main(argv=None) -> int:
     finally:
         tmc._lib = saved
     ev = buf.astype(np.int64).reshape(MAX_WAVES, EVENTS)
-    command = "python3 aicompiler-test_amd/attention_timeline.py --json OUT.json --md OUT.md"
-    rec = {"workload": WORKLOAD, "command": command, "plain_us": round(plain_us, 2),
+    flag = " --workload c3" if args.workload == "c3" else ""
+    command = f"python3 aicompiler-test_amd/attention_timeline.py{flag} --json OUT.json --md OUT.md"
+    rec = {"workload": WORKLOADS[args.workload], "command": command, "plain_us": round(plain_us, 2),
            "timeline_us": round(timeline_us, 2), "timeline": analyse(ev)}
     with open(args.json, "w") as f:
         json.dump(rec, f, indent=1)

@@ -38,9 +38,9 @@ constexpr size_t kScratchBytes = 16u << 20;
 constexpr size_t kScratchCounterBytes = 64u << 10;  // merge counters at the scratch's start
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
-// Build switch: 1 records per-wave timestamps of the split kernel for
-// 16-position pages in 4-wave blocks (the GQA decode shape of bench.py's C4)
-// into `timeline`, read back by tmc_attention_timeline.  Per wave
+// Build switch: 1 records per-wave timestamps of the 4-wave split kernel for
+// contiguous caches and 16-position pages (bench.py's C3 and C4) into
+// `timeline`, read back by tmc_attention_timeline.  Per wave
 // (block-linear index * 4 + wave), kTimelineEvents slots: 0 / 1 the 100 MHz
 // real-time clock at entry and exit, 2 HW_ID | XCC_ID << 32, 3 the shader
 // clock (s_memtime) at entry, 4 before the first step, 5 before the
@@ -866,7 +866,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   __shared__ h8 s_k[kVia ? WAVES : 1][kVia ? kMfmaTiles * 256 : 1];
 
   const int b = blockIdx.z, kvh = blockIdx.x, split = blockIdx.y;
-  constexpr bool TL = TMC_ATTN_TIMELINE && MODE == 1 && WAVES == kWaves;
+  constexpr bool TL = TMC_ATTN_TIMELINE && MODE != 2 && WAVES == kWaves;
   if constexpr (TL) {
     timeline_put<TL>(0, __builtin_amdgcn_s_memrealtime());
     timeline_put<TL>(3, shader_clock());

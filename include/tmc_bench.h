@@ -44,8 +44,8 @@ int tmc_paged_gather_probe(const void *key_pool, const void *value_pool,
                            int64_t max_pages, int64_t pool_pages, int64_t page_stride,
                            int64_t head_stride, void *sink, void *stream);
 
-/* Per-wave timestamps of the last launches of the paged split-attention
- * kernel (16-position pages, 4-wave blocks), for a library built with
+/* Per-wave timestamps of the last launches of the 4-wave split-attention
+ * kernel (contiguous caches and 16-position pages), for a library built with
  * TMC_ATTN_TIMELINE=1 (libtmc_hip_timeline.so): copies `waves` x 48 slots
  * (layout beside the switch in attention.hip) to the host array `events`,
  * after a device synchronize.  Other builds return an error.  No counterpart
