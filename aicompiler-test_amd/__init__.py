@@ -133,6 +133,7 @@ def _declare(l):
         "tmc_buf_write": (i32, [vp, vp, sz, sz]),
         "tmc_buf_write_raw": (i32, [vp, vp, sz, sz]),
         "tmc_buf_write_raw_async": (i32, [vp, vp, sz, sz]),
+        "tmc_buf_write_sparse_async": (i32, [vp, vp, sz]),
         "tmc_buf_copy_async": (i32, [vp, sz, vp, sz, sz]),
         "tmc_buf_read_raw": (i32, [vp, vp, sz, sz]),
         "tmc_buf_read": (i32, [vp, vp]),
@@ -914,6 +915,16 @@ class Buffer:
         src = np.ascontiguousarray(data, dtype=dt).ravel()
         check(lib().tmc_buf_write_raw_async(self.handle, src.ctypes.data_as(C.c_void_p), src.size,
                                             offset), "tmc_buf_write_raw_async")
+
+    def write_sparse_async(self, indices, values) -> None:
+        """int32 values stored at increasing element indices, queued on the
+        runtime stream (applied by a kernel that reads the staged pairs)."""
+        import numpy as np
+        pairs = np.stack([np.asarray(indices, np.int32).ravel(),
+                          np.asarray(values, np.int32).ravel()], axis=1)
+        pairs = np.ascontiguousarray(pairs)
+        check(lib().tmc_buf_write_sparse_async(self.handle, pairs.ctypes.data_as(C.c_void_p),
+                                               pairs.shape[0]), "tmc_buf_write_sparse_async")
 
     def read_raw(self):
         import numpy as np

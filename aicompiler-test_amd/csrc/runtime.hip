@@ -169,11 +169,12 @@ struct tmc_runtime {
   hipStream_t stream = nullptr;
   hipDeviceProp_t props{};
   int fail_next = 0;
-  // Pinned staging of tmc_buf_write_raw_async: copies are appended at
-  // `staged`; once `staged_done` (recorded after the last queued copy) has
-  // completed, every staged byte has reached the device and the area is
-  // reused from the start.
+  // Pinned staging of tmc_buf_write_raw_async and tmc_buf_write_sparse_async:
+  // copies and scatter launches are appended at `staged`; once `staged_done`
+  // (recorded after the last queued one) has completed, every staged byte has
+  // reached the device and the area is reused from the start.
   char* staging = nullptr;
+  char* staging_device = nullptr;  // the same pinned area as the device addresses it
   size_t staged = 0;
   hipEvent_t staged_done = nullptr;
 };
@@ -1235,31 +1236,30 @@ extern "C" int tmc_buf_write_raw(tmc_buffer* buf, const void* data, size_t count
 
 namespace {
 constexpr size_t kStagingBytes = size_t(4) << 20;
-}  // namespace
 
-extern "C" int tmc_buf_write_raw_async(tmc_buffer* buf, const void* data, size_t count,
-                                       size_t offset) {
-  clear_error();
-  if (!buf || !data || count == 0 || offset > buf->count || count > buf->count - offset)
-    return fail("tmc_buf_write_raw_async: invalid range.");
-  tmc_runtime* rt = buf->rt;
-  // a captured copy would replay whatever the staging slot holds later
+bool stream_captured(const tmc_runtime* rt) {
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(rt->stream, &capture) == hipSuccess &&
-      capture != hipStreamCaptureStatusNone)
-    return fail("tmc_buf_write_raw_async: not allowed while the runtime stream is captured.");
-  const size_t bytes = count * element_bytes(buf->dtype);
+  return hipStreamIsCapturing(rt->stream, &capture) == hipSuccess &&
+         capture != hipStreamCaptureStatusNone;
+}
+
+// `bytes` (rounded up to 256) of the runtime's pinned staging area for work
+// queued next on the runtime stream; the caller records staged_done after
+// that work.  Waits only when the area is full and its last user has not run.
+int stage_reserve(tmc_runtime* rt, size_t bytes, char*& slot_out) {
   const size_t slot = (bytes + 255) / 256 * 256;
-  if (slot > kStagingBytes) return tmc_buf_write_raw(buf, data, count, offset);
   if (!rt->staging) {
     void* pinned = nullptr;
     if (hip_ok(hipHostMalloc(&pinned, kStagingBytes, hipHostMallocDefault), "staging allocation"))
       return 1;
-    if (hip_ok(hipEventCreateWithFlags(&rt->staged_done, hipEventDisableTiming), "staging event")) {
+    void* mapped = nullptr;
+    if (hip_ok(hipHostGetDevicePointer(&mapped, pinned, 0), "staging device address") ||
+        hip_ok(hipEventCreateWithFlags(&rt->staged_done, hipEventDisableTiming), "staging event")) {
       (void)hipHostFree(pinned);
       return 1;
     }
     rt->staging = static_cast<char*>(pinned);
+    rt->staging_device = static_cast<char*>(mapped);
     rt->staged = 0;
   }
   if (rt->staged != 0) {
@@ -1273,13 +1273,75 @@ extern "C" int tmc_buf_write_raw_async(tmc_buffer* buf, const void* data, size_t
       rt->staged = 0;
     }
   }
-  char* stage = rt->staging + rt->staged;
+  slot_out = rt->staging + rt->staged;
+  rt->staged += slot;
+  return 0;
+}
+
+// dst[pairs[2i]] = pairs[2i + 1] for i < count.  The pairs sit in pinned
+// host memory that the host filled before queuing the launch; system-scope
+// loads read them past the device caches, so a reused staging slot is never
+// seen stale.  Indices are distinct (checked on the host), so the stores do
+// not race.
+__global__ __launch_bounds__(256) void scatter_pairs_kernel(const int32_t* pairs, int32_t* dst,
+                                                            int count) {
+  int32_t* src = const_cast<int32_t*>(pairs);
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x) {
+    const int32_t index = __hip_atomic_load(src + 2 * i, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_SYSTEM);
+    const int32_t value = __hip_atomic_load(src + 2 * i + 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_SYSTEM);
+    dst[index] = value;
+  }
+}
+}  // namespace
+
+extern "C" int tmc_buf_write_raw_async(tmc_buffer* buf, const void* data, size_t count,
+                                       size_t offset) {
+  clear_error();
+  if (!buf || !data || count == 0 || offset > buf->count || count > buf->count - offset)
+    return fail("tmc_buf_write_raw_async: invalid range.");
+  tmc_runtime* rt = buf->rt;
+  // a captured copy would replay whatever the staging slot holds later
+  if (stream_captured(rt))
+    return fail("tmc_buf_write_raw_async: not allowed while the runtime stream is captured.");
+  const size_t bytes = count * element_bytes(buf->dtype);
+  if ((bytes + 255) / 256 * 256 > kStagingBytes) return tmc_buf_write_raw(buf, data, count, offset);
+  char* stage = nullptr;
+  if (stage_reserve(rt, bytes, stage)) return 1;
   std::memcpy(stage, data, bytes);
   if (hip_ok(hipMemcpyAsync(static_cast<char*>(buf->ptr) + offset * element_bytes(buf->dtype),
                             stage, bytes, hipMemcpyHostToDevice, rt->stream),
              "staged write"))
     return 1;
-  rt->staged += slot;
+  return hip_ok(hipEventRecord(rt->staged_done, rt->stream), "staging event");
+}
+
+extern "C" int tmc_buf_write_sparse_async(tmc_buffer* buf, const int32_t* pairs, size_t count) {
+  clear_error();
+  if (!buf || !pairs || count == 0)
+    return fail("tmc_buf_write_sparse_async: null buffer or pairs, or no pairs.");
+  if (buf->dtype != TMC_I32)
+    return fail("tmc_buf_write_sparse_async: the buffer must hold int32 elements.");
+  if (count > kStagingBytes / (2 * sizeof(int32_t)))
+    return fail("tmc_buf_write_sparse_async: at most 524288 pairs per call.");
+  for (size_t i = 0; i < count; ++i) {
+    const int32_t index = pairs[2 * i];
+    if (index < 0 || (size_t)index >= buf->count || (i > 0 && index <= pairs[2 * i - 2]))
+      return fail("tmc_buf_write_sparse_async: indices must increase and lie inside the buffer.");
+  }
+  tmc_runtime* rt = buf->rt;
+  if (stream_captured(rt))
+    return fail("tmc_buf_write_sparse_async: not allowed while the runtime stream is captured.");
+  const size_t bytes = count * 2 * sizeof(int32_t);
+  char* stage = nullptr;
+  if (stage_reserve(rt, bytes, stage)) return 1;
+  std::memcpy(stage, pairs, bytes);
+  const auto* mapped = reinterpret_cast<const int32_t*>(rt->staging_device + (stage - rt->staging));
+  const unsigned blocks = (unsigned)std::min<size_t>((count + 255) / 256, 64);
+  hipLaunchKernelGGL(scatter_pairs_kernel, dim3(blocks), dim3(256), 0, rt->stream, mapped,
+                     static_cast<int32_t*>(buf->ptr), (int)count);
+  if (check_launch("scatter_pairs_kernel")) return 1;
   return hip_ok(hipEventRecord(rt->staged_done, rt->stream), "staging event");
 }
 

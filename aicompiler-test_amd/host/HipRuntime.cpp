@@ -123,6 +123,14 @@ std::string HipBuffer::writeRawAsync(const void* data, std::size_t count,
              : lastError("Buffer write failed.");
 }
 
+std::string HipBuffer::writeSparseAsync(const std::vector<std::int32_t>& pairs) const {
+  if (pairs.empty()) return {};
+  if (pairs.size() % 2 != 0) return "Sparse buffer write needs (index, value) pairs.";
+  return tmc_buf_write_sparse_async(buffer_, pairs.data(), pairs.size() / 2) == 0
+             ? std::string()
+             : lastError("Buffer write failed.");
+}
+
 std::string HipBuffer::copyFromAsync(const HipBuffer& source, std::size_t count,
                                      std::size_t offset, std::size_t sourceOffset) const {
   if (count == 0) return {};

@@ -104,6 +104,10 @@ class HipBuffer {
   // waiting: later launches on the stream see the data.
   [[nodiscard]] std::string writeRawAsync(const void* data, std::size_t count,
                                           std::size_t offset = 0) const;
+  // int32 buffers: values stored at increasing element indices (`pairs` =
+  // index, value, index, value, ...), queued on the runtime stream like
+  // writeRawAsync and applied by a kernel instead of a DMA copy.
+  [[nodiscard]] std::string writeSparseAsync(const std::vector<std::int32_t>& pairs) const;
   // Device copy of `count` elements from `source` (same dtype), queued on
   // the runtime stream.
   [[nodiscard]] std::string copyFromAsync(const HipBuffer& source, std::size_t count,

@@ -100,6 +100,17 @@ int tmc_buf_read_raw(const tmc_buffer *buf, void *data, size_t count, size_t off
  * larger than the staging area (4 MiB) fall back to tmc_buf_write_raw.
  * Refused while the runtime stream is being captured. */
 int tmc_buf_write_raw_async(tmc_buffer *buf, const void *data, size_t count, size_t offset);
+/* Sparse form of tmc_buf_write_raw_async for a TMC_I32 buffer: `pairs` holds
+ * `count` (element index, value) pairs, indices increasing and inside the
+ * buffer.  The pairs are copied into the same pinned staging area and a
+ * kernel on the runtime stream stores each value at its index, reading the
+ * pairs from the pinned host memory (no DMA transfer is queued; one of
+ * 512 KiB cost about 80 us between two graph launches on MI355X, the kernel
+ * about 6 us).  No counterpart in the reference: it is for the per-step
+ * block-table changes of a batched decode, one entry per layer for each
+ * request that enters a new page.  At most 524288 pairs; refused while the
+ * runtime stream is being captured. */
+int tmc_buf_write_sparse_async(tmc_buffer *buf, const int32_t *pairs, size_t count);
 /* Device-to-device copy of `count` elements (same dtype, same runtime),
  * queued on the runtime stream.  No counterpart in the reference: the
  * chained decode loop uses it to feed each step's greedy tokens to the next

@@ -84,6 +84,8 @@ def test_argument_validation_fails_before_device_work(tmc):
     assert "null" in tmc.last_error()
     assert lib.tmc_buf_write_raw_async(None, p, 1, 0) != 0
     assert "invalid range" in tmc.last_error()
+    assert lib.tmc_buf_write_sparse_async(None, p, 1) != 0
+    assert "null buffer" in tmc.last_error()
     # graph-path element-wise kernels: the tuner's workgroup sizes only
     assert lib.tmc_elementwise(0, p, p, p, 0, 64, 512, None) != 0
     assert "threads must be 64, 128 or 256" in tmc.last_error()

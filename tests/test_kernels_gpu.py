@@ -1191,6 +1191,46 @@ def test_async_raw_writes_reach_the_device_in_order(tmc, torch):
         buf.write_raw_async(np.zeros(4, np.int32), n - 3)
 
 
+def test_sparse_writes_reach_the_device_in_order(tmc, torch):
+    """tmc_buf_write_sparse_async: scattered (index, value) pairs land in
+    queue order with the dense staged writes around them, through enough
+    calls to wrap the staging area; bad pairs are refused before anything is
+    queued."""
+    rt = tmc.Runtime()
+    n = 1 << 20
+    buf = rt.create_buffer(n, tmc.I32)
+    rng = np.random.default_rng(78)
+    expect = rng.integers(-2**31, 2**31 - 1, n, dtype=np.int32)
+    buf.write_raw_async(expect)
+    for step in range(400):
+        if step % 7 == 3:  # a dense span in between
+            count = int(rng.integers(1, 30000))
+            offset = int(rng.integers(0, n - count))
+            data = rng.integers(-2**31, 2**31 - 1, count, dtype=np.int32)
+            expect[offset:offset + count] = data
+            buf.write_raw_async(data, offset)
+            continue
+        count = int(rng.integers(1, 5000)) if step % 5 else 1
+        idx = np.sort(rng.choice(n, count, replace=False)).astype(np.int32)
+        if step % 11 == 0:
+            idx[-1] = n - 1  # the last element
+        idx = np.unique(idx)
+        vals = rng.integers(-2**31, 2**31 - 1, idx.size, dtype=np.int32)
+        expect[idx] = vals
+        buf.write_sparse_async(idx, vals)
+    assert np.array_equal(buf.read_raw(), expect)
+    before = buf.read_raw()
+    for idx, vals in (([3, 3], [1, 2]), ([5, 4], [1, 2]), ([n], [1]), ([-1], [1])):
+        with pytest.raises(tmc.TmcError, match="indices must increase"):
+            buf.write_sparse_async(idx, vals)
+    with pytest.raises(tmc.TmcError, match="at most 524288 pairs"):
+        buf.write_sparse_async(np.arange(524289), np.zeros(524289))
+    half = rt.create_buffer(64, tmc.F16)
+    with pytest.raises(tmc.TmcError, match="int32"):
+        half.write_sparse_async([0], [1])
+    assert np.array_equal(buf.read_raw(), before)
+
+
 # ---------------------------------------------------------------- batch > 1 folded norms
 @pytest.mark.parametrize("batch,k,n,layout,out_dtype", [
     (16, 4096, 4096, 1, "f16"), (5, 1160, 200, 0, "f32"), (20, 4096, 12288, 3, "f16"),
