@@ -134,6 +134,7 @@ def _declare(l):
         "tmc_buf_write_raw": (i32, [vp, vp, sz, sz]),
         "tmc_buf_write_raw_async": (i32, [vp, vp, sz, sz]),
         "tmc_buf_write_sparse_async": (i32, [vp, vp, sz]),
+        "tmc_decode_chain": (i32, [vp, vp, vp, vp, i64, vp]),
         "tmc_buf_copy_async": (i32, [vp, sz, vp, sz, sz]),
         "tmc_buf_read_raw": (i32, [vp, vp, sz, sz]),
         "tmc_buf_read": (i32, [vp, vp]),

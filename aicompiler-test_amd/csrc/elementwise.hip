@@ -1118,6 +1118,36 @@ extern "C" int tmc_argmax_f32(const float* logits, int32_t* tokens, int64_t rows
   return check_launch("argmax_kernel");
 }
 
+namespace tmc {
+namespace {
+// Between two chained greedy-decode steps: row r's token becomes the next
+// step's input token and the step's history entry, and its length grows by
+// one (the position the next step appends).
+__global__ __launch_bounds__(64) void decode_chain_kernel(const int32_t* __restrict__ next,
+                                                          int32_t* __restrict__ tokens,
+                                                          int32_t* __restrict__ lengths,
+                                                          int32_t* __restrict__ history,
+                                                          int rows) {
+  for (int r = blockIdx.x * 64 + threadIdx.x; r < rows; r += gridDim.x * 64) {
+    const int32_t token = next[r];
+    tokens[r] = token;
+    if (history) history[r] = token;
+    if (lengths) lengths[r] += 1;
+  }
+}
+}  // namespace
+}  // namespace tmc
+
+extern "C" int tmc_decode_chain(const int32_t* next_tokens, int32_t* tokens, int32_t* lengths,
+                                int32_t* history, int64_t rows, void* stream) {
+  TMC_REQUIRE(next_tokens && tokens, "Decode chain: null device pointer.");
+  TMC_REQUIRE(rows > 0 && rows <= (1LL << 20), "Decode chain: rows must be in [1, 2^20].");
+  const unsigned blocks = (unsigned)std::min<int64_t>((rows + 63) / 64, 64);
+  hipLaunchKernelGGL(tmc::decode_chain_kernel, dim3(blocks), dim3(64), 0, as_stream(stream),
+                     next_tokens, tokens, lengths, history, (int)rows);
+  return check_launch("decode_chain_kernel");
+}
+
 extern "C" int tmc_fill_normal(void* ptr, int dtype, int64_t count, uint64_t seed, float mean,
                                float std, void* stream) {
   TMC_REQUIRE(ptr && count > 0 && float_dtype(dtype), "Fill: invalid arguments.");

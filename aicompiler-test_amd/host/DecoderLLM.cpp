@@ -826,6 +826,12 @@ std::string BatchedDecodeExecutor::upload(const std::vector<std::int32_t>& token
     if (!error.empty()) return error;
     metaShadow_ = std::move(meta);
   }
+  return uploadTables(tables);
+}
+
+std::string BatchedDecodeExecutor::uploadTables(
+    const std::vector<std::vector<std::int32_t>>& tables) {
+  const std::size_t M = maximumBatchSize_;
   // Pack [layer][M][maxPages] and write what changed.
   std::vector<std::int32_t> packed(tableShadow_.size(), -1);
   for (std::size_t l = 0; l < tables.size(); ++l)
@@ -906,21 +912,43 @@ std::string BatchedDecodeExecutor::launchChained(
   std::size_t index = 0;
   while (buckets_[index]->rows < rows) ++index;
   auto& bucket = *buckets_[index];
-  // Tokens fed back on the device leave the host shadow stale: upload the
-  // metadata in full, then overwrite the token slots from nextTokens_.
+  // After a chained step the device holds that step's tokens in the token
+  // slots and its lengths advanced by one (tmc_decode_chain below).  The
+  // metadata goes up in full for the first step; later steps send only the
+  // lengths, and only when they do not follow the previous step's by one.
+  const std::size_t M = maximumBatchSize_;
   std::fill(metaShadow_.begin(), metaShadow_.end(), std::numeric_limits<std::int32_t>::min());
-  const std::vector<std::int32_t> placeholder(rows, 0);
-  error = upload(tokenIds.empty() ? placeholder : tokenIds, validLengths, blockTables, rows,
-                 bucket.rows);
-  if (error.empty() && tokenIds.empty()) error = tokensView_->copyFromAsync(*nextTokens_, rows);
+  if (!tokenIds.empty()) {
+    error = upload(tokenIds, validLengths, blockTables, rows, bucket.rows);
+  } else {
+    bool follows = chainedLengths_.size() == rows;
+    for (std::size_t r = 0; follows && r < rows; ++r)
+      follows = validLengths[r] == chainedLengths_[r] + 1;
+    if (!follows) {
+      std::vector<std::int32_t> lengths(M + 1, 0);
+      std::copy(validLengths.begin(), validLengths.end(), lengths.begin());
+      lengths[M] = static_cast<std::int32_t>(rows);
+      error = meta_->writeRawAsync(lengths.data(), lengths.size(), M);
+    }
+    if (error.empty()) error = uploadTables(blockTables);
+  }
   hip::PreparedSequence* sequence = nullptr;
   if (error.empty()) error = stepSequence(bucket, false, sequence);
   if (error.empty()) error = sequence->launch();
   if (error.empty() && registry_) registry_->completed(bucket.uses);
-  if (error.empty())
-    error = history_->copyFromAsync(*nextTokens_, rows, historyStep * maximumBatchSize_);
+  if (error.empty() &&
+      tmc_decode_chain(static_cast<const std::int32_t*>(nextTokens_->devicePointer()),
+                       static_cast<std::int32_t*>(tokensView_->devicePointer()),
+                       static_cast<std::int32_t*>(lengthsView_->devicePointer()),
+                       static_cast<std::int32_t*>(history_->devicePointer()) + historyStep * M,
+                       static_cast<std::int64_t>(rows), runtime_->stream()) != 0)
+    error = std::string("Chained decode: ") + tmc_last_error();
   std::fill(metaShadow_.begin(), metaShadow_.end(), std::numeric_limits<std::int32_t>::min());
   chainedRows_ = error.empty() ? rows : 0;
+  if (error.empty())
+    chainedLengths_ = validLengths;
+  else
+    chainedLengths_.clear();
   return error;
 }
 

@@ -215,8 +215,8 @@ class BatchedDecodeExecutor {
 
   // Chained decode: steps queued back to back with no host wait.  A step
   // with empty `tokenIds` takes the previous step's greedy tokens on the
-  // device (same row count); every step's next tokens are also copied to
-  // history slot `historyStep` (reserveHistory first).  readHistory waits for
+  // device (same row count); every step's next tokens also go to history
+  // slot `historyStep` (reserveHistory first).  readHistory waits for
   // the stream and returns [steps][maximumBatchSize()] token ids.  Same
   // checks and results as run(); the loop of measureDecodeThroughput.
   [[nodiscard]] std::string reserveHistory(std::size_t steps);
@@ -278,6 +278,7 @@ class BatchedDecodeExecutor {
                                    const std::vector<std::int32_t>& lengths,
                                    const std::vector<std::vector<std::int32_t>>& tables,
                                    std::size_t rows, std::size_t bucket);
+  [[nodiscard]] std::string uploadTables(const std::vector<std::vector<std::int32_t>>& tables);
   [[nodiscard]] std::string checkStep(const std::vector<std::int32_t>* tokenIds,
                                       const std::vector<std::int32_t>& validLengths,
                                       const std::vector<std::vector<std::int32_t>>& blockTables) const;
@@ -312,6 +313,7 @@ class BatchedDecodeExecutor {
   std::vector<std::int32_t> metaShadow_, tableShadow_;
   hip::BufferHandle history_;  // int32 [steps][M], chained decode
   std::size_t historySteps_ = 0, chainedRows_ = 0;
+  std::vector<std::int32_t> chainedLengths_;  // lengths the last chained step ran with
 };
 
 struct BatchedDecodeExecutor::Creation {

@@ -718,6 +718,14 @@ int tmc_prefill_attention_rows_f16(const void *q, const void *key_pool, const vo
 int tmc_argmax_f32(const float *logits, int32_t *tokens, int64_t rows, int64_t vocabulary,
                    void *stream);
 
+/* Chained greedy decode, queued between two step graphs: for r < rows,
+ * tokens[r] = history[r] = next_tokens[r] and lengths[r] += 1 (history and
+ * lengths may be null).  No counterpart in the reference, whose steps return
+ * to the host: it replaces three queued copies per step (tokens, history,
+ * lengths) with one launch. */
+int tmc_decode_chain(const int32_t *next_tokens, int32_t *tokens, int32_t *lengths,
+                     int32_t *history, int64_t rows, void *stream);
+
 /* Token-only LM head (the decode step's tail when no logits are read,
  * DecoderLLMExecutor.cpp:837-845,929-930): a partial pass computes the LM
  * head's logits and keeps, per block, the greatest (value, index) in the
