@@ -46,7 +46,7 @@ import sys
 
 
 def short_name(name: str) -> str:
-    m = re.search(r"tmc::\(anonymous namespace\)::(\w+)(<[^>]*>)?", name)
+    m = re.search(r"(?:tmc::)?\(anonymous namespace\)::(\w+)(<[^>]*>)?", name)
     if m:
         return m.group(1) + (m.group(2) or "")
     m = re.search(r"GLOBAL__N_1\d+(\w+?)I(.*)EEv", name)
