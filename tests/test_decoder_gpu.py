@@ -332,6 +332,55 @@ def test_batched_executor_rows_match_oracle(host, orc, rt):
     assert "capacity" in ex.run([1] * 5, [0] + lengths[1:], tables, False, False)["error"]
 
 
+def test_launch_chained_matches_run_with_a_repeated_length(host, orc, rt):
+    """BatchedDecodeExecutor.launch_chained against run(): three rows decode
+    from empty caches across page boundaries.  The chained executor keeps each
+    step's greedy tokens and the lengths advanced by one on the device (one
+    tmc_decode_chain launch between steps); one step repeats the previous
+    length (a rollback by one position), so its lengths do not follow and go
+    up again.  Every step's tokens equal those of a second executor over its
+    own pools that reads each step's tokens back and uploads them (run)."""
+    cfg = CONFIGS["serve"]
+    m = _weights(orc, cfg, 81)
+    w = _workload(host, orc, cfg, m)
+    model = host.create_model_resources(rt, w)
+    L, rows, pages = cfg["layers"], 3, 16
+    execs, states = [], []
+    for _ in range(2):
+        pools = [host.create_kv_page_pool(rt, w.plan.kv_plan(), P, pages) for _ in range(L)]
+        execs.append(host.create_batched_decode_executor(rt, model, pools, rows))
+        states.append([[host.create_kv_cache_state(rt, w.plan.kv_plan(), pools[l], False)
+                        for l in range(L)] for _ in range(rows)])
+    max_pages = execs[0].max_pages()
+    schedule = list(range(1, 21)) + [20] + list(range(21, 41))
+
+    def stage(e, n):
+        tables = [[] for _ in range(L)]
+        for r in range(rows):
+            for l, st in enumerate(states[e][r]):
+                assert st.stage_length(rt, n) == ""
+                st.commit_length(n)
+                tables[l] += st.page_table() + [-1] * (max_pages - len(st.page_table()))
+        return tables
+
+    first = [11, 222, 2999]
+    chained, stepped = execs
+    chained.reserve_history(len(schedule))
+    want, tokens = [], list(first)
+    for step, n in enumerate(schedule):
+        chained.launch_chained(first if step == 0 else [], [n] * rows, stage(0, n), step)
+        out = stepped.run(tokens, [n] * rows, stage(1, n), False, False)
+        assert out["passed"], out["error"]
+        tokens = [int(t) for t in out["next_token_ids"]]
+        want.append(tokens)
+    got = chained.read_history(len(schedule))
+    for step in range(len(schedule)):
+        assert list(got[step * rows:(step + 1) * rows]) == want[step], step
+    # a chained step without tokens needs the previous step's row count
+    with pytest.raises(RuntimeError, match="row count"):
+        chained.launch_chained([], [41, 41], stage(0, 41), 0)
+
+
 @pytest.mark.parametrize("chunk,per_chunk", [(0, 1), (8, 1), (64, 4)])
 def test_serving_matches_single_request_decoding(host, orc, rt, chunk, per_chunk):
     """chunk 0: prompts by decode in the batched ticks; chunk > 0: prompts
