@@ -1,9 +1,12 @@
-"""Per-wave timeline of the C4 paged (or C3 contiguous) attention kernel (MI355X).
+"""Per-wave timeline of the C4 paged (or C3, or batch-16 decode) attention kernel (MI355X).
 
 Runs bench.py's C4 workload (16 requests, 32 query / 8 kv heads of 128,
 16-position pages, lengths U[65, 4096], 6 rotating block-table sets), or with
 --workload c3 its C3 workload (one request, 32 heads of 128, L = 4095 + 1 of a
-4096 capacity, 8 rotating K/V copies), through
+4096 capacity, 8 rotating K/V copies), or with --workload b16 the attention of
+the batch-16 7B decode step (16 requests, 32 heads of 128, 16-position pages
+of a 1024 capacity, the C5 prompt lengths + 64: one 8-wave block per
+(request, head)), through
 the library built with TMC_ATTN_TIMELINE=1 (libtmc_hip_timeline.so), reads
 the per-wave timestamps of the last launch (tmc_attention_timeline; slot
 layout beside the switch in csrc/attention.hip) and reduces them to:
@@ -20,7 +23,7 @@ The timed figure of the plain library is printed beside it: the timeline
 build waits for each step's loads before stamping it, which costs about 10%.
 
 Usage (repo root, GPU box):
-  python3 aicompiler-test_amd/attention_timeline.py [--workload c3] --json OUT.json --md OUT.md
+  python3 aicompiler-test_amd/attention_timeline.py [--workload c3|b16] --json OUT.json --md OUT.md
 """
 from __future__ import annotations
 
@@ -41,7 +44,10 @@ WORKLOADS = {
     "c4": ("C4 paged GQA decode attention: 16 requests, 32 q / 8 kv heads x 128, pages of 16, "
            "lengths U[65, 4096] (seed 403), 2 pools x 3 disjoint block-table sets"),
     "c3": ("C3 contiguous decode attention: 1 request, 32 heads x 128, L = 4096 of a 4096 "
-           "capacity, 8 rotating K/V copies")}
+           "capacity, 8 rotating K/V copies"),
+    "b16": ("Batch-16 decode attention of the 7B step: 16 requests, 32 heads x 128, pages of 16, "
+            "capacity 1024, lengths = the C5 prompt lengths (U[32, 512], seed 502) + 64, "
+            "2 pools x 3 disjoint block-table sets")}
 
 
 def c4_setup(tmc, torch):
@@ -80,6 +86,49 @@ def c4_setup(tmc, torch):
                                    max_pages, kvh * p * d, p * d, ws)
 
     return launch, int(lengths.sum()) * kvh * d * 2 * 2
+
+
+def b16_setup(tmc, torch):
+    """The batch-16 decode step's paged MHA attention at C5's prompt lengths
+    plus 64 decoded tokens: returns (launch(i), K/V bytes per launch)."""
+    f16 = torch.float16
+    d, batch, heads, p, cap = 128, 16, 32, 16, 1024
+    max_pages = cap // p
+    rng = np.random.default_rng(502)
+    lengths = np.array([len(rng.integers(0, 32000, rng.integers(32, 513))) for _ in range(batch)])
+    lengths = lengths + 64
+    need = (lengths + p - 1) // p
+    pages = 3 * int(need.sum())
+    sets, pools = [], []
+    for pool in range(2):
+        perm = np.random.default_rng(504 + pool).permutation(pages).astype(np.int32)
+        kp = torch.empty((pages, heads, p, d), dtype=f16, device="cuda")
+        vp = torch.empty((pages, heads, p, d), dtype=f16, device="cuda")
+        tmc.fill_normal(kp, 501 + 7 * pool)
+        tmc.fill_normal(vp, 502 + 7 * pool)
+        pools.append((kp, vp))
+        cursor = 0
+        for _ in range(3):
+            t = np.full((batch, max_pages), -1, np.int32)
+            for i in range(batch):
+                t[i, :need[i]] = perm[cursor:cursor + need[i]]
+                cursor += need[i]
+            sets.append((pool, torch.from_numpy(t).cuda()))
+    q = torch.empty((batch, heads * d), dtype=f16, device="cuda")
+    tmc.fill_normal(q, 505)
+    out = torch.empty((batch, heads * d), dtype=f16, device="cuda")
+    valid = torch.from_numpy(lengths.astype(np.int32)).cuda()
+    active = torch.tensor([batch], dtype=torch.int32, device="cuda")
+    ws_bytes = tmc.attention_workspace_bytes(batch, heads, heads, d, cap)
+    ws = torch.zeros(max(ws_bytes // 4, 1), dtype=torch.float32, device="cuda")
+
+    def launch(i: int) -> None:
+        pool, table = sets[i % len(sets)]
+        kp, vp = pools[pool]
+        tmc.paged_decode_attention(q, kp, vp, valid, table, active, out, batch, heads, heads, d,
+                                   p, max_pages, heads * p * d, p * d, ws)
+
+    return launch, int(lengths.sum()) * heads * d * 2 * 2
 
 
 def c3_setup(tmc, torch):
@@ -249,7 +298,8 @@ def main(argv=None) -> int:
     import torch
     import bench
     tmc = bench.load_tmc()
-    launch, _ = (c3_setup if args.workload == "c3" else c4_setup)(tmc, torch)
+    setup = {"c3": c3_setup, "c4": c4_setup, "b16": b16_setup}[args.workload]
+    launch, _ = setup(tmc, torch)
     plain_us = bench.time_loop(torch, launch, 60) * 1e6
     saved = tmc.lib()
     variant = tmc.open_variant("libtmc_hip_timeline.so")
@@ -265,7 +315,7 @@ def main(argv=None) -> int:
     finally:
         tmc._lib = saved
     ev = buf.astype(np.int64).reshape(MAX_WAVES, EVENTS)
-    flag = " --workload c3" if args.workload == "c3" else ""
+    flag = "" if args.workload == "c4" else f" --workload {args.workload}"
     command = f"python3 aicompiler-test_amd/attention_timeline.py{flag} --json OUT.json --md OUT.md"
     rec = {"workload": WORKLOADS[args.workload], "command": command, "plain_us": round(plain_us, 2),
            "timeline_us": round(timeline_us, 2), "timeline": analyse(ev)}

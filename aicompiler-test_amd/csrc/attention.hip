@@ -38,10 +38,11 @@ constexpr size_t kScratchBytes = 16u << 20;
 constexpr size_t kScratchCounterBytes = 64u << 10;  // merge counters at the scratch's start
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
-// Build switch: 1 records per-wave timestamps of the 4-wave split kernel for
-// contiguous caches and 16-position pages (bench.py's C3 and C4) into
+// Build switch: 1 records per-wave timestamps of the 4-wave split kernel and
+// the 8-wave one-split kernel for contiguous caches and 16-position pages
+// (bench.py's C3 and C4, the batch-16 7B decode step's attention) into
 // `timeline`, read back by tmc_attention_timeline.  Per wave
-// (block-linear index * 4 + wave), kTimelineEvents slots: 0 / 1 the 100 MHz
+// (block-linear index * waves per block + wave), kTimelineEvents slots: 0 / 1 the 100 MHz
 // real-time clock at entry and exit, 2 HW_ID | XCC_ID << 32, 3 the shader
 // clock (s_memtime) at entry, 4 before the first step, 5 before the
 // cross-wave merge and partial write, 6 after it, 7 at exit, 8 the wave's
@@ -150,6 +151,35 @@ __device__ __forceinline__ int slot_in_page(const AttnParams& p, int pos) {
 template <bool PAGED>
 __device__ __forceinline__ int valid_length(const AttnParams& p, int b) {
   return PAGED ? p.valid[b] : p.valid[0];
+}
+
+// Request of the one-split 8-wave block in request slot `slot` (batch > 1
+// MHA: `rows` requests x kv_heads blocks, two blocks per CU).  The blocks of
+// slots z and z + per_round (per_round = 256 / kv_heads, the slots of one
+// round over MI355X's 256 CUs) land on one CU, so a CU's time follows the
+// sum of two rows' lengths.  Slots [0, per_round) take the requests in
+// order of decreasing length and the rest in increasing order, pairing long
+// rows with short ones; every block derives the same permutation from the
+// lengths (ties by index; rows at or past the active count last), so each
+// request is still attended once per head.  Two barriers; every thread of
+// the block calls it.
+constexpr int kDealMax = 64;
+__device__ int dealt_request(const AttnParams& p, int slot, int rows, int per_round) {
+  __shared__ int s_len[kDealMax];
+  __shared__ int s_order[kDealMax];
+  if (rows > kDealMax || per_round < 1 || rows <= per_round) return slot;
+  const int t = threadIdx.x;
+  const int active = p.active ? p.active[0] : rows;
+  if (t < rows) s_len[t] = t < active ? p.valid[t] : -1;
+  __syncthreads();
+  if (t < rows) {
+    const int mine = s_len[t];
+    int rank = 0;
+    for (int u = 0; u < rows; ++u) rank += s_len[u] > mine || (s_len[u] == mine && u < t);
+    s_order[rank] = t;
+  }
+  __syncthreads();
+  return s_order[slot < per_round ? slot : rows - 1 - (slot - per_round)];
 }
 
 // Positions per split of the D = 128 kernel for a row of `valid` positions.
@@ -865,8 +895,8 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   constexpr bool kVia = MODE != 2;
   __shared__ h8 s_k[kVia ? WAVES : 1][kVia ? kMfmaTiles * 256 : 1];
 
-  const int b = blockIdx.z, kvh = blockIdx.x, split = blockIdx.y;
-  constexpr bool TL = TMC_ATTN_TIMELINE && MODE != 2 && WAVES == kWaves;
+  const int kvh = blockIdx.x, split = blockIdx.y;
+  constexpr bool TL = TMC_ATTN_TIMELINE && MODE != 2 && (WAVES == kWaves || WAVES == kMidWaves);
   if constexpr (TL) {
     timeline_put<TL>(0, __builtin_amdgcn_s_memrealtime());
     timeline_put<TL>(3, shader_clock());
@@ -877,6 +907,9 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   // One-split blocks (the whole row, max_pages <= the block's threads): each
   // thread fetches one block-table entry together with the row's length, so
   // the K/V addresses wait on one memory round trip instead of two.
+  int b = blockIdx.z;
+  if constexpr (PAGED && WAVES == kMidWaves)
+    b = dealt_request(p, b, (int)gridDim.z, 256 / (int)gridDim.x);
   int early_page = -1;
   if constexpr (PAGED && WAVES == kWideWaves) {
     if ((int)threadIdx.x < p.max_pages)

@@ -45,7 +45,8 @@ int tmc_paged_gather_probe(const void *key_pool, const void *value_pool,
                            int64_t head_stride, void *sink, void *stream);
 
 /* Per-wave timestamps of the last launches of the 4-wave split-attention
- * kernel (contiguous caches and 16-position pages), for a library built with
+ * kernel and the 8-wave one-split kernel (contiguous caches and 16-position
+ * pages), for a library built with
  * TMC_ATTN_TIMELINE=1 (libtmc_hip_timeline.so): copies `waves` x 48 slots
  * (layout beside the switch in attention.hip) to the host array `events`,
  * after a device synchronize.  Other builds return an error.  No counterpart
