@@ -153,33 +153,42 @@ __device__ __forceinline__ int valid_length(const AttnParams& p, int b) {
   return PAGED ? p.valid[b] : p.valid[0];
 }
 
-// Request of the one-split 8-wave block in request slot `slot` (batch > 1
-// MHA: `rows` requests x kv_heads blocks, two blocks per CU).  The blocks of
-// slots z and z + per_round (per_round = 256 / kv_heads, the slots of one
-// round over MI355X's 256 CUs) land on one CU, so a CU's time follows the
-// sum of two rows' lengths.  Slots [0, per_round) take the requests in
-// order of decreasing length and the rest in increasing order, pairing long
-// rows with short ones; every block derives the same permutation from the
-// lengths (ties by index; rows at or past the active count last), so each
-// request is still attended once per head.  Two barriers; every thread of
-// the block calls it.
+// (request, split) unit of a paged block of the 4-wave split kernel or the
+// 8-wave one-split kernel.  A launch runs `rows` x `splits` units per kv head
+// (slot v = split + splits * request, the grid's order); blocks whose slots
+// are `per_round` apart (per_round = 256 / kv_heads, the slots of one round
+// over MI355X's 256 CUs) land on one CU, so a CU's time follows the sum of
+// two units' positions.  Slots [0, per_round) take the units in order of
+// decreasing positions (a unit holds min(chunk, length - split * chunk) of
+// its request's positions, 0 past the request's end) and the rest in
+// increasing order, pairing heavy units with light or empty ones.  Every
+// block derives the same permutation from all rows' lengths (ties by slot;
+// rows at or past the active count hold no positions), so each unit still
+// runs once.  Two barriers; every thread of the block calls it.
 constexpr int kDealMax = 64;
-__device__ int dealt_request(const AttnParams& p, int slot, int rows, int per_round) {
-  __shared__ int s_len[kDealMax];
+__device__ int dealt_unit(const AttnParams& p, int slot, int rows, int splits, int chunk,
+                          int per_round) {
+  __shared__ int s_work[kDealMax];
   __shared__ int s_order[kDealMax];
-  if (rows > kDealMax || per_round < 1 || rows <= per_round) return slot;
+  const int units = rows * splits;
+  if (units > kDealMax || per_round < 1 || units <= per_round) return slot;
   const int t = threadIdx.x;
   const int active = p.active ? p.active[0] : rows;
-  if (t < rows) s_len[t] = t < active ? p.valid[t] : -1;
+  if (t < units) {
+    const int row = t / splits;
+    const int length = row < active ? p.valid[row] : 0;
+    const int ok = length >= 1 && length <= p.capacity;
+    s_work[t] = ok ? max(0, min(chunk, length - (t % splits) * chunk)) : 0;
+  }
   __syncthreads();
-  if (t < rows) {
-    const int mine = s_len[t];
+  if (t < units) {
+    const int mine = s_work[t];
     int rank = 0;
-    for (int u = 0; u < rows; ++u) rank += s_len[u] > mine || (s_len[u] == mine && u < t);
+    for (int u = 0; u < units; ++u) rank += s_work[u] > mine || (s_work[u] == mine && u < t);
     s_order[rank] = t;
   }
   __syncthreads();
-  return s_order[slot < per_round ? slot : rows - 1 - (slot - per_round)];
+  return s_order[slot < per_round ? slot : units - 1 - (slot - per_round)];
 }
 
 // Positions per split of the D = 128 kernel for a row of `valid` positions.
@@ -895,7 +904,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   constexpr bool kVia = MODE != 2;
   __shared__ h8 s_k[kVia ? WAVES : 1][kVia ? kMfmaTiles * 256 : 1];
 
-  const int kvh = blockIdx.x, split = blockIdx.y;
+  const int kvh = blockIdx.x;
   constexpr bool TL = TMC_ATTN_TIMELINE && MODE != 2 && (WAVES == kWaves || WAVES == kMidWaves);
   if constexpr (TL) {
     timeline_put<TL>(0, __builtin_amdgcn_s_memrealtime());
@@ -907,9 +916,13 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
   // One-split blocks (the whole row, max_pages <= the block's threads): each
   // thread fetches one block-table entry together with the row's length, so
   // the K/V addresses wait on one memory round trip instead of two.
-  int b = blockIdx.z;
-  if constexpr (PAGED && WAVES == kMidWaves)
-    b = dealt_request(p, b, (int)gridDim.z, 256 / (int)gridDim.x);
+  int b = blockIdx.z, split = blockIdx.y;
+  if constexpr (PAGED && (WAVES == kWaves || WAVES == kMidWaves)) {
+    const int unit = dealt_unit(p, split + (int)gridDim.y * b, (int)gridDim.z, (int)gridDim.y,
+                                p.chunk, 256 / (int)gridDim.x);
+    b = unit / (int)gridDim.y;
+    split = unit % (int)gridDim.y;
+  }
   int early_page = -1;
   if constexpr (PAGED && WAVES == kWideWaves) {
     if ((int)threadIdx.x < p.max_pages)
