@@ -169,6 +169,7 @@ def analyse(ev: np.ndarray, step_bytes: int = 16384) -> dict:
            "shader_clock_mhz": round(float(clock), 1),
            "span_us": round(float((rt1.max() - base) / 100.0), 2),
            "entry_to_first_step_us_p10_50_90": pct(us(live[:, 4] - live[:, 3]), [10, 50, 90]),
+           "entry_to_unit_known_us_p10_50_90": pct(us(live[:, 9] - live[:, 3]), [10, 50, 90]),
            "wave_end_us_p10_50_90_max": pct((rt1 - base) / 100.0, [10, 50, 90, 100])}
     per_step = []
     for s in range(STEPS):
@@ -252,6 +253,8 @@ def markdown(rec: dict, command: str) -> str:
              f"shader clock {a['shader_clock_mhz']} MHz; span {a['span_us']} us.", "",
              f"- entry to first step (length, block table): p10/50/90 "
              f"{a['entry_to_first_step_us_p10_50_90']} us",
+             f"- entry to the block knowing its (request, split) unit (the dealing, paged "
+             f"blocks): p10/50/90 {a['entry_to_unit_known_us_p10_50_90']} us",
              f"- wave end: p10/50/90/max {a['wave_end_us_p10_50_90_max']} us",
              f"- last step's stamp to the loop exit: p10/50/90 "
              f"{a['last_step_to_loop_exit_us_p10_50_90']} us",

@@ -44,7 +44,8 @@ static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 // `timeline`, read back by tmc_attention_timeline.  Per wave
 // (block-linear index * waves per block + wave), kTimelineEvents slots: 0 / 1 the 100 MHz
 // real-time clock at entry and exit, 2 HW_ID | XCC_ID << 32, 3 the shader
-// clock (s_memtime) at entry, 4 before the first step, 5 before the
+// clock (s_memtime) at entry, 9 once the block knows its unit (dealt
+// blocks; else the entry clock), 4 before the first step, 5 before the
 // cross-wave merge and partial write, 6 after it, 7 at exit, 8 the wave's
 // step count (99: the block had no work), and for steps s < 12: 10 + 3s
 // before the step's loads, 11 + 3s once they have all arrived, 12 + 3s
@@ -164,28 +165,37 @@ __device__ __forceinline__ int valid_length(const AttnParams& p, int b) {
 // increasing order, pairing heavy units with light or empty ones.  Every
 // block derives the same permutation from all rows' lengths (ties by slot;
 // rows at or past the active count hold no positions), so each unit still
-// runs once.  Two barriers; every thread of the block calls it.
-constexpr int kDealMax = 64;
+// runs once.  The first wave sorts the units (one per lane) with a bitonic
+// network of lane exchanges, 21 dependent steps instead of a pass over every
+// other unit per lane; one barrier; every thread of the block calls it.
+constexpr int kDealMax = kWave;
 __device__ int dealt_unit(const AttnParams& p, int slot, int rows, int splits, int chunk,
                           int per_round) {
-  __shared__ int s_work[kDealMax];
   __shared__ int s_order[kDealMax];
   const int units = rows * splits;
   if (units > kDealMax || per_round < 1 || units <= per_round) return slot;
   const int t = threadIdx.x;
-  const int active = p.active ? p.active[0] : rows;
-  if (t < units) {
-    const int row = t / splits;
-    const int length = row < active ? p.valid[row] : 0;
-    const int ok = length >= 1 && length <= p.capacity;
-    s_work[t] = ok ? max(0, min(chunk, length - (t % splits) * chunk)) : 0;
-  }
-  __syncthreads();
-  if (t < units) {
-    const int mine = s_work[t];
-    int rank = 0;
-    for (int u = 0; u < units; ++u) rank += s_work[u] > mine || (s_work[u] == mine && u < t);
-    s_order[rank] = t;
+  if (t < kWave) {
+    const int active = p.active ? p.active[0] : rows;
+    // key: positions, then the lower unit first; lanes past the units last
+    int key = -1;
+    if (t < units) {
+      const int row = t / splits;
+      const int length = row < active ? p.valid[row] : 0;
+      const int ok = length >= 1 && length <= p.capacity;
+      const int work = ok ? max(0, min(chunk, length - (t % splits) * chunk)) : 0;
+      key = work * kWave + (kWave - 1 - t);
+    }
+    // descending bitonic sort over the wave's 64 lanes
+#pragma unroll
+    for (int k = 2; k <= kWave; k <<= 1)
+#pragma unroll
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        const int other = __shfl_xor(key, j, kWave);
+        const bool take_max = ((t & k) == 0) == ((t & j) == 0);
+        key = take_max ? max(key, other) : min(key, other);
+      }
+    if (t < units) s_order[t] = kWave - 1 - (key & (kWave - 1));
   }
   __syncthreads();
   return s_order[slot < per_round ? slot : units - 1 - (slot - per_round)];
@@ -923,6 +933,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_mfma_kernel(AttnParams p) 
     b = unit / (int)gridDim.y;
     split = unit % (int)gridDim.y;
   }
+  if constexpr (TL) timeline_put<TL>(9, shader_clock());
   int early_page = -1;
   if constexpr (PAGED && WAVES == kWideWaves) {
     if ((int)threadIdx.x < p.max_pages)
