@@ -1428,7 +1428,7 @@ def test_attention_timeline_build(tmc, orc, torch):
     assert len(live) == expect
     assert (steps == 99).sum() + len(live) + ((steps == 0) & (ev[:, 0] > 0)).sum() == waves
     for w in live:
-        marks = [w[3], w[4]]
+        marks = [w[3], w[9], w[4]]  # entry, unit dealt, first step
         for s in range(min(int(w[8]), 12)):
             marks += [w[10 + 3 * s], w[11 + 3 * s], w[12 + 3 * s]]
         marks += [w[5], w[6], w[7]]
