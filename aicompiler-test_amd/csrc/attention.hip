@@ -180,9 +180,10 @@ __device__ int dealt_unit(const AttnParams& p, int slot, int rows, int splits, i
     // key: positions, then the lower unit first; lanes past the units last
     int key = -1;
     if (t < units) {
+      // the length and the active count are read together (both in bounds)
       const int row = t / splits;
-      const int length = row < active ? p.valid[row] : 0;
-      const int ok = length >= 1 && length <= p.capacity;
+      const int length = p.valid[row];
+      const int ok = row < active && length >= 1 && length <= p.capacity;
       const int work = ok ? max(0, min(chunk, length - (t % splits) * chunk)) : 0;
       key = work * kWave + (kWave - 1 - t);
     }
