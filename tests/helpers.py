@@ -47,15 +47,25 @@ def assert_f16_path(actual, reference, what=""):
     return err.max(), rel_rms
 
 
-def assert_f32_rel(actual, reference, rel=1e-4, what=""):
-    """|a - r| <= rel * max(|r|, rms(r)) per element (the RMS floor keeps
-    near-zero references from demanding absolute exactness)."""
+F32_ATOL = 1e-5  # the fp32 (absolute, relative) pair: (1e-5, 1e-4), GraphExecutor.cpp:31-34
+
+
+def assert_f32_rel(actual, reference, rel=1e-4, what="", atol=F32_ATOL):
+    """The reference's element rule for fp32 outputs, |a - r| <= atol + rel * |r|
+    for every element (validation/Validator.cpp:26, with GraphExecutor.cpp's
+    fp32 tolerance pair 1e-5 / 1e-4 and RMSNormTuner.cpp:19-20's).  Both
+    sides fp32-accumulate the same fp16 products, so only the summation order
+    differs: at K = 4096 that moves an output by about 1e-6, well inside the
+    1e-5 floor."""
     a = np.asarray(actual, np.float64).ravel()
     r = np.asarray(reference, np.float64).ravel()
     assert a.shape == r.shape, what
     assert np.all(np.isfinite(a)), f"{what}: non-finite output"
-    floor = np.sqrt(np.mean(r ** 2))
-    bound = rel * np.maximum(np.abs(r), floor)
-    worst = np.max(np.abs(a - r) / np.maximum(np.abs(r), floor))
-    assert np.all(np.abs(a - r) <= bound), f"{what}: worst relative err {worst:.3e} > {rel}"
+    err = np.abs(a - r)
+    bound = atol + rel * np.abs(r)
+    worst = float(np.max(err / bound)) if err.size else 0.0
+    i = int(np.argmax(err / bound)) if err.size else 0
+    assert np.all(err <= bound), (
+        f"{what}: element {i} expected {r[i]:.8g} got {a[i]:.8g} "
+        f"(|err| {err[i]:.3e} > {atol} + {rel} * |expected|)")
     return worst
